@@ -1,0 +1,205 @@
+"""CPU oracle for the exact-max shared-selection path -- TEST INFRASTRUCTURE ONLY.
+
+Only tests/, ``__graft_entry__.smoke()`` and ``bench.py``'s cpu_baseline leg may import this
+module.  The product library never calls it and never falls back to it.
+
+Thin ctypes/numpy wrapper over ``libsta_oracle.so`` (built from ``sta_oracle.c`` by the Makefile
+next to it).  Each function names the reference lines it restates:
+
+  select_vote  <- shared_selection_triton_exact_2.py:50-140   (Kernel A, freq mode)
+  build_sets   <- shared_selection_triton_exact_2.py:277-426  (_build_sets, freq mode)
+  gather_attn  <- shared_selection_triton_exact_2.py:146-225  (Kernel C)
+  shared_pi_attention <- shared_selection_triton_exact_2.py:432-486 (composition) and, with two
+                         geometries, shared_selection_triton_hybrid_exact.py:450-510
+
+Arrays are numpy.  Half-precision tensors travel as uint16 bit patterns with a dtype code:
+0 = fp32, 1 = bf16, 2 = fp16.
+"""
+import ctypes
+import math
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB = None
+
+F32, BF16, F16 = 0, 1, 2
+_DTYPE_CODES = {"float32": F32, "bfloat16": BF16, "float16": F16}
+
+
+def build():
+    """Compile libsta_oracle.so with the Makefile next to this file."""
+    subprocess.run(["make", "-s", "-C", _HERE], check=True)
+
+
+def lib():
+    global _LIB
+    if _LIB is None:
+        path = os.path.join(_HERE, "libsta_oracle.so")
+        if not os.path.exists(path) or os.path.getmtime(path) < os.path.getmtime(
+                os.path.join(_HERE, "sta_oracle.c")):
+            build()
+        _LIB = ctypes.CDLL(path)
+    return _LIB
+
+
+def _p(a):
+    return a.ctypes.data_as(ctypes.c_void_p) if a is not None else None
+
+
+def _c(a, dt):
+    return np.ascontiguousarray(a, dtype=dt)
+
+
+def num_threads():
+    return int(lib().oracle_num_threads())
+
+
+def set_num_threads(n):
+    lib().oracle_set_num_threads(ctypes.c_int(int(n)))
+
+
+# ---------------------------------------------------------------------------------------------
+# dtype helpers
+# ---------------------------------------------------------------------------------------------
+def from_torch(t):
+    """torch tensor -> (numpy array, dtype code).  bf16/fp16 become uint16 bit patterns."""
+    import torch
+    t = t.detach().cpu().contiguous()
+    if t.dtype == torch.float32:
+        return t.numpy(), F32
+    if t.dtype == torch.bfloat16:
+        return t.view(torch.int16).numpy().view(np.uint16), BF16
+    if t.dtype == torch.float16:
+        return t.view(torch.int16).numpy().view(np.uint16), F16
+    raise TypeError(f"unsupported dtype {t.dtype}")
+
+
+def to_f32(a, dtype):
+    a = np.ascontiguousarray(a)
+    out = np.empty(a.shape, np.float32)
+    lib().oracle_to_f32(_p(a), _p(out), ctypes.c_size_t(a.size), ctypes.c_int(dtype))
+    return out
+
+
+def round_to_dtype(x, dtype):
+    """fp32 array -> dtype storage (RNE); uint16 bit patterns for bf16/fp16."""
+    x = _c(x, np.float32)
+    out = np.empty(x.shape, np.float32 if dtype == F32 else np.uint16)
+    lib().oracle_round_to_dtype(_p(x), _p(out), ctypes.c_size_t(x.size), ctypes.c_int(dtype))
+    return out
+
+
+# ---------------------------------------------------------------------------------------------
+# the three stages
+# ---------------------------------------------------------------------------------------------
+def rope_rotate(x, dtype, posf, inv_freq, rope_scale):
+    """Rotate rows of x (rows, D) at fp32 angle bases posf (rows,)."""
+    x = np.ascontiguousarray(x)
+    rows, D = x.shape
+    out = np.empty((rows, D), np.float32)
+    lib().oracle_rope_rotate(_p(x), ctypes.c_int(dtype), ctypes.c_int(rows), ctypes.c_int(D),
+                             _p(_c(posf, np.float32)), _p(_c(inv_freq, np.float32)),
+                             ctypes.c_float(rope_scale), _p(out))
+    return out
+
+
+def select_vote(q, k, dtype, tau, inv_freq, pos_scale, rope_scale, sm_scale, tile, q_pos_base=0,
+                band_eps=1e-3, want_band=False, want_keep=False):
+    """Kernel A (exact_2.py:50-140).  q (H,N,D), k (Hkv,N,D).  Returns a dict with
+    votes (H,nt,N) int32, row_counts (H,N) int32, row_max (H,N) fp32 and optionally
+    band (H,nt,N) int32 and keep (H,N,N) uint8."""
+    q = np.ascontiguousarray(q)
+    k = np.ascontiguousarray(k)
+    H, N, D = q.shape
+    Hkv = k.shape[0]
+    nt = (N + tile - 1) // tile
+    votes = np.empty((H, nt, N), np.int32)
+    row_counts = np.empty((H, N), np.int32)
+    row_max = np.empty((H, N), np.float32)
+    band = np.empty((H, nt, N), np.int32) if want_band else None
+    keep = np.empty((H, N, N), np.uint8) if want_keep else None
+    lib().oracle_select_vote(
+        _p(q), _p(k), ctypes.c_int(dtype), ctypes.c_int(H), ctypes.c_int(Hkv), ctypes.c_int(N),
+        ctypes.c_int(D), _p(_c(tau, np.float32)), _p(_c(inv_freq, np.float32)),
+        ctypes.c_float(pos_scale), ctypes.c_float(rope_scale), ctypes.c_float(sm_scale),
+        ctypes.c_int(tile), ctypes.c_int(q_pos_base), _p(votes), _p(row_counts), _p(row_max),
+        _p(band), ctypes.c_float(band_eps), _p(keep))
+    out = {"votes": votes, "row_counts": row_counts, "row_max": row_max}
+    if want_band:
+        out["band"] = band
+    if want_keep:
+        out["keep"] = keep
+    return out
+
+
+def start_pct_of(pct):
+    """start_pct = max(0, int(round(pct))) with Python's round-half-even (exact_2.py:309)."""
+    return max(0, int(round(pct)))
+
+
+def build_sets(votes, pos_scale, n_global, n_local, pct, T, k_max, q_pos_base=0, measure=False):
+    """_build_sets (exact_2.py:277-426), freq mode.  votes (H,nt,N) int.  Returns the reference's
+    9-tuple (idx, newpos_k, newpos_q, shared_size, kept_size, chosen, orig_overflow, kpct_meas,
+    overflow20) as numpy arrays."""
+    votes = _c(votes, np.int32)
+    H, nt, N = votes.shape
+    idx = np.empty((H, nt, k_max), np.int32)
+    npk = np.empty((H, nt, k_max), np.float32)
+    npq = np.empty((H, nt, T), np.float32)
+    ss = np.empty((H, nt), np.int32)
+    ks = np.empty((H, nt), np.int32)
+    ch = np.empty((H, nt), np.int32)
+    oo = np.empty((H, nt), np.uint8)
+    km = np.empty((H, nt), np.int32)
+    o20 = np.empty((H, nt), np.uint8)
+    lib().oracle_build_sets(
+        _p(votes), ctypes.c_int(H), ctypes.c_int(nt), ctypes.c_int(N), ctypes.c_float(pos_scale),
+        ctypes.c_int(n_global), ctypes.c_int(n_local), ctypes.c_int(start_pct_of(pct)),
+        ctypes.c_int(T), ctypes.c_int(k_max), ctypes.c_int(q_pos_base), ctypes.c_int(int(measure)),
+        _p(idx), _p(npk), _p(npq), _p(ss), _p(ks), _p(ch), _p(oo), _p(km), _p(o20))
+    return idx, npk, npq, ss, ks, ch, oo.astype(bool), km, o20.astype(bool)
+
+
+def gather_attn(q, k, v, dtype, idx, newpos_k, newpos_q, inv_freq, rope_scale, sm_scale, T,
+                k_max, block_k=64, q_pos_base=0):
+    """Kernel C (exact_2.py:146-225).  Returns the fp32 accumulator (H,N,D) before the final cast."""
+    q = np.ascontiguousarray(q)
+    k = np.ascontiguousarray(k)
+    v = np.ascontiguousarray(v)
+    H, N, D = q.shape
+    Hkv = k.shape[0]
+    out = np.full((H, N, D), np.nan, np.float32)
+    lib().oracle_gather_attn(
+        _p(q), _p(k), _p(v), ctypes.c_int(dtype), ctypes.c_int(H), ctypes.c_int(Hkv),
+        ctypes.c_int(N), ctypes.c_int(D), _p(_c(inv_freq, np.float32)), ctypes.c_float(rope_scale),
+        ctypes.c_float(sm_scale), ctypes.c_int(T), ctypes.c_int(k_max), ctypes.c_int(block_k),
+        ctypes.c_int(q_pos_base), _p(_c(idx, np.int32)), _p(_c(newpos_k, np.float32)),
+        _p(_c(newpos_q, np.float32)), _p(out))
+    return out
+
+
+def shared_pi_attention(q, k, v, dtype, tau, inv_freq_a, pos_scale_a, rope_scale_a,
+                        inv_freq_c=None, pos_scale_c=None, rope_scale_c=None, pct=30.0,
+                        sm_scale=None, n_global=32, n_local=32, tile=32, k_max=1024, block_k=64,
+                        q_pos_base=0, measure=False):
+    """Composition of the three stages (exact_2.py:432-486).  With the *_c triple given it is the
+    hybrid entry point (hybrid_exact.py:450-510): Kernel A under the a-geometry, _build_sets'
+    reposition and Kernel C under the c-geometry.  Returns
+    (out_f32, shared_size, kept_size, kpct, overflow, kpct_meas, overflow20, extras)."""
+    H, N, D = q.shape
+    if sm_scale is None:
+        sm_scale = 1.0 / math.sqrt(D)
+    if inv_freq_c is None:
+        inv_freq_c, pos_scale_c, rope_scale_c = inv_freq_a, pos_scale_a, rope_scale_a
+    a = select_vote(q, k, dtype, tau, inv_freq_a, pos_scale_a, rope_scale_a, sm_scale, tile,
+                    q_pos_base)
+    idx, npk, npq, ss, ks, ch, oo, km, o20 = build_sets(
+        a["votes"], pos_scale_c, n_global, n_local, pct, tile, k_max, q_pos_base, measure)
+    out = gather_attn(q, k, v, dtype, idx, npk, npq, inv_freq_c, rope_scale_c, sm_scale, tile,
+                      k_max, block_k, q_pos_base)
+    extras = {"votes": a["votes"], "row_max": a["row_max"], "row_counts": a["row_counts"],
+              "idx": idx, "newpos_k": npk, "newpos_q": npq}
+    return out, ss, ks, ch, oo, km, o20, extras
