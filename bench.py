@@ -1,0 +1,185 @@
+#!/usr/bin/env python3
+"""Prefill throughput of exact-max shared-selection thresholded attention on one MI355X.
+
+A step is one pass of the whole prefill path over one attention layer of synthetic input
+(config 1 of the benchmark table: 32 heads x d128 x 12288 tokens bf16, PI 4096 -> 12288,
+tau 5, tile 64, top-30% with the 25/20% fallback under the 2048-key cap): RoPE pre-kernels,
+pass 1 (exact row max), pass 2 (threshold + votes), LDS selection and the sparse
+gather-attention, all through the C ABI with inputs already resident in HBM and outputs /
+workspace allocated before the timed region.
+
+Prints one JSON line (rank 0).  Only one GPU is supported: --gpus above 1 exits with a message.
+Besides the throughput it reports per-stage times measured with HIP events recorded on the
+launch stream inside the timed region, the roofline fraction of the dominant kernel, and the
+CPU oracle timed on a bounded sample of the same workload.
+"""
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.join(ROOT, "sparse-thresholded-attention_amd")
+for _p in (ROOT, PKG):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+METRIC = "prefill tokens/sec @32h x d128 x 12k bf16; % MFMA peak (score) / % HBM peak (gather)"
+PEAK_BF16_TFLOPS = 2500.0      # MI355X dense bf16 MFMA
+PEAK_FP32_TFLOPS = 157.3
+PEAK_HBM_GBS = 8000.0          # MI355X HBM3E
+STAGES = ["rope", "score", "select", "gather"]
+
+
+def parse():
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--config", default="c1")
+    ap.add_argument("--cpu-baseline-seconds", type=float, default=15.0,
+                    help="target CPU time of the oracle sample (0 disables it)")
+    ap.add_argument("--traffic-file", default=None,
+                    help="rocprofv3 FETCH_SIZE/WRITE_SIZE summary with a 'traffic_bytes' line")
+    return ap.parse_args()
+
+
+def gather_bytes(kept, k_max, D, esz, H, N):
+    """Algorithmic bytes of the gather: every kept (tile, head) slot requests one K row and one V
+    row plus its idx/newpos entries; Q is read and O written once."""
+    slots = kept.clamp(max=k_max).to(torch.int64).sum().item()
+    return slots * 2 * D * esz + slots * 8 + 2 * H * N * D * esz
+
+
+def read_traffic(path):
+    if not path or not os.path.exists(path):
+        return None
+    for line in open(path):
+        if line.startswith("traffic_bytes"):
+            return float(line.split(":", 1)[1].split()[0])
+    return None
+
+
+def cpu_baseline(cfg, q, k, v, invf, ps, rs, budget_s):
+    """The oracle (C port of the reference's three stages) on whole heads of the same workload."""
+    import numpy as np
+    from oracle import sta_oracle as orc
+    sm = 1.0 / math.sqrt(cfg.D)
+    threads = orc.num_threads()
+
+    def one(h):
+        qn, dt = orc.from_torch(q[0, h:h + 1])
+        kn, _ = orc.from_torch(k[0, h // (cfg.H // cfg.Hkv):h // (cfg.H // cfg.Hkv) + 1])
+        vn, _ = orc.from_torch(v[0, h // (cfg.H // cfg.Hkv):h // (cfg.H // cfg.Hkv) + 1])
+        t0 = time.perf_counter()
+        a = orc.select_vote(qn, kn, dt, np.full(1, cfg.tau, np.float32), invf.numpy(), ps, rs, sm, cfg.tile)
+        s = orc.build_sets(a["votes"], ps, cfg.n_global, cfg.n_local, cfg.pct, cfg.tile, cfg.k_max)
+        orc.gather_attn(qn, kn, vn, dt, s[0], s[1], s[2], invf.numpy(), rs, sm, cfg.tile, cfg.k_max)
+        return time.perf_counter() - t0
+
+    t_first = one(0)
+    heads = max(1, min(cfg.H, int(budget_s / max(t_first, 1e-3))))
+    total = t_first + sum(one(h) for h in range(1, heads))
+    per_head = total / heads
+    return {"value": round(cfg.N / (per_head * cfg.H), 3), "unit": "tokens/s", "cores": threads,
+            "kind": "port",
+            "sample": f"{heads} of {cfg.H} heads of the same workload through the CPU oracle "
+                      f"(Kernel A + _build_sets + Kernel C, {threads} OpenMP threads), scaled x{cfg.H / heads:g}"}
+
+
+def main():
+    args = parse()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}, WORLD_SIZE {world}); "
+              "heads would shard across GPUs with no exchange, which is not built here.",
+              file=sys.stderr)
+        return 2
+    global torch
+    import torch
+    import _sta_native as native
+    from synthetic import CONFIGS
+
+    cfg = CONFIGS[args.config]
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    q_cpu, k_cpu, v_cpu = cfg.inputs("cpu")
+    q, k, v = q_cpu.to(dev), k_cpu.to(dev), v_cpu.to(dev)
+    invf, ps, rs = cfg.geometry()
+    tau = torch.full((cfg.H,), cfg.tau)
+    plan = native.SharedPlan(q, k, v, tau, invf, ps, rs, invf, ps, rs, pct=cfg.pct, tile=cfg.tile,
+                             k_max=cfg.k_max, n_global=cfg.n_global, n_local=cfg.n_local)
+    stream = torch.cuda.current_stream(dev)
+    for _ in range(args.warmup):
+        plan.run()
+    torch.cuda.synchronize()
+    print(f"[bench] warmup done ({args.warmup} steps), timing {args.steps} steps", file=sys.stderr, flush=True)
+
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(5)] for _ in range(args.steps)]
+    for row in evs:                      # materialise the event handles outside the timed region
+        for e in row:
+            e.record(stream)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        plan.run(evs[i])
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    ms_per_step = elapsed * 1000.0 / args.steps
+    stage_ms = {s: sum(evs[i][j].elapsed_time(evs[i][j + 1]) for i in range(args.steps)) / args.steps
+                for j, s in enumerate(STAGES)}
+    r = plan.out
+    esz = q.element_size()
+    kept = r["kept_size"]
+    gbytes = gather_bytes(kept, cfg.k_max, cfg.D, esz, cfg.H, cfg.N)
+    score_tf = cfg.score_flops() / (stage_ms["score"] * 1e-3) / 1e12
+    gather_gbs = gbytes / (stage_ms["gather"] * 1e-3) / 1e9
+    peak_tf = PEAK_FP32_TFLOPS if q.dtype == torch.float32 else PEAK_BF16_TFLOPS
+    roof_score = {"kernel": "score_kernel (pass 1 + pass 2)", "bound": "mfma", "achieved": round(score_tf, 2),
+                  "peak": peak_tf, "unit": "TFLOP/s", "frac": round(score_tf / peak_tf, 4),
+                  "algorithmic_per_launch": cfg.score_flops(), "traffic": None}
+    roof_gather = {"kernel": "gather_kernel", "bound": "hbm", "achieved": round(gather_gbs, 1),
+                   "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(gather_gbs / PEAK_HBM_GBS, 4),
+                   "algorithmic_per_launch": int(gbytes), "traffic": None}
+    dominant = roof_score if stage_ms["score"] >= stage_ms["gather"] else roof_gather
+    dominant = dict(dominant)
+    dominant["traffic"] = read_traffic(args.traffic_file)
+    print(f"[bench] {ms_per_step:.3f} ms/step; stages {stage_ms}", file=sys.stderr, flush=True)
+
+    cpu = None
+    if args.cpu_baseline_seconds > 0:
+        print("[bench] timing the CPU oracle sample", file=sys.stderr, flush=True)
+        cpu = cpu_baseline(cfg, q_cpu, k_cpu, v_cpu, invf, ps, rs, args.cpu_baseline_seconds)
+
+    line = {
+        "metric": METRIC,
+        "value": round(cfg.N / (ms_per_step * 1e-3), 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": {torch.bfloat16: "bf16", torch.float16: "fp16", torch.float32: "fp32"}[q.dtype],
+        "data": "synthetic (seeded Gaussian Q/K/V with planted keys)",
+        "config": {"workload": cfg.name, "heads": cfg.H, "kv_heads": cfg.Hkv, "seq_len": cfg.N,
+                   "head_dim": cfg.D, "tile": cfg.tile, "tau": cfg.tau, "pct": cfg.pct, "k_max": cfg.k_max,
+                   "pos_scale": ps, "rope_scale": rs, "parallelism": "none (1 GPU)"},
+        "stages_ms": {s: round(t, 4) for s, t in stage_ms.items()},
+        "roofline": dominant,
+        "rooflines": {"score": roof_score, "gather": roof_gather},
+        "selection": {"kept_mean": round(kept.float().mean().item(), 1),
+                      "overflow20_tiles": int(r["overflow20"].sum().item()),
+                      "tiles": int(kept.numel())},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

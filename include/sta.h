@@ -1,0 +1,121 @@
+/*
+ * sta.h -- C ABI of libsta_hip.so: exact-max shared-selection thresholded attention (prefill)
+ * on AMD Instinct MI355X (gfx950).
+ *
+ * Plain C: device pointers, sizes and a HIP stream handle (passed as void*).  No framework
+ * types.  Every entry point is asynchronous on `stream`, performs no host synchronisation and no
+ * device allocation: the caller owns every output and passes one workspace buffer whose size
+ * comes from sta_shared_workspace_size().  Calls that share a workspace must not overlap.
+ *
+ * Geometry.  Kernel A (the two score passes) rotates queries and keys with the a-triple
+ * (inv_freq_a, pos_scale_a, rope_scale_a); the reposition and the gather-attention use the
+ * c-triple.  PI_exact and YaRN_exact pass the same triple twice; the hybrid file passes two.
+ *
+ * Tensor layout.  q is (H, N, D), k and v are (Hkv, N, D) with H % Hkv == 0 (kv head = h / (H /
+ * Hkv), which is what repeat_kv materialises in the reference).  Element strides per head and
+ * per token; the head_dim stride is 1; rows must be 16-byte aligned.  out is (H, N, D)
+ * contiguous in the input dtype.  Supported: D in {64, 128}, tile in {32, 64}.
+ *
+ * Return value: STA_OK or a negative STA_ERR_*; sta_last_error() describes the last failure on
+ * the calling thread.
+ */
+#ifndef STA_H_
+#define STA_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define STA_OK 0
+#define STA_ERR_INVALID_ARG (-1)
+#define STA_ERR_UNSUPPORTED (-2)
+#define STA_ERR_HIP (-3)
+#define STA_ERR_WORKSPACE (-4)
+
+#define STA_DTYPE_F32 0
+#define STA_DTYPE_BF16 1
+#define STA_DTYPE_F16 2
+
+typedef struct sta_shared_args {
+  /* inputs */
+  const void* q;
+  const void* k;
+  const void* v;
+  int64_t q_head_stride, q_tok_stride;
+  int64_t k_head_stride, k_tok_stride;
+  int64_t v_head_stride, v_tok_stride;
+  int32_t dtype;           /* STA_DTYPE_* of q, k, v and out */
+  int32_t H, Hkv, N, D;
+  const float* tau;        /* (H,) threshold below the exact row max */
+  const float* inv_freq_a; /* (D/2,) Kernel A geometry */
+  float pos_scale_a, rope_scale_a;
+  const float* inv_freq_c; /* (D/2,) reposition + attend geometry */
+  float pos_scale_c, rope_scale_c;
+  float sm_scale;
+  int32_t start_pct;       /* max(0, int(round(pct))) with round-half-even, as the reference */
+  int32_t n_global, n_local, tile, k_max, q_pos_base, measure;
+  /* outputs (device) */
+  void* out;               /* (H, N, D) */
+  int32_t* idx;            /* (H, nt, k_max) ascending kept key positions, sentinel N */
+  float* newpos_k;         /* (H, nt, k_max) repositioned key positions, 0 at sentinels */
+  float* newpos_q;         /* (H, nt, tile) repositioned query positions */
+  int32_t* shared_size;    /* (H, nt) |top-X% voted set| */
+  int32_t* kept_size;      /* (H, nt) |voted set U forced global/local| before truncation */
+  int32_t* chosen;         /* (H, nt) pct step that fit k_max, 0 if none */
+  uint8_t* orig_overflow;  /* (H, nt) the requested pct exceeded k_max */
+  int32_t* kpct_meas;      /* (H, nt) chosen, refined in 1% steps when measure != 0 */
+  uint8_t* overflow20;     /* (H, nt) still over k_max at the floor pct */
+  /* optional outputs (NULL to skip) */
+  int32_t* votes;          /* (H, nt, N) per-tile key occurrence counts */
+  int32_t* row_counts;     /* (H, N) kept keys per query (Kernel A's RowCounts) */
+  float* row_max;          /* (H, N) exact row max m of every query */
+  /* scratch */
+  void* workspace;
+  size_t workspace_bytes;
+  /* optional instrumentation: NULL, or 5 hipEvent_t handles that sta_shared_attention records
+   * on `stream` before the RoPE pre-kernels, before the score kernel, before selection, before
+   * the gather and after it (stage durations without a host sync) */
+  void* const* stage_events;
+} sta_shared_args;
+
+/* ABI version of this header (bumped on any layout change of sta_shared_args). */
+int sta_abi_version(void);
+
+/* Description of the last error returned on the calling thread ("" if none). */
+const char* sta_last_error(void);
+
+/* Bytes of device workspace the entry points below need for these arguments (shape fields). */
+size_t sta_shared_workspace_size(const sta_shared_args* args);
+
+/* The whole prefill path: RoPE remap, pass 1 (exact row max), pass 2 (threshold + votes),
+ * LDS selection (top-X% with the 30->25->20 fallback under k_max, compaction, reposition) and
+ * the sparse gather-attention.
+ * Replaces shared_pi_attention, shared_selection_triton_exact_2.py:432-486 (also
+ * shared_selection_triton_exact.py:376-423, shared_selection_triton_YaRN_exact.py:442-496 and,
+ * with two geometries, shared_selection_triton_hybrid_exact.py:450-510). */
+int sta_shared_attention(const sta_shared_args* args, void* stream);
+
+/* Kernel A alone: writes votes (required), row_counts and row_max (optional).
+ * Replaces the _select_vote_kernel launch, shared_selection_triton_exact_2.py:50-140, 454-465. */
+int sta_select_vote(const sta_shared_args* args, void* stream);
+
+/* _build_sets alone (freq ranking) from int32 votes (H, num_tiles, N) with values in [0, 255];
+ * writes idx, newpos_k, newpos_q and the six statistics, all with num_tiles tiles (the
+ * reference takes the tile count from the votes tensor, not from N).  Uses pos_scale_c,
+ * n_global, n_local, start_pct, tile, k_max, q_pos_base, measure.
+ * Replaces _build_sets, shared_selection_triton_exact_2.py:277-426. */
+int sta_build_sets(const sta_shared_args* args, const int32_t* votes, int32_t num_tiles, void* stream);
+
+/* Kernel C alone: gather + repositioned attention from idx / newpos_k / newpos_q under the
+ * c-geometry.  kept_size, when non-NULL, bounds the slots swept; otherwise all k_max slots are.
+ * Replaces the _gather_attn_kernel launch, shared_selection_triton_exact_2.py:146-225, 471-485. */
+int sta_gather_attention(const sta_shared_args* args, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* STA_H_ */

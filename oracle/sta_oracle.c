@@ -176,13 +176,14 @@ static inline float score_of(const float* a, const float* b, int D, float sm_sca
  * row_max    (H, N)     fp32 or NULL: the exact max m of each query (exact_2.py:88-103)
  * band       (H, nt, N) int32 or NULL: per key, # of the tile's queries whose score lies within
  *                       band_eps of that query's threshold m - tau (the parity tolerance band)
+ * band_rows  (H, N)     int32 or NULL: per query, # of its causal keys inside that band
  * keep_bits  (H, N, N)  uint8 or NULL: keep(q, k) for every pair (small shapes only)
  */
 void oracle_select_vote(const void* q, const void* k, int dtype, int H, int Hkv, int N, int D,
                         const float* tau, const float* inv_freq, float pos_scale, float rope_scale,
                         float sm_scale, int tile, int q_pos_base, int32_t* votes,
-                        int32_t* row_counts, float* row_max, int32_t* band, float band_eps,
-                        uint8_t* keep_bits) {
+                        int32_t* row_counts, float* row_max, int32_t* band, int32_t* band_rows,
+                        float band_eps, uint8_t* keep_bits) {
   const int T = tile;
   const int nt = (N + T - 1) / T;
   const int group = H / Hkv;
@@ -190,6 +191,7 @@ void oracle_select_vote(const void* q, const void* k, int dtype, int H, int Hkv,
   memset(votes, 0, sizeof(int32_t) * (size_t)H * nt * N);
   if (row_counts) memset(row_counts, 0, sizeof(int32_t) * (size_t)H * N);
   if (band) memset(band, 0, sizeof(int32_t) * (size_t)H * nt * N);
+  if (band_rows) memset(band_rows, 0, sizeof(int32_t) * (size_t)H * N);
   if (keep_bits) memset(keep_bits, 0, (size_t)H * N * N);
 
   /* rotated K per kv head (keys >= N are the zero rows the reference's masked loads produce) */
@@ -236,13 +238,15 @@ void oracle_select_vote(const void* q, const void* k, int dtype, int H, int Hkv,
         }
         if (row_max) row_max[(size_t)h * N + row] = m;
         volatile float thr = m - tau_h;
-        int cnt = 0;
+        int cnt = 0, nband = 0;
         for (int j = 0; j < hi; ++j) { /* pass 2, exact_2.py:107-125 */
           if (qpos < j) continue;
           const float s = srow[j];
           const int keep = s >= thr;
-          if (band && j < N && fabsf(s - thr) < band_eps)
-            band[((size_t)h * nt + t) * N + j] += 1;
+          if (fabsf(s - thr) < band_eps) {
+            nband += 1;
+            if (band && j < N) band[((size_t)h * nt + t) * N + j] += 1;
+          }
           if (!keep) continue;
           cnt += 1;
           if (j < N) {
@@ -252,6 +256,7 @@ void oracle_select_vote(const void* q, const void* k, int dtype, int H, int Hkv,
           }
         }
         if (row_counts) row_counts[(size_t)h * N + row] = cnt;
+        if (band_rows) band_rows[(size_t)h * N + row] = nband;
       }
     }
     free(qr);
@@ -449,7 +454,7 @@ void oracle_gather_attn(const void* q, const void* k, const void* v, int dtype, 
 #pragma omp parallel
   {
     float* qr = (float*)malloc(sizeof(float) * (size_t)D);
-    float* kr = (float*)malloc(sizeof(float) * (size_t)block_k * D);
+    float* kr = (float*)malloc(sizeof(float) * (size_t)k_max * D); /* rotated slots of one tile */
     float* sblk = (float*)malloc(sizeof(float) * (size_t)block_k);
     float* acc = (float*)malloc(sizeof(float) * (size_t)D);
     double* dotv = (double*)malloc(sizeof(double) * (size_t)D);
@@ -460,6 +465,12 @@ void oracle_gather_attn(const void* q, const void* k, const void* v, int dtype, 
       const int32_t* irow = idx + ((size_t)h * nt + t) * k_max;
       const float* nkrow = newpos_k + ((size_t)h * nt + t) * k_max;
       const float* nqrow = newpos_q + ((size_t)h * nt + t) * T;
+      /* K rotated at newpos_k once per slot (exact_2.py:199-207); shared by the tile's rows */
+      for (int s = 0; s < k_max; ++s) {
+        const int j = irow[s];
+        if (j < N) rope_row(k, dtype, ((size_t)hk * N + j) * D, D, nkrow[s], inv_freq, rope_scale,
+                            kr + (size_t)s * D);
+      }
       for (int r = 0; r < T; ++r) {
         const int row = t * T + r;
         if (row >= N) continue;
@@ -476,9 +487,7 @@ void oracle_gather_attn(const void* q, const void* k, const void* v, int dtype, 
             const int j = irow[s0 + b];
             if (j >= N) continue;           /* padding slot */
             if (qpos < j) continue;         /* causal on ORIGINAL positions (exact_2.py:210) */
-            rope_row(k, dtype, ((size_t)hk * N + j) * D, D, nkrow[s0 + b], inv_freq, rope_scale,
-                     kr + (size_t)b * D);
-            const float s = score_of(qr, kr + (size_t)b * D, D, sm_scale);
+            const float s = score_of(qr, kr + (size_t)(s0 + b) * D, D, sm_scale);
             sblk[b] = s;
             if (s > bmax) bmax = s;
           }

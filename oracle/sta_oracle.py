@@ -120,16 +120,18 @@ def select_vote(q, k, dtype, tau, inv_freq, pos_scale, rope_scale, sm_scale, til
     row_counts = np.empty((H, N), np.int32)
     row_max = np.empty((H, N), np.float32)
     band = np.empty((H, nt, N), np.int32) if want_band else None
+    band_rows = np.empty((H, N), np.int32) if want_band else None
     keep = np.empty((H, N, N), np.uint8) if want_keep else None
     lib().oracle_select_vote(
         _p(q), _p(k), ctypes.c_int(dtype), ctypes.c_int(H), ctypes.c_int(Hkv), ctypes.c_int(N),
         ctypes.c_int(D), _p(_c(tau, np.float32)), _p(_c(inv_freq, np.float32)),
         ctypes.c_float(pos_scale), ctypes.c_float(rope_scale), ctypes.c_float(sm_scale),
         ctypes.c_int(tile), ctypes.c_int(q_pos_base), _p(votes), _p(row_counts), _p(row_max),
-        _p(band), ctypes.c_float(band_eps), _p(keep))
+        _p(band), _p(band_rows), ctypes.c_float(band_eps), _p(keep))
     out = {"votes": votes, "row_counts": row_counts, "row_max": row_max}
     if want_band:
         out["band"] = band
+        out["band_rows"] = band_rows
     if want_keep:
         out["keep"] = keep
     return out

@@ -1,0 +1,296 @@
+"""ctypes binding of libsta_hip.so (the C ABI declared in include/sta.h).
+
+The library is built in-tree by build.py.  There is no other code path: if the library is
+missing, cannot be loaded, or the tensors are not on a HIP device, these functions raise.
+PyTorch is used only for device memory and the current stream.
+"""
+import ctypes
+import math
+import os
+
+import torch
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libsta_hip.so")
+_LIB = None
+
+STA_OK = 0
+DTYPES = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
+EXPORTS = ["sta_abi_version", "sta_last_error", "sta_shared_workspace_size", "sta_shared_attention",
+           "sta_select_vote", "sta_build_sets", "sta_gather_attention"]
+
+
+class ShareArgs(ctypes.Structure):
+    """Mirror of sta_shared_args (include/sta.h)."""
+    _fields_ = [
+        ("q", ctypes.c_void_p), ("k", ctypes.c_void_p), ("v", ctypes.c_void_p),
+        ("q_head_stride", ctypes.c_int64), ("q_tok_stride", ctypes.c_int64),
+        ("k_head_stride", ctypes.c_int64), ("k_tok_stride", ctypes.c_int64),
+        ("v_head_stride", ctypes.c_int64), ("v_tok_stride", ctypes.c_int64),
+        ("dtype", ctypes.c_int32), ("H", ctypes.c_int32), ("Hkv", ctypes.c_int32),
+        ("N", ctypes.c_int32), ("D", ctypes.c_int32),
+        ("tau", ctypes.c_void_p),
+        ("inv_freq_a", ctypes.c_void_p), ("pos_scale_a", ctypes.c_float), ("rope_scale_a", ctypes.c_float),
+        ("inv_freq_c", ctypes.c_void_p), ("pos_scale_c", ctypes.c_float), ("rope_scale_c", ctypes.c_float),
+        ("sm_scale", ctypes.c_float),
+        ("start_pct", ctypes.c_int32), ("n_global", ctypes.c_int32), ("n_local", ctypes.c_int32),
+        ("tile", ctypes.c_int32), ("k_max", ctypes.c_int32), ("q_pos_base", ctypes.c_int32),
+        ("measure", ctypes.c_int32),
+        ("out", ctypes.c_void_p), ("idx", ctypes.c_void_p), ("newpos_k", ctypes.c_void_p),
+        ("newpos_q", ctypes.c_void_p), ("shared_size", ctypes.c_void_p), ("kept_size", ctypes.c_void_p),
+        ("chosen", ctypes.c_void_p), ("orig_overflow", ctypes.c_void_p), ("kpct_meas", ctypes.c_void_p),
+        ("overflow20", ctypes.c_void_p),
+        ("votes", ctypes.c_void_p), ("row_counts", ctypes.c_void_p), ("row_max", ctypes.c_void_p),
+        ("workspace", ctypes.c_void_p), ("workspace_bytes", ctypes.c_size_t),
+        ("stage_events", ctypes.c_void_p),
+    ]
+
+
+def lib():
+    """Load libsta_hip.so once; raise loudly if it is absent."""
+    global _LIB
+    if _LIB is None:
+        if not os.path.exists(LIB_PATH):
+            raise ImportError(f"{LIB_PATH} is missing: build it with "
+                              f"`python sparse-thresholded-attention_amd/build.py`")
+        L = ctypes.CDLL(LIB_PATH)
+        L.sta_abi_version.restype = ctypes.c_int
+        L.sta_last_error.restype = ctypes.c_char_p
+        L.sta_shared_workspace_size.restype = ctypes.c_size_t
+        L.sta_shared_workspace_size.argtypes = [ctypes.POINTER(ShareArgs)]
+        for name in ("sta_shared_attention", "sta_select_vote", "sta_gather_attention"):
+            fn = getattr(L, name)
+            fn.restype = ctypes.c_int
+            fn.argtypes = [ctypes.POINTER(ShareArgs), ctypes.c_void_p]
+        L.sta_build_sets.restype = ctypes.c_int
+        L.sta_build_sets.argtypes = [ctypes.POINTER(ShareArgs), ctypes.c_void_p, ctypes.c_int32,
+                                     ctypes.c_void_p]
+        if L.sta_abi_version() != 1:
+            raise ImportError("libsta_hip.so ABI version mismatch")
+        _LIB = L
+    return _LIB
+
+
+def _check(rc, what):
+    if rc != STA_OK:
+        msg = lib().sta_last_error().decode(errors="replace")
+        raise RuntimeError(f"{what} failed ({rc}): {msg}")
+
+
+def _ptr(t):
+    return ctypes.c_void_p(t.data_ptr()) if t is not None else None
+
+
+def _heads_view(x):
+    """(1, H, N, D) or (H, N, D) -> (H, N, D) view with unit dim stride and 16-byte rows."""
+    if x.dim() == 4:
+        assert x.shape[0] == 1, "batch size must be 1"
+        x = x[0]
+    esz = x.element_size()
+    if (x.stride(2) != 1 or (x.stride(0) * esz) % 16 or (x.stride(1) * esz) % 16
+            or x.data_ptr() % 16):
+        x = x.contiguous()
+    return x
+
+
+def _stream(dev):
+    return ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+
+
+def start_pct_of(pct):
+    """max(0, int(round(pct))) with Python's round-half-even (exact_2.py:309)."""
+    return max(0, int(round(pct)))
+
+
+def _fill_common(a, q, k, v, tau, inv_freq_a, pos_scale_a, rope_scale_a, inv_freq_c, pos_scale_c,
+                 rope_scale_c, sm_scale, pct, n_global, n_local, tile, k_max, q_pos_base, measure):
+    H, N, D = q.shape
+    a.q, a.k = _ptr(q), _ptr(k)
+    a.v = _ptr(v) if v is not None else None
+    a.q_head_stride, a.q_tok_stride = q.stride(0), q.stride(1)
+    a.k_head_stride, a.k_tok_stride = k.stride(0), k.stride(1)
+    if v is not None:
+        a.v_head_stride, a.v_tok_stride = v.stride(0), v.stride(1)
+    a.dtype = DTYPES[q.dtype]
+    a.H, a.Hkv, a.N, a.D = H, k.shape[0], N, D
+    a.tau = _ptr(tau)
+    a.inv_freq_a, a.pos_scale_a, a.rope_scale_a = _ptr(inv_freq_a), float(pos_scale_a), float(rope_scale_a)
+    a.inv_freq_c, a.pos_scale_c, a.rope_scale_c = _ptr(inv_freq_c), float(pos_scale_c), float(rope_scale_c)
+    a.sm_scale = float(sm_scale)
+    a.start_pct = start_pct_of(pct)
+    a.n_global, a.n_local, a.tile, a.k_max = int(n_global), int(n_local), int(tile), int(k_max)
+    a.q_pos_base, a.measure = int(q_pos_base), int(bool(measure))
+
+
+def _prep_inputs(q, k, v, tau, inv_freq_a, inv_freq_c):
+    if not q.is_cuda:
+        raise RuntimeError("sparse-thresholded attention runs on a HIP device only; got a CPU tensor")
+    if q.dtype not in DTYPES:
+        raise TypeError(f"unsupported dtype {q.dtype}")
+    dev = q.device
+    qh = _heads_view(q)
+    kh = _heads_view(k.to(dev))
+    vh = _heads_view(v.to(dev)) if v is not None else None
+    if kh.dtype != qh.dtype or (vh is not None and vh.dtype != qh.dtype):
+        raise TypeError("q, k and v must share one dtype")
+    tau = tau.to(device=dev, dtype=torch.float32).contiguous()
+    ifa = inv_freq_a.to(device=dev, dtype=torch.float32).contiguous()
+    ifc = inv_freq_c.to(device=dev, dtype=torch.float32).contiguous() if inv_freq_c is not None else ifa
+    return qh, kh, vh, tau, ifa, ifc
+
+
+def _workspace(a, dev):
+    n = lib().sta_shared_workspace_size(ctypes.byref(a))
+    if n == 0:
+        _check(-1, "sta_shared_workspace_size")
+    ws = torch.empty(n, dtype=torch.uint8, device=dev)
+    assert ws.data_ptr() % 256 == 0
+    a.workspace, a.workspace_bytes = _ptr(ws), n
+    return ws
+
+
+class SharedPlan:
+    """Outputs and workspace for one shape, allocated once; run() launches the whole prefill path
+    on the current stream and allocates nothing.  Successive runs overwrite the outputs."""
+
+    def __init__(self, q, k, v, tau, inv_freq_a, pos_scale_a, rope_scale_a, inv_freq_c, pos_scale_c,
+                 rope_scale_c, pct=30.0, sm_scale=None, n_global=32, n_local=32, tile=32,
+                 k_max=1024, q_pos_base=0, measure=False, want_votes=False, want_row_max=False,
+                 want_row_counts=False):
+        qh, kh, vh, tau, ifa, ifc = _prep_inputs(q, k, v, tau, inv_freq_a, inv_freq_c)
+        H, N, D = qh.shape
+        self.device = qh.device
+        if sm_scale is None:
+            sm_scale = 1.0 / math.sqrt(D)
+        self.args = a = ShareArgs()
+        _fill_common(a, qh, kh, vh, tau, ifa, pos_scale_a, rope_scale_a, ifc, pos_scale_c, rope_scale_c,
+                     sm_scale, pct, n_global, n_local, tile, k_max, q_pos_base, measure)
+        self._keep = (qh, kh, vh, tau, ifa, ifc)
+        self.out = _alloc_outputs(a, H, N, D, qh.dtype, tile, k_max, self.device, want_votes,
+                                  want_row_max, want_row_counts)
+        self.workspace = _workspace(a, self.device)
+        self._events = None
+
+    def run(self, events=None):
+        """events: None or 5 recorded torch.cuda.Event(enable_timing=True) marking the stages."""
+        if events is not None:
+            self._events = (ctypes.c_void_p * 5)(*[e.cuda_event for e in events])
+            self.args.stage_events = ctypes.cast(self._events, ctypes.c_void_p)
+        else:
+            self.args.stage_events = None
+        _check(lib().sta_shared_attention(ctypes.byref(self.args), _stream(self.device)),
+               "sta_shared_attention")
+        return self.out
+
+
+def _alloc_outputs(a, H, N, D, dtype, tile, k_max, dev, want_votes, want_row_max, want_row_counts):
+    nt = (N + tile - 1) // tile
+    r = {
+        "out": torch.empty((H, N, D), dtype=dtype, device=dev),
+        "idx": torch.empty((H, nt, k_max), dtype=torch.int32, device=dev),
+        "newpos_k": torch.empty((H, nt, k_max), dtype=torch.float32, device=dev),
+        "newpos_q": torch.empty((H, nt, tile), dtype=torch.float32, device=dev),
+        "shared_size": torch.empty((H, nt), dtype=torch.int32, device=dev),
+        "kept_size": torch.empty((H, nt), dtype=torch.int32, device=dev),
+        "chosen": torch.empty((H, nt), dtype=torch.int32, device=dev),
+        "orig_overflow": torch.empty((H, nt), dtype=torch.bool, device=dev),
+        "kpct_meas": torch.empty((H, nt), dtype=torch.int32, device=dev),
+        "overflow20": torch.empty((H, nt), dtype=torch.bool, device=dev),
+    }
+    if want_votes:
+        r["votes"] = torch.empty((H, nt, N), dtype=torch.int32, device=dev)
+    if want_row_max:
+        r["row_max"] = torch.empty((H, N), dtype=torch.float32, device=dev)
+    if want_row_counts:
+        r["row_counts"] = torch.empty((H, N), dtype=torch.int32, device=dev)
+    for name in ("out", "idx", "newpos_k", "newpos_q", "shared_size", "kept_size", "chosen",
+                 "orig_overflow", "kpct_meas", "overflow20"):
+        setattr(a, name, _ptr(r[name]))
+    a.votes = _ptr(r.get("votes"))
+    a.row_max = _ptr(r.get("row_max"))
+    a.row_counts = _ptr(r.get("row_counts"))
+    return r
+
+
+def shared_attention(q, k, v, tau, inv_freq_a, pos_scale_a, rope_scale_a, inv_freq_c, pos_scale_c,
+                     rope_scale_c, pct=30.0, sm_scale=None, n_global=32, n_local=32, tile=32,
+                     k_max=1024, q_pos_base=0, measure=False, want_votes=False, want_row_max=False,
+                     want_row_counts=False):
+    """Run the whole prefill path on the device.  q (1,H,N,D) / k, v (1,Hkv,N,D).
+    Returns a dict of device tensors (see include/sta.h for their meaning).  The workspace is
+    released on return; the caching allocator hands it out again only to work queued later on
+    the same stream."""
+    plan = SharedPlan(q, k, v, tau, inv_freq_a, pos_scale_a, rope_scale_a, inv_freq_c, pos_scale_c,
+                      rope_scale_c, pct, sm_scale, n_global, n_local, tile, k_max, q_pos_base, measure,
+                      want_votes, want_row_max, want_row_counts)
+    return plan.run()
+
+
+def select_vote(q, k, tau, inv_freq, pos_scale, rope_scale, sm_scale, tile, q_pos_base=0,
+                want_row_counts=True):
+    """Kernel A alone: votes (H,nt,N) int32, row_counts (H,N) int32, row_max (H,N) fp32."""
+    qh, kh, _, tau, ifa, _ = _prep_inputs(q, k, None, tau, inv_freq, None)
+    H, N, D = qh.shape
+    dev = qh.device
+    nt = (N + tile - 1) // tile
+    a = ShareArgs()
+    _fill_common(a, qh, kh, None, tau, ifa, pos_scale, rope_scale, ifa, pos_scale, rope_scale,
+                 sm_scale, 30.0, 0, 0, tile, 1, q_pos_base, False)
+    votes = torch.empty((H, nt, N), dtype=torch.int32, device=dev)
+    rc = torch.empty((H, N), dtype=torch.int32, device=dev) if want_row_counts else None
+    rm = torch.empty((H, N), dtype=torch.float32, device=dev)
+    a.votes, a.row_counts, a.row_max = _ptr(votes), _ptr(rc), _ptr(rm)
+    ws = _workspace(a, dev)
+    _check(lib().sta_select_vote(ctypes.byref(a), _stream(dev)), "sta_select_vote")
+    del ws
+    return votes, rc, rm
+
+
+def build_sets(votes, pos_scale, n_global, n_local, pct, T, k_max, q_pos_base=0, measure=False):
+    """_build_sets on the device from int32 votes (H, nt, N).  Returns the reference's 9-tuple
+    (exact_2.py:418-426) with shared_size / kept_size as int64 like the reference's sums."""
+    if not votes.is_cuda:
+        raise RuntimeError("build_sets runs on a HIP device only; got a CPU tensor")
+    votes = votes.to(torch.int32).contiguous()
+    H, nt, N = votes.shape
+    dev = votes.device
+    a = ShareArgs()
+    a.dtype, a.H, a.Hkv, a.N, a.D = 1, H, H, N, 64
+    a.pos_scale_c = float(pos_scale)
+    a.start_pct = start_pct_of(pct)
+    a.n_global, a.n_local, a.tile, a.k_max = int(n_global), int(n_local), int(T), int(k_max)
+    a.q_pos_base, a.measure = int(q_pos_base), int(bool(measure))
+    idx = torch.empty((H, nt, k_max), dtype=torch.int32, device=dev)
+    npk = torch.empty((H, nt, k_max), dtype=torch.float32, device=dev)
+    npq = torch.empty((H, nt, T), dtype=torch.float32, device=dev)
+    ss = torch.empty((H, nt), dtype=torch.int32, device=dev)
+    ks = torch.empty((H, nt), dtype=torch.int32, device=dev)
+    ch = torch.empty((H, nt), dtype=torch.int32, device=dev)
+    oo = torch.empty((H, nt), dtype=torch.bool, device=dev)
+    km = torch.empty((H, nt), dtype=torch.int32, device=dev)
+    o20 = torch.empty((H, nt), dtype=torch.bool, device=dev)
+    a.idx, a.newpos_k, a.newpos_q = _ptr(idx), _ptr(npk), _ptr(npq)
+    a.shared_size, a.kept_size, a.chosen = _ptr(ss), _ptr(ks), _ptr(ch)
+    a.orig_overflow, a.kpct_meas, a.overflow20 = _ptr(oo), _ptr(km), _ptr(o20)
+    _check(lib().sta_build_sets(ctypes.byref(a), _ptr(votes), nt, _stream(dev)), "sta_build_sets")
+    return idx, npk, npq, ss.long(), ks.long(), ch, oo, km, o20
+
+
+def gather_attention(q, k, v, inv_freq, idx, newpos_k, newpos_q, sm_scale, rope_scale, tile, k_max,
+                     q_pos_base=0, kept_size=None):
+    """Kernel C alone.  Returns out (H, N, D) in q.dtype."""
+    qh, kh, vh, _, ifc, _ = _prep_inputs(q, k, v, torch.zeros(1), inv_freq, None)
+    H, N, D = qh.shape
+    dev = qh.device
+    a = ShareArgs()
+    _fill_common(a, qh, kh, vh, torch.zeros(1, device=dev), ifc, 1.0, rope_scale, ifc, 1.0, rope_scale,
+                 sm_scale, 30.0, 0, 0, tile, k_max, q_pos_base, False)
+    out = torch.empty((H, N, D), dtype=qh.dtype, device=dev)
+    idx = idx.to(device=dev, dtype=torch.int32).contiguous()
+    newpos_k = newpos_k.to(device=dev, dtype=torch.float32).contiguous()
+    newpos_q = newpos_q.to(device=dev, dtype=torch.float32).contiguous()
+    a.out, a.idx, a.newpos_k, a.newpos_q = _ptr(out), _ptr(idx), _ptr(newpos_k), _ptr(newpos_q)
+    ks = kept_size.to(device=dev, dtype=torch.int32).contiguous() if kept_size is not None else None
+    a.kept_size = _ptr(ks)
+    _check(lib().sta_gather_attention(ctypes.byref(a), _stream(dev)), "sta_gather_attention")
+    return out

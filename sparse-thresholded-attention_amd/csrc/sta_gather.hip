@@ -1,0 +1,335 @@
+// sta_gather.hip -- gather + repositioned attention over the selected keys (Kernel C).
+//
+// Reference: shared_selection_triton_exact_2.py:146-225 (_gather_attn_kernel).  Per (head,
+// tile): rotate Q at newpos_q, then for 64-slot blocks gather the selected K and V rows, rotate
+// K at newpos_k, mask causally on ORIGINAL positions (exact_2.py:210), run the -inf-safe online
+// softmax (213-217) and accumulate P.V with P cast to the input dtype (220).  The reference
+// always sweeps all k_max slots; slots past min(kept_size, k_max) are sentinels that contribute
+// exactly nothing to the online softmax, so they are skipped.
+//
+// One workgroup per (head, tile); wave w owns query rows 16w .. 16w+15.  Scores are computed
+// transposed, S^T = K_rot . Q_rot^T (16x16x32 MFMA, lane <-> query row), so the P fragment the
+// P.V product needs as its B operand is exactly the score accumulator the lane already holds:
+//   O^T (dims x rows) += V^T (dims x slots) . P^T (slots x rows)
+// with the contraction order over slots permuted identically in V^T and P^T.  V is written to
+// LDS transposed (dim-major) once per block.  K rows arrive row-major (256 B per row at d128 bf16,
+// 16-byte loads), are rotated in fp32 and stored to LDS as bf16.
+#include "sta_device.h"
+#include "sta_kernels.h"
+
+namespace sta {
+
+template <int DT, int D, int NW>
+struct GatherCfg {
+  static constexpr int NT = NW * 64;           // threads
+  static constexpr int TPS = NT / 64;          // threads per slot for the K rotation
+  static constexpr int FP = (D / 2) / TPS;     // frequencies per thread
+  static constexpr bool X3 = (DT == DT_F32);   // fp32 inputs: three-term bf16 products
+  static constexpr int KSTR = D + 8;           // K LDS row stride (bf16 elements)
+  static constexpr int VSTR = 64 + 8;          // V^T LDS row stride (elements)
+  static constexpr int KHALVES = X3 ? 2 : 1;
+  static constexpr size_t LDS = (size_t)KHALVES * 64 * KSTR * 2 + (size_t)KHALVES * D * VSTR * 2;
+};
+
+template <int DT, int D, int NW>
+__global__ __launch_bounds__(NW * 64) void gather_kernel(GatherArgs a) {
+  using Cfg = GatherCfg<DT, D, NW>;
+  constexpr int NT = Cfg::NT, TPS = Cfg::TPS, FP = Cfg::FP;
+  constexpr bool X3 = Cfg::X3;
+  constexpr int KSTR = Cfg::KSTR, VSTR = Cfg::VSTR;
+  constexpr int T = NW * 16;
+  constexpr int KS = D / 32;                   // k steps of the score MFMA
+  constexpr int DB = D / 16;                   // 16-dim blocks of the output
+  extern __shared__ __align__(16) uint16_t sh[];
+  uint16_t* kr_hi = sh;                                    // [64][KSTR]
+  uint16_t* kr_lo = sh + 64 * KSTR;                        // [64][KSTR] (X3 only)
+  uint16_t* vt_hi = sh + Cfg::KHALVES * 64 * KSTR;         // [D][VSTR]
+  uint16_t* vt_lo = vt_hi + D * VSTR;                      // [D][VSTR] (X3 only)
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  int h, t;
+  {
+    const int bid = blockIdx.x;
+    if ((a.H & 7) == 0) {
+      const int hpx = a.H >> 3;
+      const int r = bid >> 3;
+      h = (bid & 7) * hpx + r % hpx;
+      t = a.nt - 1 - r / hpx;
+    } else {
+      h = bid % a.H;
+      t = a.nt - 1 - bid / a.H;
+    }
+  }
+  const int kvh = h / (a.H / a.Hkv);
+  const int N = a.N;
+  const float rs = a.rope_scale;
+  const float* invf = a.inv_freq;
+
+  // ---- this lane's query row, rotated at newpos_q (exact_2.py:174-185) ----
+  const int r = wave * 16 + (lane & 15);
+  const int qrow = t * T + r;
+  const bool row_ok = qrow < N;
+  const int64_t qpos = (int64_t)a.q_pos_base + qrow;
+  u32x4 qf_hi[KS], qf_lo[KS];
+  {
+    const float npq = a.newpos_q[((int64_t)h * a.nt + t) * T + r];
+    const int64_t qb = (int64_t)h * a.q_head_stride + (int64_t)qrow * a.q_tok_stride;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      const int d0 = ks * 32 + 8 * (lane >> 4);
+      float own[8], other[8], out[8];
+      const bool first = d0 < D / 2;
+      const int i0 = first ? d0 : d0 - D / 2;
+      if (row_ok) {
+        load8<DT>(a.q, qb + d0, own);
+        load8<DT>(a.q, qb + (first ? d0 + D / 2 : d0 - D / 2), other);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) { own[e] = 0.0f; other[e] = 0.0f; }
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        float sn, cs;
+        fast_sincos(npq * invf[i0 + e], sn, cs);
+        cs *= rs;
+        sn *= rs;
+        out[e] = first ? own[e] * cs - other[e] * sn : own[e] * cs + other[e] * sn;
+      }
+      if constexpr (X3) split_bf16x8(out, qf_hi[ks], qf_lo[ks]);
+      else qf_hi[ks] = pack_bf16x8(out);
+    }
+  }
+
+  floatx4 oacc[DB];
+#pragma unroll
+  for (int db = 0; db < DB; ++db) oacc[db] = floatx4{0.f, 0.f, 0.f, 0.f};
+  float mR = -INFINITY, l_i = 0.0f;
+
+  const int64_t tile_off = ((int64_t)h * a.nt + t) * a.k_max;
+  const int32_t* idx = a.idx + tile_off;
+  const float* npk = a.newpos_k + tile_off;
+  const int nvalid = a.kept_size ? min(a.kept_size[h * a.nt + t], a.k_max) : a.k_max;
+  const int nblk = (nvalid + 63) / 64;
+  const int64_t kbase = (int64_t)kvh * a.k_head_stride;
+  const int64_t vbase = (int64_t)kvh * a.v_head_stride;
+
+  for (int b = 0; b < nblk; ++b) {
+    const int s0 = b * 64;
+    // ---- K rows: gather, rotate at newpos_k (exact_2.py:193-207), store bf16 to LDS ----
+    {
+      const int slot = tid / TPS, part = tid % TPS;
+      const int s = s0 + slot;
+      const int j = s < a.k_max ? idx[s] : N;
+      float x1[FP], x2[FP], o1[FP], o2[FP];
+      if ((unsigned)j < (unsigned)N) {  // sentinel N (and any out-of-range index) -> zero row
+        const int64_t rb = kbase + (int64_t)j * a.k_tok_stride + part * FP;
+#pragma unroll
+        for (int c = 0; c < FP / 8; ++c) {
+          load8<DT>(a.k, rb + 8 * c, x1 + 8 * c);
+          load8<DT>(a.k, rb + D / 2 + 8 * c, x2 + 8 * c);
+        }
+        const float np = npk[s];
+#pragma unroll
+        for (int e = 0; e < FP; ++e) {
+          float sn, cs;
+          fast_sincos(np * invf[part * FP + e], sn, cs);
+          cs *= rs;
+          sn *= rs;
+          o1[e] = x1[e] * cs - x2[e] * sn;
+          o2[e] = x2[e] * cs + x1[e] * sn;
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < FP; ++e) { o1[e] = 0.0f; o2[e] = 0.0f; }
+      }
+#pragma unroll
+      for (int c = 0; c < FP / 8; ++c) {
+        u32x4* d1 = (u32x4*)(kr_hi + slot * KSTR + part * FP + 8 * c);
+        u32x4* d2 = (u32x4*)(kr_hi + slot * KSTR + D / 2 + part * FP + 8 * c);
+        if constexpr (X3) {
+          u32x4 h1, l1, h2, l2;
+          split_bf16x8(o1 + 8 * c, h1, l1);
+          split_bf16x8(o2 + 8 * c, h2, l2);
+          *d1 = h1;
+          *d2 = h2;
+          *(u32x4*)(kr_lo + slot * KSTR + part * FP + 8 * c) = l1;
+          *(u32x4*)(kr_lo + slot * KSTR + D / 2 + part * FP + 8 * c) = l2;
+        } else {
+          *d1 = pack_bf16x8(o1 + 8 * c);
+          *d2 = pack_bf16x8(o2 + 8 * c);
+        }
+      }
+    }
+    // ---- V rows: gather 4 slots x 8 dims per unit, store transposed (dim-major) ----
+    for (int u = tid; u < 16 * (D / 8); u += NT) {
+      const int sg = u / (D / 8), dc = u % (D / 8);
+      float vv[4][8];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int s = s0 + sg * 4 + k;
+        const int j = s < a.k_max ? idx[s] : N;
+        if ((unsigned)j < (unsigned)N) {
+          load8<DT>(a.v, vbase + (int64_t)j * a.v_tok_stride + dc * 8, vv[k]);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) vv[k][e] = 0.0f;
+        }
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        float col[4] = {vv[0][e], vv[1][e], vv[2][e], vv[3][e]};
+        u32x2 w;
+        if constexpr (DT == DT_F16) {
+          w[0] = f32_to_f16_bits(col[0]) | (f32_to_f16_bits(col[1]) << 16);
+          w[1] = f32_to_f16_bits(col[2]) | (f32_to_f16_bits(col[3]) << 16);
+        } else {
+          w[0] = f32_to_bf16_bits(col[0]) | (f32_to_bf16_bits(col[1]) << 16);
+          w[1] = f32_to_bf16_bits(col[2]) | (f32_to_bf16_bits(col[3]) << 16);
+        }
+        *(u32x2*)(vt_hi + (dc * 8 + e) * VSTR + sg * 4) = w;
+        if constexpr (X3) {
+          u32x2 wl;
+          float lo[4];
+#pragma unroll
+          for (int k = 0; k < 4; ++k) lo[k] = col[k] - bf16_bits_to_f32(f32_to_bf16_bits(col[k]));
+          wl[0] = f32_to_bf16_bits(lo[0]) | (f32_to_bf16_bits(lo[1]) << 16);
+          wl[1] = f32_to_bf16_bits(lo[2]) | (f32_to_bf16_bits(lo[3]) << 16);
+          *(u32x2*)(vt_lo + (dc * 8 + e) * VSTR + sg * 4) = wl;
+        }
+      }
+    }
+    __syncthreads();
+
+    // ---- S^T = K_rot . Q_rot^T for 64 slots x this wave's 16 rows ----
+    floatx4 sacc[4];
+#pragma unroll
+    for (int sb = 0; sb < 4; ++sb) {
+      sacc[sb] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        const int off = (sb * 16 + (lane & 15)) * KSTR + ks * 32 + 8 * (lane >> 4);
+        const u32x4 kh = *(const u32x4*)(kr_hi + off);
+        if constexpr (X3) {
+          const u32x4 kl = *(const u32x4*)(kr_lo + off);
+          sacc[sb] = mfma16(kl, qf_hi[ks], sacc[sb]);
+          sacc[sb] = mfma16(kh, qf_lo[ks], sacc[sb]);
+        }
+        sacc[sb] = mfma16(kh, qf_hi[ks], sacc[sb]);
+      }
+    }
+    // ---- mask + online softmax (exact_2.py:209-217) ----
+    float p[4][4];
+    float bmax = -INFINITY;
+#pragma unroll
+    for (int sb = 0; sb < 4; ++sb) {
+      const int sl = s0 + sb * 16 + 4 * (lane >> 4);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int s = sl + i;
+        const int j = s < a.k_max ? idx[s] : N;
+        const bool keep = ((unsigned)j < (unsigned)N) && (qpos >= j);
+        const float v = keep ? sacc[sb][i] * a.sm_scale : -INFINITY;
+        p[sb][i] = v;
+        bmax = fmaxf(bmax, v);
+      }
+    }
+    bmax = fmaxf(bmax, __shfl_xor(bmax, 16, 64));
+    bmax = fmaxf(bmax, __shfl_xor(bmax, 32, 64));
+    const float mnew = fmaxf(mR, bmax);
+    const float msafe = (mnew == -INFINITY) ? 0.0f : mnew;
+    const float alpha = __expf(mR - msafe);
+    float psum = 0.0f;
+#pragma unroll
+    for (int sb = 0; sb < 4; ++sb)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        p[sb][i] = __expf(p[sb][i] - msafe);
+        psum += p[sb][i];
+      }
+    psum += __shfl_xor(psum, 16, 64);
+    psum += __shfl_xor(psum, 32, 64);
+    l_i = l_i * alpha + psum;
+    mR = mnew;
+#pragma unroll
+    for (int db = 0; db < DB; ++db) oacc[db] *= alpha;
+
+    // ---- O^T += V^T . P^T (exact_2.py:218-220) ----
+#pragma unroll
+    for (int k2 = 0; k2 < 2; ++k2) {
+      const int sb0 = 2 * k2, sb1 = 2 * k2 + 1;
+      float pv[8] = {p[sb0][0], p[sb0][1], p[sb0][2], p[sb0][3], p[sb1][0], p[sb1][1], p[sb1][2], p[sb1][3]};
+      u32x4 pb, pbl;
+      if constexpr (DT == DT_F16) pb = pack_f16x8(pv);
+      else if constexpr (X3) split_bf16x8(pv, pb, pbl);
+      else pb = pack_bf16x8(pv);
+#pragma unroll
+      for (int db = 0; db < DB; ++db) {
+        const int row = db * 16 + (lane & 15);
+        const int c0 = sb0 * 16 + 4 * (lane >> 4), c1 = sb1 * 16 + 4 * (lane >> 4);
+        const u32x2 a0 = *(const u32x2*)(vt_hi + row * VSTR + c0);
+        const u32x2 a1 = *(const u32x2*)(vt_hi + row * VSTR + c1);
+        const u32x4 va = u32x4{a0[0], a0[1], a1[0], a1[1]};
+        if constexpr (DT == DT_F16) {
+          oacc[db] = mfma16_f16(va, pb, oacc[db]);
+        } else if constexpr (X3) {
+          const u32x2 b0 = *(const u32x2*)(vt_lo + row * VSTR + c0);
+          const u32x2 b1 = *(const u32x2*)(vt_lo + row * VSTR + c1);
+          const u32x4 vl = u32x4{b0[0], b0[1], b1[0], b1[1]};
+          oacc[db] = mfma16(vl, pb, oacc[db]);
+          oacc[db] = mfma16(va, pbl, oacc[db]);
+          oacc[db] = mfma16(va, pb, oacc[db]);
+        } else {
+          oacc[db] = mfma16(va, pb, oacc[db]);
+        }
+      }
+    }
+    __syncthreads();
+  }
+
+  // ---- out = acc / l (exact_2.py:223-225) ----
+  if (row_ok) {
+    const int64_t ob = ((int64_t)h * N + qrow) * D;
+#pragma unroll
+    for (int db = 0; db < DB; ++db) {
+      const int d0 = db * 16 + 4 * (lane >> 4);
+      float o[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) o[i] = oacc[db][i] / l_i;
+      if constexpr (DT == DT_F32) {
+        *(float4*)((float*)a.out + ob + d0) = make_float4(o[0], o[1], o[2], o[3]);
+      } else if constexpr (DT == DT_BF16) {
+        u32x2 w;
+        w[0] = f32_to_bf16_bits(o[0]) | (f32_to_bf16_bits(o[1]) << 16);
+        w[1] = f32_to_bf16_bits(o[2]) | (f32_to_bf16_bits(o[3]) << 16);
+        *(u32x2*)((uint16_t*)a.out + ob + d0) = w;
+      } else {
+        u32x2 w;
+        w[0] = f32_to_f16_bits(o[0]) | (f32_to_f16_bits(o[1]) << 16);
+        w[1] = f32_to_f16_bits(o[2]) | (f32_to_f16_bits(o[3]) << 16);
+        *(u32x2*)((uint16_t*)a.out + ob + d0) = w;
+      }
+    }
+  }
+}
+
+template <int DT, int D, int NW>
+static hipError_t launch_gather_t(const GatherArgs& a, hipStream_t st) {
+  using Cfg = GatherCfg<DT, D, NW>;
+  hipError_t e = hipFuncSetAttribute((const void*)gather_kernel<DT, D, NW>,
+                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)Cfg::LDS);
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL((gather_kernel<DT, D, NW>), dim3(a.H * a.nt), dim3(Cfg::NT), Cfg::LDS, st, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_gather(int dtype, int D, int tile, const GatherArgs& a, hipStream_t st) {
+#define STA_G(DT_, D_, NW_) \
+  if (dtype == DT_ && D == D_ && tile == NW_ * 16) return launch_gather_t<DT_, D_, NW_>(a, st);
+  STA_G(DT_F32, 64, 2) STA_G(DT_F32, 64, 4) STA_G(DT_F32, 128, 2) STA_G(DT_F32, 128, 4)
+  STA_G(DT_BF16, 64, 2) STA_G(DT_BF16, 64, 4) STA_G(DT_BF16, 128, 2) STA_G(DT_BF16, 128, 4)
+  STA_G(DT_F16, 64, 2) STA_G(DT_F16, 64, 4) STA_G(DT_F16, 128, 2) STA_G(DT_F16, 128, 4)
+#undef STA_G
+  return hipErrorInvalidValue;
+}
+
+}  // namespace sta

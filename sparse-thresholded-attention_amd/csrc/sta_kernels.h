@@ -1,0 +1,70 @@
+// sta_kernels.h -- internal argument blocks and launchers of the gfx950 kernels.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include "sta_device.h"
+
+namespace sta {
+
+struct ScoreArgs {
+  const u32x4* qfrag;     // selection-geometry Q fragments (hi/lo), rows padded to nt*tile
+  const u32x4* kfrag;     // selection-geometry K fragments (hi/lo), rows padded to k_rows_pad
+  int H, Hkv, N, nt;
+  int q_rows_pad, k_rows_pad;
+  int q_pos_base;
+  const float* tau;       // (H,)
+  float sm_scale;
+  uint8_t* votes;         // (H, nt, votes_stride): keys < min(N, hi_t) written
+  int64_t votes_stride;
+  float* row_max;         // (H, N) or null
+  int32_t* row_counts;    // (H, N) or null
+};
+
+struct SelectArgs {
+  const void* votes;      // uint8 or int32 (H, nt, votes_stride), values in [0, 255]
+  int64_t votes_stride;
+  int votes_dense;        // 1: all N votes are valid; 0: keys >= min(N, tile end) are zero
+  int H, nt, N, T, k_max, q_pos_base, n_global, n_local;
+  float pos_scale;
+  int nsteps;
+  int steps[3];
+  int64_t K_ord;
+  int start_pct, measure;
+  int32_t* idx;
+  float* newpos_k;
+  float* newpos_q;
+  int32_t* shared_size;
+  int32_t* kept_size;
+  int32_t* chosen;
+  uint8_t* orig_overflow;
+  int32_t* kpct_meas;
+  uint8_t* overflow20;
+  int32_t* votes_out;     // optional dense int32 copy (H, nt, N)
+};
+
+struct GatherArgs {
+  const void* q;
+  const void* k;
+  const void* v;
+  int64_t q_head_stride, q_tok_stride, k_head_stride, k_tok_stride, v_head_stride, v_tok_stride;
+  int H, Hkv, N, nt, k_max, q_pos_base;
+  const float* inv_freq;
+  float rope_scale, sm_scale;
+  const int32_t* idx;
+  const float* newpos_k;
+  const float* newpos_q;
+  const int32_t* kept_size;  // (H, nt) or null (then every k_max slot is swept)
+  void* out;                 // (H, N, D) contiguous
+};
+
+hipError_t launch_rope_frag(int dtype, int D, const void* x, int64_t head_stride, int64_t tok_stride,
+                            int heads, int N, int rows_pad, int pos_base, float pos_scale,
+                            float rope_scale, const float* inv_freq, u32x4* frag, hipStream_t st);
+hipError_t launch_score(int D, int tile, const ScoreArgs& a, hipStream_t st);
+size_t select_lds_bytes(int N, int k_max);
+hipError_t launch_select(const SelectArgs& a, int vote_bytes, hipStream_t st);
+hipError_t launch_expand_votes(const uint8_t* v8, int64_t stride, int H, int nt, int N, int T,
+                               int q_pos_base, int32_t* out, hipStream_t st);
+hipError_t launch_gather(int dtype, int D, int tile, const GatherArgs& a, hipStream_t st);
+
+}  // namespace sta

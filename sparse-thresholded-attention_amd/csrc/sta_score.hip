@@ -1,0 +1,313 @@
+// sta_score.hip -- selection-geometry RoPE pre-kernel and the two score passes.
+//
+// Reference: shared_selection_triton_exact_2.py:50-140 (_select_vote_kernel).  The reference
+// re-rotates Q and K inside both passes; here the rotation runs once per (row, head) and writes
+// the rotated rows in MFMA operand order.  The reference's score dots are fp32 (exact_2.py:100,
+// 118); here each rotated fp32 row is split into bf16 hi + lo parts and every score is
+//   hi(q).hi(k) + hi(q).lo(k) + lo(q).hi(k)   (three bf16 MFMAs, fp32 accumulation),
+// whose error against the fp32 dot is below 3 * 2^-16 * sum|q_i k_i| -- well inside the 1e-3
+// selection band -- instead of the ~2^-8 a single bf16 product would give.
+//
+// Fragment layout (one unit = 8 bf16 = 16 bytes, u32x4):
+//   frag[head][rb][s][hl][lane]   rb = row/32, s = dim/16 (16-wide k step), hl = 0 hi / 1 lo,
+//   lane = row%32 + 32*((dim%16)/8), holding dims 8*(lane/32) .. +7 of step s.
+// A 32-row block's operand for one k step is one contiguous 1 KB load per wave.
+#include "sta_device.h"
+#include "sta_kernels.h"
+
+namespace sta {
+
+// ------------------------------------------------------------------------------------------
+// RoPE pre-kernel: rotate rows in the selection geometry, split hi/lo, write fragments.
+// angle = fl(fl(float(pos) * pos_scale) * inv_freq[i])          (exact_2.py:79, 95)
+// c, s  = fl(cos(angle) * rope_scale), fl(sin(angle) * rope_scale)   (exact_2.py:80-81)
+// r1 = fl(fl(x1*c) - fl(x2*s)), r2 = fl(fl(x2*c) + fl(x1*s))   (exact_2.py:82-83)
+// Rows >= N (tile padding, and the zero "phantom" keys the reference's masked loads produce
+// when q_pos_base > 0) are written as zeros.
+// ------------------------------------------------------------------------------------------
+template <int DT, int D>
+__global__ __launch_bounds__(256) void rope_frag_kernel(const void* __restrict__ x, int64_t head_stride,
+                                                        int64_t tok_stride, int heads, int N, int rows_pad,
+                                                        int pos_base, float pos_scale, float rope_scale,
+                                                        const float* __restrict__ inv_freq,
+                                                        u32x4* __restrict__ frag) {
+#pragma clang fp contract(off)
+  constexpr int C = D / 8;
+  const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t total = (int64_t)heads * rows_pad * C;
+  if (gid >= total) return;
+  const int c = (int)(gid % C);
+  const int64_t hr = gid / C;
+  const int row = (int)(hr % rows_pad);
+  const int head = (int)(hr / rows_pad);
+  const int d0 = c * 8;
+  float out[8];
+  if (row < N) {
+    const bool first = d0 < D / 2;
+    const int i0 = first ? d0 : d0 - D / 2;
+    float a[8], b[8];
+    const int64_t base = (int64_t)head * head_stride + (int64_t)row * tok_stride;
+    load8<DT>(x, base + i0, a);
+    load8<DT>(x, base + D / 2 + i0, b);
+    const float pf = (float)(pos_base + row) * pos_scale;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float ang = pf * inv_freq[i0 + e];
+      float sn, cs;
+      sincosf(ang, &sn, &cs);
+      cs = cs * rope_scale;
+      sn = sn * rope_scale;
+      if (first) {
+        const float p = a[e] * cs, q = b[e] * sn;
+        out[e] = p - q;
+      } else {
+        const float p = b[e] * cs, q = a[e] * sn;
+        out[e] = p + q;
+      }
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) out[e] = 0.0f;
+  }
+  u32x4 hi, lo;
+  split_bf16x8(out, hi, lo);
+  const int rb = row >> 5, lr = row & 31, s = d0 >> 4, g = (d0 & 15) >> 3;
+  const int64_t unit = (((int64_t)head * (rows_pad >> 5) + rb) * (D / 16) + s) * 2 * 64 + lr + 32 * g;
+  frag[unit] = hi;
+  frag[unit + 64] = lo;
+}
+
+// ------------------------------------------------------------------------------------------
+// Score kernel: pass 1 (exact row max) and pass 2 (keep + votes), exact_2.py:87-140.
+//
+// One workgroup = one head and FOUR consecutive query tiles; wave w owns tile 4g+w and holds
+// that tile's Q fragments in registers.  Key chunks of 128 rows are staged once in LDS and read
+// by all four waves, so each K byte fetched from L2 feeds 4 tiles.  Every wave sees every key of
+// its tile, so row maxima and per-key votes complete inside one wave: no cross-wave reduction.
+// ------------------------------------------------------------------------------------------
+template <int D, int RB, bool RC>
+__global__ __launch_bounds__(256, 1) void score_kernel(ScoreArgs a) {
+#pragma clang fp contract(off)
+  constexpr int S = D / 16;             // k steps of 16
+  constexpr int T = RB * 32;            // tile rows
+  constexpr int CHUNK_UNITS = 4 * S * 2 * 64;   // u32x4 units per 128-key chunk
+  constexpr int PF = CHUNK_UNITS / 256;          // units per thread per chunk
+  extern __shared__ u32x4 lds[];        // 2 x CHUNK_UNITS
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int ngroups = (a.nt + 3) >> 2;
+  int h, g;
+  {
+    const int bid = blockIdx.x;
+    if ((a.H & 7) == 0) {  // XCD-aware: workgroup i runs on XCD i % 8; keep a head on one XCD
+      const int hpx = a.H >> 3;
+      const int r = bid >> 3;
+      h = (bid & 7) * hpx + r % hpx;
+      g = ngroups - 1 - r / hpx;
+    } else {
+      h = bid % a.H;
+      g = ngroups - 1 - bid / a.H;
+    }
+  }
+  const int kvh = h / (a.H / a.Hkv);
+  const int t = g * 4 + wave;
+  const bool active = t < a.nt;
+  const int t_last = min(g * 4 + 3, a.nt - 1);
+  const int hi_max = a.q_pos_base + (t_last + 1) * T;
+  const int hi_t = a.q_pos_base + (t + 1) * T;     // exact_2.py:85
+  const int qpos0 = a.q_pos_base + t * T;          // position of the tile's first query
+  const int nchunks = (hi_max + 127) >> 7;
+  const float tau = a.tau[h];
+
+  // ---- Q fragments of this wave's tile ----
+  u32x4 qhi[RB][S], qlo[RB][S];
+  if (active) {
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+      for (int s = 0; s < S; ++s) {
+        const int64_t u = (((int64_t)h * (a.q_rows_pad >> 5) + t * RB + rb) * S + s) * 128 + lane;
+        qhi[rb][s] = a.qfrag[u];
+        qlo[rb][s] = a.qfrag[u + 64];
+      }
+  } else {
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+      for (int s = 0; s < S; ++s) { qhi[rb][s] = u32x4{0, 0, 0, 0}; qlo[rb][s] = u32x4{0, 0, 0, 0}; }
+  }
+
+  const u32x4* kbase = a.kfrag + (int64_t)kvh * (a.k_rows_pad >> 5) * S * 128;
+
+  float mx[RB][16];
+  float thr[RB][16];
+  int rc[RB][16];
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) { mx[rb][i] = -INFINITY; thr[rb][i] = 0.0f; rc[rb][i] = 0; }
+
+  u32x4 pf[PF];
+  for (int pass = 0; pass < 2; ++pass) {
+    // stage chunk 0
+#pragma unroll
+    for (int e = 0; e < PF; ++e) pf[e] = kbase[e * 256 + threadIdx.x];
+#pragma unroll
+    for (int e = 0; e < PF; ++e) lds[e * 256 + threadIdx.x] = pf[e];
+    __syncthreads();
+    for (int c = 0; c < nchunks; ++c) {
+      const bool more = c + 1 < nchunks;
+      if (more) {
+        const u32x4* src = kbase + (int64_t)(c + 1) * CHUNK_UNITS;
+#pragma unroll
+        for (int e = 0; e < PF; ++e) pf[e] = src[e * 256 + threadIdx.x];
+      }
+      const u32x4* buf = lds + (c & 1) * CHUNK_UNITS;
+      if (active) {
+        for (int sb = 0; sb < 4; ++sb) {
+          const int key0 = c * 128 + sb * 32;
+          if (key0 >= hi_t) break;
+          floatx16 acc[RB];
+#pragma unroll
+          for (int rb = 0; rb < RB; ++rb) acc[rb] = floatx16{};
+#pragma unroll
+          for (int s = 0; s < S; ++s) {
+            const u32x4 bh = buf[(sb * S + s) * 128 + lane];
+            const u32x4 bl = buf[(sb * S + s) * 128 + 64 + lane];
+#pragma unroll
+            for (int rb = 0; rb < RB; ++rb) acc[rb] = mfma32(qlo[rb][s], bh, acc[rb]);
+#pragma unroll
+            for (int rb = 0; rb < RB; ++rb) acc[rb] = mfma32(qhi[rb][s], bl, acc[rb]);
+#pragma unroll
+            for (int rb = 0; rb < RB; ++rb) acc[rb] = mfma32(qhi[rb][s], bh, acc[rb]);
+          }
+          const int key = key0 + (lane & 31);
+          const bool diag = key0 + 31 > qpos0;
+          if (pass == 0) {
+#pragma unroll
+            for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+              for (int i = 0; i < 16; ++i) {
+                const int row = rb * 32 + (i >> 2) * 8 + (lane >> 5) * 4 + (i & 3);
+                float v = acc[rb][i];
+                if (diag && key > qpos0 + row) v = -INFINITY;   // exact_2.py:101-102
+                mx[rb][i] = fmaxf(mx[rb][i], v);
+              }
+          } else {
+            int cnt = 0;
+#pragma unroll
+            for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+              for (int i = 0; i < 16; ++i) {
+                const int row = rb * 32 + (i >> 2) * 8 + (lane >> 5) * 4 + (i & 3);
+                const float sc = acc[rb][i] * a.sm_scale;
+                bool keep = sc >= thr[rb][i];                   // exact_2.py:121
+                if (diag) keep = keep && key <= qpos0 + row;
+                keep = keep && (t * T + row < a.N);
+                cnt += keep;
+                if constexpr (RC) rc[rb][i] += keep;
+              }
+            cnt += __shfl_xor(cnt, 32, 64);                     // exact_2.py:123
+            if (lane < 32 && key < a.N)
+              a.votes[((int64_t)h * a.nt + t) * a.votes_stride + key] = (uint8_t)cnt;
+          }
+        }
+      }
+      if (more) {
+        u32x4* dst = lds + ((c + 1) & 1) * CHUNK_UNITS;
+#pragma unroll
+        for (int e = 0; e < PF; ++e) dst[e * 256 + threadIdx.x] = pf[e];
+      }
+      __syncthreads();
+    }
+    if (pass == 0 && active) {
+      // complete the row max over the 32 lanes holding a row's keys, then the threshold
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          float v = mx[rb][i];
+          v = fmaxf(v, __shfl_xor(v, 1, 64));
+          v = fmaxf(v, __shfl_xor(v, 2, 64));
+          v = fmaxf(v, __shfl_xor(v, 4, 64));
+          v = fmaxf(v, __shfl_xor(v, 8, 64));
+          v = fmaxf(v, __shfl_xor(v, 16, 64));
+          const float m = v * a.sm_scale;   // fl(max * c) == max of fl(s * c) for c > 0
+          thr[rb][i] = m - tau;
+          const int row = rb * 32 + (i >> 2) * 8 + (lane >> 5) * 4 + (i & 3);
+          if (a.row_max && (lane & 31) == 0 && t * T + row < a.N)
+            a.row_max[(int64_t)h * a.N + t * T + row] = m;
+        }
+    }
+  }
+  if constexpr (RC) {
+    if (active) {
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          int v = rc[rb][i];
+          v += __shfl_xor(v, 1, 64);
+          v += __shfl_xor(v, 2, 64);
+          v += __shfl_xor(v, 4, 64);
+          v += __shfl_xor(v, 8, 64);
+          v += __shfl_xor(v, 16, 64);
+          const int row = rb * 32 + (i >> 2) * 8 + (lane >> 5) * 4 + (i & 3);
+          if ((lane & 31) == 0 && t * T + row < a.N) a.row_counts[(int64_t)h * a.N + t * T + row] = v;
+        }
+    }
+  }
+}
+
+// ------------------------------------------------------------------------------------------
+// host launchers
+// ------------------------------------------------------------------------------------------
+template <int DT, int D>
+static hipError_t launch_rope_frag_t(const void* x, int64_t hs, int64_t ts, int heads, int N, int rows_pad,
+                                     int pos_base, float pos_scale, float rope_scale, const float* inv_freq,
+                                     u32x4* frag, hipStream_t st) {
+  const int64_t total = (int64_t)heads * rows_pad * (D / 8);
+  const int64_t blocks = (total + 255) / 256;
+  hipLaunchKernelGGL((rope_frag_kernel<DT, D>), dim3((unsigned)blocks), dim3(256), 0, st, x, hs, ts, heads, N,
+                     rows_pad, pos_base, pos_scale, rope_scale, inv_freq, frag);
+  return hipGetLastError();
+}
+
+hipError_t launch_rope_frag(int dtype, int D, const void* x, int64_t hs, int64_t ts, int heads, int N,
+                            int rows_pad, int pos_base, float pos_scale, float rope_scale,
+                            const float* inv_freq, u32x4* frag, hipStream_t st) {
+#define STA_RF(DT_, D_) \
+  if (dtype == DT_ && D == D_) return launch_rope_frag_t<DT_, D_>(x, hs, ts, heads, N, rows_pad, pos_base, pos_scale, rope_scale, inv_freq, frag, st);
+  STA_RF(DT_F32, 64) STA_RF(DT_F32, 128) STA_RF(DT_BF16, 64) STA_RF(DT_BF16, 128)
+  STA_RF(DT_F16, 64) STA_RF(DT_F16, 128)
+#undef STA_RF
+  return hipErrorInvalidValue;
+}
+
+template <int D, int RB, bool RC>
+static hipError_t launch_score_t(const ScoreArgs& a, hipStream_t st) {
+  constexpr int S = D / 16;
+  const size_t lds_bytes = 2 * (size_t)(4 * S * 2 * 64) * 16;
+  static bool attr_set = false;
+  if (!attr_set) {
+    hipError_t e = hipFuncSetAttribute((const void*)score_kernel<D, RB, RC>,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_bytes);
+    if (e != hipSuccess) return e;
+    attr_set = true;
+  }
+  const int ngroups = (a.nt + 3) / 4;
+  hipLaunchKernelGGL((score_kernel<D, RB, RC>), dim3(a.H * ngroups), dim3(256), lds_bytes, st, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_score(int D, int tile, const ScoreArgs& a, hipStream_t st) {
+  const bool rc = a.row_counts != nullptr;
+#define STA_SC(D_, RB_) \
+  if (D == D_ && tile == RB_ * 32) return rc ? launch_score_t<D_, RB_, true>(a, st) : launch_score_t<D_, RB_, false>(a, st);
+  STA_SC(64, 1) STA_SC(64, 2) STA_SC(128, 1) STA_SC(128, 2)
+#undef STA_SC
+  return hipErrorInvalidValue;
+}
+
+}  // namespace sta

@@ -1,0 +1,22 @@
+"""Drop-in for shared_selection_triton_exact.py (the original exact-max kernel, freq votes).
+
+Its _build_sets sorts where exact_2 uses topk/scatter; in frequency mode both produce the same
+sets (shared_selection_triton_exact.py:253-370 vs shared_selection_triton_exact_2.py:277-426), so
+both files map onto the same HIP path.
+"""
+from _shared_prefill import build_sets as _device_build_sets
+from _shared_prefill import shared_prefill
+
+
+def _build_sets(votes, pos_scale, n_global, n_local, pct, T, k_max, q_pos_base=0, measure=False):
+    """shared_selection_triton_exact.py:254-370."""
+    return _device_build_sets(votes, pos_scale, n_global, n_local, pct, T, k_max, q_pos_base, measure)
+
+
+def shared_pi_attention(q, k, v, tau, inv_freq, pos_scale=1.0, pct=30.0, sm_scale=None,
+                        rope_scale=1.0, n_global=32, n_local=32, tile=32, k_max=1024,
+                        block_n=64, block_k=64, q_pos_base=0, measure=False):
+    """shared_selection_triton_exact.py:376-423."""
+    return shared_prefill(q, k, v, tau, inv_freq, pos_scale, rope_scale, inv_freq, pos_scale,
+                          rope_scale, pct, sm_scale, n_global, n_local, tile, k_max, q_pos_base,
+                          measure, "freq")

@@ -1,0 +1,101 @@
+"""CPU checks of the C-ABI library: it loads, exports every entry point include/sta.h declares,
+and rejects bad arguments with the documented error codes.  No call here reaches a GPU."""
+import ctypes
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "sta.h")
+
+
+def _declared():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:int|size_t|const char\*)\s+(sta_\w+)\s*\(", text, re.M)))
+
+
+def test_header_declares_entry_points():
+    names = _declared()
+    assert "sta_shared_attention" in names and "sta_build_sets" in names
+    assert len(names) >= 7
+
+
+def test_library_exports_every_declared_symbol():
+    import _sta_native as native
+    lib = native.lib()
+    for name in _declared():
+        assert hasattr(lib, name), name
+    assert sorted(native.EXPORTS) == _declared()
+    assert lib.sta_abi_version() == 1
+
+
+def _args(**kw):
+    import _sta_native as native
+    a = native.ShareArgs()
+    a.dtype, a.H, a.Hkv, a.N, a.D, a.tile, a.k_max = 1, 32, 32, 12288, 128, 64, 2048
+    a.start_pct, a.n_global, a.n_local = 30, 32, 32
+    for k, v in kw.items():
+        setattr(a, k, v)
+    return a
+
+
+def test_workspace_size_matches_layout():
+    import _sta_native as native
+    lib = native.lib()
+    a = _args()
+    n = lib.sta_shared_workspace_size(ctypes.byref(a))
+    nt = 12288 // 64
+    q = 32 * 12288 * 128 * 4            # q fragments, hi + lo bf16
+    k = 32 * 12288 * 128 * 4            # k fragments
+    votes = 32 * nt * 12288             # byte votes
+    assert n >= q + k + votes and n < q + k + votes + 4096
+
+
+@pytest.mark.parametrize("field,value,code", [
+    ("D", 96, -2), ("tile", 48, -2), ("Hkv", 5, -1), ("k_max", 0, -1), ("N", 0, -1),
+    ("dtype", 7, -1), ("q_pos_base", -1, -1),
+])
+def test_invalid_arguments_are_rejected(field, value, code):
+    import _sta_native as native
+    lib = native.lib()
+    a = _args(**{field: value})
+    assert lib.sta_shared_workspace_size(ctypes.byref(a)) == 0
+    assert lib.sta_shared_attention(ctypes.byref(a), None) == code
+    assert len(lib.sta_last_error()) > 0
+
+
+def test_missing_pointers_are_rejected_before_any_launch():
+    import _sta_native as native
+    lib = native.lib()
+    a = _args()
+    assert lib.sta_shared_attention(ctypes.byref(a), None) == -1       # q is NULL
+    assert b"NULL" in lib.sta_last_error()
+    assert lib.sta_shared_attention(None, None) == -1
+
+
+def test_product_path_refuses_cpu_tensors():
+    import torch
+    import shared_selection_triton_exact_2 as st
+    q = torch.zeros(1, 2, 64, 64)
+    with pytest.raises(RuntimeError, match="HIP device"):
+        st.shared_pi_attention(q, q, q, torch.ones(2), torch.ones(32), tile=64)
+
+
+def test_yarn_geometry_matches_transformers():
+    """The YaRN frequencies of config 2 against transformers' own initialiser."""
+    import torch
+    from synthetic import yarn_inv_freq
+    tr = pytest.importorskip("transformers")
+    from transformers import LlamaConfig
+    from transformers.modeling_rope_utils import ROPE_INIT_FUNCTIONS
+    cfg = LlamaConfig(hidden_size=4096, num_attention_heads=32, head_dim=128,
+                      max_position_embeddings=32768,
+                      rope_parameters={"rope_type": "yarn", "rope_theta": 500000.0, "factor": 4.0,
+                                       "original_max_position_embeddings": 8192,
+                                       "beta_fast": 32.0, "beta_slow": 1.0})
+    ref_f, ref_m = ROPE_INIT_FUNCTIONS["yarn"](cfg, "cpu")
+    f, m = yarn_inv_freq(128, 500000.0, 4.0, 8192, 32.0, 1.0)
+    assert torch.equal(f, ref_f.float())
+    assert abs(m - ref_m) < 1e-12
+    assert abs(m - 1.1386294361119891) < 1e-12
