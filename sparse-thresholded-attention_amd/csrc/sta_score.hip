@@ -15,6 +15,8 @@
 #include "sta_device.h"
 #include "sta_kernels.h"
 
+#include <type_traits>
+
 namespace sta {
 
 // ------------------------------------------------------------------------------------------
@@ -84,15 +86,38 @@ __global__ __launch_bounds__(256) void rope_frag_kernel(const void* __restrict__
 // that tile's Q fragments in registers.  Key chunks of 128 rows are staged once in LDS and read
 // by all four waves, so each K byte fetched from L2 feeds 4 tiles.  Every wave sees every key of
 // its tile, so row maxima and per-key votes complete inside one wave: no cross-wave reduction.
+//
+// Chunks whose keys are causal for every query of the workgroup (all but the last one or two)
+// take a fully unrolled path that software-pipelines the per-block epilogue (row max in pass 1,
+// threshold + vote count in pass 2) of 32-key block n into the MFMA stream of block n + 1; the
+// chunks on the diagonal take a per-block path with causal masking.
+//
+// Pass 2 compares the raw accumulator against x0 = the smallest float with fl(x0 * sm_scale)
+// >= m - tau.  fl(x * c) is monotone in x for c > 0, so acc >= x0 <=> fl(acc * sm_scale) >=
+// fl(m - tau), exactly the reference's keep test (exact_2.py:121), with one compare per score.
 // ------------------------------------------------------------------------------------------
+__device__ __forceinline__ float min_arg_for(float thr, float c) {
+#pragma clang fp contract(off)
+  if (thr != thr || thr == -INFINITY || thr == INFINITY) return thr;
+  float x = thr / c;
+  for (int i = 0; i < 4; ++i) {
+    const float y = nextafterf(x, -INFINITY);
+    if (y * c >= thr) x = y; else break;
+  }
+  for (int i = 0; i < 4 && !(x * c >= thr); ++i) x = nextafterf(x, INFINITY);
+  return x;
+}
+
 template <int D, int RB, bool RC>
 __global__ __launch_bounds__(256, 1) void score_kernel(ScoreArgs a) {
 #pragma clang fp contract(off)
-  constexpr int S = D / 16;             // k steps of 16
-  constexpr int T = RB * 32;            // tile rows
-  constexpr int CHUNK_UNITS = 4 * S * 2 * 64;   // u32x4 units per 128-key chunk
+  constexpr int S = D / 16;                      // k steps of 16
+  constexpr int T = RB * 32;                     // tile rows
+  constexpr int CHUNK_UNITS = 4 * S * 2 * 64;    // u32x4 units per 128-key chunk
   constexpr int PF = CHUNK_UNITS / 256;          // units per thread per chunk
-  extern __shared__ u32x4 lds[];        // 2 x CHUNK_UNITS
+  constexpr int PER = 16 * RB / S;               // epilogue elements finished per k step
+  static_assert(PER * S == 16 * RB, "epilogue split");
+  extern __shared__ u32x4 lds[];                 // 2 x CHUNK_UNITS
 
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -118,7 +143,10 @@ __global__ __launch_bounds__(256, 1) void score_kernel(ScoreArgs a) {
   const int hi_t = a.q_pos_base + (t + 1) * T;     // exact_2.py:85
   const int qpos0 = a.q_pos_base + t * T;          // position of the tile's first query
   const int nchunks = (hi_max + 127) >> 7;
+  // chunks entirely below N whose keys are causal for every query of the workgroup
+  const int nfull = min(min(nchunks, (a.q_pos_base + g * 4 * T + 1) >> 7), a.N >> 7);
   const float tau = a.tau[h];
+  uint8_t* vrow = a.votes + ((int64_t)h * a.nt + t) * a.votes_stride;
 
   // ---- Q fragments of this wave's tile ----
   u32x4 qhi[RB][S], qlo[RB][S];
@@ -137,25 +165,95 @@ __global__ __launch_bounds__(256, 1) void score_kernel(ScoreArgs a) {
 #pragma unroll
       for (int s = 0; s < S; ++s) { qhi[rb][s] = u32x4{0, 0, 0, 0}; qlo[rb][s] = u32x4{0, 0, 0, 0}; }
   }
-
   const u32x4* kbase = a.kfrag + (int64_t)kvh * (a.k_rows_pad >> 5) * S * 128;
 
-  float mx[RB][16];
-  float thr[RB][16];
+  float mx[RB][16];   // pass 1: running max of the raw dot per row slot
+  float x0[RB][16];   // pass 2: keep threshold on the raw dot per row slot
   int rc[RB][16];
 #pragma unroll
   for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
-    for (int i = 0; i < 16; ++i) { mx[rb][i] = -INFINITY; thr[rb][i] = 0.0f; rc[rb][i] = 0; }
+    for (int i = 0; i < 16; ++i) { mx[rb][i] = -INFINITY; x0[rb][i] = INFINITY; rc[rb][i] = 0; }
+
+  // 32 keys x this wave's rows: hi.hi + hi.lo + lo.hi, small terms first
+  auto mfma_step = [&](const u32x4* buf, int sb, int s, floatx16* acc) {
+    const u32x4 bh = buf[(sb * S + s) * 128 + lane];
+    const u32x4 bl = buf[(sb * S + s) * 128 + 64 + lane];
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) acc[rb] = mfma32(qlo[rb][s], bh, acc[rb]);
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) acc[rb] = mfma32(qhi[rb][s], bl, acc[rb]);
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) acc[rb] = mfma32(qhi[rb][s], bh, acc[rb]);
+  };
+  // MFMAs of block sb into accN; when HAS_PREV, the epilogue of the previous (unmasked) block
+  // accO at keys keyO.. is finished in slices between the k steps
+  auto fused_block = [&](auto passc, auto prevc, const u32x4* buf, int sb, floatx16* accN,
+                         const floatx16* accO, int keyO) {
+    constexpr int pass = decltype(passc)::value;
+    constexpr bool HAS_PREV = decltype(prevc)::value;
+    int cnt = 0;
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) accN[rb] = floatx16{};
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+      mfma_step(buf, sb, s, accN);
+      if constexpr (HAS_PREV) {
+#pragma unroll
+        for (int e = 0; e < PER; ++e) {
+          const int idx = s * PER + e, rb = idx / 16, i = idx % 16;
+          const float v = accO[rb][i];
+          if constexpr (pass == 0) {
+            mx[rb][i] = v > mx[rb][i] ? v : mx[rb][i];
+          } else {
+            const int keep = v >= x0[rb][i];
+            cnt += keep;
+            if constexpr (RC) rc[rb][i] += keep;
+          }
+        }
+      }
+    }
+    if constexpr (HAS_PREV && pass == 1) {
+      cnt += __shfl_xor(cnt, 32, 64);   // exact_2.py:123; both lane halves now hold the total
+      vrow[keyO + (lane & 31)] = (uint8_t)cnt;
+    }
+  };
+  // the last block's epilogue when nothing follows it
+  auto flush = [&](auto passc, const floatx16* acc, int key0) {
+    constexpr int pass = decltype(passc)::value;
+    int cnt = 0;
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const float v = acc[rb][i];
+        if constexpr (pass == 0) {
+          mx[rb][i] = v > mx[rb][i] ? v : mx[rb][i];
+        } else {
+          const int keep = v >= x0[rb][i];
+          cnt += keep;
+          if constexpr (RC) rc[rb][i] += keep;
+        }
+      }
+    if constexpr (pass == 1) {
+      cnt += __shfl_xor(cnt, 32, 64);
+      vrow[key0 + (lane & 31)] = (uint8_t)cnt;
+    }
+  };
 
   u32x4 pf[PF];
-  for (int pass = 0; pass < 2; ++pass) {
-    // stage chunk 0
+  auto run_pass = [&](auto passc) {
+    constexpr int pass = decltype(passc)::value;
+    constexpr std::integral_constant<bool, true> kPrev{};
+    constexpr std::integral_constant<bool, false> kNoPrev{};
 #pragma unroll
     for (int e = 0; e < PF; ++e) pf[e] = kbase[e * 256 + threadIdx.x];
 #pragma unroll
     for (int e = 0; e < PF; ++e) lds[e * 256 + threadIdx.x] = pf[e];
     __syncthreads();
+    floatx16 accA[RB], accB[RB];
+    bool pendingB = false;   // accB holds an unmasked block whose epilogue is still due
+    int keyB = 0;
     for (int c = 0; c < nchunks; ++c) {
       const bool more = c + 1 < nchunks;
       if (more) {
@@ -165,52 +263,47 @@ __global__ __launch_bounds__(256, 1) void score_kernel(ScoreArgs a) {
       }
       const u32x4* buf = lds + (c & 1) * CHUNK_UNITS;
       if (active) {
-        for (int sb = 0; sb < 4; ++sb) {
-          const int key0 = c * 128 + sb * 32;
-          if (key0 >= hi_t) break;
-          floatx16 acc[RB];
+        if (c < nfull) {
+          if (c == 0) fused_block(passc, kNoPrev, buf, 0, accA, accB, 0);
+          else fused_block(passc, kPrev, buf, 0, accA, accB, keyB);
+          fused_block(passc, kPrev, buf, 1, accB, accA, c * 128);
+          fused_block(passc, kPrev, buf, 2, accA, accB, c * 128 + 32);
+          fused_block(passc, kPrev, buf, 3, accB, accA, c * 128 + 64);
+          pendingB = true;
+          keyB = c * 128 + 96;
+        } else {
+          if (pendingB) flush(passc, accB, keyB);
+          pendingB = false;
+          for (int sb = 0; sb < 4; ++sb) {
+            const int key0 = c * 128 + sb * 32;
+            if (key0 >= hi_t) break;
+            floatx16 acc[RB];
 #pragma unroll
-          for (int rb = 0; rb < RB; ++rb) acc[rb] = floatx16{};
+            for (int rb = 0; rb < RB; ++rb) acc[rb] = floatx16{};
 #pragma unroll
-          for (int s = 0; s < S; ++s) {
-            const u32x4 bh = buf[(sb * S + s) * 128 + lane];
-            const u32x4 bl = buf[(sb * S + s) * 128 + 64 + lane];
-#pragma unroll
-            for (int rb = 0; rb < RB; ++rb) acc[rb] = mfma32(qlo[rb][s], bh, acc[rb]);
-#pragma unroll
-            for (int rb = 0; rb < RB; ++rb) acc[rb] = mfma32(qhi[rb][s], bl, acc[rb]);
-#pragma unroll
-            for (int rb = 0; rb < RB; ++rb) acc[rb] = mfma32(qhi[rb][s], bh, acc[rb]);
-          }
-          const int key = key0 + (lane & 31);
-          const bool diag = key0 + 31 > qpos0;
-          if (pass == 0) {
-#pragma unroll
-            for (int rb = 0; rb < RB; ++rb)
-#pragma unroll
-              for (int i = 0; i < 16; ++i) {
-                const int row = rb * 32 + (i >> 2) * 8 + (lane >> 5) * 4 + (i & 3);
-                float v = acc[rb][i];
-                if (diag && key > qpos0 + row) v = -INFINITY;   // exact_2.py:101-102
-                mx[rb][i] = fmaxf(mx[rb][i], v);
-              }
-          } else {
+            for (int s = 0; s < S; ++s) mfma_step(buf, sb, s, acc);
+            const int key = key0 + (lane & 31);
+            const bool diag = key0 + 31 > qpos0;
             int cnt = 0;
 #pragma unroll
             for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
               for (int i = 0; i < 16; ++i) {
                 const int row = rb * 32 + (i >> 2) * 8 + (lane >> 5) * 4 + (i & 3);
-                const float sc = acc[rb][i] * a.sm_scale;
-                bool keep = sc >= thr[rb][i];                   // exact_2.py:121
-                if (diag) keep = keep && key <= qpos0 + row;
-                keep = keep && (t * T + row < a.N);
-                cnt += keep;
-                if constexpr (RC) rc[rb][i] += keep;
+                const bool causal = !diag || key <= qpos0 + row;   // exact_2.py:101, 119
+                const float v = acc[rb][i];
+                if constexpr (pass == 0) {
+                  if (causal && v > mx[rb][i]) mx[rb][i] = v;
+                } else {
+                  const int keep = causal && v >= x0[rb][i];
+                  cnt += keep;
+                  if constexpr (RC) rc[rb][i] += keep;
+                }
               }
-            cnt += __shfl_xor(cnt, 32, 64);                     // exact_2.py:123
-            if (lane < 32 && key < a.N)
-              a.votes[((int64_t)h * a.nt + t) * a.votes_stride + key] = (uint8_t)cnt;
+            if constexpr (pass == 1) {
+              cnt += __shfl_xor(cnt, 32, 64);
+              if (lane < 32 && key < a.N) vrow[key] = (uint8_t)cnt;
+            }
           }
         }
       }
@@ -221,26 +314,32 @@ __global__ __launch_bounds__(256, 1) void score_kernel(ScoreArgs a) {
       }
       __syncthreads();
     }
-    if (pass == 0 && active) {
-      // complete the row max over the 32 lanes holding a row's keys, then the threshold
+    if (active && pendingB) flush(passc, accB, keyB);
+    if constexpr (pass == 0) {
+      if (active) {
+        // complete the row max over the 32 lanes holding a row's keys, then the threshold
 #pragma unroll
-      for (int rb = 0; rb < RB; ++rb)
+        for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          float v = mx[rb][i];
-          v = fmaxf(v, __shfl_xor(v, 1, 64));
-          v = fmaxf(v, __shfl_xor(v, 2, 64));
-          v = fmaxf(v, __shfl_xor(v, 4, 64));
-          v = fmaxf(v, __shfl_xor(v, 8, 64));
-          v = fmaxf(v, __shfl_xor(v, 16, 64));
-          const float m = v * a.sm_scale;   // fl(max * c) == max of fl(s * c) for c > 0
-          thr[rb][i] = m - tau;
-          const int row = rb * 32 + (i >> 2) * 8 + (lane >> 5) * 4 + (i & 3);
-          if (a.row_max && (lane & 31) == 0 && t * T + row < a.N)
-            a.row_max[(int64_t)h * a.N + t * T + row] = m;
-        }
+          for (int i = 0; i < 16; ++i) {
+            float v = mx[rb][i];
+            v = fmaxf(v, __shfl_xor(v, 1, 64));
+            v = fmaxf(v, __shfl_xor(v, 2, 64));
+            v = fmaxf(v, __shfl_xor(v, 4, 64));
+            v = fmaxf(v, __shfl_xor(v, 8, 64));
+            v = fmaxf(v, __shfl_xor(v, 16, 64));
+            const float m = v * a.sm_scale;   // fl(max * c) == max of fl(s * c) for c > 0
+            const int row = rb * 32 + (i >> 2) * 8 + (lane >> 5) * 4 + (i & 3);
+            const bool ok = t * T + row < a.N;  // padded rows never vote (exact_2.py:121)
+            x0[rb][i] = ok ? min_arg_for(m - tau, a.sm_scale) : INFINITY;
+            if (a.row_max && (lane & 31) == 0 && ok) a.row_max[(int64_t)h * a.N + t * T + row] = m;
+          }
+      }
     }
-  }
+  };
+  run_pass(std::integral_constant<int, 0>{});
+  run_pass(std::integral_constant<int, 1>{});
+
   if constexpr (RC) {
     if (active) {
 #pragma unroll
