@@ -193,6 +193,8 @@ int run_kernel_a(const sta_shared_args* a, const Layout& L, hipStream_t st) {
 }
 
 int run_gather(const sta_shared_args* a, const Layout& L, hipStream_t st) {
+  if (gather_lds_bytes(a->dtype, a->D, a->k_max) > 160 * 1024)
+    return fail(STA_ERR_UNSUPPORTED, "k_max=%d needs more than 160 KB of LDS in the gather", a->k_max);
   GatherArgs g;
   g.q = a->q;
   g.k = a->k;

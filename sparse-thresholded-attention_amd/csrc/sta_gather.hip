@@ -24,17 +24,55 @@ struct GatherCfg {
   static constexpr int NT = NW * 64;           // threads
   static constexpr int TPS = NT / 64;          // threads per slot for the K rotation
   static constexpr int FP = (D / 2) / TPS;     // frequencies per thread
+  static constexpr int VUNITS = 16 * (D / 8);  // (4 slots x 8 dims) V units per block
+  static constexpr int VU = (VUNITS + NT - 1) / NT;   // V units per thread
   static constexpr bool X3 = (DT == DT_F32);   // fp32 inputs: three-term bf16 products
   static constexpr int KSTR = D + 8;           // K LDS row stride (bf16 elements)
   static constexpr int VSTR = 64 + 8;          // V^T LDS row stride (elements)
   static constexpr int KHALVES = X3 ? 2 : 1;
-  static constexpr size_t LDS = (size_t)KHALVES * 64 * KSTR * 2 + (size_t)KHALVES * D * VSTR * 2;
+  static constexpr size_t LDS_FIXED = (size_t)KHALVES * 64 * KSTR * 2 + (size_t)KHALVES * D * VSTR * 2;
+  // + the tile's idx and newpos_k (8 bytes per slot, rounded up to whole 64-slot blocks)
+  static size_t lds_bytes(int k_max) { return LDS_FIXED + (size_t)((k_max + 63) / 64) * 64 * 8; }
+};
+
+// 8 consecutive elements in their storage format (loaded now, converted later)
+template <int DT>
+struct Raw8 {
+  u32x4 w;
+  __device__ __forceinline__ void load(const void* p, int64_t i) { w = *(const u32x4*)((const uint16_t*)p + i); }
+  __device__ __forceinline__ void zero() { w = u32x4{0, 0, 0, 0}; }
+  __device__ __forceinline__ void to_f32(float* o) const {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      if constexpr (DT == DT_BF16) {
+        o[2 * e] = __uint_as_float(w[e] << 16);
+        o[2 * e + 1] = __uint_as_float(w[e] & 0xffff0000u);
+      } else {
+        o[2 * e] = f16_bits_to_f32(w[e] & 0xffffu);
+        o[2 * e + 1] = f16_bits_to_f32(w[e] >> 16);
+      }
+    }
+  }
+};
+template <>
+struct Raw8<DT_F32> {
+  u32x4 a, b;
+  __device__ __forceinline__ void load(const void* p, int64_t i) {
+    const u32x4* q = (const u32x4*)((const float*)p + i);
+    a = q[0];
+    b = q[1];
+  }
+  __device__ __forceinline__ void zero() { a = u32x4{0, 0, 0, 0}; b = a; }
+  __device__ __forceinline__ void to_f32(float* o) const {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) { o[e] = __uint_as_float(a[e]); o[4 + e] = __uint_as_float(b[e]); }
+  }
 };
 
 template <int DT, int D, int NW>
 __global__ __launch_bounds__(NW * 64) void gather_kernel(GatherArgs a) {
   using Cfg = GatherCfg<DT, D, NW>;
-  constexpr int NT = Cfg::NT, TPS = Cfg::TPS, FP = Cfg::FP;
+  constexpr int NT = Cfg::NT, TPS = Cfg::TPS, FP = Cfg::FP, VU = Cfg::VU;
   constexpr bool X3 = Cfg::X3;
   constexpr int KSTR = Cfg::KSTR, VSTR = Cfg::VSTR;
   constexpr int T = NW * 16;
@@ -45,7 +83,7 @@ __global__ __launch_bounds__(NW * 64) void gather_kernel(GatherArgs a) {
   uint16_t* kr_lo = sh + 64 * KSTR;                        // [64][KSTR] (X3 only)
   uint16_t* vt_hi = sh + Cfg::KHALVES * 64 * KSTR;         // [D][VSTR]
   uint16_t* vt_lo = vt_hi + D * VSTR;                      // [D][VSTR] (X3 only)
-
+  int32_t* sidx = (int32_t*)(sh + Cfg::LDS_FIXED / 2);     // the tile's kept positions
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   int h, t;
   {
@@ -64,6 +102,18 @@ __global__ __launch_bounds__(NW * 64) void gather_kernel(GatherArgs a) {
   const int N = a.N;
   const float rs = a.rope_scale;
   const float* invf = a.inv_freq;
+  const int64_t tile_off = ((int64_t)h * a.nt + t) * a.k_max;
+  const int nvalid = a.kept_size ? min(a.kept_size[h * a.nt + t], a.k_max) : a.k_max;
+  const int nblk = (nvalid + 63) / 64;
+  float* snpk = (float*)(sidx + nblk * 64);
+  const int64_t kbase = (int64_t)kvh * a.k_head_stride;
+  const int64_t vbase = (int64_t)kvh * a.v_head_stride;
+
+  // ---- stage the tile's slots (sentinel N past the kept count) ----
+  for (int s = tid; s < nblk * 64; s += NT) {
+    sidx[s] = s < nvalid ? a.idx[tile_off + s] : N;
+    snpk[s] = s < nvalid ? a.newpos_k[tile_off + s] : 0.0f;
+  }
 
   // ---- this lane's query row, rotated at newpos_q (exact_2.py:174-185) ----
   const int r = wave * 16 + (lane & 15);
@@ -99,106 +149,111 @@ __global__ __launch_bounds__(NW * 64) void gather_kernel(GatherArgs a) {
       else qf_hi[ks] = pack_bf16x8(out);
     }
   }
+  __syncthreads();
 
-  floatx4 oacc[DB];
-#pragma unroll
-  for (int db = 0; db < DB; ++db) oacc[db] = floatx4{0.f, 0.f, 0.f, 0.f};
-  float mR = -INFINITY, l_i = 0.0f;
-
-  const int64_t tile_off = ((int64_t)h * a.nt + t) * a.k_max;
-  const int32_t* idx = a.idx + tile_off;
-  const float* npk = a.newpos_k + tile_off;
-  const int nvalid = a.kept_size ? min(a.kept_size[h * a.nt + t], a.k_max) : a.k_max;
-  const int nblk = (nvalid + 63) / 64;
-  const int64_t kbase = (int64_t)kvh * a.k_head_stride;
-  const int64_t vbase = (int64_t)kvh * a.v_head_stride;
-
-  for (int b = 0; b < nblk; ++b) {
-    const int s0 = b * 64;
-    // ---- K rows: gather, rotate at newpos_k (exact_2.py:193-207), store bf16 to LDS ----
-    {
-      const int slot = tid / TPS, part = tid % TPS;
-      const int s = s0 + slot;
-      const int j = s < a.k_max ? idx[s] : N;
-      float x1[FP], x2[FP], o1[FP], o2[FP];
-      if ((unsigned)j < (unsigned)N) {  // sentinel N (and any out-of-range index) -> zero row
-        const int64_t rb = kbase + (int64_t)j * a.k_tok_stride + part * FP;
-#pragma unroll
-        for (int c = 0; c < FP / 8; ++c) {
-          load8<DT>(a.k, rb + 8 * c, x1 + 8 * c);
-          load8<DT>(a.k, rb + D / 2 + 8 * c, x2 + 8 * c);
-        }
-        const float np = npk[s];
-#pragma unroll
-        for (int e = 0; e < FP; ++e) {
-          float sn, cs;
-          fast_sincos(np * invf[part * FP + e], sn, cs);
-          cs *= rs;
-          sn *= rs;
-          o1[e] = x1[e] * cs - x2[e] * sn;
-          o2[e] = x2[e] * cs + x1[e] * sn;
-        }
-      } else {
-#pragma unroll
-        for (int e = 0; e < FP; ++e) { o1[e] = 0.0f; o2[e] = 0.0f; }
-      }
+  // ---- raw K / V rows of one block, held in registers until the LDS buffers are free ----
+  const int kslot = tid / TPS, kpart = tid % TPS;
+  Raw8<DT> kx1[FP / 8], kx2[FP / 8], vx[VU][4];
+  auto load_block = [&](int b) {
+    const int j = sidx[b * 64 + kslot];
+    if ((unsigned)j < (unsigned)N) {   // sentinel N (and any out-of-range index) -> zero row
+      const int64_t rb = kbase + (int64_t)j * a.k_tok_stride + kpart * FP;
 #pragma unroll
       for (int c = 0; c < FP / 8; ++c) {
-        u32x4* d1 = (u32x4*)(kr_hi + slot * KSTR + part * FP + 8 * c);
-        u32x4* d2 = (u32x4*)(kr_hi + slot * KSTR + D / 2 + part * FP + 8 * c);
-        if constexpr (X3) {
-          u32x4 h1, l1, h2, l2;
-          split_bf16x8(o1 + 8 * c, h1, l1);
-          split_bf16x8(o2 + 8 * c, h2, l2);
-          *d1 = h1;
-          *d2 = h2;
-          *(u32x4*)(kr_lo + slot * KSTR + part * FP + 8 * c) = l1;
-          *(u32x4*)(kr_lo + slot * KSTR + D / 2 + part * FP + 8 * c) = l2;
-        } else {
-          *d1 = pack_bf16x8(o1 + 8 * c);
-          *d2 = pack_bf16x8(o2 + 8 * c);
-        }
+        kx1[c].load(a.k, rb + 8 * c);
+        kx2[c].load(a.k, rb + D / 2 + 8 * c);
+      }
+    } else {
+#pragma unroll
+      for (int c = 0; c < FP / 8; ++c) { kx1[c].zero(); kx2[c].zero(); }
+    }
+#pragma unroll
+    for (int vu = 0; vu < VU; ++vu) {
+      const int u = tid + vu * NT;
+      const int sg = u / (D / 8), dc = u % (D / 8);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int jv = sidx[b * 64 + (sg * 4 + k) % 64];
+        if (u < Cfg::VUNITS && (unsigned)jv < (unsigned)N) vx[vu][k].load(a.v, vbase + (int64_t)jv * a.v_tok_stride + dc * 8);
+        else vx[vu][k].zero();
       }
     }
-    // ---- V rows: gather 4 slots x 8 dims per unit, store transposed (dim-major) ----
-    for (int u = tid; u < 16 * (D / 8); u += NT) {
+  };
+  // rotate K at newpos_k (exact_2.py:203-207) and write K and V^T of the block to LDS
+  auto store_block = [&](int b) {
+    const float np = snpk[b * 64 + kslot];
+#pragma unroll
+    for (int c = 0; c < FP / 8; ++c) {
+      float x1[8], x2[8], o1[8], o2[8];
+      kx1[c].to_f32(x1);
+      kx2[c].to_f32(x2);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        float sn, cs;
+        fast_sincos(np * invf[kpart * FP + 8 * c + e], sn, cs);
+        cs *= rs;
+        sn *= rs;
+        o1[e] = x1[e] * cs - x2[e] * sn;
+        o2[e] = x2[e] * cs + x1[e] * sn;
+      }
+      u32x4* d1 = (u32x4*)(kr_hi + kslot * KSTR + kpart * FP + 8 * c);
+      u32x4* d2 = (u32x4*)(kr_hi + kslot * KSTR + D / 2 + kpart * FP + 8 * c);
+      if constexpr (X3) {
+        u32x4 h1, l1, h2, l2;
+        split_bf16x8(o1, h1, l1);
+        split_bf16x8(o2, h2, l2);
+        *d1 = h1;
+        *d2 = h2;
+        *(u32x4*)(kr_lo + kslot * KSTR + kpart * FP + 8 * c) = l1;
+        *(u32x4*)(kr_lo + kslot * KSTR + D / 2 + kpart * FP + 8 * c) = l2;
+      } else {
+        *d1 = pack_bf16x8(o1);
+        *d2 = pack_bf16x8(o2);
+      }
+    }
+#pragma unroll
+    for (int vu = 0; vu < VU; ++vu) {
+      const int u = tid + vu * NT;
+      if (u >= Cfg::VUNITS) continue;
       const int sg = u / (D / 8), dc = u % (D / 8);
       float vv[4][8];
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const int s = s0 + sg * 4 + k;
-        const int j = s < a.k_max ? idx[s] : N;
-        if ((unsigned)j < (unsigned)N) {
-          load8<DT>(a.v, vbase + (int64_t)j * a.v_tok_stride + dc * 8, vv[k]);
-        } else {
-#pragma unroll
-          for (int e = 0; e < 8; ++e) vv[k][e] = 0.0f;
-        }
-      }
+      for (int k = 0; k < 4; ++k) vx[vu][k].to_f32(vv[k]);
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        float col[4] = {vv[0][e], vv[1][e], vv[2][e], vv[3][e]};
         u32x2 w;
         if constexpr (DT == DT_F16) {
-          w[0] = f32_to_f16_bits(col[0]) | (f32_to_f16_bits(col[1]) << 16);
-          w[1] = f32_to_f16_bits(col[2]) | (f32_to_f16_bits(col[3]) << 16);
+          w[0] = f32_to_f16_bits(vv[0][e]) | (f32_to_f16_bits(vv[1][e]) << 16);
+          w[1] = f32_to_f16_bits(vv[2][e]) | (f32_to_f16_bits(vv[3][e]) << 16);
         } else {
-          w[0] = f32_to_bf16_bits(col[0]) | (f32_to_bf16_bits(col[1]) << 16);
-          w[1] = f32_to_bf16_bits(col[2]) | (f32_to_bf16_bits(col[3]) << 16);
+          w[0] = f32_to_bf16_bits(vv[0][e]) | (f32_to_bf16_bits(vv[1][e]) << 16);
+          w[1] = f32_to_bf16_bits(vv[2][e]) | (f32_to_bf16_bits(vv[3][e]) << 16);
         }
         *(u32x2*)(vt_hi + (dc * 8 + e) * VSTR + sg * 4) = w;
         if constexpr (X3) {
-          u32x2 wl;
           float lo[4];
 #pragma unroll
-          for (int k = 0; k < 4; ++k) lo[k] = col[k] - bf16_bits_to_f32(f32_to_bf16_bits(col[k]));
+          for (int k = 0; k < 4; ++k) lo[k] = vv[k][e] - bf16_bits_to_f32(f32_to_bf16_bits(vv[k][e]));
+          u32x2 wl;
           wl[0] = f32_to_bf16_bits(lo[0]) | (f32_to_bf16_bits(lo[1]) << 16);
           wl[1] = f32_to_bf16_bits(lo[2]) | (f32_to_bf16_bits(lo[3]) << 16);
           *(u32x2*)(vt_lo + (dc * 8 + e) * VSTR + sg * 4) = wl;
         }
       }
     }
+  };
+
+  floatx4 oacc[DB];
+#pragma unroll
+  for (int db = 0; db < DB; ++db) oacc[db] = floatx4{0.f, 0.f, 0.f, 0.f};
+  float mR = -INFINITY, l_i = 0.0f;
+
+  if (nblk > 0) load_block(0);
+  for (int b = 0; b < nblk; ++b) {
+    const int s0 = b * 64;
+    store_block(b);
     __syncthreads();
+    if (b + 1 < nblk) load_block(b + 1);   // in flight while this block is attended
 
     // ---- S^T = K_rot . Q_rot^T for 64 slots x this wave's 16 rows ----
     floatx4 sacc[4];
@@ -225,9 +280,8 @@ __global__ __launch_bounds__(NW * 64) void gather_kernel(GatherArgs a) {
       const int sl = s0 + sb * 16 + 4 * (lane >> 4);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int s = sl + i;
-        const int j = s < a.k_max ? idx[s] : N;
-        const bool keep = ((unsigned)j < (unsigned)N) && (qpos >= j);
+        const int j = sidx[sl + i];
+        const bool keep = ((unsigned)j < (unsigned)N) && (qpos >= j);   // causal on original positions
         const float v = keep ? sacc[sb][i] * a.sm_scale : -INFINITY;
         p[sb][i] = v;
         bmax = fmaxf(bmax, v);
@@ -315,11 +369,17 @@ __global__ __launch_bounds__(NW * 64) void gather_kernel(GatherArgs a) {
 template <int DT, int D, int NW>
 static hipError_t launch_gather_t(const GatherArgs& a, hipStream_t st) {
   using Cfg = GatherCfg<DT, D, NW>;
+  const size_t lds = Cfg::lds_bytes(a.k_max);
   hipError_t e = hipFuncSetAttribute((const void*)gather_kernel<DT, D, NW>,
-                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)Cfg::LDS);
+                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL((gather_kernel<DT, D, NW>), dim3(a.H * a.nt), dim3(Cfg::NT), Cfg::LDS, st, a);
+  hipLaunchKernelGGL((gather_kernel<DT, D, NW>), dim3(a.H * a.nt), dim3(Cfg::NT), lds, st, a);
   return hipGetLastError();
+}
+
+size_t gather_lds_bytes(int dtype, int D, int k_max) {
+  const size_t fixed = (dtype == DT_F32 ? 2 : 1) * ((size_t)64 * (D + 8) * 2 + (size_t)D * 72 * 2);
+  return fixed + (size_t)((k_max + 63) / 64) * 64 * 8;
 }
 
 hipError_t launch_gather(int dtype, int D, int tile, const GatherArgs& a, hipStream_t st) {

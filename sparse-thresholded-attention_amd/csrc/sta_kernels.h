@@ -65,6 +65,7 @@ size_t select_lds_bytes(int N, int k_max);
 hipError_t launch_select(const SelectArgs& a, int vote_bytes, hipStream_t st);
 hipError_t launch_expand_votes(const uint8_t* v8, int64_t stride, int H, int nt, int N, int T,
                                int q_pos_base, int32_t* out, hipStream_t st);
+size_t gather_lds_bytes(int dtype, int D, int k_max);
 hipError_t launch_gather(int dtype, int D, int tile, const GatherArgs& a, hipStream_t st);
 
 }  // namespace sta
