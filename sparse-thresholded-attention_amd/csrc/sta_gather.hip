@@ -7,7 +7,7 @@
 // always sweeps all k_max slots; slots past min(kept_size, k_max) are sentinels that contribute
 // exactly nothing to the online softmax, so they are skipped.
 //
-// One workgroup per (head, tile); wave w owns query rows 16w .. 16w+15.  Scores are computed
+// One workgroup per (head, tile); consumer wave w owns query rows 16w .. 16w+15.  Scores are computed
 // transposed, S^T = K_rot . Q_rot^T (16x16x32 MFMA, lane <-> query row), so the P fragment the
 // P.V product needs as its B operand is exactly the score accumulator the lane already holds:
 //   O^T (dims x rows) += V^T (dims x slots) . P^T (slots x rows)
@@ -21,18 +21,22 @@ namespace sta {
 
 template <int DT, int D, int NW>
 struct GatherCfg {
-  static constexpr int NT = NW * 64;           // threads
-  static constexpr int TPS = NT / 64;          // threads per slot for the K rotation
-  static constexpr int FP = (D / 2) / TPS;     // frequencies per thread
+  static constexpr int NC = NW * 64;           // consumer threads: wave w attends rows 16w..16w+15
+  static constexpr int NP = 256;               // producer threads: gather, rotate, stage K / V
+  static constexpr int NT = NC + NP;
+  static constexpr int TPS = NP / 64;          // producer threads per slot for the K rotation
+  static constexpr int FP = (D / 2) / TPS;     // frequencies per producer thread
   static constexpr int VUNITS = 16 * (D / 8);  // (4 slots x 8 dims) V units per block
-  static constexpr int VU = (VUNITS + NT - 1) / NT;   // V units per thread
+  static constexpr int VU = (VUNITS + NP - 1) / NP;   // V units per producer thread
   static constexpr bool X3 = (DT == DT_F32);   // fp32 inputs: three-term bf16 products
   static constexpr int KSTR = D + 8;           // K LDS row stride (bf16 elements)
   static constexpr int VSTR = 64 + 8;          // V^T LDS row stride (elements)
   static constexpr int KHALVES = X3 ? 2 : 1;
-  static constexpr size_t LDS_FIXED = (size_t)KHALVES * 64 * KSTR * 2 + (size_t)KHALVES * D * VSTR * 2;
-  // + the tile's idx and newpos_k (8 bytes per slot, rounded up to whole 64-slot blocks)
-  static size_t lds_bytes(int k_max) { return LDS_FIXED + (size_t)((k_max + 63) / 64) * 64 * 8; }
+  static constexpr int KBUF = KHALVES * 64 * KSTR;     // elements of one K buffer
+  static constexpr int VBUF = KHALVES * D * VSTR;      // elements of one V^T buffer
+  static constexpr size_t LDS_FIXED = (size_t)2 * (KBUF + VBUF) * 2;   // double-buffered
+  // + the tile's kept positions (4 bytes per slot, rounded up to whole 64-slot blocks)
+  static size_t lds_bytes(int k_max) { return LDS_FIXED + (size_t)((k_max + 63) / 64) * 64 * 4; }
 };
 
 // 8 consecutive elements in their storage format (loaded now, converted later)
@@ -69,26 +73,30 @@ struct Raw8<DT_F32> {
   }
 };
 
+// One workgroup per (head, tile), specialised waves.  Producer waves gather block b + 1's K and
+// V rows (issued one block ahead of that), rotate K and write both to one half of a
+// double-buffered LDS area while the consumer waves attend block b from the other half; one
+// barrier per block hands the halves over.  A block then costs max(produce, consume).
 template <int DT, int D, int NW>
-__global__ __launch_bounds__(NW * 64) void gather_kernel(GatherArgs a) {
+__global__ __launch_bounds__(NW * 64 + 256, 1) void gather_kernel(GatherArgs a) {
   using Cfg = GatherCfg<DT, D, NW>;
-  constexpr int NT = Cfg::NT, TPS = Cfg::TPS, FP = Cfg::FP, VU = Cfg::VU;
+  constexpr int NC = Cfg::NC, NT = Cfg::NT, TPS = Cfg::TPS, FP = Cfg::FP, VU = Cfg::VU;
   constexpr bool X3 = Cfg::X3;
   constexpr int KSTR = Cfg::KSTR, VSTR = Cfg::VSTR;
   constexpr int T = NW * 16;
   constexpr int KS = D / 32;                   // k steps of the score MFMA
   constexpr int DB = D / 16;                   // 16-dim blocks of the output
   extern __shared__ __align__(16) uint16_t sh[];
-  uint16_t* kr_hi = sh;                                    // [64][KSTR]
-  uint16_t* kr_lo = sh + 64 * KSTR;                        // [64][KSTR] (X3 only)
-  uint16_t* vt_hi = sh + Cfg::KHALVES * 64 * KSTR;         // [D][VSTR]
-  uint16_t* vt_lo = vt_hi + D * VSTR;                      // [D][VSTR] (X3 only)
+  // buffer p: K [64][KSTR] (hi, then lo when X3) followed by V^T [D][VSTR] (hi, then lo)
+  auto kbuf = [&](int p) { return sh + p * (Cfg::KBUF + Cfg::VBUF); };
+  auto vbuf = [&](int p) { return sh + p * (Cfg::KBUF + Cfg::VBUF) + Cfg::KBUF; };
   int32_t* sidx = (int32_t*)(sh + Cfg::LDS_FIXED / 2);     // the tile's kept positions
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const bool consumer = tid < NC;
   int h, t;
   {
     const int bid = blockIdx.x;
-    if ((a.H & 7) == 0) {
+    if ((a.H & 7) == 0) {   // XCD-aware: keep a head's tiles on one XCD (workgroup i -> XCD i % 8)
       const int hpx = a.H >> 3;
       const int r = bid >> 3;
       h = (bid & 7) * hpx + r % hpx;
@@ -105,21 +113,136 @@ __global__ __launch_bounds__(NW * 64) void gather_kernel(GatherArgs a) {
   const int64_t tile_off = ((int64_t)h * a.nt + t) * a.k_max;
   const int nvalid = a.kept_size ? min(a.kept_size[h * a.nt + t], a.k_max) : a.k_max;
   const int nblk = (nvalid + 63) / 64;
-  float* snpk = (float*)(sidx + nblk * 64);
-  const int64_t kbase = (int64_t)kvh * a.k_head_stride;
-  const int64_t vbase = (int64_t)kvh * a.v_head_stride;
 
-  // ---- stage the tile's slots (sentinel N past the kept count) ----
-  for (int s = tid; s < nblk * 64; s += NT) {
-    sidx[s] = s < nvalid ? a.idx[tile_off + s] : N;
-    snpk[s] = s < nvalid ? a.newpos_k[tile_off + s] : 0.0f;
+  // ---- stage the tile's kept positions (sentinel N past the kept count) ----
+  for (int s = tid; s < nblk * 64; s += NT) sidx[s] = s < nvalid ? a.idx[tile_off + s] : N;
+  __syncthreads();
+
+  if (!consumer) {
+    // =================================== producers ===================================
+    const int ptid = tid - NC;
+    const int kslot = ptid / TPS, kpart = ptid % TPS;
+    const int64_t kbase = (int64_t)kvh * a.k_head_stride;
+    const int64_t vbase = (int64_t)kvh * a.v_head_stride;
+    Raw8<DT> kx1[FP / 8], kx2[FP / 8], vx[VU][4];
+    float np = 0.0f;
+    auto load_block = [&](int b) {
+      const int j = sidx[b * 64 + kslot];
+      if ((unsigned)j < (unsigned)N) {   // sentinel N (and any out-of-range index) -> zero row
+        np = a.newpos_k[tile_off + b * 64 + kslot];
+        const int64_t rb = kbase + (int64_t)j * a.k_tok_stride + kpart * FP;
+#pragma unroll
+        for (int c = 0; c < FP / 8; ++c) {
+          kx1[c].load(a.k, rb + 8 * c);
+          kx2[c].load(a.k, rb + D / 2 + 8 * c);
+        }
+      } else {
+#pragma unroll
+        for (int c = 0; c < FP / 8; ++c) { kx1[c].zero(); kx2[c].zero(); }
+      }
+#pragma unroll
+      for (int vu = 0; vu < VU; ++vu) {
+        const int u = ptid + vu * 256;
+        const int sg = (u / (D / 8)) & 15, dc = u % (D / 8);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const int jv = sidx[b * 64 + sg * 4 + k];
+          if (u < Cfg::VUNITS && (unsigned)jv < (unsigned)N)
+            vx[vu][k].load(a.v, vbase + (int64_t)jv * a.v_tok_stride + dc * 8);
+          else
+            vx[vu][k].zero();
+        }
+      }
+    };
+    // rotate K at newpos_k (exact_2.py:203-207); write K and V^T of block b to buffer b & 1
+    auto store_block = [&](int b) {
+      uint16_t* kr_hi = kbuf(b & 1);
+      uint16_t* kr_lo = kr_hi + 64 * KSTR;
+      uint16_t* vt_hi = vbuf(b & 1);
+      uint16_t* vt_lo = vt_hi + D * VSTR;
+#pragma unroll
+      for (int c = 0; c < FP / 8; ++c) {
+        float x1[8], x2[8], o1[8], o2[8];
+        kx1[c].to_f32(x1);
+        kx2[c].to_f32(x2);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          float sn, cs;
+          fast_sincos(np * invf[kpart * FP + 8 * c + e], sn, cs);
+          cs *= rs;
+          sn *= rs;
+          o1[e] = x1[e] * cs - x2[e] * sn;
+          o2[e] = x2[e] * cs + x1[e] * sn;
+        }
+        u32x4* d1 = (u32x4*)(kr_hi + kslot * KSTR + kpart * FP + 8 * c);
+        u32x4* d2 = (u32x4*)(kr_hi + kslot * KSTR + D / 2 + kpart * FP + 8 * c);
+        if constexpr (X3) {
+          u32x4 h1, l1, h2, l2;
+          split_bf16x8(o1, h1, l1);
+          split_bf16x8(o2, h2, l2);
+          *d1 = h1;
+          *d2 = h2;
+          *(u32x4*)(kr_lo + kslot * KSTR + kpart * FP + 8 * c) = l1;
+          *(u32x4*)(kr_lo + kslot * KSTR + D / 2 + kpart * FP + 8 * c) = l2;
+        } else {
+          *d1 = pack_bf16x8(o1);
+          *d2 = pack_bf16x8(o2);
+        }
+      }
+#pragma unroll
+      for (int vu = 0; vu < VU; ++vu) {
+        const int u = ptid + vu * 256;
+        if (u >= Cfg::VUNITS) continue;
+        const int sg = u / (D / 8), dc = u % (D / 8);
+        float vv[4][8];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) vx[vu][k].to_f32(vv[k]);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          u32x2 w;
+          if constexpr (DT == DT_F16) {
+            w[0] = f32_to_f16_bits(vv[0][e]) | (f32_to_f16_bits(vv[1][e]) << 16);
+            w[1] = f32_to_f16_bits(vv[2][e]) | (f32_to_f16_bits(vv[3][e]) << 16);
+          } else {
+            w[0] = f32_to_bf16_bits(vv[0][e]) | (f32_to_bf16_bits(vv[1][e]) << 16);
+            w[1] = f32_to_bf16_bits(vv[2][e]) | (f32_to_bf16_bits(vv[3][e]) << 16);
+          }
+          *(u32x2*)(vt_hi + (dc * 8 + e) * VSTR + sg * 4) = w;
+          if constexpr (X3) {
+            float lo[4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) lo[k] = vv[k][e] - bf16_bits_to_f32(f32_to_bf16_bits(vv[k][e]));
+            u32x2 wl;
+            wl[0] = f32_to_bf16_bits(lo[0]) | (f32_to_bf16_bits(lo[1]) << 16);
+            wl[1] = f32_to_bf16_bits(lo[2]) | (f32_to_bf16_bits(lo[3]) << 16);
+            *(u32x2*)(vt_lo + (dc * 8 + e) * VSTR + sg * 4) = wl;
+          }
+        }
+      }
+    };
+    if (nblk > 0) {
+      load_block(0);
+      store_block(0);
+      if (nblk > 1) load_block(1);
+    }
+    __syncthreads();
+    for (int b = 0; b < nblk; ++b) {
+      if (b + 1 < nblk) {
+        store_block(b + 1);                  // rows loaded one block earlier
+        if (b + 2 < nblk) load_block(b + 2); // in flight during the next block
+      }
+      __syncthreads();
+    }
+    return;
   }
 
-  // ---- this lane's query row, rotated at newpos_q (exact_2.py:174-185) ----
+  // =================================== consumers ===================================
+  // this lane's query row, rotated at newpos_q (exact_2.py:174-185)
   const int r = wave * 16 + (lane & 15);
   const int qrow = t * T + r;
   const bool row_ok = qrow < N;
   const int64_t qpos = (int64_t)a.q_pos_base + qrow;
+  const int64_t qpos_first = (int64_t)a.q_pos_base + (int64_t)t * T;
   u32x4 qf_hi[KS], qf_lo[KS];
   {
     const float npq = a.newpos_q[((int64_t)h * a.nt + t) * T + r];
@@ -149,112 +272,19 @@ __global__ __launch_bounds__(NW * 64) void gather_kernel(GatherArgs a) {
       else qf_hi[ks] = pack_bf16x8(out);
     }
   }
-  __syncthreads();
-
-  // ---- raw K / V rows of one block, held in registers until the LDS buffers are free ----
-  const int kslot = tid / TPS, kpart = tid % TPS;
-  Raw8<DT> kx1[FP / 8], kx2[FP / 8], vx[VU][4];
-  auto load_block = [&](int b) {
-    const int j = sidx[b * 64 + kslot];
-    if ((unsigned)j < (unsigned)N) {   // sentinel N (and any out-of-range index) -> zero row
-      const int64_t rb = kbase + (int64_t)j * a.k_tok_stride + kpart * FP;
-#pragma unroll
-      for (int c = 0; c < FP / 8; ++c) {
-        kx1[c].load(a.k, rb + 8 * c);
-        kx2[c].load(a.k, rb + D / 2 + 8 * c);
-      }
-    } else {
-#pragma unroll
-      for (int c = 0; c < FP / 8; ++c) { kx1[c].zero(); kx2[c].zero(); }
-    }
-#pragma unroll
-    for (int vu = 0; vu < VU; ++vu) {
-      const int u = tid + vu * NT;
-      const int sg = u / (D / 8), dc = u % (D / 8);
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const int jv = sidx[b * 64 + (sg * 4 + k) % 64];
-        if (u < Cfg::VUNITS && (unsigned)jv < (unsigned)N) vx[vu][k].load(a.v, vbase + (int64_t)jv * a.v_tok_stride + dc * 8);
-        else vx[vu][k].zero();
-      }
-    }
-  };
-  // rotate K at newpos_k (exact_2.py:203-207) and write K and V^T of the block to LDS
-  auto store_block = [&](int b) {
-    const float np = snpk[b * 64 + kslot];
-#pragma unroll
-    for (int c = 0; c < FP / 8; ++c) {
-      float x1[8], x2[8], o1[8], o2[8];
-      kx1[c].to_f32(x1);
-      kx2[c].to_f32(x2);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        float sn, cs;
-        fast_sincos(np * invf[kpart * FP + 8 * c + e], sn, cs);
-        cs *= rs;
-        sn *= rs;
-        o1[e] = x1[e] * cs - x2[e] * sn;
-        o2[e] = x2[e] * cs + x1[e] * sn;
-      }
-      u32x4* d1 = (u32x4*)(kr_hi + kslot * KSTR + kpart * FP + 8 * c);
-      u32x4* d2 = (u32x4*)(kr_hi + kslot * KSTR + D / 2 + kpart * FP + 8 * c);
-      if constexpr (X3) {
-        u32x4 h1, l1, h2, l2;
-        split_bf16x8(o1, h1, l1);
-        split_bf16x8(o2, h2, l2);
-        *d1 = h1;
-        *d2 = h2;
-        *(u32x4*)(kr_lo + kslot * KSTR + kpart * FP + 8 * c) = l1;
-        *(u32x4*)(kr_lo + kslot * KSTR + D / 2 + kpart * FP + 8 * c) = l2;
-      } else {
-        *d1 = pack_bf16x8(o1);
-        *d2 = pack_bf16x8(o2);
-      }
-    }
-#pragma unroll
-    for (int vu = 0; vu < VU; ++vu) {
-      const int u = tid + vu * NT;
-      if (u >= Cfg::VUNITS) continue;
-      const int sg = u / (D / 8), dc = u % (D / 8);
-      float vv[4][8];
-#pragma unroll
-      for (int k = 0; k < 4; ++k) vx[vu][k].to_f32(vv[k]);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        u32x2 w;
-        if constexpr (DT == DT_F16) {
-          w[0] = f32_to_f16_bits(vv[0][e]) | (f32_to_f16_bits(vv[1][e]) << 16);
-          w[1] = f32_to_f16_bits(vv[2][e]) | (f32_to_f16_bits(vv[3][e]) << 16);
-        } else {
-          w[0] = f32_to_bf16_bits(vv[0][e]) | (f32_to_bf16_bits(vv[1][e]) << 16);
-          w[1] = f32_to_bf16_bits(vv[2][e]) | (f32_to_bf16_bits(vv[3][e]) << 16);
-        }
-        *(u32x2*)(vt_hi + (dc * 8 + e) * VSTR + sg * 4) = w;
-        if constexpr (X3) {
-          float lo[4];
-#pragma unroll
-          for (int k = 0; k < 4; ++k) lo[k] = vv[k][e] - bf16_bits_to_f32(f32_to_bf16_bits(vv[k][e]));
-          u32x2 wl;
-          wl[0] = f32_to_bf16_bits(lo[0]) | (f32_to_bf16_bits(lo[1]) << 16);
-          wl[1] = f32_to_bf16_bits(lo[2]) | (f32_to_bf16_bits(lo[3]) << 16);
-          *(u32x2*)(vt_lo + (dc * 8 + e) * VSTR + sg * 4) = wl;
-        }
-      }
-    }
-  };
 
   floatx4 oacc[DB];
 #pragma unroll
   for (int db = 0; db < DB; ++db) oacc[db] = floatx4{0.f, 0.f, 0.f, 0.f};
   float mR = -INFINITY, l_i = 0.0f;
+  __syncthreads();   // block 0 is staged
 
-  if (nblk > 0) load_block(0);
   for (int b = 0; b < nblk; ++b) {
     const int s0 = b * 64;
-    store_block(b);
-    __syncthreads();
-    if (b + 1 < nblk) load_block(b + 1);   // in flight while this block is attended
-
+    const uint16_t* kr_hi = kbuf(b & 1);
+    const uint16_t* kr_lo = kr_hi + 64 * KSTR;
+    const uint16_t* vt_hi = vbuf(b & 1);
+    const uint16_t* vt_lo = vt_hi + D * VSTR;
     // ---- S^T = K_rot . Q_rot^T for 64 slots x this wave's 16 rows ----
     floatx4 sacc[4];
 #pragma unroll
@@ -273,15 +303,20 @@ __global__ __launch_bounds__(NW * 64) void gather_kernel(GatherArgs a) {
       }
     }
     // ---- mask + online softmax (exact_2.py:209-217) ----
+    // slots ascend and sentinels trail, so a block whose last slot is a real key before the
+    // tile's first query needs no causal mask for any row
+    const int jlast = sidx[s0 + 63];
+    const bool unmasked = jlast < N && jlast <= qpos_first;
     float p[4][4];
     float bmax = -INFINITY;
 #pragma unroll
     for (int sb = 0; sb < 4; ++sb) {
       const int sl = s0 + sb * 16 + 4 * (lane >> 4);
+      const int4 j4 = *(const int4*)(sidx + sl);
+      const int jj[4] = {j4.x, j4.y, j4.z, j4.w};
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int j = sidx[sl + i];
-        const bool keep = ((unsigned)j < (unsigned)N) && (qpos >= j);   // causal on original positions
+        const bool keep = unmasked || (((unsigned)jj[i] < (unsigned)N) && (qpos >= jj[i]));  // exact_2.py:210
         const float v = keep ? sacc[sb][i] * a.sm_scale : -INFINITY;
         p[sb][i] = v;
         bmax = fmaxf(bmax, v);
@@ -337,7 +372,7 @@ __global__ __launch_bounds__(NW * 64) void gather_kernel(GatherArgs a) {
         }
       }
     }
-    __syncthreads();
+    __syncthreads();   // hand this buffer back to the producers
   }
 
   // ---- out = acc / l (exact_2.py:223-225) ----
@@ -378,8 +413,9 @@ static hipError_t launch_gather_t(const GatherArgs& a, hipStream_t st) {
 }
 
 size_t gather_lds_bytes(int dtype, int D, int k_max) {
-  const size_t fixed = (dtype == DT_F32 ? 2 : 1) * ((size_t)64 * (D + 8) * 2 + (size_t)D * 72 * 2);
-  return fixed + (size_t)((k_max + 63) / 64) * 64 * 8;
+  const size_t halves = dtype == DT_F32 ? 2 : 1;
+  const size_t fixed = 2 * halves * ((size_t)64 * (D + 8) * 2 + (size_t)D * 72 * 2);
+  return fixed + (size_t)((k_max + 63) / 64) * 64 * 4;
 }
 
 hipError_t launch_gather(int dtype, int D, int tile, const GatherArgs& a, hipStream_t st) {
