@@ -41,9 +41,25 @@ def parse():
     ap.add_argument("--config", default="c1")
     ap.add_argument("--cpu-baseline-seconds", type=float, default=15.0,
                     help="target CPU time of the oracle sample (0 disables it)")
-    ap.add_argument("--traffic-file", default=None,
-                    help="rocprofv3 FETCH_SIZE/WRITE_SIZE summary with a 'traffic_bytes' line")
+    ap.add_argument("--traffic-file", default=os.path.join(ROOT, "profiles", "prefill_c1_hbm_traffic.md"),
+                    help="summary of the rocprofv3 FETCH_SIZE/WRITE_SIZE runs, with one "
+                         "'<kernel> traffic_bytes: <bytes per launch>' line per kernel")
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
+                    help="only run a plain device-to-device copy of MIB MiB (3 times) and exit: "
+                         "the known-size reference for the HBM byte counters")
     return ap.parse_args()
+
+
+def calibrate_copy(mib):
+    import torch
+    n = mib * 1024 * 1024
+    src = torch.ones(n, dtype=torch.uint8, device="cuda:0")
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"calibration_copy_bytes": n, "launches": 3}), flush=True)
+    return 0
 
 
 def gather_bytes(kept, k_max, D, esz, H, N):
@@ -53,12 +69,15 @@ def gather_bytes(kept, k_max, D, esz, H, N):
     return slots * 2 * D * esz + slots * 8 + 2 * H * N * D * esz
 
 
-def read_traffic(path):
+def read_traffic(path, kernel):
+    """HBM bytes per launch of `kernel` from the counter summary (None when not measured)."""
     if not path or not os.path.exists(path):
         return None
+    key = f"{kernel} traffic_bytes:"
     for line in open(path):
-        if line.startswith("traffic_bytes"):
-            return float(line.split(":", 1)[1].split()[0])
+        line = line.strip().strip("`")
+        if line.startswith(key):
+            return float(line[len(key):].split()[0])
     return None
 
 
@@ -91,6 +110,8 @@ def cpu_baseline(cfg, q, k, v, invf, ps, rs, budget_s):
 
 def main():
     args = parse()
+    if args.calibrate_copy:
+        return calibrate_copy(args.calibrate_copy)
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}, WORLD_SIZE {world}); "
@@ -137,15 +158,15 @@ def main():
     score_tf = cfg.score_flops() / (stage_ms["score"] * 1e-3) / 1e12
     gather_gbs = gbytes / (stage_ms["gather"] * 1e-3) / 1e9
     peak_tf = PEAK_FP32_TFLOPS if q.dtype == torch.float32 else PEAK_BF16_TFLOPS
-    roof_score = {"kernel": "score_kernel (pass 1 + pass 2)", "bound": "mfma", "achieved": round(score_tf, 2),
+    roof_score = {"kernel": "score_kernel", "bound": "mfma", "achieved": round(score_tf, 2),
                   "peak": peak_tf, "unit": "TFLOP/s", "frac": round(score_tf / peak_tf, 4),
                   "algorithmic_per_launch": cfg.score_flops(), "traffic": None}
     roof_gather = {"kernel": "gather_kernel", "bound": "hbm", "achieved": round(gather_gbs, 1),
                    "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(gather_gbs / PEAK_HBM_GBS, 4),
                    "algorithmic_per_launch": int(gbytes), "traffic": None}
+    roof_score["traffic"] = read_traffic(args.traffic_file, "score_kernel")
+    roof_gather["traffic"] = read_traffic(args.traffic_file, "gather_kernel")
     dominant = roof_score if stage_ms["score"] >= stage_ms["gather"] else roof_gather
-    dominant = dict(dominant)
-    dominant["traffic"] = read_traffic(args.traffic_file)
     print(f"[bench] {ms_per_step:.3f} ms/step; stages {stage_ms}", file=sys.stderr, flush=True)
 
     cpu = None
