@@ -37,133 +37,18 @@
 #include <omp.h>
 #endif
 
-/* ------------------------------------------------------------------------------------------- */
-/* scalar conversions                                                                          */
-/* ------------------------------------------------------------------------------------------- */
-static inline float bf16_to_f32(uint16_t h) {
-  uint32_t u = ((uint32_t)h) << 16;
-  float f;
-  memcpy(&f, &u, 4);
-  return f;
-}
-
-static inline uint16_t f32_to_bf16_rne(float f) {
-  uint32_t u;
-  memcpy(&u, &f, 4);
-  if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu)) return (uint16_t)((u >> 16) | 0x40);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return (uint16_t)(u >> 16);
-}
-
-static inline float f16_to_f32(uint16_t h) {
-  uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
-  uint32_t exp = (h >> 10) & 0x1fu;
-  uint32_t man = h & 0x3ffu;
-  uint32_t u;
-  if (exp == 0) {
-    if (man == 0) {
-      u = sign;
-    } else { /* subnormal: value = man * 2^-24 */
-      float f = (float)man * 5.9604644775390625e-08f;
-      memcpy(&u, &f, 4);
-      u |= sign;
-    }
-  } else if (exp == 31) {
-    u = sign | 0x7f800000u | (man << 13);
-  } else {
-    u = sign | ((exp + 112u) << 23) | (man << 13);
-  }
-  float f;
-  memcpy(&f, &u, 4);
-  return f;
-}
-
-static inline uint16_t f32_to_f16_rne(float f) {
-  uint32_t u;
-  memcpy(&u, &f, 4);
-  uint32_t sign = (u >> 16) & 0x8000u;
-  uint32_t a = u & 0x7fffffffu;
-  if (a >= 0x7f800000u) return (uint16_t)(sign | 0x7c00u | (a > 0x7f800000u ? 0x200u : 0u));
-  if (a >= 0x477ff000u) return (uint16_t)(sign | 0x7c00u); /* rounds to >= 65520 -> inf */
-  if (a < 0x38800000u) {                                   /* subnormal / zero in fp16 */
-    float af;
-    memcpy(&af, &a, 4);
-    float q = af * 16777216.0f; /* exact: scale by 2^24, then round to integer (RNE) */
-    uint32_t m = (uint32_t)nearbyintf(q);
-    return (uint16_t)(sign | m);
-  }
-  uint32_t exp = ((a >> 23) - 112u) << 10;
-  uint32_t man = (a >> 13) & 0x3ffu;
-  uint32_t rest = a & 0x1fffu;
-  uint32_t h = exp | man;
-  if (rest > 0x1000u || (rest == 0x1000u && (h & 1u))) h += 1u;
-  return (uint16_t)(sign | h);
-}
-
-static inline float load_elem(const void* base, int dtype, size_t i) {
-  if (dtype == 0) return ((const float*)base)[i];
-  if (dtype == 1) return bf16_to_f32(((const uint16_t*)base)[i]);
-  return f16_to_f32(((const uint16_t*)base)[i]);
-}
-
-/* value after a cast to the input dtype (p.to(vv.dtype), exact_2.py:220) */
-static inline float round_to_dtype(float x, int dtype) {
-  if (dtype == 0) return x;
-  if (dtype == 1) return bf16_to_f32(f32_to_bf16_rne(x));
-  return f16_to_f32(f32_to_f16_rne(x));
-}
+#include "sta_oracle_common.h"
 
 void oracle_round_to_dtype(const float* in, void* out, size_t n, int dtype) {
-  for (size_t i = 0; i < n; ++i) {
-    if (dtype == 0) ((float*)out)[i] = in[i];
-    else if (dtype == 1) ((uint16_t*)out)[i] = f32_to_bf16_rne(in[i]);
-    else ((uint16_t*)out)[i] = f32_to_f16_rne(in[i]);
-  }
+  oracle_round_to_dtype_impl(in, out, n, dtype);
 }
 
-void oracle_to_f32(const void* in, float* out, size_t n, int dtype) {
-  for (size_t i = 0; i < n; ++i) out[i] = load_elem(in, dtype, i);
-}
-
-/* ------------------------------------------------------------------------------------------- */
-/* RoPE, half-split (Llama) form                                                               */
-/* ------------------------------------------------------------------------------------------- */
-/* Rotate row x (D values, dtype) at an fp32 angle base `posf` (already pos*pos_scale, or newpos).
- * exact_2.py:74-83 (Kernel A), 174-185 / 199-207 (Kernel C), torch twin _rope_rotate 495-502. */
-static void rope_row(const void* x, int dtype, size_t off, int D, float posf, const float* inv_freq,
-                     float rope_scale, float* out) {
-  const int half = D / 2;
-  for (int i = 0; i < half; ++i) {
-    volatile float ang = posf * inv_freq[i];
-    volatile float c = cosf(ang) * rope_scale;
-    volatile float s = sinf(ang) * rope_scale;
-    float x1 = load_elem(x, dtype, off + i);
-    float x2 = load_elem(x, dtype, off + half + i);
-    volatile float a = x1 * c;
-    volatile float b = x2 * s;
-    volatile float e = x2 * c;
-    volatile float f = x1 * s;
-    out[i] = a - b;
-    out[half + i] = e + f;
-  }
-}
+void oracle_to_f32(const void* in, float* out, size_t n, int dtype) { oracle_to_f32_impl(in, out, n, dtype); }
 
 void oracle_rope_rotate(const void* x, int dtype, int rows, int D, const float* posf,
                         const float* inv_freq, float rope_scale, float* out) {
   for (int r = 0; r < rows; ++r)
     rope_row(x, dtype, (size_t)r * D, D, posf[r], inv_freq, rope_scale, out + (size_t)r * D);
-}
-
-/* fl(fl(dot(a[:h], b[:h]) + dot(a[h:], b[h:])) * sm_scale) with each half dot accumulated in double */
-static inline float score_of(const float* a, const float* b, int D, float sm_scale) {
-  const int half = D / 2;
-  double d1 = 0.0, d2 = 0.0;
-  for (int i = 0; i < half; ++i) d1 += (double)a[i] * (double)b[i];
-  for (int i = half; i < D; ++i) d2 += (double)a[i] * (double)b[i];
-  volatile float f1 = (float)d1;
-  volatile float f2 = (float)d2;
-  volatile float sum = f1 + f2;
-  return sum * sm_scale;
 }
 
 /* ------------------------------------------------------------------------------------------- */
@@ -444,10 +329,11 @@ void oracle_build_sets(const int32_t* votes, int H, int nt, int N, float pos_sca
  * (exact_2.py:223-225); rows >= N are not written.  block_k is the slot block of the online
  * softmax (the reference's BLOCK_K); it matters only through the cast of P to the input dtype.
  */
-void oracle_gather_attn(const void* q, const void* k, const void* v, int dtype, int H, int Hkv,
+static void gather_core(const void* q, const void* k, const void* v, int dtype, int H, int Hkv,
                         int N, int D, const float* inv_freq, float rope_scale, float sm_scale,
                         int tile, int k_max, int block_k, int q_pos_base, const int32_t* idx,
-                        const float* newpos_k, const float* newpos_q, float* out) {
+                        const float* newpos_k, const float* newpos_q, const int32_t* mask,
+                        float* out) {
   const int T = tile;
   const int nt = (N + T - 1) / T;
   const int group = H / Hkv;
@@ -487,6 +373,8 @@ void oracle_gather_attn(const void* q, const void* k, const void* v, int dtype, 
             const int j = irow[s0 + b];
             if (j >= N) continue;           /* padding slot */
             if (qpos < j) continue;         /* causal on ORIGINAL positions (exact_2.py:210) */
+            /* per-query bit test of the PQ Union gather (perquery.py:296-297) */
+            if (mask && !(((uint32_t)mask[((size_t)h * nt + t) * k_max + s0 + b] >> r) & 1u)) continue;
             const float s = score_of(qr, kr + (size_t)(s0 + b) * D, D, sm_scale);
             sblk[b] = s;
             if (s > bmax) bmax = s;
@@ -524,6 +412,25 @@ void oracle_gather_attn(const void* q, const void* k, const void* v, int dtype, 
     free(acc);
     free(dotv);
   }
+}
+
+void oracle_gather_attn(const void* q, const void* k, const void* v, int dtype, int H, int Hkv,
+                        int N, int D, const float* inv_freq, float rope_scale, float sm_scale,
+                        int tile, int k_max, int block_k, int q_pos_base, const int32_t* idx,
+                        const float* newpos_k, const float* newpos_q, float* out) {
+  gather_core(q, k, v, dtype, H, Hkv, N, D, inv_freq, rope_scale, sm_scale, tile, k_max, block_k,
+              q_pos_base, idx, newpos_k, newpos_q, NULL, out);
+}
+
+/* Kernel C of the PQ Union file: the same gather with the per-slot query bitmask
+ * (shared_selection_triton_perquery.py:226-312); mask (H, nt, k_max) int32, bit r = row r. */
+void oracle_gather_attn_mask(const void* q, const void* k, const void* v, int dtype, int H, int Hkv,
+                             int N, int D, const float* inv_freq, float rope_scale, float sm_scale,
+                             int tile, int k_max, int block_k, int q_pos_base, const int32_t* idx,
+                             const float* newpos_k, const float* newpos_q, const int32_t* mask,
+                             float* out) {
+  gather_core(q, k, v, dtype, H, Hkv, N, D, inv_freq, rope_scale, sm_scale, tile, k_max, block_k,
+              q_pos_base, idx, newpos_k, newpos_q, mask, out);
 }
 
 int oracle_num_threads(void) {

@@ -11,6 +11,11 @@ next to it).  Each function names the reference lines it restates:
   gather_attn  <- shared_selection_triton_exact_2.py:146-225  (Kernel C)
   shared_pi_attention <- shared_selection_triton_exact_2.py:432-486 (composition) and, with two
                          geometries, shared_selection_triton_hybrid_exact.py:450-510
+  select_bits  <- shared_selection_triton_perquery.py:119-218 (PQ Union Kernel A)
+  build_sets_pq <- shared_selection_triton_perquery.py:363-453 (_build_sets_pq)
+  gather_attn_mask <- shared_selection_triton_perquery.py:226-312 (PQ Union Kernel C)
+  shared_pq_attention <- shared_selection_triton_perquery.py:459-525 (composition)
+  pqstream     <- pqstream_kernel.py:174-368, 498-564 (the fused PQ Stream kernel)
 
 Arrays are numpy.  Half-precision tensors travel as uint16 bit patterns with a dtype code:
 0 = fp32, 1 = bf16, 2 = fp16.
@@ -38,8 +43,9 @@ def lib():
     global _LIB
     if _LIB is None:
         path = os.path.join(_HERE, "libsta_oracle.so")
-        if not os.path.exists(path) or os.path.getmtime(path) < os.path.getmtime(
-                os.path.join(_HERE, "sta_oracle.c")):
+        srcs = ["sta_oracle.c", "sta_oracle_pq.c", "sta_oracle_common.h"]
+        if not os.path.exists(path) or any(os.path.getmtime(path) < os.path.getmtime(
+                os.path.join(_HERE, f)) for f in srcs):
             build()
         _LIB = ctypes.CDLL(path)
     return _LIB
@@ -205,3 +211,128 @@ def shared_pi_attention(q, k, v, dtype, tau, inv_freq_a, pos_scale_a, rope_scale
     extras = {"votes": a["votes"], "row_max": a["row_max"], "row_counts": a["row_counts"],
               "idx": idx, "newpos_k": npk, "newpos_q": npq}
     return out, ss, ks, ch, oo, km, o20, extras
+
+
+# ---------------------------------------------------------------------------------------------
+# PQ Union (per-query sets through a tile union + bitmask) and PQ Stream
+# ---------------------------------------------------------------------------------------------
+WMODES = {"freq": 0, "margin": 1, "expmass": 2}
+
+
+def select_bits(q, k, dtype, tau, inv_freq, pos_scale, rope_scale, sm_scale, tile=32, q_pos_base=0,
+                wmode=2, band_eps=1e-3, want_band=False):
+    """PQ Union Kernel A (perquery.py:119-218).  Returns a dict with votes, bits (int32, bit i =
+    row i), wvotes (fp32, zeros for wmode 0), row_counts, row_max and optionally band/band_rows."""
+    q = np.ascontiguousarray(q)
+    k = np.ascontiguousarray(k)
+    H, N, D = q.shape
+    Hkv = k.shape[0]
+    nt = (N + tile - 1) // tile
+    votes = np.empty((H, nt, N), np.int32)
+    bits = np.empty((H, nt, N), np.int32)
+    wv = np.zeros((H, nt, N), np.float32)
+    rc = np.empty((H, N), np.int32)
+    rm = np.empty((H, N), np.float32)
+    band = np.empty((H, nt, N), np.int32) if want_band else None
+    band_rows = np.empty((H, N), np.int32) if want_band else None
+    lib().oracle_select_bits(
+        _p(q), _p(k), ctypes.c_int(dtype), ctypes.c_int(H), ctypes.c_int(Hkv), ctypes.c_int(N),
+        ctypes.c_int(D), _p(_c(tau, np.float32)), _p(_c(inv_freq, np.float32)),
+        ctypes.c_float(pos_scale), ctypes.c_float(rope_scale), ctypes.c_float(sm_scale),
+        ctypes.c_int(tile), ctypes.c_int(q_pos_base), ctypes.c_int(wmode), _p(votes), _p(bits),
+        _p(wv) if wmode > 0 else None, _p(rc), _p(rm), _p(band), _p(band_rows),
+        ctypes.c_float(band_eps))
+    out = {"votes": votes, "bits": bits, "wvotes": wv, "row_counts": rc, "row_max": rm}
+    if want_band:
+        out["band"] = band
+        out["band_rows"] = band_rows
+    return out
+
+
+def build_sets_pq(votes, bits, wvotes, n_global, n_local, T, k_max, q_pos_base=0, rank_mode=2):
+    """_build_sets_pq (perquery.py:363-453).  rank_mode 0 ranks overflow candidates by votes,
+    otherwise by wvotes + 1e-6 votes.  Returns (idx, newpos_k, newpos_q, mask, usize, kept_size,
+    overflow) as numpy arrays; equal rank values at the cut are taken in ascending key order."""
+    votes = _c(votes, np.int32)
+    bits = _c(bits, np.int32)
+    H, nt, N = votes.shape
+    wv = _c(wvotes, np.float32) if (wvotes is not None and rank_mode != 0) else None
+    idx = np.empty((H, nt, k_max), np.int32)
+    npk = np.empty((H, nt, k_max), np.float32)
+    npq = np.empty((H, nt, T), np.float32)
+    mask = np.empty((H, nt, k_max), np.int32)
+    us = np.empty((H, nt), np.int32)
+    ks = np.empty((H, nt), np.int32)
+    ov = np.empty((H, nt), np.uint8)
+    lib().oracle_build_sets_pq(
+        _p(votes), _p(bits), _p(wv), ctypes.c_int(H), ctypes.c_int(nt), ctypes.c_int(N),
+        ctypes.c_int(n_global), ctypes.c_int(n_local), ctypes.c_int(T), ctypes.c_int(k_max),
+        ctypes.c_int(q_pos_base), ctypes.c_int(rank_mode), _p(idx), _p(npk), _p(npq), _p(mask),
+        _p(us), _p(ks), _p(ov))
+    return idx, npk, npq, mask, us, ks, ov.astype(bool)
+
+
+def gather_attn_mask(q, k, v, dtype, idx, newpos_k, newpos_q, mask, inv_freq, rope_scale, sm_scale,
+                     T, k_max, block_k=64, q_pos_base=0):
+    """PQ Union Kernel C (perquery.py:226-312): Kernel C with the per-slot query bitmask."""
+    q = np.ascontiguousarray(q)
+    k = np.ascontiguousarray(k)
+    v = np.ascontiguousarray(v)
+    H, N, D = q.shape
+    Hkv = k.shape[0]
+    out = np.full((H, N, D), np.nan, np.float32)
+    lib().oracle_gather_attn_mask(
+        _p(q), _p(k), _p(v), ctypes.c_int(dtype), ctypes.c_int(H), ctypes.c_int(Hkv),
+        ctypes.c_int(N), ctypes.c_int(D), _p(_c(inv_freq, np.float32)), ctypes.c_float(rope_scale),
+        ctypes.c_float(sm_scale), ctypes.c_int(T), ctypes.c_int(k_max), ctypes.c_int(block_k),
+        ctypes.c_int(q_pos_base), _p(_c(idx, np.int32)), _p(_c(newpos_k, np.float32)),
+        _p(_c(newpos_q, np.float32)), _p(_c(mask, np.int32)), _p(out))
+    return out
+
+
+def shared_pq_attention(q, k, v, dtype, tau, inv_freq_a, inv_freq_c, pos_scale_a=1.0,
+                        rope_scale_a=1.0, sm_scale=None, n_global=32, n_local=32, tile=32,
+                        k_max=4096, block_k=64, q_pos_base=0, select_score="expmass"):
+    """Composition (perquery.py:459-525).  Returns (out_f32, usize, kept_size, overflow, extras)."""
+    H, N, D = q.shape
+    if sm_scale is None:
+        sm_scale = 1.0 / math.sqrt(D)
+    wmode = WMODES[select_score]
+    a = select_bits(q, k, dtype, tau, inv_freq_a, pos_scale_a, rope_scale_a, sm_scale, tile,
+                    q_pos_base, wmode)
+    idx, npk, npq, mask, us, ks, ov = build_sets_pq(a["votes"], a["bits"], a["wvotes"], n_global,
+                                                    n_local, tile, k_max, q_pos_base, wmode)
+    out = gather_attn_mask(q, k, v, dtype, idx, npk, npq, mask, inv_freq_c, 1.0, sm_scale, tile,
+                           k_max, block_k, q_pos_base)
+    extras = dict(a, idx=idx, newpos_k=npk, newpos_q=npq, mask=mask)
+    return out, us, ks, ov, extras
+
+
+def pqstream(q, k, v, dtype, tau, inv_freq_a, inv_freq_c, pos_scale_a=1.0, rope_scale_a=1.0,
+             sm_scale=None, n_global=32, n_local=32, tile=32, block_n=32, pos_advance="max",
+             use_skip=True, band_eps=1e-3):
+    """The fused PQ Stream kernel (pqstream_kernel.py:174-368).  Returns (out_f32, span, kept,
+    blocks, skipped, band_rows)."""
+    q = np.ascontiguousarray(q)
+    k = np.ascontiguousarray(k)
+    v = np.ascontiguousarray(v)
+    H, N, D = q.shape
+    Hkv = k.shape[0]
+    nt = (N + tile - 1) // tile
+    if sm_scale is None:
+        sm_scale = 1.0 / math.sqrt(D)
+    out = np.full((H, N, D), np.nan, np.float32)
+    span = np.empty((H, nt), np.float32)
+    blocks = np.empty((H, nt), np.float32)
+    skipped = np.empty((H, nt), np.float32)
+    kept = np.empty((H, N), np.int32)
+    band_rows = np.empty((H, N), np.int32)
+    lib().oracle_pqstream(
+        _p(q), _p(k), _p(v), ctypes.c_int(dtype), ctypes.c_int(H), ctypes.c_int(Hkv),
+        ctypes.c_int(N), ctypes.c_int(D), _p(_c(tau, np.float32)), _p(_c(inv_freq_a, np.float32)),
+        _p(_c(inv_freq_c, np.float32)), ctypes.c_float(pos_scale_a), ctypes.c_float(rope_scale_a),
+        ctypes.c_float(sm_scale), ctypes.c_int(n_global), ctypes.c_int(n_local), ctypes.c_int(tile),
+        ctypes.c_int(block_n), ctypes.c_int(1 if pos_advance == "full" else 0),
+        ctypes.c_int(int(use_skip)), _p(out), _p(span), _p(kept), _p(blocks), _p(skipped),
+        _p(band_rows), ctypes.c_float(band_eps))
+    return out, span, kept, blocks, skipped, band_rows

@@ -1,0 +1,396 @@
+/*
+ * sta_oracle_pq.c -- CPU restatement of the two per-query variants: PQ Union and PQ Stream.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This file is the checker the HIP product path is compared against.
+ * Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may load it; the product
+ * library never links it and never falls back to it.
+ *
+ * It follows the reference line by line (all citations are into the reference repository):
+ *   oracle_select_bits    <- shared_selection_triton_perquery.py:119-218  (_select_bits_kernel)
+ *   oracle_build_sets_pq  <- shared_selection_triton_perquery.py:363-453  (_build_sets_pq)
+ *   oracle_gather_attn_mask (in sta_oracle.c) <- perquery.py:226-312      (_gather_attn_pq_kernel)
+ *   oracle_pqstream       <- pqstream_kernel.py:174-368                    (_pqstream_kernel)
+ *
+ * fp32 rounding points are those of sta_oracle.c (build with -ffp-contract=off).  The weighted
+ * votes (margin / expmass) are sums over a tile's rows; the reference sums them in fp32 in the
+ * order of its reduction tree, here they are accumulated in double and rounded once, so they
+ * agree with the reference to a few fp32 ulps, not bit for bit.
+ *
+ * Ties in the overflow ranking.  The reference keeps the top-budget candidates by torch.topk
+ * (perquery.py:404-406), whose choice among equal rank values is unspecified.  Here equal rank
+ * values are taken in ascending key order; tests compare modulo the tied keys at the cut.
+ */
+#include "sta_oracle_common.h"
+
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+/* ------------------------------------------------------------------------------------------- */
+/* Kernel A of PQ Union: keep + votes + packed per-query bits + weighted votes                 */
+/* ------------------------------------------------------------------------------------------- */
+/*
+ * votes      (H, nt, N) int32     # of the tile's queries keeping key j           (perquery.py:197)
+ * bits       (H, nt, N) int32     bit i = keep(row i of the tile, key j)          (:200-203)
+ * wvotes     (H, nt, N) fp32/NULL wmode 1: sum of fl(s - fl(m - tau)) over keeping rows (:208-212)
+ *                                 wmode 2: sum of exp(fl(s - m)) over keeping rows      (:213-217)
+ * row_counts (H, N) int32/NULL, row_max (H, N) fp32/NULL, band (H, nt, N) int32/NULL and
+ * band_rows (H, N) int32/NULL as in oracle_select_vote.
+ * tile <= 32 (the reference asserts tile == 32 at its entry point, perquery.py:470).
+ */
+void oracle_select_bits(const void* q, const void* k, int dtype, int H, int Hkv, int N, int D,
+                        const float* tau, const float* inv_freq, float pos_scale, float rope_scale,
+                        float sm_scale, int tile, int q_pos_base, int wmode, int32_t* votes,
+                        int32_t* bits, float* wvotes, int32_t* row_counts, float* row_max,
+                        int32_t* band, int32_t* band_rows, float band_eps) {
+  const int T = tile;
+  const int nt = (N + T - 1) / T;
+  const int group = H / Hkv;
+  const int kmax_key = q_pos_base + nt * T;
+  memset(votes, 0, sizeof(int32_t) * (size_t)H * nt * N);
+  memset(bits, 0, sizeof(int32_t) * (size_t)H * nt * N);
+  if (wvotes) memset(wvotes, 0, sizeof(float) * (size_t)H * nt * N);
+  if (row_counts) memset(row_counts, 0, sizeof(int32_t) * (size_t)H * N);
+  if (band) memset(band, 0, sizeof(int32_t) * (size_t)H * nt * N);
+  if (band_rows) memset(band_rows, 0, sizeof(int32_t) * (size_t)H * N);
+
+  float* krot = (float*)malloc(sizeof(float) * (size_t)Hkv * kmax_key * D);
+  for (int hk = 0; hk < Hkv; ++hk)
+    for (int j = 0; j < kmax_key; ++j) {
+      float* dst = krot + ((size_t)hk * kmax_key + j) * D;
+      if (j < N) {
+        volatile float cp = (float)j * pos_scale;
+        rope_row(k, dtype, ((size_t)hk * N + j) * D, D, cp, inv_freq, rope_scale, dst);
+      } else {
+        memset(dst, 0, sizeof(float) * D);
+      }
+    }
+
+#pragma omp parallel
+  {
+    float* qr = (float*)malloc(sizeof(float) * (size_t)D);
+    float* srow = (float*)malloc(sizeof(float) * (size_t)kmax_key);
+    double* wacc = (double*)malloc(sizeof(double) * (size_t)kmax_key);
+#pragma omp for schedule(dynamic, 1)
+    for (int ht = 0; ht < H * nt; ++ht) {
+      const int h = ht / nt, t = ht % nt;
+      const int hk = h / group;
+      const int hi = q_pos_base + (t + 1) * T; /* perquery.py:161 */
+      const float tau_h = tau[h];
+      for (int j = 0; j < hi; ++j) wacc[j] = 0.0;
+      for (int r = 0; r < T; ++r) {
+        const int row = t * T + r;
+        if (row >= N) continue; /* padded rows never vote (perquery.py:195) */
+        const int qpos = q_pos_base + row;
+        volatile float cp = (float)qpos * pos_scale;
+        rope_row(q, dtype, ((size_t)h * N + row) * D, D, cp, inv_freq, rope_scale, qr);
+        float m = -INFINITY;
+        for (int j = 0; j < hi; ++j) { /* pass 1, perquery.py:164-179 */
+          if (qpos < j) { srow[j] = -INFINITY; continue; }
+          const float s = score_of(qr, krot + ((size_t)hk * kmax_key + j) * D, D, sm_scale);
+          srow[j] = s;
+          if (s > m) m = s;
+        }
+        if (row_max) row_max[(size_t)h * N + row] = m;
+        volatile float thr = m - tau_h;
+        int cnt = 0, nband = 0;
+        for (int j = 0; j < hi; ++j) { /* pass 2, perquery.py:181-217 */
+          if (qpos < j) continue;
+          const float s = srow[j];
+          if (fabsf(s - thr) < band_eps) {
+            nband += 1;
+            if (band && j < N) band[((size_t)h * nt + t) * N + j] += 1;
+          }
+          if (!(s >= thr)) continue;
+          cnt += 1;
+          if (j >= N) continue;
+          const size_t o = ((size_t)h * nt + t) * N + j;
+          votes[o] += 1;
+          bits[o] = (int32_t)((uint32_t)bits[o] | (1u << r));
+          if (wmode == 1) {
+            volatile float c = s - thr;
+            wacc[j] += (double)c;
+          } else if (wmode == 2) {
+            volatile float dl = s - m;
+            wacc[j] += (double)expf(dl);
+          }
+        }
+        if (row_counts) row_counts[(size_t)h * N + row] = cnt;
+        if (band_rows) band_rows[(size_t)h * N + row] = nband;
+      }
+      if (wvotes && wmode > 0)
+        for (int j = 0; j < hi && j < N; ++j) wvotes[((size_t)h * nt + t) * N + j] = (float)wacc[j];
+    }
+    free(qr);
+    free(srow);
+    free(wacc);
+  }
+  free(krot);
+}
+
+/* ------------------------------------------------------------------------------------------- */
+/* _build_sets_pq                                                 perquery.py:363-453           */
+/* ------------------------------------------------------------------------------------------- */
+typedef struct { float v; int j; } rank_item;
+
+static int cmp_rank_desc(const void* a, const void* b) {
+  const rank_item* x = (const rank_item*)a;
+  const rank_item* y = (const rank_item*)b;
+  if (x->v != y->v) return (x->v < y->v) - (x->v > y->v);
+  return (x->j > y->j) - (x->j < y->j); /* equal values: ascending key */
+}
+
+/*
+ * votes, bits (H, nt, N) int32; wvotes (H, nt, N) fp32 or NULL; rank_mode 0 = freq (rank by
+ * votes), otherwise rank by fl(wvotes + fl(1e-6 * votes)) (perquery.py:394-397).
+ * Outputs as perquery.py:446-453: idx (H,nt,k_max) int32 ascending, sentinel N; newpos_k
+ * (H,nt,k_max) fp32 dense ranks (0 at sentinels); newpos_q (H,nt,T) fp32; mask (H,nt,k_max)
+ * int32 (bits at idx, forced -> -1, sentinels -> 0); usize, kept_size (H,nt) int32; overflow
+ * (H,nt) uint8.
+ */
+void oracle_build_sets_pq(const int32_t* votes, const int32_t* bits, const float* wvotes, int H,
+                          int nt, int N, int n_global, int n_local, int T, int k_max,
+                          int q_pos_base, int rank_mode, int32_t* idx, float* newpos_k,
+                          float* newpos_q, int32_t* mask, int32_t* usize, int32_t* kept_size,
+                          uint8_t* overflow) {
+#pragma omp parallel
+  {
+    uint8_t* forced = (uint8_t*)malloc((size_t)N);
+    uint8_t* kept = (uint8_t*)malloc((size_t)N);
+    float* rank0 = (float*)malloc(sizeof(float) * (size_t)N);
+    rank_item* cand = (rank_item*)malloc(sizeof(rank_item) * (size_t)N);
+#pragma omp for schedule(dynamic, 4)
+    for (int ht = 0; ht < H * nt; ++ht) {
+      const int h = ht / nt, t = ht % nt;
+      const size_t row = ((size_t)h * nt + t) * N;
+      const long tstart = (long)q_pos_base + (long)t * T;  /* perquery.py:377 */
+      const long lo = tstart - n_local + 1, hi = tstart + T - 1;
+      long nu = 0, nfull = 0, nforced = 0;
+      for (int j = 0; j < N; ++j) {
+        forced[j] = (j < n_global) || (j >= lo && j <= hi); /* perquery.py:376-381 */
+        const int u = votes[row + j] > 0;                     /* :383 */
+        nu += u;
+        kept[j] = u || forced[j];                             /* :385 */
+        nfull += kept[j];
+        nforced += forced[j];
+      }
+      const int ovf = nfull > k_max;                          /* :386 */
+      if (ovf) {                                              /* :393-410 */
+        long budget = (long)k_max - nforced;
+        if (budget < 0) budget = 0;
+        int nc = 0;
+        for (int j = 0; j < N; ++j) {
+          if (!(votes[row + j] > 0) || forced[j]) continue;   /* cand = union & ~forced */
+          float rv;
+          if (rank_mode == 0 || !wvotes) {
+            rv = (float)votes[row + j];
+          } else {
+            volatile float tb = 1e-6f * (float)votes[row + j];
+            volatile float s = wvotes[row + j] + tb;
+            rv = s;
+          }
+          cand[nc].v = rv;
+          cand[nc].j = j;
+          nc += 1;
+        }
+        qsort(cand, (size_t)nc, sizeof(rank_item), cmp_rank_desc);
+        for (int j = 0; j < N; ++j) kept[j] = forced[j];
+        for (int c = 0; c < nc && c < budget; ++c) kept[cand[c].j] = 1;
+      }
+      long rank = -1, nk = 0;
+      for (int j = 0; j < N; ++j) { /* rank0 = cumsum(kept) - 1   perquery.py:414 */
+        if (kept[j]) { rank += 1; nk += 1; }
+        rank0[j] = (float)rank;
+      }
+      int32_t* irow = idx + ((size_t)h * nt + t) * k_max;
+      float* nkrow = newpos_k + ((size_t)h * nt + t) * k_max;
+      int32_t* mrow = mask + ((size_t)h * nt + t) * k_max;
+      for (int s = 0; s < k_max; ++s) { irow[s] = N; nkrow[s] = 0.0f; mrow[s] = 0; }
+      long slot = 0;
+      for (int j = 0; j < N && slot < k_max; ++j) { /* scatter compaction, :423-433 */
+        if (!kept[j]) continue;
+        irow[slot] = j;
+        nkrow[slot] = rank0[j];
+        mrow[slot] = forced[j] ? -1 : bits[row + j]; /* :437-442 */
+        slot += 1;
+      }
+      float* nqrow = newpos_q + ((size_t)h * nt + t) * T;
+      for (int i = 0; i < T; ++i) { /* :444-446 */
+        long qp = tstart + i;
+        if (qp > N - 1) qp = N - 1;
+        nqrow[i] = rank0[qp];
+      }
+      usize[(size_t)h * nt + t] = (int32_t)nu;
+      kept_size[(size_t)h * nt + t] = (int32_t)nk;
+      overflow[(size_t)h * nt + t] = (uint8_t)ovf;
+    }
+    free(forced);
+    free(kept);
+    free(rank0);
+    free(cand);
+  }
+}
+
+/* ------------------------------------------------------------------------------------------- */
+/* PQ Stream: fused exact max + per-query keep + streamed positions + attend                  */
+/* ------------------------------------------------------------------------------------------- */
+/*
+ * pqstream_kernel.py:174-368, prefill (q_pos_base 0).  One (head, 32-query tile) at a time:
+ *   P_top = min(last row of the tile, N-1), nblk = ceil((P_top+1)/BN)
+ *   pass 1: m_i = exact max of the select-geometry scores over causal keys
+ *   pass 2: blocks t = 0..nblk-1 at start = (nblk-1-t)*BN (descending), hi_t = min(P_top, start+BN-1)
+ *     keep_ij = (s_ij >= m_i - tau | forced_j) & causal & row < N & key < N
+ *     adv = max_i c_i (adv_full: hi_t - start + 1); skipped when adv == 0 and use_skip
+ *     npk_j = -(d + (hi_t - j)), npq_i = qpos_i - P_top, base RoPE (inv_freq_c, scale 1)
+ *     online softmax over kept keys, P cast to the input dtype before P.V; d += adv
+ * out (H, N, D) fp32 accumulator before the final cast; span, blocks, skipped (H, nt) fp32;
+ * kept (H, N) int32 (kept keys per query); band_rows (H, N) int32 or NULL: per query, # of its
+ * causal non-forced keys whose select score lies within band_eps of m - tau.
+ */
+void oracle_pqstream(const void* q, const void* k, const void* v, int dtype, int H, int Hkv, int N,
+                     int D, const float* tau, const float* inv_freq_a, const float* inv_freq_c,
+                     float pos_scale_a, float rope_scale_a, float sm_scale, int n_global,
+                     int n_local, int tile, int block_n, int adv_full, int use_skip, float* out,
+                     float* span, int32_t* kept, float* blocks, float* skipped, int32_t* band_rows,
+                     float band_eps) {
+  const int T = tile, BN = block_n;
+  const int nt = (N + T - 1) / T;
+  const int group = H / Hkv;
+  /* select-geometry keys, rotated once per kv head */
+  float* ks = (float*)malloc(sizeof(float) * (size_t)Hkv * N * D);
+  for (int hk = 0; hk < Hkv; ++hk)
+    for (int j = 0; j < N; ++j) {
+      volatile float cp = (float)j * pos_scale_a;
+      rope_row(k, dtype, ((size_t)hk * N + j) * D, D, cp, inv_freq_a, rope_scale_a,
+               ks + ((size_t)hk * N + j) * D);
+    }
+  if (band_rows) memset(band_rows, 0, sizeof(int32_t) * (size_t)H * N);
+
+#pragma omp parallel
+  {
+    float* qs = (float*)malloc(sizeof(float) * (size_t)T * D);   /* select geometry */
+    float* qa = (float*)malloc(sizeof(float) * (size_t)T * D);   /* attend geometry */
+    float* m = (float*)malloc(sizeof(float) * (size_t)T);
+    float* sel = (float*)malloc(sizeof(float) * (size_t)T * BN);
+    uint8_t* keep = (uint8_t*)malloc((size_t)T * BN);
+    float* kra = (float*)malloc(sizeof(float) * (size_t)BN * D);
+    float* mR = (float*)malloc(sizeof(float) * (size_t)T);
+    float* l = (float*)malloc(sizeof(float) * (size_t)T);
+    float* acc = (float*)malloc(sizeof(float) * (size_t)T * D);
+    int32_t* kr = (int32_t*)malloc(sizeof(int32_t) * (size_t)T);
+    double* dotv = (double*)malloc(sizeof(double) * (size_t)D);
+    float* sblk = (float*)malloc(sizeof(float) * (size_t)BN);
+#pragma omp for schedule(dynamic, 1)
+    for (int ht = 0; ht < H * nt; ++ht) {
+      const int h = ht / nt, t = ht % nt;
+      const int hk = h / group;
+      const int r0 = t * T;
+      const int P_top = (r0 + T - 1 < N - 1) ? r0 + T - 1 : N - 1; /* :203-204 */
+      const int hi = P_top + 1;
+      const int nblk = (hi + BN - 1) / BN;
+      const float tau_h = tau[h];
+      for (int r = 0; r < T; ++r) {
+        const int row = r0 + r;
+        m[r] = -INFINITY;
+        mR[r] = -INFINITY;
+        l[r] = 0.0f;
+        kr[r] = 0;
+        for (int d = 0; d < D; ++d) acc[(size_t)r * D + d] = 0.0f;
+        if (row >= N) continue;
+        volatile float cp = (float)row * pos_scale_a;                 /* :215 */
+        rope_row(q, dtype, ((size_t)h * N + row) * D, D, cp, inv_freq_a, rope_scale_a, qs + (size_t)r * D);
+        volatile float npq = (float)(row - P_top);                    /* :222 */
+        rope_row(q, dtype, ((size_t)h * N + row) * D, D, npq, inv_freq_c, 1.0f, qa + (size_t)r * D);
+        for (int j = 0; j <= row; ++j) {                              /* pass 1, :229-244 */
+          const float s = score_of(qs + (size_t)r * D, ks + ((size_t)hk * N + j) * D, D, sm_scale);
+          if (s > m[r]) m[r] = s;
+        }
+      }
+      const long loc_lo = (long)r0 - n_local + 1, loc_hi = (long)r0 + T - 1; /* :260-261 */
+      float d = 0.0f;
+      int n_used = 0;
+      for (int tb = 0; tb < nblk; ++tb) {                             /* :264-358 */
+        const int start = (nblk - 1 - tb) * BN;
+        const int hi_t = (P_top < start + BN - 1) ? P_top : start + BN - 1;
+        int cmax = 0;
+        for (int r = 0; r < T; ++r) {
+          const int row = r0 + r;
+          int c = 0;
+          for (int b = 0; b < BN; ++b) {
+            const int j = start + b;
+            keep[r * BN + b] = 0;
+            if (row >= N || j >= N || j > row) continue;              /* causal, row_ok, n_ok */
+            const int forced = (j < n_global) || (j >= loc_lo && j <= loc_hi);
+            const float s = score_of(qs + (size_t)r * D, ks + ((size_t)hk * N + j) * D, D, sm_scale);
+            volatile float thr = m[r] - tau_h;
+            if (!forced && band_rows && fabsf(s - thr) < band_eps) band_rows[(size_t)h * N + row] += 1;
+            const int kp = (s >= thr) || forced;                      /* :285-286 */
+            keep[r * BN + b] = (uint8_t)kp;
+            c += kp;
+          }
+          sel[r] = (float)c;
+          if (c > cmax) cmax = c;
+        }
+        const float adv = adv_full ? (float)(hi_t - start + 1) : (float)cmax; /* :303-306 */
+        if (use_skip && !(adv > 0.0f)) continue;                      /* :319-322 */
+        /* attend-geometry keys of this block at npk_j = -(d + o_j), o_j = hi_t - j  (:270, 325-332) */
+        for (int b = 0; b < BN; ++b) {
+          const int j = start + b;
+          if (j >= N) { memset(kra + (size_t)b * D, 0, sizeof(float) * D); continue; }
+          volatile float o = (float)(hi_t - j);
+          volatile float dpo = d + o;
+          const float npk = -dpo;
+          rope_row(k, dtype, ((size_t)hk * N + j) * D, D, npk, inv_freq_c, 1.0f, kra + (size_t)b * D);
+        }
+        for (int r = 0; r < T; ++r) {                                 /* :334-344 */
+          const int row = r0 + r;
+          float bmax = -INFINITY;
+          for (int b = 0; b < BN; ++b) {
+            sblk[b] = -INFINITY;
+            if (row >= N || !keep[r * BN + b]) continue;
+            const float s = score_of(qa + (size_t)r * D, kra + (size_t)b * D, D, sm_scale);
+            sblk[b] = s;
+            if (s > bmax) bmax = s;
+          }
+          const float mnew = mR[r] > bmax ? mR[r] : bmax;
+          const float msafe = (mnew == -INFINITY) ? 0.0f : mnew;
+          volatile float alpha = expf(mR[r] - msafe);
+          double psum = 0.0;
+          for (int e = 0; e < D; ++e) dotv[e] = 0.0;
+          for (int b = 0; b < BN; ++b) {
+            volatile float dl = sblk[b] - msafe;
+            const float p = expf(dl);
+            psum += p;
+            if (p == 0.0f) continue;
+            const float pc = round_to_dtype(p, dtype);               /* :345 */
+            const int j = start + b;
+            for (int e = 0; e < D; ++e)
+              dotv[e] += (double)pc * (double)load_elem(v, dtype, ((size_t)hk * N + j) * D + e);
+          }
+          volatile float la = l[r] * alpha;
+          l[r] = la + (float)psum;
+          for (int e = 0; e < D; ++e) {
+            volatile float aa = acc[(size_t)r * D + e] * alpha;
+            acc[(size_t)r * D + e] = aa + (float)dotv[e];
+          }
+          mR[r] = mnew;
+          kr[r] += (int32_t)sel[r];                                   /* :347 */
+        }
+        d = d + adv;                                                  /* :348 */
+        n_used += 1;
+      }
+      for (int r = 0; r < T; ++r) {
+        const int row = r0 + r;
+        if (row >= N) continue;
+        for (int e = 0; e < D; ++e) out[((size_t)h * N + row) * D + e] = acc[(size_t)r * D + e] / l[r];
+        kept[(size_t)h * N + row] = kr[r];
+      }
+      span[(size_t)h * nt + t] = d;
+      blocks[(size_t)h * nt + t] = (float)nblk;
+      skipped[(size_t)h * nt + t] = (float)(nblk - n_used);
+    }
+    free(qs); free(qa); free(m); free(sel); free(keep); free(kra); free(mR); free(l); free(acc);
+    free(kr); free(dotv); free(sblk);
+  }
+  free(ks);
+}

@@ -68,3 +68,52 @@ def gpu_sets_numpy(r):
 
 def out_f32(t):
     return t.float().cpu().numpy()
+
+
+# ------------------------------------------------------------------------------------------------
+# PQ Union: sets may differ only among keys tied at the overflow cut
+# ------------------------------------------------------------------------------------------------
+PQ_SET_NAMES = ["idx", "newpos_k", "newpos_q", "mask", "usize", "kept_size", "overflow"]
+
+
+def pq_rank_values(votes, wvotes, rank_mode):
+    """fl(wvotes + fl(1e-6 * votes)) (perquery.py:397), or votes for freq ranking."""
+    if rank_mode == 0 or wvotes is None:
+        return votes.astype(np.float32)
+    return (wvotes.astype(np.float32) + np.float32(1e-6) * votes.astype(np.float32)).astype(np.float32)
+
+
+def kept_mask_of(idx, N):
+    H, nt, _ = idx.shape
+    m = np.zeros((H, nt, N + 1), bool)
+    np.put_along_axis(m, idx.astype(np.int64), True, axis=-1)
+    return m[..., :N]
+
+
+def compare_pq_sets(got, ref, rank_vals, N, rel=0.0):
+    """got/ref: dicts of the 7 outputs.  Tiles whose kept sets agree must agree in every output;
+    in the others every differing key must carry a rank value within `rel` (relative) of the
+    reference's cut (its smallest kept non-forced rank value) -- equal values for exact inputs,
+    where torch.topk's choice among ties is unspecified -- and the sizes must agree.
+    Returns the number of tiles whose sets differ."""
+    kg, kr = kept_mask_of(got["idx"], N), kept_mask_of(ref["idx"], N)
+    differ = (kg != kr).any(-1)
+    for n in ("usize", "kept_size", "overflow"):
+        assert np.array_equal(np.asarray(got[n]).astype(np.int64), np.asarray(ref[n]).astype(np.int64)), n
+    same = ~differ
+    for n in ("idx", "newpos_k", "newpos_q", "mask"):
+        a, b = np.asarray(got[n]), np.asarray(ref[n])
+        if a.dtype == np.float32:
+            eq = a.view(np.uint32) == b.view(np.uint32)
+        else:
+            eq = a.astype(np.int64) == b.astype(np.int64)
+        assert eq[same].all(), f"{n} differs in a tile whose kept set agrees"
+    for h, t in np.argwhere(differ):
+        keys = np.nonzero(kg[h, t] != kr[h, t])[0]
+        forced = ref["mask"][h, t] == -1
+        sel = ref["idx"][h, t][(ref["idx"][h, t] < N) & ~forced]
+        cut = rank_vals[h, t, sel].min()
+        rv = rank_vals[h, t, keys]
+        tol = rel * abs(float(cut))
+        assert np.all(np.abs(rv - cut) <= tol), (h, t, keys[:8].tolist(), rv[:8].tolist(), float(cut))
+    return int(differ.sum())
