@@ -41,9 +41,10 @@ def parse():
     ap.add_argument("--config", default="c1")
     ap.add_argument("--cpu-baseline-seconds", type=float, default=15.0,
                     help="target CPU time of the oracle sample (0 disables it)")
-    ap.add_argument("--traffic-file", default=os.path.join(ROOT, "profiles", "prefill_c1_hbm_traffic.md"),
+    ap.add_argument("--traffic-file", default=None,
                     help="summary of the rocprofv3 FETCH_SIZE/WRITE_SIZE runs, with one "
-                         "'<kernel> traffic_bytes: <bytes per launch>' line per kernel")
+                         "'<kernel> traffic_bytes: <bytes per launch>' line per kernel "
+                         "(default: profiles/prefill_<config>_hbm_traffic.md)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="only run a plain device-to-device copy of MIB MiB (3 times) and exit: "
                          "the known-size reference for the HBM byte counters")
@@ -92,20 +93,27 @@ def cpu_baseline(cfg, q, k, v, invf, ps, rs, budget_s):
         qn, dt = orc.from_torch(q[0, h:h + 1])
         kn, _ = orc.from_torch(k[0, h // (cfg.H // cfg.Hkv):h // (cfg.H // cfg.Hkv) + 1])
         vn, _ = orc.from_torch(v[0, h // (cfg.H // cfg.Hkv):h // (cfg.H // cfg.Hkv) + 1])
+        tau = np.full(1, cfg.tau, np.float32)
         t0 = time.perf_counter()
-        a = orc.select_vote(qn, kn, dt, np.full(1, cfg.tau, np.float32), invf.numpy(), ps, rs, sm, cfg.tile)
-        s = orc.build_sets(a["votes"], ps, cfg.n_global, cfg.n_local, cfg.pct, cfg.tile, cfg.k_max)
-        orc.gather_attn(qn, kn, vn, dt, s[0], s[1], s[2], invf.numpy(), rs, sm, cfg.tile, cfg.k_max)
+        if cfg.variant == "pq":
+            orc.shared_pq_attention(qn, kn, vn, dt, tau, invf.numpy(), invf.numpy(), ps, rs, sm,
+                                    cfg.n_global, cfg.n_local, cfg.tile, cfg.k_max, 64, 0, cfg.select_score)
+        else:
+            a = orc.select_vote(qn, kn, dt, tau, invf.numpy(), ps, rs, sm, cfg.tile)
+            s = orc.build_sets(a["votes"], ps, cfg.n_global, cfg.n_local, cfg.pct, cfg.tile, cfg.k_max)
+            orc.gather_attn(qn, kn, vn, dt, s[0], s[1], s[2], invf.numpy(), rs, sm, cfg.tile, cfg.k_max)
         return time.perf_counter() - t0
 
     t_first = one(0)
     heads = max(1, min(cfg.H, int(budget_s / max(t_first, 1e-3))))
     total = t_first + sum(one(h) for h in range(1, heads))
     per_head = total / heads
+    stages = ("Kernel A + _build_sets_pq + masked Kernel C" if cfg.variant == "pq"
+              else "Kernel A + _build_sets + Kernel C")
     return {"value": round(cfg.N / (per_head * cfg.H), 3), "unit": "tokens/s", "cores": threads,
             "kind": "port",
             "sample": f"{heads} of {cfg.H} heads of the same workload through the CPU oracle "
-                      f"(Kernel A + _build_sets + Kernel C, {threads} OpenMP threads), scaled x{cfg.H / heads:g}"}
+                      f"({stages}, {threads} OpenMP threads), scaled x{cfg.H / heads:g}"}
 
 
 def main():
@@ -124,14 +132,20 @@ def main():
     from synthetic import CONFIGS
 
     cfg = CONFIGS[args.config]
+    if args.traffic_file is None:
+        args.traffic_file = os.path.join(ROOT, "profiles", f"prefill_{args.config}_hbm_traffic.md")
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     q_cpu, k_cpu, v_cpu = cfg.inputs("cpu")
     q, k, v = q_cpu.to(dev), k_cpu.to(dev), v_cpu.to(dev)
     invf, ps, rs = cfg.geometry()
     tau = torch.full((cfg.H,), cfg.tau)
-    plan = native.SharedPlan(q, k, v, tau, invf, ps, rs, invf, ps, rs, pct=cfg.pct, tile=cfg.tile,
-                             k_max=cfg.k_max, n_global=cfg.n_global, n_local=cfg.n_local)
+    if cfg.variant == "pq":
+        plan = native.PqPlan(q, k, v, tau, invf, invf, ps, rs, tile=cfg.tile, k_max=cfg.k_max,
+                             n_global=cfg.n_global, n_local=cfg.n_local, select_score=cfg.select_score)
+    else:
+        plan = native.SharedPlan(q, k, v, tau, invf, ps, rs, invf, ps, rs, pct=cfg.pct, tile=cfg.tile,
+                                 k_max=cfg.k_max, n_global=cfg.n_global, n_local=cfg.n_local)
     stream = torch.cuda.current_stream(dev)
     for _ in range(args.warmup):
         plan.run()
@@ -187,15 +201,20 @@ def main():
         "vs_baseline": None,
         "dtype": {torch.bfloat16: "bf16", torch.float16: "fp16", torch.float32: "fp32"}[q.dtype],
         "data": "synthetic (seeded Gaussian Q/K/V with planted keys)",
-        "config": {"workload": cfg.name, "heads": cfg.H, "kv_heads": cfg.Hkv, "seq_len": cfg.N,
-                   "head_dim": cfg.D, "tile": cfg.tile, "tau": cfg.tau, "pct": cfg.pct, "k_max": cfg.k_max,
+        "config": {"workload": cfg.name, "variant": cfg.variant, "heads": cfg.H, "kv_heads": cfg.Hkv,
+                   "seq_len": cfg.N, "head_dim": cfg.D, "tile": cfg.tile, "tau": cfg.tau,
+                   "pct": cfg.pct if cfg.variant == "shared" else None,
+                   "select_score": cfg.select_score, "k_max": cfg.k_max,
                    "pos_scale": ps, "rope_scale": rs, "parallelism": "none (1 GPU)"},
         "stages_ms": {s: round(t, 4) for s, t in stage_ms.items()},
         "roofline": dominant,
         "rooflines": {"score": roof_score, "gather": roof_gather},
-        "selection": {"kept_mean": round(kept.float().mean().item(), 1),
-                      "overflow20_tiles": int(r["overflow20"].sum().item()),
-                      "tiles": int(kept.numel())},
+        "selection": ({"kept_mean": round(kept.float().mean().item(), 1),
+                       "overflow_tiles": int(r["overflow"].sum().item()),
+                       "tiles": int(kept.numel())} if cfg.variant == "pq" else
+                      {"kept_mean": round(kept.float().mean().item(), 1),
+                       "overflow20_tiles": int(r["overflow20"].sum().item()),
+                       "tiles": int(kept.numel())}),
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

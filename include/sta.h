@@ -114,6 +114,74 @@ int sta_build_sets(const sta_shared_args* args, const int32_t* votes, int32_t nu
  * Replaces the _gather_attn_kernel launch, shared_selection_triton_exact_2.py:146-225, 471-485. */
 int sta_gather_attention(const sta_shared_args* args, void* stream);
 
+/* ------------------------------------------------------------------------------------------ */
+/* Per-query variant, PQ Union: every query keeps its own threshold passers; the tile's union  */
+/* (plus forced global / local keys) is gathered once and a per-slot bitmask selects, for each */
+/* query, the keys it attends.  Positions are dense ranks over the kept set, attended under    */
+/* base RoPE (inv_freq_c, rope scale 1).  tile must be 32 (one bit per query in an int32).     */
+/* ------------------------------------------------------------------------------------------ */
+#define STA_SCORE_FREQ 0    /* overflow ranking by votes */
+#define STA_SCORE_MARGIN 1  /* by the summed margin fl(s - fl(m - tau)) + 1e-6 votes */
+#define STA_SCORE_EXPMASS 2 /* by the summed exp(fl(s - m)) + 1e-6 votes */
+
+typedef struct sta_pq_args {
+  /* inputs (layout rules as sta_shared_args) */
+  const void* q;
+  const void* k;
+  const void* v;
+  int64_t q_head_stride, q_tok_stride;
+  int64_t k_head_stride, k_tok_stride;
+  int64_t v_head_stride, v_tok_stride;
+  int32_t dtype;
+  int32_t H, Hkv, N, D;
+  const float* tau;         /* (H,) */
+  const float* inv_freq_a;  /* (D/2,) selection geometry */
+  float pos_scale_a, rope_scale_a;
+  const float* inv_freq_c;  /* (D/2,) attend geometry (base RoPE at dense ranks, scale 1) */
+  float sm_scale;
+  int32_t n_global, n_local, tile, k_max, q_pos_base;
+  int32_t select_score;     /* STA_SCORE_*: ranking when |union U forced| > k_max */
+  /* outputs (device) */
+  void* out;                /* (H, N, D) */
+  int32_t* idx;             /* (H, nt, k_max) ascending kept keys, sentinel N */
+  float* newpos_k;          /* (H, nt, k_max) dense rank of each slot, 0 at sentinels */
+  float* newpos_q;          /* (H, nt, tile) dense rank of each query's own position */
+  int32_t* mask;            /* (H, nt, k_max) per-slot query bits, forced keys -1, sentinels 0 */
+  int32_t* usize;           /* (H, nt) |union| before forced keys */
+  int32_t* kept_size;       /* (H, nt) |kept| after any truncation */
+  uint8_t* overflow;        /* (H, nt) the union with forced keys exceeded k_max */
+  /* optional outputs (NULL to skip) */
+  int32_t* votes;           /* (H, nt, N) */
+  int32_t* bits;            /* (H, nt, N) bit i = keep(query i of the tile, key) */
+  float* wvotes;            /* (H, nt, N) weighted votes (zero for STA_SCORE_FREQ) */
+  int32_t* row_counts;      /* (H, N) */
+  float* row_max;           /* (H, N) */
+  void* workspace;
+  size_t workspace_bytes;
+  void* const* stage_events; /* NULL or 5 hipEvent_t, as for sta_shared_args */
+} sta_pq_args;
+
+/* Bytes of device workspace the PQ entry points need for these arguments. */
+size_t sta_pq_workspace_size(const sta_pq_args* args);
+
+/* The whole PQ Union prefill.  Replaces shared_pq_attention,
+ * shared_selection_triton_perquery.py:459-525. */
+int sta_pq_attention(const sta_pq_args* args, void* stream);
+
+/* PQ Kernel A alone: writes votes, bits and wvotes (required) and row_counts / row_max
+ * (optional).  Replaces the _select_bits_kernel launch, perquery.py:119-218, 495-508. */
+int sta_pq_select_bits(const sta_pq_args* args, void* stream);
+
+/* _build_sets_pq alone from dense (H, num_tiles, N) votes, bits and wvotes (wvotes may be NULL
+ * for STA_SCORE_FREQ); writes idx, newpos_k, newpos_q, mask, usize, kept_size and overflow.
+ * Replaces _build_sets_pq, perquery.py:363-453. */
+int sta_pq_build_sets(const sta_pq_args* args, const int32_t* votes, const int32_t* bits,
+                      const float* wvotes, int32_t num_tiles, void* stream);
+
+/* PQ Kernel C alone: gather + dense-rank attention with the per-slot query bitmask.
+ * Replaces the _gather_attn_pq_kernel launch, perquery.py:226-312, 511-524. */
+int sta_pq_gather_attention(const sta_pq_args* args, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -17,7 +17,10 @@ _LIB = None
 STA_OK = 0
 DTYPES = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
 EXPORTS = ["sta_abi_version", "sta_last_error", "sta_shared_workspace_size", "sta_shared_attention",
-           "sta_select_vote", "sta_build_sets", "sta_gather_attention"]
+           "sta_select_vote", "sta_build_sets", "sta_gather_attention",
+           "sta_pq_workspace_size", "sta_pq_attention", "sta_pq_select_bits", "sta_pq_build_sets",
+           "sta_pq_gather_attention"]
+SCORES = {"freq": 0, "margin": 1, "expmass": 2}
 
 
 class ShareArgs(ctypes.Structure):
@@ -46,6 +49,30 @@ class ShareArgs(ctypes.Structure):
     ]
 
 
+class PqArgs(ctypes.Structure):
+    """Mirror of sta_pq_args (include/sta.h)."""
+    _fields_ = [
+        ("q", ctypes.c_void_p), ("k", ctypes.c_void_p), ("v", ctypes.c_void_p),
+        ("q_head_stride", ctypes.c_int64), ("q_tok_stride", ctypes.c_int64),
+        ("k_head_stride", ctypes.c_int64), ("k_tok_stride", ctypes.c_int64),
+        ("v_head_stride", ctypes.c_int64), ("v_tok_stride", ctypes.c_int64),
+        ("dtype", ctypes.c_int32), ("H", ctypes.c_int32), ("Hkv", ctypes.c_int32),
+        ("N", ctypes.c_int32), ("D", ctypes.c_int32),
+        ("tau", ctypes.c_void_p),
+        ("inv_freq_a", ctypes.c_void_p), ("pos_scale_a", ctypes.c_float), ("rope_scale_a", ctypes.c_float),
+        ("inv_freq_c", ctypes.c_void_p), ("sm_scale", ctypes.c_float),
+        ("n_global", ctypes.c_int32), ("n_local", ctypes.c_int32), ("tile", ctypes.c_int32),
+        ("k_max", ctypes.c_int32), ("q_pos_base", ctypes.c_int32), ("select_score", ctypes.c_int32),
+        ("out", ctypes.c_void_p), ("idx", ctypes.c_void_p), ("newpos_k", ctypes.c_void_p),
+        ("newpos_q", ctypes.c_void_p), ("mask", ctypes.c_void_p), ("usize", ctypes.c_void_p),
+        ("kept_size", ctypes.c_void_p), ("overflow", ctypes.c_void_p),
+        ("votes", ctypes.c_void_p), ("bits", ctypes.c_void_p), ("wvotes", ctypes.c_void_p),
+        ("row_counts", ctypes.c_void_p), ("row_max", ctypes.c_void_p),
+        ("workspace", ctypes.c_void_p), ("workspace_bytes", ctypes.c_size_t),
+        ("stage_events", ctypes.c_void_p),
+    ]
+
+
 def lib():
     """Load libsta_hip.so once; raise loudly if it is absent."""
     global _LIB
@@ -65,6 +92,15 @@ def lib():
         L.sta_build_sets.restype = ctypes.c_int
         L.sta_build_sets.argtypes = [ctypes.POINTER(ShareArgs), ctypes.c_void_p, ctypes.c_int32,
                                      ctypes.c_void_p]
+        L.sta_pq_workspace_size.restype = ctypes.c_size_t
+        L.sta_pq_workspace_size.argtypes = [ctypes.POINTER(PqArgs)]
+        for name in ("sta_pq_attention", "sta_pq_select_bits", "sta_pq_gather_attention"):
+            fn = getattr(L, name)
+            fn.restype = ctypes.c_int
+            fn.argtypes = [ctypes.POINTER(PqArgs), ctypes.c_void_p]
+        L.sta_pq_build_sets.restype = ctypes.c_int
+        L.sta_pq_build_sets.argtypes = [ctypes.POINTER(PqArgs), ctypes.c_void_p, ctypes.c_void_p,
+                                        ctypes.c_void_p, ctypes.c_int32, ctypes.c_void_p]
         if L.sta_abi_version() != 1:
             raise ImportError("libsta_hip.so ABI version mismatch")
         _LIB = L
@@ -293,4 +329,172 @@ def gather_attention(q, k, v, inv_freq, idx, newpos_k, newpos_q, sm_scale, rope_
     ks = kept_size.to(device=dev, dtype=torch.int32).contiguous() if kept_size is not None else None
     a.kept_size = _ptr(ks)
     _check(lib().sta_gather_attention(ctypes.byref(a), _stream(dev)), "sta_gather_attention")
+    return out
+
+
+# ---------------------------------------------------------------------------------------------
+# PQ Union (per-query sets through the tile union + per-slot bitmask)
+# ---------------------------------------------------------------------------------------------
+def _fill_pq(a, q, k, v, tau, inv_freq_a, pos_scale_a, rope_scale_a, inv_freq_c, sm_scale, n_global,
+             n_local, tile, k_max, q_pos_base, select_score):
+    H, N, D = q.shape
+    a.q, a.k = _ptr(q), _ptr(k)
+    a.v = _ptr(v) if v is not None else None
+    a.q_head_stride, a.q_tok_stride = q.stride(0), q.stride(1)
+    a.k_head_stride, a.k_tok_stride = k.stride(0), k.stride(1)
+    if v is not None:
+        a.v_head_stride, a.v_tok_stride = v.stride(0), v.stride(1)
+    a.dtype = DTYPES[q.dtype]
+    a.H, a.Hkv, a.N, a.D = H, k.shape[0], N, D
+    a.tau = _ptr(tau)
+    a.inv_freq_a, a.pos_scale_a, a.rope_scale_a = _ptr(inv_freq_a), float(pos_scale_a), float(rope_scale_a)
+    a.inv_freq_c = _ptr(inv_freq_c)
+    a.sm_scale = float(sm_scale)
+    a.n_global, a.n_local, a.tile, a.k_max = int(n_global), int(n_local), int(tile), int(k_max)
+    a.q_pos_base = int(q_pos_base)
+    if select_score not in SCORES:
+        raise ValueError(f"select_score must be one of {sorted(SCORES)}, got {select_score!r}")
+    a.select_score = SCORES[select_score]
+
+
+def _pq_set_outputs(a, H, nt, tile, k_max, dev):
+    r = {
+        "idx": torch.empty((H, nt, k_max), dtype=torch.int32, device=dev),
+        "newpos_k": torch.empty((H, nt, k_max), dtype=torch.float32, device=dev),
+        "newpos_q": torch.empty((H, nt, tile), dtype=torch.float32, device=dev),
+        "mask": torch.empty((H, nt, k_max), dtype=torch.int32, device=dev),
+        "usize": torch.empty((H, nt), dtype=torch.int32, device=dev),
+        "kept_size": torch.empty((H, nt), dtype=torch.int32, device=dev),
+        "overflow": torch.empty((H, nt), dtype=torch.bool, device=dev),
+    }
+    for name, t in r.items():
+        setattr(a, name, _ptr(t))
+    return r
+
+
+def _pq_workspace(a, dev):
+    n = lib().sta_pq_workspace_size(ctypes.byref(a))
+    if n == 0:
+        _check(-1, "sta_pq_workspace_size")
+    ws = torch.empty(n, dtype=torch.uint8, device=dev)
+    assert ws.data_ptr() % 256 == 0
+    a.workspace, a.workspace_bytes = _ptr(ws), n
+    return ws
+
+
+class PqPlan:
+    """Outputs and workspace of the PQ Union prefill for one shape, allocated once; run()
+    launches the whole path on the current stream and allocates nothing."""
+
+    def __init__(self, q, k, v, tau, inv_freq_a, inv_freq_c, pos_scale_a=1.0, rope_scale_a=1.0,
+                 sm_scale=None, n_global=32, n_local=32, tile=32, k_max=4096, q_pos_base=0,
+                 select_score="expmass", want_votes=False, want_row_max=False, want_row_counts=False):
+        qh, kh, vh, tau, ifa, ifc = _prep_inputs(q, k, v, tau, inv_freq_a, inv_freq_c)
+        H, N, D = qh.shape
+        self.device = dev = qh.device
+        if sm_scale is None:
+            sm_scale = 1.0 / math.sqrt(D)
+        self.args = a = PqArgs()
+        _fill_pq(a, qh, kh, vh, tau, ifa, pos_scale_a, rope_scale_a, ifc, sm_scale, n_global, n_local,
+                 tile, k_max, q_pos_base, select_score)
+        self._keep = (qh, kh, vh, tau, ifa, ifc)
+        nt = (N + tile - 1) // tile
+        r = _pq_set_outputs(a, H, nt, tile, k_max, dev)
+        r["out"] = torch.empty((H, N, D), dtype=qh.dtype, device=dev)
+        a.out = _ptr(r["out"])
+        if want_votes:
+            r["votes"] = torch.empty((H, nt, N), dtype=torch.int32, device=dev)
+            r["bits"] = torch.empty((H, nt, N), dtype=torch.int32, device=dev)
+            r["wvotes"] = torch.empty((H, nt, N), dtype=torch.float32, device=dev)
+        if want_row_max:
+            r["row_max"] = torch.empty((H, N), dtype=torch.float32, device=dev)
+        if want_row_counts:
+            r["row_counts"] = torch.empty((H, N), dtype=torch.int32, device=dev)
+        for name in ("votes", "bits", "wvotes", "row_max", "row_counts"):
+            setattr(a, name, _ptr(r.get(name)))
+        self.out = r
+        self.workspace = _pq_workspace(a, dev)
+        self._events = None
+
+    def run(self, events=None):
+        if events is not None:
+            self._events = (ctypes.c_void_p * 5)(*[e.cuda_event for e in events])
+            self.args.stage_events = ctypes.cast(self._events, ctypes.c_void_p)
+        else:
+            self.args.stage_events = None
+        _check(lib().sta_pq_attention(ctypes.byref(self.args), _stream(self.device)), "sta_pq_attention")
+        return self.out
+
+
+def pq_attention(q, k, v, tau, inv_freq_a, inv_freq_c, pos_scale_a=1.0, rope_scale_a=1.0, sm_scale=None,
+                 n_global=32, n_local=32, tile=32, k_max=4096, q_pos_base=0, select_score="expmass",
+                 want_votes=False, want_row_max=False, want_row_counts=False):
+    """The whole PQ Union prefill on the device; returns a dict of device tensors."""
+    return PqPlan(q, k, v, tau, inv_freq_a, inv_freq_c, pos_scale_a, rope_scale_a, sm_scale, n_global,
+                  n_local, tile, k_max, q_pos_base, select_score, want_votes, want_row_max,
+                  want_row_counts).run()
+
+
+def pq_select_bits(q, k, tau, inv_freq, pos_scale, rope_scale, sm_scale, tile=32, q_pos_base=0,
+                   select_score="expmass"):
+    """PQ Kernel A alone: votes, bits (H,nt,N) int32, wvotes (H,nt,N) fp32, row_counts, row_max."""
+    qh, kh, _, tau, ifa, _ = _prep_inputs(q, k, None, tau, inv_freq, None)
+    H, N, D = qh.shape
+    dev = qh.device
+    nt = (N + tile - 1) // tile
+    a = PqArgs()
+    _fill_pq(a, qh, kh, None, tau, ifa, pos_scale, rope_scale, ifa, sm_scale, 0, 0, tile, 1, q_pos_base,
+             select_score)
+    r = {"votes": torch.empty((H, nt, N), dtype=torch.int32, device=dev),
+         "bits": torch.empty((H, nt, N), dtype=torch.int32, device=dev),
+         "wvotes": torch.empty((H, nt, N), dtype=torch.float32, device=dev),
+         "row_counts": torch.empty((H, N), dtype=torch.int32, device=dev),
+         "row_max": torch.empty((H, N), dtype=torch.float32, device=dev)}
+    for name, t in r.items():
+        setattr(a, name, _ptr(t))
+    ws = _pq_workspace(a, dev)
+    _check(lib().sta_pq_select_bits(ctypes.byref(a), _stream(dev)), "sta_pq_select_bits")
+    del ws
+    return r
+
+
+def pq_build_sets(votes, bits, wvotes, n_global, n_local, T, k_max, q_pos_base=0, select_score="expmass"):
+    """_build_sets_pq on the device from dense (H, nt, N) votes / bits / wvotes.  Returns the
+    reference's 7-tuple (idx, newpos_k, newpos_q, mask, usize, kept_size, overflow)."""
+    if not votes.is_cuda:
+        raise RuntimeError("pq_build_sets runs on a HIP device only; got a CPU tensor")
+    votes = votes.to(torch.int32).contiguous()
+    bits = bits.to(torch.int32).contiguous()
+    H, nt, N = votes.shape
+    dev = votes.device
+    use_w = select_score != "freq" and wvotes is not None and wvotes.shape[-1] == N
+    wv = wvotes.to(torch.float32).contiguous() if use_w else None
+    a = PqArgs()
+    a.dtype, a.H, a.Hkv, a.N, a.D = 1, H, H, N, 64
+    a.n_global, a.n_local, a.tile, a.k_max = int(n_global), int(n_local), int(T), int(k_max)
+    a.q_pos_base = int(q_pos_base)
+    a.select_score = SCORES[select_score] if use_w else SCORES["freq"]
+    r = _pq_set_outputs(a, H, nt, T, k_max, dev)
+    _check(lib().sta_pq_build_sets(ctypes.byref(a), _ptr(votes), _ptr(bits), _ptr(wv), nt, _stream(dev)),
+           "sta_pq_build_sets")
+    return (r["idx"], r["newpos_k"], r["newpos_q"], r["mask"], r["usize"], r["kept_size"], r["overflow"])
+
+
+def pq_gather_attention(q, k, v, inv_freq_c, idx, newpos_k, newpos_q, mask, sm_scale, tile, k_max,
+                        q_pos_base=0, kept_size=None):
+    """PQ Kernel C alone.  Returns out (H, N, D) in q.dtype."""
+    qh, kh, vh, _, ifc, _ = _prep_inputs(q, k, v, torch.zeros(1), inv_freq_c, None)
+    H, N, D = qh.shape
+    dev = qh.device
+    a = PqArgs()
+    _fill_pq(a, qh, kh, vh, torch.zeros(1, device=dev), ifc, 1.0, 1.0, ifc, sm_scale, 0, 0, tile, k_max,
+             q_pos_base, "expmass")
+    out = torch.empty((H, N, D), dtype=qh.dtype, device=dev)
+    keep = [t.to(device=dev, dtype=dt).contiguous() for t, dt in
+            ((idx, torch.int32), (newpos_k, torch.float32), (newpos_q, torch.float32), (mask, torch.int32))]
+    a.out = _ptr(out)
+    a.idx, a.newpos_k, a.newpos_q, a.mask = (_ptr(t) for t in keep)
+    ks = kept_size.to(device=dev, dtype=torch.int32).contiguous() if kept_size is not None else None
+    a.kept_size = _ptr(ks)
+    _check(lib().sta_pq_gather_attention(ctypes.byref(a), _stream(dev)), "sta_pq_gather_attention")
     return out

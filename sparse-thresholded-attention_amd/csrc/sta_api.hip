@@ -6,15 +6,15 @@
 #include <string>
 
 #include "../../include/sta.h"
+#include "sta_api_util.h"
 #include "sta_kernels.h"
 
 using namespace sta;
 
-namespace {
+namespace sta_api {
 
 thread_local std::string g_last_error;
 
-int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
 int fail(int code, const char* fmt, ...) {
   char buf[512];
   va_list ap;
@@ -25,11 +25,28 @@ int fail(int code, const char* fmt, ...) {
   return code;
 }
 
-int hip_fail(hipError_t e, const char* what) {
-  return fail(STA_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+int check_qkv_ptrs(int dtype, const void* q, const void* k, const void* v, const int64_t strides[6],
+                   bool need_v) {
+  const int es = esize(dtype);
+  const void* ptrs[3] = {q, k, v};
+  for (int i = 0; i < (need_v ? 3 : 2); ++i) {
+    if (!ptrs[i]) return fail(STA_ERR_INVALID_ARG, "%c is NULL", "qkv"[i]);
+    if (!aligned16(ptrs[i])) return fail(STA_ERR_UNSUPPORTED, "%c is not 16-byte aligned", "qkv"[i]);
+    for (int j = 0; j < 2; ++j) {
+      const int64_t s = strides[2 * i + j];
+      if (s < 0 || (s * es) % 16 != 0)
+        return fail(STA_ERR_UNSUPPORTED, "%c %s stride %lld is negative or not 16-byte aligned",
+                    "qkv"[i], j ? "token" : "head", (long long)s);
+    }
+  }
+  return STA_OK;
 }
 
-size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+}  // namespace sta_api
+
+using namespace sta_api;
+
+namespace {
 
 struct Layout {
   int nt, q_rows_pad, k_rows_pad;
@@ -55,10 +72,6 @@ Layout layout_of(const sta_shared_args* a) {
   return L;
 }
 
-int esize(int dtype) { return dtype == STA_DTYPE_F32 ? 4 : 2; }
-
-bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
-
 // shape / parameter checks shared by every entry point
 int check_common(const sta_shared_args* a) {
   if (!a) return fail(STA_ERR_INVALID_ARG, "args is NULL");
@@ -78,21 +91,9 @@ int check_common(const sta_shared_args* a) {
 }
 
 int check_qkv(const sta_shared_args* a, bool need_v) {
-  const int es = esize(a->dtype);
-  const void* ptrs[3] = {a->q, a->k, a->v};
   const int64_t strides[6] = {a->q_head_stride, a->q_tok_stride, a->k_head_stride,
                               a->k_tok_stride, a->v_head_stride, a->v_tok_stride};
-  for (int i = 0; i < (need_v ? 3 : 2); ++i) {
-    if (!ptrs[i]) return fail(STA_ERR_INVALID_ARG, "%c is NULL", "qkv"[i]);
-    if (!aligned16(ptrs[i])) return fail(STA_ERR_UNSUPPORTED, "%c is not 16-byte aligned", "qkv"[i]);
-    for (int j = 0; j < 2; ++j) {
-      const int64_t s = strides[2 * i + j];
-      if (s < 0 || (s * es) % 16 != 0)
-        return fail(STA_ERR_UNSUPPORTED, "%c %s stride %lld is negative or not 16-byte aligned",
-                    "qkv"[i], j ? "token" : "head", (long long)s);
-    }
-  }
-  return STA_OK;
+  return check_qkv_ptrs(a->dtype, a->q, a->k, a->v, strides, need_v);
 }
 
 int check_workspace(const sta_shared_args* a, const Layout& L) {
@@ -151,11 +152,7 @@ SelectArgs select_args_of(const sta_shared_args* a, const Layout& L) {
   return s;
 }
 
-int mark(const sta_shared_args* a, int i, hipStream_t st) {
-  if (!a->stage_events) return STA_OK;
-  hipError_t e = hipEventRecord((hipEvent_t)a->stage_events[i], st);
-  return e == hipSuccess ? STA_OK : hip_fail(e, "stage event record");
-}
+int mark(const sta_shared_args* a, int i, hipStream_t st) { return mark_event(a->stage_events, i, st); }
 
 int run_kernel_a(const sta_shared_args* a, const Layout& L, hipStream_t st) {
   char* ws = (char*)a->workspace;
@@ -171,7 +168,7 @@ int run_kernel_a(const sta_shared_args* a, const Layout& L, hipStream_t st) {
                        L.k_rows_pad, 0, a->pos_scale_a, a->rope_scale_a, a->inv_freq_a, kfrag, st);
   if (e != hipSuccess) return hip_fail(e, "rope pre-kernel (k)");
   if ((rc = mark(a, 1, st)) != STA_OK) return rc;
-  ScoreArgs sa;
+  ScoreArgs sa{};
   sa.qfrag = qfrag;
   sa.kfrag = kfrag;
   sa.H = a->H;
@@ -195,7 +192,7 @@ int run_kernel_a(const sta_shared_args* a, const Layout& L, hipStream_t st) {
 int run_gather(const sta_shared_args* a, const Layout& L, hipStream_t st) {
   if (gather_lds_bytes(a->dtype, a->D, a->k_max) > 160 * 1024)
     return fail(STA_ERR_UNSUPPORTED, "k_max=%d needs more than 160 KB of LDS in the gather", a->k_max);
-  GatherArgs g;
+  GatherArgs g{};
   g.q = a->q;
   g.k = a->k;
   g.v = a->v;

@@ -314,9 +314,17 @@ __global__ __launch_bounds__(NW * 64 + 256, 1) void gather_kernel(GatherArgs a) 
       const int sl = s0 + sb * 16 + 4 * (lane >> 4);
       const int4 j4 = *(const int4*)(sidx + sl);
       const int jj[4] = {j4.x, j4.y, j4.z, j4.w};
+      // per-query variant: bit r of the slot's mask says whether this lane's row attends it
+      // (shared_selection_triton_perquery.py:296-297); slots past k_max read as empty
+      uint32_t mk[4] = {~0u, ~0u, ~0u, ~0u};
+      if (a.mask) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) mk[i] = sl + i < a.k_max ? (uint32_t)a.mask[tile_off + sl + i] : 0u;
+      }
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const bool keep = unmasked || (((unsigned)jj[i] < (unsigned)N) && (qpos >= jj[i]));  // exact_2.py:210
+        const bool keep = (unmasked || (((unsigned)jj[i] < (unsigned)N) && (qpos >= jj[i])))  // exact_2.py:210
+                          && (a.mask == nullptr || ((mk[i] >> (r & 31)) & 1u));
         const float v = keep ? sacc[sb][i] * a.sm_scale : -INFINITY;
         p[sb][i] = v;
         bmax = fmaxf(bmax, v);

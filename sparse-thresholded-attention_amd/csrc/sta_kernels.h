@@ -16,6 +16,8 @@ struct ScoreArgs {
   float sm_scale;
   uint8_t* votes;         // (H, nt, votes_stride): keys < min(N, hi_t) written
   int64_t votes_stride;
+  uint32_t* bits;         // per-query variant: (H, nt, votes_stride) keep bits, bit i = row i
+  float* wvotes;          // per-query variant: (H, nt, votes_stride) margin / expmass votes
   float* row_max;         // (H, N) or null
   int32_t* row_counts;    // (H, N) or null
 };
@@ -54,13 +56,37 @@ struct GatherArgs {
   const float* newpos_k;
   const float* newpos_q;
   const int32_t* kept_size;  // (H, nt) or null (then every k_max slot is swept)
+  const int32_t* mask;       // (H, nt, k_max) per-slot query bits (tile 32) or null
   void* out;                 // (H, N, D) contiguous
+};
+
+// per-query (PQ Union) set construction: shared_selection_triton_perquery.py:363-453
+struct PqSelectArgs {
+  const uint32_t* bits;   // (H, nt, stride) keep bits
+  const float* wvotes;    // (H, nt, stride) weighted votes, or null (rank by votes)
+  const int32_t* votes;   // (H, nt, stride) votes, or null (popcount of the bits)
+  int64_t stride;
+  int dense;              // 1: all N keys valid; 0: keys >= min(N, tile end) read as zero
+  int H, nt, N, T, k_max, q_pos_base, n_global, n_local;
+  int32_t* idx;
+  float* newpos_k;
+  float* newpos_q;
+  int32_t* mask;
+  int32_t* usize;
+  int32_t* kept_size;
+  uint8_t* overflow;
 };
 
 hipError_t launch_rope_frag(int dtype, int D, const void* x, int64_t head_stride, int64_t tok_stride,
                             int heads, int N, int rows_pad, int pos_base, float pos_scale,
                             float rope_scale, const float* inv_freq, u32x4* frag, hipStream_t st);
 hipError_t launch_score(int D, int tile, const ScoreArgs& a, hipStream_t st);
+hipError_t launch_score_pq(int D, int wmode, const ScoreArgs& a, hipStream_t st);
+size_t pq_select_lds_bytes(int N, int k_max);
+hipError_t launch_pq_select(const PqSelectArgs& a, hipStream_t st);
+hipError_t launch_expand_pq(const uint32_t* bits, const float* wv, int64_t stride, int H, int nt, int N,
+                            int T, int q_pos_base, int32_t* votes_out, int32_t* bits_out,
+                            float* wv_out, hipStream_t st);
 size_t select_lds_bytes(int N, int k_max);
 hipError_t launch_select(const SelectArgs& a, int vote_bytes, hipStream_t st);
 hipError_t launch_expand_votes(const uint8_t* v8, int64_t stride, int H, int nt, int N, int T,

@@ -108,7 +108,11 @@ __device__ __forceinline__ float min_arg_for(float thr, float c) {
   return x;
 }
 
-template <int D, int RB, bool RC>
+// PQ selects the pass-2 epilogue: 0 = byte votes (shared selection); 1..3 = the per-query
+// variant (tile 32): packed keep bits per key, plus weighted votes for PQ 2 (margin,
+// sum of fl(s - fl(m - tau))) and PQ 3 (expmass, sum of exp(fl(s - m))) over the keeping rows
+// (shared_selection_triton_perquery.py:181-217).
+template <int D, int RB, bool RC, int PQ>
 __global__ __launch_bounds__(256, 1) void score_kernel(ScoreArgs a) {
 #pragma clang fp contract(off)
   constexpr int S = D / 16;                      // k steps of 16
@@ -117,6 +121,7 @@ __global__ __launch_bounds__(256, 1) void score_kernel(ScoreArgs a) {
   constexpr int PF = CHUNK_UNITS / 256;          // units per thread per chunk
   constexpr int PER = 16 * RB / S;               // epilogue elements finished per k step
   static_assert(PER * S == 16 * RB, "epilogue split");
+  static_assert(PQ == 0 || RB == 1, "per-query bits pack one 32-row tile");
   extern __shared__ u32x4 lds[];                 // 2 x CHUNK_UNITS
 
   const int lane = threadIdx.x & 63;
@@ -147,6 +152,16 @@ __global__ __launch_bounds__(256, 1) void score_kernel(ScoreArgs a) {
   const int nfull = min(min(nchunks, (a.q_pos_base + g * 4 * T + 1) >> 7), a.N >> 7);
   const float tau = a.tau[h];
   uint8_t* vrow = a.votes + ((int64_t)h * a.nt + t) * a.votes_stride;
+  uint32_t* brow = a.bits + ((int64_t)h * a.nt + t) * a.votes_stride;
+  uint32_t* wrow = (uint32_t*)a.wvotes + ((int64_t)h * a.nt + t) * a.votes_stride;
+  // one store per key and lane half: lanes 0-31 the bits, lanes 32-63 the weighted vote
+  auto store_pq = [&](int key, uint32_t bm, float w) {
+    bm <<= 4 * (lane >> 5);                 // rows of the upper lane half sit 4 bits higher
+    bm |= __shfl_xor(bm, 32, 64);
+    if constexpr (PQ >= 2) w += __shfl_xor(w, 32, 64);
+    if (lane < 32) brow[key] = bm;
+    else if constexpr (PQ >= 2) wrow[key] = __float_as_uint(w);
+  };
 
   // ---- Q fragments of this wave's tile ----
   u32x4 qhi[RB][S], qlo[RB][S];
@@ -167,7 +182,24 @@ __global__ __launch_bounds__(256, 1) void score_kernel(ScoreArgs a) {
   }
   const u32x4* kbase = a.kfrag + (int64_t)kvh * (a.k_rows_pad >> 5) * S * 128;
 
-  float mx[RB][16];   // pass 1: running max of the raw dot per row slot
+  // per-query epilogue of one score: bit `row` of the key's mask, and its weighted vote
+  // (i indexes the lane's 16 accumulator rows: row = (i/4)*8 + 4*(lane/32) + i%4; the lane
+  // half's 4-row offset is applied when the mask is stored)
+  auto pq_acc = [&](int keep, float v, float ref, int i, uint32_t& bm, float& w) {
+#pragma clang fp contract(off)
+    bm |= (uint32_t)keep << ((i >> 2) * 8 + (i & 3));
+    if constexpr (PQ == 2) {
+      const float qk = v * a.sm_scale;
+      const float c = qk - ref;
+      w += keep ? c : 0.0f;
+    } else if constexpr (PQ == 3) {
+      const float qk = v * a.sm_scale;
+      const float e = __expf(qk - ref);
+      w += keep ? e : 0.0f;
+    }
+  };
+  float mx[RB][16];   // pass 1: running max of the raw dot per row slot; pass 2 (PQ 2 / 3):
+                      // fl(m - tau) / m of the row, the reference point of the weighted vote
   float x0[RB][16];   // pass 2: keep threshold on the raw dot per row slot
   int rc[RB][16];
 #pragma unroll
@@ -193,6 +225,8 @@ __global__ __launch_bounds__(256, 1) void score_kernel(ScoreArgs a) {
     constexpr int pass = decltype(passc)::value;
     constexpr bool HAS_PREV = decltype(prevc)::value;
     int cnt = 0;
+    uint32_t bm = 0;
+    float w = 0.0f;
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) accN[rb] = floatx16{};
 #pragma unroll
@@ -207,21 +241,28 @@ __global__ __launch_bounds__(256, 1) void score_kernel(ScoreArgs a) {
             mx[rb][i] = v > mx[rb][i] ? v : mx[rb][i];
           } else {
             const int keep = v >= x0[rb][i];
-            cnt += keep;
+            if constexpr (PQ == 0) cnt += keep;
+            else pq_acc(keep, v, mx[rb][i], i, bm, w);
             if constexpr (RC) rc[rb][i] += keep;
           }
         }
       }
     }
     if constexpr (HAS_PREV && pass == 1) {
-      cnt += __shfl_xor(cnt, 32, 64);   // exact_2.py:123; both lane halves now hold the total
-      vrow[keyO + (lane & 31)] = (uint8_t)cnt;
+      if constexpr (PQ == 0) {
+        cnt += __shfl_xor(cnt, 32, 64);   // exact_2.py:123; both lane halves now hold the total
+        vrow[keyO + (lane & 31)] = (uint8_t)cnt;
+      } else {
+        store_pq(keyO + (lane & 31), bm, w);
+      }
     }
   };
   // the last block's epilogue when nothing follows it
   auto flush = [&](auto passc, const floatx16* acc, int key0) {
     constexpr int pass = decltype(passc)::value;
     int cnt = 0;
+    uint32_t bm = 0;
+    float w = 0.0f;
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
@@ -231,13 +272,18 @@ __global__ __launch_bounds__(256, 1) void score_kernel(ScoreArgs a) {
           mx[rb][i] = v > mx[rb][i] ? v : mx[rb][i];
         } else {
           const int keep = v >= x0[rb][i];
-          cnt += keep;
+          if constexpr (PQ == 0) cnt += keep;
+          else pq_acc(keep, v, mx[rb][i], i, bm, w);
           if constexpr (RC) rc[rb][i] += keep;
         }
       }
     if constexpr (pass == 1) {
-      cnt += __shfl_xor(cnt, 32, 64);
-      vrow[key0 + (lane & 31)] = (uint8_t)cnt;
+      if constexpr (PQ == 0) {
+        cnt += __shfl_xor(cnt, 32, 64);
+        vrow[key0 + (lane & 31)] = (uint8_t)cnt;
+      } else {
+        store_pq(key0 + (lane & 31), bm, w);
+      }
     }
   };
 
@@ -285,6 +331,8 @@ __global__ __launch_bounds__(256, 1) void score_kernel(ScoreArgs a) {
             const int key = key0 + (lane & 31);
             const bool diag = key0 + 31 > qpos0;
             int cnt = 0;
+            uint32_t bm = 0;
+            float w = 0.0f;
 #pragma unroll
             for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
@@ -296,13 +344,25 @@ __global__ __launch_bounds__(256, 1) void score_kernel(ScoreArgs a) {
                   if (causal && v > mx[rb][i]) mx[rb][i] = v;
                 } else {
                   const int keep = causal && v >= x0[rb][i];
-                  cnt += keep;
+                  if constexpr (PQ == 0) cnt += keep;
+                  else pq_acc(keep, v, mx[rb][i], i, bm, w);
                   if constexpr (RC) rc[rb][i] += keep;
                 }
               }
             if constexpr (pass == 1) {
-              cnt += __shfl_xor(cnt, 32, 64);
-              if (lane < 32 && key < a.N) vrow[key] = (uint8_t)cnt;
+              if constexpr (PQ == 0) {
+                cnt += __shfl_xor(cnt, 32, 64);
+                if (lane < 32 && key < a.N) vrow[key] = (uint8_t)cnt;
+              } else {
+                // the shuffles inside run on every lane; only the store is guarded
+                bm <<= 4 * (lane >> 5);
+                bm |= __shfl_xor(bm, 32, 64);
+                if constexpr (PQ >= 2) w += __shfl_xor(w, 32, 64);
+                if (key < a.N) {
+                  if (lane < 32) brow[key] = bm;
+                  else if constexpr (PQ >= 2) wrow[key] = __float_as_uint(w);
+                }
+              }
             }
           }
         }
@@ -332,6 +392,8 @@ __global__ __launch_bounds__(256, 1) void score_kernel(ScoreArgs a) {
             const int row = rb * 32 + (i >> 2) * 8 + (lane >> 5) * 4 + (i & 3);
             const bool ok = t * T + row < a.N;  // padded rows never vote (exact_2.py:121)
             x0[rb][i] = ok ? min_arg_for(m - tau, a.sm_scale) : INFINITY;
+            if constexpr (PQ == 2) mx[rb][i] = m - tau;   // perquery.py:210
+            if constexpr (PQ == 3) mx[rb][i] = m;         // perquery.py:215
             if (a.row_max && (lane & 31) == 0 && ok) a.row_max[(int64_t)h * a.N + t * T + row] = m;
           }
       }
@@ -384,28 +446,33 @@ hipError_t launch_rope_frag(int dtype, int D, const void* x, int64_t hs, int64_t
   return hipErrorInvalidValue;
 }
 
-template <int D, int RB, bool RC>
+template <int D, int RB, bool RC, int PQ>
 static hipError_t launch_score_t(const ScoreArgs& a, hipStream_t st) {
   constexpr int S = D / 16;
   const size_t lds_bytes = 2 * (size_t)(4 * S * 2 * 64) * 16;
-  static bool attr_set = false;
-  if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute((const void*)score_kernel<D, RB, RC>,
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_bytes);
-    if (e != hipSuccess) return e;
-    attr_set = true;
-  }
+  hipError_t e = hipFuncSetAttribute((const void*)score_kernel<D, RB, RC, PQ>,
+                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_bytes);
+  if (e != hipSuccess) return e;
   const int ngroups = (a.nt + 3) / 4;
-  hipLaunchKernelGGL((score_kernel<D, RB, RC>), dim3(a.H * ngroups), dim3(256), lds_bytes, st, a);
+  hipLaunchKernelGGL((score_kernel<D, RB, RC, PQ>), dim3(a.H * ngroups), dim3(256), lds_bytes, st, a);
   return hipGetLastError();
 }
 
 hipError_t launch_score(int D, int tile, const ScoreArgs& a, hipStream_t st) {
   const bool rc = a.row_counts != nullptr;
 #define STA_SC(D_, RB_) \
-  if (D == D_ && tile == RB_ * 32) return rc ? launch_score_t<D_, RB_, true>(a, st) : launch_score_t<D_, RB_, false>(a, st);
+  if (D == D_ && tile == RB_ * 32) return rc ? launch_score_t<D_, RB_, true, 0>(a, st) : launch_score_t<D_, RB_, false, 0>(a, st);
   STA_SC(64, 1) STA_SC(64, 2) STA_SC(128, 1) STA_SC(128, 2)
 #undef STA_SC
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_score_pq(int D, int wmode, const ScoreArgs& a, hipStream_t st) {
+  const bool rc = a.row_counts != nullptr;
+#define STA_SP(D_, PQ_) \
+  if (D == D_ && wmode + 1 == PQ_) return rc ? launch_score_t<D_, 1, true, PQ_>(a, st) : launch_score_t<D_, 1, false, PQ_>(a, st);
+  STA_SP(64, 1) STA_SP(64, 2) STA_SP(64, 3) STA_SP(128, 1) STA_SP(128, 2) STA_SP(128, 3)
+#undef STA_SP
   return hipErrorInvalidValue;
 }
 

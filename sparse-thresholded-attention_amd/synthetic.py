@@ -76,6 +76,8 @@ class Config:
     k_max: int = 2048
     n_global: int = 32
     n_local: int = 32
+    variant: str = "shared"     # "shared" (tile-shared sets), "pq" (PQ Union), "pqstream"
+    select_score: str = "freq"  # overflow ranking of the per-query variant
 
     def geometry(self):
         """(inv_freq, pos_scale, rope_scale) of the selection + attend geometry."""
@@ -102,4 +104,8 @@ CONFIGS = {
     # 2: YaRN_exact Llama-3-8B GQA layer, factor 4 from 8192
     "c2": Config("c2_yarn_exact_32q8kv_d128_32k_bf16", 32, 8, 32768, 128, torch.bfloat16, 64, 5.0, 0.005,
                  500000.0, 1.0, yarn=(4.0, 8192, 32.0, 1.0)),
+    # 3: per-query selection (PQ Union), PI 4096 -> 16384 for selection, base RoPE at dense ranks
+    #    for attention, tau 4, tile 32, k_max 2048
+    "c3": Config("c3_pq_union_32h_d128_16k_bf16", 32, 32, 16384, 128, torch.bfloat16, 32, 4.0, 0.01,
+                 10000.0, pi_pos_scale(4096, 16384), variant="pq", select_score="expmass"),
 }
