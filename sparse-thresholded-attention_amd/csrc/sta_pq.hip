@@ -52,8 +52,14 @@ __global__ __launch_bounds__(256) void pq_select_kernel(PqSelectArgs a) {
   const int h = blockIdx.x / a.nt, t = blockIdx.x % a.nt;
   const int N = a.N, T = a.T;
   const int per = (N + 255) / 256;
-  uint32_t* rk = pq_smem;                                   // 256 * per rank keys (0: not a candidate)
-  int* hist = (int*)(rk + 256 * per);                       // 256
+  // thread tid scans keys [tid*per, tid*per + per); its keys sit at a row of odd stride PS so the
+  // 64 lanes of a scan step fall in distinct LDS banks
+  const int PS = per | 1;
+  uint32_t* rkb = pq_smem;                                  // 256 rows x PS rank keys (0: not a candidate)
+  uint32_t* myrow = rkb + tid * PS;                         // this thread's keys j0 .. j0 + per - 1
+  // j / per by a reciprocal multiply (per >= 2): exact for per <= 256 and j < 2^24
+  const uint32_t inv_per = per > 1 ? (uint32_t)((0x100000000ull + per - 1) / per) : 0u;
+  int* hist = (int*)(rkb + 256 * PS);                       // 256
   int* tmp = hist + 256;                                    // 8
   int* misc = tmp + 8;                                      // 8
   float* qnp = (float*)(misc + 8);                          // T (<= 64)
@@ -67,62 +73,117 @@ __global__ __launch_bounds__(256) void pq_select_kernel(PqSelectArgs a) {
   auto is_forced = [&](int j) { return j < a.n_global || (j >= lo && j <= hi_l); };
 
   // ---- union, forced, candidates and their rank values (perquery.py:381-397) ----
+  // staged with coalesced loads (key j by thread j % 256); the scans below walk contiguous ranges
   int cu = 0, cf = 0, cfo = 0;
-  for (int j = j0; j < j0 + per; ++j) {
-    uint32_t key = 0;
-    if (j < j1) {
-      int vt = 0;
-      float wv = 0.0f;
-      if (j < hi_keys) {
-        vt = a.votes ? a.votes[roff + j] : __popc(brow[j]);
-        if (a.wvotes) wv = a.wvotes[roff + j];
-      }
-      const bool un = vt > 0, fo = is_forced(j);
-      cu += un;
-      cf += un || fo;
-      cfo += fo;
-      if (un && !fo) {
-        float rv;
-        if (a.wvotes) {
-          const float tb = 1e-6f * (float)vt;
-          rv = wv + tb;
-        } else {
-          rv = (float)vt;
-        }
-        key = __float_as_uint(rv);
-        if (key == 0 || key >= 0x80000000u) key = 1;   // a non-positive value stays a candidate, lowest
-      }
+  constexpr int U = 16;   // loads in flight per lane
+  for (int jb = 0; jb < 256 * per; jb += 256 * U) {
+    uint32_t bv[U];
+    int vv[U];
+    float wvv[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int j = jb + u * 256 + tid;
+      const bool ok = j < hi_keys;
+      bv[u] = (ok && !a.votes) ? brow[j] : 0u;
+      vv[u] = (ok && a.votes) ? a.votes[roff + j] : 0;
+      wvv[u] = (ok && a.wvotes) ? a.wvotes[roff + j] : 0.0f;
     }
-    rk[j - j0 + tid * per] = key;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int j = jb + u * 256 + tid;
+      if (j >= 256 * per) break;
+      uint32_t key = 0;
+      if (j < N) {
+        const int vt = a.votes ? vv[u] : __popc(bv[u]);
+        const bool un = vt > 0, fo = is_forced(j);
+        cu += un;
+        cf += un || fo;
+        cfo += fo;
+        if (un && !fo) {
+          float rv;
+          if (a.wvotes) {
+            const float tb = 1e-6f * (float)vt;
+            rv = wvv[u] + tb;
+          } else {
+            rv = (float)vt;
+          }
+          key = __float_as_uint(rv);
+          if (key == 0 || key >= 0x80000000u) key = 1;   // a non-positive value stays a candidate, lowest
+        }
+      }
+      const uint32_t row = per == 1 ? (uint32_t)j : __umulhi((uint32_t)j, inv_per);
+      rkb[row * PS + (j - row * per)] = key;
+    }
   }
+  __syncthreads();
   const int usize = pq_block_sum(cu, tmp);
   const int nfull = pq_block_sum(cf, tmp);
   const int nforced = pq_block_sum(cfo, tmp);
   const bool overflow = nfull > a.k_max;                    // perquery.py:386
   const int budget = max(a.k_max - nforced, 0);             // perquery.py:399-400
 
-  // ---- overflow: radix select of the budget-th largest rank key ----
+  // ---- overflow: radix select of the budget-th largest rank key, 8-bit digits ----
+  // Rank values of one tile share few exponents, so the top digits of most keys coincide: that
+  // pass aggregates its histogram increments per wave (one LDS atomic per distinct digit) instead
+  // of 64 conflicting lane atomics.
   uint32_t V = 0;
   int need_eq = 0;
   if (overflow && budget > 0) {
+    const int lane = tid & 63;
     uint32_t prefix = 0, pmask = 0;
     int need = budget;
     for (int shift = 24; shift >= 0; shift -= 8) {
       hist[tid] = 0;
       __syncthreads();
-      for (int j = j0; j < j1; ++j) {
-        const uint32_t k = rk[j];
-        if (k != 0 && (k & pmask) == prefix) atomicAdd(&hist[(k >> shift) & 255u], 1);
+      if (shift == 24) {
+        // top digit (sign + high exponent bits): few distinct values per wave -> one atomic per
+        // distinct digit
+        for (int i = 0; i < per; ++i) {                // same trip count on every lane
+          const uint32_t k = myrow[i];
+          bool act = k != 0 && j0 + i < N;
+          const int d = (int)(k >> 24);
+          uint64_t m = __ballot(act);
+          while (m) {
+            const int leader = __ffsll((unsigned long long)m) - 1;
+            const int dl = __shfl(d, leader, 64);
+            const uint64_t same = __ballot(act && d == dl);
+            if (lane == leader) atomicAdd(&hist[dl], (int)__popcll(same));
+            if (act && d == dl) act = false;
+            m &= ~same;
+          }
+        }
+      } else {
+        // lower digits are spread over the bins: plain LDS atomics
+        for (int i = 0; i < per; ++i) {
+          const uint32_t k = myrow[i];
+          if (k != 0 && (k & pmask) == prefix) atomicAdd(&hist[(k >> shift) & 255u], 1);
+        }
       }
       __syncthreads();
-      if (tid == 0) {
-        int acc = 0, d = 255;
-        for (; d > 0; --d) {
-          if (acc + hist[d] >= need) break;
-          acc += hist[d];
+      if (tid < 64) {
+        // wave 0 finds the digit: lane l holds bins 255-4l .. 252-4l (descending)
+        int c[4], sl = 0;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) { c[e] = hist[255 - 4 * lane - e]; sl += c[e]; }
+        int incl = sl;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+          const int y = __shfl_up(incl, o, 64);
+          if (lane >= o) incl += y;
         }
-        misc[0] = d;
-        misc[1] = need - acc;
+        const uint64_t hit = __ballot(incl >= need);
+        const int first = hit ? __ffsll((unsigned long long)hit) - 1 : 63;
+        if (lane == first) {
+          int acc = incl - sl, d = 255 - 4 * lane;
+#pragma unroll
+          for (int e = 0; e < 3; ++e) {
+            if (acc + c[e] >= need) break;
+            acc += c[e];
+            d -= 1;
+          }
+          misc[0] = d;
+          misc[1] = need - acc;
+        }
       }
       __syncthreads();
       prefix |= (uint32_t)misc[0] << shift;
@@ -135,7 +196,7 @@ __global__ __launch_bounds__(256) void pq_select_kernel(PqSelectArgs a) {
   }
   auto kept_of = [&](int j, int eq_before) -> bool {
     if (is_forced(j)) return true;
-    const uint32_t k = rk[j];
+    const uint32_t k = myrow[j - j0];
     if (k == 0) return false;                 // not in the union (or forced, handled above)
     if (!overflow) return true;
     if (budget == 0) return false;
@@ -146,7 +207,7 @@ __global__ __launch_bounds__(256) void pq_select_kernel(PqSelectArgs a) {
   int eq_base = 0;
   if (overflow && budget > 0) {
     int ceq = 0;
-    for (int j = j0; j < j1; ++j) ceq += rk[j] == V && !is_forced(j);
+    for (int j = j0; j < j1; ++j) ceq += myrow[j - j0] == V && !is_forced(j);
     eq_base = pq_block_exclusive_sum(ceq, tmp);
   }
   // ---- compaction: dense ranks (perquery.py:414-442) ----
@@ -155,7 +216,7 @@ __global__ __launch_bounds__(256) void pq_select_kernel(PqSelectArgs a) {
     int eq = eq_base;
     for (int j = j0; j < j1; ++j) {
       const bool kp = kept_of(j, eq);
-      eq += rk[j] == V && !is_forced(j) && overflow && budget > 0;
+      eq += myrow[j - j0] == V && !is_forced(j) && overflow && budget > 0;
       ck += kp;
     }
   }
@@ -171,7 +232,7 @@ __global__ __launch_bounds__(256) void pq_select_kernel(PqSelectArgs a) {
     int rank = base - 1;
     for (int j = j0; j < j1; ++j) {
       const bool kp = kept_of(j, eq);
-      eq += rk[j] == V && !is_forced(j) && overflow && budget > 0;
+      eq += myrow[j - j0] == V && !is_forced(j) && overflow && budget > 0;
       if (kp) {
         rank += 1;
         if (rank < a.k_max) {
@@ -224,7 +285,7 @@ __global__ __launch_bounds__(256) void expand_pq_kernel(const uint32_t* __restri
 size_t pq_select_lds_bytes(int N, int k_max) {
   (void)k_max;
   const size_t per = (size_t)(N + 255) / 256;
-  return 256 * per * 4 + (256 + 8 + 8) * 4 + 64 * 4;
+  return 256 * (per | 1) * 4 + (256 + 8 + 8) * 4 + 64 * 4;
 }
 
 hipError_t launch_pq_select(const PqSelectArgs& a, hipStream_t st) {
