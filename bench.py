@@ -31,6 +31,7 @@ PEAK_BF16_TFLOPS = 2500.0      # MI355X dense bf16 MFMA
 PEAK_FP32_TFLOPS = 157.3
 PEAK_HBM_GBS = 8000.0          # MI355X HBM3E
 STAGES = ["rope", "score", "select", "gather"]
+STREAM_STAGES = ["rope", "score", "attend_rope", "stream"]
 
 
 def parse():
@@ -95,7 +96,10 @@ def cpu_baseline(cfg, q, k, v, invf, ps, rs, budget_s):
         vn, _ = orc.from_torch(v[0, h // (cfg.H // cfg.Hkv):h // (cfg.H // cfg.Hkv) + 1])
         tau = np.full(1, cfg.tau, np.float32)
         t0 = time.perf_counter()
-        if cfg.variant == "pq":
+        if cfg.variant == "pqstream":
+            orc.pqstream(qn, kn, vn, dt, tau, invf.numpy(), invf.numpy(), ps, rs, sm, cfg.n_global,
+                         cfg.n_local, cfg.tile, 32, "max", True, want_band=False)
+        elif cfg.variant == "pq":
             orc.shared_pq_attention(qn, kn, vn, dt, tau, invf.numpy(), invf.numpy(), ps, rs, sm,
                                     cfg.n_global, cfg.n_local, cfg.tile, cfg.k_max, 64, 0, cfg.select_score)
         else:
@@ -108,8 +112,8 @@ def cpu_baseline(cfg, q, k, v, invf, ps, rs, budget_s):
     heads = max(1, min(cfg.H, int(budget_s / max(t_first, 1e-3))))
     total = t_first + sum(one(h) for h in range(1, heads))
     per_head = total / heads
-    stages = ("Kernel A + _build_sets_pq + masked Kernel C" if cfg.variant == "pq"
-              else "Kernel A + _build_sets + Kernel C")
+    stages = {"pq": "Kernel A + _build_sets_pq + masked Kernel C",
+              "pqstream": "the fused PQ Stream kernel"}.get(cfg.variant, "Kernel A + _build_sets + Kernel C")
     return {"value": round(cfg.N / (per_head * cfg.H), 3), "unit": "tokens/s", "cores": threads,
             "kind": "port",
             "sample": f"{heads} of {cfg.H} heads of the same workload through the CPU oracle "
@@ -140,7 +144,10 @@ def main():
     q, k, v = q_cpu.to(dev), k_cpu.to(dev), v_cpu.to(dev)
     invf, ps, rs = cfg.geometry()
     tau = torch.full((cfg.H,), cfg.tau)
-    if cfg.variant == "pq":
+    if cfg.variant == "pqstream":
+        plan = native.StreamPlan(q, k, v, tau, invf, invf, ps, rs, tile=cfg.tile, block_n=32,
+                                 n_global=cfg.n_global, n_local=cfg.n_local)
+    elif cfg.variant == "pq":
         plan = native.PqPlan(q, k, v, tau, invf, invf, ps, rs, tile=cfg.tile, k_max=cfg.k_max,
                              n_global=cfg.n_global, n_local=cfg.n_local, select_score=cfg.select_score)
     else:
@@ -163,24 +170,47 @@ def main():
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     ms_per_step = elapsed * 1000.0 / args.steps
+    stages = STREAM_STAGES if cfg.variant == "pqstream" else STAGES
     stage_ms = {s: sum(evs[i][j].elapsed_time(evs[i][j + 1]) for i in range(args.steps)) / args.steps
-                for j, s in enumerate(STAGES)}
+                for j, s in enumerate(stages)}
     r = plan.out
     esz = q.element_size()
-    kept = r["kept_size"]
-    gbytes = gather_bytes(kept, cfg.k_max, cfg.D, esz, cfg.H, cfg.N)
-    score_tf = cfg.score_flops() / (stage_ms["score"] * 1e-3) / 1e12
-    gather_gbs = gbytes / (stage_ms["gather"] * 1e-3) / 1e9
     peak_tf = PEAK_FP32_TFLOPS if q.dtype == torch.float32 else PEAK_BF16_TFLOPS
+    score_tf = cfg.score_flops() / (stage_ms["score"] * 1e-3) / 1e12
     roof_score = {"kernel": "score_kernel", "bound": "mfma", "achieved": round(score_tf, 2),
                   "peak": peak_tf, "unit": "TFLOP/s", "frac": round(score_tf / peak_tf, 4),
-                  "algorithmic_per_launch": cfg.score_flops(), "traffic": None}
-    roof_gather = {"kernel": "gather_kernel", "bound": "hbm", "achieved": round(gather_gbs, 1),
-                   "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(gather_gbs / PEAK_HBM_GBS, 4),
-                   "algorithmic_per_launch": int(gbytes), "traffic": None}
-    roof_score["traffic"] = read_traffic(args.traffic_file, "score_kernel")
-    roof_gather["traffic"] = read_traffic(args.traffic_file, "gather_kernel")
-    dominant = roof_score if stage_ms["score"] >= stage_ms["gather"] else roof_gather
+                  "algorithmic_per_launch": cfg.score_flops(),
+                  "traffic": read_traffic(args.traffic_file, "score_kernel")}
+    if cfg.variant == "pqstream":
+        # the sweep's products: Q.K^T and P.V over the causal pairs
+        sflops = 2 * 2 * cfg.D * cfg.H * cfg.N * (cfg.N + 1) // 2
+        stream_tf = sflops / (stage_ms["stream"] * 1e-3) / 1e12
+        roof_second = {"kernel": "stream_kernel", "bound": "mfma", "achieved": round(stream_tf, 2),
+                       "peak": peak_tf, "unit": "TFLOP/s", "frac": round(stream_tf / peak_tf, 4),
+                       "algorithmic_per_launch": sflops,
+                       "traffic": read_traffic(args.traffic_file, "stream_kernel")}
+        second = "stream"
+        kept = r["kept"]
+        selection = {"kept_per_query_mean": round(kept.float().mean().item(), 1),
+                     "span_max": float(r["span"].max().item()),
+                     "skipped_blocks": int(r["skipped"].sum().item()),
+                     "blocks": int(r["blocks"].sum().item())}
+    else:
+        kept = r["kept_size"]
+        gbytes = gather_bytes(kept, cfg.k_max, cfg.D, esz, cfg.H, cfg.N)
+        gather_gbs = gbytes / (stage_ms["gather"] * 1e-3) / 1e9
+        roof_second = {"kernel": "gather_kernel", "bound": "hbm", "achieved": round(gather_gbs, 1),
+                       "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(gather_gbs / PEAK_HBM_GBS, 4),
+                       "algorithmic_per_launch": int(gbytes),
+                       "traffic": read_traffic(args.traffic_file, "gather_kernel")}
+        second = "gather"
+        if cfg.variant == "pq":
+            selection = {"kept_mean": round(kept.float().mean().item(), 1),
+                         "overflow_tiles": int(r["overflow"].sum().item()), "tiles": int(kept.numel())}
+        else:
+            selection = {"kept_mean": round(kept.float().mean().item(), 1),
+                         "overflow20_tiles": int(r["overflow20"].sum().item()), "tiles": int(kept.numel())}
+    dominant = roof_score if stage_ms["score"] >= stage_ms[second] else roof_second
     print(f"[bench] {ms_per_step:.3f} ms/step; stages {stage_ms}", file=sys.stderr, flush=True)
 
     cpu = None
@@ -208,13 +238,8 @@ def main():
                    "pos_scale": ps, "rope_scale": rs, "parallelism": "none (1 GPU)"},
         "stages_ms": {s: round(t, 4) for s, t in stage_ms.items()},
         "roofline": dominant,
-        "rooflines": {"score": roof_score, "gather": roof_gather},
-        "selection": ({"kept_mean": round(kept.float().mean().item(), 1),
-                       "overflow_tiles": int(r["overflow"].sum().item()),
-                       "tiles": int(kept.numel())} if cfg.variant == "pq" else
-                      {"kept_mean": round(kept.float().mean().item(), 1),
-                       "overflow20_tiles": int(r["overflow20"].sum().item()),
-                       "tiles": int(kept.numel())}),
+        "rooflines": {"score": roof_score, second: roof_second},
+        "selection": selection,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

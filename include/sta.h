@@ -182,6 +182,51 @@ int sta_pq_build_sets(const sta_pq_args* args, const int32_t* votes, const int32
  * Replaces the _gather_attn_pq_kernel launch, perquery.py:226-312, 511-524. */
 int sta_pq_gather_attention(const sta_pq_args* args, void* stream);
 
+/* ------------------------------------------------------------------------------------------ */
+/* Per-query variant, PQ Stream: every query keeps its own threshold passers (plus forced      */
+/* global / local keys) and attends them in one sweep over aligned key blocks, newest first;   */
+/* key positions stream: npk = -(d + hi_t - j), d advancing per block by the largest per-query */
+/* kept count (or the block's slot count).  No index sets, no k_max.  tile must be 32.          */
+/* ------------------------------------------------------------------------------------------ */
+#define STA_ADV_MAX 0   /* d += max_i c_i */
+#define STA_ADV_FULL 1  /* d += slots the block occupies (native RoPE distances) */
+
+typedef struct sta_pqstream_args {
+  const void* q;
+  const void* k;
+  const void* v;
+  int64_t q_head_stride, q_tok_stride;
+  int64_t k_head_stride, k_tok_stride;
+  int64_t v_head_stride, v_tok_stride;
+  int32_t dtype;
+  int32_t H, Hkv, N, D;
+  const float* tau;         /* (H,) */
+  const float* inv_freq_a;  /* (D/2,) selection geometry */
+  float pos_scale_a, rope_scale_a;
+  const float* inv_freq_c;  /* (D/2,) attend geometry (base RoPE, scale 1) */
+  float sm_scale;
+  int32_t n_global, n_local, tile, block_n, pos_advance, use_skip, q_pos_base;
+  /* outputs (device) */
+  void* out;                /* (H, N, D) */
+  float* span;              /* (H, nt) final base d of each tile */
+  int32_t* kept;            /* (H, N) keys each query attended */
+  float* blocks;            /* (H, nt) key blocks of each tile */
+  float* skipped;           /* (H, nt) blocks no query kept a key of */
+  /* optional outputs (NULL to skip) */
+  float* row_max;           /* (H, N) exact row max under the selection geometry */
+  void* workspace;
+  size_t workspace_bytes;
+  void* const* stage_events; /* NULL or 5 hipEvent_t: before RoPE, before the score passes,
+                                before the attend pre-rotation, before the sweep, after it */
+} sta_pqstream_args;
+
+/* Bytes of device workspace sta_pqstream_attention needs for these arguments. */
+size_t sta_pqstream_workspace_size(const sta_pqstream_args* args);
+
+/* The PQ Stream prefill.  Replaces pqstream_attention and its fused _pqstream_kernel,
+ * pqstream_kernel.py:174-368, 498-564.  block_n in {32, 64}; q_pos_base must be 0 (:512). */
+int sta_pqstream_attention(const sta_pqstream_args* args, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

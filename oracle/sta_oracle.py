@@ -310,9 +310,10 @@ def shared_pq_attention(q, k, v, dtype, tau, inv_freq_a, inv_freq_c, pos_scale_a
 
 def pqstream(q, k, v, dtype, tau, inv_freq_a, inv_freq_c, pos_scale_a=1.0, rope_scale_a=1.0,
              sm_scale=None, n_global=32, n_local=32, tile=32, block_n=32, pos_advance="max",
-             use_skip=True, band_eps=1e-3):
+             use_skip=True, band_eps=1e-3, bits_in=None, want_band=True):
     """The fused PQ Stream kernel (pqstream_kernel.py:174-368).  Returns (out_f32, span, kept,
-    blocks, skipped, band_rows)."""
+    blocks, skipped, band_rows).  With bits_in (H, nt, N) int32 the threshold decisions are taken
+    from those bits (bit i = row i of the tile) instead of being recomputed."""
     q = np.ascontiguousarray(q)
     k = np.ascontiguousarray(k)
     v = np.ascontiguousarray(v)
@@ -326,13 +327,14 @@ def pqstream(q, k, v, dtype, tau, inv_freq_a, inv_freq_c, pos_scale_a=1.0, rope_
     blocks = np.empty((H, nt), np.float32)
     skipped = np.empty((H, nt), np.float32)
     kept = np.empty((H, N), np.int32)
-    band_rows = np.empty((H, N), np.int32)
+    band_rows = np.empty((H, N), np.int32) if want_band else None
+    bits_c = _c(bits_in, np.int32) if bits_in is not None else None
     lib().oracle_pqstream(
         _p(q), _p(k), _p(v), ctypes.c_int(dtype), ctypes.c_int(H), ctypes.c_int(Hkv),
         ctypes.c_int(N), ctypes.c_int(D), _p(_c(tau, np.float32)), _p(_c(inv_freq_a, np.float32)),
         _p(_c(inv_freq_c, np.float32)), ctypes.c_float(pos_scale_a), ctypes.c_float(rope_scale_a),
         ctypes.c_float(sm_scale), ctypes.c_int(n_global), ctypes.c_int(n_local), ctypes.c_int(tile),
         ctypes.c_int(block_n), ctypes.c_int(1 if pos_advance == "full" else 0),
-        ctypes.c_int(int(use_skip)), _p(out), _p(span), _p(kept), _p(blocks), _p(skipped),
-        _p(band_rows), ctypes.c_float(band_eps))
+        ctypes.c_int(int(use_skip)), _p(bits_c), _p(out), _p(span), _p(kept), _p(blocks),
+        _p(skipped), _p(band_rows), ctypes.c_float(band_eps))
     return out, span, kept, blocks, skipped, band_rows

@@ -246,13 +246,16 @@ void oracle_build_sets_pq(const int32_t* votes, const int32_t* bits, const float
  * out (H, N, D) fp32 accumulator before the final cast; span, blocks, skipped (H, nt) fp32;
  * kept (H, N) int32 (kept keys per query); band_rows (H, N) int32 or NULL: per query, # of its
  * causal non-forced keys whose select score lies within band_eps of m - tau.
+ * bits_in (H, nt, N) int32 or NULL: when given, the threshold decision s >= m - tau of row i for
+ * key j is bit i of bits_in[h, t, j] instead of the scores computed here (forced keys, the
+ * causal mask and everything after the decision are unchanged).
  */
 void oracle_pqstream(const void* q, const void* k, const void* v, int dtype, int H, int Hkv, int N,
                      int D, const float* tau, const float* inv_freq_a, const float* inv_freq_c,
                      float pos_scale_a, float rope_scale_a, float sm_scale, int n_global,
-                     int n_local, int tile, int block_n, int adv_full, int use_skip, float* out,
-                     float* span, int32_t* kept, float* blocks, float* skipped, int32_t* band_rows,
-                     float band_eps) {
+                     int n_local, int tile, int block_n, int adv_full, int use_skip,
+                     const int32_t* bits_in, float* out, float* span, int32_t* kept, float* blocks,
+                     float* skipped, int32_t* band_rows, float band_eps) {
   const int T = tile, BN = block_n;
   const int nt = (N + T - 1) / T;
   const int group = H / Hkv;
@@ -301,6 +304,7 @@ void oracle_pqstream(const void* q, const void* k, const void* v, int dtype, int
         rope_row(q, dtype, ((size_t)h * N + row) * D, D, cp, inv_freq_a, rope_scale_a, qs + (size_t)r * D);
         volatile float npq = (float)(row - P_top);                    /* :222 */
         rope_row(q, dtype, ((size_t)h * N + row) * D, D, npq, inv_freq_c, 1.0f, qa + (size_t)r * D);
+        if (bits_in && !band_rows) continue;                          /* decisions are given */
         for (int j = 0; j <= row; ++j) {                              /* pass 1, :229-244 */
           const float s = score_of(qs + (size_t)r * D, ks + ((size_t)hk * N + j) * D, D, sm_scale);
           if (s > m[r]) m[r] = s;
@@ -321,10 +325,16 @@ void oracle_pqstream(const void* q, const void* k, const void* v, int dtype, int
             keep[r * BN + b] = 0;
             if (row >= N || j >= N || j > row) continue;              /* causal, row_ok, n_ok */
             const int forced = (j < n_global) || (j >= loc_lo && j <= loc_hi);
-            const float s = score_of(qs + (size_t)r * D, ks + ((size_t)hk * N + j) * D, D, sm_scale);
-            volatile float thr = m[r] - tau_h;
-            if (!forced && band_rows && fabsf(s - thr) < band_eps) band_rows[(size_t)h * N + row] += 1;
-            const int kp = (s >= thr) || forced;                      /* :285-286 */
+            int pass;
+            if (bits_in && !band_rows) {
+              pass = ((uint32_t)bits_in[((size_t)h * nt + t) * N + j] >> r) & 1u;
+            } else {
+              const float s = score_of(qs + (size_t)r * D, ks + ((size_t)hk * N + j) * D, D, sm_scale);
+              volatile float thr = m[r] - tau_h;
+              if (!forced && band_rows && fabsf(s - thr) < band_eps) band_rows[(size_t)h * N + row] += 1;
+              pass = bits_in ? (int)(((uint32_t)bits_in[((size_t)h * nt + t) * N + j] >> r) & 1u) : (s >= thr);
+            }
+            const int kp = pass || forced;                            /* :285-286 */
             keep[r * BN + b] = (uint8_t)kp;
             c += kp;
           }

@@ -19,7 +19,7 @@ DTYPES = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
 EXPORTS = ["sta_abi_version", "sta_last_error", "sta_shared_workspace_size", "sta_shared_attention",
            "sta_select_vote", "sta_build_sets", "sta_gather_attention",
            "sta_pq_workspace_size", "sta_pq_attention", "sta_pq_select_bits", "sta_pq_build_sets",
-           "sta_pq_gather_attention"]
+           "sta_pq_gather_attention", "sta_pqstream_workspace_size", "sta_pqstream_attention"]
 SCORES = {"freq": 0, "margin": 1, "expmass": 2}
 
 
@@ -73,6 +73,28 @@ class PqArgs(ctypes.Structure):
     ]
 
 
+class StreamArgsC(ctypes.Structure):
+    """Mirror of sta_pqstream_args (include/sta.h)."""
+    _fields_ = [
+        ("q", ctypes.c_void_p), ("k", ctypes.c_void_p), ("v", ctypes.c_void_p),
+        ("q_head_stride", ctypes.c_int64), ("q_tok_stride", ctypes.c_int64),
+        ("k_head_stride", ctypes.c_int64), ("k_tok_stride", ctypes.c_int64),
+        ("v_head_stride", ctypes.c_int64), ("v_tok_stride", ctypes.c_int64),
+        ("dtype", ctypes.c_int32), ("H", ctypes.c_int32), ("Hkv", ctypes.c_int32),
+        ("N", ctypes.c_int32), ("D", ctypes.c_int32),
+        ("tau", ctypes.c_void_p),
+        ("inv_freq_a", ctypes.c_void_p), ("pos_scale_a", ctypes.c_float), ("rope_scale_a", ctypes.c_float),
+        ("inv_freq_c", ctypes.c_void_p), ("sm_scale", ctypes.c_float),
+        ("n_global", ctypes.c_int32), ("n_local", ctypes.c_int32), ("tile", ctypes.c_int32),
+        ("block_n", ctypes.c_int32), ("pos_advance", ctypes.c_int32), ("use_skip", ctypes.c_int32),
+        ("q_pos_base", ctypes.c_int32),
+        ("out", ctypes.c_void_p), ("span", ctypes.c_void_p), ("kept", ctypes.c_void_p),
+        ("blocks", ctypes.c_void_p), ("skipped", ctypes.c_void_p), ("row_max", ctypes.c_void_p),
+        ("workspace", ctypes.c_void_p), ("workspace_bytes", ctypes.c_size_t),
+        ("stage_events", ctypes.c_void_p),
+    ]
+
+
 def lib():
     """Load libsta_hip.so once; raise loudly if it is absent."""
     global _LIB
@@ -101,6 +123,10 @@ def lib():
         L.sta_pq_build_sets.restype = ctypes.c_int
         L.sta_pq_build_sets.argtypes = [ctypes.POINTER(PqArgs), ctypes.c_void_p, ctypes.c_void_p,
                                         ctypes.c_void_p, ctypes.c_int32, ctypes.c_void_p]
+        L.sta_pqstream_workspace_size.restype = ctypes.c_size_t
+        L.sta_pqstream_workspace_size.argtypes = [ctypes.POINTER(StreamArgsC)]
+        L.sta_pqstream_attention.restype = ctypes.c_int
+        L.sta_pqstream_attention.argtypes = [ctypes.POINTER(StreamArgsC), ctypes.c_void_p]
         if L.sta_abi_version() != 1:
             raise ImportError("libsta_hip.so ABI version mismatch")
         _LIB = L
@@ -498,3 +524,74 @@ def pq_gather_attention(q, k, v, inv_freq_c, idx, newpos_k, newpos_q, mask, sm_s
     a.kept_size = _ptr(ks)
     _check(lib().sta_pq_gather_attention(ctypes.byref(a), _stream(dev)), "sta_pq_gather_attention")
     return out
+
+
+# ---------------------------------------------------------------------------------------------
+# PQ Stream (per-query keep sets, streamed block positions, one attend sweep)
+# ---------------------------------------------------------------------------------------------
+ADVANCES = {"max": 0, "full": 1}
+
+
+class StreamPlan:
+    """Outputs and workspace of the PQ Stream prefill for one shape, allocated once; run()
+    launches the whole path on the current stream and allocates nothing."""
+
+    def __init__(self, q, k, v, tau, inv_freq_a, inv_freq_c, pos_scale_a=1.0, rope_scale_a=1.0,
+                 sm_scale=None, n_global=32, n_local=32, tile=32, block_n=32, pos_advance="max",
+                 q_pos_base=0, use_skip=True, want_row_max=False):
+        qh, kh, vh, tau, ifa, ifc = _prep_inputs(q, k, v, tau, inv_freq_a, inv_freq_c)
+        H, N, D = qh.shape
+        self.device = dev = qh.device
+        if sm_scale is None:
+            sm_scale = 1.0 / math.sqrt(D)
+        if pos_advance not in ADVANCES:
+            raise KeyError(pos_advance)
+        self.args = a = StreamArgsC()
+        a.q, a.k, a.v = _ptr(qh), _ptr(kh), _ptr(vh)
+        a.q_head_stride, a.q_tok_stride = qh.stride(0), qh.stride(1)
+        a.k_head_stride, a.k_tok_stride = kh.stride(0), kh.stride(1)
+        a.v_head_stride, a.v_tok_stride = vh.stride(0), vh.stride(1)
+        a.dtype = DTYPES[qh.dtype]
+        a.H, a.Hkv, a.N, a.D = H, kh.shape[0], N, D
+        a.tau = _ptr(tau)
+        a.inv_freq_a, a.pos_scale_a, a.rope_scale_a = _ptr(ifa), float(pos_scale_a), float(rope_scale_a)
+        a.inv_freq_c, a.sm_scale = _ptr(ifc), float(sm_scale)
+        a.n_global, a.n_local, a.tile, a.block_n = int(n_global), int(n_local), int(tile), int(block_n)
+        a.pos_advance, a.use_skip, a.q_pos_base = ADVANCES[pos_advance], int(bool(use_skip)), int(q_pos_base)
+        self._keep = (qh, kh, vh, tau, ifa, ifc)
+        nt = (N + tile - 1) // tile
+        r = {"out": torch.empty((H, N, D), dtype=qh.dtype, device=dev),
+             "span": torch.empty((H, nt), dtype=torch.float32, device=dev),
+             "kept": torch.empty((H, N), dtype=torch.int32, device=dev),
+             "blocks": torch.empty((H, nt), dtype=torch.float32, device=dev),
+             "skipped": torch.empty((H, nt), dtype=torch.float32, device=dev)}
+        if want_row_max:
+            r["row_max"] = torch.empty((H, N), dtype=torch.float32, device=dev)
+        for name in ("out", "span", "kept", "blocks", "skipped", "row_max"):
+            setattr(a, name, _ptr(r.get(name)))
+        self.out = r
+        n = lib().sta_pqstream_workspace_size(ctypes.byref(a))
+        if n == 0:
+            _check(-1, "sta_pqstream_workspace_size")
+        self.workspace = torch.empty(n, dtype=torch.uint8, device=dev)
+        a.workspace, a.workspace_bytes = _ptr(self.workspace), n
+        self._events = None
+
+    def run(self, events=None):
+        if events is not None:
+            self._events = (ctypes.c_void_p * 5)(*[e.cuda_event for e in events])
+            self.args.stage_events = ctypes.cast(self._events, ctypes.c_void_p)
+        else:
+            self.args.stage_events = None
+        _check(lib().sta_pqstream_attention(ctypes.byref(self.args), _stream(self.device)),
+               "sta_pqstream_attention")
+        return self.out
+
+
+def pqstream_attention(q, k, v, tau, inv_freq_a, inv_freq_c, pos_scale_a=1.0, rope_scale_a=1.0,
+                       sm_scale=None, n_global=32, n_local=32, tile=32, block_n=32, pos_advance="max",
+                       q_pos_base=0, use_skip=True, want_row_max=False):
+    """The whole PQ Stream prefill on the device; returns a dict of device tensors."""
+    return StreamPlan(q, k, v, tau, inv_freq_a, inv_freq_c, pos_scale_a, rope_scale_a, sm_scale,
+                      n_global, n_local, tile, block_n, pos_advance, q_pos_base, use_skip,
+                      want_row_max).run()

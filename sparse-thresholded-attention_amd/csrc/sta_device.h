@@ -108,6 +108,11 @@ __device__ __forceinline__ floatx16 mfma32(const u32x4& a, const u32x4& b, float
                                                  __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
 }
 
+__device__ __forceinline__ floatx16 mfma32_f16(const u32x4& a, const u32x4& b, floatx16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
+                                                __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+}
+
 __device__ __forceinline__ floatx4 mfma16(const u32x4& a, const u32x4& b, floatx4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
                                                  __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
@@ -117,6 +122,41 @@ __device__ __forceinline__ floatx4 mfma16_f16(const u32x4& a, const u32x4& b, fl
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
                                                 __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
 }
+
+// ------------------------------------------------------------------------------------------
+// 8 consecutive elements in their storage format (loaded now, converted later)
+template <int DT>
+struct Raw8 {
+  u32x4 w;
+  __device__ __forceinline__ void load(const void* p, int64_t i) { w = *(const u32x4*)((const uint16_t*)p + i); }
+  __device__ __forceinline__ void zero() { w = u32x4{0, 0, 0, 0}; }
+  __device__ __forceinline__ void to_f32(float* o) const {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      if constexpr (DT == DT_BF16) {
+        o[2 * e] = __uint_as_float(w[e] << 16);
+        o[2 * e + 1] = __uint_as_float(w[e] & 0xffff0000u);
+      } else {
+        o[2 * e] = f16_bits_to_f32(w[e] & 0xffffu);
+        o[2 * e + 1] = f16_bits_to_f32(w[e] >> 16);
+      }
+    }
+  }
+};
+template <>
+struct Raw8<DT_F32> {
+  u32x4 a, b;
+  __device__ __forceinline__ void load(const void* p, int64_t i) {
+    const u32x4* q = (const u32x4*)((const float*)p + i);
+    a = q[0];
+    b = q[1];
+  }
+  __device__ __forceinline__ void zero() { a = u32x4{0, 0, 0, 0}; b = a; }
+  __device__ __forceinline__ void to_f32(float* o) const {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) { o[e] = __uint_as_float(a[e]); o[4 + e] = __uint_as_float(b[e]); }
+  }
+};
 
 // ------------------------------------------------------------------------------------------
 // sin/cos of an fp32 angle for the attend-side rotation.

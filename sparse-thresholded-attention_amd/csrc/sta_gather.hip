@@ -39,40 +39,6 @@ struct GatherCfg {
   static size_t lds_bytes(int k_max) { return LDS_FIXED + (size_t)((k_max + 63) / 64) * 64 * 4; }
 };
 
-// 8 consecutive elements in their storage format (loaded now, converted later)
-template <int DT>
-struct Raw8 {
-  u32x4 w;
-  __device__ __forceinline__ void load(const void* p, int64_t i) { w = *(const u32x4*)((const uint16_t*)p + i); }
-  __device__ __forceinline__ void zero() { w = u32x4{0, 0, 0, 0}; }
-  __device__ __forceinline__ void to_f32(float* o) const {
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      if constexpr (DT == DT_BF16) {
-        o[2 * e] = __uint_as_float(w[e] << 16);
-        o[2 * e + 1] = __uint_as_float(w[e] & 0xffff0000u);
-      } else {
-        o[2 * e] = f16_bits_to_f32(w[e] & 0xffffu);
-        o[2 * e + 1] = f16_bits_to_f32(w[e] >> 16);
-      }
-    }
-  }
-};
-template <>
-struct Raw8<DT_F32> {
-  u32x4 a, b;
-  __device__ __forceinline__ void load(const void* p, int64_t i) {
-    const u32x4* q = (const u32x4*)((const float*)p + i);
-    a = q[0];
-    b = q[1];
-  }
-  __device__ __forceinline__ void zero() { a = u32x4{0, 0, 0, 0}; b = a; }
-  __device__ __forceinline__ void to_f32(float* o) const {
-#pragma unroll
-    for (int e = 0; e < 4; ++e) { o[e] = __uint_as_float(a[e]); o[4 + e] = __uint_as_float(b[e]); }
-  }
-};
-
 // One workgroup per (head, tile), specialised waves.  Producer waves gather block b + 1's K and
 // V rows (issued one block ahead of that), rotate K and write both to one half of a
 // double-buffered LDS area while the consumer waves attend block b from the other half; one

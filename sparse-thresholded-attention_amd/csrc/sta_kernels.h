@@ -77,6 +77,25 @@ struct PqSelectArgs {
   uint8_t* overflow;
 };
 
+// PQ Stream attend sweep: pqstream_kernel.py:174-368
+struct StreamArgs {
+  const void* q;
+  int64_t q_head_stride, q_tok_stride;
+  const uint16_t* ktil;     // (Hkv, Npad, P, D) keys rotated at their absolute positions
+  const void* v;
+  int64_t v_head_stride, v_tok_stride;
+  const uint32_t* bits;     // (H, nt, bits_stride) threshold keep bits, bit i = row i
+  int64_t bits_stride;
+  const float* inv_freq;    // attend geometry (base RoPE)
+  float sm_scale;
+  int H, Hkv, N, nt, Npad, n_global, n_local, adv_full, use_skip;
+  void* out;                // (H, N, D)
+  float* span;              // (H, nt)
+  int32_t* kept;            // (H, N)
+  float* blocks;            // (H, nt)
+  float* skipped;           // (H, nt)
+};
+
 hipError_t launch_rope_frag(int dtype, int D, const void* x, int64_t head_stride, int64_t tok_stride,
                             int heads, int N, int rows_pad, int pos_base, float pos_scale,
                             float rope_scale, const float* inv_freq, u32x4* frag, hipStream_t st);
@@ -92,6 +111,10 @@ hipError_t launch_select(const SelectArgs& a, int vote_bytes, hipStream_t st);
 hipError_t launch_expand_votes(const uint8_t* v8, int64_t stride, int H, int nt, int N, int T,
                                int q_pos_base, int32_t* out, hipStream_t st);
 size_t gather_lds_bytes(int dtype, int D, int k_max);
+hipError_t launch_abs_rope(int dtype, int D, const void* x, int64_t hs, int64_t ts, int heads, int N, int Npad,
+                           const float* inv_freq, uint16_t* out, hipStream_t st);
+size_t stream_lds_bytes(int dtype, int D, int BN);
+hipError_t launch_stream(int dtype, int D, int BN, const StreamArgs& a, hipStream_t st);
 hipError_t launch_gather(int dtype, int D, int tile, const GatherArgs& a, hipStream_t st);
 
 }  // namespace sta

@@ -108,4 +108,7 @@ CONFIGS = {
     #    for attention, tau 4, tile 32, k_max 2048
     "c3": Config("c3_pq_union_32h_d128_16k_bf16", 32, 32, 16384, 128, torch.bfloat16, 32, 4.0, 0.01,
                  10000.0, pi_pos_scale(4096, 16384), variant="pq", select_score="expmass"),
+    # 3s: the same shape through PQ Stream (per-query keep, streamed positions, no k_max), BN 32
+    "c3s": Config("c3s_pq_stream_32h_d128_16k_bf16", 32, 32, 16384, 128, torch.bfloat16, 32, 4.0, 0.01,
+                  10000.0, pi_pos_scale(4096, 16384), variant="pqstream"),
 }
