@@ -32,6 +32,7 @@ PEAK_FP32_TFLOPS = 157.3
 PEAK_HBM_GBS = 8000.0          # MI355X HBM3E
 STAGES = ["rope", "score", "select", "gather"]
 STREAM_STAGES = ["rope", "score", "attend_rope", "stream"]
+DCA_STAGES = ["rope", "attention"]
 
 
 def parse():
@@ -96,6 +97,17 @@ def cpu_baseline(cfg, q, k, v, invf, ps, rs, budget_s):
         vn, _ = orc.from_torch(v[0, h // (cfg.H // cfg.Hkv):h // (cfg.H // cfg.Hkv) + 1])
         tau = np.full(1, cfg.tau, np.float32)
         t0 = time.perf_counter()
+        if cfg.variant == "dca":
+            # per-row cost from two evenly spaced row samples (64 and 128 rows); the key rotation
+            # both pay is counted once
+            t = []
+            for n in (64, 128):
+                rows = np.linspace(0, cfg.N - 1, n).astype(np.int32)
+                t1 = time.perf_counter()
+                orc.dca_attention(qn, kn, vn, dt, invf.numpy(), cfg.dca[0], cfg.dca[1], cfg.dca[2], rows=rows)
+                t.append(time.perf_counter() - t1)
+            per_row = max(t[1] - t[0], 1e-9) / 64
+            return max(t[0] - 64 * per_row, 0.0) + per_row * cfg.N
         if cfg.variant == "pqstream":
             orc.pqstream(qn, kn, vn, dt, tau, invf.numpy(), invf.numpy(), ps, rs, sm, cfg.n_global,
                          cfg.n_local, cfg.tile, 32, "max", True, want_band=False)
@@ -113,7 +125,9 @@ def cpu_baseline(cfg, q, k, v, invf, ps, rs, budget_s):
     total = t_first + sum(one(h) for h in range(1, heads))
     per_head = total / heads
     stages = {"pq": "Kernel A + _build_sets_pq + masked Kernel C",
-              "pqstream": "the fused PQ Stream kernel"}.get(cfg.variant, "Kernel A + _build_sets + Kernel C")
+              "pqstream": "the fused PQ Stream kernel",
+              "dca": "the DCA prefill on 64 and 128 evenly spaced query rows, scaled to all rows"}.get(
+                  cfg.variant, "Kernel A + _build_sets + Kernel C")
     return {"value": round(cfg.N / (per_head * cfg.H), 3), "unit": "tokens/s", "cores": threads,
             "kind": "port",
             "sample": f"{heads} of {cfg.H} heads of the same workload through the CPU oracle "
@@ -144,7 +158,9 @@ def main():
     q, k, v = q_cpu.to(dev), k_cpu.to(dev), v_cpu.to(dev)
     invf, ps, rs = cfg.geometry()
     tau = torch.full((cfg.H,), cfg.tau)
-    if cfg.variant == "pqstream":
+    if cfg.variant == "dca":
+        plan = native.DcaPlan(q, k, v, invf, cfg.dca[0], cfg.dca[1], cfg.dca[2])
+    elif cfg.variant == "pqstream":
         plan = native.StreamPlan(q, k, v, tau, invf, invf, ps, rs, tile=cfg.tile, block_n=32,
                                  n_global=cfg.n_global, n_local=cfg.n_local)
     elif cfg.variant == "pq":
@@ -159,7 +175,8 @@ def main():
     torch.cuda.synchronize()
     print(f"[bench] warmup done ({args.warmup} steps), timing {args.steps} steps", file=sys.stderr, flush=True)
 
-    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(5)] for _ in range(args.steps)]
+    stages = {"pqstream": STREAM_STAGES, "dca": DCA_STAGES}.get(cfg.variant, STAGES)
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(len(stages) + 1)] for _ in range(args.steps)]
     for row in evs:                      # materialise the event handles outside the timed region
         for e in row:
             e.record(stream)
@@ -170,18 +187,29 @@ def main():
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     ms_per_step = elapsed * 1000.0 / args.steps
-    stages = STREAM_STAGES if cfg.variant == "pqstream" else STAGES
     stage_ms = {s: sum(evs[i][j].elapsed_time(evs[i][j + 1]) for i in range(args.steps)) / args.steps
                 for j, s in enumerate(stages)}
     r = plan.out
     esz = q.element_size()
     peak_tf = PEAK_FP32_TFLOPS if q.dtype == torch.float32 else PEAK_BF16_TFLOPS
-    score_tf = cfg.score_flops() / (stage_ms["score"] * 1e-3) / 1e12
-    roof_score = {"kernel": "score_kernel", "bound": "mfma", "achieved": round(score_tf, 2),
-                  "peak": peak_tf, "unit": "TFLOP/s", "frac": round(score_tf / peak_tf, 4),
-                  "algorithmic_per_launch": cfg.score_flops(),
-                  "traffic": read_traffic(args.traffic_file, "score_kernel")}
-    if cfg.variant == "pqstream":
+    if cfg.variant != "dca":
+        score_tf = cfg.score_flops() / (stage_ms["score"] * 1e-3) / 1e12
+        roof_score = {"kernel": "score_kernel", "bound": "mfma", "achieved": round(score_tf, 2),
+                      "peak": peak_tf, "unit": "TFLOP/s", "frac": round(score_tf / peak_tf, 4),
+                      "algorithmic_per_launch": cfg.score_flops(),
+                      "traffic": read_traffic(args.traffic_file, "score_kernel")}
+    if cfg.variant == "dca":
+        # dense: Q.K^T and P.V over the causal pairs; no selection passes
+        sflops = 2 * 2 * cfg.D * cfg.H * cfg.N * (cfg.N + 1) // 2
+        attn_tf = sflops / (stage_ms["attention"] * 1e-3) / 1e12
+        roof_score = {"kernel": "dca_attn_kernel", "bound": "mfma", "achieved": round(attn_tf, 2),
+                      "peak": peak_tf, "unit": "TFLOP/s", "frac": round(attn_tf / peak_tf, 4),
+                      "algorithmic_per_launch": sflops,
+                      "traffic": read_traffic(args.traffic_file, "dca_attn_kernel")}
+        roof_second = None
+        second = None
+        selection = None
+    elif cfg.variant == "pqstream":
         # the sweep's products: Q.K^T and P.V over the causal pairs
         sflops = 2 * 2 * cfg.D * cfg.H * cfg.N * (cfg.N + 1) // 2
         stream_tf = sflops / (stage_ms["stream"] * 1e-3) / 1e12
@@ -210,7 +238,10 @@ def main():
         else:
             selection = {"kept_mean": round(kept.float().mean().item(), 1),
                          "overflow20_tiles": int(r["overflow20"].sum().item()), "tiles": int(kept.numel())}
-    dominant = roof_score if stage_ms["score"] >= stage_ms[second] else roof_second
+    if second is None:
+        dominant = roof_score
+    else:
+        dominant = roof_score if stage_ms["score"] >= stage_ms[second] else roof_second
     print(f"[bench] {ms_per_step:.3f} ms/step; stages {stage_ms}", file=sys.stderr, flush=True)
 
     cpu = None
@@ -234,11 +265,13 @@ def main():
         "config": {"workload": cfg.name, "variant": cfg.variant, "heads": cfg.H, "kv_heads": cfg.Hkv,
                    "seq_len": cfg.N, "head_dim": cfg.D, "tile": cfg.tile, "tau": cfg.tau,
                    "pct": cfg.pct if cfg.variant == "shared" else None,
-                   "select_score": cfg.select_score, "k_max": cfg.k_max,
+                   "select_score": cfg.select_score,
+                   "k_max": cfg.k_max if cfg.variant in ("shared", "pq") else None,
+                   "dca_chunk_pretrain_local": cfg.dca,
                    "pos_scale": ps, "rope_scale": rs, "parallelism": "none (1 GPU)"},
         "stages_ms": {s: round(t, 4) for s, t in stage_ms.items()},
         "roofline": dominant,
-        "rooflines": {"score": roof_score, second: roof_second},
+        "rooflines": ({"attention": roof_score} if second is None else {"score": roof_score, second: roof_second}),
         "selection": selection,
         "cpu_baseline": cpu,
     }

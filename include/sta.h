@@ -227,6 +227,39 @@ size_t sta_pqstream_workspace_size(const sta_pqstream_args* args);
  * pqstream_kernel.py:174-368, 498-564.  block_n in {32, 64}; q_pos_base must be 0 (:512). */
 int sta_pqstream_attention(const sta_pqstream_args* args, void* stream);
 
+/* ------------------------------------------------------------------------------------------ */
+/* DCA (dual chunk attention) prefill: dense causal attention with chunk-remapped RoPE         */
+/* positions.  Keys at j mod L (L = chunk_size - local_window); a query i scores its own chunk */
+/* at i mod L, the previous chunk at min(i mod L + L, chunk_size) and older chunks at          */
+/* min(2L - 1, chunk_size); tables cos/sin(t * inv_freq) * mscale in the model dtype, mscale = */
+/* 0.05 ln(N / pretrain_len) + 1 above pretrain_len.  L must be a multiple of 64.               */
+/* ------------------------------------------------------------------------------------------ */
+typedef struct sta_dca_args {
+  const void* q;            /* (H, N, D) raw, before any rotation */
+  const void* k;            /* (Hkv, N, D) raw */
+  const void* v;            /* (Hkv, N, D) */
+  int64_t q_head_stride, q_tok_stride;
+  int64_t k_head_stride, k_tok_stride;
+  int64_t v_head_stride, v_tok_stride;
+  int32_t dtype;
+  int32_t H, Hkv, N, D;
+  const float* inv_freq;    /* (D/2,) base RoPE frequencies */
+  int32_t chunk_size, pretrain_len, local_window;
+  float scale;              /* softmax scale (the module's scaling, 1/sqrt(D) for Llama) */
+  void* out;                /* (H, N, D) */
+  void* workspace;
+  size_t workspace_bytes;
+  void* const* stage_events; /* NULL or 3 hipEvent_t: before the rotations, before the sweep, after */
+} sta_dca_args;
+
+/* Bytes of device workspace sta_dca_attention needs for these arguments. */
+size_t sta_dca_workspace_size(const sta_dca_args* args);
+
+/* The DCA prefill attention core.  Replaces the prefill branch of dca_forward with its position
+ * tables and the log-sum-exp merge of its three attention blocks, dca_kernel.py:166-231,
+ * 278-366, 372-489 (the module the reference installs with install_dca_forward, :660-663). */
+int sta_dca_attention(const sta_dca_args* args, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

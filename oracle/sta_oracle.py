@@ -338,3 +338,34 @@ def pqstream(q, k, v, dtype, tau, inv_freq_a, inv_freq_c, pos_scale_a=1.0, rope_
         ctypes.c_int(int(use_skip)), _p(bits_c), _p(out), _p(span), _p(kept), _p(blocks),
         _p(skipped), _p(band_rows), ctypes.c_float(band_eps))
     return out, span, kept, blocks, skipped, band_rows
+
+
+# ---------------------------------------------------------------------------------------------
+# DCA (dense attention, dual-chunk positions)
+# ---------------------------------------------------------------------------------------------
+def dca_mscale(seq_len, pretrain_len):
+    """The ChunkLlama attention factor: 0.05 ln(seq_len / c) + 1 above c, else 1
+    (dca_kernel.py:163-170; the tables are rebuilt at the prefill length when it exceeds c)."""
+    scale = seq_len / pretrain_len
+    return 1.0 if scale <= 1 else 0.05 * math.log(scale) + 1.0
+
+
+def dca_attention(q, k, v, dtype, inv_freq, chunk_size, pretrain_len, local_window, scale=None,
+                  rows=None):
+    """The prefill branch of dca_forward (dca_kernel.py:372-489) on raw q (H,N,D), k/v (Hkv,N,D).
+    Returns out (H, N, D) fp32; with `rows` only those query rows are computed (others NaN)."""
+    q = np.ascontiguousarray(q)
+    k = np.ascontiguousarray(k)
+    v = np.ascontiguousarray(v)
+    H, N, D = q.shape
+    Hkv = k.shape[0]
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    ms = np.float32(dca_mscale(N, pretrain_len))
+    out = np.full((H, N, D), np.nan, np.float32)
+    r = _c(rows, np.int32) if rows is not None else None
+    lib().oracle_dca(_p(q), _p(k), _p(v), ctypes.c_int(dtype), ctypes.c_int(H), ctypes.c_int(Hkv),
+                     ctypes.c_int(N), ctypes.c_int(D), _p(_c(inv_freq, np.float32)), ctypes.c_int(chunk_size),
+                     ctypes.c_int(local_window), ctypes.c_float(ms), ctypes.c_float(scale), _p(r),
+                     ctypes.c_int(len(r) if r is not None else 0), _p(out))
+    return out

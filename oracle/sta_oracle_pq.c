@@ -404,3 +404,112 @@ void oracle_pqstream(const void* q, const void* k, const void* v, int dtype, int
   }
   free(ks);
 }
+
+/* ------------------------------------------------------------------------------------------- */
+/* DCA: dense attention with dual-chunk positions                 dca_kernel.py:166-231, 278-366, */
+/*                                                                 372-489 (prefill branch)      */
+/* ------------------------------------------------------------------------------------------- */
+/*
+ * Tables (ChunkLlamaRotaryEmbedding._set_cos_sin_cache, dca_kernel.py:166-231): for a position
+ * value t, cos/sin of fl(t * inv_freq[i]) in fp32, times mscale in fp32, then cast to the model
+ * dtype.  Keys sit at j mod L (L = chunk_size - local_window); queries at i mod L (intra chunk),
+ * min(i mod L + L, chunk_size) (one chunk back) and min(2L - 1, chunk_size) (further back).
+ * Rotation x*cos + rotate_half(x)*sin in the model dtype, each product and the sum rounded
+ * (dca_kernel.py:278-286).  Attention: one softmax over every causal key (the reference's three
+ * blocks merged by log-sum-exp, :372-400, 453-489), scores and weights in double, scale `scale`.
+ * rows: the query rows to compute (n_rows of them; NULL = all N).  out (H, N, D) fp32, only
+ * those rows written.
+ */
+static void dca_table(float t, const float* inv_freq, int D, float mscale, int dtype, float* c, float* s) {
+  const int half = D / 2;
+  for (int i = 0; i < half; ++i) {
+    volatile float ang = t * inv_freq[i];
+    volatile float cc = cosf(ang) * mscale;
+    volatile float ss = sinf(ang) * mscale;
+    c[i] = round_to_dtype(cc, dtype);
+    s[i] = round_to_dtype(ss, dtype);
+  }
+}
+
+static void dca_rotate(const void* x, int dtype, size_t off, int D, const float* c, const float* s, float* out) {
+  const int half = D / 2;
+  for (int i = 0; i < half; ++i) {
+    const float x1 = load_elem(x, dtype, off + i), x2 = load_elem(x, dtype, off + half + i);
+    volatile float a = round_to_dtype(x1 * c[i], dtype);
+    volatile float b = round_to_dtype(-x2 * s[i], dtype);
+    volatile float e = round_to_dtype(x2 * c[i], dtype);
+    volatile float f = round_to_dtype(x1 * s[i], dtype);
+    out[i] = round_to_dtype(a + b, dtype);
+    out[half + i] = round_to_dtype(e + f, dtype);
+  }
+}
+
+void oracle_dca(const void* q, const void* k, const void* v, int dtype, int H, int Hkv, int N, int D,
+                const float* inv_freq, int chunk_size, int local_window, float mscale, float scale,
+                const int32_t* rows, int n_rows, float* out) {
+  const int L = chunk_size - local_window;
+  const int half = D / 2;
+  const int group = H / Hkv;
+  const int nr = rows ? n_rows : N;
+  float* kr = (float*)malloc(sizeof(float) * (size_t)Hkv * N * D);
+  {
+    float* c = (float*)malloc(sizeof(float) * half);
+    float* s = (float*)malloc(sizeof(float) * half);
+    for (int j = 0; j < N; ++j) {
+      dca_table((float)(j % L), inv_freq, D, mscale, dtype, c, s);     /* keys: j mod L (:187-190) */
+      for (int hk = 0; hk < Hkv; ++hk)
+        dca_rotate(k, dtype, ((size_t)hk * N + j) * D, D, c, s, kr + ((size_t)hk * N + j) * D);
+    }
+    free(c);
+    free(s);
+  }
+#pragma omp parallel
+  {
+    float* c = (float*)malloc(sizeof(float) * half);
+    float* s = (float*)malloc(sizeof(float) * half);
+    float* qv = (float*)malloc(sizeof(float) * 3 * D);
+    double* sc = (double*)malloc(sizeof(double) * (size_t)N);
+    double* acc = (double*)malloc(sizeof(double) * D);
+#pragma omp for schedule(dynamic, 1)
+    for (int x = 0; x < H * nr; ++x) {
+      const int h = x / nr;
+      const int i = rows ? rows[x % nr] : x % nr;
+      const int hk = h / group;
+      const int pid = i % L;
+      const int cq = i / L;
+      /* intra (:181-182), succ (:185-186), inter at the clamped index L-1 (:464-467) */
+      const int pos_succ = (pid + L) < chunk_size ? pid + L : chunk_size;
+      const int pos_inter = (2 * L - 1) < chunk_size ? 2 * L - 1 : chunk_size;
+      dca_table((float)pid, inv_freq, D, mscale, dtype, c, s);
+      dca_rotate(q, dtype, ((size_t)h * N + i) * D, D, c, s, qv);
+      dca_table((float)pos_succ, inv_freq, D, mscale, dtype, c, s);
+      dca_rotate(q, dtype, ((size_t)h * N + i) * D, D, c, s, qv + D);
+      dca_table((float)pos_inter, inv_freq, D, mscale, dtype, c, s);
+      dca_rotate(q, dtype, ((size_t)h * N + i) * D, D, c, s, qv + 2 * D);
+      double mx = -INFINITY;
+      for (int j = 0; j <= i; ++j) {
+        const int di = cq - j / L;
+        const float* qq = qv + (di == 0 ? 0 : (di == 1 ? D : 2 * D));
+        const float* kk = kr + ((size_t)hk * N + j) * D;
+        double d = 0.0;
+        for (int e = 0; e < D; ++e) d += (double)qq[e] * (double)kk[e];
+        sc[j] = d * (double)scale;
+        if (sc[j] > mx) mx = sc[j];
+      }
+      double l = 0.0;
+      for (int e = 0; e < D; ++e) acc[e] = 0.0;
+      for (int j = 0; j <= i; ++j) {
+        const double p = exp(sc[j] - mx);
+        l += p;
+        for (int e = 0; e < D; ++e) acc[e] += p * (double)load_elem(v, dtype, ((size_t)hk * N + j) * D + e);
+      }
+      for (int e = 0; e < D; ++e) out[((size_t)h * N + i) * D + e] = (float)(acc[e] / l);
+    }
+    free(c);
+    free(s);
+    free(qv);
+    free(sc);
+    free(acc);
+  }
+  free(kr);
+}

@@ -19,7 +19,8 @@ DTYPES = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
 EXPORTS = ["sta_abi_version", "sta_last_error", "sta_shared_workspace_size", "sta_shared_attention",
            "sta_select_vote", "sta_build_sets", "sta_gather_attention",
            "sta_pq_workspace_size", "sta_pq_attention", "sta_pq_select_bits", "sta_pq_build_sets",
-           "sta_pq_gather_attention", "sta_pqstream_workspace_size", "sta_pqstream_attention"]
+           "sta_pq_gather_attention", "sta_pqstream_workspace_size", "sta_pqstream_attention",
+           "sta_dca_workspace_size", "sta_dca_attention"]
 SCORES = {"freq": 0, "margin": 1, "expmass": 2}
 
 
@@ -95,6 +96,23 @@ class StreamArgsC(ctypes.Structure):
     ]
 
 
+class DcaArgsC(ctypes.Structure):
+    """Mirror of sta_dca_args (include/sta.h)."""
+    _fields_ = [
+        ("q", ctypes.c_void_p), ("k", ctypes.c_void_p), ("v", ctypes.c_void_p),
+        ("q_head_stride", ctypes.c_int64), ("q_tok_stride", ctypes.c_int64),
+        ("k_head_stride", ctypes.c_int64), ("k_tok_stride", ctypes.c_int64),
+        ("v_head_stride", ctypes.c_int64), ("v_tok_stride", ctypes.c_int64),
+        ("dtype", ctypes.c_int32), ("H", ctypes.c_int32), ("Hkv", ctypes.c_int32),
+        ("N", ctypes.c_int32), ("D", ctypes.c_int32),
+        ("inv_freq", ctypes.c_void_p),
+        ("chunk_size", ctypes.c_int32), ("pretrain_len", ctypes.c_int32), ("local_window", ctypes.c_int32),
+        ("scale", ctypes.c_float), ("out", ctypes.c_void_p),
+        ("workspace", ctypes.c_void_p), ("workspace_bytes", ctypes.c_size_t),
+        ("stage_events", ctypes.c_void_p),
+    ]
+
+
 def lib():
     """Load libsta_hip.so once; raise loudly if it is absent."""
     global _LIB
@@ -127,6 +145,10 @@ def lib():
         L.sta_pqstream_workspace_size.argtypes = [ctypes.POINTER(StreamArgsC)]
         L.sta_pqstream_attention.restype = ctypes.c_int
         L.sta_pqstream_attention.argtypes = [ctypes.POINTER(StreamArgsC), ctypes.c_void_p]
+        L.sta_dca_workspace_size.restype = ctypes.c_size_t
+        L.sta_dca_workspace_size.argtypes = [ctypes.POINTER(DcaArgsC)]
+        L.sta_dca_attention.restype = ctypes.c_int
+        L.sta_dca_attention.argtypes = [ctypes.POINTER(DcaArgsC), ctypes.c_void_p]
         if L.sta_abi_version() != 1:
             raise ImportError("libsta_hip.so ABI version mismatch")
         _LIB = L
@@ -595,3 +617,52 @@ def pqstream_attention(q, k, v, tau, inv_freq_a, inv_freq_c, pos_scale_a=1.0, ro
     return StreamPlan(q, k, v, tau, inv_freq_a, inv_freq_c, pos_scale_a, rope_scale_a, sm_scale,
                       n_global, n_local, tile, block_n, pos_advance, q_pos_base, use_skip,
                       want_row_max).run()
+
+
+# ---------------------------------------------------------------------------------------------
+# DCA (dense attention, dual-chunk positions)
+# ---------------------------------------------------------------------------------------------
+class DcaPlan:
+    """Output and workspace of the DCA prefill for one shape, allocated once; run() launches the
+    rotations and the attention sweep on the current stream and allocates nothing."""
+
+    def __init__(self, q, k, v, inv_freq, chunk_size, pretrain_len, local_window, scale=None):
+        qh, kh, vh, _, ifc, _ = _prep_inputs(q, k, v, torch.zeros(1), inv_freq, None)
+        H, N, D = qh.shape
+        self.device = dev = qh.device
+        if scale is None:
+            scale = 1.0 / math.sqrt(D)
+        self.args = a = DcaArgsC()
+        a.q, a.k, a.v = _ptr(qh), _ptr(kh), _ptr(vh)
+        a.q_head_stride, a.q_tok_stride = qh.stride(0), qh.stride(1)
+        a.k_head_stride, a.k_tok_stride = kh.stride(0), kh.stride(1)
+        a.v_head_stride, a.v_tok_stride = vh.stride(0), vh.stride(1)
+        a.dtype = DTYPES[qh.dtype]
+        a.H, a.Hkv, a.N, a.D = H, kh.shape[0], N, D
+        a.inv_freq = _ptr(ifc)
+        a.chunk_size, a.pretrain_len, a.local_window = int(chunk_size), int(pretrain_len), int(local_window)
+        a.scale = float(scale)
+        self._keep = (qh, kh, vh, ifc)
+        self.out = {"out": torch.empty((H, N, D), dtype=qh.dtype, device=dev)}
+        a.out = _ptr(self.out["out"])
+        n = lib().sta_dca_workspace_size(ctypes.byref(a))
+        if n == 0:
+            _check(-1, "sta_dca_workspace_size")
+        self.workspace = torch.empty(n, dtype=torch.uint8, device=dev)
+        a.workspace, a.workspace_bytes = _ptr(self.workspace), n
+        self._events = None
+
+    def run(self, events=None):
+        """events: None or 3 recorded torch.cuda.Event(enable_timing=True)."""
+        if events is not None:
+            self._events = (ctypes.c_void_p * 3)(*[e.cuda_event for e in events])
+            self.args.stage_events = ctypes.cast(self._events, ctypes.c_void_p)
+        else:
+            self.args.stage_events = None
+        _check(lib().sta_dca_attention(ctypes.byref(self.args), _stream(self.device)), "sta_dca_attention")
+        return self.out
+
+
+def dca_attention(q, k, v, inv_freq, chunk_size, pretrain_len, local_window, scale=None):
+    """The DCA prefill on the device; returns out (H, N, D) in q.dtype."""
+    return DcaPlan(q, k, v, inv_freq, chunk_size, pretrain_len, local_window, scale).run()["out"]

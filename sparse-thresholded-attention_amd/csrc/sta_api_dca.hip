@@ -1,0 +1,106 @@
+// sta_api_dca.hip -- the C ABI of the DCA prefill (include/sta.h, sta_dca_*).
+#include <math.h>
+#include <string.h>
+
+#include "../../include/sta.h"
+#include "sta_api_util.h"
+#include "sta_kernels.h"
+
+using namespace sta;
+using namespace sta_api;
+
+namespace {
+
+struct DcaLayout {
+  int Npad, planes;
+  size_t krot_off, qrot_off, total;
+};
+
+DcaLayout dca_layout_of(const sta_dca_args* a) {
+  DcaLayout L;
+  L.Npad = (a->N + 63) / 64 * 64;
+  L.planes = a->dtype == STA_DTYPE_F32 ? 2 : 1;
+  size_t off = 0;
+  L.krot_off = off;
+  off = align256(off + (size_t)a->Hkv * L.Npad * L.planes * a->D * 2);
+  L.qrot_off = off;
+  off = align256(off + (size_t)3 * a->H * L.Npad * L.planes * a->D * 2);
+  L.total = off;
+  return L;
+}
+
+int dca_check(const sta_dca_args* a) {
+  if (!a) return fail(STA_ERR_INVALID_ARG, "args is NULL");
+  if (a->dtype != STA_DTYPE_F32 && a->dtype != STA_DTYPE_BF16 && a->dtype != STA_DTYPE_F16)
+    return fail(STA_ERR_INVALID_ARG, "dtype %d is not one of STA_DTYPE_F32/BF16/F16", a->dtype);
+  if (a->H < 1 || a->Hkv < 1 || a->H % a->Hkv != 0)
+    return fail(STA_ERR_INVALID_ARG, "H=%d must be a positive multiple of Hkv=%d", a->H, a->Hkv);
+  if (a->N < 1 || a->N >= (1 << 24)) return fail(STA_ERR_INVALID_ARG, "N=%d out of range [1, 2^24)", a->N);
+  if (a->D != 64 && a->D != 128) return fail(STA_ERR_UNSUPPORTED, "head_dim %d not in {64, 128}", a->D);
+  // dca_kernel.py:552: 0 < w < s
+  if (!(a->local_window > 0 && a->local_window < a->chunk_size))
+    return fail(STA_ERR_INVALID_ARG, "need 0 < local_window(%d) < chunk_size(%d)", a->local_window, a->chunk_size);
+  if (a->pretrain_len < 1) return fail(STA_ERR_INVALID_ARG, "pretrain_len=%d must be >= 1", a->pretrain_len);
+  const int L = a->chunk_size - a->local_window;
+  if (L % 64 != 0)
+    return fail(STA_ERR_UNSUPPORTED, "chunk_size - local_window = %d is not a multiple of 64", L);
+  return STA_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t sta_dca_workspace_size(const sta_dca_args* args) {
+  if (dca_check(args) != STA_OK) return 0;
+  return dca_layout_of(args).total;
+}
+
+int sta_dca_attention(const sta_dca_args* a, void* stream) {
+  int rc = dca_check(a);
+  if (rc != STA_OK) return rc;
+  const int64_t strides[6] = {a->q_head_stride, a->q_tok_stride, a->k_head_stride,
+                              a->k_tok_stride, a->v_head_stride, a->v_tok_stride};
+  if ((rc = check_qkv_ptrs(a->dtype, a->q, a->k, a->v, strides, true)) != STA_OK) return rc;
+  if (!a->inv_freq || !a->out) return fail(STA_ERR_INVALID_ARG, "inv_freq and out must be non-NULL");
+  const DcaLayout L = dca_layout_of(a);
+  if (!a->workspace || a->workspace_bytes < L.total)
+    return fail(STA_ERR_WORKSPACE, "workspace of %zu bytes at %p is smaller than the %zu needed",
+                a->workspace_bytes, a->workspace, L.total);
+  if (((uintptr_t)a->workspace & 255u) != 0) return fail(STA_ERR_WORKSPACE, "workspace must be 256-byte aligned");
+  hipStream_t st = (hipStream_t)stream;
+  char* ws = (char*)a->workspace;
+  uint16_t* krot = (uint16_t*)(ws + L.krot_off);
+  uint16_t* qrot = (uint16_t*)(ws + L.qrot_off);
+  const int Lc = a->chunk_size - a->local_window;
+  // mscale = get_mscale(N / c): 0.05 ln(N / c) + 1 when the prefill outruns c, else 1 (:163-170)
+  const double ratio = (double)a->N / (double)a->pretrain_len;
+  const float mscale = ratio <= 1.0 ? 1.0f : (float)(0.05 * log(ratio) + 1.0);
+
+  if ((rc = mark_event(a->stage_events, 0, st)) != STA_OK) return rc;
+  hipError_t e = launch_dca_rope(a->dtype, a->D, a->k, a->k_head_stride, a->k_tok_stride, a->Hkv, a->N, L.Npad,
+                                 Lc, a->chunk_size, mscale, 1, a->inv_freq, krot, st);
+  if (e != hipSuccess) return hip_fail(e, "dca rotation (k)");
+  e = launch_dca_rope(a->dtype, a->D, a->q, a->q_head_stride, a->q_tok_stride, a->H, a->N, L.Npad, Lc,
+                      a->chunk_size, mscale, 0, a->inv_freq, qrot, st);
+  if (e != hipSuccess) return hip_fail(e, "dca rotation (q)");
+  if ((rc = mark_event(a->stage_events, 1, st)) != STA_OK) return rc;
+  DcaArgs d{};
+  d.qrot = qrot;
+  d.krot = krot;
+  d.v = a->v;
+  d.v_head_stride = a->v_head_stride;
+  d.v_tok_stride = a->v_tok_stride;
+  d.H = a->H;
+  d.Hkv = a->Hkv;
+  d.N = a->N;
+  d.Npad = L.Npad;
+  d.L = Lc;
+  d.scale = a->scale;
+  d.out = a->out;
+  e = launch_dca_attn(a->dtype, a->D, d, st);
+  if (e != hipSuccess) return hip_fail(e, "dca attention");
+  return mark_event(a->stage_events, 2, st);
+}
+
+}  // extern "C"

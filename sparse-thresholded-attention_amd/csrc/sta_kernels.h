@@ -96,6 +96,17 @@ struct StreamArgs {
   float* skipped;           // (H, nt)
 };
 
+// DCA attention sweep: dca_kernel.py:372-489
+struct DcaArgs {
+  const uint16_t* qrot;     // (3, H, Npad, P, D) queries in their intra / succ / inter positions
+  const uint16_t* krot;     // (Hkv, Npad, P, D) keys at j mod L
+  const void* v;
+  int64_t v_head_stride, v_tok_stride;
+  int H, Hkv, N, Npad, L;
+  float scale;
+  void* out;                // (H, N, D)
+};
+
 hipError_t launch_rope_frag(int dtype, int D, const void* x, int64_t head_stride, int64_t tok_stride,
                             int heads, int N, int rows_pad, int pos_base, float pos_scale,
                             float rope_scale, const float* inv_freq, u32x4* frag, hipStream_t st);
@@ -114,6 +125,11 @@ size_t gather_lds_bytes(int dtype, int D, int k_max);
 hipError_t launch_abs_rope(int dtype, int D, const void* x, int64_t hs, int64_t ts, int heads, int N, int Npad,
                            const float* inv_freq, uint16_t* out, hipStream_t st);
 size_t stream_lds_bytes(int dtype, int D, int BN);
+hipError_t launch_dca_rope(int dtype, int D, const void* x, int64_t hs, int64_t ts, int heads, int N, int Npad,
+                           int L, int chunk_size, float mscale, int is_key, const float* inv_freq,
+                           uint16_t* out, hipStream_t st);
+size_t dca_lds_bytes(int dtype, int D);
+hipError_t launch_dca_attn(int dtype, int D, const DcaArgs& a, hipStream_t st);
 hipError_t launch_stream(int dtype, int D, int BN, const StreamArgs& a, hipStream_t st);
 hipError_t launch_gather(int dtype, int D, int tile, const GatherArgs& a, hipStream_t st);
 

@@ -76,8 +76,9 @@ class Config:
     k_max: int = 2048
     n_global: int = 32
     n_local: int = 32
-    variant: str = "shared"     # "shared" (tile-shared sets), "pq" (PQ Union), "pqstream"
+    variant: str = "shared"     # "shared" (tile-shared sets), "pq" (PQ Union), "pqstream", "dca"
     select_score: str = "freq"  # overflow ranking of the per-query variant
+    dca: tuple = None           # (chunk_size, pretrain_len, local_window) of the DCA variant
 
     def geometry(self):
         """(inv_freq, pos_scale, rope_scale) of the selection + attend geometry."""
@@ -111,4 +112,8 @@ CONFIGS = {
     # 3s: the same shape through PQ Stream (per-query keep, streamed positions, no k_max), BN 32
     "c3s": Config("c3s_pq_stream_32h_d128_16k_bf16", 32, 32, 16384, 128, torch.bfloat16, 32, 4.0, 0.01,
                   10000.0, pi_pos_scale(4096, 16384), variant="pqstream"),
+    # 4: dual chunk attention at 64k: chunk 4096, local window 512, pretraining length 4096
+    #    (chunk_len 3584), base RoPE, dense causal attention with remapped positions
+    "c4": Config("c4_dca_32h_d128_64k_bf16", 32, 32, 65536, 128, torch.bfloat16, 64, 5.0, 0.0025,
+                 10000.0, 1.0, variant="dca", dca=(4096, 4096, 512)),
 }
