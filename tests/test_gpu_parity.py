@@ -374,3 +374,15 @@ def test_config1_full_size_head_spot_check():
         err = check_output(r["out"][h:h + 1].float().cpu().numpy(), out_ref, dt, f"c1 head {h}")
         print(f"[result] config 1 head {h}: vote entries differing {ndiff} (band pairs {nband}), "
               f"max out err {err:.2e}", flush=True)
+
+
+def test_config2_full_length_gqa_group():
+    """config 2's geometry at full length (YaRN factor 4 from 8192, theta 5e5, 32768 tokens,
+    d128, bf16) on one GQA group of two query heads sharing a KV head, three-layer check."""
+    from synthetic import CONFIGS, planted_inputs
+    c = CONFIGS["c2"]
+    q, k, v = planted_inputs(0, 2, 1, c.N, c.D, c.frac, c.dtype, DEV)
+    invf, ps, rs = c.geometry()
+    tau = torch.full((2,), c.tau, device=DEV)
+    full_check(q, k, v, tau, invf.to(DEV), ps, rs, pct=c.pct, tile=c.tile, k_max=c.k_max,
+               n_global=c.n_global, n_local=c.n_local, what="config 2 full length, 2 q heads / 1 kv head")

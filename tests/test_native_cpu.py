@@ -99,3 +99,104 @@ def test_yarn_geometry_matches_transformers():
     assert torch.equal(f, ref_f.float())
     assert abs(m - ref_m) < 1e-12
     assert abs(m - 1.1386294361119891) < 1e-12
+
+
+# ------------------------------------------------------------------------------------------------
+# per-query variants and DCA: argument validation, no GPU
+# ------------------------------------------------------------------------------------------------
+def _pq_args(**kw):
+    import _sta_native as native
+    a = native.PqArgs()
+    a.dtype, a.H, a.Hkv, a.N, a.D, a.tile, a.k_max = 1, 32, 32, 16384, 128, 32, 2048
+    a.n_global, a.n_local, a.select_score = 32, 32, 2
+    for k, v in kw.items():
+        setattr(a, k, v)
+    return a
+
+
+@pytest.mark.parametrize("field,value,code", [
+    ("tile", 64, -1), ("D", 80, -2), ("select_score", 5, -1), ("N", 100000, -2), ("k_max", 0, -1),
+])
+def test_pq_invalid_arguments_are_rejected(field, value, code):
+    import _sta_native as native
+    lib = native.lib()
+    a = _pq_args(**{field: value})
+    assert lib.sta_pq_workspace_size(ctypes.byref(a)) == 0
+    assert lib.sta_pq_attention(ctypes.byref(a), None) == code
+    assert len(lib.sta_last_error()) > 0
+
+
+def test_pq_forced_set_must_fit_k_max():
+    """perquery.py:474-476: n_global + n_local + tile - 1 <= k_max, checked before any launch."""
+    import _sta_native as native
+    lib = native.lib()
+    a = _pq_args(k_max=64)
+    buf = ctypes.create_string_buffer(64)
+    a.q = a.k = a.v = ctypes.cast(buf, ctypes.c_void_p)  # non-NULL, 16-byte aligned host memory
+    a.q_tok_stride = a.k_tok_stride = a.v_tok_stride = 128
+    a.tau = a.inv_freq_a = a.inv_freq_c = a.out = ctypes.cast(buf, ctypes.c_void_p)
+    if ctypes.addressof(buf) % 16:
+        pytest.skip("host buffer not 16-byte aligned")
+    assert lib.sta_pq_attention(ctypes.byref(a), None) == -1
+    assert b"forced set" in lib.sta_last_error()
+
+
+def _stream_args(**kw):
+    import _sta_native as native
+    a = native.StreamArgsC()
+    a.dtype, a.H, a.Hkv, a.N, a.D, a.tile, a.block_n = 1, 32, 32, 16384, 128, 32, 32
+    a.n_global, a.n_local, a.pos_advance, a.use_skip = 32, 32, 0, 1
+    for k, v in kw.items():
+        setattr(a, k, v)
+    return a
+
+
+@pytest.mark.parametrize("field,value,code", [
+    ("tile", 64, -1), ("q_pos_base", 3, -1), ("block_n", 16, -1), ("block_n", 128, -2),
+    ("pos_advance", 2, -1), ("D", 96, -2),
+])
+def test_pqstream_invalid_arguments_are_rejected(field, value, code):
+    import _sta_native as native
+    lib = native.lib()
+    a = _stream_args(**{field: value})
+    assert lib.sta_pqstream_workspace_size(ctypes.byref(a)) == 0
+    assert lib.sta_pqstream_attention(ctypes.byref(a), None) == code
+
+
+def test_pqstream_workspace_size_matches_layout():
+    import _sta_native as native
+    lib = native.lib()
+    n = lib.sta_pqstream_workspace_size(ctypes.byref(_stream_args()))
+    N, H, D = 16384, 32, 128
+    need = 2 * H * N * D * 4 + H * (N // 32) * N * 4 + H * N * D * 2   # q/k frags, bits, K~
+    assert need <= n < need + 8192
+
+
+def _dca_args(**kw):
+    import _sta_native as native
+    a = native.DcaArgsC()
+    a.dtype, a.H, a.Hkv, a.N, a.D = 1, 32, 32, 65536, 128
+    a.chunk_size, a.pretrain_len, a.local_window, a.scale = 4096, 4096, 512, 128 ** -0.5
+    for k, v in kw.items():
+        setattr(a, k, v)
+    return a
+
+
+@pytest.mark.parametrize("field,value,code", [
+    ("local_window", 0, -1), ("local_window", 4096, -1), ("chunk_size", 4100, -2), ("D", 32, -2),
+    ("pretrain_len", 0, -1),
+])
+def test_dca_invalid_arguments_are_rejected(field, value, code):
+    import _sta_native as native
+    lib = native.lib()
+    a = _dca_args(**{field: value})
+    assert lib.sta_dca_workspace_size(ctypes.byref(a)) == 0
+    assert lib.sta_dca_attention(ctypes.byref(a), None) == code
+
+
+def test_dca_workspace_size_matches_layout():
+    import _sta_native as native
+    lib = native.lib()
+    n = lib.sta_dca_workspace_size(ctypes.byref(_dca_args()))
+    need = 32 * 65536 * 128 * 2 * 4          # rotated keys + three query variants, bf16
+    assert need <= n < need + 4096
