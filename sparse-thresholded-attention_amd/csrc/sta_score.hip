@@ -82,10 +82,12 @@ __global__ __launch_bounds__(256) void rope_frag_kernel(const void* __restrict__
 // ------------------------------------------------------------------------------------------
 // Score kernel: pass 1 (exact row max) and pass 2 (keep + votes), exact_2.py:87-140.
 //
-// One workgroup = one head and FOUR consecutive query tiles; wave w owns tile 4g+w and holds
-// that tile's Q fragments in registers.  Key chunks of 128 rows are staged once in LDS and read
-// by all four waves, so each K byte fetched from L2 feeds 4 tiles.  Every wave sees every key of
-// its tile, so row maxima and per-key votes complete inside one wave: no cross-wave reduction.
+// One workgroup = one head and 256 consecutive query rows in eight waves of 32 rows (two waves
+// per SIMD, so one wave's epilogue and LDS reads overlap the other's MFMAs).  A wave holds its
+// rows' Q fragments in registers.  Key chunks of 128 rows are staged once in LDS and read by all
+// eight waves, so each K byte fetched from L2 feeds 256 queries.  Row maxima complete inside a
+// wave; a 64-row tile's votes are the sum of its two waves' counts, which are stored as two byte
+// planes and added by the selection kernel.
 //
 // Chunks whose keys are causal for every query of the workgroup (all but the last one or two)
 // take a fully unrolled path that software-pipelines the per-block epilogue (row max in pass 1,
@@ -112,21 +114,24 @@ __device__ __forceinline__ float min_arg_for(float thr, float c) {
 // variant (tile 32): packed keep bits per key, plus weighted votes for PQ 2 (margin,
 // sum of fl(s - fl(m - tau))) and PQ 3 (expmass, sum of exp(fl(s - m))) over the keeping rows
 // (shared_selection_triton_perquery.py:181-217).
-template <int D, int RB, bool RC, int PQ>
-__global__ __launch_bounds__(256, 1) void score_kernel(ScoreArgs a) {
+template <int D, int T, bool RC, int PQ>
+__global__ __launch_bounds__(512, 1) void score_kernel(ScoreArgs a) {
 #pragma clang fp contract(off)
+  constexpr int RB = 1;                          // 32-row blocks per wave
+  constexpr int NTH = 512;                       // eight waves
+  constexpr int HALVES = T / 32;                 // waves (vote planes) per tile
+  constexpr int TPW = 8 / HALVES;                // tiles per workgroup
   constexpr int S = D / 16;                      // k steps of 16
-  constexpr int T = RB * 32;                     // tile rows
   constexpr int CHUNK_UNITS = 4 * S * 2 * 64;    // u32x4 units per 128-key chunk
-  constexpr int PF = CHUNK_UNITS / 256;          // units per thread per chunk
+  constexpr int PF = CHUNK_UNITS / NTH;          // units per thread per chunk
   constexpr int PER = 16 * RB / S;               // epilogue elements finished per k step
   static_assert(PER * S == 16 * RB, "epilogue split");
-  static_assert(PQ == 0 || RB == 1, "per-query bits pack one 32-row tile");
+  static_assert(PQ == 0 || T == 32, "per-query bits pack one 32-row tile");
   extern __shared__ u32x4 lds[];                 // 2 x CHUNK_UNITS
 
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int ngroups = (a.nt + 3) >> 2;
+  const int ngroups = (a.nt + TPW - 1) / TPW;
   int h, g;
   {
     const int bid = blockIdx.x;
@@ -141,17 +146,19 @@ __global__ __launch_bounds__(256, 1) void score_kernel(ScoreArgs a) {
     }
   }
   const int kvh = h / (a.H / a.Hkv);
-  const int t = g * 4 + wave;
+  const int t = g * TPW + wave / HALVES;
+  const int hv = wave % HALVES;                    // which 32 rows of the tile
   const bool active = t < a.nt;
-  const int t_last = min(g * 4 + 3, a.nt - 1);
+  const int t_last = min(g * TPW + TPW - 1, a.nt - 1);
   const int hi_max = a.q_pos_base + (t_last + 1) * T;
-  const int hi_t = a.q_pos_base + (t + 1) * T;     // exact_2.py:85
-  const int qpos0 = a.q_pos_base + t * T;          // position of the tile's first query
+  const int row0 = t * T + 32 * hv;                // first row of this wave
+  const int qpos0 = a.q_pos_base + row0;           // its position
+  const int hi_w = qpos0 + 32;                     // keys past the wave's last query are masked
   const int nchunks = (hi_max + 127) >> 7;
   // chunks entirely below N whose keys are causal for every query of the workgroup
-  const int nfull = min(min(nchunks, (a.q_pos_base + g * 4 * T + 1) >> 7), a.N >> 7);
+  const int nfull = min(min(nchunks, (a.q_pos_base + g * TPW * T + 1) >> 7), a.N >> 7);
   const float tau = a.tau[h];
-  uint8_t* vrow = a.votes + ((int64_t)h * a.nt + t) * a.votes_stride;
+  uint8_t* vrow = a.votes + (((int64_t)h * a.nt + t) * HALVES + hv) * a.votes_stride;
   uint32_t* brow = a.bits + ((int64_t)h * a.nt + t) * a.votes_stride;
   uint32_t* wrow = (uint32_t*)a.wvotes + ((int64_t)h * a.nt + t) * a.votes_stride;
   // one store per key and lane half: lanes 0-31 the bits, lanes 32-63 the weighted vote
@@ -170,7 +177,7 @@ __global__ __launch_bounds__(256, 1) void score_kernel(ScoreArgs a) {
     for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
       for (int s = 0; s < S; ++s) {
-        const int64_t u = (((int64_t)h * (a.q_rows_pad >> 5) + t * RB + rb) * S + s) * 128 + lane;
+        const int64_t u = (((int64_t)h * (a.q_rows_pad >> 5) + row0 / 32 + rb) * S + s) * 128 + lane;
         qhi[rb][s] = a.qfrag[u];
         qlo[rb][s] = a.qfrag[u + 64];
       }
@@ -293,9 +300,9 @@ __global__ __launch_bounds__(256, 1) void score_kernel(ScoreArgs a) {
     constexpr std::integral_constant<bool, true> kPrev{};
     constexpr std::integral_constant<bool, false> kNoPrev{};
 #pragma unroll
-    for (int e = 0; e < PF; ++e) pf[e] = kbase[e * 256 + threadIdx.x];
+    for (int e = 0; e < PF; ++e) pf[e] = kbase[e * NTH + threadIdx.x];
 #pragma unroll
-    for (int e = 0; e < PF; ++e) lds[e * 256 + threadIdx.x] = pf[e];
+    for (int e = 0; e < PF; ++e) lds[e * NTH + threadIdx.x] = pf[e];
     __syncthreads();
     floatx16 accA[RB], accB[RB];
     bool pendingB = false;   // accB holds an unmasked block whose epilogue is still due
@@ -305,7 +312,7 @@ __global__ __launch_bounds__(256, 1) void score_kernel(ScoreArgs a) {
       if (more) {
         const u32x4* src = kbase + (int64_t)(c + 1) * CHUNK_UNITS;
 #pragma unroll
-        for (int e = 0; e < PF; ++e) pf[e] = src[e * 256 + threadIdx.x];
+        for (int e = 0; e < PF; ++e) pf[e] = src[e * NTH + threadIdx.x];
       }
       const u32x4* buf = lds + (c & 1) * CHUNK_UNITS;
       if (active) {
@@ -322,7 +329,7 @@ __global__ __launch_bounds__(256, 1) void score_kernel(ScoreArgs a) {
           pendingB = false;
           for (int sb = 0; sb < 4; ++sb) {
             const int key0 = c * 128 + sb * 32;
-            if (key0 >= hi_t) break;
+            if (key0 >= hi_w) break;
             floatx16 acc[RB];
 #pragma unroll
             for (int rb = 0; rb < RB; ++rb) acc[rb] = floatx16{};
@@ -370,7 +377,7 @@ __global__ __launch_bounds__(256, 1) void score_kernel(ScoreArgs a) {
       if (more) {
         u32x4* dst = lds + ((c + 1) & 1) * CHUNK_UNITS;
 #pragma unroll
-        for (int e = 0; e < PF; ++e) dst[e * 256 + threadIdx.x] = pf[e];
+        for (int e = 0; e < PF; ++e) dst[e * NTH + threadIdx.x] = pf[e];
       }
       __syncthreads();
     }
@@ -390,11 +397,11 @@ __global__ __launch_bounds__(256, 1) void score_kernel(ScoreArgs a) {
             v = fmaxf(v, __shfl_xor(v, 16, 64));
             const float m = v * a.sm_scale;   // fl(max * c) == max of fl(s * c) for c > 0
             const int row = rb * 32 + (i >> 2) * 8 + (lane >> 5) * 4 + (i & 3);
-            const bool ok = t * T + row < a.N;  // padded rows never vote (exact_2.py:121)
+            const bool ok = row0 + row < a.N;   // padded rows never vote (exact_2.py:121)
             x0[rb][i] = ok ? min_arg_for(m - tau, a.sm_scale) : INFINITY;
             if constexpr (PQ == 2) mx[rb][i] = m - tau;   // perquery.py:210
             if constexpr (PQ == 3) mx[rb][i] = m;         // perquery.py:215
-            if (a.row_max && (lane & 31) == 0 && ok) a.row_max[(int64_t)h * a.N + t * T + row] = m;
+            if (a.row_max && (lane & 31) == 0 && ok) a.row_max[(int64_t)h * a.N + row0 + row] = m;
           }
       }
     }
@@ -415,7 +422,7 @@ __global__ __launch_bounds__(256, 1) void score_kernel(ScoreArgs a) {
           v += __shfl_xor(v, 8, 64);
           v += __shfl_xor(v, 16, 64);
           const int row = rb * 32 + (i >> 2) * 8 + (lane >> 5) * 4 + (i & 3);
-          if ((lane & 31) == 0 && t * T + row < a.N) a.row_counts[(int64_t)h * a.N + t * T + row] = v;
+          if ((lane & 31) == 0 && row0 + row < a.N) a.row_counts[(int64_t)h * a.N + row0 + row] = v;
         }
     }
   }
@@ -446,23 +453,24 @@ hipError_t launch_rope_frag(int dtype, int D, const void* x, int64_t hs, int64_t
   return hipErrorInvalidValue;
 }
 
-template <int D, int RB, bool RC, int PQ>
+template <int D, int T, bool RC, int PQ>
 static hipError_t launch_score_t(const ScoreArgs& a, hipStream_t st) {
   constexpr int S = D / 16;
   const size_t lds_bytes = 2 * (size_t)(4 * S * 2 * 64) * 16;
-  hipError_t e = hipFuncSetAttribute((const void*)score_kernel<D, RB, RC, PQ>,
+  hipError_t e = hipFuncSetAttribute((const void*)score_kernel<D, T, RC, PQ>,
                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_bytes);
   if (e != hipSuccess) return e;
-  const int ngroups = (a.nt + 3) / 4;
-  hipLaunchKernelGGL((score_kernel<D, RB, RC, PQ>), dim3(a.H * ngroups), dim3(256), lds_bytes, st, a);
+  const int tpw = 256 / T;
+  const int ngroups = (a.nt + tpw - 1) / tpw;
+  hipLaunchKernelGGL((score_kernel<D, T, RC, PQ>), dim3(a.H * ngroups), dim3(512), lds_bytes, st, a);
   return hipGetLastError();
 }
 
 hipError_t launch_score(int D, int tile, const ScoreArgs& a, hipStream_t st) {
   const bool rc = a.row_counts != nullptr;
-#define STA_SC(D_, RB_) \
-  if (D == D_ && tile == RB_ * 32) return rc ? launch_score_t<D_, RB_, true, 0>(a, st) : launch_score_t<D_, RB_, false, 0>(a, st);
-  STA_SC(64, 1) STA_SC(64, 2) STA_SC(128, 1) STA_SC(128, 2)
+#define STA_SC(D_, T_) \
+  if (D == D_ && tile == T_) return rc ? launch_score_t<D_, T_, true, 0>(a, st) : launch_score_t<D_, T_, false, 0>(a, st);
+  STA_SC(64, 32) STA_SC(64, 64) STA_SC(128, 32) STA_SC(128, 64)
 #undef STA_SC
   return hipErrorInvalidValue;
 }
@@ -470,7 +478,7 @@ hipError_t launch_score(int D, int tile, const ScoreArgs& a, hipStream_t st) {
 hipError_t launch_score_pq(int D, int wmode, const ScoreArgs& a, hipStream_t st) {
   const bool rc = a.row_counts != nullptr;
 #define STA_SP(D_, PQ_) \
-  if (D == D_ && wmode + 1 == PQ_) return rc ? launch_score_t<D_, 1, true, PQ_>(a, st) : launch_score_t<D_, 1, false, PQ_>(a, st);
+  if (D == D_ && wmode + 1 == PQ_) return rc ? launch_score_t<D_, 32, true, PQ_>(a, st) : launch_score_t<D_, 32, false, PQ_>(a, st);
   STA_SP(64, 1) STA_SP(64, 2) STA_SP(64, 3) STA_SP(128, 1) STA_SP(128, 2) STA_SP(128, 3)
 #undef STA_SP
   return hipErrorInvalidValue;

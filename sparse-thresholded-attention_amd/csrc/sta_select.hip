@@ -94,9 +94,17 @@ __global__ __launch_bounds__(256) void select_kernel(SelectArgs a) {
   float* snp = (float*)(sidx + a.k_max);                                    // k_max
 
   for (int i = tid; i < 260; i += 256) { hist[i] = 0; fhist[i] = 0; }
-  // ---- stage the vote row (zero past the causal range) ----
-  const VT* vrow = (const VT*)a.votes + ((int64_t)h * a.nt + t) * a.votes_stride;
-  for (int j = tid; j < 256 * per; j += 256) vb[j] = (j < hi_keys) ? (uint8_t)vrow[j] : (uint8_t)0;
+  // ---- stage the vote row: the sum of the tile's partial-count planes, zero past each plane's
+  //      causal range ----
+  const VT* vrow = (const VT*)a.votes + ((int64_t)h * a.nt + t) * a.vote_planes * a.votes_stride;
+  for (int j = tid; j < 256 * per; j += 256) {
+    uint32_t sum = 0;
+    for (int pl = 0; pl < a.vote_planes; ++pl) {
+      const int64_t hp = a.votes_dense ? N : min((int64_t)N, tstart + 32 * (pl + 1));
+      if (j < hp) sum += (uint32_t)vrow[pl * a.votes_stride + j];
+    }
+    vb[j] = (uint8_t)sum;
+  }
   __syncthreads();
   if (a.votes_out) {
     int32_t* vo = a.votes_out + ((int64_t)h * a.nt + t) * N;
@@ -230,21 +238,26 @@ __global__ __launch_bounds__(256) void select_kernel(SelectArgs a) {
   }
 }
 
-// byte votes (keys < min(N, hi_t) valid) -> the reference's dense int32 (H, nt, N) layout
+// byte vote planes (plane p: keys < min(N, tile start + 32 (p+1)) valid) -> the reference's
+// dense int32 (H, nt, N) layout
 __global__ __launch_bounds__(256) void expand_votes_kernel(const uint8_t* __restrict__ v8, int64_t stride,
-                                                           int nt, int N, int T, int q_pos_base,
+                                                           int planes, int nt, int N, int T, int q_pos_base,
                                                            int32_t* __restrict__ out) {
   const int ht = blockIdx.y;
   const int t = ht % nt;
-  const int64_t hi = min((int64_t)N, (int64_t)q_pos_base + (int64_t)(t + 1) * T);
-  for (int j = blockIdx.x * 256 + threadIdx.x; j < N; j += gridDim.x * 256)
-    out[(int64_t)ht * N + j] = j < hi ? (int32_t)v8[(int64_t)ht * stride + j] : 0;
+  const int64_t tstart = (int64_t)q_pos_base + (int64_t)t * T;
+  for (int j = blockIdx.x * 256 + threadIdx.x; j < N; j += gridDim.x * 256) {
+    int32_t sum = 0;
+    for (int pl = 0; pl < planes; ++pl)
+      if (j < min((int64_t)N, tstart + 32 * (pl + 1))) sum += v8[((int64_t)ht * planes + pl) * stride + j];
+    out[(int64_t)ht * N + j] = sum;
+  }
 }
 
-hipError_t launch_expand_votes(const uint8_t* v8, int64_t stride, int H, int nt, int N, int T,
+hipError_t launch_expand_votes(const uint8_t* v8, int64_t stride, int planes, int H, int nt, int N, int T,
                                int q_pos_base, int32_t* out, hipStream_t st) {
   const int bx = (N + 255) / 256 < 64 ? (N + 255) / 256 : 64;
-  hipLaunchKernelGGL(expand_votes_kernel, dim3(bx, H * nt), dim3(256), 0, st, v8, stride, nt, N, T,
+  hipLaunchKernelGGL(expand_votes_kernel, dim3(bx, H * nt), dim3(256), 0, st, v8, stride, planes, nt, N, T,
                      q_pos_base, out);
   return hipGetLastError();
 }
