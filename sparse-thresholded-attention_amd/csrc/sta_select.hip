@@ -97,13 +97,31 @@ __global__ __launch_bounds__(256) void select_kernel(SelectArgs a) {
   // ---- stage the vote row: the sum of the tile's partial-count planes, zero past each plane's
   //      causal range ----
   const VT* vrow = (const VT*)a.votes + ((int64_t)h * a.nt + t) * a.vote_planes * a.votes_stride;
-  for (int j = tid; j < 256 * per; j += 256) {
-    uint32_t sum = 0;
-    for (int pl = 0; pl < a.vote_planes; ++pl) {
-      const int64_t hp = a.votes_dense ? N : min((int64_t)N, tstart + 32 * (pl + 1));
-      if (j < hp) sum += (uint32_t)vrow[pl * a.votes_stride + j];
+  if constexpr (sizeof(VT) == 1) {
+    // four keys per word; byte votes are <= 64 each, so the planes add without carries
+    for (int wi = tid; wi < 64 * per; wi += 256) {
+      const int j = wi * 4;
+      uint32_t sum = 0;
+      for (int pl = 0; pl < a.vote_planes; ++pl) {
+        const int64_t hp = a.votes_dense ? N : min((int64_t)N, tstart + 32 * (pl + 1));
+        if (j < hp) {   // j + 3 < roundup(N, 4) <= votes_stride: the word is inside the row
+          uint32_t w = ((const uint32_t*)(vrow + pl * a.votes_stride))[wi];
+          const int64_t valid = hp - j;
+          if (valid < 4) w &= (1u << (8 * valid)) - 1u;
+          sum += w;
+        }
+      }
+      ((uint32_t*)vb)[wi] = sum;
     }
-    vb[j] = (uint8_t)sum;
+  } else {
+    for (int j = tid; j < 256 * per; j += 256) {
+      uint32_t sum = 0;
+      for (int pl = 0; pl < a.vote_planes; ++pl) {
+        const int64_t hp = a.votes_dense ? N : min((int64_t)N, tstart + 32 * (pl + 1));
+        if (j < hp) sum += (uint32_t)vrow[pl * a.votes_stride + j];
+      }
+      vb[j] = (uint8_t)sum;
+    }
   }
   __syncthreads();
   if (a.votes_out) {
