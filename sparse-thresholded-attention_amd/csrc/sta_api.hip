@@ -67,7 +67,7 @@ Layout layout_of(const sta_shared_args* a) {
   L.kfrag_off = off;
   off = align256(off + (size_t)a->Hkv * L.k_rows_pad * a->D * 4);
   L.votes_off = off;
-  off = align256(off + (size_t)a->H * L.nt * (a->tile / 32) * L.votes_stride);   // one plane per 32 rows
+  off = align256(off + (size_t)a->H * L.nt * L.votes_stride);
   L.total = off;
   return L;
 }
@@ -249,7 +249,6 @@ int sta_shared_attention(const sta_shared_args* args, void* stream) {
   SelectArgs s = select_args_of(args, L);
   s.votes = (const void*)((char*)args->workspace + L.votes_off);
   s.votes_stride = L.votes_stride;
-  s.vote_planes = args->tile / 32;
   hipError_t e = launch_select(s, 1, st);
   if (e != hipSuccess) return hip_fail(e, "select kernel");
   if ((rc = mark(args, 3, st)) != STA_OK) return rc;
@@ -268,8 +267,7 @@ int sta_select_vote(const sta_shared_args* args, void* stream) {
   hipStream_t st = (hipStream_t)stream;
   if ((rc = run_kernel_a(args, L, st)) != STA_OK) return rc;
   hipError_t e = launch_expand_votes((const uint8_t*)((char*)args->workspace + L.votes_off), L.votes_stride,
-                                     args->tile / 32, args->H, L.nt, args->N, args->tile, args->q_pos_base,
-                                     args->votes, st);
+                                     args->H, L.nt, args->N, args->tile, args->q_pos_base, args->votes, st);
   if (e != hipSuccess) return hip_fail(e, "vote expansion");
   return STA_OK;
 }
@@ -285,7 +283,6 @@ int sta_build_sets(const sta_shared_args* args, const int32_t* votes, int32_t nu
   SelectArgs s = select_args_of(args, L);
   s.votes = votes;
   s.votes_stride = args->N;
-  s.vote_planes = 1;
   s.votes_dense = 1;
   s.votes_out = nullptr;
   hipError_t e = launch_select(s, 4, (hipStream_t)stream);

@@ -23,10 +23,9 @@ struct ScoreArgs {
 };
 
 struct SelectArgs {
-  const void* votes;      // uint8 or int32 (H, nt, vote_planes, votes_stride), values in [0, 255]
+  const void* votes;      // uint8 or int32 (H, nt, votes_stride), values in [0, 255]
   int64_t votes_stride;
-  int vote_planes;        // partial counts per tile (one per 32 query rows), summed here
-  int votes_dense;        // 1: all N votes are valid; 0: plane p holds keys < min(N, tile start + 32 (p+1))
+  int votes_dense;        // 1: all N votes are valid; 0: keys < min(N, tile end) are valid
   int H, nt, N, T, k_max, q_pos_base, n_global, n_local;
   float pos_scale;
   int nsteps;
@@ -120,8 +119,8 @@ hipError_t launch_expand_pq(const uint32_t* bits, const float* wv, int64_t strid
                             float* wv_out, hipStream_t st);
 size_t select_lds_bytes(int N, int k_max);
 hipError_t launch_select(const SelectArgs& a, int vote_bytes, hipStream_t st);
-hipError_t launch_expand_votes(const uint8_t* v8, int64_t stride, int planes, int H, int nt, int N, int T,
-                               int q_pos_base, int32_t* out, hipStream_t st);
+hipError_t launch_expand_votes(const uint8_t* v8, int64_t stride, int H, int nt, int N, int T, int q_pos_base,
+                               int32_t* out, hipStream_t st);
 size_t gather_lds_bytes(int dtype, int D, int k_max);
 hipError_t launch_abs_rope(int dtype, int D, const void* x, int64_t hs, int64_t ts, int heads, int N, int Npad,
                            const float* inv_freq, uint16_t* out, hipStream_t st);

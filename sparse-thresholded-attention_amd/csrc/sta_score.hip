@@ -82,12 +82,12 @@ __global__ __launch_bounds__(256) void rope_frag_kernel(const void* __restrict__
 // ------------------------------------------------------------------------------------------
 // Score kernel: pass 1 (exact row max) and pass 2 (keep + votes), exact_2.py:87-140.
 //
-// One workgroup = one head and 256 consecutive query rows in eight waves of 32 rows (two waves
-// per SIMD, so one wave's epilogue and LDS reads overlap the other's MFMAs).  A wave holds its
-// rows' Q fragments in registers.  Key chunks of 128 rows are staged once in LDS and read by all
-// eight waves, so each K byte fetched from L2 feeds 256 queries.  Row maxima complete inside a
-// wave; a 64-row tile's votes are the sum of its two waves' counts, which are stored as two byte
-// planes and added by the selection kernel.
+// One workgroup = one head and 256 consecutive query rows in four waves of 64 rows, one wave per
+// SIMD.  A wave holds its rows' Q fragments in registers, so each K fragment it reads from LDS
+// feeds two 32x32 products per k step.  Key chunks of 128 rows are copied from global memory
+// straight into LDS (global_load_lds: no register staging), double-buffered, and read by all four
+// waves, so each K byte fetched from L2 feeds 256 queries.  Row maxima complete inside a wave, and
+// so do a tile's votes (a wave holds one 64-row tile or two 32-row tiles): one byte plane per tile.
 //
 // Chunks whose keys are causal for every query of the workgroup (all but the last one or two)
 // take a fully unrolled path that software-pipelines the per-block epilogue (row max in pass 1,
@@ -110,28 +110,38 @@ __device__ __forceinline__ float min_arg_for(float thr, float c) {
   return x;
 }
 
+#define STA_GLOBAL(p) ((const __attribute__((address_space(1))) void*)(p))
+#define STA_LDS(p) ((__attribute__((address_space(3))) void*)(p))
+
 // PQ selects the pass-2 epilogue: 0 = byte votes (shared selection); 1..3 = the per-query
 // variant (tile 32): packed keep bits per key, plus weighted votes for PQ 2 (margin,
 // sum of fl(s - fl(m - tau))) and PQ 3 (expmass, sum of exp(fl(s - m))) over the keeping rows
 // (shared_selection_triton_perquery.py:181-217).
-template <int D, int T, bool RC, int PQ>
-__global__ __launch_bounds__(512, 1) void score_kernel(ScoreArgs a) {
+template <int D, int T, bool RC, int PQ, int RB>
+__global__ __launch_bounds__(256, 1) void score_kernel(ScoreArgs a) {
 #pragma clang fp contract(off)
-  constexpr int RB = 1;                          // 32-row blocks per wave
-  constexpr int NTH = 512;                       // eight waves
-  constexpr int HALVES = T / 32;                 // waves (vote planes) per tile
-  constexpr int TPW = 8 / HALVES;                // tiles per workgroup
+  // RB 32-row blocks per wave (RB = 2: 64 query rows, RB = 4: 128); four waves, one per SIMD
+  constexpr int NW = 4;
+  constexpr int WG_ROWS = NW * 32 * RB;          // query rows per workgroup
+  constexpr int NTW = 32 * RB / T;               // tiles per wave
   constexpr int S = D / 16;                      // k steps of 16
-  constexpr int CHUNK_UNITS = 4 * S * 2 * 64;    // u32x4 units per 128-key chunk
-  constexpr int PF = CHUNK_UNITS / NTH;          // units per thread per chunk
+  constexpr int CK = 64;                         // keys per LDS chunk
+  constexpr int NBUF = 4;                        // chunk buffers: copies run NBUF - 1 chunks ahead
+  constexpr int SBC = CK / 32;                   // 32-key blocks per chunk
+  constexpr int CHUNK_UNITS = SBC * S * 2 * 64;  // u32x4 units per chunk
+  constexpr int LOADS = CHUNK_UNITS / (64 * NW); // 1 KB copies per wave per chunk
+  static_assert(LOADS * (NBUF - 2) < 64, "vmcnt range");
   constexpr int PER = 16 * RB / S;               // epilogue elements finished per k step
   static_assert(PER * S == 16 * RB, "epilogue split");
+  static_assert(RB == 2 || RB == 4, "row blocks per wave");
+  static_assert(T == 32 || T == 64, "tile");
   static_assert(PQ == 0 || T == 32, "per-query bits pack one 32-row tile");
-  extern __shared__ u32x4 lds[];                 // 2 x CHUNK_UNITS
+  __shared__ u32x4 lds[NBUF][CHUNK_UNITS];
 
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int ngroups = (a.nt + TPW - 1) / TPW;
+  const int rows_total = a.nt * T;               // == q_rows_pad
+  const int ngroups = (rows_total + WG_ROWS - 1) / WG_ROWS;
   int h, g;
   {
     const int bid = blockIdx.x;
@@ -146,52 +156,67 @@ __global__ __launch_bounds__(512, 1) void score_kernel(ScoreArgs a) {
     }
   }
   const int kvh = h / (a.H / a.Hkv);
-  const int t = g * TPW + wave / HALVES;
-  const int hv = wave % HALVES;                    // which 32 rows of the tile
-  const bool active = t < a.nt;
-  const int t_last = min(g * TPW + TPW - 1, a.nt - 1);
-  const int hi_max = a.q_pos_base + (t_last + 1) * T;
-  const int row0 = t * T + 32 * hv;                // first row of this wave
-  const int qpos0 = a.q_pos_base + row0;           // its position
-  const int hi_w = qpos0 + 32;                     // keys past the wave's last query are masked
-  const int nchunks = (hi_max + 127) >> 7;
+  const int wrow0 = g * WG_ROWS + wave * 32 * RB;  // first row of this wave
+  const bool active = wrow0 < rows_total;
+  const int hi_max = a.q_pos_base + min(g * WG_ROWS + WG_ROWS, rows_total);
+  const int qpos0 = a.q_pos_base + wrow0;          // position of the wave's first row
+  const int hi_w = qpos0 + 32 * RB;                // keys past the wave's last query are masked
+  const int nchunks = (hi_max + CK - 1) / CK;
   // chunks entirely below N whose keys are causal for every query of the workgroup
-  const int nfull = min(min(nchunks, (a.q_pos_base + g * TPW * T + 1) >> 7), a.N >> 7);
+  const int nfull = min(min(nchunks, (a.q_pos_base + g * WG_ROWS + 1) / CK), a.N / CK);
   const float tau = a.tau[h];
-  uint8_t* vrow = a.votes + (((int64_t)h * a.nt + t) * HALVES + hv) * a.votes_stride;
-  uint32_t* brow = a.bits + ((int64_t)h * a.nt + t) * a.votes_stride;
-  uint32_t* wrow = (uint32_t*)a.wvotes + ((int64_t)h * a.nt + t) * a.votes_stride;
-  // one store per key and lane half: lanes 0-31 the bits, lanes 32-63 the weighted vote
-  auto store_pq = [&](int key, uint32_t bm, float w) {
-    bm <<= 4 * (lane >> 5);                 // rows of the upper lane half sit 4 bits higher
-    bm |= __shfl_xor(bm, 32, 64);
-    if constexpr (PQ >= 2) w += __shfl_xor(w, 32, 64);
-    if (lane < 32) brow[key] = bm;
-    else if constexpr (PQ >= 2) wrow[key] = __float_as_uint(w);
-  };
+  // the wave's tiles j = 0 .. NTW-1 start at row wrow0 + j T; one store instruction writes two
+  // tiles' rows of a key (lanes 0-31 tile j, lanes 32-63 tile j + 1)
+  const int64_t trow0 = (int64_t)h * a.nt + wrow0 / T;
+  uint8_t* vrow = a.votes + trow0 * a.votes_stride;
+  uint32_t* brow = a.bits + trow0 * a.votes_stride;
+  uint32_t* wrow = (uint32_t*)a.wvotes + trow0 * a.votes_stride;
+  auto tile_ok = [&](int j) { return wrow0 + j * T < rows_total; };
 
-  // ---- Q fragments of this wave's tile ----
+  // ---- Q fragments of this wave's rows (kept in AGPRs: they are only MFMA operands) ----
   u32x4 qhi[RB][S], qlo[RB][S];
-  if (active) {
 #pragma unroll
-    for (int rb = 0; rb < RB; ++rb)
+  for (int rb = 0; rb < RB; ++rb) {
+    const bool ok = wrow0 + 32 * rb < rows_total;
 #pragma unroll
-      for (int s = 0; s < S; ++s) {
-        const int64_t u = (((int64_t)h * (a.q_rows_pad >> 5) + row0 / 32 + rb) * S + s) * 128 + lane;
+    for (int s = 0; s < S; ++s) {
+      if (ok) {
+        const int64_t u = (((int64_t)h * (a.q_rows_pad >> 5) + wrow0 / 32 + rb) * S + s) * 128 + lane;
         qhi[rb][s] = a.qfrag[u];
         qlo[rb][s] = a.qfrag[u + 64];
+      } else {
+        qhi[rb][s] = u32x4{0, 0, 0, 0};
+        qlo[rb][s] = u32x4{0, 0, 0, 0};
       }
-  } else {
-#pragma unroll
-    for (int rb = 0; rb < RB; ++rb)
-#pragma unroll
-      for (int s = 0; s < S; ++s) { qhi[rb][s] = u32x4{0, 0, 0, 0}; qlo[rb][s] = u32x4{0, 0, 0, 0}; }
+      asm volatile("" : "+a"(qhi[rb][s]));
+      asm volatile("" : "+a"(qlo[rb][s]));
+    }
   }
   const u32x4* kbase = a.kfrag + (int64_t)kvh * (a.k_rows_pad >> 5) * S * 128;
+  // copy key chunk c into dst: 1 KB per instruction, lane l's 16 bytes land at dst + 16 l
+  auto issue = [&](int c, u32x4* dst) {
+    const u32x4* src = kbase + (int64_t)c * CHUNK_UNITS + lane;
+#pragma unroll
+    for (int e = 0; e < LOADS; ++e) {
+      const int u = (e * NW + wave) * 64;
+      __builtin_amdgcn_global_load_lds(STA_GLOBAL(src + u), STA_LDS(dst + u), 16, 0, 0);
+    }
+  };
+  // wait until at most n chunks' copies of this wave are in flight.  Vector memory operations
+  // complete in issue order, so this leaves only the n most recently issued chunks pending (vote
+  // stores issued in between only make the wait stricter).
+  auto wait_copies = [&](int n) {
+    constexpr int E = (7 << 4) | (15 << 8);   // expcnt / lgkmcnt: no wait
+    constexpr int L1 = LOADS, L2 = 2 * LOADS;
+    if (n <= 0) __builtin_amdgcn_s_waitcnt(E);
+    else if (n == 1) __builtin_amdgcn_s_waitcnt(E | (L1 & 15) | ((L1 >> 4) << 14));
+    else __builtin_amdgcn_s_waitcnt(E | (L2 & 15) | ((L2 >> 4) << 14));
+  };
+  static_assert(NBUF == 4, "wait_copies covers up to two newer chunks");
 
   // per-query epilogue of one score: bit `row` of the key's mask, and its weighted vote
-  // (i indexes the lane's 16 accumulator rows: row = (i/4)*8 + 4*(lane/32) + i%4; the lane
-  // half's 4-row offset is applied when the mask is stored)
+  // (i indexes the lane's 16 accumulator rows of a 32-row block: row = (i/4)*8 + 4*(lane/32) +
+  // i%4; the lane half's 4-row offset is applied when the mask is stored)
   auto pq_acc = [&](int keep, float v, float ref, int i, uint32_t& bm, float& w) {
 #pragma clang fp contract(off)
     bm |= (uint32_t)keep << ((i >> 2) * 8 + (i & 3));
@@ -205,19 +230,60 @@ __global__ __launch_bounds__(512, 1) void score_kernel(ScoreArgs a) {
       w += keep ? e : 0.0f;
     }
   };
-  float mx[RB][16];   // pass 1: running max of the raw dot per row slot; pass 2 (PQ 2 / 3):
-                      // fl(m - tau) / m of the row, the reference point of the weighted vote
-  float x0[RB][16];   // pass 2: keep threshold on the raw dot per row slot
+  // the key's pass-2 results of this wave's rows -> votes (exact_2.py:123) or bits + weighted
+  // votes; lanes 0-31 and 32-63 hold complementary rows of the same key
+  auto store_key = [&](int key, bool check, const int* cnt, const uint32_t* bm, const float* w) {
+    const bool key_ok = !check || key < a.N;
+    if constexpr (PQ == 0) {
+      int tot[NTW];
+#pragma unroll
+      for (int j = 0; j < NTW; ++j) {
+        int c = 0;
+#pragma unroll
+        for (int rb = j * T / 32; rb < (j + 1) * T / 32; ++rb) c += cnt[rb];
+        tot[j] = c + __shfl_xor(c, 32, 64);
+      }
+      if constexpr (NTW == 1) {
+        if (lane < 32 && active && key_ok) vrow[key] = (uint8_t)tot[0];
+      } else {
+#pragma unroll
+        for (int j2 = 0; j2 < NTW; j2 += 2) {
+          const int j = j2 + (lane >> 5);
+          if (tile_ok(j) && key_ok) vrow[j * a.votes_stride + key] = (uint8_t)(lane < 32 ? tot[j2] : tot[j2 + 1]);
+        }
+      }
+    } else {   // tile 32: one tile per row block
+      uint32_t b[RB];
+      float ww[RB];
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb) {
+        b[rb] = bm[rb] << (4 * (lane >> 5));   // rows of the upper lane half sit 4 bits higher
+        b[rb] |= __shfl_xor(b[rb], 32, 64);
+        ww[rb] = w[rb];
+        if constexpr (PQ >= 2) ww[rb] += __shfl_xor(w[rb], 32, 64);
+      }
+#pragma unroll
+      for (int j2 = 0; j2 < RB; j2 += 2) {
+        const int j = j2 + (lane >> 5);
+        if (tile_ok(j) && key_ok) {
+          brow[j * a.votes_stride + key] = lane < 32 ? b[j2] : b[j2 + 1];
+          if constexpr (PQ >= 2) wrow[j * a.votes_stride + key] = __float_as_uint(lane < 32 ? ww[j2] : ww[j2 + 1]);
+        }
+      }
+    }
+  };
+
+  float mx[RB][16];   // pass 1: running max of the raw dot per row slot; pass 2: the keep
+                      // threshold x0 on the raw dot
+  float ref[RB][16];  // pass 2, PQ 2 / 3: fl(m - tau) / m of the row, the weighted vote's origin
   int rc[RB][16];
 #pragma unroll
   for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
-    for (int i = 0; i < 16; ++i) { mx[rb][i] = -INFINITY; x0[rb][i] = INFINITY; rc[rb][i] = 0; }
+    for (int i = 0; i < 16; ++i) { mx[rb][i] = -INFINITY; ref[rb][i] = 0.0f; rc[rb][i] = 0; }
 
-  // 32 keys x this wave's rows: hi.hi + hi.lo + lo.hi, small terms first
-  auto mfma_step = [&](const u32x4* buf, int sb, int s, floatx16* acc) {
-    const u32x4 bh = buf[(sb * S + s) * 128 + lane];
-    const u32x4 bl = buf[(sb * S + s) * 128 + 64 + lane];
+  // 32 keys x this wave's rows, one k step: hi.hi + hi.lo + lo.hi, small terms first
+  auto mfma3 = [&](u32x4 bh, u32x4 bl, int s, floatx16* acc) {
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) acc[rb] = mfma32(qlo[rb][s], bh, acc[rb]);
 #pragma unroll
@@ -225,121 +291,129 @@ __global__ __launch_bounds__(512, 1) void score_kernel(ScoreArgs a) {
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) acc[rb] = mfma32(qhi[rb][s], bh, acc[rb]);
   };
+  auto ldb = [&](const u32x4* buf, int sb, int s, int hl) { return buf[(sb * S + s) * 128 + 64 * hl + lane]; };
+  // Instruction schedule of one 32-key block (S k steps): the K fragments of step s + 1 are read
+  // while step s's MFMAs run, and the VALU work available (the previous block's epilogue) is
+  // interleaved between the MFMAs.  One wave per SIMD has no other wave to hide LDS latency.  The
+  // reads for step s + 2 follow step s + 1's first MFMA, so the LDS wait in front of that MFMA
+  // covers only reads issued a whole step earlier.
+  auto block_schedule = [&](auto valuc) {
+    constexpr int valu_per_mfma = decltype(valuc)::value;
+    __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);        // reads of steps 0 and 1
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+#pragma unroll
+      for (int m = 0; m < 3 * RB; ++m) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);    // MFMA
+        if (m == 0 && s >= 1 && s + 1 < S) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // step s + 1
+        if constexpr (valu_per_mfma > 0) __builtin_amdgcn_sched_group_barrier(0x002, valu_per_mfma, 0);
+      }
+    }
+  };
+  // all k steps of block sb, with the next step's K fragments read ahead
+  auto mfma_block = [&](const u32x4* buf, int sb, floatx16* acc) {
+    u32x4 bh = ldb(buf, sb, 0, 0), bl = ldb(buf, sb, 0, 1);
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+      u32x4 nh = bh, nl = bl;
+      if (s + 1 < S) { nh = ldb(buf, sb, s + 1, 0); nl = ldb(buf, sb, s + 1, 1); }
+      mfma3(bh, bl, s, acc);
+      bh = nh;
+      bl = nl;
+    }
+    block_schedule(std::integral_constant<int, 0>{});
+  };
+  // epilogue of one (unmasked) score
+  auto epi = [&](auto passc, float v, int rb, int i, int* cnt, uint32_t* bm, float* w) {
+    constexpr int pass = decltype(passc)::value;
+    if constexpr (pass == 0) {
+      mx[rb][i] = __builtin_amdgcn_fmed3f(v, mx[rb][i], INFINITY);   // max; scores are finite
+    } else {
+      const int keep = v >= mx[rb][i];
+      if constexpr (PQ == 0) cnt[rb] += keep;
+      else pq_acc(keep, v, ref[rb][i], i, bm[rb], w[rb]);
+      if constexpr (RC) rc[rb][i] += keep;
+    }
+  };
   // MFMAs of block sb into accN; when HAS_PREV, the epilogue of the previous (unmasked) block
   // accO at keys keyO.. is finished in slices between the k steps
   auto fused_block = [&](auto passc, auto prevc, const u32x4* buf, int sb, floatx16* accN,
                          const floatx16* accO, int keyO) {
     constexpr int pass = decltype(passc)::value;
     constexpr bool HAS_PREV = decltype(prevc)::value;
-    int cnt = 0;
-    uint32_t bm = 0;
-    float w = 0.0f;
+    int cnt[RB] = {};
+    uint32_t bm[RB] = {};
+    float w[RB] = {};
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) accN[rb] = floatx16{};
+    u32x4 bh = ldb(buf, sb, 0, 0), bl = ldb(buf, sb, 0, 1);
 #pragma unroll
     for (int s = 0; s < S; ++s) {
-      mfma_step(buf, sb, s, accN);
+      u32x4 nh = bh, nl = bl;
+      if (s + 1 < S) { nh = ldb(buf, sb, s + 1, 0); nl = ldb(buf, sb, s + 1, 1); }
+      mfma3(bh, bl, s, accN);
+      bh = nh;
+      bl = nl;
       if constexpr (HAS_PREV) {
 #pragma unroll
         for (int e = 0; e < PER; ++e) {
           const int idx = s * PER + e, rb = idx / 16, i = idx % 16;
-          const float v = accO[rb][i];
-          if constexpr (pass == 0) {
-            mx[rb][i] = v > mx[rb][i] ? v : mx[rb][i];
-          } else {
-            const int keep = v >= x0[rb][i];
-            if constexpr (PQ == 0) cnt += keep;
-            else pq_acc(keep, v, mx[rb][i], i, bm, w);
-            if constexpr (RC) rc[rb][i] += keep;
-          }
+          epi(passc, accO[rb][i], rb, i, cnt, bm, w);
         }
       }
     }
-    if constexpr (HAS_PREV && pass == 1) {
-      if constexpr (PQ == 0) {
-        cnt += __shfl_xor(cnt, 32, 64);   // exact_2.py:123; both lane halves now hold the total
-        vrow[keyO + (lane & 31)] = (uint8_t)cnt;
-      } else {
-        store_pq(keyO + (lane & 31), bm, w);
-      }
-    }
+    if constexpr (HAS_PREV && pass == 1) store_key(keyO + (lane & 31), false, cnt, bm, w);
+    block_schedule(std::integral_constant<int, HAS_PREV ? 2 : 0>{});
   };
   // the last block's epilogue when nothing follows it
   auto flush = [&](auto passc, const floatx16* acc, int key0) {
     constexpr int pass = decltype(passc)::value;
-    int cnt = 0;
-    uint32_t bm = 0;
-    float w = 0.0f;
+    int cnt[RB] = {};
+    uint32_t bm[RB] = {};
+    float w[RB] = {};
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const float v = acc[rb][i];
-        if constexpr (pass == 0) {
-          mx[rb][i] = v > mx[rb][i] ? v : mx[rb][i];
-        } else {
-          const int keep = v >= x0[rb][i];
-          if constexpr (PQ == 0) cnt += keep;
-          else pq_acc(keep, v, mx[rb][i], i, bm, w);
-          if constexpr (RC) rc[rb][i] += keep;
-        }
-      }
-    if constexpr (pass == 1) {
-      if constexpr (PQ == 0) {
-        cnt += __shfl_xor(cnt, 32, 64);
-        vrow[key0 + (lane & 31)] = (uint8_t)cnt;
-      } else {
-        store_pq(key0 + (lane & 31), bm, w);
-      }
-    }
+      for (int i = 0; i < 16; ++i) epi(passc, acc[rb][i], rb, i, cnt, bm, w);
+    if constexpr (pass == 1) store_key(key0 + (lane & 31), false, cnt, bm, w);
   };
 
-  u32x4 pf[PF];
   auto run_pass = [&](auto passc) {
     constexpr int pass = decltype(passc)::value;
     constexpr std::integral_constant<bool, true> kPrev{};
     constexpr std::integral_constant<bool, false> kNoPrev{};
-#pragma unroll
-    for (int e = 0; e < PF; ++e) pf[e] = kbase[e * NTH + threadIdx.x];
-#pragma unroll
-    for (int e = 0; e < PF; ++e) lds[e * NTH + threadIdx.x] = pf[e];
+    for (int c = 0; c < NBUF - 1 && c < nchunks; ++c) issue(c, lds[c]);
+    wait_copies(min(nchunks, NBUF - 1) - 1);
     __syncthreads();
     floatx16 accA[RB], accB[RB];
     bool pendingB = false;   // accB holds an unmasked block whose epilogue is still due
     int keyB = 0;
     for (int c = 0; c < nchunks; ++c) {
-      const bool more = c + 1 < nchunks;
-      if (more) {
-        const u32x4* src = kbase + (int64_t)(c + 1) * CHUNK_UNITS;
-#pragma unroll
-        for (int e = 0; e < PF; ++e) pf[e] = src[e * NTH + threadIdx.x];
-      }
-      const u32x4* buf = lds + (c & 1) * CHUNK_UNITS;
+      // the buffer chunk c + NBUF - 1 lands in was last read in chunk c - 1, before the barrier
+      if (c + NBUF - 1 < nchunks) issue(c + NBUF - 1, lds[(c + NBUF - 1) % NBUF]);
+      const u32x4* buf = lds[c % NBUF];
       if (active) {
         if (c < nfull) {
           if (c == 0) fused_block(passc, kNoPrev, buf, 0, accA, accB, 0);
           else fused_block(passc, kPrev, buf, 0, accA, accB, keyB);
-          fused_block(passc, kPrev, buf, 1, accB, accA, c * 128);
-          fused_block(passc, kPrev, buf, 2, accA, accB, c * 128 + 32);
-          fused_block(passc, kPrev, buf, 3, accB, accA, c * 128 + 64);
+          fused_block(passc, kPrev, buf, 1, accB, accA, c * CK);
           pendingB = true;
-          keyB = c * 128 + 96;
+          keyB = c * CK + 32;
         } else {
           if (pendingB) flush(passc, accB, keyB);
           pendingB = false;
-          for (int sb = 0; sb < 4; ++sb) {
-            const int key0 = c * 128 + sb * 32;
+          for (int sb = 0; sb < SBC; ++sb) {
+            const int key0 = c * CK + sb * 32;
             if (key0 >= hi_w) break;
             floatx16 acc[RB];
 #pragma unroll
             for (int rb = 0; rb < RB; ++rb) acc[rb] = floatx16{};
-#pragma unroll
-            for (int s = 0; s < S; ++s) mfma_step(buf, sb, s, acc);
+            mfma_block(buf, sb, acc);
             const int key = key0 + (lane & 31);
             const bool diag = key0 + 31 > qpos0;
-            int cnt = 0;
-            uint32_t bm = 0;
-            float w = 0.0f;
+            int cnt[RB] = {};
+            uint32_t bm[RB] = {};
+            float w[RB] = {};
 #pragma unroll
             for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
@@ -350,35 +424,18 @@ __global__ __launch_bounds__(512, 1) void score_kernel(ScoreArgs a) {
                 if constexpr (pass == 0) {
                   if (causal && v > mx[rb][i]) mx[rb][i] = v;
                 } else {
-                  const int keep = causal && v >= x0[rb][i];
-                  if constexpr (PQ == 0) cnt += keep;
-                  else pq_acc(keep, v, mx[rb][i], i, bm, w);
+                  const int keep = causal && v >= mx[rb][i];
+                  if constexpr (PQ == 0) cnt[rb] += keep;
+                  else pq_acc(keep, v, ref[rb][i], i, bm[rb], w[rb]);
                   if constexpr (RC) rc[rb][i] += keep;
                 }
               }
-            if constexpr (pass == 1) {
-              if constexpr (PQ == 0) {
-                cnt += __shfl_xor(cnt, 32, 64);
-                if (lane < 32 && key < a.N) vrow[key] = (uint8_t)cnt;
-              } else {
-                // the shuffles inside run on every lane; only the store is guarded
-                bm <<= 4 * (lane >> 5);
-                bm |= __shfl_xor(bm, 32, 64);
-                if constexpr (PQ >= 2) w += __shfl_xor(w, 32, 64);
-                if (key < a.N) {
-                  if (lane < 32) brow[key] = bm;
-                  else if constexpr (PQ >= 2) wrow[key] = __float_as_uint(w);
-                }
-              }
-            }
+            if constexpr (pass == 1) store_key(key, true, cnt, bm, w);
           }
         }
       }
-      if (more) {
-        u32x4* dst = lds + ((c + 1) & 1) * CHUNK_UNITS;
-#pragma unroll
-        for (int e = 0; e < PF; ++e) dst[e * NTH + threadIdx.x] = pf[e];
-      }
+      // chunk c + 1's copies have landed in LDS and every wave is done with chunk c
+      if (c + 1 < nchunks) wait_copies(min(nchunks - 1, c + NBUF - 1) - (c + 1));
       __syncthreads();
     }
     if (active && pendingB) flush(passc, accB, keyB);
@@ -397,11 +454,11 @@ __global__ __launch_bounds__(512, 1) void score_kernel(ScoreArgs a) {
             v = fmaxf(v, __shfl_xor(v, 16, 64));
             const float m = v * a.sm_scale;   // fl(max * c) == max of fl(s * c) for c > 0
             const int row = rb * 32 + (i >> 2) * 8 + (lane >> 5) * 4 + (i & 3);
-            const bool ok = row0 + row < a.N;   // padded rows never vote (exact_2.py:121)
-            x0[rb][i] = ok ? min_arg_for(m - tau, a.sm_scale) : INFINITY;
-            if constexpr (PQ == 2) mx[rb][i] = m - tau;   // perquery.py:210
-            if constexpr (PQ == 3) mx[rb][i] = m;         // perquery.py:215
-            if (a.row_max && (lane & 31) == 0 && ok) a.row_max[(int64_t)h * a.N + row0 + row] = m;
+            const bool ok = wrow0 + row < a.N;   // padded rows never vote (exact_2.py:121)
+            mx[rb][i] = ok ? min_arg_for(m - tau, a.sm_scale) : INFINITY;
+            if constexpr (PQ == 2) ref[rb][i] = m - tau;   // perquery.py:210
+            if constexpr (PQ == 3) ref[rb][i] = m;         // perquery.py:215
+            if (a.row_max && (lane & 31) == 0 && ok) a.row_max[(int64_t)h * a.N + wrow0 + row] = m;
           }
       }
     }
@@ -422,7 +479,7 @@ __global__ __launch_bounds__(512, 1) void score_kernel(ScoreArgs a) {
           v += __shfl_xor(v, 8, 64);
           v += __shfl_xor(v, 16, 64);
           const int row = rb * 32 + (i >> 2) * 8 + (lane >> 5) * 4 + (i & 3);
-          if ((lane & 31) == 0 && row0 + row < a.N) a.row_counts[(int64_t)h * a.N + row0 + row] = v;
+          if ((lane & 31) == 0 && wrow0 + row < a.N) a.row_counts[(int64_t)h * a.N + wrow0 + row] = v;
         }
     }
   }
@@ -455,14 +512,9 @@ hipError_t launch_rope_frag(int dtype, int D, const void* x, int64_t hs, int64_t
 
 template <int D, int T, bool RC, int PQ>
 static hipError_t launch_score_t(const ScoreArgs& a, hipStream_t st) {
-  constexpr int S = D / 16;
-  const size_t lds_bytes = 2 * (size_t)(4 * S * 2 * 64) * 16;
-  hipError_t e = hipFuncSetAttribute((const void*)score_kernel<D, T, RC, PQ>,
-                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_bytes);
-  if (e != hipSuccess) return e;
-  const int tpw = 256 / T;
-  const int ngroups = (a.nt + tpw - 1) / tpw;
-  hipLaunchKernelGGL((score_kernel<D, T, RC, PQ>), dim3(a.H * ngroups), dim3(512), lds_bytes, st, a);
+  constexpr int RB = 2;   // 64 query rows per wave (128-row waves spill and balance worse)
+  const int ngroups = (a.nt * T + 128 * RB - 1) / (128 * RB);   // four waves of 32 RB rows
+  hipLaunchKernelGGL((score_kernel<D, T, RC, PQ, RB>), dim3(a.H * ngroups), dim3(256), 0, st, a);
   return hipGetLastError();
 }
 

@@ -94,34 +94,21 @@ __global__ __launch_bounds__(256) void select_kernel(SelectArgs a) {
   float* snp = (float*)(sidx + a.k_max);                                    // k_max
 
   for (int i = tid; i < 260; i += 256) { hist[i] = 0; fhist[i] = 0; }
-  // ---- stage the vote row: the sum of the tile's partial-count planes, zero past each plane's
-  //      causal range ----
-  const VT* vrow = (const VT*)a.votes + ((int64_t)h * a.nt + t) * a.vote_planes * a.votes_stride;
+  // ---- stage the vote row, zero past the keys the score kernel wrote (its causal range) ----
+  const VT* vrow = (const VT*)a.votes + ((int64_t)h * a.nt + t) * a.votes_stride;
   if constexpr (sizeof(VT) == 1) {
-    // four keys per word; byte votes are <= 64 each, so the planes add without carries
-    for (int wi = tid; wi < 64 * per; wi += 256) {
+    for (int wi = tid; wi < 64 * per; wi += 256) {   // four keys per word
       const int j = wi * 4;
-      uint32_t sum = 0;
-      for (int pl = 0; pl < a.vote_planes; ++pl) {
-        const int64_t hp = a.votes_dense ? N : min((int64_t)N, tstart + 32 * (pl + 1));
-        if (j < hp) {   // j + 3 < roundup(N, 4) <= votes_stride: the word is inside the row
-          uint32_t w = ((const uint32_t*)(vrow + pl * a.votes_stride))[wi];
-          const int64_t valid = hp - j;
-          if (valid < 4) w &= (1u << (8 * valid)) - 1u;
-          sum += w;
-        }
+      uint32_t w = 0;
+      if (j < hi_keys) {   // j + 3 < roundup(N, 4) <= votes_stride: the word is inside the row
+        w = ((const uint32_t*)vrow)[wi];
+        const int valid = hi_keys - j;
+        if (valid < 4) w &= (1u << (8 * valid)) - 1u;
       }
-      ((uint32_t*)vb)[wi] = sum;
+      ((uint32_t*)vb)[wi] = w;
     }
   } else {
-    for (int j = tid; j < 256 * per; j += 256) {
-      uint32_t sum = 0;
-      for (int pl = 0; pl < a.vote_planes; ++pl) {
-        const int64_t hp = a.votes_dense ? N : min((int64_t)N, tstart + 32 * (pl + 1));
-        if (j < hp) sum += (uint32_t)vrow[pl * a.votes_stride + j];
-      }
-      vb[j] = (uint8_t)sum;
-    }
+    for (int j = tid; j < 256 * per; j += 256) vb[j] = j < hi_keys ? (uint8_t)vrow[j] : 0;
   }
   __syncthreads();
   if (a.votes_out) {
@@ -256,27 +243,22 @@ __global__ __launch_bounds__(256) void select_kernel(SelectArgs a) {
   }
 }
 
-// byte vote planes (plane p: keys < min(N, tile start + 32 (p+1)) valid) -> the reference's
-// dense int32 (H, nt, N) layout
+// byte votes (keys < min(N, tile end) valid) -> the reference's dense int32 (H, nt, N) votes
 __global__ __launch_bounds__(256) void expand_votes_kernel(const uint8_t* __restrict__ v8, int64_t stride,
-                                                           int planes, int nt, int N, int T, int q_pos_base,
+                                                           int nt, int N, int T, int q_pos_base,
                                                            int32_t* __restrict__ out) {
   const int ht = blockIdx.y;
   const int t = ht % nt;
-  const int64_t tstart = (int64_t)q_pos_base + (int64_t)t * T;
-  for (int j = blockIdx.x * 256 + threadIdx.x; j < N; j += gridDim.x * 256) {
-    int32_t sum = 0;
-    for (int pl = 0; pl < planes; ++pl)
-      if (j < min((int64_t)N, tstart + 32 * (pl + 1))) sum += v8[((int64_t)ht * planes + pl) * stride + j];
-    out[(int64_t)ht * N + j] = sum;
-  }
+  const int64_t hp = min((int64_t)N, (int64_t)q_pos_base + (int64_t)t * T + T);
+  for (int j = blockIdx.x * 256 + threadIdx.x; j < N; j += gridDim.x * 256)
+    out[(int64_t)ht * N + j] = j < hp ? (int32_t)v8[(int64_t)ht * stride + j] : 0;
 }
 
-hipError_t launch_expand_votes(const uint8_t* v8, int64_t stride, int planes, int H, int nt, int N, int T,
-                               int q_pos_base, int32_t* out, hipStream_t st) {
+hipError_t launch_expand_votes(const uint8_t* v8, int64_t stride, int H, int nt, int N, int T, int q_pos_base,
+                               int32_t* out, hipStream_t st) {
   const int bx = (N + 255) / 256 < 64 ? (N + 255) / 256 : 64;
-  hipLaunchKernelGGL(expand_votes_kernel, dim3(bx, H * nt), dim3(256), 0, st, v8, stride, planes, nt, N, T,
-                     q_pos_base, out);
+  hipLaunchKernelGGL(expand_votes_kernel, dim3(bx, H * nt), dim3(256), 0, st, v8, stride, nt, N, T, q_pos_base,
+                     out);
   return hipGetLastError();
 }
 

@@ -48,7 +48,7 @@ def test_workspace_size_matches_layout():
     nt = 12288 // 64
     q = 32 * 12288 * 128 * 4            # q fragments, hi + lo bf16
     k = 32 * 12288 * 128 * 4            # k fragments
-    votes = 32 * nt * (64 // 32) * 12288  # byte votes, one plane per 32 query rows of a tile
+    votes = 32 * nt * 12288             # byte votes, one row per tile
     assert n >= q + k + votes and n < q + k + votes + 4096
 
 
