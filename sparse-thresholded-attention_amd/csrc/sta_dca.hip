@@ -218,27 +218,26 @@ __global__ __launch_bounds__(G * 64, 1) void dca_attn_kernel(DcaArgs a) {
       const int e = tid + u * NTH;
       if (e >= Cfg::VUNITS) continue;
       const int sg = e / (D / 8), dc = e % (D / 8);
-      float vv[4][8];
+      if constexpr (!X3) {   // 16-bit storage: transpose the raw bits
+        u32x2 cols[8];
+        transpose4x8_16(vreg[u][0].w, vreg[u][1].w, vreg[u][2].w, vreg[u][3].w, cols);
 #pragma unroll
-      for (int k = 0; k < 4; ++k) vreg[u][k].to_f32(vv[k]);
+        for (int e8 = 0; e8 < 8; ++e8) *(u32x2*)(vd + (dc * 8 + e8) * VSTR + sg * 4) = cols[e8];
+      } else {              // fp32: bf16 hi and lo planes
+        float vv[4][8];
 #pragma unroll
-      for (int e8 = 0; e8 < 8; ++e8) {
-        u32x2 w;
-        if constexpr (DT == DT_F16) {
-          w[0] = f32_to_f16_bits(vv[0][e8]) | (f32_to_f16_bits(vv[1][e8]) << 16);
-          w[1] = f32_to_f16_bits(vv[2][e8]) | (f32_to_f16_bits(vv[3][e8]) << 16);
-        } else {
-          w[0] = f32_to_bf16_bits(vv[0][e8]) | (f32_to_bf16_bits(vv[1][e8]) << 16);
-          w[1] = f32_to_bf16_bits(vv[2][e8]) | (f32_to_bf16_bits(vv[3][e8]) << 16);
-        }
-        *(u32x2*)(vd + (dc * 8 + e8) * VSTR + sg * 4) = w;
-        if constexpr (X3) {
+        for (int k = 0; k < 4; ++k) vreg[u][k].to_f32(vv[k]);
+#pragma unroll
+        for (int e8 = 0; e8 < 8; ++e8) {
+          u32x2 w, wl;
+          w[0] = pack2_bf16(vv[0][e8], vv[1][e8]);
+          w[1] = pack2_bf16(vv[2][e8], vv[3][e8]);
           float lo[4];
 #pragma unroll
           for (int k = 0; k < 4; ++k) lo[k] = vv[k][e8] - bf16_bits_to_f32(f32_to_bf16_bits(vv[k][e8]));
-          u32x2 wl;
-          wl[0] = f32_to_bf16_bits(lo[0]) | (f32_to_bf16_bits(lo[1]) << 16);
-          wl[1] = f32_to_bf16_bits(lo[2]) | (f32_to_bf16_bits(lo[3]) << 16);
+          wl[0] = pack2_bf16(lo[0], lo[1]);
+          wl[1] = pack2_bf16(lo[2], lo[3]);
+          *(u32x2*)(vd + (dc * 8 + e8) * VSTR + sg * 4) = w;
           *(u32x2*)(vd + D * VSTR + (dc * 8 + e8) * VSTR + sg * 4) = wl;
         }
       }
@@ -372,13 +371,13 @@ __global__ __launch_bounds__(G * 64, 1) void dca_attn_kernel(DcaArgs a) {
           *(float4*)((float*)a.out + ob + d0) = make_float4(o[0], o[1], o[2], o[3]);
         } else if constexpr (DT == DT_BF16) {
           u32x2 w;
-          w[0] = f32_to_bf16_bits(o[0]) | (f32_to_bf16_bits(o[1]) << 16);
-          w[1] = f32_to_bf16_bits(o[2]) | (f32_to_bf16_bits(o[3]) << 16);
+          w[0] = pack2_bf16(o[0], o[1]);
+          w[1] = pack2_bf16(o[2], o[3]);
           *(u32x2*)((uint16_t*)a.out + ob + d0) = w;
         } else {
           u32x2 w;
-          w[0] = f32_to_f16_bits(o[0]) | (f32_to_f16_bits(o[1]) << 16);
-          w[1] = f32_to_f16_bits(o[2]) | (f32_to_f16_bits(o[3]) << 16);
+          w[0] = pack2_f16(o[0], o[1]);
+          w[1] = pack2_f16(o[2], o[3]);
           *(u32x2*)((uint16_t*)a.out + ob + d0) = w;
         }
       }

@@ -26,12 +26,17 @@ enum DType { DT_F32 = 0, DT_BF16 = 1, DT_F16 = 2 };
 // ------------------------------------------------------------------------------------------
 __device__ __forceinline__ float bf16_bits_to_f32(uint32_t h) { return __uint_as_float(h << 16); }
 
-__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu)) return (u >> 16) | 0x40u;
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return u >> 16;
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float float2_t __attribute__((ext_vector_type(2)));
+
+// Two fp32 values -> packed bf16 (a in the low half), rounded to nearest even by the hardware
+// conversion (v_cvt_pk_bf16_f32; checked against a bitwise RNE on 2^24 inputs including ties).
+__device__ __forceinline__ uint32_t pack2_bf16(float a, float b) {
+  const float2_t v = {a, b};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
 }
+
+__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) { return pack2_bf16(f, f) & 0xffffu; }
 
 __device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
   _Float16 x = __builtin_bit_cast(_Float16, (uint16_t)h);
@@ -41,6 +46,30 @@ __device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
 __device__ __forceinline__ uint32_t f32_to_f16_bits(float f) {
   _Float16 x = (_Float16)f;  // hardware conversion rounds to nearest even
   return (uint32_t)__builtin_bit_cast(uint16_t, x);
+}
+
+__device__ __forceinline__ uint32_t pack2_f16(float a, float b) {
+  return f32_to_f16_bits(a) | (f32_to_f16_bits(b) << 16);
+}
+
+// two fp32 values in the 16-bit storage format DT (bf16 or f16)
+template <int DT>
+__device__ __forceinline__ uint32_t pack2_dt(float a, float b) {
+  if constexpr (DT == 2) return pack2_f16(a, b);
+  else return pack2_bf16(a, b);
+}
+
+// Transpose four rows of eight 16-bit elements (u32x4 each) into eight columns of four:
+// out[e] = {r0[e] | r1[e] << 16, r2[e] | r3[e] << 16}.  Pure bit moves.
+__device__ __forceinline__ void transpose4x8_16(const u32x4& r0, const u32x4& r1, const u32x4& r2,
+                                                const u32x4& r3, u32x2* out) {
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    out[2 * w][0] = __builtin_amdgcn_perm(r1[w], r0[w], 0x05040100u);       // low halves
+    out[2 * w][1] = __builtin_amdgcn_perm(r3[w], r2[w], 0x05040100u);
+    out[2 * w + 1][0] = __builtin_amdgcn_perm(r1[w], r0[w], 0x07060302u);   // high halves
+    out[2 * w + 1][1] = __builtin_amdgcn_perm(r3[w], r2[w], 0x07060302u);
+  }
 }
 
 template <int DT>
@@ -78,25 +107,24 @@ __device__ __forceinline__ void load8(const void* p, int64_t i, float* out) {
 __device__ __forceinline__ void split_bf16x8(const float* x, u32x4& hi, u32x4& lo) {
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
-    uint32_t h0 = f32_to_bf16_bits(x[2 * e]), h1 = f32_to_bf16_bits(x[2 * e + 1]);
-    float r0 = x[2 * e] - bf16_bits_to_f32(h0), r1 = x[2 * e + 1] - bf16_bits_to_f32(h1);
-    uint32_t l0 = f32_to_bf16_bits(r0), l1 = f32_to_bf16_bits(r1);
-    hi[e] = h0 | (h1 << 16);
-    lo[e] = l0 | (l1 << 16);
+    const uint32_t h = pack2_bf16(x[2 * e], x[2 * e + 1]);
+    const float r0 = x[2 * e] - __uint_as_float(h << 16), r1 = x[2 * e + 1] - __uint_as_float(h & 0xffff0000u);
+    hi[e] = h;
+    lo[e] = pack2_bf16(r0, r1);
   }
 }
 
 __device__ __forceinline__ u32x4 pack_bf16x8(const float* x) {
   u32x4 r;
 #pragma unroll
-  for (int e = 0; e < 4; ++e) r[e] = f32_to_bf16_bits(x[2 * e]) | (f32_to_bf16_bits(x[2 * e + 1]) << 16);
+  for (int e = 0; e < 4; ++e) r[e] = pack2_bf16(x[2 * e], x[2 * e + 1]);
   return r;
 }
 
 __device__ __forceinline__ u32x4 pack_f16x8(const float* x) {
   u32x4 r;
 #pragma unroll
-  for (int e = 0; e < 4; ++e) r[e] = f32_to_f16_bits(x[2 * e]) | (f32_to_f16_bits(x[2 * e + 1]) << 16);
+  for (int e = 0; e < 4; ++e) r[e] = pack2_f16(x[2 * e], x[2 * e + 1]);
   return r;
 }
 

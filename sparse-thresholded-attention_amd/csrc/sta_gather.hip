@@ -160,27 +160,26 @@ __global__ __launch_bounds__(NW * 64 + 256, 1) void gather_kernel(GatherArgs a) 
         const int u = ptid + vu * 256;
         if (u >= Cfg::VUNITS) continue;
         const int sg = u / (D / 8), dc = u % (D / 8);
-        float vv[4][8];
+        if constexpr (!X3) {   // 16-bit storage: transpose the raw bits
+          u32x2 cols[8];
+          transpose4x8_16(vx[vu][0].w, vx[vu][1].w, vx[vu][2].w, vx[vu][3].w, cols);
 #pragma unroll
-        for (int k = 0; k < 4; ++k) vx[vu][k].to_f32(vv[k]);
+          for (int e = 0; e < 8; ++e) *(u32x2*)(vt_hi + (dc * 8 + e) * VSTR + sg * 4) = cols[e];
+        } else {              // fp32: bf16 hi and lo planes
+          float vv[4][8];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          u32x2 w;
-          if constexpr (DT == DT_F16) {
-            w[0] = f32_to_f16_bits(vv[0][e]) | (f32_to_f16_bits(vv[1][e]) << 16);
-            w[1] = f32_to_f16_bits(vv[2][e]) | (f32_to_f16_bits(vv[3][e]) << 16);
-          } else {
-            w[0] = f32_to_bf16_bits(vv[0][e]) | (f32_to_bf16_bits(vv[1][e]) << 16);
-            w[1] = f32_to_bf16_bits(vv[2][e]) | (f32_to_bf16_bits(vv[3][e]) << 16);
-          }
-          *(u32x2*)(vt_hi + (dc * 8 + e) * VSTR + sg * 4) = w;
-          if constexpr (X3) {
+          for (int k = 0; k < 4; ++k) vx[vu][k].to_f32(vv[k]);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            u32x2 w, wl;
+            w[0] = pack2_bf16(vv[0][e], vv[1][e]);
+            w[1] = pack2_bf16(vv[2][e], vv[3][e]);
             float lo[4];
 #pragma unroll
             for (int k = 0; k < 4; ++k) lo[k] = vv[k][e] - bf16_bits_to_f32(f32_to_bf16_bits(vv[k][e]));
-            u32x2 wl;
-            wl[0] = f32_to_bf16_bits(lo[0]) | (f32_to_bf16_bits(lo[1]) << 16);
-            wl[1] = f32_to_bf16_bits(lo[2]) | (f32_to_bf16_bits(lo[3]) << 16);
+            wl[0] = pack2_bf16(lo[0], lo[1]);
+            wl[1] = pack2_bf16(lo[2], lo[3]);
+            *(u32x2*)(vt_hi + (dc * 8 + e) * VSTR + sg * 4) = w;
             *(u32x2*)(vt_lo + (dc * 8 + e) * VSTR + sg * 4) = wl;
           }
         }
@@ -362,13 +361,13 @@ __global__ __launch_bounds__(NW * 64 + 256, 1) void gather_kernel(GatherArgs a) 
         *(float4*)((float*)a.out + ob + d0) = make_float4(o[0], o[1], o[2], o[3]);
       } else if constexpr (DT == DT_BF16) {
         u32x2 w;
-        w[0] = f32_to_bf16_bits(o[0]) | (f32_to_bf16_bits(o[1]) << 16);
-        w[1] = f32_to_bf16_bits(o[2]) | (f32_to_bf16_bits(o[3]) << 16);
+        w[0] = pack2_bf16(o[0], o[1]);
+        w[1] = pack2_bf16(o[2], o[3]);
         *(u32x2*)((uint16_t*)a.out + ob + d0) = w;
       } else {
         u32x2 w;
-        w[0] = f32_to_f16_bits(o[0]) | (f32_to_f16_bits(o[1]) << 16);
-        w[1] = f32_to_f16_bits(o[2]) | (f32_to_f16_bits(o[3]) << 16);
+        w[0] = pack2_f16(o[0], o[1]);
+        w[1] = pack2_f16(o[2], o[3]);
         *(u32x2*)((uint16_t*)a.out + ob + d0) = w;
       }
     }
