@@ -30,7 +30,9 @@ struct GatherCfg {
   static constexpr int VU = (VUNITS + NP - 1) / NP;   // V units per producer thread
   static constexpr bool X3 = (DT == DT_F32);   // fp32 inputs: three-term bf16 products
   static constexpr int KSTR = D + 8;           // K LDS row stride (bf16 elements)
-  static constexpr int VSTR = 64 + 8;          // V^T LDS row stride (elements)
+  using VL = VtLayout<64, false>;              // V^T LDS layout (padded rows; the swizzled
+                                               // layout measured slower here: more address registers)
+  static constexpr int VSTR = VL::STR;
   static constexpr int KHALVES = X3 ? 2 : 1;
   static constexpr int KBUF = KHALVES * 64 * KSTR;     // elements of one K buffer
   static constexpr int VBUF = KHALVES * D * VSTR;      // elements of one V^T buffer
@@ -135,8 +137,10 @@ __global__ __launch_bounds__(NW * 64 + 256, 1) void gather_kernel(GatherArgs a) 
         for (int e = 0; e < 8; ++e) {
           float sn, cs;
           fast_sincos(np * invf[kpart * FP + 8 * c + e], sn, cs);
-          cs *= rs;
-          sn *= rs;
+          if (rs != 1.0f) {   // uniform: rope_scale is 1 except under YaRN
+            cs *= rs;
+            sn *= rs;
+          }
           o1[e] = x1[e] * cs - x2[e] * sn;
           o2[e] = x2[e] * cs + x1[e] * sn;
         }
@@ -164,7 +168,7 @@ __global__ __launch_bounds__(NW * 64 + 256, 1) void gather_kernel(GatherArgs a) 
           u32x2 cols[8];
           transpose4x8_16(vx[vu][0].w, vx[vu][1].w, vx[vu][2].w, vx[vu][3].w, cols);
 #pragma unroll
-          for (int e = 0; e < 8; ++e) *(u32x2*)(vt_hi + (dc * 8 + e) * VSTR + sg * 4) = cols[e];
+          for (int e = 0; e < 8; ++e) *(u32x2*)(vt_hi + Cfg::VL::off(dc * 8 + e, sg)) = cols[e];
         } else {              // fp32: bf16 hi and lo planes
           float vv[4][8];
 #pragma unroll
@@ -179,8 +183,8 @@ __global__ __launch_bounds__(NW * 64 + 256, 1) void gather_kernel(GatherArgs a) 
             for (int k = 0; k < 4; ++k) lo[k] = vv[k][e] - bf16_bits_to_f32(f32_to_bf16_bits(vv[k][e]));
             wl[0] = pack2_bf16(lo[0], lo[1]);
             wl[1] = pack2_bf16(lo[2], lo[3]);
-            *(u32x2*)(vt_hi + (dc * 8 + e) * VSTR + sg * 4) = w;
-            *(u32x2*)(vt_lo + (dc * 8 + e) * VSTR + sg * 4) = wl;
+            *(u32x2*)(vt_hi + Cfg::VL::off(dc * 8 + e, sg)) = w;
+            *(u32x2*)(vt_lo + Cfg::VL::off(dc * 8 + e, sg)) = wl;
           }
         }
       }
@@ -208,6 +212,9 @@ __global__ __launch_bounds__(NW * 64 + 256, 1) void gather_kernel(GatherArgs a) 
   const bool row_ok = qrow < N;
   const int64_t qpos = (int64_t)a.q_pos_base + qrow;
   const int64_t qpos_first = (int64_t)a.q_pos_base + (int64_t)t * T;
+  // Q is rotated, then scaled by sm_scale * log2(e): scores come out in base-2 units and the
+  // softmax uses exp2 (the scale commutes with the max and cancels in acc / l)
+  const float qscale = a.sm_scale * 1.4426950408889634f;
   u32x4 qf_hi[KS], qf_lo[KS];
   {
     const float npq = a.newpos_q[((int64_t)h * a.nt + t) * T + r];
@@ -231,7 +238,7 @@ __global__ __launch_bounds__(NW * 64 + 256, 1) void gather_kernel(GatherArgs a) 
         fast_sincos(npq * invf[i0 + e], sn, cs);
         cs *= rs;
         sn *= rs;
-        out[e] = first ? own[e] * cs - other[e] * sn : own[e] * cs + other[e] * sn;
+        out[e] = (first ? own[e] * cs - other[e] * sn : own[e] * cs + other[e] * sn) * qscale;
       }
       if constexpr (X3) split_bf16x8(out, qf_hi[ks], qf_lo[ks]);
       else qf_hi[ks] = pack_bf16x8(out);
@@ -290,30 +297,38 @@ __global__ __launch_bounds__(NW * 64 + 256, 1) void gather_kernel(GatherArgs a) 
       for (int i = 0; i < 4; ++i) {
         const bool keep = (unmasked || (((unsigned)jj[i] < (unsigned)N) && (qpos >= jj[i])))  // exact_2.py:210
                           && (a.mask == nullptr || ((mk[i] >> (r & 31)) & 1u));
-        const float v = keep ? sacc[sb][i] * a.sm_scale : -INFINITY;
+        const float v = keep ? sacc[sb][i] : -INFINITY;
         p[sb][i] = v;
         bmax = fmaxf(bmax, v);
       }
     }
     bmax = fmaxf(bmax, __shfl_xor(bmax, 16, 64));
     bmax = fmaxf(bmax, __shfl_xor(bmax, 32, 64));
-    const float mnew = fmaxf(mR, bmax);
-    const float msafe = (mnew == -INFINITY) ? 0.0f : mnew;
-    const float alpha = __expf(mR - msafe);
+    // Online softmax with a lazily raised reference (exact_2.py:213-217 in exact arithmetic): the
+    // reference mR only moves when a row's block max exceeds it by more than 2^8, so the rescale
+    // of l and the accumulator is skipped for most blocks; exponents stay <= 8, which fp32 and the
+    // bf16 P operand hold without loss of range.
+    const bool raise = bmax > mR + 8.0f;
+    if (__builtin_amdgcn_ballot_w64(raise) != 0) {
+      const float mnew = raise ? bmax : mR;
+      const float alpha = raise ? __builtin_amdgcn_exp2f(mR - mnew) : 1.0f;   // 0 when mR = -inf
+      l_i *= alpha;
+#pragma unroll
+      for (int db = 0; db < DB; ++db) oacc[db] *= alpha;
+      mR = mnew;
+    }
+    const float msafe = (mR == -INFINITY) ? 0.0f : mR;
     float psum = 0.0f;
 #pragma unroll
     for (int sb = 0; sb < 4; ++sb)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        p[sb][i] = __expf(p[sb][i] - msafe);
+        p[sb][i] = __builtin_amdgcn_exp2f(p[sb][i] - msafe);
         psum += p[sb][i];
       }
     psum += __shfl_xor(psum, 16, 64);
     psum += __shfl_xor(psum, 32, 64);
-    l_i = l_i * alpha + psum;
-    mR = mnew;
-#pragma unroll
-    for (int db = 0; db < DB; ++db) oacc[db] *= alpha;
+    l_i += psum;
 
     // ---- O^T += V^T . P^T (exact_2.py:218-220) ----
 #pragma unroll
@@ -328,14 +343,15 @@ __global__ __launch_bounds__(NW * 64 + 256, 1) void gather_kernel(GatherArgs a) 
       for (int db = 0; db < DB; ++db) {
         const int row = db * 16 + (lane & 15);
         const int c0 = sb0 * 16 + 4 * (lane >> 4), c1 = sb1 * 16 + 4 * (lane >> 4);
-        const u32x2 a0 = *(const u32x2*)(vt_hi + row * VSTR + c0);
-        const u32x2 a1 = *(const u32x2*)(vt_hi + row * VSTR + c1);
+        const int o0 = Cfg::VL::off(row, c0 >> 2), o1 = Cfg::VL::off(row, c1 >> 2);
+        const u32x2 a0 = *(const u32x2*)(vt_hi + o0);
+        const u32x2 a1 = *(const u32x2*)(vt_hi + o1);
         const u32x4 va = u32x4{a0[0], a0[1], a1[0], a1[1]};
         if constexpr (DT == DT_F16) {
           oacc[db] = mfma16_f16(va, pb, oacc[db]);
         } else if constexpr (X3) {
-          const u32x2 b0 = *(const u32x2*)(vt_lo + row * VSTR + c0);
-          const u32x2 b1 = *(const u32x2*)(vt_lo + row * VSTR + c1);
+          const u32x2 b0 = *(const u32x2*)(vt_lo + o0);
+          const u32x2 b1 = *(const u32x2*)(vt_lo + o1);
           const u32x4 vl = u32x4{b0[0], b0[1], b1[0], b1[1]};
           oacc[db] = mfma16(vl, pb, oacc[db]);
           oacc[db] = mfma16(va, pbl, oacc[db]);
@@ -387,7 +403,7 @@ static hipError_t launch_gather_t(const GatherArgs& a, hipStream_t st) {
 
 size_t gather_lds_bytes(int dtype, int D, int k_max) {
   const size_t halves = dtype == DT_F32 ? 2 : 1;
-  const size_t fixed = 2 * halves * ((size_t)64 * (D + 8) * 2 + (size_t)D * 72 * 2);
+  const size_t fixed = 2 * halves * ((size_t)64 * (D + 8) * 2 + (size_t)D * VtLayout<64, false>::STR * 2);
   return fixed + (size_t)((k_max + 63) / 64) * 64 * 4;
 }
 

@@ -96,7 +96,9 @@ struct StreamCfg {
   static constexpr int P = X3 ? 2 : 1;              // planes (hi, lo)
   static constexpr int NTH = G * 64;
   static constexpr int KSTR = D + 8;                // K~ LDS row stride (elements)
-  static constexpr int VSTR = BN + 8;               // V^T LDS row stride (elements)
+  using VL = VtLayout<BN, false>;   // V^T LDS layout (padded rows: measured faster than the
+                                    // swizzled layout in this kernel)
+  static constexpr int VSTR = VL::STR;               // V^T LDS row stride (elements)
   static constexpr int KBUF = P * BN * KSTR;        // elements of one K~ buffer
   static constexpr int VBUF = P * D * VSTR;         // elements of one V^T buffer
   static constexpr int KUNITS = P * BN * D / 8;     // 16-byte units of a K~ block
@@ -222,7 +224,7 @@ __global__ __launch_bounds__(G * 64, 1) void stream_kernel(StreamArgs a) {
         u32x2 cols[8];
         transpose4x8_16(vreg[u][0].w, vreg[u][1].w, vreg[u][2].w, vreg[u][3].w, cols);
 #pragma unroll
-        for (int e8 = 0; e8 < 8; ++e8) *(u32x2*)(vd + (dc * 8 + e8) * VSTR + sg * 4) = cols[e8];
+        for (int e8 = 0; e8 < 8; ++e8) *(u32x2*)(vd + Cfg::VL::off(dc * 8 + e8, sg)) = cols[e8];
       } else {              // fp32: bf16 hi and lo planes
         float vv[4][8];
 #pragma unroll
@@ -237,8 +239,8 @@ __global__ __launch_bounds__(G * 64, 1) void stream_kernel(StreamArgs a) {
           for (int k = 0; k < 4; ++k) lo[k] = vv[k][e8] - bf16_bits_to_f32(f32_to_bf16_bits(vv[k][e8]));
           wl[0] = pack2_bf16(lo[0], lo[1]);
           wl[1] = pack2_bf16(lo[2], lo[3]);
-          *(u32x2*)(vd + (dc * 8 + e8) * VSTR + sg * 4) = w;
-          *(u32x2*)(vd + D * VSTR + (dc * 8 + e8) * VSTR + sg * 4) = wl;
+          *(u32x2*)(vd + Cfg::VL::off(dc * 8 + e8, sg)) = w;
+          *(u32x2*)(vd + D * VSTR + Cfg::VL::off(dc * 8 + e8, sg)) = wl;
         }
       }
     }
@@ -425,14 +427,15 @@ __global__ __launch_bounds__(G * 64, 1) void stream_kernel(StreamArgs a) {
 #pragma unroll
             for (int rb = 0; rb < RBS; ++rb) {
               const int r = rb * 32 + q;
-              const u32x2 a0 = *(const u32x2*)(vt + r * VSTR + c0);
-              const u32x2 a1 = *(const u32x2*)(vt + r * VSTR + c1);
+              const int o0 = Cfg::VL::off(r, c0 >> 2), o1 = Cfg::VL::off(r, c1 >> 2);
+              const u32x2 a0 = *(const u32x2*)(vt + o0);
+              const u32x2 a1 = *(const u32x2*)(vt + o1);
               const u32x4 va = u32x4{a0[0], a0[1], a1[0], a1[1]};
               if constexpr (DT == DT_F16) {
                 oacc[rb] = mfma32_f16(va, pb, oacc[rb]);
               } else if constexpr (X3) {
-                const u32x2 b0 = *(const u32x2*)(vt + D * VSTR + r * VSTR + c0);
-                const u32x2 b1 = *(const u32x2*)(vt + D * VSTR + r * VSTR + c1);
+                const u32x2 b0 = *(const u32x2*)(vt + D * VSTR + o0);
+                const u32x2 b1 = *(const u32x2*)(vt + D * VSTR + o1);
                 const u32x4 vl = u32x4{b0[0], b0[1], b1[0], b1[1]};
                 oacc[rb] = mfma32(vl, pb, oacc[rb]);
                 oacc[rb] = mfma32(va, pbl, oacc[rb]);
