@@ -76,12 +76,13 @@ __device__ __forceinline__ void transpose4x8_16(const u32x4& r0, const u32x4& r1
 // elements), read as an MFMA operand 4 slots at a time.  SWZ: the 4-slot column groups are
 // XOR-swizzled by row so that both access patterns hit distinct banks: the transposing stores
 // (16 lanes on rows 8 apart, one column group) and the operand reads (16 lanes on 16 consecutive
-// rows starting at a multiple of 16, one column group).  Without SWZ the rows are padded by 8
-// elements (fewer address registers, 2-way read conflicts).
+// rows starting at a multiple of 16, one column group).  Without SWZ the rows are padded by 4
+// elements: the row stride is then 8 bytes times an odd number, so the operand reads are
+// conflict-free with no extra address registers (the stores keep 8-way conflicts).
 template <int BN, bool SWZ = true>
 struct VtLayout {
   static_assert(BN == 32 || BN == 64, "slots per block");
-  static constexpr int STR = !SWZ ? BN + 8 : (BN == 64 ? 64 : 36);   // row stride in elements
+  static constexpr int STR = !SWZ ? BN + 4 : (BN == 64 ? 64 : 36);   // row stride in elements
   __device__ static __forceinline__ int off(int row, int grp) {
     if constexpr (!SWZ) return row * STR + (grp << 2);
     const int g = BN == 64 ? ((row ^ (row >> 3)) & 15) : ((row >> 4) & 7);
