@@ -169,6 +169,17 @@ __device__ __forceinline__ floatx4 mfma16_f16(const u32x4& a, const u32x4& b, fl
                                                 __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
 }
 
+// ds_read_b64_tr_b16 (gfx950): within each group of 16 lanes, lane L reads 4 16-bit elements at
+// its own address and the group's 64 elements are transposed: lane i receives element i % 4 of
+// lanes i/4, 4 + i/4, 8 + i/4 and 12 + i/4 (layout checked on an MI355X).  Addressing slot
+// base + L/4, columns c + 4 (L % 4) .. +3 of a row-major tile hands lane L column c + L of
+// slots base .. base + 3: a k-contiguous MFMA operand from a k-strided layout.
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ u32x2 tr_read16x4(const uint16_t* p) {
+  const s16x4 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)(p));
+  return __builtin_bit_cast(u32x2, r);
+}
+
 // ------------------------------------------------------------------------------------------
 // 8 consecutive elements in their storage format (loaded now, converted later)
 template <int DT>

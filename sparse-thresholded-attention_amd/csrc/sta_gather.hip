@@ -11,9 +11,10 @@
 // transposed, S^T = K_rot . Q_rot^T (16x16x32 MFMA, lane <-> query row), so the P fragment the
 // P.V product needs as its B operand is exactly the score accumulator the lane already holds:
 //   O^T (dims x rows) += V^T (dims x slots) . P^T (slots x rows)
-// with the contraction order over slots permuted identically in V^T and P^T.  V is written to
-// LDS transposed (dim-major) once per block.  K rows arrive row-major (256 B per row at d128 bf16,
-// 16-byte loads), are rotated in fp32 and stored to LDS as bf16.
+// with the contraction order over slots permuted identically in V^T and P^T.  V rows are stored
+// row-major in LDS (16-byte writes) and read as the V^T operand by transposing LDS reads
+// (ds_read_b64_tr_b16).  K rows arrive row-major (256 B per row at d128 bf16, 16-byte loads), are
+// rotated in fp32 and stored to LDS as bf16.
 #include "sta_device.h"
 #include "sta_kernels.h"
 
@@ -30,12 +31,12 @@ struct GatherCfg {
   static constexpr int VU = (VUNITS + NP - 1) / NP;   // V units per producer thread
   static constexpr bool X3 = (DT == DT_F32);   // fp32 inputs: three-term bf16 products
   static constexpr int KSTR = D + 8;           // K LDS row stride (bf16 elements)
-  using VL = VtLayout<64, false>;              // V^T LDS layout (padded rows; the swizzled
-                                               // layout measured slower here: more address registers)
-  static constexpr int VSTR = VL::STR;
+  // V rows are kept row-major in LDS; a row stride of D + 16 elements puts the 4 rows one
+  // transposing read touches (32 bytes each) in distinct bank windows
+  static constexpr int VRS = D + 16;
   static constexpr int KHALVES = X3 ? 2 : 1;
   static constexpr int KBUF = KHALVES * 64 * KSTR;     // elements of one K buffer
-  static constexpr int VBUF = KHALVES * D * VSTR;      // elements of one V^T buffer
+  static constexpr int VBUF = KHALVES * 64 * VRS;      // elements of one V buffer
   static constexpr size_t LDS_FIXED = (size_t)2 * (KBUF + VBUF) * 2;   // double-buffered
   // + the tile's kept positions (4 bytes per slot, rounded up to whole 64-slot blocks)
   static size_t lds_bytes(int k_max) { return LDS_FIXED + (size_t)((k_max + 63) / 64) * 64 * 4; }
@@ -50,12 +51,12 @@ __global__ __launch_bounds__(NW * 64 + 256, 1) void gather_kernel(GatherArgs a) 
   using Cfg = GatherCfg<DT, D, NW>;
   constexpr int NC = Cfg::NC, NT = Cfg::NT, TPS = Cfg::TPS, FP = Cfg::FP, VU = Cfg::VU;
   constexpr bool X3 = Cfg::X3;
-  constexpr int KSTR = Cfg::KSTR, VSTR = Cfg::VSTR;
+  constexpr int KSTR = Cfg::KSTR, VRS = Cfg::VRS;
   constexpr int T = NW * 16;
   constexpr int KS = D / 32;                   // k steps of the score MFMA
   constexpr int DB = D / 16;                   // 16-dim blocks of the output
   extern __shared__ __align__(16) uint16_t sh[];
-  // buffer p: K [64][KSTR] (hi, then lo when X3) followed by V^T [D][VSTR] (hi, then lo)
+  // buffer p: K [64][KSTR] (hi, then lo when X3) followed by V [64][VRS] (hi, then lo)
   auto kbuf = [&](int p) { return sh + p * (Cfg::KBUF + Cfg::VBUF); };
   auto vbuf = [&](int p) { return sh + p * (Cfg::KBUF + Cfg::VBUF) + Cfg::KBUF; };
   int32_t* sidx = (int32_t*)(sh + Cfg::LDS_FIXED / 2);     // the tile's kept positions
@@ -126,8 +127,8 @@ __global__ __launch_bounds__(NW * 64 + 256, 1) void gather_kernel(GatherArgs a) 
     auto store_block = [&](int b) {
       uint16_t* kr_hi = kbuf(b & 1);
       uint16_t* kr_lo = kr_hi + 64 * KSTR;
-      uint16_t* vt_hi = vbuf(b & 1);
-      uint16_t* vt_lo = vt_hi + D * VSTR;
+      uint16_t* v_hi = vbuf(b & 1);
+      uint16_t* v_lo = v_hi + 64 * VRS;
 #pragma unroll
       for (int c = 0; c < FP / 8; ++c) {
         float x1[8], x2[8], o1[8], o2[8];
@@ -164,27 +165,18 @@ __global__ __launch_bounds__(NW * 64 + 256, 1) void gather_kernel(GatherArgs a) 
         const int u = ptid + vu * 256;
         if (u >= Cfg::VUNITS) continue;
         const int sg = u / (D / 8), dc = u % (D / 8);
-        if constexpr (!X3) {   // 16-bit storage: transpose the raw bits
-          u32x2 cols[8];
-          transpose4x8_16(vx[vu][0].w, vx[vu][1].w, vx[vu][2].w, vx[vu][3].w, cols);
 #pragma unroll
-          for (int e = 0; e < 8; ++e) *(u32x2*)(vt_hi + Cfg::VL::off(dc * 8 + e, sg)) = cols[e];
-        } else {              // fp32: bf16 hi and lo planes
-          float vv[4][8];
-#pragma unroll
-          for (int k = 0; k < 4; ++k) vx[vu][k].to_f32(vv[k]);
-#pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            u32x2 w, wl;
-            w[0] = pack2_bf16(vv[0][e], vv[1][e]);
-            w[1] = pack2_bf16(vv[2][e], vv[3][e]);
-            float lo[4];
-#pragma unroll
-            for (int k = 0; k < 4; ++k) lo[k] = vv[k][e] - bf16_bits_to_f32(f32_to_bf16_bits(vv[k][e]));
-            wl[0] = pack2_bf16(lo[0], lo[1]);
-            wl[1] = pack2_bf16(lo[2], lo[3]);
-            *(u32x2*)(vt_hi + Cfg::VL::off(dc * 8 + e, sg)) = w;
-            *(u32x2*)(vt_lo + Cfg::VL::off(dc * 8 + e, sg)) = wl;
+        for (int k = 0; k < 4; ++k) {   // slot sg * 4 + k, dims dc * 8 .. dc * 8 + 7
+          const int o = (sg * 4 + k) * VRS + dc * 8;
+          if constexpr (!X3) {
+            *(u32x4*)(v_hi + o) = vx[vu][k].w;
+          } else {                      // fp32: bf16 hi and lo planes
+            float vv[8];
+            vx[vu][k].to_f32(vv);
+            u32x4 hi, lo;
+            split_bf16x8(vv, hi, lo);
+            *(u32x4*)(v_hi + o) = hi;
+            *(u32x4*)(v_lo + o) = lo;
           }
         }
       }
@@ -255,8 +247,8 @@ __global__ __launch_bounds__(NW * 64 + 256, 1) void gather_kernel(GatherArgs a) 
     const int s0 = b * 64;
     const uint16_t* kr_hi = kbuf(b & 1);
     const uint16_t* kr_lo = kr_hi + 64 * KSTR;
-    const uint16_t* vt_hi = vbuf(b & 1);
-    const uint16_t* vt_lo = vt_hi + D * VSTR;
+    const uint16_t* v_hi = vbuf(b & 1);
+    const uint16_t* v_lo = v_hi + 64 * VRS;
     // ---- S^T = K_rot . Q_rot^T for 64 slots x this wave's 16 rows ----
     floatx4 sacc[4];
 #pragma unroll
@@ -341,17 +333,20 @@ __global__ __launch_bounds__(NW * 64 + 256, 1) void gather_kernel(GatherArgs a) 
       else pb = pack_bf16x8(pv);
 #pragma unroll
       for (int db = 0; db < DB; ++db) {
-        const int row = db * 16 + (lane & 15);
-        const int c0 = sb0 * 16 + 4 * (lane >> 4), c1 = sb1 * 16 + 4 * (lane >> 4);
-        const int o0 = Cfg::VL::off(row, c0 >> 2), o1 = Cfg::VL::off(row, c1 >> 2);
-        const u32x2 a0 = *(const u32x2*)(vt_hi + o0);
-        const u32x2 a1 = *(const u32x2*)(vt_hi + o1);
+        // V^T operand (dims db*16 + lane%16, slots {sb0, sb1}*16 + 4*(lane/16) + 0..3) by
+        // transposing reads of row-major V: in each 16-lane group, lane L addresses slot
+        // base + L/4, dims db*16 + 4*(L%4) .. +3, and receives dim db*16 + L of slots base .. base+3
+        const int L = lane & 15;
+        const int o0 = (sb0 * 16 + 4 * (lane >> 4) + (L >> 2)) * VRS + db * 16 + 4 * (L & 3);
+        const int o1 = o0 + 16 * VRS;
+        const u32x2 a0 = tr_read16x4(v_hi + o0);
+        const u32x2 a1 = tr_read16x4(v_hi + o1);
         const u32x4 va = u32x4{a0[0], a0[1], a1[0], a1[1]};
         if constexpr (DT == DT_F16) {
           oacc[db] = mfma16_f16(va, pb, oacc[db]);
         } else if constexpr (X3) {
-          const u32x2 b0 = *(const u32x2*)(vt_lo + o0);
-          const u32x2 b1 = *(const u32x2*)(vt_lo + o1);
+          const u32x2 b0 = tr_read16x4(v_lo + o0);
+          const u32x2 b1 = tr_read16x4(v_lo + o1);
           const u32x4 vl = u32x4{b0[0], b0[1], b1[0], b1[1]};
           oacc[db] = mfma16(vl, pb, oacc[db]);
           oacc[db] = mfma16(va, pbl, oacc[db]);
@@ -403,7 +398,7 @@ static hipError_t launch_gather_t(const GatherArgs& a, hipStream_t st) {
 
 size_t gather_lds_bytes(int dtype, int D, int k_max) {
   const size_t halves = dtype == DT_F32 ? 2 : 1;
-  const size_t fixed = 2 * halves * ((size_t)64 * (D + 8) * 2 + (size_t)D * VtLayout<64, false>::STR * 2);
+  const size_t fixed = 2 * halves * ((size_t)64 * (D + 8) * 2 + (size_t)64 * (D + 16) * 2);
   return fixed + (size_t)((k_max + 63) / 64) * 64 * 4;
 }
 
