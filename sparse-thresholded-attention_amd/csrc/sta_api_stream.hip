@@ -31,9 +31,9 @@ StreamLayout stream_layout_of(const sta_pqstream_args* a) {
   L.stride = ((int64_t)a->N + 15) / 16 * 16;
   size_t off = 0;
   L.qfrag_off = off;
-  off = align256(off + (size_t)a->H * L.q_rows_pad * a->D * 4);
+  off = align256(off + frag_region_bytes(a->H, L.q_rows_pad, a->D));
   L.kfrag_off = off;
-  off = align256(off + (size_t)a->Hkv * L.k_rows_pad * a->D * 4);
+  off = align256(off + frag_region_bytes(a->Hkv, L.k_rows_pad, a->D));
   L.bits_off = off;
   off = align256(off + (size_t)a->H * L.nt * L.stride * 4);
   L.ktil_off = off;
@@ -110,6 +110,8 @@ int sta_pqstream_attention(const sta_pqstream_args* a, void* stream) {
   ScoreArgs sa{};
   sa.qfrag = qfrag;
   sa.kfrag = kfrag;
+  sa.qnorm = frag_norms(qfrag, a->H, L.q_rows_pad, a->D);
+  sa.knorm_max = frag_norm_max(kfrag, a->Hkv, L.k_rows_pad, a->D);
   sa.H = a->H;
   sa.Hkv = a->Hkv;
   sa.N = a->N;

@@ -233,6 +233,19 @@ __device__ __forceinline__ void fast_sincos(float x, float& s, float& c) {
   c = __builtin_amdgcn_cosf(t);
 }
 
+// 16 bytes per lane from global memory straight into LDS, lane l's bytes at lds_base + 16 l
+// (global_load_lds_dwordx4; lds_base is wave-uniform and goes to M0).  Issued through inline
+// assembly so that the compiler does not track it as an LDS write: its own wait insertion would
+// otherwise drain every copy in flight (s_waitcnt vmcnt(0)) in front of the next LDS read and
+// serialise a multi-buffered copy pipeline.  Callers order the copies themselves with explicit
+// s_waitcnt vmcnt and barriers.
+__device__ __forceinline__ void copy16_to_lds(const void* gsrc, uint32_t lds_base) {
+  asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(gsrc), "{m0}"(lds_base) : "memory");
+}
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(size_t)(const __attribute__((address_space(3))) void*)p;
+}
+
 // xor-butterfly helpers over a 64-lane wavefront
 __device__ __forceinline__ float wave_shfl_xor(float v, int m) { return __shfl_xor(v, m, 64); }
 __device__ __forceinline__ int wave_shfl_xor(int v, int m) { return __shfl_xor(v, m, 64); }

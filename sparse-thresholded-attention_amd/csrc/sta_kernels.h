@@ -6,9 +6,24 @@
 
 namespace sta {
 
+// Workspace region of the selection-geometry fragments of `heads` x `rows_pad` rows: the
+// fragments (hi/lo bf16, 4 bytes per element), then per row (||hi||, ||lo||), then per head the
+// maxima of those two norms over its rows.  The RoPE pre-kernel writes all three.
+inline size_t frag_region_bytes(int heads, int rows_pad, int D) {
+  return (size_t)heads * rows_pad * D * 4 + (size_t)heads * rows_pad * 8 + (size_t)heads * 8;
+}
+inline float2* frag_norms(const u32x4* frag, int heads, int rows_pad, int D) {
+  return (float2*)((char*)frag + (size_t)heads * rows_pad * D * 4);
+}
+inline float2* frag_norm_max(const u32x4* frag, int heads, int rows_pad, int D) {
+  return frag_norms(frag, heads, rows_pad, D) + (size_t)heads * rows_pad;
+}
+
 struct ScoreArgs {
   const u32x4* qfrag;     // selection-geometry Q fragments (hi/lo), rows padded to nt*tile
   const u32x4* kfrag;     // selection-geometry K fragments (hi/lo), rows padded to k_rows_pad
+  const float2* qnorm;    // (H, q_rows_pad) (||q_hi||, ||q_lo||) of every fragment row
+  const float2* knorm_max;// (Hkv,) maxima of (||k_hi||, ||k_lo||) over the head's rows
   int H, Hkv, N, nt;
   int q_rows_pad, k_rows_pad;
   int q_pos_base;
@@ -20,6 +35,8 @@ struct ScoreArgs {
   float* wvotes;          // per-query variant: (H, nt, votes_stride) margin / expmass votes
   float* row_max;         // (H, N) or null
   int32_t* row_counts;    // (H, N) or null
+  int ib;                 // set by the launcher: block-index bits of the screened pass 1, 0 = off
+  int exact_pass1;        // 1: always run the three-product pass 1 sweep
 };
 
 struct SelectArgs {

@@ -15,6 +15,9 @@
 #include "sta_device.h"
 #include "sta_kernels.h"
 
+#include <float.h>
+#include <stdlib.h>
+
 #include <type_traits>
 
 namespace sta {
@@ -25,14 +28,15 @@ namespace sta {
 // c, s  = fl(cos(angle) * rope_scale), fl(sin(angle) * rope_scale)   (exact_2.py:80-81)
 // r1 = fl(fl(x1*c) - fl(x2*s)), r2 = fl(fl(x2*c) + fl(x1*s))   (exact_2.py:82-83)
 // Rows >= N (tile padding, and the zero "phantom" keys the reference's masked loads produce
-// when q_pos_base > 0) are written as zeros.
+// when q_pos_base > 0) are written as zeros.  Each row's (||hi||, ||lo||) goes to `norms`: the
+// screened pass 1 of the score kernel bounds its single-product error with them.
 // ------------------------------------------------------------------------------------------
 template <int DT, int D>
 __global__ __launch_bounds__(256) void rope_frag_kernel(const void* __restrict__ x, int64_t head_stride,
                                                         int64_t tok_stride, int heads, int N, int rows_pad,
                                                         int pos_base, float pos_scale, float rope_scale,
                                                         const float* __restrict__ inv_freq,
-                                                        u32x4* __restrict__ frag) {
+                                                        u32x4* __restrict__ frag, float2* __restrict__ norms) {
 #pragma clang fp contract(off)
   constexpr int C = D / 8;
   const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
@@ -77,6 +81,58 @@ __global__ __launch_bounds__(256) void rope_frag_kernel(const void* __restrict__
   const int64_t unit = (((int64_t)head * (rows_pad >> 5) + rb) * (D / 16) + s) * 2 * 64 + lr + 32 * g;
   frag[unit] = hi;
   frag[unit + 64] = lo;
+  // squared norms of the row's hi and lo parts: this thread's 8 elements, then the C threads of
+  // the row (consecutive lanes of one wave; a row's threads all pass or all fail the bound check)
+  float sh = 0.0f, sl = 0.0f;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const float h0 = __uint_as_float(hi[e] << 16), h1 = __uint_as_float(hi[e] & 0xffff0000u);
+    const float l0 = __uint_as_float(lo[e] << 16), l1 = __uint_as_float(lo[e] & 0xffff0000u);
+    sh = fmaf(h0, h0, sh);
+    sh = fmaf(h1, h1, sh);
+    sl = fmaf(l0, l0, sl);
+    sl = fmaf(l1, l1, sl);
+  }
+#pragma unroll
+  for (int o = 1; o < C; o <<= 1) {
+    sh += __shfl_xor(sh, o, 64);
+    sl += __shfl_xor(sl, o, 64);
+  }
+  if (c == 0) norms[(int64_t)head * rows_pad + row] = make_float2(sqrtf(sh), sqrtf(sl));
+}
+
+// per head: the maxima of (||hi||, ||lo||) over its rows_pad rows (rows_pad even); 1024 threads
+// read two rows per 16-byte load, several loads in flight per thread
+__global__ __launch_bounds__(1024) void norm_max_kernel(const float2* __restrict__ norms, int rows_pad,
+                                                        float2* __restrict__ out) {
+  __shared__ float red[2][16];
+  const int head = blockIdx.x, tid = threadIdx.x;
+  const float4* p = (const float4*)(norms + (int64_t)head * rows_pad);
+  const int n4 = rows_pad / 2;
+  float mh = 0.0f, ml = 0.0f;
+#pragma unroll 4
+  for (int r = tid; r < n4; r += 1024) {
+    const float4 v = p[r];
+    mh = fmaxf(mh, fmaxf(v.x, v.z));
+    ml = fmaxf(ml, fmaxf(v.y, v.w));
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    mh = fmaxf(mh, __shfl_xor(mh, o, 64));
+    ml = fmaxf(ml, __shfl_xor(ml, o, 64));
+  }
+  if ((tid & 63) == 0) { red[0][tid >> 6] = mh; red[1][tid >> 6] = ml; }
+  __syncthreads();
+  if (tid < 64) {
+    mh = tid < 16 ? red[0][tid] : 0.0f;
+    ml = tid < 16 ? red[1][tid] : 0.0f;
+#pragma unroll
+    for (int o = 8; o >= 1; o >>= 1) {
+      mh = fmaxf(mh, __shfl_xor(mh, o, 64));
+      ml = fmaxf(ml, __shfl_xor(ml, o, 64));
+    }
+    if (tid == 0) out[head] = make_float2(mh, ml);
+  }
 }
 
 // ------------------------------------------------------------------------------------------
@@ -140,6 +196,10 @@ __global__ __launch_bounds__(256, 1) void score_kernel(ScoreArgs a) {
 
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
+  // +inf hidden from the optimiser: med3(x, y, pinf) = max(x, y) stays one v_med3_f32, where a
+  // literal +inf is rewritten into a max with two canonicalisations
+  float pinf = INFINITY;
+  asm volatile("" : "+s"(pinf));
   const int rows_total = a.nt * T;               // == q_rows_pad
   const int ngroups = (rows_total + WG_ROWS - 1) / WG_ROWS;
   int h, g;
@@ -199,7 +259,7 @@ __global__ __launch_bounds__(256, 1) void score_kernel(ScoreArgs a) {
 #pragma unroll
     for (int e = 0; e < LOADS; ++e) {
       const int u = (e * NW + wave) * 64;
-      __builtin_amdgcn_global_load_lds(STA_GLOBAL(src + u), STA_LDS(dst + u), 16, 0, 0);
+      copy16_to_lds(src + u, lds_addr(dst + u));
     }
   };
   // wait until at most n chunks' copies of this wave are in flight.  Vector memory operations
@@ -280,7 +340,7 @@ __global__ __launch_bounds__(256, 1) void score_kernel(ScoreArgs a) {
 #pragma unroll
   for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
-    for (int i = 0; i < 16; ++i) { mx[rb][i] = -INFINITY; ref[rb][i] = 0.0f; rc[rb][i] = 0; }
+    for (int i = 0; i < 16; ++i) { ref[rb][i] = 0.0f; rc[rb][i] = 0; }
 
   // 32 keys x this wave's rows, one k step: hi.hi + hi.lo + lo.hi, small terms first
   auto mfma3 = [&](u32x4 bh, u32x4 bl, int s, floatx16* acc) {
@@ -327,7 +387,7 @@ __global__ __launch_bounds__(256, 1) void score_kernel(ScoreArgs a) {
   auto epi = [&](auto passc, float v, int rb, int i, int* cnt, uint32_t* bm, float* w) {
     constexpr int pass = decltype(passc)::value;
     if constexpr (pass == 0) {
-      mx[rb][i] = __builtin_amdgcn_fmed3f(v, mx[rb][i], INFINITY);   // max; scores are finite
+      mx[rb][i] = __builtin_amdgcn_fmed3f(v, mx[rb][i], pinf);   // max; scores are finite
     } else {
       const int keep = v >= mx[rb][i];
       if constexpr (PQ == 0) cnt[rb] += keep;
@@ -378,10 +438,312 @@ __global__ __launch_bounds__(256, 1) void score_kernel(ScoreArgs a) {
     if constexpr (pass == 1) store_key(key0 + (lane & 31), false, cnt, bm, w);
   };
 
+  // ---- screened pass 1 ----------------------------------------------------------------------
+  // The sweep computes only s1 = hi(q).hi(k), one product instead of three.  With x = hi + lo per
+  // operand, the three-product score differs from s1 by the cross terms, so by Cauchy-Schwarz
+  //   |x(q).x(k) - s1| <= ||q_hi|| ||k_lo|| + ||q_lo|| ||k_hi|| + ||q_lo|| ||k_lo|| + (rounding),
+  // and with E that bound (maximised over the head's keys), only keys whose s1 lies within 2 E of
+  // the row's largest s1 can hold the row's exact maximum.  Each accumulator slot (one row, the
+  // keys of one lane column) keeps its three largest s1 values with the 32-key block index packed
+  // into the low `ib` mantissa bits (a relative change below 2^(ib-23), added to E).  After the
+  // sweep the candidates -- slot values within 2 E of the row maximum -- are evaluated exactly as
+  // fp32 dot products of the (hi + lo) operands, and the row maximum is their maximum.  A slot
+  // whose third value is a candidate may hide a fourth, and a row may collect more than CMAX
+  // candidates: then the whole workgroup runs the three-product sweep instead (a few percent of
+  // workgroups on Gaussian inputs; always on inputs with many tied scores).
+  constexpr int CMAX = 8;                        // candidates evaluated per row
+  constexpr int LOADS_H = LOADS / 2;             // 1 KB copies per wave per chunk, hi halves only
+  static_assert(LOADS_H * NW * 2 * 64 == CHUNK_UNITS, "hi-half copies");
+  auto issue_hi = [&](int c, u32x4* dst) {
+    const u32x4* src = kbase + (int64_t)c * CHUNK_UNITS + lane;
+#pragma unroll
+    for (int e = 0; e < LOADS_H; ++e) {
+      const int u = 2 * (e * NW + wave) * 64;   // the hi unit block of (32-key block, k step) e NW + wave
+      copy16_to_lds(src + u, lds_addr(dst + u));
+    }
+  };
+  auto wait_hi = [&](int n) {
+    constexpr int E = (7 << 4) | (15 << 8);
+    constexpr int L1 = LOADS_H, L2 = 2 * LOADS_H;
+    if (n <= 0) __builtin_amdgcn_s_waitcnt(E);
+    else if (n == 1) __builtin_amdgcn_s_waitcnt(E | (L1 & 15) | ((L1 >> 4) << 14));
+    else __builtin_amdgcn_s_waitcnt(E | (L2 & 15) | ((L2 >> 4) << 14));
+  };
+  float t1[RB][16], t2[RB][16], t3[RB][16];
+  const uint32_t blk_mask = (1u << a.ib) - 1u;
+  // fold one score into its slot's top three (v finite; masked scores arrive as -FLT_MAX); blk
+  // sits in a VGPR so that the packing is one v_and_or_b32 with the mask in an SGPR
+  auto sepi = [&](float v, int rb, int i, uint32_t blk) {
+    const float p = __uint_as_float((__float_as_uint(v) & ~blk_mask) | blk);
+    t3[rb][i] = __builtin_amdgcn_fmed3f(t2[rb][i], t3[rb][i], p);
+    t2[rb][i] = __builtin_amdgcn_fmed3f(t1[rb][i], t2[rb][i], p);
+    t1[rb][i] = __builtin_amdgcn_fmed3f(t1[rb][i], p, pinf);
+  };
+  auto vgpr = [](uint32_t x) {
+    asm("" : "+v"(x));
+    return x;
+  };
+  auto s_schedule = [&](auto valuc) {
+    constexpr int V = decltype(valuc)::value;
+    __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);        // reads of steps 0 and 1
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+#pragma unroll
+      for (int m = 0; m < RB; ++m) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);    // MFMA
+        if (m == 0 && s >= 1 && s + 1 < S) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // step s + 1
+        if constexpr (V > 0) __builtin_amdgcn_sched_group_barrier(0x002, V, 0);
+      }
+    }
+  };
+  // hi.hi products of block sb into accN; with HAS_PREV the previous (unmasked) block accO of
+  // 32-key block index blkO is folded into the top threes between the k steps
+  auto s_block = [&](auto prevc, const u32x4* buf, int sb, floatx16* accN, const floatx16* accO, uint32_t blkO) {
+    constexpr bool HAS_PREV = decltype(prevc)::value;
+    const uint32_t bv = HAS_PREV ? vgpr(blkO) : 0u;
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) accN[rb] = floatx16{};
+    u32x4 bh = ldb(buf, sb, 0, 0);
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+      u32x4 nh = bh;
+      if (s + 1 < S) nh = ldb(buf, sb, s + 1, 0);
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb) accN[rb] = mfma32(qhi[rb][s], bh, accN[rb]);
+      bh = nh;
+      if constexpr (HAS_PREV) {
+#pragma unroll
+        for (int e = 0; e < PER; ++e) {
+          const int idx = s * PER + e;
+          sepi(accO[idx / 16][idx % 16], idx / 16, idx % 16, bv);
+        }
+      }
+    }
+    s_schedule(std::integral_constant<int, HAS_PREV ? 4 * PER / RB : 0>{});
+  };
+  auto s_flush = [&](const floatx16* acc, uint32_t blk) {
+    const uint32_t bv = vgpr(blk);
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) sepi(acc[rb][i], rb, i, bv);
+  };
+  // returns true when the workgroup has to run the three-product sweep; otherwise mx holds every
+  // row's exact raw maximum
+  auto run_screened = [&]() -> bool {
+    constexpr std::integral_constant<bool, true> kPrev{};
+    const float lowest = __uint_as_float(0xff7fffffu & ~blk_mask);   // -FLT_MAX, block 0
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) { t1[rb][i] = lowest; t2[rb][i] = lowest; t3[rb][i] = lowest; }
+    // nothing the compiler tracks is in flight past this point: its own waits then stay out of
+    // the sweep, whose copies it does not see
+    __builtin_amdgcn_s_waitcnt(0);
+    for (int c = 0; c < NBUF - 1; ++c) issue_hi(min(c, nchunks - 1), lds[c]);
+    wait_hi(NBUF - 2);
+    __syncthreads();
+    floatx16 accA[RB], accB[RB];
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) accB[rb][i] = lowest;
+    // one loop per kind of chunk, each with a single path through its body (loop-carried top
+    // threes then keep their registers instead of being copied at every join)
+    // Every step issues one chunk's copies: past the last chunk it copies the last chunk again
+    // into the buffer no later step reads, which keeps the body branch-free and the waits fixed
+    // (the stray copies are drained before the buffers are reused).
+    auto step_begin = [&](int c) {
+      issue_hi(min(c + NBUF - 1, nchunks - 1), lds[(c + NBUF - 1) % NBUF]);
+    };
+    auto step_end = [&](int c) {   // chunk c + 1's copies have landed, every wave is done with c
+      (void)c;
+      wait_hi(NBUF - 2);
+      __syncthreads();
+    };
+    int c = 0;
+    if (active) {
+      for (; c < nfull; ++c) {
+        step_begin(c);
+        const u32x4* buf = lds[c % NBUF];
+        const uint32_t blk0 = (uint32_t)(c * SBC);
+        // accB: the previous chunk's second block (before the first chunk: `lowest`, a no-op)
+        s_block(kPrev, buf, 0, accA, accB, c > 0 ? blk0 - 1 : 0u);
+        s_block(kPrev, buf, 1, accB, accA, blk0);
+        step_end(c);
+      }
+      s_flush(accB, nfull > 0 ? (uint32_t)(nfull * SBC - 1) : 0u);
+      for (; c < nchunks; ++c) {
+        step_begin(c);
+        const u32x4* buf = lds[c % NBUF];
+        for (int sb = 0; sb < SBC; ++sb) {
+          const int key0 = c * CK + sb * 32;
+          if (key0 >= hi_w) break;
+          floatx16 acc[RB];
+#pragma unroll
+          for (int rb = 0; rb < RB; ++rb) acc[rb] = floatx16{};
+#pragma unroll
+          for (int s = 0; s < S; ++s) {
+            const u32x4 bh = ldb(buf, sb, s, 0);
+#pragma unroll
+            for (int rb = 0; rb < RB; ++rb) acc[rb] = mfma32(qhi[rb][s], bh, acc[rb]);
+          }
+          // key <= qpos0 + row, with the slot's row split into a lane part and a constant
+          const int dk = key0 + (lane & 31) - qpos0 - (lane >> 5) * 4;
+          const bool diag = key0 + 31 > qpos0;
+          const uint32_t bv = vgpr((uint32_t)(key0 >> 5));
+#pragma unroll
+          for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+              const bool causal = !diag || dk <= rb * 32 + (i >> 2) * 8 + (i & 3);   // exact_2.py:101
+              sepi(causal ? acc[rb][i] : -FLT_MAX, rb, i, bv);
+            }
+        }
+        step_end(c);
+      }
+    } else {
+      for (; c < nchunks; ++c) {
+        step_begin(c);
+        step_end(c);
+      }
+    }
+    wait_hi(0);        // the stray copies past the last chunk
+    __syncthreads();
+
+    // ---- candidates: per row, slot values within 2 E of the row's largest s1 ----
+    int* cnt = (int*)&lds[0][0] + wave * (64 + 64 * CMAX);   // this wave's 64 row counters
+    int* ckeys = cnt + 64;                                     // 64 rows x CMAX candidate keys
+    cnt[lane] = 0;
+    const float2 kn = a.knorm_max[kvh];
+    // 2^-14 covers the fp32 accumulation of s1 and of the exact dots; 2^(ib-23) the packing
+    const float gam = 0x1p-14f + __uint_as_float((uint32_t)(127 + a.ib - 23) << 23);
+    bool amb = false;
+    __syncthreads();
+    if (active) {
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          float v = t1[rb][i];
+#pragma unroll
+          for (int o = 1; o < 32; o <<= 1) v = __builtin_amdgcn_fmed3f(v, __shfl_xor(v, o, 64), INFINITY);
+          const int row = rb * 32 + (i >> 2) * 8 + (lane >> 5) * 4 + (i & 3);
+          if (wrow0 + row >= a.N) continue;   // padded rows never vote: their maximum is unused
+          const float2 qn = a.qnorm[(int64_t)h * a.q_rows_pad + wrow0 + row];
+          const float E = 1.001f * (qn.x * kn.y + qn.y * kn.x + qn.y * kn.y + gam * qn.x * kn.x) +
+                          0x1p-20f * fabsf(v);
+          const float thr = v - 2.0f * E;
+          amb |= !(thr > -1e38f) || t3[rb][i] >= thr;
+          const uint32_t col = (uint32_t)(lane & 31);
+          const float tv[3] = {t1[rb][i], t2[rb][i], t3[rb][i]};
+#pragma unroll
+          for (int k3 = 0; k3 < 3; ++k3) {
+            if (tv[k3] >= thr) {
+              const int sl = atomicAdd(&cnt[row], 1);
+              if (sl < CMAX) ckeys[row * CMAX + sl] = (int)(((__float_as_uint(tv[k3]) & blk_mask) << 5) | col);
+            }
+          }
+        }
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb) amb |= cnt[rb * 32 + (lane & 31)] > CMAX;
+    }
+    if (__syncthreads_or(amb)) return true;
+
+    // ---- exact dots of the candidates: lanes r and r + 32 own row rb*32 + r, half the dims each ----
+    if (active) {
+      float best[RB];
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb) {
+        best[rb] = 0.0f;
+        if (wrow0 + 32 * rb >= a.N) continue;   // no row of this block votes
+        const int R = rb * 32 + (lane & 31);
+        const int n = cnt[R];
+        int nmax = n;
+#pragma unroll
+        for (int o = 1; o < 32; o <<= 1) nmax = max(nmax, __shfl_xor(nmax, o, 64));
+        // this lane's Q units of row R, reloaded (the AGPR copies feed only the MFMAs)
+        u32x4 qh[S], ql[S];
+        {
+          const int64_t u0 = (((int64_t)h * (a.q_rows_pad >> 5) + wrow0 / 32 + rb) * S) * 128 + lane;
+#pragma unroll
+          for (int s = 0; s < S; ++s) { qh[s] = a.qfrag[u0 + s * 128]; ql[s] = a.qfrag[u0 + s * 128 + 64]; }
+        }
+        float bv = -INFINITY;
+#pragma unroll 1
+        for (int j = 0; j < nmax; ++j) {
+          const int key = j < n ? ckeys[R * CMAX + j] : 0;
+          const u32x4* kp = kbase + (int64_t)(key >> 5) * S * 128 + (key & 31) + 32 * (lane >> 5);
+          u32x4 kh[S], kl[S];
+#pragma unroll
+          for (int s = 0; s < S; ++s) { kh[s] = kp[s * 128]; kl[s] = kp[s * 128 + 64]; }
+          float acc = 0.0f;
+#pragma unroll
+          for (int s = 0; s < S; ++s) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const float x0 = __uint_as_float(qh[s][e] << 16) + __uint_as_float(ql[s][e] << 16);
+              const float x1 = __uint_as_float(qh[s][e] & 0xffff0000u) + __uint_as_float(ql[s][e] & 0xffff0000u);
+              const float y0 = __uint_as_float(kh[s][e] << 16) + __uint_as_float(kl[s][e] << 16);
+              const float y1 = __uint_as_float(kh[s][e] & 0xffff0000u) + __uint_as_float(kl[s][e] & 0xffff0000u);
+              acc = fmaf(x0, y0, acc);
+              acc = fmaf(x1, y1, acc);
+            }
+          }
+          const float tot = acc + __shfl_xor(acc, 32, 64);
+          if (j < n) bv = fmaxf(bv, tot);
+        }
+        best[rb] = bv;
+      }
+      // every slot takes its row's exact maximum from the row's owner lane
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) mx[rb][i] = __shfl(best[rb], (i >> 2) * 8 + (lane >> 5) * 4 + (i & 3), 64);
+    }
+    __syncthreads();   // the candidate lists are read before the next sweep's copies land
+    return false;
+  };
+
+  // row max over the 32 lanes holding a row's keys (mx: the raw dot's running max per row slot),
+  // then the keep threshold x0 on the raw dot, and the weighted-vote origins
+  auto finish1 = [&]() {
+    if (active) {
+      // complete the row max over the 32 lanes holding a row's keys, then the threshold
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          float v = mx[rb][i];
+          v = fmaxf(v, __shfl_xor(v, 1, 64));
+          v = fmaxf(v, __shfl_xor(v, 2, 64));
+          v = fmaxf(v, __shfl_xor(v, 4, 64));
+          v = fmaxf(v, __shfl_xor(v, 8, 64));
+          v = fmaxf(v, __shfl_xor(v, 16, 64));
+          const float m = v * a.sm_scale;   // fl(max * c) == max of fl(s * c) for c > 0
+          const int row = rb * 32 + (i >> 2) * 8 + (lane >> 5) * 4 + (i & 3);
+          const bool ok = wrow0 + row < a.N;   // padded rows never vote (exact_2.py:121)
+          mx[rb][i] = ok ? min_arg_for(m - tau, a.sm_scale) : INFINITY;
+          if constexpr (PQ == 2) ref[rb][i] = m - tau;   // perquery.py:210
+          if constexpr (PQ == 3) ref[rb][i] = m;         // perquery.py:215
+          if (a.row_max && (lane & 31) == 0 && ok) a.row_max[(int64_t)h * a.N + wrow0 + row] = m;
+        }
+    }
+  };
+
   auto run_pass = [&](auto passc) {
     constexpr int pass = decltype(passc)::value;
     constexpr std::integral_constant<bool, true> kPrev{};
     constexpr std::integral_constant<bool, false> kNoPrev{};
+    if constexpr (pass == 0) {
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) mx[rb][i] = -INFINITY;
+    }
+    // nothing the compiler tracks is in flight past this point: its own waits then stay out of
+    // the sweep, whose copies it does not see
+    __builtin_amdgcn_s_waitcnt(0);
     for (int c = 0; c < NBUF - 1 && c < nchunks; ++c) issue(c, lds[c]);
     wait_copies(min(nchunks, NBUF - 1) - 1);
     __syncthreads();
@@ -410,6 +772,7 @@ __global__ __launch_bounds__(256, 1) void score_kernel(ScoreArgs a) {
             for (int rb = 0; rb < RB; ++rb) acc[rb] = floatx16{};
             mfma_block(buf, sb, acc);
             const int key = key0 + (lane & 31);
+            const int dk = key - qpos0 - (lane >> 5) * 4;   // causal: dk <= the slot's row constant
             const bool diag = key0 + 31 > qpos0;
             int cnt[RB] = {};
             uint32_t bm[RB] = {};
@@ -418,8 +781,7 @@ __global__ __launch_bounds__(256, 1) void score_kernel(ScoreArgs a) {
             for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
               for (int i = 0; i < 16; ++i) {
-                const int row = rb * 32 + (i >> 2) * 8 + (lane >> 5) * 4 + (i & 3);
-                const bool causal = !diag || key <= qpos0 + row;   // exact_2.py:101, 119
+                const bool causal = !diag || dk <= rb * 32 + (i >> 2) * 8 + (i & 3);   // exact_2.py:101, 119
                 const float v = acc[rb][i];
                 if constexpr (pass == 0) {
                   if (causal && v > mx[rb][i]) mx[rb][i] = v;
@@ -439,31 +801,11 @@ __global__ __launch_bounds__(256, 1) void score_kernel(ScoreArgs a) {
       __syncthreads();
     }
     if (active && pendingB) flush(passc, accB, keyB);
-    if constexpr (pass == 0) {
-      if (active) {
-        // complete the row max over the 32 lanes holding a row's keys, then the threshold
-#pragma unroll
-        for (int rb = 0; rb < RB; ++rb)
-#pragma unroll
-          for (int i = 0; i < 16; ++i) {
-            float v = mx[rb][i];
-            v = fmaxf(v, __shfl_xor(v, 1, 64));
-            v = fmaxf(v, __shfl_xor(v, 2, 64));
-            v = fmaxf(v, __shfl_xor(v, 4, 64));
-            v = fmaxf(v, __shfl_xor(v, 8, 64));
-            v = fmaxf(v, __shfl_xor(v, 16, 64));
-            const float m = v * a.sm_scale;   // fl(max * c) == max of fl(s * c) for c > 0
-            const int row = rb * 32 + (i >> 2) * 8 + (lane >> 5) * 4 + (i & 3);
-            const bool ok = wrow0 + row < a.N;   // padded rows never vote (exact_2.py:121)
-            mx[rb][i] = ok ? min_arg_for(m - tau, a.sm_scale) : INFINITY;
-            if constexpr (PQ == 2) ref[rb][i] = m - tau;   // perquery.py:210
-            if constexpr (PQ == 3) ref[rb][i] = m;         // perquery.py:215
-            if (a.row_max && (lane & 31) == 0 && ok) a.row_max[(int64_t)h * a.N + wrow0 + row] = m;
-          }
-      }
-    }
+    if constexpr (pass == 0) finish1();
   };
-  run_pass(std::integral_constant<int, 0>{});
+  // pass 1: the screened sweep, or the three-product sweep when screening is off or inconclusive
+  if (a.ib == 0 || a.exact_pass1 || run_screened()) run_pass(std::integral_constant<int, 0>{});
+  else finish1();
   run_pass(std::integral_constant<int, 1>{});
 
   if constexpr (RC) {
@@ -494,8 +836,13 @@ static hipError_t launch_rope_frag_t(const void* x, int64_t hs, int64_t ts, int 
                                      u32x4* frag, hipStream_t st) {
   const int64_t total = (int64_t)heads * rows_pad * (D / 8);
   const int64_t blocks = (total + 255) / 256;
+  float2* norms = frag_norms(frag, heads, rows_pad, D);
   hipLaunchKernelGGL((rope_frag_kernel<DT, D>), dim3((unsigned)blocks), dim3(256), 0, st, x, hs, ts, heads, N,
-                     rows_pad, pos_base, pos_scale, rope_scale, inv_freq, frag);
+                     rows_pad, pos_base, pos_scale, rope_scale, inv_freq, frag, norms);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(norm_max_kernel, dim3(heads), dim3(1024), 0, st, (const float2*)norms, rows_pad,
+                     frag_norm_max(frag, heads, rows_pad, D));
   return hipGetLastError();
 }
 
@@ -510,9 +857,23 @@ hipError_t launch_rope_frag(int dtype, int D, const void* x, int64_t hs, int64_t
   return hipErrorInvalidValue;
 }
 
+// STA_EXACT_PASS1=1 in the environment (read at every launch) makes every workgroup run the
+// three-product pass 1 sweep, for comparisons against the screened sweep
+static int exact_pass1_forced() {
+  const char* e = getenv("STA_EXACT_PASS1");
+  return e && e[0] == '1' ? 1 : 0;
+}
+
 template <int D, int T, bool RC, int PQ>
-static hipError_t launch_score_t(const ScoreArgs& a, hipStream_t st) {
+static hipError_t launch_score_t(const ScoreArgs& a0, hipStream_t st) {
   constexpr int RB = 2;   // 64 query rows per wave (128-row waves spill and balance worse)
+  ScoreArgs a = a0;
+  // block indices of the screened pass 1 need ib bits; its packing error 2^(ib-23) stays small
+  // for ib <= 13 (up to 262144 keys), longer rows take the three-product sweep
+  int ib = 1;
+  while ((1 << ib) < a.k_rows_pad / 32) ++ib;
+  a.ib = (ib <= 13 && a.qnorm && a.knorm_max) ? ib : 0;
+  a.exact_pass1 = exact_pass1_forced();
   const int ngroups = (a.nt * T + 128 * RB - 1) / (128 * RB);   // four waves of 32 RB rows
   hipLaunchKernelGGL((score_kernel<D, T, RC, PQ, RB>), dim3(a.H * ngroups), dim3(256), 0, st, a);
   return hipGetLastError();

@@ -1,0 +1,115 @@
+"""GPU: the screened pass 1 of the score kernel against the three-product sweep and the oracle.
+
+The score kernel's pass 1 (exact row max, shared_selection_triton_exact_2.py:87-103) normally
+sweeps with one bf16 product per score and evaluates exactly only the keys that can hold a row's
+maximum; STA_EXACT_PASS1=1 forces the three-product sweep.  Both must give the oracle's row max
+(within 1e-4) and votes that differ from the oracle's only inside the 1e-3 band.  Inputs with
+tied scores make the screen inconclusive, which sends the workgroup to the three-product sweep:
+those cases check that fallback.
+"""
+import math
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import sta_oracle as orc
+from parity_helpers import BAND, check_votes, np_of
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+
+
+def say(msg):
+    print(f"[case] {msg}", flush=True)
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _need_gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("no HIP device")
+    import _sta_native
+    _sta_native.lib()
+
+
+def _kernel_a(q, k, tau, invf, ps, rs, tile, q_pos_base, exact):
+    import _sta_native as native
+    old = os.environ.pop("STA_EXACT_PASS1", None)
+    try:
+        if exact:
+            os.environ["STA_EXACT_PASS1"] = "1"
+        votes, _, rm = native.select_vote(q, k, tau, invf, ps, rs, 1.0 / math.sqrt(q.shape[-1]), tile,
+                                          q_pos_base)
+        torch.cuda.synchronize()
+    finally:
+        os.environ.pop("STA_EXACT_PASS1", None)
+        if old is not None:
+            os.environ["STA_EXACT_PASS1"] = old
+    return votes.cpu().numpy(), rm.cpu().numpy()
+
+
+def _check_both(q, k, tau, invf, ps, rs, tile, q_pos_base, what):
+    say(what)
+    D = q.shape[-1]
+    qn, dt = np_of(q[0])
+    kn, _ = np_of(k[0])
+    a = orc.select_vote(qn, kn, dt, tau.cpu().numpy(), invf.cpu().numpy(), ps, rs, 1.0 / math.sqrt(D), tile,
+                        q_pos_base, band_eps=BAND, want_band=True)
+    res = {}
+    for exact in (False, True):
+        votes, rm = _kernel_a(q, k, tau, invf.to(DEV), ps, rs, tile, q_pos_base, exact)
+        err = float(np.max(np.abs(rm - a["row_max"])))
+        assert err < 1e-4, f"{what} (exact={exact}): row max differs from the oracle by {err:.3e}"
+        ndiff, nband = check_votes(votes, a["votes"], a["band"])
+        res[exact] = (votes, rm, ndiff)
+        print(f"[result] {what} exact_pass1={exact}: row max err {err:.2e}, vote entries differing "
+              f"{ndiff} (band pairs {nband})", flush=True)
+    # the two sweeps find the same maxima up to the rounding of the dropped lo.lo term
+    d = float(np.max(np.abs(res[False][1] - res[True][1])))
+    assert d < 1e-4, f"{what}: screened and three-product row maxima differ by {d:.3e}"
+    return res
+
+
+@pytest.mark.parametrize("case", [
+    # (H, Hkv, N, D, dtype, tile, q_pos_base, pos_scale)
+    (2, 1, 3000, 128, torch.bfloat16, 64, 0, 0.25),
+    (2, 2, 1000, 64, torch.float32, 32, 0, 1.0),
+    (4, 2, 4133, 128, torch.bfloat16, 64, 37, 1.0 / 3.0),
+    (2, 2, 2049, 128, torch.float16, 32, 0, 0.5),
+])
+def test_screened_pass1_matches_exact_sweep(case):
+    from synthetic import base_inv_freq, planted_inputs
+    H, Hkv, N, D, dt, tile, qpb, ps = case
+    q, k, _ = planted_inputs(3, H, Hkv, N, D, 0.01, dt, DEV)
+    invf = base_inv_freq(D, 10000.0)
+    tau = torch.full((H,), 5.0)
+    _check_both(q, k, tau, invf, ps, 1.0, tile, qpb,
+                f"screened vs exact pass 1: H={H} Hkv={Hkv} N={N} D={D} {dt} tile={tile} q_pos_base={qpb}")
+
+
+def test_screened_pass1_ties_fall_back():
+    """Every key of a head identical (all of a row's scores tie) and some query rows zero: the
+    screen cannot single out a maximum, so those workgroups take the three-product sweep."""
+    from synthetic import base_inv_freq
+    H, N, D = 2, 1500, 128
+    g = torch.Generator("cpu").manual_seed(5)
+    q = torch.randn(1, H, N, D, generator=g)
+    q[:, :, 300:700] = 0.0
+    k = torch.randn(1, H, N, D, generator=g)
+    k[:, 0] = k[:, 0, :1]                      # head 0: one key repeated
+    q, k = q.to(torch.bfloat16).to(DEV), k.to(torch.bfloat16).to(DEV)
+    invf = base_inv_freq(D, 10000.0)
+    tau = torch.full((H,), 5.0)
+    # position-free geometry (pos_scale 0): repeated keys give exactly tied scores
+    _check_both(q, k, tau, invf, 0.0, 1.0, 64, 0, "tied scores: repeated keys, zero query rows")
+
+
+def test_screened_pass1_full_length_config1_head():
+    """config 1's shape and geometry on one head (12288 keys): the screened sweep against the
+    oracle and the three-product sweep."""
+    from synthetic import CONFIGS, planted_inputs
+    c = CONFIGS["c1"]
+    q, k, _ = planted_inputs(0, 1, 1, c.N, c.D, c.frac, c.dtype, DEV)
+    invf, ps, rs = c.geometry()
+    _check_both(q, k, torch.full((1,), c.tau), invf, ps, rs, c.tile, 0, "config 1 shape, one head")
