@@ -6,8 +6,9 @@
  * library never links it and never falls back to it.
  *
  * It follows the reference line by line (all citations are into the reference repository):
- *   oracle_select_vote  <- shared_selection_triton_exact_2.py:50-140   (Kernel A, freq mode)
- *   oracle_build_sets   <- shared_selection_triton_exact_2.py:277-426  (_build_sets, freq mode)
+ *   oracle_select_vote  <- shared_selection_triton_exact_2.py:50-140   (Kernel A, WMODE 0/1/2)
+ *   oracle_build_sets   <- shared_selection_triton_exact_2.py:277-426  (_build_sets, freq /
+ *                          margin / expmass ranking)
  *   oracle_gather_attn  <- shared_selection_triton_exact_2.py:146-225  (Kernel C)
  * The same three functions serve the YaRN and hybrid files, whose kernels are identical and whose
  * entry points differ only in the (inv_freq, pos_scale, rope_scale) triples they pass
@@ -52,7 +53,7 @@ void oracle_rope_rotate(const void* x, int dtype, int rows, int D, const float* 
 }
 
 /* ------------------------------------------------------------------------------------------- */
-/* Kernel A: exact row max (pass 1) + keep/votes (pass 2)       exact_2.py:50-140, freq mode  */
+/* Kernel A: exact row max (pass 1) + keep/votes (pass 2)       exact_2.py:50-140             */
 /* ------------------------------------------------------------------------------------------- */
 /*
  * votes      (H, nt, N) int32, written for every key (0 where no query keeps it)
@@ -63,12 +64,17 @@ void oracle_rope_rotate(const void* x, int dtype, int rows, int D, const float* 
  *                       band_eps of that query's threshold m - tau (the parity tolerance band)
  * band_rows  (H, N)     int32 or NULL: per query, # of its causal keys inside that band
  * keep_bits  (H, N, N)  uint8 or NULL: keep(q, k) for every pair (small shapes only)
+ * wvotes     (H, nt, N) fp32 or NULL, written for wmode 1 / 2 (WMODE, exact_2.py:126-138):
+ *                       wmode 1 (margin):  sum over the tile's keeping rows of fl(s - fl(m - tau))
+ *                       wmode 2 (expmass): sum over the tile's keeping rows of exp(fl(s - m))
+ *                       The reference sums a tile's rows in fp32 in its reduction tree's order;
+ *                       here the sum is accumulated in double and rounded once (a few ulps apart).
  */
 void oracle_select_vote(const void* q, const void* k, int dtype, int H, int Hkv, int N, int D,
                         const float* tau, const float* inv_freq, float pos_scale, float rope_scale,
                         float sm_scale, int tile, int q_pos_base, int32_t* votes,
                         int32_t* row_counts, float* row_max, int32_t* band, int32_t* band_rows,
-                        float band_eps, uint8_t* keep_bits) {
+                        float band_eps, uint8_t* keep_bits, int wmode, float* wvotes) {
   const int T = tile;
   const int nt = (N + T - 1) / T;
   const int group = H / Hkv;
@@ -78,6 +84,7 @@ void oracle_select_vote(const void* q, const void* k, int dtype, int H, int Hkv,
   if (band) memset(band, 0, sizeof(int32_t) * (size_t)H * nt * N);
   if (band_rows) memset(band_rows, 0, sizeof(int32_t) * (size_t)H * N);
   if (keep_bits) memset(keep_bits, 0, (size_t)H * N * N);
+  if (wvotes) memset(wvotes, 0, sizeof(float) * (size_t)H * nt * N);
 
   /* rotated K per kv head (keys >= N are the zero rows the reference's masked loads produce) */
   float* krot = (float*)malloc(sizeof(float) * (size_t)Hkv * kmax_key * D);
@@ -97,12 +104,14 @@ void oracle_select_vote(const void* q, const void* k, int dtype, int H, int Hkv,
   {
     float* qr = (float*)malloc(sizeof(float) * (size_t)T * D);
     float* sc = (float*)malloc(sizeof(float) * (size_t)T * kmax_key);
+    double* wacc = (double*)malloc(sizeof(double) * (size_t)kmax_key);
 #pragma omp for schedule(dynamic, 1)
     for (int ht = 0; ht < H * nt; ++ht) {
       const int h = ht / nt, t = ht % nt;
       const int hk = h / group;
       const int hi = q_pos_base + (t + 1) * T; /* exact_2.py:85 */
       const float tau_h = tau[h];
+      for (int j = 0; j < hi; ++j) wacc[j] = 0.0;
       for (int r = 0; r < T; ++r) {
         const int row = t * T + r;
         if (row >= N) continue;
@@ -138,20 +147,30 @@ void oracle_select_vote(const void* q, const void* k, int dtype, int H, int Hkv,
             /* different rows of one tile touch the same key, but one tile belongs to one thread */
             votes[((size_t)h * nt + t) * N + j] += 1;
             if (keep_bits) keep_bits[((size_t)h * N + row) * N + j] = 1;
+            if (wmode == 1) { /* exact_2.py:129-131: qk - (m - tau) */
+              volatile float c = s - thr;
+              wacc[j] += (double)c;
+            } else if (wmode == 2) { /* exact_2.py:134-136: exp(qk - m) */
+              volatile float dl = s - m;
+              wacc[j] += (double)expf(dl);
+            }
           }
         }
         if (row_counts) row_counts[(size_t)h * N + row] = cnt;
         if (band_rows) band_rows[(size_t)h * N + row] = nband;
       }
+      if (wvotes && wmode > 0)
+        for (int j = 0; j < hi && j < N; ++j) wvotes[((size_t)h * nt + t) * N + j] = (float)wacc[j];
     }
     free(qr);
     free(sc);
+    free(wacc);
   }
   free(krot);
 }
 
 /* ------------------------------------------------------------------------------------------- */
-/* _build_sets (freq mode)                                       exact_2.py:277-426            */
+/* _build_sets                                                   exact_2.py:277-426            */
 /* ------------------------------------------------------------------------------------------- */
 static int cmp_desc_f(const void* a, const void* b) {
   const float x = *(const float*)a, y = *(const float*)b;
@@ -173,12 +192,15 @@ static long budget_of(int p, long usize) {
  *   newpos_q (H,nt,T) fp32; shared_size, kept_size, chosen (H,nt) int32;
  *   orig_overflow, overflow20 (H,nt) uint8; kpct_meas (H,nt) int32.
  * start_pct = max(0, int(round(pct))) is computed by the caller (Python round semantics).
+ * wvotes (H, nt, N) fp32 or NULL: with it the ranking metric is the weighted score with frequency
+ * as an epsilon tiebreak, rank = fl(wvotes + fl(1e-6 * votes)) (exact_2.py:299-302); the union
+ * size and budgets stay frequency-based (exact_2.py:296).  NULL ranks by votes (freq).
  */
 void oracle_build_sets(const int32_t* votes, int H, int nt, int N, float pos_scale, int n_global,
                        int n_local, int start_pct, int T, int k_max, int q_pos_base, int measure,
                        int32_t* idx, float* newpos_k, float* newpos_q, int32_t* shared_size,
                        int32_t* kept_size, int32_t* chosen, uint8_t* orig_overflow,
-                       int32_t* kpct_meas, uint8_t* overflow20) {
+                       int32_t* kpct_meas, uint8_t* overflow20, const float* wvotes) {
   /* pct_steps = [start] + [c for c in (25, 20) if c < start]            (exact_2.py:309-310) */
   int steps[3], nsteps = 0;
   steps[nsteps++] = start_pct;
@@ -195,6 +217,7 @@ void oracle_build_sets(const int32_t* votes, int H, int nt, int N, float pos_sca
 #pragma omp parallel
   {
     float* sv = (float*)malloc(sizeof(float) * (size_t)N);
+    float* rv = (float*)malloc(sizeof(float) * (size_t)N);
     uint8_t* forced = (uint8_t*)malloc((size_t)N);
     uint8_t* kept = (uint8_t*)malloc((size_t)N);
     uint8_t* shared = (uint8_t*)malloc((size_t)N);
@@ -206,9 +229,17 @@ void oracle_build_sets(const int32_t* votes, int H, int nt, int N, float pos_sca
       const long tstart = (long)q_pos_base + (long)t * T; /* exact_2.py:291 */
       const long lo = tstart - n_local + 1, hi_l = tstart + T - 1;
       long usize = 0;
+      const float* wrow = wvotes ? wvotes + ((size_t)h * nt + t) * N : NULL;
       for (int j = 0; j < N; ++j) {
         forced[j] = (j < n_global) || (j >= lo && j <= hi_l); /* exact_2.py:290-293, 303 */
-        sv[j] = (float)vrow[j];
+        if (wrow) { /* exact_2.py:302: rank_val = wvotes.float() + 1e-6 * vf, in float32 */
+          volatile float tb = 1e-6f * (float)vrow[j];
+          volatile float r = wrow[j] + tb;
+          rv[j] = r;
+        } else {
+          rv[j] = (float)vrow[j]; /* exact_2.py:300 */
+        }
+        sv[j] = rv[j];
         if (vrow[j] > 0) usize += 1; /* exact_2.py:296 */
       }
       /* topk(K_ord, sorted) == first K_ord entries of a descending sort (exact_2.py:321) */
@@ -226,7 +257,7 @@ void oracle_build_sets(const int32_t* votes, int H, int nt, int N, float pos_sca
         if (bi > K_ord - 1) bi = K_ord - 1;
         const float v_cut = sv[bi]; /* exact_2.py:330 */
         long size = 0;
-        for (int j = 0; j < N; ++j) size += ((float)vrow[j] >= v_cut) || forced[j];
+        for (int j = 0; j < N; ++j) size += (rv[j] >= v_cut) || forced[j];
         if (p == start_pct) oflow = size > k_max; /* exact_2.py:333-334 */
         if (!resolved) {
           /* unresolved tiles keep the last step's sets (exact_2.py:347-350) */
@@ -253,7 +284,7 @@ void oracle_build_sets(const int32_t* votes, int H, int nt, int N, float pos_sca
           if (bi > K_ord - 1) bi = K_ord - 1;
           const float v_cut = sv[bi];
           long size = 0;
-          for (int j = 0; j < N; ++j) size += ((float)vrow[j] >= v_cut) || forced[j];
+          for (int j = 0; j < N; ++j) size += (rv[j] >= v_cut) || forced[j];
           if (size <= k_max) {
             kmeas = p;
             break;
@@ -263,7 +294,7 @@ void oracle_build_sets(const int32_t* votes, int H, int nt, int N, float pos_sca
 
       long nshared = 0, nkept = 0;
       for (int j = 0; j < N; ++j) {
-        shared[j] = use_forced_only ? 0 : ((float)vrow[j] >= cut_final);
+        shared[j] = use_forced_only ? 0 : (rv[j] >= cut_final);
         kept[j] = shared[j] || forced[j];
         nshared += shared[j];
         nkept += kept[j];
@@ -314,6 +345,7 @@ void oracle_build_sets(const int32_t* votes, int H, int nt, int N, float pos_sca
       kpct_meas[o] = kmeas;
     }
     free(sv);
+    free(rv);
     free(forced);
     free(kept);
     free(shared);

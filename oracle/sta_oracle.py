@@ -113,10 +113,11 @@ def rope_rotate(x, dtype, posf, inv_freq, rope_scale):
 
 
 def select_vote(q, k, dtype, tau, inv_freq, pos_scale, rope_scale, sm_scale, tile, q_pos_base=0,
-                band_eps=1e-3, want_band=False, want_keep=False):
+                band_eps=1e-3, want_band=False, want_keep=False, wmode=0):
     """Kernel A (exact_2.py:50-140).  q (H,N,D), k (Hkv,N,D).  Returns a dict with
     votes (H,nt,N) int32, row_counts (H,N) int32, row_max (H,N) fp32 and optionally
-    band (H,nt,N) int32 and keep (H,N,N) uint8."""
+    band (H,nt,N) int32, keep (H,N,N) uint8 and, for wmode 1 (margin) / 2 (expmass), the
+    weighted votes wvotes (H,nt,N) fp32 (exact_2.py:126-138)."""
     q = np.ascontiguousarray(q)
     k = np.ascontiguousarray(k)
     H, N, D = q.shape
@@ -128,13 +129,16 @@ def select_vote(q, k, dtype, tau, inv_freq, pos_scale, rope_scale, sm_scale, til
     band = np.empty((H, nt, N), np.int32) if want_band else None
     band_rows = np.empty((H, N), np.int32) if want_band else None
     keep = np.empty((H, N, N), np.uint8) if want_keep else None
+    wvotes = np.empty((H, nt, N), np.float32) if wmode else None
     lib().oracle_select_vote(
         _p(q), _p(k), ctypes.c_int(dtype), ctypes.c_int(H), ctypes.c_int(Hkv), ctypes.c_int(N),
         ctypes.c_int(D), _p(_c(tau, np.float32)), _p(_c(inv_freq, np.float32)),
         ctypes.c_float(pos_scale), ctypes.c_float(rope_scale), ctypes.c_float(sm_scale),
         ctypes.c_int(tile), ctypes.c_int(q_pos_base), _p(votes), _p(row_counts), _p(row_max),
-        _p(band), _p(band_rows), ctypes.c_float(band_eps), _p(keep))
+        _p(band), _p(band_rows), ctypes.c_float(band_eps), _p(keep), ctypes.c_int(wmode), _p(wvotes))
     out = {"votes": votes, "row_counts": row_counts, "row_max": row_max}
+    if wmode:
+        out["wvotes"] = wvotes
     if want_band:
         out["band"] = band
         out["band_rows"] = band_rows
@@ -143,16 +147,24 @@ def select_vote(q, k, dtype, tau, inv_freq, pos_scale, rope_scale, sm_scale, til
     return out
 
 
+WMODES = {"freq": 0, "margin": 1, "expmass": 2}
+
+
 def start_pct_of(pct):
     """start_pct = max(0, int(round(pct))) with Python's round-half-even (exact_2.py:309)."""
     return max(0, int(round(pct)))
 
 
-def build_sets(votes, pos_scale, n_global, n_local, pct, T, k_max, q_pos_base=0, measure=False):
-    """_build_sets (exact_2.py:277-426), freq mode.  votes (H,nt,N) int.  Returns the reference's
-    9-tuple (idx, newpos_k, newpos_q, shared_size, kept_size, chosen, orig_overflow, kpct_meas,
-    overflow20) as numpy arrays."""
+def build_sets(votes, pos_scale, n_global, n_local, pct, T, k_max, q_pos_base=0, measure=False,
+               wvotes=None):
+    """_build_sets (exact_2.py:277-426).  votes (H,nt,N) int; wvotes (H,nt,N) fp32 switches the
+    ranking to fl(wvotes + fl(1e-6 votes)) (margin / expmass, exact_2.py:299-302), None ranks by
+    votes.  Returns the reference's 9-tuple (idx, newpos_k, newpos_q, shared_size, kept_size,
+    chosen, orig_overflow, kpct_meas, overflow20) as numpy arrays."""
     votes = _c(votes, np.int32)
+    if wvotes is not None:
+        wvotes = _c(wvotes, np.float32)
+        assert wvotes.shape == votes.shape
     H, nt, N = votes.shape
     idx = np.empty((H, nt, k_max), np.int32)
     npk = np.empty((H, nt, k_max), np.float32)
@@ -167,7 +179,7 @@ def build_sets(votes, pos_scale, n_global, n_local, pct, T, k_max, q_pos_base=0,
         _p(votes), ctypes.c_int(H), ctypes.c_int(nt), ctypes.c_int(N), ctypes.c_float(pos_scale),
         ctypes.c_int(n_global), ctypes.c_int(n_local), ctypes.c_int(start_pct_of(pct)),
         ctypes.c_int(T), ctypes.c_int(k_max), ctypes.c_int(q_pos_base), ctypes.c_int(int(measure)),
-        _p(idx), _p(npk), _p(npq), _p(ss), _p(ks), _p(ch), _p(oo), _p(km), _p(o20))
+        _p(idx), _p(npk), _p(npq), _p(ss), _p(ks), _p(ch), _p(oo), _p(km), _p(o20), _p(wvotes))
     return idx, npk, npq, ss, ks, ch, oo.astype(bool), km, o20.astype(bool)
 
 
@@ -192,23 +204,27 @@ def gather_attn(q, k, v, dtype, idx, newpos_k, newpos_q, inv_freq, rope_scale, s
 def shared_pi_attention(q, k, v, dtype, tau, inv_freq_a, pos_scale_a, rope_scale_a,
                         inv_freq_c=None, pos_scale_c=None, rope_scale_c=None, pct=30.0,
                         sm_scale=None, n_global=32, n_local=32, tile=32, k_max=1024, block_k=64,
-                        q_pos_base=0, measure=False):
+                        q_pos_base=0, measure=False, select_score="freq"):
     """Composition of the three stages (exact_2.py:432-486).  With the *_c triple given it is the
     hybrid entry point (hybrid_exact.py:450-510): Kernel A under the a-geometry, _build_sets'
-    reposition and Kernel C under the c-geometry.  Returns
+    reposition and Kernel C under the c-geometry.  select_score "margin" / "expmass" ranks by
+    Kernel A's weighted votes (exact_2.py:450-453, 467-469).  Returns
     (out_f32, shared_size, kept_size, kpct, overflow, kpct_meas, overflow20, extras)."""
     H, N, D = q.shape
     if sm_scale is None:
         sm_scale = 1.0 / math.sqrt(D)
     if inv_freq_c is None:
         inv_freq_c, pos_scale_c, rope_scale_c = inv_freq_a, pos_scale_a, rope_scale_a
+    wmode = WMODES[select_score]
     a = select_vote(q, k, dtype, tau, inv_freq_a, pos_scale_a, rope_scale_a, sm_scale, tile,
-                    q_pos_base)
+                    q_pos_base, wmode=wmode)
     idx, npk, npq, ss, ks, ch, oo, km, o20 = build_sets(
-        a["votes"], pos_scale_c, n_global, n_local, pct, tile, k_max, q_pos_base, measure)
+        a["votes"], pos_scale_c, n_global, n_local, pct, tile, k_max, q_pos_base, measure,
+        wvotes=a.get("wvotes"))
     out = gather_attn(q, k, v, dtype, idx, npk, npq, inv_freq_c, rope_scale_c, sm_scale, tile,
                       k_max, block_k, q_pos_base)
-    extras = {"votes": a["votes"], "row_max": a["row_max"], "row_counts": a["row_counts"],
+    extras = {"votes": a["votes"], "wvotes": a.get("wvotes"), "row_max": a["row_max"],
+              "row_counts": a["row_counts"],
               "idx": idx, "newpos_k": npk, "newpos_q": npq}
     return out, ss, ks, ch, oo, km, o20, extras
 
@@ -216,9 +232,6 @@ def shared_pi_attention(q, k, v, dtype, tau, inv_freq_a, pos_scale_a, rope_scale
 # ---------------------------------------------------------------------------------------------
 # PQ Union (per-query sets through a tile union + bitmask) and PQ Stream
 # ---------------------------------------------------------------------------------------------
-WMODES = {"freq": 0, "margin": 1, "expmass": 2}
-
-
 def select_bits(q, k, dtype, tau, inv_freq, pos_scale, rope_scale, sm_scale, tile=32, q_pos_base=0,
                 wmode=2, band_eps=1e-3, want_band=False):
     """PQ Union Kernel A (perquery.py:119-218).  Returns a dict with votes, bits (int32, bit i =
