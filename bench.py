@@ -115,8 +115,10 @@ def cpu_baseline(cfg, q, k, v, invf, ps, rs, budget_s):
             orc.shared_pq_attention(qn, kn, vn, dt, tau, invf.numpy(), invf.numpy(), ps, rs, sm,
                                     cfg.n_global, cfg.n_local, cfg.tile, cfg.k_max, 64, 0, cfg.select_score)
         else:
-            a = orc.select_vote(qn, kn, dt, tau, invf.numpy(), ps, rs, sm, cfg.tile)
-            s = orc.build_sets(a["votes"], ps, cfg.n_global, cfg.n_local, cfg.pct, cfg.tile, cfg.k_max)
+            a = orc.select_vote(qn, kn, dt, tau, invf.numpy(), ps, rs, sm, cfg.tile,
+                                wmode=orc.WMODES[cfg.select_score])
+            s = orc.build_sets(a["votes"], ps, cfg.n_global, cfg.n_local, cfg.pct, cfg.tile, cfg.k_max,
+                               wvotes=a.get("wvotes"))
             orc.gather_attn(qn, kn, vn, dt, s[0], s[1], s[2], invf.numpy(), rs, sm, cfg.tile, cfg.k_max)
         return time.perf_counter() - t0
 
@@ -168,7 +170,8 @@ def main():
                              n_global=cfg.n_global, n_local=cfg.n_local, select_score=cfg.select_score)
     else:
         plan = native.SharedPlan(q, k, v, tau, invf, ps, rs, invf, ps, rs, pct=cfg.pct, tile=cfg.tile,
-                                 k_max=cfg.k_max, n_global=cfg.n_global, n_local=cfg.n_local)
+                                 k_max=cfg.k_max, n_global=cfg.n_global, n_local=cfg.n_local,
+                                 select_score=cfg.select_score)
     stream = torch.cuda.current_stream(dev)
     for _ in range(args.warmup):
         plan.run()

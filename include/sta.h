@@ -39,6 +39,11 @@ extern "C" {
 #define STA_DTYPE_BF16 1
 #define STA_DTYPE_F16 2
 
+/* key ranking (select_score): frequency, or a weighted vote with frequency as a 1e-6 tiebreak */
+#define STA_SCORE_FREQ 0    /* rank by votes */
+#define STA_SCORE_MARGIN 1  /* by the summed margin fl(s - fl(m - tau)) + 1e-6 votes */
+#define STA_SCORE_EXPMASS 2 /* by the summed exp(fl(s - m)) + 1e-6 votes */
+
 typedef struct sta_shared_args {
   /* inputs */
   const void* q;
@@ -79,9 +84,13 @@ typedef struct sta_shared_args {
    * on `stream` before the RoPE pre-kernels, before the score kernel, before selection, before
    * the gather and after it (stage durations without a host sync) */
   void* const* stage_events;
+  /* ranking of the top-X% cut (added in ABI version 2) */
+  int32_t select_score;    /* STA_SCORE_*: the reference's select_score (exact_2.py:450) */
+  float* wvotes;           /* optional output (H, nt, N): Kernel A's weighted votes (WMODE 1 / 2);
+                            * NULL to skip; ignored for STA_SCORE_FREQ */
 } sta_shared_args;
 
-/* ABI version of this header (bumped on any layout change of sta_shared_args). */
+/* ABI version of this header (bumped on any layout change of sta_shared_args): 2. */
 int sta_abi_version(void);
 
 /* Description of the last error returned on the calling thread ("" if none). */
@@ -98,7 +107,8 @@ size_t sta_shared_workspace_size(const sta_shared_args* args);
  * with two geometries, shared_selection_triton_hybrid_exact.py:450-510). */
 int sta_shared_attention(const sta_shared_args* args, void* stream);
 
-/* Kernel A alone: writes votes (required), row_counts and row_max (optional).
+/* Kernel A alone: writes votes (required), row_counts, row_max and, for a weighted
+ * select_score, wvotes (optional).
  * Replaces the _select_vote_kernel launch, shared_selection_triton_exact_2.py:50-140, 454-465. */
 int sta_select_vote(const sta_shared_args* args, void* stream);
 
@@ -108,6 +118,13 @@ int sta_select_vote(const sta_shared_args* args, void* stream);
  * n_global, n_local, start_pct, tile, k_max, q_pos_base, measure.
  * Replaces _build_sets, shared_selection_triton_exact_2.py:277-426. */
 int sta_build_sets(const sta_shared_args* args, const int32_t* votes, int32_t num_tiles, void* stream);
+
+/* _build_sets ranked by weighted votes (select_score "margin" / "expmass"): as sta_build_sets,
+ * with the fp32 weighted votes wvotes (H, num_tiles, N) beside the int32 votes; the ranking
+ * value is fl(wvotes + fl(1e-6 votes)) and the union size and budgets stay frequency-based.
+ * Replaces _build_sets(..., wvotes=..., select_score=...), exact_2.py:277-426 (:299-302). */
+int sta_build_sets_weighted(const sta_shared_args* args, const int32_t* votes, const float* wvotes,
+                            int32_t num_tiles, void* stream);
 
 /* Kernel C alone: gather + repositioned attention from idx / newpos_k / newpos_q under the
  * c-geometry.  kept_size, when non-NULL, bounds the slots swept; otherwise all k_max slots are.
@@ -120,9 +137,6 @@ int sta_gather_attention(const sta_shared_args* args, void* stream);
 /* query, the keys it attends.  Positions are dense ranks over the kept set, attended under    */
 /* base RoPE (inv_freq_c, rope scale 1).  tile must be 32 (one bit per query in an int32).     */
 /* ------------------------------------------------------------------------------------------ */
-#define STA_SCORE_FREQ 0    /* overflow ranking by votes */
-#define STA_SCORE_MARGIN 1  /* by the summed margin fl(s - fl(m - tau)) + 1e-6 votes */
-#define STA_SCORE_EXPMASS 2 /* by the summed exp(fl(s - m)) + 1e-6 votes */
 
 typedef struct sta_pq_args {
   /* inputs (layout rules as sta_shared_args) */

@@ -18,10 +18,6 @@ _WMODES = {"freq": 0, "margin": 1, "expmass": 2}
 def _check_select_score(select_score):
     if select_score not in _WMODES:
         raise KeyError(select_score)  # the reference's dict lookup (exact_2.py:450)
-    if select_score != "freq":
-        raise NotImplementedError(
-            f"select_score={select_score!r}: only frequency ranking ('freq') is implemented on the "
-            "HIP path; weighted ranking is not available")
 
 
 def _pct_steps(pct):
@@ -52,7 +48,7 @@ def shared_prefill(q, k, v, tau, inv_freq_a, pos_scale_a, rope_scale_a, inv_freq
     r = native.shared_attention(q, k, v, tau, inv_freq_a, pos_scale_a, rope_scale_a, inv_freq_c,
                                 pos_scale_c, rope_scale_c, pct=pct, sm_scale=sm_scale,
                                 n_global=n_global, n_local=n_local, tile=tile, k_max=k_max,
-                                q_pos_base=q_pos_base, measure=measure)
+                                q_pos_base=q_pos_base, measure=measure, select_score=select_score)
     if measure:
         report_measure(r["chosen"], r["orig_overflow"], r["overflow20"], pct, k_max)
     return (r["out"].unsqueeze(0), r["shared_size"].long(), r["kept_size"].long(), r["chosen"],
@@ -61,10 +57,13 @@ def shared_prefill(q, k, v, tau, inv_freq_a, pos_scale_a, rope_scale_a, inv_freq
 
 def build_sets(votes, pos_scale, n_global, n_local, pct, T, k_max, q_pos_base=0, measure=False,
                wvotes=None, select_score="freq"):
-    """_build_sets (exact_2.py:277-426) on the device.  Same 9-tuple."""
+    """_build_sets (exact_2.py:277-426) on the device.  Same 9-tuple.  As in the reference, the
+    weighted votes rank the keys only when select_score is not "freq" and wvotes is given
+    (exact_2.py:299-302)."""
     _check_select_score(select_score)
+    use_w = select_score != "freq" and wvotes is not None
     res = native.build_sets(votes, pos_scale, n_global, n_local, pct, T, k_max,
-                            q_pos_base=q_pos_base, measure=measure)
+                            q_pos_base=q_pos_base, measure=measure, wvotes=wvotes if use_w else None)
     if measure:
         report_measure(res[5], res[6], res[8], pct, k_max)
     return res

@@ -17,7 +17,7 @@ _LIB = None
 STA_OK = 0
 DTYPES = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
 EXPORTS = ["sta_abi_version", "sta_last_error", "sta_shared_workspace_size", "sta_shared_attention",
-           "sta_select_vote", "sta_build_sets", "sta_gather_attention",
+           "sta_select_vote", "sta_build_sets", "sta_build_sets_weighted", "sta_gather_attention",
            "sta_pq_workspace_size", "sta_pq_attention", "sta_pq_select_bits", "sta_pq_build_sets",
            "sta_pq_gather_attention", "sta_pqstream_workspace_size", "sta_pqstream_attention",
            "sta_dca_workspace_size", "sta_dca_attention"]
@@ -47,6 +47,7 @@ class ShareArgs(ctypes.Structure):
         ("votes", ctypes.c_void_p), ("row_counts", ctypes.c_void_p), ("row_max", ctypes.c_void_p),
         ("workspace", ctypes.c_void_p), ("workspace_bytes", ctypes.c_size_t),
         ("stage_events", ctypes.c_void_p),
+        ("select_score", ctypes.c_int32), ("wvotes", ctypes.c_void_p),
     ]
 
 
@@ -132,6 +133,9 @@ def lib():
         L.sta_build_sets.restype = ctypes.c_int
         L.sta_build_sets.argtypes = [ctypes.POINTER(ShareArgs), ctypes.c_void_p, ctypes.c_int32,
                                      ctypes.c_void_p]
+        L.sta_build_sets_weighted.restype = ctypes.c_int
+        L.sta_build_sets_weighted.argtypes = [ctypes.POINTER(ShareArgs), ctypes.c_void_p, ctypes.c_void_p,
+                                              ctypes.c_int32, ctypes.c_void_p]
         L.sta_pq_workspace_size.restype = ctypes.c_size_t
         L.sta_pq_workspace_size.argtypes = [ctypes.POINTER(PqArgs)]
         for name in ("sta_pq_attention", "sta_pq_select_bits", "sta_pq_gather_attention"):
@@ -149,7 +153,7 @@ def lib():
         L.sta_dca_workspace_size.argtypes = [ctypes.POINTER(DcaArgsC)]
         L.sta_dca_attention.restype = ctypes.c_int
         L.sta_dca_attention.argtypes = [ctypes.POINTER(DcaArgsC), ctypes.c_void_p]
-        if L.sta_abi_version() != 1:
+        if L.sta_abi_version() != 2:
             raise ImportError("libsta_hip.so ABI version mismatch")
         _LIB = L
     return _LIB
@@ -187,7 +191,8 @@ def start_pct_of(pct):
 
 
 def _fill_common(a, q, k, v, tau, inv_freq_a, pos_scale_a, rope_scale_a, inv_freq_c, pos_scale_c,
-                 rope_scale_c, sm_scale, pct, n_global, n_local, tile, k_max, q_pos_base, measure):
+                 rope_scale_c, sm_scale, pct, n_global, n_local, tile, k_max, q_pos_base, measure,
+                 select_score="freq"):
     H, N, D = q.shape
     a.q, a.k = _ptr(q), _ptr(k)
     a.v = _ptr(v) if v is not None else None
@@ -204,6 +209,7 @@ def _fill_common(a, q, k, v, tau, inv_freq_a, pos_scale_a, rope_scale_a, inv_fre
     a.start_pct = start_pct_of(pct)
     a.n_global, a.n_local, a.tile, a.k_max = int(n_global), int(n_local), int(tile), int(k_max)
     a.q_pos_base, a.measure = int(q_pos_base), int(bool(measure))
+    a.select_score = SCORES[select_score]
 
 
 def _prep_inputs(q, k, v, tau, inv_freq_a, inv_freq_c):
@@ -240,7 +246,7 @@ class SharedPlan:
     def __init__(self, q, k, v, tau, inv_freq_a, pos_scale_a, rope_scale_a, inv_freq_c, pos_scale_c,
                  rope_scale_c, pct=30.0, sm_scale=None, n_global=32, n_local=32, tile=32,
                  k_max=1024, q_pos_base=0, measure=False, want_votes=False, want_row_max=False,
-                 want_row_counts=False):
+                 want_row_counts=False, select_score="freq"):
         qh, kh, vh, tau, ifa, ifc = _prep_inputs(q, k, v, tau, inv_freq_a, inv_freq_c)
         H, N, D = qh.shape
         self.device = qh.device
@@ -248,10 +254,10 @@ class SharedPlan:
             sm_scale = 1.0 / math.sqrt(D)
         self.args = a = ShareArgs()
         _fill_common(a, qh, kh, vh, tau, ifa, pos_scale_a, rope_scale_a, ifc, pos_scale_c, rope_scale_c,
-                     sm_scale, pct, n_global, n_local, tile, k_max, q_pos_base, measure)
+                     sm_scale, pct, n_global, n_local, tile, k_max, q_pos_base, measure, select_score)
         self._keep = (qh, kh, vh, tau, ifa, ifc)
         self.out = _alloc_outputs(a, H, N, D, qh.dtype, tile, k_max, self.device, want_votes,
-                                  want_row_max, want_row_counts)
+                                  want_row_max, want_row_counts, want_wvotes=want_votes and select_score != "freq")
         self.workspace = _workspace(a, self.device)
         self._events = None
 
@@ -267,7 +273,8 @@ class SharedPlan:
         return self.out
 
 
-def _alloc_outputs(a, H, N, D, dtype, tile, k_max, dev, want_votes, want_row_max, want_row_counts):
+def _alloc_outputs(a, H, N, D, dtype, tile, k_max, dev, want_votes, want_row_max, want_row_counts,
+                   want_wvotes=False):
     nt = (N + tile - 1) // tile
     r = {
         "out": torch.empty((H, N, D), dtype=dtype, device=dev),
@@ -287,55 +294,69 @@ def _alloc_outputs(a, H, N, D, dtype, tile, k_max, dev, want_votes, want_row_max
         r["row_max"] = torch.empty((H, N), dtype=torch.float32, device=dev)
     if want_row_counts:
         r["row_counts"] = torch.empty((H, N), dtype=torch.int32, device=dev)
+    if want_wvotes:
+        r["wvotes"] = torch.empty((H, nt, N), dtype=torch.float32, device=dev)
     for name in ("out", "idx", "newpos_k", "newpos_q", "shared_size", "kept_size", "chosen",
                  "orig_overflow", "kpct_meas", "overflow20"):
         setattr(a, name, _ptr(r[name]))
     a.votes = _ptr(r.get("votes"))
     a.row_max = _ptr(r.get("row_max"))
     a.row_counts = _ptr(r.get("row_counts"))
+    a.wvotes = _ptr(r.get("wvotes"))
     return r
 
 
 def shared_attention(q, k, v, tau, inv_freq_a, pos_scale_a, rope_scale_a, inv_freq_c, pos_scale_c,
                      rope_scale_c, pct=30.0, sm_scale=None, n_global=32, n_local=32, tile=32,
                      k_max=1024, q_pos_base=0, measure=False, want_votes=False, want_row_max=False,
-                     want_row_counts=False):
+                     want_row_counts=False, select_score="freq"):
     """Run the whole prefill path on the device.  q (1,H,N,D) / k, v (1,Hkv,N,D).
-    Returns a dict of device tensors (see include/sta.h for their meaning).  The workspace is
-    released on return; the caching allocator hands it out again only to work queued later on
-    the same stream."""
+    Returns a dict of device tensors (see include/sta.h for their meaning; with want_votes and a
+    weighted select_score also "wvotes").  The workspace is released on return; the caching
+    allocator hands it out again only to work queued later on the same stream."""
     plan = SharedPlan(q, k, v, tau, inv_freq_a, pos_scale_a, rope_scale_a, inv_freq_c, pos_scale_c,
                       rope_scale_c, pct, sm_scale, n_global, n_local, tile, k_max, q_pos_base, measure,
-                      want_votes, want_row_max, want_row_counts)
+                      want_votes, want_row_max, want_row_counts, select_score)
     return plan.run()
 
 
 def select_vote(q, k, tau, inv_freq, pos_scale, rope_scale, sm_scale, tile, q_pos_base=0,
-                want_row_counts=True):
-    """Kernel A alone: votes (H,nt,N) int32, row_counts (H,N) int32, row_max (H,N) fp32."""
+                want_row_counts=True, select_score="freq"):
+    """Kernel A alone: votes (H,nt,N) int32, row_counts (H,N) int32, row_max (H,N) fp32; with a
+    weighted select_score a fourth result, the weighted votes (H,nt,N) fp32."""
     qh, kh, _, tau, ifa, _ = _prep_inputs(q, k, None, tau, inv_freq, None)
     H, N, D = qh.shape
     dev = qh.device
     nt = (N + tile - 1) // tile
     a = ShareArgs()
     _fill_common(a, qh, kh, None, tau, ifa, pos_scale, rope_scale, ifa, pos_scale, rope_scale,
-                 sm_scale, 30.0, 0, 0, tile, 1, q_pos_base, False)
+                 sm_scale, 30.0, 0, 0, tile, 1, q_pos_base, False, select_score)
     votes = torch.empty((H, nt, N), dtype=torch.int32, device=dev)
     rc = torch.empty((H, N), dtype=torch.int32, device=dev) if want_row_counts else None
     rm = torch.empty((H, N), dtype=torch.float32, device=dev)
-    a.votes, a.row_counts, a.row_max = _ptr(votes), _ptr(rc), _ptr(rm)
+    wv = torch.empty((H, nt, N), dtype=torch.float32, device=dev) if select_score != "freq" else None
+    a.votes, a.row_counts, a.row_max, a.wvotes = _ptr(votes), _ptr(rc), _ptr(rm), _ptr(wv)
     ws = _workspace(a, dev)
     _check(lib().sta_select_vote(ctypes.byref(a), _stream(dev)), "sta_select_vote")
     del ws
+    if wv is not None:
+        return votes, rc, rm, wv
     return votes, rc, rm
 
 
-def build_sets(votes, pos_scale, n_global, n_local, pct, T, k_max, q_pos_base=0, measure=False):
-    """_build_sets on the device from int32 votes (H, nt, N).  Returns the reference's 9-tuple
-    (exact_2.py:418-426) with shared_size / kept_size as int64 like the reference's sums."""
+def build_sets(votes, pos_scale, n_global, n_local, pct, T, k_max, q_pos_base=0, measure=False,
+               wvotes=None):
+    """_build_sets on the device from int32 votes (H, nt, N) and, for weighted ranking, fp32
+    wvotes (H, nt, N) (rank = fl(wvotes + fl(1e-6 votes)), exact_2.py:299-302).  Returns the
+    reference's 9-tuple (exact_2.py:418-426) with shared_size / kept_size as int64 like the
+    reference's sums."""
     if not votes.is_cuda:
         raise RuntimeError("build_sets runs on a HIP device only; got a CPU tensor")
     votes = votes.to(torch.int32).contiguous()
+    if wvotes is not None:
+        wvotes = wvotes.to(device=votes.device, dtype=torch.float32).contiguous()
+        if wvotes.shape != votes.shape:
+            raise ValueError(f"wvotes {tuple(wvotes.shape)} and votes {tuple(votes.shape)} differ in shape")
     H, nt, N = votes.shape
     dev = votes.device
     a = ShareArgs()
@@ -356,7 +377,12 @@ def build_sets(votes, pos_scale, n_global, n_local, pct, T, k_max, q_pos_base=0,
     a.idx, a.newpos_k, a.newpos_q = _ptr(idx), _ptr(npk), _ptr(npq)
     a.shared_size, a.kept_size, a.chosen = _ptr(ss), _ptr(ks), _ptr(ch)
     a.orig_overflow, a.kpct_meas, a.overflow20 = _ptr(oo), _ptr(km), _ptr(o20)
-    _check(lib().sta_build_sets(ctypes.byref(a), _ptr(votes), nt, _stream(dev)), "sta_build_sets")
+    if wvotes is not None:
+        a.select_score = SCORES["margin"]   # any weighted ranking: the rank value is the same
+        _check(lib().sta_build_sets_weighted(ctypes.byref(a), _ptr(votes), _ptr(wvotes), nt, _stream(dev)),
+               "sta_build_sets_weighted")
+    else:
+        _check(lib().sta_build_sets(ctypes.byref(a), _ptr(votes), nt, _stream(dev)), "sta_build_sets")
     return idx, npk, npq, ss.long(), ks.long(), ch, oo, km, o20
 
 

@@ -51,7 +51,7 @@ namespace {
 struct Layout {
   int nt, q_rows_pad, k_rows_pad;
   int64_t votes_stride;
-  size_t qfrag_off, kfrag_off, votes_off, total;
+  size_t qfrag_off, kfrag_off, votes_off, wv_off, total;
 };
 
 Layout layout_of(const sta_shared_args* a) {
@@ -68,6 +68,8 @@ Layout layout_of(const sta_shared_args* a) {
   off = align256(off + frag_region_bytes(a->Hkv, L.k_rows_pad, a->D));
   L.votes_off = off;
   off = align256(off + (size_t)a->H * L.nt * L.votes_stride);
+  L.wv_off = off;   // weighted votes (H, nt, votes_stride) fp32, for a weighted select_score only
+  if (a->select_score != STA_SCORE_FREQ) off = align256(off + (size_t)a->H * L.nt * L.votes_stride * 4);
   L.total = off;
   return L;
 }
@@ -87,6 +89,8 @@ int check_common(const sta_shared_args* a) {
   if (a->q_pos_base < 0) return fail(STA_ERR_INVALID_ARG, "q_pos_base=%d must be >= 0", a->q_pos_base);
   if (a->n_global < 0 || a->n_local < 0)
     return fail(STA_ERR_INVALID_ARG, "n_global=%d / n_local=%d must be >= 0", a->n_global, a->n_local);
+  if (a->select_score < STA_SCORE_FREQ || a->select_score > STA_SCORE_EXPMASS)
+    return fail(STA_ERR_INVALID_ARG, "select_score %d is not one of STA_SCORE_*", a->select_score);
   return STA_OK;
 }
 
@@ -111,6 +115,10 @@ int check_sets_outputs(const sta_shared_args* a) {
     return fail(STA_ERR_INVALID_ARG, "a selection output pointer is NULL");
   if (select_lds_bytes(a->N, a->k_max) > 160 * 1024)
     return fail(STA_ERR_UNSUPPORTED, "N=%d with k_max=%d needs more than 160 KB of LDS for selection",
+                a->N, a->k_max);
+  if (a->select_score != STA_SCORE_FREQ && select_w_lds_bytes(a->N, a->k_max) > 160 * 1024)
+    return fail(STA_ERR_UNSUPPORTED,
+                "weighted ranking at N=%d with k_max=%d needs more than 160 KB of LDS for selection",
                 a->N, a->k_max);
   return STA_OK;
 }
@@ -149,6 +157,7 @@ SelectArgs select_args_of(const sta_shared_args* a, const Layout& L) {
   s.kpct_meas = a->kpct_meas;
   s.overflow20 = a->overflow20;
   s.votes_out = a->votes;
+  s.wvotes_out = a->select_score != STA_SCORE_FREQ ? a->wvotes : nullptr;
   return s;
 }
 
@@ -186,7 +195,12 @@ int run_kernel_a(const sta_shared_args* a, const Layout& L, hipStream_t st) {
   sa.votes_stride = L.votes_stride;
   sa.row_max = a->row_max;
   sa.row_counts = a->row_counts;
-  e = launch_score(a->D, a->tile, sa, st);
+  if (a->select_score != STA_SCORE_FREQ) {
+    sa.wvotes = (float*)(ws + L.wv_off);
+    e = launch_score_weighted(a->D, a->tile, a->select_score, sa, st);
+  } else {
+    e = launch_score(a->D, a->tile, sa, st);
+  }
   if (e != hipSuccess) return hip_fail(e, "score kernel");
   return STA_OK;
 }
@@ -227,7 +241,7 @@ int run_gather(const sta_shared_args* a, const Layout& L, hipStream_t st) {
 
 extern "C" {
 
-int sta_abi_version(void) { return 1; }
+int sta_abi_version(void) { return 2; }
 
 const char* sta_last_error(void) { return g_last_error.c_str(); }
 
@@ -251,7 +265,13 @@ int sta_shared_attention(const sta_shared_args* args, void* stream) {
   SelectArgs s = select_args_of(args, L);
   s.votes = (const void*)((char*)args->workspace + L.votes_off);
   s.votes_stride = L.votes_stride;
-  hipError_t e = launch_select(s, 1, st);
+  hipError_t e;
+  if (args->select_score != STA_SCORE_FREQ) {
+    s.wvotes = (const float*)((char*)args->workspace + L.wv_off);
+    e = launch_select_weighted(s, 1, st);
+  } else {
+    e = launch_select(s, 1, st);
+  }
   if (e != hipSuccess) return hip_fail(e, "select kernel");
   if ((rc = mark(args, 3, st)) != STA_OK) return rc;
   if ((rc = run_gather(args, L, st)) != STA_OK) return rc;
@@ -268,8 +288,11 @@ int sta_select_vote(const sta_shared_args* args, void* stream) {
   if ((rc = check_workspace(args, L)) != STA_OK) return rc;
   hipStream_t st = (hipStream_t)stream;
   if ((rc = run_kernel_a(args, L, st)) != STA_OK) return rc;
+  const bool wv = args->select_score != STA_SCORE_FREQ && args->wvotes;
   hipError_t e = launch_expand_votes((const uint8_t*)((char*)args->workspace + L.votes_off), L.votes_stride,
-                                     args->H, L.nt, args->N, args->tile, args->q_pos_base, args->votes, st);
+                                     args->H, L.nt, args->N, args->tile, args->q_pos_base, args->votes,
+                                     wv ? (const float*)((char*)args->workspace + L.wv_off) : nullptr,
+                                     wv ? args->wvotes : nullptr, st);
   if (e != hipSuccess) return hip_fail(e, "vote expansion");
   return STA_OK;
 }
@@ -289,6 +312,32 @@ int sta_build_sets(const sta_shared_args* args, const int32_t* votes, int32_t nu
   s.votes_out = nullptr;
   hipError_t e = launch_select(s, 4, (hipStream_t)stream);
   if (e != hipSuccess) return hip_fail(e, "select kernel");
+  return STA_OK;
+}
+
+int sta_build_sets_weighted(const sta_shared_args* args, const int32_t* votes, const float* wvotes,
+                            int32_t num_tiles, void* stream) {
+  int rc = check_common(args);
+  if (rc != STA_OK) return rc;
+  if (!votes || !wvotes) return fail(STA_ERR_INVALID_ARG, "votes and wvotes must be non-NULL");
+  if (num_tiles < 1) return fail(STA_ERR_INVALID_ARG, "num_tiles=%d must be >= 1", num_tiles);
+  if (args->tile > 256) return fail(STA_ERR_UNSUPPORTED, "tile %d above 256", args->tile);
+  if ((rc = check_sets_outputs(args)) != STA_OK) return rc;
+  if (select_w_lds_bytes(args->N, args->k_max) > 160 * 1024)
+    return fail(STA_ERR_UNSUPPORTED,
+                "weighted ranking at N=%d with k_max=%d needs more than 160 KB of LDS for selection",
+                args->N, args->k_max);
+  Layout L = layout_of(args);
+  L.nt = num_tiles;
+  SelectArgs s = select_args_of(args, L);
+  s.votes = votes;
+  s.wvotes = wvotes;
+  s.votes_stride = args->N;
+  s.votes_dense = 1;
+  s.votes_out = nullptr;
+  s.wvotes_out = nullptr;
+  hipError_t e = launch_select_weighted(s, 4, (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(e, "weighted select kernel");
   return STA_OK;
 }
 

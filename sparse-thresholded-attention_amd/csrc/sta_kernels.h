@@ -32,7 +32,7 @@ struct ScoreArgs {
   uint8_t* votes;         // (H, nt, votes_stride): keys < min(N, hi_t) written
   int64_t votes_stride;
   uint32_t* bits;         // per-query variant: (H, nt, votes_stride) keep bits, bit i = row i
-  float* wvotes;          // per-query variant: (H, nt, votes_stride) margin / expmass votes
+  float* wvotes;          // (H, nt, votes_stride) margin / expmass votes (per-query or shared)
   float* row_max;         // (H, N) or null
   int32_t* row_counts;    // (H, N) or null
   int ib;                 // set by the launcher: block-index bits of the screened pass 1, 0 = off
@@ -59,6 +59,8 @@ struct SelectArgs {
   int32_t* kpct_meas;
   uint8_t* overflow20;
   int32_t* votes_out;     // optional dense int32 copy (H, nt, N)
+  const float* wvotes;    // weighted ranking: (H, nt, votes_stride) margin / expmass votes
+  float* wvotes_out;      // optional dense fp32 copy (H, nt, N) of the weighted votes
 };
 
 struct GatherArgs {
@@ -129,6 +131,8 @@ hipError_t launch_rope_frag(int dtype, int D, const void* x, int64_t head_stride
                             float rope_scale, const float* inv_freq, u32x4* frag, hipStream_t st);
 hipError_t launch_score(int D, int tile, const ScoreArgs& a, hipStream_t st);
 hipError_t launch_score_pq(int D, int wmode, const ScoreArgs& a, hipStream_t st);
+// shared selection with weighted votes: wmode 1 margin / 2 expmass, byte votes + fp32 wvotes
+hipError_t launch_score_weighted(int D, int tile, int wmode, const ScoreArgs& a, hipStream_t st);
 size_t pq_select_lds_bytes(int N, int k_max);
 hipError_t launch_pq_select(const PqSelectArgs& a, hipStream_t st);
 hipError_t launch_expand_pq(const uint32_t* bits, const float* wv, int64_t stride, int H, int nt, int N,
@@ -136,8 +140,11 @@ hipError_t launch_expand_pq(const uint32_t* bits, const float* wv, int64_t strid
                             float* wv_out, hipStream_t st);
 size_t select_lds_bytes(int N, int k_max);
 hipError_t launch_select(const SelectArgs& a, int vote_bytes, hipStream_t st);
+// _build_sets ranked by weighted votes (select_score margin / expmass)
+size_t select_w_lds_bytes(int N, int k_max);
+hipError_t launch_select_weighted(const SelectArgs& a, int vote_bytes, hipStream_t st);
 hipError_t launch_expand_votes(const uint8_t* v8, int64_t stride, int H, int nt, int N, int T, int q_pos_base,
-                               int32_t* out, hipStream_t st);
+                               int32_t* out, const float* wv, float* wv_out, hipStream_t st);
 size_t gather_lds_bytes(int dtype, int D, int k_max);
 hipError_t launch_abs_rope(int dtype, int D, const void* x, int64_t hs, int64_t ts, int heads, int N, int Npad,
                            const float* inv_freq, uint16_t* out, hipStream_t st);

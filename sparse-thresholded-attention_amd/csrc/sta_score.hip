@@ -172,7 +172,9 @@ __device__ __forceinline__ float min_arg_for(float thr, float c) {
 // PQ selects the pass-2 epilogue: 0 = byte votes (shared selection); 1..3 = the per-query
 // variant (tile 32): packed keep bits per key, plus weighted votes for PQ 2 (margin,
 // sum of fl(s - fl(m - tau))) and PQ 3 (expmass, sum of exp(fl(s - m))) over the keeping rows
-// (shared_selection_triton_perquery.py:181-217).
+// (shared_selection_triton_perquery.py:181-217); 4 / 5 = shared selection with byte votes plus
+// the tile's margin / expmass weighted votes (WMODE 1 / 2, shared_selection_triton_exact_2.py:
+// 126-138).
 template <int D, int T, bool RC, int PQ, int RB>
 __global__ __launch_bounds__(256, 1) void score_kernel(ScoreArgs a) {
 #pragma clang fp contract(off)
@@ -191,7 +193,9 @@ __global__ __launch_bounds__(256, 1) void score_kernel(ScoreArgs a) {
   static_assert(PER * S == 16 * RB, "epilogue split");
   static_assert(RB == 2 || RB == 4, "row blocks per wave");
   static_assert(T == 32 || T == 64, "tile");
-  static_assert(PQ == 0 || T == 32, "per-query bits pack one 32-row tile");
+  static_assert(PQ == 0 || PQ >= 4 || T == 32, "per-query bits pack one 32-row tile");
+  constexpr bool BITS = PQ >= 1 && PQ <= 3;                          // per-query keep bits
+  constexpr int WM = (PQ == 2 || PQ == 4) ? 1 : ((PQ == 3 || PQ == 5) ? 2 : 0);   // weighted votes
   __shared__ u32x4 lds[NBUF][CHUNK_UNITS];
 
   const int lane = threadIdx.x & 63;
@@ -279,22 +283,27 @@ __global__ __launch_bounds__(256, 1) void score_kernel(ScoreArgs a) {
   // i%4; the lane half's 4-row offset is applied when the mask is stored)
   auto pq_acc = [&](int keep, float v, float ref, int i, uint32_t& bm, float& w) {
 #pragma clang fp contract(off)
-    bm |= (uint32_t)keep << ((i >> 2) * 8 + (i & 3));
-    if constexpr (PQ == 2) {
+    if constexpr (BITS) bm |= (uint32_t)keep << ((i >> 2) * 8 + (i & 3));
+    if constexpr (WM == 1) {
       const float qk = v * a.sm_scale;
       const float c = qk - ref;
       w += keep ? c : 0.0f;
-    } else if constexpr (PQ == 3) {
+    } else if constexpr (WM == 2) {
       const float qk = v * a.sm_scale;
       const float e = __expf(qk - ref);
       w += keep ? e : 0.0f;
     }
   };
+  // pass-2 accumulation of one score: the vote count, and bits / weighted votes
+  auto acc2 = [&](int keep, float v, float ref, int i, int& cnt, uint32_t& bm, float& w) {
+    if constexpr (!BITS) cnt += keep;
+    if constexpr (PQ != 0) pq_acc(keep, v, ref, i, bm, w);
+  };
   // the key's pass-2 results of this wave's rows -> votes (exact_2.py:123) or bits + weighted
   // votes; lanes 0-31 and 32-63 hold complementary rows of the same key
   auto store_key = [&](int key, bool check, const int* cnt, const uint32_t* bm, const float* w) {
     const bool key_ok = !check || key < a.N;
-    if constexpr (PQ == 0) {
+    if constexpr (!BITS) {
       int tot[NTW];
 #pragma unroll
       for (int j = 0; j < NTW; ++j) {
@@ -303,13 +312,29 @@ __global__ __launch_bounds__(256, 1) void score_kernel(ScoreArgs a) {
         for (int rb = j * T / 32; rb < (j + 1) * T / 32; ++rb) c += cnt[rb];
         tot[j] = c + __shfl_xor(c, 32, 64);
       }
+      float wt[NTW];   // the tile's weighted vote (WMODE 1 / 2), summed like the counts
+      if constexpr (WM > 0) {
+#pragma unroll
+        for (int j = 0; j < NTW; ++j) {
+          float x = 0.0f;
+#pragma unroll
+          for (int rb = j * T / 32; rb < (j + 1) * T / 32; ++rb) x += w[rb];
+          wt[j] = x + __shfl_xor(x, 32, 64);
+        }
+      }
       if constexpr (NTW == 1) {
-        if (lane < 32 && active && key_ok) vrow[key] = (uint8_t)tot[0];
+        if (lane < 32 && active && key_ok) {
+          vrow[key] = (uint8_t)tot[0];
+          if constexpr (WM > 0) wrow[key] = __float_as_uint(wt[0]);
+        }
       } else {
 #pragma unroll
         for (int j2 = 0; j2 < NTW; j2 += 2) {
           const int j = j2 + (lane >> 5);
-          if (tile_ok(j) && key_ok) vrow[j * a.votes_stride + key] = (uint8_t)(lane < 32 ? tot[j2] : tot[j2 + 1]);
+          if (tile_ok(j) && key_ok) {
+            vrow[j * a.votes_stride + key] = (uint8_t)(lane < 32 ? tot[j2] : tot[j2 + 1]);
+            if constexpr (WM > 0) wrow[j * a.votes_stride + key] = __float_as_uint(lane < 32 ? wt[j2] : wt[j2 + 1]);
+          }
         }
       }
     } else {   // tile 32: one tile per row block
@@ -320,14 +345,14 @@ __global__ __launch_bounds__(256, 1) void score_kernel(ScoreArgs a) {
         b[rb] = bm[rb] << (4 * (lane >> 5));   // rows of the upper lane half sit 4 bits higher
         b[rb] |= __shfl_xor(b[rb], 32, 64);
         ww[rb] = w[rb];
-        if constexpr (PQ >= 2) ww[rb] += __shfl_xor(w[rb], 32, 64);
+        if constexpr (WM > 0) ww[rb] += __shfl_xor(w[rb], 32, 64);
       }
 #pragma unroll
       for (int j2 = 0; j2 < RB; j2 += 2) {
         const int j = j2 + (lane >> 5);
         if (tile_ok(j) && key_ok) {
           brow[j * a.votes_stride + key] = lane < 32 ? b[j2] : b[j2 + 1];
-          if constexpr (PQ >= 2) wrow[j * a.votes_stride + key] = __float_as_uint(lane < 32 ? ww[j2] : ww[j2 + 1]);
+          if constexpr (WM > 0) wrow[j * a.votes_stride + key] = __float_as_uint(lane < 32 ? ww[j2] : ww[j2 + 1]);
         }
       }
     }
@@ -335,7 +360,7 @@ __global__ __launch_bounds__(256, 1) void score_kernel(ScoreArgs a) {
 
   float mx[RB][16];   // pass 1: running max of the raw dot per row slot; pass 2: the keep
                       // threshold x0 on the raw dot
-  float ref[RB][16];  // pass 2, PQ 2 / 3: fl(m - tau) / m of the row, the weighted vote's origin
+  float ref[RB][16];  // pass 2, weighted votes: fl(m - tau) / m of the row, the weight's origin
   int rc[RB][16];
 #pragma unroll
   for (int rb = 0; rb < RB; ++rb)
@@ -390,8 +415,7 @@ __global__ __launch_bounds__(256, 1) void score_kernel(ScoreArgs a) {
       mx[rb][i] = __builtin_amdgcn_fmed3f(v, mx[rb][i], pinf);   // max; scores are finite
     } else {
       const int keep = v >= mx[rb][i];
-      if constexpr (PQ == 0) cnt[rb] += keep;
-      else pq_acc(keep, v, ref[rb][i], i, bm[rb], w[rb]);
+      acc2(keep, v, ref[rb][i], i, cnt[rb], bm[rb], w[rb]);
       if constexpr (RC) rc[rb][i] += keep;
     }
   };
@@ -724,8 +748,8 @@ __global__ __launch_bounds__(256, 1) void score_kernel(ScoreArgs a) {
           const int row = rb * 32 + (i >> 2) * 8 + (lane >> 5) * 4 + (i & 3);
           const bool ok = wrow0 + row < a.N;   // padded rows never vote (exact_2.py:121)
           mx[rb][i] = ok ? min_arg_for(m - tau, a.sm_scale) : INFINITY;
-          if constexpr (PQ == 2) ref[rb][i] = m - tau;   // perquery.py:210
-          if constexpr (PQ == 3) ref[rb][i] = m;         // perquery.py:215
+          if constexpr (WM == 1) ref[rb][i] = m - tau;   // perquery.py:210; exact_2.py:130
+          if constexpr (WM == 2) ref[rb][i] = m;         // perquery.py:215; exact_2.py:135
           if (a.row_max && (lane & 31) == 0 && ok) a.row_max[(int64_t)h * a.N + wrow0 + row] = m;
         }
     }
@@ -787,8 +811,7 @@ __global__ __launch_bounds__(256, 1) void score_kernel(ScoreArgs a) {
                   if (causal && v > mx[rb][i]) mx[rb][i] = v;
                 } else {
                   const int keep = causal && v >= mx[rb][i];
-                  if constexpr (PQ == 0) cnt[rb] += keep;
-                  else pq_acc(keep, v, ref[rb][i], i, bm[rb], w[rb]);
+                  acc2(keep, v, ref[rb][i], i, cnt[rb], bm[rb], w[rb]);
                   if constexpr (RC) rc[rb][i] += keep;
                 }
               }
@@ -885,6 +908,16 @@ hipError_t launch_score(int D, int tile, const ScoreArgs& a, hipStream_t st) {
   if (D == D_ && tile == T_) return rc ? launch_score_t<D_, T_, true, 0>(a, st) : launch_score_t<D_, T_, false, 0>(a, st);
   STA_SC(64, 32) STA_SC(64, 64) STA_SC(128, 32) STA_SC(128, 64)
 #undef STA_SC
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_score_weighted(int D, int tile, int wmode, const ScoreArgs& a, hipStream_t st) {
+  const bool rc = a.row_counts != nullptr;
+#define STA_SW(D_, T_, PQ_) \
+  if (D == D_ && tile == T_ && wmode + 3 == PQ_) return rc ? launch_score_t<D_, T_, true, PQ_>(a, st) : launch_score_t<D_, T_, false, PQ_>(a, st);
+  STA_SW(64, 32, 4) STA_SW(64, 32, 5) STA_SW(64, 64, 4) STA_SW(64, 64, 5)
+  STA_SW(128, 32, 4) STA_SW(128, 32, 5) STA_SW(128, 64, 4) STA_SW(128, 64, 5)
+#undef STA_SW
   return hipErrorInvalidValue;
 }
 

@@ -243,22 +243,27 @@ __global__ __launch_bounds__(256) void select_kernel(SelectArgs a) {
   }
 }
 
-// byte votes (keys < min(N, tile end) valid) -> the reference's dense int32 (H, nt, N) votes
+// byte votes (keys < min(N, tile end) valid) -> the reference's dense int32 (H, nt, N) votes, and
+// the weighted votes (when wv is given) -> dense fp32 (H, nt, N)
 __global__ __launch_bounds__(256) void expand_votes_kernel(const uint8_t* __restrict__ v8, int64_t stride,
                                                            int nt, int N, int T, int q_pos_base,
-                                                           int32_t* __restrict__ out) {
+                                                           int32_t* __restrict__ out,
+                                                           const float* __restrict__ wv,
+                                                           float* __restrict__ wv_out) {
   const int ht = blockIdx.y;
   const int t = ht % nt;
   const int64_t hp = min((int64_t)N, (int64_t)q_pos_base + (int64_t)t * T + T);
-  for (int j = blockIdx.x * 256 + threadIdx.x; j < N; j += gridDim.x * 256)
+  for (int j = blockIdx.x * 256 + threadIdx.x; j < N; j += gridDim.x * 256) {
     out[(int64_t)ht * N + j] = j < hp ? (int32_t)v8[(int64_t)ht * stride + j] : 0;
+    if (wv_out) wv_out[(int64_t)ht * N + j] = j < hp ? wv[(int64_t)ht * stride + j] : 0.0f;
+  }
 }
 
 hipError_t launch_expand_votes(const uint8_t* v8, int64_t stride, int H, int nt, int N, int T, int q_pos_base,
-                               int32_t* out, hipStream_t st) {
+                               int32_t* out, const float* wv, float* wv_out, hipStream_t st) {
   const int bx = (N + 255) / 256 < 64 ? (N + 255) / 256 : 64;
   hipLaunchKernelGGL(expand_votes_kernel, dim3(bx, H * nt), dim3(256), 0, st, v8, stride, nt, N, T, q_pos_base,
-                     out);
+                     out, wv, wv_out);
   return hipGetLastError();
 }
 

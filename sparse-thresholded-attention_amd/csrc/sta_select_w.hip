@@ -1,0 +1,384 @@
+// sta_select_w.hip -- per-(head, tile) key-set selection ranked by weighted votes, the device
+// form of _build_sets with select_score "margin" / "expmass".
+//
+// Reference: shared_selection_triton_exact_2.py:277-426 with wvotes.  The ranking metric is the
+// weighted vote with frequency as an epsilon tiebreak, rank = fl(wvotes + fl(1e-6 votes))
+// (:299-302); the union size U = #(votes > 0) and the budgets ceil(fl(p/100 * U)) stay
+// frequency-based (:296, :329).  The order statistic the reference reads from topk (:321, :330)
+// is the budget-th largest rank value; here it is a radix select over the tile's rank values
+// staged in LDS (order-preserving 32-bit keys, 8-bit digits) that finds the cuts of all fallback
+// steps in one traversal, and the set sizes follow from its last histograms: #(rank >= cut) is
+// the keys above the cut plus those equal to it.  The forced
+// keys with a rank below the cut are counted directly.  The 30 -> 25 -> 20 fallback, the pct = 0
+// case, the measure loop, compaction and the fp32 reposition recurrence are those of the
+// frequency-ranked select kernel.
+#include "sta_device.h"
+#include "sta_kernels.h"
+
+namespace sta {
+
+namespace {
+
+__device__ __forceinline__ int w_block_sum(int v, int* tmp) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+  if (lane == 0) tmp[wave] = v;
+  __syncthreads();
+  const int total = tmp[0] + tmp[1] + tmp[2] + tmp[3];
+  __syncthreads();
+  return total;
+}
+
+__device__ __forceinline__ int w_block_exclusive_sum(int v, int* tmp) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  int x = v;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int y = __shfl_up(x, o, 64);
+    if (lane >= o) x += y;
+  }
+  if (lane == 63) tmp[wave] = x;
+  __syncthreads();
+  int base = 0;
+  for (int w = 0; w < wave; ++w) base += tmp[w];
+  __syncthreads();
+  return base + x - v;
+}
+
+__device__ __forceinline__ float w_block_exclusive_max(float v, float* tmp) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  float x = v;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const float y = __shfl_up(x, o, 64);
+    if (lane >= o) x = fmaxf(x, y);
+  }
+  float prev = __shfl_up(x, 1, 64);
+  if (lane == 0) prev = -INFINITY;
+  if (lane == 63) tmp[wave] = x;
+  __syncthreads();
+  float base = -INFINITY;
+  for (int w = 0; w < wave; ++w) base = fmaxf(base, tmp[w]);
+  __syncthreads();
+  return fmaxf(base, prev);
+}
+
+// budget = ceil(fl(float32(p/100.0) * float32(U))).clamp(min=1)   (exact_2.py:329)
+__device__ __forceinline__ int64_t w_budget_of(int p, int64_t usize) {
+#pragma clang fp contract(off)
+  const float frac = (float)((double)p / 100.0);
+  const float prod = frac * (float)usize;
+  float b = ceilf(prod);
+  if (b < 1.0f) b = 1.0f;
+  return (int64_t)b;
+}
+
+// fp32 -> unsigned key with the same order (-0 folded into +0 first); key 0 marks "no key"
+__device__ __forceinline__ uint32_t order_key(float r) {
+  const uint32_t b = __float_as_uint(r + 0.0f);
+  return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+
+}  // namespace
+
+// LDS: per thread a contiguous key range of `per` keys at an odd row stride (conflict-free scans)
+size_t select_w_lds_bytes(int N, int k_max) {
+  const size_t per = (size_t)(N + 255) / 256;
+  return 256 * (per | 1) * 4 + (3 * 256 + 16 + 16 + 16) * 4 + 256 * 4 + (size_t)k_max * 8;
+}
+
+template <typename VT>
+__global__ __launch_bounds__(256) void select_w_kernel(SelectArgs a) {
+#pragma clang fp contract(off)
+  extern __shared__ __align__(16) uint32_t wsm[];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int h = blockIdx.x / a.nt, t = blockIdx.x % a.nt;
+  const int N = a.N, T = a.T;
+  const int per = (N + 255) / 256;
+  const int PS = per | 1;
+  uint32_t* rkb = wsm;                                   // 256 rows x PS order keys
+  uint32_t* myrow = rkb + tid * PS;                      // keys j0 .. j0 + per - 1
+  const uint32_t inv_per = per > 1 ? (uint32_t)((0x100000000ull + per - 1) / per) : 0u;
+  int* hist = (int*)(rkb + 256 * PS);                    // 3 x 256
+  int* tmp = hist + 3 * 256;                             // 16
+  int* misc = tmp + 16;                                  // 16
+  float* tmpf = (float*)(misc + 16);                     // 16
+  float* qnp = tmpf + 16;                                // T (<= 256)
+  int32_t* sidx = (int32_t*)(qnp + 256);                 // k_max
+  float* snp = (float*)(sidx + a.k_max);                 // k_max
+
+  const int64_t tstart = (int64_t)a.q_pos_base + (int64_t)t * T;          // exact_2.py:291
+  const int64_t lo = tstart - a.n_local + 1, hi_l = tstart + T - 1;
+  const int hi_keys = a.votes_dense ? N : (int)min((int64_t)N, tstart + T);
+  const int64_t roff = ((int64_t)h * a.nt + t) * a.votes_stride;
+  const VT* vrow = (const VT*)a.votes + roff;
+  const float* wrow = a.wvotes + roff;
+  const int j0 = tid * per, j1 = min(j0 + per, N);
+  auto is_forced = [&](int j) { return j < a.n_global || (j >= lo && j <= hi_l); };   // exact_2.py:290-293
+
+  // ---- stage the rank keys (coalesced: key j by thread j % 256), U = #(votes > 0) ----
+  int cu = 0;
+  for (int j = tid; j < 256 * per; j += 256) {
+    uint32_t key = 0;
+    if (j < N) {
+      const int v = j < hi_keys ? (int)vrow[j] : 0;
+      const float w = j < hi_keys ? wrow[j] : 0.0f;
+      cu += v > 0;                                                         // exact_2.py:296
+      const float tb = 1e-6f * (float)v;                                   // exact_2.py:302
+      key = order_key(w + tb);
+      if (a.votes_out) a.votes_out[((int64_t)h * a.nt + t) * N + j] = v;
+      if (a.wvotes_out) a.wvotes_out[((int64_t)h * a.nt + t) * N + j] = w;
+    }
+    const uint32_t row = per == 1 ? (uint32_t)j : __umulhi((uint32_t)j, inv_per);
+    rkb[row * PS + (j - row * per)] = key;
+  }
+  __syncthreads();
+  const int64_t usize = w_block_sum(cu, tmp);
+
+  // Order statistics for up to three targets at once: target t is the need[t]-th largest key
+  // (1 <= need[t] <= N).  The targets walk the radix tree together, one pass over the keys per
+  // 8-bit digit; targets whose prefixes coincide share a histogram (at most three distinct
+  // prefixes, and a key matches at most one of them).  Results: V[t] the key, GE[t] = #(keys >= V[t]).
+  auto kth_multi = [&](int ntarg, const int* need_in, uint32_t* V, int* GE) {
+    uint32_t prefix[3], pmask = 0;
+    int need[3], ge[3], hid[3];
+#pragma unroll
+    for (int u = 0; u < 3; ++u) { prefix[u] = 0; need[u] = u < ntarg ? need_in[u] : 1; ge[u] = 0; hid[u] = 0; }
+    for (int shift = 24; shift >= 0; shift -= 8) {
+      // distinct prefixes of this level -> histogram slots
+      // (fixed-bound loops: the small arrays stay in registers)
+      int nh = 0;
+      uint32_t hp[3] = {0u, 0u, 0u};
+#pragma unroll
+      for (int u = 0; u < 3; ++u) {
+        if (u < ntarg) {
+          int f = -1;
+#pragma unroll
+          for (int w = 0; w < 3; ++w) f = (f < 0 && w < nh && hp[w] == prefix[u]) ? w : f;
+          if (f < 0) {
+#pragma unroll
+            for (int w = 0; w < 3; ++w) hp[w] = w == nh ? prefix[u] : hp[w];
+            f = nh++;
+          }
+          hid[u] = f;
+        }
+      }
+      for (int i = tid; i < 256 * nh; i += 256) hist[i] = 0;
+      __syncthreads();
+      if (shift == 24) {
+        // the top digit (sign and high exponent bits) takes few values in a tile: one LDS atomic
+        // per distinct digit of a wave
+        for (int i = 0; i < per; ++i) {                  // same trip count on every lane
+          const uint32_t k = myrow[i];
+          bool act = k != 0 && j0 + i < N;
+          const int d = (int)(k >> 24);
+          uint64_t m = __ballot(act);
+          while (m) {
+            const int leader = __ffsll((unsigned long long)m) - 1;
+            const int dl = __shfl(d, leader, 64);
+            const uint64_t same = __ballot(act && d == dl);
+            if (lane == leader) atomicAdd(&hist[dl], (int)__popcll(same));
+            if (act && d == dl) act = false;
+            m &= ~same;
+          }
+        }
+      } else {
+        for (int i = 0; i < per; ++i) {
+          const uint32_t k = myrow[i];
+          if (k == 0 || j0 + i >= N) continue;
+          const uint32_t kp = k & pmask;
+#pragma unroll
+          for (int w = 0; w < 3; ++w)
+            if (w < nh && kp == hp[w]) atomicAdd(&hist[w * 256 + ((k >> shift) & 255u)], 1);
+        }
+      }
+      __syncthreads();
+#pragma unroll
+      for (int u = 0; u < 3; ++u) {
+        if (u < ntarg && tid < 64) {
+          // wave 0 finds target u's digit: lane l holds bins 255-4l .. 252-4l (descending)
+          const int* hu = hist + hid[u] * 256;
+          int c[4], sl = 0;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) { c[e] = hu[255 - 4 * lane - e]; sl += c[e]; }
+          int incl = sl;
+#pragma unroll
+          for (int o = 1; o < 64; o <<= 1) {
+            const int y = __shfl_up(incl, o, 64);
+            if (lane >= o) incl += y;
+          }
+          const uint64_t hit = __ballot(incl >= need[u]);
+          const int first = hit ? __ffsll((unsigned long long)hit) - 1 : 63;
+          if (lane == first) {
+            int acc = incl - sl, d = 255 - 4 * lane, e = 0;
+            for (; e < 3; ++e) {
+              if (acc + c[e] >= need[u]) break;
+              acc += c[e];
+              d -= 1;
+            }
+            misc[4 * u + 0] = d;
+            misc[4 * u + 1] = need[u] - acc;   // how far into digit d's keys the statistic lies
+            misc[4 * u + 2] = acc;             // keys with a larger digit (above the prefix range)
+            misc[4 * u + 3] = c[e];            // keys with digit d
+          }
+        }
+      }
+      __syncthreads();
+#pragma unroll
+      for (int u = 0; u < 3; ++u) {
+        if (u >= ntarg) continue;
+        prefix[u] |= (uint32_t)misc[4 * u] << shift;
+        ge[u] += misc[4 * u + 2];
+        need[u] = misc[4 * u + 1];
+        if (shift == 0) ge[u] += misc[4 * u + 3];   // the last digit's bin: the keys equal to V
+      }
+      pmask |= 255u << shift;
+      __syncthreads();
+    }
+#pragma unroll
+    for (int u = 0; u < 3; ++u)
+      if (u < ntarg) { V[u] = prefix[u]; GE[u] = ge[u]; }
+  };
+  auto kth = [&](int need) {
+    uint32_t V;
+    int GE;
+    kth_multi(1, &need, &V, &GE);
+    return make_int2((int)V, GE);
+  };
+  // forced keys whose rank lies below a cut (exact_2.py:332: kept = shared | forced)
+  const int gA = min(a.n_global, N);
+  const int bl = (int)max(lo, (int64_t)gA);
+  const int bh = (int)min(hi_l, (int64_t)N - 1);
+  const int nB = bh >= bl ? bh - bl + 1 : 0;
+  auto key_of = [&](int j) {
+    const uint32_t row = per == 1 ? (uint32_t)j : __umulhi((uint32_t)j, inv_per);
+    return rkb[row * PS + (j - row * per)];
+  };
+  auto forced_below = [&](uint32_t cut) {
+    int c = 0;
+    for (int i = tid; i < gA + nB; i += 256) {
+      const int j = i < gA ? i : bl + (i - gA);
+      c += key_of(j) < cut;
+    }
+    return w_block_sum(c, tmp);
+  };
+  const int nforced = gA + nB;
+
+  // ---- the 30 -> 25 -> 20 fallback (exact_2.py:328-350): every step's cut in one traversal ----
+  int resolved = 0, ch = 0, oflow = 0, forced_only = 0;
+  uint32_t cut = 0;
+  {
+    int needs[3];
+    uint32_t Vs[3];
+    int GEs[3];
+    for (int si = 0; si < a.nsteps; ++si) {
+      int64_t need = w_budget_of(a.steps[si], usize);
+      needs[si] = (int)(need > a.K_ord ? a.K_ord : need);                 // exact_2.py:330
+    }
+    kth_multi(a.nsteps, needs, Vs, GEs);
+    for (int si = 0; si < a.nsteps; ++si) {
+      const int p = a.steps[si];
+      const int64_t size = (int64_t)GEs[si] + forced_below(Vs[si]);
+      if (p == a.start_pct) oflow = size > a.k_max;
+      if (!resolved) {
+        cut = Vs[si];
+        if (size <= a.k_max) { resolved = 1; ch = p; }
+      }
+    }
+  }
+  if (a.start_pct == 0) {                                                   // exact_2.py:343-346
+    oflow = nforced > a.k_max;
+    if (!resolved) forced_only = 1;
+  }
+  int kmeas = ch;
+  if (a.measure && !resolved) {                                             // exact_2.py:357-371
+    const int floor_pct = a.steps[a.nsteps - 1];
+    for (int p = floor_pct - 1; p > 0; --p) {
+      int64_t need = w_budget_of(p, usize);
+      need = need > a.K_ord ? a.K_ord : need;
+      const int2 r = kth((int)need);
+      if ((int64_t)r.y + forced_below((uint32_t)r.x) <= a.k_max) { kmeas = p; break; }
+    }
+  }
+
+  // ---- compaction + reposition (exact_2.py:383-412) ----
+  auto kept_of = [&](int j) { return is_forced(j) || (!forced_only && myrow[j - j0] >= cut); };
+  int cnt = 0, csh = 0;
+  for (int j = j0; j < j1; ++j) {
+    cnt += kept_of(j);
+    csh += !forced_only && myrow[j - j0] >= cut;
+  }
+  const int base = w_block_exclusive_sum(cnt, tmp);
+  const int kept_total = w_block_sum(cnt, tmp);
+  const int shared_total = w_block_sum(csh, tmp);
+  float mloc = -INFINITY;
+  {
+    int rank = base - 1;
+    for (int j = j0; j < j1; ++j) {
+      if (kept_of(j)) {
+        rank += 1;
+        const float cp = (float)j * a.pos_scale;        // exact_2.py:384
+        mloc = fmaxf(mloc, cp - (float)rank);           // exact_2.py:385
+      }
+    }
+  }
+  float run = w_block_exclusive_max(mloc, tmpf);
+  const int qlo = (int)min(tstart, (int64_t)N - 1);
+  const int qhi = (int)min(tstart + T - 1, (int64_t)N - 1);
+  {
+    int rank = base - 1;
+    for (int j = j0; j < j1; ++j) {
+      const bool kept = kept_of(j);
+      if (kept) {
+        rank += 1;
+        const float cp = (float)j * a.pos_scale;
+        run = fmaxf(run, cp - (float)rank);
+      }
+      const float np = (float)rank + run;              // exact_2.py:386
+      if (kept && rank < a.k_max) { sidx[rank] = j; snp[rank] = np; }
+      if (j >= qlo && j <= qhi) qnp[j - qlo] = np;
+    }
+  }
+  __syncthreads();
+  const int nvalid = min(kept_total, a.k_max);
+  int32_t* irow = a.idx + ((int64_t)h * a.nt + t) * a.k_max;
+  float* nkrow = a.newpos_k + ((int64_t)h * a.nt + t) * a.k_max;
+  for (int s = tid; s < a.k_max; s += 256) {          // exact_2.py:401-408
+    irow[s] = s < nvalid ? sidx[s] : N;
+    nkrow[s] = s < nvalid ? snp[s] : 0.0f;
+  }
+  float* nqrow = a.newpos_q + ((int64_t)h * a.nt + t) * T;
+  for (int i = tid; i < T; i += 256) {                  // exact_2.py:410-412
+    const int qp = (int)min(tstart + i, (int64_t)N - 1);
+    nqrow[i] = qnp[qp - qlo];
+  }
+  if (tid == 0) {
+    const int o = h * a.nt + t;
+    a.shared_size[o] = shared_total;
+    a.kept_size[o] = kept_total;
+    a.chosen[o] = ch;
+    a.orig_overflow[o] = (uint8_t)oflow;
+    a.overflow20[o] = (uint8_t)(oflow && !resolved);   // exact_2.py:354
+    a.kpct_meas[o] = kmeas;
+  }
+}
+
+hipError_t launch_select_weighted(const SelectArgs& a, int vote_bytes, hipStream_t st) {
+  const size_t lds = select_w_lds_bytes(a.N, a.k_max);
+  if (lds > 160 * 1024 || a.T > 256 || !a.wvotes) return hipErrorInvalidValue;
+  if (vote_bytes == 1) {
+    hipError_t e = hipFuncSetAttribute((const void*)select_w_kernel<uint8_t>,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(select_w_kernel<uint8_t>, dim3(a.H * a.nt), dim3(256), lds, st, a);
+  } else {
+    hipError_t e = hipFuncSetAttribute((const void*)select_w_kernel<int32_t>,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(select_w_kernel<int32_t>, dim3(a.H * a.nt), dim3(256), lds, st, a);
+  }
+  return hipGetLastError();
+}
+
+}  // namespace sta

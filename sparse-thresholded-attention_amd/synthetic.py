@@ -77,7 +77,7 @@ class Config:
     n_global: int = 32
     n_local: int = 32
     variant: str = "shared"     # "shared" (tile-shared sets), "pq" (PQ Union), "pqstream", "dca"
-    select_score: str = "freq"  # overflow ranking of the per-query variant
+    select_score: str = "freq"  # key ranking: votes, or margin / expmass weighted votes
     dca: tuple = None           # (chunk_size, pretrain_len, local_window) of the DCA variant
 
     def geometry(self):
@@ -102,6 +102,9 @@ CONFIGS = {
     # 1: PI_exact Llama-2-7B layer, 4096 -> 12288
     "c1": Config("c1_pi_exact_32h_d128_12k_bf16", 32, 32, 12288, 128, torch.bfloat16, 64, 5.0, 0.01,
                  10000.0, pi_pos_scale(4096, 12288)),
+    # 1e: config 1 ranked by expmass weighted votes (select_score="expmass", the harness default)
+    "c1e": Config("c1e_pi_exact_expmass_32h_d128_12k_bf16", 32, 32, 12288, 128, torch.bfloat16, 64, 5.0, 0.01,
+                  10000.0, pi_pos_scale(4096, 12288), select_score="expmass"),
     # 2: YaRN_exact Llama-3-8B GQA layer, factor 4 from 8192
     "c2": Config("c2_yarn_exact_32q8kv_d128_32k_bf16", 32, 8, 32768, 128, torch.bfloat16, 64, 5.0, 0.005,
                  500000.0, 1.0, yarn=(4.0, 8192, 32.0, 1.0)),
