@@ -472,10 +472,10 @@ __global__ __launch_bounds__(256, 1) void score_kernel(ScoreArgs a) {
   // into the low `ib` mantissa bits (a relative change below 2^(ib-23), added to E).  After the
   // sweep the candidates -- slot values within 2 E of the row maximum -- are evaluated exactly as
   // fp32 dot products of the (hi + lo) operands, and the row maximum is their maximum.  A slot
-  // whose third value is a candidate may hide a fourth, and a row may collect more than CMAX
+  // whose third value is a candidate may hide a fourth, and a wave may collect more than FMAX
   // candidates: then the whole workgroup runs the three-product sweep instead (a few percent of
   // workgroups on Gaussian inputs; always on inputs with many tied scores).
-  constexpr int CMAX = 8;                        // candidates evaluated per row
+  constexpr int FMAX = 512;                      // candidate (row, key) pairs per wave
   constexpr int LOADS_H = LOADS / 2;             // 1 KB copies per wave per chunk, hi halves only
   static_assert(LOADS_H * NW * 2 * 64 == CHUNK_UNITS, "hi-half copies");
   auto issue_hi = [&](int c, u32x4* dst) {
@@ -635,10 +635,17 @@ __global__ __launch_bounds__(256, 1) void score_kernel(ScoreArgs a) {
     wait_hi(0);        // the stray copies past the last chunk
     __syncthreads();
 
-    // ---- candidates: per row, slot values within 2 E of the row's largest s1 ----
-    int* cnt = (int*)&lds[0][0] + wave * (64 + 64 * CMAX);   // this wave's 64 row counters
-    int* ckeys = cnt + 64;                                     // 64 rows x CMAX candidate keys
-    cnt[lane] = 0;
+    // ---- candidates: per row, slot values within 2 E of the row's largest s1, into one flat
+    // (row, key) list per wave ----
+    constexpr int WR = 32 * RB;                                // rows of a wave
+    static_assert((2 + WR + 2 * FMAX) * 4 * NW <= (int)sizeof(lds), "candidate lists fit the chunk buffers");
+    int* wl = (int*)&lds[0][0] + wave * (2 + WR + 2 * FMAX);
+    int* nflat = wl;                                           // list length
+    uint32_t* rowbest = (uint32_t*)(wl + 2);                  // WR rows: order key of the max
+    int* frow = wl + 2 + WR;                                   // FMAX rows
+    int* fkey = frow + FMAX;                                   // FMAX keys
+    if (lane == 0) nflat[0] = 0;
+    for (int r = lane; r < WR; r += 64) rowbest[r] = 0u;
     const float2 kn = a.knorm_max[kvh];
     // 2^-14 covers the fp32 accumulation of s1 and of the exact dots; 2^(ib-23) the packing
     const float gam = 0x1p-14f + __uint_as_float((uint32_t)(127 + a.ib - 23) << 23);
@@ -664,66 +671,71 @@ __global__ __launch_bounds__(256, 1) void score_kernel(ScoreArgs a) {
 #pragma unroll
           for (int k3 = 0; k3 < 3; ++k3) {
             if (tv[k3] >= thr) {
-              const int sl = atomicAdd(&cnt[row], 1);
-              if (sl < CMAX) ckeys[row * CMAX + sl] = (int)(((__float_as_uint(tv[k3]) & blk_mask) << 5) | col);
+              const int f = atomicAdd(nflat, 1);
+              if (f < FMAX) {
+                frow[f] = row;
+                fkey[f] = (int)(((__float_as_uint(tv[k3]) & blk_mask) << 5) | col);
+              }
             }
           }
         }
-#pragma unroll
-      for (int rb = 0; rb < RB; ++rb) amb |= cnt[rb * 32 + (lane & 31)] > CMAX;
     }
+    __syncthreads();
+    const int total = nflat[0];
+    amb |= total > FMAX;
     if (__syncthreads_or(amb)) return true;
 
-    // ---- exact dots of the candidates: lanes r and r + 32 own row rb*32 + r, half the dims each ----
+    // ---- exact dots of the candidates: pair f is evaluated by lanes f % 32 and f % 32 + 32,
+    // each over half of the dims (the fragment layout's lane halves), 32 pairs per round ----
     if (active) {
-      float best[RB];
+      const int g = lane >> 5;
+      for (int it = 0; it * 32 < total; ++it) {
+        const int f = it * 32 + (lane & 31);
+        const bool valid = f < total;
+        const int row = valid ? frow[f] : 0;
+        const int key = valid ? fkey[f] : 0;
+        const int qr = wrow0 + row;
+        const u32x4* qp = a.qfrag + (((int64_t)h * (a.q_rows_pad >> 5) + (qr >> 5)) * S) * 128 + (qr & 31) + 32 * g;
+        const u32x4* kp = kbase + (int64_t)(key >> 5) * S * 128 + (key & 31) + 32 * g;
+        u32x4 qh[S], ql[S], kh[S], kl[S];
 #pragma unroll
-      for (int rb = 0; rb < RB; ++rb) {
-        best[rb] = 0.0f;
-        if (wrow0 + 32 * rb >= a.N) continue;   // no row of this block votes
-        const int R = rb * 32 + (lane & 31);
-        const int n = cnt[R];
-        int nmax = n;
-#pragma unroll
-        for (int o = 1; o < 32; o <<= 1) nmax = max(nmax, __shfl_xor(nmax, o, 64));
-        // this lane's Q units of row R, reloaded (the AGPR copies feed only the MFMAs)
-        u32x4 qh[S], ql[S];
-        {
-          const int64_t u0 = (((int64_t)h * (a.q_rows_pad >> 5) + wrow0 / 32 + rb) * S) * 128 + lane;
-#pragma unroll
-          for (int s = 0; s < S; ++s) { qh[s] = a.qfrag[u0 + s * 128]; ql[s] = a.qfrag[u0 + s * 128 + 64]; }
+        for (int s = 0; s < S; ++s) {
+          qh[s] = qp[s * 128];
+          ql[s] = qp[s * 128 + 64];
+          kh[s] = kp[s * 128];
+          kl[s] = kp[s * 128 + 64];
         }
-        float bv = -INFINITY;
-#pragma unroll 1
-        for (int j = 0; j < nmax; ++j) {
-          const int key = j < n ? ckeys[R * CMAX + j] : 0;
-          const u32x4* kp = kbase + (int64_t)(key >> 5) * S * 128 + (key & 31) + 32 * (lane >> 5);
-          u32x4 kh[S], kl[S];
+        float acc = 0.0f;
 #pragma unroll
-          for (int s = 0; s < S; ++s) { kh[s] = kp[s * 128]; kl[s] = kp[s * 128 + 64]; }
-          float acc = 0.0f;
+        for (int s = 0; s < S; ++s) {
 #pragma unroll
-          for (int s = 0; s < S; ++s) {
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              const float x0 = __uint_as_float(qh[s][e] << 16) + __uint_as_float(ql[s][e] << 16);
-              const float x1 = __uint_as_float(qh[s][e] & 0xffff0000u) + __uint_as_float(ql[s][e] & 0xffff0000u);
-              const float y0 = __uint_as_float(kh[s][e] << 16) + __uint_as_float(kl[s][e] << 16);
-              const float y1 = __uint_as_float(kh[s][e] & 0xffff0000u) + __uint_as_float(kl[s][e] & 0xffff0000u);
-              acc = fmaf(x0, y0, acc);
-              acc = fmaf(x1, y1, acc);
-            }
+          for (int e = 0; e < 4; ++e) {
+            const float x0 = __uint_as_float(qh[s][e] << 16) + __uint_as_float(ql[s][e] << 16);
+            const float x1 = __uint_as_float(qh[s][e] & 0xffff0000u) + __uint_as_float(ql[s][e] & 0xffff0000u);
+            const float y0 = __uint_as_float(kh[s][e] << 16) + __uint_as_float(kl[s][e] << 16);
+            const float y1 = __uint_as_float(kh[s][e] & 0xffff0000u) + __uint_as_float(kl[s][e] & 0xffff0000u);
+            acc = fmaf(x0, y0, acc);
+            acc = fmaf(x1, y1, acc);
           }
-          const float tot = acc + __shfl_xor(acc, 32, 64);
-          if (j < n) bv = fmaxf(bv, tot);
         }
-        best[rb] = bv;
+        const float tot = acc + __shfl_xor(acc, 32, 64);
+        // order-preserving key of an fp32 value (every key of a real value is nonzero)
+        const uint32_t tb = __float_as_uint(tot + 0.0f);
+        const uint32_t okey = (tb & 0x80000000u) ? ~tb : (tb | 0x80000000u);
+        if (valid && g == 0) atomicMax(&rowbest[row], okey);
       }
-      // every slot takes its row's exact maximum from the row's owner lane
+    }
+    __syncthreads();
+    if (active) {
+      // every slot takes its row's exact maximum
 #pragma unroll
       for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
-        for (int i = 0; i < 16; ++i) mx[rb][i] = __shfl(best[rb], (i >> 2) * 8 + (lane >> 5) * 4 + (i & 3), 64);
+        for (int i = 0; i < 16; ++i) {
+          const uint32_t k = rowbest[rb * 32 + (i >> 2) * 8 + (lane >> 5) * 4 + (i & 3)];
+          const uint32_t b = (k & 0x80000000u) ? (k & 0x7fffffffu) : ~k;
+          mx[rb][i] = k ? __uint_as_float(b) : 0.0f;   // 0: a padded row, never used
+        }
     }
     __syncthreads();   // the candidate lists are read before the next sweep's copies land
     return false;
