@@ -274,6 +274,70 @@ size_t sta_dca_workspace_size(const sta_dca_args* args);
  * 278-366, 372-489 (the module the reference installs with install_dca_forward, :660-663). */
 int sta_dca_attention(const sta_dca_args* args, void* stream);
 
+/* ------------------------------------------------------------------------------------------ */
+/* Decode: each query selects its own key set over the KV cache and attends it.  A batch of Q   */
+/* queries shares one cache of M raw (unrotated) keys; query i sits at position q_pos0 + i and  */
+/* sees the keys [0, m_i), m_i = M - (Q - 1 - i): the cache prefix K[:, :P + 1] of the         */
+/* reference's per-token loop when q_pos0 + Q == M.  Q = 1 is one call of the reference on M   */
+/* keys at q_pos = q_pos0.  Selection: keep s >= max - tau, the top pct_decode% of those by    */
+/* score when pct_decode < 100, plus the forced keys [0, n_global) U [q_pos - n_local + 1,     */
+/* q_pos]; above k_max the forced keys and the best-scored others (tie-inclusive); positions   */
+/* repositioned as in the prefill (pos_scale); idx ascending, truncated to k_max, sentinel m_i. */
+/* ------------------------------------------------------------------------------------------ */
+typedef struct sta_decode_args {
+  const void* q;            /* (H, Q, D) raw queries */
+  const void* k;            /* (Hkv, M, D) raw cache */
+  const void* v;            /* (Hkv, M, D) */
+  int64_t q_head_stride, q_tok_stride;
+  int64_t k_head_stride, k_tok_stride;
+  int64_t v_head_stride, v_tok_stride;
+  int32_t dtype;
+  int32_t H, Hkv, Q, M, D;
+  const float* tau;         /* (H,) */
+  const float* inv_freq;    /* (D/2,) */
+  float pos_scale, rope_scale, sm_scale;
+  int32_t q_pos0;           /* position of query 0; q_pos0 + Q <= M (any q_pos0 >= 0 for the
+                               scores alone) */
+  int32_t n_global, n_local, k_max;
+  double pct_decode;        /* the reference's pct_decode (100 = keep every passer) */
+  int32_t causal;           /* attend: 0 masks sentinel slots only (_decode_attend_torch); 1 also
+                               slots past the query's position (Kernel C, _decode_attend_kernelC) */
+  /* outputs (device) */
+  void* out;                /* (H, Q, D) contiguous, input dtype */
+  int32_t* idx;             /* (H, Q, k_max) ascending kept positions, sentinel m_i */
+  float* newpos_k;          /* (H, Q, k_max) repositioned key positions, 0 at sentinels */
+  float* newpos_q;          /* (H, Q) repositioned query positions */
+  /* optional outputs (NULL to skip) */
+  int32_t* set_size;        /* (H, Q) |selected set| before the truncation to k_max */
+  float* scores;            /* (H, Q, M) per-key scores; entries past m_i are not written */
+  void* workspace;
+  size_t workspace_bytes;
+  void* const* stage_events; /* NULL or 4 hipEvent_t: before the scores, before the selection,
+                                before the attend, after it */
+} sta_decode_args;
+
+/* Bytes of device workspace the decode entry points need for these arguments. */
+size_t sta_decode_workspace_size(const sta_decode_args* args);
+
+/* Per-key scores of every query under (inv_freq, pos_scale, rope_scale) into `scores`
+ * (H, Q, M) fp32 (row (h, i) written for keys < m_i).
+ * Replaces _decode_scores_kernel / _decode_select_kernel, shared_selection_triton_exact_2.py:
+ * 235-271, 505-525. */
+int sta_decode_scores(const sta_decode_args* args, float* scores, void* stream);
+
+/* Selection from given scores (H, Q, M): writes idx, newpos_k, newpos_q (and set_size).
+ * Replaces _decode_build_sets, shared_selection_triton_exact_2.py:527-604. */
+int sta_decode_build_sets(const sta_decode_args* args, const float* scores, void* stream);
+
+/* Attend over idx / newpos_k / newpos_q (set_size, when non-NULL, bounds the slots swept).
+ * Replaces _decode_attend_torch (causal = 0) and _decode_attend_kernelC (causal = 1),
+ * shared_selection_triton_exact_2.py:608-655. */
+int sta_decode_attend(const sta_decode_args* args, void* stream);
+
+/* Scores, selection and attend in one call: the body of the decode branch of spi_forward,
+ * shared_selection_triton_exact_2.py:734-762, for all Q queries at once. */
+int sta_decode_attention(const sta_decode_args* args, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -16,6 +16,10 @@ next to it).  Each function names the reference lines it restates:
   gather_attn_mask <- shared_selection_triton_perquery.py:226-312 (PQ Union Kernel C)
   shared_pq_attention <- shared_selection_triton_perquery.py:459-525 (composition)
   pqstream     <- pqstream_kernel.py:174-368, 498-564 (the fused PQ Stream kernel)
+  decode_scores     <- shared_selection_triton_exact_2.py:235-271, 505-525 (_decode_select_kernel)
+  decode_build_sets <- shared_selection_triton_exact_2.py:527-604 (_decode_build_sets)
+  decode_attend     <- shared_selection_triton_exact_2.py:608-623 (_decode_attend_torch) and, with
+                       causal=True, the slot rule of _decode_attend_kernelC (:626-655)
 
 Arrays are numpy.  Half-precision tensors travel as uint16 bit patterns with a dtype code:
 0 = fp32, 1 = bf16, 2 = fp16.
@@ -43,7 +47,7 @@ def lib():
     global _LIB
     if _LIB is None:
         path = os.path.join(_HERE, "libsta_oracle.so")
-        srcs = ["sta_oracle.c", "sta_oracle_pq.c", "sta_oracle_common.h"]
+        srcs = ["sta_oracle.c", "sta_oracle_pq.c", "sta_oracle_decode.c", "sta_oracle_common.h"]
         if not os.path.exists(path) or any(os.path.getmtime(path) < os.path.getmtime(
                 os.path.join(_HERE, f)) for f in srcs):
             build()
@@ -381,4 +385,56 @@ def dca_attention(q, k, v, dtype, inv_freq, chunk_size, pretrain_len, local_wind
                      ctypes.c_int(N), ctypes.c_int(D), _p(_c(inv_freq, np.float32)), ctypes.c_int(chunk_size),
                      ctypes.c_int(local_window), ctypes.c_float(ms), ctypes.c_float(scale), _p(r),
                      ctypes.c_int(len(r) if r is not None else 0), _p(out))
+    return out
+
+
+# ---------------------------------------------------------------------------------------------
+# decode: a batch of Q queries over one cache of M keys; query i at position q_pos0 + i sees the
+# keys [0, M - (Q - 1 - i)) (the cache prefix of spi_forward's per-token loop, exact_2.py:743-745)
+# ---------------------------------------------------------------------------------------------
+def decode_scores(q, k, dtype, inv_freq, pos_scale, rope_scale, sm_scale, q_pos0):
+    """q (H,Q,D), k (Hkv,M,D) -> scores (H,Q,M) fp32, NaN past each query's key range."""
+    q = np.ascontiguousarray(q)
+    k = np.ascontiguousarray(k)
+    H, Q, D = q.shape
+    Hkv, M = k.shape[0], k.shape[1]
+    out = np.empty((H, Q, M), np.float32)
+    lib().oracle_decode_scores(_p(q), _p(k), ctypes.c_int(dtype), ctypes.c_int(H), ctypes.c_int(Hkv),
+                               ctypes.c_int(Q), ctypes.c_int(M), ctypes.c_int(D), _p(_c(inv_freq, np.float32)),
+                               ctypes.c_float(pos_scale), ctypes.c_float(rope_scale), ctypes.c_float(sm_scale),
+                               ctypes.c_int(q_pos0), _p(out))
+    return out
+
+
+def decode_build_sets(scores, tau, q_pos0, pos_scale, n_global, n_local, k_max, pct_decode=100.0):
+    """_decode_build_sets from scores (H,Q,M) -> idx (H,Q,k_max) int32 (sentinel m_i),
+    newpos_k (H,Q,k_max), newpos_q (H,Q), set_size (H,Q) (|set| before the k_max truncation)."""
+    scores = _c(scores, np.float32)
+    H, Q, M = scores.shape
+    idx = np.empty((H, Q, k_max), np.int32)
+    npk = np.empty((H, Q, k_max), np.float32)
+    npq = np.empty((H, Q), np.float32)
+    size = np.empty((H, Q), np.int32)
+    lib().oracle_decode_build_sets(_p(scores), ctypes.c_int(H), ctypes.c_int(Q), ctypes.c_int(M),
+                                   _p(_c(tau, np.float32)), ctypes.c_int(q_pos0), ctypes.c_float(pos_scale),
+                                   ctypes.c_int(n_global), ctypes.c_int(n_local), ctypes.c_int(k_max),
+                                   ctypes.c_double(pct_decode), _p(idx), _p(npk), _p(npq), _p(size))
+    return idx, npk, npq, size
+
+
+def decode_attend(q, k, v, dtype, inv_freq, rope_scale, sm_scale, q_pos0, idx, newpos_k, newpos_q,
+                  causal=False):
+    """Attention of each query over its slots -> (H,Q,D) fp32 before the cast to the dtype."""
+    q = np.ascontiguousarray(q)
+    k = np.ascontiguousarray(k)
+    v = np.ascontiguousarray(v)
+    H, Q, D = q.shape
+    Hkv, M = k.shape[0], k.shape[1]
+    k_max = idx.shape[-1]
+    out = np.empty((H, Q, D), np.float32)
+    lib().oracle_decode_attend(_p(q), _p(k), _p(v), ctypes.c_int(dtype), ctypes.c_int(H), ctypes.c_int(Hkv),
+                               ctypes.c_int(Q), ctypes.c_int(M), ctypes.c_int(D), _p(_c(inv_freq, np.float32)),
+                               ctypes.c_float(rope_scale), ctypes.c_float(sm_scale), ctypes.c_int(q_pos0),
+                               ctypes.c_int(k_max), _p(_c(idx, np.int32)), _p(_c(newpos_k, np.float32)),
+                               _p(_c(newpos_q, np.float32)), ctypes.c_int(int(bool(causal))), _p(out))
     return out

@@ -20,7 +20,8 @@ EXPORTS = ["sta_abi_version", "sta_last_error", "sta_shared_workspace_size", "st
            "sta_select_vote", "sta_build_sets", "sta_build_sets_weighted", "sta_gather_attention",
            "sta_pq_workspace_size", "sta_pq_attention", "sta_pq_select_bits", "sta_pq_build_sets",
            "sta_pq_gather_attention", "sta_pqstream_workspace_size", "sta_pqstream_attention",
-           "sta_dca_workspace_size", "sta_dca_attention"]
+           "sta_dca_workspace_size", "sta_dca_attention", "sta_decode_workspace_size", "sta_decode_scores",
+           "sta_decode_build_sets", "sta_decode_attend", "sta_decode_attention"]
 SCORES = {"freq": 0, "margin": 1, "expmass": 2}
 
 
@@ -114,6 +115,26 @@ class DcaArgsC(ctypes.Structure):
     ]
 
 
+class DecodeArgsC(ctypes.Structure):
+    """Mirror of sta_decode_args (include/sta.h)."""
+    _fields_ = [
+        ("q", ctypes.c_void_p), ("k", ctypes.c_void_p), ("v", ctypes.c_void_p),
+        ("q_head_stride", ctypes.c_int64), ("q_tok_stride", ctypes.c_int64),
+        ("k_head_stride", ctypes.c_int64), ("k_tok_stride", ctypes.c_int64),
+        ("v_head_stride", ctypes.c_int64), ("v_tok_stride", ctypes.c_int64),
+        ("dtype", ctypes.c_int32), ("H", ctypes.c_int32), ("Hkv", ctypes.c_int32),
+        ("Q", ctypes.c_int32), ("M", ctypes.c_int32), ("D", ctypes.c_int32),
+        ("tau", ctypes.c_void_p), ("inv_freq", ctypes.c_void_p),
+        ("pos_scale", ctypes.c_float), ("rope_scale", ctypes.c_float), ("sm_scale", ctypes.c_float),
+        ("q_pos0", ctypes.c_int32), ("n_global", ctypes.c_int32), ("n_local", ctypes.c_int32),
+        ("k_max", ctypes.c_int32), ("pct_decode", ctypes.c_double), ("causal", ctypes.c_int32),
+        ("out", ctypes.c_void_p), ("idx", ctypes.c_void_p), ("newpos_k", ctypes.c_void_p),
+        ("newpos_q", ctypes.c_void_p), ("set_size", ctypes.c_void_p), ("scores", ctypes.c_void_p),
+        ("workspace", ctypes.c_void_p), ("workspace_bytes", ctypes.c_size_t),
+        ("stage_events", ctypes.c_void_p),
+    ]
+
+
 def lib():
     """Load libsta_hip.so once; raise loudly if it is absent."""
     global _LIB
@@ -153,6 +174,16 @@ def lib():
         L.sta_dca_workspace_size.argtypes = [ctypes.POINTER(DcaArgsC)]
         L.sta_dca_attention.restype = ctypes.c_int
         L.sta_dca_attention.argtypes = [ctypes.POINTER(DcaArgsC), ctypes.c_void_p]
+        L.sta_decode_workspace_size.restype = ctypes.c_size_t
+        L.sta_decode_workspace_size.argtypes = [ctypes.POINTER(DecodeArgsC)]
+        for name in ("sta_decode_attend", "sta_decode_attention"):
+            fn = getattr(L, name)
+            fn.restype = ctypes.c_int
+            fn.argtypes = [ctypes.POINTER(DecodeArgsC), ctypes.c_void_p]
+        for name in ("sta_decode_scores", "sta_decode_build_sets"):
+            fn = getattr(L, name)
+            fn.restype = ctypes.c_int
+            fn.argtypes = [ctypes.POINTER(DecodeArgsC), ctypes.c_void_p, ctypes.c_void_p]
         if L.sta_abi_version() != 2:
             raise ImportError("libsta_hip.so ABI version mismatch")
         _LIB = L
@@ -692,3 +723,116 @@ class DcaPlan:
 def dca_attention(q, k, v, inv_freq, chunk_size, pretrain_len, local_window, scale=None):
     """The DCA prefill on the device; returns out (H, N, D) in q.dtype."""
     return DcaPlan(q, k, v, inv_freq, chunk_size, pretrain_len, local_window, scale).run()["out"]
+
+
+# ---------------------------------------------------------------------------------------------
+# decode: Q queries over one cache of M keys, query i at position q_pos0 + i seeing the keys
+# [0, M - (Q - 1 - i))
+# ---------------------------------------------------------------------------------------------
+def _queries_view(x):
+    """(H, D) one query per head, (H, Q, D) or (1, H, Q, D) -> (H, Q, D) with unit dim stride."""
+    if x.dim() == 2:
+        x = x.unsqueeze(1)
+    return _heads_view(x)
+
+
+class DecodePlan:
+    """Outputs and workspace of the decode path for one shape, allocated once; run() launches the
+    scores, the selection and the attend on the current stream and allocates nothing."""
+
+    def __init__(self, q, k, v, tau, inv_freq, q_pos0, pos_scale=1.0, rope_scale=1.0, sm_scale=None,
+                 n_global=32, n_local=32, k_max=1024, pct_decode=100.0, causal=False, want_scores=False):
+        if not q.is_cuda:
+            raise RuntimeError("sparse-thresholded attention runs on a HIP device only; got a CPU tensor")
+        if q.dtype not in DTYPES:
+            raise TypeError(f"unsupported dtype {q.dtype}")
+        dev = q.device
+        qh = _queries_view(q)
+        kh = _heads_view(k.to(dev))
+        vh = _heads_view(v.to(dev)) if v is not None else None
+        if kh.dtype != qh.dtype or (vh is not None and vh.dtype != qh.dtype):
+            raise TypeError("q, k and v must share one dtype")
+        H, Q, D = qh.shape
+        M = kh.shape[1]
+        self.device = dev
+        if sm_scale is None:
+            sm_scale = 1.0 / math.sqrt(D)
+        tau = tau.to(device=dev, dtype=torch.float32).reshape(-1).contiguous()
+        if tau.numel() == 1 and H > 1:
+            tau = tau.expand(H).contiguous()
+        ifr = inv_freq.to(device=dev, dtype=torch.float32).contiguous()
+        self.args = a = DecodeArgsC()
+        a.q, a.k = _ptr(qh), _ptr(kh)
+        a.v = _ptr(vh) if vh is not None else None
+        a.q_head_stride, a.q_tok_stride = qh.stride(0), qh.stride(1)
+        a.k_head_stride, a.k_tok_stride = kh.stride(0), kh.stride(1)
+        if vh is not None:
+            a.v_head_stride, a.v_tok_stride = vh.stride(0), vh.stride(1)
+        a.dtype = DTYPES[qh.dtype]
+        a.H, a.Hkv, a.Q, a.M, a.D = H, kh.shape[0], Q, M, D
+        a.tau, a.inv_freq = _ptr(tau), _ptr(ifr)
+        a.pos_scale, a.rope_scale, a.sm_scale = float(pos_scale), float(rope_scale), float(sm_scale)
+        a.q_pos0, a.n_global, a.n_local, a.k_max = int(q_pos0), int(n_global), int(n_local), int(k_max)
+        a.pct_decode, a.causal = float(pct_decode), int(bool(causal))
+        self._keep = (qh, kh, vh, tau, ifr)
+        self.out = {
+            "out": torch.empty((H, Q, D), dtype=qh.dtype, device=dev),
+            "idx": torch.empty((H, Q, k_max), dtype=torch.int32, device=dev),
+            "newpos_k": torch.empty((H, Q, k_max), dtype=torch.float32, device=dev),
+            "newpos_q": torch.empty((H, Q), dtype=torch.float32, device=dev),
+            "set_size": torch.empty((H, Q), dtype=torch.int32, device=dev),
+        }
+        if want_scores:
+            self.out["scores"] = torch.empty((H, Q, M), dtype=torch.float32, device=dev)
+        for name in ("out", "idx", "newpos_k", "newpos_q", "set_size"):
+            setattr(a, name, _ptr(self.out[name]))
+        a.scores = _ptr(self.out.get("scores"))
+        n = lib().sta_decode_workspace_size(ctypes.byref(a))
+        if n == 0:
+            _check(-1, "sta_decode_workspace_size")
+        self.workspace = torch.empty(n, dtype=torch.uint8, device=dev)
+        a.workspace, a.workspace_bytes = _ptr(self.workspace), n
+        self._events = None
+
+    def run(self, events=None):
+        """events: None or 4 recorded torch.cuda.Event(enable_timing=True) marking the stages."""
+        if events is not None:
+            self._events = (ctypes.c_void_p * 4)(*[e.cuda_event for e in events])
+            self.args.stage_events = ctypes.cast(self._events, ctypes.c_void_p)
+        else:
+            self.args.stage_events = None
+        _check(lib().sta_decode_attention(ctypes.byref(self.args), _stream(self.device)), "sta_decode_attention")
+        return self.out
+
+    def scores(self, out):
+        """Scores alone into out (H, Q, M) fp32."""
+        _check(lib().sta_decode_scores(ctypes.byref(self.args), _ptr(out), _stream(self.device)),
+               "sta_decode_scores")
+        return out
+
+    def build_sets(self, scores):
+        """Selection alone from scores (H, Q, M) fp32 into idx / newpos_k / newpos_q / set_size."""
+        _check(lib().sta_decode_build_sets(ctypes.byref(self.args), _ptr(scores), _stream(self.device)),
+               "sta_decode_build_sets")
+        return self.out
+
+    def attend(self, idx, newpos_k, newpos_q, set_size=None):
+        """Attend alone over given sets (H, Q, k_max) int32 / fp32 and (H, Q) fp32 into out."""
+        a = self.args
+        saved = (a.idx, a.newpos_k, a.newpos_q, a.set_size)
+        a.idx, a.newpos_k, a.newpos_q = _ptr(idx), _ptr(newpos_k), _ptr(newpos_q)
+        a.set_size = _ptr(set_size)
+        try:
+            _check(lib().sta_decode_attend(ctypes.byref(a), _stream(self.device)), "sta_decode_attend")
+        finally:
+            a.idx, a.newpos_k, a.newpos_q, a.set_size = saved
+        return self.out["out"]
+
+
+def decode_attention(q, k, v, tau, inv_freq, q_pos0, pos_scale=1.0, rope_scale=1.0, sm_scale=None,
+                     n_global=32, n_local=32, k_max=1024, pct_decode=100.0, causal=False, want_scores=False):
+    """Scores, selection and attend of Q queries (H, Q, D) over the cache k, v (Hkv, M, D).
+    Returns a dict of device tensors: out (H, Q, D), idx (H, Q, k_max) int32 (sentinel m_i),
+    newpos_k, newpos_q, set_size and, with want_scores, scores (H, Q, M)."""
+    return DecodePlan(q, k, v, tau, inv_freq, q_pos0, pos_scale, rope_scale, sm_scale, n_global, n_local,
+                      k_max, pct_decode, causal, want_scores).run()

@@ -1,0 +1,186 @@
+// sta_api_decode.hip -- the C ABI of the decode path (include/sta.h, sta_decode_*).
+#include <string.h>
+
+#include "../../include/sta.h"
+#include "sta_api_util.h"
+#include "sta_kernels.h"
+
+using namespace sta;
+using namespace sta_api;
+
+namespace {
+
+struct DecLayout {
+  int nsplit;
+  size_t qrot_off, scores_off, keys_off, size_off, part_off, total;
+};
+
+DecLayout dec_layout_of(const sta_decode_args* a) {
+  DecLayout L;
+  L.nsplit = decode_nsplit(a->k_max);
+  const size_t hq = (size_t)a->H * a->Q;
+  size_t off = 0;
+  L.qrot_off = off;                                   // rotated queries (H, Q, D) fp32
+  off = align256(off + hq * a->D * 4);
+  L.scores_off = off;                                 // scores (H, Q, M) when not an output
+  off = align256(off + hq * a->M * 4);
+  L.keys_off = off;                                   // key store of long caches
+  off = align256(off + decode_keys_bytes(a->H, a->Q, a->M));
+  L.size_off = off;                                   // set sizes (H, Q) when not an output
+  off = align256(off + hq * 4);
+  L.part_off = off;                                   // attend split states
+  off = align256(off + hq * L.nsplit * (a->D + 2) * 4);
+  L.total = off;
+  return L;
+}
+
+// need_pos: the entry point selects or attends, so every query's position must lie inside its
+// key range (forced[q_pos], exact_2.py:555); the scores alone take any position
+int dec_check(const sta_decode_args* a, bool need_pos = true) {
+  if (!a) return fail(STA_ERR_INVALID_ARG, "args is NULL");
+  if (a->dtype != STA_DTYPE_F32 && a->dtype != STA_DTYPE_BF16 && a->dtype != STA_DTYPE_F16)
+    return fail(STA_ERR_INVALID_ARG, "dtype %d is not one of STA_DTYPE_F32/BF16/F16", a->dtype);
+  if (a->H < 1 || a->Hkv < 1 || a->H % a->Hkv != 0)
+    return fail(STA_ERR_INVALID_ARG, "H=%d must be a positive multiple of Hkv=%d", a->H, a->Hkv);
+  if (a->D != 64 && a->D != 128) return fail(STA_ERR_UNSUPPORTED, "head_dim %d not in {64, 128}", a->D);
+  if (a->M < 1 || a->M >= (1 << 24)) return fail(STA_ERR_INVALID_ARG, "M=%d out of range [1, 2^24)", a->M);
+  if (a->Q < 1) return fail(STA_ERR_INVALID_ARG, "Q=%d must be >= 1", a->Q);
+  if (a->q_pos0 < 0 || (need_pos && (int64_t)a->q_pos0 + a->Q > a->M))
+    return fail(STA_ERR_INVALID_ARG, "need 0 <= q_pos0 (%d) and q_pos0 + Q (%d) <= M (%d)", a->q_pos0, a->Q, a->M);
+  if (a->k_max < 1) return fail(STA_ERR_INVALID_ARG, "k_max=%d must be >= 1", a->k_max);
+  if (a->n_global < 0 || a->n_local < 0)
+    return fail(STA_ERR_UNSUPPORTED, "n_global=%d / n_local=%d must be >= 0", a->n_global, a->n_local);
+  if ((size_t)a->H * a->Q >= (1u << 31)) return fail(STA_ERR_INVALID_ARG, "H * Q too large");
+  return STA_OK;
+}
+
+int dec_check_ws(const sta_decode_args* a, const DecLayout& L) {
+  if (!a->workspace || a->workspace_bytes < L.total)
+    return fail(STA_ERR_WORKSPACE, "workspace of %zu bytes at %p is smaller than the %zu needed",
+                a->workspace_bytes, a->workspace, L.total);
+  if (((uintptr_t)a->workspace & 255u) != 0) return fail(STA_ERR_WORKSPACE, "workspace must be 256-byte aligned");
+  return STA_OK;
+}
+
+DecodeArgs dec_args_of(const sta_decode_args* a, const DecLayout& L) {
+  char* ws = (char*)a->workspace;
+  DecodeArgs d{};
+  d.q = a->q;
+  d.q_hs = a->q_head_stride;
+  d.q_ts = a->q_tok_stride;
+  d.k = a->k;
+  d.k_hs = a->k_head_stride;
+  d.k_ts = a->k_tok_stride;
+  d.v = a->v;
+  d.v_hs = a->v_head_stride;
+  d.v_ts = a->v_tok_stride;
+  d.H = a->H;
+  d.Hkv = a->Hkv;
+  d.Q = a->Q;
+  d.M = a->M;
+  d.q_pos0 = a->q_pos0;
+  d.inv_freq = a->inv_freq;
+  d.pos_scale = a->pos_scale;
+  d.rope_scale = a->rope_scale;
+  d.sm_scale = a->sm_scale;
+  d.tau = a->tau;
+  d.n_global = a->n_global;
+  d.n_local = a->n_local;
+  d.k_max = a->k_max;
+  d.use_pct = a->pct_decode < 100.0;                              // exact_2.py:559
+  d.pct_frac = (float)(a->pct_decode / 100.0);                    // the float32 scalar of :561
+  d.scores = a->scores ? a->scores : (float*)(ws + L.scores_off);
+  d.keys = decode_select_in_lds(a->M) ? nullptr : (uint32_t*)(ws + L.keys_off);
+  d.idx = a->idx;
+  d.newpos_k = a->newpos_k;
+  d.newpos_q = a->newpos_q;
+  d.set_size = a->set_size;
+  d.causal = a->causal ? 1 : 0;
+  d.part = (float*)(ws + L.part_off);
+  d.out = a->out;
+  return d;
+}
+
+int dec_scores(const sta_decode_args* a, const DecLayout& L, DecodeArgs d, float* scores, hipStream_t st) {
+  const int64_t strides[6] = {a->q_head_stride, a->q_tok_stride, a->k_head_stride, a->k_tok_stride, 0, 0};
+  int rc = check_qkv_ptrs(a->dtype, a->q, a->k, nullptr, strides, false);
+  if (rc != STA_OK) return rc;
+  if (!a->inv_freq) return fail(STA_ERR_INVALID_ARG, "inv_freq must be non-NULL");
+  if (!scores) return fail(STA_ERR_INVALID_ARG, "scores must be non-NULL");
+  d.scores = scores;
+  hipError_t e = launch_decode_scores(a->dtype, a->D, d, (float*)((char*)a->workspace + L.qrot_off), st);
+  return e == hipSuccess ? STA_OK : hip_fail(e, "decode scores");
+}
+
+int dec_select(const sta_decode_args* a, DecodeArgs d, const float* scores, hipStream_t st) {
+  if (!a->tau || !a->idx || !a->newpos_k || !a->newpos_q)
+    return fail(STA_ERR_INVALID_ARG, "tau, idx, newpos_k and newpos_q must be non-NULL");
+  if (!scores) return fail(STA_ERR_INVALID_ARG, "scores must be non-NULL");
+  d.scores = (float*)scores;
+  hipError_t e = launch_decode_select(d, st);
+  return e == hipSuccess ? STA_OK : hip_fail(e, "decode selection");
+}
+
+int dec_attend(const sta_decode_args* a, const DecodeArgs& d, hipStream_t st) {
+  const int64_t strides[6] = {a->q_head_stride, a->q_tok_stride, a->k_head_stride,
+                              a->k_tok_stride, a->v_head_stride, a->v_tok_stride};
+  int rc = check_qkv_ptrs(a->dtype, a->q, a->k, a->v, strides, true);
+  if (rc != STA_OK) return rc;
+  if (!a->inv_freq || !a->out || !a->idx || !a->newpos_k || !a->newpos_q)
+    return fail(STA_ERR_INVALID_ARG, "inv_freq, out, idx, newpos_k and newpos_q must be non-NULL");
+  hipError_t e = launch_decode_attend(a->dtype, a->D, d, st);
+  return e == hipSuccess ? STA_OK : hip_fail(e, "decode attend");
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t sta_decode_workspace_size(const sta_decode_args* args) {
+  if (dec_check(args, false) != STA_OK) return 0;
+  return dec_layout_of(args).total;
+}
+
+int sta_decode_scores(const sta_decode_args* a, float* scores, void* stream) {
+  int rc = dec_check(a, false);
+  if (rc != STA_OK) return rc;
+  const DecLayout L = dec_layout_of(a);
+  if ((rc = dec_check_ws(a, L)) != STA_OK) return rc;
+  return dec_scores(a, L, dec_args_of(a, L), scores, (hipStream_t)stream);
+}
+
+int sta_decode_build_sets(const sta_decode_args* a, const float* scores, void* stream) {
+  int rc = dec_check(a);
+  if (rc != STA_OK) return rc;
+  const DecLayout L = dec_layout_of(a);
+  if ((rc = dec_check_ws(a, L)) != STA_OK) return rc;
+  return dec_select(a, dec_args_of(a, L), scores, (hipStream_t)stream);
+}
+
+int sta_decode_attend(const sta_decode_args* a, void* stream) {
+  int rc = dec_check(a);
+  if (rc != STA_OK) return rc;
+  const DecLayout L = dec_layout_of(a);
+  if ((rc = dec_check_ws(a, L)) != STA_OK) return rc;
+  return dec_attend(a, dec_args_of(a, L), (hipStream_t)stream);
+}
+
+int sta_decode_attention(const sta_decode_args* a, void* stream) {
+  int rc = dec_check(a);
+  if (rc != STA_OK) return rc;
+  const DecLayout L = dec_layout_of(a);
+  if ((rc = dec_check_ws(a, L)) != STA_OK) return rc;
+  hipStream_t st = (hipStream_t)stream;
+  DecodeArgs d = dec_args_of(a, L);
+  // the attend sweeps only the selected slots: the set sizes always exist (output or workspace)
+  if (!d.set_size) d.set_size = (int32_t*)((char*)a->workspace + L.size_off);
+  if ((rc = mark_event(a->stage_events, 0, st)) != STA_OK) return rc;
+  if ((rc = dec_scores(a, L, d, d.scores, st)) != STA_OK) return rc;
+  if ((rc = mark_event(a->stage_events, 1, st)) != STA_OK) return rc;
+  if ((rc = dec_select(a, d, d.scores, st)) != STA_OK) return rc;
+  if ((rc = mark_event(a->stage_events, 2, st)) != STA_OK) return rc;
+  if ((rc = dec_attend(a, d, st)) != STA_OK) return rc;
+  return mark_event(a->stage_events, 3, st);
+}
+
+}  // extern "C"

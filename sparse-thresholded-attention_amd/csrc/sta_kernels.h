@@ -126,6 +126,40 @@ struct DcaArgs {
   void* out;                // (H, N, D)
 };
 
+// decode: Q queries over one cache of M keys, query i at position q_pos0 + i seeing keys
+// [0, M - (Q - 1 - i)): shared_selection_triton_exact_2.py:235-271, 505-655
+struct DecodeArgs {
+  const void* q;          // (H, Q, D) raw
+  int64_t q_hs, q_ts;
+  const void* k;          // (Hkv, M, D) raw cache
+  int64_t k_hs, k_ts;
+  const void* v;
+  int64_t v_hs, v_ts;
+  int H, Hkv, Q, M, q_pos0;
+  const float* inv_freq;
+  float pos_scale, rope_scale, sm_scale;
+  const float* tau;       // (H,)
+  int n_global, n_local, k_max;
+  int use_pct;            // pct_decode < 100
+  float pct_frac;         // float32(pct_decode / 100)
+  float* scores;          // (H, Q, M)
+  uint32_t* keys;         // key store of the selection when the cache is too long for LDS
+  int32_t* idx;           // (H, Q, k_max)
+  float* newpos_k;        // (H, Q, k_max)
+  float* newpos_q;        // (H, Q)
+  int32_t* set_size;      // (H, Q) or null
+  int causal;             // attend also masks slots past the query's position
+  float* part;            // (H * Q, nsplit, D + 2) split states of the attend
+  void* out;              // (H, Q, D)
+};
+
+hipError_t launch_decode_scores(int dtype, int D, const DecodeArgs& a, float* qrot, hipStream_t st);
+bool decode_select_in_lds(int M);
+size_t decode_keys_bytes(int H, int Q, int M);
+hipError_t launch_decode_select(const DecodeArgs& a, hipStream_t st);
+int decode_nsplit(int k_max);
+hipError_t launch_decode_attend(int dtype, int D, const DecodeArgs& a, hipStream_t st);
+
 hipError_t launch_rope_frag(int dtype, int D, const void* x, int64_t head_stride, int64_t tok_stride,
                             int heads, int N, int rows_pad, int pos_base, float pos_scale,
                             float rope_scale, const float* inv_freq, u32x4* frag, hipStream_t st);

@@ -24,3 +24,38 @@ def shared_pi_attention(q, k, v, tau, inv_freq, pos_scale=1.0, pct=30.0, sm_scal
     return shared_prefill(q, k, v, tau, inv_freq, pos_scale, rope_scale, inv_freq, pos_scale,
                           rope_scale, pct, sm_scale, n_global, n_local, tile, k_max, q_pos_base,
                           measure, select_score)
+
+
+# ---------------------------------------------------------------------------------------------
+# decode (one query per call): shared_selection_triton_exact_2.py:505-655
+# ---------------------------------------------------------------------------------------------
+def _decode_scores_kernel(q, K, inv_freq, q_pos, pos_scale, rope_scale, sm_scale, block_n=64):
+    """Per-key scores (H,M) for one query.  q:(H,D), K:(H,M,D) (or Hkv heads).
+    shared_selection_triton_exact_2.py:505-525 (the _decode_select_kernel launch)."""
+    from _decode import decode_scores
+    return decode_scores(q, K, inv_freq, q_pos, pos_scale, rope_scale, sm_scale)
+
+
+def _decode_build_sets(q, K, tau, inv_freq, q_pos, pos_scale, rope_scale, sm_scale, n_global, n_local,
+                       k_max, pct_decode, scores=None):
+    """Per-query selection + PI reposition: (idx (H,k_max) long, sentinel M; newpos_k (H,k_max);
+    newpos_q (H,)).  shared_selection_triton_exact_2.py:527-604."""
+    from _decode import decode_build_sets
+    return decode_build_sets(q, K, tau, inv_freq, q_pos, pos_scale, rope_scale, sm_scale, n_global, n_local,
+                             k_max, pct_decode, scores)
+
+
+def _decode_attend_torch(q, K, V, idx, newpos_k, newpos_q, inv_freq, rope_scale, sm_scale):
+    """Attend over the selected set -> (H,D) in q.dtype (slots valid where idx < M).
+    shared_selection_triton_exact_2.py:608-623."""
+    from _decode import decode_attend
+    return decode_attend(q, K, V, idx, newpos_k, newpos_q, inv_freq, rope_scale, sm_scale)
+
+
+def _decode_attend_kernelC(q, K, V, idx, newpos_k, newpos_q, inv_freq, rope_scale, sm_scale, k_max, q_pos,
+                           block_m=16, block_k=32):
+    """Attend with Kernel C's slot rule (idx < M and idx <= q_pos) -> (H,D).  block_m / block_k are
+    the reference's tile knobs, accepted and ignored.  shared_selection_triton_exact_2.py:626-655."""
+    from _decode import decode_attend
+    return decode_attend(q, K, V, idx[..., :k_max], newpos_k[..., :k_max], newpos_q, inv_freq, rope_scale,
+                         sm_scale, q_pos=q_pos)

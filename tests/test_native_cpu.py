@@ -202,3 +202,47 @@ def test_dca_workspace_size_matches_layout():
     n = lib.sta_dca_workspace_size(ctypes.byref(_dca_args()))
     need = 32 * 65536 * 128 * 2 * 4          # rotated keys + three query variants, bf16
     assert need <= n < need + 4096
+
+
+def _decode_args(**kw):
+    import _sta_native as native
+    a = native.DecodeArgsC()
+    a.dtype, a.H, a.Hkv, a.Q, a.M, a.D = 1, 32, 8, 1, 12288, 128
+    a.q_pos0, a.n_global, a.n_local, a.k_max = 12287, 32, 32, 2048
+    a.pos_scale, a.rope_scale, a.sm_scale, a.pct_decode = 1.0 / 3.0, 1.0, 0.0884, 100.0
+    for k, v in kw.items():
+        setattr(a, k, v)
+    return a
+
+
+@pytest.mark.parametrize("field,value,code", [
+    ("D", 96, -2), ("M", 0, -1), ("Q", 0, -1), ("q_pos0", 12288, -1), ("k_max", 0, -1), ("Hkv", 5, -1),
+    ("n_local", -1, -2), ("dtype", 7, -1),
+])
+def test_decode_invalid_arguments_are_rejected(field, value, code):
+    import _sta_native as native
+    lib = native.lib()
+    a = _decode_args(**{field: value})
+    assert lib.sta_decode_attention(ctypes.byref(a), None) == code
+    assert lib.sta_decode_build_sets(ctypes.byref(a), None, None) == code
+
+
+def test_decode_scores_take_any_position_and_need_a_workspace():
+    import _sta_native as native
+    lib = native.lib()
+    a = _decode_args(q_pos0=50000)       # the scores alone: any query position
+    assert lib.sta_decode_workspace_size(ctypes.byref(a)) > 0
+    assert lib.sta_decode_scores(ctypes.byref(a), None, None) == -4      # no workspace
+    assert lib.sta_decode_attention(ctypes.byref(a), None) == -1         # q_pos0 + Q > M
+
+
+def test_decode_workspace_size_matches_layout():
+    import _sta_native as native
+    lib = native.lib()
+    n = lib.sta_decode_workspace_size(ctypes.byref(_decode_args()))
+    need = 32 * 128 * 4 + 32 * 12288 * 4 + 32 * 4 + 32 * 32 * 130 * 4    # qrot, scores, sizes, splits
+    assert need <= n < need + 5 * 256
+    # past the LDS key store (M > 35840) the selection keeps its keys in the workspace
+    n2 = lib.sta_decode_workspace_size(ctypes.byref(_decode_args(M=40000, q_pos0=39999)))
+    need2 = 32 * 128 * 4 + 32 * 40000 * 4 + 32 * 1024 * 40 * 4 + 32 * 4 + 32 * 32 * 130 * 4
+    assert need2 <= n2 < need2 + 5 * 256
