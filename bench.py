@@ -33,6 +33,8 @@ PEAK_HBM_GBS = 8000.0          # MI355X HBM3E
 STAGES = ["rope", "score", "select", "gather"]
 STREAM_STAGES = ["rope", "score", "attend_rope", "stream"]
 DCA_STAGES = ["rope", "attention"]
+DECODE_STAGES = ["scores", "select", "attend"]
+DECODE_METRIC = "decode tokens/sec (one attention layer, one new query per head over the KV cache)"
 
 
 def parse():
@@ -136,6 +138,103 @@ def cpu_baseline(cfg, q, k, v, invf, ps, rs, budget_s):
                       f"({stages}, {threads} OpenMP threads), scaled x{cfg.H / heads:g}"}
 
 
+def bench_decode(args, cfg, q, k, v, q_cpu, k_cpu, v_cpu, invf, ps, rs, tau):
+    """Decode steps: the last decode_q positions query the cache of N keys (scores, selection,
+    attend).  ms_per_step is the wall clock per step, launches included."""
+    import _sta_native as native
+    Q, N = cfg.decode_q, cfg.N
+    dev = q.device
+    qd = q[0, :, N - Q:, :].contiguous()
+    plan = native.DecodePlan(qd, k, v, tau, invf, N - Q, ps, rs, None, cfg.n_global, cfg.n_local, cfg.k_max,
+                             cfg.pct_decode)
+    stream = torch.cuda.current_stream(dev)
+    for _ in range(args.warmup):
+        plan.run()
+    torch.cuda.synchronize()
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(len(DECODE_STAGES) + 1)] for _ in range(args.steps)]
+    for row in evs:
+        for e in row:
+            e.record(stream)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        plan.run(evs[i])
+    torch.cuda.synchronize()
+    ms_per_step = (time.perf_counter() - t0) * 1000.0 / args.steps
+    stage_ms = {s: sum(evs[i][j].elapsed_time(evs[i][j + 1]) for i in range(args.steps)) / args.steps
+                for j, s in enumerate(DECODE_STAGES)}
+    r = plan.out
+    esz = q.element_size()
+    # scores: the cache's keys once per kv head, the scores written once
+    sbytes = cfg.Hkv * N * cfg.D * esz + cfg.H * Q * N * 4
+    kept = r["set_size"].clamp(max=cfg.k_max)
+    abytes = int(kept.sum().item()) * (2 * cfg.D * esz + 8) + 2 * cfg.H * Q * cfg.D * esz
+    roof = {}
+    for name, kern, b in (("scores", "decode_score_kernel", sbytes), ("attend", "decode_attend_kernel", abytes)):
+        gbs = b / (stage_ms[name] * 1e-3) / 1e9
+        roof[name] = {"kernel": kern, "bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS,
+                      "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4), "algorithmic_per_launch": int(b),
+                      "traffic": read_traffic(args.traffic_file, kern)}
+    dominant = roof["scores"] if stage_ms["scores"] >= stage_ms["attend"] else roof["attend"]
+    print(f"[bench] {ms_per_step:.4f} ms/step; stages {stage_ms}", file=sys.stderr, flush=True)
+    cpu = None
+    if args.cpu_baseline_seconds > 0:
+        cpu = cpu_baseline_decode(cfg, q_cpu, k_cpu, v_cpu, invf, ps, rs, args.cpu_baseline_seconds)
+    line = {
+        "metric": DECODE_METRIC,
+        "value": round(Q / (ms_per_step * 1e-3), 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": {torch.bfloat16: "bf16", torch.float16: "fp16", torch.float32: "fp32"}[q.dtype],
+        "data": "synthetic (seeded Gaussian Q/K/V with planted keys)",
+        "config": {"workload": cfg.name, "variant": "decode", "heads": cfg.H, "kv_heads": cfg.Hkv,
+                   "cache_len": N, "queries": Q, "head_dim": cfg.D, "tau": cfg.tau, "k_max": cfg.k_max,
+                   "pct_decode": cfg.pct_decode, "pos_scale": ps, "rope_scale": rs,
+                   "parallelism": "none (1 GPU)"},
+        "stages_ms": {s: round(t, 5) for s, t in stage_ms.items()},
+        "gpu_ms_per_step": round(sum(stage_ms.values()), 5),
+        "roofline": dominant,
+        "rooflines": roof,
+        "selection": {"set_size_mean": round(r["set_size"].float().mean().item(), 1),
+                      "capped": int((r["set_size"] > cfg.k_max).sum().item()), "queries": int(kept.numel())},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+def cpu_baseline_decode(cfg, q, k, v, invf, ps, rs, budget_s):
+    """The oracle's decode (scores, selection, attend) for one query per head, all heads."""
+    import numpy as np
+    from oracle import sta_oracle as orc
+    sm = 1.0 / math.sqrt(cfg.D)
+    Q, N = cfg.decode_q, cfg.N
+    qn, dt = orc.from_torch(q[0, :, N - Q:, :])
+    kn, _ = orc.from_torch(k[0])
+    vn, _ = orc.from_torch(v[0])
+    tau = np.full(cfg.H, cfg.tau, np.float32)
+    steps, t0 = 0, time.perf_counter()
+    while True:
+        s = orc.decode_scores(qn, kn, dt, invf.numpy(), ps, rs, sm, N - Q)
+        idx, npk, npq, _ = orc.decode_build_sets(s, tau, N - Q, ps, cfg.n_global, cfg.n_local, cfg.k_max,
+                                                 cfg.pct_decode)
+        orc.decode_attend(qn, kn, vn, dt, invf.numpy(), rs, sm, N - Q, idx, npk, npq)
+        steps += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s or steps >= 50:
+            break
+    threads = orc.num_threads()
+    return {"value": round(Q * steps / el, 3), "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"{steps} decode steps of the same workload (all {cfg.H} heads) through the CPU "
+                      f"oracle's scores, selection and attend ({threads} OpenMP threads)"}
+
+
 def main():
     args = parse()
     if args.calibrate_copy:
@@ -160,6 +259,8 @@ def main():
     q, k, v = q_cpu.to(dev), k_cpu.to(dev), v_cpu.to(dev)
     invf, ps, rs = cfg.geometry()
     tau = torch.full((cfg.H,), cfg.tau)
+    if cfg.variant == "decode":
+        return bench_decode(args, cfg, q, k, v, q_cpu, k_cpu, v_cpu, invf, ps, rs, tau)
     if cfg.variant == "dca":
         plan = native.DcaPlan(q, k, v, invf, cfg.dca[0], cfg.dca[1], cfg.dca[2])
     elif cfg.variant == "pqstream":

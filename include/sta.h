@@ -298,7 +298,7 @@ typedef struct sta_decode_args {
   float pos_scale, rope_scale, sm_scale;
   int32_t q_pos0;           /* position of query 0; q_pos0 + Q <= M (any q_pos0 >= 0 for the
                                scores alone) */
-  int32_t n_global, n_local, k_max;
+  int32_t n_global, n_local, k_max;   /* k_max <= 16384 */
   double pct_decode;        /* the reference's pct_decode (100 = keep every passer) */
   int32_t causal;           /* attend: 0 masks sentinel slots only (_decode_attend_torch); 1 also
                                slots past the query's position (Kernel C, _decode_attend_kernelC) */

@@ -47,7 +47,8 @@ int dec_check(const sta_decode_args* a, bool need_pos = true) {
   if (a->Q < 1) return fail(STA_ERR_INVALID_ARG, "Q=%d must be >= 1", a->Q);
   if (a->q_pos0 < 0 || (need_pos && (int64_t)a->q_pos0 + a->Q > a->M))
     return fail(STA_ERR_INVALID_ARG, "need 0 <= q_pos0 (%d) and q_pos0 + Q (%d) <= M (%d)", a->q_pos0, a->Q, a->M);
-  if (a->k_max < 1) return fail(STA_ERR_INVALID_ARG, "k_max=%d must be >= 1", a->k_max);
+  if (a->k_max < 1 || a->k_max > 16384)
+    return fail(STA_ERR_UNSUPPORTED, "k_max=%d outside [1, 16384]", a->k_max);
   if (a->n_global < 0 || a->n_local < 0)
     return fail(STA_ERR_UNSUPPORTED, "n_global=%d / n_local=%d must be >= 0", a->n_global, a->n_local);
   if ((size_t)a->H * a->Q >= (1u << 31)) return fail(STA_ERR_INVALID_ARG, "H * Q too large");
@@ -97,6 +98,7 @@ DecodeArgs dec_args_of(const sta_decode_args* a, const DecLayout& L) {
   d.set_size = a->set_size;
   d.causal = a->causal ? 1 : 0;
   d.part = (float*)(ws + L.part_off);
+  d.qrot = nullptr;
   d.out = a->out;
   return d;
 }

@@ -5,15 +5,18 @@
 //
 //   decode_qrot_kernel    the query rotated at fl(float(q_pos) * pos_scale)        (exact_2.py:250-257)
 //   decode_score_kernel   per-key scores under the selection geometry            (exact_2.py:235-271)
-//                         64 keys x up to 8 kv heads per workgroup: the key rotation's
-//                         sin / cos is computed once per (key, frequency) and shared by the heads
+//                         64 keys x up to 4 kv heads per workgroup: the key rotation's
+//                         sin / cos is computed once per (key, frequency) and shared by the heads;
+//                         the query rows are rotated in the workgroup's LDS (decode_qrot_kernel
+//                         precomputes them when they outgrow it)
 //   decode_select_kernel  _decode_build_sets (exact_2.py:527-604) for one query per workgroup:
 //                         the scores staged in LDS as order-preserving keys, exact max, the
 //                         top-pct cut and the k_max cap cut as radix selections (8-bit digits),
 //                         compaction and the fp32 reposition recurrence
 //   decode_attend_kernel  the attend over the selected slots (exact_2.py:608-655) split over
-//                         workgroups of 64 slots, 16 lanes per slot, each split an online
-//                         softmax state; decode_combine_kernel merges the splits
+//                         workgroups of 64 slots, 16 lanes per slot and four slots per lane
+//                         group (every row request in flight at once), each split a softmax
+//                         state; decode_combine_kernel merges the splits
 #include <float.h>
 
 #include "sta_device.h"
@@ -101,21 +104,67 @@ __global__ __launch_bounds__(D / 2) void decode_qrot_kernel(DecodeArgs a, float*
 }
 
 // ------------------------------------------------------------------------------------------
-// per-key scores (H, Q, M): 64 keys x HG kv heads per workgroup, 4 lanes per key
+// per-key scores (H, Q, M): 64 keys x HG kv heads per workgroup, 4 lanes per key.  Every head's
+// key rows are requested first (kept packed in registers), then the workgroup rotates its query
+// rows into LDS and computes the keys' sin / cos -- once per (key, frequency), shared by the
+// heads -- while the rows are in flight.
 // ------------------------------------------------------------------------------------------
-constexpr int DEC_HG = 8;   // kv heads per score workgroup
+constexpr int DEC_QLDS = 32 * 1024;           // LDS for rotated query rows
 
-template <int DT, int D>
-__global__ __launch_bounds__(256) void decode_score_kernel(DecodeArgs a, const float* qrot) {
+template <int DT>
+constexpr int dec_hg() { return 4; }   // 4 kv heads: ~140 VGPRs, 3 waves per SIMD (8 heads: 2)
+
+// kv heads of one score workgroup and whether its rotated query rows fit its LDS
+int decode_score_hg(int dtype) { return dtype == DT_F32 ? dec_hg<DT_F32>() : dec_hg<DT_BF16>(); }
+bool decode_qrot_in_lds(int dtype, int H, int Hkv, int Q, int D) {
+  return (size_t)decode_score_hg(dtype) * (H / Hkv) * Q * D * 4 <= DEC_QLDS;
+}
+
+template <int DT, int D, bool QLDS>
+__global__ __launch_bounds__(256) void decode_score_kernel(DecodeArgs a) {
 #pragma clang fp contract(off)
-  constexpr int NP = D / 8;                  // rotation pairs per lane
+  constexpr int HG = dec_hg<DT>();
+  constexpr int NP = D / 8;                   // rotation pairs per lane
+  constexpr int ES = DT == DT_F32 ? 4 : 2;
+  constexpr int UH = NP * ES / 16;            // 16-byte units per half row per lane
+  __shared__ __align__(16) float qs[QLDS ? DEC_QLDS / 4 : 1];
   const int t = threadIdx.x & 3;
   const int j = blockIdx.x * 64 + (threadIdx.x >> 2);
-  const bool valid = j < a.M;
-  const int jc = valid ? j : a.M - 1;
-  const int hk0 = blockIdx.y * DEC_HG;
+  const int jc = j < a.M ? j : a.M - 1;
+  const int hk0 = blockIdx.y * HG;
+  const int nh = min(HG, a.Hkv - hk0);        // kv heads of this workgroup
   const int G = a.H / a.Hkv;
-  // cos / sin of this key's frequencies t*NP .. t*NP + NP - 1, shared by the heads
+  u32x4 raw[HG][2 * UH];
+#pragma unroll
+  for (int g = 0; g < HG; ++g) {
+    const int hk = hk0 + min(g, nh - 1);       // heads past Hkv reload a valid row, store nothing
+    const char* row = (const char*)a.k + ((int64_t)hk * a.k_hs + (int64_t)jc * a.k_ts + t * NP) * ES;
+#pragma unroll
+    for (int u = 0; u < UH; ++u) {
+      raw[g][u] = *(const u32x4*)(row + 16 * u);
+      raw[g][UH + u] = *(const u32x4*)(row + (D / 2) * ES + 16 * u);
+    }
+  }
+  const int R = nh * G * a.Q;                  // query rows: (kv head, q head of its group, query)
+  if constexpr (QLDS) {
+    // rotated at fl(float(q_pos0 + i) * pos_scale) (exact_2.py:250-257)
+    for (int x = threadIdx.x; x < R * (D / 2); x += 256) {
+      const int r = x / (D / 2), f = x % (D / 2);
+      const int i = r % a.Q, hq = hk0 * G + r / a.Q;
+      const int64_t base = (int64_t)hq * a.q_hs + (int64_t)i * a.q_ts;
+      const float x1 = load1<DT>(a.q, base + f), x2 = load1<DT>(a.q, base + D / 2 + f);
+      const float pb = (float)(a.q_pos0 + i) * a.pos_scale;
+      const float ang = pb * a.inv_freq[f];
+      float sn, cs;
+      sincosf(ang, &sn, &cs);
+      cs = cs * a.rope_scale;
+      sn = sn * a.rope_scale;
+      const float p1 = x1 * cs, p2 = x2 * sn, p3 = x2 * cs, p4 = x1 * sn;
+      qs[r * D + f] = p1 - p2;
+      qs[r * D + D / 2 + f] = p3 + p4;
+    }
+  }
+  // cos / sin of this key's frequencies t*NP .. t*NP + NP - 1
   float cs[NP], sn[NP];
   {
     const float kb = (float)j * a.pos_scale;                            // exact_2.py:264
@@ -127,38 +176,49 @@ __global__ __launch_bounds__(256) void decode_score_kernel(DecodeArgs a, const f
       sn[p] = sn[p] * a.rope_scale;
     }
   }
-  for (int g = 0; g < DEC_HG; ++g) {
-    const int hk = hk0 + g;
-    if (hk >= a.Hkv) break;
-    float x1[NP], x2[NP], k1[NP], k2[NP];
-    const int64_t kb = (int64_t)hk * a.k_hs + (int64_t)jc * a.k_ts + t * NP;
-    load_n<DT, NP>(a.k, kb, x1);
-    load_n<DT, NP>(a.k, kb + D / 2, x2);
+  if constexpr (QLDS) __syncthreads();
+  const float* qsrc = QLDS ? qs : a.qrot + (int64_t)hk0 * G * a.Q * D;
+#pragma unroll
+  for (int g = 0; g < HG; ++g) {
+    if (g >= nh) break;
+    float k1[NP], k2[NP];
 #pragma unroll
     for (int p = 0; p < NP; ++p) {                                        // exact_2.py:266-267
-      const float u = x1[p] * cs[p], w = x2[p] * sn[p], y = x2[p] * cs[p], z = x1[p] * sn[p];
+      float x1, x2;
+      if constexpr (DT == DT_F32) {
+        x1 = __uint_as_float(raw[g][p / 4][p % 4]);
+        x2 = __uint_as_float(raw[g][UH + p / 4][p % 4]);
+      } else {
+        const uint32_t w1 = raw[g][p / 8][(p % 8) / 2], w2 = raw[g][UH + p / 8][(p % 8) / 2];
+        const uint32_t h1 = (p & 1) ? (w1 >> 16) : (w1 & 0xffffu), h2 = (p & 1) ? (w2 >> 16) : (w2 & 0xffffu);
+        x1 = DT == DT_BF16 ? __uint_as_float(h1 << 16) : f16_bits_to_f32(h1);
+        x2 = DT == DT_BF16 ? __uint_as_float(h2 << 16) : f16_bits_to_f32(h2);
+      }
+      const float u = x1 * cs[p], w = x2 * sn[p], y = x2 * cs[p], z = x1 * sn[p];
       k1[p] = u - w;
       k2[p] = y + z;
     }
-    for (int hq = hk * G; hq < hk * G + G; ++hq) {
-      for (int i = 0; i < a.Q; ++i) {
-        const float* qr = qrot + ((int64_t)hq * a.Q + i) * D;
-        float q1[NP], q2[NP];
+    for (int r = g * G * a.Q; r < (g + 1) * G * a.Q; ++r) {
+      const float* qr = qsrc + (int64_t)r * D;
+      float acc = 0.0f;
 #pragma unroll
-        for (int p = 0; p < NP; p += 4) {
-          const float4 u = *(const float4*)(qr + t * NP + p);
-          const float4 w = *(const float4*)(qr + D / 2 + t * NP + p);
-          q1[p] = u.x; q1[p + 1] = u.y; q1[p + 2] = u.z; q1[p + 3] = u.w;
-          q2[p] = w.x; q2[p + 1] = w.y; q2[p + 2] = w.z; q2[p + 3] = w.w;
-        }
-        float acc = 0.0f;
-#pragma unroll
-        for (int p = 0; p < NP; ++p) acc = fmaf(q2[p], k2[p], fmaf(q1[p], k1[p], acc));
-        acc += __shfl_xor(acc, 1, 64);
-        acc += __shfl_xor(acc, 2, 64);
-        const int m = a.M - (a.Q - 1 - i);
-        if (t == 0 && j < m) a.scores[((int64_t)hq * a.Q + i) * a.M + j] = acc * a.sm_scale;   // :270
+      for (int p = 0; p < NP; p += 4) {
+        const float4 u = *(const float4*)(qr + t * NP + p);
+        const float4 w = *(const float4*)(qr + D / 2 + t * NP + p);
+        acc = fmaf(u.x, k1[p], acc);
+        acc = fmaf(w.x, k2[p], acc);
+        acc = fmaf(u.y, k1[p + 1], acc);
+        acc = fmaf(w.y, k2[p + 1], acc);
+        acc = fmaf(u.z, k1[p + 2], acc);
+        acc = fmaf(w.z, k2[p + 2], acc);
+        acc = fmaf(u.w, k1[p + 3], acc);
+        acc = fmaf(w.w, k2[p + 3], acc);
       }
+      acc += __shfl_xor(acc, 1, 64);
+      acc += __shfl_xor(acc, 2, 64);
+      const int i = r % a.Q, hq = hk0 * G + r / a.Q;
+      const int m = a.M - (a.Q - 1 - i);
+      if (t == 0 && j < m) a.scores[((int64_t)hq * a.Q + i) * a.M + j] = acc * a.sm_scale;   // :270
     }
   }
 }
@@ -197,7 +257,8 @@ __device__ __forceinline__ uint32_t dmax_u(uint32_t v, uint32_t* tmp) {
   return r;
 }
 
-__device__ __forceinline__ int dexcl_sum(int v, int* tmp) {
+// exclusive prefix sum over the block's threads; *total (optional) receives the block sum
+__device__ __forceinline__ int dexcl_sum(int v, int* tmp, int* total = nullptr) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   int x = v;
 #pragma unroll
@@ -207,9 +268,14 @@ __device__ __forceinline__ int dexcl_sum(int v, int* tmp) {
   }
   if (lane == 63) tmp[wave] = x;
   __syncthreads();
-  int base = 0;
-  for (int w = 0; w < wave; ++w) base += tmp[w];
+  int base = 0, all = 0;
+#pragma unroll
+  for (int w = 0; w < DEC_SEL_NW; ++w) {
+    base += w < wave ? tmp[w] : 0;
+    all += tmp[w];
+  }
   __syncthreads();
+  if (total) *total = all;
   return base + x - v;
 }
 
@@ -235,13 +301,15 @@ __device__ __forceinline__ float dexcl_max(float v, float* tmp) {
 
 // Keys of the LDS store: per thread a contiguous range of `per` keys at the odd row stride
 // per | 1 (conflict-free scans); the global store (caches too long for LDS) uses stride per.
-bool decode_select_in_lds(int M) {   // up to 144 KB of the CU's 160 KB (M <= 35840)
+constexpr int DEC_CAND = 512;                // keys of a bin ranked directly
+constexpr size_t DEC_AUX = 4096 * 4 + DEC_SEL_NT * 4 + 256;   // histogram, candidates, scratch
+bool decode_select_in_lds(int M) {   // the CU's 160 KB: M <= 33792
   const int per = (M + DEC_SEL_NT - 1) / DEC_SEL_NT;
-  return (size_t)DEC_SEL_NT * (per | 1) * 4 + 2048 <= 144 * 1024;
+  return (size_t)DEC_SEL_NT * (per | 1) * 4 + DEC_AUX <= 160 * 1024;
 }
 size_t decode_select_lds_bytes(int M) {
   const int per = (M + DEC_SEL_NT - 1) / DEC_SEL_NT;
-  return (decode_select_in_lds(M) ? (size_t)DEC_SEL_NT * (per | 1) * 4 : 0) + 2048;
+  return (decode_select_in_lds(M) ? (size_t)DEC_SEL_NT * (per | 1) * 4 : 0) + DEC_AUX;
 }
 size_t decode_keys_bytes(int H, int Q, int M) {
   if (decode_select_in_lds(M)) return 0;
@@ -262,26 +330,38 @@ __global__ __launch_bounds__(DEC_SEL_NT) void decode_select_kernel(DecodeArgs a)
   const int per = (m + DEC_SEL_NT - 1) / DEC_SEL_NT;
   const int PS = GKEYS ? per : (per | 1);
   uint32_t* ks = GKEYS ? a.keys + (int64_t)hi * DEC_SEL_NT * per_max : dsm;
-  int* hist = (int*)(dsm + (GKEYS ? 0 : DEC_SEL_NT * (per_max | 1)));   // 256
-  int* tmp = hist + 256;                       // DEC_SEL_NW
+  int* hist = (int*)(dsm + (GKEYS ? 0 : DEC_SEL_NT * (per_max | 1)));   // 4096
+  uint32_t* cand = (uint32_t*)(hist + 4096);   // DEC_SEL_NT (16-byte aligned)
+  int* tmp = (int*)(cand + DEC_SEL_NT);        // DEC_SEL_NW
   int* misc = tmp + DEC_SEL_NW;                // 8
   const int j0 = tid * per, j1 = min(j0 + per, m);
   uint32_t* myrow = ks + tid * PS;
   const float* srow = a.scores + (int64_t)hi * a.M;
 
-  // ---- stage the scores as keys (coalesced reads), exact max (exact_2.py:549) ----
+  // ---- stage the scores as keys (coalesced reads, eight in flight per lane), exact max
+  // (exact_2.py:549) ----
+  const float tau_h = a.tau[h];
   uint32_t kmax = 0;
-  for (int j = tid; j < DEC_SEL_NT * per; j += DEC_SEL_NT) {
-    uint32_t key = 0;
-    if (j < m) {
-      key = okey(srow[j]);
-      kmax = max(kmax, key);
+  for (int e0 = 0; e0 < per; e0 += 8) {
+    float sv[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int j = tid + (e0 + u) * DEC_SEL_NT;
+      sv[u] = (e0 + u < per && j < m) ? srow[j] : 0.0f;
     }
-    const int row = j / per;
-    ks[row * PS + (j - row * per)] = key;
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int j = tid + (e0 + u) * DEC_SEL_NT;
+      if (e0 + u < per) {
+        const uint32_t key = j < m ? okey(sv[u]) : 0u;
+        kmax = max(kmax, key);
+        const int row = j / per;
+        ks[row * PS + (j - row * per)] = key;
+      }
+    }
   }
   kmax = dmax_u(kmax, (uint32_t*)tmp);         // the barrier inside also publishes the stores
-  const float thr = okey_value(kmax) - a.tau[h];                       // exact_2.py:550
+  const float thr = okey_value(kmax) - tau_h;                          // exact_2.py:550
   const uint32_t kthr = okey(thr);
 
   // forced keys: [0, g) U [lo, p] (global, local window, self; exact_2.py:552-555)
@@ -291,69 +371,78 @@ __global__ __launch_bounds__(DEC_SEL_NT) void decode_select_kernel(DecodeArgs a)
   const int nforced = g + max(nB, 0);
   auto forced_j = [&](int f) { return f < g ? f : max(lo, g) + (f - g); };   // f < nforced
 
-  // need-th largest key (1 <= need <= #nonzero keys) -> (V, #keys >= V), 8-bit digits
+  // need-th largest key (1 <= need <= #nonzero keys) -> (V, #keys >= V).  Radix levels of 12,
+  // 12 and 8 bits (LDS histograms with plain atomics); as soon as the bin holding the statistic
+  // has at most DEC_CAND keys they are collected and ranked directly.
   auto kth = [&](int need) -> uint2 {
     uint32_t prefix = 0, pmask = 0;
     int ge = 0;
-    for (int shift = 24; shift >= 0; shift -= 8) {
-      for (int b = tid; b < 256; b += DEC_SEL_NT) hist[b] = 0;
+    for (int lv = 0; lv < 3; ++lv) {
+      const int shift = lv == 0 ? 20 : (lv == 1 ? 8 : 0);
+      const int nb = lv == 2 ? 256 : 4096;
+      for (int b = tid; b < nb; b += DEC_SEL_NT) hist[b] = 0;
+      cand[tid] = 0u;                          // 0 ranks below every key
+      if (tid == 0) misc[4] = 0;
       __syncthreads();
-      if (shift == 24) {
-        // the top digit (sign and high exponent bits) takes few values: one LDS atomic per
-        // distinct digit of a wave
-        for (int e = 0; e < per; ++e) {
-          const uint32_t k = myrow[e];
-          bool act = k != 0 && j0 + e < m;
-          const int d = (int)(k >> 24);
-          uint64_t msk = __ballot(act);
-          while (msk) {
-            const int leader = __ffsll((unsigned long long)msk) - 1;
-            const int dl = __shfl(d, leader, 64);
-            const uint64_t same = __ballot(act && d == dl);
-            if (lane == leader) atomicAdd(&hist[dl], (int)__popcll(same));
-            if (act && d == dl) act = false;
-            msk &= ~same;
-          }
-        }
-      } else {
-        for (int e = 0; e < per; ++e) {
-          const uint32_t k = myrow[e];
-          if (k != 0 && j0 + e < m && (k & pmask) == prefix) atomicAdd(&hist[(k >> shift) & 255u], 1);
-        }
+      for (int e = 0; e < per; ++e) {
+        const uint32_t k = myrow[e];
+        if (k != 0 && j0 + e < m && (k & pmask) == prefix) atomicAdd(&hist[(k >> shift) & (uint32_t)(nb - 1)], 1);
       }
       __syncthreads();
-      if (wave == 0) {
-        // lane l holds bins 255-4l .. 252-4l (descending)
-        int c[4], sl = 0;
+      // bins in descending order, four per thread
+      const bool own = 4 * tid < nb;
+      int c[4], sl = 0;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) { c[e] = hist[255 - 4 * lane - e]; sl += c[e]; }
-        int incl = sl;
-#pragma unroll
-        for (int o = 1; o < 64; o <<= 1) {
-          const int y = __shfl_up(incl, o, 64);
-          if (lane >= o) incl += y;
+      for (int e = 0; e < 4; ++e) { c[e] = own ? hist[nb - 1 - 4 * tid - e] : 0; sl += c[e]; }
+      const int excl = dexcl_sum(sl, tmp);
+      if (own && excl < need && excl + sl >= need) {
+        int acc = excl, d = nb - 1 - 4 * tid, e = 0;
+        for (; e < 3; ++e) {
+          if (acc + c[e] >= need) break;
+          acc += c[e];
+          d -= 1;
         }
-        const uint64_t hit = __ballot(incl >= need);
-        const int first = hit ? __ffsll((unsigned long long)hit) - 1 : 63;
-        if (lane == first) {
-          int acc = incl - sl, d = 255 - 4 * lane, e = 0;
-          for (; e < 3; ++e) {
-            if (acc + c[e] >= need) break;
-            acc += c[e];
-            d -= 1;
-          }
-          misc[0] = d;
-          misc[1] = need - acc;
-          misc[2] = acc;
-          misc[3] = c[e];
-        }
+        misc[0] = d;
+        misc[1] = need - acc;   // how far into bin d's keys the statistic lies
+        misc[2] = acc;          // keys in the bins above
+        misc[3] = c[e];         // keys in bin d
       }
       __syncthreads();
-      prefix |= (uint32_t)misc[0] << shift;
-      ge += misc[2];
+      const int d = misc[0], cd = misc[3];
       need = misc[1];
-      if (shift == 0) ge += misc[3];
-      pmask |= 255u << shift;
+      ge += misc[2];
+      prefix |= (uint32_t)d << shift;
+      pmask |= (uint32_t)(nb - 1) << shift;
+      if (lv == 2) {            // every key of the last bin equals prefix
+        ge += cd;
+        __syncthreads();
+        break;
+      }
+      if (cd <= DEC_CAND) {
+        for (int e = 0; e < per; ++e) {
+          const uint32_t k = myrow[e];
+          if (k != 0 && j0 + e < m && (k & pmask) == prefix) cand[atomicAdd(&misc[4], 1)] = k;
+        }
+        __syncthreads();
+        if (tid < cd) {
+          const uint32_t v = cand[tid];
+          int gt = 0, eq = 0;
+          for (int u = 0; u < cd; u += 4) {
+            const uint4 w = *(const uint4*)&cand[u];
+            gt += (w.x > v) + (w.y > v) + (w.z > v) + (w.w > v);
+            eq += (w.x == v) + (w.y == v) + (w.z == v) + (w.w == v);
+          }
+          if (gt < need && gt + eq >= need) {   // the keys equal to the statistic agree
+            misc[5] = (int)v;
+            misc[6] = gt + eq;
+          }
+        }
+        __syncthreads();
+        const uint32_t V = (uint32_t)misc[5];
+        ge += misc[6];
+        __syncthreads();
+        return make_uint2(V, (uint32_t)ge);
+      }
       __syncthreads();
     }
     return make_uint2(prefix, (uint32_t)ge);
@@ -420,8 +509,8 @@ __global__ __launch_bounds__(DEC_SEL_NT) void decode_select_kernel(DecodeArgs a)
   // ---- compaction + reposition (exact_2.py:587-603) ----
   int cnt = 0;
   for (int e = 0; e < j1 - j0; ++e) cnt += final_j(j0 + e, myrow[e]);
-  const int base = dexcl_sum(cnt, tmp);
-  const int total = dsum(cnt, tmp);
+  int total;
+  const int base = dexcl_sum(cnt, tmp, &total);
   float mloc = -INFINITY;
   {
     int rank = base - 1;
@@ -506,51 +595,67 @@ __global__ __launch_bounds__(256) void decode_attend_kernel(DecodeArgs a) {
       q2[e] = x2[e] * cs + x1[e] * sn;
     }
   }
-  float mrun = -INFINITY, lrun = 0.0f, acc1[NPL], acc2[NPL];
-#pragma unroll
-  for (int e = 0; e < NPL; ++e) { acc1[e] = 0.0f; acc2[e] = 0.0f; }
+  // this group's four slots: indices first, then every K / V row request, then the arithmetic
   const int32_t* irow = a.idx + (int64_t)hi * a.k_max;
   const float* nrow = a.newpos_k + (int64_t)hi * a.k_max;
-  for (int sb = s0; sb < s1; sb += 16) {
-    const int s = sb + grp;
+  constexpr int U = DEC_SPL / 16;            // slots per group
+  int jv[U];
+  bool okv[U];
+  float npk[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int s = s0 + grp * U + u;
     const int j = s < s1 ? irow[s] : -1;
-    const bool ok = j >= 0 && j < m && (!a.causal || j <= p);   // sentinel m (exact_2.py:615; :195, 210)
-    const int jc = ok ? j : 0;
-    float x1[NPL], x2[NPL], v1[NPL], v2[NPL];
-    const int64_t kb = (int64_t)hk * a.k_hs + (int64_t)jc * a.k_ts + d0;
-    const int64_t vb = (int64_t)hk * a.v_hs + (int64_t)jc * a.v_ts + d0;
-    load_n<DT, NPL>(a.k, kb, x1);
-    load_n<DT, NPL>(a.k, kb + D / 2, x2);
-    load_n<DT, NPL>(a.v, vb, v1);
-    load_n<DT, NPL>(a.v, vb + D / 2, v2);
-    const float npk = ok ? nrow[s] : 0.0f;
+    okv[u] = j >= 0 && j < m && (!a.causal || j <= p);   // sentinel m (exact_2.py:615; :195, 210)
+    jv[u] = okv[u] ? j : 0;
+    npk[u] = s < s1 ? nrow[s] : 0.0f;
+  }
+  float x1[U][NPL], x2[U][NPL], v1[U][NPL], v2[U][NPL];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int64_t kb = (int64_t)hk * a.k_hs + (int64_t)jv[u] * a.k_ts + d0;
+    const int64_t vb = (int64_t)hk * a.v_hs + (int64_t)jv[u] * a.v_ts + d0;
+    load_n<DT, NPL>(a.k, kb, x1[u]);
+    load_n<DT, NPL>(a.k, kb + D / 2, x2[u]);
+    load_n<DT, NPL>(a.v, vb, v1[u]);
+    load_n<DT, NPL>(a.v, vb + D / 2, v2[u]);
+  }
+  float sc[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
     float part = 0.0f;
 #pragma unroll
     for (int e = 0; e < NPL; ++e) {
       float sn, cs;
-      fast_sincos(npk * invf[e], sn, cs);
+      fast_sincos(npk[u] * invf[e], sn, cs);
       cs = cs * a.rope_scale;
       sn = sn * a.rope_scale;
-      const float k1 = x1[e] * cs - x2[e] * sn;
-      const float k2 = x2[e] * cs + x1[e] * sn;
+      const float k1 = x1[u][e] * cs - x2[u][e] * sn;
+      const float k2 = x2[u][e] * cs + x1[u][e] * sn;
       part = fmaf(q2[e], k2, fmaf(q1[e], k1, part));
     }
     part += __shfl_xor(part, 1, 64);
     part += __shfl_xor(part, 2, 64);
     part += __shfl_xor(part, 4, 64);
     part += __shfl_xor(part, 8, 64);
-    if (ok) {
-      const float sc = part * a.sm_scale;
-      const float mnew = fmaxf(mrun, sc);
-      const float alpha = __expf(mrun - mnew);        // 0 on the group's first slot
-      const float pw = __expf(sc - mnew);
-      lrun = lrun * alpha + pw;
+    sc[u] = okv[u] ? part * a.sm_scale : -INFINITY;
+  }
+  float mrun = -INFINITY;
+#pragma unroll
+  for (int u = 0; u < U; ++u) mrun = fmaxf(mrun, sc[u]);
+  float lrun = 0.0f, acc1[NPL], acc2[NPL];
+#pragma unroll
+  for (int e = 0; e < NPL; ++e) { acc1[e] = 0.0f; acc2[e] = 0.0f; }
+  if (mrun > -INFINITY) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const float pw = okv[u] ? __expf(sc[u] - mrun) : 0.0f;
+      lrun += pw;
 #pragma unroll
       for (int e = 0; e < NPL; ++e) {
-        acc1[e] = acc1[e] * alpha + pw * v1[e];
-        acc2[e] = acc2[e] * alpha + pw * v2[e];
+        acc1[e] = fmaf(pw, v1[u][e], acc1[e]);
+        acc2[e] = fmaf(pw, v2[u][e], acc2[e]);
       }
-      mrun = mnew;
     }
   }
   if (l16 == 0) { sm_m[grp] = mrun; sm_l[grp] = lrun; }
@@ -580,36 +685,58 @@ __global__ __launch_bounds__(256) void decode_attend_kernel(DecodeArgs a) {
   }
 }
 
+// merge the splits of one query: 256 threads, 256 / D per dim
 template <int DT, int D>
-__global__ __launch_bounds__(D) void decode_combine_kernel(DecodeArgs a, int nsplit) {
-  const int hi = blockIdx.x, d = threadIdx.x;
-  const float* part = a.part + (int64_t)hi * nsplit * (D + 2);
-  float M = -INFINITY;
-  for (int s = 0; s < nsplit; ++s) M = fmaxf(M, part[s * (D + 2) + D]);
-  float A = 0.0f, L = 0.0f;
-  if (M > -INFINITY) {
-    for (int s = 0; s < nsplit; ++s) {
-      const float ms = part[s * (D + 2) + D];
-      if (ms == -INFINITY) continue;
-      const float w = __expf(ms - M);
-      A += part[s * (D + 2) + d] * w;
-      L += part[s * (D + 2) + D + 1] * w;
-    }
+__global__ __launch_bounds__(256) void decode_combine_kernel(DecodeArgs a, int ns) {
+  __shared__ float msplit[256], lsplit[256], wsplit[256];
+  __shared__ float red[256 / D][D];
+  const int hi = blockIdx.x;
+  const float* parts = a.part + (int64_t)hi * ns * (D + 2);
+  for (int u = threadIdx.x; u < ns; u += 256) {
+    msplit[u] = parts[u * (D + 2) + D];
+    lsplit[u] = parts[u * (D + 2) + D + 1];
   }
-  const float o = L > 0.0f ? A / L : 0.0f;      // no valid slot: zeros
-  const int64_t oi = (int64_t)hi * D + d;
-  if constexpr (DT == DT_F32) ((float*)a.out)[oi] = o;
-  else ((uint16_t*)a.out)[oi] = (uint16_t)(DT == DT_BF16 ? f32_to_bf16_bits(o) : f32_to_f16_bits(o));
+  __syncthreads();
+  float Mx = -INFINITY;
+  for (int u = 0; u < ns; ++u) Mx = fmaxf(Mx, msplit[u]);
+  for (int u = threadIdx.x; u < ns; u += 256)
+    wsplit[u] = (Mx > -INFINITY && msplit[u] > -INFINITY) ? __expf(msplit[u] - Mx) : 0.0f;
+  __syncthreads();
+  float L = 0.0f;
+  for (int u = 0; u < ns; ++u) L += lsplit[u] * wsplit[u];
+  constexpr int NH = 256 / D;
+  const int dd = threadIdx.x % D, hf = threadIdx.x / D;
+  float A = 0.0f;
+#pragma unroll 8
+  for (int u = hf; u < ns; u += NH) A += parts[u * (D + 2) + dd] * wsplit[u];
+  red[hf][dd] = A;
+  __syncthreads();
+  if (hf == 0) {
+    float At = 0.0f;
+#pragma unroll
+    for (int u = 0; u < NH; ++u) At += red[u][dd];
+    const float o = L > 0.0f ? At / L : 0.0f;      // no valid slot: zeros
+    const int64_t oi = (int64_t)hi * D + dd;
+    if constexpr (DT == DT_F32) ((float*)a.out)[oi] = o;
+    else ((uint16_t*)a.out)[oi] = (uint16_t)(DT == DT_BF16 ? f32_to_bf16_bits(o) : f32_to_f16_bits(o));
+  }
 }
+
 
 // ------------------------------------------------------------------------------------------
 // launchers
 // ------------------------------------------------------------------------------------------
 template <int DT, int D>
-static hipError_t launch_scores_t(const DecodeArgs& a, float* qrot, hipStream_t st) {
-  hipLaunchKernelGGL((decode_qrot_kernel<DT, D>), dim3(a.H * a.Q), dim3(D / 2), 0, st, a, qrot);
-  dim3 grid((a.M + 63) / 64, (a.Hkv + DEC_HG - 1) / DEC_HG);
-  hipLaunchKernelGGL((decode_score_kernel<DT, D>), grid, dim3(256), 0, st, a, (const float*)qrot);
+static hipError_t launch_scores_t(const DecodeArgs& a0, float* qrot, hipStream_t st) {
+  DecodeArgs a = a0;
+  dim3 grid((a.M + 63) / 64, (a.Hkv + dec_hg<DT>() - 1) / dec_hg<DT>());
+  if (decode_qrot_in_lds(DT, a.H, a.Hkv, a.Q, D)) {
+    hipLaunchKernelGGL((decode_score_kernel<DT, D, true>), grid, dim3(256), 0, st, a);
+  } else {
+    hipLaunchKernelGGL((decode_qrot_kernel<DT, D>), dim3(a.H * a.Q), dim3(D / 2), 0, st, a, qrot);
+    a.qrot = qrot;
+    hipLaunchKernelGGL((decode_score_kernel<DT, D, false>), grid, dim3(256), 0, st, a);
+  }
   return hipGetLastError();
 }
 
@@ -638,8 +765,9 @@ hipError_t launch_decode_select(const DecodeArgs& a, hipStream_t st) {
 template <int DT, int D>
 static hipError_t launch_attend_t(const DecodeArgs& a, hipStream_t st) {
   const int ns = decode_nsplit(a.k_max);
+  if (ns > 256) return hipErrorInvalidValue;
   hipLaunchKernelGGL((decode_attend_kernel<DT, D>), dim3(ns, a.H * a.Q), dim3(256), 0, st, a);
-  hipLaunchKernelGGL((decode_combine_kernel<DT, D>), dim3(a.H * a.Q), dim3(D), 0, st, a, ns);
+  hipLaunchKernelGGL((decode_combine_kernel<DT, D>), dim3(a.H * a.Q), dim3(256), 0, st, a, ns);
   return hipGetLastError();
 }
 

@@ -150,9 +150,11 @@ struct DecodeArgs {
   int32_t* set_size;      // (H, Q) or null
   int causal;             // attend also masks slots past the query's position
   float* part;            // (H * Q, nsplit, D + 2) split states of the attend
+  const float* qrot;      // (H, Q, D) rotated queries, or null (the score kernel rotates them)
   void* out;              // (H, Q, D)
 };
 
+// qrot: workspace of (H, Q, D) floats, used when a workgroup's query rows outgrow its LDS
 hipError_t launch_decode_scores(int dtype, int D, const DecodeArgs& a, float* qrot, hipStream_t st);
 bool decode_select_in_lds(int M);
 size_t decode_keys_bytes(int H, int Q, int M);

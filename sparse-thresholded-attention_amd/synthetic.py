@@ -79,6 +79,8 @@ class Config:
     variant: str = "shared"     # "shared" (tile-shared sets), "pq" (PQ Union), "pqstream", "dca"
     select_score: str = "freq"  # key ranking: votes, or margin / expmass weighted votes
     dca: tuple = None           # (chunk_size, pretrain_len, local_window) of the DCA variant
+    decode_q: int = 1           # decode variant: queries per step (the last decode_q positions)
+    pct_decode: float = 100.0   # decode variant: top-% of the threshold passers kept
 
     def geometry(self):
         """(inv_freq, pos_scale, rope_scale) of the selection + attend geometry."""
@@ -115,6 +117,12 @@ CONFIGS = {
     # 3s: the same shape through PQ Stream (per-query keep, streamed positions, no k_max), BN 32
     "c3s": Config("c3s_pq_stream_32h_d128_16k_bf16", 32, 32, 16384, 128, torch.bfloat16, 32, 4.0, 0.01,
                   10000.0, pi_pos_scale(4096, 16384), variant="pqstream"),
+    # decode at config 1's shape: one new query per head over a 12288-key cache (PI 4096 -> 12288)
+    "c1d": Config("c1d_decode_pi_32h_d128_12k_bf16", 32, 32, 12288, 128, torch.bfloat16, 64, 5.0, 0.01,
+                  10000.0, pi_pos_scale(4096, 12288), variant="decode"),
+    # decode at config 2's shape: GQA 32q / 8kv over a 32768-key cache, YaRN geometry
+    "c2d": Config("c2d_decode_yarn_32q8kv_d128_32k_bf16", 32, 8, 32768, 128, torch.bfloat16, 64, 5.0, 0.005,
+                  500000.0, 1.0, yarn=(4.0, 8192, 32.0, 1.0), variant="decode"),
     # 4: dual chunk attention at 64k: chunk 4096, local window 512, pretraining length 4096
     #    (chunk_len 3584), base RoPE, dense causal attention with remapped positions
     "c4": Config("c4_dca_32h_d128_64k_bf16", 32, 32, 65536, 128, torch.bfloat16, 64, 5.0, 0.0025,

@@ -216,7 +216,8 @@ def _decode_args(**kw):
 
 
 @pytest.mark.parametrize("field,value,code", [
-    ("D", 96, -2), ("M", 0, -1), ("Q", 0, -1), ("q_pos0", 12288, -1), ("k_max", 0, -1), ("Hkv", 5, -1),
+    ("D", 96, -2), ("M", 0, -1), ("Q", 0, -1), ("q_pos0", 12288, -1), ("k_max", 0, -2), ("k_max", 20000, -2),
+    ("Hkv", 5, -1),
     ("n_local", -1, -2), ("dtype", 7, -1),
 ])
 def test_decode_invalid_arguments_are_rejected(field, value, code):
@@ -242,7 +243,7 @@ def test_decode_workspace_size_matches_layout():
     n = lib.sta_decode_workspace_size(ctypes.byref(_decode_args()))
     need = 32 * 128 * 4 + 32 * 12288 * 4 + 32 * 4 + 32 * 32 * 130 * 4    # qrot, scores, sizes, splits
     assert need <= n < need + 5 * 256
-    # past the LDS key store (M > 35840) the selection keeps its keys in the workspace
+    # past the LDS key store (M > 33792) the selection keeps its keys in the workspace
     n2 = lib.sta_decode_workspace_size(ctypes.byref(_decode_args(M=40000, q_pos0=39999)))
     need2 = 32 * 128 * 4 + 32 * 40000 * 4 + 32 * 1024 * 40 * 4 + 32 * 4 + 32 * 32 * 130 * 4
     assert need2 <= n2 < need2 + 5 * 256
