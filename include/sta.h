@@ -282,7 +282,9 @@ int sta_dca_attention(const sta_dca_args* args, void* stream);
 /* keys at q_pos = q_pos0.  Selection: keep s >= max - tau, the top pct_decode% of those by    */
 /* score when pct_decode < 100, plus the forced keys [0, n_global) U [q_pos - n_local + 1,     */
 /* q_pos]; above k_max the forced keys and the best-scored others (tie-inclusive); positions   */
-/* repositioned as in the prefill (pos_scale); idx ascending, truncated to k_max, sentinel m_i. */
+/* repositioned as in the prefill; idx ascending, truncated to k_max, sentinel m_i.  Scores   */
+/* under the a-triple, reposition with pos_scale_c, attend under (inv_freq_c, rope_scale_c):   */
+/* PI_exact / exact / YaRN_exact pass one geometry twice, the hybrid file two.                 */
 /* ------------------------------------------------------------------------------------------ */
 typedef struct sta_decode_args {
   const void* q;            /* (H, Q, D) raw queries */
@@ -294,8 +296,11 @@ typedef struct sta_decode_args {
   int32_t dtype;
   int32_t H, Hkv, Q, M, D;
   const float* tau;         /* (H,) */
-  const float* inv_freq;    /* (D/2,) */
-  float pos_scale, rope_scale, sm_scale;
+  const float* inv_freq_a;  /* (D/2,) scores (selection geometry) */
+  float pos_scale_a, rope_scale_a;
+  float pos_scale_c;        /* reposition: cpos = key * pos_scale_c */
+  const float* inv_freq_c;  /* (D/2,) attend geometry */
+  float rope_scale_c, sm_scale;
   int32_t q_pos0;           /* position of query 0; q_pos0 + Q <= M (any q_pos0 >= 0 for the
                                scores alone) */
   int32_t n_global, n_local, k_max;   /* k_max <= 16384 */

@@ -1,0 +1,154 @@
+"""Model integration: route a Llama model's attention through the HIP kernels.
+
+The reference patches ``LlamaAttention.forward`` (shared_selection_triton_exact_2.py:658-767,
+shared_selection_triton_exact.py:595-700, shared_selection_triton_YaRN_exact.py:668-776,
+shared_selection_triton_hybrid_exact.py:683-811).  The patched forward here keeps its contract:
+
+* the KV cache holds the raw (unrotated) K and V -- the kernels rotate internally;
+* pos_scale = min(1, context_window / L) is frozen at prefill (L = max_len, else the prefill
+  length) and reused by every decode step;
+* a prefill (empty cache) with prefill_mode "shared" runs the shared-selection prefill and keeps
+  its statistics on the module (spi_last_shared, spi_last_kept, spi_last_kpct, ...);
+* every other call -- decode steps, and prefill with prefill_mode "perquery" -- lets each query
+  select its own set over the cache prefix up to its position.
+
+Differences by design: K and V keep their kv heads (grouped-query attention runs natively instead
+of through repeat_kv); the per-query path serves all of a call's queries in batches of up to
+``PER_QUERY_BATCH`` through one launch sequence each, instead of a Python loop per token; the
+decode backends ("torch" / "triton") select between the reference's two attend rules, which agree
+whenever a query's position is the last key it sees, as in the model.
+"""
+
+import torch
+
+from _decode import decode_attention
+from _shared_prefill import shared_prefill
+
+PER_QUERY_BATCH = 256          # queries per per-query launch: bounds the (H, Q, M) score buffer
+
+
+def base_inv_freq_of(model):
+    """theta^(-2i/D) from the model config (the hybrid file's Kernel C frequencies,
+    hybrid_exact.py:712-726)."""
+    cfg = model.config
+    head_dim = getattr(cfg, "head_dim", None) or (cfg.hidden_size // cfg.num_attention_heads)
+    theta = 10000.0
+    rp = getattr(cfg, "rope_parameters", None) or getattr(cfg, "rope_scaling", None)
+    if isinstance(rp, dict) and rp.get("rope_theta"):
+        theta = float(rp["rope_theta"])
+    elif getattr(cfg, "rope_theta", None):
+        theta = float(cfg.rope_theta)
+    return 1.0 / (theta ** (torch.arange(0, head_dim, 2, dtype=torch.float32) / head_dim))
+
+
+def install(model, geometry, pct=30.0, context_window=4096, n_global=32, n_local=32, tile=32, k_max=1024,
+            block_n=32, block_k=32, max_len=None, pct_decode=100.0, decode_backend="torch",
+            select_backend="torch", prefill_mode="shared", measure=False, select_score="freq", rope_scale=None):
+    """geometry: "pi" (rotary frequencies, positions compressed by the frozen pos_scale), "yarn"
+    (rotary frequencies as loaded, raw positions) or a dict for "hybrid" {"inv_freq_a",
+    "rope_scale_a", "inv_freq_c"} (selection under a raw-position geometry, reposition and attend
+    under base RoPE with the frozen pos_scale).  rope_scale: the rotation scale of "pi" / "yarn"
+    (default: the rotary embedding's attention_scaling)."""
+    import transformers.models.llama.modeling_llama as ml
+    rotary = model.model.rotary_emb
+    inv_freq = rotary.inv_freq.detach().float()
+    if rope_scale is None:
+        rope_scale = float(getattr(rotary, "attention_scaling", 1.0))
+    for li, layer in enumerate(model.model.layers):
+        sa = layer.self_attn
+        dev = sa.q_proj.weight.device
+        if isinstance(geometry, dict):
+            sa.spi_geometry = "hybrid"
+            sa.spi_inv_freq_a = geometry["inv_freq_a"].to(dev)
+            sa.spi_rope_scale_a = float(geometry["rope_scale_a"])
+            sa.spi_inv_freq_c = geometry["inv_freq_c"].to(dev)
+            sa.spi_rope_scale_c = 1.0
+            sa.spi_pos_scale_c = None
+        else:
+            sa.spi_geometry = geometry
+            sa.spi_inv_freq = inv_freq.to(dev)
+            sa.spi_rope_scale = float(rope_scale)
+        sa.spi_pct = pct
+        sa.spi_W = context_window
+        sa.spi_ng = n_global
+        sa.spi_nl = n_local
+        sa.spi_tile = tile
+        sa.spi_kmax = k_max
+        sa.spi_block_n = block_n
+        sa.spi_block_k = block_k
+        sa.spi_layer_idx = getattr(sa, "layer_idx", li)
+        sa.spi_max_len = max_len
+        sa.spi_pos_scale = None
+        sa.spi_pct_decode = pct_decode
+        sa.spi_decode_backend = decode_backend
+        sa.spi_select_backend = select_backend
+        sa.spi_prefill_mode = prefill_mode
+        sa.spi_measure = measure
+        sa.spi_select_score = select_score
+    ml.LlamaAttention.forward = spi_forward
+
+
+def _geometry(self, pos_frozen):
+    """(inv_freq_a, pos_scale_a, rope_scale_a, inv_freq_c, pos_scale_c, rope_scale_c)."""
+    if self.spi_geometry == "hybrid":
+        return (self.spi_inv_freq_a, 1.0, self.spi_rope_scale_a, self.spi_inv_freq_c, pos_frozen,
+                self.spi_rope_scale_c)
+    ps = 1.0 if self.spi_geometry == "yarn" else pos_frozen
+    return self.spi_inv_freq, ps, self.spi_rope_scale, self.spi_inv_freq, ps, self.spi_rope_scale
+
+
+def spi_forward(self, hidden_states, position_embeddings=None, attention_mask=None, past_key_values=None,
+                **kwargs):
+    B, N, _ = hidden_states.shape
+    assert B == 1, "batch size must be 1 (the kernels take one sequence, as the reference's)"
+    hs = (B, N, -1, self.head_dim)
+    q = self.q_proj(hidden_states).view(hs).transpose(1, 2)
+    k = self.k_proj(hidden_states).view(hs).transpose(1, 2)
+    v = self.v_proj(hidden_states).view(hs).transpose(1, 2)
+
+    # the cache holds raw k, v; HF may pass it as past_key_values or (older) past_key_value
+    cache = past_key_values if past_key_values is not None else kwargs.get("past_key_value", None)
+    past_len = 0
+    if cache is not None:
+        try:
+            past_len = int(cache.get_seq_length(self.spi_layer_idx))
+        except TypeError:
+            past_len = int(cache.get_seq_length())
+        k, v = cache.update(k, v, self.spi_layer_idx)
+
+    # pos_scale frozen at prefill from max_len (or the prefill length), reused at decode
+    if past_len == 0:
+        L_target = self.spi_max_len if self.spi_max_len is not None else N
+        frozen = min(1.0, self.spi_W / float(L_target))
+        if self.spi_geometry == "hybrid":
+            self.spi_pos_scale_c = frozen
+        else:
+            self.spi_pos_scale = frozen
+    frozen = self.spi_pos_scale_c if self.spi_geometry == "hybrid" else self.spi_pos_scale
+    ifa, psa, rsa, ifc, psc, rsc = _geometry(self, frozen)
+
+    if past_len == 0 and self.spi_prefill_mode == "shared":
+        out, shared_size, kept_size, kpct, overflow, kpct_meas, overflow20 = shared_prefill(
+            q, k, v, self.tau_head_vec, ifa, psa, rsa, ifc, psc, rsc, self.spi_pct, self.scaling, self.spi_ng,
+            self.spi_nl, self.spi_tile, self.spi_kmax, past_len, self.spi_measure, self.spi_select_score)
+        self.spi_last_shared = shared_size.detach()
+        self.spi_last_kept = kept_size.detach()
+        self.spi_last_kpct = kpct.detach()
+        self.spi_last_overflow = overflow.detach()
+        self.spi_last_kpct_meas = kpct_meas.detach()
+        self.spi_last_overflow20 = overflow20.detach()
+    else:
+        # each query at position past_len + i over the keys [0, past_len + i]
+        causal = self.spi_decode_backend == "triton"
+        outs = []
+        for c0 in range(0, N, PER_QUERY_BATCH):
+            c1 = min(N, c0 + PER_QUERY_BATCH)
+            M = past_len + c1
+            outs.append(decode_attention(
+                q[0, :, c0:c1, :], k[:, :, :M, :], v[:, :, :M, :], self.tau_head_vec, ifa, past_len + c0, psa, rsa,
+                self.scaling, self.spi_ng, self.spi_nl, self.spi_kmax, self.spi_pct_decode, causal,
+                inv_freq_c=ifc, pos_scale_c=psc, rope_scale_c=rsc))
+        out = torch.cat(outs, dim=1).unsqueeze(0)              # (1, H, N, D)
+
+    attn_output = out.transpose(1, 2).reshape(B, N, -1).contiguous()
+    return self.o_proj(attn_output), None

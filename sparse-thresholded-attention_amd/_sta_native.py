@@ -124,8 +124,9 @@ class DecodeArgsC(ctypes.Structure):
         ("v_head_stride", ctypes.c_int64), ("v_tok_stride", ctypes.c_int64),
         ("dtype", ctypes.c_int32), ("H", ctypes.c_int32), ("Hkv", ctypes.c_int32),
         ("Q", ctypes.c_int32), ("M", ctypes.c_int32), ("D", ctypes.c_int32),
-        ("tau", ctypes.c_void_p), ("inv_freq", ctypes.c_void_p),
-        ("pos_scale", ctypes.c_float), ("rope_scale", ctypes.c_float), ("sm_scale", ctypes.c_float),
+        ("tau", ctypes.c_void_p), ("inv_freq_a", ctypes.c_void_p),
+        ("pos_scale_a", ctypes.c_float), ("rope_scale_a", ctypes.c_float), ("pos_scale_c", ctypes.c_float),
+        ("inv_freq_c", ctypes.c_void_p), ("rope_scale_c", ctypes.c_float), ("sm_scale", ctypes.c_float),
         ("q_pos0", ctypes.c_int32), ("n_global", ctypes.c_int32), ("n_local", ctypes.c_int32),
         ("k_max", ctypes.c_int32), ("pct_decode", ctypes.c_double), ("causal", ctypes.c_int32),
         ("out", ctypes.c_void_p), ("idx", ctypes.c_void_p), ("newpos_k", ctypes.c_void_p),
@@ -741,7 +742,10 @@ class DecodePlan:
     scores, the selection and the attend on the current stream and allocates nothing."""
 
     def __init__(self, q, k, v, tau, inv_freq, q_pos0, pos_scale=1.0, rope_scale=1.0, sm_scale=None,
-                 n_global=32, n_local=32, k_max=1024, pct_decode=100.0, causal=False, want_scores=False):
+                 n_global=32, n_local=32, k_max=1024, pct_decode=100.0, causal=False, want_scores=False,
+                 inv_freq_c=None, pos_scale_c=None, rope_scale_c=None):
+        """inv_freq / pos_scale / rope_scale: the selection geometry; the *_c triple (default: the
+        same) repositions (pos_scale_c) and attends (inv_freq_c, rope_scale_c)."""
         if not q.is_cuda:
             raise RuntimeError("sparse-thresholded attention runs on a HIP device only; got a CPU tensor")
         if q.dtype not in DTYPES:
@@ -761,6 +765,9 @@ class DecodePlan:
         if tau.numel() == 1 and H > 1:
             tau = tau.expand(H).contiguous()
         ifr = inv_freq.to(device=dev, dtype=torch.float32).contiguous()
+        ifc = inv_freq_c.to(device=dev, dtype=torch.float32).contiguous() if inv_freq_c is not None else ifr
+        pos_scale_c = pos_scale if pos_scale_c is None else pos_scale_c
+        rope_scale_c = rope_scale if rope_scale_c is None else rope_scale_c
         self.args = a = DecodeArgsC()
         a.q, a.k = _ptr(qh), _ptr(kh)
         a.v = _ptr(vh) if vh is not None else None
@@ -770,11 +777,12 @@ class DecodePlan:
             a.v_head_stride, a.v_tok_stride = vh.stride(0), vh.stride(1)
         a.dtype = DTYPES[qh.dtype]
         a.H, a.Hkv, a.Q, a.M, a.D = H, kh.shape[0], Q, M, D
-        a.tau, a.inv_freq = _ptr(tau), _ptr(ifr)
-        a.pos_scale, a.rope_scale, a.sm_scale = float(pos_scale), float(rope_scale), float(sm_scale)
+        a.tau, a.inv_freq_a, a.inv_freq_c = _ptr(tau), _ptr(ifr), _ptr(ifc)
+        a.pos_scale_a, a.rope_scale_a, a.sm_scale = float(pos_scale), float(rope_scale), float(sm_scale)
+        a.pos_scale_c, a.rope_scale_c = float(pos_scale_c), float(rope_scale_c)
         a.q_pos0, a.n_global, a.n_local, a.k_max = int(q_pos0), int(n_global), int(n_local), int(k_max)
         a.pct_decode, a.causal = float(pct_decode), int(bool(causal))
-        self._keep = (qh, kh, vh, tau, ifr)
+        self._keep = (qh, kh, vh, tau, ifr, ifc)
         self.out = {
             "out": torch.empty((H, Q, D), dtype=qh.dtype, device=dev),
             "idx": torch.empty((H, Q, k_max), dtype=torch.int32, device=dev),
@@ -830,9 +838,10 @@ class DecodePlan:
 
 
 def decode_attention(q, k, v, tau, inv_freq, q_pos0, pos_scale=1.0, rope_scale=1.0, sm_scale=None,
-                     n_global=32, n_local=32, k_max=1024, pct_decode=100.0, causal=False, want_scores=False):
+                     n_global=32, n_local=32, k_max=1024, pct_decode=100.0, causal=False, want_scores=False,
+                     inv_freq_c=None, pos_scale_c=None, rope_scale_c=None):
     """Scores, selection and attend of Q queries (H, Q, D) over the cache k, v (Hkv, M, D).
     Returns a dict of device tensors: out (H, Q, D), idx (H, Q, k_max) int32 (sentinel m_i),
     newpos_k, newpos_q, set_size and, with want_scores, scores (H, Q, M)."""
     return DecodePlan(q, k, v, tau, inv_freq, q_pos0, pos_scale, rope_scale, sm_scale, n_global, n_local,
-                      k_max, pct_decode, causal, want_scores).run()
+                      k_max, pct_decode, causal, want_scores, inv_freq_c, pos_scale_c, rope_scale_c).run()

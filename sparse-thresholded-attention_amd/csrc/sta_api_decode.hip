@@ -80,9 +80,12 @@ DecodeArgs dec_args_of(const sta_decode_args* a, const DecLayout& L) {
   d.Q = a->Q;
   d.M = a->M;
   d.q_pos0 = a->q_pos0;
-  d.inv_freq = a->inv_freq;
-  d.pos_scale = a->pos_scale;
-  d.rope_scale = a->rope_scale;
+  d.inv_freq_a = a->inv_freq_a;
+  d.pos_scale_a = a->pos_scale_a;
+  d.rope_scale_a = a->rope_scale_a;
+  d.pos_scale_c = a->pos_scale_c;
+  d.inv_freq_c = a->inv_freq_c;
+  d.rope_scale_c = a->rope_scale_c;
   d.sm_scale = a->sm_scale;
   d.tau = a->tau;
   d.n_global = a->n_global;
@@ -107,7 +110,7 @@ int dec_scores(const sta_decode_args* a, const DecLayout& L, DecodeArgs d, float
   const int64_t strides[6] = {a->q_head_stride, a->q_tok_stride, a->k_head_stride, a->k_tok_stride, 0, 0};
   int rc = check_qkv_ptrs(a->dtype, a->q, a->k, nullptr, strides, false);
   if (rc != STA_OK) return rc;
-  if (!a->inv_freq) return fail(STA_ERR_INVALID_ARG, "inv_freq must be non-NULL");
+  if (!a->inv_freq_a) return fail(STA_ERR_INVALID_ARG, "inv_freq_a must be non-NULL");
   if (!scores) return fail(STA_ERR_INVALID_ARG, "scores must be non-NULL");
   d.scores = scores;
   hipError_t e = launch_decode_scores(a->dtype, a->D, d, (float*)((char*)a->workspace + L.qrot_off), st);
@@ -128,8 +131,8 @@ int dec_attend(const sta_decode_args* a, const DecodeArgs& d, hipStream_t st) {
                               a->k_tok_stride, a->v_head_stride, a->v_tok_stride};
   int rc = check_qkv_ptrs(a->dtype, a->q, a->k, a->v, strides, true);
   if (rc != STA_OK) return rc;
-  if (!a->inv_freq || !a->out || !a->idx || !a->newpos_k || !a->newpos_q)
-    return fail(STA_ERR_INVALID_ARG, "inv_freq, out, idx, newpos_k and newpos_q must be non-NULL");
+  if (!a->inv_freq_c || !a->out || !a->idx || !a->newpos_k || !a->newpos_q)
+    return fail(STA_ERR_INVALID_ARG, "inv_freq_c, out, idx, newpos_k and newpos_q must be non-NULL");
   hipError_t e = launch_decode_attend(a->dtype, a->D, d, st);
   return e == hipSuccess ? STA_OK : hip_fail(e, "decode attend");
 }

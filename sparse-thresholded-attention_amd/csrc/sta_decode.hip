@@ -91,12 +91,12 @@ __global__ __launch_bounds__(D / 2) void decode_qrot_kernel(DecodeArgs a, float*
   const int64_t base = (int64_t)h * a.q_hs + (int64_t)i * a.q_ts;
   const float x1 = load1<DT>(a.q, base + d);
   const float x2 = load1<DT>(a.q, base + D / 2 + d);
-  const float pb = (float)(a.q_pos0 + i) * a.pos_scale;
-  const float ang = pb * a.inv_freq[d];
+  const float pb = (float)(a.q_pos0 + i) * a.pos_scale_a;
+  const float ang = pb * a.inv_freq_a[d];
   float sn, cs;
   sincosf(ang, &sn, &cs);
-  cs = cs * a.rope_scale;
-  sn = sn * a.rope_scale;
+  cs = cs * a.rope_scale_a;
+  sn = sn * a.rope_scale_a;
   float* o = qrot + (int64_t)hi * D;
   const float p1 = x1 * cs, p2 = x2 * sn, p3 = x2 * cs, p4 = x1 * sn;
   o[d] = p1 - p2;                             // exact_2.py:256-257
@@ -153,12 +153,12 @@ __global__ __launch_bounds__(256) void decode_score_kernel(DecodeArgs a) {
       const int i = r % a.Q, hq = hk0 * G + r / a.Q;
       const int64_t base = (int64_t)hq * a.q_hs + (int64_t)i * a.q_ts;
       const float x1 = load1<DT>(a.q, base + f), x2 = load1<DT>(a.q, base + D / 2 + f);
-      const float pb = (float)(a.q_pos0 + i) * a.pos_scale;
-      const float ang = pb * a.inv_freq[f];
+      const float pb = (float)(a.q_pos0 + i) * a.pos_scale_a;
+      const float ang = pb * a.inv_freq_a[f];
       float sn, cs;
       sincosf(ang, &sn, &cs);
-      cs = cs * a.rope_scale;
-      sn = sn * a.rope_scale;
+      cs = cs * a.rope_scale_a;
+      sn = sn * a.rope_scale_a;
       const float p1 = x1 * cs, p2 = x2 * sn, p3 = x2 * cs, p4 = x1 * sn;
       qs[r * D + f] = p1 - p2;
       qs[r * D + D / 2 + f] = p3 + p4;
@@ -167,13 +167,13 @@ __global__ __launch_bounds__(256) void decode_score_kernel(DecodeArgs a) {
   // cos / sin of this key's frequencies t*NP .. t*NP + NP - 1
   float cs[NP], sn[NP];
   {
-    const float kb = (float)j * a.pos_scale;                            // exact_2.py:264
+    const float kb = (float)j * a.pos_scale_a;                            // exact_2.py:264
 #pragma unroll
     for (int p = 0; p < NP; ++p) {
-      const float ang = kb * a.inv_freq[t * NP + p];
+      const float ang = kb * a.inv_freq_a[t * NP + p];
       sincosf(ang, &sn[p], &cs[p]);
-      cs[p] = cs[p] * a.rope_scale;
-      sn[p] = sn[p] * a.rope_scale;
+      cs[p] = cs[p] * a.rope_scale_a;
+      sn[p] = sn[p] * a.rope_scale_a;
     }
   }
   if constexpr (QLDS) __syncthreads();
@@ -517,7 +517,7 @@ __global__ __launch_bounds__(DEC_SEL_NT) void decode_select_kernel(DecodeArgs a)
     for (int e = 0; e < j1 - j0; ++e) {
       if (final_j(j0 + e, myrow[e])) {
         rank += 1;
-        const float cp = (float)(j0 + e) * a.pos_scale;                  // exact_2.py:590
+        const float cp = (float)(j0 + e) * a.pos_scale_c;                  // exact_2.py:590
         mloc = fmaxf(mloc, cp - (float)rank);                            // :591
       }
     }
@@ -532,7 +532,7 @@ __global__ __launch_bounds__(DEC_SEL_NT) void decode_select_kernel(DecodeArgs a)
       const bool f = final_j(j, myrow[e]);
       if (f) {
         rank += 1;
-        const float cp = (float)j * a.pos_scale;
+        const float cp = (float)j * a.pos_scale_c;
         run = fmaxf(run, cp - (float)rank);
       }
       const float np = (float)rank + run;                                // exact_2.py:592
@@ -576,7 +576,7 @@ __global__ __launch_bounds__(256) void decode_attend_kernel(DecodeArgs a) {
   const int s0 = split * DEC_SPL, s1 = min(s0 + DEC_SPL, nslots);
   float invf[NPL];
 #pragma unroll
-  for (int e = 0; e < NPL; ++e) invf[e] = a.inv_freq[d0 + e];
+  for (int e = 0; e < NPL; ++e) invf[e] = a.inv_freq_c[d0 + e];
   // the query rotated at newpos_q
   float q1[NPL], q2[NPL];
   {
@@ -589,8 +589,8 @@ __global__ __launch_bounds__(256) void decode_attend_kernel(DecodeArgs a) {
     for (int e = 0; e < NPL; ++e) {
       float sn, cs;
       fast_sincos(npq * invf[e], sn, cs);
-      cs = cs * a.rope_scale;
-      sn = sn * a.rope_scale;
+      cs = cs * a.rope_scale_c;
+      sn = sn * a.rope_scale_c;
       q1[e] = x1[e] * cs - x2[e] * sn;
       q2[e] = x2[e] * cs + x1[e] * sn;
     }
@@ -628,8 +628,8 @@ __global__ __launch_bounds__(256) void decode_attend_kernel(DecodeArgs a) {
     for (int e = 0; e < NPL; ++e) {
       float sn, cs;
       fast_sincos(npk[u] * invf[e], sn, cs);
-      cs = cs * a.rope_scale;
-      sn = sn * a.rope_scale;
+      cs = cs * a.rope_scale_c;
+      sn = sn * a.rope_scale_c;
       const float k1 = x1[u][e] * cs - x2[u][e] * sn;
       const float k2 = x2[u][e] * cs + x1[u][e] * sn;
       part = fmaf(q2[e], k2, fmaf(q1[e], k1, part));

@@ -136,8 +136,11 @@ struct DecodeArgs {
   const void* v;
   int64_t v_hs, v_ts;
   int H, Hkv, Q, M, q_pos0;
-  const float* inv_freq;
-  float pos_scale, rope_scale, sm_scale;
+  const float* inv_freq_a;  // selection geometry (scores)
+  float pos_scale_a, rope_scale_a;
+  float pos_scale_c;        // reposition
+  const float* inv_freq_c;  // attend geometry
+  float rope_scale_c, sm_scale;
   const float* tau;       // (H,)
   int n_global, n_local, k_max;
   int use_pct;            // pct_decode < 100

@@ -59,3 +59,18 @@ def _decode_attend_kernelC(q, K, V, idx, newpos_k, newpos_q, inv_freq, rope_scal
     from _decode import decode_attend
     return decode_attend(q, K, V, idx[..., :k_max], newpos_k[..., :k_max], newpos_q, inv_freq, rope_scale,
                          sm_scale, q_pos=q_pos)
+
+
+# ---------------------------------------------------------------------------------------------
+# model integration: shared_selection_triton_exact_2.py:658-767
+# ---------------------------------------------------------------------------------------------
+def install_shared_pi_forward(model, pct=30.0, context_window=4096, n_global=32, n_local=32,
+                              tile=32, k_max=1024, block_n=32, block_k=32, max_len=None,
+                              pct_decode=100.0, decode_backend="torch", select_backend="torch",
+                              prefill_mode="shared", measure=False, select_score="freq"):
+    """Patch LlamaAttention.forward to route prefill and decode through the HIP kernels (PI
+    geometry: the model's rotary frequencies, positions compressed by pos_scale = min(1, W / L)
+    frozen at prefill).  Each attention module needs ``tau_head_vec`` (H,) set by the caller."""
+    from _install import install
+    install(model, "pi", pct, context_window, n_global, n_local, tile, k_max, block_n, block_k, max_len,
+            pct_decode, decode_backend, select_backend, prefill_mode, measure, select_score)

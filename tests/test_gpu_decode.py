@@ -212,3 +212,36 @@ def test_decode_rejects_bad_arguments():
                                 torch.zeros((2, 10, 96), device=DEV), torch.ones(2), torch.ones(48), 9, k_max=4)
     with pytest.raises(RuntimeError, match="CPU"):
         native.decode_attention(q.cpu(), k, k, torch.ones(2), torch.ones(32), 7, k_max=4)
+
+
+def test_decode_hybrid_two_geometries():
+    """Selection under YaRN (a-triple), reposition with PI pos_scale_c, attend under base RoPE:
+    the hybrid file's decode (hybrid_exact.py:551-629, 776-800), through its drop-in helpers."""
+    import _sta_native as native
+    import shared_selection_triton_hybrid_exact as hyb
+    from synthetic import base_inv_freq, planted_inputs, yarn_inv_freq
+    H, M, D = 4, 2600, 128
+    qa, k, v = planted_inputs(23, H, H, M, D, 0.01, torch.bfloat16, DEV)
+    q = qa[0, :, M - 1, :].contiguous()                 # (H, D): the newest position
+    invf_a, msc = yarn_inv_freq(D, 500000.0, 4.0, 8192, 32.0, 1.0)
+    invf_c = base_inv_freq(D, 10000.0)
+    ps_c, sm = 1.0 / 3.0, 1.0 / math.sqrt(D)
+    tau = torch.full((H,), 5.0)
+    say("decode hybrid: YaRN selection, PI reposition, base-RoPE attend")
+    idx, npk, npq = hyb._decode_build_sets(q, k[0], tau, invf_a, M - 1, 1.0, msc, sm, 32, 32, 300, 100.0, ps_c)
+    out = hyb._decode_attend_torch(q, k[0], v[0], idx, npk, npq, invf_c, 1.0, sm)
+    r = native.decode_attention(q, k, v, tau, invf_a, M - 1, 1.0, msc, sm, 32, 32, 300, 100.0, want_scores=True,
+                                inv_freq_c=invf_c, pos_scale_c=ps_c, rope_scale_c=1.0)
+    torch.cuda.synchronize()
+    assert torch.equal(idx.to(torch.int32), r["idx"][:, 0]) and torch.equal(out, r["out"][:, 0])
+    qn, dc = np_of(q[:, None, :])
+    kn, _ = np_of(k[0])
+    vn, _ = np_of(v[0])
+    s_gpu = r["scores"].cpu().numpy()
+    s_ref = orc.decode_scores(qn, kn, dc, invf_a.numpy(), 1.0, msc, sm, M - 1)
+    assert np.max(np.abs(s_gpu - s_ref)) < 1e-4
+    oi, on, oq, _ = orc.decode_build_sets(s_gpu, tau.numpy(), M - 1, ps_c, 32, 32, 300)
+    assert np.array_equal(r["idx"].cpu().numpy(), oi)
+    assert _bits_equal(r["newpos_k"].cpu().numpy(), on) and _bits_equal(r["newpos_q"].cpu().numpy(), oq)
+    ref = orc.decode_attend(qn, kn, vn, dc, invf_c.numpy(), 1.0, sm, M - 1, oi, on, oq)
+    check_output(out_f32(r["out"]), ref, dc, "decode hybrid")

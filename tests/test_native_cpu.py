@@ -209,7 +209,8 @@ def _decode_args(**kw):
     a = native.DecodeArgsC()
     a.dtype, a.H, a.Hkv, a.Q, a.M, a.D = 1, 32, 8, 1, 12288, 128
     a.q_pos0, a.n_global, a.n_local, a.k_max = 12287, 32, 32, 2048
-    a.pos_scale, a.rope_scale, a.sm_scale, a.pct_decode = 1.0 / 3.0, 1.0, 0.0884, 100.0
+    a.pos_scale_a, a.rope_scale_a, a.sm_scale, a.pct_decode = 1.0 / 3.0, 1.0, 0.0884, 100.0
+    a.pos_scale_c, a.rope_scale_c = 1.0 / 3.0, 1.0
     for k, v in kw.items():
         setattr(a, k, v)
     return a
