@@ -8,15 +8,24 @@ namespace sta {
 
 // Workspace region of the selection-geometry fragments of `heads` x `rows_pad` rows: the
 // fragments (hi/lo bf16, 4 bytes per element), then per row (||hi||, ||lo||), then per head the
-// maxima of those two norms over its rows.  The RoPE pre-kernel writes all three.
+// maxima of those two norms over its rows -- all three written by the RoPE pre-kernel -- then,
+// for the query side, the screened pass 1's results: each row's exact raw maximum and one
+// fallback flag per 256-row workgroup.
 inline size_t frag_region_bytes(int heads, int rows_pad, int D) {
-  return (size_t)heads * rows_pad * D * 4 + (size_t)heads * rows_pad * 8 + (size_t)heads * 8;
+  return (size_t)heads * rows_pad * D * 4 + (size_t)heads * rows_pad * 8 + (size_t)heads * 8 +
+         (size_t)heads * rows_pad * 4 + (size_t)heads * (rows_pad / 256 + 1) * 4;
 }
 inline float2* frag_norms(const u32x4* frag, int heads, int rows_pad, int D) {
   return (float2*)((char*)frag + (size_t)heads * rows_pad * D * 4);
 }
 inline float2* frag_norm_max(const u32x4* frag, int heads, int rows_pad, int D) {
   return frag_norms(frag, heads, rows_pad, D) + (size_t)heads * rows_pad;
+}
+inline float* frag_rowmax(const u32x4* frag, int heads, int rows_pad, int D) {
+  return (float*)(frag_norm_max(frag, heads, rows_pad, D) + heads);
+}
+inline int* frag_flags(const u32x4* frag, int heads, int rows_pad, int D) {
+  return (int*)(frag_rowmax(frag, heads, rows_pad, D) + (size_t)heads * rows_pad);
 }
 
 struct ScoreArgs {
@@ -37,6 +46,9 @@ struct ScoreArgs {
   int32_t* row_counts;    // (H, N) or null
   int ib;                 // set by the launcher: block-index bits of the screened pass 1, 0 = off
   int exact_pass1;        // 1: always run the three-product pass 1 sweep
+  int screened;           // set by the launcher: the screen kernel ran before the pass-2 kernel
+  float* srmax;           // (H, q_rows_pad) the screen's exact raw row maxima
+  int* sflags;            // (H, ngroups) the screen's fallback flags
 };
 
 struct SelectArgs {

@@ -175,8 +175,11 @@ __device__ __forceinline__ float min_arg_for(float thr, float c) {
 // (shared_selection_triton_perquery.py:181-217); 4 / 5 = shared selection with byte votes plus
 // the tile's margin / expmass weighted votes (WMODE 1 / 2, shared_selection_triton_exact_2.py:
 // 126-138).
-template <int D, int T, bool RC, int PQ, int RB>
-__global__ __launch_bounds__(256, 1) void score_kernel(ScoreArgs a) {
+// MODE 1 runs only the screened pass 1 (hi products, half the registers and LDS of the full
+// kernel, two waves per SIMD) and leaves each row's exact maximum, or the workgroup's fallback
+// flag, for MODE 0, which runs pass 2 (and the three-product pass 1 where the screen fell back).
+template <int D, int T, bool RC, int PQ, int RB, int MODE>
+__global__ __launch_bounds__(256, MODE == 1 ? 2 : 1) void score_kernel(ScoreArgs a) {
 #pragma clang fp contract(off)
   // RB 32-row blocks per wave (RB = 2: 64 query rows, RB = 4: 128); four waves, one per SIMD
   constexpr int NW = 4;
@@ -196,7 +199,10 @@ __global__ __launch_bounds__(256, 1) void score_kernel(ScoreArgs a) {
   static_assert(PQ == 0 || PQ >= 4 || T == 32, "per-query bits pack one 32-row tile");
   constexpr bool BITS = PQ >= 1 && PQ <= 3;                          // per-query keep bits
   constexpr int WM = (PQ == 2 || PQ == 4) ? 1 : ((PQ == 3 || PQ == 5) ? 2 : 0);   // weighted votes
-  __shared__ u32x4 lds[NBUF][CHUNK_UNITS];
+  // the screen keeps only the hi halves of each chunk, packed: (block, k step) unit b at b * 64;
+  // after its sweep the buffers hold its candidate lists (about 50 KB)
+  constexpr int LDS_UNITS = MODE == 1 ? (CHUNK_UNITS / 2 > 800 ? CHUNK_UNITS / 2 : 800) : CHUNK_UNITS;
+  __shared__ u32x4 lds[NBUF][LDS_UNITS];
 
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -244,16 +250,13 @@ __global__ __launch_bounds__(256, 1) void score_kernel(ScoreArgs a) {
     const bool ok = wrow0 + 32 * rb < rows_total;
 #pragma unroll
     for (int s = 0; s < S; ++s) {
-      if (ok) {
-        const int64_t u = (((int64_t)h * (a.q_rows_pad >> 5) + wrow0 / 32 + rb) * S + s) * 128 + lane;
-        qhi[rb][s] = a.qfrag[u];
-        qlo[rb][s] = a.qfrag[u + 64];
-      } else {
-        qhi[rb][s] = u32x4{0, 0, 0, 0};
-        qlo[rb][s] = u32x4{0, 0, 0, 0};
+      const int64_t u = (((int64_t)h * (a.q_rows_pad >> 5) + wrow0 / 32 + rb) * S + s) * 128 + lane;
+      qhi[rb][s] = ok ? a.qfrag[u] : u32x4{0, 0, 0, 0};
+      if constexpr (MODE == 0) asm volatile("" : "+a"(qhi[rb][s]));
+      if constexpr (MODE == 0) {
+        qlo[rb][s] = ok ? a.qfrag[u + 64] : u32x4{0, 0, 0, 0};
+        asm volatile("" : "+a"(qlo[rb][s]));
       }
-      asm volatile("" : "+a"(qhi[rb][s]));
-      asm volatile("" : "+a"(qlo[rb][s]));
     }
   }
   const u32x4* kbase = a.kfrag + (int64_t)kvh * (a.k_rows_pad >> 5) * S * 128;
@@ -472,20 +475,22 @@ __global__ __launch_bounds__(256, 1) void score_kernel(ScoreArgs a) {
   // into the low `ib` mantissa bits (a relative change below 2^(ib-23), added to E).  After the
   // sweep the candidates -- slot values within 2 E of the row maximum -- are evaluated exactly as
   // fp32 dot products of the (hi + lo) operands, and the row maximum is their maximum.  A slot
-  // whose third value is a candidate may hide a fourth, and a wave may collect more than FMAX
-  // candidates: then the whole workgroup runs the three-product sweep instead (a few percent of
-  // workgroups on Gaussian inputs; always on inputs with many tied scores).
-  constexpr int FMAX = 512;                      // candidate (row, key) pairs per wave
+  // whose third value is a candidate may hide a fourth: then every key of that slot is evaluated
+  // (a few hundred keys; about 5% of workgroups meet one on Gaussian inputs).  A wave that
+  // collects more than FMAX candidates sends its workgroup to the three-product sweep instead
+  // (inputs with many tied scores).
+  constexpr int FMAX = 1536;                     // candidate (row, key) pairs per wave
   constexpr int LOADS_H = LOADS / 2;             // 1 KB copies per wave per chunk, hi halves only
   static_assert(LOADS_H * NW * 2 * 64 == CHUNK_UNITS, "hi-half copies");
   auto issue_hi = [&](int c, u32x4* dst) {
     const u32x4* src = kbase + (int64_t)c * CHUNK_UNITS + lane;
 #pragma unroll
     for (int e = 0; e < LOADS_H; ++e) {
-      const int u = 2 * (e * NW + wave) * 64;   // the hi unit block of (32-key block, k step) e NW + wave
-      copy16_to_lds(src + u, lds_addr(dst + u));
+      const int b = e * NW + wave;             // (32-key block, k step) b: its hi units, packed
+      copy16_to_lds(src + 128 * b, lds_addr(dst + 64 * b));
     }
   };
+  auto ldbh = [&](const u32x4* buf, int sb, int s) { return buf[(sb * S + s) * 64 + lane]; };
   auto wait_hi = [&](int n) {
     constexpr int E = (7 << 4) | (15 << 8);
     constexpr int L1 = LOADS_H, L2 = 2 * LOADS_H;
@@ -527,11 +532,11 @@ __global__ __launch_bounds__(256, 1) void score_kernel(ScoreArgs a) {
     const uint32_t bv = HAS_PREV ? vgpr(blkO) : 0u;
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) accN[rb] = floatx16{};
-    u32x4 bh = ldb(buf, sb, 0, 0);
+    u32x4 bh = ldbh(buf, sb, 0);
 #pragma unroll
     for (int s = 0; s < S; ++s) {
       u32x4 nh = bh;
-      if (s + 1 < S) nh = ldb(buf, sb, s + 1, 0);
+      if (s + 1 < S) nh = ldbh(buf, sb, s + 1);
 #pragma unroll
       for (int rb = 0; rb < RB; ++rb) accN[rb] = mfma32(qhi[rb][s], bh, accN[rb]);
       bh = nh;
@@ -608,7 +613,7 @@ __global__ __launch_bounds__(256, 1) void score_kernel(ScoreArgs a) {
           for (int rb = 0; rb < RB; ++rb) acc[rb] = floatx16{};
 #pragma unroll
           for (int s = 0; s < S; ++s) {
-            const u32x4 bh = ldb(buf, sb, s, 0);
+            const u32x4 bh = ldbh(buf, sb, s);
 #pragma unroll
             for (int rb = 0; rb < RB; ++rb) acc[rb] = mfma32(qhi[rb][s], bh, acc[rb]);
           }
@@ -665,16 +670,28 @@ __global__ __launch_bounds__(256, 1) void score_kernel(ScoreArgs a) {
           const float E = 1.001f * (qn.x * kn.y + qn.y * kn.x + qn.y * kn.y + gam * qn.x * kn.x) +
                           0x1p-20f * fabsf(v);
           const float thr = v - 2.0f * E;
-          amb |= !(thr > -1e38f) || t3[rb][i] >= thr;
+          amb |= !(thr > -1e38f);
           const uint32_t col = (uint32_t)(lane & 31);
-          const float tv[3] = {t1[rb][i], t2[rb][i], t3[rb][i]};
+          if (t3[rb][i] >= thr) {
+            // a fourth value may hide behind the slot's three: every key of the slot (its
+            // column's causal keys j <= the row's position) becomes a candidate
+            const int qpos = a.q_pos_base + wrow0 + row;
+            const int nk = qpos >= (int)col ? (qpos - (int)col) / 32 + 1 : 0;
+            const int f0 = atomicAdd(nflat, nk);
+            for (int b = 0; b < nk && f0 + b < FMAX; ++b) {
+              frow[f0 + b] = row;
+              fkey[f0 + b] = (int)col + 32 * b;
+            }
+          } else {
+            const float tv[3] = {t1[rb][i], t2[rb][i], t3[rb][i]};
 #pragma unroll
-          for (int k3 = 0; k3 < 3; ++k3) {
-            if (tv[k3] >= thr) {
-              const int f = atomicAdd(nflat, 1);
-              if (f < FMAX) {
-                frow[f] = row;
-                fkey[f] = (int)(((__float_as_uint(tv[k3]) & blk_mask) << 5) | col);
+            for (int k3 = 0; k3 < 3; ++k3) {
+              if (tv[k3] >= thr) {
+                const int f = atomicAdd(nflat, 1);
+                if (f < FMAX) {
+                  frow[f] = row;
+                  fkey[f] = (int)(((__float_as_uint(tv[k3]) & blk_mask) << 5) | col);
+                }
               }
             }
           }
@@ -838,10 +855,40 @@ __global__ __launch_bounds__(256, 1) void score_kernel(ScoreArgs a) {
     if (active && pendingB) flush(passc, accB, keyB);
     if constexpr (pass == 0) finish1();
   };
-  // pass 1: the screened sweep, or the three-product sweep when screening is off or inconclusive
-  if (a.ib == 0 || a.exact_pass1 || run_screened()) run_pass(std::integral_constant<int, 0>{});
-  else finish1();
-  run_pass(std::integral_constant<int, 1>{});
+  if constexpr (MODE == 1) {
+    // the screen: each row's exact raw maximum, or the workgroup's fallback flag
+    const bool fallback = run_screened();
+    if (threadIdx.x == 0) a.sflags[h * ngroups + g] = fallback ? 1 : 0;
+    if (!fallback && active && (lane & 31) == 0) {
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          // a wave's rows may run past q_rows_pad (a multiple of the tile, not of 64)
+          const int row = wrow0 + rb * 32 + (i >> 2) * 8 + (lane >> 5) * 4 + (i & 3);
+          if (row < rows_total) a.srmax[(int64_t)h * a.q_rows_pad + row] = mx[rb][i];
+        }
+    }
+    return;
+  } else {
+    // pass 1: the screen's row maxima, or the three-product sweep where it fell back or is off
+    bool exact1 = true;
+    if (a.screened && a.sflags[h * ngroups + g] == 0) {
+      exact1 = false;
+      if (active) {
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            const int row = wrow0 + rb * 32 + (i >> 2) * 8 + (lane >> 5) * 4 + (i & 3);
+            mx[rb][i] = row < rows_total ? a.srmax[(int64_t)h * a.q_rows_pad + row] : 0.0f;
+          }
+      }
+    }
+    if (exact1) run_pass(std::integral_constant<int, 0>{});
+    else finish1();
+    run_pass(std::integral_constant<int, 1>{});
+  }
 
   if constexpr (RC) {
     if (active) {
@@ -910,7 +957,15 @@ static hipError_t launch_score_t(const ScoreArgs& a0, hipStream_t st) {
   a.ib = (ib <= 13 && a.qnorm && a.knorm_max) ? ib : 0;
   a.exact_pass1 = exact_pass1_forced();
   const int ngroups = (a.nt * T + 128 * RB - 1) / (128 * RB);   // four waves of 32 RB rows
-  hipLaunchKernelGGL((score_kernel<D, T, RC, PQ, RB>), dim3(a.H * ngroups), dim3(256), 0, st, a);
+  // the screen's results sit behind the Q fragments' norms in the fragment region
+  a.srmax = frag_rowmax(a.qfrag, a.H, a.q_rows_pad, D);
+  a.sflags = frag_flags(a.qfrag, a.H, a.q_rows_pad, D);
+  a.screened = a.ib != 0 && !a.exact_pass1;
+  if (a.screened) {
+    // the screen is the same for every pass-2 epilogue: one instance per (D, T)
+    hipLaunchKernelGGL((score_kernel<D, T, false, 0, RB, 1>), dim3(a.H * ngroups), dim3(256), 0, st, a);
+  }
+  hipLaunchKernelGGL((score_kernel<D, T, RC, PQ, RB, 0>), dim3(a.H * ngroups), dim3(256), 0, st, a);
   return hipGetLastError();
 }
 

@@ -46,9 +46,11 @@ def test_workspace_size_matches_layout():
     a = _args()
     n = lib.sta_shared_workspace_size(ctypes.byref(a))
     nt = 12288 // 64
-    # q / k fragments (hi + lo bf16), per-row (||hi||, ||lo||) and per-head maxima of those
-    q = 32 * 12288 * 128 * 4 + 32 * 12288 * 8 + 32 * 8
-    k = 32 * 12288 * 128 * 4 + 32 * 12288 * 8 + 32 * 8
+    # q / k fragments (hi + lo bf16), per-row (||hi||, ||lo||) and per-head maxima of those, then
+    # the screened pass 1's row maxima and per-workgroup flags
+    screen = 32 * 12288 * 4 + 32 * (12288 // 256 + 1) * 4
+    q = 32 * 12288 * 128 * 4 + 32 * 12288 * 8 + 32 * 8 + screen
+    k = 32 * 12288 * 128 * 4 + 32 * 12288 * 8 + 32 * 8 + screen
     votes = 32 * nt * 12288             # byte votes, one row per tile
     assert n >= q + k + votes and n < q + k + votes + 4096
 
@@ -169,7 +171,7 @@ def test_pqstream_workspace_size_matches_layout():
     lib = native.lib()
     n = lib.sta_pqstream_workspace_size(ctypes.byref(_stream_args()))
     N, H, D = 16384, 32, 128
-    frags = 2 * (H * N * D * 4 + H * N * 8 + H * 8)   # q/k fragments with their row norms
+    frags = 2 * (H * N * D * 4 + H * N * 8 + H * 8 + H * N * 4 + H * (N // 256 + 1) * 4)   # q/k fragments
     need = frags + H * (N // 32) * N * 4 + H * N * D * 2   # + keep bits, K~
     assert need <= n < need + 8192
 
