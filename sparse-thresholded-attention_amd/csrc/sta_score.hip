@@ -178,11 +178,21 @@ __device__ __forceinline__ float min_arg_for(float thr, float c) {
 // MODE 1 runs only the screened pass 1 (hi products, half the registers and LDS of the full
 // kernel, two waves per SIMD) and leaves each row's exact maximum, or the workgroup's fallback
 // flag, for MODE 0, which runs pass 2 (and the three-product pass 1 where the screen fell back).
+// Waves per workgroup.  The screen: 4 (one per SIMD, two workgroups per CU).  Pass 2 with plain
+// votes: 8 (two per SIMD sharing each LDS chunk; each block's epilogue follows its own MFMAs and
+// the SIMD's other wave fills the gap).  Pass 2 with per-query bits, weighted votes or row counts
+// needs more registers: 4 waves, each overlapping a block's epilogue with the next block's MFMAs.
+template <bool RC, int PQ, int MODE>
+constexpr int score_waves() { return MODE == 1 ? 4 : ((PQ == 0 && !RC) ? 8 : 4); }
+
 template <int D, int T, bool RC, int PQ, int RB, int MODE>
-__global__ __launch_bounds__(256, MODE == 1 ? 2 : 1) void score_kernel(ScoreArgs a) {
+__global__ __launch_bounds__((64 * score_waves<RC, PQ, MODE>()), (MODE == 1 ? 2 : 1))
+void score_kernel(ScoreArgs a) {
 #pragma clang fp contract(off)
   // RB 32-row blocks per wave (RB = 2: 64 query rows, RB = 4: 128); four waves, one per SIMD
-  constexpr int NW = 4;
+  constexpr int NW = score_waves<RC, PQ, MODE>();
+  constexpr bool FUSED = NW == 4;                // a block's epilogue overlaps the next one's MFMAs
+  constexpr bool PLAIN = PQ == 0 && !RC;         // pass 2 writes byte votes only
   constexpr int WG_ROWS = NW * 32 * RB;          // query rows per workgroup
   constexpr int NTW = 32 * RB / T;               // tiles per wave
   constexpr int S = D / 16;                      // k steps of 16
@@ -416,6 +426,10 @@ __global__ __launch_bounds__(256, MODE == 1 ? 2 : 1) void score_kernel(ScoreArgs
     constexpr int pass = decltype(passc)::value;
     if constexpr (pass == 0) {
       mx[rb][i] = __builtin_amdgcn_fmed3f(v, mx[rb][i], pinf);   // max; scores are finite
+    } else if constexpr (PLAIN) {
+      // rows dropped: the sign of v - x0 (exact: two distinct floats never subtract to zero,
+      // equal ones give +0; x0 = +inf on padded rows), counted with one shift-add
+      cnt[rb] += (int)(__float_as_uint(v - mx[rb][i]) >> 31);
     } else {
       const int keep = v >= mx[rb][i];
       acc2(keep, v, ref[rb][i], i, cnt[rb], bm[rb], w[rb]);
@@ -449,8 +463,51 @@ __global__ __launch_bounds__(256, MODE == 1 ? 2 : 1) void score_kernel(ScoreArgs
         }
       }
     }
-    if constexpr (HAS_PREV && pass == 1) store_key(keyO + (lane & 31), false, cnt, bm, w);
+    if constexpr (HAS_PREV && pass == 1) {
+      if constexpr (PLAIN) {
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb) cnt[rb] = 16 - cnt[rb];   // dropped -> kept of the 16 rows
+      }
+      store_key(keyO + (lane & 31), false, cnt, bm, w);
+    }
     block_schedule(std::integral_constant<int, HAS_PREV ? 2 : 0>{});
+  };
+  // Pass 2 of the 8-wave workgroups on fully causal chunks: one row block's MFMAs at a time, the
+  // other row block's vote epilogue interleaved between them (two accumulators; the epilogue of
+  // the block's first row block runs under its second's MFMAs, that of the second under the next
+  // block's first).  A per-chunk barrier starts both waves of a SIMD in the same phase, so the
+  // epilogue has to hide inside each wave's own MFMA stream.
+  constexpr int NE = 16 / S;                   // epilogue scores per k step (16 rows per slot set)
+  static_assert(NE * S == 16, "epilogue slices");
+  auto half_block = [&](const u32x4* buf, int sb, int rbn, floatx16& acc, const floatx16& accE,
+                        int rbe, int& dropped) {
+    acc = floatx16{};
+    u32x4 bh = ldb(buf, sb, 0, 0), bl = ldb(buf, sb, 0, 1);
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+      u32x4 nh = bh, nl = bl;
+      if (s + 1 < S) { nh = ldb(buf, sb, s + 1, 0); nl = ldb(buf, sb, s + 1, 1); }
+      acc = mfma32(qlo[rbn][s], bh, acc);
+      acc = mfma32(qhi[rbn][s], bl, acc);
+      acc = mfma32(qhi[rbn][s], bh, acc);
+#pragma unroll
+      for (int e = 0; e < NE; ++e) {
+        const int i = s * NE + e;
+        dropped += (int)(__float_as_uint(accE[i] - mx[rbe][i]) >> 31);
+      }
+      bh = nh;
+      bl = nl;
+    }
+    __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);        // reads of step 0
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+#pragma unroll
+      for (int m = 0; m < 3; ++m) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);    // MFMA
+        if (m == 0 && s + 1 < S) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // step s + 1
+        __builtin_amdgcn_sched_group_barrier(0x002, 2 * NE / 3 + 1, 0);
+      }
+    }
   };
   // the last block's epilogue when nothing follows it
   auto flush = [&](auto passc, const floatx16* acc, int key0) {
@@ -462,7 +519,13 @@ __global__ __launch_bounds__(256, MODE == 1 ? 2 : 1) void score_kernel(ScoreArgs
     for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
       for (int i = 0; i < 16; ++i) epi(passc, acc[rb][i], rb, i, cnt, bm, w);
-    if constexpr (pass == 1) store_key(key0 + (lane & 31), false, cnt, bm, w);
+    if constexpr (pass == 1) {
+      if constexpr (PLAIN) {
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb) cnt[rb] = 16 - cnt[rb];
+      }
+      store_key(key0 + (lane & 31), false, cnt, bm, w);
+    }
   };
 
   // ---- screened pass 1 ----------------------------------------------------------------------
@@ -643,7 +706,7 @@ __global__ __launch_bounds__(256, MODE == 1 ? 2 : 1) void score_kernel(ScoreArgs
     // ---- candidates: per row, slot values within 2 E of the row's largest s1, into one flat
     // (row, key) list per wave ----
     constexpr int WR = 32 * RB;                                // rows of a wave
-    static_assert((2 + WR + 2 * FMAX) * 4 * NW <= (int)sizeof(lds), "candidate lists fit the chunk buffers");
+    static_assert(MODE != 1 || (2 + WR + 2 * FMAX) * 4 * NW <= (int)sizeof(lds), "candidate lists fit the chunk buffers");
     int* wl = (int*)&lds[0][0] + wave * (2 + WR + 2 * FMAX);
     int* nflat = wl;                                           // list length
     uint32_t* rowbest = (uint32_t*)(wl + 2);                  // WR rows: order key of the max
@@ -803,12 +866,58 @@ __global__ __launch_bounds__(256, MODE == 1 ? 2 : 1) void score_kernel(ScoreArgs
     floatx16 accA[RB], accB[RB];
     bool pendingB = false;   // accB holds an unmasked block whose epilogue is still due
     int keyB = 0;
-    for (int c = 0; c < nchunks; ++c) {
-      // the buffer chunk c + NBUF - 1 lands in was last read in chunk c - 1, before the barrier
+    // the buffer chunk c + NBUF - 1 lands in was last read in chunk c - 1, before the barrier
+    auto chunk_begin = [&](int c) {
       if (c + NBUF - 1 < nchunks) issue(c + NBUF - 1, lds[(c + NBUF - 1) % NBUF]);
+    };
+    // chunk c + 1's copies have landed in LDS and every wave is done with chunk c
+    auto chunk_end = [&](int c) {
+      if (c + 1 < nchunks) wait_copies(min(nchunks - 1, c + NBUF - 1) - (c + 1));
+      __syncthreads();
+    };
+    int c = 0;
+    // the row-block pipeline (8-wave pass 2) over the fully causal chunks: pacc1 holds the
+    // pending block's second row block, pdrop0 its first one's dropped-row count
+    constexpr bool PIPE = !FUSED && PLAIN && pass == 1 && RB == 2;
+    if constexpr (PIPE) {
+      floatx16 pacc0 = floatx16{}, pacc1 = floatx16{};
+      int pdrop0 = 0, pkey = 0;
+      auto pipe_store = [&](int drop1) {
+        int cnt[RB];
+        cnt[0] = 16 - pdrop0;
+        cnt[RB - 1] = 16 - drop1;
+        uint32_t bm[RB] = {};
+        float w[RB] = {};
+        store_key(pkey + (lane & 31), false, cnt, bm, w);
+      };
+      for (; c < nfull; ++c) {
+        chunk_begin(c);
+        const u32x4* buf = lds[c % NBUF];
+        if (active) {
+#pragma unroll
+          for (int sb = 0; sb < SBC; ++sb) {
+            int d1 = 0, d0 = 0;
+            half_block(buf, sb, 0, pacc0, pacc1, RB - 1, d1);     // row block 0; previous block's 1
+            if (c > 0 || sb > 0) pipe_store(d1);
+            half_block(buf, sb, RB - 1, pacc1, pacc0, 0, d0);     // row block 1; this block's 0
+            pdrop0 = d0;
+            pkey = c * CK + sb * 32;
+          }
+        }
+        chunk_end(c);
+      }
+      if (active && nfull > 0) {
+        int d1 = 0;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) d1 += (int)(__float_as_uint(pacc1[i] - mx[RB - 1][i]) >> 31);
+        pipe_store(d1);
+      }
+    }
+    for (; c < nchunks; ++c) {
+      chunk_begin(c);
       const u32x4* buf = lds[c % NBUF];
       if (active) {
-        if (c < nfull) {
+        if (FUSED && c < nfull) {
           if (c == 0) fused_block(passc, kNoPrev, buf, 0, accA, accB, 0);
           else fused_block(passc, kPrev, buf, 0, accA, accB, keyB);
           fused_block(passc, kPrev, buf, 1, accB, accA, c * CK);
@@ -838,19 +947,25 @@ __global__ __launch_bounds__(256, MODE == 1 ? 2 : 1) void score_kernel(ScoreArgs
                 const float v = acc[rb][i];
                 if constexpr (pass == 0) {
                   if (causal && v > mx[rb][i]) mx[rb][i] = v;
+                } else if constexpr (PLAIN) {
+                  cnt[rb] += causal ? (int)(__float_as_uint(v - mx[rb][i]) >> 31) : 1;
                 } else {
                   const int keep = causal && v >= mx[rb][i];
                   acc2(keep, v, ref[rb][i], i, cnt[rb], bm[rb], w[rb]);
                   if constexpr (RC) rc[rb][i] += keep;
                 }
               }
-            if constexpr (pass == 1) store_key(key, true, cnt, bm, w);
+            if constexpr (pass == 1) {
+              if constexpr (PLAIN) {
+#pragma unroll
+                for (int rb = 0; rb < RB; ++rb) cnt[rb] = 16 - cnt[rb];
+              }
+              store_key(key, true, cnt, bm, w);
+            }
           }
         }
       }
-      // chunk c + 1's copies have landed in LDS and every wave is done with chunk c
-      if (c + 1 < nchunks) wait_copies(min(nchunks - 1, c + NBUF - 1) - (c + 1));
-      __syncthreads();
+      chunk_end(c);
     }
     if (active && pendingB) flush(passc, accB, keyB);
     if constexpr (pass == 0) finish1();
@@ -872,8 +987,16 @@ __global__ __launch_bounds__(256, MODE == 1 ? 2 : 1) void score_kernel(ScoreArgs
     return;
   } else {
     // pass 1: the screen's row maxima, or the three-product sweep where it fell back or is off
+    // the screen's workgroups covering this one's rows (4 waves of 32 RB rows each)
     bool exact1 = true;
-    if (a.screened && a.sflags[h * ngroups + g] == 0) {
+    bool screen_ok = a.screened;
+    {
+      constexpr int SG = score_waves<false, 0, 1>() * 32 * RB;
+      const int ng_s = (rows_total + SG - 1) / SG;
+      for (int gs = g * WG_ROWS / SG; gs < min((g + 1) * WG_ROWS / SG, ng_s); ++gs)
+        screen_ok = screen_ok && a.sflags[h * ng_s + gs] == 0;
+    }
+    if (screen_ok) {
       exact1 = false;
       if (active) {
 #pragma unroll
@@ -956,16 +1079,19 @@ static hipError_t launch_score_t(const ScoreArgs& a0, hipStream_t st) {
   while ((1 << ib) < a.k_rows_pad / 32) ++ib;
   a.ib = (ib <= 13 && a.qnorm && a.knorm_max) ? ib : 0;
   a.exact_pass1 = exact_pass1_forced();
-  const int ngroups = (a.nt * T + 128 * RB - 1) / (128 * RB);   // four waves of 32 RB rows
+  const int rows = a.nt * T;
+  constexpr int WS = score_waves<false, 0, 1>(), W2 = score_waves<RC, PQ, 0>();
+  const int ng_s = (rows + 32 * RB * WS - 1) / (32 * RB * WS);
+  const int ng_2 = (rows + 32 * RB * W2 - 1) / (32 * RB * W2);
   // the screen's results sit behind the Q fragments' norms in the fragment region
   a.srmax = frag_rowmax(a.qfrag, a.H, a.q_rows_pad, D);
   a.sflags = frag_flags(a.qfrag, a.H, a.q_rows_pad, D);
   a.screened = a.ib != 0 && !a.exact_pass1;
   if (a.screened) {
     // the screen is the same for every pass-2 epilogue: one instance per (D, T)
-    hipLaunchKernelGGL((score_kernel<D, T, false, 0, RB, 1>), dim3(a.H * ngroups), dim3(256), 0, st, a);
+    hipLaunchKernelGGL((score_kernel<D, T, false, 0, RB, 1>), dim3(a.H * ng_s), dim3(64 * WS), 0, st, a);
   }
-  hipLaunchKernelGGL((score_kernel<D, T, RC, PQ, RB, 0>), dim3(a.H * ngroups), dim3(256), 0, st, a);
+  hipLaunchKernelGGL((score_kernel<D, T, RC, PQ, RB, 0>), dim3(a.H * ng_2), dim3(64 * W2), 0, st, a);
   return hipGetLastError();
 }
 
