@@ -217,18 +217,18 @@ struct Raw8<DT_F32> {
 
 // ------------------------------------------------------------------------------------------
 // sin/cos of an fp32 angle for the attend-side rotation.
-// Two-constant Cody-Waite reduction by 2*pi with fused multiply-adds (the product k*C is exact
-// inside the fma), then the hardware sine/cosine, which take their argument in revolutions.
-// Absolute error about 5e-7 for |x| < 2^17; the angle itself is the reference's fp32 product.
+// The argument is reduced straight to revolutions, t = x / (2 pi) - k, with 1 / (2 pi) split
+// into two fp32 terms kH + kL: fma(x, kH, -k) is the exact product minus the integer k, rounded
+// once, and fma(x, kL, .) adds the low term.  The hardware sine/cosine take t in revolutions.
+// Reduction error below 3e-8 revolutions for |x| < 5000 (two-constant Cody-Waite by 2 pi, one
+// instruction longer, reaches 6e-8); the angle itself is the reference's fp32 product.
 // ------------------------------------------------------------------------------------------
 __device__ __forceinline__ void fast_sincos(float x, float& s, float& c) {
-  const float kInv2Pi = 0.15915494309189535f;
-  const float kC1 = 6.28318548202514648f;        // fp32(2*pi)
-  const float kC2 = -1.7484555314695172e-07f;    // fp32(2*pi - kC1)
-  float k = rintf(x * kInv2Pi);
-  float r = fmaf(-k, kC1, x);
-  r = fmaf(-k, kC2, r);
-  float t = r * kInv2Pi;
+  const float kH = 0.15915494f;        // fp32(1 / (2 pi)), 0x3e22f983
+  const float kL = 6.4206382e-09f;     // fp32(1 / (2 pi) - kH), 0x31dc9c88
+  const float k = rintf(x * kH);
+  float t = fmaf(x, kH, -k);
+  t = fmaf(x, kL, t);
   s = __builtin_amdgcn_sinf(t);
   c = __builtin_amdgcn_cosf(t);
 }

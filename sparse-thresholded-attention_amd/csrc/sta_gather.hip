@@ -46,7 +46,8 @@ struct GatherCfg {
 // V rows (issued one block ahead of that), rotate K and write both to one half of a
 // double-buffered LDS area while the consumer waves attend block b from the other half; one
 // barrier per block hands the halves over.  A block then costs max(produce, consume).
-template <int DT, int D, int NW>
+// PQM: the per-query variant, whose slots carry a row mask (a.mask non-NULL)
+template <int DT, int D, int NW, bool PQM>
 __global__ __launch_bounds__(NW * 64 + 256, 1) void gather_kernel(GatherArgs a) {
   using Cfg = GatherCfg<DT, D, NW>;
   constexpr int NC = Cfg::NC, NT = Cfg::NT, TPS = Cfg::TPS, FP = Cfg::FP, VU = Cfg::VU;
@@ -95,6 +96,9 @@ __global__ __launch_bounds__(NW * 64 + 256, 1) void gather_kernel(GatherArgs a) 
     const int64_t vbase = (int64_t)kvh * a.v_head_stride;
     Raw8<DT> kx1[FP / 8], kx2[FP / 8], vx[VU][4];
     float np = 0.0f;
+    float fr[FP];   // this thread's rotary frequencies
+#pragma unroll
+    for (int e = 0; e < FP; ++e) fr[e] = invf[kpart * FP + e];
     auto load_block = [&](int b) {
       const int j = sidx[b * 64 + kslot];
       if ((unsigned)j < (unsigned)N) {   // sentinel N (and any out-of-range index) -> zero row
@@ -123,8 +127,10 @@ __global__ __launch_bounds__(NW * 64 + 256, 1) void gather_kernel(GatherArgs a) 
         }
       }
     };
-    // rotate K at newpos_k (exact_2.py:203-207); write K and V^T of block b to buffer b & 1
-    auto store_block = [&](int b) {
+    // rotate K at newpos_k (exact_2.py:203-207); write K and V^T of block b to buffer b & 1.
+    // SCALE: rope_scale != 1 (YaRN); otherwise the products with it are identities and skipped
+    auto store_block = [&](auto scalec, int b) {
+      constexpr bool SCALE = decltype(scalec)::value;
       uint16_t* kr_hi = kbuf(b & 1);
       uint16_t* kr_lo = kr_hi + 64 * KSTR;
       uint16_t* v_hi = vbuf(b & 1);
@@ -137,8 +143,8 @@ __global__ __launch_bounds__(NW * 64 + 256, 1) void gather_kernel(GatherArgs a) 
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
           float sn, cs;
-          fast_sincos(np * invf[kpart * FP + 8 * c + e], sn, cs);
-          if (rs != 1.0f) {   // uniform: rope_scale is 1 except under YaRN
+          fast_sincos(np * fr[8 * c + e], sn, cs);
+          if constexpr (SCALE) {
             cs *= rs;
             sn *= rs;
           }
@@ -181,19 +187,23 @@ __global__ __launch_bounds__(NW * 64 + 256, 1) void gather_kernel(GatherArgs a) 
         }
       }
     };
-    if (nblk > 0) {
-      load_block(0);
-      store_block(0);
-      if (nblk > 1) load_block(1);
-    }
-    __syncthreads();
-    for (int b = 0; b < nblk; ++b) {
-      if (b + 1 < nblk) {
-        store_block(b + 1);                  // rows loaded one block earlier
-        if (b + 2 < nblk) load_block(b + 2); // in flight during the next block
+    auto produce = [&](auto scalec) {
+      if (nblk > 0) {
+        load_block(0);
+        store_block(scalec, 0);
+        if (nblk > 1) load_block(1);
       }
       __syncthreads();
-    }
+      for (int b = 0; b < nblk; ++b) {
+        if (b + 1 < nblk) {
+          store_block(scalec, b + 1);          // rows loaded one block earlier
+          if (b + 2 < nblk) load_block(b + 2); // in flight during the next block
+        }
+        __syncthreads();
+      }
+    };
+    if (rs == 1.0f) produce(std::false_type{});   // uniform: rope_scale is 1 except under YaRN
+    else produce(std::true_type{});
     return;
   }
 
@@ -204,6 +214,8 @@ __global__ __launch_bounds__(NW * 64 + 256, 1) void gather_kernel(GatherArgs a) 
   const bool row_ok = qrow < N;
   const int64_t qpos = (int64_t)a.q_pos_base + qrow;
   const int64_t qpos_first = (int64_t)a.q_pos_base + (int64_t)t * T;
+  // kept positions are below N < 2^31: clamping the row's position keeps every comparison
+  const int qpos32 = (int)(qpos < (int64_t)INT32_MAX ? qpos : (int64_t)INT32_MAX);
   // Q is rotated, then scaled by sm_scale * log2(e): scores come out in base-2 units and the
   // softmax uses exp2 (the scale commutes with the max and cancels in acc / l)
   const float qscale = a.sm_scale * 1.4426950408889634f;
@@ -273,25 +285,36 @@ __global__ __launch_bounds__(NW * 64 + 256, 1) void gather_kernel(GatherArgs a) 
     const bool unmasked = jlast < N && jlast <= qpos_first;
     float p[4][4];
     float bmax = -INFINITY;
+    if (!PQM && unmasked) {   // uniform: every slot of the block is causal for every row
 #pragma unroll
-    for (int sb = 0; sb < 4; ++sb) {
-      const int sl = s0 + sb * 16 + 4 * (lane >> 4);
-      const int4 j4 = *(const int4*)(sidx + sl);
-      const int jj[4] = {j4.x, j4.y, j4.z, j4.w};
-      // per-query variant: bit r of the slot's mask says whether this lane's row attends it
-      // (shared_selection_triton_perquery.py:296-297); slots past k_max read as empty
-      uint32_t mk[4] = {~0u, ~0u, ~0u, ~0u};
-      if (a.mask) {
+      for (int sb = 0; sb < 4; ++sb)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) mk[i] = sl + i < a.k_max ? (uint32_t)a.mask[tile_off + sl + i] : 0u;
-      }
+        for (int i = 0; i < 4; ++i) {
+          p[sb][i] = sacc[sb][i];
+          bmax = fmaxf(bmax, p[sb][i]);
+        }
+    } else {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const bool keep = (unmasked || (((unsigned)jj[i] < (unsigned)N) && (qpos >= jj[i])))  // exact_2.py:210
-                          && (a.mask == nullptr || ((mk[i] >> (r & 31)) & 1u));
-        const float v = keep ? sacc[sb][i] : -INFINITY;
-        p[sb][i] = v;
-        bmax = fmaxf(bmax, v);
+      for (int sb = 0; sb < 4; ++sb) {
+        const int sl = s0 + sb * 16 + 4 * (lane >> 4);
+        const int4 j4 = *(const int4*)(sidx + sl);
+        const int jj[4] = {j4.x, j4.y, j4.z, j4.w};
+        // per-query variant: bit r of the slot's mask says whether this lane's row attends it
+        // (shared_selection_triton_perquery.py:296-297); slots past k_max read as empty
+        uint32_t mk[4] = {~0u, ~0u, ~0u, ~0u};
+        if constexpr (PQM) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) mk[i] = sl + i < a.k_max ? (uint32_t)a.mask[tile_off + sl + i] : 0u;
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          // exact_2.py:210, evaluated without short circuits (no per-slot branches)
+          const bool causal = unmasked | (((unsigned)jj[i] < (unsigned)N) & (qpos32 >= jj[i]));
+          const bool keep = causal & (!PQM || ((mk[i] >> (r & 31)) & 1u));
+          const float v = keep ? sacc[sb][i] : -INFINITY;
+          p[sb][i] = v;
+          bmax = fmaxf(bmax, v);
+        }
       }
     }
     bmax = fmaxf(bmax, __shfl_xor(bmax, 16, 64));
@@ -385,15 +408,26 @@ __global__ __launch_bounds__(NW * 64 + 256, 1) void gather_kernel(GatherArgs a) 
   }
 }
 
-template <int DT, int D, int NW>
-static hipError_t launch_gather_t(const GatherArgs& a, hipStream_t st) {
+template <int DT, int D, int NW, bool PQM>
+static hipError_t launch_gather_m(const GatherArgs& a, hipStream_t st) {
   using Cfg = GatherCfg<DT, D, NW>;
   const size_t lds = Cfg::lds_bytes(a.k_max);
-  hipError_t e = hipFuncSetAttribute((const void*)gather_kernel<DT, D, NW>,
+  hipError_t e = hipFuncSetAttribute((const void*)gather_kernel<DT, D, NW, PQM>,
                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL((gather_kernel<DT, D, NW>), dim3(a.H * a.nt), dim3(Cfg::NT), lds, st, a);
+  hipLaunchKernelGGL((gather_kernel<DT, D, NW, PQM>), dim3(a.H * a.nt), dim3(Cfg::NT), lds, st, a);
   return hipGetLastError();
+}
+
+// the per-query variant's row masks cover one 32-row tile (two consumer waves)
+template <int DT, int D, int NW>
+static hipError_t launch_gather_t(const GatherArgs& a, hipStream_t st) {
+  if constexpr (NW == 2) {
+    if (a.mask) return launch_gather_m<DT, D, NW, true>(a, st);
+  } else {
+    if (a.mask) return hipErrorInvalidValue;
+  }
+  return launch_gather_m<DT, D, NW, false>(a, st);
 }
 
 size_t gather_lds_bytes(int dtype, int D, int k_max) {

@@ -31,6 +31,11 @@ namespace sta {
 // when q_pos_base > 0) are written as zeros.  Each row's (||hi||, ||lo||) goes to `norms`: the
 // screened pass 1 of the score kernel bounds its single-product error with them.
 // ------------------------------------------------------------------------------------------
+// A thread takes one row and 8 frequencies i0..i0+7 (both rotation halves, dims i0.. and
+// D/2+i0..) for ROPE_HG consecutive heads: the 8 sin / cos pairs depend on (row, i) only, so
+// they are computed once and reused for every head of the group.
+constexpr int ROPE_HG = 4;
+
 template <int DT, int D>
 __global__ __launch_bounds__(256) void rope_frag_kernel(const void* __restrict__ x, int64_t head_stride,
                                                         int64_t tok_stride, int heads, int N, int rows_pad,
@@ -38,67 +43,81 @@ __global__ __launch_bounds__(256) void rope_frag_kernel(const void* __restrict__
                                                         const float* __restrict__ inv_freq,
                                                         u32x4* __restrict__ frag, float2* __restrict__ norms) {
 #pragma clang fp contract(off)
-  constexpr int C = D / 8;
+  constexpr int C2 = D / 16;                 // threads per row
   const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  const int64_t total = (int64_t)heads * rows_pad * C;
-  if (gid >= total) return;
-  const int c = (int)(gid % C);
-  const int64_t hr = gid / C;
-  const int row = (int)(hr % rows_pad);
-  const int head = (int)(hr / rows_pad);
-  const int d0 = c * 8;
-  float out[8];
-  if (row < N) {
-    const bool first = d0 < D / 2;
-    const int i0 = first ? d0 : d0 - D / 2;
-    float a[8], b[8];
-    const int64_t base = (int64_t)head * head_stride + (int64_t)row * tok_stride;
-    load8<DT>(x, base + i0, a);
-    load8<DT>(x, base + D / 2 + i0, b);
+  if (gid >= (int64_t)rows_pad * C2) return;
+  const int c = (int)(gid % C2);
+  const int row = (int)(gid / C2);
+  const int h0 = blockIdx.y * ROPE_HG;
+  const int h1 = h0 + ROPE_HG < heads ? h0 + ROPE_HG : heads;
+  const int i0 = c * 8;
+  const bool live = row < N;
+  float cs[8], sn[8];
+  if (live) {
     const float pf = (float)(pos_base + row) * pos_scale;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       const float ang = pf * inv_freq[i0 + e];
-      float sn, cs;
-      sincosf(ang, &sn, &cs);
-      cs = cs * rope_scale;
-      sn = sn * rope_scale;
-      if (first) {
-        const float p = a[e] * cs, q = b[e] * sn;
-        out[e] = p - q;
-      } else {
-        const float p = b[e] * cs, q = a[e] * sn;
-        out[e] = p + q;
-      }
+      sincosf(ang, &sn[e], &cs[e]);
+      cs[e] = cs[e] * rope_scale;
+      sn[e] = sn[e] * rope_scale;
     }
-  } else {
-#pragma unroll
-    for (int e = 0; e < 8; ++e) out[e] = 0.0f;
   }
-  u32x4 hi, lo;
-  split_bf16x8(out, hi, lo);
-  const int rb = row >> 5, lr = row & 31, s = d0 >> 4, g = (d0 & 15) >> 3;
-  const int64_t unit = (((int64_t)head * (rows_pad >> 5) + rb) * (D / 16) + s) * 2 * 64 + lr + 32 * g;
-  frag[unit] = hi;
-  frag[unit + 64] = lo;
-  // squared norms of the row's hi and lo parts: this thread's 8 elements, then the C threads of
-  // the row (consecutive lanes of one wave; a row's threads all pass or all fail the bound check)
-  float sh = 0.0f, sl = 0.0f;
+  const int rb = row >> 5, lr = row & 31, g = c & 1;
+  for (int head = h0; head < h1; ++head) {
+    float o1[8], o2[8];
+    if (live) {
+      float a[8], b[8];
+      const int64_t base = (int64_t)head * head_stride + (int64_t)row * tok_stride;
+      load8<DT>(x, base + i0, a);
+      load8<DT>(x, base + D / 2 + i0, b);
 #pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const float h0 = __uint_as_float(hi[e] << 16), h1 = __uint_as_float(hi[e] & 0xffff0000u);
-    const float l0 = __uint_as_float(lo[e] << 16), l1 = __uint_as_float(lo[e] & 0xffff0000u);
-    sh = fmaf(h0, h0, sh);
-    sh = fmaf(h1, h1, sh);
-    sl = fmaf(l0, l0, sl);
-    sl = fmaf(l1, l1, sl);
-  }
+      for (int e = 0; e < 8; ++e) {
+        const float p1 = a[e] * cs[e], q1 = b[e] * sn[e];
+        o1[e] = p1 - q1;
+        const float p2 = b[e] * cs[e], q2 = a[e] * sn[e];
+        o2[e] = p2 + q2;
+      }
+    } else {
 #pragma unroll
-  for (int o = 1; o < C; o <<= 1) {
-    sh += __shfl_xor(sh, o, 64);
-    sl += __shfl_xor(sl, o, 64);
+      for (int e = 0; e < 8; ++e) o1[e] = o2[e] = 0.0f;
+    }
+    u32x4 hi1, lo1, hi2, lo2;
+    split_bf16x8(o1, hi1, lo1);
+    split_bf16x8(o2, hi2, lo2);
+    // dims i0.. sit in k step i0/16, dims D/2+i0.. in step (D/2+i0)/16, both in half g of the step
+    const int64_t rbase = ((int64_t)head * (rows_pad >> 5) + rb) * (D / 16);
+    const int64_t u1 = (rbase + (i0 >> 4)) * 2 * 64 + lr + 32 * g;
+    const int64_t u2 = (rbase + ((D / 2 + i0) >> 4)) * 2 * 64 + lr + 32 * g;
+    frag[u1] = hi1;
+    frag[u1 + 64] = lo1;
+    frag[u2] = hi2;
+    frag[u2 + 64] = lo2;
+    // squared norms of the row's hi and lo parts: this thread's 16 elements, then the C2 threads
+    // of the row (consecutive lanes of one wave; a row's threads all pass or all fail the bounds)
+    float sh = 0.0f, sl = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float h0a = __uint_as_float(hi1[e] << 16), h1a = __uint_as_float(hi1[e] & 0xffff0000u);
+      const float l0a = __uint_as_float(lo1[e] << 16), l1a = __uint_as_float(lo1[e] & 0xffff0000u);
+      const float h0b = __uint_as_float(hi2[e] << 16), h1b = __uint_as_float(hi2[e] & 0xffff0000u);
+      const float l0b = __uint_as_float(lo2[e] << 16), l1b = __uint_as_float(lo2[e] & 0xffff0000u);
+      sh = fmaf(h0a, h0a, sh);
+      sh = fmaf(h1a, h1a, sh);
+      sh = fmaf(h0b, h0b, sh);
+      sh = fmaf(h1b, h1b, sh);
+      sl = fmaf(l0a, l0a, sl);
+      sl = fmaf(l1a, l1a, sl);
+      sl = fmaf(l0b, l0b, sl);
+      sl = fmaf(l1b, l1b, sl);
+    }
+#pragma unroll
+    for (int o = 1; o < C2; o <<= 1) {
+      sh += __shfl_xor(sh, o, 64);
+      sl += __shfl_xor(sl, o, 64);
+    }
+    if (c == 0) norms[(int64_t)head * rows_pad + row] = make_float2(sqrtf(sh), sqrtf(sl));
   }
-  if (c == 0) norms[(int64_t)head * rows_pad + row] = make_float2(sqrtf(sh), sqrtf(sl));
 }
 
 // per head: the maxima of (||hi||, ||lo||) over its rows_pad rows (rows_pad even); 1024 threads
@@ -1039,10 +1058,11 @@ template <int DT, int D>
 static hipError_t launch_rope_frag_t(const void* x, int64_t hs, int64_t ts, int heads, int N, int rows_pad,
                                      int pos_base, float pos_scale, float rope_scale, const float* inv_freq,
                                      u32x4* frag, hipStream_t st) {
-  const int64_t total = (int64_t)heads * rows_pad * (D / 8);
+  const int64_t total = (int64_t)rows_pad * (D / 16);
   const int64_t blocks = (total + 255) / 256;
   float2* norms = frag_norms(frag, heads, rows_pad, D);
-  hipLaunchKernelGGL((rope_frag_kernel<DT, D>), dim3((unsigned)blocks), dim3(256), 0, st, x, hs, ts, heads, N,
+  const dim3 grid((unsigned)blocks, (unsigned)((heads + ROPE_HG - 1) / ROPE_HG));
+  hipLaunchKernelGGL((rope_frag_kernel<DT, D>), grid, dim3(256), 0, st, x, hs, ts, heads, N,
                      rows_pad, pos_base, pos_scale, rope_scale, inv_freq, frag, norms);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
