@@ -230,7 +230,7 @@ void score_kernel(ScoreArgs a) {
   constexpr int WM = (PQ == 2 || PQ == 4) ? 1 : ((PQ == 3 || PQ == 5) ? 2 : 0);   // weighted votes
   // the screen keeps only the hi halves of each chunk, packed: (block, k step) unit b at b * 64;
   // after its sweep the buffers hold its candidate lists (about 50 KB)
-  constexpr int LDS_UNITS = MODE == 1 ? (CHUNK_UNITS / 2 > 800 ? CHUNK_UNITS / 2 : 800) : CHUNK_UNITS;
+  constexpr int LDS_UNITS = MODE == 1 ? (CHUNK_UNITS / 2 > 808 ? CHUNK_UNITS / 2 : 808) : CHUNK_UNITS;
   __shared__ u32x4 lds[NBUF][LDS_UNITS];
 
   const int lane = threadIdx.x & 63;
@@ -648,6 +648,17 @@ void score_kernel(ScoreArgs a) {
     for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
       for (int i = 0; i < 16; ++i) { t1[rb][i] = lowest; t2[rb][i] = lowest; t3[rb][i] = lowest; }
+    static_assert(MODE != 1 || 32 * RB == 64, "one wave row per lane");
+    // the norm part of row (wave row `lane`)'s error bound E, loaded before the sweep: the
+    // candidate phase reads it with a lane shuffle instead of one dependent load per slot
+    const float2 kn = a.knorm_max[kvh];
+    // 2^-14 covers the fp32 accumulation of s1 and of the exact dots; 2^(ib-23) the packing
+    const float gam = 0x1p-14f + __uint_as_float((uint32_t)(127 + a.ib - 23) << 23);
+    float ebase = 0.0f;
+    if (active && wrow0 + lane < a.N) {
+      const float2 qn = a.qnorm[(int64_t)h * a.q_rows_pad + wrow0 + lane];
+      ebase = 1.001f * (qn.x * kn.y + qn.y * kn.x + qn.y * kn.y + gam * qn.x * kn.x);
+    }
     // nothing the compiler tracks is in flight past this point: its own waits then stay out of
     // the sweep, whose copies it does not see
     __builtin_amdgcn_s_waitcnt(0);
@@ -725,54 +736,115 @@ void score_kernel(ScoreArgs a) {
     // ---- candidates: per row, slot values within 2 E of the row's largest s1, into one flat
     // (row, key) list per wave ----
     constexpr int WR = 32 * RB;                                // rows of a wave
-    static_assert(MODE != 1 || (2 + WR + 2 * FMAX) * 4 * NW <= (int)sizeof(lds), "candidate lists fit the chunk buffers");
-    int* wl = (int*)&lds[0][0] + wave * (2 + WR + 2 * FMAX);
+    static_assert(MODE != 1 || (2 + 2 * WR + 2 * FMAX) * 4 * NW <= (int)sizeof(lds), "candidate lists fit the chunk buffers");
+    int* wl = (int*)&lds[0][0] + wave * (2 + 2 * WR + 2 * FMAX);
     int* nflat = wl;                                           // list length
     uint32_t* rowbest = (uint32_t*)(wl + 2);                  // WR rows: order key of the max
-    int* frow = wl + 2 + WR;                                   // FMAX rows
+    int* rowcnt = wl + 2 + WR;                                 // WR rows: candidates, then fill points
+    int* frow = wl + 2 + 2 * WR;                               // FMAX rows
     int* fkey = frow + FMAX;                                   // FMAX keys
     if (lane == 0) nflat[0] = 0;
-    for (int r = lane; r < WR; r += 64) rowbest[r] = 0u;
-    const float2 kn = a.knorm_max[kvh];
-    // 2^-14 covers the fp32 accumulation of s1 and of the exact dots; 2^(ib-23) the packing
-    const float gam = 0x1p-14f + __uint_as_float((uint32_t)(127 + a.ib - 23) << 23);
+    for (int r = lane; r < WR; r += 64) {
+      rowbest[r] = 0u;
+      rowcnt[r] = 0;
+    }
     bool amb = false;
+    __syncthreads();
+    float thr[RB][16];
+    const int col = lane & 31;
+    auto slot_keys = [&](int row) {
+      const int qpos = a.q_pos_base + wrow0 + row;
+      return qpos >= col ? (qpos - col) / 32 + 1 : 0;
+    };
+    // the number of list entries of a slot: every key of the slot when its third value is a
+    // candidate (a fourth may hide behind it; its column's causal keys j <= the row's position),
+    // otherwise its values within the threshold
+    auto slot_count = [&](int rb, int i) {
+      const int row = rb * 32 + (i >> 2) * 8 + (lane >> 5) * 4 + (i & 3);
+      const float th = thr[rb][i];
+      const int n3 = (int)(t1[rb][i] >= th) + (int)(t2[rb][i] >= th) + (int)(t3[rb][i] >= th);
+      return t3[rb][i] >= th ? slot_keys(row) : n3;
+    };
+    if (active) {
+      // row maxima and thresholds of all slots first, with no control flow: the 32 butterfly
+      // reductions interleave instead of waiting out one shuffle latency after another
+      // (lane-to-lane moves in registers: DPP within 16-lane rows, then a swap of row pairs)
+      auto dpp = [](float v, auto ctrlc) {
+        return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), decltype(ctrlc)::value, 0xF, 0xF, false));
+      };
+      auto row32_max = [&](float v) {
+        v = __builtin_amdgcn_fmed3f(v, dpp(v, std::integral_constant<int, 0xB1>{}), pinf);    // lane ^ 1
+        v = __builtin_amdgcn_fmed3f(v, dpp(v, std::integral_constant<int, 0x4E>{}), pinf);    // lane ^ 2
+        v = __builtin_amdgcn_fmed3f(v, dpp(v, std::integral_constant<int, 0x141>{}), pinf);   // 7 - lane in 8
+        v = __builtin_amdgcn_fmed3f(v, dpp(v, std::integral_constant<int, 0x140>{}), pinf);   // 15 - lane in 16
+        const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+        return __builtin_amdgcn_fmed3f(__uint_as_float(r[0]), __uint_as_float(r[1]), pinf);  // rows 2k, 2k+1
+      };
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const float v = row32_max(t1[rb][i]);
+          const int row = rb * 32 + (i >> 2) * 8 + (lane >> 5) * 4 + (i & 3);
+          const int r0 = rb * 32 + (i >> 2) * 8 + (i & 3);     // the row of lanes 0-31; lanes 32-63: + 4
+          const float e0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ebase), r0));
+          const float e1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ebase), r0 + 4));
+          const float E = (lane < 32 ? e0 : e1) + 0x1p-20f * fabsf(v);
+          const float th = v - 2.0f * E;
+          // padded rows never vote: their maximum is unused (no value reaches +inf)
+          const bool valid = wrow0 + row < a.N;
+          amb |= valid && !(th > -1e38f);
+          thr[rb][i] = valid ? th : INFINITY;
+        }
+      // the list is ordered by row (neighbouring pairs share the Q fragments' cache lines):
+      // per-row counts first
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int n = slot_count(rb, i);
+          if (n > 0) atomicAdd(&rowcnt[rb * 32 + (i >> 2) * 8 + (lane >> 5) * 4 + (i & 3)], n);
+        }
+    }
+    __syncthreads();
+    if (active) {   // row starts: an exclusive scan of the wave's 64 row counts, lane = row
+      const int c = rowcnt[lane];
+      int incl = c;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const int y = __shfl_up(incl, o, 64);
+        if (lane >= o) incl += y;
+      }
+      rowcnt[lane] = incl - c;
+      if (lane == 63) nflat[0] = incl;
+    }
     __syncthreads();
     if (active) {
 #pragma unroll
       for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-          float v = t1[rb][i];
-#pragma unroll
-          for (int o = 1; o < 32; o <<= 1) v = __builtin_amdgcn_fmed3f(v, __shfl_xor(v, o, 64), INFINITY);
-          const int row = rb * 32 + (i >> 2) * 8 + (lane >> 5) * 4 + (i & 3);
-          if (wrow0 + row >= a.N) continue;   // padded rows never vote: their maximum is unused
-          const float2 qn = a.qnorm[(int64_t)h * a.q_rows_pad + wrow0 + row];
-          const float E = 1.001f * (qn.x * kn.y + qn.y * kn.x + qn.y * kn.y + gam * qn.x * kn.x) +
-                          0x1p-20f * fabsf(v);
-          const float thr = v - 2.0f * E;
-          amb |= !(thr > -1e38f);
-          const uint32_t col = (uint32_t)(lane & 31);
-          if (t3[rb][i] >= thr) {
-            // a fourth value may hide behind the slot's three: every key of the slot (its
-            // column's causal keys j <= the row's position) becomes a candidate
-            const int qpos = a.q_pos_base + wrow0 + row;
-            const int nk = qpos >= (int)col ? (qpos - (int)col) / 32 + 1 : 0;
-            const int f0 = atomicAdd(nflat, nk);
-            for (int b = 0; b < nk && f0 + b < FMAX; ++b) {
-              frow[f0 + b] = row;
-              fkey[f0 + b] = (int)col + 32 * b;
-            }
-          } else {
-            const float tv[3] = {t1[rb][i], t2[rb][i], t3[rb][i]};
-#pragma unroll
-            for (int k3 = 0; k3 < 3; ++k3) {
-              if (tv[k3] >= thr) {
-                const int f = atomicAdd(nflat, 1);
+          const int n = slot_count(rb, i);
+          if (n > 0) {
+            const int row = rb * 32 + (i >> 2) * 8 + (lane >> 5) * 4 + (i & 3);
+            const float th = thr[rb][i];
+            int f = atomicAdd(&rowcnt[row], n);
+            if (t3[rb][i] >= th) {
+              for (int b = 0; b < n; ++b, ++f)
                 if (f < FMAX) {
                   frow[f] = row;
-                  fkey[f] = (int)(((__float_as_uint(tv[k3]) & blk_mask) << 5) | col);
+                  fkey[f] = col + 32 * b;
+                }
+            } else {
+              const float tv[3] = {t1[rb][i], t2[rb][i], t3[rb][i]};
+#pragma unroll
+              for (int k3 = 0; k3 < 3; ++k3) {
+                if (tv[k3] >= th) {
+                  if (f < FMAX) {
+                    frow[f] = row;
+                    fkey[f] = (int)(((__float_as_uint(tv[k3]) & blk_mask) << 5) | (uint32_t)col);
+                  }
+                  ++f;
                 }
               }
             }
