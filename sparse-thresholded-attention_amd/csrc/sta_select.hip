@@ -94,6 +94,7 @@ __global__ __launch_bounds__(256) void select_kernel(SelectArgs a) {
   float* snp = (float*)(sidx + a.k_max);                                    // k_max
 
   for (int i = tid; i < 260; i += 256) { hist[i] = 0; fhist[i] = 0; }
+  if (tid == 0) misc[1] = 0;
   // ---- stage the vote row, zero past the keys the score kernel wrote (its causal range) ----
   const VT* vrow = (const VT*)a.votes + ((int64_t)h * a.nt + t) * a.votes_stride;
   if constexpr (sizeof(VT) == 1) {
@@ -115,8 +116,31 @@ __global__ __launch_bounds__(256) void select_kernel(SelectArgs a) {
     int32_t* vo = a.votes_out + ((int64_t)h * a.nt + t) * N;
     for (int j = tid; j < N; j += 256) vo[j] = vb[j];
   }
-  // ---- vote histogram over all N keys ----
-  for (int j = tid; j < hi_keys; j += 256) atomicAdd(&hist[vb[j]], 1);
+  // Thread tid owns keys [tid * per, tid * per + per) for the histogram and the compaction; its
+  // vote bytes are read 16 at a time.
+  const int j0 = tid * per;
+  auto seg_bytes = [&](int jb) { return *(const u32x4*)(vb + jb); };
+  auto byte_of = [](const u32x4& w, int e) { return (int)((w[e >> 2] >> (8 * (e & 3))) & 0xffu); };
+  // ---- vote histogram over all N keys: the nonzero votes by LDS atomics, the zero bin by
+  // subtraction (most keys of a tile have no vote, and one bin taking them all serialises) ----
+  {
+    const int jend = min(j0 + per, hi_keys);
+    int nz = 0;
+    for (int jb = j0; jb < jend; jb += 16) {
+      const u32x4 w = seg_bytes(jb);
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int b = byte_of(w, e);
+        if (jb + e < jend && b != 0) {
+          atomicAdd(&hist[b], 1);
+          ++nz;
+        }
+      }
+    }
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) nz += __shfl_xor(nz, o, 64);
+    if ((tid & 63) == 0) atomicAdd(&misc[1], nz);
+  }
   // forced = [0, n_global) U [tstart - n_local + 1, tstart + T - 1]   (exact_2.py:290-293)
   const int gA = min(a.n_global, N);
   const int64_t lo = tstart - a.n_local + 1, hi_l = tstart + T - 1;
@@ -128,7 +152,7 @@ __global__ __launch_bounds__(256) void select_kernel(SelectArgs a) {
     atomicAdd(&fhist[vb[j]], 1);
   }
   __syncthreads();
-  if (tid == 0) hist[0] += N - hi_keys;
+  if (tid == 0) hist[0] = N - misc[1];   // keys past hi_keys have no vote either
   __syncthreads();
   // ---- C[v] = #(votes >= v) (suffix sums) and F[v] = #(forced with vote < v) (prefix sums) ----
   {
@@ -189,23 +213,32 @@ __global__ __launch_bounds__(256) void select_kernel(SelectArgs a) {
   const int vc = misc[0];
   // ---- compaction + reposition over keys [0, scan_end) ----
   const int scan_end = (vc == 0) ? N : min(N, max(hi_keys, max(gA, bh + 1)));
-  const int j0 = tid * per;
   const int j1 = min(j0 + per, scan_end);
   int cnt = 0;
-  for (int j = j0; j < j1; ++j) {
-    const bool forced = (j < gA) || (j >= bl && j <= bh);
-    cnt += (vb[j] >= vc) || forced;
+  for (int jb = j0; jb < j1; jb += 16) {
+    const u32x4 w = seg_bytes(jb);
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const int j = jb + e;
+      const bool forced = (j < gA) || (j >= bl && j <= bh);
+      cnt += j < j1 && ((byte_of(w, e) >= vc) || forced);
+    }
   }
   const int base = block_exclusive_sum(cnt, tmpi);
   float mloc = -INFINITY;
   {
     int rank = base - 1;
-    for (int j = j0; j < j1; ++j) {
-      const bool forced = (j < gA) || (j >= bl && j <= bh);
-      if ((vb[j] >= vc) || forced) {
-        rank += 1;
-        const float cp = (float)j * a.pos_scale;        // exact_2.py:384
-        mloc = fmaxf(mloc, cp - (float)rank);           // exact_2.py:385
+    for (int jb = j0; jb < j1; jb += 16) {
+      const u32x4 w = seg_bytes(jb);
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int j = jb + e;
+        const bool forced = (j < gA) || (j >= bl && j <= bh);
+        if (j < j1 && ((byte_of(w, e) >= vc) || forced)) {
+          rank += 1;
+          const float cp = (float)j * a.pos_scale;      // exact_2.py:384
+          mloc = fmaxf(mloc, cp - (float)rank);         // exact_2.py:385
+        }
       }
     }
   }
@@ -214,17 +247,24 @@ __global__ __launch_bounds__(256) void select_kernel(SelectArgs a) {
   const int qhi = (int)min(tstart + T - 1, (int64_t)N - 1);
   {
     int rank = base - 1;
-    for (int j = j0; j < j1; ++j) {
-      const bool forced = (j < gA) || (j >= bl && j <= bh);
-      const bool kept = (vb[j] >= vc) || forced;
-      if (kept) {
-        rank += 1;
-        const float cp = (float)j * a.pos_scale;
-        run = fmaxf(run, cp - (float)rank);
+    for (int jb = j0; jb < j1; jb += 16) {
+      const u32x4 w = seg_bytes(jb);
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int j = jb + e;
+        if (j < j1) {
+          const bool forced = (j < gA) || (j >= bl && j <= bh);
+          const bool kept = (byte_of(w, e) >= vc) || forced;
+          if (kept) {
+            rank += 1;
+            const float cp = (float)j * a.pos_scale;
+            run = fmaxf(run, cp - (float)rank);
+          }
+          const float np = (float)rank + run;          // exact_2.py:386
+          if (kept && rank < a.k_max) { sidx[rank] = j; snp[rank] = np; }
+          if (j >= qlo && j <= qhi) qnp[j - qlo] = np;
+        }
       }
-      const float np = (float)rank + run;              // exact_2.py:386
-      if (kept && rank < a.k_max) { sidx[rank] = j; snp[rank] = np; }
-      if (j >= qlo && j <= qhi) qnp[j - qlo] = np;
     }
   }
   __syncthreads();
