@@ -860,35 +860,70 @@ void score_kernel(ScoreArgs a) {
     // each over half of the dims (the fragment layout's lane halves), 32 pairs per round ----
     if (active) {
       const int g = lane >> 5;
+      // Q operands come from registers: qhi is held since the sweep, qlo is loaded once here in
+      // the same layout (lane l holds row l % 32 of each row block, dims half l / 32), and a pair's
+      // row is fetched from its owner lane with a bpermute; only the keys are gathered from memory.
+      u32x4 qlo1[RB][S];
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb) {
+        const bool ok = wrow0 + 32 * rb < rows_total;
+#pragma unroll
+        for (int s = 0; s < S; ++s) {
+          const int64_t u = (((int64_t)h * (a.q_rows_pad >> 5) + wrow0 / 32 + rb) * S + s) * 128 + lane;
+          qlo1[rb][s] = ok ? a.qfrag[u + 64] : u32x4{0, 0, 0, 0};
+        }
+      }
+      auto bperm = [](int addr, const u32x4& x) {
+        u32x4 r;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) r[e] = (uint32_t)__builtin_amdgcn_ds_bpermute(addr, (int)x[e]);
+        return r;
+      };
       for (int it = 0; it * 32 < total; ++it) {
         const int f = it * 32 + (lane & 31);
         const bool valid = f < total;
         const int row = valid ? frow[f] : 0;
         const int key = valid ? fkey[f] : 0;
-        const int qr = wrow0 + row;
-        const u32x4* qp = a.qfrag + (((int64_t)h * (a.q_rows_pad >> 5) + (qr >> 5)) * S) * 128 + (qr & 31) + 32 * g;
         const u32x4* kp = kbase + (int64_t)(key >> 5) * S * 128 + (key & 31) + 32 * g;
-        u32x4 qh[S], ql[S], kh[S], kl[S];
+        u32x4 kh[S], kl[S];
 #pragma unroll
         for (int s = 0; s < S; ++s) {
-          qh[s] = qp[s * 128];
-          ql[s] = qp[s * 128 + 64];
           kh[s] = kp[s * 128];
           kl[s] = kp[s * 128 + 64];
         }
+        const int src = ((row & 31) + (lane & 32)) << 2;   // the row's owner lane, same dims half
+        const int rbr = row >> 5;
+        // rows are listed in order, so a round's pairs mostly share one row block
+        const bool in0 = __ballot(valid && rbr == 0) != 0, in1 = __ballot(valid && rbr == 1) != 0;
         float acc = 0.0f;
+        auto dot = [&](auto modec) {
+          constexpr int MODE_RB = decltype(modec)::value;   // 0 / 1: that row block; 2: either
 #pragma unroll
-        for (int s = 0; s < S; ++s) {
+          for (int s = 0; s < S; ++s) {
+            u32x4 qh, ql;
+            if constexpr (MODE_RB < 2) {
+              qh = bperm(src, qhi[MODE_RB][s]);
+              ql = bperm(src, qlo1[MODE_RB][s]);
+            } else {
+              const u32x4 h0 = bperm(src, qhi[0][s]), h1 = bperm(src, qhi[RB - 1][s]);
+              const u32x4 l0 = bperm(src, qlo1[0][s]), l1 = bperm(src, qlo1[RB - 1][s]);
+              qh = rbr == 0 ? h0 : h1;
+              ql = rbr == 0 ? l0 : l1;
+            }
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const float x0 = __uint_as_float(qh[s][e] << 16) + __uint_as_float(ql[s][e] << 16);
-            const float x1 = __uint_as_float(qh[s][e] & 0xffff0000u) + __uint_as_float(ql[s][e] & 0xffff0000u);
-            const float y0 = __uint_as_float(kh[s][e] << 16) + __uint_as_float(kl[s][e] << 16);
-            const float y1 = __uint_as_float(kh[s][e] & 0xffff0000u) + __uint_as_float(kl[s][e] & 0xffff0000u);
-            acc = fmaf(x0, y0, acc);
-            acc = fmaf(x1, y1, acc);
+            for (int e = 0; e < 4; ++e) {
+              const float x0 = __uint_as_float(qh[e] << 16) + __uint_as_float(ql[e] << 16);
+              const float x1 = __uint_as_float(qh[e] & 0xffff0000u) + __uint_as_float(ql[e] & 0xffff0000u);
+              const float y0 = __uint_as_float(kh[s][e] << 16) + __uint_as_float(kl[s][e] << 16);
+              const float y1 = __uint_as_float(kh[s][e] & 0xffff0000u) + __uint_as_float(kl[s][e] & 0xffff0000u);
+              acc = fmaf(x0, y0, acc);
+              acc = fmaf(x1, y1, acc);
+            }
           }
-        }
+        };
+        if (!in1) dot(std::integral_constant<int, 0>{});
+        else if (!in0) dot(std::integral_constant<int, RB - 1>{});
+        else dot(std::integral_constant<int, 2>{});
         const float tot = acc + __shfl_xor(acc, 32, 64);
         // order-preserving key of an fp32 value (every key of a real value is nonzero)
         const uint32_t tb = __float_as_uint(tot + 0.0f);
