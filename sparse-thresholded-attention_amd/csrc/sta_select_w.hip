@@ -166,32 +166,15 @@ __global__ __launch_bounds__(256) void select_w_kernel(SelectArgs a) {
       }
       for (int i = tid; i < 256 * nh; i += 256) hist[i] = 0;
       __syncthreads();
-      if (shift == 24) {
-        // the top digit (sign and high exponent bits) takes few values in a tile: one LDS atomic
-        // per distinct digit of a wave
-        for (int i = 0; i < per; ++i) {                  // same trip count on every lane
-          const uint32_t k = myrow[i];
-          bool act = k != 0 && j0 + i < N;
-          const int d = (int)(k >> 24);
-          uint64_t m = __ballot(act);
-          while (m) {
-            const int leader = __ffsll((unsigned long long)m) - 1;
-            const int dl = __shfl(d, leader, 64);
-            const uint64_t same = __ballot(act && d == dl);
-            if (lane == leader) atomicAdd(&hist[dl], (int)__popcll(same));
-            if (act && d == dl) act = false;
-            m &= ~same;
-          }
-        }
-      } else {
-        for (int i = 0; i < per; ++i) {
-          const uint32_t k = myrow[i];
-          if (k == 0 || j0 + i >= N) continue;
-          const uint32_t kp = k & pmask;
+      // plain LDS atomics on every level, the top digit included (a per-wave aggregation of the
+      // top digit's few distinct values by ballots measured slower)
+      for (int i = 0; i < per; ++i) {
+        const uint32_t k = myrow[i];
+        if (k == 0 || j0 + i >= N) continue;
+        const uint32_t kp = k & pmask;
 #pragma unroll
-          for (int w = 0; w < 3; ++w)
-            if (w < nh && kp == hp[w]) atomicAdd(&hist[w * 256 + ((k >> shift) & 255u)], 1);
-        }
+        for (int w = 0; w < 3; ++w)
+          if (w < nh && kp == hp[w]) atomicAdd(&hist[w * 256 + ((k >> shift) & 255u)], 1);
       }
       __syncthreads();
 #pragma unroll
