@@ -135,9 +135,10 @@ __global__ __launch_bounds__(256) void pq_select_kernel(PqSelectArgs a) {
     for (int shift = 24; shift >= 0; shift -= 8) {
       hist[tid] = 0;
       __syncthreads();
-      if (shift == 24) {
-        // top digit (sign + high exponent bits): few distinct values per wave -> one atomic per
-        // distinct digit
+      if (shift == 24 && !a.wvotes) {
+        // top digit (sign + high exponent bits) of vote counts: a handful of distinct values per
+        // wave -> one atomic per distinct digit (weighted rank values spread over more exponents,
+        // where plain atomics measured faster)
         for (int i = 0; i < per; ++i) {                // same trip count on every lane
           const uint32_t k = myrow[i];
           bool act = k != 0 && j0 + i < N;
