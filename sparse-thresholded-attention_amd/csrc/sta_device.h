@@ -220,7 +220,7 @@ struct Raw8<DT_F32> {
 // The argument is reduced straight to revolutions, t = x / (2 pi) - k, with 1 / (2 pi) split
 // into two fp32 terms kH + kL: fma(x, kH, -k) is the exact product minus the integer k, rounded
 // once, and fma(x, kL, .) adds the low term.  The hardware sine/cosine take t in revolutions.
-// Reduction error below 3e-8 revolutions for |x| < 5000 (two-constant Cody-Waite by 2 pi, one
+// Reduction error below 4e-8 revolutions for |x| < 5000 (two-constant Cody-Waite by 2 pi, one
 // instruction longer, reaches 6e-8); the angle itself is the reference's fp32 product.
 // ------------------------------------------------------------------------------------------
 __device__ __forceinline__ void fast_sincos(float x, float& s, float& c) {
