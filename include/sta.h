@@ -112,7 +112,9 @@ int sta_shared_attention(const sta_shared_args* args, void* stream);
  * Replaces the _select_vote_kernel launch, shared_selection_triton_exact_2.py:50-140, 454-465. */
 int sta_select_vote(const sta_shared_args* args, void* stream);
 
-/* _build_sets alone (freq ranking) from int32 votes (H, num_tiles, N) with values in [0, 255];
+/* _build_sets alone (freq ranking) from int32 votes (H, num_tiles, N) with values in [0, 255]
+ * (a tile's vote count is at most its tile size; the votes are staged as bytes and values outside
+ * that range are not detected: they wrap modulo 256, so the caller must keep them in range);
  * writes idx, newpos_k, newpos_q and the six statistics, all with num_tiles tiles (the
  * reference takes the tile count from the votes tensor, not from N).  Uses pos_scale_c,
  * n_global, n_local, start_pct, tile, k_max, q_pos_base, measure.

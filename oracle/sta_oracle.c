@@ -195,12 +195,15 @@ static long budget_of(int p, long usize) {
  * wvotes (H, nt, N) fp32 or NULL: with it the ranking metric is the weighted score with frequency
  * as an epsilon tiebreak, rank = fl(wvotes + fl(1e-6 * votes)) (exact_2.py:299-302); the union
  * size and budgets stay frequency-based (exact_2.py:296).  NULL ranks by votes (freq).
+ * cut (H, nt) fp32 or NULL: the rank-value threshold v_cut of the step whose sets were kept
+ * (exact_2.py:330, 348-350), +inf where only the forced keys are kept (pct 0).  Not a reference
+ * output: the parity tests use it to tell a key moved by a shifted cut from a flipped key.
  */
 void oracle_build_sets(const int32_t* votes, int H, int nt, int N, float pos_scale, int n_global,
                        int n_local, int start_pct, int T, int k_max, int q_pos_base, int measure,
                        int32_t* idx, float* newpos_k, float* newpos_q, int32_t* shared_size,
                        int32_t* kept_size, int32_t* chosen, uint8_t* orig_overflow,
-                       int32_t* kpct_meas, uint8_t* overflow20, const float* wvotes) {
+                       int32_t* kpct_meas, uint8_t* overflow20, const float* wvotes, float* cut) {
   /* pct_steps = [start] + [c for c in (25, 20) if c < start]            (exact_2.py:309-310) */
   int steps[3], nsteps = 0;
   steps[nsteps++] = start_pct;
@@ -343,6 +346,7 @@ void oracle_build_sets(const int32_t* votes, int H, int nt, int N, float pos_sca
       orig_overflow[o] = (uint8_t)oflow;
       overflow20[o] = (uint8_t)ovf20;
       kpct_meas[o] = kmeas;
+      if (cut) cut[o] = use_forced_only ? INFINITY : cut_final;
     }
     free(sv);
     free(rv);

@@ -160,11 +160,12 @@ def start_pct_of(pct):
 
 
 def build_sets(votes, pos_scale, n_global, n_local, pct, T, k_max, q_pos_base=0, measure=False,
-               wvotes=None):
+               wvotes=None, want_cut=False):
     """_build_sets (exact_2.py:277-426).  votes (H,nt,N) int; wvotes (H,nt,N) fp32 switches the
     ranking to fl(wvotes + fl(1e-6 votes)) (margin / expmass, exact_2.py:299-302), None ranks by
     votes.  Returns the reference's 9-tuple (idx, newpos_k, newpos_q, shared_size, kept_size,
-    chosen, orig_overflow, kpct_meas, overflow20) as numpy arrays."""
+    chosen, orig_overflow, kpct_meas, overflow20) as numpy arrays; with want_cut a 10th entry,
+    the (H, nt) fp32 rank-value cut of the kept step (+inf where only forced keys are kept)."""
     votes = _c(votes, np.int32)
     if wvotes is not None:
         wvotes = _c(wvotes, np.float32)
@@ -179,12 +180,15 @@ def build_sets(votes, pos_scale, n_global, n_local, pct, T, k_max, q_pos_base=0,
     oo = np.empty((H, nt), np.uint8)
     km = np.empty((H, nt), np.int32)
     o20 = np.empty((H, nt), np.uint8)
+    cut = np.empty((H, nt), np.float32) if want_cut else None
     lib().oracle_build_sets(
         _p(votes), ctypes.c_int(H), ctypes.c_int(nt), ctypes.c_int(N), ctypes.c_float(pos_scale),
         ctypes.c_int(n_global), ctypes.c_int(n_local), ctypes.c_int(start_pct_of(pct)),
         ctypes.c_int(T), ctypes.c_int(k_max), ctypes.c_int(q_pos_base), ctypes.c_int(int(measure)),
-        _p(idx), _p(npk), _p(npq), _p(ss), _p(ks), _p(ch), _p(oo), _p(km), _p(o20), _p(wvotes))
-    return idx, npk, npq, ss, ks, ch, oo.astype(bool), km, o20.astype(bool)
+        _p(idx), _p(npk), _p(npq), _p(ss), _p(ks), _p(ch), _p(oo), _p(km), _p(o20), _p(wvotes),
+        _p(cut))
+    res = (idx, npk, npq, ss, ks, ch, oo.astype(bool), km, o20.astype(bool))
+    return res + (cut,) if want_cut else res
 
 
 def gather_attn(q, k, v, dtype, idx, newpos_k, newpos_q, inv_freq, rope_scale, sm_scale, T,

@@ -385,6 +385,11 @@ def build_sets(votes, pos_scale, n_global, n_local, pct, T, k_max, q_pos_base=0,
     if not votes.is_cuda:
         raise RuntimeError("build_sets runs on a HIP device only; got a CPU tensor")
     votes = votes.to(torch.int32).contiguous()
+    # the library stages votes as bytes (a tile's count is at most its 32 or 64 queries) and does
+    # not check them; a value outside [0, 255] would wrap, so it is rejected here (one sync, as the
+    # reference's own _build_sets syncs)
+    if votes.numel() and (int(votes.min()) < 0 or int(votes.max()) > 255):
+        raise ValueError("votes must lie in [0, 255] (a tile's vote count is at most its tile size)")
     if wvotes is not None:
         wvotes = wvotes.to(device=votes.device, dtype=torch.float32).contiguous()
         if wvotes.shape != votes.shape:

@@ -220,8 +220,10 @@ struct Raw8<DT_F32> {
 // The argument is reduced straight to revolutions, t = x / (2 pi) - k, with 1 / (2 pi) split
 // into two fp32 terms kH + kL: fma(x, kH, -k) is the exact product minus the integer k, rounded
 // once, and fma(x, kL, .) adds the low term.  The hardware sine/cosine take t in revolutions.
-// Reduction error below 4e-8 revolutions for |x| < 5000 (two-constant Cody-Waite by 2 pi, one
-// instruction longer, reaches 6e-8); the angle itself is the reference's fp32 product.
+// Reduction error below 4e-8 revolutions for |x| < 5000 and below 6e-8 up to |x| = 65536, where
+// k can round to the neighbouring integer and |t| slightly exceeds 0.5 (a two-constant Cody-Waite
+// reduction by 2 pi takes one more instruction and reaches 6e-8 already below 5000); the angle
+// itself is the reference's fp32 product.
 // ------------------------------------------------------------------------------------------
 __device__ __forceinline__ void fast_sincos(float x, float& s, float& c) {
   const float kH = 0.15915494f;        // fp32(1 / (2 pi)), 0x3e22f983

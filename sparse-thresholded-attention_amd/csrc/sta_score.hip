@@ -948,8 +948,15 @@ void score_kernel(ScoreArgs a) {
   };
 
   // row max over the 32 lanes holding a row's keys (mx: the raw dot's running max per row slot),
-  // then the keep threshold x0 on the raw dot, and the weighted-vote origins
-  auto finish1 = [&]() {
+  // then the keep threshold x0 on the raw dot, and the weighted-vote origins.
+  // screened: the maximum came from the screen's fp32 dots of the (hi + lo) operands, which
+  // differ from pass 2's three-product value of the same key by the lo.lo term and the two
+  // summation orders.  The threshold is then capped at max - delta, with delta a bound on that
+  // difference, so the row's best key keeps its vote for any tau (the reference's two passes
+  // share one dot, exact_2.py:100, 118, so qk == m always passes); for tau above delta * scale
+  // (1e-5 at unit-scale rows) the cap changes nothing.
+  auto finish1 = [&](bool screened) {
+    const float2 knm = a.knorm_max[kvh];
     if (active) {
       // complete the row max over the 32 lanes holding a row's keys, then the threshold
 #pragma unroll
@@ -965,7 +972,13 @@ void score_kernel(ScoreArgs a) {
           const float m = v * a.sm_scale;   // fl(max * c) == max of fl(s * c) for c > 0
           const int row = rb * 32 + (i >> 2) * 8 + (lane >> 5) * 4 + (i & 3);
           const bool ok = wrow0 + row < a.N;   // padded rows never vote (exact_2.py:121)
-          mx[rb][i] = ok ? min_arg_for(m - tau, a.sm_scale) : INFINITY;
+          float x0 = ok ? min_arg_for(m - tau, a.sm_scale) : INFINITY;
+          if (screened && ok) {
+            const float2 qn = a.qnorm[(int64_t)h * a.q_rows_pad + wrow0 + row];
+            const float delta = 1.001f * (qn.y * knm.y + 0x1p-15f * (qn.x + qn.y) * (knm.x + knm.y));
+            x0 = fminf(x0, v - delta);
+          }
+          mx[rb][i] = x0;
           if constexpr (WM == 1) ref[rb][i] = m - tau;   // perquery.py:210; exact_2.py:130
           if constexpr (WM == 2) ref[rb][i] = m;         // perquery.py:215; exact_2.py:135
           if (a.row_max && (lane & 31) == 0 && ok) a.row_max[(int64_t)h * a.N + wrow0 + row] = m;
@@ -1094,7 +1107,7 @@ void score_kernel(ScoreArgs a) {
       chunk_end(c);
     }
     if (active && pendingB) flush(passc, accB, keyB);
-    if constexpr (pass == 0) finish1();
+    if constexpr (pass == 0) finish1(false);
   };
   if constexpr (MODE == 1) {
     // the screen: each row's exact raw maximum, or the workgroup's fallback flag
@@ -1135,7 +1148,7 @@ void score_kernel(ScoreArgs a) {
       }
     }
     if (exact1) run_pass(std::integral_constant<int, 0>{});
-    else finish1();
+    else finish1(true);
     run_pass(std::integral_constant<int, 1>{});
   }
 

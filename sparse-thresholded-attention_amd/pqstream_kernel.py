@@ -11,65 +11,48 @@ import math
 import torch
 
 import _sta_native as native
+from _counters import PhaseCounters, ratio
 
 ADV_MAX = 0
 ADV_FULL = 1
 _ADV = {"max": ADV_MAX, "full": ADV_FULL}
 
 
-def _fresh():
-    return {"cells": 0, "span_sum": None, "span_max": None,
-            "kept_sum": None, "rows": 0, "blocks": None, "skipped": None}
-
-
-_STATS = {"prefill": _fresh(), "decode": _fresh()}
+# measurement-only statistics per phase (the reference's get_overflow_stats keys,
+# pqstream_kernel.py:85-150): a cell is a (head, tile), a row is one query
+_STATS = {p: PhaseCounters(sums=("span", "kept", "blocks", "skipped"), maxes=("span",),
+                           counts=("cells", "rows")) for p in ("prefill", "decode")}
 
 
 def reset_overflow_stats():
     """Zero the cumulative span / kept / skip counters."""
-    _STATS["prefill"] = _fresh()
-    _STATS["decode"] = _fresh()
+    for c in _STATS.values():
+        c.clear()
 
 
 reset_span_stats = reset_overflow_stats
 
 
-def _phase_stats(d):
-    tot = d["cells"]
-    ssum = float(d["span_sum"].item()) if d["span_sum"] is not None else 0.0
-    smax = float(d["span_max"].item()) if d["span_max"] is not None else 0.0
-    ksum = float(d["kept_sum"].item()) if d["kept_sum"] is not None else 0.0
-    blk = int(d["blocks"].item()) if d["blocks"] is not None else 0
-    skp = int(d["skipped"].item()) if d["skipped"] is not None else 0
-    return {"total_cells": tot, "span_mean": (ssum / tot) if tot else 0.0, "span_max": smax,
-            "kept_mean": (ksum / d["rows"]) if d["rows"] else 0.0, "blocks": blk, "skipped": skp,
-            "skip_frac": (skp / blk) if blk else 0.0, "overflow_cells": 0, "overflow_frac": 0.0}
+def _summary(c):
+    n, s, m = c.read()
+    blocks, skipped = int(s["blocks"]), int(s["skipped"])
+    # PQ Stream has no k_max: the two overflow fields are always 0 (kept for pq_exact callers)
+    return {"total_cells": n["cells"], "span_mean": ratio(s["span"], n["cells"]), "span_max": m["span"],
+            "kept_mean": ratio(s["kept"], n["rows"]), "blocks": blocks, "skipped": skipped,
+            "skip_frac": ratio(skipped, blocks), "overflow_cells": 0, "overflow_frac": 0.0}
 
 
 def get_overflow_stats():
     """Cumulative since the last reset, per phase (one host sync here, none during the run)."""
-    return {"prefill": _phase_stats(_STATS["prefill"]), "decode": _phase_stats(_STATS["decode"])}
+    return {p: _summary(c) for p, c in _STATS.items()}
 
 
-def _acc(dst, key, val, reduce="sum"):
-    if dst[key] is None:
-        dst[key] = val
-    elif reduce == "max":
-        dst[key] = torch.maximum(dst[key], val)
-    else:
-        dst[key] = dst[key] + val
-
-
-def _stats_accumulate(span, kept, blocks, skipped, phase="prefill"):
-    """Measurement only, on the device (pqstream_kernel.py:138-150)."""
-    d = _STATS[phase]
-    d["cells"] += span.numel()
-    d["rows"] += kept.numel()
-    _acc(d, "span_sum", span.double().sum())
-    _acc(d, "span_max", span.max(), reduce="max")
-    _acc(d, "kept_sum", kept.double().sum())
-    _acc(d, "blocks", blocks.long().sum())
-    _acc(d, "skipped", skipped.long().sum())
+def _record(span, kept, blocks, skipped, phase="prefill"):
+    """span (H,nt) fp32, kept (H,N) int32, blocks / skipped (H,nt) int32, all on the device."""
+    _STATS[phase].add({"cells": span.numel(), "rows": kept.numel()},
+                      (span.sum(dtype=torch.float64), kept.sum(dtype=torch.float64),
+                       blocks.sum(dtype=torch.float64), skipped.sum(dtype=torch.float64)),
+                      (span.max(),))
 
 
 def pqstream_attention(q, k, v, tau, inv_freq_a, inv_freq_c, pos_scale_a=1.0, rope_scale_a=1.0,
@@ -89,5 +72,5 @@ def pqstream_attention(q, k, v, tau, inv_freq_a, inv_freq_c, pos_scale_a=1.0, ro
         sm_scale = 1.0 / math.sqrt(D)
     r = native.pqstream_attention(q, k, v, tau, inv_freq_a, inv_freq_c, pos_scale_a, rope_scale_a, sm_scale,
                                   n_global, n_local, tile, block_n, pos_advance, q_pos_base, use_skip)
-    _stats_accumulate(r["span"], r["kept"], r["blocks"], r["skipped"], phase="prefill")
+    _record(r["span"], r["kept"], r["blocks"], r["skipped"], phase="prefill")
     return r["out"].unsqueeze(0), r["span"], r["kept"], r["blocks"], r["skipped"]

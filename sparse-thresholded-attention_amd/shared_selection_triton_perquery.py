@@ -16,46 +16,37 @@ import math
 import torch
 
 import _sta_native as native
+from _counters import PhaseCounters, ratio
 
 
-def _fresh():
-    return {"cells": 0, "overflow": None, "union_sum": None, "union_max": None}
-
-
-_OVF_STATS = {"prefill": _fresh(), "decode": _fresh()}
+# measurement-only statistics per phase (the reference's get_overflow_stats keys,
+# perquery.py:52-112): a prefill cell is a (head, 32-query tile), a decode cell a (head, query)
+_OVF_STATS = {p: PhaseCounters(sums=("overflow", "union"), maxes=("union",)) for p in ("prefill", "decode")}
 
 
 def reset_overflow_stats():
     """Zero the cumulative overflow / union counters."""
-    _OVF_STATS["prefill"] = _fresh()
-    _OVF_STATS["decode"] = _fresh()
+    for c in _OVF_STATS.values():
+        c.clear()
 
 
-def _phase_stats(d):
-    tot = d["cells"]
-    ovf = int(d["overflow"].item()) if d["overflow"] is not None else 0
-    usum = int(d["union_sum"].item()) if d["union_sum"] is not None else 0
-    umax = int(d["union_max"].item()) if d["union_max"] is not None else 0
-    return {"total_cells": tot, "overflow_cells": ovf, "overflow_frac": (ovf / tot) if tot else 0.0,
-            "union_mean": (usum / tot) if tot else 0.0, "union_max": umax}
+def _summary(c):
+    n, s, m = c.read()
+    cells, ovf = n["cells"], int(s["overflow"])
+    return {"total_cells": cells, "overflow_cells": ovf, "overflow_frac": ratio(ovf, cells),
+            "union_mean": ratio(s["union"], cells), "union_max": int(m["union"])}
 
 
 def get_overflow_stats():
     """Cumulative since the last reset, per phase (one host sync here, none during the run)."""
-    return {"prefill": _phase_stats(_OVF_STATS["prefill"]), "decode": _phase_stats(_OVF_STATS["decode"])}
+    return {p: _summary(c) for p, c in _OVF_STATS.items()}
 
 
-def _ovf_accumulate(overflow, usize, phase="prefill"):
-    """Measurement only; accumulated on the device (perquery.py:97-112)."""
-    d = _OVF_STATS[phase]
-    d["cells"] += overflow.numel()
-    ov, us, um = overflow.sum(), usize.long().sum(), usize.max()
-    if d["overflow"] is None:
-        d["overflow"], d["union_sum"], d["union_max"] = ov, us, um
-    else:
-        d["overflow"] = d["overflow"] + ov
-        d["union_sum"] = d["union_sum"] + us
-        d["union_max"] = torch.maximum(d["union_max"], um)
+def _record(overflow, usize, phase="prefill"):
+    """overflow (H, n) bool, usize (H, n) int32, on the device."""
+    _OVF_STATS[phase].add({"cells": overflow.numel()},
+                          (overflow.sum(dtype=torch.float64), usize.sum(dtype=torch.float64)),
+                          (usize.max(),))
 
 
 def _build_sets_pq(votes, bits, wvotes, n_global, n_local, T, k_max, q_pos_base=0,
@@ -63,7 +54,7 @@ def _build_sets_pq(votes, bits, wvotes, n_global, n_local, T, k_max, q_pos_base=
     """votes / bits (H,nt,N) int32, wvotes (H,nt,N) fp32 (or a dummy) -> (idx, newpos_k,
     newpos_q, mask, usize, kept_size, overflow).  shared_selection_triton_perquery.py:363-453."""
     res = native.pq_build_sets(votes, bits, wvotes, n_global, n_local, T, k_max, q_pos_base, select_score)
-    _ovf_accumulate(res[6], res[4])
+    _record(res[6], res[4])
     return res
 
 
@@ -85,5 +76,5 @@ def shared_pq_attention(q, k, v, tau, inv_freq_a, inv_freq_c, pos_scale_a=1.0, r
         sm_scale = 1.0 / math.sqrt(D)
     r = native.pq_attention(q, k, v, tau, inv_freq_a, inv_freq_c, pos_scale_a, rope_scale_a, sm_scale,
                             n_global, n_local, tile, k_max, q_pos_base, select_score)
-    _ovf_accumulate(r["overflow"], r["usize"])
+    _record(r["overflow"], r["usize"])
     return r["out"].unsqueeze(0), r["usize"], r["kept_size"], r["overflow"]

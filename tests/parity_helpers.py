@@ -66,6 +66,71 @@ def gpu_sets_numpy(r):
     return {n: r[n].cpu().numpy() for n in SET_NAMES}
 
 
+def forced_mask(nt, N, T, n_global, n_local, q_pos_base=0):
+    """(nt, N) bool: global keys and each tile's local window (exact_2.py:290-293, 303)."""
+    j = np.arange(N)[None, :]
+    tstart = q_pos_base + np.arange(nt)[:, None] * T
+    return (j < n_global) | ((j >= tstart - n_local + 1) & (j <= tstart + T - 1))
+
+
+def classify_set_diffs(votes_g, votes_o, band, sets_g, sets_o, cut_g, cut_o, T, k_max, n_global,
+                       n_local, q_pos_base=0, rank_g=None, rank_o=None):
+    """Count the keys whose membership in the selected sets differs between the GPU (sets built
+    from its own votes) and the oracle (sets built from the oracle's votes), and classify each:
+
+      band  - the key itself has a score within BAND of the threshold m - tau of one of the
+              tile's queries (its vote may legitimately differ);
+      cut   - the key's rank value is the same on both sides and lies between the two sides'
+              cuts v_cut (tie-inclusive, exact_2.py:330-331): a band flip elsewhere in the tile
+              moved the cut (or the chosen fallback step) past it;
+      trunc - the tile is truncated to its k_max smallest kept keys (exact_2.py:394-405) on
+              either side and the key lies past the first key where the untruncated sets differ,
+              so the truncation boundary moved with it.
+    Anything else fails.  rank_* default to the votes (frequency ranking); cut_* are the oracle's
+    per-tile cuts for each side's votes.  Returns a dict of counts."""
+    H, nt, N = votes_g.shape
+    rank_g = votes_g.astype(np.float32) if rank_g is None else rank_g
+    rank_o = votes_o.astype(np.float32) if rank_o is None else rank_o
+    kg, ko = kept_mask_of(sets_g["idx"], N), kept_mask_of(sets_o["idx"], N)
+    forced = forced_mask(nt, N, T, n_global, n_local, q_pos_base)
+    counts = {"tiles": H * nt, "tiles_differ": 0, "keys": 0, "band": 0, "cut": 0, "trunc": 0}
+    for h, t in np.argwhere((kg != ko).any(-1)):
+        counts["tiles_differ"] += 1
+        assert (votes_g[h, t] != votes_o[h, t]).any(), f"tile ({h},{t}): sets differ with equal votes"
+        fg = (rank_g[h, t] >= cut_g[h, t]) | forced[t]
+        fo = (rank_o[h, t] >= cut_o[h, t]) | forced[t]
+        full_diff = np.nonzero(fg != fo)[0]
+        lo_c, hi_c = sorted((float(cut_g[h, t]), float(cut_o[h, t])))
+        for j in full_diff:
+            if band[h, t, j] > 0:
+                continue
+            same = rank_g[h, t, j] == rank_o[h, t, j]
+            assert same and lo_c <= rank_g[h, t, j] <= hi_c, (
+                f"tile ({h},{t}) key {j}: not a band key and not between the cuts "
+                f"(rank {rank_g[h, t, j]} / {rank_o[h, t, j]}, cuts {lo_c} {hi_c})")
+        keys = np.nonzero(kg[h, t] != ko[h, t])[0]
+        first = full_diff.min() if full_diff.size else N
+        truncated = fg.sum() > k_max or fo.sum() > k_max
+        for j in keys:
+            counts["keys"] += 1
+            if j in full_diff:
+                counts["band" if band[h, t, j] > 0 else "cut"] += 1
+            else:
+                assert truncated and j > first, (
+                    f"tile ({h},{t}) key {j}: differs only after truncation but the tile is not "
+                    f"truncated past an earlier difference (first {first})")
+                counts["trunc"] += 1
+    return counts
+
+
+def report_set_diffs(what, c):
+    msg = (f"[sets] {what}: {c['tiles_differ']} of {c['tiles']} tiles differ from the oracle's sets; "
+           f"{c['keys']} keys: {c['band']} band keys, {c['cut']} moved by a shifted cut, "
+           f"{c['trunc']} moved by the truncation boundary")
+    print(msg, flush=True)
+    return msg
+
+
 def out_f32(t):
     return t.float().cpu().numpy()
 
@@ -117,3 +182,48 @@ def compare_pq_sets(got, ref, rank_vals, N, rel=0.0):
         tol = rel * abs(float(cut))
         assert np.all(np.abs(rv - cut) <= tol), (h, t, keys[:8].tolist(), rv[:8].tolist(), float(cut))
     return int(differ.sum())
+
+
+def classify_pq_set_diffs(band, sets_g, sets_o, rank_g, rank_o, N, rel=1e-4):
+    """PQ Union: count the keys whose membership in the tile's union set differs between the GPU
+    (sets from its own bits / weighted votes) and the oracle (sets from its own), classified:
+
+      band - one of the tile's rows has the key's score within BAND of its threshold, so the
+             key's keep bit (and its weighted vote) may differ;
+      cut  - the tile overflows k_max on either side (perquery.py:393-410), the key's rank value
+             is the same on both sides and lies between the two sides' cuts (the smallest kept
+             non-forced rank value); "same" and "between" are widened by `rel` for the fp32
+             summation order of the weighted votes.
+    Anything else fails.  Returns a dict of counts."""
+    kg, ko = kept_mask_of(sets_g["idx"], N), kept_mask_of(sets_o["idx"], N)
+    H, nt = kg.shape[:2]
+    counts = {"tiles": H * nt, "tiles_differ": 0, "keys": 0, "band": 0, "cut": 0}
+
+    def cut_of(s, rank, h, t):
+        idx, mask = s["idx"][h, t], s["mask"][h, t]
+        sel = idx[(idx < N) & (mask != -1)]
+        return float(rank[h, t, sel].min()) if sel.size else float("inf")
+
+    for h, t in np.argwhere((kg != ko).any(-1)):
+        counts["tiles_differ"] += 1
+        over = bool(sets_g["overflow"][h, t]) or bool(sets_o["overflow"][h, t])
+        lo_c, hi_c = sorted((cut_of(sets_g, rank_g, h, t), cut_of(sets_o, rank_o, h, t)))
+        for j in np.nonzero(kg[h, t] != ko[h, t])[0]:
+            counts["keys"] += 1
+            if band[h, t, j] > 0:
+                counts["band"] += 1
+                continue
+            r = (float(rank_g[h, t, j]), float(rank_o[h, t, j]))
+            same = abs(r[0] - r[1]) <= rel * max(abs(r[0]), abs(r[1]))
+            ok = over and same and any(lo_c - rel * abs(lo_c) <= x <= hi_c + rel * abs(hi_c) for x in r)
+            assert ok, (f"tile ({h},{t}) key {j}: not a band key and not at the overflow cut "
+                        f"(rank {r}, cuts {lo_c} {hi_c}, overflow {over})")
+            counts["cut"] += 1
+    return counts
+
+
+def report_pq_set_diffs(what, c):
+    msg = (f"[sets] {what}: {c['tiles_differ']} of {c['tiles']} tiles differ from the oracle's sets; "
+           f"{c['keys']} keys: {c['band']} band keys, {c['cut']} at the overflow cut")
+    print(msg, flush=True)
+    return msg

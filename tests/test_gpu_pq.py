@@ -19,8 +19,8 @@ import pytest
 import torch
 
 from oracle import sta_oracle as orc
-from parity_helpers import (BAND, PQ_SET_NAMES, check_output, compare_pq_sets, np_of, out_f32,
-                            pq_rank_values)
+from parity_helpers import (BAND, PQ_SET_NAMES, check_output, classify_pq_set_diffs, compare_pq_sets,
+                            np_of, out_f32, pq_rank_values, report_pq_set_diffs)
 
 pytestmark = pytest.mark.gpu
 GOLD = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
@@ -97,6 +97,14 @@ def pq_full_check(q, k, v, tau, invf_a, ps_a, rs_a, invf_c, n_global=32, n_local
             assert np.array_equal(gv.view(np.uint32), rv.view(np.uint32)), name
         else:
             assert np.array_equal(gv.astype(np.int64), rv.astype(np.int64)), name
+    # sets against the oracle's sets from the oracle's own bits: every differing key classified
+    ro = orc.build_sets_pq(a["votes"], a["bits"], a["wvotes"], n_global, n_local, 32, k_max, q_pos_base, mode)
+    sd = classify_pq_set_diffs(a["band"], g, dict(zip(PQ_SET_NAMES, ro)),
+                               pq_rank_values(g["votes"], g["wvotes"], mode),
+                               pq_rank_values(a["votes"], a["wvotes"], mode), N)
+    report_pq_set_diffs(what, sd)
+    if ndiff == 0 and mode == 0:
+        assert sd["keys"] == 0
     out_ref = orc.gather_attn_mask(qn, kn, vn, dt, g["idx"], g["newpos_k"], g["newpos_q"], g["mask"],
                                    invf_c.cpu().numpy(), 1.0, sm, 32, k_max, 64, q_pos_base)
     err = check_output(out_f32(r["out"]), out_ref, dt, what)

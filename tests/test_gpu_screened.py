@@ -113,3 +113,37 @@ def test_screened_pass1_full_length_config1_head():
     q, k, _ = planted_inputs(0, 1, 1, c.N, c.D, c.frac, c.dtype, DEV)
     invf, ps, rs = c.geometry()
     _check_both(q, k, torch.full((1,), c.tau), invf, ps, rs, c.tile, 0, "config 1 shape, one head")
+
+
+def test_tau_zero_keeps_each_rows_best_key():
+    """tau = 0: every valid row keeps its own maximum (qk == m passes the reference's keep test,
+    exact_2.py:121), with the screened pass 1 as with the three-product one.  The screen's row max
+    comes from fp32 dots of the (hi + lo) operands and pass 2 scores with three bf16 products, so
+    the threshold is capped just below the maximum; keys within that cap of m are band keys."""
+    import _sta_native as native
+    from synthetic import base_inv_freq, planted_inputs
+    H, N, D, tile = 2, 2000, 128, 64
+    q, k, _ = planted_inputs(12, H, H, N, D, 0.01, torch.bfloat16, DEV)
+    invf = base_inv_freq(D, 10000.0).to(DEV)
+    tau = torch.zeros(H)
+    qn, dt = np_of(q[0])
+    kn, _ = np_of(k[0])
+    a = orc.select_vote(qn, kn, dt, tau.numpy(), invf.cpu().numpy(), 0.5, 1.0, 1.0 / math.sqrt(D), tile,
+                        band_eps=BAND, want_band=True)
+    for exact in (False, True):
+        say(f"tau 0, exact_pass1={exact}")
+        old = os.environ.pop("STA_EXACT_PASS1", None)
+        try:
+            if exact:
+                os.environ["STA_EXACT_PASS1"] = "1"
+            votes, rc, rm = native.select_vote(q, k, tau, invf, 0.5, 1.0, 1.0 / math.sqrt(D), tile)
+            torch.cuda.synchronize()
+        finally:
+            os.environ.pop("STA_EXACT_PASS1", None)
+            if old is not None:
+                os.environ["STA_EXACT_PASS1"] = old
+        rc = rc.cpu().numpy()
+        assert (rc >= 1).all(), f"exact_pass1={exact}: {int((rc < 1).sum())} rows keep no key"
+        ndiff, nband = check_votes(votes.cpu().numpy(), a["votes"], a["band"])
+        print(f"[result] tau 0 exact_pass1={exact}: min row count {int(rc.min())}, vote entries "
+              f"differing {ndiff} (band pairs {nband})", flush=True)
