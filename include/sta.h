@@ -5,7 +5,8 @@
  * Plain C: device pointers, sizes and a HIP stream handle (passed as void*).  No framework
  * types.  Every entry point is asynchronous on `stream`, performs no host synchronisation and no
  * device allocation: the caller owns every output and passes one workspace buffer whose size
- * comes from sta_shared_workspace_size().  Calls that share a workspace must not overlap.
+ * comes from sta_shared_workspace_size() (sta_shared_attention_noalloc uses a fixed array inside
+ * the library instead).  Calls that share a workspace must not overlap.
  *
  * Geometry.  Kernel A (the two score passes) rotates queries and keys with the a-triple
  * (inv_freq_a, pos_scale_a, rope_scale_a); the reposition and the gather-attention use the
@@ -106,6 +107,20 @@ size_t sta_shared_workspace_size(const sta_shared_args* args);
  * shared_selection_triton_exact.py:376-423, shared_selection_triton_YaRN_exact.py:442-496 and,
  * with two geometries, shared_selection_triton_hybrid_exact.py:450-510). */
 int sta_shared_attention(const sta_shared_args* args, void* stream);
+
+/* Bytes of the fixed scratch array behind sta_shared_attention_noalloc (64 MiB per GPU). */
+#define STA_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
+
+/* sta_shared_attention without a caller workspace and without any device allocation: the
+ * workspace is a fixed device array of STA_NOALLOC_SCRATCH_BYTES inside the library, one copy
+ * per GPU, held until the process ends.  args->workspace / workspace_bytes are ignored; the
+ * caller still passes every input and output.  Shapes whose workspace
+ * (sta_shared_workspace_size) exceeds STA_NOALLOC_SCRATCH_BYTES return STA_ERR_WORKSPACE.
+ * Every call on one GPU shares that GPU's array (it keeps the last call's contents), so calls
+ * that overlap on one GPU race: serialise them on one stream.
+ * No counterpart in the reference: it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). */
+int sta_shared_attention_noalloc(const sta_shared_args* args, void* stream);
 
 /* Kernel A alone: writes votes (required), row_counts, row_max and, for a weighted
  * select_score, wvotes (optional).

@@ -17,6 +17,7 @@ _LIB = None
 STA_OK = 0
 DTYPES = {torch.float32: 0, torch.bfloat16: 1, torch.float16: 2}
 EXPORTS = ["sta_abi_version", "sta_last_error", "sta_shared_workspace_size", "sta_shared_attention",
+           "sta_shared_attention_noalloc",
            "sta_select_vote", "sta_build_sets", "sta_build_sets_weighted", "sta_gather_attention",
            "sta_pq_workspace_size", "sta_pq_attention", "sta_pq_select_bits", "sta_pq_build_sets",
            "sta_pq_gather_attention", "sta_pqstream_workspace_size", "sta_pqstream_attention",
@@ -148,7 +149,8 @@ def lib():
         L.sta_last_error.restype = ctypes.c_char_p
         L.sta_shared_workspace_size.restype = ctypes.c_size_t
         L.sta_shared_workspace_size.argtypes = [ctypes.POINTER(ShareArgs)]
-        for name in ("sta_shared_attention", "sta_select_vote", "sta_gather_attention"):
+        for name in ("sta_shared_attention", "sta_shared_attention_noalloc", "sta_select_vote",
+                     "sta_gather_attention"):
             fn = getattr(L, name)
             fn.restype = ctypes.c_int
             fn.argtypes = [ctypes.POINTER(ShareArgs), ctypes.c_void_p]
@@ -350,6 +352,31 @@ def shared_attention(q, k, v, tau, inv_freq_a, pos_scale_a, rope_scale_a, inv_fr
                       rope_scale_c, pct, sm_scale, n_global, n_local, tile, k_max, q_pos_base, measure,
                       want_votes, want_row_max, want_row_counts, select_score)
     return plan.run()
+
+
+NOALLOC_SCRATCH_BYTES = 64 << 20   # STA_NOALLOC_SCRATCH_BYTES (include/sta.h)
+
+
+def shared_attention_noalloc(q, k, v, tau, inv_freq_a, pos_scale_a, rope_scale_a, inv_freq_c,
+                             pos_scale_c, rope_scale_c, pct=30.0, sm_scale=None, n_global=32,
+                             n_local=32, tile=32, k_max=1024, q_pos_base=0, measure=False,
+                             want_votes=False, want_row_max=False, select_score="freq"):
+    """The whole prefill path through sta_shared_attention_noalloc: the library's fixed scratch
+    array replaces the workspace, so no device memory is allocated for it (the outputs still
+    are, here).  Same results as shared_attention."""
+    qh, kh, vh, tau, ifa, ifc = _prep_inputs(q, k, v, tau, inv_freq_a, inv_freq_c)
+    H, N, D = qh.shape
+    if sm_scale is None:
+        sm_scale = 1.0 / math.sqrt(D)
+    a = ShareArgs()
+    _fill_common(a, qh, kh, vh, tau, ifa, pos_scale_a, rope_scale_a, ifc, pos_scale_c, rope_scale_c,
+                 sm_scale, pct, n_global, n_local, tile, k_max, q_pos_base, measure, select_score)
+    out = _alloc_outputs(a, H, N, D, qh.dtype, tile, k_max, qh.device, want_votes, want_row_max, False,
+                         want_wvotes=want_votes and select_score != "freq")
+    a.workspace, a.workspace_bytes = None, 0
+    _check(lib().sta_shared_attention_noalloc(ctypes.byref(a), _stream(qh.device)),
+           "sta_shared_attention_noalloc")
+    return out
 
 
 def select_vote(q, k, tau, inv_freq, pos_scale, rope_scale, sm_scale, tile, q_pos_base=0,

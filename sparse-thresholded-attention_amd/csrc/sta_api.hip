@@ -3,6 +3,7 @@
 #include <stdarg.h>
 #include <stdio.h>
 #include <string.h>
+#include <mutex>
 #include <string>
 
 #include "../../include/sta.h"
@@ -237,6 +238,51 @@ int run_gather(const sta_shared_args* a, const Layout& L, hipStream_t st) {
   return STA_OK;
 }
 
+// the whole prefill path on `st`, with args->workspace holding at least L.total bytes
+int run_shared(const sta_shared_args* args, const Layout& L, hipStream_t st);
+
+int check_shared_call(const sta_shared_args* args) {
+  int rc = check_common(args);
+  if (rc != STA_OK) return rc;
+  if ((rc = check_qkv(args, true)) != STA_OK) return rc;
+  if (!args->tau || !args->inv_freq_a || !args->inv_freq_c || !args->out)
+    return fail(STA_ERR_INVALID_ARG, "tau, inv_freq_a, inv_freq_c and out must be non-NULL");
+  return check_sets_outputs(args);
+}
+
+// ------------------------------------------------------------------------------------------
+// Scratch of the allocation-free entry point: a fixed device array in this library's code
+// object, one copy per GPU, held until the process ends.  Its name is a host-side handle, not a
+// device address: the device address of each GPU's copy comes from hipGetSymbolAddress, taken
+// once per device with that device current and kept here.  Every call on one GPU shares that
+// GPU's copy, so calls that overlap on one GPU race.  Nothing in it has to start at zero: every
+// byte the kernels read is written earlier in the same call.
+// ------------------------------------------------------------------------------------------
+constexpr size_t kScratchBytes = STA_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices];
+
+int scratch_of_current_device(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+  if (dev < 0 || dev >= kMaxDevices) return fail(STA_ERR_UNSUPPORTED, "device %d above %d", dev, kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress(scratch)");
+    if (!p || ((uintptr_t)p & 255u) != 0)
+      return fail(STA_ERR_HIP, "scratch of device %d at %p is not 256-byte aligned", dev, p);
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return STA_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -251,15 +297,36 @@ size_t sta_shared_workspace_size(const sta_shared_args* args) {
 }
 
 int sta_shared_attention(const sta_shared_args* args, void* stream) {
-  int rc = check_common(args);
+  int rc = check_shared_call(args);
   if (rc != STA_OK) return rc;
-  if ((rc = check_qkv(args, true)) != STA_OK) return rc;
-  if (!args->tau || !args->inv_freq_a || !args->inv_freq_c || !args->out)
-    return fail(STA_ERR_INVALID_ARG, "tau, inv_freq_a, inv_freq_c and out must be non-NULL");
-  if ((rc = check_sets_outputs(args)) != STA_OK) return rc;
   const Layout L = layout_of(args);
   if ((rc = check_workspace(args, L)) != STA_OK) return rc;
-  hipStream_t st = (hipStream_t)stream;
+  return run_shared(args, L, (hipStream_t)stream);
+}
+
+int sta_shared_attention_noalloc(const sta_shared_args* args, void* stream) {
+  int rc = check_shared_call(args);
+  if (rc != STA_OK) return rc;
+  const Layout L = layout_of(args);
+  if (L.total > kScratchBytes)
+    return fail(STA_ERR_WORKSPACE,
+                "sta_shared_attention_noalloc: this shape needs %zu bytes of scratch, above the "
+                "library's fixed %zu (use sta_shared_attention with a caller workspace)",
+                L.total, kScratchBytes);
+  void* ws = nullptr;
+  if ((rc = scratch_of_current_device(&ws)) != STA_OK) return rc;
+  sta_shared_args a = *args;   // the same call with the library's scratch as its workspace
+  a.workspace = ws;
+  a.workspace_bytes = kScratchBytes;
+  return run_shared(&a, L, (hipStream_t)stream);
+}
+
+}  // extern "C"
+
+namespace {
+
+int run_shared(const sta_shared_args* args, const Layout& L, hipStream_t st) {
+  int rc;
   if ((rc = run_kernel_a(args, L, st)) != STA_OK) return rc;
   if ((rc = mark(args, 2, st)) != STA_OK) return rc;
   SelectArgs s = select_args_of(args, L);
@@ -277,6 +344,10 @@ int sta_shared_attention(const sta_shared_args* args, void* stream) {
   if ((rc = run_gather(args, L, st)) != STA_OK) return rc;
   return mark(args, 4, st);
 }
+
+}  // namespace
+
+extern "C" {
 
 int sta_select_vote(const sta_shared_args* args, void* stream) {
   int rc = check_common(args);
