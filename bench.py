@@ -209,6 +209,122 @@ def bench_decode(args, cfg, q, k, v, q_cpu, k_cpu, v_cpu, invf, ps, rs, tau):
     return 0
 
 
+def bench_perquery(args, cfg, q, k, v, q_cpu, k_cpu, v_cpu, invf, ps, rs, tau):
+    """Config 3 as written: every prompt position selects its own keys (threshold passers plus the
+    forced keys, capped at k_max by score, dense-rank positions) and attends them -- the per-query
+    rule of perquery.py:651-720 at every position (prefill_mode="perquery", :905-924).  Stages are
+    summed over the head groups of the plan."""
+    import _sta_native as native
+    plan = native.PerQueryPrefillPlan(q, k, v, tau, invf.to(q.device), invf.to(q.device), ps, rs,
+                                      n_global=cfg.n_global, n_local=cfg.n_local, k_max=cfg.k_max)
+    stream = torch.cuda.current_stream(q.device)
+    for _ in range(args.warmup):
+        plan.run()
+    torch.cuda.synchronize()
+    print(f"[bench] warmup done ({args.warmup} steps, {len(plan.plans)} head groups), timing {args.steps} steps",
+          file=sys.stderr, flush=True)
+    ng = len(plan.plans)
+    evs = [[[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(ng)] for _ in range(args.steps)]
+    for step in evs:
+        for grp in step:
+            for e in grp:
+                e.record(stream)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        plan.run(evs[i])
+    torch.cuda.synchronize()
+    ms_per_step = (time.perf_counter() - t0) * 1000.0 / args.steps
+    stage_ms = {s: sum(evs[i][g][j].elapsed_time(evs[i][g][j + 1]) for i in range(args.steps) for g in range(ng))
+                / args.steps for j, s in enumerate(DECODE_STAGES)}
+    r = plan.out
+    esz = q.element_size()
+    # scores: one fp32 dot of D per causal (query, key) pair; attend: each query's kept K and V
+    # rows plus its 8 B of index / position per slot, the query read and the output written
+    sflops = 2 * cfg.D * cfg.H * cfg.N * (cfg.N + 1) // 2
+    kept = r["set_size"].clamp(max=cfg.k_max).to(torch.int64)
+    abytes = int(kept.sum().item()) * (2 * cfg.D * esz + 8) + 2 * cfg.H * cfg.N * cfg.D * esz
+    s_tf = sflops / (stage_ms["scores"] * 1e-3) / 1e12
+    a_gbs = abytes / (stage_ms["attend"] * 1e-3) / 1e9
+    roof = {
+        "scores": {"kernel": "decode_score_kernel", "bound": "fp32 valu", "achieved": round(s_tf, 2),
+                   "peak": PEAK_FP32_TFLOPS, "unit": "TFLOP/s", "frac": round(s_tf / PEAK_FP32_TFLOPS, 4),
+                   "algorithmic_per_launch": sflops,
+                   "traffic": read_traffic(args.traffic_file, "decode_score_kernel")},
+        "attend": {"kernel": "decode_attend_kernel", "bound": "hbm", "achieved": round(a_gbs, 1),
+                   "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(a_gbs / PEAK_HBM_GBS, 4),
+                   "algorithmic_per_launch": abytes,
+                   "traffic": read_traffic(args.traffic_file, "decode_attend_kernel")},
+    }
+    dominant = max(("scores", "attend"), key=lambda n: stage_ms[n])
+    print(f"[bench] {ms_per_step:.3f} ms/step; stages {stage_ms}", file=sys.stderr, flush=True)
+    cpu = None
+    if args.cpu_baseline_seconds > 0:
+        print("[bench] timing the CPU oracle sample", file=sys.stderr, flush=True)
+        cpu = cpu_baseline_perquery(cfg, q_cpu, k_cpu, v_cpu, invf, ps, rs, args.cpu_baseline_seconds)
+    line = {
+        "metric": METRIC,
+        "value": round(cfg.N / (ms_per_step * 1e-3), 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": {torch.bfloat16: "bf16", torch.float16: "fp16", torch.float32: "fp32"}[q.dtype],
+        "data": "synthetic (seeded Gaussian Q/K/V with planted keys)",
+        "config": {"workload": cfg.name, "variant": cfg.variant, "heads": cfg.H, "kv_heads": cfg.Hkv,
+                   "seq_len": cfg.N, "head_dim": cfg.D, "tau": cfg.tau, "k_max": cfg.k_max,
+                   "rule": "per-query threshold + forced keys, capped at k_max by score, dense ranks",
+                   "head_groups": ng, "pos_scale": ps, "rope_scale": rs, "parallelism": "none (1 GPU)"},
+        "stages_ms": {s: round(t, 4) for s, t in stage_ms.items()},
+        "roofline": roof[dominant],
+        "rooflines": roof,
+        "selection": {"set_size_mean": round(r["set_size"].float().mean().item(), 1),
+                      "capped_queries": int(r["overflow"].sum().item()), "queries": int(r["overflow"].numel()),
+                      "usize_mean": round(r["usize"].float().mean().item(), 1)},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+def cpu_baseline_perquery(cfg, q, k, v, invf, ps, rs, budget_s):
+    """The oracle's per-query rule (scores, _decode_build_sets_pq, attend) on evenly spaced query
+    rows of one head at a time, scaled to every row of every head by the causal key count."""
+    import numpy as np
+    from oracle import sta_oracle as orc
+    sm = 1.0 / math.sqrt(cfg.D)
+    threads = orc.num_threads()
+    N = cfg.N
+    rows_done, keys_done, t_total, heads = 0, 0, 0.0, 0
+    while t_total < budget_s and heads < cfg.H:
+        h = heads
+        hk = h // (cfg.H // cfg.Hkv)
+        rows = np.linspace(0, N - 1, 64).astype(np.int64)
+        kn, dt = orc.from_torch(k[0, hk:hk + 1])
+        vn, _ = orc.from_torch(v[0, hk:hk + 1])
+        t0 = time.perf_counter()
+        for r in rows:
+            qn, _ = orc.from_torch(q[0, h:h + 1, r:r + 1])
+            s = orc.decode_scores(qn, kn[:, :r + 1], dt, invf.numpy(), ps, rs, sm, int(r))
+            idx, npk, npq, *_ = orc.decode_build_sets_pq(s, np.full(1, cfg.tau, np.float32), int(r), cfg.n_global,
+                                                         cfg.n_local, cfg.k_max)
+            orc.decode_attend(qn, kn[:, :r + 1], vn[:, :r + 1], dt, invf.numpy(), 1.0, sm, int(r), idx, npk, npq)
+        t_total += time.perf_counter() - t0
+        rows_done += len(rows)
+        keys_done += int((rows + 1).sum())
+        heads += 1
+    per_key = t_total / keys_done
+    total = per_key * cfg.H * N * (N + 1) / 2
+    return {"value": round(N / total, 3), "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"{rows_done} query rows ({heads} heads x 64 evenly spaced positions) through the CPU "
+                      f"oracle's scores, per-query selection and attend ({threads} OpenMP threads), scaled "
+                      f"to all {cfg.H} x {N} rows by their causal key counts"}
+
+
 def cpu_baseline_decode(cfg, q, k, v, invf, ps, rs, budget_s):
     """The oracle's decode (scores, selection, attend) for one query per head, all heads."""
     import numpy as np
@@ -261,6 +377,8 @@ def main():
     tau = torch.full((cfg.H,), cfg.tau)
     if cfg.variant == "decode":
         return bench_decode(args, cfg, q, k, v, q_cpu, k_cpu, v_cpu, invf, ps, rs, tau)
+    if cfg.variant == "perquery":
+        return bench_perquery(args, cfg, q, k, v, q_cpu, k_cpu, v_cpu, invf, ps, rs, tau)
     if cfg.variant == "dca":
         plan = native.DcaPlan(q, k, v, invf, cfg.dca[0], cfg.dca[1], cfg.dca[2])
     elif cfg.variant == "pqstream":

@@ -303,6 +303,20 @@ int sta_dca_attention(const sta_dca_args* args, void* stream);
 /* under the a-triple, reposition with pos_scale_c, attend under (inv_freq_c, rope_scale_c):   */
 /* PI_exact / exact / YaRN_exact pass one geometry twice, the hybrid file two.                 */
 /* ------------------------------------------------------------------------------------------ */
+/* Per-query selection rules of the decode entry points.
+ * STA_RULE_SHARED: _decode_build_sets of the shared files (shared_selection_triton_exact_2.py:
+ *   527-604): threshold passers, optional top-pct_decode%, forced global / local / self keys, the
+ *   k_max cap by score with a tie-inclusive cut, positions by the fp32 reposition recurrence.
+ * STA_RULE_PQ: _decode_build_sets_pq of the per-query file (shared_selection_triton_perquery.py:
+ *   651-720): every passer (pct_decode ignored), the forced keys, above k_max the forced keys plus
+ *   the top-(k_max - n_forced) others by score with an exact budget (equal scores at the cut
+ *   taken in ascending key order), positions = dense ranks over the final set (pos_scale_c
+ *   unused); attend with rope_scale_c = 1 and inv_freq_c = the base frequencies, as the
+ *   reference's _decode_attend_*_pq do.  Run with Q = M, q_pos0 = 0 it is the per-query prefill
+ *   (prefill_mode="perquery", perquery.py:905-924). */
+#define STA_RULE_SHARED 0
+#define STA_RULE_PQ 1
+
 typedef struct sta_decode_args {
   const void* q;            /* (H, Q, D) raw queries */
   const void* k;            /* (Hkv, M, D) raw cache */
@@ -336,6 +350,10 @@ typedef struct sta_decode_args {
   size_t workspace_bytes;
   void* const* stage_events; /* NULL or 4 hipEvent_t: before the scores, before the selection,
                                 before the attend, after it */
+  /* ABI 3: the selection rule and its per-query counters */
+  int32_t rule;             /* STA_RULE_SHARED or STA_RULE_PQ */
+  int32_t* usize;           /* (H, Q) or NULL: STA_RULE_PQ, |threshold passers| before the forced keys */
+  uint8_t* overflow;        /* (H, Q) or NULL: STA_RULE_PQ, 1 where passers U forced exceed k_max */
 } sta_decode_args;
 
 /* Bytes of device workspace the decode entry points need for these arguments. */
@@ -347,17 +365,22 @@ size_t sta_decode_workspace_size(const sta_decode_args* args);
  * 235-271, 505-525. */
 int sta_decode_scores(const sta_decode_args* args, float* scores, void* stream);
 
-/* Selection from given scores (H, Q, M): writes idx, newpos_k, newpos_q (and set_size).
- * Replaces _decode_build_sets, shared_selection_triton_exact_2.py:527-604. */
+/* Selection from given scores (H, Q, M): writes idx, newpos_k, newpos_q (and set_size; usize and
+ * overflow under STA_RULE_PQ).
+ * Replaces _decode_build_sets, shared_selection_triton_exact_2.py:527-604 (STA_RULE_SHARED), and
+ * _decode_build_sets_pq, shared_selection_triton_perquery.py:651-720 (STA_RULE_PQ). */
 int sta_decode_build_sets(const sta_decode_args* args, const float* scores, void* stream);
 
 /* Attend over idx / newpos_k / newpos_q (set_size, when non-NULL, bounds the slots swept).
  * Replaces _decode_attend_torch (causal = 0) and _decode_attend_kernelC (causal = 1),
- * shared_selection_triton_exact_2.py:608-655. */
+ * shared_selection_triton_exact_2.py:608-655; with the dense ranks of STA_RULE_PQ and
+ * rope_scale_c = 1, _decode_attend_torch_pq / _decode_attend_kernelC_pq,
+ * shared_selection_triton_perquery.py:723-778. */
 int sta_decode_attend(const sta_decode_args* args, void* stream);
 
 /* Scores, selection and attend in one call: the body of the decode branch of spi_forward,
- * shared_selection_triton_exact_2.py:734-762, for all Q queries at once. */
+ * shared_selection_triton_exact_2.py:734-762 (perquery.py:893-924 under STA_RULE_PQ), for all
+ * Q queries at once. */
 int sta_decode_attention(const sta_decode_args* args, void* stream);
 
 #ifdef __cplusplus

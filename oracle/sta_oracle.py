@@ -426,6 +426,26 @@ def decode_build_sets(scores, tau, q_pos0, pos_scale, n_global, n_local, k_max, 
     return idx, npk, npq, size
 
 
+def decode_build_sets_pq(scores, tau, q_pos0, n_global, n_local, k_max):
+    """_decode_build_sets_pq (perquery.py:651-720) from scores (H,Q,M) -> idx (H,Q,k_max) int32
+    (sentinel m_i), newpos_k (H,Q,k_max) dense ranks, newpos_q (H,Q), set_size (H,Q),
+    usize (H,Q) (|keep| before the forced keys) and overflow (H,Q) bool; equal scores at the
+    k_max cut are taken in ascending key order."""
+    scores = _c(scores, np.float32)
+    H, Q, M = scores.shape
+    idx = np.empty((H, Q, k_max), np.int32)
+    npk = np.empty((H, Q, k_max), np.float32)
+    npq = np.empty((H, Q), np.float32)
+    size = np.empty((H, Q), np.int32)
+    us = np.empty((H, Q), np.int32)
+    ov = np.empty((H, Q), np.uint8)
+    lib().oracle_decode_build_sets_pq(_p(scores), ctypes.c_int(H), ctypes.c_int(Q), ctypes.c_int(M),
+                                      _p(_c(tau, np.float32)), ctypes.c_int(q_pos0), ctypes.c_int(n_global),
+                                      ctypes.c_int(n_local), ctypes.c_int(k_max), _p(idx), _p(npk), _p(npq),
+                                      _p(size), _p(us), _p(ov))
+    return idx, npk, npq, size, us, ov.astype(bool)
+
+
 def decode_attend(q, k, v, dtype, inv_freq, rope_scale, sm_scale, q_pos0, idx, newpos_k, newpos_q,
                   causal=False):
     """Attention of each query over its slots -> (H,Q,D) fp32 before the cast to the dtype."""

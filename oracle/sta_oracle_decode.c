@@ -10,7 +10,14 @@
  *   oracle_decode_build_sets <- shared_selection_triton_exact_2.py:527-604 (_decode_build_sets)
  *   oracle_decode_attend     <- shared_selection_triton_exact_2.py:608-623 (_decode_attend_torch);
  *                               with causal != 0 the slot rule of Kernel C as
- *                               _decode_attend_kernelC runs it (:626-655, key <= q_pos)
+ *                               _decode_attend_kernelC runs it (:626-655, key <= q_pos); with
+ *                               rope_scale 1 and the dense ranks of the per-query rule it is
+ *                               shared_selection_triton_perquery.py:723-740 (_decode_attend_torch_pq)
+ *                               and :743-778 (_decode_attend_kernelC_pq)
+ *   oracle_decode_build_sets_pq <- shared_selection_triton_perquery.py:651-720
+ *                               (_decode_build_sets_pq): no top-pct cut, the k_max cap as forced +
+ *                               the top-(k_max - n_forced) non-forced keys by score with an exact
+ *                               budget, dense-rank positions
  *
  * A batch of Q queries shares one cache of M keys: query i sits at position q_pos0 + i and sees
  * the keys [0, m_i), m_i = M - (Q - 1 - i) -- the cache prefix K[:, :P + 1] that spi_forward's
@@ -249,5 +256,107 @@ void oracle_decode_attend(const void* q, const void* k, const void* v, int dtype
     free(kr);
     free(sc);
     free(acc);
+  }
+}
+
+/* (score, key) pairs in descending score, ties in ascending key order */
+typedef struct {
+  float s;
+  int j;
+} scored_key;
+
+static int cmp_scored_desc(const void* a, const void* b) {
+  const scored_key* x = (const scored_key*)a;
+  const scored_key* y = (const scored_key*)b;
+  if (x->s != y->s) return (x->s < y->s) - (x->s > y->s);
+  return (x->j > y->j) - (x->j < y->j);
+}
+
+/*
+ * _decode_build_sets_pq (shared_selection_triton_perquery.py:651-720) from given scores (H, Q, M),
+ * batched like oracle_decode_build_sets (query i at q_pos0 + i over the keys [0, m_i)).
+ *   thr = fl(max - tau); keep = s >= thr                                   (:676-677)
+ *   forced = global [0, n_global) U local [q_pos - n_local + 1, q_pos] U self (:679-683)
+ *   usize = |keep|, over = |keep U forced| > k_max                         (:686-688)
+ *   over: forced U the top-(k_max - n_forced) non-forced kept keys by score (:690-701); the
+ *   reference takes them with torch.topk, whose order among equal scores is unspecified: here
+ *   equal scores at the cut are taken in ascending key order
+ *   positions: dense ranks over the final set (rank0 = cumsum - 1), newpos_q = rank0[q_pos]
+ *   (:703-719); idx ascending, first k_max, sentinel m_i, newpos_k 0 at sentinels.
+ * set_size = |final set|; usize and overflow are the reference's measurement counters
+ * (_ovf_accumulate(over, usize, "decode"), :688); each output pointer may be NULL.
+ */
+void oracle_decode_build_sets_pq(const float* scores, int H, int Q, int M, const float* tau, int q_pos0,
+                                 int n_global, int n_local, int k_max, int32_t* idx, float* newpos_k,
+                                 float* newpos_q, int32_t* set_size, int32_t* usize, uint8_t* overflow) {
+#pragma omp parallel
+  {
+    scored_key* cand = (scored_key*)malloc(sizeof(scored_key) * (size_t)M);
+    uint8_t* fin = (uint8_t*)malloc((size_t)M);
+    uint8_t* forced = (uint8_t*)malloc((size_t)M);
+    int32_t* rank0 = (int32_t*)malloc(sizeof(int32_t) * (size_t)M);
+#pragma omp for schedule(dynamic, 1)
+    for (int hi = 0; hi < H * Q; ++hi) {
+      const int h = hi / Q, i = hi % Q;
+      const int m = M - (Q - 1 - i);
+      const int p = q_pos0 + i;
+      const float* s = scores + ((size_t)h * Q + i) * M;
+      float mx = -INFINITY;
+      for (int j = 0; j < m; ++j) mx = s[j] > mx ? s[j] : mx;
+      volatile float thr = mx - tau[h];
+      const int g = n_global < m ? n_global : m;
+      int lo = p - n_local + 1;
+      if (lo < 0) lo = 0;
+      int n_forced = 0, n_keep = 0, count = 0;
+      for (int j = 0; j < m; ++j) {
+        forced[j] = (uint8_t)(j < g || (j >= lo && j <= p) || j == p);
+        const int keep = s[j] >= thr;
+        n_forced += forced[j];
+        n_keep += keep;
+        fin[j] = (uint8_t)(keep || forced[j]);
+        count += fin[j];
+      }
+      const int over = count > k_max;
+      if (over) {
+        const int budget = k_max - n_forced > 0 ? k_max - n_forced : 0;
+        int nc = 0;
+        for (int j = 0; j < m; ++j)
+          if (fin[j] && !forced[j]) {
+            cand[nc].s = s[j];
+            cand[nc].j = j;
+            ++nc;
+          }
+        qsort(cand, (size_t)nc, sizeof(scored_key), cmp_scored_desc);
+        for (int j = 0; j < m; ++j) fin[j] = forced[j];
+        for (int c = 0; c < nc && c < budget; ++c) fin[cand[c].j] = 1;
+      }
+      int rank = -1, total = 0;
+      for (int j = 0; j < m; ++j) {
+        if (fin[j]) rank += 1;
+        rank0[j] = rank;
+        total += fin[j];
+      }
+      int32_t* irow = idx + ((size_t)h * Q + i) * k_max;
+      float* nrow = newpos_k + ((size_t)h * Q + i) * k_max;
+      int r = 0;
+      for (int j = 0; j < m && r < k_max; ++j)
+        if (fin[j]) {
+          irow[r] = j;
+          nrow[r] = (float)rank0[j];
+          ++r;
+        }
+      for (; r < k_max; ++r) {
+        irow[r] = m;
+        nrow[r] = 0.0f;
+      }
+      newpos_q[(size_t)h * Q + i] = (float)rank0[p];
+      if (set_size) set_size[(size_t)h * Q + i] = total;
+      if (usize) usize[(size_t)h * Q + i] = n_keep;
+      if (overflow) overflow[(size_t)h * Q + i] = (uint8_t)over;
+    }
+    free(cand);
+    free(fin);
+    free(forced);
+    free(rank0);
   }
 }

@@ -152,3 +152,97 @@ def spi_forward(self, hidden_states, position_embeddings=None, attention_mask=No
 
     attn_output = out.transpose(1, 2).reshape(B, N, -1).contiguous()
     return self.o_proj(attn_output), None
+
+
+# ---------------------------------------------------------------------------------------------
+# the per-query file's model integration (shared_selection_triton_perquery.py:784-930)
+# ---------------------------------------------------------------------------------------------
+def install_perquery(model, select_geom, apply_mscale, context_window, n_global, n_local, tile, k_max,
+                     max_len, decode_backend, prefill_mode, select_score, block_n=32, block_k=32):
+    """Selection under select_geom ("pi": base frequencies, compressed positions; "yarn": the
+    rotary frequencies as loaded, raw positions, attention scaling as the rope scale when
+    apply_mscale); attention under base RoPE at dense ranks, scale 1 (perquery.py:800-852)."""
+    import transformers.models.llama.modeling_llama as ml
+    rotary = model.model.rotary_emb
+    inv_freq_rot = rotary.inv_freq.detach().float()
+    attn_scaling = float(getattr(rotary, "attention_scaling", 1.0))
+    inv_freq_base = base_inv_freq_of(model)
+    if select_geom == "yarn":
+        inv_freq_a, rope_scale_a = inv_freq_rot, (attn_scaling if apply_mscale else 1.0)
+    else:
+        inv_freq_a, rope_scale_a = inv_freq_base, 1.0
+    assert inv_freq_base.numel() == inv_freq_a.numel(), \
+        f"inv_freq length mismatch: {inv_freq_base.numel()} vs {inv_freq_a.numel()}"
+    for li, layer in enumerate(model.model.layers):
+        sa = layer.self_attn
+        dev = sa.q_proj.weight.device
+        sa.spi_inv_freq_a = inv_freq_a.to(dev)
+        sa.spi_rope_scale_a = rope_scale_a
+        sa.spi_inv_freq_c = inv_freq_base.to(dev)
+        sa.spi_geom = select_geom
+        sa.spi_W = context_window
+        sa.spi_ng = n_global
+        sa.spi_nl = n_local
+        sa.spi_tile = tile
+        sa.spi_kmax = k_max
+        sa.spi_block_n = block_n
+        sa.spi_block_k = block_k
+        sa.spi_layer_idx = getattr(sa, "layer_idx", li)
+        sa.spi_max_len = max_len
+        sa.spi_pos_scale_a = None
+        sa.spi_select_score = select_score
+        sa.spi_decode_backend = decode_backend
+        sa.spi_prefill_mode = prefill_mode
+    ml.LlamaAttention.forward = pq_forward
+
+
+def pq_forward(self, hidden_states, position_embeddings=None, attention_mask=None, past_key_values=None,
+               **kwargs):
+    import shared_selection_triton_perquery as pqm
+    B, N, _ = hidden_states.shape
+    assert B == 1, "batch size must be 1 (the kernels take one sequence, as the reference's)"
+    hs = (B, N, -1, self.head_dim)
+    q = self.q_proj(hidden_states).view(hs).transpose(1, 2)
+    k = self.k_proj(hidden_states).view(hs).transpose(1, 2)
+    v = self.v_proj(hidden_states).view(hs).transpose(1, 2)
+    cache = past_key_values if past_key_values is not None else kwargs.get("past_key_value", None)
+    past_len = 0
+    if cache is not None:
+        try:
+            past_len = int(cache.get_seq_length(self.spi_layer_idx))
+        except TypeError:
+            past_len = int(cache.get_seq_length())
+        k, v = cache.update(k, v, self.spi_layer_idx)
+    # the selection's pos_scale, frozen at prefill: pi -> min(1, W / L), yarn -> raw positions
+    if past_len == 0:
+        if self.spi_geom == "yarn":
+            self.spi_pos_scale_a = 1.0
+        else:
+            L_target = self.spi_max_len if self.spi_max_len is not None else N
+            self.spi_pos_scale_a = min(1.0, self.spi_W / float(L_target))
+    if past_len == 0 and self.spi_prefill_mode == "shared":
+        out, usize, kept_size, overflow = pqm.shared_pq_attention(
+            q, k, v, self.tau_head_vec, self.spi_inv_freq_a, self.spi_inv_freq_c,
+            pos_scale_a=self.spi_pos_scale_a, rope_scale_a=self.spi_rope_scale_a, sm_scale=self.scaling,
+            n_global=self.spi_ng, n_local=self.spi_nl, tile=self.spi_tile, k_max=self.spi_kmax,
+            q_pos_base=past_len, select_score=self.spi_select_score)
+        self.spi_last_usize = usize.detach()
+        self.spi_last_kept = kept_size.detach()
+        self.spi_last_overflow = overflow.detach()
+    else:
+        # each query at position past_len + i over the keys [0, past_len + i], per-query rule
+        causal = self.spi_decode_backend == "triton"
+        outs = []
+        for c0 in range(0, N, PER_QUERY_BATCH):
+            c1 = min(N, c0 + PER_QUERY_BATCH)
+            M = past_len + c1
+            st = {}
+            outs.append(decode_attention(
+                q[0, :, c0:c1, :], k[:, :, :M, :], v[:, :, :M, :], self.tau_head_vec, self.spi_inv_freq_a,
+                past_len + c0, self.spi_pos_scale_a, self.spi_rope_scale_a, self.scaling, self.spi_ng, self.spi_nl,
+                self.spi_kmax, 100.0, causal, inv_freq_c=self.spi_inv_freq_c, pos_scale_c=1.0, rope_scale_c=1.0,
+                rule="pq", stats=st))
+            pqm._record(st["overflow"], st["usize"], phase="decode")
+        out = torch.cat(outs, dim=1).unsqueeze(0)
+    attn_output = out.transpose(1, 2).reshape(B, N, -1).contiguous()
+    return self.o_proj(attn_output), None

@@ -134,7 +134,11 @@ class DecodeArgsC(ctypes.Structure):
         ("newpos_q", ctypes.c_void_p), ("set_size", ctypes.c_void_p), ("scores", ctypes.c_void_p),
         ("workspace", ctypes.c_void_p), ("workspace_bytes", ctypes.c_size_t),
         ("stage_events", ctypes.c_void_p),
+        ("rule", ctypes.c_int32), ("usize", ctypes.c_void_p), ("overflow", ctypes.c_void_p),
     ]
+
+
+RULES = {"shared": 0, "pq": 1}    # STA_RULE_SHARED / STA_RULE_PQ
 
 
 def lib():
@@ -187,7 +191,7 @@ def lib():
             fn = getattr(L, name)
             fn.restype = ctypes.c_int
             fn.argtypes = [ctypes.POINTER(DecodeArgsC), ctypes.c_void_p, ctypes.c_void_p]
-        if L.sta_abi_version() != 2:
+        if L.sta_abi_version() != 3:
             raise ImportError("libsta_hip.so ABI version mismatch")
         _LIB = L
     return _LIB
@@ -775,9 +779,12 @@ class DecodePlan:
 
     def __init__(self, q, k, v, tau, inv_freq, q_pos0, pos_scale=1.0, rope_scale=1.0, sm_scale=None,
                  n_global=32, n_local=32, k_max=1024, pct_decode=100.0, causal=False, want_scores=False,
-                 inv_freq_c=None, pos_scale_c=None, rope_scale_c=None):
+                 inv_freq_c=None, pos_scale_c=None, rope_scale_c=None, rule="shared"):
         """inv_freq / pos_scale / rope_scale: the selection geometry; the *_c triple (default: the
-        same) repositions (pos_scale_c) and attends (inv_freq_c, rope_scale_c)."""
+        same) repositions (pos_scale_c) and attends (inv_freq_c, rope_scale_c).  rule "shared" is
+        _decode_build_sets (exact_2.py:527-604), "pq" _decode_build_sets_pq (perquery.py:651-720:
+        dense ranks, exact cap budget; pass rope_scale_c=1 and the base inv_freq_c); "pq" also
+        fills usize and overflow (H, Q)."""
         if not q.is_cuda:
             raise RuntimeError("sparse-thresholded attention runs on a HIP device only; got a CPU tensor")
         if q.dtype not in DTYPES:
@@ -814,6 +821,7 @@ class DecodePlan:
         a.pos_scale_c, a.rope_scale_c = float(pos_scale_c), float(rope_scale_c)
         a.q_pos0, a.n_global, a.n_local, a.k_max = int(q_pos0), int(n_global), int(n_local), int(k_max)
         a.pct_decode, a.causal = float(pct_decode), int(bool(causal))
+        a.rule = RULES[rule]
         self._keep = (qh, kh, vh, tau, ifr, ifc)
         self.out = {
             "out": torch.empty((H, Q, D), dtype=qh.dtype, device=dev),
@@ -824,9 +832,13 @@ class DecodePlan:
         }
         if want_scores:
             self.out["scores"] = torch.empty((H, Q, M), dtype=torch.float32, device=dev)
+        if rule == "pq":
+            self.out["usize"] = torch.empty((H, Q), dtype=torch.int32, device=dev)
+            self.out["overflow"] = torch.empty((H, Q), dtype=torch.bool, device=dev)
         for name in ("out", "idx", "newpos_k", "newpos_q", "set_size"):
             setattr(a, name, _ptr(self.out[name]))
         a.scores = _ptr(self.out.get("scores"))
+        a.usize, a.overflow = _ptr(self.out.get("usize")), _ptr(self.out.get("overflow"))
         n = lib().sta_decode_workspace_size(ctypes.byref(a))
         if n == 0:
             _check(-1, "sta_decode_workspace_size")
@@ -871,9 +883,112 @@ class DecodePlan:
 
 def decode_attention(q, k, v, tau, inv_freq, q_pos0, pos_scale=1.0, rope_scale=1.0, sm_scale=None,
                      n_global=32, n_local=32, k_max=1024, pct_decode=100.0, causal=False, want_scores=False,
-                     inv_freq_c=None, pos_scale_c=None, rope_scale_c=None):
+                     inv_freq_c=None, pos_scale_c=None, rope_scale_c=None, rule="shared"):
     """Scores, selection and attend of Q queries (H, Q, D) over the cache k, v (Hkv, M, D).
     Returns a dict of device tensors: out (H, Q, D), idx (H, Q, k_max) int32 (sentinel m_i),
-    newpos_k, newpos_q, set_size and, with want_scores, scores (H, Q, M)."""
+    newpos_k, newpos_q, set_size, with want_scores scores (H, Q, M), and under rule "pq" usize
+    and overflow (H, Q)."""
     return DecodePlan(q, k, v, tau, inv_freq, q_pos0, pos_scale, rope_scale, sm_scale, n_global, n_local,
-                      k_max, pct_decode, causal, want_scores, inv_freq_c, pos_scale_c, rope_scale_c).run()
+                      k_max, pct_decode, causal, want_scores, inv_freq_c, pos_scale_c, rope_scale_c,
+                      rule).run()
+
+
+class PerQueryPrefillPlan:
+    """The per-query prefill (perquery.py:905-924, prefill_mode="perquery"): every position P of
+    the N prompt tokens selects its own set over the keys [0, P] by the per-query rule and attends
+    it.  Runs as the batched decode path with Q = M = N, q_pos0 = 0, over groups of heads so that
+    the per-query score rows (heads x N x N fp32) stay bounded; outputs and one workspace are
+    allocated once and run() allocates nothing.
+
+    Outputs: out (H, N, D) in the input dtype; set_size, usize (H, N) int32 and overflow (H, N)
+    bool per query.  The per-group idx / newpos buffers are reused from group to group."""
+
+    def __init__(self, q, k, v, tau, inv_freq_a, inv_freq_c, pos_scale_a=1.0, rope_scale_a=1.0,
+                 sm_scale=None, n_global=32, n_local=32, k_max=4096, heads_per_group=None,
+                 score_bytes_budget=2 << 30):
+        qh = _heads_view(q)
+        kh = _heads_view(k.to(qh.device))
+        vh = _heads_view(v.to(qh.device))
+        H, N, D = qh.shape
+        Hkv = kh.shape[0]
+        G = H // Hkv
+        dev = qh.device
+        if heads_per_group is None:
+            # whole kv groups, as many as the score budget allows
+            per_head = N * N * 4
+            heads_per_group = max(G, (score_bytes_budget // per_head) // G * G)
+        hg = min(H, heads_per_group)
+        if hg % G:
+            raise ValueError(f"heads_per_group={hg} must be a multiple of the GQA group {G}")
+        if sm_scale is None:
+            sm_scale = 1.0 / math.sqrt(D)
+        tau = tau.to(device=dev, dtype=torch.float32).reshape(-1).contiguous()
+        if tau.numel() == 1 and H > 1:
+            tau = tau.expand(H).contiguous()
+        self.device = dev
+        self.out = {
+            "out": torch.empty((H, N, D), dtype=qh.dtype, device=dev),
+            "set_size": torch.empty((H, N), dtype=torch.int32, device=dev),
+            "usize": torch.empty((H, N), dtype=torch.int32, device=dev),
+            "overflow": torch.empty((H, N), dtype=torch.bool, device=dev),
+        }
+        self._idx = torch.empty((hg, N, k_max), dtype=torch.int32, device=dev)
+        self._npk = torch.empty((hg, N, k_max), dtype=torch.float32, device=dev)
+        self._npq = torch.empty((hg, N), dtype=torch.float32, device=dev)
+        self._keep = (qh, kh, vh, tau)
+        self.plans = []
+        ws = None
+        for h0 in range(0, H, hg):
+            h1 = min(H, h0 + hg)
+            p = DecodePlan.__new__(DecodePlan)
+            p.device = dev
+            p._events = None
+            a = p.args = DecodeArgsC()
+            a.q, a.k, a.v = _ptr(qh[h0:h1]), _ptr(kh[h0 // G:h1 // G]), _ptr(vh[h0 // G:h1 // G])
+            a.q_head_stride, a.q_tok_stride = qh.stride(0), qh.stride(1)
+            a.k_head_stride, a.k_tok_stride = kh.stride(0), kh.stride(1)
+            a.v_head_stride, a.v_tok_stride = vh.stride(0), vh.stride(1)
+            a.dtype = DTYPES[qh.dtype]
+            a.H, a.Hkv, a.Q, a.M, a.D = h1 - h0, (h1 - h0) // G, N, N, D
+            a.tau = _ptr(tau[h0:h1])
+            a.inv_freq_a = _ptr(inv_freq_a)
+            a.inv_freq_c = _ptr(inv_freq_c)
+            a.pos_scale_a, a.rope_scale_a, a.sm_scale = float(pos_scale_a), float(rope_scale_a), float(sm_scale)
+            a.pos_scale_c, a.rope_scale_c = 1.0, 1.0
+            a.q_pos0, a.n_global, a.n_local, a.k_max = 0, int(n_global), int(n_local), int(k_max)
+            a.pct_decode, a.causal, a.rule = 100.0, 0, RULES["pq"]
+            a.out = _ptr(self.out["out"][h0:h1])
+            a.idx, a.newpos_k, a.newpos_q = _ptr(self._idx), _ptr(self._npk), _ptr(self._npq)
+            a.set_size = _ptr(self.out["set_size"][h0:h1])
+            a.usize = _ptr(self.out["usize"][h0:h1])
+            a.overflow = _ptr(self.out["overflow"][h0:h1])
+            n = lib().sta_decode_workspace_size(ctypes.byref(a))
+            if n == 0:
+                _check(-1, "sta_decode_workspace_size")
+            if ws is None or ws.numel() < n:
+                ws = torch.empty(n, dtype=torch.uint8, device=dev)
+            self.plans.append(p)
+        for p in self.plans:
+            p.args.workspace, p.args.workspace_bytes = _ptr(ws), ws.numel()
+        self.workspace = ws
+        self._keep = self._keep + (inv_freq_a, inv_freq_c)
+
+    def run(self, events=None):
+        """events: None or one list of 4 recorded events per head group (len(self.plans)),
+        marking that group's scores, selection and attend."""
+        for i, p in enumerate(self.plans):
+            p.args.stage_events = None
+            if events is not None:
+                p._events = (ctypes.c_void_p * 4)(*[e.cuda_event for e in events[i]])
+                p.args.stage_events = ctypes.cast(p._events, ctypes.c_void_p)
+            _check(lib().sta_decode_attention(ctypes.byref(p.args), _stream(self.device)), "sta_decode_attention")
+        return self.out
+
+
+def perquery_prefill_attention(q, k, v, tau, inv_freq_a, inv_freq_c, pos_scale_a=1.0, rope_scale_a=1.0,
+                               sm_scale=None, n_global=32, n_local=32, k_max=4096, heads_per_group=None):
+    """Per-query prefill of (1, H, N, D) inputs; returns the PerQueryPrefillPlan's outputs."""
+    ia = inv_freq_a.to(device=q.device, dtype=torch.float32).contiguous()
+    ic = inv_freq_c.to(device=q.device, dtype=torch.float32).contiguous()
+    return PerQueryPrefillPlan(q, k, v, tau, ia, ic, pos_scale_a, rope_scale_a, sm_scale, n_global, n_local,
+                               k_max, heads_per_group).run()

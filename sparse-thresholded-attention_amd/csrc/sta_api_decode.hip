@@ -10,14 +10,23 @@ using namespace sta_api;
 
 namespace {
 
+// batches of at least this many queries take their scores from the matrix cores (RoPE fragments +
+// score_rows_kernel); smaller ones from the decode score kernel's fp32 dots
+constexpr int ROWS_MIN_Q = 64;
+
 struct DecLayout {
   int nsplit;
-  size_t qrot_off, scores_off, keys_off, size_off, part_off, total;
+  bool rows;                                          // scores through the fragments
+  int q_rows_pad, k_rows_pad;
+  size_t qrot_off, scores_off, keys_off, size_off, part_off, qfrag_off, kfrag_off, total;
 };
 
 DecLayout dec_layout_of(const sta_decode_args* a) {
   DecLayout L;
   L.nsplit = decode_nsplit(a->k_max);
+  L.rows = a->Q >= ROWS_MIN_Q;
+  L.q_rows_pad = (a->Q + 31) / 32 * 32;
+  L.k_rows_pad = (a->M + 31) / 32 * 32;
   const size_t hq = (size_t)a->H * a->Q;
   size_t off = 0;
   L.qrot_off = off;                                   // rotated queries (H, Q, D) fp32
@@ -30,6 +39,12 @@ DecLayout dec_layout_of(const sta_decode_args* a) {
   off = align256(off + hq * 4);
   L.part_off = off;                                   // attend split states
   off = align256(off + hq * L.nsplit * (a->D + 2) * 4);
+  L.qfrag_off = L.kfrag_off = off;                    // rotated hi / lo fragments (rows mode)
+  if (L.rows) {
+    off = align256(off + frag_region_bytes(a->H, L.q_rows_pad, a->D));
+    L.kfrag_off = off;
+    off = align256(off + frag_region_bytes(a->Hkv, L.k_rows_pad, a->D));
+  }
   L.total = off;
   return L;
 }
@@ -52,6 +67,11 @@ int dec_check(const sta_decode_args* a, bool need_pos = true) {
   if (a->n_global < 0 || a->n_local < 0)
     return fail(STA_ERR_UNSUPPORTED, "n_global=%d / n_local=%d must be >= 0", a->n_global, a->n_local);
   if ((size_t)a->H * a->Q >= (1u << 31)) return fail(STA_ERR_INVALID_ARG, "H * Q too large");
+  if (a->rule != STA_RULE_SHARED && a->rule != STA_RULE_PQ)
+    return fail(STA_ERR_INVALID_ARG, "rule %d is not STA_RULE_SHARED or STA_RULE_PQ", a->rule);
+  if (a->rule == STA_RULE_PQ && (int64_t)a->n_global + a->n_local > a->k_max)
+    return fail(STA_ERR_INVALID_ARG, "per-query rule: n_global (%d) + n_local (%d) exceeds k_max (%d)",
+                a->n_global, a->n_local, a->k_max);
   return STA_OK;
 }
 
@@ -91,7 +111,11 @@ DecodeArgs dec_args_of(const sta_decode_args* a, const DecLayout& L) {
   d.n_global = a->n_global;
   d.n_local = a->n_local;
   d.k_max = a->k_max;
-  d.use_pct = a->pct_decode < 100.0;                              // exact_2.py:559
+  d.rule = a->rule;
+  d.usize = a->rule == STA_RULE_PQ ? a->usize : nullptr;
+  d.overflow = a->rule == STA_RULE_PQ ? a->overflow : nullptr;
+  // the per-query rule keeps every passer (perquery.py:651-720 has no top-pct cut)
+  d.use_pct = a->rule == STA_RULE_SHARED && a->pct_decode < 100.0;   // exact_2.py:559
   d.pct_frac = (float)(a->pct_decode / 100.0);                    // the float32 scalar of :561
   d.scores = a->scores ? a->scores : (float*)(ws + L.scores_off);
   d.keys = decode_select_in_lds(a->M) ? nullptr : (uint32_t*)(ws + L.keys_off);
@@ -113,8 +137,36 @@ int dec_scores(const sta_decode_args* a, const DecLayout& L, DecodeArgs d, float
   if (!a->inv_freq_a) return fail(STA_ERR_INVALID_ARG, "inv_freq_a must be non-NULL");
   if (!scores) return fail(STA_ERR_INVALID_ARG, "scores must be non-NULL");
   d.scores = scores;
-  hipError_t e = launch_decode_scores(a->dtype, a->D, d, (float*)((char*)a->workspace + L.qrot_off), st);
-  return e == hipSuccess ? STA_OK : hip_fail(e, "decode scores");
+  if (!L.rows) {
+    hipError_t e = launch_decode_scores(a->dtype, a->D, d, (float*)((char*)a->workspace + L.qrot_off), st);
+    return e == hipSuccess ? STA_OK : hip_fail(e, "decode scores");
+  }
+  // a batch of queries: rotate queries (at q_pos0 + i) and keys once into hi / lo fragments under
+  // the selection geometry, then one matrix product per head
+  char* ws = (char*)a->workspace;
+  u32x4* qfrag = (u32x4*)(ws + L.qfrag_off);
+  u32x4* kfrag = (u32x4*)(ws + L.kfrag_off);
+  hipError_t e = launch_rope_frag(a->dtype, a->D, a->q, a->q_head_stride, a->q_tok_stride, a->H, a->Q,
+                                  L.q_rows_pad, a->q_pos0, a->pos_scale_a, a->rope_scale_a, a->inv_freq_a,
+                                  qfrag, st);
+  if (e != hipSuccess) return hip_fail(e, "decode scores: rope pre-kernel (q)");
+  e = launch_rope_frag(a->dtype, a->D, a->k, a->k_head_stride, a->k_tok_stride, a->Hkv, a->M, L.k_rows_pad, 0,
+                       a->pos_scale_a, a->rope_scale_a, a->inv_freq_a, kfrag, st);
+  if (e != hipSuccess) return hip_fail(e, "decode scores: rope pre-kernel (k)");
+  RowsArgs r{};
+  r.qfrag = qfrag;
+  r.kfrag = kfrag;
+  r.H = a->H;
+  r.Hkv = a->Hkv;
+  r.Q = a->Q;
+  r.M = a->M;
+  r.q_pos0 = a->q_pos0;
+  r.q_rows_pad = L.q_rows_pad;
+  r.k_rows_pad = L.k_rows_pad;
+  r.sm_scale = a->sm_scale;
+  r.scores = scores;
+  e = launch_score_rows(a->D, r, st);
+  return e == hipSuccess ? STA_OK : hip_fail(e, "decode scores: score rows");
 }
 
 int dec_select(const sta_decode_args* a, DecodeArgs d, const float* scores, hipStream_t st) {

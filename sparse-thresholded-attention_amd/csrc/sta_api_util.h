@@ -32,7 +32,7 @@ int check_qkv_ptrs(int dtype, const void* q, const void* k, const void* v, const
 
 // record stage event i on st when events were given
 inline int mark_event(void* const* events, int i, hipStream_t st) {
-  if (!events) return STA_OK;
+  if (!events || !events[i]) return STA_OK;   // a NULL entry skips that mark
   hipError_t e = hipEventRecord((hipEvent_t)events[i], st);
   return e == hipSuccess ? STA_OK : hip_fail(e, "stage event record");
 }

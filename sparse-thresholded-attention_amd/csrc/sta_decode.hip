@@ -483,9 +483,21 @@ __global__ __launch_bounds__(DEC_SEL_NT) void decode_select_kernel(DecodeArgs a)
     count = ge + dsum(c, tmp);
   }
 
-  // ---- cap by score over the non-forced keys (exact_2.py:571-585) ----
+  // the per-query rule's measurement counters: |passers| and the overflow flag (perquery.py:686-688)
+  const bool pq = a.rule == 1;
+  if (pq && tid == 0) {
+    if (a.usize) a.usize[hi] = ge;
+    if (a.overflow) a.overflow[hi] = count > a.k_max ? 1 : 0;
+  }
+
+  // ---- cap by score over the non-forced keys (exact_2.py:571-585; perquery.py:690-701) ----
   uint32_t fin_thr = kp_thr;
   bool only_forced = false;
+  // per-query rule: an exact budget (torch.topk, perquery.py:695-698) -- every key above the cut
+  // and, of the keys equal to it, the first `quota` in key order; tie_base = this thread's first
+  // tie index
+  bool exact_cut = false;
+  int quota = 0, tie_base = 0;
   if (count > a.k_max) {
     const int budget_c = a.k_max - nforced;
     if (budget_c <= 0) {
@@ -500,42 +512,63 @@ __global__ __launch_bounds__(DEC_SEL_NT) void decode_select_kernel(DecodeArgs a)
       }
       __syncthreads();
       fin_thr = kth(budget_c).x;
+      if (pq) {
+        int c = 0, t = 0;
+        for (int e = 0; e < j1 - j0; ++e) {
+          c += myrow[e] > fin_thr;
+          t += myrow[e] == fin_thr;
+        }
+        quota = budget_c - dsum(c, tmp);
+        tie_base = dexcl_sum(t, tmp);
+        exact_cut = true;
+      }
     }
   }
-  auto final_j = [&](int j, uint32_t k) {
-    return j < g || (j >= lo && j <= p) || (!only_forced && k >= fin_thr);
+  // tie: the running index of this thread's keys equal to the cut (advanced in key order)
+  auto final_j = [&](int j, uint32_t k, int& tie) {
+    if (j < g || (j >= lo && j <= p)) return true;
+    if (only_forced) return false;
+    if (!exact_cut) return k >= fin_thr;
+    if (k == fin_thr) return tie++ < quota;
+    return k > fin_thr;
   };
 
-  // ---- compaction + reposition (exact_2.py:587-603) ----
+  // ---- compaction + reposition (exact_2.py:587-603); dense ranks (perquery.py:703-719) ----
   int cnt = 0;
-  for (int e = 0; e < j1 - j0; ++e) cnt += final_j(j0 + e, myrow[e]);
+  {
+    int tie = tie_base;
+    for (int e = 0; e < j1 - j0; ++e) cnt += final_j(j0 + e, myrow[e], tie);
+  }
   int total;
   const int base = dexcl_sum(cnt, tmp, &total);
   float mloc = -INFINITY;
-  {
-    int rank = base - 1;
+  if (!pq) {
+    int rank = base - 1, tie = tie_base;
     for (int e = 0; e < j1 - j0; ++e) {
-      if (final_j(j0 + e, myrow[e])) {
+      if (final_j(j0 + e, myrow[e], tie)) {
         rank += 1;
         const float cp = (float)(j0 + e) * a.pos_scale_c;                  // exact_2.py:590
         mloc = fmaxf(mloc, cp - (float)rank);                            // :591
       }
     }
   }
-  float run = dexcl_max(mloc, (float*)tmp);
+  float run = pq ? 0.0f : dexcl_max(mloc, (float*)tmp);
   int32_t* irow = a.idx + (int64_t)hi * a.k_max;
   float* nrow = a.newpos_k + (int64_t)hi * a.k_max;
   {
-    int rank = base - 1;
+    int rank = base - 1, tie = tie_base;
     for (int e = 0; e < j1 - j0; ++e) {
       const int j = j0 + e;
-      const bool f = final_j(j, myrow[e]);
+      const bool f = final_j(j, myrow[e], tie);
       if (f) {
         rank += 1;
-        const float cp = (float)j * a.pos_scale_c;
-        run = fmaxf(run, cp - (float)rank);
+        if (!pq) {
+          const float cp = (float)j * a.pos_scale_c;
+          run = fmaxf(run, cp - (float)rank);
+        }
       }
-      const float np = (float)rank + run;                                // exact_2.py:592
+      // the shared rule's reposition (exact_2.py:592), or the dense rank itself (perquery.py:707)
+      const float np = pq ? (float)rank : (float)rank + run;
       if (f && rank < a.k_max) {
         irow[rank] = j;
         nrow[rank] = np;

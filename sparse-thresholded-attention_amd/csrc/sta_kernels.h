@@ -167,7 +167,21 @@ struct DecodeArgs {
   float* part;            // (H * Q, nsplit, D + 2) split states of the attend
   const float* qrot;      // (H, Q, D) rotated queries, or null (the score kernel rotates them)
   void* out;              // (H, Q, D)
+  int rule;               // 0: _decode_build_sets (shared files); 1: _decode_build_sets_pq
+  int32_t* usize;         // (H, Q) or null: rule 1, |threshold passers|
+  uint8_t* overflow;      // (H, Q) or null: rule 1, passers U forced above k_max
 };
+
+// scores of a batch of queries from the RoPE pre-kernel's fragments (matrix cores)
+struct RowsArgs {
+  const u32x4* qfrag;     // (H, q_rows_pad) query fragments, rows at positions q_pos0 + i
+  const u32x4* kfrag;     // (Hkv, k_rows_pad) key fragments, rows at positions 0 ..
+  int H, Hkv, Q, M, q_pos0;
+  int q_rows_pad, k_rows_pad;   // multiples of 32; k_rows_pad >= M
+  float sm_scale;
+  float* scores;          // (H, Q, M): row i written for its keys [0, M - (Q - 1 - i))
+};
+hipError_t launch_score_rows(int D, const RowsArgs& a, hipStream_t st);
 
 // qrot: workspace of (H, Q, D) floats, used when a workgroup's query rows outgrow its LDS
 hipError_t launch_decode_scores(int dtype, int D, const DecodeArgs& a, float* qrot, hipStream_t st);

@@ -1,0 +1,124 @@
+// sta_rows.hip -- per-key scores of a batch of queries on the matrix cores.
+//
+// The per-query selection rules (shared_selection_triton_exact_2.py:527-604,
+// shared_selection_triton_perquery.py:651-720) take each query's full row of scores
+// fl(dot(rot(q), rot(k)) * sm_scale) over the keys it sees.  For one or a few decode queries the
+// decode score kernel computes them with fp32 dots; for a batch of queries -- the per-query
+// prefill (every prompt position, perquery.py:905-924) -- this kernel computes them as a
+// matrix product on the rotated hi / lo bf16 fragments of the RoPE pre-kernel:
+//   dot = lo(q) . hi(k) + hi(q) . lo(k) + hi(q) . hi(k)
+// with fp32 accumulation in v_mfma_f32_32x32x16_bf16, the score kernel's pass-2 product (error
+// <= 3 * 2^-16 * sum |q_i k_i|, about 1e-6 on unit-scale rows).
+//
+// One workgroup = one head and 256 consecutive queries in four waves of 64 (two 32-row blocks,
+// whose Q fragments stay in registers).  The keys run in 32-key chunks that every wave reads
+// from LDS: the next chunk's fragments are loaded into registers while the current chunk's
+// products run, then stored into the other LDS buffer.  Query i sees the keys
+// [0, M - (Q - 1 - i)) (its cache prefix: [0, q_pos0 + i] when the batch ends at the cache's last
+// key); scores past that are not written.  Workgroups with the
+// longest rows start first.
+#include "sta_device.h"
+#include "sta_kernels.h"
+
+namespace sta {
+
+template <int D>
+__global__ __launch_bounds__(256) void score_rows_kernel(RowsArgs a) {
+  constexpr int S = D / 16;                  // k steps of 16
+  constexpr int CH = S * 2 * 64;             // 16-byte units of one 32-key block (hi, lo)
+  constexpr int PER = CH / 256;              // units per thread and chunk
+  __shared__ u32x4 lds[2][CH];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int ngroups = (a.Q + 255) / 256;
+  const int g = ngroups - 1 - (int)blockIdx.x;            // longest rows first
+  const int h = blockIdx.y;
+  const int kvh = h / (a.H / a.Hkv);
+  const int r0 = g * 256;
+  const int wrow0 = r0 + wave * 64;
+  const int last_row = min(r0 + 256, a.Q) - 1;
+  // row i sees the keys [0, m_i), m_i = M - (Q - 1 - i): the cache prefix of the decode contract
+  const int kend = a.M - (a.Q - 1 - last_row);            // keys any row of the group sees
+  const int nchunks = (kend + 31) / 32;
+  const int wlast = min(wrow0 + 63, a.Q - 1);
+  const int wkend = wrow0 < a.Q ? a.M - (a.Q - 1 - wlast) : 0;
+
+  // the wave's Q fragments: two 32-row blocks x S steps x (hi, lo)
+  u32x4 qh[2][S], ql[2][S];
+  const int qblocks = a.q_rows_pad >> 5;
+#pragma unroll
+  for (int rb = 0; rb < 2; ++rb) {
+    const int blk = (wrow0 >> 5) + rb;
+    const u32x4* src = a.qfrag + ((int64_t)h * qblocks + blk) * S * 128 + lane;
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+      if (blk < qblocks) {
+        qh[rb][s] = src[s * 128];
+        ql[rb][s] = src[s * 128 + 64];
+      } else {
+        qh[rb][s] = u32x4{0, 0, 0, 0};
+        ql[rb][s] = u32x4{0, 0, 0, 0};
+      }
+    }
+  }
+
+  const u32x4* kf = a.kfrag + (int64_t)kvh * (a.k_rows_pad >> 5) * CH;
+  u32x4 pre[PER];
+  auto load_chunk = [&](int c) {
+#pragma unroll
+    for (int e = 0; e < PER; ++e) pre[e] = kf[(int64_t)c * CH + e * 256 + tid];
+  };
+  auto store_chunk = [&](int buf) {
+#pragma unroll
+    for (int e = 0; e < PER; ++e) lds[buf][e * 256 + tid] = pre[e];
+  };
+  if (nchunks > 0) {
+    load_chunk(0);
+    store_chunk(0);
+  }
+  __syncthreads();
+  float* srow = a.scores + (int64_t)h * a.Q * a.M;
+  for (int c = 0; c < nchunks; ++c) {
+    const int buf = c & 1;
+    if (c + 1 < nchunks) load_chunk(c + 1);
+    const int key0 = c * 32;
+    if (key0 < wkend) {                      // wave-uniform: some row of the wave sees the chunk
+      floatx16 acc[2];
+#pragma unroll
+      for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) acc[rb][i] = 0.0f;
+#pragma unroll
+      for (int s = 0; s < S; ++s) {
+        const u32x4 bh = lds[buf][s * 128 + lane];
+        const u32x4 bl = lds[buf][s * 128 + 64 + lane];
+#pragma unroll
+        for (int rb = 0; rb < 2; ++rb) {
+          acc[rb] = mfma32(ql[rb][s], bh, acc[rb]);
+          acc[rb] = mfma32(qh[rb][s], bl, acc[rb]);
+          acc[rb] = mfma32(qh[rb][s], bh, acc[rb]);
+        }
+      }
+      const int key = key0 + (lane & 31);
+#pragma unroll
+      for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int row = wrow0 + rb * 32 + (i >> 2) * 8 + (lane >> 5) * 4 + (i & 3);
+          if (row < a.Q && key < a.M - (a.Q - 1 - row))
+            srow[(int64_t)row * a.M + key] = acc[rb][i] * a.sm_scale;
+        }
+    }
+    if (c + 1 < nchunks) store_chunk(buf ^ 1);   // that buffer was last read before the barrier
+    __syncthreads();
+  }
+}
+
+hipError_t launch_score_rows(int D, const RowsArgs& a, hipStream_t st) {
+  const dim3 grid((unsigned)((a.Q + 255) / 256), (unsigned)a.H);
+  if (D == 64) hipLaunchKernelGGL(score_rows_kernel<64>, grid, dim3(256), 0, st, a);
+  else if (D == 128) hipLaunchKernelGGL(score_rows_kernel<128>, grid, dim3(256), 0, st, a);
+  else return hipErrorInvalidValue;
+  return hipGetLastError();
+}
+
+}  // namespace sta

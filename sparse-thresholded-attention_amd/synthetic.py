@@ -76,7 +76,8 @@ class Config:
     k_max: int = 2048
     n_global: int = 32
     n_local: int = 32
-    variant: str = "shared"     # "shared" (tile-shared sets), "pq" (PQ Union), "pqstream", "dca"
+    variant: str = "shared"     # "shared" (tile-shared sets), "pq" (PQ Union), "perquery" (own sets
+                                # per query, capped by score), "pqstream", "dca"
     select_score: str = "freq"  # key ranking: votes, or margin / expmass weighted votes
     dca: tuple = None           # (chunk_size, pretrain_len, local_window) of the DCA variant
     decode_q: int = 1           # decode variant: queries per step (the last decode_q positions)
@@ -114,6 +115,11 @@ CONFIGS = {
     #    for attention, tau 4, tile 32, k_max 2048
     "c3": Config("c3_pq_union_32h_d128_16k_bf16", 32, 32, 16384, 128, torch.bfloat16, 32, 4.0, 0.01,
                  10000.0, pi_pos_scale(4096, 16384), variant="pq", select_score="expmass"),
+    # 3q: config 3 as written -- every query keeps its own passers, capped at 2048 keys per query
+    #    by score rank (the per-query rule, perquery.py:651-720, run at every prompt position as
+    #    prefill_mode="perquery" does), dense-rank positions, base RoPE attention
+    "c3q": Config("c3q_pq_perquery_cap_32h_d128_16k_bf16", 32, 32, 16384, 128, torch.bfloat16, 32, 4.0, 0.01,
+                  10000.0, pi_pos_scale(4096, 16384), variant="perquery"),
     # 3s: the same shape through PQ Stream (per-query keep, streamed positions, no k_max), BN 32
     "c3s": Config("c3s_pq_stream_32h_d128_16k_bf16", 32, 32, 16384, 128, torch.bfloat16, 32, 4.0, 0.01,
                   10000.0, pi_pos_scale(4096, 16384), variant="pqstream"),

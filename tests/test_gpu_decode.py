@@ -167,6 +167,9 @@ def test_decode_batched_matches_per_token_loop():
     (2, 2, 3, 1800, 64, torch.float32, 1024, 100.0, False, 1.0, 1.0),
     (4, 4, 2, 39000, 128, torch.bfloat16, 2048, 100.0, False, 1.0 / 3.0, 1.0),   # global key store
     (2, 1, 16, 700, 128, torch.bfloat16, 96, 50.0, True, 0.25, 1.0),
+    # batches of 64+ queries take their scores from the matrix cores (fragments + score rows)
+    (4, 2, 200, 1500, 128, torch.bfloat16, 256, 100.0, False, 0.5, 1.0),
+    (2, 2, 96, 900, 64, torch.float16, 128, 30.0, True, 1.0, 1.1386294),
 ])
 def test_decode_three_layer(case):
     import _sta_native as native
