@@ -291,6 +291,115 @@ def bench_perquery(args, cfg, q, k, v, q_cpu, k_cpu, v_cpu, invf, ps, rs, tau):
     return 0
 
 
+DCA_SELECT_STAGES = ["rope", "votes", "select", "attention"]
+
+
+def bench_dca_select(args, cfg, q, k, v, q_cpu, k_cpu, v_cpu, invf, tau):
+    """Config 4: DCA positions with exact-max selection over each 64-query tile's inter-chunk keys
+    (two score passes of one product per pair), the tile selection, then the attention over the
+    selected inter keys plus the dense local keys."""
+    import _sta_native as native
+    s, c, w = cfg.dca
+    plan = native.DcaPlan(q, k, v, invf, s, c, w, None, tau, cfg.pct, cfg.k_max, cfg.n_global)
+    stream = torch.cuda.current_stream(q.device)
+    for _ in range(args.warmup):
+        plan.run()
+    torch.cuda.synchronize()
+    print(f"[bench] warmup done ({args.warmup} steps), timing {args.steps} steps", file=sys.stderr, flush=True)
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(5)] for _ in range(args.steps)]
+    for row in evs:
+        for e in row:
+            e.record(stream)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        plan.run(evs[i])
+    torch.cuda.synchronize()
+    ms_per_step = (time.perf_counter() - t0) * 1000.0 / args.steps
+    stage_ms = {st: sum(evs[i][j].elapsed_time(evs[i][j + 1]) for i in range(args.steps)) / args.steps
+                for j, st in enumerate(DCA_SELECT_STAGES)}
+    r = plan.out
+    L = s - w
+    N, D, H = cfg.N, cfg.D, cfg.H
+    rows = torch.arange(N, dtype=torch.int64)
+    chunk = rows // L
+    ext = torch.where(chunk >= 2, (chunk - 1) * L, torch.zeros_like(chunk))   # inter keys per row
+    local = rows + 1 - ext                                                     # dense local keys per row
+    inter_pairs = int(ext.sum().item()) * H
+    # votes: pass 1 (row max) and pass 2 (threshold) over the inter pairs, one product each
+    vflops = 2 * 2 * D * inter_pairs
+    nsel = r["kept_size"].clamp(max=cfg.k_max).to(torch.int64).cpu()          # (H, nt)
+    sel_rows = nsel.repeat_interleave(64, dim=1)[:, :N].sum().item()
+    aflops = 2 * 2 * D * (int(sel_rows) + H * int(local.sum().item()))       # QK^T and PV
+    peak = PEAK_FP32_TFLOPS if q.dtype == torch.float32 else PEAK_BF16_TFLOPS
+    v_tf = vflops / (stage_ms["votes"] * 1e-3) / 1e12
+    a_tf = aflops / (stage_ms["attention"] * 1e-3) / 1e12
+    roof = {
+        "votes": {"kernel": "dca_vote_kernel", "bound": "mfma", "achieved": round(v_tf, 2), "peak": peak,
+                  "unit": "TFLOP/s", "frac": round(v_tf / peak, 4), "algorithmic_per_launch": vflops,
+                  "traffic": read_traffic(args.traffic_file, "dca_vote_kernel")},
+        "attention": {"kernel": "dca_attn_kernel", "bound": "mfma", "achieved": round(a_tf, 2), "peak": peak,
+                      "unit": "TFLOP/s", "frac": round(a_tf / peak, 4), "algorithmic_per_launch": aflops,
+                      "traffic": read_traffic(args.traffic_file, "dca_attn_kernel")},
+    }
+    dominant = roof["votes"] if stage_ms["votes"] >= stage_ms["attention"] else roof["attention"]
+    print(f"[bench] {ms_per_step:.3f} ms/step; stages {stage_ms}", file=sys.stderr, flush=True)
+    cpu = None
+    if args.cpu_baseline_seconds > 0:
+        print("[bench] timing the CPU oracle sample", file=sys.stderr, flush=True)
+        cpu = cpu_baseline_dca_select(cfg, q_cpu, k_cpu, v_cpu, invf, args.cpu_baseline_seconds)
+    line = {
+        "metric": METRIC,
+        "value": round(N / (ms_per_step * 1e-3), 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": {torch.bfloat16: "bf16", torch.float16: "fp16", torch.float32: "fp32"}[q.dtype],
+        "data": "synthetic (seeded Gaussian Q/K/V with planted keys)",
+        "config": {"workload": cfg.name, "variant": cfg.variant, "heads": H, "kv_heads": cfg.Hkv, "seq_len": N,
+                   "head_dim": D, "tile": 64, "tau": cfg.tau, "pct": cfg.pct, "k_max": cfg.k_max,
+                   "dca_chunk_pretrain_local": cfg.dca, "parallelism": "none (1 GPU)"},
+        "stages_ms": {st: round(t, 4) for st, t in stage_ms.items()},
+        "roofline": dominant,
+        "rooflines": roof,
+        "selection": {"kept_mean": round(r["kept_size"].float().mean().item(), 1),
+                      "overflow20_tiles": int(r["overflow20"].sum().item()), "tiles": int(r["kept_size"].numel()),
+                      "inter_pairs": inter_pairs},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+def cpu_baseline_dca_select(cfg, q, k, v, invf, budget_s):
+    """The config-4 oracle on whole heads of a shorter prefix (votes, selection, attention), timed
+    per head at two lengths and scaled quadratically to the full length."""
+    import numpy as np
+    from oracle import sta_oracle as orc
+    s, c, w = cfg.dca
+    threads = orc.num_threads()
+    t = {}
+    for n in (8192, 16384):
+        qn, dt = orc.from_torch(q[0, :1, :n])
+        kn, _ = orc.from_torch(k[0, :1, :n])
+        vn, _ = orc.from_torch(v[0, :1, :n])
+        t0 = time.perf_counter()
+        orc.dca_select_attention(qn, kn, vn, dt, invf.numpy(), s, c, w, np.full(1, cfg.tau, np.float32), cfg.pct,
+                                 cfg.k_max, cfg.n_global)
+        t[n] = time.perf_counter() - t0
+    # quadratic in the length: scale the longer sample
+    per_head = t[16384] * (cfg.N / 16384) ** 2
+    return {"value": round(cfg.N / (per_head * cfg.H), 3), "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"one head at 8192 and 16384 tokens through the CPU oracle (inter votes, selection, "
+                      f"attention; {threads} OpenMP threads), the 16384-token time scaled by (N / 16384)^2 to "
+                      f"{cfg.N} tokens and by {cfg.H} heads"}
+
+
 def cpu_baseline_perquery(cfg, q, k, v, invf, ps, rs, budget_s):
     """The oracle's per-query rule (scores, _decode_build_sets_pq, attend) on evenly spaced query
     rows of one head at a time, scaled to every row of every head by the causal key count."""
@@ -379,6 +488,8 @@ def main():
         return bench_decode(args, cfg, q, k, v, q_cpu, k_cpu, v_cpu, invf, ps, rs, tau)
     if cfg.variant == "perquery":
         return bench_perquery(args, cfg, q, k, v, q_cpu, k_cpu, v_cpu, invf, ps, rs, tau)
+    if cfg.variant == "dca_select":
+        return bench_dca_select(args, cfg, q, k, v, q_cpu, k_cpu, v_cpu, invf, tau)
     if cfg.variant == "dca":
         plan = native.DcaPlan(q, k, v, invf, cfg.dca[0], cfg.dca[1], cfg.dca[2])
     elif cfg.variant == "pqstream":

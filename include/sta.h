@@ -280,7 +280,33 @@ typedef struct sta_dca_args {
   void* out;                /* (H, N, D) */
   void* workspace;
   size_t workspace_bytes;
-  void* const* stage_events; /* NULL or 3 hipEvent_t: before the rotations, before the sweep, after */
+  void* const* stage_events; /* NULL or hipEvent_t: dense, 3 (before the rotations, before the
+                                sweep, after); with select, 5 (before the rotations, the votes,
+                                the selection and the attention, after) */
+  /* ABI 3: config 4 -- exact-max selection over the inter-chunk keys (select = 1).  Each 64-query
+   * tile of DCA chunk c >= 2 scores its inter keys [0, (c - 1) L) at DCA's inter positions
+   * (dca_kernel.py:481-487), takes the exact row max, votes s >= m - tau and selects among them by
+   * _build_sets (shared_selection_triton_exact_2.py:277-426) applied to that key range: top
+   * start_pct% with the 25 / 20% fallback, tie-inclusive cut, the global keys [0, n_global)
+   * forced, k_max cap, unresolved tiles truncated to their k_max smallest keys.  The query then
+   * attends the selected inter keys (inter position) plus every key of its own and the previous
+   * chunk densely (intra / succ positions), in one softmax.  No repositioning: DCA's positions
+   * already stay inside the pretraining window.  With tau = inf, start_pct = 100 and k_max >= N
+   * it is the dense DCA attention. */
+  int32_t select;           /* 0: dense DCA (the fields below are ignored); 1: config 4 */
+  const float* tau;         /* (H,) */
+  int32_t start_pct;        /* max(0, round(pct)) */
+  int32_t k_max, n_global, measure;
+  int32_t* idx;             /* (H, nt, k_max), nt = ceil(N / 64): selected inter keys ascending,
+                               sentinel = the tile's inter key count */
+  int32_t* shared_size;     /* (H, nt) statistics of the selection, as sta_shared_args */
+  int32_t* kept_size;
+  int32_t* chosen;
+  uint8_t* orig_overflow;
+  int32_t* kpct_meas;
+  uint8_t* overflow20;
+  int32_t* votes;           /* optional (H, nt, N) dense int32 votes (0 past a tile's inter keys) */
+  float* row_max;           /* optional (H, N) exact max over the inter keys, -inf without any */
 } sta_dca_args;
 
 /* Bytes of device workspace sta_dca_attention needs for these arguments. */
@@ -288,7 +314,9 @@ size_t sta_dca_workspace_size(const sta_dca_args* args);
 
 /* The DCA prefill attention core.  Replaces the prefill branch of dca_forward with its position
  * tables and the log-sum-exp merge of its three attention blocks, dca_kernel.py:166-231,
- * 278-366, 372-489 (the module the reference installs with install_dca_forward, :660-663). */
+ * 278-366, 372-489 (the module the reference installs with install_dca_forward, :660-663).
+ * With select = 1, config 4: DCA positions with exact-max selection over the inter-chunk keys
+ * (no reference combines them; the rule is described at sta_dca_args.select). */
 int sta_dca_attention(const sta_dca_args* args, void* stream);
 
 /* ------------------------------------------------------------------------------------------ */

@@ -393,6 +393,86 @@ def dca_attention(q, k, v, dtype, inv_freq, chunk_size, pretrain_len, local_wind
 
 
 # ---------------------------------------------------------------------------------------------
+# config 4: DCA positions with exact-max selection over the inter-chunk keys (build-defined
+# composition of dca_kernel.py's positions and exact_2.py's Kernel A + _build_sets)
+# ---------------------------------------------------------------------------------------------
+def dca_inter_votes(q, k, dtype, inv_freq, chunk_size, pretrain_len, local_window, tau, scale=None, T=64,
+                    band_eps=1e-3, want_band=False):
+    """Votes (H, nt, N) int32 over each 64-query tile's inter keys [0, (c - 1) L), row_max (H, N)
+    (-inf without inter keys) and optionally band (H, nt, N)."""
+    q = np.ascontiguousarray(q)
+    k = np.ascontiguousarray(k)
+    H, N, D = q.shape
+    Hkv = k.shape[0]
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    nt = (N + T - 1) // T
+    votes = np.empty((H, nt, N), np.int32)
+    rm = np.empty((H, N), np.float32)
+    band = np.empty((H, nt, N), np.int32) if want_band else None
+    ms = np.float32(dca_mscale(N, pretrain_len))
+    lib().oracle_dca_inter_votes(_p(q), _p(k), ctypes.c_int(dtype), ctypes.c_int(H), ctypes.c_int(Hkv),
+                                 ctypes.c_int(N), ctypes.c_int(D), _p(_c(inv_freq, np.float32)),
+                                 ctypes.c_int(chunk_size), ctypes.c_int(local_window), ctypes.c_float(ms),
+                                 ctypes.c_float(scale), _p(_c(tau, np.float32)), ctypes.c_int(T),
+                                 ctypes.c_float(band_eps), _p(votes), _p(rm), _p(band))
+    out = {"votes": votes, "row_max": rm}
+    if want_band:
+        out["band"] = band
+    return out
+
+
+def dca_build_sets(votes, chunk_size, local_window, n_global, pct, k_max, T=64, measure=False, want_cut=False):
+    """_build_sets over each tile's inter keys.  Returns (idx, shared_size, kept_size, chosen,
+    orig_overflow, kpct_meas, overflow20[, cut])."""
+    votes = _c(votes, np.int32)
+    H, nt, N = votes.shape
+    idx = np.empty((H, nt, k_max), np.int32)
+    ss, ks, ch, km = (np.empty((H, nt), np.int32) for _ in range(4))
+    oo, o20 = np.empty((H, nt), np.uint8), np.empty((H, nt), np.uint8)
+    cut = np.empty((H, nt), np.float32) if want_cut else None
+    lib().oracle_dca_build_sets(_p(votes), ctypes.c_int(H), ctypes.c_int(N), ctypes.c_int(chunk_size),
+                                ctypes.c_int(local_window), ctypes.c_int(T), ctypes.c_int(n_global),
+                                ctypes.c_int(start_pct_of(pct)), ctypes.c_int(k_max), ctypes.c_int(int(measure)),
+                                _p(idx), _p(ss), _p(ks), _p(ch), _p(oo), _p(km), _p(o20), _p(cut))
+    res = (idx, ss, ks, ch, oo.astype(bool), km, o20.astype(bool))
+    return res + (cut,) if want_cut else res
+
+
+def dca_select_attn(q, k, v, dtype, inv_freq, chunk_size, pretrain_len, local_window, idx, kept_size, scale=None,
+                    T=64, rows=None):
+    """Attention given each tile's selected inter keys: out (H, N, D) fp32 (NaN outside `rows`)."""
+    q = np.ascontiguousarray(q)
+    k = np.ascontiguousarray(k)
+    v = np.ascontiguousarray(v)
+    H, N, D = q.shape
+    Hkv = k.shape[0]
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    ms = np.float32(dca_mscale(N, pretrain_len))
+    out = np.full((H, N, D), np.nan, np.float32)
+    r = _c(rows, np.int32) if rows is not None else None
+    idx = _c(idx, np.int32)
+    lib().oracle_dca_select_attn(_p(q), _p(k), _p(v), ctypes.c_int(dtype), ctypes.c_int(H), ctypes.c_int(Hkv),
+                                 ctypes.c_int(N), ctypes.c_int(D), _p(_c(inv_freq, np.float32)),
+                                 ctypes.c_int(chunk_size), ctypes.c_int(local_window), ctypes.c_float(ms),
+                                 ctypes.c_float(scale), ctypes.c_int(T), _p(idx), _p(_c(kept_size, np.int32)),
+                                 ctypes.c_int(idx.shape[-1]), _p(r), ctypes.c_int(len(r) if r is not None else 0),
+                                 _p(out))
+    return out
+
+
+def dca_select_attention(q, k, v, dtype, inv_freq, chunk_size, pretrain_len, local_window, tau, pct=30.0,
+                         k_max=2048, n_global=32, scale=None, T=64, measure=False, rows=None):
+    """Config 4 composed: inter votes, selection, attention.  Returns (out, sets tuple, votes dict)."""
+    a = dca_inter_votes(q, k, dtype, inv_freq, chunk_size, pretrain_len, local_window, tau, scale, T)
+    sets = dca_build_sets(a["votes"], chunk_size, local_window, n_global, pct, k_max, T, measure)
+    out = dca_select_attn(q, k, v, dtype, inv_freq, chunk_size, pretrain_len, local_window, sets[0], sets[2],
+                          scale, T, rows)
+    return out, sets, a
+
+
+# ---------------------------------------------------------------------------------------------
 # decode: a batch of Q queries over one cache of M keys; query i at position q_pos0 + i sees the
 # keys [0, M - (Q - 1 - i)) (the cache prefix of spi_forward's per-token loop, exact_2.py:743-745)
 # ---------------------------------------------------------------------------------------------

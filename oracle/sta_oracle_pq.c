@@ -423,9 +423,13 @@ void oracle_pqstream(const void* q, const void* k, const void* v, int dtype, int
 static void dca_table(float t, const float* inv_freq, int D, float mscale, int dtype, float* c, float* s) {
   const int half = D / 2;
   for (int i = 0; i < half; ++i) {
+    /* cos / sin of the fp32 angle correctly rounded to fp32 (through double), then the fp32
+     * product with mscale: the table is rounded to the model dtype next, where a one-ulp
+     * difference between fp32 cosine implementations could flip a bf16 entry */
     volatile float ang = t * inv_freq[i];
-    volatile float cc = cosf(ang) * mscale;
-    volatile float ss = sinf(ang) * mscale;
+    volatile float c32 = (float)cos((double)ang), s32 = (float)sin((double)ang);
+    volatile float cc = c32 * mscale;
+    volatile float ss = s32 * mscale;
     c[i] = round_to_dtype(cc, dtype);
     s[i] = round_to_dtype(ss, dtype);
   }
@@ -512,4 +516,211 @@ void oracle_dca(const void* q, const void* k, const void* v, int dtype, int H, i
     free(acc);
   }
   free(kr);
+}
+
+/* ------------------------------------------------------------------------------------------- */
+/* Config 4: DCA positions with exact-max selection over the inter-chunk keys                 */
+/* ------------------------------------------------------------------------------------------- */
+/*
+ * No reference file combines the two; the build defines the composition from reference parts:
+ *   - positions and rotations of dca_kernel.py (keys at j mod L, queries at intra / succ / inter
+ *     positions, model-dtype tables and rotation, :166-231, 278-286, 456-489);
+ *   - for a query of chunk c >= 2, the inter keys [0, (c - 1) L) -- the keys DCA's inter block
+ *     attends at the constant query position (:481-487) -- are scored, thresholded at the exact
+ *     row max minus tau and voted per 64-query tile as Kernel A does
+ *     (shared_selection_triton_exact_2.py:87-125: s = fl(fl(dot) * scale), keep s >= fl(m - tau));
+ *   - each tile's inter votes, as a key axis of length (c - 1) L, go through _build_sets
+ *     (exact_2.py:277-426, here oracle_build_sets with that length and the tile's start as
+ *     q_pos_base, so its local window lies past the axis and only the global keys are forced);
+ *   - each query attends its tile's selected inter keys at the inter position plus every key of
+ *     its own and the previous chunk (intra / succ positions), in one softmax.
+ * Kernel-A-style scores here are dots of the model-dtype rotated vectors accumulated in double
+ * and rounded once to fp32.
+ */
+void oracle_build_sets(const int32_t* votes, int H, int nt, int N, float pos_scale, int n_global,
+                       int n_local, int start_pct, int T, int k_max, int q_pos_base, int measure,
+                       int32_t* idx, float* newpos_k, float* newpos_q, int32_t* shared_size,
+                       int32_t* kept_size, int32_t* chosen, uint8_t* orig_overflow,
+                       int32_t* kpct_meas, uint8_t* overflow20, const float* wvotes, float* cut);
+
+/* rotated keys (Hkv, N, D) and the three query variants (3, H, N, D) as fp32 values */
+static void dca_rotate_all(const void* q, const void* k, int dtype, int H, int Hkv, int N, int D,
+                           const float* inv_freq, int chunk_size, int L, float mscale, float* kr, float* qr) {
+  const int half = D / 2;
+#pragma omp parallel
+  {
+    float* c = (float*)malloc(sizeof(float) * half);
+    float* s = (float*)malloc(sizeof(float) * half);
+#pragma omp for schedule(static)
+    for (int j = 0; j < N; ++j) {
+      dca_table((float)(j % L), inv_freq, D, mscale, dtype, c, s);
+      for (int hk = 0; hk < Hkv; ++hk)
+        dca_rotate(k, dtype, ((size_t)hk * N + j) * D, D, c, s, kr + ((size_t)hk * N + j) * D);
+      const int pid = j % L;
+      const int pos[3] = {pid, (pid + L) < chunk_size ? pid + L : chunk_size,
+                          (2 * L - 1) < chunk_size ? 2 * L - 1 : chunk_size};
+      for (int var = 0; var < 3; ++var) {
+        dca_table((float)pos[var], inv_freq, D, mscale, dtype, c, s);
+        for (int h = 0; h < H; ++h)
+          dca_rotate(q, dtype, ((size_t)h * N + j) * D, D, c, s, qr + (((size_t)var * H + h) * N + j) * D);
+      }
+    }
+    free(c);
+    free(s);
+  }
+}
+
+static inline float dot_f32(const float* a, const float* b, int D) {
+  double d = 0.0;
+  for (int e = 0; e < D; ++e) d += (double)a[e] * (double)b[e];
+  return (float)d;
+}
+
+/*
+ * Inter votes: votes (H, nt, N) int32 (0 past each tile's inter keys), row_max (H, N) fp32 (-inf
+ * for rows without inter keys), band (H, nt, N) int32 or NULL (# of the tile's rows whose score for
+ * the key lies within band_eps of that row's threshold).  T = 64.
+ */
+void oracle_dca_inter_votes(const void* q, const void* k, int dtype, int H, int Hkv, int N, int D,
+                            const float* inv_freq, int chunk_size, int local_window, float mscale, float scale,
+                            const float* tau, int T, float band_eps, int32_t* votes, float* row_max,
+                            int32_t* band) {
+  const int L = chunk_size - local_window;
+  const int group = H / Hkv;
+  const int nt = (N + T - 1) / T;
+  float* kr = (float*)malloc(sizeof(float) * (size_t)Hkv * N * D);
+  float* qr = (float*)malloc(sizeof(float) * (size_t)3 * H * N * D);
+  dca_rotate_all(q, k, dtype, H, Hkv, N, D, inv_freq, chunk_size, L, mscale, kr, qr);
+  memset(votes, 0, sizeof(int32_t) * (size_t)H * nt * N);
+  if (band) memset(band, 0, sizeof(int32_t) * (size_t)H * nt * N);
+#pragma omp parallel
+  {
+    float* sc = (float*)malloc(sizeof(float) * (size_t)N);
+#pragma omp for schedule(dynamic, 1)
+    for (int ht = 0; ht < H * nt; ++ht) {
+      const int h = ht / nt, t = ht % nt, hk = h / group;
+      const int c = (t * T) / L;
+      const int ext = c >= 2 ? (c - 1) * L : 0;
+      int32_t* vrow = votes + (size_t)ht * N;
+      int32_t* brow = band ? band + (size_t)ht * N : NULL;
+      for (int i = t * T; i < t * T + T && i < N; ++i) {
+        const float* qq = qr + (((size_t)2 * H + h) * N + i) * D;
+        float mx = -INFINITY;
+        for (int j = 0; j < ext; ++j) {
+          volatile float d = dot_f32(qq, kr + ((size_t)hk * N + j) * D, D);
+          volatile float s = d * scale;
+          sc[j] = s;
+          mx = s > mx ? s : mx;
+        }
+        row_max[(size_t)h * N + i] = ext > 0 ? mx : -INFINITY;
+        if (ext == 0) continue;
+        volatile float thr = mx - tau[h];
+        for (int j = 0; j < ext; ++j) {
+          vrow[j] += sc[j] >= thr;
+          if (brow && fabsf(sc[j] - thr) <= band_eps) brow[j] += 1;
+        }
+      }
+    }
+    free(sc);
+  }
+  free(kr);
+  free(qr);
+}
+
+/*
+ * _build_sets over each tile's inter keys: idx (H, nt, k_max) (sentinel: the tile's inter key
+ * count), shared_size / kept_size / chosen / kpct_meas (H, nt) int32, orig_overflow / overflow20
+ * (H, nt) uint8, cut (H, nt) fp32 or NULL.  Tiles without inter keys get an empty set (all
+ * statistics 0, idx 0).
+ */
+void oracle_dca_build_sets(const int32_t* votes, int H, int N, int chunk_size, int local_window, int T,
+                           int n_global, int start_pct, int k_max, int measure, int32_t* idx,
+                           int32_t* shared_size, int32_t* kept_size, int32_t* chosen, uint8_t* orig_overflow,
+                           int32_t* kpct_meas, uint8_t* overflow20, float* cut) {
+  const int L = chunk_size - local_window;
+  const int nt = (N + T - 1) / T;
+  float* npk = (float*)malloc(sizeof(float) * (size_t)k_max);
+  float* npq = (float*)malloc(sizeof(float) * (size_t)T);
+  for (int ht = 0; ht < H * nt; ++ht) {
+    const int t = ht % nt;
+    const int c = (t * T) / L;
+    const int ext = c >= 2 ? (c - 1) * L : 0;
+    int32_t* irow = idx + (size_t)ht * k_max;
+    if (ext == 0) {
+      for (int s = 0; s < k_max; ++s) irow[s] = 0;
+      shared_size[ht] = kept_size[ht] = chosen[ht] = kpct_meas[ht] = 0;
+      orig_overflow[ht] = overflow20[ht] = 0;
+      if (cut) cut[ht] = INFINITY;
+      continue;
+    }
+    oracle_build_sets(votes + (size_t)ht * N, 1, 1, ext, 1.0f, n_global, 0, start_pct, T, k_max, t * T,
+                      measure, irow, npk, npq, shared_size + ht, kept_size + ht, chosen + ht,
+                      orig_overflow + ht, kpct_meas + ht, overflow20 + ht, NULL, cut ? cut + ht : NULL);
+  }
+  free(npk);
+  free(npq);
+}
+
+/*
+ * Attention given the selection: out (H, N, D) fp32 for the listed rows (all when rows is NULL),
+ * the softmax over the tile's selected inter keys idx[h][t][0 .. min(kept, k_max)) at the inter
+ * position and the keys [max(0, (c - 1) L), i] at the intra / succ positions, in double.
+ */
+void oracle_dca_select_attn(const void* q, const void* k, const void* v, int dtype, int H, int Hkv, int N, int D,
+                            const float* inv_freq, int chunk_size, int local_window, float mscale, float scale,
+                            int T, const int32_t* idx, const int32_t* kept_size, int k_max, const int32_t* rows,
+                            int n_rows, float* out) {
+  const int L = chunk_size - local_window;
+  const int group = H / Hkv;
+  const int nt = (N + T - 1) / T;
+  const int nr = rows ? n_rows : N;
+  float* kr = (float*)malloc(sizeof(float) * (size_t)Hkv * N * D);
+  float* qr = (float*)malloc(sizeof(float) * (size_t)3 * H * N * D);
+  dca_rotate_all(q, k, dtype, H, Hkv, N, D, inv_freq, chunk_size, L, mscale, kr, qr);
+#pragma omp parallel
+  {
+    double* sc = (double*)malloc(sizeof(double) * ((size_t)k_max + 2 * (size_t)L + 64));
+    int32_t* key = (int32_t*)malloc(sizeof(int32_t) * ((size_t)k_max + 2 * (size_t)L + 64));
+    double* acc = (double*)malloc(sizeof(double) * D);
+#pragma omp for schedule(dynamic, 1)
+    for (int x = 0; x < H * nr; ++x) {
+      const int h = x / nr;
+      const int i = rows ? rows[x % nr] : x % nr;
+      const int hk = h / group, t = i / T, c = i / L;
+      const int lo = c >= 2 ? (c - 1) * L : 0;
+      int n = 0;
+      double mx = -INFINITY;
+      const int ks = kept_size[(size_t)h * nt + t];
+      const int nsel = ks < k_max ? ks : k_max;
+      const int32_t* irow = idx + ((size_t)h * nt + t) * k_max;
+      for (int s = 0; s < nsel; ++s) {                  /* selected inter keys, inter position */
+        const int j = irow[s];
+        key[n] = j;
+        sc[n] = (double)dot_f32(qr + (((size_t)2 * H + h) * N + i) * D, kr + ((size_t)hk * N + j) * D, D) * scale;
+        mx = sc[n] > mx ? sc[n] : mx;
+        ++n;
+      }
+      for (int j = lo; j <= i; ++j) {                   /* local keys, succ / intra positions */
+        const int var = (j / L == c) ? 0 : 1;
+        key[n] = j;
+        sc[n] = (double)dot_f32(qr + (((size_t)var * H + h) * N + i) * D, kr + ((size_t)hk * N + j) * D, D) *
+                scale;
+        mx = sc[n] > mx ? sc[n] : mx;
+        ++n;
+      }
+      double l = 0.0;
+      for (int e = 0; e < D; ++e) acc[e] = 0.0;
+      for (int u = 0; u < n; ++u) {
+        const double p = exp(sc[u] - mx);
+        l += p;
+        for (int e = 0; e < D; ++e) acc[e] += p * (double)load_elem(v, dtype, ((size_t)hk * N + key[u]) * D + e);
+      }
+      for (int e = 0; e < D; ++e) out[((size_t)h * N + i) * D + e] = (float)(acc[e] / l);
+    }
+    free(sc);
+    free(key);
+    free(acc);
+  }
+  free(kr);
+  free(qr);
 }

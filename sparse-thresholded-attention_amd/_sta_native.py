@@ -113,6 +113,11 @@ class DcaArgsC(ctypes.Structure):
         ("scale", ctypes.c_float), ("out", ctypes.c_void_p),
         ("workspace", ctypes.c_void_p), ("workspace_bytes", ctypes.c_size_t),
         ("stage_events", ctypes.c_void_p),
+        ("select", ctypes.c_int32), ("tau", ctypes.c_void_p), ("start_pct", ctypes.c_int32),
+        ("k_max", ctypes.c_int32), ("n_global", ctypes.c_int32), ("measure", ctypes.c_int32),
+        ("idx", ctypes.c_void_p), ("shared_size", ctypes.c_void_p), ("kept_size", ctypes.c_void_p),
+        ("chosen", ctypes.c_void_p), ("orig_overflow", ctypes.c_void_p), ("kpct_meas", ctypes.c_void_p),
+        ("overflow20", ctypes.c_void_p), ("votes", ctypes.c_void_p), ("row_max", ctypes.c_void_p),
     ]
 
 
@@ -720,7 +725,11 @@ class DcaPlan:
     """Output and workspace of the DCA prefill for one shape, allocated once; run() launches the
     rotations and the attention sweep on the current stream and allocates nothing."""
 
-    def __init__(self, q, k, v, inv_freq, chunk_size, pretrain_len, local_window, scale=None):
+    def __init__(self, q, k, v, inv_freq, chunk_size, pretrain_len, local_window, scale=None, tau=None,
+                 pct=30.0, k_max=2048, n_global=32, measure=False, want_votes=False, want_row_max=False):
+        """tau given: config 4 (exact-max selection over the inter-chunk keys, 64-query tiles);
+        the outputs then also hold the selection (idx, shared_size, kept_size, chosen,
+        orig_overflow, kpct_meas, overflow20; votes / row_max on request)."""
         qh, kh, vh, _, ifc, _ = _prep_inputs(q, k, v, torch.zeros(1), inv_freq, None)
         H, N, D = qh.shape
         self.device = dev = qh.device
@@ -739,6 +748,28 @@ class DcaPlan:
         self._keep = (qh, kh, vh, ifc)
         self.out = {"out": torch.empty((H, N, D), dtype=qh.dtype, device=dev)}
         a.out = _ptr(self.out["out"])
+        self.select = tau is not None
+        if self.select:
+            nt = (N + 63) // 64
+            tau = tau.to(device=dev, dtype=torch.float32).reshape(-1).contiguous()
+            if tau.numel() == 1 and H > 1:
+                tau = tau.expand(H).contiguous()
+            self._keep = self._keep + (tau,)
+            a.select, a.tau, a.start_pct = 1, _ptr(tau), start_pct_of(pct)
+            a.k_max, a.n_global, a.measure = int(k_max), int(n_global), int(bool(measure))
+            o = self.out
+            o["idx"] = torch.empty((H, nt, k_max), dtype=torch.int32, device=dev)
+            for name in ("shared_size", "kept_size", "chosen", "kpct_meas"):
+                o[name] = torch.empty((H, nt), dtype=torch.int32, device=dev)
+            for name in ("orig_overflow", "overflow20"):
+                o[name] = torch.empty((H, nt), dtype=torch.bool, device=dev)
+            if want_votes:
+                o["votes"] = torch.empty((H, nt, N), dtype=torch.int32, device=dev)
+            if want_row_max:
+                o["row_max"] = torch.empty((H, N), dtype=torch.float32, device=dev)
+            for name in ("idx", "shared_size", "kept_size", "chosen", "orig_overflow", "kpct_meas", "overflow20",
+                         "votes", "row_max"):
+                setattr(a, name, _ptr(o.get(name)))
         n = lib().sta_dca_workspace_size(ctypes.byref(a))
         if n == 0:
             _check(-1, "sta_dca_workspace_size")
@@ -747,9 +778,11 @@ class DcaPlan:
         self._events = None
 
     def run(self, events=None):
-        """events: None or 3 recorded torch.cuda.Event(enable_timing=True)."""
+        """events: None or recorded torch.cuda.Event(enable_timing=True): 3 (dense: rotations,
+        sweep) or 5 (selection: rotations, votes, selection, attention)."""
         if events is not None:
-            self._events = (ctypes.c_void_p * 3)(*[e.cuda_event for e in events])
+            n = 5 if self.select else 3
+            self._events = (ctypes.c_void_p * n)(*[e.cuda_event for e in events])
             self.args.stage_events = ctypes.cast(self._events, ctypes.c_void_p)
         else:
             self.args.stage_events = None
@@ -760,6 +793,14 @@ class DcaPlan:
 def dca_attention(q, k, v, inv_freq, chunk_size, pretrain_len, local_window, scale=None):
     """The DCA prefill on the device; returns out (H, N, D) in q.dtype."""
     return DcaPlan(q, k, v, inv_freq, chunk_size, pretrain_len, local_window, scale).run()["out"]
+
+
+def dca_select_attention(q, k, v, inv_freq, chunk_size, pretrain_len, local_window, tau, pct=30.0, k_max=2048,
+                         n_global=32, scale=None, measure=False, want_votes=False, want_row_max=False):
+    """Config 4 on the device: DCA positions, exact-max selection over each 64-query tile's
+    inter-chunk keys, dense local keys.  Returns the dict of outputs (out, idx, statistics, ...)."""
+    return DcaPlan(q, k, v, inv_freq, chunk_size, pretrain_len, local_window, scale, tau, pct, k_max, n_global,
+                   measure, want_votes, want_row_max).run()
 
 
 # ---------------------------------------------------------------------------------------------

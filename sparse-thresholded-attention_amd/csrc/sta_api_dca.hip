@@ -11,20 +11,38 @@ using namespace sta_api;
 
 namespace {
 
+constexpr int kDcaSelTile = 64;   // queries per selection tile (config 4)
+
 struct DcaLayout {
-  int Npad, planes;
-  size_t krot_off, qrot_off, total;
+  int Npad, planes, nt;
+  int64_t votes_stride;
+  size_t krot_off, qrot_off, votes_off, rmax_off, npk_off, npq_off, state_off, total;
 };
 
 DcaLayout dca_layout_of(const sta_dca_args* a) {
   DcaLayout L;
   L.Npad = (a->N + 63) / 64 * 64;
   L.planes = a->dtype == STA_DTYPE_F32 ? 2 : 1;
+  L.nt = (a->N + kDcaSelTile - 1) / kDcaSelTile;
+  L.votes_stride = ((int64_t)a->N + 15) / 16 * 16;
   size_t off = 0;
   L.krot_off = off;
   off = align256(off + (size_t)a->Hkv * L.Npad * L.planes * a->D * 2);
   L.qrot_off = off;
   off = align256(off + (size_t)3 * a->H * L.Npad * L.planes * a->D * 2);
+  L.votes_off = L.rmax_off = L.npk_off = L.npq_off = L.state_off = off;
+  if (a->select) {
+    L.votes_off = off;                                 // byte votes (H, nt, votes_stride)
+    off = align256(off + (size_t)a->H * L.nt * L.votes_stride);
+    L.rmax_off = off;                                  // raw inter row maxima (H, Npad)
+    off = align256(off + (size_t)a->H * L.Npad * 4);
+    L.npk_off = off;                                   // selection positions (unused by DCA)
+    off = align256(off + (size_t)a->H * L.nt * a->k_max * 4);
+    L.npq_off = off;
+    off = align256(off + (size_t)a->H * L.nt * kDcaSelTile * 4);
+    L.state_off = off;                                 // partial softmax states (H, Npad, D + 4)
+    off = align256(off + (size_t)a->H * L.Npad * (a->D + 4) * 4);
+  }
   L.total = off;
   return L;
 }
@@ -44,7 +62,78 @@ int dca_check(const sta_dca_args* a) {
   const int L = a->chunk_size - a->local_window;
   if (L % 64 != 0)
     return fail(STA_ERR_UNSUPPORTED, "chunk_size - local_window = %d is not a multiple of 64", L);
+  if (a->select != 0 && a->select != 1) return fail(STA_ERR_INVALID_ARG, "select=%d is not 0 or 1", a->select);
+  if (a->select) {
+    if (a->k_max < 1) return fail(STA_ERR_INVALID_ARG, "k_max=%d must be >= 1", a->k_max);
+    if (a->n_global < 0) return fail(STA_ERR_INVALID_ARG, "n_global=%d must be >= 0", a->n_global);
+    if (a->start_pct < 0) return fail(STA_ERR_INVALID_ARG, "start_pct=%d must be >= 0", a->start_pct);
+    if (select_lds_bytes(a->N, a->k_max) > 160 * 1024)
+      return fail(STA_ERR_UNSUPPORTED, "N=%d with k_max=%d needs more than 160 KB of LDS for selection",
+                  a->N, a->k_max);
+  }
   return STA_OK;
+}
+
+// config 4's selection: inter-key votes (two passes), then _build_sets over each tile's inter keys
+int dca_select(const sta_dca_args* a, const DcaLayout& L, const uint16_t* krot, const uint16_t* qrot, int Lc,
+               hipStream_t st) {
+  if (!a->tau || !a->idx || !a->shared_size || !a->kept_size || !a->chosen || !a->orig_overflow ||
+      !a->kpct_meas || !a->overflow20)
+    return fail(STA_ERR_INVALID_ARG, "select: tau and the selection outputs must be non-NULL");
+  char* ws = (char*)a->workspace;
+  DcaVoteArgs v{};
+  v.qrot = qrot;
+  v.krot = krot;
+  v.H = a->H;
+  v.Hkv = a->Hkv;
+  v.N = a->N;
+  v.Npad = L.Npad;
+  v.L = Lc;
+  v.nt = L.nt;
+  v.scale = a->scale;
+  v.tau = a->tau;
+  v.rmax = (float*)(ws + L.rmax_off);
+  v.row_max = a->row_max;
+  v.votes = (uint8_t*)(ws + L.votes_off);
+  v.votes_stride = L.votes_stride;
+  hipError_t e = launch_dca_votes(a->dtype, a->D, v, st);
+  if (e != hipSuccess) return hip_fail(e, "dca inter votes");
+  int rc = mark_event(a->stage_events, 2, st);
+  if (rc != STA_OK) return rc;
+  SelectArgs s;
+  memset(&s, 0, sizeof(s));
+  s.votes = ws + L.votes_off;
+  s.votes_stride = L.votes_stride;
+  s.votes_dense = 0;
+  s.H = a->H;
+  s.nt = L.nt;
+  s.N = a->N;
+  s.T = kDcaSelTile;
+  s.k_max = a->k_max;
+  s.q_pos_base = 0;
+  s.n_global = a->n_global;
+  s.n_local = 0;
+  s.pos_scale = 1.0f;
+  s.nsteps = 0;
+  s.steps[s.nsteps++] = a->start_pct;                  // exact_2.py:309-310
+  if (25 < a->start_pct) s.steps[s.nsteps++] = 25;
+  if (20 < a->start_pct) s.steps[s.nsteps++] = 20;
+  s.K_ord = 1;                                         // per tile under dca_L
+  s.start_pct = a->start_pct;
+  s.measure = a->measure;
+  s.idx = a->idx;
+  s.newpos_k = (float*)(ws + L.npk_off);
+  s.newpos_q = (float*)(ws + L.npq_off);
+  s.shared_size = a->shared_size;
+  s.kept_size = a->kept_size;
+  s.chosen = a->chosen;
+  s.orig_overflow = a->orig_overflow;
+  s.kpct_meas = a->kpct_meas;
+  s.overflow20 = a->overflow20;
+  s.votes_out = a->votes;
+  s.dca_L = Lc;
+  e = launch_select(s, 1, st);
+  return e == hipSuccess ? STA_OK : hip_fail(e, "dca inter selection");
 }
 
 }  // namespace
@@ -85,6 +174,10 @@ int sta_dca_attention(const sta_dca_args* a, void* stream) {
                       a->chunk_size, mscale, 0, a->inv_freq, qrot, st);
   if (e != hipSuccess) return hip_fail(e, "dca rotation (q)");
   if ((rc = mark_event(a->stage_events, 1, st)) != STA_OK) return rc;
+  if (a->select) {
+    if ((rc = dca_select(a, L, krot, qrot, Lc, st)) != STA_OK) return rc;
+    if ((rc = mark_event(a->stage_events, 3, st)) != STA_OK) return rc;
+  }
   DcaArgs d{};
   d.qrot = qrot;
   d.krot = krot;
@@ -98,9 +191,16 @@ int sta_dca_attention(const sta_dca_args* a, void* stream) {
   d.L = Lc;
   d.scale = a->scale;
   d.out = a->out;
+  if (a->select) {
+    d.idx = a->idx;
+    d.kept_size = a->kept_size;
+    d.k_max = a->k_max;
+    d.nt64 = L.nt;
+    d.state = (float*)(ws + L.state_off);
+  }
   e = launch_dca_attn(a->dtype, a->D, d, st);
   if (e != hipSuccess) return hip_fail(e, "dca attention");
-  return mark_event(a->stage_events, 2, st);
+  return mark_event(a->stage_events, a->select ? 4 : 2, st);
 }
 
 }  // extern "C"

@@ -73,10 +73,14 @@ __global__ __launch_bounds__(256) void dca_rope_kernel(const void* __restrict__ 
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       const float ang = tf * inv_freq[i0 + e];
-      float sn, cs;
-      sincosf(ang, &sn, &cs);
-      cs = round_dt<DT>(cs * mscale);                            // table value in the model dtype
-      sn = round_dt<DT>(sn * mscale);
+      // cos / sin of the fp32 angle, correctly rounded to fp32 (through double): the table is then
+      // rounded to the model dtype, where a one-ulp difference between fp32 cosine implementations
+      // can flip a bf16 entry; the correctly rounded value is the one every implementation
+      // approximates, and the CPU oracle computes the same
+      double sd, cd;
+      sincos((double)ang, &sd, &cd);
+      float cs = round_dt<DT>((float)cd * mscale);               // table value in the model dtype
+      float sn = round_dt<DT>((float)sd * mscale);
       if (first) {                                               // x1*cos + (-x2)*sin
         const float p = round_dt<DT>(a[e] * cs), q = round_dt<DT>(-b[e] * sn);
         o[e] = round_dt<DT>(p + q);
@@ -123,7 +127,14 @@ struct DcaCfg {
   static constexpr size_t lds_bytes = (size_t)2 * (KBUF + VBUF) * 2;
 };
 
-template <int DT, int D, int G>
+// MODE 0: dense DCA attention (every causal key).
+// MODE 1 (config 4, selected inter keys): one workgroup = one 64-query selection tile (G = 2);
+//   the sweep runs over the tile's selected inter keys idx[h][t][0 .. min(kept, k_max)), gathered
+//   block by block, with the inter query variant, and leaves each row's unnormalised softmax
+//   state (o, m, l) in a.state.
+// MODE 2 (config 4, local keys): as MODE 0 over the keys of the query's own and previous chunk
+//   only ([max(0, (c - 1) L), i]), starting from the MODE 1 state of each row.
+template <int DT, int D, int G, int MODE = 0>
 __global__ __launch_bounds__(G * 64, 1) void dca_attn_kernel(DcaArgs a) {
 #pragma clang fp contract(off)
   using Cfg = DcaCfg<DT, D, G>;
@@ -162,10 +173,17 @@ __global__ __launch_bounds__(G * 64, 1) void dca_attn_kernel(DcaArgs a) {
   const int r0 = t * 32;
   const int row = r0 + q;
   const bool row_ok = tile_ok && row < N;
-  const int nblk = tile_ok ? min(r0 + 31, N - 1) / BN + 1 : 0;   // keys 0 .. last row
-  const int t_last = min(g * G + G - 1, nt - 1);
-  const int nb_wg = min(t_last * 32 + 31, N - 1) / BN + 1;
   const int cq = r0 / L;                                          // the tile's chunk
+  // MODE 1: the selection tile's valid slots; MODE 2: the first local key
+  const int nsel = MODE == 1 ? min(a.kept_size[(int64_t)h * a.nt64 + g], a.k_max) : 0;
+  const int kstart = MODE == 2 && cq >= 2 ? (cq - 1) * L : 0;
+  const int nblk = MODE == 1 ? (nsel + BN - 1) / BN
+                             : (tile_ok ? min(r0 + 31, N - 1) / BN + 1 : 0);   // keys 0 .. last row
+  const int t_last = min(g * G + G - 1, nt - 1);
+  const int nb_wg = MODE == 1 ? nblk : min(t_last * 32 + 31, N - 1) / BN + 1;
+  // MODE 2: the workgroup's sweep starts at its first tile's first local key (a multiple of 64)
+  const int b_begin = MODE == 2 ? ((g * G * 32) / L >= 2 ? ((g * G * 32) / L - 1) * L / BN : 0) : 0;
+  const int32_t* sel = MODE == 1 ? a.idx + ((int64_t)h * a.nt64 + g) * a.k_max : nullptr;
 
   // ---- query fragments of the current position variant (B operand, dims 16s + 8hf + e) ----
   u32x4 qf[KS], qfl[KS];
@@ -184,12 +202,30 @@ __global__ __launch_bounds__(G * 64, 1) void dca_attn_kernel(DcaArgs a) {
   const int64_t vhb = (int64_t)kvh * a.v_head_stride;
   u32x4 kreg[KU];
   Raw8<DT> vreg[VU][4];
+  // the key of block b's slot r: contiguous keys, or (MODE 1) the selected inter keys, with
+  // -1 past the tile's valid slots
+  auto key_of = [&](int b, int r) -> int {
+    if constexpr (MODE == 1) {
+      const int s = b * BN + r;
+      return s < nsel ? sel[s] : -1;
+    } else {
+      const int j = b * BN + r;
+      return j < N ? j : -1;
+    }
+  };
   auto load_block = [&](int b) {
-    const uint16_t* src = kt + (int64_t)b * BN * P * D;
 #pragma unroll
     for (int u = 0; u < KU; ++u) {
       const int e = tid + u * NTH;
-      if (e < Cfg::KUNITS) kreg[u] = *(const u32x4*)(src + e * 8);
+      if (e < Cfg::KUNITS) {
+        if constexpr (MODE == 1) {
+          const int r = e / (P * D / 8), rem = e % (P * D / 8);
+          const int j = key_of(b, r);
+          kreg[u] = j >= 0 ? *(const u32x4*)(kt + (int64_t)j * P * D + rem * 8) : u32x4{0, 0, 0, 0};
+        } else {
+          kreg[u] = *(const u32x4*)(kt + (int64_t)b * BN * P * D + e * 8);
+        }
+      }
     }
 #pragma unroll
     for (int u = 0; u < VU; ++u) {
@@ -197,8 +233,8 @@ __global__ __launch_bounds__(G * 64, 1) void dca_attn_kernel(DcaArgs a) {
       const int sg = e / (D / 8), dc = e % (D / 8);
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
-        const int j = b * BN + sg * 4 + k;
-        if (e < Cfg::VUNITS && j < N) vreg[u][k].load(a.v, vhb + (int64_t)j * a.v_tok_stride + dc * 8);
+        const int j = e < Cfg::VUNITS ? key_of(b, sg * 4 + k) : -1;
+        if (j >= 0) vreg[u][k].load(a.v, vhb + (int64_t)j * a.v_tok_stride + dc * 8);
         else vreg[u][k].zero();
       }
     }
@@ -249,19 +285,39 @@ __global__ __launch_bounds__(G * 64, 1) void dca_attn_kernel(DcaArgs a) {
 #pragma unroll
   for (int rb = 0; rb < RBS; ++rb) oacc[rb] = floatx16{};
   float mR = -INFINITY, l_i = 0.0f;
+  // state row of this lane's query (D + 4 floats, 16-byte rows): o (unnormalised), m, l
+  float* srow = (MODE != 0 && row_ok) ? a.state + ((int64_t)h * a.Npad + row) * (D + 4) : nullptr;
+  if constexpr (MODE == 2) {
+    if (srow) {
+#pragma unroll
+      for (int rb = 0; rb < RBS; ++rb)
+#pragma unroll
+        for (int g4 = 0; g4 < 4; ++g4) {
+          const float4 o = *(const float4*)(srow + rb * 32 + g4 * 8 + 4 * hf);
+          oacc[rb][g4 * 4 + 0] = o.x;
+          oacc[rb][g4 * 4 + 1] = o.y;
+          oacc[rb][g4 * 4 + 2] = o.z;
+          oacc[rb][g4 * 4 + 3] = o.w;
+        }
+      mR = srow[D];
+      l_i = srow[D + 1];
+    }
+  }
 
-  load_block(0);
-  store_block(0);
+  if (b_begin < nb_wg) {
+    load_block(b_begin);
+    store_block(b_begin & 1);
+  }
   __syncthreads();
 
-  for (int b = 0; b < nb_wg; ++b) {
+  for (int b = b_begin; b < nb_wg; ++b) {
     const int p = b & 1;
     const bool more = b + 1 < nb_wg;
     if (more) load_block(b + 1);
-    if (tile_ok && b < nblk) {
+    if (tile_ok && b < nblk && b * BN >= kstart) {
       const int start = b * BN;
       const int di = cq - start / L;                               // chunk distance of the block
-      const int var = di == 0 ? 0 : (di == 1 ? 1 : 2);
+      const int var = MODE == 1 ? 2 : (di == 0 ? 0 : (di == 1 ? 1 : 2));
       if (var != cur_var) {                                        // inter -> succ -> intra
         load_q(var);
         cur_var = var;
@@ -287,15 +343,16 @@ __global__ __launch_bounds__(G * 64, 1) void dca_attn_kernel(DcaArgs a) {
           }
         }
       }
-      // causal mask only where the block reaches the tile's rows (intra chunk, :411-413)
-      const bool diag = start + BN - 1 > r0;
+      // causal mask only where the block reaches the tile's rows (intra chunk, :411-413); the
+      // selected inter keys all precede the tile, only slots past the valid ones are masked
+      const bool diag = MODE == 1 ? start + BN > nsel : start + BN - 1 > r0;
       float bmax = -INFINITY;
 #pragma unroll
       for (int sb = 0; sb < NSB; ++sb)
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
           const int key = start + sb * 32 + (i >> 2) * 8 + 4 * hf + (i & 3);
-          const bool ok = !diag || key <= row;
+          const bool ok = !diag || (MODE == 1 ? key < nsel : key <= row);
           const float v = ok ? sacc[sb][i] * a.scale : -INFINITY;
           sacc[sb][i] = v;
           bmax = fmaxf(bmax, v);
@@ -359,6 +416,21 @@ __global__ __launch_bounds__(G * 64, 1) void dca_attn_kernel(DcaArgs a) {
     __syncthreads();
   }
 
+  if constexpr (MODE == 1) {
+    if (srow) {
+#pragma unroll
+      for (int rb = 0; rb < RBS; ++rb)
+#pragma unroll
+        for (int g4 = 0; g4 < 4; ++g4)
+          *(float4*)(srow + rb * 32 + g4 * 8 + 4 * hf) =
+              make_float4(oacc[rb][g4 * 4], oacc[rb][g4 * 4 + 1], oacc[rb][g4 * 4 + 2], oacc[rb][g4 * 4 + 3]);
+      if (hf == 0) {
+        srow[D] = mR;
+        srow[D + 1] = l_i;
+      }
+    }
+    return;
+  }
   if (row_ok) {
     const int64_t ob = ((int64_t)h * N + row) * D;
 #pragma unroll
@@ -421,17 +493,27 @@ size_t dca_lds_bytes(int dtype, int D) {
   return 0;
 }
 
-template <int DT, int D>
-static hipError_t launch_dca_attn_t(const DcaArgs& a, hipStream_t st) {
-  using Cfg = DcaCfg<DT, D, kDcaTiles>;
-  hipError_t e = hipFuncSetAttribute((const void*)dca_attn_kernel<DT, D, kDcaTiles>,
+template <int DT, int D, int G, int MODE>
+static hipError_t launch_dca_attn_g(const DcaArgs& a, hipStream_t st) {
+  using Cfg = DcaCfg<DT, D, G>;
+  hipError_t e = hipFuncSetAttribute((const void*)dca_attn_kernel<DT, D, G, MODE>,
                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)Cfg::lds_bytes);
   if (e != hipSuccess) return e;
   const int nt = (a.N + 31) / 32;
-  const int ngroups = (nt + kDcaTiles - 1) / kDcaTiles;
-  hipLaunchKernelGGL((dca_attn_kernel<DT, D, kDcaTiles>), dim3(a.H * ngroups), dim3(Cfg::NTH), Cfg::lds_bytes,
+  const int ngroups = (nt + G - 1) / G;
+  hipLaunchKernelGGL((dca_attn_kernel<DT, D, G, MODE>), dim3(a.H * ngroups), dim3(Cfg::NTH), Cfg::lds_bytes,
                      st, a);
   return hipGetLastError();
+}
+
+// dense (a.state == null), or config 4's two sweeps: the selected inter keys of each 64-query
+// tile (two waves per workgroup), then the local keys from the partial states
+template <int DT, int D>
+static hipError_t launch_dca_attn_t(const DcaArgs& a, hipStream_t st) {
+  if (!a.state) return launch_dca_attn_g<DT, D, kDcaTiles, 0>(a, st);
+  hipError_t e = launch_dca_attn_g<DT, D, 2, 1>(a, st);
+  if (e != hipSuccess) return e;
+  return launch_dca_attn_g<DT, D, kDcaTiles, 2>(a, st);
 }
 
 hipError_t launch_dca_attn(int dtype, int D, const DcaArgs& a, hipStream_t st) {

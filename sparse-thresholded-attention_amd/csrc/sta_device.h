@@ -235,6 +235,21 @@ __device__ __forceinline__ void fast_sincos(float x, float& s, float& c) {
   c = __builtin_amdgcn_cosf(t);
 }
 
+// The smallest float x with fl(x * c) >= thr, for c > 0: fl(x * c) is monotone in x, so
+// acc >= x0 <=> fl(acc * c) >= thr, the reference's keep test on the scaled score with one
+// compare on the raw dot.  Non-finite thresholds pass through.
+__device__ __forceinline__ float min_arg_for(float thr, float c) {
+#pragma clang fp contract(off)
+  if (thr != thr || thr == -INFINITY || thr == INFINITY) return thr;
+  float x = thr / c;
+  for (int i = 0; i < 4; ++i) {
+    const float y = nextafterf(x, -INFINITY);
+    if (y * c >= thr) x = y; else break;
+  }
+  for (int i = 0; i < 4 && !(x * c >= thr); ++i) x = nextafterf(x, INFINITY);
+  return x;
+}
+
 // 16 bytes per lane from global memory straight into LDS, lane l's bytes at lds_base + 16 l
 // (global_load_lds_dwordx4; lds_base is wave-uniform and goes to M0).  Issued through inline
 // assembly so that the compiler does not track it as an LDS write: its own wait insertion would

@@ -73,6 +73,10 @@ struct SelectArgs {
   int32_t* votes_out;     // optional dense int32 copy (H, nt, N)
   const float* wvotes;    // weighted ranking: (H, nt, votes_stride) margin / expmass votes
   float* wvotes_out;      // optional dense fp32 copy (H, nt, N) of the weighted votes
+  int dca_L;              // > 0: DCA inter-key selection -- tile t of chunk c = tstart / dca_L
+                          // selects among its inter keys [0, max(0, (c - 1) dca_L)) as if they
+                          // were the whole key axis (N and K_ord per tile; the local window then
+                          // falls outside it); 0: the shared selection over [0, N)
 };
 
 struct GatherArgs {
@@ -136,7 +140,26 @@ struct DcaArgs {
   int H, Hkv, N, Npad, L;
   float scale;
   void* out;                // (H, N, D)
+  // config 4 (selected inter keys + dense local keys); state == null: dense DCA
+  const int32_t* idx;       // (H, nt64, k_max) each 64-query tile's selected inter keys
+  const int32_t* kept_size; // (H, nt64) its selected count (slots past min(kept, k_max) unused)
+  int k_max, nt64;
+  float* state;             // (H, Npad, D + 4) per row: unnormalised o (D), running max, sum
 };
+
+// config 4's selection over DCA's inter-chunk keys (sta_dca_sel.hip)
+struct DcaVoteArgs {
+  const uint16_t* qrot;   // (3, H, Npad, P, D) rotated queries; variant 2 = the inter position
+  const uint16_t* krot;   // (Hkv, Npad, P, D) rotated keys
+  int H, Hkv, N, Npad, L, nt;   // nt: 64-query tiles
+  float scale;
+  const float* tau;       // (H,)
+  float* rmax;            // (H, Npad) raw maxima over the inter keys (pass 0 writes, pass 1 reads)
+  float* row_max;         // (H, N) or null: fl(max * scale), -inf where a row has no inter keys
+  uint8_t* votes;         // (H, nt, votes_stride): tile t's votes for its inter keys [0, ext_t)
+  int64_t votes_stride;
+};
+hipError_t launch_dca_votes(int dtype, int D, const DcaVoteArgs& a, hipStream_t st);
 
 // decode: Q queries over one cache of M keys, query i at position q_pos0 + i seeing keys
 // [0, M - (Q - 1 - i)): shared_selection_triton_exact_2.py:235-271, 505-655

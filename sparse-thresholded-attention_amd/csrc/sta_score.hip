@@ -173,17 +173,6 @@ __global__ __launch_bounds__(1024) void norm_max_kernel(const float2* __restrict
 // >= m - tau.  fl(x * c) is monotone in x for c > 0, so acc >= x0 <=> fl(acc * sm_scale) >=
 // fl(m - tau), exactly the reference's keep test (exact_2.py:121), with one compare per score.
 // ------------------------------------------------------------------------------------------
-__device__ __forceinline__ float min_arg_for(float thr, float c) {
-#pragma clang fp contract(off)
-  if (thr != thr || thr == -INFINITY || thr == INFINITY) return thr;
-  float x = thr / c;
-  for (int i = 0; i < 4; ++i) {
-    const float y = nextafterf(x, -INFINITY);
-    if (y * c >= thr) x = y; else break;
-  }
-  for (int i = 0; i < 4 && !(x * c >= thr); ++i) x = nextafterf(x, INFINITY);
-  return x;
-}
 
 #define STA_GLOBAL(p) ((const __attribute__((address_space(1))) void*)(p))
 #define STA_LDS(p) ((__attribute__((address_space(3))) void*)(p))

@@ -77,12 +77,41 @@ __global__ __launch_bounds__(256) void select_kernel(SelectArgs a) {
   extern __shared__ __align__(16) uint8_t smem[];
   const int tid = threadIdx.x;
   const int h = blockIdx.x / a.nt, t = blockIdx.x % a.nt;
-  const int N = a.N, T = a.T;
+  const int T = a.T;
   const int64_t tstart = (int64_t)a.q_pos_base + (int64_t)t * T;          // exact_2.py:291
+  // the key axis: [0, N); under DCA inter selection the tile's inter keys, with the budget's
+  // K_ord = max(1, min(N, ceil(start_pct / 100 N))) of that axis (exact_2.py:320)
+  int N = a.N;
+  int64_t K_ord = a.K_ord;
+  if (a.dca_L > 0) {
+    const int64_t c = tstart / a.dca_L;
+    N = c >= 2 ? (int)min((int64_t)a.N, (c - 1) * a.dca_L) : 0;
+    K_ord = (int64_t)ceil((double)a.start_pct / 100.0 * (double)N);
+    K_ord = K_ord > N ? N : (K_ord < 1 ? 1 : K_ord);
+    if (N == 0) {                 // no inter keys (the first two chunks): an empty set
+      const int o = h * a.nt + t;
+      if (threadIdx.x == 0) {
+        a.shared_size[o] = 0;
+        a.kept_size[o] = 0;
+        a.chosen[o] = 0;
+        a.orig_overflow[o] = 0;
+        a.overflow20[o] = 0;
+        a.kpct_meas[o] = 0;
+      }
+      for (int s = threadIdx.x; s < a.k_max; s += 256) {
+        a.idx[(int64_t)o * a.k_max + s] = 0;
+        a.newpos_k[(int64_t)o * a.k_max + s] = 0.0f;
+      }
+      for (int i = threadIdx.x; i < T; i += 256) a.newpos_q[(int64_t)o * T + i] = 0.0f;
+      if (a.votes_out)
+        for (int j = threadIdx.x; j < a.N; j += 256) a.votes_out[(int64_t)o * a.N + j] = 0;
+      return;
+    }
+  }
   // votes are read for keys [0, hi_keys); Kernel A leaves keys past the tile's causal end
   // unwritten (their count is 0), a caller-supplied dense tensor is read in full
   const int hi_keys = a.votes_dense ? N : (int)min((int64_t)N, tstart + T);
-  const int per = ((((N + 255) / 256) + 15) / 16) * 16;                    // keys per thread, x16
+  const int per = ((((a.N + 255) / 256) + 15) / 16) * 16;                  // keys per thread, x16
   uint8_t* vb = smem;                                                       // 256 * per vote bytes
   int* hist = (int*)(smem + 256 * per);                                     // 256 bins -> C[v] (257)
   int* fhist = hist + 260;                                                  // 256 bins -> F[v] (257)
@@ -113,8 +142,8 @@ __global__ __launch_bounds__(256) void select_kernel(SelectArgs a) {
   }
   __syncthreads();
   if (a.votes_out) {
-    int32_t* vo = a.votes_out + ((int64_t)h * a.nt + t) * N;
-    for (int j = tid; j < N; j += 256) vo[j] = vb[j];
+    int32_t* vo = a.votes_out + ((int64_t)h * a.nt + t) * a.N;
+    for (int j = tid; j < a.N; j += 256) vo[j] = vb[j];
   }
   // Thread tid owns keys [tid * per, tid * per + per) for the histogram and the compaction; its
   // vote bytes are read 16 at a time.
@@ -177,7 +206,7 @@ __global__ __launch_bounds__(256) void select_kernel(SelectArgs a) {
     for (int si = 0; si < a.nsteps; ++si) {             // exact_2.py:328-342
       const int p = a.steps[si];
       int64_t bi = budget_of(p, usize) - 1;
-      bi = bi < 0 ? 0 : (bi > a.K_ord - 1 ? a.K_ord - 1 : bi);
+      bi = bi < 0 ? 0 : (bi > K_ord - 1 ? K_ord - 1 : bi);
       const int v_cut = cut_for(C, bi + 1);             // sv[bi] (exact_2.py:330)
       const int64_t size = (int64_t)C[v_cut] + F[v_cut];
       if (p == a.start_pct) oflow = size > a.k_max;
@@ -195,7 +224,7 @@ __global__ __launch_bounds__(256) void select_kernel(SelectArgs a) {
       const int floor_pct = a.steps[a.nsteps - 1];
       for (int p = floor_pct - 1; p > 0; --p) {
         int64_t bi = budget_of(p, usize) - 1;
-        bi = bi < 0 ? 0 : (bi > a.K_ord - 1 ? a.K_ord - 1 : bi);
+        bi = bi < 0 ? 0 : (bi > K_ord - 1 ? K_ord - 1 : bi);
         const int v_cut = cut_for(C, bi + 1);
         if ((int64_t)C[v_cut] + F[v_cut] <= a.k_max) { kmeas = p; break; }
       }

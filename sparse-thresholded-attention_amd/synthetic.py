@@ -77,7 +77,8 @@ class Config:
     n_global: int = 32
     n_local: int = 32
     variant: str = "shared"     # "shared" (tile-shared sets), "pq" (PQ Union), "perquery" (own sets
-                                # per query, capped by score), "pqstream", "dca"
+                                # per query, capped by score), "pqstream", "dca" (dense DCA),
+                                # "dca_select" (DCA + selection over the inter-chunk keys)
     select_score: str = "freq"  # key ranking: votes, or margin / expmass weighted votes
     dca: tuple = None           # (chunk_size, pretrain_len, local_window) of the DCA variant
     decode_q: int = 1           # decode variant: queries per step (the last decode_q positions)
@@ -129,8 +130,13 @@ CONFIGS = {
     # decode at config 2's shape: GQA 32q / 8kv over a 32768-key cache, YaRN geometry
     "c2d": Config("c2d_decode_yarn_32q8kv_d128_32k_bf16", 32, 8, 32768, 128, torch.bfloat16, 64, 5.0, 0.005,
                   500000.0, 1.0, yarn=(4.0, 8192, 32.0, 1.0), variant="decode"),
-    # 4: dual chunk attention at 64k: chunk 4096, local window 512, pretraining length 4096
-    #    (chunk_len 3584), base RoPE, dense causal attention with remapped positions
-    "c4": Config("c4_dca_32h_d128_64k_bf16", 32, 32, 65536, 128, torch.bfloat16, 64, 5.0, 0.0025,
-                 10000.0, 1.0, variant="dca", dca=(4096, 4096, 512)),
+    # 4: dual chunk attention at 64k (chunk 4096, local window 512, pretraining length 4096, so
+    #    chunk_len 3584; base RoPE) with exact-max threshold selection (tau 5, tile 64, top 30%,
+    #    2048 cap) over each tile's inter-chunk keys and dense attention over its own and the
+    #    previous chunk
+    "c4": Config("c4_dca_select_32h_d128_64k_bf16", 32, 32, 65536, 128, torch.bfloat16, 64, 5.0, 0.0025,
+                 10000.0, 1.0, variant="dca_select", dca=(4096, 4096, 512)),
+    # 4d: the same shape through the reference's dense DCA (every causal key, remapped positions)
+    "c4d": Config("c4d_dca_dense_32h_d128_64k_bf16", 32, 32, 65536, 128, torch.bfloat16, 64, 5.0, 0.0025,
+                  10000.0, 1.0, variant="dca", dca=(4096, 4096, 512)),
 }
