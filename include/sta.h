@@ -344,6 +344,12 @@ int sta_dca_attention(const sta_dca_args* args, void* stream);
  *   (prefill_mode="perquery", perquery.py:905-924). */
 #define STA_RULE_SHARED 0
 #define STA_RULE_PQ 1
+/* STA_RULE_STREAM: _decode_build_sets_pqs of PQ Stream (pqstream_kernel.py:695-797): every passer
+ *   and forced key (no cap: give k_max >= M, the reference's buffer rounds M up to 1024), at
+ *   streamed positions -- blocks of block_n keys aligned at 0 walked from the query backwards, key
+ *   j of block b at newpos = -(kept keys after b + min(q_pos, end of b) - j), newpos_q = 0; attend
+ *   with rope_scale_c = 1 and the base inv_freq_c (_decode_attend_torch / _triton, :800-850). */
+#define STA_RULE_STREAM 2
 
 typedef struct sta_decode_args {
   const void* q;            /* (H, Q, D) raw queries */
@@ -362,7 +368,7 @@ typedef struct sta_decode_args {
   float rope_scale_c, sm_scale;
   int32_t q_pos0;           /* position of query 0; q_pos0 + Q <= M (any q_pos0 >= 0 for the
                                scores alone) */
-  int32_t n_global, n_local, k_max;   /* k_max <= 16384 */
+  int32_t n_global, n_local, k_max;   /* k_max <= 65536 */
   double pct_decode;        /* the reference's pct_decode (100 = keep every passer) */
   int32_t causal;           /* attend: 0 masks sentinel slots only (_decode_attend_torch); 1 also
                                slots past the query's position (Kernel C, _decode_attend_kernelC) */
@@ -378,10 +384,11 @@ typedef struct sta_decode_args {
   size_t workspace_bytes;
   void* const* stage_events; /* NULL or 4 hipEvent_t: before the scores, before the selection,
                                 before the attend, after it */
-  /* ABI 3: the selection rule and its per-query counters */
-  int32_t rule;             /* STA_RULE_SHARED or STA_RULE_PQ */
+  /* ABI 3: the selection rule, its per-query counters and PQ Stream's position blocks */
+  int32_t rule;             /* STA_RULE_SHARED, STA_RULE_PQ or STA_RULE_STREAM */
   int32_t* usize;           /* (H, Q) or NULL: STA_RULE_PQ, |threshold passers| before the forced keys */
   uint8_t* overflow;        /* (H, Q) or NULL: STA_RULE_PQ, 1 where passers U forced exceed k_max */
+  int32_t block_n;          /* STA_RULE_STREAM: keys per position block */
 } sta_decode_args;
 
 /* Bytes of device workspace the decode entry points need for these arguments. */

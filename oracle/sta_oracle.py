@@ -526,6 +526,27 @@ def decode_build_sets_pq(scores, tau, q_pos0, n_global, n_local, k_max):
     return idx, npk, npq, size, us, ov.astype(bool)
 
 
+def decode_build_sets_pqs(scores, tau, q_pos0, n_global, n_local, block_n, k_max=None):
+    """_decode_build_sets_pqs (pqstream_kernel.py:695-797) from scores (H,Q,M) -> idx (H,Q,k_max)
+    int32 (sentinel m_i), newpos_k (streamed, -dist), newpos_q (0), set_size, span (H,Q) fp32 and
+    skipped (H,Q).  k_max defaults to the reference's buffer, M rounded up to a multiple of 1024."""
+    scores = _c(scores, np.float32)
+    H, Q, M = scores.shape
+    if k_max is None:
+        k_max = max(1024, -(-M // 1024) * 1024)
+    idx = np.empty((H, Q, k_max), np.int32)
+    npk = np.empty((H, Q, k_max), np.float32)
+    npq = np.empty((H, Q), np.float32)
+    size = np.empty((H, Q), np.int32)
+    span = np.empty((H, Q), np.float32)
+    skp = np.empty((H, Q), np.int32)
+    lib().oracle_decode_build_sets_pqs(_p(scores), ctypes.c_int(H), ctypes.c_int(Q), ctypes.c_int(M),
+                                       _p(_c(tau, np.float32)), ctypes.c_int(q_pos0), ctypes.c_int(n_global),
+                                       ctypes.c_int(n_local), ctypes.c_int(block_n), ctypes.c_int(k_max), _p(idx),
+                                       _p(npk), _p(npq), _p(size), _p(span), _p(skp))
+    return idx, npk, npq, size, span, skp
+
+
 def decode_attend(q, k, v, dtype, inv_freq, rope_scale, sm_scale, q_pos0, idx, newpos_k, newpos_q,
                   causal=False):
     """Attention of each query over its slots -> (H,Q,D) fp32 before the cast to the dtype."""

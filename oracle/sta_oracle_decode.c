@@ -14,6 +14,8 @@
  *                               rope_scale 1 and the dense ranks of the per-query rule it is
  *                               shared_selection_triton_perquery.py:723-740 (_decode_attend_torch_pq)
  *                               and :743-778 (_decode_attend_kernelC_pq)
+ *   oracle_decode_build_sets_pqs <- pqstream_kernel.py:695-797 (_decode_build_sets_pqs): every
+ *                               passer and forced key, streamed positions over aligned blocks
  *   oracle_decode_build_sets_pq <- shared_selection_triton_perquery.py:651-720
  *                               (_decode_build_sets_pq): no top-pct cut, the k_max cap as forced +
  *                               the top-(k_max - n_forced) non-forced keys by score with an exact
@@ -358,5 +360,81 @@ void oracle_decode_build_sets_pq(const float* scores, int H, int Q, int M, const
     free(fin);
     free(forced);
     free(rank0);
+  }
+}
+
+/*
+ * _decode_build_sets_pqs (pqstream_kernel.py:695-797) from given scores (H, Q, M), batched like
+ * oracle_decode_build_sets (query i at q_pos0 + i over the keys [0, m_i)).
+ *   keep = s >= fl(max - tau), plus the forced global / local / self keys; no cap   (:727-734)
+ *   streamed positions (:736-749): blocks of block_n keys aligned at 0; c[b] = kept keys of block
+ *   b; d[b] = kept keys of the blocks after b (nearer the query); a key j of block b sits at
+ *   dist = d[b] + (min(q_pos, b block_n + block_n - 1) - j), newpos_k = -dist (fp32, -0 for the
+ *   query itself), newpos_q = 0
+ *   idx: every kept key ascending, then the sentinel m_i up to k_max slots (the reference's kbuf)
+ * set_size (H, Q) = kept count; span (H, Q) fp32 = the largest dist among kept keys; skipped (H, Q)
+ * = blocks without a kept key (the reference's decode counters, :786-791).  Pointers after
+ * newpos_q may be NULL.
+ */
+void oracle_decode_build_sets_pqs(const float* scores, int H, int Q, int M, const float* tau, int q_pos0,
+                                  int n_global, int n_local, int block_n, int k_max, int32_t* idx,
+                                  float* newpos_k, float* newpos_q, int32_t* set_size, float* span,
+                                  int32_t* skipped) {
+#pragma omp parallel
+  {
+    uint8_t* kp = (uint8_t*)malloc((size_t)M);
+    int32_t* cnt = (int32_t*)malloc(sizeof(int32_t) * ((size_t)M / (block_n > 0 ? block_n : 1) + 2));
+#pragma omp for schedule(dynamic, 1)
+    for (int hi = 0; hi < H * Q; ++hi) {
+      const int h = hi / Q, i = hi % Q;
+      const int m = M - (Q - 1 - i);
+      const int p = q_pos0 + i;
+      const float* s = scores + ((size_t)h * Q + i) * M;
+      float mx = -INFINITY;
+      for (int j = 0; j < m; ++j) mx = s[j] > mx ? s[j] : mx;
+      volatile float thr = mx - tau[h];
+      const int g = n_global < m ? n_global : m;
+      int lo = p - n_local + 1;
+      if (lo < 0) lo = 0;
+      const int nblk = (m + block_n - 1) / block_n;
+      for (int b = 0; b < nblk; ++b) cnt[b] = 0;
+      int total = 0;
+      for (int j = 0; j < m; ++j) {
+        kp[j] = (uint8_t)(s[j] >= thr || j < g || (j >= lo && j <= p) || j == p);
+        cnt[j / block_n] += kp[j];
+        total += kp[j];
+      }
+      int32_t* irow = idx + ((size_t)h * Q + i) * k_max;
+      float* nrow = newpos_k + ((size_t)h * Q + i) * k_max;
+      int after = 0, r = total, skip = 0;
+      float sp = 0.0f;
+      /* descending blocks: d[b] = kept keys of the blocks after b */
+      for (int b = nblk - 1; b >= 0; --b) {
+        skip += cnt[b] == 0;
+        const int hb = (b * block_n + block_n - 1) < p ? b * block_n + block_n - 1 : p;
+        const int j1 = (b * block_n + block_n) < m ? b * block_n + block_n : m;
+        for (int j = j1 - 1; j >= b * block_n; --j) {
+          if (!kp[j]) continue;
+          --r;
+          volatile float dist = (float)after + (float)(hb - j);
+          if (dist > sp) sp = dist;
+          if (r < k_max) {
+            irow[r] = j;
+            nrow[r] = -dist;
+          }
+        }
+        after += cnt[b];
+      }
+      for (int u = total; u < k_max; ++u) {
+        irow[u] = m;
+        nrow[u] = 0.0f;
+      }
+      newpos_q[(size_t)h * Q + i] = 0.0f;
+      if (set_size) set_size[(size_t)h * Q + i] = total;
+      if (span) span[(size_t)h * Q + i] = sp;
+      if (skipped) skipped[(size_t)h * Q + i] = skip;
+    }
+    free(kp);
+    free(cnt);
   }
 }

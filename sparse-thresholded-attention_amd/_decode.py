@@ -62,7 +62,7 @@ def decode_attend(q, K, V, idx, newpos_k, newpos_q, inv_freq, rope_scale, sm_sca
 
 def decode_attention(q, k, v, tau, inv_freq, q_pos0, pos_scale=1.0, rope_scale=1.0, sm_scale=None, n_global=32,
                      n_local=32, k_max=1024, pct_decode=100.0, causal=False, inv_freq_c=None, pos_scale_c=None,
-                     rope_scale_c=None, rule="shared", stats=None):
+                     rope_scale_c=None, rule="shared", stats=None, block_n=32):
     """Q queries q (1, H, Q, D) or (H, Q, D) at positions q_pos0 .. q_pos0 + Q - 1 over the cache
     k, v (1, Hkv, M, D) with q_pos0 + Q <= M; query i sees the keys [0, M - (Q - 1 - i)).
     Returns out (H, Q, D) in q.dtype -- the decode branch of spi_forward (exact_2.py:734-762)
@@ -75,7 +75,9 @@ def decode_attention(q, k, v, tau, inv_freq, q_pos0, pos_scale=1.0, rope_scale=1
         sm_scale = 1.0 / math.sqrt(qh.shape[-1])
     r = native.decode_attention(qh, k, v, _tau_of(tau, qh.shape[0]), inv_freq, q_pos0, pos_scale, rope_scale,
                                 sm_scale, n_global, n_local, k_max, pct_decode, causal, inv_freq_c=inv_freq_c,
-                                pos_scale_c=pos_scale_c, rope_scale_c=rope_scale_c, rule=rule)
+                                pos_scale_c=pos_scale_c, rope_scale_c=rope_scale_c, rule=rule, block_n=block_n)
     if stats is not None and rule == "pq":
         stats["usize"], stats["overflow"] = r["usize"], r["overflow"]
+    if stats is not None and rule == "stream":
+        stats.update(idx=r["idx"], newpos_k=r["newpos_k"], set_size=r["set_size"])
     return r["out"]

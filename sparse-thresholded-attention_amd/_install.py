@@ -246,3 +246,99 @@ def pq_forward(self, hidden_states, position_embeddings=None, attention_mask=Non
         out = torch.cat(outs, dim=1).unsqueeze(0)
     attn_output = out.transpose(1, 2).reshape(B, N, -1).contiguous()
     return self.o_proj(attn_output), None
+
+
+# ---------------------------------------------------------------------------------------------
+# the PQ Stream file's model integration (pqstream_kernel.py:834-998)
+# ---------------------------------------------------------------------------------------------
+def install_pqstream(model, select_geom, apply_mscale, context_window, n_global, n_local, tile, block_n, block_k,
+                     max_len, decode_backend, prefill_mode, pos_advance, use_skip):
+    """Selection under select_geom ("pi": base frequencies at positions compressed by the frozen
+    pos_scale; "yarn": the rotary frequencies as loaded at raw positions, the attention scaling
+    as the rope scale when apply_mscale); attention under base RoPE at the streamed positions
+    (pqstream_kernel.py:856-917)."""
+    import transformers.models.llama.modeling_llama as ml
+    rotary = model.model.rotary_emb
+    inv_freq_rot = rotary.inv_freq.detach().float()
+    attn_scaling = float(getattr(rotary, "attention_scaling", 1.0))
+    inv_freq_base = base_inv_freq_of(model)
+    if select_geom == "yarn":
+        inv_freq_a, rope_scale_a = inv_freq_rot, (attn_scaling if apply_mscale else 1.0)
+    else:
+        inv_freq_a, rope_scale_a = inv_freq_base, 1.0
+    assert inv_freq_base.numel() == inv_freq_a.numel(), \
+        f"inv_freq length mismatch: {inv_freq_base.numel()} vs {inv_freq_a.numel()}"
+    for li, layer in enumerate(model.model.layers):
+        sa = layer.self_attn
+        dev = sa.q_proj.weight.device
+        sa.pqs_inv_freq_a = inv_freq_a.to(dev)
+        sa.pqs_rope_scale_a = rope_scale_a
+        sa.pqs_inv_freq_c = inv_freq_base.to(dev)
+        sa.pqs_geom = select_geom
+        sa.pqs_W = context_window
+        sa.pqs_ng = n_global
+        sa.pqs_nl = n_local
+        sa.pqs_tile = tile
+        sa.pqs_block_n = block_n
+        sa.pqs_block_k = block_k
+        sa.pqs_layer_idx = getattr(sa, "layer_idx", li)
+        sa.pqs_max_len = max_len
+        sa.pqs_pos_scale_a = None
+        sa.pqs_advance = pos_advance
+        sa.pqs_use_skip = bool(use_skip)
+        sa.pqs_decode_backend = decode_backend
+        sa.pqs_prefill_mode = prefill_mode
+    ml.LlamaAttention.forward = pqs_forward
+
+
+def pqs_forward(self, hidden_states, position_embeddings=None, attention_mask=None, past_key_values=None,
+                **kwargs):
+    import pqstream_kernel as pqs
+    B, N, _ = hidden_states.shape
+    assert B == 1, "batch size must be 1 (the kernels take one sequence, as the reference's)"
+    hs = (B, N, -1, self.head_dim)
+    q = self.q_proj(hidden_states).view(hs).transpose(1, 2)
+    k = self.k_proj(hidden_states).view(hs).transpose(1, 2)
+    v = self.v_proj(hidden_states).view(hs).transpose(1, 2)
+    cache = past_key_values if past_key_values is not None else kwargs.get("past_key_value", None)
+    past_len = 0
+    if cache is not None:
+        try:
+            past_len = int(cache.get_seq_length(self.pqs_layer_idx))
+        except TypeError:
+            past_len = int(cache.get_seq_length())
+        k, v = cache.update(k, v, self.pqs_layer_idx)
+    if past_len == 0:
+        if self.pqs_geom == "yarn":
+            self.pqs_pos_scale_a = 1.0
+        else:
+            L_target = self.pqs_max_len if self.pqs_max_len is not None else N
+            self.pqs_pos_scale_a = min(1.0, self.pqs_W / float(L_target))
+    if past_len == 0 and self.pqs_prefill_mode == "stream":
+        out, span, kept, blocks, skipped = pqs.pqstream_attention(
+            q, k, v, self.tau_head_vec, self.pqs_inv_freq_a, self.pqs_inv_freq_c,
+            pos_scale_a=self.pqs_pos_scale_a, rope_scale_a=self.pqs_rope_scale_a, sm_scale=self.scaling,
+            n_global=self.pqs_ng, n_local=self.pqs_nl, tile=self.pqs_tile, block_n=self.pqs_block_n,
+            pos_advance=self.pqs_advance, q_pos_base=past_len, use_skip=self.pqs_use_skip)
+        self.pqs_last_span = span.detach()
+        self.pqs_last_kept = kept.detach()
+        self.pqs_last_skipped = skipped.detach()
+    else:
+        # each query at position past_len + i over the keys [0, past_len + i], the stream rule; the
+        # slot buffer is the batch's cache length rounded up to 1024
+        causal = self.pqs_decode_backend == "triton"
+        outs = []
+        for c0 in range(0, N, PER_QUERY_BATCH):
+            c1 = min(N, c0 + PER_QUERY_BATCH)
+            M = past_len + c1
+            st = {}
+            outs.append(decode_attention(
+                q[0, :, c0:c1, :], k[:, :, :M, :], v[:, :, :M, :], self.tau_head_vec, self.pqs_inv_freq_a,
+                past_len + c0, self.pqs_pos_scale_a, self.pqs_rope_scale_a, self.scaling, self.pqs_ng,
+                self.pqs_nl, pqs._kbuf(M), 100.0, causal, inv_freq_c=self.pqs_inv_freq_c, pos_scale_c=1.0,
+                rope_scale_c=1.0, rule="stream", stats=st, block_n=self.pqs_block_n))
+            m = torch.arange(past_len + c0 + 1, M + 1, device=q.device)
+            pqs._record_decode(st["idx"], st["newpos_k"], st["set_size"], m, self.pqs_block_n)
+        out = torch.cat(outs, dim=1).unsqueeze(0)
+    attn_output = out.transpose(1, 2).reshape(B, N, -1).contiguous()
+    return self.o_proj(attn_output), None

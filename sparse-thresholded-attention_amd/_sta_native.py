@@ -140,10 +140,11 @@ class DecodeArgsC(ctypes.Structure):
         ("workspace", ctypes.c_void_p), ("workspace_bytes", ctypes.c_size_t),
         ("stage_events", ctypes.c_void_p),
         ("rule", ctypes.c_int32), ("usize", ctypes.c_void_p), ("overflow", ctypes.c_void_p),
+        ("block_n", ctypes.c_int32),
     ]
 
 
-RULES = {"shared": 0, "pq": 1}    # STA_RULE_SHARED / STA_RULE_PQ
+RULES = {"shared": 0, "pq": 1, "stream": 2}    # STA_RULE_SHARED / STA_RULE_PQ / STA_RULE_STREAM
 
 
 def lib():
@@ -820,12 +821,14 @@ class DecodePlan:
 
     def __init__(self, q, k, v, tau, inv_freq, q_pos0, pos_scale=1.0, rope_scale=1.0, sm_scale=None,
                  n_global=32, n_local=32, k_max=1024, pct_decode=100.0, causal=False, want_scores=False,
-                 inv_freq_c=None, pos_scale_c=None, rope_scale_c=None, rule="shared"):
+                 inv_freq_c=None, pos_scale_c=None, rope_scale_c=None, rule="shared", block_n=32):
         """inv_freq / pos_scale / rope_scale: the selection geometry; the *_c triple (default: the
         same) repositions (pos_scale_c) and attends (inv_freq_c, rope_scale_c).  rule "shared" is
         _decode_build_sets (exact_2.py:527-604), "pq" _decode_build_sets_pq (perquery.py:651-720:
         dense ranks, exact cap budget; pass rope_scale_c=1 and the base inv_freq_c); "pq" also
-        fills usize and overflow (H, Q)."""
+        fills usize and overflow (H, Q).  "stream" is _decode_build_sets_pqs (pqstream_kernel.py:
+        695-797: every passer and forced key, no cap, streamed positions over blocks of block_n
+        keys walked back from the query; k_max is the slot buffer, M rounded up to 1024)."""
         if not q.is_cuda:
             raise RuntimeError("sparse-thresholded attention runs on a HIP device only; got a CPU tensor")
         if q.dtype not in DTYPES:
@@ -863,6 +866,7 @@ class DecodePlan:
         a.q_pos0, a.n_global, a.n_local, a.k_max = int(q_pos0), int(n_global), int(n_local), int(k_max)
         a.pct_decode, a.causal = float(pct_decode), int(bool(causal))
         a.rule = RULES[rule]
+        a.block_n = int(block_n)
         self._keep = (qh, kh, vh, tau, ifr, ifc)
         self.out = {
             "out": torch.empty((H, Q, D), dtype=qh.dtype, device=dev),
@@ -924,14 +928,14 @@ class DecodePlan:
 
 def decode_attention(q, k, v, tau, inv_freq, q_pos0, pos_scale=1.0, rope_scale=1.0, sm_scale=None,
                      n_global=32, n_local=32, k_max=1024, pct_decode=100.0, causal=False, want_scores=False,
-                     inv_freq_c=None, pos_scale_c=None, rope_scale_c=None, rule="shared"):
+                     inv_freq_c=None, pos_scale_c=None, rope_scale_c=None, rule="shared", block_n=32):
     """Scores, selection and attend of Q queries (H, Q, D) over the cache k, v (Hkv, M, D).
     Returns a dict of device tensors: out (H, Q, D), idx (H, Q, k_max) int32 (sentinel m_i),
     newpos_k, newpos_q, set_size, with want_scores scores (H, Q, M), and under rule "pq" usize
     and overflow (H, Q)."""
     return DecodePlan(q, k, v, tau, inv_freq, q_pos0, pos_scale, rope_scale, sm_scale, n_global, n_local,
                       k_max, pct_decode, causal, want_scores, inv_freq_c, pos_scale_c, rope_scale_c,
-                      rule).run()
+                      rule, block_n).run()
 
 
 class PerQueryPrefillPlan:

@@ -62,13 +62,19 @@ int dec_check(const sta_decode_args* a, bool need_pos = true) {
   if (a->Q < 1) return fail(STA_ERR_INVALID_ARG, "Q=%d must be >= 1", a->Q);
   if (a->q_pos0 < 0 || (need_pos && (int64_t)a->q_pos0 + a->Q > a->M))
     return fail(STA_ERR_INVALID_ARG, "need 0 <= q_pos0 (%d) and q_pos0 + Q (%d) <= M (%d)", a->q_pos0, a->Q, a->M);
-  if (a->k_max < 1 || a->k_max > 16384)
-    return fail(STA_ERR_UNSUPPORTED, "k_max=%d outside [1, 16384]", a->k_max);
+  if (a->k_max < 1 || a->k_max > 65536)
+    return fail(STA_ERR_UNSUPPORTED, "k_max=%d outside [1, 65536]", a->k_max);
   if (a->n_global < 0 || a->n_local < 0)
     return fail(STA_ERR_UNSUPPORTED, "n_global=%d / n_local=%d must be >= 0", a->n_global, a->n_local);
   if ((size_t)a->H * a->Q >= (1u << 31)) return fail(STA_ERR_INVALID_ARG, "H * Q too large");
-  if (a->rule != STA_RULE_SHARED && a->rule != STA_RULE_PQ)
-    return fail(STA_ERR_INVALID_ARG, "rule %d is not STA_RULE_SHARED or STA_RULE_PQ", a->rule);
+  if (a->rule != STA_RULE_SHARED && a->rule != STA_RULE_PQ && a->rule != STA_RULE_STREAM)
+    return fail(STA_ERR_INVALID_ARG, "rule %d is not STA_RULE_SHARED, STA_RULE_PQ or STA_RULE_STREAM", a->rule);
+  if (a->rule == STA_RULE_STREAM) {
+    if (a->block_n < 1) return fail(STA_ERR_INVALID_ARG, "stream rule: block_n=%d must be >= 1", a->block_n);
+    // the block-end counts live in the selection's 4096-entry histogram
+    if ((a->M + a->block_n - 1) / a->block_n > 4096)
+      return fail(STA_ERR_UNSUPPORTED, "stream rule: M=%d over block_n=%d exceeds 4096 blocks", a->M, a->block_n);
+  }
   if (a->rule == STA_RULE_PQ && (int64_t)a->n_global + a->n_local > a->k_max)
     return fail(STA_ERR_INVALID_ARG, "per-query rule: n_global (%d) + n_local (%d) exceeds k_max (%d)",
                 a->n_global, a->n_local, a->k_max);
@@ -112,10 +118,12 @@ DecodeArgs dec_args_of(const sta_decode_args* a, const DecLayout& L) {
   d.n_local = a->n_local;
   d.k_max = a->k_max;
   d.rule = a->rule;
+  d.block_n = a->rule == STA_RULE_STREAM ? a->block_n : 0;
   d.usize = a->rule == STA_RULE_PQ ? a->usize : nullptr;
   d.overflow = a->rule == STA_RULE_PQ ? a->overflow : nullptr;
   // the per-query rule keeps every passer (perquery.py:651-720 has no top-pct cut)
-  d.use_pct = a->rule == STA_RULE_SHARED && a->pct_decode < 100.0;   // exact_2.py:559
+  d.use_pct = a->rule == STA_RULE_SHARED && a->pct_decode < 100.0;   // exact_2.py:559 (the others keep
+                                                                     // every passer)
   d.pct_frac = (float)(a->pct_decode / 100.0);                    // the float32 scalar of :561
   d.scores = a->scores ? a->scores : (float*)(ws + L.scores_off);
   d.keys = decode_select_in_lds(a->M) ? nullptr : (uint32_t*)(ws + L.keys_off);

@@ -485,6 +485,7 @@ __global__ __launch_bounds__(DEC_SEL_NT) void decode_select_kernel(DecodeArgs a)
 
   // the per-query rule's measurement counters: |passers| and the overflow flag (perquery.py:686-688)
   const bool pq = a.rule == 1;
+  const bool stream = a.rule == 2;   // PQ Stream: every passer and forced key, no cap
   if (pq && tid == 0) {
     if (a.usize) a.usize[hi] = ge;
     if (a.overflow) a.overflow[hi] = count > a.k_max ? 1 : 0;
@@ -498,7 +499,7 @@ __global__ __launch_bounds__(DEC_SEL_NT) void decode_select_kernel(DecodeArgs a)
   // tie index
   bool exact_cut = false;
   int quota = 0, tie_base = 0;
-  if (count > a.k_max) {
+  if (count > a.k_max && !stream) {
     const int budget_c = a.k_max - nforced;
     if (budget_c <= 0) {
       only_forced = true;
@@ -555,6 +556,20 @@ __global__ __launch_bounds__(DEC_SEL_NT) void decode_select_kernel(DecodeArgs a)
   float run = pq ? 0.0f : dexcl_max(mloc, (float*)tmp);
   int32_t* irow = a.idx + (int64_t)hi * a.k_max;
   float* nrow = a.newpos_k + (int64_t)hi * a.k_max;
+  // PQ Stream's positions (pqstream_kernel.py:736-749): aligned blocks of block_n keys walked
+  // from the query backwards; key j of block b sits at dist = d[b] + (min(q_pos, end of b) - j)
+  // with d[b] = kept keys after block b = total - (kept keys up to the end of b).  The inclusive
+  // count at every block end goes to LDS (over the histogram, free by now).
+  int* bend = hist;
+  if (stream) {
+    int rank = base - 1, tie = tie_base;
+    for (int e = 0; e < j1 - j0; ++e) {
+      const int j = j0 + e;
+      if (final_j(j, myrow[e], tie)) rank += 1;
+      if ((j + 1) % a.block_n == 0 || j == m - 1) bend[j / a.block_n] = rank + 1;
+    }
+    __syncthreads();
+  }
   {
     int rank = base - 1, tie = tie_base;
     for (int e = 0; e < j1 - j0; ++e) {
@@ -567,13 +582,22 @@ __global__ __launch_bounds__(DEC_SEL_NT) void decode_select_kernel(DecodeArgs a)
           run = fmaxf(run, cp - (float)rank);
         }
       }
-      // the shared rule's reposition (exact_2.py:592), or the dense rank itself (perquery.py:707)
-      const float np = pq ? (float)rank : (float)rank + run;
+      // the shared rule's reposition (exact_2.py:592), the dense rank itself (perquery.py:707),
+      // or the streamed distance, negated (pqstream_kernel.py:749; -0 for the query itself)
+      float np;
+      if (stream) {
+        const int b = j / a.block_n;
+        const int hb = min(p, b * a.block_n + a.block_n - 1);
+        const float dist = (float)(total - bend[b]) + (float)(hb - j);
+        np = -dist;
+      } else {
+        np = pq ? (float)rank : (float)rank + run;
+      }
       if (f && rank < a.k_max) {
         irow[rank] = j;
         nrow[rank] = np;
       }
-      if (j == p) a.newpos_q[hi] = np;                                   // :603
+      if (j == p) a.newpos_q[hi] = stream ? 0.0f : np;                   // :603; pqstream :770
     }
   }
   for (int s = min(total, a.k_max) + tid; s < a.k_max; s += DEC_SEL_NT) {   // sentinel m (:594-600)
@@ -721,7 +745,7 @@ __global__ __launch_bounds__(256) void decode_attend_kernel(DecodeArgs a) {
 // merge the splits of one query: 256 threads, 256 / D per dim
 template <int DT, int D>
 __global__ __launch_bounds__(256) void decode_combine_kernel(DecodeArgs a, int ns) {
-  __shared__ float msplit[256], lsplit[256], wsplit[256];
+  __shared__ float msplit[1024], lsplit[1024], wsplit[1024];   // ns <= 1024: k_max <= 65536
   __shared__ float red[256 / D][D];
   const int hi = blockIdx.x;
   const float* parts = a.part + (int64_t)hi * ns * (D + 2);

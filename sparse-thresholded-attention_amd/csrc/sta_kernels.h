@@ -190,7 +190,9 @@ struct DecodeArgs {
   float* part;            // (H * Q, nsplit, D + 2) split states of the attend
   const float* qrot;      // (H, Q, D) rotated queries, or null (the score kernel rotates them)
   void* out;              // (H, Q, D)
-  int rule;               // 0: _decode_build_sets (shared files); 1: _decode_build_sets_pq
+  int rule;               // 0: _decode_build_sets (shared files); 1: _decode_build_sets_pq;
+                          // 2: _decode_build_sets_pqs (PQ Stream, streamed positions)
+  int block_n;            // rule 2: the position blocks
   int32_t* usize;         // (H, Q) or null: rule 1, |threshold passers|
   uint8_t* overflow;      // (H, Q) or null: rule 1, passers U forced above k_max
 };

@@ -54,9 +54,10 @@ def _prompt(n, seed=1):
 
 
 def _greedy(model, ids, steps):
+    # an explicit all-ones mask: generate() would otherwise mask every prompt token equal to the pad id
     with torch.no_grad():
-        r = model.generate(ids, max_new_tokens=steps, do_sample=False, output_logits=True,
-                           return_dict_in_generate=True, pad_token_id=0)
+        r = model.generate(ids, attention_mask=torch.ones_like(ids), max_new_tokens=steps, do_sample=False,
+                           output_logits=True, return_dict_in_generate=True, pad_token_id=0)
     return r.sequences, torch.stack(r.logits, 0)
 
 
@@ -126,3 +127,50 @@ def test_finite_threshold_prefill_and_decode():
         assert sa.spi_pos_scale == 256 / 700           # frozen at prefill: min(1, W / N)
         assert int(sa.spi_last_kept.max()) <= 2 * 700
         assert sa.spi_last_kept.shape == (4, 11)      # (heads, tiles)
+
+
+def test_pqstream_everything_kept_reproduces_the_dense_model():
+    """PQ Stream installed with tau = inf: every key kept, each block advances by its full length and
+    every key streams to its natural distance, so prefill (the fused kernel) and decode (the stream
+    rule) reproduce the dense model under base RoPE."""
+    import pqstream_kernel as pqs
+    say("pqstream dense known answer")
+    model = _model(None, seed=11)
+    ids = _prompt(300, seed=12)
+    with torch.no_grad():
+        ref_logits = model(ids).logits
+    ref_seq, ref_steps = _greedy(model, ids, 6)
+    pqs.install_pqstream_forward(model, context_window=128, n_global=8, n_local=8, block_n=32)
+    _set_tau(model, math.inf)
+    pqs.reset_overflow_stats()
+    with torch.no_grad():
+        logits = model(ids).logits
+    err = (logits - ref_logits).abs().max().item()
+    assert err < 2e-3, f"prefill logits differ by {err:.2e}"
+    seq, steps = _greedy(model, ids, 6)
+    assert torch.equal(seq, ref_seq)
+    derr = (steps - ref_steps).abs().max().item()
+    assert derr < 2e-3, f"decode logits differ by {derr:.2e}"
+    st = pqs.get_overflow_stats()
+    assert st["decode"]["total_cells"] > 0 and st["decode"]["skip_frac"] == 0.0
+    print(f"[result] pqstream: prefill logits max err {err:.2e}, decode {derr:.2e}, decode span max "
+          f"{st['decode']['span_max']:.0f}", flush=True)
+
+
+def test_pqstream_per_query_prompt_matches_prefill_plus_one_decode_step():
+    import pqstream_kernel as pqs
+    say("pqstream per-query prefill of N tokens vs N - 1 tokens + one decode step")
+    model = _model(None, seed=13)
+    pqs.install_pqstream_forward(model, context_window=200, n_global=8, n_local=8, block_n=32, max_len=600,
+                                 prefill_mode="perquery")
+    _set_tau(model, 2.0)
+    ids = _prompt(513, seed=14)
+    with torch.no_grad():
+        full = model(ids).logits[0, -1]
+        from transformers import DynamicCache
+        cache = DynamicCache(config=model.config)
+        model(ids[:, :-1], past_key_values=cache, use_cache=True)
+        step = model(ids[:, -1:], past_key_values=cache, use_cache=True).logits[0, -1]
+    assert torch.isfinite(full).all()
+    err = (full - step).abs().max().item()
+    assert err < 1e-4, f"per-query prompt vs decode step differ by {err:.2e}"

@@ -219,8 +219,8 @@ def _decode_args(**kw):
 
 
 @pytest.mark.parametrize("field,value,code", [
-    ("D", 96, -2), ("M", 0, -1), ("Q", 0, -1), ("q_pos0", 12288, -1), ("k_max", 0, -2), ("k_max", 20000, -2),
-    ("Hkv", 5, -1),
+    ("D", 96, -2), ("M", 0, -1), ("Q", 0, -1), ("q_pos0", 12288, -1), ("k_max", 0, -2),
+    ("k_max", 70000, -2), ("rule", 3, -1), ("Hkv", 5, -1),
     ("n_local", -1, -2), ("dtype", 7, -1),
 ])
 def test_decode_invalid_arguments_are_rejected(field, value, code):
