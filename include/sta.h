@@ -91,7 +91,9 @@ typedef struct sta_shared_args {
                             * NULL to skip; ignored for STA_SCORE_FREQ */
 } sta_shared_args;
 
-/* ABI version of this header (bumped on any layout change of sta_shared_args): 2. */
+/* ABI version of this header (bumped on any layout change of an argument struct): 4.
+ * 2: sta_shared_args.select_score; 3: the rule fields of sta_decode_args and config 4's fields of
+ * sta_dca_args; 4: sta_dca_args.mscale, sta_dca_rotate_keys and sta_dca_decode. */
 int sta_abi_version(void);
 
 /* Description of the last error returned on the calling thread ("" if none). */
@@ -307,6 +309,10 @@ typedef struct sta_dca_args {
   uint8_t* overflow20;
   int32_t* votes;           /* optional (H, nt, N) dense int32 votes (0 past a tile's inter keys) */
   float* row_max;           /* optional (H, N) exact max over the inter keys, -inf without any */
+  /* ABI 4: the table factor.  > 0: use it -- a patched model's rotary keeps the factor of the
+   * length its tables were last built for (dca_kernel.py:174-231: rebuilt only when a call's
+   * length exceeds the last build's length + 512); 0: get_mscale(N / pretrain_len). */
+  float mscale;
 } sta_dca_args;
 
 /* Bytes of device workspace sta_dca_attention needs for these arguments. */
@@ -318,6 +324,54 @@ size_t sta_dca_workspace_size(const sta_dca_args* args);
  * With select = 1, config 4: DCA positions with exact-max selection over the inter-chunk keys
  * (no reference combines them; the rule is described at sta_dca_args.select). */
 int sta_dca_attention(const sta_dca_args* args, void* stream);
+
+/* Keys of N new tokens at positions pos0 .. pos0 + N - 1, rotated at (pos mod L) with the key
+ * table for the KV cache: the cache of a DCA model holds rotated keys.  Replaces
+ * k = apply_rotary_pos_emb(k, k_cos, k_sin, position_ids) of dca_forward (dca_kernel.py:434-435)
+ * with the cyclic key table of ChunkLlamaRotaryEmbedding (:187-190, 198-206). */
+typedef struct sta_dca_rotate_args {
+  const void* x;            /* (heads, N, D) raw keys */
+  int64_t x_head_stride, x_tok_stride;
+  void* out;                /* (heads, N, D) rotated keys in the model dtype */
+  int64_t out_head_stride, out_tok_stride;
+  int32_t dtype, heads, N, D;
+  int32_t pos0;             /* absolute position of row 0 */
+  const float* inv_freq;    /* (D/2,) */
+  int32_t chunk_size, local_window;
+  float mscale;             /* the table factor (> 0) */
+} sta_dca_rotate_args;
+
+int sta_dca_rotate_keys(const sta_dca_rotate_args* args, void* stream);
+
+/* DCA at decode: the new token's query at position M - 1 over a cache of M rotated keys.  The
+ * query is rotated three ways (intra at (M-1) mod L, succ at min((M-1) mod L + L, chunk_size),
+ * inter at min(2L - 1, chunk_size)) and scores the keys [0, inter_end) inter, [inter_end,
+ * chunk_start) succ, [chunk_start, M) intra, chunk_start = floor((M-1) / L) L, inter_end =
+ * max(0, chunk_start - L); one softmax.  The reference's model-dtype matmuls are kept: scores
+ * rnd(rnd(q.k) * scale), weights rnd(softmax in fp32), output rnd(P.V) with rnd the rounding to
+ * the model dtype.  Replaces the decode branch of dca_forward, dca_kernel.py:491-522.  Any
+ * L = chunk_size - local_window >= 1; H / Hkv <= 16. */
+typedef struct sta_dca_decode_args {
+  const void* q;            /* (H, D) raw query of the new token */
+  int64_t q_head_stride;
+  const void* k;            /* (Hkv, M, D) cached keys, rotated (sta_dca_rotate_keys) */
+  int64_t k_head_stride, k_tok_stride;
+  const void* v;            /* (Hkv, M, D) */
+  int64_t v_head_stride, v_tok_stride;
+  int32_t dtype, H, Hkv, M, D;
+  const float* inv_freq;    /* (D/2,) */
+  int32_t chunk_size, local_window;
+  float mscale;             /* the table factor (> 0) */
+  float scale;              /* softmax scale */
+  void* out;                /* (H, D) model dtype */
+  void* workspace;
+  size_t workspace_bytes;
+} sta_dca_decode_args;
+
+/* Bytes of device workspace sta_dca_decode needs for these arguments (0 if they are invalid). */
+size_t sta_dca_decode_workspace_size(const sta_dca_decode_args* args);
+
+int sta_dca_decode(const sta_dca_decode_args* args, void* stream);
 
 /* ------------------------------------------------------------------------------------------ */
 /* Decode: each query selects its own key set over the KV cache and attends it.  A batch of Q   */

@@ -372,9 +372,10 @@ def dca_mscale(seq_len, pretrain_len):
 
 
 def dca_attention(q, k, v, dtype, inv_freq, chunk_size, pretrain_len, local_window, scale=None,
-                  rows=None):
+                  rows=None, mscale=None):
     """The prefill branch of dca_forward (dca_kernel.py:372-489) on raw q (H,N,D), k/v (Hkv,N,D).
-    Returns out (H, N, D) fp32; with `rows` only those query rows are computed (others NaN)."""
+    Returns out (H, N, D) fp32; with `rows` only those query rows are computed (others NaN).
+    mscale: the table factor (default get_mscale(N / pretrain_len))."""
     q = np.ascontiguousarray(q)
     k = np.ascontiguousarray(k)
     v = np.ascontiguousarray(v)
@@ -382,13 +383,43 @@ def dca_attention(q, k, v, dtype, inv_freq, chunk_size, pretrain_len, local_wind
     Hkv = k.shape[0]
     if scale is None:
         scale = 1.0 / math.sqrt(D)
-    ms = np.float32(dca_mscale(N, pretrain_len))
+    ms = np.float32(dca_mscale(N, pretrain_len) if mscale is None else mscale)
     out = np.full((H, N, D), np.nan, np.float32)
     r = _c(rows, np.int32) if rows is not None else None
     lib().oracle_dca(_p(q), _p(k), _p(v), ctypes.c_int(dtype), ctypes.c_int(H), ctypes.c_int(Hkv),
                      ctypes.c_int(N), ctypes.c_int(D), _p(_c(inv_freq, np.float32)), ctypes.c_int(chunk_size),
                      ctypes.c_int(local_window), ctypes.c_float(ms), ctypes.c_float(scale), _p(r),
                      ctypes.c_int(len(r) if r is not None else 0), _p(out))
+    return out
+
+
+def dca_rotate_keys(k, dtype, inv_freq, chunk_size, local_window, mscale, pos0=0):
+    """Raw keys (heads, N, D) at positions pos0.. rotated with the cyclic key table
+    (dca_kernel.py:187-190, 434-435) -> (heads, N, D) fp32 holding model-dtype values."""
+    k = np.ascontiguousarray(k)
+    heads, N, D = k.shape
+    out = np.empty((heads, N, D), np.float32)
+    lib().oracle_dca_rotate_keys(_p(k), ctypes.c_int(dtype), ctypes.c_int(heads), ctypes.c_int(N), ctypes.c_int(D),
+                                 ctypes.c_int(pos0), _p(_c(inv_freq, np.float32)), ctypes.c_int(chunk_size),
+                                 ctypes.c_int(local_window), ctypes.c_float(mscale), _p(out))
+    return out
+
+
+def dca_decode(q, krot, v, dtype, inv_freq, chunk_size, local_window, mscale, scale=None):
+    """The decode branch of dca_forward (dca_kernel.py:491-522): q (H, D) raw at position M - 1 over
+    the rotated cache krot and v (Hkv, M, D), all in the storage of `dtype` -> (H, D) fp32 holding
+    model-dtype values."""
+    q = np.ascontiguousarray(q)
+    krot = np.ascontiguousarray(krot)
+    v = np.ascontiguousarray(v)
+    H, D = q.shape
+    Hkv, M = krot.shape[0], krot.shape[1]
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    out = np.empty((H, D), np.float32)
+    lib().oracle_dca_decode(_p(q), _p(krot), _p(v), ctypes.c_int(dtype), ctypes.c_int(H), ctypes.c_int(Hkv),
+                            ctypes.c_int(M), ctypes.c_int(D), _p(_c(inv_freq, np.float32)), ctypes.c_int(chunk_size),
+                            ctypes.c_int(local_window), ctypes.c_float(mscale), ctypes.c_float(scale), _p(out))
     return out
 
 

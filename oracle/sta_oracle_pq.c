@@ -724,3 +724,91 @@ void oracle_dca_select_attn(const void* q, const void* k, const void* v, int dty
   free(kr);
   free(qr);
 }
+
+/* ------------------------------------------------------------------------------------------- */
+/* DCA at decode (dca_kernel.py:491-522) and the rotated key cache (:434-435)                   */
+/* ------------------------------------------------------------------------------------------- */
+/*
+ * oracle_dca_rotate_keys: raw keys (heads, N, D) at positions pos0 .. pos0 + N - 1 rotated with
+ * the cyclic key table (:187-190, 198-206): table position (pos mod L), model-dtype table and
+ * rotation as in the prefill.  out (heads, N, D) fp32 holding model-dtype values.
+ */
+void oracle_dca_rotate_keys(const void* k, int dtype, int heads, int N, int D, int pos0, const float* inv_freq,
+                            int chunk_size, int local_window, float mscale, float* out) {
+  const int L = chunk_size - local_window;
+  float* c = (float*)malloc(sizeof(float) * (D / 2));
+  float* s = (float*)malloc(sizeof(float) * (D / 2));
+  for (int j = 0; j < N; ++j) {
+    dca_table((float)((pos0 + j) % L), inv_freq, D, mscale, dtype, c, s);
+    for (int h = 0; h < heads; ++h)
+      dca_rotate(k, dtype, ((size_t)h * N + j) * D, D, c, s, out + ((size_t)h * N + j) * D);
+  }
+  free(c);
+  free(s);
+}
+
+/*
+ * oracle_dca_decode: the decode branch.  q (H, D) raw at position cur = M - 1; krot (Hkv, M, D)
+ * the cached keys, already rotated (model dtype); v (Hkv, M, D).  The query is rotated at
+ * pid = cur mod L (intra, :497), at min(pid + L, s) (succ, :510) and at min(2L - 1, s) (inter:
+ * the clamped table index L - 1, :504-505).  Keys [0, inter_end) are scored with the inter
+ * variant, [inter_end, chunk_start) with succ, [chunk_start, M) with intra (:494-495, 502-517).
+ * Every matmul of the reference runs in the model dtype: each dot accumulates in fp32 (in key
+ * dimension order here) and is rounded to the dtype, the scale product is rounded to the dtype
+ * (:506-517); the softmax is fp32 (max, then exp(s - max) / sum) and its weights are cast to
+ * the dtype (:520-521); P.V accumulates in fp32 (in key order) and is rounded (:522).
+ * out (H, D) fp32 holding model-dtype values.
+ */
+void oracle_dca_decode(const void* q, const void* krot, const void* v, int dtype, int H, int Hkv, int M, int D,
+                       const float* inv_freq, int chunk_size, int local_window, float mscale, float scale,
+                       float* out) {
+  const int L = chunk_size - local_window;
+  const int half = D / 2;
+  const int group = H / Hkv;
+  const int cur = M - 1;
+  const int chunk_start = (cur / L) * L;
+  const int inter_end = chunk_start - L > 0 ? chunk_start - L : 0;
+  const int pid = cur % L;
+  const int pos[3] = {pid, pid + L < chunk_size ? pid + L : chunk_size, 2 * L - 1 < chunk_size ? 2 * L - 1 : chunk_size};
+  float* c = (float*)malloc(sizeof(float) * half);
+  float* s = (float*)malloc(sizeof(float) * half);
+  float* qv = (float*)malloc(sizeof(float) * 3 * D);
+  float* sc = (float*)malloc(sizeof(float) * (size_t)M);
+  float* acc = (float*)malloc(sizeof(float) * D);
+  for (int h = 0; h < H; ++h) {
+    const int hk = h / group;
+    for (int var = 0; var < 3; ++var) {
+      dca_table((float)pos[var], inv_freq, D, mscale, dtype, c, s);
+      dca_rotate(q, dtype, (size_t)h * D, D, c, s, qv + var * D);
+    }
+    float mx = -INFINITY;
+    for (int j = 0; j < M; ++j) {
+      const float* qq = qv + (j < inter_end ? 2 : (j < chunk_start ? 1 : 0)) * D;
+      float d = 0.0f;
+      for (int e = 0; e < D; ++e) {
+        volatile float prod = qq[e] * load_elem(krot, dtype, ((size_t)hk * M + j) * D + e);
+        d = d + prod;
+      }
+      volatile float sd = round_to_dtype(d, dtype) * scale;
+      sc[j] = round_to_dtype(sd, dtype);
+      if (sc[j] > mx) mx = sc[j];
+    }
+    float l = 0.0f;
+    for (int j = 0; j < M; ++j) l += expf(sc[j] - mx);
+    for (int e = 0; e < D; ++e) acc[e] = 0.0f;
+    for (int j = 0; j < M; ++j) {
+      volatile float pj = expf(sc[j] - mx) / l;
+      const float p = round_to_dtype(pj, dtype);
+      for (int e = 0; e < D; ++e) {
+        volatile float prod = p * load_elem(v, dtype, ((size_t)hk * M + j) * D + e);
+        acc[e] = acc[e] + prod;
+      }
+    }
+    for (int e = 0; e < D; ++e) out[(size_t)h * D + e] = round_to_dtype(acc[e], dtype);
+  }
+  free(c);
+  free(s);
+  free(qv);
+  free(sc);
+  free(acc);
+}

@@ -21,7 +21,8 @@ EXPORTS = ["sta_abi_version", "sta_last_error", "sta_shared_workspace_size", "st
            "sta_select_vote", "sta_build_sets", "sta_build_sets_weighted", "sta_gather_attention",
            "sta_pq_workspace_size", "sta_pq_attention", "sta_pq_select_bits", "sta_pq_build_sets",
            "sta_pq_gather_attention", "sta_pqstream_workspace_size", "sta_pqstream_attention",
-           "sta_dca_workspace_size", "sta_dca_attention", "sta_decode_workspace_size", "sta_decode_scores",
+           "sta_dca_workspace_size", "sta_dca_attention", "sta_dca_rotate_keys", "sta_dca_decode_workspace_size",
+           "sta_dca_decode", "sta_decode_workspace_size", "sta_decode_scores",
            "sta_decode_build_sets", "sta_decode_attend", "sta_decode_attention"]
 SCORES = {"freq": 0, "margin": 1, "expmass": 2}
 
@@ -118,6 +119,32 @@ class DcaArgsC(ctypes.Structure):
         ("idx", ctypes.c_void_p), ("shared_size", ctypes.c_void_p), ("kept_size", ctypes.c_void_p),
         ("chosen", ctypes.c_void_p), ("orig_overflow", ctypes.c_void_p), ("kpct_meas", ctypes.c_void_p),
         ("overflow20", ctypes.c_void_p), ("votes", ctypes.c_void_p), ("row_max", ctypes.c_void_p),
+        ("mscale", ctypes.c_float),
+    ]
+
+
+class DcaRotateArgsC(ctypes.Structure):
+    """Mirror of sta_dca_rotate_args (include/sta.h)."""
+    _fields_ = [
+        ("x", ctypes.c_void_p), ("x_head_stride", ctypes.c_int64), ("x_tok_stride", ctypes.c_int64),
+        ("out", ctypes.c_void_p), ("out_head_stride", ctypes.c_int64), ("out_tok_stride", ctypes.c_int64),
+        ("dtype", ctypes.c_int32), ("heads", ctypes.c_int32), ("N", ctypes.c_int32), ("D", ctypes.c_int32),
+        ("pos0", ctypes.c_int32), ("inv_freq", ctypes.c_void_p),
+        ("chunk_size", ctypes.c_int32), ("local_window", ctypes.c_int32), ("mscale", ctypes.c_float),
+    ]
+
+
+class DcaDecodeArgsC(ctypes.Structure):
+    """Mirror of sta_dca_decode_args (include/sta.h)."""
+    _fields_ = [
+        ("q", ctypes.c_void_p), ("q_head_stride", ctypes.c_int64),
+        ("k", ctypes.c_void_p), ("k_head_stride", ctypes.c_int64), ("k_tok_stride", ctypes.c_int64),
+        ("v", ctypes.c_void_p), ("v_head_stride", ctypes.c_int64), ("v_tok_stride", ctypes.c_int64),
+        ("dtype", ctypes.c_int32), ("H", ctypes.c_int32), ("Hkv", ctypes.c_int32), ("M", ctypes.c_int32),
+        ("D", ctypes.c_int32), ("inv_freq", ctypes.c_void_p),
+        ("chunk_size", ctypes.c_int32), ("local_window", ctypes.c_int32),
+        ("mscale", ctypes.c_float), ("scale", ctypes.c_float), ("out", ctypes.c_void_p),
+        ("workspace", ctypes.c_void_p), ("workspace_bytes", ctypes.c_size_t),
     ]
 
 
@@ -197,7 +224,13 @@ def lib():
             fn = getattr(L, name)
             fn.restype = ctypes.c_int
             fn.argtypes = [ctypes.POINTER(DecodeArgsC), ctypes.c_void_p, ctypes.c_void_p]
-        if L.sta_abi_version() != 3:
+        L.sta_dca_rotate_keys.restype = ctypes.c_int
+        L.sta_dca_rotate_keys.argtypes = [ctypes.POINTER(DcaRotateArgsC), ctypes.c_void_p]
+        L.sta_dca_decode_workspace_size.restype = ctypes.c_size_t
+        L.sta_dca_decode_workspace_size.argtypes = [ctypes.POINTER(DcaDecodeArgsC)]
+        L.sta_dca_decode.restype = ctypes.c_int
+        L.sta_dca_decode.argtypes = [ctypes.POINTER(DcaDecodeArgsC), ctypes.c_void_p]
+        if L.sta_abi_version() != 4:
             raise ImportError("libsta_hip.so ABI version mismatch")
         _LIB = L
     return _LIB
@@ -727,10 +760,12 @@ class DcaPlan:
     rotations and the attention sweep on the current stream and allocates nothing."""
 
     def __init__(self, q, k, v, inv_freq, chunk_size, pretrain_len, local_window, scale=None, tau=None,
-                 pct=30.0, k_max=2048, n_global=32, measure=False, want_votes=False, want_row_max=False):
+                 pct=30.0, k_max=2048, n_global=32, measure=False, want_votes=False, want_row_max=False,
+                 mscale=None):
         """tau given: config 4 (exact-max selection over the inter-chunk keys, 64-query tiles);
         the outputs then also hold the selection (idx, shared_size, kept_size, chosen,
-        orig_overflow, kpct_meas, overflow20; votes / row_max on request)."""
+        orig_overflow, kpct_meas, overflow20; votes / row_max on request).  mscale: the table
+        factor (default get_mscale(N / pretrain_len))."""
         qh, kh, vh, _, ifc, _ = _prep_inputs(q, k, v, torch.zeros(1), inv_freq, None)
         H, N, D = qh.shape
         self.device = dev = qh.device
@@ -746,6 +781,7 @@ class DcaPlan:
         a.inv_freq = _ptr(ifc)
         a.chunk_size, a.pretrain_len, a.local_window = int(chunk_size), int(pretrain_len), int(local_window)
         a.scale = float(scale)
+        a.mscale = 0.0 if mscale is None else float(mscale)
         self._keep = (qh, kh, vh, ifc)
         self.out = {"out": torch.empty((H, N, D), dtype=qh.dtype, device=dev)}
         a.out = _ptr(self.out["out"])
@@ -791,9 +827,66 @@ class DcaPlan:
         return self.out
 
 
-def dca_attention(q, k, v, inv_freq, chunk_size, pretrain_len, local_window, scale=None):
+def dca_attention(q, k, v, inv_freq, chunk_size, pretrain_len, local_window, scale=None, mscale=None):
     """The DCA prefill on the device; returns out (H, N, D) in q.dtype."""
-    return DcaPlan(q, k, v, inv_freq, chunk_size, pretrain_len, local_window, scale).run()["out"]
+    return DcaPlan(q, k, v, inv_freq, chunk_size, pretrain_len, local_window, scale, mscale=mscale).run()["out"]
+
+
+def dca_rotate_keys(k, pos0, inv_freq, chunk_size, local_window, mscale, out=None):
+    """Keys k (heads, N, D) or (1, heads, N, D) at positions pos0.. rotated at (pos mod L) with the
+    key table, in the model dtype -> out (heads, N, D) (allocated when not given)."""
+    kh = _heads_view(k)
+    if not kh.is_cuda:
+        raise RuntimeError("sparse-thresholded attention runs on a HIP device only; got a CPU tensor")
+    if kh.dtype not in DTYPES:
+        raise TypeError(f"unsupported dtype {kh.dtype}")
+    heads, N, D = kh.shape
+    if out is None:
+        out = torch.empty((heads, N, D), dtype=kh.dtype, device=kh.device)
+    ifr = inv_freq.to(device=kh.device, dtype=torch.float32).contiguous()
+    a = DcaRotateArgsC()
+    a.x, a.x_head_stride, a.x_tok_stride = _ptr(kh), kh.stride(0), kh.stride(1)
+    a.out, a.out_head_stride, a.out_tok_stride = _ptr(out), out.stride(0), out.stride(1)
+    a.dtype, a.heads, a.N, a.D = DTYPES[kh.dtype], heads, N, D
+    a.pos0, a.inv_freq = int(pos0), _ptr(ifr)
+    a.chunk_size, a.local_window, a.mscale = int(chunk_size), int(local_window), float(mscale)
+    _check(lib().sta_dca_rotate_keys(ctypes.byref(a), _stream(kh.device)), "sta_dca_rotate_keys")
+    return out
+
+
+def dca_decode(q, k, v, inv_freq, chunk_size, local_window, mscale, scale=None):
+    """DCA at decode: the query q (H, D) (or (1, H, 1, D)) at position M - 1 over the cache of
+    rotated keys k and values v (Hkv, M, D) (or (1, Hkv, M, D)) -> out (H, D) in q.dtype."""
+    qh = q.reshape(q.shape[-3] if q.dim() == 4 else q.shape[0], q.shape[-1])
+    if qh.stride(-1) != 1:
+        qh = qh.contiguous()
+    kh, vh = _heads_view(k), _heads_view(v)
+    if not qh.is_cuda:
+        raise RuntimeError("sparse-thresholded attention runs on a HIP device only; got a CPU tensor")
+    if qh.dtype not in DTYPES or kh.dtype != qh.dtype or vh.dtype != qh.dtype:
+        raise TypeError("q, k and v must share one supported dtype")
+    H, D = qh.shape
+    Hkv, M = kh.shape[0], kh.shape[1]
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    dev = qh.device
+    ifr = inv_freq.to(device=dev, dtype=torch.float32).contiguous()
+    out = torch.empty((H, D), dtype=qh.dtype, device=dev)
+    a = DcaDecodeArgsC()
+    a.q, a.q_head_stride = _ptr(qh), qh.stride(0)
+    a.k, a.k_head_stride, a.k_tok_stride = _ptr(kh), kh.stride(0), kh.stride(1)
+    a.v, a.v_head_stride, a.v_tok_stride = _ptr(vh), vh.stride(0), vh.stride(1)
+    a.dtype, a.H, a.Hkv, a.M, a.D = DTYPES[qh.dtype], H, Hkv, M, D
+    a.inv_freq = _ptr(ifr)
+    a.chunk_size, a.local_window = int(chunk_size), int(local_window)
+    a.mscale, a.scale, a.out = float(mscale), float(scale), _ptr(out)
+    n = lib().sta_dca_decode_workspace_size(ctypes.byref(a))
+    if n == 0:
+        _check(-1, "sta_dca_decode_workspace_size")
+    ws = torch.empty(n, dtype=torch.uint8, device=dev)
+    a.workspace, a.workspace_bytes = _ptr(ws), n
+    _check(lib().sta_dca_decode(ctypes.byref(a), _stream(dev)), "sta_dca_decode")
+    return out
 
 
 def dca_select_attention(q, k, v, inv_freq, chunk_size, pretrain_len, local_window, tau, pct=30.0, k_max=2048,

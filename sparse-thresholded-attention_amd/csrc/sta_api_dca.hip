@@ -59,6 +59,8 @@ int dca_check(const sta_dca_args* a) {
   if (!(a->local_window > 0 && a->local_window < a->chunk_size))
     return fail(STA_ERR_INVALID_ARG, "need 0 < local_window(%d) < chunk_size(%d)", a->local_window, a->chunk_size);
   if (a->pretrain_len < 1) return fail(STA_ERR_INVALID_ARG, "pretrain_len=%d must be >= 1", a->pretrain_len);
+  if (!(a->mscale >= 0.0f) || isinf(a->mscale))
+    return fail(STA_ERR_INVALID_ARG, "mscale=%g must be finite and >= 0 (0: derived from N)", (double)a->mscale);
   const int L = a->chunk_size - a->local_window;
   if (L % 64 != 0)
     return fail(STA_ERR_UNSUPPORTED, "chunk_size - local_window = %d is not a multiple of 64", L);
@@ -72,6 +74,67 @@ int dca_check(const sta_dca_args* a) {
                   a->N, a->k_max);
   }
   return STA_OK;
+}
+
+int check_rows(const char* what, int dtype, const void* p, int64_t hs, int64_t ts) {
+  const int es = esize(dtype);
+  if (!p) return fail(STA_ERR_INVALID_ARG, "%s is NULL", what);
+  if (!aligned16(p)) return fail(STA_ERR_UNSUPPORTED, "%s is not 16-byte aligned", what);
+  if (hs < 0 || ts < 0 || (hs * es) % 16 != 0 || (ts * es) % 16 != 0)
+    return fail(STA_ERR_UNSUPPORTED, "%s strides (%lld, %lld) are negative or not 16-byte aligned", what,
+                (long long)hs, (long long)ts);
+  return STA_OK;
+}
+
+int check_dtype_dim(int dtype, int D) {
+  if (dtype != STA_DTYPE_F32 && dtype != STA_DTYPE_BF16 && dtype != STA_DTYPE_F16)
+    return fail(STA_ERR_INVALID_ARG, "dtype %d is not one of STA_DTYPE_F32/BF16/F16", dtype);
+  if (D != 64 && D != 128) return fail(STA_ERR_UNSUPPORTED, "head_dim %d not in {64, 128}", D);
+  return STA_OK;
+}
+
+int check_chunks(int chunk_size, int local_window, float mscale) {
+  if (!(local_window > 0 && local_window < chunk_size))
+    return fail(STA_ERR_INVALID_ARG, "need 0 < local_window(%d) < chunk_size(%d)", local_window, chunk_size);
+  if (!(mscale > 0.0f) || isinf(mscale)) return fail(STA_ERR_INVALID_ARG, "mscale=%g must be finite and > 0",
+                                                     (double)mscale);
+  return STA_OK;
+}
+
+struct DcaDecLayout {
+  int nb;
+  size_t qrot_off, scores_off, pmax_off, psum_off, part_off, total;
+};
+
+DcaDecLayout dca_dec_layout_of(const sta_dca_decode_args* a) {
+  DcaDecLayout L;
+  L.nb = dca_dec_nblocks(a->M);
+  size_t off = 0;
+  L.qrot_off = off;
+  off = align256(off + (size_t)a->H * 3 * a->D * 4);
+  L.scores_off = off;
+  off = align256(off + (size_t)a->H * a->M * 4);
+  L.pmax_off = off;
+  off = align256(off + (size_t)a->H * L.nb * 4);
+  L.psum_off = off;
+  off = align256(off + (size_t)a->H * L.nb * 4);
+  L.part_off = off;
+  off = align256(off + (size_t)a->H * L.nb * a->D * 4);
+  L.total = off;
+  return L;
+}
+
+int dca_dec_check(const sta_dca_decode_args* a) {
+  if (!a) return fail(STA_ERR_INVALID_ARG, "args is NULL");
+  int rc = check_dtype_dim(a->dtype, a->D);
+  if (rc != STA_OK) return rc;
+  if (a->H < 1 || a->Hkv < 1 || a->H % a->Hkv != 0)
+    return fail(STA_ERR_INVALID_ARG, "H=%d must be a positive multiple of Hkv=%d", a->H, a->Hkv);
+  if (a->H / a->Hkv > dca_dec_max_group())
+    return fail(STA_ERR_UNSUPPORTED, "H / Hkv = %d exceeds %d heads per kv head", a->H / a->Hkv,
+                dca_dec_max_group());
+  if (a->M < 1 || a->M >= (1 << 24)) return fail(STA_ERR_INVALID_ARG, "M=%d out of range [1, 2^24)", a->M);
+  return check_chunks(a->chunk_size, a->local_window, a->mscale);
 }
 
 // config 4's selection: inter-key votes (two passes), then _build_sets over each tile's inter keys
@@ -162,9 +225,10 @@ int sta_dca_attention(const sta_dca_args* a, void* stream) {
   uint16_t* krot = (uint16_t*)(ws + L.krot_off);
   uint16_t* qrot = (uint16_t*)(ws + L.qrot_off);
   const int Lc = a->chunk_size - a->local_window;
-  // mscale = get_mscale(N / c): 0.05 ln(N / c) + 1 when the prefill outruns c, else 1 (:163-170)
+  // mscale = get_mscale(N / c): 0.05 ln(N / c) + 1 when the prefill outruns c, else 1 (:163-170),
+  // unless the caller passes the factor its tables were built with
   const double ratio = (double)a->N / (double)a->pretrain_len;
-  const float mscale = ratio <= 1.0 ? 1.0f : (float)(0.05 * log(ratio) + 1.0);
+  const float mscale = a->mscale > 0.0f ? a->mscale : (ratio <= 1.0 ? 1.0f : (float)(0.05 * log(ratio) + 1.0));
 
   if ((rc = mark_event(a->stage_events, 0, st)) != STA_OK) return rc;
   hipError_t e = launch_dca_rope(a->dtype, a->D, a->k, a->k_head_stride, a->k_tok_stride, a->Hkv, a->N, L.Npad,
@@ -201,6 +265,80 @@ int sta_dca_attention(const sta_dca_args* a, void* stream) {
   e = launch_dca_attn(a->dtype, a->D, d, st);
   if (e != hipSuccess) return hip_fail(e, "dca attention");
   return mark_event(a->stage_events, a->select ? 4 : 2, st);
+}
+
+int sta_dca_rotate_keys(const sta_dca_rotate_args* a, void* stream) {
+  if (!a) return fail(STA_ERR_INVALID_ARG, "args is NULL");
+  int rc = check_dtype_dim(a->dtype, a->D);
+  if (rc != STA_OK) return rc;
+  if (a->heads < 1 || a->N < 0 || a->pos0 < 0 || (int64_t)a->pos0 + a->N >= (1ll << 31))
+    return fail(STA_ERR_INVALID_ARG, "heads=%d, N=%d, pos0=%d out of range", a->heads, a->N, a->pos0);
+  if ((rc = check_chunks(a->chunk_size, a->local_window, a->mscale)) != STA_OK) return rc;
+  if (!a->inv_freq) return fail(STA_ERR_INVALID_ARG, "inv_freq is NULL");
+  if (a->N == 0) return STA_OK;
+  if ((rc = check_rows("x", a->dtype, a->x, a->x_head_stride, a->x_tok_stride)) != STA_OK) return rc;
+  if ((rc = check_rows("out", a->dtype, a->out, a->out_head_stride, a->out_tok_stride)) != STA_OK) return rc;
+  DcaRotArgs d{};
+  d.x = a->x;
+  d.x_head_stride = a->x_head_stride;
+  d.x_tok_stride = a->x_tok_stride;
+  d.out = a->out;
+  d.out_head_stride = a->out_head_stride;
+  d.out_tok_stride = a->out_tok_stride;
+  d.heads = a->heads;
+  d.N = a->N;
+  d.pos0 = a->pos0;
+  d.L = a->chunk_size - a->local_window;
+  d.mscale = a->mscale;
+  d.inv_freq = a->inv_freq;
+  hipError_t e = launch_dca_rotate_keys(a->dtype, a->D, d, (hipStream_t)stream);
+  return e == hipSuccess ? STA_OK : hip_fail(e, "dca key rotation");
+}
+
+size_t sta_dca_decode_workspace_size(const sta_dca_decode_args* a) {
+  if (dca_dec_check(a) != STA_OK) return 0;
+  return dca_dec_layout_of(a).total;
+}
+
+int sta_dca_decode(const sta_dca_decode_args* a, void* stream) {
+  int rc = dca_dec_check(a);
+  if (rc != STA_OK) return rc;
+  if ((rc = check_rows("q", a->dtype, a->q, a->q_head_stride, 0)) != STA_OK) return rc;
+  if ((rc = check_rows("k", a->dtype, a->k, a->k_head_stride, a->k_tok_stride)) != STA_OK) return rc;
+  if ((rc = check_rows("v", a->dtype, a->v, a->v_head_stride, a->v_tok_stride)) != STA_OK) return rc;
+  if (!a->inv_freq || !a->out) return fail(STA_ERR_INVALID_ARG, "inv_freq and out must be non-NULL");
+  const DcaDecLayout L = dca_dec_layout_of(a);
+  if (!a->workspace || a->workspace_bytes < L.total)
+    return fail(STA_ERR_WORKSPACE, "workspace of %zu bytes at %p is smaller than the %zu needed",
+                a->workspace_bytes, a->workspace, L.total);
+  if (((uintptr_t)a->workspace & 255u) != 0) return fail(STA_ERR_WORKSPACE, "workspace must be 256-byte aligned");
+  char* ws = (char*)a->workspace;
+  DcaDecArgs d{};
+  d.q = a->q;
+  d.q_head_stride = a->q_head_stride;
+  d.k = a->k;
+  d.k_head_stride = a->k_head_stride;
+  d.k_tok_stride = a->k_tok_stride;
+  d.v = a->v;
+  d.v_head_stride = a->v_head_stride;
+  d.v_tok_stride = a->v_tok_stride;
+  d.H = a->H;
+  d.Hkv = a->Hkv;
+  d.M = a->M;
+  d.L = a->chunk_size - a->local_window;
+  d.chunk_size = a->chunk_size;
+  d.nb = L.nb;
+  d.mscale = a->mscale;
+  d.scale = a->scale;
+  d.inv_freq = a->inv_freq;
+  d.out = a->out;
+  d.qrot = (float*)(ws + L.qrot_off);
+  d.scores = (float*)(ws + L.scores_off);
+  d.pmax = (float*)(ws + L.pmax_off);
+  d.psum = (float*)(ws + L.psum_off);
+  d.part = (float*)(ws + L.part_off);
+  hipError_t e = launch_dca_decode(a->dtype, a->D, d, (hipStream_t)stream);
+  return e == hipSuccess ? STA_OK : hip_fail(e, "dca decode");
 }
 
 }  // extern "C"

@@ -16,17 +16,11 @@
 // (double-buffered, V transposed) and read by all G waves.  S^T = K . Q^T (32x32x16 MFMA, lane =
 // query), so the softmax weights are already the B operand of O^T += V^T . P^T.
 // Requires L % 64 == 0: every 32-query tile and every 64-key block then lies in one chunk.
+#include "sta_dca_rot.h"
 #include "sta_device.h"
 #include "sta_kernels.h"
 
 namespace sta {
-
-template <int DT>
-__device__ __forceinline__ float round_dt(float x) {
-  if constexpr (DT == DT_BF16) return bf16_bits_to_f32(f32_to_bf16_bits(x));
-  else if constexpr (DT == DT_F16) return f16_bits_to_f32(f32_to_f16_bits(x));
-  else return x;
-}
 
 // ------------------------------------------------------------------------------------------
 // Rotated keys (variant -1) and queries (variants 0 intra, 1 succ, 2 inter).  out layout:
@@ -69,26 +63,7 @@ __global__ __launch_bounds__(256) void dca_rope_kernel(const void* __restrict__ 
     const int64_t base = (int64_t)head * head_stride + (int64_t)row * tok_stride;
     load8<DT>(x, base + i0, a);
     load8<DT>(x, base + D / 2 + i0, b);
-    const float tf = (float)t;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float ang = tf * inv_freq[i0 + e];
-      // cos / sin of the fp32 angle, correctly rounded to fp32 (through double): the table is then
-      // rounded to the model dtype, where a one-ulp difference between fp32 cosine implementations
-      // can flip a bf16 entry; the correctly rounded value is the one every implementation
-      // approximates, and the CPU oracle computes the same
-      double sd, cd;
-      sincos((double)ang, &sd, &cd);
-      float cs = round_dt<DT>((float)cd * mscale);               // table value in the model dtype
-      float sn = round_dt<DT>((float)sd * mscale);
-      if (first) {                                               // x1*cos + (-x2)*sin
-        const float p = round_dt<DT>(a[e] * cs), q = round_dt<DT>(-b[e] * sn);
-        o[e] = round_dt<DT>(p + q);
-      } else {                                                   // x2*cos + x1*sin
-        const float p = round_dt<DT>(b[e] * cs), q = round_dt<DT>(a[e] * sn);
-        o[e] = round_dt<DT>(p + q);
-      }
-    }
+    dca_rot8<DT>(a, b, t, i0, first, inv_freq, mscale, o);
   } else {
 #pragma unroll
     for (int e = 0; e < 8; ++e) o[e] = 0.0f;

@@ -161,6 +161,39 @@ struct DcaVoteArgs {
 };
 hipError_t launch_dca_votes(int dtype, int D, const DcaVoteArgs& a, hipStream_t st);
 
+// DCA key rotation into the cache and DCA decode (sta_dca_dec.hip)
+struct DcaRotArgs {
+  const void* x;            // (heads, N, D) raw keys
+  int64_t x_head_stride, x_tok_stride;
+  void* out;                // (heads, N, D) rotated, model dtype
+  int64_t out_head_stride, out_tok_stride;
+  int heads, N, pos0, L;
+  float mscale;
+  const float* inv_freq;
+};
+hipError_t launch_dca_rotate_keys(int dtype, int D, const DcaRotArgs& a, hipStream_t st);
+
+struct DcaDecArgs {
+  const void* q;            // (H, D) the new token's raw query, at position M - 1
+  int64_t q_head_stride;
+  const void* k;            // (Hkv, M, D) cached keys, rotated at j mod L
+  int64_t k_head_stride, k_tok_stride;
+  const void* v;            // (Hkv, M, D)
+  int64_t v_head_stride, v_tok_stride;
+  int H, Hkv, M, L, chunk_size, nb;
+  float mscale, scale;
+  const float* inv_freq;
+  void* out;                // (H, D) model dtype
+  float* qrot;              // workspace: (H, 3, D) rotated query variants
+  float* scores;            // (H, M)
+  float* pmax;              // (H, nb) per 256-key block: max score, sum of exp(s - max)
+  float* psum;
+  float* part;              // (H, nb, D) partial P.V
+};
+int dca_dec_nblocks(int M);
+int dca_dec_max_group();
+hipError_t launch_dca_decode(int dtype, int D, const DcaDecArgs& a, hipStream_t st);
+
 // decode: Q queries over one cache of M keys, query i at position q_pos0 + i seeing keys
 // [0, M - (Q - 1 - i)): shared_selection_triton_exact_2.py:235-271, 505-655
 struct DecodeArgs {

@@ -27,7 +27,7 @@ def test_library_exports_every_declared_symbol():
     for name in _declared():
         assert hasattr(lib, name), name
     assert sorted(native.EXPORTS) == _declared()
-    assert lib.sta_abi_version() == 3
+    assert lib.sta_abi_version() == 4
 
 
 def _args(**kw):
@@ -250,3 +250,49 @@ def test_decode_workspace_size_matches_layout():
     n2 = lib.sta_decode_workspace_size(ctypes.byref(_decode_args(M=40000, q_pos0=39999)))
     need2 = 32 * 128 * 4 + 32 * 40000 * 4 + 32 * 1024 * 40 * 4 + 32 * 4 + 32 * 32 * 130 * 4
     assert need2 <= n2 < need2 + 5 * 256
+
+
+def _dca_decode_args(**kw):
+    import _sta_native as native
+    a = native.DcaDecodeArgsC()
+    a.dtype, a.H, a.Hkv, a.M, a.D = 1, 32, 8, 5000, 128
+    a.chunk_size, a.local_window, a.mscale, a.scale = 3072, 512, 1.0, 0.088
+    for k, v in kw.items():
+        setattr(a, k, v)
+    return a
+
+
+def test_dca_decode_workspace_size():
+    import _sta_native as native
+    lib = native.lib()
+    n = lib.sta_dca_decode_workspace_size(ctypes.byref(_dca_decode_args()))
+    nb = (5000 + 255) // 256
+    need = 32 * 3 * 128 * 4 + 32 * 5000 * 4 + 2 * 32 * nb * 4 + 32 * nb * 128 * 4
+    assert need <= n < need + 5 * 256
+
+
+@pytest.mark.parametrize("field,value,code", [
+    ("D", 96, -2), ("Hkv", 5, -1), ("M", 0, -1), ("dtype", 7, -1), ("local_window", 0, -1),
+    ("local_window", 3072, -1), ("mscale", 0.0, -1), ("mscale", float("inf"), -1), ("Hkv", 1, -2),
+])
+def test_dca_decode_invalid_arguments_are_rejected(field, value, code):
+    import _sta_native as native
+    lib = native.lib()
+    a = _dca_decode_args(**{field: value})
+    assert lib.sta_dca_decode_workspace_size(ctypes.byref(a)) == 0
+    assert lib.sta_dca_decode(ctypes.byref(a), None) == code
+    assert len(lib.sta_last_error()) > 0
+
+
+def test_dca_rotate_keys_rejects_bad_arguments_before_any_launch():
+    import _sta_native as native
+    lib = native.lib()
+    a = native.DcaRotateArgsC()
+    a.dtype, a.heads, a.N, a.D, a.pos0 = 1, 8, 4, 128, 100
+    a.chunk_size, a.local_window, a.mscale = 3072, 512, 1.0
+    assert lib.sta_dca_rotate_keys(ctypes.byref(a), None) == -1            # inv_freq is NULL
+    a.D = 80
+    assert lib.sta_dca_rotate_keys(ctypes.byref(a), None) == -2
+    a.D, a.mscale = 128, -1.0
+    assert lib.sta_dca_rotate_keys(ctypes.byref(a), None) == -1
+    assert lib.sta_dca_rotate_keys(None, None) == -1
