@@ -216,6 +216,39 @@ int sta_pq_build_sets(const sta_pq_args* args, const int32_t* votes, const int32
 int sta_pq_gather_attention(const sta_pq_args* args, void* stream);
 
 /* ------------------------------------------------------------------------------------------ */
+/* Chunk-granular selection ("chunk_exact"): keys grouped into fixed chunks of chunk_size; per   */
+/* tile, the forced global / local chunks plus the n_chunk visible chunks of largest value (the */
+/* sum, or the mean over its threshold passers, of the passers' rank values: weighted votes for */
+/* STA_SCORE_MARGIN / EXPMASS, votes for FREQ; equal values in ascending chunk order) are kept; */
+/* their keys up to the tile's last query are attended by every query of the tile (pooled) at   */
+/* dense ranks under base RoPE.  At most (forced + n_chunk) chunks: the budget is exact.  The   */
+/* prefill runs on sta_pq_args (tile 32): PQ Kernel A, the chunk selection, PQ Kernel C with a  */
+/* pooled mask (every valid slot -1).                                                           */
+/* ------------------------------------------------------------------------------------------ */
+#define STA_CHUNK_SUM 0
+#define STA_CHUNK_MEAN 1
+
+typedef struct sta_chunk_params {
+  int32_t chunk_size;       /* C: keys per chunk (>= 1) */
+  int32_t n_chunk;          /* chunks selected beyond the forced ones (>= 1) */
+  int32_t chunk_agg;        /* STA_CHUNK_SUM or STA_CHUNK_MEAN */
+  int32_t* passers_kept;    /* optional (H, nt) at prefill, (H, Q) at decode: threshold passers
+                               among the kept keys (the measurement counter, chunked.py:205-208) */
+} sta_chunk_params;
+
+/* The whole chunked prefill.  Replaces shared_chunk_attention,
+ * shared_selection_triton_chunked.py:249-322; requires min(nC, forced + n_chunk) * chunk_size <=
+ * k_max (:270-278), forced = ceil(n_global / C) + ceil((n_local + tile - 1) / C) + 1 chunks.
+ * args->overflow may be NULL (a chunked tile never overflows). */
+int sta_chunk_attention(const sta_pq_args* args, const sta_chunk_params* chunk, void* stream);
+
+/* _build_sets_chunk alone from dense (H, num_tiles, N) votes and weighted votes (NULL for
+ * STA_SCORE_FREQ); writes idx, newpos_k, newpos_q, mask (pooled), usize, kept_size.  Replaces
+ * _build_sets_chunk, shared_selection_triton_chunked.py:149-243.  No workspace. */
+int sta_chunk_build_sets(const sta_pq_args* args, const sta_chunk_params* chunk, const int32_t* votes,
+                         const float* wvotes, int32_t num_tiles, void* stream);
+
+/* ------------------------------------------------------------------------------------------ */
 /* Per-query variant, PQ Stream: every query keeps its own threshold passers (plus forced      */
 /* global / local keys) and attends them in one sweep over aligned key blocks, newest first;   */
 /* key positions stream: npk = -(d + hi_t - j), d advancing per block by the largest per-query */
@@ -447,6 +480,18 @@ typedef struct sta_decode_args {
 
 /* Bytes of device workspace the decode entry points need for these arguments. */
 size_t sta_decode_workspace_size(const sta_decode_args* args);
+
+/* The chunk rule at decode from given scores (H, Q, M) fp32: per query, keep = s >= max - tau,
+ * chunk values over the query's keys (exp(s - max) of the kept keys, or 1 for STA_SCORE_FREQ;
+ * summed or averaged), the forced global chunks and the chunks of the local window, the n_chunk
+ * visible others of largest value, then the chunks' keys up to the query and the query itself
+ * at dense ranks into idx / newpos_k / newpos_q / set_size (kept count), and, when
+ * args->usize is non-NULL, each query's threshold passers into it.  args->rule and
+ * args->pct_decode are ignored.  Replaces _decode_build_sets_chunk,
+ * shared_selection_triton_chunked.py:411-489; attend with sta_decode_attend (base RoPE at the
+ * ranks, rope_scale_c 1). */
+int sta_decode_build_sets_chunk(const sta_decode_args* args, const sta_chunk_params* chunk, int32_t select_score,
+                                const float* scores, void* stream);
 
 /* Per-key scores of every query under (inv_freq, pos_scale, rope_scale) into `scores`
  * (H, Q, M) fp32 (row (h, i) written for keys < m_i).

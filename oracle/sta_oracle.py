@@ -20,6 +20,9 @@ next to it).  Each function names the reference lines it restates:
   decode_build_sets <- shared_selection_triton_exact_2.py:527-604 (_decode_build_sets)
   decode_attend     <- shared_selection_triton_exact_2.py:608-623 (_decode_attend_torch) and, with
                        causal=True, the slot rule of _decode_attend_kernelC (:626-655)
+  build_sets_chunk  <- shared_selection_triton_chunked.py:149-243 (_build_sets_chunk)
+  decode_build_sets_chunk <- shared_selection_triton_chunked.py:411-489 (_decode_build_sets_chunk)
+  dca_rotate_keys / dca_decode <- dca_kernel.py:434-435, 491-522 (the cached keys and decode)
 
 Arrays are numpy.  Half-precision tensors travel as uint16 bit patterns with a dtype code:
 0 = fp32, 1 = bf16, 2 = fp16.
@@ -47,7 +50,7 @@ def lib():
     global _LIB
     if _LIB is None:
         path = os.path.join(_HERE, "libsta_oracle.so")
-        srcs = ["sta_oracle.c", "sta_oracle_pq.c", "sta_oracle_decode.c", "sta_oracle_common.h"]
+        srcs = ["sta_oracle.c", "sta_oracle_pq.c", "sta_oracle_decode.c", "sta_oracle_chunk.c", "sta_oracle_common.h"]
         if not os.path.exists(path) or any(os.path.getmtime(path) < os.path.getmtime(
                 os.path.join(_HERE, f)) for f in srcs):
             build()
@@ -327,6 +330,85 @@ def shared_pq_attention(q, k, v, dtype, tau, inv_freq_a, inv_freq_c, pos_scale_a
                            k_max, block_k, q_pos_base)
     extras = dict(a, idx=idx, newpos_k=npk, newpos_q=npq, mask=mask)
     return out, us, ks, ov, extras
+
+
+# ---------------------------------------------------------------------------------------------
+# chunk-granular selection (shared_selection_triton_chunked.py)
+# ---------------------------------------------------------------------------------------------
+CHUNK_AGG = {"sum": 0, "mean": 1}
+
+
+def n_forced_chunks(chunk_size, n_global, n_local, tile):
+    """Chunks the forced global + local keys can occupy (chunked.py:115-129)."""
+    C = chunk_size
+    return (n_global + C - 1) // C + (n_local + tile - 1 + C - 1) // C + 1
+
+
+def derive_n_chunk(k_max, chunk_size, n_global, n_local, tile):
+    """Chunks to select so that forced + selected fill k_max (chunked.py:132-146)."""
+    assert k_max % chunk_size == 0
+    n = k_max // chunk_size - n_forced_chunks(chunk_size, n_global, n_local, tile)
+    assert n > 0
+    return n
+
+
+def build_sets_chunk(votes, wvotes, n_global, n_local, T, k_max, chunk_size, n_chunk, q_pos_base=0,
+                     select_score="expmass", chunk_agg="sum"):
+    """_build_sets_chunk (chunked.py:149-243).  Returns (idx, newpos_k, newpos_q, mask, usize,
+    kept_size, passers_kept); equal chunk values are taken in ascending chunk order."""
+    votes = _c(votes, np.int32)
+    H, nt, N = votes.shape
+    weighted = select_score != "freq" and wvotes is not None and wvotes.shape[-1] == N
+    wv = _c(wvotes, np.float32) if weighted else None
+    idx = np.empty((H, nt, k_max), np.int32)
+    npk = np.empty((H, nt, k_max), np.float32)
+    npq = np.empty((H, nt, T), np.float32)
+    mask = np.empty((H, nt, k_max), np.int32)
+    us, ks, pk = (np.empty((H, nt), np.int32) for _ in range(3))
+    lib().oracle_build_sets_chunk(
+        _p(votes), _p(wv), ctypes.c_int(H), ctypes.c_int(nt), ctypes.c_int(N), ctypes.c_int(T),
+        ctypes.c_int(k_max), ctypes.c_int(chunk_size), ctypes.c_int(n_chunk), ctypes.c_int(q_pos_base),
+        ctypes.c_int(n_global), ctypes.c_int(n_local), ctypes.c_int(int(weighted)),
+        ctypes.c_int(CHUNK_AGG[chunk_agg]), _p(idx), _p(npk), _p(npq), _p(mask), _p(us), _p(ks), _p(pk))
+    return idx, npk, npq, mask, us, ks, pk
+
+
+def decode_build_sets_chunk(scores, tau, q_pos0, n_global, n_local, k_max, chunk_size, n_chunk,
+                            select_score="expmass", chunk_agg="sum"):
+    """_decode_build_sets_chunk (chunked.py:411-489) for Q queries (H, Q, M) at q_pos0 + i over
+    the keys [0, M - (Q - 1 - i)).  Returns (idx (sentinel m_i), newpos_k, newpos_q, kept_size,
+    passers_kept)."""
+    scores = _c(scores, np.float32)
+    H, Q, M = scores.shape
+    idx = np.empty((H, Q, k_max), np.int32)
+    npk = np.empty((H, Q, k_max), np.float32)
+    npq = np.empty((H, Q), np.float32)
+    ks, pk = np.empty((H, Q), np.int32), np.empty((H, Q), np.int32)
+    lib().oracle_decode_build_sets_chunk(
+        _p(scores), ctypes.c_int(H), ctypes.c_int(Q), ctypes.c_int(M), _p(_c(tau, np.float32)),
+        ctypes.c_int(q_pos0), ctypes.c_int(n_global), ctypes.c_int(n_local), ctypes.c_int(k_max),
+        ctypes.c_int(chunk_size), ctypes.c_int(n_chunk), ctypes.c_int(int(select_score != "freq")),
+        ctypes.c_int(CHUNK_AGG[chunk_agg]), _p(idx), _p(npk), _p(npq), _p(ks), _p(pk))
+    return idx, npk, npq, ks, pk
+
+
+def shared_chunk_attention(q, k, v, dtype, tau, inv_freq_a, inv_freq_c, pos_scale_a=1.0, rope_scale_a=1.0,
+                           sm_scale=None, n_global=32, n_local=32, tile=32, k_max=4096, chunk_size=16,
+                           n_chunk=None, q_pos_base=0, select_score="expmass", chunk_agg="sum"):
+    """Composition (chunked.py:249-322): PQ Kernel A, _build_sets_chunk, pooled Kernel C.
+    Returns (out_f32, usize, kept_size, extras)."""
+    H, N, D = q.shape
+    if sm_scale is None:
+        sm_scale = 1.0 / math.sqrt(D)
+    if n_chunk is None:
+        n_chunk = derive_n_chunk(k_max, chunk_size, n_global, n_local, tile)
+    a = select_bits(q, k, dtype, tau, inv_freq_a, pos_scale_a, rope_scale_a, sm_scale, tile, q_pos_base,
+                    WMODES[select_score])
+    idx, npk, npq, mask, us, ks, pk = build_sets_chunk(a["votes"], a["wvotes"], n_global, n_local, tile, k_max,
+                                                       chunk_size, n_chunk, q_pos_base, select_score, chunk_agg)
+    out = gather_attn_mask(q, k, v, dtype, idx, npk, npq, mask, inv_freq_c, 1.0, sm_scale, tile, k_max,
+                           q_pos_base=q_pos_base)
+    return out, us, ks, dict(a, idx=idx, newpos_k=npk, newpos_q=npq, mask=mask, passers_kept=pk)
 
 
 def pqstream(q, k, v, dtype, tau, inv_freq_a, inv_freq_c, pos_scale_a=1.0, rope_scale_a=1.0,

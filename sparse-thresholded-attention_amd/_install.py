@@ -342,3 +342,80 @@ def pqs_forward(self, hidden_states, position_embeddings=None, attention_mask=No
         out = torch.cat(outs, dim=1).unsqueeze(0)
     attn_output = out.transpose(1, 2).reshape(B, N, -1).contiguous()
     return self.o_proj(attn_output), None
+
+
+# ---------------------------------------------------------------------------------------------
+# the chunked file's model integration (shared_selection_triton_chunked.py:495-643)
+# ---------------------------------------------------------------------------------------------
+def install_chunked(model, select_geom, apply_mscale, context_window, n_global, n_local, tile, k_max, max_len,
+                    decode_backend, prefill_mode, select_score, measure, chunk_size, n_chunk, chunk_agg):
+    """The per-query file's geometry (selection under select_geom, attention under base RoPE at
+    dense ranks, scale 1) with chunk selection at prefill and decode."""
+    install_perquery(model, select_geom, apply_mscale, context_window, n_global, n_local, tile, k_max, max_len,
+                     decode_backend, prefill_mode, select_score)
+    import transformers.models.llama.modeling_llama as ml
+    for layer in model.model.layers:
+        sa = layer.self_attn
+        sa.spi_chunk_size = chunk_size
+        sa.spi_n_chunk = n_chunk
+        sa.spi_chunk_agg = chunk_agg
+        sa.spi_measure = measure
+    ml.LlamaAttention.forward = chunk_forward
+
+
+def chunk_forward(self, hidden_states, position_embeddings=None, attention_mask=None, past_key_values=None,
+                  **kwargs):
+    import shared_selection_triton_chunked as chm
+    import _sta_native as native
+    B, N, _ = hidden_states.shape
+    assert B == 1, "batch size must be 1 (the kernels take one sequence, as the reference's)"
+    hs = (B, N, -1, self.head_dim)
+    q = self.q_proj(hidden_states).view(hs).transpose(1, 2)
+    k = self.k_proj(hidden_states).view(hs).transpose(1, 2)
+    v = self.v_proj(hidden_states).view(hs).transpose(1, 2)
+    cache = past_key_values if past_key_values is not None else kwargs.get("past_key_value", None)
+    past_len = 0
+    if cache is not None:
+        try:
+            past_len = int(cache.get_seq_length(self.spi_layer_idx))
+        except TypeError:
+            past_len = int(cache.get_seq_length())
+        k, v = cache.update(k, v, self.spi_layer_idx)
+    if past_len == 0:
+        if self.spi_geom == "yarn":
+            self.spi_pos_scale_a = 1.0
+        else:
+            L_target = self.spi_max_len if self.spi_max_len is not None else N
+            self.spi_pos_scale_a = min(1.0, self.spi_W / float(L_target))
+    if past_len == 0 and self.spi_prefill_mode == "shared":
+        out, usize, kept_size = chm.shared_chunk_attention(
+            q, k, v, self.tau_head_vec, self.spi_inv_freq_a, self.spi_inv_freq_c, pos_scale_a=self.spi_pos_scale_a,
+            rope_scale_a=self.spi_rope_scale_a, sm_scale=self.scaling, n_global=self.spi_ng, n_local=self.spi_nl,
+            tile=self.spi_tile, k_max=self.spi_kmax, chunk_size=self.spi_chunk_size, n_chunk=self.spi_n_chunk,
+            q_pos_base=past_len, select_score=self.spi_select_score, chunk_agg=self.spi_chunk_agg,
+            measure=self.spi_measure)
+        self.spi_last_usize = usize.detach()
+        self.spi_last_kept = kept_size.detach()
+    else:
+        # each query at position past_len + i over the keys [0, past_len + i], chunk rule
+        causal = self.spi_decode_backend == "triton"
+        outs = []
+        H = q.shape[1]
+        for c0 in range(0, N, PER_QUERY_BATCH):
+            c1 = min(N, c0 + PER_QUERY_BATCH)
+            M = past_len + c1
+            plan = native.DecodePlan(q[0, :, c0:c1, :], k[:, :, :M, :], v[:, :, :M, :], self.tau_head_vec,
+                                     self.spi_inv_freq_a, past_len + c0, self.spi_pos_scale_a, self.spi_rope_scale_a,
+                                     self.scaling, self.spi_ng, self.spi_nl, self.spi_kmax, 100.0, causal,
+                                     inv_freq_c=self.spi_inv_freq_c, pos_scale_c=1.0, rope_scale_c=1.0)
+            s = plan.scores(torch.empty((H, c1 - c0, M), dtype=torch.float32, device=q.device))
+            pk = torch.empty((H, c1 - c0), dtype=torch.int32, device=q.device)
+            us = torch.empty((H, c1 - c0), dtype=torch.int32, device=q.device)
+            r = plan.build_sets_chunk(s, self.spi_chunk_size, self.spi_n_chunk, self.spi_select_score,
+                                      self.spi_chunk_agg, passers_kept=pk, usize=us)
+            outs.append(plan.attend(r["idx"], r["newpos_k"], r["newpos_q"], r["set_size"]).clone())
+            if self.spi_measure:
+                chm._stat_acc(pk, us, r["set_size"], "decode")
+        out = torch.cat(outs, dim=1).unsqueeze(0)
+    attn_output = out.transpose(1, 2).reshape(B, N, -1).contiguous()
+    return self.o_proj(attn_output), None

@@ -20,10 +20,11 @@ EXPORTS = ["sta_abi_version", "sta_last_error", "sta_shared_workspace_size", "st
            "sta_shared_attention_noalloc",
            "sta_select_vote", "sta_build_sets", "sta_build_sets_weighted", "sta_gather_attention",
            "sta_pq_workspace_size", "sta_pq_attention", "sta_pq_select_bits", "sta_pq_build_sets",
-           "sta_pq_gather_attention", "sta_pqstream_workspace_size", "sta_pqstream_attention",
+           "sta_pq_gather_attention", "sta_chunk_attention", "sta_chunk_build_sets",
+           "sta_pqstream_workspace_size", "sta_pqstream_attention",
            "sta_dca_workspace_size", "sta_dca_attention", "sta_dca_rotate_keys", "sta_dca_decode_workspace_size",
            "sta_dca_decode", "sta_decode_workspace_size", "sta_decode_scores",
-           "sta_decode_build_sets", "sta_decode_attend", "sta_decode_attention"]
+           "sta_decode_build_sets", "sta_decode_build_sets_chunk", "sta_decode_attend", "sta_decode_attention"]
 SCORES = {"freq": 0, "margin": 1, "expmass": 2}
 
 
@@ -121,6 +122,15 @@ class DcaArgsC(ctypes.Structure):
         ("overflow20", ctypes.c_void_p), ("votes", ctypes.c_void_p), ("row_max", ctypes.c_void_p),
         ("mscale", ctypes.c_float),
     ]
+
+
+class ChunkParamsC(ctypes.Structure):
+    """Mirror of sta_chunk_params (include/sta.h)."""
+    _fields_ = [("chunk_size", ctypes.c_int32), ("n_chunk", ctypes.c_int32), ("chunk_agg", ctypes.c_int32),
+                ("passers_kept", ctypes.c_void_p)]
+
+
+CHUNK_AGG = {"sum": 0, "mean": 1}
 
 
 class DcaRotateArgsC(ctypes.Structure):
@@ -224,6 +234,14 @@ def lib():
             fn = getattr(L, name)
             fn.restype = ctypes.c_int
             fn.argtypes = [ctypes.POINTER(DecodeArgsC), ctypes.c_void_p, ctypes.c_void_p]
+        L.sta_chunk_attention.restype = ctypes.c_int
+        L.sta_chunk_attention.argtypes = [ctypes.POINTER(PqArgs), ctypes.POINTER(ChunkParamsC), ctypes.c_void_p]
+        L.sta_chunk_build_sets.restype = ctypes.c_int
+        L.sta_chunk_build_sets.argtypes = [ctypes.POINTER(PqArgs), ctypes.POINTER(ChunkParamsC), ctypes.c_void_p,
+                                           ctypes.c_void_p, ctypes.c_int32, ctypes.c_void_p]
+        L.sta_decode_build_sets_chunk.restype = ctypes.c_int
+        L.sta_decode_build_sets_chunk.argtypes = [ctypes.POINTER(DecodeArgsC), ctypes.POINTER(ChunkParamsC),
+                                                  ctypes.c_int32, ctypes.c_void_p, ctypes.c_void_p]
         L.sta_dca_rotate_keys.restype = ctypes.c_int
         L.sta_dca_rotate_keys.argtypes = [ctypes.POINTER(DcaRotateArgsC), ctypes.c_void_p]
         L.sta_dca_decode_workspace_size.restype = ctypes.c_size_t
@@ -661,6 +679,113 @@ def pq_build_sets(votes, bits, wvotes, n_global, n_local, T, k_max, q_pos_base=0
     return (r["idx"], r["newpos_k"], r["newpos_q"], r["mask"], r["usize"], r["kept_size"], r["overflow"])
 
 
+# ---------------------------------------------------------------------------------------------
+# chunk-granular selection (chunked variant)
+# ---------------------------------------------------------------------------------------------
+def _chunk_params(chunk_size, n_chunk, chunk_agg, passers_kept=None):
+    cp = ChunkParamsC()
+    cp.chunk_size, cp.n_chunk, cp.chunk_agg = int(chunk_size), int(n_chunk), CHUNK_AGG[chunk_agg]
+    cp.passers_kept = _ptr(passers_kept)
+    return cp
+
+
+class ChunkPlan:
+    """Outputs and workspace of the chunked prefill for one shape, allocated once; run() launches
+    PQ Kernel A, the chunk selection and the pooled Kernel C on the current stream and allocates
+    nothing.  Outputs: out, idx, newpos_k, newpos_q, mask, usize, kept_size, passers_kept (and
+    votes / bits / wvotes on request)."""
+
+    def __init__(self, q, k, v, tau, inv_freq_a, inv_freq_c, pos_scale_a=1.0, rope_scale_a=1.0, sm_scale=None,
+                 n_global=32, n_local=32, tile=32, k_max=4096, chunk_size=16, n_chunk=None, q_pos_base=0,
+                 select_score="expmass", chunk_agg="sum", want_votes=False):
+        qh, kh, vh, tau, ifa, ifc = _prep_inputs(q, k, v, tau, inv_freq_a, inv_freq_c)
+        H, N, D = qh.shape
+        self.device = dev = qh.device
+        if sm_scale is None:
+            sm_scale = 1.0 / math.sqrt(D)
+        if n_chunk is None:
+            n_chunk = derive_n_chunk(k_max, chunk_size, n_global, n_local, tile)
+        self.args = a = PqArgs()
+        _fill_pq(a, qh, kh, vh, tau, ifa, pos_scale_a, rope_scale_a, ifc, sm_scale, n_global, n_local,
+                 tile, k_max, q_pos_base, select_score)
+        self._keep = (qh, kh, vh, tau, ifa, ifc)
+        nt = (N + tile - 1) // tile
+        r = _pq_set_outputs(a, H, nt, tile, k_max, dev)
+        r["out"] = torch.empty((H, N, D), dtype=qh.dtype, device=dev)
+        r["passers_kept"] = torch.empty((H, nt), dtype=torch.int32, device=dev)
+        a.out = _ptr(r["out"])
+        if want_votes:
+            r["votes"] = torch.empty((H, nt, N), dtype=torch.int32, device=dev)
+            r["bits"] = torch.empty((H, nt, N), dtype=torch.int32, device=dev)
+            r["wvotes"] = torch.empty((H, nt, N), dtype=torch.float32, device=dev)
+        for name in ("votes", "bits", "wvotes"):
+            setattr(a, name, _ptr(r.get(name)))
+        self.chunk = _chunk_params(chunk_size, n_chunk, chunk_agg, r["passers_kept"])
+        self.out = r
+        self.workspace = _pq_workspace(a, dev)
+        self._events = None
+
+    def run(self, events=None):
+        """events: None or 5 recorded torch.cuda.Event(enable_timing=True), as for PqPlan."""
+        if events is not None:
+            self._events = (ctypes.c_void_p * 5)(*[e.cuda_event for e in events])
+            self.args.stage_events = ctypes.cast(self._events, ctypes.c_void_p)
+        else:
+            self.args.stage_events = None
+        _check(lib().sta_chunk_attention(ctypes.byref(self.args), ctypes.byref(self.chunk), _stream(self.device)),
+               "sta_chunk_attention")
+        return self.out
+
+
+def n_forced_chunks(chunk_size, n_global, n_local, tile):
+    """Worst-case chunks of the forced global + local keys (chunked.py:115-129)."""
+    C = chunk_size
+    return (n_global + C - 1) // C + (n_local + tile - 1 + C - 1) // C + 1
+
+
+def derive_n_chunk(k_max, chunk_size, n_global, n_local, tile):
+    """Chunks to select so that forced + selected fill k_max exactly (chunked.py:132-146)."""
+    C = chunk_size
+    assert k_max % C == 0, f"k_max={k_max} must be divisible by chunk_size={C}"
+    nf = n_forced_chunks(C, n_global, n_local, tile)
+    n = k_max // C - nf
+    assert n > 0, (f"chunk_size={C} leaves no budget: forced needs {nf} chunks ({nf * C} slots) of "
+                   f"k_max={k_max}. Raise k_max or lower chunk_size/n_global/n_local.")
+    return n
+
+
+def chunk_attention(q, k, v, tau, inv_freq_a, inv_freq_c, pos_scale_a=1.0, rope_scale_a=1.0, sm_scale=None,
+                    n_global=32, n_local=32, tile=32, k_max=4096, chunk_size=16, n_chunk=None, q_pos_base=0,
+                    select_score="expmass", chunk_agg="sum", want_votes=False):
+    """The whole chunked prefill on the device; returns a dict of device tensors."""
+    return ChunkPlan(q, k, v, tau, inv_freq_a, inv_freq_c, pos_scale_a, rope_scale_a, sm_scale, n_global, n_local,
+                     tile, k_max, chunk_size, n_chunk, q_pos_base, select_score, chunk_agg, want_votes).run()
+
+
+def chunk_build_sets(votes, wvotes, n_global, n_local, T, k_max, chunk_size, n_chunk, q_pos_base=0,
+                     select_score="expmass", chunk_agg="sum"):
+    """_build_sets_chunk on the device from dense (H, nt, N) votes / wvotes.  Returns the
+    reference's 6-tuple (idx, newpos_k, newpos_q, mask, usize, kept_size) and passers_kept."""
+    if not votes.is_cuda:
+        raise RuntimeError("chunk_build_sets runs on a HIP device only; got a CPU tensor")
+    votes = votes.to(torch.int32).contiguous()
+    H, nt, N = votes.shape
+    dev = votes.device
+    use_w = select_score != "freq" and wvotes is not None and wvotes.shape[-1] == N
+    wv = wvotes.to(torch.float32).contiguous() if use_w else None
+    a = PqArgs()
+    a.dtype, a.H, a.Hkv, a.N, a.D = 1, H, H, N, 64
+    a.n_global, a.n_local, a.tile, a.k_max = int(n_global), int(n_local), int(T), int(k_max)
+    a.q_pos_base = int(q_pos_base)
+    a.select_score = SCORES[select_score] if use_w else SCORES["freq"]
+    r = _pq_set_outputs(a, H, nt, T, k_max, dev)
+    pk = torch.empty((H, nt), dtype=torch.int32, device=dev)
+    cp = _chunk_params(chunk_size, n_chunk, chunk_agg, pk)
+    _check(lib().sta_chunk_build_sets(ctypes.byref(a), ctypes.byref(cp), _ptr(votes), _ptr(wv), nt, _stream(dev)),
+           "sta_chunk_build_sets")
+    return (r["idx"], r["newpos_k"], r["newpos_q"], r["mask"], r["usize"], r["kept_size"]), pk
+
+
 def pq_gather_attention(q, k, v, inv_freq_c, idx, newpos_k, newpos_q, mask, sm_scale, tile, k_max,
                         q_pos_base=0, kept_size=None):
     """PQ Kernel C alone.  Returns out (H, N, D) in q.dtype."""
@@ -1004,6 +1129,23 @@ class DecodePlan:
         """Selection alone from scores (H, Q, M) fp32 into idx / newpos_k / newpos_q / set_size."""
         _check(lib().sta_decode_build_sets(ctypes.byref(self.args), _ptr(scores), _stream(self.device)),
                "sta_decode_build_sets")
+        return self.out
+
+    def build_sets_chunk(self, scores, chunk_size, n_chunk, select_score="expmass", chunk_agg="sum",
+                         passers_kept=None, usize=None):
+        """The chunk rule (_decode_build_sets_chunk, chunked.py:411-489) from scores (H, Q, M) fp32
+        into idx / newpos_k / newpos_q / set_size (the kept count); passers_kept and usize (H, Q)
+        int32 receive the threshold passers among the kept keys and in all, when given."""
+        cp = _chunk_params(chunk_size, n_chunk, chunk_agg, passers_kept)
+        a = self.args
+        saved = a.usize
+        a.usize = _ptr(usize)
+        try:
+            _check(lib().sta_decode_build_sets_chunk(ctypes.byref(a), ctypes.byref(cp), SCORES[select_score],
+                                                     _ptr(scores), _stream(self.device)),
+                   "sta_decode_build_sets_chunk")
+        finally:
+            a.usize = saved
         return self.out
 
     def attend(self, idx, newpos_k, newpos_q, set_size=None):

@@ -19,7 +19,7 @@ HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = os.environ.get("STA_OFFLOAD_ARCH", "gfx950")
 SOURCES = ["sta_score.hip", "sta_select.hip", "sta_select_w.hip", "sta_gather.hip", "sta_pq.hip", "sta_stream.hip", "sta_api.hip",
            "sta_dca.hip", "sta_api_pq.hip", "sta_api_stream.hip", "sta_api_dca.hip", "sta_decode.hip",
-           "sta_api_decode.hip", "sta_rows.hip", "sta_dca_sel.hip", "sta_dca_dec.hip"]
+           "sta_api_decode.hip", "sta_rows.hip", "sta_dca_sel.hip", "sta_dca_dec.hip", "sta_chunk.hip"]
 FLAGS = ["--offload-arch=" + ARCH, "-O3", "-fPIC", "-std=c++17", "-Wall",
          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
          "-I" + CSRC, "-I" + os.path.join(os.path.dirname(HERE), "include")]

@@ -222,6 +222,46 @@ int sta_decode_build_sets(const sta_decode_args* a, const float* scores, void* s
   return dec_select(a, dec_args_of(a, L), scores, (hipStream_t)stream);
 }
 
+int sta_decode_build_sets_chunk(const sta_decode_args* a, const sta_chunk_params* cp, int32_t select_score,
+                                const float* scores, void* stream) {
+  int rc = dec_check(a);
+  if (rc != STA_OK) return rc;
+  if (!cp) return fail(STA_ERR_INVALID_ARG, "chunk params are NULL");
+  if (!scores) return fail(STA_ERR_INVALID_ARG, "scores must be non-NULL");
+  if (cp->chunk_size < 1 || cp->n_chunk < 1)
+    return fail(STA_ERR_INVALID_ARG, "chunk_size=%d and n_chunk=%d must be >= 1", cp->chunk_size, cp->n_chunk);
+  if (cp->chunk_agg != STA_CHUNK_SUM && cp->chunk_agg != STA_CHUNK_MEAN)
+    return fail(STA_ERR_INVALID_ARG, "chunk_agg %d is not STA_CHUNK_SUM or STA_CHUNK_MEAN", cp->chunk_agg);
+  if (select_score < STA_SCORE_FREQ || select_score > STA_SCORE_EXPMASS)
+    return fail(STA_ERR_INVALID_ARG, "select_score %d is not one of STA_SCORE_*", select_score);
+  if (chunk_select_lds_bytes(a->M, cp->chunk_size) > 160 * 1024)
+    return fail(STA_ERR_UNSUPPORTED, "M=%d in chunks of %d needs more than 160 KB of LDS", a->M, cp->chunk_size);
+  if (!a->tau || !a->idx || !a->newpos_k || !a->newpos_q || !a->set_size)
+    return fail(STA_ERR_INVALID_ARG, "tau, idx, newpos_k, newpos_q and set_size must be non-NULL");
+  ChunkDecodeArgs d{};
+  d.scores = scores;
+  d.tau = a->tau;
+  d.H = a->H;
+  d.Q = a->Q;
+  d.M = a->M;
+  d.q_pos0 = a->q_pos0;
+  d.k_max = a->k_max;
+  d.n_global = a->n_global;
+  d.n_local = a->n_local;
+  d.C = cp->chunk_size;
+  d.n_chunk = cp->n_chunk;
+  d.weighted = select_score != STA_SCORE_FREQ;
+  d.mean = cp->chunk_agg == STA_CHUNK_MEAN;
+  d.idx = a->idx;
+  d.newpos_k = a->newpos_k;
+  d.newpos_q = a->newpos_q;
+  d.kept_size = a->set_size;
+  d.passers_kept = cp->passers_kept;
+  d.usize = a->usize;
+  hipError_t e = launch_chunk_decode_select(d, (hipStream_t)stream);
+  return e == hipSuccess ? STA_OK : hip_fail(e, "chunk decode select kernel");
+}
+
 int sta_decode_attend(const sta_decode_args* a, void* stream) {
   int rc = dec_check(a);
   if (rc != STA_OK) return rc;

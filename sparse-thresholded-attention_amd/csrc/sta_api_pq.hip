@@ -175,6 +175,52 @@ int pq_run_gather(const sta_pq_args* a, int nt, hipStream_t st) {
   return STA_OK;
 }
 
+// the chunked variant's parameters and its exact budget (chunked.py:115-146, 270-278)
+int chunk_check(const sta_pq_args* a, const sta_chunk_params* cp) {
+  if (!cp) return fail(STA_ERR_INVALID_ARG, "chunk params are NULL");
+  if (cp->chunk_size < 1) return fail(STA_ERR_INVALID_ARG, "chunk_size=%d must be >= 1", cp->chunk_size);
+  if (cp->n_chunk < 1) return fail(STA_ERR_INVALID_ARG, "n_chunk=%d must be >= 1", cp->n_chunk);
+  if (cp->chunk_agg != STA_CHUNK_SUM && cp->chunk_agg != STA_CHUNK_MEAN)
+    return fail(STA_ERR_INVALID_ARG, "chunk_agg %d is not STA_CHUNK_SUM or STA_CHUNK_MEAN", cp->chunk_agg);
+  const int64_t C = cp->chunk_size;
+  const int64_t nf = (a->n_global + C - 1) / C + (a->n_local + a->tile - 1 + C - 1) / C + 1;
+  const int64_t nC = (a->N + C - 1) / C;
+  const int64_t chunks = nC < nf + cp->n_chunk ? nC : nf + cp->n_chunk;
+  if (chunks * C > a->k_max)
+    return fail(STA_ERR_INVALID_ARG, "budget overflow: min(nC=%lld, %lld forced + %d selected) * %d > k_max=%d",
+                (long long)nC, (long long)nf, cp->n_chunk, cp->chunk_size, a->k_max);
+  if (chunk_select_lds_bytes(a->N, cp->chunk_size) > 160 * 1024)
+    return fail(STA_ERR_UNSUPPORTED, "N=%d in chunks of %d needs more than 160 KB of LDS", a->N, cp->chunk_size);
+  if (!a->idx || !a->newpos_k || !a->newpos_q || !a->mask || !a->usize || !a->kept_size)
+    return fail(STA_ERR_INVALID_ARG, "a selection output pointer is NULL");
+  return STA_OK;
+}
+
+ChunkSelectArgs chunk_select_args_of(const sta_pq_args* a, const sta_chunk_params* cp, int nt) {
+  ChunkSelectArgs s;
+  memset(&s, 0, sizeof(s));
+  s.H = a->H;
+  s.nt = nt;
+  s.N = a->N;
+  s.T = a->tile;
+  s.k_max = a->k_max;
+  s.q_pos_base = a->q_pos_base;
+  s.n_global = a->n_global;
+  s.n_local = a->n_local;
+  s.C = cp->chunk_size;
+  s.n_chunk = cp->n_chunk;
+  s.mean = cp->chunk_agg == STA_CHUNK_MEAN;
+  s.idx = a->idx;
+  s.newpos_k = a->newpos_k;
+  s.newpos_q = a->newpos_q;
+  s.mask = a->mask;
+  s.usize = a->usize;
+  s.kept_size = a->kept_size;
+  s.overflow = a->overflow;
+  s.passers_kept = cp->passers_kept;
+  return s;
+}
+
 }  // namespace
 
 extern "C" {
@@ -267,6 +313,54 @@ int sta_pq_gather_attention(const sta_pq_args* args, void* stream) {
     return fail(STA_ERR_INVALID_ARG, "inv_freq_c, out, idx, newpos_k, newpos_q and mask must be non-NULL");
   const int nt = (args->N + args->tile - 1) / args->tile;
   return pq_run_gather(args, nt, (hipStream_t)stream);   // kept_size, when given, bounds the slots
+}
+
+int sta_chunk_build_sets(const sta_pq_args* args, const sta_chunk_params* cp, const int32_t* votes,
+                         const float* wvotes, int32_t num_tiles, void* stream) {
+  int rc = pq_check_common(args);
+  if (rc != STA_OK) return rc;
+  if ((rc = chunk_check(args, cp)) != STA_OK) return rc;
+  if (!votes) return fail(STA_ERR_INVALID_ARG, "votes must be non-NULL");
+  if (args->select_score != STA_SCORE_FREQ && !wvotes)
+    return fail(STA_ERR_INVALID_ARG, "wvotes is NULL but select_score ranks by weighted votes");
+  if (num_tiles < 1) return fail(STA_ERR_INVALID_ARG, "num_tiles=%d must be >= 1", num_tiles);
+  ChunkSelectArgs s = chunk_select_args_of(args, cp, num_tiles);
+  s.votes = votes;
+  s.wvotes = args->select_score == STA_SCORE_FREQ ? nullptr : wvotes;
+  s.stride = args->N;
+  s.dense = 1;
+  hipError_t e = launch_chunk_select(s, (hipStream_t)stream);
+  return e == hipSuccess ? STA_OK : hip_fail(e, "chunk select kernel");
+}
+
+int sta_chunk_attention(const sta_pq_args* args, const sta_chunk_params* cp, void* stream) {
+  int rc = pq_check_common(args);
+  if (rc != STA_OK) return rc;
+  if ((rc = chunk_check(args, cp)) != STA_OK) return rc;
+  if ((rc = pq_check_qkv(args, true)) != STA_OK) return rc;
+  if (!args->tau || !args->inv_freq_a || !args->inv_freq_c || !args->out)
+    return fail(STA_ERR_INVALID_ARG, "tau, inv_freq_a, inv_freq_c and out must be non-NULL");
+  const PqLayout L = pq_layout_of(args);
+  if ((rc = pq_check_workspace(args, L)) != STA_OK) return rc;
+  hipStream_t st = (hipStream_t)stream;
+  if ((rc = pq_run_kernel_a(args, L, st)) != STA_OK) return rc;
+  if ((rc = mark_event(args->stage_events, 2, st)) != STA_OK) return rc;
+  char* ws = (char*)args->workspace;
+  ChunkSelectArgs s = chunk_select_args_of(args, cp, L.nt);
+  s.bits = (const uint32_t*)(ws + L.bits_off);
+  s.wvotes = args->select_score == STA_SCORE_FREQ ? nullptr : (const float*)(ws + L.wv_off);
+  s.stride = L.stride;
+  s.dense = 0;
+  hipError_t e = launch_chunk_select(s, st);
+  if (e != hipSuccess) return hip_fail(e, "chunk select kernel");
+  if (args->votes || args->bits || args->wvotes) {
+    e = launch_expand_pq(s.bits, s.wvotes, L.stride, args->H, L.nt, args->N, args->tile, args->q_pos_base,
+                         args->votes, args->bits, args->wvotes, st);
+    if (e != hipSuccess) return hip_fail(e, "vote expansion (chunked)");
+  }
+  if ((rc = mark_event(args->stage_events, 3, st)) != STA_OK) return rc;
+  if ((rc = pq_run_gather(args, L.nt, st)) != STA_OK) return rc;
+  return mark_event(args->stage_events, 4, st);
 }
 
 }  // extern "C"

@@ -112,6 +112,38 @@ struct PqSelectArgs {
   uint8_t* overflow;
 };
 
+// chunk-granular set construction: shared_selection_triton_chunked.py:149-243, 411-489
+struct ChunkSelectArgs {
+  const uint32_t* bits;   // (H, nt, stride) compact keep bits (votes = popcount), or null
+  const int32_t* votes;   // (H, nt, stride) votes, or null
+  const float* wvotes;    // (H, nt, stride) weighted votes, or null (rank by votes)
+  int64_t stride;
+  int dense;              // 1: all N keys valid; 0: keys >= min(N, tile end) read as zero
+  int H, nt, N, T, k_max, q_pos_base, n_global, n_local, C, n_chunk, mean;
+  int32_t* idx;
+  float* newpos_k;
+  float* newpos_q;
+  int32_t* mask;          // or null
+  int32_t* usize;
+  int32_t* kept_size;
+  uint8_t* overflow;      // or null (always 0)
+  int32_t* passers_kept;  // or null
+};
+struct ChunkDecodeArgs {
+  const float* scores;    // (H, Q, M)
+  const float* tau;       // (H,)
+  int H, Q, M, q_pos0, k_max, n_global, n_local, C, n_chunk, weighted, mean;
+  int32_t* idx;           // (H, Q, k_max), sentinel m_i
+  float* newpos_k;
+  float* newpos_q;        // (H, Q)
+  int32_t* kept_size;     // (H, Q)
+  int32_t* passers_kept;  // or null
+  int32_t* usize;         // or null: (H, Q) threshold passers of the query
+};
+size_t chunk_select_lds_bytes(int n_keys, int C);
+hipError_t launch_chunk_select(const ChunkSelectArgs& a, hipStream_t st);
+hipError_t launch_chunk_decode_select(const ChunkDecodeArgs& a, hipStream_t st);
+
 // PQ Stream attend sweep: pqstream_kernel.py:174-368
 struct StreamArgs {
   const void* q;
