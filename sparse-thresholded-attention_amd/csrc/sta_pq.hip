@@ -63,6 +63,7 @@ __global__ __launch_bounds__(256) void pq_select_kernel(PqSelectArgs a) {
   int* tmp = hist + 256;                                    // 8
   int* misc = tmp + 8;                                      // 8
   float* qnp = (float*)(misc + 8);                          // T (<= 64)
+  int32_t* sidx = (int32_t*)(qnp + 64);                     // k_max: kept keys in rank order
 
   const int64_t tstart = (int64_t)a.q_pos_base + (int64_t)t * T;   // perquery.py:377
   const int64_t lo = tstart - a.n_local + 1, hi_l = tstart + T - 1;
@@ -236,20 +237,27 @@ __global__ __launch_bounds__(256) void pq_select_kernel(PqSelectArgs a) {
       eq += myrow[j - j0] == V && !is_forced(j) && overflow && budget > 0;
       if (kp) {
         rank += 1;
-        if (rank < a.k_max) {
-          irow[rank] = j;
-          nkrow[rank] = (float)rank;
-          mrow[rank] = is_forced(j) ? -1 : (int32_t)(j < hi_keys ? brow[j] : 0u);
-        }
+        if (rank < a.k_max) sidx[rank] = j;
       }
       if (j >= qlo && j <= qhi) qnp[j - qlo] = (float)rank;   // rank0 = cumsum - 1
     }
   }
   __syncthreads();
-  for (int s = min(kept_total, a.k_max) + tid; s < a.k_max; s += 256) {
-    irow[s] = N;
-    nkrow[s] = 0.0f;
-    mrow[s] = 0;
+  // slots in order, one per lane: coalesced stores (the ranks above are contiguous per thread,
+  // which would scatter every store instruction over 64 cache lines); the kept keys ascend with
+  // the slot, so the bit reads for the mask are nearly coalesced too
+  const int nk = min(kept_total, a.k_max);
+  for (int s = tid; s < a.k_max; s += 256) {
+    if (s < nk) {
+      const int j = sidx[s];
+      irow[s] = j;
+      nkrow[s] = (float)s;
+      mrow[s] = is_forced(j) ? -1 : (int32_t)(j < hi_keys ? brow[j] : 0u);
+    } else {
+      irow[s] = N;
+      nkrow[s] = 0.0f;
+      mrow[s] = 0;
+    }
   }
   float* nqrow = a.newpos_q + ((int64_t)h * a.nt + t) * T;
   for (int i = tid; i < T; i += 256) {
@@ -284,9 +292,8 @@ __global__ __launch_bounds__(256) void expand_pq_kernel(const uint32_t* __restri
 }
 
 size_t pq_select_lds_bytes(int N, int k_max) {
-  (void)k_max;
   const size_t per = (size_t)(N + 255) / 256;
-  return 256 * (per | 1) * 4 + (256 + 8 + 8) * 4 + 64 * 4;
+  return 256 * (per | 1) * 4 + (256 + 8 + 8) * 4 + 64 * 4 + (size_t)k_max * 4;
 }
 
 hipError_t launch_pq_select(const PqSelectArgs& a, hipStream_t st) {

@@ -117,21 +117,37 @@ __global__ __launch_bounds__(256) void select_w_kernel(SelectArgs a) {
   const int j0 = tid * per, j1 = min(j0 + per, N);
   auto is_forced = [&](int j) { return j < a.n_global || (j >= lo && j <= hi_l); };   // exact_2.py:290-293
 
-  // ---- stage the rank keys (coalesced: key j by thread j % 256), U = #(votes > 0) ----
+  // ---- stage the rank keys (coalesced: key j by thread j % 256), U = #(votes > 0); SU loads of
+  //      each array in flight per lane ----
   int cu = 0;
-  for (int j = tid; j < 256 * per; j += 256) {
-    uint32_t key = 0;
-    if (j < N) {
-      const int v = j < hi_keys ? (int)vrow[j] : 0;
-      const float w = j < hi_keys ? wrow[j] : 0.0f;
-      cu += v > 0;                                                         // exact_2.py:296
-      const float tb = 1e-6f * (float)v;                                   // exact_2.py:302
-      key = order_key(w + tb);
-      if (a.votes_out) a.votes_out[((int64_t)h * a.nt + t) * N + j] = v;
-      if (a.wvotes_out) a.wvotes_out[((int64_t)h * a.nt + t) * N + j] = w;
+  constexpr int SU = 8;
+  for (int jb = 0; jb < 256 * per; jb += 256 * SU) {
+    int vv[SU];
+    float wv[SU];
+#pragma unroll
+    for (int u = 0; u < SU; ++u) {
+      const int j = jb + u * 256 + tid;
+      const bool ok = j < hi_keys;
+      vv[u] = ok ? (int)vrow[j] : 0;
+      wv[u] = ok ? wrow[j] : 0.0f;
     }
-    const uint32_t row = per == 1 ? (uint32_t)j : __umulhi((uint32_t)j, inv_per);
-    rkb[row * PS + (j - row * per)] = key;
+#pragma unroll
+    for (int u = 0; u < SU; ++u) {
+      const int j = jb + u * 256 + tid;
+      if (j >= 256 * per) break;
+      uint32_t key = 0;
+      if (j < N) {
+        const int v = vv[u];
+        const float w = wv[u];
+        cu += v > 0;                                                       // exact_2.py:296
+        const float tb = 1e-6f * (float)v;                                 // exact_2.py:302
+        key = order_key(w + tb);
+        if (a.votes_out) a.votes_out[((int64_t)h * a.nt + t) * N + j] = v;
+        if (a.wvotes_out) a.wvotes_out[((int64_t)h * a.nt + t) * N + j] = w;
+      }
+      const uint32_t row = per == 1 ? (uint32_t)j : __umulhi((uint32_t)j, inv_per);
+      rkb[row * PS + (j - row * per)] = key;
+    }
   }
   __syncthreads();
   const int64_t usize = w_block_sum(cu, tmp);
