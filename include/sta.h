@@ -91,9 +91,10 @@ typedef struct sta_shared_args {
                             * NULL to skip; ignored for STA_SCORE_FREQ */
 } sta_shared_args;
 
-/* ABI version of this header (bumped on any layout change of an argument struct): 4.
+/* ABI version of this header (bumped on any layout change of an argument struct): 5.
  * 2: sta_shared_args.select_score; 3: the rule fields of sta_decode_args and config 4's fields of
- * sta_dca_args; 4: sta_dca_args.mscale, sta_dca_rotate_keys and sta_dca_decode. */
+ * sta_dca_args; 4: sta_dca_args.mscale, sta_dca_rotate_keys and sta_dca_decode; 5: the chunked
+ * entry points and sta_pqstream_args.bits. */
 int sta_abi_version(void);
 
 /* Description of the last error returned on the calling thread ("" if none). */
@@ -284,13 +285,29 @@ typedef struct sta_pqstream_args {
   size_t workspace_bytes;
   void* const* stage_events; /* NULL or 5 hipEvent_t: before RoPE, before the score passes,
                                 before the attend pre-rotation, before the sweep, after it */
+  /* ABI 5: optional (H, nt, N) int32 threshold keep bits s >= m - tau (bit i = row i of the
+   * tile, causal, rows < N; forced keys not included), as the sweep applied them.  Only keys up
+   * to each tile's last query are written: pass zeroed memory. */
+  int32_t* bits;
+  /* ABI 5: STA_STREAM_AUTO (0): the separate keep-bit pass while its buffer, H * ceil(N / 32) *
+   * N * 4 bytes, stays within 4 GiB, the fused sweep beyond; STA_STREAM_FUSED (1): always the
+   * fused sweep (error where none exists: fp32 inputs with block_n 64); STA_STREAM_UNFUSED (2). */
+  int32_t fused;
 } sta_pqstream_args;
+
+#define STA_STREAM_AUTO 0
+#define STA_STREAM_FUSED 1
+#define STA_STREAM_UNFUSED 2
 
 /* Bytes of device workspace sta_pqstream_attention needs for these arguments. */
 size_t sta_pqstream_workspace_size(const sta_pqstream_args* args);
 
 /* The PQ Stream prefill.  Replaces pqstream_attention and its fused _pqstream_kernel,
- * pqstream_kernel.py:174-368, 498-564.  block_n in {32, 64}; q_pos_base must be 0 (:512). */
+ * pqstream_kernel.py:174-368, 498-564.  block_n in {32, 64}; q_pos_base must be 0 (:512).
+ * Pass 1 (each query's exact row max) runs first.  Fused (sta_pqstream_args.fused), the sweep
+ * then computes each block's keep bits itself, as the reference's fused kernel does, with no
+ * keep-bit buffer; unfused, pass 2 writes one keep bit per (query, key) and the sweep reads them
+ * -- faster at moderate N, but the buffer grows as H N^2 / 8 bytes. */
 int sta_pqstream_attention(const sta_pqstream_args* args, void* stream);
 
 /* ------------------------------------------------------------------------------------------ */

@@ -97,8 +97,11 @@ class StreamArgsC(ctypes.Structure):
         ("out", ctypes.c_void_p), ("span", ctypes.c_void_p), ("kept", ctypes.c_void_p),
         ("blocks", ctypes.c_void_p), ("skipped", ctypes.c_void_p), ("row_max", ctypes.c_void_p),
         ("workspace", ctypes.c_void_p), ("workspace_bytes", ctypes.c_size_t),
-        ("stage_events", ctypes.c_void_p),
+        ("stage_events", ctypes.c_void_p), ("bits", ctypes.c_void_p), ("fused", ctypes.c_int32),
     ]
+
+
+STREAM_FUSED = {"auto": 0, "fused": 1, "unfused": 2}
 
 
 class DcaArgsC(ctypes.Structure):
@@ -248,7 +251,7 @@ def lib():
         L.sta_dca_decode_workspace_size.argtypes = [ctypes.POINTER(DcaDecodeArgsC)]
         L.sta_dca_decode.restype = ctypes.c_int
         L.sta_dca_decode.argtypes = [ctypes.POINTER(DcaDecodeArgsC), ctypes.c_void_p]
-        if L.sta_abi_version() != 4:
+        if L.sta_abi_version() != 5:
             raise ImportError("libsta_hip.so ABI version mismatch")
         _LIB = L
     return _LIB
@@ -818,7 +821,10 @@ class StreamPlan:
 
     def __init__(self, q, k, v, tau, inv_freq_a, inv_freq_c, pos_scale_a=1.0, rope_scale_a=1.0,
                  sm_scale=None, n_global=32, n_local=32, tile=32, block_n=32, pos_advance="max",
-                 q_pos_base=0, use_skip=True, want_row_max=False):
+                 q_pos_base=0, use_skip=True, want_row_max=False, want_bits=False, fused="auto"):
+        """want_bits: also return bits (H, nt, N) int32, the threshold keep bits the sweep applied
+        (zero past each tile's last query).  fused: "auto" (the separate keep-bit pass while its
+        buffer stays within 4 GiB), "fused" (the sweep computes the keep bits) or "unfused"."""
         qh, kh, vh, tau, ifa, ifc = _prep_inputs(q, k, v, tau, inv_freq_a, inv_freq_c)
         H, N, D = qh.shape
         self.device = dev = qh.device
@@ -838,6 +844,7 @@ class StreamPlan:
         a.inv_freq_c, a.sm_scale = _ptr(ifc), float(sm_scale)
         a.n_global, a.n_local, a.tile, a.block_n = int(n_global), int(n_local), int(tile), int(block_n)
         a.pos_advance, a.use_skip, a.q_pos_base = ADVANCES[pos_advance], int(bool(use_skip)), int(q_pos_base)
+        a.fused = STREAM_FUSED[fused]
         self._keep = (qh, kh, vh, tau, ifa, ifc)
         nt = (N + tile - 1) // tile
         r = {"out": torch.empty((H, N, D), dtype=qh.dtype, device=dev),
@@ -847,7 +854,9 @@ class StreamPlan:
              "skipped": torch.empty((H, nt), dtype=torch.float32, device=dev)}
         if want_row_max:
             r["row_max"] = torch.empty((H, N), dtype=torch.float32, device=dev)
-        for name in ("out", "span", "kept", "blocks", "skipped", "row_max"):
+        if want_bits:
+            r["bits"] = torch.zeros((H, nt, N), dtype=torch.int32, device=dev)
+        for name in ("out", "span", "kept", "blocks", "skipped", "row_max", "bits"):
             setattr(a, name, _ptr(r.get(name)))
         self.out = r
         n = lib().sta_pqstream_workspace_size(ctypes.byref(a))
@@ -870,11 +879,11 @@ class StreamPlan:
 
 def pqstream_attention(q, k, v, tau, inv_freq_a, inv_freq_c, pos_scale_a=1.0, rope_scale_a=1.0,
                        sm_scale=None, n_global=32, n_local=32, tile=32, block_n=32, pos_advance="max",
-                       q_pos_base=0, use_skip=True, want_row_max=False):
+                       q_pos_base=0, use_skip=True, want_row_max=False, want_bits=False, fused="auto"):
     """The whole PQ Stream prefill on the device; returns a dict of device tensors."""
     return StreamPlan(q, k, v, tau, inv_freq_a, inv_freq_c, pos_scale_a, rope_scale_a, sm_scale,
                       n_global, n_local, tile, block_n, pos_advance, q_pos_base, use_skip,
-                      want_row_max).run()
+                      want_row_max, want_bits, fused).run()
 
 
 # ---------------------------------------------------------------------------------------------

@@ -287,7 +287,7 @@ int scratch_of_current_device(void** out) {
 
 extern "C" {
 
-int sta_abi_version(void) { return 4; }
+int sta_abi_version(void) { return 5; }
 
 const char* sta_last_error(void) { return g_last_error.c_str(); }
 

@@ -1,8 +1,11 @@
 // sta_api_stream.hip -- the C ABI of PQ Stream (include/sta.h, sta_pqstream_*).
 //
-// Four launches on one stream: the selection-geometry RoPE pre-kernel (Q and K fragments), the
-// two score passes with the per-query epilogue (exact row max, then one keep bit per (query,
-// key)), the attend-geometry pre-rotation of K at absolute positions, and the stream sweep.
+// Launches on one stream: the selection-geometry RoPE pre-kernel (Q and K fragments), pass 1 of
+// the score kernel (each query's exact row max, left as its keep threshold on the raw dot), the
+// attend-geometry pre-rotation of K at absolute positions, and the stream sweep, which computes
+// the keep bits itself (the fused sweep).  Where the fused sweep's staging does not fit the LDS
+// (fp32 inputs with block_n 64) pass 2 of the score kernel writes the keep bits instead and the
+// sweep reads them.
 #include <string.h>
 
 #include "../../include/sta.h"
@@ -14,10 +17,13 @@ using namespace sta_api;
 
 namespace {
 
+constexpr size_t kStreamBitsAuto = (size_t)4 << 30;   // 4 GiB
+
 struct StreamLayout {
   int nt, q_rows_pad, k_rows_pad, Npad, planes;
+  bool fused;
   int64_t stride;
-  size_t qfrag_off, kfrag_off, bits_off, ktil_off, total;
+  size_t qfrag_off, kfrag_off, bits_off, xthr_off, ktil_off, total;
 };
 
 StreamLayout stream_layout_of(const sta_pqstream_args* a) {
@@ -34,8 +40,14 @@ StreamLayout stream_layout_of(const sta_pqstream_args* a) {
   off = align256(off + frag_region_bytes(a->H, L.q_rows_pad, a->D));
   L.kfrag_off = off;
   off = align256(off + frag_region_bytes(a->Hkv, L.k_rows_pad, a->D));
-  L.bits_off = off;
-  off = align256(off + (size_t)a->H * L.nt * L.stride * 4);
+  // the keep-bit buffer holds H * nt * N words: the fused sweep replaces it where asked to, or
+  // automatically once it would pass kStreamBitsAuto bytes
+  const size_t bits_bytes = (size_t)a->H * L.nt * L.stride * 4;
+  const bool can = stream_can_fuse(a->dtype, a->D, a->block_n);
+  L.fused = can && (a->fused == STA_STREAM_FUSED || (a->fused == STA_STREAM_AUTO && bits_bytes > kStreamBitsAuto));
+  L.bits_off = L.xthr_off = off;
+  if (L.fused) off = align256(off + (size_t)a->H * L.q_rows_pad * 4);        // thresholds
+  else off = align256(off + (size_t)a->H * L.nt * L.stride * 4);             // keep bits
   L.ktil_off = off;
   off = align256(off + (size_t)a->Hkv * L.Npad * L.planes * a->D * 2);
   L.total = off;
@@ -62,7 +74,11 @@ int stream_check(const sta_pqstream_args* a) {
     return fail(STA_ERR_INVALID_ARG, "pos_advance %d is not STA_ADV_MAX / STA_ADV_FULL", a->pos_advance);
   if (a->n_global < 0 || a->n_local < 0)
     return fail(STA_ERR_INVALID_ARG, "n_global=%d / n_local=%d must be >= 0", a->n_global, a->n_local);
-  if (stream_lds_bytes(a->dtype, a->D, a->block_n) > 160 * 1024)
+  if (a->fused != STA_STREAM_AUTO && a->fused != STA_STREAM_FUSED && a->fused != STA_STREAM_UNFUSED)
+    return fail(STA_ERR_INVALID_ARG, "fused=%d is not STA_STREAM_AUTO / FUSED / UNFUSED", a->fused);
+  if (a->fused == STA_STREAM_FUSED && !stream_can_fuse(a->dtype, a->D, a->block_n))
+    return fail(STA_ERR_UNSUPPORTED, "no fused sweep for this dtype with block_n=%d (LDS)", a->block_n);
+  if (stream_lds_bytes(a->dtype, a->D, a->block_n, false) > 160 * 1024)
     return fail(STA_ERR_UNSUPPORTED, "block_n=%d needs more than 160 KB of LDS", a->block_n);
   return STA_OK;
 }
@@ -94,7 +110,8 @@ int sta_pqstream_attention(const sta_pqstream_args* a, void* stream) {
   char* ws = (char*)a->workspace;
   u32x4* qfrag = (u32x4*)(ws + L.qfrag_off);
   u32x4* kfrag = (u32x4*)(ws + L.kfrag_off);
-  uint32_t* bits = (uint32_t*)(ws + L.bits_off);
+  uint32_t* bits = L.fused ? nullptr : (uint32_t*)(ws + L.bits_off);
+  float* xthr = L.fused ? (float*)(ws + L.xthr_off) : nullptr;
   uint16_t* ktil = (uint16_t*)(ws + L.ktil_off);
 
   if ((rc = mark_event(a->stage_events, 0, st)) != STA_OK) return rc;
@@ -123,9 +140,19 @@ int sta_pqstream_attention(const sta_pqstream_args* a, void* stream) {
   sa.sm_scale = a->sm_scale;
   sa.votes_stride = L.stride;
   sa.bits = bits;
+  sa.xthr = xthr;
   sa.row_max = a->row_max;
-  e = launch_score_pq(a->D, STA_SCORE_FREQ, sa, st);
-  if (e != hipSuccess) return hip_fail(e, "score kernel (keep bits)");
+  if (L.fused) {
+    e = launch_score_thresholds(a->D, sa, st);
+    if (e != hipSuccess) return hip_fail(e, "score kernel (thresholds)");
+  } else {
+    e = launch_score_pq(a->D, STA_SCORE_FREQ, sa, st);
+    if (e != hipSuccess) return hip_fail(e, "score kernel (keep bits)");
+    if (a->bits) {
+      e = launch_expand_pq(bits, nullptr, L.stride, a->H, L.nt, a->N, a->tile, 0, nullptr, a->bits, nullptr, st);
+      if (e != hipSuccess) return hip_fail(e, "keep-bit copy");
+    }
+  }
 
   // keys at their absolute positions under the attend geometry
   if ((rc = mark_event(a->stage_events, 2, st)) != STA_OK) return rc;
@@ -143,7 +170,13 @@ int sta_pqstream_attention(const sta_pqstream_args* a, void* stream) {
   s.v_head_stride = a->v_head_stride;
   s.v_tok_stride = a->v_tok_stride;
   s.bits = bits;
-  s.bits_stride = L.stride;
+  s.bits_stride = L.fused ? a->N : L.stride;
+  s.qfrag = L.fused ? qfrag : nullptr;
+  s.kfrag = L.fused ? kfrag : nullptr;
+  s.q_rows_pad = L.q_rows_pad;
+  s.k_rows_pad = L.k_rows_pad;
+  s.xthr = xthr;
+  s.bits_out = L.fused ? (uint32_t*)a->bits : nullptr;
   s.inv_freq = a->inv_freq_c;
   s.sm_scale = a->sm_scale;
   s.H = a->H;

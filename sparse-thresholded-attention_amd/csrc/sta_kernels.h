@@ -49,6 +49,7 @@ struct ScoreArgs {
   int screened;           // set by the launcher: the screen kernel ran before the pass-2 kernel
   float* srmax;           // (H, q_rows_pad) the screen's exact raw row maxima
   int* sflags;            // (H, ngroups) the screen's fallback flags
+  float* xthr;            // thresholds-only instance: (H, q_rows_pad) each row's x0 (+inf: no row)
 };
 
 struct SelectArgs {
@@ -151,8 +152,14 @@ struct StreamArgs {
   const uint16_t* ktil;     // (Hkv, Npad, P, D) keys rotated at their absolute positions
   const void* v;
   int64_t v_head_stride, v_tok_stride;
-  const uint32_t* bits;     // (H, nt, bits_stride) threshold keep bits, bit i = row i
+  const uint32_t* bits;     // unfused sweep: (H, nt, bits_stride) threshold keep bits, bit i = row i
   int64_t bits_stride;
+  // fused sweep: the keep bits are computed in the sweep from the selection-geometry fragments
+  const u32x4* qfrag;       // (H, q_rows_pad) Q fragments (hi / lo), score-kernel layout
+  const u32x4* kfrag;       // (Hkv, k_rows_pad) K fragments
+  int q_rows_pad, k_rows_pad;
+  const float* xthr;        // (H, q_rows_pad) keep threshold on the raw dot, +inf past N
+  uint32_t* bits_out;       // optional (H, nt, bits_stride): the threshold bits the sweep computed
   const float* inv_freq;    // attend geometry (base RoPE)
   float sm_scale;
   int H, Hkv, N, nt, Npad, n_global, n_local, adv_full, use_skip;
@@ -286,6 +293,8 @@ hipError_t launch_rope_frag(int dtype, int D, const void* x, int64_t head_stride
                             float rope_scale, const float* inv_freq, u32x4* frag, hipStream_t st);
 hipError_t launch_score(int D, int tile, const ScoreArgs& a, hipStream_t st);
 hipError_t launch_score_pq(int D, int wmode, const ScoreArgs& a, hipStream_t st);
+// the screen + pass 1 only, writing each row's keep threshold to a.xthr (tile 32)
+hipError_t launch_score_thresholds(int D, const ScoreArgs& a, hipStream_t st);
 // shared selection with weighted votes: wmode 1 margin / 2 expmass, byte votes + fp32 wvotes
 hipError_t launch_score_weighted(int D, int tile, int wmode, const ScoreArgs& a, hipStream_t st);
 size_t pq_select_lds_bytes(int N, int k_max);
@@ -303,7 +312,9 @@ hipError_t launch_expand_votes(const uint8_t* v8, int64_t stride, int H, int nt,
 size_t gather_lds_bytes(int dtype, int D, int k_max);
 hipError_t launch_abs_rope(int dtype, int D, const void* x, int64_t hs, int64_t ts, int heads, int N, int Npad,
                            const float* inv_freq, uint16_t* out, hipStream_t st);
-size_t stream_lds_bytes(int dtype, int D, int BN);
+size_t stream_lds_bytes(int dtype, int D, int BN, bool fused);
+bool stream_can_fuse(int dtype, int D, int BN);   // a sweep that computes the keep bits itself exists
+// launch_stream runs the fused sweep when a.qfrag is set, else the sweep that reads a.bits
 hipError_t launch_dca_rope(int dtype, int D, const void* x, int64_t hs, int64_t ts, int heads, int N, int Npad,
                            int L, int chunk_size, float mscale, int is_key, const float* inv_freq,
                            uint16_t* out, hipStream_t st);

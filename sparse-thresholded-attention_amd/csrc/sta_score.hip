@@ -177,6 +177,8 @@ __global__ __launch_bounds__(1024) void norm_max_kernel(const float2* __restrict
 #define STA_GLOBAL(p) ((const __attribute__((address_space(1))) void*)(p))
 #define STA_LDS(p) ((__attribute__((address_space(3))) void*)(p))
 
+// PQ 6 stops after pass 1: each row's keep threshold x0 on the raw dot goes to ScoreArgs.xthr
+// (the fused PQ Stream sweep applies it itself).
 // PQ selects the pass-2 epilogue: 0 = byte votes (shared selection); 1..3 = the per-query
 // variant (tile 32): packed keep bits per key, plus weighted votes for PQ 2 (margin,
 // sum of fl(s - fl(m - tau))) and PQ 3 (expmass, sum of exp(fl(s - m))) over the keeping rows
@@ -1138,7 +1140,21 @@ void score_kernel(ScoreArgs a) {
     }
     if (exact1) run_pass(std::integral_constant<int, 0>{});
     else finish1(true);
-    run_pass(std::integral_constant<int, 1>{});
+    if constexpr (PQ == 6) {
+      // thresholds only: every row's x0, replicated over the 32 lanes holding its keys
+      if (active && (lane & 31) == 0) {
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            const int row = wrow0 + rb * 32 + (i >> 2) * 8 + (lane >> 5) * 4 + (i & 3);
+            if (row < rows_total) a.xthr[(int64_t)h * a.q_rows_pad + row] = mx[rb][i];
+          }
+      }
+      return;
+    } else {
+      run_pass(std::integral_constant<int, 1>{});
+    }
   }
 
   if constexpr (RC) {
@@ -1240,6 +1256,12 @@ hipError_t launch_score_weighted(int D, int tile, int wmode, const ScoreArgs& a,
   STA_SW(64, 32, 4) STA_SW(64, 32, 5) STA_SW(64, 64, 4) STA_SW(64, 64, 5)
   STA_SW(128, 32, 4) STA_SW(128, 32, 5) STA_SW(128, 64, 4) STA_SW(128, 64, 5)
 #undef STA_SW
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_score_thresholds(int D, const ScoreArgs& a, hipStream_t st) {
+  if (D == 64) return launch_score_t<64, 32, false, 6>(a, st);
+  if (D == 128) return launch_score_t<128, 32, false, 6>(a, st);
   return hipErrorInvalidValue;
 }
 

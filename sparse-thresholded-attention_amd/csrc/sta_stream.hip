@@ -10,8 +10,14 @@
 //   -inf-safe online softmax over the kept keys, P cast to the input dtype, d += adv  (:334-348)
 // Blocks where no query keeps a key are skipped (adv == 0), leaving d unchanged.
 //
-// Here the threshold bits s_ij >= m_i - tau come from the two score passes (the per-query epilogue
-// of the score kernel, one bit per (query, key)).  The position rule is applied by rotation
+// Fused sweep (the default): pass 1 of the score kernel leaves each query's keep threshold x0 on
+// the raw dot; the sweep stages each block's selection-geometry K fragments beside K~ and V and
+// computes the tile's selection scores itself -- S_a^T = K_a . Q_a^T as hi.lo + lo.hi + hi.hi
+// bf16 MFMAs in the score kernel's order, so each keep bit equals the one the score kernel's
+// pass 2 would write -- then keeps s >= x0 (causal, rows < N), so no keep-bit buffer exists.
+// The unfused sweep reads those bits from the score kernel's pass 2 instead; it serves the
+// configurations whose LDS the fused staging would overflow (fp32 inputs with block_n 64).
+// The position rule is applied by rotation
 // algebra instead of per-slot trigonometry: with K~_j = R(j) k_j (keys rotated once at their
 // absolute positions by the pre-kernel below), R(npk_j) k_j = R(-w) K~_j for w = d + hi_t, so
 //   q_att_i . R(npk_j) k_j = (R(w) q_att_i) . K~_j .
@@ -90,7 +96,7 @@ __global__ __launch_bounds__(256) void abs_rope_kernel(const void* __restrict__ 
 // ------------------------------------------------------------------------------------------
 // the stream kernel
 // ------------------------------------------------------------------------------------------
-template <int DT, int D, int BN, int G>
+template <int DT, int D, int BN, int G, bool FUSED = false>
 struct StreamCfg {
   static constexpr bool X3 = DT == DT_F32;          // fp32 inputs: three-term bf16 products
   static constexpr int P = X3 ? 2 : 1;              // planes (hi, lo)
@@ -105,13 +111,17 @@ struct StreamCfg {
   static constexpr int KU = (KUNITS + NTH - 1) / NTH;
   static constexpr int VUNITS = (BN / 4) * (D / 8); // (4 keys x 8 dims) units of a V block
   static constexpr int VU = (VUNITS + NTH - 1) / NTH;
-  static constexpr size_t lds_bytes = (size_t)2 * (KBUF + VBUF) * 2 + (size_t)G * (D / 2) * 8;
+  static constexpr int S = D / 16;                  // k steps of a selection-geometry fragment
+  static constexpr int KAUNITS = FUSED ? (BN / 32) * S * 2 * 64 : 0;   // 16-byte units of a K_a block
+  static constexpr int KAU = FUSED ? (KAUNITS + NTH - 1) / NTH : 0;
+  static constexpr size_t lds_bytes =
+      (size_t)2 * (KBUF + VBUF) * 2 + (size_t)2 * KAUNITS * 16 + (size_t)G * (D / 2) * 8;
 };
 
-template <int DT, int D, int BN, int G>
+template <int DT, int D, int BN, int G, bool FUSED>
 __global__ __launch_bounds__(G * 64, 1) void stream_kernel(StreamArgs a) {
 #pragma clang fp contract(off)
-  using Cfg = StreamCfg<DT, D, BN, G>;
+  using Cfg = StreamCfg<DT, D, BN, G, FUSED>;
   constexpr bool X3 = Cfg::X3;
   constexpr int P = Cfg::P, NTH = Cfg::NTH, KSTR = Cfg::KSTR, VSTR = Cfg::VSTR;
   constexpr int KS = D / 16;          // k steps of the 32x32x16 score product
@@ -121,7 +131,9 @@ __global__ __launch_bounds__(G * 64, 1) void stream_kernel(StreamArgs a) {
   extern __shared__ __align__(16) uint16_t sm[];
   auto kbuf = [&](int p) { return sm + p * (Cfg::KBUF + Cfg::VBUF); };
   auto vbuf = [&](int p) { return sm + p * (Cfg::KBUF + Cfg::VBUF) + Cfg::KBUF; };
-  float* cstab_all = (float*)(sm + 2 * (Cfg::KBUF + Cfg::VBUF));
+  u32x4* kabuf_all = (u32x4*)(sm + 2 * (Cfg::KBUF + Cfg::VBUF));      // 2 x KAUNITS (fused)
+  auto kabuf = [&](int p) { return kabuf_all + p * Cfg::KAUNITS; };
+  float* cstab_all = (float*)(kabuf_all + 2 * Cfg::KAUNITS);
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int hf = lane >> 5, q = lane & 31;
@@ -180,17 +192,42 @@ __global__ __launch_bounds__(G * 64, 1) void stream_kernel(StreamArgs a) {
     }
   }
 
+  // ---- fused: the tile's selection-geometry Q fragments (B operand: column = query, lane q)
+  //      and the lane's query threshold x0 on the raw dot ----
+  constexpr int S = Cfg::S;
+  u32x4 qsel[FUSED ? S : 1][2];
+  float x0q = INFINITY;
+  if constexpr (FUSED) {
+    const u32x4* qf = a.qfrag + ((int64_t)h * (a.q_rows_pad / 32) + (tile_ok ? t : 0)) * S * 128;
+#pragma unroll
+    for (int s = 0; s < S; ++s)
+#pragma unroll
+      for (int hl = 0; hl < 2; ++hl) qsel[s][hl] = tile_ok ? qf[s * 128 + hl * 64 + lane] : u32x4{0u, 0u, 0u, 0u};
+    if (tile_ok) x0q = a.xthr[(int64_t)h * a.q_rows_pad + row];
+  }
+
   // ---- staging of K~ / V blocks into LDS (all threads) ----
   const uint16_t* kt = a.ktil + (int64_t)kvh * a.Npad * P * D;
   const int64_t vhb = (int64_t)kvh * a.v_head_stride;
   u32x4 kreg[KU];
+  u32x4 kareg[FUSED ? Cfg::KAU : 1];
   Raw8<DT> vreg[VU][4];
+  const u32x4* kaf = FUSED ? a.kfrag + (int64_t)kvh * (a.k_rows_pad / 32) * S * 128 : nullptr;
   auto load_block = [&](int b) {
     const uint16_t* src = kt + (int64_t)b * BN * P * D;   // rows b*BN .. +BN-1 are < Npad
 #pragma unroll
     for (int u = 0; u < KU; ++u) {
       const int e = tid + u * NTH;
       if (e < Cfg::KUNITS) kreg[u] = *(const u32x4*)(src + e * 8);
+    }
+    if constexpr (FUSED) {
+      // the block's 32-key fragment blocks b*BN/32 .. are contiguous (rows < k_rows_pad)
+      const u32x4* ksrc = kaf + (int64_t)b * (BN / 32) * S * 128;
+#pragma unroll
+      for (int u = 0; u < Cfg::KAU; ++u) {
+        const int e = tid + u * NTH;
+        if (e < Cfg::KAUNITS) kareg[u] = ksrc[e];
+      }
     }
 #pragma unroll
     for (int u = 0; u < VU; ++u) {
@@ -207,6 +244,14 @@ __global__ __launch_bounds__(G * 64, 1) void stream_kernel(StreamArgs a) {
   auto store_block = [&](int p) {
     uint16_t* kd = kbuf(p);
     uint16_t* vd = vbuf(p);
+    if constexpr (FUSED) {
+      u32x4* kad = kabuf(p);
+#pragma unroll
+      for (int u = 0; u < Cfg::KAU; ++u) {
+        const int e = tid + u * NTH;
+        if (e < Cfg::KAUNITS) kad[e] = kareg[u];
+      }
+    }
 #pragma unroll
     for (int u = 0; u < KU; ++u) {
       const int e = tid + u * NTH;
@@ -247,10 +292,11 @@ __global__ __launch_bounds__(G * 64, 1) void stream_kernel(StreamArgs a) {
   };
 
   // ---- the tile's keep bits of one block: lane l < BN holds key start + l ----
-  const uint32_t* brow = a.bits + ((int64_t)h * a.nt + (tile_ok ? t : 0)) * a.bits_stride;
+  const uint32_t* brow = FUSED ? nullptr : a.bits + ((int64_t)h * a.nt + (tile_ok ? t : 0)) * a.bits_stride;
   const int64_t loc_lo = (int64_t)t * 32 - a.n_local + 1, loc_hi = (int64_t)t * 32 + 31;   // :260-261
   const int rows_hi = min(32, N - t * 32);                        // rows < N
   auto load_bits = [&](int b) -> uint32_t {
+    if constexpr (FUSED) return 0u;
     const int j = b * BN + lane;
     return (tile_ok && lane < BN && b >= 0 && j <= P_top) ? brow[j] : 0u;
   };
@@ -278,33 +324,77 @@ __global__ __launch_bounds__(G * 64, 1) void stream_kernel(StreamArgs a) {
     if (tile_ok && b < nblk) {
       const int start = b * BN;
       const int hi_t = min(P_top, start + BN - 1);                  // :271
-      // keep word of key start + lane: threshold bits, or every causal row when forced
-      uint32_t kw = 0;
-      {
-        const int j = start + lane;
-        if (lane < BN && j <= P_top) {
-          kw = bits_cur;
-          const bool forced = j < a.n_global || (j >= loc_lo && j <= loc_hi);   // :284
-          if (forced) {
-            const int lo_r = max(0, j - t * 32);                  // causal: qpos_i >= j
-            const uint32_t hi_mask = rows_hi >= 32 ? 0xffffffffu : ((1u << rows_hi) - 1u);
-            kw |= hi_mask & ~((1u << lo_r) - 1u);
-          }
-        }
-      }
       // this lane's mask bits: query q, keys 32 sb + (i/4)*8 + 4 hf + i%4
       uint32_t mbits[NSB];
       int cnt = 0;
+      if constexpr (FUSED) {
+        // S_a^T = K_a . Q_a^T (key rows, query columns), hi.lo terms first as in the score
+        // kernel's pass 2; keep = s >= x0 (rows < N through x0 = +inf), causal, or forced (:285-286)
+        const u32x4* ka = kabuf(p);
+        floatx16 sel[NSB];
 #pragma unroll
-      for (int sb = 0; sb < NSB; ++sb) {
-        mbits[sb] = 0;
+        for (int sb = 0; sb < NSB; ++sb) sel[sb] = floatx16{};
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const int key = sb * 32 + (i >> 2) * 8 + 4 * hf + (i & 3);
-          const uint32_t w = (uint32_t)__shfl((int)kw, key, 64);
-          mbits[sb] |= ((w >> q) & 1u) << i;
+        for (int s = 0; s < S; ++s)
+#pragma unroll
+          for (int sb = 0; sb < NSB; ++sb) {
+            const u32x4 kh = ka[(sb * S + s) * 128 + lane];
+            const u32x4 kl = ka[(sb * S + s) * 128 + 64 + lane];
+            sel[sb] = mfma32(kh, qsel[s][1], sel[sb]);
+            sel[sb] = mfma32(kl, qsel[s][0], sel[sb]);
+            sel[sb] = mfma32(kh, qsel[s][0], sel[sb]);
+          }
+#pragma unroll
+        for (int sb = 0; sb < NSB; ++sb) {
+          uint32_t tb = 0, fb = 0;
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            const int j = start + sb * 32 + (i >> 2) * 8 + 4 * hf + (i & 3);
+            const bool causal = row_ok && j <= row;
+            const bool forced = j < a.n_global || (j >= loc_lo && j <= loc_hi);   // :284
+            tb |= (uint32_t)(causal && sel[sb][i] >= x0q) << i;
+            fb |= (uint32_t)(causal && forced) << i;
+          }
+          mbits[sb] = tb | fb;
+          cnt += __popc(mbits[sb]);
+          if (a.bits_out) {
+            // the threshold bits as the score kernel lays them out: one word per key, bit = row
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+              const uint64_t w = __ballot((tb >> i) & 1u);
+              const int j = start + sb * 32 + (i >> 2) * 8 + (i & 3);
+              uint32_t* bo = a.bits_out + ((int64_t)h * a.nt + t) * a.bits_stride;
+              if (lane == 0 && j <= P_top) bo[j] = (uint32_t)w;
+              if (lane == 0 && j + 4 <= P_top) bo[j + 4] = (uint32_t)(w >> 32);
+            }
+          }
         }
-        cnt += __popc(mbits[sb]);
+      } else {
+        // keep word of key start + lane: threshold bits, or every causal row when forced
+        uint32_t kw = 0;
+        {
+          const int j = start + lane;
+          if (lane < BN && j <= P_top) {
+            kw = bits_cur;
+            const bool forced = j < a.n_global || (j >= loc_lo && j <= loc_hi);   // :284
+            if (forced) {
+              const int lo_r = max(0, j - t * 32);                  // causal: qpos_i >= j
+              const uint32_t hi_mask = rows_hi >= 32 ? 0xffffffffu : ((1u << rows_hi) - 1u);
+              kw |= hi_mask & ~((1u << lo_r) - 1u);
+            }
+          }
+        }
+#pragma unroll
+        for (int sb = 0; sb < NSB; ++sb) {
+          mbits[sb] = 0;
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            const int key = sb * 32 + (i >> 2) * 8 + 4 * hf + (i & 3);
+            const uint32_t w = (uint32_t)__shfl((int)kw, key, 64);
+            mbits[sb] |= ((w >> q) & 1u) << i;
+          }
+          cnt += __popc(mbits[sb]);
+        }
       }
       const int c_q = cnt + __shfl_xor(cnt, 32, 64);               // keys of query q (:288)
       int adv_i;
@@ -512,11 +602,33 @@ hipError_t launch_abs_rope(int dtype, int D, const void* x, int64_t hs, int64_t 
   return hipErrorInvalidValue;
 }
 
-constexpr int kStreamTiles = 8;   // tiles (waves) per workgroup
+constexpr int kStreamTiles = 8;        // tiles (waves) per workgroup, unfused sweep
+constexpr int kStreamTilesFused = 4;   // fused sweep: one wave per SIMD, the register room the
+                                       // selection fragments need
 
-size_t stream_lds_bytes(int dtype, int D, int BN) {
-#define STA_SL(DT_, D_, BN_) \
-  if (dtype == DT_ && D == D_ && BN == BN_) return StreamCfg<DT_, D_, BN_, kStreamTiles>::lds_bytes;
+// the fused sweep exists where its staging fits the LDS (everything but fp32 inputs with block_n 64)
+template <int DT, int D, int BN>
+constexpr bool stream_fused() { return StreamCfg<DT, D, BN, kStreamTilesFused, true>::lds_bytes <= 160 * 1024; }
+
+bool stream_can_fuse(int dtype, int D, int BN) {
+#define STA_SF(DT_, D_, BN_) if (dtype == DT_ && D == D_ && BN == BN_) return stream_fused<DT_, D_, BN_>();
+  STA_SF(DT_F32, 64, 32) STA_SF(DT_F32, 64, 64) STA_SF(DT_F32, 128, 32) STA_SF(DT_F32, 128, 64)
+  STA_SF(DT_BF16, 64, 32) STA_SF(DT_BF16, 64, 64) STA_SF(DT_BF16, 128, 32) STA_SF(DT_BF16, 128, 64)
+  STA_SF(DT_F16, 64, 32) STA_SF(DT_F16, 64, 64) STA_SF(DT_F16, 128, 32) STA_SF(DT_F16, 128, 64)
+#undef STA_SF
+  return false;
+}
+
+template <int DT, int D, int BN>
+constexpr size_t stream_lds_t(bool fused) {
+  if constexpr (stream_fused<DT, D, BN>()) {
+    if (fused) return StreamCfg<DT, D, BN, kStreamTilesFused, true>::lds_bytes;
+  }
+  return StreamCfg<DT, D, BN, kStreamTiles, false>::lds_bytes;
+}
+
+size_t stream_lds_bytes(int dtype, int D, int BN, bool fused) {
+#define STA_SL(DT_, D_, BN_) if (dtype == DT_ && D == D_ && BN == BN_) return stream_lds_t<DT_, D_, BN_>(fused);
   STA_SL(DT_F32, 64, 32) STA_SL(DT_F32, 64, 64) STA_SL(DT_F32, 128, 32) STA_SL(DT_F32, 128, 64)
   STA_SL(DT_BF16, 64, 32) STA_SL(DT_BF16, 64, 64) STA_SL(DT_BF16, 128, 32) STA_SL(DT_BF16, 128, 64)
   STA_SL(DT_F16, 64, 32) STA_SL(DT_F16, 64, 64) STA_SL(DT_F16, 128, 32) STA_SL(DT_F16, 128, 64)
@@ -524,16 +636,25 @@ size_t stream_lds_bytes(int dtype, int D, int BN) {
   return 0;
 }
 
-template <int DT, int D, int BN>
-static hipError_t launch_stream_t(const StreamArgs& a, hipStream_t st) {
-  using Cfg = StreamCfg<DT, D, BN, kStreamTiles>;
-  hipError_t e = hipFuncSetAttribute((const void*)stream_kernel<DT, D, BN, kStreamTiles>,
+template <int DT, int D, int BN, int G, bool FUSED>
+static hipError_t launch_stream_g(const StreamArgs& a, hipStream_t st) {
+  using Cfg = StreamCfg<DT, D, BN, G, FUSED>;
+  hipError_t e = hipFuncSetAttribute((const void*)stream_kernel<DT, D, BN, G, FUSED>,
                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)Cfg::lds_bytes);
   if (e != hipSuccess) return e;
-  const int ngroups = (a.nt + kStreamTiles - 1) / kStreamTiles;
-  hipLaunchKernelGGL((stream_kernel<DT, D, BN, kStreamTiles>), dim3(a.H * ngroups), dim3(Cfg::NTH),
-                     Cfg::lds_bytes, st, a);
+  const int ngroups = (a.nt + G - 1) / G;
+  hipLaunchKernelGGL((stream_kernel<DT, D, BN, G, FUSED>), dim3(a.H * ngroups), dim3(Cfg::NTH), Cfg::lds_bytes,
+                     st, a);
   return hipGetLastError();
+}
+
+template <int DT, int D, int BN>
+static hipError_t launch_stream_t(const StreamArgs& a, hipStream_t st) {
+  if constexpr (stream_fused<DT, D, BN>()) {
+    if (a.qfrag) return launch_stream_g<DT, D, BN, kStreamTilesFused, true>(a, st);
+  }
+  if (!a.bits) return hipErrorInvalidValue;
+  return launch_stream_g<DT, D, BN, kStreamTiles, false>(a, st);
 }
 
 hipError_t launch_stream(int dtype, int D, int BN, const StreamArgs& a, hipStream_t st) {

@@ -1,9 +1,10 @@
 """GPU parity of PQ Stream through the C ABI.
 
 Layers:
-  1. keep bits: the GPU's threshold bits (the same score kernel, read out through
-     sta_pq_select_bits) differ from the oracle's only in rows whose score lies within BAND of the
-     row's threshold;
+  1. keep bits: the threshold bits the sweep applied (computed inside the fused sweep, read out
+     through sta_pqstream_args.bits) equal the score kernel's pass 2 (sta_pq_select_bits) bit for
+     bit, and differ from the oracle's only in rows whose score lies within BAND of the row's
+     threshold;
   2. given the GPU's bits, the oracle's restatement of the fused kernel reproduces span, kept,
      blocks and skipped exactly, and the output within 1e-4 (fp32) or 2e-2 abs + 1e-2 rel
      (bf16 / fp16).
@@ -53,10 +54,19 @@ def stream_check(q, k, v, tau, ia, psa, rsa, ic, ng=32, nl=32, bn=32, adv="max",
     H, N, D = q.shape[1], q.shape[2], q.shape[3]
     sm = 1.0 / math.sqrt(D)
     say(f"{what}: H={H} Hkv={k.shape[1]} N={N} D={D} block_n={bn} advance={adv} skip={skip} {q.dtype}")
-    r = native.pqstream_attention(q, k, v, tau, ia, ic, psa, rsa, sm, ng, nl, 32, bn, adv, 0, skip)
+    r = native.pqstream_attention(q, k, v, tau, ia, ic, psa, rsa, sm, ng, nl, 32, bn, adv, 0, skip, want_bits=True,
+                                  fused="fused")
+    ru = native.pqstream_attention(q, k, v, tau, ia, ic, psa, rsa, sm, ng, nl, 32, bn, adv, 0, skip, want_bits=True,
+                                   fused="unfused")
     b = native.pq_select_bits(q, k, tau, ia, psa, rsa, sm, 32, 0, "freq")
     torch.cuda.synchronize()
-    bits_g = b["bits"].cpu().numpy()
+    # the fused sweep's own keep bits equal the score kernel's pass 2, and the two sweeps agree
+    # bit for bit
+    bits_g = r["bits"].cpu().numpy()
+    assert np.array_equal(bits_g, b["bits"].cpu().numpy()), f"{what}: the fused sweep's keep bits differ from pass 2's"
+    assert np.array_equal(ru["bits"].cpu().numpy(), bits_g), f"{what}: the unfused sweep read other bits"
+    for name in ("out", "span", "kept", "blocks", "skipped"):
+        assert torch.equal(r[name], ru[name]), f"{what}: fused and unfused sweeps differ in {name}"
     qn, dt = np_of(q[0])
     kn, _ = np_of(k[0])
     vn, _ = np_of(v[0])

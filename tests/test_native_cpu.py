@@ -27,7 +27,7 @@ def test_library_exports_every_declared_symbol():
     for name in _declared():
         assert hasattr(lib, name), name
     assert sorted(native.EXPORTS) == _declared()
-    assert lib.sta_abi_version() == 4
+    assert lib.sta_abi_version() == 5
 
 
 def _args(**kw):
