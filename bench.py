@@ -86,12 +86,42 @@ def read_traffic(path, kernel):
     return None
 
 
+def cpu_model():
+    """The host CPU's model name (first /proc/cpuinfo entry), or the platform string."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import platform
+    return platform.processor() or platform.machine()
+
+
+def with_traffic(roof, stage_ms):
+    """Add the measured-traffic rate beside the algorithmic one: the counter bytes of one launch
+    (rocprofv3 FETCH_SIZE + WRITE_SIZE, from the traffic file) over the stage time."""
+    if roof.get("traffic"):
+        gbs = roof["traffic"] / (stage_ms * 1e-3) / 1e9
+        roof["traffic_gbs"] = round(gbs, 1)
+        roof["traffic_frac_of_hbm"] = round(gbs / PEAK_HBM_GBS, 4)
+    return roof
+
+
 def cpu_baseline(cfg, q, k, v, invf, ps, rs, budget_s):
     """The oracle (C port of the reference's three stages) on whole heads of the same workload."""
     import numpy as np
     from oracle import sta_oracle as orc
     sm = 1.0 / math.sqrt(cfg.D)
     threads = orc.num_threads()
+    stage_s = {}
+
+    def timed(name, fn, *args, **kw):
+        t1 = time.perf_counter()
+        out = fn(*args, **kw)
+        stage_s[name] = stage_s.get(name, 0.0) + time.perf_counter() - t1
+        return out
 
     def one(h):
         qn, dt = orc.from_torch(q[0, h:h + 1])
@@ -114,14 +144,19 @@ def cpu_baseline(cfg, q, k, v, invf, ps, rs, budget_s):
             orc.pqstream(qn, kn, vn, dt, tau, invf.numpy(), invf.numpy(), ps, rs, sm, cfg.n_global,
                          cfg.n_local, cfg.tile, 32, "max", True, want_band=False)
         elif cfg.variant == "pq":
-            orc.shared_pq_attention(qn, kn, vn, dt, tau, invf.numpy(), invf.numpy(), ps, rs, sm,
-                                    cfg.n_global, cfg.n_local, cfg.tile, cfg.k_max, 64, 0, cfg.select_score)
+            wm = orc.WMODES[cfg.select_score]
+            a = timed("kernel_a", orc.select_bits, qn, kn, dt, tau, invf.numpy(), ps, rs, sm, cfg.tile, 0, wm)
+            s = timed("build_sets", orc.build_sets_pq, a["votes"], a["bits"], a["wvotes"], cfg.n_global, cfg.n_local,
+                      cfg.tile, cfg.k_max, 0, wm)
+            timed("kernel_c", orc.gather_attn_mask, qn, kn, vn, dt, s[0], s[1], s[2], s[3], invf.numpy(), 1.0, sm,
+                  cfg.tile, cfg.k_max)
         else:
-            a = orc.select_vote(qn, kn, dt, tau, invf.numpy(), ps, rs, sm, cfg.tile,
-                                wmode=orc.WMODES[cfg.select_score])
-            s = orc.build_sets(a["votes"], ps, cfg.n_global, cfg.n_local, cfg.pct, cfg.tile, cfg.k_max,
-                               wvotes=a.get("wvotes"))
-            orc.gather_attn(qn, kn, vn, dt, s[0], s[1], s[2], invf.numpy(), rs, sm, cfg.tile, cfg.k_max)
+            a = timed("kernel_a", orc.select_vote, qn, kn, dt, tau, invf.numpy(), ps, rs, sm, cfg.tile,
+                      wmode=orc.WMODES[cfg.select_score])
+            s = timed("build_sets", orc.build_sets, a["votes"], ps, cfg.n_global, cfg.n_local, cfg.pct, cfg.tile,
+                      cfg.k_max, wvotes=a.get("wvotes"))
+            timed("kernel_c", orc.gather_attn, qn, kn, vn, dt, s[0], s[1], s[2], invf.numpy(), rs, sm, cfg.tile,
+                  cfg.k_max)
         return time.perf_counter() - t0
 
     t_first = one(0)
@@ -132,10 +167,15 @@ def cpu_baseline(cfg, q, k, v, invf, ps, rs, budget_s):
               "pqstream": "the fused PQ Stream kernel",
               "dca": "the DCA prefill on 64 and 128 evenly spaced query rows, scaled to all rows"}.get(
                   cfg.variant, "Kernel A + _build_sets + Kernel C")
-    return {"value": round(cfg.N / (per_head * cfg.H), 3), "unit": "tokens/s", "cores": threads,
-            "kind": "port",
-            "sample": f"{heads} of {cfg.H} heads of the same workload through the CPU oracle "
-                      f"({stages}, {threads} OpenMP threads), scaled x{cfg.H / heads:g}"}
+    out = {"value": round(cfg.N / (per_head * cfg.H), 3), "unit": "tokens/s", "cores": threads,
+           "kind": "port",
+           "sample": f"{heads} of {cfg.H} heads of the same workload through the CPU oracle "
+                     f"({stages}, {threads} OpenMP threads), scaled x{cfg.H / heads:g}",
+           "cpu_model": cpu_model()}
+    if stage_s:
+        # seconds per step (all heads) of each reference stage, from the sampled heads
+        out["stage_seconds_per_step"] = {n: round(t / heads * cfg.H, 3) for n, t in stage_s.items()}
+    return out
 
 
 def bench_decode(args, cfg, q, k, v, q_cpu, k_cpu, v_cpu, invf, ps, rs, tau):
@@ -395,6 +435,7 @@ def cpu_baseline_dca_select(cfg, q, k, v, invf, budget_s):
     # quadratic in the length: scale the longer sample
     per_head = t[16384] * (cfg.N / 16384) ** 2
     return {"value": round(cfg.N / (per_head * cfg.H), 3), "unit": "tokens/s", "cores": threads, "kind": "port",
+            "cpu_model": cpu_model(),
             "sample": f"one head at 8192 and 16384 tokens through the CPU oracle (inter votes, selection, "
                       f"attention; {threads} OpenMP threads), the 16384-token time scaled by (N / 16384)^2 to "
                       f"{cfg.N} tokens and by {cfg.H} heads"}
@@ -429,6 +470,7 @@ def cpu_baseline_perquery(cfg, q, k, v, invf, ps, rs, budget_s):
     per_key = t_total / keys_done
     total = per_key * cfg.H * N * (N + 1) / 2
     return {"value": round(N / total, 3), "unit": "tokens/s", "cores": threads, "kind": "port",
+            "cpu_model": cpu_model(),
             "sample": f"{rows_done} query rows ({heads} heads x 64 evenly spaced positions) through the CPU "
                       f"oracle's scores, per-query selection and attend ({threads} OpenMP threads), scaled "
                       f"to all {cfg.H} x {N} rows by their causal key counts"}
@@ -456,6 +498,7 @@ def cpu_baseline_decode(cfg, q, k, v, invf, ps, rs, budget_s):
             break
     threads = orc.num_threads()
     return {"value": round(Q * steps / el, 3), "unit": "tokens/s", "cores": threads, "kind": "port",
+            "cpu_model": cpu_model(),
             "sample": f"{steps} decode steps of the same workload (all {cfg.H} heads) through the CPU "
                       f"oracle's scores, selection and attend ({threads} OpenMP threads)"}
 
@@ -571,6 +614,12 @@ def main():
         else:
             selection = {"kept_mean": round(kept.float().mean().item(), 1),
                          "overflow20_tiles": int(r["overflow20"].sum().item()), "tiles": int(kept.numel())}
+    if cfg.variant == "dca":
+        with_traffic(roof_score, stage_ms["attention"])
+    else:
+        with_traffic(roof_score, stage_ms["score"])
+    if second is not None:
+        with_traffic(roof_second, stage_ms[second])
     if second is None:
         dominant = roof_score
     else:
