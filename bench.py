@@ -49,6 +49,9 @@ def parse():
                     help="summary of the rocprofv3 FETCH_SIZE/WRITE_SIZE runs, with one "
                          "'<kernel> traffic_bytes: <bytes per launch>' line per kernel "
                          "(default: profiles/prefill_<config>_hbm_traffic.md)")
+    ap.add_argument("--stream-mode", default="auto", choices=["auto", "fused", "unfused"],
+                    help="PQ Stream configs: the keep bits from a separate pass ('unfused'), "
+                         "computed inside the sweep ('fused'), or chosen by the bit buffer's size")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="only run a plain device-to-device copy of MIB MiB (3 times) and exit: "
                          "the known-size reference for the HBM byte counters")
@@ -537,7 +540,7 @@ def main():
         plan = native.DcaPlan(q, k, v, invf, cfg.dca[0], cfg.dca[1], cfg.dca[2])
     elif cfg.variant == "pqstream":
         plan = native.StreamPlan(q, k, v, tau, invf, invf, ps, rs, tile=cfg.tile, block_n=32,
-                                 n_global=cfg.n_global, n_local=cfg.n_local)
+                                 n_global=cfg.n_global, n_local=cfg.n_local, fused=args.stream_mode)
     elif cfg.variant == "pq":
         plan = native.PqPlan(q, k, v, tau, invf, invf, ps, rs, tile=cfg.tile, k_max=cfg.k_max,
                              n_global=cfg.n_global, n_local=cfg.n_local, select_score=cfg.select_score)
@@ -650,6 +653,7 @@ def main():
                    "select_score": cfg.select_score,
                    "k_max": cfg.k_max if cfg.variant in ("shared", "pq") else None,
                    "dca_chunk_pretrain_local": cfg.dca,
+                   "stream_mode": args.stream_mode if cfg.variant == "pqstream" else None,
                    "pos_scale": ps, "rope_scale": rs, "parallelism": "none (1 GPU)"},
         "stages_ms": {s: round(t, 4) for s, t in stage_ms.items()},
         "roofline": dominant,

@@ -174,3 +174,54 @@ def test_pqstream_per_query_prompt_matches_prefill_plus_one_decode_step():
     assert torch.isfinite(full).all()
     err = (full - step).abs().max().item()
     assert err < 1e-4, f"per-query prompt vs decode step differ by {err:.2e}"
+
+
+@pytest.mark.parametrize("prefill_mode", ["shared", "perquery"])
+def test_perquery_everything_kept_reproduces_the_dense_model(prefill_mode):
+    """The perquery module installed with tau = inf and k_max above the sequence: every key passes,
+    no cap applies and the dense ranks are the natural positions, so the PQ Union prefill
+    (prefill_mode "shared"), the per-query prefill ("perquery") and the per-query decode reproduce
+    the dense model under base RoPE."""
+    import shared_selection_triton_perquery as spq
+    say(f"perquery module dense known answer, prefill_mode {prefill_mode}")
+    model = _model(None, seed=15)
+    ids = _prompt(300, seed=16)
+    with torch.no_grad():
+        ref_logits = model(ids).logits
+    ref_seq, ref_steps = _greedy(model, ids, 6)
+    spq.install_shared_pi_forward(model, context_window=128, n_global=8, n_local=8, tile=32, k_max=1024,
+                                  prefill_mode=prefill_mode, select_score="expmass")
+    _set_tau(model, math.inf)
+    spq.reset_overflow_stats()
+    with torch.no_grad():
+        logits = model(ids).logits
+    err = (logits - ref_logits).abs().max().item()
+    assert err < 2e-3, f"prefill logits differ by {err:.2e}"
+    seq, steps = _greedy(model, ids, 6)
+    assert torch.equal(seq, ref_seq)
+    derr = (steps - ref_steps).abs().max().item()
+    assert derr < 2e-3, f"decode logits differ by {derr:.2e}"
+    st = spq.get_overflow_stats()
+    assert st["decode"]["overflow_frac"] == 0.0
+    print(f"[result] perquery {prefill_mode}: prefill logits max err {err:.2e}, decode {derr:.2e}", flush=True)
+
+
+def test_perquery_module_prompt_matches_prefill_plus_one_decode_step():
+    """Finite tau and a cap below the union: the per-query prefill of N tokens gives the last
+    position the same logits as N - 1 tokens followed by one decode step."""
+    import shared_selection_triton_perquery as spq
+    say("perquery module: per-query prefill of N tokens vs N - 1 tokens + one decode step")
+    model = _model(None, seed=17)
+    spq.install_shared_pi_forward(model, context_window=200, n_global=8, n_local=8, tile=32, k_max=96,
+                                  max_len=600, prefill_mode="perquery", select_score="expmass")
+    _set_tau(model, 2.0)
+    ids = _prompt(513, seed=18)
+    with torch.no_grad():
+        full = model(ids).logits[0, -1]
+        from transformers import DynamicCache
+        cache = DynamicCache(config=model.config)
+        model(ids[:, :-1], past_key_values=cache, use_cache=True)
+        step = model(ids[:, -1:], past_key_values=cache, use_cache=True).logits[0, -1]
+    assert torch.isfinite(full).all()
+    err = (full - step).abs().max().item()
+    assert err < 1e-4, f"per-query prompt vs decode step differ by {err:.2e}"
