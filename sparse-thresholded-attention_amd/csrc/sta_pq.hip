@@ -7,29 +7,26 @@
 // full-width torch.topk; positions are dense ranks over the kept set and every slot carries the
 // key's per-query bits (forced columns: all bits).
 //
-// Here one workgroup owns one (head, tile).  The tile's rank values are staged in LDS as their
-// fp32 bit patterns (all positive, so unsigned order is value order) and the cut is a 4-pass
-// radix select on 8-bit digits: the budget-th largest value V, then every candidate above V and
-// the first (in key order) of those equal to V.  torch.topk leaves the choice among ties
-// unspecified; ascending key order is the rule here.  Compaction is a block prefix sum; the
-// dense rank of slot s is s itself.
+// Here one workgroup owns one (head, tile) and scans only the keys the tile can keep: the causal
+// range plus the global keys (all N keys for caller-given dense votes).  The tile's rank values
+// are staged in LDS as order-preserving unsigned keys and the budget cut -- the budget-th largest key V, every candidate above V and the first
+// (in key order) of those equal to V -- is a radix select:
+//   level 1 (during staging): an 11-bit digit per candidate, the vote count itself for frequency
+//     ranking (exact) or the sign and bits 30..20 of weighted rank values;
+//   weighted: the keys of the statistic's level-1 bin (a few percent of the candidates) are
+//     gathered into an LDS list and the remaining 20 bits are resolved on the list;
+//   a bin too large for the list (or a vote count >= 2047) resolves the remaining bits over all
+//     keys instead.
+// torch.topk leaves the choice among ties unspecified; ascending key order is the rule here.
+// Compaction is a block prefix sum; the dense rank of slot s is s itself.
 #include "sta_device.h"
 #include "sta_kernels.h"
 
 namespace sta {
 
-__device__ __forceinline__ int pq_block_sum(int v, int* tmp) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
-  if (lane == 0) tmp[wave] = v;
-  __syncthreads();
-  const int total = tmp[0] + tmp[1] + tmp[2] + tmp[3];
-  __syncthreads();
-  return total;
-}
-
-__device__ __forceinline__ int pq_block_exclusive_sum(int v, int* tmp) {
+// inclusive block scan of one int per thread (256 threads); returns the exclusive prefix and the
+// block total through *total
+__device__ __forceinline__ int pq_block_scan(int v, int* tmp, int* total) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   int x = v;
 #pragma unroll
@@ -40,40 +37,104 @@ __device__ __forceinline__ int pq_block_exclusive_sum(int v, int* tmp) {
   if (lane == 63) tmp[wave] = x;
   __syncthreads();
   int base = 0;
-  for (int w = 0; w < wave; ++w) base += tmp[w];
+#pragma unroll
+  for (int w = 0; w < 4; ++w) base += w < wave ? tmp[w] : 0;
+  *total = tmp[0] + tmp[1] + tmp[2] + tmp[3];
   __syncthreads();
   return base + x - v;
+}
+
+__device__ __forceinline__ int pq_block_sum(int v, int* tmp) {
+  int total;
+  pq_block_scan(v, tmp, &total);
+  return total;
+}
+
+// The digit holding the need-th largest count of a histogram of 256 * B bins (descending), and
+// how many of its keys are still needed: misc[0], misc[1].  Thread t owns bins
+// 256B-1-Bt .. 256B-B-Bt.  Requires need >= 1 and at least `need` counts in the histogram.
+template <int B>
+__device__ __forceinline__ void pq_find_digit(const int* hist, int need, int* tmp, int* misc) {
+  const int tid = threadIdx.x;
+  const int top = 256 * B - 1 - B * tid;
+  int c[B], sl = 0;
+#pragma unroll
+  for (int e = 0; e < B; ++e) {
+    c[e] = hist[top - e];
+    sl += c[e];
+  }
+  int total;
+  const int excl = pq_block_scan(sl, tmp, &total);
+  if (excl < need && excl + sl >= need) {
+    int acc = excl, d = top;
+    bool found = false;
+#pragma unroll
+    for (int e = 0; e < B - 1; ++e) {
+      found = found || acc + c[e] >= need;
+      if (!found) {
+        acc += c[e];
+        d -= 1;
+      }
+    }
+    misc[0] = d;
+    misc[1] = need - acc;
+  }
+  __syncthreads();
+}
+
+// fp32 -> unsigned key of the same order (-0 folded into +0); never 0, which marks "not a candidate"
+__device__ __forceinline__ uint32_t pq_order_key(float r) {
+  const uint32_t b = __float_as_uint(r + 0.0f);
+  const uint32_t k = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+  return k ? k : 1u;
 }
 
 __global__ __launch_bounds__(256) void pq_select_kernel(PqSelectArgs a) {
 #pragma clang fp contract(off)
   extern __shared__ __align__(16) uint32_t pq_smem[];
   const int tid = threadIdx.x;
-  const int h = blockIdx.x / a.nt, t = blockIdx.x % a.nt;
   const int N = a.N, T = a.T;
-  const int per = (N + 255) / 256;
+  // the longest key ranges (the last tiles) start first
+  const int h = (int)(blockIdx.x % a.H);
+  const int t = a.nt - 1 - (int)(blockIdx.x / a.H);
+  const int64_t tstart = (int64_t)a.q_pos_base + (int64_t)t * T;   // perquery.py:377
+  const int64_t lo = tstart - a.n_local + 1, hi_l = tstart + T - 1;
+  const int hi_keys = a.dense ? N : (int)min((int64_t)N, tstart + T);
+  // keys at or past R are neither union members (no votes) nor forced
+  const int R = a.dense ? N : (int)min((int64_t)N, max(tstart + T, (int64_t)a.n_global));
+  const int per = (R + 255) / 256;
   // thread tid scans keys [tid*per, tid*per + per); its keys sit at a row of odd stride PS so the
   // 64 lanes of a scan step fall in distinct LDS banks
   const int PS = per | 1;
+  const int PSMAX = ((N + 255) / 256) | 1;
   uint32_t* rkb = pq_smem;                                  // 256 rows x PS rank keys (0: not a candidate)
   uint32_t* myrow = rkb + tid * PS;                         // this thread's keys j0 .. j0 + per - 1
   // j / per by a reciprocal multiply (per >= 2): exact for per <= 256 and j < 2^24
   const uint32_t inv_per = per > 1 ? (uint32_t)((0x100000000ull + per - 1) / per) : 0u;
-  int* hist = (int*)(rkb + 256 * PS);                       // 256
+  int* hist = (int*)(rkb + 256 * PSMAX);                    // 256 bins (list and fallback levels)
   int* tmp = hist + 256;                                    // 8
   int* misc = tmp + 8;                                      // 8
   float* qnp = (float*)(misc + 8);                          // T (<= 64)
-  int32_t* sidx = (int32_t*)(qnp + 64);                     // k_max: kept keys in rank order
+  // region A, max(2048, k_max) words: the level-1 histogram (2048 bins), then the list of the
+  // statistic's bin, then the kept keys in rank order
+  uint32_t* areg = (uint32_t*)(qnp + 64);
+  int* hist1 = (int*)areg;
+  uint32_t* list = areg;
+  int32_t* sidx = (int32_t*)areg;
+  const int list_cap = max(2048, a.k_max);
 
-  const int64_t tstart = (int64_t)a.q_pos_base + (int64_t)t * T;   // perquery.py:377
-  const int64_t lo = tstart - a.n_local + 1, hi_l = tstart + T - 1;
-  const int hi_keys = a.dense ? N : (int)min((int64_t)N, tstart + T);
   const int64_t roff = ((int64_t)h * a.nt + t) * a.stride;
   const uint32_t* brow = a.bits + roff;
-  const int j0 = tid * per, j1 = min(j0 + per, N);
+  const int j0 = tid * per, j1 = min(j0 + per, R);
   auto is_forced = [&](int j) { return j < a.n_global || (j >= lo && j <= hi_l); };
+  const bool weighted = a.wvotes != nullptr;
 
-  // ---- union, forced, candidates and their rank values (perquery.py:381-397) ----
+#pragma unroll
+  for (int e = 0; e < 8; ++e) hist1[tid + 256 * e] = 0;
+  if (tid == 0) misc[2] = 0;
+  __syncthreads();
+
+  // ---- union, forced, candidates, their rank keys and the level-1 histogram (perquery.py:381-397) ----
   // staged with coalesced loads (key j by thread j % 256); the scans below walk contiguous ranges
   int cu = 0, cf = 0, cfo = 0;
   constexpr int U = 16;   // loads in flight per lane
@@ -87,33 +148,37 @@ __global__ __launch_bounds__(256) void pq_select_kernel(PqSelectArgs a) {
       const bool ok = j < hi_keys;
       bv[u] = (ok && !a.votes) ? brow[j] : 0u;
       vv[u] = (ok && a.votes) ? a.votes[roff + j] : 0;
-      wvv[u] = (ok && a.wvotes) ? a.wvotes[roff + j] : 0.0f;
+      wvv[u] = (ok && weighted) ? a.wvotes[roff + j] : 0.0f;
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int j = jb + u * 256 + tid;
-      if (j >= 256 * per) break;
       uint32_t key = 0;
-      if (j < N) {
+      if (j < R) {
         const int vt = a.votes ? vv[u] : __popc(bv[u]);
         const bool un = vt > 0, fo = is_forced(j);
         cu += un;
         cf += un || fo;
         cfo += fo;
         if (un && !fo) {
-          float rv;
-          if (a.wvotes) {
+          int d1;
+          if (weighted) {
             const float tb = 1e-6f * (float)vt;
-            rv = wvv[u] + tb;
+            key = pq_order_key(wvv[u] + tb);
+            // digit 0: negative values; 1 + bits 30..20 of a non-negative value (the top two
+            // share digit 2047)
+            d1 = key >= 0x80000000u ? 1 + min((int)((key & 0x7FFFFFFFu) >> 20), 2046) : 0;
           } else {
-            rv = (float)vt;
+            key = pq_order_key((float)vt);
+            d1 = min(vt, 2047);
           }
-          key = __float_as_uint(rv);
-          if (key == 0 || key >= 0x80000000u) key = 1;   // a non-positive value stays a candidate, lowest
+          atomicAdd(&hist1[d1], 1);
         }
       }
-      const uint32_t row = per == 1 ? (uint32_t)j : __umulhi((uint32_t)j, inv_per);
-      rkb[row * PS + (j - row * per)] = key;
+      if (j < 256 * per) {
+        const uint32_t row = per == 1 ? (uint32_t)j : __umulhi((uint32_t)j, inv_per);
+        rkb[row * PS + (j - row * per)] = key;
+      }
     }
   }
   __syncthreads();
@@ -122,80 +187,100 @@ __global__ __launch_bounds__(256) void pq_select_kernel(PqSelectArgs a) {
   const int nforced = pq_block_sum(cfo, tmp);
   const bool overflow = nfull > a.k_max;                    // perquery.py:386
   const int budget = max(a.k_max - nforced, 0);             // perquery.py:399-400
+  const bool cut = overflow && budget > 0;
 
-  // ---- overflow: radix select of the budget-th largest rank key, 8-bit digits ----
-  // Rank values of one tile share few exponents, so the top digits of most keys coincide: that
-  // pass aggregates its histogram increments per wave (one LDS atomic per distinct digit) instead
-  // of 64 conflicting lane atomics.
+  // ---- overflow: the budget-th largest rank key V and how many keys equal to V are taken ----
   uint32_t V = 0;
   int need_eq = 0;
-  if (overflow && budget > 0) {
-    const int lane = tid & 63;
-    uint32_t prefix = 0, pmask = 0;
-    int need = budget;
-    for (int shift = 24; shift >= 0; shift -= 8) {
+  if (cut) {
+    pq_find_digit<8>(hist1, budget, tmp, misc);
+    const int d1 = misc[0];
+    int need = misc[1];
+    const int bin_count = hist1[d1];
+    uint32_t prefix, pmask;
+    bool from_list = false;
+    if (!weighted && d1 < 2047) {
+      // the digit is the vote count: exact
+      prefix = pq_order_key((float)d1);
+      pmask = 0xFFFFFFFFu;
+    } else if (weighted) {
+      // the bin's keys share a prefix with the statistic; the rest from the bin's list when it fits
+      if (d1 == 0) {
+        prefix = 0;
+        pmask = 0x80000000u;
+      } else if (d1 < 2047) {
+        prefix = 0x80000000u | ((uint32_t)(d1 - 1) << 20);
+        pmask = 0xFFF00000u;
+      } else {
+        prefix = 0x80000000u | (2046u << 20);
+        pmask = 0xFFE00000u;
+      }
+      from_list = bin_count <= list_cap;
+    } else {
+      // a vote count of 2047 or more holds the statistic: resolve the float keys from the top
+      prefix = 0;
+      pmask = 0;
+      need = budget;
+    }
+    __syncthreads();   // every thread has read hist1 before the list overwrites it
+    int cnt = 0;
+    if (from_list) {
+      for (int i = 0; i < per; ++i) {
+        const uint32_t k = myrow[i];
+        if (k != 0 && (k & pmask) == prefix) list[atomicAdd(&misc[2], 1)] = k;
+      }
+      __syncthreads();
+      cnt = misc[2];
+    }
+    // remaining levels: 8-bit digits below the prefix, the last one narrower when the bits run out
+    while (pmask != 0xFFFFFFFFu) {
+      const int nfree = 32 - __clz(~pmask);          // pmask covers the top 32 - nfree bits
+      const int width = min(8, nfree), sh = nfree - width;
+      const uint32_t dmask = (1u << width) - 1u;
       hist[tid] = 0;
       __syncthreads();
-      if (shift == 24 && !a.wvotes) {
-        // top digit (sign + high exponent bits) of vote counts: a handful of distinct values per
-        // wave -> one atomic per distinct digit (weighted rank values spread over more exponents,
-        // where plain atomics measured faster)
-        for (int i = 0; i < per; ++i) {                // same trip count on every lane
-          const uint32_t k = myrow[i];
-          bool act = k != 0 && j0 + i < N;
-          const int d = (int)(k >> 24);
-          uint64_t m = __ballot(act);
-          while (m) {
-            const int leader = __ffsll((unsigned long long)m) - 1;
-            const int dl = __shfl(d, leader, 64);
-            const uint64_t same = __ballot(act && d == dl);
-            if (lane == leader) atomicAdd(&hist[dl], (int)__popcll(same));
-            if (act && d == dl) act = false;
-            m &= ~same;
-          }
+      if (from_list) {
+        for (int i = tid; i < cnt; i += 256) {
+          const uint32_t k = list[i];
+          if ((k & pmask) == prefix) atomicAdd(&hist[(k >> sh) & dmask], 1);
         }
       } else {
-        // lower digits are spread over the bins: plain LDS atomics
         for (int i = 0; i < per; ++i) {
           const uint32_t k = myrow[i];
-          if (k != 0 && (k & pmask) == prefix) atomicAdd(&hist[(k >> shift) & 255u], 1);
+          if (k != 0 && (k & pmask) == prefix) atomicAdd(&hist[(k >> sh) & dmask], 1);
         }
       }
       __syncthreads();
-      if (tid < 64) {
-        // wave 0 finds the digit: lane l holds bins 255-4l .. 252-4l (descending)
-        int c[4], sl = 0;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) { c[e] = hist[255 - 4 * lane - e]; sl += c[e]; }
-        int incl = sl;
-#pragma unroll
-        for (int o = 1; o < 64; o <<= 1) {
-          const int y = __shfl_up(incl, o, 64);
-          if (lane >= o) incl += y;
-        }
-        const uint64_t hit = __ballot(incl >= need);
-        const int first = hit ? __ffsll((unsigned long long)hit) - 1 : 63;
-        if (lane == first) {
-          int acc = incl - sl, d = 255 - 4 * lane;
-#pragma unroll
-          for (int e = 0; e < 3; ++e) {
-            if (acc + c[e] >= need) break;
-            acc += c[e];
-            d -= 1;
-          }
-          misc[0] = d;
-          misc[1] = need - acc;
-        }
-      }
-      __syncthreads();
-      prefix |= (uint32_t)misc[0] << shift;
-      pmask |= 255u << shift;
+      pq_find_digit<1>(hist, need, tmp, misc);
+      prefix |= (uint32_t)misc[0] << sh;
+      pmask |= dmask << sh;
       need = misc[1];
       __syncthreads();
     }
     V = prefix;
     need_eq = need;   // how many keys equal to V are taken, first in key order
   }
+  __syncthreads();   // the list is dead: region A becomes sidx
+
+  // ---- counts: kept keys strictly above the cut (and forced), keys at the cut ----
+  int cstrict = 0, ceq = 0;
+  for (int j = j0; j < j1; ++j) {
+    const uint32_t k = myrow[j - j0];
+    if (is_forced(j)) {
+      ++cstrict;
+    } else if (k != 0) {
+      if (!overflow) ++cstrict;
+      else if (cut) {
+        cstrict += k > V;
+        ceq += k == V;
+      }
+    }
+  }
+  int eq_base = 0, eq_total;
+  if (cut) eq_base = pq_block_scan(ceq, tmp, &eq_total);
+  const int taken_eq = cut ? max(0, min(ceq, need_eq - eq_base)) : 0;
+  int kept_total;
+  const int base = pq_block_scan(cstrict + taken_eq, tmp, &kept_total);
   auto kept_of = [&](int j, int eq_before) -> bool {
     if (is_forced(j)) return true;
     const uint32_t k = myrow[j - j0];
@@ -205,25 +290,8 @@ __global__ __launch_bounds__(256) void pq_select_kernel(PqSelectArgs a) {
     if (k > V) return true;
     return k == V && eq_before < need_eq;
   };
-  // ties at V: exclusive count of equal keys before each thread's range
-  int eq_base = 0;
-  if (overflow && budget > 0) {
-    int ceq = 0;
-    for (int j = j0; j < j1; ++j) ceq += myrow[j - j0] == V && !is_forced(j);
-    eq_base = pq_block_exclusive_sum(ceq, tmp);
-  }
+
   // ---- compaction: dense ranks (perquery.py:414-442) ----
-  int ck = 0;
-  {
-    int eq = eq_base;
-    for (int j = j0; j < j1; ++j) {
-      const bool kp = kept_of(j, eq);
-      eq += myrow[j - j0] == V && !is_forced(j) && overflow && budget > 0;
-      ck += kp;
-    }
-  }
-  const int base = pq_block_exclusive_sum(ck, tmp);
-  const int kept_total = pq_block_sum(ck, tmp);
   const int qlo = (int)min(tstart, (int64_t)N - 1);
   const int qhi = (int)min(tstart + T - 1, (int64_t)N - 1);
   int32_t* irow = a.idx + ((int64_t)h * a.nt + t) * a.k_max;
@@ -234,7 +302,7 @@ __global__ __launch_bounds__(256) void pq_select_kernel(PqSelectArgs a) {
     int rank = base - 1;
     for (int j = j0; j < j1; ++j) {
       const bool kp = kept_of(j, eq);
-      eq += myrow[j - j0] == V && !is_forced(j) && overflow && budget > 0;
+      eq += cut && myrow[j - j0] == V && !is_forced(j);
       if (kp) {
         rank += 1;
         if (rank < a.k_max) sidx[rank] = j;
@@ -293,7 +361,8 @@ __global__ __launch_bounds__(256) void expand_pq_kernel(const uint32_t* __restri
 
 size_t pq_select_lds_bytes(int N, int k_max) {
   const size_t per = (size_t)(N + 255) / 256;
-  return 256 * (per | 1) * 4 + (256 + 8 + 8) * 4 + 64 * 4 + (size_t)k_max * 4;
+  const size_t region_a = (size_t)(k_max > 2048 ? k_max : 2048) * 4;
+  return 256 * (per | 1) * 4 + (256 + 8 + 8) * 4 + 64 * 4 + region_a;
 }
 
 hipError_t launch_pq_select(const PqSelectArgs& a, hipStream_t st) {

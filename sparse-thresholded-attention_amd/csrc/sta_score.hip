@@ -942,10 +942,11 @@ void score_kernel(ScoreArgs a) {
   // then the keep threshold x0 on the raw dot, and the weighted-vote origins.
   // screened: the maximum came from the screen's fp32 dots of the (hi + lo) operands, which
   // differ from pass 2's three-product value of the same key by the lo.lo term and the two
-  // summation orders.  The threshold is then capped at max - delta, with delta a bound on that
-  // difference, so the row's best key keeps its vote for any tau (the reference's two passes
-  // share one dot, exact_2.py:100, 118, so qk == m always passes); for tau above delta * scale
-  // (1e-5 at unit-scale rows) the cap changes nothing.
+  // summation orders.  For tau >= 0 the threshold is then capped at max - delta, with delta a
+  // bound on that difference, so the row's best key keeps its vote (the reference's two passes
+  // share one dot, exact_2.py:100, 118, so qk == m passes whenever tau >= 0); for tau above
+  // delta * scale (1e-5 at unit-scale rows) the cap changes nothing.  A negative tau keeps no key
+  // in the reference, and no cap applies.
   auto finish1 = [&](bool screened) {
     const float2 knm = a.knorm_max[kvh];
     if (active) {
@@ -964,7 +965,7 @@ void score_kernel(ScoreArgs a) {
           const int row = rb * 32 + (i >> 2) * 8 + (lane >> 5) * 4 + (i & 3);
           const bool ok = wrow0 + row < a.N;   // padded rows never vote (exact_2.py:121)
           float x0 = ok ? min_arg_for(m - tau, a.sm_scale) : INFINITY;
-          if (screened && ok) {
+          if (screened && ok && tau >= 0.0f) {
             const float2 qn = a.qnorm[(int64_t)h * a.q_rows_pad + wrow0 + row];
             const float delta = 1.001f * (qn.y * knm.y + 0x1p-15f * (qn.x + qn.y) * (knm.x + knm.y));
             x0 = fminf(x0, v - delta);

@@ -93,14 +93,21 @@ __global__ __launch_bounds__(256) void select_w_kernel(SelectArgs a) {
 #pragma clang fp contract(off)
   extern __shared__ __align__(16) uint32_t wsm[];
   const int tid = threadIdx.x, lane = tid & 63;
-  const int h = blockIdx.x / a.nt, t = blockIdx.x % a.nt;
   const int N = a.N, T = a.T;
-  const int per = (N + 255) / 256;
-  const int PS = per | 1;
+  // the longest key ranges (the last tiles) start first
+  const int h = (int)(blockIdx.x % a.H);
+  const int t = a.nt - 1 - (int)(blockIdx.x / a.H);
+  const int64_t tstart = (int64_t)a.q_pos_base + (int64_t)t * T;          // exact_2.py:291
+  const int64_t lo = tstart - a.n_local + 1, hi_l = tstart + T - 1;
+  const int hi_keys = a.votes_dense ? N : (int)min((int64_t)N, tstart + T);
+  // Keys at or past R carry no votes and are not forced: rank value 0, order key ZK.  They are not
+  // staged: they lie below every cut as long as at least `need` staged keys rank above zero, which
+  // the staging counts; a tile where that fails stages all N keys instead.
+  constexpr uint32_t ZK = 0x80000000u;                   // order_key(0.0f)
+  int R = a.votes_dense ? N : (int)min((int64_t)N, max(tstart + T, (int64_t)a.n_global));
+  const int PSMAX = ((N + 255) / 256) | 1;
   uint32_t* rkb = wsm;                                   // 256 rows x PS order keys
-  uint32_t* myrow = rkb + tid * PS;                      // keys j0 .. j0 + per - 1
-  const uint32_t inv_per = per > 1 ? (uint32_t)((0x100000000ull + per - 1) / per) : 0u;
-  int* hist = (int*)(rkb + 256 * PS);                    // 3 x 256
+  int* hist = (int*)(rkb + 256 * PSMAX);                 // 3 x 256
   int* tmp = hist + 3 * 256;                             // 16
   int* misc = tmp + 16;                                  // 16
   float* tmpf = (float*)(misc + 16);                     // 16
@@ -108,49 +115,72 @@ __global__ __launch_bounds__(256) void select_w_kernel(SelectArgs a) {
   int32_t* sidx = (int32_t*)(qnp + 256);                 // k_max
   float* snp = (float*)(sidx + a.k_max);                 // k_max
 
-  const int64_t tstart = (int64_t)a.q_pos_base + (int64_t)t * T;          // exact_2.py:291
-  const int64_t lo = tstart - a.n_local + 1, hi_l = tstart + T - 1;
-  const int hi_keys = a.votes_dense ? N : (int)min((int64_t)N, tstart + T);
   const int64_t roff = ((int64_t)h * a.nt + t) * a.votes_stride;
   const VT* vrow = (const VT*)a.votes + roff;
   const float* wrow = a.wvotes + roff;
-  const int j0 = tid * per, j1 = min(j0 + per, N);
   auto is_forced = [&](int j) { return j < a.n_global || (j >= lo && j <= hi_l); };   // exact_2.py:290-293
 
-  // ---- stage the rank keys (coalesced: key j by thread j % 256), U = #(votes > 0); SU loads of
-  //      each array in flight per lane ----
-  int cu = 0;
+  // ---- stage the rank keys of [0, R) (coalesced: key j by thread j % 256), U = #(votes > 0) and
+  //      the keys ranked above zero; SU loads of each array in flight per lane ----
+  int per = 0, PS = 1, cu = 0, cpos = 0;
+  uint32_t inv_per = 0;
   constexpr int SU = 8;
-  for (int jb = 0; jb < 256 * per; jb += 256 * SU) {
-    int vv[SU];
-    float wv[SU];
+  auto stage = [&]() {
+    per = (R + 255) / 256;
+    PS = per | 1;
+    inv_per = per > 1 ? (uint32_t)((0x100000000ull + per - 1) / per) : 0u;
+    cu = 0;
+    cpos = 0;
+    for (int jb = 0; jb < 256 * per; jb += 256 * SU) {
+      int vv[SU];
+      float wv[SU];
 #pragma unroll
-    for (int u = 0; u < SU; ++u) {
-      const int j = jb + u * 256 + tid;
-      const bool ok = j < hi_keys;
-      vv[u] = ok ? (int)vrow[j] : 0;
-      wv[u] = ok ? wrow[j] : 0.0f;
-    }
-#pragma unroll
-    for (int u = 0; u < SU; ++u) {
-      const int j = jb + u * 256 + tid;
-      if (j >= 256 * per) break;
-      uint32_t key = 0;
-      if (j < N) {
-        const int v = vv[u];
-        const float w = wv[u];
-        cu += v > 0;                                                       // exact_2.py:296
-        const float tb = 1e-6f * (float)v;                                 // exact_2.py:302
-        key = order_key(w + tb);
-        if (a.votes_out) a.votes_out[((int64_t)h * a.nt + t) * N + j] = v;
-        if (a.wvotes_out) a.wvotes_out[((int64_t)h * a.nt + t) * N + j] = w;
+      for (int u = 0; u < SU; ++u) {
+        const int j = jb + u * 256 + tid;
+        const bool ok = j < hi_keys;
+        vv[u] = ok ? (int)vrow[j] : 0;
+        wv[u] = ok ? wrow[j] : 0.0f;
       }
-      const uint32_t row = per == 1 ? (uint32_t)j : __umulhi((uint32_t)j, inv_per);
-      rkb[row * PS + (j - row * per)] = key;
+#pragma unroll
+      for (int u = 0; u < SU; ++u) {
+        const int j = jb + u * 256 + tid;
+        if (j >= 256 * per) break;
+        uint32_t key = 0;
+        if (j < R) {
+          const int v = vv[u];
+          const float w = wv[u];
+          cu += v > 0;                                                       // exact_2.py:296
+          const float tb = 1e-6f * (float)v;                                 // exact_2.py:302
+          key = order_key(w + tb);
+          cpos += key > ZK;
+        }
+        const uint32_t row = per == 1 ? (uint32_t)j : __umulhi((uint32_t)j, inv_per);
+        rkb[row * PS + (j - row * per)] = key;
+      }
+    }
+    __syncthreads();
+  };
+  stage();
+  const int64_t usize = w_block_sum(cu, tmp);   // no votes past R
+  {
+    // the largest order statistic any step asks for (exact_2.py:329-330): the first step's
+    int64_t need = w_budget_of(a.steps[0], usize);
+    need = need > a.K_ord ? a.K_ord : need;
+    if (R < N && (int64_t)w_block_sum(cpos, tmp) < need) {
+      R = N;
+      stage();
     }
   }
-  __syncthreads();
-  const int64_t usize = w_block_sum(cu, tmp);
+  if (a.votes_out || a.wvotes_out) {
+    // the reference's dense (H, nt, N) votes / wvotes, zero past the tile's causal end
+    for (int j = tid; j < N; j += 256) {
+      const bool ok = j < hi_keys;
+      if (a.votes_out) a.votes_out[((int64_t)h * a.nt + t) * N + j] = ok ? (int)vrow[j] : 0;
+      if (a.wvotes_out) a.wvotes_out[((int64_t)h * a.nt + t) * N + j] = ok ? wrow[j] : 0.0f;
+    }
+  }
+  uint32_t* myrow = rkb + tid * PS;                      // keys j0 .. j0 + per - 1
+  const int j0 = tid * per, j1 = min(j0 + per, R);
 
   // Order statistics for up to three targets at once: target t is the need[t]-th largest key
   // (1 <= need[t] <= N).  The targets walk the radix tree together, one pass over the keys per
@@ -186,7 +216,7 @@ __global__ __launch_bounds__(256) void select_w_kernel(SelectArgs a) {
       // top digit's few distinct values by ballots measured slower)
       for (int i = 0; i < per; ++i) {
         const uint32_t k = myrow[i];
-        if (k == 0 || j0 + i >= N) continue;
+        if (k == 0 || j0 + i >= R) continue;
         const uint32_t kp = k & pmask;
 #pragma unroll
         for (int w = 0; w < 3; ++w)

@@ -134,6 +134,57 @@ def test_pq_build_sets_goldens():
             assert np.array_equal(np.asarray(got[name]).astype(np.float64), rv.astype(np.float64)), (i, name)
 
 
+def _radix_case(seed, N, nt, kind):
+    """Dense (1, nt, N) votes / bits / wvotes that steer _build_sets_pq's budget cut through one
+    path of the device's radix select."""
+    g = np.random.default_rng(seed)
+    votes = g.integers(1, 33, size=(1, nt, N)).astype(np.int32)
+    votes[:, :, g.random(N) < 0.2] = 0                       # some keys outside the union
+    bits = g.integers(-2**31, 2**31 - 1, size=(1, nt, N), dtype=np.int64).astype(np.int32)
+    if kind == "wide_bin":
+        # ~4000 candidates share key bits 31..20 (values in [1, 1.125)) and hold the cut: more
+        # than the LDS list holds, so the remaining bits resolve over all keys
+        wv = (1.0 + 0.125 * g.random((1, nt, N))).astype(np.float32)
+        wv[:, :, :100] = 4.0 + g.random((1, nt, 100)).astype(np.float32)
+        wv[:, :, 200:260] = wv[:, :, 300:360]                 # exact ties
+    elif kind == "list_bin":
+        # the cut's bin holds a few hundred keys: the list path, with ties at the cut
+        wv = (0.01 + 10.0 * g.random((1, nt, N)) ** 3).astype(np.float32)
+        wv[:, :, 1000:1400] = wv[:, :, 1400:1800]
+    elif kind == "nonpositive":
+        # the cut falls among negative rank values (caller-given weighted votes), with ties
+        wv = -(0.001 + np.abs(g.normal(size=(1, nt, N)))).astype(np.float32)
+        wv[:, :, :100] = -wv[:, :, :100]
+        wv[:, :, 1000:1200] = wv[:, :, 1200:1400]
+    elif kind == "big_votes":
+        # caller votes of 2047 and more hold the statistic: the full float-key radix
+        votes = np.where(votes > 0, g.integers(2000, 2100, size=(1, nt, N)), 0).astype(np.int32)
+        wv = np.zeros((1, nt, N), np.float32)
+    else:   # "small_votes": the vote count is the level-1 digit
+        wv = np.zeros((1, nt, N), np.float32)
+    return votes, bits, wv
+
+
+@pytest.mark.parametrize("kind,mode", [("wide_bin", 2), ("list_bin", 1), ("nonpositive", 1), ("big_votes", 0),
+                                       ("small_votes", 0)])
+def test_pq_build_sets_radix_paths(kind, mode):
+    """Every path of the device's budget cut (vote-count digit, weighted list, weighted bin too wide
+    for the list, caller votes of 2047 and more, non-positive rank values) against the oracle, bit
+    for bit, with exact ties at the cut."""
+    import _sta_native as native
+    N, nt, T, kmax, ng, nl = 6000, 3, 32, 256, 8, 8
+    votes, bits, wv = _radix_case(7, N, nt, kind)
+    say(f"pq radix path {kind}, rank mode {mode}")
+    res = native.pq_build_sets(torch.from_numpy(votes).to(DEV), torch.from_numpy(bits).to(DEV),
+                               torch.from_numpy(wv).to(DEV), ng, nl, T, kmax, N - nt * T,
+                               ["freq", "margin", "expmass"][mode])
+    got = {n: t.cpu().numpy() for n, t in zip(PQ_SET_NAMES, res)}
+    ref = orc.build_sets_pq(votes, bits, wv, ng, nl, T, kmax, N - nt * T, mode)
+    assert bool(np.asarray(got["overflow"]).all())
+    for name, rv in zip(PQ_SET_NAMES, ref):
+        assert np.array_equal(np.asarray(got[name]).astype(np.float64), rv.astype(np.float64)), name
+
+
 def test_pq_composed_goldens():
     import _sta_native as native
     g = _gold("pq_composed_golden.npz")

@@ -147,3 +147,27 @@ def test_tau_zero_keeps_each_rows_best_key():
         ndiff, nband = check_votes(votes.cpu().numpy(), a["votes"], a["band"])
         print(f"[result] tau 0 exact_pass1={exact}: min row count {int(rc.min())}, vote entries "
               f"differing {ndiff} (band pairs {nband})", flush=True)
+
+
+def test_negative_tau_keeps_no_key():
+    """tau < 0 puts the threshold above every row's maximum: the reference keeps no key
+    (exact_2.py:121), with the screened pass 1 as with the three-product one."""
+    import _sta_native as native
+    from synthetic import base_inv_freq, planted_inputs
+    H, N, D, tile = 2, 1500, 128, 64
+    q, k, _ = planted_inputs(14, H, H, N, D, 0.01, torch.bfloat16, DEV)
+    invf = base_inv_freq(D, 10000.0).to(DEV)
+    tau = torch.tensor([-0.5, -3.0])
+    for exact in (False, True):
+        say(f"tau < 0, exact_pass1={exact}")
+        old = os.environ.pop("STA_EXACT_PASS1", None)
+        try:
+            if exact:
+                os.environ["STA_EXACT_PASS1"] = "1"
+            votes, rc, _ = native.select_vote(q, k, tau, invf, 0.5, 1.0, 1.0 / math.sqrt(D), tile)
+            torch.cuda.synchronize()
+        finally:
+            os.environ.pop("STA_EXACT_PASS1", None)
+            if old is not None:
+                os.environ["STA_EXACT_PASS1"] = old
+        assert int(votes.abs().sum()) == 0 and int(rc.abs().sum()) == 0, f"exact_pass1={exact}"

@@ -132,6 +132,19 @@ def test_weighted_three_layer(case):
                     q_pos_base=qb, measure=meas, what=f"weighted {mode} {dt} N={N} tile={tile}")
 
 
+@pytest.mark.parametrize("mode", ["expmass", "margin"])
+def test_weighted_empty_union_stages_every_key(mode):
+    """tau < 0 on one head: no key passes, every rank value is zero and the cut falls on the keys
+    past the causal end too (the select kernel then stages all N keys, not just the causal ones);
+    the other head selects normally."""
+    from synthetic import base_inv_freq, planted_inputs
+    H, N, D = 2, 900, 64
+    q, k, v = planted_inputs(13, H, H, N, D, 0.02, torch.bfloat16, DEV)
+    invf = base_inv_freq(D, 10000.0)
+    _check_weighted(q, k, v, torch.tensor([-1.0, 5.0]), invf.to(DEV), 0.5, 1.0, 64, 200, mode,
+                    what=f"weighted {mode}, empty union on head 0")
+
+
 def test_weighted_dropin_entry_points():
     """select_score through the reference's entry points (exact_2 / YaRN / hybrid) and _build_sets."""
     import shared_selection_triton_exact_2 as ex2
