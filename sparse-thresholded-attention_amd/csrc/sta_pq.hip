@@ -24,8 +24,12 @@
 
 namespace sta {
 
-// inclusive block scan of one int per thread (256 threads); returns the exclusive prefix and the
-// block total through *total
+// one workgroup per (head, tile): PQ_NT threads in PQ_NW waves
+constexpr int PQ_NT = 512;
+constexpr int PQ_NW = PQ_NT / 64;
+
+// inclusive block scan of one int per thread; returns the exclusive prefix and the block total
+// through *total
 __device__ __forceinline__ int pq_block_scan(int v, int* tmp, int* total) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   int x = v;
@@ -36,27 +40,60 @@ __device__ __forceinline__ int pq_block_scan(int v, int* tmp, int* total) {
   }
   if (lane == 63) tmp[wave] = x;
   __syncthreads();
-  int base = 0;
+  int base = 0, tot = 0;
 #pragma unroll
-  for (int w = 0; w < 4; ++w) base += w < wave ? tmp[w] : 0;
-  *total = tmp[0] + tmp[1] + tmp[2] + tmp[3];
+  for (int w = 0; w < PQ_NW; ++w) {
+    base += w < wave ? tmp[w] : 0;
+    tot += tmp[w];
+  }
+  *total = tot;
   __syncthreads();
   return base + x - v;
 }
 
-__device__ __forceinline__ int pq_block_sum(int v, int* tmp) {
-  int total;
-  pq_block_scan(v, tmp, &total);
-  return total;
+// three block sums in one exchange (tmp holds 3 * PQ_NW ints)
+__device__ __forceinline__ void pq_block_sum3(int x, int y, int z, int* tmp, int* sx, int* sy, int* sz) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    x += __shfl_xor(x, o, 64);
+    y += __shfl_xor(y, o, 64);
+    z += __shfl_xor(z, o, 64);
+  }
+  if (lane == 0) {
+    tmp[wave] = x;
+    tmp[PQ_NW + wave] = y;
+    tmp[2 * PQ_NW + wave] = z;
+  }
+  __syncthreads();
+  int a = 0, b = 0, c = 0;
+#pragma unroll
+  for (int w = 0; w < PQ_NW; ++w) {
+    a += tmp[w];
+    b += tmp[PQ_NW + w];
+    c += tmp[2 * PQ_NW + w];
+  }
+  *sx = a;
+  *sy = b;
+  *sz = c;
+  __syncthreads();
 }
 
-// The digit holding the need-th largest count of a histogram of 256 * B bins (descending), and
-// how many of its keys are still needed: misc[0], misc[1].  Thread t owns bins
-// 256B-1-Bt .. 256B-B-Bt.  Requires need >= 1 and at least `need` counts in the histogram.
+// KB keys of this thread's row from index i0 on (0 past `per`), read together so that one wait
+// covers them all
+constexpr int PQ_KB = 8;
+__device__ __forceinline__ void pq_load_keys(const uint32_t* row, int i0, int per, uint32_t (&k)[PQ_KB]) {
+#pragma unroll
+  for (int e = 0; e < PQ_KB; ++e) k[e] = i0 + e < per ? row[i0 + e] : 0u;
+}
+
+// The digit holding the need-th largest count of a histogram of PQ_NT * B bins (descending),
+// and how many of its keys are still needed: misc[0], misc[1].  Thread t owns bins
+// PQ_NT*B-1-Bt .. PQ_NT*B-B-Bt.  Requires need >= 1 and at least `need` counts in the histogram.
 template <int B>
 __device__ __forceinline__ void pq_find_digit(const int* hist, int need, int* tmp, int* misc) {
   const int tid = threadIdx.x;
-  const int top = 256 * B - 1 - B * tid;
+  const int top = PQ_NT * B - 1 - B * tid;
   int c[B], sl = 0;
 #pragma unroll
   for (int e = 0; e < B; ++e) {
@@ -89,7 +126,7 @@ __device__ __forceinline__ uint32_t pq_order_key(float r) {
   return k ? k : 1u;
 }
 
-__global__ __launch_bounds__(256) void pq_select_kernel(PqSelectArgs a) {
+__global__ __launch_bounds__(PQ_NT) void pq_select_kernel(PqSelectArgs a) {
 #pragma clang fp contract(off)
   extern __shared__ __align__(16) uint32_t pq_smem[];
   const int tid = threadIdx.x;
@@ -102,18 +139,18 @@ __global__ __launch_bounds__(256) void pq_select_kernel(PqSelectArgs a) {
   const int hi_keys = a.dense ? N : (int)min((int64_t)N, tstart + T);
   // keys at or past R are neither union members (no votes) nor forced
   const int R = a.dense ? N : (int)min((int64_t)N, max(tstart + T, (int64_t)a.n_global));
-  const int per = (R + 255) / 256;
+  const int per = (R + PQ_NT - 1) / PQ_NT;
   // thread tid scans keys [tid*per, tid*per + per); its keys sit at a row of odd stride PS so the
   // 64 lanes of a scan step fall in distinct LDS banks
   const int PS = per | 1;
-  const int PSMAX = ((N + 255) / 256) | 1;
-  uint32_t* rkb = pq_smem;                                  // 256 rows x PS rank keys (0: not a candidate)
+  const int PSMAX = ((N + PQ_NT - 1) / PQ_NT) | 1;
+  uint32_t* rkb = pq_smem;                                  // PQ_NT rows x PS rank keys (0: not a candidate)
   uint32_t* myrow = rkb + tid * PS;                         // this thread's keys j0 .. j0 + per - 1
   // j / per by a reciprocal multiply (per >= 2): exact for per <= 256 and j < 2^24
   const uint32_t inv_per = per > 1 ? (uint32_t)((0x100000000ull + per - 1) / per) : 0u;
-  int* hist = (int*)(rkb + 256 * PSMAX);                    // 256 bins (list and fallback levels)
-  int* tmp = hist + 256;                                    // 8
-  int* misc = tmp + 8;                                      // 8
+  int* hist = (int*)(rkb + PQ_NT * PSMAX);                  // PQ_NT bins (list and fallback levels)
+  int* tmp = hist + PQ_NT;                                  // 3 * PQ_NW
+  int* misc = tmp + 3 * PQ_NW;                              // 8
   float* qnp = (float*)(misc + 8);                          // T (<= 64)
   // region A, max(2048, k_max) words: the level-1 histogram (2048 bins), then the list of the
   // statistic's bin, then the kept keys in rank order
@@ -130,21 +167,21 @@ __global__ __launch_bounds__(256) void pq_select_kernel(PqSelectArgs a) {
   const bool weighted = a.wvotes != nullptr;
 
 #pragma unroll
-  for (int e = 0; e < 8; ++e) hist1[tid + 256 * e] = 0;
+  for (int e = 0; e < 2048 / PQ_NT; ++e) hist1[tid + PQ_NT * e] = 0;
   if (tid == 0) misc[2] = 0;
   __syncthreads();
 
   // ---- union, forced, candidates, their rank keys and the level-1 histogram (perquery.py:381-397) ----
-  // staged with coalesced loads (key j by thread j % 256); the scans below walk contiguous ranges
+  // staged with coalesced loads (key j by thread j % PQ_NT); the scans below walk contiguous ranges
   int cu = 0, cf = 0, cfo = 0;
   constexpr int U = 16;   // loads in flight per lane
-  for (int jb = 0; jb < 256 * per; jb += 256 * U) {
+  for (int jb = 0; jb < PQ_NT * per; jb += PQ_NT * U) {
     uint32_t bv[U];
     int vv[U];
     float wvv[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int j = jb + u * 256 + tid;
+      const int j = jb + u * PQ_NT + tid;
       const bool ok = j < hi_keys;
       bv[u] = (ok && !a.votes) ? brow[j] : 0u;
       vv[u] = (ok && a.votes) ? a.votes[roff + j] : 0;
@@ -152,7 +189,7 @@ __global__ __launch_bounds__(256) void pq_select_kernel(PqSelectArgs a) {
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int j = jb + u * 256 + tid;
+      const int j = jb + u * PQ_NT + tid;
       uint32_t key = 0;
       if (j < R) {
         const int vt = a.votes ? vv[u] : __popc(bv[u]);
@@ -175,16 +212,15 @@ __global__ __launch_bounds__(256) void pq_select_kernel(PqSelectArgs a) {
           atomicAdd(&hist1[d1], 1);
         }
       }
-      if (j < 256 * per) {
+      if (j < PQ_NT * per) {
         const uint32_t row = per == 1 ? (uint32_t)j : __umulhi((uint32_t)j, inv_per);
         rkb[row * PS + (j - row * per)] = key;
       }
     }
   }
   __syncthreads();
-  const int usize = pq_block_sum(cu, tmp);
-  const int nfull = pq_block_sum(cf, tmp);
-  const int nforced = pq_block_sum(cfo, tmp);
+  int usize, nfull, nforced;
+  pq_block_sum3(cu, cf, cfo, tmp, &usize, &nfull, &nforced);
   const bool overflow = nfull > a.k_max;                    // perquery.py:386
   const int budget = max(a.k_max - nforced, 0);             // perquery.py:399-400
   const bool cut = overflow && budget > 0;
@@ -193,7 +229,7 @@ __global__ __launch_bounds__(256) void pq_select_kernel(PqSelectArgs a) {
   uint32_t V = 0;
   int need_eq = 0;
   if (cut) {
-    pq_find_digit<8>(hist1, budget, tmp, misc);
+    pq_find_digit<2048 / PQ_NT>(hist1, budget, tmp, misc);
     const int d1 = misc[0];
     int need = misc[1];
     const int bin_count = hist1[d1];
@@ -225,9 +261,12 @@ __global__ __launch_bounds__(256) void pq_select_kernel(PqSelectArgs a) {
     __syncthreads();   // every thread has read hist1 before the list overwrites it
     int cnt = 0;
     if (from_list) {
-      for (int i = 0; i < per; ++i) {
-        const uint32_t k = myrow[i];
-        if (k != 0 && (k & pmask) == prefix) list[atomicAdd(&misc[2], 1)] = k;
+      for (int i0 = 0; i0 < per; i0 += PQ_KB) {
+        uint32_t kk[PQ_KB];
+        pq_load_keys(myrow, i0, per, kk);
+#pragma unroll
+        for (int e = 0; e < PQ_KB; ++e)
+          if (kk[e] != 0 && (kk[e] & pmask) == prefix) list[atomicAdd(&misc[2], 1)] = kk[e];
       }
       __syncthreads();
       cnt = misc[2];
@@ -240,14 +279,17 @@ __global__ __launch_bounds__(256) void pq_select_kernel(PqSelectArgs a) {
       hist[tid] = 0;
       __syncthreads();
       if (from_list) {
-        for (int i = tid; i < cnt; i += 256) {
+        for (int i = tid; i < cnt; i += PQ_NT) {
           const uint32_t k = list[i];
           if ((k & pmask) == prefix) atomicAdd(&hist[(k >> sh) & dmask], 1);
         }
       } else {
-        for (int i = 0; i < per; ++i) {
-          const uint32_t k = myrow[i];
-          if (k != 0 && (k & pmask) == prefix) atomicAdd(&hist[(k >> sh) & dmask], 1);
+        for (int i0 = 0; i0 < per; i0 += PQ_KB) {
+          uint32_t kk[PQ_KB];
+          pq_load_keys(myrow, i0, per, kk);
+#pragma unroll
+          for (int e = 0; e < PQ_KB; ++e)
+            if (kk[e] != 0 && (kk[e] & pmask) == prefix) atomicAdd(&hist[(kk[e] >> sh) & dmask], 1);
         }
       }
       __syncthreads();
@@ -263,16 +305,25 @@ __global__ __launch_bounds__(256) void pq_select_kernel(PqSelectArgs a) {
   __syncthreads();   // the list is dead: region A becomes sidx
 
   // ---- counts: kept keys strictly above the cut (and forced), keys at the cut ----
+  // (forced keys hold key 0; a candidate's key is never 0)
   int cstrict = 0, ceq = 0;
-  for (int j = j0; j < j1; ++j) {
-    const uint32_t k = myrow[j - j0];
-    if (is_forced(j)) {
-      ++cstrict;
-    } else if (k != 0) {
-      if (!overflow) ++cstrict;
-      else if (cut) {
-        cstrict += k > V;
-        ceq += k == V;
+  for (int i0 = 0; i0 < per; i0 += PQ_KB) {
+    uint32_t kk[PQ_KB];
+    pq_load_keys(myrow, i0, per, kk);
+#pragma unroll
+    for (int e = 0; e < PQ_KB; ++e) {
+      const int j = j0 + i0 + e;
+      if (j < j1) {
+        const uint32_t k = kk[e];
+        if (is_forced(j)) {
+          ++cstrict;
+        } else if (k != 0) {
+          if (!overflow) ++cstrict;
+          else if (cut) {
+            cstrict += k > V;
+            ceq += k == V;
+          }
+        }
       }
     }
   }
@@ -281,9 +332,8 @@ __global__ __launch_bounds__(256) void pq_select_kernel(PqSelectArgs a) {
   const int taken_eq = cut ? max(0, min(ceq, need_eq - eq_base)) : 0;
   int kept_total;
   const int base = pq_block_scan(cstrict + taken_eq, tmp, &kept_total);
-  auto kept_of = [&](int j, int eq_before) -> bool {
+  auto kept_of = [&](int j, uint32_t k, int eq_before) -> bool {
     if (is_forced(j)) return true;
-    const uint32_t k = myrow[j - j0];
     if (k == 0) return false;                 // not in the union (or forced, handled above)
     if (!overflow) return true;
     if (budget == 0) return false;
@@ -300,14 +350,22 @@ __global__ __launch_bounds__(256) void pq_select_kernel(PqSelectArgs a) {
   {
     int eq = eq_base;
     int rank = base - 1;
-    for (int j = j0; j < j1; ++j) {
-      const bool kp = kept_of(j, eq);
-      eq += cut && myrow[j - j0] == V && !is_forced(j);
-      if (kp) {
-        rank += 1;
-        if (rank < a.k_max) sidx[rank] = j;
+    for (int i0 = 0; i0 < per; i0 += PQ_KB) {
+      uint32_t kk[PQ_KB];
+      pq_load_keys(myrow, i0, per, kk);
+#pragma unroll
+      for (int e = 0; e < PQ_KB; ++e) {
+        const int j = j0 + i0 + e;
+        if (j < j1) {
+          const bool kp = kept_of(j, kk[e], eq);
+          eq += cut && kk[e] == V;
+          if (kp) {
+            rank += 1;
+            if (rank < a.k_max) sidx[rank] = j;
+          }
+          if (j >= qlo && j <= qhi) qnp[j - qlo] = (float)rank;   // rank0 = cumsum - 1
+        }
       }
-      if (j >= qlo && j <= qhi) qnp[j - qlo] = (float)rank;   // rank0 = cumsum - 1
     }
   }
   __syncthreads();
@@ -315,20 +373,28 @@ __global__ __launch_bounds__(256) void pq_select_kernel(PqSelectArgs a) {
   // which would scatter every store instruction over 64 cache lines); the kept keys ascend with
   // the slot, so the bit reads for the mask are nearly coalesced too
   const int nk = min(kept_total, a.k_max);
-  for (int s = tid; s < a.k_max; s += 256) {
-    if (s < nk) {
-      const int j = sidx[s];
-      irow[s] = j;
-      nkrow[s] = (float)s;
-      mrow[s] = is_forced(j) ? -1 : (int32_t)(j < hi_keys ? brow[j] : 0u);
-    } else {
-      irow[s] = N;
-      nkrow[s] = 0.0f;
-      mrow[s] = 0;
+  for (int s0 = tid; s0 < a.k_max; s0 += 4 * PQ_NT) {
+    int jj[4];
+    uint32_t bb[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {               // every bit read in flight before the stores
+      const int s = s0 + PQ_NT * e;
+      jj[e] = s < nk ? sidx[s] : N;
+      bb[e] = (s < nk && !is_forced(jj[e]) && jj[e] < hi_keys) ? brow[jj[e]] : 0u;
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int s = s0 + PQ_NT * e;
+      if (s < a.k_max) {
+        const bool valid = s < nk;
+        irow[s] = jj[e];
+        nkrow[s] = valid ? (float)s : 0.0f;
+        mrow[s] = valid ? (is_forced(jj[e]) ? -1 : (int32_t)bb[e]) : 0;
+      }
     }
   }
   float* nqrow = a.newpos_q + ((int64_t)h * a.nt + t) * T;
-  for (int i = tid; i < T; i += 256) {
+  for (int i = tid; i < T; i += PQ_NT) {
     const int qp = (int)min(tstart + i, (int64_t)N - 1);
     nqrow[i] = qnp[qp - qlo];
   }
@@ -360,9 +426,9 @@ __global__ __launch_bounds__(256) void expand_pq_kernel(const uint32_t* __restri
 }
 
 size_t pq_select_lds_bytes(int N, int k_max) {
-  const size_t per = (size_t)(N + 255) / 256;
+  const size_t per = (size_t)(N + PQ_NT - 1) / PQ_NT;
   const size_t region_a = (size_t)(k_max > 2048 ? k_max : 2048) * 4;
-  return 256 * (per | 1) * 4 + (256 + 8 + 8) * 4 + 64 * 4 + region_a;
+  return PQ_NT * (per | 1) * 4 + (PQ_NT + 3 * PQ_NW + 8) * 4 + 64 * 4 + region_a;
 }
 
 hipError_t launch_pq_select(const PqSelectArgs& a, hipStream_t st) {
@@ -371,7 +437,7 @@ hipError_t launch_pq_select(const PqSelectArgs& a, hipStream_t st) {
   hipError_t e = hipFuncSetAttribute((const void*)pq_select_kernel,
                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(pq_select_kernel, dim3(a.H * a.nt), dim3(256), lds, st, a);
+  hipLaunchKernelGGL(pq_select_kernel, dim3(a.H * a.nt), dim3(PQ_NT), lds, st, a);
   return hipGetLastError();
 }
 

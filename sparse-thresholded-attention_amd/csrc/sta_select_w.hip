@@ -19,13 +19,19 @@ namespace sta {
 
 namespace {
 
+// one workgroup per (head, tile): W_NT threads in W_NW waves
+constexpr int W_NT = 512;
+constexpr int W_NW = W_NT / 64;
+
 __device__ __forceinline__ int w_block_sum(int v, int* tmp) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
   if (lane == 0) tmp[wave] = v;
   __syncthreads();
-  const int total = tmp[0] + tmp[1] + tmp[2] + tmp[3];
+  int total = 0;
+#pragma unroll
+  for (int w = 0; w < W_NW; ++w) total += tmp[w];
   __syncthreads();
   return total;
 }
@@ -80,16 +86,24 @@ __device__ __forceinline__ uint32_t order_key(float r) {
   return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
 }
 
+// KB keys of this thread's row from index i0 on (0 past `per`), read together so that one wait
+// covers them all
+constexpr int W_KB = 8;
+__device__ __forceinline__ void w_load_keys(const uint32_t* row, int i0, int per, uint32_t (&k)[W_KB]) {
+#pragma unroll
+  for (int e = 0; e < W_KB; ++e) k[e] = i0 + e < per ? row[i0 + e] : 0u;
+}
+
 }  // namespace
 
 // LDS: per thread a contiguous key range of `per` keys at an odd row stride (conflict-free scans)
 size_t select_w_lds_bytes(int N, int k_max) {
-  const size_t per = (size_t)(N + 255) / 256;
-  return 256 * (per | 1) * 4 + (3 * 256 + 16 + 16 + 16) * 4 + 256 * 4 + (size_t)k_max * 8;
+  const size_t per = (size_t)(N + W_NT - 1) / W_NT;
+  return W_NT * (per | 1) * 4 + (3 * 256 + 16 + 16 + 16) * 4 + 256 * 4 + (size_t)k_max * 8;
 }
 
 template <typename VT>
-__global__ __launch_bounds__(256) void select_w_kernel(SelectArgs a) {
+__global__ __launch_bounds__(W_NT) void select_w_kernel(SelectArgs a) {
 #pragma clang fp contract(off)
   extern __shared__ __align__(16) uint32_t wsm[];
   const int tid = threadIdx.x, lane = tid & 63;
@@ -105,9 +119,9 @@ __global__ __launch_bounds__(256) void select_w_kernel(SelectArgs a) {
   // the staging counts; a tile where that fails stages all N keys instead.
   constexpr uint32_t ZK = 0x80000000u;                   // order_key(0.0f)
   int R = a.votes_dense ? N : (int)min((int64_t)N, max(tstart + T, (int64_t)a.n_global));
-  const int PSMAX = ((N + 255) / 256) | 1;
-  uint32_t* rkb = wsm;                                   // 256 rows x PS order keys
-  int* hist = (int*)(rkb + 256 * PSMAX);                 // 3 x 256
+  const int PSMAX = ((N + W_NT - 1) / W_NT) | 1;
+  uint32_t* rkb = wsm;                                   // W_NT rows x PS order keys
+  int* hist = (int*)(rkb + W_NT * PSMAX);                // 3 x 256
   int* tmp = hist + 3 * 256;                             // 16
   int* misc = tmp + 16;                                  // 16
   float* tmpf = (float*)(misc + 16);                     // 16
@@ -120,31 +134,31 @@ __global__ __launch_bounds__(256) void select_w_kernel(SelectArgs a) {
   const float* wrow = a.wvotes + roff;
   auto is_forced = [&](int j) { return j < a.n_global || (j >= lo && j <= hi_l); };   // exact_2.py:290-293
 
-  // ---- stage the rank keys of [0, R) (coalesced: key j by thread j % 256), U = #(votes > 0) and
+  // ---- stage the rank keys of [0, R) (coalesced: key j by thread j % W_NT), U = #(votes > 0) and
   //      the keys ranked above zero; SU loads of each array in flight per lane ----
   int per = 0, PS = 1, cu = 0, cpos = 0;
   uint32_t inv_per = 0;
   constexpr int SU = 8;
   auto stage = [&]() {
-    per = (R + 255) / 256;
+    per = (R + W_NT - 1) / W_NT;
     PS = per | 1;
     inv_per = per > 1 ? (uint32_t)((0x100000000ull + per - 1) / per) : 0u;
     cu = 0;
     cpos = 0;
-    for (int jb = 0; jb < 256 * per; jb += 256 * SU) {
+    for (int jb = 0; jb < W_NT * per; jb += W_NT * SU) {
       int vv[SU];
       float wv[SU];
 #pragma unroll
       for (int u = 0; u < SU; ++u) {
-        const int j = jb + u * 256 + tid;
+        const int j = jb + u * W_NT + tid;
         const bool ok = j < hi_keys;
         vv[u] = ok ? (int)vrow[j] : 0;
         wv[u] = ok ? wrow[j] : 0.0f;
       }
 #pragma unroll
       for (int u = 0; u < SU; ++u) {
-        const int j = jb + u * 256 + tid;
-        if (j >= 256 * per) break;
+        const int j = jb + u * W_NT + tid;
+        if (j >= W_NT * per) break;
         uint32_t key = 0;
         if (j < R) {
           const int v = vv[u];
@@ -173,7 +187,7 @@ __global__ __launch_bounds__(256) void select_w_kernel(SelectArgs a) {
   }
   if (a.votes_out || a.wvotes_out) {
     // the reference's dense (H, nt, N) votes / wvotes, zero past the tile's causal end
-    for (int j = tid; j < N; j += 256) {
+    for (int j = tid; j < N; j += W_NT) {
       const bool ok = j < hi_keys;
       if (a.votes_out) a.votes_out[((int64_t)h * a.nt + t) * N + j] = ok ? (int)vrow[j] : 0;
       if (a.wvotes_out) a.wvotes_out[((int64_t)h * a.nt + t) * N + j] = ok ? wrow[j] : 0.0f;
@@ -210,17 +224,22 @@ __global__ __launch_bounds__(256) void select_w_kernel(SelectArgs a) {
           hid[u] = f;
         }
       }
-      for (int i = tid; i < 256 * nh; i += 256) hist[i] = 0;
+      for (int i = tid; i < 256 * nh; i += W_NT) hist[i] = 0;
       __syncthreads();
       // plain LDS atomics on every level, the top digit included (a per-wave aggregation of the
       // top digit's few distinct values by ballots measured slower)
-      for (int i = 0; i < per; ++i) {
-        const uint32_t k = myrow[i];
-        if (k == 0 || j0 + i >= R) continue;
-        const uint32_t kp = k & pmask;
+      for (int i0 = 0; i0 < per; i0 += W_KB) {
+        uint32_t kk[W_KB];
+        w_load_keys(myrow, i0, per, kk);
 #pragma unroll
-        for (int w = 0; w < 3; ++w)
-          if (w < nh && kp == hp[w]) atomicAdd(&hist[w * 256 + ((k >> shift) & 255u)], 1);
+        for (int e = 0; e < W_KB; ++e) {
+          const uint32_t k = kk[e];
+          if (k == 0 || j0 + i0 + e >= R) continue;
+          const uint32_t kp = k & pmask;
+#pragma unroll
+          for (int w = 0; w < 3; ++w)
+            if (w < nh && kp == hp[w]) atomicAdd(&hist[w * 256 + ((k >> shift) & 255u)], 1);
+        }
       }
       __syncthreads();
 #pragma unroll
@@ -286,7 +305,7 @@ __global__ __launch_bounds__(256) void select_w_kernel(SelectArgs a) {
   };
   auto forced_below = [&](uint32_t cut) {
     int c = 0;
-    for (int i = tid; i < gA + nB; i += 256) {
+    for (int i = tid; i < gA + nB; i += W_NT) {
       const int j = i < gA ? i : bl + (i - gA);
       c += key_of(j) < cut;
     }
@@ -332,11 +351,19 @@ __global__ __launch_bounds__(256) void select_w_kernel(SelectArgs a) {
   }
 
   // ---- compaction + reposition (exact_2.py:383-412) ----
-  auto kept_of = [&](int j) { return is_forced(j) || (!forced_only && myrow[j - j0] >= cut); };
+  auto kept_of = [&](int j, uint32_t k) { return is_forced(j) || (!forced_only && k >= cut); };
   int cnt = 0, csh = 0;
-  for (int j = j0; j < j1; ++j) {
-    cnt += kept_of(j);
-    csh += !forced_only && myrow[j - j0] >= cut;
+  for (int i0 = 0; i0 < per; i0 += W_KB) {
+    uint32_t kk[W_KB];
+    w_load_keys(myrow, i0, per, kk);
+#pragma unroll
+    for (int e = 0; e < W_KB; ++e) {
+      const int j = j0 + i0 + e;
+      if (j < j1) {
+        cnt += kept_of(j, kk[e]);
+        csh += !forced_only && kk[e] >= cut;
+      }
+    }
   }
   const int base = w_block_exclusive_sum(cnt, tmp);
   const int kept_total = w_block_sum(cnt, tmp);
@@ -344,11 +371,17 @@ __global__ __launch_bounds__(256) void select_w_kernel(SelectArgs a) {
   float mloc = -INFINITY;
   {
     int rank = base - 1;
-    for (int j = j0; j < j1; ++j) {
-      if (kept_of(j)) {
-        rank += 1;
-        const float cp = (float)j * a.pos_scale;        // exact_2.py:384
-        mloc = fmaxf(mloc, cp - (float)rank);           // exact_2.py:385
+    for (int i0 = 0; i0 < per; i0 += W_KB) {
+      uint32_t kk[W_KB];
+      w_load_keys(myrow, i0, per, kk);
+#pragma unroll
+      for (int e = 0; e < W_KB; ++e) {
+        const int j = j0 + i0 + e;
+        if (j < j1 && kept_of(j, kk[e])) {
+          rank += 1;
+          const float cp = (float)j * a.pos_scale;        // exact_2.py:384
+          mloc = fmaxf(mloc, cp - (float)rank);           // exact_2.py:385
+        }
       }
     }
   }
@@ -357,28 +390,36 @@ __global__ __launch_bounds__(256) void select_w_kernel(SelectArgs a) {
   const int qhi = (int)min(tstart + T - 1, (int64_t)N - 1);
   {
     int rank = base - 1;
-    for (int j = j0; j < j1; ++j) {
-      const bool kept = kept_of(j);
-      if (kept) {
-        rank += 1;
-        const float cp = (float)j * a.pos_scale;
-        run = fmaxf(run, cp - (float)rank);
+    for (int i0 = 0; i0 < per; i0 += W_KB) {
+      uint32_t kk[W_KB];
+      w_load_keys(myrow, i0, per, kk);
+#pragma unroll
+      for (int e = 0; e < W_KB; ++e) {
+        const int j = j0 + i0 + e;
+        if (j < j1) {
+          const bool kept = kept_of(j, kk[e]);
+          if (kept) {
+            rank += 1;
+            const float cp = (float)j * a.pos_scale;
+            run = fmaxf(run, cp - (float)rank);
+          }
+          const float np = (float)rank + run;              // exact_2.py:386
+          if (kept && rank < a.k_max) { sidx[rank] = j; snp[rank] = np; }
+          if (j >= qlo && j <= qhi) qnp[j - qlo] = np;
+        }
       }
-      const float np = (float)rank + run;              // exact_2.py:386
-      if (kept && rank < a.k_max) { sidx[rank] = j; snp[rank] = np; }
-      if (j >= qlo && j <= qhi) qnp[j - qlo] = np;
     }
   }
   __syncthreads();
   const int nvalid = min(kept_total, a.k_max);
   int32_t* irow = a.idx + ((int64_t)h * a.nt + t) * a.k_max;
   float* nkrow = a.newpos_k + ((int64_t)h * a.nt + t) * a.k_max;
-  for (int s = tid; s < a.k_max; s += 256) {          // exact_2.py:401-408
+  for (int s = tid; s < a.k_max; s += W_NT) {         // exact_2.py:401-408
     irow[s] = s < nvalid ? sidx[s] : N;
     nkrow[s] = s < nvalid ? snp[s] : 0.0f;
   }
   float* nqrow = a.newpos_q + ((int64_t)h * a.nt + t) * T;
-  for (int i = tid; i < T; i += 256) {                  // exact_2.py:410-412
+  for (int i = tid; i < T; i += W_NT) {                 // exact_2.py:410-412
     const int qp = (int)min(tstart + i, (int64_t)N - 1);
     nqrow[i] = qnp[qp - qlo];
   }
@@ -400,12 +441,12 @@ hipError_t launch_select_weighted(const SelectArgs& a, int vote_bytes, hipStream
     hipError_t e = hipFuncSetAttribute((const void*)select_w_kernel<uint8_t>,
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(select_w_kernel<uint8_t>, dim3(a.H * a.nt), dim3(256), lds, st, a);
+    hipLaunchKernelGGL(select_w_kernel<uint8_t>, dim3(a.H * a.nt), dim3(W_NT), lds, st, a);
   } else {
     hipError_t e = hipFuncSetAttribute((const void*)select_w_kernel<int32_t>,
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(select_w_kernel<int32_t>, dim3(a.H * a.nt), dim3(256), lds, st, a);
+    hipLaunchKernelGGL(select_w_kernel<int32_t>, dim3(a.H * a.nt), dim3(W_NT), lds, st, a);
   }
   return hipGetLastError();
 }
