@@ -76,7 +76,9 @@ __global__ __launch_bounds__(256) void select_kernel(SelectArgs a) {
 #pragma clang fp contract(off)
   extern __shared__ __align__(16) uint8_t smem[];
   const int tid = threadIdx.x;
-  const int h = blockIdx.x / a.nt, t = blockIdx.x % a.nt;
+  // the longest key ranges (the last tiles) start first
+  const int h = (int)(blockIdx.x % a.H);
+  const int t = a.nt - 1 - (int)(blockIdx.x / a.H);
   const int T = a.T;
   const int64_t tstart = (int64_t)a.q_pos_base + (int64_t)t * T;          // exact_2.py:291
   // the key axis: [0, N); under DCA inter selection the tile's inter keys, with the budget's
@@ -111,7 +113,9 @@ __global__ __launch_bounds__(256) void select_kernel(SelectArgs a) {
   // votes are read for keys [0, hi_keys); Kernel A leaves keys past the tile's causal end
   // unwritten (their count is 0), a caller-supplied dense tensor is read in full
   const int hi_keys = a.votes_dense ? N : (int)min((int64_t)N, tstart + T);
-  const int per = ((((a.N + 255) / 256) + 15) / 16) * 16;                  // keys per thread, x16
+  // keys per thread for a scan over [0, n): a multiple of 16 (the vote bytes are read 16 at a time)
+  auto per_of = [](int n) { return (((n + 255) / 256 + 15) / 16) * 16; };
+  const int per = per_of(a.N);                                              // the staged row
   uint8_t* vb = smem;                                                       // 256 * per vote bytes
   int* hist = (int*)(smem + 256 * per);                                     // 256 bins -> C[v] (257)
   int* fhist = hist + 260;                                                  // 256 bins -> F[v] (257)
@@ -145,17 +149,18 @@ __global__ __launch_bounds__(256) void select_kernel(SelectArgs a) {
     int32_t* vo = a.votes_out + ((int64_t)h * a.nt + t) * a.N;
     for (int j = tid; j < a.N; j += 256) vo[j] = vb[j];
   }
-  // Thread tid owns keys [tid * per, tid * per + per) for the histogram and the compaction; its
-  // vote bytes are read 16 at a time.
-  const int j0 = tid * per;
+  // Thread tid owns a contiguous key range for the histogram and one for the compaction, each
+  // sized by the range the scan covers; its vote bytes are read 16 at a time.
   auto seg_bytes = [&](int jb) { return *(const u32x4*)(vb + jb); };
   auto byte_of = [](const u32x4& w, int e) { return (int)((w[e >> 2] >> (8 * (e & 3))) & 0xffu); };
   // ---- vote histogram over all N keys: the nonzero votes by LDS atomics, the zero bin by
   // subtraction (most keys of a tile have no vote, and one bin taking them all serialises) ----
   {
-    const int jend = min(j0 + per, hi_keys);
+    const int per_h = per_of(hi_keys);
+    const int jh0 = tid * per_h;
+    const int jend = min(jh0 + per_h, hi_keys);
     int nz = 0;
-    for (int jb = j0; jb < jend; jb += 16) {
+    for (int jb = jh0; jb < jend; jb += 16) {
       const u32x4 w = seg_bytes(jb);
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
@@ -242,7 +247,9 @@ __global__ __launch_bounds__(256) void select_kernel(SelectArgs a) {
   const int vc = misc[0];
   // ---- compaction + reposition over keys [0, scan_end) ----
   const int scan_end = (vc == 0) ? N : min(N, max(hi_keys, max(gA, bh + 1)));
-  const int j1 = min(j0 + per, scan_end);
+  const int per_c = per_of(scan_end);
+  const int j0 = tid * per_c;
+  const int j1 = min(j0 + per_c, scan_end);
   int cnt = 0;
   for (int jb = j0; jb < j1; jb += 16) {
     const u32x4 w = seg_bytes(jb);
