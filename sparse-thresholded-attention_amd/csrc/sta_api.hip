@@ -117,10 +117,9 @@ int check_sets_outputs(const sta_shared_args* a) {
   if (select_lds_bytes(a->N, a->k_max) > 160 * 1024)
     return fail(STA_ERR_UNSUPPORTED, "N=%d with k_max=%d needs more than 160 KB of LDS for selection",
                 a->N, a->k_max);
-  if (a->select_score != STA_SCORE_FREQ && select_w_lds_bytes(a->N, a->k_max) > 160 * 1024)
+  if (a->select_score != STA_SCORE_FREQ && select_w_lds_bytes(a->N, a->k_max, true) > 160 * 1024)
     return fail(STA_ERR_UNSUPPORTED,
-                "weighted ranking at N=%d with k_max=%d needs more than 160 KB of LDS for selection",
-                a->N, a->k_max);
+                "weighted ranking with k_max=%d needs more than 160 KB of LDS for selection", a->k_max);
   return STA_OK;
 }
 
@@ -394,10 +393,9 @@ int sta_build_sets_weighted(const sta_shared_args* args, const int32_t* votes, c
   if (num_tiles < 1) return fail(STA_ERR_INVALID_ARG, "num_tiles=%d must be >= 1", num_tiles);
   if (args->tile > 256) return fail(STA_ERR_UNSUPPORTED, "tile %d above 256", args->tile);
   if ((rc = check_sets_outputs(args)) != STA_OK) return rc;
-  if (select_w_lds_bytes(args->N, args->k_max) > 160 * 1024)
+  if (select_w_lds_bytes(args->N, args->k_max, true) > 160 * 1024)
     return fail(STA_ERR_UNSUPPORTED,
-                "weighted ranking at N=%d with k_max=%d needs more than 160 KB of LDS for selection",
-                args->N, args->k_max);
+                "weighted ranking with k_max=%d needs more than 160 KB of LDS for selection", args->k_max);
   Layout L = layout_of(args);
   L.nt = num_tiles;
   SelectArgs s = select_args_of(args, L);

@@ -305,7 +305,7 @@ hipError_t launch_expand_pq(const uint32_t* bits, const float* wv, int64_t strid
 size_t select_lds_bytes(int N, int k_max);
 hipError_t launch_select(const SelectArgs& a, int vote_bytes, hipStream_t st);
 // _build_sets ranked by weighted votes (select_score margin / expmass)
-size_t select_w_lds_bytes(int N, int k_max);
+size_t select_w_lds_bytes(int N, int k_max, bool global_keys);
 hipError_t launch_select_weighted(const SelectArgs& a, int vote_bytes, hipStream_t st);
 hipError_t launch_expand_votes(const uint8_t* v8, int64_t stride, int H, int nt, int N, int T, int q_pos_base,
                                int32_t* out, const float* wv, float* wv_out, hipStream_t st);

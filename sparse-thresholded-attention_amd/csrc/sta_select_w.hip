@@ -96,13 +96,18 @@ __device__ __forceinline__ void w_load_keys(const uint32_t* row, int i0, int per
 
 }  // namespace
 
-// LDS: per thread a contiguous key range of `per` keys at an odd row stride (conflict-free scans)
-size_t select_w_lds_bytes(int N, int k_max) {
+// LDS: per thread a contiguous key range of `per` keys at an odd row stride (conflict-free
+// scans), unless the keys are read from the vote rows at every pass (global_keys)
+size_t select_w_lds_bytes(int N, int k_max, bool global_keys) {
   const size_t per = (size_t)(N + W_NT - 1) / W_NT;
-  return W_NT * (per | 1) * 4 + (3 * 256 + 16 + 16 + 16) * 4 + 256 * 4 + (size_t)k_max * 8;
+  const size_t keys = global_keys ? 0 : W_NT * (per | 1) * 4;
+  return keys + (3 * 256 + 16 + 16 + 16) * 4 + 256 * 4 + (size_t)k_max * 8;
 }
 
-template <typename VT>
+// GK = false: the tile's rank keys are staged in LDS once.  GK = true (rows too long for LDS):
+// every pass recomputes each key from the vote and weighted-vote rows in the workspace (L2
+// resident for the workgroups in flight), with the same fp32 operations as the staging.
+template <typename VT, bool GK>
 __global__ __launch_bounds__(W_NT) void select_w_kernel(SelectArgs a) {
 #pragma clang fp contract(off)
   extern __shared__ __align__(16) uint32_t wsm[];
@@ -119,8 +124,8 @@ __global__ __launch_bounds__(W_NT) void select_w_kernel(SelectArgs a) {
   // the staging counts; a tile where that fails stages all N keys instead.
   constexpr uint32_t ZK = 0x80000000u;                   // order_key(0.0f)
   int R = a.votes_dense ? N : (int)min((int64_t)N, max(tstart + T, (int64_t)a.n_global));
-  const int PSMAX = ((N + W_NT - 1) / W_NT) | 1;
-  uint32_t* rkb = wsm;                                   // W_NT rows x PS order keys
+  const int PSMAX = GK ? 0 : ((N + W_NT - 1) / W_NT) | 1;
+  uint32_t* rkb = wsm;                                   // W_NT rows x PS order keys (LDS staging)
   int* hist = (int*)(rkb + W_NT * PSMAX);                // 3 x 256
   int* tmp = hist + 3 * 256;                             // 16
   int* misc = tmp + 16;                                  // 16
@@ -168,8 +173,10 @@ __global__ __launch_bounds__(W_NT) void select_w_kernel(SelectArgs a) {
           key = order_key(w + tb);
           cpos += key > ZK;
         }
-        const uint32_t row = per == 1 ? (uint32_t)j : __umulhi((uint32_t)j, inv_per);
-        rkb[row * PS + (j - row * per)] = key;
+        if constexpr (!GK) {
+          const uint32_t row = per == 1 ? (uint32_t)j : __umulhi((uint32_t)j, inv_per);
+          rkb[row * PS + (j - row * per)] = key;
+        }
       }
     }
     __syncthreads();
@@ -193,8 +200,26 @@ __global__ __launch_bounds__(W_NT) void select_w_kernel(SelectArgs a) {
       if (a.wvotes_out) a.wvotes_out[((int64_t)h * a.nt + t) * N + j] = ok ? wrow[j] : 0.0f;
     }
   }
-  uint32_t* myrow = rkb + tid * PS;                      // keys j0 .. j0 + per - 1
+  uint32_t* myrow = rkb + tid * PS;                      // keys j0 .. j0 + per - 1 (LDS staging)
   const int j0 = tid * per, j1 = min(j0 + per, R);
+  // the rank key of key j from the vote rows (GK): the staging's operations, 0 past R
+  auto gkey = [&](int j) -> uint32_t {
+    if (j >= R) return 0u;
+    const bool ok = j < hi_keys;
+    const int v = ok ? (int)vrow[j] : 0;
+    const float w = ok ? wrow[j] : 0.0f;
+    const float tb = 1e-6f * (float)v;
+    return order_key(w + tb);
+  };
+  // this thread's keys i0 .. i0 + W_KB - 1 of its contiguous range [j0, j0 + per)
+  auto range_keys = [&](int i0, uint32_t (&kk)[W_KB]) {
+    if constexpr (GK) {
+#pragma unroll
+      for (int e = 0; e < W_KB; ++e) kk[e] = i0 + e < per ? gkey(j0 + i0 + e) : 0u;
+    } else {
+      w_load_keys(myrow, i0, per, kk);
+    }
+  };
 
   // Order statistics for up to three targets at once: target t is the need[t]-th largest key
   // (1 <= need[t] <= N).  The targets walk the radix tree together, one pass over the keys per
@@ -230,11 +255,17 @@ __global__ __launch_bounds__(W_NT) void select_w_kernel(SelectArgs a) {
       // top digit's few distinct values by ballots measured slower)
       for (int i0 = 0; i0 < per; i0 += W_KB) {
         uint32_t kk[W_KB];
-        w_load_keys(myrow, i0, per, kk);
+        if constexpr (GK) {
+          // the histograms ignore key order: key (i0 + e) * W_NT + tid, coalesced
+#pragma unroll
+          for (int e = 0; e < W_KB; ++e) kk[e] = i0 + e < per ? gkey((i0 + e) * W_NT + tid) : 0u;
+        } else {
+          w_load_keys(myrow, i0, per, kk);
+        }
 #pragma unroll
         for (int e = 0; e < W_KB; ++e) {
           const uint32_t k = kk[e];
-          if (k == 0 || j0 + i0 + e >= R) continue;
+          if (k == 0 || (!GK && j0 + i0 + e >= R)) continue;
           const uint32_t kp = k & pmask;
 #pragma unroll
           for (int w = 0; w < 3; ++w)
@@ -299,9 +330,13 @@ __global__ __launch_bounds__(W_NT) void select_w_kernel(SelectArgs a) {
   const int bl = (int)max(lo, (int64_t)gA);
   const int bh = (int)min(hi_l, (int64_t)N - 1);
   const int nB = bh >= bl ? bh - bl + 1 : 0;
-  auto key_of = [&](int j) {
-    const uint32_t row = per == 1 ? (uint32_t)j : __umulhi((uint32_t)j, inv_per);
-    return rkb[row * PS + (j - row * per)];
+  auto key_of = [&](int j) -> uint32_t {
+    if constexpr (GK) {
+      return gkey(j);
+    } else {
+      const uint32_t row = per == 1 ? (uint32_t)j : __umulhi((uint32_t)j, inv_per);
+      return rkb[row * PS + (j - row * per)];
+    }
   };
   auto forced_below = [&](uint32_t cut) {
     int c = 0;
@@ -355,7 +390,7 @@ __global__ __launch_bounds__(W_NT) void select_w_kernel(SelectArgs a) {
   int cnt = 0, csh = 0;
   for (int i0 = 0; i0 < per; i0 += W_KB) {
     uint32_t kk[W_KB];
-    w_load_keys(myrow, i0, per, kk);
+    range_keys(i0, kk);
 #pragma unroll
     for (int e = 0; e < W_KB; ++e) {
       const int j = j0 + i0 + e;
@@ -373,7 +408,7 @@ __global__ __launch_bounds__(W_NT) void select_w_kernel(SelectArgs a) {
     int rank = base - 1;
     for (int i0 = 0; i0 < per; i0 += W_KB) {
       uint32_t kk[W_KB];
-      w_load_keys(myrow, i0, per, kk);
+      range_keys(i0, kk);
 #pragma unroll
       for (int e = 0; e < W_KB; ++e) {
         const int j = j0 + i0 + e;
@@ -392,7 +427,7 @@ __global__ __launch_bounds__(W_NT) void select_w_kernel(SelectArgs a) {
     int rank = base - 1;
     for (int i0 = 0; i0 < per; i0 += W_KB) {
       uint32_t kk[W_KB];
-      w_load_keys(myrow, i0, per, kk);
+      range_keys(i0, kk);
 #pragma unroll
       for (int e = 0; e < W_KB; ++e) {
         const int j = j0 + i0 + e;
@@ -434,21 +469,24 @@ __global__ __launch_bounds__(W_NT) void select_w_kernel(SelectArgs a) {
   }
 }
 
-hipError_t launch_select_weighted(const SelectArgs& a, int vote_bytes, hipStream_t st) {
-  const size_t lds = select_w_lds_bytes(a.N, a.k_max);
-  if (lds > 160 * 1024 || a.T > 256 || !a.wvotes) return hipErrorInvalidValue;
-  if (vote_bytes == 1) {
-    hipError_t e = hipFuncSetAttribute((const void*)select_w_kernel<uint8_t>,
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(select_w_kernel<uint8_t>, dim3(a.H * a.nt), dim3(W_NT), lds, st, a);
-  } else {
-    hipError_t e = hipFuncSetAttribute((const void*)select_w_kernel<int32_t>,
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(select_w_kernel<int32_t>, dim3(a.H * a.nt), dim3(W_NT), lds, st, a);
-  }
+template <typename VT, bool GK>
+static hipError_t launch_select_w_t(const SelectArgs& a, size_t lds, hipStream_t st) {
+  hipError_t e = hipFuncSetAttribute((const void*)select_w_kernel<VT, GK>,
+                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL((select_w_kernel<VT, GK>), dim3(a.H * a.nt), dim3(W_NT), lds, st, a);
   return hipGetLastError();
+}
+
+hipError_t launch_select_weighted(const SelectArgs& a, int vote_bytes, hipStream_t st) {
+  if (a.T > 256 || !a.wvotes) return hipErrorInvalidValue;
+  // the rank keys in LDS while they fit, else read from the vote rows at every pass
+  const bool gk = select_w_lds_bytes(a.N, a.k_max, false) > 160 * 1024;
+  const size_t lds = select_w_lds_bytes(a.N, a.k_max, gk);
+  if (lds > 160 * 1024) return hipErrorInvalidValue;
+  if (vote_bytes == 1)
+    return gk ? launch_select_w_t<uint8_t, true>(a, lds, st) : launch_select_w_t<uint8_t, false>(a, lds, st);
+  return gk ? launch_select_w_t<int32_t, true>(a, lds, st) : launch_select_w_t<int32_t, false>(a, lds, st);
 }
 
 }  // namespace sta

@@ -185,3 +185,48 @@ def test_weighted_config1_shape_one_head():
     invf, ps, rs = c.geometry()
     _check_weighted(q, k, v, torch.full((1,), c.tau), invf.to(DEV), ps, rs, c.tile, c.k_max, "expmass",
                     what="config 1 shape, one head, expmass")
+
+
+def test_weighted_long_rows_dense_votes():
+    """Rows too long for the rank keys in LDS (N = 40000 at k_max 2048): the select kernel reads
+    the keys from the vote rows at every pass; bit-exact against the oracle's _build_sets on the
+    same dense votes, with tied weighted votes at the cuts and the measure loop."""
+    import _sta_native as native
+    N, nt, T, kmax = 40000, 6, 64, 2048
+    g = np.random.default_rng(21)
+    votes = g.integers(0, T + 1, size=(1, nt, N)).astype(np.int32)
+    votes[:, :, g.random(N) < 0.5] = 0
+    wv = (votes * g.random((1, nt, N)) * 3.0).astype(np.float32)
+    wv[:, :, 5000:9000] = wv[:, :, 9000:13000]
+    for pct, meas in ((30.0, False), (22.5, True)):
+        say(f"weighted long rows, dense votes, N={N}, pct {pct}")
+        qb = N - nt * T
+        res = native.build_sets(torch.from_numpy(votes).to(DEV), 0.5, 32, 32, pct, T, kmax, qb, meas,
+                                wvotes=torch.from_numpy(wv).to(DEV))
+        torch.cuda.synchronize()
+        refs = orc.build_sets(votes, 0.5, 32, 32, pct, T, kmax, qb, meas, wvotes=wv)
+        for name, got, rr in zip(SET_NAMES, res, refs):
+            assert _same(got.cpu().numpy(), rr), name
+
+
+def test_weighted_long_rows_fused():
+    """The fused prefill with expmass ranking past the LDS limit (N = 37000, one head): sets
+    bit-exact against the oracle's _build_sets on the GPU's own votes and weighted votes."""
+    import _sta_native as native
+    from synthetic import base_inv_freq, planted_inputs
+    H, N, D, T, kmax = 1, 37000, 64, 64, 2048
+    q, k, v = planted_inputs(17, H, H, N, D, 0.02, torch.bfloat16, DEV)
+    invf = base_inv_freq(D, 10000.0).to(DEV)
+    tau = torch.full((H,), 5.0)
+    say(f"weighted long rows, fused, N={N}")
+    r = native.shared_attention(q, k, v, tau, invf, 1 / 3, 1.0, invf, 1 / 3, 1.0, pct=30.0, tile=T, k_max=kmax,
+                                want_votes=True, select_score="expmass")
+    torch.cuda.synchronize()
+    votes_g, wv_g = r["votes"].cpu().numpy(), r["wvotes"].cpu().numpy()
+    sets_g = gpu_sets_numpy(r)
+    refs = orc.build_sets(votes_g, 1 / 3, 32, 32, 30.0, T, kmax, 0, False, wvotes=wv_g)
+    for name, rr in zip(SET_NAMES, refs):
+        assert _same(sets_g[name], rr), name
+    assert torch.isfinite(r["out"].float()).all()
+    print(f"[result] weighted long rows fused: kept mean {sets_g['kept_size'].mean():.1f}, "
+          f"overflow20 {int(sets_g['overflow20'].sum())}", flush=True)
