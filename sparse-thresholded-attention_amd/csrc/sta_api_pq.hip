@@ -57,8 +57,9 @@ int pq_check_common(const sta_pq_args* a) {
     return fail(STA_ERR_INVALID_ARG, "n_global=%d / n_local=%d must be >= 0", a->n_global, a->n_local);
   if (a->select_score < STA_SCORE_FREQ || a->select_score > STA_SCORE_EXPMASS)
     return fail(STA_ERR_INVALID_ARG, "select_score %d is not one of STA_SCORE_*", a->select_score);
-  if (pq_select_lds_bytes(a->N, a->k_max) > 160 * 1024)
-    return fail(STA_ERR_UNSUPPORTED, "N=%d needs more than 160 KB of LDS for per-query selection", a->N);
+  if (pq_select_lds_bytes(a->N, a->k_max, true) > 160 * 1024)
+    return fail(STA_ERR_UNSUPPORTED, "k_max=%d needs more than 160 KB of LDS for per-query selection",
+                a->k_max);
   return STA_OK;
 }
 

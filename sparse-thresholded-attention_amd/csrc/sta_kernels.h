@@ -297,7 +297,7 @@ hipError_t launch_score_pq(int D, int wmode, const ScoreArgs& a, hipStream_t st)
 hipError_t launch_score_thresholds(int D, const ScoreArgs& a, hipStream_t st);
 // shared selection with weighted votes: wmode 1 margin / 2 expmass, byte votes + fp32 wvotes
 hipError_t launch_score_weighted(int D, int tile, int wmode, const ScoreArgs& a, hipStream_t st);
-size_t pq_select_lds_bytes(int N, int k_max);
+size_t pq_select_lds_bytes(int N, int k_max, bool global_keys);
 hipError_t launch_pq_select(const PqSelectArgs& a, hipStream_t st);
 hipError_t launch_expand_pq(const uint32_t* bits, const float* wv, int64_t stride, int H, int nt, int N,
                             int T, int q_pos_base, int32_t* votes_out, int32_t* bits_out,

@@ -126,6 +126,10 @@ __device__ __forceinline__ uint32_t pq_order_key(float r) {
   return k ? k : 1u;
 }
 
+// GK = false: the tile's rank keys are staged in LDS once.  GK = true (rows too long for LDS):
+// every pass recomputes each key from the bits / votes / weighted-vote rows in the workspace
+// (L2-resident for the workgroups in flight), with the staging's operations.
+template <bool GK>
 __global__ __launch_bounds__(PQ_NT) void pq_select_kernel(PqSelectArgs a) {
 #pragma clang fp contract(off)
   extern __shared__ __align__(16) uint32_t pq_smem[];
@@ -143,7 +147,7 @@ __global__ __launch_bounds__(PQ_NT) void pq_select_kernel(PqSelectArgs a) {
   // thread tid scans keys [tid*per, tid*per + per); its keys sit at a row of odd stride PS so the
   // 64 lanes of a scan step fall in distinct LDS banks
   const int PS = per | 1;
-  const int PSMAX = ((N + PQ_NT - 1) / PQ_NT) | 1;
+  const int PSMAX = GK ? 0 : ((N + PQ_NT - 1) / PQ_NT) | 1;
   uint32_t* rkb = pq_smem;                                  // PQ_NT rows x PS rank keys (0: not a candidate)
   uint32_t* myrow = rkb + tid * PS;                         // this thread's keys j0 .. j0 + per - 1
   // j / per by a reciprocal multiply (per >= 2): exact for per <= 256 and j < 2^24
@@ -212,7 +216,7 @@ __global__ __launch_bounds__(PQ_NT) void pq_select_kernel(PqSelectArgs a) {
           atomicAdd(&hist1[d1], 1);
         }
       }
-      if (j < PQ_NT * per) {
+      if (!GK && j < PQ_NT * per) {
         const uint32_t row = per == 1 ? (uint32_t)j : __umulhi((uint32_t)j, inv_per);
         rkb[row * PS + (j - row * per)] = key;
       }
@@ -224,6 +228,38 @@ __global__ __launch_bounds__(PQ_NT) void pq_select_kernel(PqSelectArgs a) {
   const bool overflow = nfull > a.k_max;                    // perquery.py:386
   const int budget = max(a.k_max - nforced, 0);             // perquery.py:399-400
   const bool cut = overflow && budget > 0;
+  // the rank key of key j from the workspace rows (GK): the staging's operations; 0 for keys past
+  // R, outside the union, or forced
+  auto gkey = [&](int j) -> uint32_t {
+    if (j >= R || is_forced(j)) return 0u;
+    const bool ok = j < hi_keys;
+    const int vt = !ok ? 0 : (a.votes ? a.votes[roff + j] : __popc(brow[j]));
+    if (vt <= 0) return 0u;
+    if (weighted) {
+      const float tb = 1e-6f * (float)vt;
+      return pq_order_key(a.wvotes[roff + j] + tb);
+    }
+    return pq_order_key((float)vt);
+  };
+  // PQ_KB keys in an order the histograms and the list ignore: strided over the threads
+  // (coalesced) when read from the workspace
+  auto order_free_keys = [&](int i0, uint32_t (&kk)[PQ_KB]) {
+    if constexpr (GK) {
+#pragma unroll
+      for (int e = 0; e < PQ_KB; ++e) kk[e] = i0 + e < per ? gkey((i0 + e) * PQ_NT + tid) : 0u;
+    } else {
+      pq_load_keys(myrow, i0, per, kk);
+    }
+  };
+  // this thread's keys i0 .. i0 + PQ_KB - 1 of its contiguous range [j0, j0 + per)
+  auto range_keys = [&](int i0, uint32_t (&kk)[PQ_KB]) {
+    if constexpr (GK) {
+#pragma unroll
+      for (int e = 0; e < PQ_KB; ++e) kk[e] = i0 + e < per ? gkey(j0 + i0 + e) : 0u;
+    } else {
+      pq_load_keys(myrow, i0, per, kk);
+    }
+  };
 
   // ---- overflow: the budget-th largest rank key V and how many keys equal to V are taken ----
   uint32_t V = 0;
@@ -263,7 +299,7 @@ __global__ __launch_bounds__(PQ_NT) void pq_select_kernel(PqSelectArgs a) {
     if (from_list) {
       for (int i0 = 0; i0 < per; i0 += PQ_KB) {
         uint32_t kk[PQ_KB];
-        pq_load_keys(myrow, i0, per, kk);
+        order_free_keys(i0, kk);
 #pragma unroll
         for (int e = 0; e < PQ_KB; ++e)
           if (kk[e] != 0 && (kk[e] & pmask) == prefix) list[atomicAdd(&misc[2], 1)] = kk[e];
@@ -286,7 +322,7 @@ __global__ __launch_bounds__(PQ_NT) void pq_select_kernel(PqSelectArgs a) {
       } else {
         for (int i0 = 0; i0 < per; i0 += PQ_KB) {
           uint32_t kk[PQ_KB];
-          pq_load_keys(myrow, i0, per, kk);
+          order_free_keys(i0, kk);
 #pragma unroll
           for (int e = 0; e < PQ_KB; ++e)
             if (kk[e] != 0 && (kk[e] & pmask) == prefix) atomicAdd(&hist[(kk[e] >> sh) & dmask], 1);
@@ -309,7 +345,7 @@ __global__ __launch_bounds__(PQ_NT) void pq_select_kernel(PqSelectArgs a) {
   int cstrict = 0, ceq = 0;
   for (int i0 = 0; i0 < per; i0 += PQ_KB) {
     uint32_t kk[PQ_KB];
-    pq_load_keys(myrow, i0, per, kk);
+    range_keys(i0, kk);
 #pragma unroll
     for (int e = 0; e < PQ_KB; ++e) {
       const int j = j0 + i0 + e;
@@ -352,7 +388,7 @@ __global__ __launch_bounds__(PQ_NT) void pq_select_kernel(PqSelectArgs a) {
     int rank = base - 1;
     for (int i0 = 0; i0 < per; i0 += PQ_KB) {
       uint32_t kk[PQ_KB];
-      pq_load_keys(myrow, i0, per, kk);
+      range_keys(i0, kk);
 #pragma unroll
       for (int e = 0; e < PQ_KB; ++e) {
         const int j = j0 + i0 + e;
@@ -425,19 +461,24 @@ __global__ __launch_bounds__(256) void expand_pq_kernel(const uint32_t* __restri
   }
 }
 
-size_t pq_select_lds_bytes(int N, int k_max) {
+size_t pq_select_lds_bytes(int N, int k_max, bool global_keys) {
   const size_t per = (size_t)(N + PQ_NT - 1) / PQ_NT;
   const size_t region_a = (size_t)(k_max > 2048 ? k_max : 2048) * 4;
-  return PQ_NT * (per | 1) * 4 + (PQ_NT + 3 * PQ_NW + 8) * 4 + 64 * 4 + region_a;
+  const size_t keys = global_keys ? 0 : PQ_NT * (per | 1) * 4;
+  return keys + (PQ_NT + 3 * PQ_NW + 8) * 4 + 64 * 4 + region_a;
 }
 
 hipError_t launch_pq_select(const PqSelectArgs& a, hipStream_t st) {
-  const size_t lds = pq_select_lds_bytes(a.N, a.k_max);
-  if (lds > 160 * 1024 || a.T > 64) return hipErrorInvalidValue;
-  hipError_t e = hipFuncSetAttribute((const void*)pq_select_kernel,
-                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+  if (a.T > 64) return hipErrorInvalidValue;
+  // the rank keys in LDS while they fit, else read from the workspace rows at every pass
+  const bool gk = pq_select_lds_bytes(a.N, a.k_max, false) > 160 * 1024;
+  const size_t lds = pq_select_lds_bytes(a.N, a.k_max, gk);
+  if (lds > 160 * 1024) return hipErrorInvalidValue;
+  const void* fn = gk ? (const void*)pq_select_kernel<true> : (const void*)pq_select_kernel<false>;
+  hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(pq_select_kernel, dim3(a.H * a.nt), dim3(PQ_NT), lds, st, a);
+  if (gk) hipLaunchKernelGGL(pq_select_kernel<true>, dim3(a.H * a.nt), dim3(PQ_NT), lds, st, a);
+  else hipLaunchKernelGGL(pq_select_kernel<false>, dim3(a.H * a.nt), dim3(PQ_NT), lds, st, a);
   return hipGetLastError();
 }
 

@@ -165,16 +165,18 @@ def _radix_case(seed, N, nt, kind):
     return votes, bits, wv
 
 
-@pytest.mark.parametrize("kind,mode", [("wide_bin", 2), ("list_bin", 1), ("nonpositive", 1), ("big_votes", 0),
-                                       ("small_votes", 0)])
-def test_pq_build_sets_radix_paths(kind, mode):
+@pytest.mark.parametrize("kind,mode,N", [("wide_bin", 2, 6000), ("list_bin", 1, 6000), ("nonpositive", 1, 6000),
+                                         ("big_votes", 0, 6000), ("small_votes", 0, 6000), ("wide_bin", 2, 40000),
+                                         ("list_bin", 2, 40000), ("small_votes", 0, 40000)])
+def test_pq_build_sets_radix_paths(kind, mode, N):
     """Every path of the device's budget cut (vote-count digit, weighted list, weighted bin too wide
     for the list, caller votes of 2047 and more, non-positive rank values) against the oracle, bit
-    for bit, with exact ties at the cut."""
+    for bit, with exact ties at the cut; at N = 40000 the rank keys outgrow the LDS and every pass
+    reads them from the vote rows."""
     import _sta_native as native
-    N, nt, T, kmax, ng, nl = 6000, 3, 32, 256, 8, 8
+    nt, T, kmax, ng, nl = 3, 32, 256, 8, 8
     votes, bits, wv = _radix_case(7, N, nt, kind)
-    say(f"pq radix path {kind}, rank mode {mode}")
+    say(f"pq radix path {kind}, rank mode {mode}, N={N}")
     res = native.pq_build_sets(torch.from_numpy(votes).to(DEV), torch.from_numpy(bits).to(DEV),
                                torch.from_numpy(wv).to(DEV), ng, nl, T, kmax, N - nt * T,
                                ["freq", "margin", "expmass"][mode])
