@@ -61,6 +61,10 @@ int dca_check(const sta_dca_args* a) {
   if (a->pretrain_len < 1) return fail(STA_ERR_INVALID_ARG, "pretrain_len=%d must be >= 1", a->pretrain_len);
   if (!(a->mscale >= 0.0f) || isinf(a->mscale))
     return fail(STA_ERR_INVALID_ARG, "mscale=%g must be finite and >= 0 (0: derived from N)", (double)a->mscale);
+  // the sweep keeps its running max on the raw dots, which orders as the scaled scores only for
+  // a positive scale
+  if (!(a->scale > 0.0f) || isinf(a->scale))
+    return fail(STA_ERR_INVALID_ARG, "scale=%g must be finite and > 0", (double)a->scale);
   const int L = a->chunk_size - a->local_window;
   if (L % 64 != 0)
     return fail(STA_ERR_UNSUPPORTED, "chunk_size - local_window = %d is not a multiple of 64", L);

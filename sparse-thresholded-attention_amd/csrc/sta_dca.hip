@@ -319,29 +319,40 @@ __global__ __launch_bounds__(G * 64, 1) void dca_attn_kernel(DcaArgs a) {
         }
       }
       // causal mask only where the block reaches the tile's rows (intra chunk, :411-413); the
-      // selected inter keys all precede the tile, only slots past the valid ones are masked
-      const bool diag = MODE == 1 ? start + BN > nsel : start + BN - 1 > r0;
+      // selected inter keys all precede the tile, only slots past the valid ones are masked.
+      // The running max mR stays in raw dot units and the weights are exp2((s - mR) * c2) with
+      // c2 = scale * log2(e): one FMA and one exp2 per score (scale > 0, so the raw max orders as
+      // the scaled one).
+      const bool diag = MODE == 1 ? start + BN > nsel : start + BN - 1 > r0;   // wave-uniform
       float bmax = -INFINITY;
+      if (diag) {
 #pragma unroll
-      for (int sb = 0; sb < NSB; ++sb)
+        for (int sb = 0; sb < NSB; ++sb)
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const int key = start + sb * 32 + (i >> 2) * 8 + 4 * hf + (i & 3);
-          const bool ok = !diag || (MODE == 1 ? key < nsel : key <= row);
-          const float v = ok ? sacc[sb][i] * a.scale : -INFINITY;
-          sacc[sb][i] = v;
-          bmax = fmaxf(bmax, v);
-        }
+          for (int i = 0; i < 16; ++i) {
+            const int key = start + sb * 32 + (i >> 2) * 8 + 4 * hf + (i & 3);
+            const bool ok = MODE == 1 ? key < nsel : key <= row;
+            const float v = ok ? sacc[sb][i] : -INFINITY;
+            sacc[sb][i] = v;
+            bmax = fmaxf(bmax, v);
+          }
+      } else {
+#pragma unroll
+        for (int sb = 0; sb < NSB; ++sb)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) bmax = fmaxf(bmax, sacc[sb][i]);
+      }
       bmax = fmaxf(bmax, __shfl_xor(bmax, 32, 64));
+      const float c2 = a.scale * 1.4426950408889634f;
       const float mnew = fmaxf(mR, bmax);
-      const float msafe = (mnew == -INFINITY) ? 0.0f : mnew;
-      const float alpha = __expf(mR - msafe);
+      const float mc = (mnew == -INFINITY) ? 0.0f : mnew * c2;   // exponent origin
+      const float alpha = __builtin_amdgcn_exp2f(mR * c2 - mc);  // mR = -inf: 0
       float psum = 0.0f;
 #pragma unroll
       for (int sb = 0; sb < NSB; ++sb)
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-          const float pv = __expf(sacc[sb][i] - msafe);
+          const float pv = __builtin_amdgcn_exp2f(fmaf(sacc[sb][i], c2, -mc));
           sacc[sb][i] = pv;
           psum += pv;
         }

@@ -68,6 +68,13 @@ def test_invalid_arguments_are_rejected(field, value, code):
     assert len(lib.sta_last_error()) > 0
 
 
+def test_pq_long_rows_are_sized():
+    """Rows past the selection's LDS (N = 100000) are supported: their rank keys are read from
+    the workspace rows."""
+    import _sta_native as native
+    assert native.lib().sta_pq_workspace_size(ctypes.byref(_pq_args(N=100000))) > 0
+
+
 def test_missing_pointers_are_rejected_before_any_launch():
     import _sta_native as native
     lib = native.lib()
@@ -118,7 +125,7 @@ def _pq_args(**kw):
 
 
 @pytest.mark.parametrize("field,value,code", [
-    ("tile", 64, -1), ("D", 80, -2), ("select_score", 5, -1), ("N", 100000, -2), ("k_max", 0, -1),
+    ("tile", 64, -1), ("D", 80, -2), ("select_score", 5, -1), ("k_max", 60000, -2), ("k_max", 0, -1),
 ])
 def test_pq_invalid_arguments_are_rejected(field, value, code):
     import _sta_native as native
@@ -188,7 +195,7 @@ def _dca_args(**kw):
 
 @pytest.mark.parametrize("field,value,code", [
     ("local_window", 0, -1), ("local_window", 4096, -1), ("chunk_size", 4100, -2), ("D", 32, -2),
-    ("pretrain_len", 0, -1),
+    ("pretrain_len", 0, -1), ("scale", 0.0, -1), ("scale", -0.1, -1), ("scale", float("inf"), -1),
 ])
 def test_dca_invalid_arguments_are_rejected(field, value, code):
     import _sta_native as native
