@@ -443,6 +443,34 @@ def shared_attention_noalloc(q, k, v, tau, inv_freq_a, pos_scale_a, rope_scale_a
     return out
 
 
+class NoallocPlan:
+    """Outputs for one shape allocated once; run() launches the whole prefill path through
+    sta_shared_attention_noalloc on the current stream, with no workspace and no allocation, so
+    it can be recorded into a HIP graph (torch.cuda.graph).  The library resolves its scratch
+    array's device address on the first call on a device: run once before capturing."""
+
+    def __init__(self, q, k, v, tau, inv_freq_a, pos_scale_a, rope_scale_a, inv_freq_c, pos_scale_c,
+                 rope_scale_c, pct=30.0, sm_scale=None, n_global=32, n_local=32, tile=32, k_max=1024,
+                 q_pos_base=0, measure=False, want_votes=False, select_score="freq"):
+        qh, kh, vh, tau, ifa, ifc = _prep_inputs(q, k, v, tau, inv_freq_a, inv_freq_c)
+        H, N, D = qh.shape
+        if sm_scale is None:
+            sm_scale = 1.0 / math.sqrt(D)
+        self.device = qh.device
+        a = self.args = ShareArgs()
+        _fill_common(a, qh, kh, vh, tau, ifa, pos_scale_a, rope_scale_a, ifc, pos_scale_c, rope_scale_c,
+                     sm_scale, pct, n_global, n_local, tile, k_max, q_pos_base, measure, select_score)
+        self.out = _alloc_outputs(a, H, N, D, qh.dtype, tile, k_max, qh.device, want_votes, False, False,
+                                  want_wvotes=want_votes and select_score != "freq")
+        a.workspace, a.workspace_bytes = None, 0
+        self._keep = (qh, kh, vh, tau, ifa, ifc)
+
+    def run(self):
+        _check(lib().sta_shared_attention_noalloc(ctypes.byref(self.args), _stream(self.device)),
+               "sta_shared_attention_noalloc")
+        return self.out
+
+
 def select_vote(q, k, tau, inv_freq, pos_scale, rope_scale, sm_scale, tile, q_pos_base=0,
                 want_row_counts=True, select_score="freq"):
     """Kernel A alone: votes (H,nt,N) int32, row_counts (H,N) int32, row_max (H,N) fp32; with a
