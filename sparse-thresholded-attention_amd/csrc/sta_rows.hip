@@ -10,27 +10,29 @@
 // with fp32 accumulation in v_mfma_f32_32x32x16_bf16, the score kernel's pass-2 product (error
 // <= 3 * 2^-16 * sum |q_i k_i|, about 1e-6 on unit-scale rows).
 //
-// One workgroup = one head and 256 consecutive queries in four waves of 64 (two 32-row blocks,
-// whose Q fragments stay in registers).  The keys run in 32-key chunks that every wave reads
-// from LDS: the next chunk's fragments are loaded into registers while the current chunk's
-// products run, then stored into the other LDS buffer.  Query i sees the keys
-// [0, M - (Q - 1 - i)) (its cache prefix: [0, q_pos0 + i] when the batch ends at the cache's last
-// key); scores past that are not written.  Workgroups with the
-// longest rows start first.
+// One workgroup = one head, 256 consecutive queries in four waves of 64 (two 32-row blocks,
+// whose Q fragments stay in registers) and one piece of at most ROWS_PIECE 32-key chunks of the
+// keys those queries see: a group's key range is split so that a launch over a few heads still
+// has thousands of equal workgroups (a group per workgroup gave one head pair 128 workgroups of
+// 1 to 64 units of work).  Every wave reads the chunks from LDS: the next chunk's fragments are
+// loaded into registers while the current chunk's products run, then stored into the other LDS
+// buffer.  Query i sees the keys [0, M - (Q - 1 - i)) (its cache prefix: [0, q_pos0 + i] when the
+// batch ends at the cache's last key); scores past that are not written.
 #include "sta_device.h"
 #include "sta_kernels.h"
 
 namespace sta {
 
+constexpr int ROWS_PIECE = 32;               // 32-key chunks per workgroup
+
 template <int D>
-__global__ __launch_bounds__(256) void score_rows_kernel(RowsArgs a) {
+__global__ __launch_bounds__(256) void score_rows_kernel(RowsArgs a, int npieces) {
   constexpr int S = D / 16;                  // k steps of 16
   constexpr int CH = S * 2 * 64;             // 16-byte units of one 32-key block (hi, lo)
   constexpr int PER = CH / 256;              // units per thread and chunk
   __shared__ u32x4 lds[2][CH];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int ngroups = (a.Q + 255) / 256;
-  const int g = ngroups - 1 - (int)blockIdx.x;            // longest rows first
+  const int g = (int)blockIdx.x / npieces, piece = (int)blockIdx.x % npieces;
   const int h = blockIdx.y;
   const int kvh = h / (a.H / a.Hkv);
   const int r0 = g * 256;
@@ -38,7 +40,9 @@ __global__ __launch_bounds__(256) void score_rows_kernel(RowsArgs a) {
   const int last_row = min(r0 + 256, a.Q) - 1;
   // row i sees the keys [0, m_i), m_i = M - (Q - 1 - i): the cache prefix of the decode contract
   const int kend = a.M - (a.Q - 1 - last_row);            // keys any row of the group sees
-  const int nchunks = (kend + 31) / 32;
+  const int c0 = piece * ROWS_PIECE;
+  const int c1 = min((kend + 31) / 32, c0 + ROWS_PIECE);  // this piece's chunks [c0, c1)
+  if (c0 >= c1) return;                                   // uniform: the group's keys end earlier
   const int wlast = min(wrow0 + 63, a.Q - 1);
   const int wkend = wrow0 < a.Q ? a.M - (a.Q - 1 - wlast) : 0;
 
@@ -71,15 +75,13 @@ __global__ __launch_bounds__(256) void score_rows_kernel(RowsArgs a) {
 #pragma unroll
     for (int e = 0; e < PER; ++e) lds[buf][e * 256 + tid] = pre[e];
   };
-  if (nchunks > 0) {
-    load_chunk(0);
-    store_chunk(0);
-  }
+  load_chunk(c0);
+  store_chunk(0);
   __syncthreads();
   float* srow = a.scores + (int64_t)h * a.Q * a.M;
-  for (int c = 0; c < nchunks; ++c) {
-    const int buf = c & 1;
-    if (c + 1 < nchunks) load_chunk(c + 1);
+  for (int c = c0; c < c1; ++c) {
+    const int buf = (c - c0) & 1;
+    if (c + 1 < c1) load_chunk(c + 1);
     const int key0 = c * 32;
     if (key0 < wkend) {                      // wave-uniform: some row of the wave sees the chunk
       floatx16 acc[2];
@@ -108,15 +110,18 @@ __global__ __launch_bounds__(256) void score_rows_kernel(RowsArgs a) {
             srow[(int64_t)row * a.M + key] = acc[rb][i] * a.sm_scale;
         }
     }
-    if (c + 1 < nchunks) store_chunk(buf ^ 1);   // that buffer was last read before the barrier
+    if (c + 1 < c1) store_chunk(buf ^ 1);   // that buffer was last read before the barrier
     __syncthreads();
   }
 }
 
 hipError_t launch_score_rows(int D, const RowsArgs& a, hipStream_t st) {
-  const dim3 grid((unsigned)((a.Q + 255) / 256), (unsigned)a.H);
-  if (D == 64) hipLaunchKernelGGL(score_rows_kernel<64>, grid, dim3(256), 0, st, a);
-  else if (D == 128) hipLaunchKernelGGL(score_rows_kernel<128>, grid, dim3(256), 0, st, a);
+  // pieces of the longest group (its last row sees all M keys); shorter groups leave the tail of
+  // their pieces empty
+  const int npieces = ((a.M + 31) / 32 + ROWS_PIECE - 1) / ROWS_PIECE;
+  const dim3 grid((unsigned)((a.Q + 255) / 256 * npieces), (unsigned)a.H);
+  if (D == 64) hipLaunchKernelGGL(score_rows_kernel<64>, grid, dim3(256), 0, st, a, npieces);
+  else if (D == 128) hipLaunchKernelGGL(score_rows_kernel<128>, grid, dim3(256), 0, st, a, npieces);
   else return hipErrorInvalidValue;
   return hipGetLastError();
 }
