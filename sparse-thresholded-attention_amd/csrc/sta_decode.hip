@@ -609,11 +609,20 @@ __global__ __launch_bounds__(DEC_SEL_NT) void decode_select_kernel(DecodeArgs a)
 
 // ------------------------------------------------------------------------------------------
 // attend: split s of query (h, i) sweeps slots [64 s, 64 s + 64); 16 lanes per slot, each lane
-// NPL rotation pairs; every 16-lane group keeps its own online-softmax state, merged in LDS
+// NPL rotation pairs; every 16-lane group keeps its own online-softmax state, merged in LDS.
+// A batch of many queries (the per-query prefill) gives each query fewer splits, down to one
+// workgroup sweeping all its slots in 64-slot steps and writing the output itself: the split
+// states and the merge kernel then cost nothing.
 // ------------------------------------------------------------------------------------------
-constexpr int DEC_SPL = 64;                    // slots per attend workgroup
+constexpr int DEC_SPL = 64;                    // slots per attend step
 
 int decode_nsplit(int k_max) { return (k_max + DEC_SPL - 1) / DEC_SPL; }
+// splits per query: the 64-slot steps of k_max for a single query, fewer as the batch grows
+// (a function of Q and k_max only, so that a query's output does not depend on the head count)
+static int decode_attend_splits(int Q, int k_max) {
+  const int want = (256 + Q - 1) / Q;
+  return max(1, min(decode_nsplit(k_max), want));
+}
 
 // (cos, sin) x rope_scale_c at every slot position 0 .. k_max - 1, computed exactly as the attend
 // computes a slot's rotation (fl(s * f), fast_sincos, one product each with rope_scale_c), so a
@@ -631,12 +640,12 @@ __global__ __launch_bounds__(256) void decode_rope_table_kernel(DecodeArgs a, fl
 
 // TAB: slot s's rotation comes from a.rope_table (the sets put slot s at position s)
 template <int DT, int D, bool TAB>
-__global__ __launch_bounds__(256) void decode_attend_kernel(DecodeArgs a) {
+__global__ __launch_bounds__(256) void decode_attend_kernel(DecodeArgs a, int steps) {
 #pragma clang fp contract(off)
   constexpr int NPL = D / 32;                  // pairs per lane
   __shared__ float sm_m[16], sm_l[16];
   __shared__ float sm_acc[16][D];
-  const int split = blockIdx.x, hi = blockIdx.y;
+  const int split = blockIdx.x, hi = blockIdx.y;   // split: `steps` 64-slot steps of the query
   const int h = hi / a.Q, i = hi % a.Q;
   const int hk = h / (a.H / a.Hkv);
   const int m = a.M - (a.Q - 1 - i);
@@ -645,7 +654,7 @@ __global__ __launch_bounds__(256) void decode_attend_kernel(DecodeArgs a) {
   const int l16 = lane & 15, grp = wave * 4 + (lane >> 4);
   const int d0 = l16 * NPL;                    // this lane's frequencies d0 .. d0 + NPL - 1
   const int nslots = a.set_size ? min(a.set_size[hi], a.k_max) : a.k_max;
-  const int s0 = split * DEC_SPL, s1 = min(s0 + DEC_SPL, nslots);
+  const int send = min(nslots, (split + 1) * steps * DEC_SPL);
   float invf[NPL];
 #pragma unroll
   for (int e = 0; e < NPL; ++e) invf[e] = a.inv_freq_c[d0 + e];
@@ -667,10 +676,16 @@ __global__ __launch_bounds__(256) void decode_attend_kernel(DecodeArgs a) {
       q2[e] = x2[e] * cs + x1[e] * sn;
     }
   }
-  // this group's four slots: indices first, then every K / V row request, then the arithmetic
   const int32_t* irow = a.idx + (int64_t)hi * a.k_max;
   const float* nrow = a.newpos_k + (int64_t)hi * a.k_max;
-  constexpr int U = DEC_SPL / 16;            // slots per group
+  constexpr int U = DEC_SPL / 16;            // slots per group and step
+  // the group's state over its steps: running max, sum and accumulators of the weights
+  float mrun = -INFINITY, lrun = 0.0f, acc1[NPL], acc2[NPL];
+#pragma unroll
+  for (int e = 0; e < NPL; ++e) { acc1[e] = 0.0f; acc2[e] = 0.0f; }
+  for (int s0 = split * steps * DEC_SPL; s0 < send; s0 += DEC_SPL) {
+  const int s1 = min(s0 + DEC_SPL, send);
+  // this group's four slots: indices first, then every K / V row request, then the arithmetic
   int jv[U];
   bool okv[U];
   float npk[U];
@@ -728,46 +743,72 @@ __global__ __launch_bounds__(256) void decode_attend_kernel(DecodeArgs a) {
     part += __shfl_xor(part, 8, 64);
     sc[u] = okv[u] ? part * a.sm_scale : -INFINITY;
   }
-  float mrun = -INFINITY;
+  // the step's own softmax state, then folded into the group's state (a first step is taken as
+  // it is, so that a one-step split is exactly the step's state)
+  float mst = -INFINITY;
 #pragma unroll
-  for (int u = 0; u < U; ++u) mrun = fmaxf(mrun, sc[u]);
-  float lrun = 0.0f, acc1[NPL], acc2[NPL];
+  for (int u = 0; u < U; ++u) mst = fmaxf(mst, sc[u]);
+  if (mst > -INFINITY) {
+    float lst = 0.0f, b1[NPL], b2[NPL];
 #pragma unroll
-  for (int e = 0; e < NPL; ++e) { acc1[e] = 0.0f; acc2[e] = 0.0f; }
-  if (mrun > -INFINITY) {
+    for (int e = 0; e < NPL; ++e) { b1[e] = 0.0f; b2[e] = 0.0f; }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const float pw = okv[u] ? __expf(sc[u] - mrun) : 0.0f;
-      lrun += pw;
+      const float pw = okv[u] ? __expf(sc[u] - mst) : 0.0f;
+      lst += pw;
 #pragma unroll
       for (int e = 0; e < NPL; ++e) {
-        acc1[e] = fmaf(pw, v1[u][e], acc1[e]);
-        acc2[e] = fmaf(pw, v2[u][e], acc2[e]);
+        b1[e] = fmaf(pw, v1[u][e], b1[e]);
+        b2[e] = fmaf(pw, v2[u][e], b2[e]);
       }
     }
+    if (mrun == -INFINITY) {
+      mrun = mst;
+      lrun = lst;
+#pragma unroll
+      for (int e = 0; e < NPL; ++e) { acc1[e] = b1[e]; acc2[e] = b2[e]; }
+    } else {
+      const float mn = fmaxf(mrun, mst);
+      const float wo = __expf(mrun - mn), wn = __expf(mst - mn);
+      lrun = lrun * wo + lst * wn;
+#pragma unroll
+      for (int e = 0; e < NPL; ++e) {
+        acc1[e] = acc1[e] * wo + b1[e] * wn;
+        acc2[e] = acc2[e] * wo + b2[e] * wn;
+      }
+      mrun = mn;
+    }
   }
+  }   // steps
   if (l16 == 0) { sm_m[grp] = mrun; sm_l[grp] = lrun; }
 #pragma unroll
   for (int e = 0; e < NPL; ++e) { sm_acc[grp][d0 + e] = acc1[e]; sm_acc[grp][D / 2 + d0 + e] = acc2[e]; }
   __syncthreads();
   // merge the 16 group states: (max, sum, D accumulators) of the split
-  float* part = a.part + ((int64_t)hi * gridDim.x + split) * (D + 2);
   float M = -INFINITY;
 #pragma unroll
   for (int u = 0; u < 16; ++u) M = fmaxf(M, sm_m[u]);
+  float L = 0.0f;
+  if (M > -INFINITY)
+    for (int u = 0; u < 16; ++u)
+      if (sm_m[u] > -INFINITY) L += sm_l[u] * __expf(sm_m[u] - M);
+  float* part = a.part + ((int64_t)hi * gridDim.x + split) * (D + 2);
   for (int d = threadIdx.x; d < D; d += 256) {
     float A = 0.0f;
     if (M > -INFINITY)
 #pragma unroll
       for (int u = 0; u < 16; ++u)
         if (sm_m[u] > -INFINITY) A += sm_acc[u][d] * __expf(sm_m[u] - M);
-    part[d] = A;
+    if (gridDim.x == 1) {     // the only split: the output (as the merge kernel writes it)
+      const float o = L > 0.0f ? A / L : 0.0f;
+      const int64_t oi = (int64_t)hi * D + d;
+      if constexpr (DT == DT_F32) ((float*)a.out)[oi] = o;
+      else ((uint16_t*)a.out)[oi] = (uint16_t)(DT == DT_BF16 ? f32_to_bf16_bits(o) : f32_to_f16_bits(o));
+    } else {
+      part[d] = A;
+    }
   }
-  if (threadIdx.x == 0) {
-    float L = 0.0f;
-    if (M > -INFINITY)
-      for (int u = 0; u < 16; ++u)
-        if (sm_m[u] > -INFINITY) L += sm_l[u] * __expf(sm_m[u] - M);
+  if (threadIdx.x == 0 && gridDim.x > 1) {
     part[D] = M;
     part[D + 1] = L;
   }
@@ -852,11 +893,14 @@ hipError_t launch_decode_select(const DecodeArgs& a, hipStream_t st) {
 
 template <int DT, int D>
 static hipError_t launch_attend_t(const DecodeArgs& a, hipStream_t st) {
-  const int ns = decode_nsplit(a.k_max);
-  if (ns > 256) return hipErrorInvalidValue;
-  if (a.rope_table) hipLaunchKernelGGL((decode_attend_kernel<DT, D, true>), dim3(ns, a.H * a.Q), dim3(256), 0, st, a);
-  else hipLaunchKernelGGL((decode_attend_kernel<DT, D, false>), dim3(ns, a.H * a.Q), dim3(256), 0, st, a);
-  hipLaunchKernelGGL((decode_combine_kernel<DT, D>), dim3(a.H * a.Q), dim3(256), 0, st, a, ns);
+  const int nmax = decode_nsplit(a.k_max);
+  if (nmax > 256) return hipErrorInvalidValue;
+  const int ns = decode_attend_splits(a.Q, a.k_max);
+  const int steps = (nmax + ns - 1) / ns;
+  const int ng = (nmax + steps - 1) / steps;     // splits that hold slots
+  if (a.rope_table) hipLaunchKernelGGL((decode_attend_kernel<DT, D, true>), dim3(ng, a.H * a.Q), dim3(256), 0, st, a, steps);
+  else hipLaunchKernelGGL((decode_attend_kernel<DT, D, false>), dim3(ng, a.H * a.Q), dim3(256), 0, st, a, steps);
+  if (ng > 1) hipLaunchKernelGGL((decode_combine_kernel<DT, D>), dim3(a.H * a.Q), dim3(256), 0, st, a, ng);
   return hipGetLastError();
 }
 
