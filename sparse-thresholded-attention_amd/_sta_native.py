@@ -1217,12 +1217,19 @@ class PerQueryPrefillPlan:
     the per-query score rows (heads x N x N fp32) stay bounded; outputs and one workspace are
     allocated once and run() allocates nothing.
 
+    The prompt runs in chunks of query_chunk positions: chunk [i0, i1) is a decode batch of
+    i1 - i0 queries at positions i0 .. over the cache prefix [0, i1), so a chunk's selection
+    workgroups size their key store by i1 rather than N (two of them fit a CU where one of N keys
+    did) and its score rows take (i1 - i0) x i1 floats per head.  A query's scores, set and output
+    do not depend on the chunking.  query_chunk=None runs the prompt as one batch.
+
     Outputs: out (H, N, D) in the input dtype; set_size, usize (H, N) int32 and overflow (H, N)
-    bool per query.  The per-group idx / newpos buffers are reused from group to group."""
+    bool per query.  The per-launch idx / newpos buffers are reused; a chunk's per-query outputs
+    land in staging buffers and are copied into place on the same stream."""
 
     def __init__(self, q, k, v, tau, inv_freq_a, inv_freq_c, pos_scale_a=1.0, rope_scale_a=1.0,
                  sm_scale=None, n_global=32, n_local=32, k_max=4096, heads_per_group=None,
-                 score_bytes_budget=2 << 30):
+                 score_bytes_budget=2 << 30, query_chunk=2048):
         qh = _heads_view(q)
         kh = _heads_view(k.to(qh.device))
         vh = _heads_view(v.to(qh.device))
@@ -1230,9 +1237,11 @@ class PerQueryPrefillPlan:
         Hkv = kh.shape[0]
         G = H // Hkv
         dev = qh.device
+        qc = N if query_chunk is None else max(1, min(int(query_chunk), N))
+        chunks = [(i0, min(N, i0 + qc)) for i0 in range(0, N, qc)]
         if heads_per_group is None:
-            # whole kv groups, as many as the score budget allows
-            per_head = N * N * 4
+            # whole kv groups, as many as the score budget allows for the largest chunk
+            per_head = qc * N * 4
             heads_per_group = max(G, (score_bytes_budget // per_head) // G * G)
         hg = min(H, heads_per_group)
         if hg % G:
@@ -1249,42 +1258,52 @@ class PerQueryPrefillPlan:
             "usize": torch.empty((H, N), dtype=torch.int32, device=dev),
             "overflow": torch.empty((H, N), dtype=torch.bool, device=dev),
         }
-        self._idx = torch.empty((hg, N, k_max), dtype=torch.int32, device=dev)
-        self._npk = torch.empty((hg, N, k_max), dtype=torch.float32, device=dev)
-        self._npq = torch.empty((hg, N), dtype=torch.float32, device=dev)
+        self._idx = torch.empty((hg, qc, k_max), dtype=torch.int32, device=dev)
+        self._npk = torch.empty((hg, qc, k_max), dtype=torch.float32, device=dev)
+        self._npq = torch.empty((hg, qc), dtype=torch.float32, device=dev)
+        whole = len(chunks) == 1
+        if not whole:   # a chunk's (heads, queries) outputs are not a contiguous slice of (H, N)
+            self._stage = {"out": torch.empty((hg, qc, D), dtype=qh.dtype, device=dev),
+                           "set_size": torch.empty((hg, qc), dtype=torch.int32, device=dev),
+                           "usize": torch.empty((hg, qc), dtype=torch.int32, device=dev),
+                           "overflow": torch.empty((hg, qc), dtype=torch.bool, device=dev)}
         self._keep = (qh, kh, vh, tau)
         self.plans = []
+        self._spans = []       # (h0, h1, i0, i1) of each plan
         ws = None
-        for h0 in range(0, H, hg):
-            h1 = min(H, h0 + hg)
-            p = DecodePlan.__new__(DecodePlan)
-            p.device = dev
-            p._events = None
-            a = p.args = DecodeArgsC()
-            a.q, a.k, a.v = _ptr(qh[h0:h1]), _ptr(kh[h0 // G:h1 // G]), _ptr(vh[h0 // G:h1 // G])
-            a.q_head_stride, a.q_tok_stride = qh.stride(0), qh.stride(1)
-            a.k_head_stride, a.k_tok_stride = kh.stride(0), kh.stride(1)
-            a.v_head_stride, a.v_tok_stride = vh.stride(0), vh.stride(1)
-            a.dtype = DTYPES[qh.dtype]
-            a.H, a.Hkv, a.Q, a.M, a.D = h1 - h0, (h1 - h0) // G, N, N, D
-            a.tau = _ptr(tau[h0:h1])
-            a.inv_freq_a = _ptr(inv_freq_a)
-            a.inv_freq_c = _ptr(inv_freq_c)
-            a.pos_scale_a, a.rope_scale_a, a.sm_scale = float(pos_scale_a), float(rope_scale_a), float(sm_scale)
-            a.pos_scale_c, a.rope_scale_c = 1.0, 1.0
-            a.q_pos0, a.n_global, a.n_local, a.k_max = 0, int(n_global), int(n_local), int(k_max)
-            a.pct_decode, a.causal, a.rule = 100.0, 0, RULES["pq"]
-            a.out = _ptr(self.out["out"][h0:h1])
-            a.idx, a.newpos_k, a.newpos_q = _ptr(self._idx), _ptr(self._npk), _ptr(self._npq)
-            a.set_size = _ptr(self.out["set_size"][h0:h1])
-            a.usize = _ptr(self.out["usize"][h0:h1])
-            a.overflow = _ptr(self.out["overflow"][h0:h1])
-            n = lib().sta_decode_workspace_size(ctypes.byref(a))
-            if n == 0:
-                _check(-1, "sta_decode_workspace_size")
-            if ws is None or ws.numel() < n:
-                ws = torch.empty(n, dtype=torch.uint8, device=dev)
-            self.plans.append(p)
+        for i0, i1 in chunks:
+            for h0 in range(0, H, hg):
+                h1 = min(H, h0 + hg)
+                p = DecodePlan.__new__(DecodePlan)
+                p.device = dev
+                p._events = None
+                a = p.args = DecodeArgsC()
+                a.q = _ptr(qh[h0:h1, i0:])
+                a.k, a.v = _ptr(kh[h0 // G:h1 // G]), _ptr(vh[h0 // G:h1 // G])
+                a.q_head_stride, a.q_tok_stride = qh.stride(0), qh.stride(1)
+                a.k_head_stride, a.k_tok_stride = kh.stride(0), kh.stride(1)
+                a.v_head_stride, a.v_tok_stride = vh.stride(0), vh.stride(1)
+                a.dtype = DTYPES[qh.dtype]
+                a.H, a.Hkv, a.Q, a.M, a.D = h1 - h0, (h1 - h0) // G, i1 - i0, i1, D
+                a.tau = _ptr(tau[h0:h1])
+                a.inv_freq_a = _ptr(inv_freq_a)
+                a.inv_freq_c = _ptr(inv_freq_c)
+                a.pos_scale_a, a.rope_scale_a, a.sm_scale = float(pos_scale_a), float(rope_scale_a), float(sm_scale)
+                a.pos_scale_c, a.rope_scale_c = 1.0, 1.0
+                a.q_pos0, a.n_global, a.n_local, a.k_max = i0, int(n_global), int(n_local), int(k_max)
+                a.pct_decode, a.causal, a.rule = 100.0, 0, RULES["pq"]
+                dst = self.out if whole else self._stage
+                a.out = _ptr(dst["out"][h0:h1] if whole else dst["out"])
+                a.idx, a.newpos_k, a.newpos_q = _ptr(self._idx), _ptr(self._npk), _ptr(self._npq)
+                for name in ("set_size", "usize", "overflow"):
+                    setattr(a, name, _ptr(dst[name][h0:h1] if whole else dst[name]))
+                n = lib().sta_decode_workspace_size(ctypes.byref(a))
+                if n == 0:
+                    _check(-1, "sta_decode_workspace_size")
+                if ws is None or ws.numel() < n:
+                    ws = torch.empty(n, dtype=torch.uint8, device=dev)
+                self.plans.append(p)
+                self._spans.append((h0, h1, i0, i1))
         for p in self.plans:
             p.args.workspace, p.args.workspace_bytes = _ptr(ws), ws.numel()
         self.workspace = ws
@@ -1293,19 +1312,25 @@ class PerQueryPrefillPlan:
     def run(self, events=None):
         """events: None or one list of 4 recorded events per head group (len(self.plans)),
         marking that group's scores, selection and attend."""
+        staged = hasattr(self, "_stage")
         for i, p in enumerate(self.plans):
             p.args.stage_events = None
             if events is not None:
                 p._events = (ctypes.c_void_p * 4)(*[e.cuda_event for e in events[i]])
                 p.args.stage_events = ctypes.cast(p._events, ctypes.c_void_p)
             _check(lib().sta_decode_attention(ctypes.byref(p.args), _stream(self.device)), "sta_decode_attention")
+            if staged:
+                h0, h1, i0, i1 = self._spans[i]
+                for name, t in self._stage.items():
+                    self.out[name][h0:h1, i0:i1].copy_(t[:h1 - h0, :i1 - i0])
         return self.out
 
 
 def perquery_prefill_attention(q, k, v, tau, inv_freq_a, inv_freq_c, pos_scale_a=1.0, rope_scale_a=1.0,
-                               sm_scale=None, n_global=32, n_local=32, k_max=4096, heads_per_group=None):
+                               sm_scale=None, n_global=32, n_local=32, k_max=4096, heads_per_group=None,
+                               query_chunk=2048):
     """Per-query prefill of (1, H, N, D) inputs; returns the PerQueryPrefillPlan's outputs."""
     ia = inv_freq_a.to(device=q.device, dtype=torch.float32).contiguous()
     ic = inv_freq_c.to(device=q.device, dtype=torch.float32).contiguous()
     return PerQueryPrefillPlan(q, k, v, tau, ia, ic, pos_scale_a, rope_scale_a, sm_scale, n_global, n_local,
-                               k_max, heads_per_group).run()
+                               k_max, heads_per_group, query_chunk=query_chunk).run()

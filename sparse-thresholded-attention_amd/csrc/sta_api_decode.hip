@@ -18,7 +18,7 @@ struct DecLayout {
   int nsplit;
   bool rows;                                          // scores through the fragments
   int q_rows_pad, k_rows_pad;
-  size_t qrot_off, scores_off, keys_off, size_off, part_off, qfrag_off, kfrag_off, rtab_off, total;
+  size_t qrot_off, scores_off, keys_off, size_off, part_off, qfrag_off, kfrag_off, total;
 };
 
 DecLayout dec_layout_of(const sta_decode_args* a) {
@@ -45,8 +45,6 @@ DecLayout dec_layout_of(const sta_decode_args* a) {
     L.kfrag_off = off;
     off = align256(off + frag_region_bytes(a->Hkv, L.k_rows_pad, a->D));
   }
-  L.rtab_off = off;                                   // slot rotations of dense-rank sets (per-query rule)
-  if (a->rule == STA_RULE_PQ) off = align256(off + (size_t)a->k_max * (a->D / 2) * 8);
   L.total = off;
   return L;
 }
@@ -286,14 +284,6 @@ int sta_decode_attention(const sta_decode_args* a, void* stream) {
   if ((rc = mark_event(a->stage_events, 1, st)) != STA_OK) return rc;
   if ((rc = dec_select(a, d, d.scores, st)) != STA_OK) return rc;
   if ((rc = mark_event(a->stage_events, 2, st)) != STA_OK) return rc;
-  if (a->rule == STA_RULE_PQ) {
-    // the per-query rule puts slot s at position s (perquery.py:707): the attend reads each
-    // slot's rotation from a table of the k_max positions instead of computing it per query
-    float2* table = (float2*)((char*)a->workspace + L.rtab_off);
-    hipError_t e = launch_decode_rope_table(a->D, d, table, st);
-    if (e != hipSuccess) return hip_fail(e, "decode slot rotation table");
-    d.rope_table = table;
-  }
   if ((rc = dec_attend(a, d, st)) != STA_OK) return rc;
   return mark_event(a->stage_events, 3, st);
 }

@@ -624,22 +624,7 @@ static int decode_attend_splits(int Q, int k_max) {
   return max(1, min(decode_nsplit(k_max), want));
 }
 
-// (cos, sin) x rope_scale_c at every slot position 0 .. k_max - 1, computed exactly as the attend
-// computes a slot's rotation (fl(s * f), fast_sincos, one product each with rope_scale_c), so a
-// table read equals the attend's own value bit for bit
-template <int D>
-__global__ __launch_bounds__(256) void decode_rope_table_kernel(DecodeArgs a, float2* table) {
-#pragma clang fp contract(off)
-  const int64_t x = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (x >= (int64_t)a.k_max * (D / 2)) return;
-  const int s = (int)(x / (D / 2)), f = (int)(x % (D / 2));
-  float sn, cs;
-  fast_sincos((float)s * a.inv_freq_c[f], sn, cs);
-  table[x] = make_float2(cs * a.rope_scale_c, sn * a.rope_scale_c);
-}
-
-// TAB: slot s's rotation comes from a.rope_table (the sets put slot s at position s)
-template <int DT, int D, bool TAB>
+template <int DT, int D>
 __global__ __launch_bounds__(256) void decode_attend_kernel(DecodeArgs a, int steps) {
 #pragma clang fp contract(off)
   constexpr int NPL = D / 32;                  // pairs per lane
@@ -698,19 +683,8 @@ __global__ __launch_bounds__(256) void decode_attend_kernel(DecodeArgs a, int st
     npk[u] = s < s1 ? nrow[s] : 0.0f;
   }
   float x1[U][NPL], x2[U][NPL], v1[U][NPL], v2[U][NPL];
-  float2 tcs[TAB ? U : 1][NPL];
 #pragma unroll
   for (int u = 0; u < U; ++u) {
-    if constexpr (TAB) {
-      const int s = min(s0 + grp * U + u, a.k_max - 1);   // slots past the set are masked
-      const float4* tr = (const float4*)(a.rope_table + (int64_t)s * (D / 2) + d0);
-#pragma unroll
-      for (int e = 0; e < NPL; e += 2) {
-        const float4 t = tr[e / 2];
-        tcs[u][e] = make_float2(t.x, t.y);
-        tcs[u][e + 1] = make_float2(t.z, t.w);
-      }
-    }
     const int64_t kb = (int64_t)hk * a.k_hs + (int64_t)jv[u] * a.k_ts + d0;
     const int64_t vb = (int64_t)hk * a.v_hs + (int64_t)jv[u] * a.v_ts + d0;
     load_n<DT, NPL>(a.k, kb, x1[u]);
@@ -725,14 +699,9 @@ __global__ __launch_bounds__(256) void decode_attend_kernel(DecodeArgs a, int st
 #pragma unroll
     for (int e = 0; e < NPL; ++e) {
       float sn, cs;
-      if constexpr (TAB) {
-        cs = tcs[u][e].x;
-        sn = tcs[u][e].y;
-      } else {
-        fast_sincos(npk[u] * invf[e], sn, cs);
-        cs = cs * a.rope_scale_c;
-        sn = sn * a.rope_scale_c;
-      }
+      fast_sincos(npk[u] * invf[e], sn, cs);
+      cs = cs * a.rope_scale_c;
+      sn = sn * a.rope_scale_c;
       const float k1 = x1[u][e] * cs - x2[u][e] * sn;
       const float k2 = x2[u][e] * cs + x1[u][e] * sn;
       part = fmaf(q2[e], k2, fmaf(q1[e], k1, part));
@@ -898,18 +867,8 @@ static hipError_t launch_attend_t(const DecodeArgs& a, hipStream_t st) {
   const int ns = decode_attend_splits(a.Q, a.k_max);
   const int steps = (nmax + ns - 1) / ns;
   const int ng = (nmax + steps - 1) / steps;     // splits that hold slots
-  if (a.rope_table) hipLaunchKernelGGL((decode_attend_kernel<DT, D, true>), dim3(ng, a.H * a.Q), dim3(256), 0, st, a, steps);
-  else hipLaunchKernelGGL((decode_attend_kernel<DT, D, false>), dim3(ng, a.H * a.Q), dim3(256), 0, st, a, steps);
+  hipLaunchKernelGGL((decode_attend_kernel<DT, D>), dim3(ng, a.H * a.Q), dim3(256), 0, st, a, steps);
   if (ng > 1) hipLaunchKernelGGL((decode_combine_kernel<DT, D>), dim3(a.H * a.Q), dim3(256), 0, st, a, ng);
-  return hipGetLastError();
-}
-
-hipError_t launch_decode_rope_table(int D, const DecodeArgs& a, float2* table, hipStream_t st) {
-  const int64_t n = (int64_t)a.k_max * (D / 2);
-  const dim3 grid((unsigned)((n + 255) / 256));
-  if (D == 64) hipLaunchKernelGGL(decode_rope_table_kernel<64>, grid, dim3(256), 0, st, a, table);
-  else if (D == 128) hipLaunchKernelGGL(decode_rope_table_kernel<128>, grid, dim3(256), 0, st, a, table);
-  else return hipErrorInvalidValue;
   return hipGetLastError();
 }
 

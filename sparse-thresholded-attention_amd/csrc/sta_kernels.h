@@ -267,8 +267,6 @@ struct DecodeArgs {
   int block_n;            // rule 2: the position blocks
   int32_t* usize;         // (H, Q) or null: rule 1, |threshold passers|
   uint8_t* overflow;      // (H, Q) or null: rule 1, passers U forced above k_max
-  const float2* rope_table;  // (k_max, D/2) or null: slot s's (cos, sin) x rope_scale_c at
-                             // position s, for sets whose slot s sits at position s (rule 1)
 };
 
 // scores of a batch of queries from the RoPE pre-kernel's fragments (matrix cores)
@@ -289,9 +287,6 @@ size_t decode_keys_bytes(int H, int Q, int M);
 hipError_t launch_decode_select(const DecodeArgs& a, hipStream_t st);
 int decode_nsplit(int k_max);
 hipError_t launch_decode_attend(int dtype, int D, const DecodeArgs& a, hipStream_t st);
-// the attend's slot rotations for dense-rank positions: table[s][f] = (cos, sin)(fl(s * inv_freq_c[f]))
-// x rope_scale_c, with the attend's own sin / cos (s < k_max)
-hipError_t launch_decode_rope_table(int D, const DecodeArgs& a, float2* table, hipStream_t st);
 
 hipError_t launch_rope_frag(int dtype, int D, const void* x, int64_t head_stride, int64_t tok_stride,
                             int heads, int N, int rows_pad, int pos_base, float pos_scale,

@@ -257,30 +257,3 @@ def test_perquery_full_prefill_plan_config3_structure():
         e = (d["out"][0, 0].float() - r["out"][h, rr].float()).abs().max().item()
         assert e <= 2e-2, (rr, e)
 
-
-@pytest.mark.parametrize("dt,D,Q,k_max,rsc", [(torch.bfloat16, 128, 300, 256, 1.0), (torch.float32, 64, 1, 512, 1.1),
-                                              (torch.float16, 128, 96, 2048, 0.9)])
-def test_perquery_slot_table_matches_per_slot_rotation(dt, D, Q, k_max, rsc):
-    """Under the per-query rule slot s sits at position s, and the combined decode entry reads each
-    slot's rotation from a table of the k_max positions built with the attend's own sin / cos: its
-    output equals, bit for bit, the attend alone over the same sets, which rotates every slot at
-    its newpos_k."""
-    import _sta_native as native
-    from synthetic import base_inv_freq, planted_inputs
-    H, Hkv, M = 4, 2, 1200
-    say(f"slot table, {dt} D={D} Q={Q} k_max={k_max} rope_scale_c={rsc}")
-    q, k, v = planted_inputs(71, H, Hkv, M, D, 0.02, dt, DEV)
-    invf = base_inv_freq(D, 10000.0).to(DEV)
-    tau = torch.full((H,), 3.0, device=DEV)
-    p = native.DecodePlan(q[0, :, M - Q:], k[0], v[0], tau, invf, M - Q, 0.5, 1.0, None, 16, 16, k_max,
-                          inv_freq_c=invf, pos_scale_c=1.0, rope_scale_c=rsc, rule="pq")
-    r = p.run()
-    torch.cuda.synchronize()
-    out_tab = r["out"].clone()
-    assert int(r["set_size"].min().item()) > 0
-    ranks = torch.arange(k_max, device=DEV, dtype=torch.float32).expand_as(r["newpos_k"])
-    live = torch.arange(k_max, device=DEV)[None, None, :] < r["set_size"][..., None]
-    assert torch.equal(torch.where(live, r["newpos_k"], ranks), ranks)   # dense ranks
-    out_rot = p.attend(r["idx"], r["newpos_k"], r["newpos_q"], r["set_size"])
-    torch.cuda.synchronize()
-    assert torch.equal(out_tab, out_rot)
