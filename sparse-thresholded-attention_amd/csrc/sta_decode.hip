@@ -226,11 +226,11 @@ __global__ __launch_bounds__(256) void decode_score_kernel(DecodeArgs a) {
 // ------------------------------------------------------------------------------------------
 // _decode_build_sets for one query per workgroup
 // ------------------------------------------------------------------------------------------
-constexpr int DEC_SEL_NT = 1024;             // threads of a selection workgroup
-constexpr int DEC_SEL_NW = DEC_SEL_NT / 64;
+constexpr int DEC_SEL_NT = 1024;             // threads of the workspace-sizing selection instance
 
 namespace {
 
+template <int NW>
 __device__ __forceinline__ int dsum(int v, int* tmp) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
 #pragma unroll
@@ -239,11 +239,12 @@ __device__ __forceinline__ int dsum(int v, int* tmp) {
   __syncthreads();
   int total = 0;
 #pragma unroll
-  for (int w = 0; w < DEC_SEL_NW; ++w) total += tmp[w];
+  for (int w = 0; w < NW; ++w) total += tmp[w];
   __syncthreads();
   return total;
 }
 
+template <int NW>
 __device__ __forceinline__ uint32_t dmax_u(uint32_t v, uint32_t* tmp) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
 #pragma unroll
@@ -252,12 +253,13 @@ __device__ __forceinline__ uint32_t dmax_u(uint32_t v, uint32_t* tmp) {
   __syncthreads();
   uint32_t r = 0;
 #pragma unroll
-  for (int w = 0; w < DEC_SEL_NW; ++w) r = max(r, tmp[w]);
+  for (int w = 0; w < NW; ++w) r = max(r, tmp[w]);
   __syncthreads();
   return r;
 }
 
 // exclusive prefix sum over the block's threads; *total (optional) receives the block sum
+template <int NW>
 __device__ __forceinline__ int dexcl_sum(int v, int* tmp, int* total = nullptr) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   int x = v;
@@ -270,7 +272,7 @@ __device__ __forceinline__ int dexcl_sum(int v, int* tmp, int* total = nullptr) 
   __syncthreads();
   int base = 0, all = 0;
 #pragma unroll
-  for (int w = 0; w < DEC_SEL_NW; ++w) {
+  for (int w = 0; w < NW; ++w) {
     base += w < wave ? tmp[w] : 0;
     all += tmp[w];
   }
@@ -279,6 +281,7 @@ __device__ __forceinline__ int dexcl_sum(int v, int* tmp, int* total = nullptr) 
   return base + x - v;
 }
 
+template <int NW>
 __device__ __forceinline__ float dexcl_max(float v, float* tmp) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   float x = v;
@@ -301,15 +304,11 @@ __device__ __forceinline__ float dexcl_max(float v, float* tmp) {
 
 // Keys of the LDS store: per thread a contiguous range of `per` keys at the odd row stride
 // per | 1 (conflict-free scans); the global store (caches too long for LDS) uses stride per.
-constexpr int DEC_CAND = 512;                // keys of a bin ranked directly
+constexpr int DEC_CAND = 128;                // keys of a bin ranked directly
 constexpr size_t DEC_AUX = 4096 * 4 + DEC_SEL_NT * 4 + 256;   // histogram, candidates, scratch
 bool decode_select_in_lds(int M) {   // the CU's 160 KB: M <= 33792
   const int per = (M + DEC_SEL_NT - 1) / DEC_SEL_NT;
   return (size_t)DEC_SEL_NT * (per | 1) * 4 + DEC_AUX <= 160 * 1024;
-}
-size_t decode_select_lds_bytes(int M) {
-  const int per = (M + DEC_SEL_NT - 1) / DEC_SEL_NT;
-  return (decode_select_in_lds(M) ? (size_t)DEC_SEL_NT * (per | 1) * 4 : 0) + DEC_AUX;
 }
 size_t decode_keys_bytes(int H, int Q, int M) {
   if (decode_select_in_lds(M)) return 0;
@@ -317,23 +316,25 @@ size_t decode_keys_bytes(int H, int Q, int M) {
   return (size_t)H * Q * DEC_SEL_NT * per * 4;
 }
 
-template <bool GKEYS>
-__global__ __launch_bounds__(DEC_SEL_NT) void decode_select_kernel(DecodeArgs a) {
+// NT threads per query: 1024 for a few queries (latency), 512 for large batches (throughput)
+template <bool GKEYS, int NT>
+__global__ __launch_bounds__(NT) void decode_select_kernel(DecodeArgs a) {
 #pragma clang fp contract(off)
+  constexpr int NW = NT / 64;
   extern __shared__ __align__(16) uint32_t dsm[];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x;
   const int hi = blockIdx.x;
   const int h = hi / a.Q, i = hi % a.Q;
   const int m = a.M - (a.Q - 1 - i);           // keys this query sees
   const int p = a.q_pos0 + i;                  // its position (p < m)
-  const int per_max = (a.M + DEC_SEL_NT - 1) / DEC_SEL_NT;
-  const int per = (m + DEC_SEL_NT - 1) / DEC_SEL_NT;
+  const int per_max = (a.M + NT - 1) / NT;
+  const int per = (m + NT - 1) / NT;
   const int PS = GKEYS ? per : (per | 1);
-  uint32_t* ks = GKEYS ? a.keys + (int64_t)hi * DEC_SEL_NT * per_max : dsm;
-  int* hist = (int*)(dsm + (GKEYS ? 0 : DEC_SEL_NT * (per_max | 1)));   // 4096
-  uint32_t* cand = (uint32_t*)(hist + 4096);   // DEC_SEL_NT (16-byte aligned)
-  int* tmp = (int*)(cand + DEC_SEL_NT);        // DEC_SEL_NW
-  int* misc = tmp + DEC_SEL_NW;                // 8
+  uint32_t* ks = GKEYS ? a.keys + (int64_t)hi * NT * per_max : dsm;
+  int* hist = (int*)(dsm + (GKEYS ? 0 : NT * (per_max | 1)));   // 4096
+  uint32_t* cand = (uint32_t*)(hist + 4096);   // NT (16-byte aligned)
+  int* tmp = (int*)(cand + NT);        // NW
+  int* misc = tmp + NW;                // 8
   const int j0 = tid * per, j1 = min(j0 + per, m);
   uint32_t* myrow = ks + tid * PS;
   const float* srow = a.scores + (int64_t)hi * a.M;
@@ -346,12 +347,12 @@ __global__ __launch_bounds__(DEC_SEL_NT) void decode_select_kernel(DecodeArgs a)
     float sv[8];
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
-      const int j = tid + (e0 + u) * DEC_SEL_NT;
+      const int j = tid + (e0 + u) * NT;
       sv[u] = (e0 + u < per && j < m) ? srow[j] : 0.0f;
     }
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
-      const int j = tid + (e0 + u) * DEC_SEL_NT;
+      const int j = tid + (e0 + u) * NT;
       if (e0 + u < per) {
         const uint32_t key = j < m ? okey(sv[u]) : 0u;
         kmax = max(kmax, key);
@@ -360,7 +361,7 @@ __global__ __launch_bounds__(DEC_SEL_NT) void decode_select_kernel(DecodeArgs a)
       }
     }
   }
-  kmax = dmax_u(kmax, (uint32_t*)tmp);         // the barrier inside also publishes the stores
+  kmax = dmax_u<NW>(kmax, (uint32_t*)tmp);         // the barrier inside also publishes the stores
   const float thr = okey_value(kmax) - tau_h;                          // exact_2.py:550
   const uint32_t kthr = okey(thr);
 
@@ -380,7 +381,7 @@ __global__ __launch_bounds__(DEC_SEL_NT) void decode_select_kernel(DecodeArgs a)
     for (int lv = 0; lv < 3; ++lv) {
       const int shift = lv == 0 ? 20 : (lv == 1 ? 8 : 0);
       const int nb = lv == 2 ? 256 : 4096;
-      for (int b = tid; b < nb; b += DEC_SEL_NT) hist[b] = 0;
+      for (int b = tid; b < nb; b += NT) hist[b] = 0;
       cand[tid] = 0u;                          // 0 ranks below every key
       if (tid == 0) misc[4] = 0;
       __syncthreads();
@@ -389,15 +390,16 @@ __global__ __launch_bounds__(DEC_SEL_NT) void decode_select_kernel(DecodeArgs a)
         if (k != 0 && j0 + e < m && (k & pmask) == prefix) atomicAdd(&hist[(k >> shift) & (uint32_t)(nb - 1)], 1);
       }
       __syncthreads();
-      // bins in descending order, four per thread
-      const bool own = 4 * tid < nb;
-      int c[4], sl = 0;
+      // bins in descending order, BPT per thread
+      constexpr int BPT = 4096 / NT;
+      const bool own = BPT * tid < nb;
+      int c[BPT], sl = 0;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) { c[e] = own ? hist[nb - 1 - 4 * tid - e] : 0; sl += c[e]; }
-      const int excl = dexcl_sum(sl, tmp);
+      for (int e = 0; e < BPT; ++e) { c[e] = own ? hist[nb - 1 - BPT * tid - e] : 0; sl += c[e]; }
+      const int excl = dexcl_sum<NW>(sl, tmp);
       if (own && excl < need && excl + sl >= need) {
-        int acc = excl, d = nb - 1 - 4 * tid, e = 0;
-        for (; e < 3; ++e) {
+        int acc = excl, d = nb - 1 - BPT * tid, e = 0;
+        for (; e < BPT - 1; ++e) {
           if (acc + c[e] >= need) break;
           acc += c[e];
           d -= 1;
@@ -459,7 +461,7 @@ __global__ __launch_bounds__(DEC_SEL_NT) void decode_select_kernel(DecodeArgs a)
   if (a.use_pct) {
     int c = 0;
     for (int e = 0; e < j1 - j0; ++e) c += myrow[e] >= kthr;
-    const int n_pass = dsum(c, tmp);
+    const int n_pass = dsum<NW>(c, tmp);
     const float prod = a.pct_frac * (float)n_pass;                       // exact_2.py:561
     float b = ceilf(prod);
     if (b < 1.0f) b = 1.0f;
@@ -470,17 +472,17 @@ __global__ __launch_bounds__(DEC_SEL_NT) void decode_select_kernel(DecodeArgs a)
     if (kp_thr != r.x) {                                                 // (only when need > n_pass)
       int c2 = 0;
       for (int e = 0; e < j1 - j0; ++e) c2 += myrow[e] >= kp_thr;
-      ge = dsum(c2, tmp);
+      ge = dsum<NW>(c2, tmp);
     }
   } else {
     int c = 0;
     for (int e = 0; e < j1 - j0; ++e) c += myrow[e] >= kp_thr;
-    ge = dsum(c, tmp);
+    ge = dsum<NW>(c, tmp);
   }
   {
     int c = 0;
-    for (int f = tid; f < nforced; f += DEC_SEL_NT) c += key_of(forced_j(f)) < kp_thr;
-    count = ge + dsum(c, tmp);
+    for (int f = tid; f < nforced; f += NT) c += key_of(forced_j(f)) < kp_thr;
+    count = ge + dsum<NW>(c, tmp);
   }
 
   // the per-query rule's measurement counters: |passers| and the overflow flag (perquery.py:686-688)
@@ -506,7 +508,7 @@ __global__ __launch_bounds__(DEC_SEL_NT) void decode_select_kernel(DecodeArgs a)
     } else {
       // the non-forced kept keys are the non-forced keys >= kp_thr and they outnumber budget_c,
       // so the budget_c-th largest non-forced key is the reference's cut
-      for (int f = tid; f < nforced; f += DEC_SEL_NT) {
+      for (int f = tid; f < nforced; f += NT) {
         const int j = forced_j(f);
         const int row = j / per;
         ks[row * PS + (j - row * per)] = 0u;
@@ -519,8 +521,8 @@ __global__ __launch_bounds__(DEC_SEL_NT) void decode_select_kernel(DecodeArgs a)
           c += myrow[e] > fin_thr;
           t += myrow[e] == fin_thr;
         }
-        quota = budget_c - dsum(c, tmp);
-        tie_base = dexcl_sum(t, tmp);
+        quota = budget_c - dsum<NW>(c, tmp);
+        tie_base = dexcl_sum<NW>(t, tmp);
         exact_cut = true;
       }
     }
@@ -541,7 +543,7 @@ __global__ __launch_bounds__(DEC_SEL_NT) void decode_select_kernel(DecodeArgs a)
     for (int e = 0; e < j1 - j0; ++e) cnt += final_j(j0 + e, myrow[e], tie);
   }
   int total;
-  const int base = dexcl_sum(cnt, tmp, &total);
+  const int base = dexcl_sum<NW>(cnt, tmp, &total);
   float mloc = -INFINITY;
   if (!pq) {
     int rank = base - 1, tie = tie_base;
@@ -553,7 +555,7 @@ __global__ __launch_bounds__(DEC_SEL_NT) void decode_select_kernel(DecodeArgs a)
       }
     }
   }
-  float run = pq ? 0.0f : dexcl_max(mloc, (float*)tmp);
+  float run = pq ? 0.0f : dexcl_max<NW>(mloc, (float*)tmp);
   int32_t* irow = a.idx + (int64_t)hi * a.k_max;
   float* nrow = a.newpos_k + (int64_t)hi * a.k_max;
   // PQ Stream's positions (pqstream_kernel.py:736-749): aligned blocks of block_n keys walked
@@ -600,7 +602,7 @@ __global__ __launch_bounds__(DEC_SEL_NT) void decode_select_kernel(DecodeArgs a)
       if (j == p) a.newpos_q[hi] = stream ? 0.0f : np;                   // :603; pqstream :770
     }
   }
-  for (int s = min(total, a.k_max) + tid; s < a.k_max; s += DEC_SEL_NT) {   // sentinel m (:594-600)
+  for (int s = min(total, a.k_max) + tid; s < a.k_max; s += NT) {   // sentinel m (:594-600)
     irow[s] = m;
     nrow[s] = 0.0f;
   }
@@ -846,18 +848,29 @@ hipError_t launch_decode_scores(int dtype, int D, const DecodeArgs& a, float* qr
   return hipErrorInvalidValue;
 }
 
-hipError_t launch_decode_select(const DecodeArgs& a, hipStream_t st) {
-  const size_t lds = decode_select_lds_bytes(a.M);
-  if (decode_select_in_lds(a.M)) {
-    hipError_t e = hipFuncSetAttribute((const void*)decode_select_kernel<false>,
+template <int NT>
+static hipError_t launch_select_t(const DecodeArgs& a, hipStream_t st) {
+  const int per = (a.M + NT - 1) / NT;
+  const bool in_lds = decode_select_in_lds(a.M);   // (the 1024-thread bound covers 512 threads)
+  const size_t lds = (in_lds ? (size_t)NT * (per | 1) * 4 : 0) + 4096 * 4 + NT * 4 + 256;
+  if (in_lds) {
+    hipError_t e = hipFuncSetAttribute((const void*)decode_select_kernel<false, NT>,
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(decode_select_kernel<false>, dim3(a.H * a.Q), dim3(DEC_SEL_NT), lds, st, a);
+    hipLaunchKernelGGL((decode_select_kernel<false, NT>), dim3(a.H * a.Q), dim3(NT), lds, st, a);
   } else {
-    if (!a.keys) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(decode_select_kernel<true>, dim3(a.H * a.Q), dim3(DEC_SEL_NT), lds, st, a);
+    if (!a.keys) return hipErrorInvalidValue;   // decode_keys_bytes (1024 threads) bounds NT * per
+    hipLaunchKernelGGL((decode_select_kernel<true, NT>), dim3(a.H * a.Q), dim3(NT), lds, st, a);
   }
   return hipGetLastError();
+}
+
+hipError_t launch_decode_select(const DecodeArgs& a, hipStream_t st) {
+  // a batch that fills the chip twice over takes the 512-thread instance: more queries per CU
+  // and half the waves in each block reduction (per-query prefill: 39.6 -> 31.4 ms at config 3);
+  // a few queries keep 1024 threads, whose shorter per-thread ranges finish each query sooner
+  if ((int64_t)a.H * a.Q >= 512) return launch_select_t<512>(a, st);
+  return launch_select_t<1024>(a, st);
 }
 
 template <int DT, int D>

@@ -86,6 +86,10 @@ def test_decode_sets_match_reference_goldens():
     (5, 2, 2, 40000, 2048, 32, 32, 100.0, None, 1.0 / 3.0),   # the global key store (past LDS)
     (6, 1, 3, 45000, 300, 16, 16, 25.0, 0.125, 1.0),      # global store with the pct and cap cuts
     (7, 4, 1, 1, 8, 32, 32, 100.0, None, 1.0),            # a single key
+    # batches of H * Q >= 512 queries take the 512-thread selection instance
+    (8, 4, 160, 2500, 256, 32, 32, 100.0, None, 1.0 / 3.0),
+    (9, 2, 300, 3000, 64, 8, 8, 30.0, 0.25, 0.5),         # ties at both cuts
+    (10, 1, 512, 36000, 300, 16, 16, 25.0, 0.125, 1.0),   # its global key store
 ])
 def test_decode_select_matches_oracle_on_crafted_scores(case):
     seed, H, Q, M, km, ng, nl, pctd, quant, ps = case
