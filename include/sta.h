@@ -271,7 +271,7 @@ typedef struct sta_pqstream_args {
   const float* inv_freq_a;  /* (D/2,) selection geometry */
   float pos_scale_a, rope_scale_a;
   const float* inv_freq_c;  /* (D/2,) attend geometry (base RoPE, scale 1) */
-  float sm_scale;
+  float sm_scale;           /* finite and > 0 */
   int32_t n_global, n_local, tile, block_n, pos_advance, use_skip, q_pos_base;
   /* outputs (device) */
   void* out;                /* (H, N, D) */

@@ -62,6 +62,10 @@ int stream_check(const sta_pqstream_args* a) {
     return fail(STA_ERR_INVALID_ARG, "H=%d must be a positive multiple of Hkv=%d", a->H, a->Hkv);
   if (a->N < 1 || a->N >= (1 << 24)) return fail(STA_ERR_INVALID_ARG, "N=%d out of range [1, 2^24)", a->N);
   if (a->D != 64 && a->D != 128) return fail(STA_ERR_UNSUPPORTED, "head_dim %d not in {64, 128}", a->D);
+  // the sweep keeps its running max on the raw dots, which orders as the scaled scores only for a
+  // positive scale
+  if (!(a->sm_scale > 0.0f && a->sm_scale < INFINITY))
+    return fail(STA_ERR_INVALID_ARG, "sm_scale=%g must be finite and > 0", (double)a->sm_scale);
   // pqstream_kernel.py:509-518
   if (a->tile != 32) return fail(STA_ERR_INVALID_ARG, "tile %d: BLOCK_M is fixed at 32", a->tile);
   if (a->q_pos_base != 0)

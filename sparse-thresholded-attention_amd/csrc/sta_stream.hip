@@ -304,7 +304,8 @@ __global__ __launch_bounds__(G * 64, 1) void stream_kernel(StreamArgs a) {
   floatx16 oacc[RBS];
 #pragma unroll
   for (int rb = 0; rb < RBS; ++rb) oacc[rb] = floatx16{};
-  float mR = -INFINITY, l_i = 0.0f;
+  float mR = -INFINITY, l_i = 0.0f;   // running max of the raw dots, running sum
+  const float c2 = a.sm_scale * 1.44269504088896341f;
   float d = 0.0f;                 // running base (:252)
   int kept_q = 0, n_used = 0;
 
@@ -434,10 +435,16 @@ __global__ __launch_bounds__(G * 64, 1) void stream_kernel(StreamArgs a) {
           for (int e = 0; e < 8; ++e) {
             const int f = s * 16 + 8 * hf + e;
             const float cs = cstab[2 * f], sn = cstab[2 * f + 1];
-            const float p1 = qa[s][e] * cs, p2 = qa[s + KS / 2][e] * sn;
-            const float p3 = qa[s + KS / 2][e] * cs, p4 = qa[s][e] * sn;
-            y1[e] = p1 - p2;
-            y2[e] = p3 + p4;
+            if constexpr (X3) {   // fp32 inputs: every product rounded, as the reference rotates
+              const float p1 = qa[s][e] * cs, p2 = qa[s + KS / 2][e] * sn;
+              const float p3 = qa[s + KS / 2][e] * cs, p4 = qa[s][e] * sn;
+              y1[e] = p1 - p2;
+              y2[e] = p3 + p4;
+            } else {              // 16-bit operands: one product and one FMA per coordinate, the
+                                  // result rounded to the operand type right after
+              y1[e] = fmaf(qa[s][e], cs, -(qa[s + KS / 2][e] * sn));
+              y2[e] = fmaf(qa[s + KS / 2][e], cs, qa[s][e] * sn);
+            }
           }
           u32x4 qh[2], ql[2];
           if constexpr (X3) {
@@ -470,26 +477,29 @@ __global__ __launch_bounds__(G * 64, 1) void stream_kernel(StreamArgs a) {
             }
           }
         }
-        // ---- mask + online softmax (:334-344) ----
+        // ---- mask + online softmax (:334-344).  The running max stays on the raw dots (the
+        //      scale is positive, so they order as the scaled scores) and each weight is
+        //      exp2(raw * c2 - max * c2) with c2 = scale * log2(e): one FMA and one exp per score ----
         float bmax = -INFINITY;
 #pragma unroll
         for (int sb = 0; sb < NSB; ++sb)
 #pragma unroll
           for (int i = 0; i < 16; ++i) {
-            const float v = ((mbits[sb] >> i) & 1u) ? sacc[sb][i] * a.sm_scale : -INFINITY;
+            const float v = ((mbits[sb] >> i) & 1u) ? sacc[sb][i] : -INFINITY;
             sacc[sb][i] = v;
             bmax = fmaxf(bmax, v);
           }
         bmax = fmaxf(bmax, __shfl_xor(bmax, 32, 64));
         const float mnew = fmaxf(mR, bmax);
         const float msafe = (mnew == -INFINITY) ? 0.0f : mnew;
-        const float alpha = __expf(mR - msafe);
+        const float alpha = __builtin_amdgcn_exp2f((mR - msafe) * c2);
+        const float moff = -msafe * c2;
         float psum = 0.0f;
 #pragma unroll
         for (int sb = 0; sb < NSB; ++sb)
 #pragma unroll
           for (int i = 0; i < 16; ++i) {
-            const float pv = __expf(sacc[sb][i] - msafe);
+            const float pv = __builtin_amdgcn_exp2f(fmaf(sacc[sb][i], c2, moff));
             sacc[sb][i] = pv;
             psum += pv;
           }

@@ -156,6 +156,7 @@ def _stream_args(**kw):
     a = native.StreamArgsC()
     a.dtype, a.H, a.Hkv, a.N, a.D, a.tile, a.block_n = 1, 32, 32, 16384, 128, 32, 32
     a.n_global, a.n_local, a.pos_advance, a.use_skip = 32, 32, 0, 1
+    a.sm_scale = 128 ** -0.5
     for k, v in kw.items():
         setattr(a, k, v)
     return a
@@ -163,7 +164,8 @@ def _stream_args(**kw):
 
 @pytest.mark.parametrize("field,value,code", [
     ("tile", 64, -1), ("q_pos_base", 3, -1), ("block_n", 16, -1), ("block_n", 128, -2),
-    ("pos_advance", 2, -1), ("D", 96, -2),
+    ("pos_advance", 2, -1), ("D", 96, -2), ("sm_scale", 0.0, -1), ("sm_scale", -0.1, -1),
+    ("sm_scale", float("inf"), -1),
 ])
 def test_pqstream_invalid_arguments_are_rejected(field, value, code):
     import _sta_native as native
