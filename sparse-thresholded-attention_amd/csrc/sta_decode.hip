@@ -876,7 +876,7 @@ hipError_t launch_decode_select(const DecodeArgs& a, hipStream_t st) {
 template <int DT, int D>
 static hipError_t launch_attend_t(const DecodeArgs& a, hipStream_t st) {
   const int nmax = decode_nsplit(a.k_max);
-  if (nmax > 256) return hipErrorInvalidValue;
+  if (nmax > 1024) return hipErrorInvalidValue;   // the merge kernel's split capacity: k_max <= 65536
   const int ns = decode_attend_splits(a.Q, a.k_max);
   const int steps = (nmax + ns - 1) / ns;
   const int ng = (nmax + steps - 1) / steps;     // splits that hold slots

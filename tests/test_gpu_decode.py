@@ -174,6 +174,8 @@ def test_decode_batched_matches_per_token_loop():
     # batches of 64+ queries take their scores from the matrix cores (fragments + score rows)
     (4, 2, 200, 1500, 128, torch.bfloat16, 256, 100.0, False, 0.5, 1.0),
     (2, 2, 96, 900, 64, torch.float16, 128, 30.0, True, 1.0, 1.1386294),
+    # sets of about 20000 keys: more than 256 attend splits per query
+    (2, 2, 1, 30000, 64, torch.bfloat16, 24000, 100.0, False, 1.0 / 3.0, 1.0),
 ])
 def test_decode_three_layer(case):
     import _sta_native as native
