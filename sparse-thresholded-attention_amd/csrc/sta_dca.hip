@@ -84,9 +84,9 @@ __global__ __launch_bounds__(256) void dca_rope_kernel(const void* __restrict__ 
 // ------------------------------------------------------------------------------------------
 // the attention sweep
 // ------------------------------------------------------------------------------------------
-template <int DT, int D, int G>
+template <int DT, int D, int G, int BNV = 64>
 struct DcaCfg {
-  static constexpr int BN = 64;                     // keys per block
+  static constexpr int BN = BNV;                    // keys per block
   static constexpr bool X3 = DT == DT_F32;
   static constexpr int P = X3 ? 2 : 1;
   static constexpr int NTH = G * 64;
@@ -109,10 +109,14 @@ struct DcaCfg {
 //   state (o, m, l) in a.state.
 // MODE 2 (config 4, local keys): as MODE 0 over the keys of the query's own and previous chunk
 //   only ([max(0, (c - 1) L), i]), starting from the MODE 1 state of each row.
+// keys per block: 64, or 32 for the selected instance, whose two waves stage each block alone
+// (half the staging registers; its workgroups hold one wave per SIMD at 64)
+constexpr int dca_block_keys(int mode) { return mode == 1 ? 32 : 64; }
+
 template <int DT, int D, int G, int MODE = 0>
-__global__ __launch_bounds__(G * 64, 1) void dca_attn_kernel(DcaArgs a) {
+__global__ __launch_bounds__(G * 64, (MODE == 1 && DT != DT_F32) ? 2 : 1) void dca_attn_kernel(DcaArgs a) {
 #pragma clang fp contract(off)
-  using Cfg = DcaCfg<DT, D, G>;
+  using Cfg = DcaCfg<DT, D, G, dca_block_keys(MODE)>;
   constexpr int BN = Cfg::BN;
   constexpr bool X3 = Cfg::X3;
   constexpr int P = Cfg::P, NTH = Cfg::NTH, KSTR = Cfg::KSTR, VSTR = Cfg::VSTR;
@@ -481,7 +485,7 @@ size_t dca_lds_bytes(int dtype, int D) {
 
 template <int DT, int D, int G, int MODE>
 static hipError_t launch_dca_attn_g(const DcaArgs& a, hipStream_t st) {
-  using Cfg = DcaCfg<DT, D, G>;
+  using Cfg = DcaCfg<DT, D, G, dca_block_keys(MODE)>;
   hipError_t e = hipFuncSetAttribute((const void*)dca_attn_kernel<DT, D, G, MODE>,
                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)Cfg::lds_bytes);
   if (e != hipSuccess) return e;
