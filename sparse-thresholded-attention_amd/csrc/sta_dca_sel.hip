@@ -186,10 +186,10 @@ __global__ __launch_bounds__(256) void dca_vote_kernel(DcaVoteArgs a) {
 // x ^ (r mod G) (G granules of 8 elements per row), and the MFMA operand read of granule j of row
 // r (lane r, half j & 1) finds it at position j ^ (r mod G): the 32 rows of a read fall in
 // distinct bank groups.
-constexpr int DV_NW = 8;                    // waves per workgroup: 512 query rows share each chunk
+constexpr int DV_NW = 4;                    // waves per workgroup: 256 query rows share each chunk
 
 template <int DT, int D, int PASS>
-__global__ __launch_bounds__(64 * DV_NW) void dca_vote16_kernel(DcaVoteArgs a) {
+__global__ __launch_bounds__(64 * DV_NW, 3) void dca_vote16_kernel(DcaVoteArgs a) {
 #pragma clang fp contract(off)
   static_assert(DT == DT_BF16 || DT == DT_F16, "16-bit key tables");
   constexpr int S = D / 16;
