@@ -1320,9 +1320,11 @@ class PerQueryPrefillPlan:
                 p.args.stage_events = ctypes.cast(p._events, ctypes.c_void_p)
             _check(lib().sta_decode_attention(ctypes.byref(p.args), _stream(self.device)), "sta_decode_attention")
             if staged:
+                # the launch wrote (heads, queries[, D]) contiguously from the staging buffers' start
                 h0, h1, i0, i1 = self._spans[i]
                 for name, t in self._stage.items():
-                    self.out[name][h0:h1, i0:i1].copy_(t[:h1 - h0, :i1 - i0])
+                    dst = self.out[name][h0:h1, i0:i1]
+                    dst.copy_(t.view(-1)[:dst.numel()].view(dst.shape))
         return self.out
 
 

@@ -257,3 +257,25 @@ def test_perquery_full_prefill_plan_config3_structure():
         e = (d["out"][0, 0].float() - r["out"][h, rr].float()).abs().max().item()
         assert e <= 2e-2, (rr, e)
 
+
+
+def test_perquery_prefill_chunking_is_transparent():
+    """The per-query prefill over chunks of positions (each a decode batch over its cache prefix)
+    gives the one-batch run's outputs bit for bit: a query's scores, set and attend depend on
+    neither the chunking nor the head grouping."""
+    import _sta_native as native
+    from synthetic import base_inv_freq, planted_inputs
+    H, Hkv, N, D = 4, 2, 2500, 128
+    q, k, v = planted_inputs(83, H, Hkv, N, D, 0.01, torch.bfloat16, DEV)
+    invf = base_inv_freq(D, 10000.0).to(DEV)
+    tau = torch.full((H,), 4.0, device=DEV)
+    say("per-query prefill: chunks of 1000 and 2 heads per group against one batch")
+    whole = native.PerQueryPrefillPlan(q, k, v, tau, invf, invf, 0.25, 1.0, None, 16, 16, 256,
+                                       query_chunk=None).run()
+    whole = {n: t.clone() for n, t in whole.items()}
+    parts = native.PerQueryPrefillPlan(q, k, v, tau, invf, invf, 0.25, 1.0, None, 16, 16, 256, heads_per_group=2,
+                                       query_chunk=1000).run()
+    torch.cuda.synchronize()
+    assert int(whole["overflow"].sum()) > 0          # the cap binds somewhere
+    for name in ("out", "set_size", "usize", "overflow"):
+        assert torch.equal(whole[name], parts[name]), name
