@@ -299,14 +299,24 @@ __global__ __launch_bounds__(64 * DV_NW, 3) void dca_vote16_kernel(DcaVoteArgs a
 #pragma unroll
             for (int i = 0; i < 16; ++i) acc[rb][i] = 0.0f;
           const int rowp = (sb * 32 + rr) * G;
+          // the K fragment of step s + 1 is read while step s's two products run
+          u32x4 bh = buf[rowp + (hf ^ (rr % G))];
 #pragma unroll
           for (int s = 0; s < S; ++s) {
-            const u32x4 bh = buf[rowp + ((2 * s + hf) ^ (rr % G))];
+            u32x4 nh = bh;
+            if (s + 1 < S) nh = buf[rowp + ((2 * (s + 1) + hf) ^ (rr % G))];
 #pragma unroll
             for (int rb = 0; rb < 2; ++rb) {
               if constexpr (DT == DT_F16) acc[rb] = mfma32_f16(qh[rb][s], bh, acc[rb]);
               else acc[rb] = mfma32(qh[rb][s], bh, acc[rb]);
             }
+            bh = nh;
+          }
+          __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);   // reads of steps 0 and 1
+#pragma unroll
+          for (int s = 0; s < S; ++s) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 2, 0); // step s's products
+            if (s + 2 < S) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // step s + 2's read
           }
           if constexpr (PASS == 0) {
 #pragma unroll
