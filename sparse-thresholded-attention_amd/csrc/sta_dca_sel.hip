@@ -192,6 +192,9 @@ template <int DT, int D, int PASS>
 __global__ __launch_bounds__(64 * DV_NW, 3) void dca_vote16_kernel(DcaVoteArgs a) {
 #pragma clang fp contract(off)
   static_assert(DT == DT_BF16 || DT == DT_F16, "16-bit key tables");
+  // +inf hidden from the optimiser: med3(x, y, pinf) = max(x, y) stays one v_med3_f32
+  float pinf = INFINITY;
+  asm volatile("" : "+s"(pinf));
   constexpr int S = D / 16;
   constexpr int G = D / 8;                   // 16-byte granules per key row
   constexpr int CK = 64;                     // keys per chunk
@@ -319,10 +322,11 @@ __global__ __launch_bounds__(64 * DV_NW, 3) void dca_vote16_kernel(DcaVoteArgs a
             if (s + 2 < S) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // step s + 2's read
           }
           if constexpr (PASS == 0) {
+            // max(st, acc) as one v_med3_f32 (scores are finite; fmaxf canonicalises both inputs)
 #pragma unroll
             for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
-              for (int i = 0; i < 16; ++i) st[rb][i] = fmaxf(st[rb][i], acc[rb][i]);
+              for (int i = 0; i < 16; ++i) st[rb][i] = __builtin_amdgcn_fmed3f(acc[rb][i], st[rb][i], pinf);
           } else {
             int cnt = 0;
 #pragma unroll
