@@ -78,6 +78,8 @@ struct SelectArgs {
                           // selects among its inter keys [0, max(0, (c - 1) dca_L)) as if they
                           // were the whole key axis (N and K_ord per tile; the local window then
                           // falls outside it); 0: the shared selection over [0, N)
+  int stage_slots;        // set by the launcher: the kept slots are gathered in LDS and written
+                          // coalesced (short rows), or written straight from the compaction
 };
 
 struct GatherArgs {

@@ -123,8 +123,8 @@ __global__ __launch_bounds__(256) void select_kernel(SelectArgs a) {
   float* tmpf = (float*)(tmpi + 8);                                         // 8
   int* misc = (int*)(tmpf + 8);                                             // 16
   float* qnp = (float*)(misc + 16);                                         // T (<= 256)
-  int32_t* sidx = (int32_t*)(qnp + 256);                                    // k_max
-  float* snp = (float*)(sidx + a.k_max);                                    // k_max
+  int32_t* sidx = (int32_t*)(qnp + 256);                                    // k_max (stage_slots)
+  float* snp = (float*)(sidx + a.k_max);                                    // k_max (stage_slots)
 
   for (int i = tid; i < 260; i += 256) { hist[i] = 0; fhist[i] = 0; }
   if (tid == 0) misc[1] = 0;
@@ -245,6 +245,15 @@ __global__ __launch_bounds__(256) void select_kernel(SelectArgs a) {
   }
   __syncthreads();
   const int vc = misc[0];
+  const int kept_total = C[vc] + F[vc];
+  const int nvalid = min(kept_total, a.k_max);
+  int32_t* irow = a.idx + ((int64_t)h * a.nt + t) * a.k_max;
+  float* nkrow = a.newpos_k + ((int64_t)h * a.nt + t) * a.k_max;
+  // the kept slots: gathered in LDS and written coalesced afterwards, or (long rows, where the
+  // k_max slots in LDS would leave one workgroup per CU) written straight from the compaction,
+  // each thread's kept keys having consecutive ranks
+  int32_t* dst_i = a.stage_slots ? sidx : irow;
+  float* dst_n = a.stage_slots ? snp : nkrow;
   // ---- compaction + reposition over keys [0, scan_end) ----
   const int scan_end = (vc == 0) ? N : min(N, max(hi_keys, max(gA, bh + 1)));
   const int per_c = per_of(scan_end);
@@ -297,20 +306,23 @@ __global__ __launch_bounds__(256) void select_kernel(SelectArgs a) {
             run = fmaxf(run, cp - (float)rank);
           }
           const float np = (float)rank + run;          // exact_2.py:386
-          if (kept && rank < a.k_max) { sidx[rank] = j; snp[rank] = np; }
+          if (kept && rank < a.k_max) { dst_i[rank] = j; dst_n[rank] = np; }
           if (j >= qlo && j <= qhi) qnp[j - qlo] = np;
         }
       }
     }
   }
   __syncthreads();
-  const int kept_total = C[vc] + F[vc];
-  const int nvalid = min(kept_total, a.k_max);
-  int32_t* irow = a.idx + ((int64_t)h * a.nt + t) * a.k_max;
-  float* nkrow = a.newpos_k + ((int64_t)h * a.nt + t) * a.k_max;
-  for (int s = tid; s < a.k_max; s += 256) {          // exact_2.py:401-408
-    irow[s] = s < nvalid ? sidx[s] : N;
-    nkrow[s] = s < nvalid ? snp[s] : 0.0f;
+  if (a.stage_slots) {
+    for (int s = tid; s < a.k_max; s += 256) {        // exact_2.py:401-408
+      irow[s] = s < nvalid ? sidx[s] : N;
+      nkrow[s] = s < nvalid ? snp[s] : 0.0f;
+    }
+  } else {
+    for (int s = nvalid + tid; s < a.k_max; s += 256) {   // sentinels (exact_2.py:401-408)
+      irow[s] = N;
+      nkrow[s] = 0.0f;
+    }
   }
   float* nqrow = a.newpos_q + ((int64_t)h * a.nt + t) * T;
   for (int i = tid; i < T; i += 256) {                  // exact_2.py:410-412
@@ -343,14 +355,21 @@ hipError_t launch_expand_votes(const uint8_t* v8, int64_t stride, int H, int nt,
   return hipGetLastError();
 }
 
+// the LDS a row needs without the slot staging (k_max * 8 bytes more with it)
 size_t select_lds_bytes(int N, int k_max) {
+  (void)k_max;
   const int per = ((((N + 255) / 256) + 15) / 16) * 16;
-  return (size_t)256 * per + (260 + 260 + 8) * 4 + 8 * 4 + 16 * 4 + 256 * 4 + (size_t)k_max * 8;
+  return (size_t)256 * per + (260 + 260 + 8) * 4 + 8 * 4 + 16 * 4 + 256 * 4;
 }
 
-hipError_t launch_select(const SelectArgs& a, int vote_bytes, hipStream_t st) {
-  const size_t lds = select_lds_bytes(a.N, a.k_max);
-  if (lds > 160 * 1024) return hipErrorInvalidValue;
+hipError_t launch_select(const SelectArgs& a0, int vote_bytes, hipStream_t st) {
+  SelectArgs a = a0;
+  const size_t base = select_lds_bytes(a.N, a.k_max);
+  if (base > 160 * 1024) return hipErrorInvalidValue;
+  // stage the slots while two workgroups still fit a CU (c4's 64k rows: 3.5 ms direct against
+  // 6.7 ms staged at one workgroup per CU; c1's rows: 0.127 ms staged, 0.137 ms direct)
+  a.stage_slots = base + (size_t)a.k_max * 8 <= 80 * 1024 ? 1 : 0;
+  const size_t lds = base + (a.stage_slots ? (size_t)a.k_max * 8 : 0);
   if (vote_bytes == 1) {
     hipError_t e = hipFuncSetAttribute((const void*)select_kernel<uint8_t>,
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);

@@ -414,3 +414,26 @@ def test_config2_full_length_gqa_group():
     tau = torch.full((2,), c.tau, device=DEV)
     full_check(q, k, v, tau, invf.to(DEV), ps, rs, pct=c.pct, tile=c.tile, k_max=c.k_max,
                n_global=c.n_global, n_local=c.n_local, what="config 2 full length, 2 q heads / 1 kv head")
+
+
+@pytest.mark.parametrize("k_max", [2048, 10000])
+def test_build_sets_slot_paths(k_max):
+    """_build_sets on random votes with the kept slots staged in LDS (k_max 2048) and written
+    straight from the compaction (k_max 10000: the staged slots would pass 80 KB of LDS):
+    bit-exact against the oracle either way."""
+    import _sta_native as native
+    rng = np.random.default_rng(97)
+    H, T, N = 2, 64, 12000
+    nt = (N + T - 1) // T
+    votes = rng.integers(0, 65, size=(H, nt, N)).astype(np.int32)
+    votes[votes < 40] = 0                                  # most keys unvoted, as in real tiles
+    say(f"build_sets slot paths: k_max={k_max}")
+    res = native.build_sets(torch.from_numpy(votes).to(DEV), 1.0 / 3.0, 32, 32, 30.0, T, k_max, 0, True)
+    ref = orc.build_sets(votes, 1.0 / 3.0, 32, 32, 30.0, T, k_max, 0, True)
+    for name, got, r in zip(SET_NAMES, res, ref):
+        got = got.cpu().numpy()
+        r = np.asarray(r)
+        if r.dtype == np.float32:
+            assert np.array_equal(got.view(np.uint32), r.view(np.uint32)), name
+        else:
+            assert np.array_equal(got.astype(r.dtype), r), name
