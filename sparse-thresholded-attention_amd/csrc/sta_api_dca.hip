@@ -16,7 +16,7 @@ constexpr int kDcaSelTile = 64;   // queries per selection tile (config 4)
 struct DcaLayout {
   int Npad, planes, nt;
   int64_t votes_stride;
-  size_t krot_off, qrot_off, votes_off, rmax_off, npk_off, npq_off, state_off, total;
+  size_t krot_off, qrot_off, votes_off, rmax_off, npk_off, npq_off, state_off, tab_off, total;
 };
 
 DcaLayout dca_layout_of(const sta_dca_args* a) {
@@ -43,6 +43,8 @@ DcaLayout dca_layout_of(const sta_dca_args* a) {
     L.state_off = off;                                 // partial softmax states (H, Npad, D + 4)
     off = align256(off + (size_t)a->H * L.Npad * (a->D + 4) * 4);
   }
+  L.tab_off = off;                                     // the remap's (cos, sin) table
+  off = align256(off + dca_table_bytes(a->D, a->chunk_size));
   L.total = off;
   return L;
 }
@@ -235,11 +237,14 @@ int sta_dca_attention(const sta_dca_args* a, void* stream) {
   const float mscale = a->mscale > 0.0f ? a->mscale : (ratio <= 1.0 ? 1.0f : (float)(0.05 * log(ratio) + 1.0));
 
   if ((rc = mark_event(a->stage_events, 0, st)) != STA_OK) return rc;
-  hipError_t e = launch_dca_rope(a->dtype, a->D, a->k, a->k_head_stride, a->k_tok_stride, a->Hkv, a->N, L.Npad,
-                                 Lc, a->chunk_size, mscale, 1, a->inv_freq, krot, st);
+  float2* table = (float2*)(ws + L.tab_off);
+  hipError_t e = launch_dca_table(a->dtype, a->D, a->inv_freq, mscale, a->chunk_size, table, st);
+  if (e != hipSuccess) return hip_fail(e, "dca table");
+  e = launch_dca_rope(a->dtype, a->D, a->k, a->k_head_stride, a->k_tok_stride, a->Hkv, a->N, L.Npad, Lc,
+                      a->chunk_size, 1, table, krot, st);
   if (e != hipSuccess) return hip_fail(e, "dca rotation (k)");
   e = launch_dca_rope(a->dtype, a->D, a->q, a->q_head_stride, a->q_tok_stride, a->H, a->N, L.Npad, Lc,
-                      a->chunk_size, mscale, 0, a->inv_freq, qrot, st);
+                      a->chunk_size, 0, table, qrot, st);
   if (e != hipSuccess) return hip_fail(e, "dca rotation (q)");
   if ((rc = mark_event(a->stage_events, 1, st)) != STA_OK) return rc;
   if (a->select) {

@@ -27,11 +27,25 @@ namespace sta {
 // keys (Hkv, Npad, P, D), queries (3, H, Npad, P, D); P = 2 (bf16 hi / lo) for fp32 inputs,
 // else the model dtype.  Rows >= N are zero.
 // ------------------------------------------------------------------------------------------
+// The table of every position the remap produces, t = 0 .. chunk_size (keys t < L, queries up
+// to the succ / inter clamps): entry (t, f) = (cos, sin) of fl(t * inv_freq[f]) times mscale in
+// the model dtype (dca_table_entry).  One sin / cos per (t, f) instead of one per (head, row, f).
+template <int DT, int D>
+__global__ __launch_bounds__(256) void dca_table_kernel(const float* __restrict__ inv_freq, float mscale,
+                                                        int chunk_size, float2* __restrict__ table) {
+  const int64_t x = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (x >= (int64_t)(chunk_size + 1) * (D / 2)) return;
+  const int t = (int)(x / (D / 2)), f = (int)(x % (D / 2));
+  float cs, sn;
+  dca_table_entry<DT>(t, inv_freq[f], mscale, cs, sn);
+  table[x] = make_float2(cs, sn);
+}
+
 template <int DT, int D>
 __global__ __launch_bounds__(256) void dca_rope_kernel(const void* __restrict__ x, int64_t head_stride,
                                                        int64_t tok_stride, int heads, int N, int Npad,
-                                                       int L, int chunk_size, float mscale, int is_key,
-                                                       const float* __restrict__ inv_freq,
+                                                       int L, int chunk_size, int is_key,
+                                                       const float2* __restrict__ table,
                                                        uint16_t* __restrict__ out) {
 #pragma clang fp contract(off)
   constexpr int C = D / 8;
@@ -63,7 +77,17 @@ __global__ __launch_bounds__(256) void dca_rope_kernel(const void* __restrict__ 
     const int64_t base = (int64_t)head * head_stride + (int64_t)row * tok_stride;
     load8<DT>(x, base + i0, a);
     load8<DT>(x, base + D / 2 + i0, b);
-    dca_rot8<DT>(a, b, t, i0, first, inv_freq, mscale, o);
+    float cs[8], sn[8];
+    const float4* tr = (const float4*)(table + (int64_t)t * (D / 2) + i0);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float4 v = tr[e];
+      cs[2 * e] = v.x;
+      sn[2 * e] = v.y;
+      cs[2 * e + 1] = v.z;
+      sn[2 * e + 1] = v.w;
+    }
+    dca_rot8_cs<DT>(a, b, cs, sn, first, o);
   } else {
 #pragma unroll
     for (int e = 0; e < 8; ++e) o[e] = 0.0f;
@@ -451,22 +475,43 @@ __global__ __launch_bounds__(G * 64, (MODE == 1 && DT != DT_F32) ? 2 : 1) void d
 // ------------------------------------------------------------------------------------------
 // host launchers
 // ------------------------------------------------------------------------------------------
+size_t dca_table_bytes(int D, int chunk_size) { return (size_t)(chunk_size + 1) * (D / 2) * sizeof(float2); }
+
+template <int DT, int D>
+static hipError_t launch_dca_table_t(const float* inv_freq, float mscale, int chunk_size, float2* table,
+                                     hipStream_t st) {
+  const int64_t total = (int64_t)(chunk_size + 1) * (D / 2);
+  hipLaunchKernelGGL((dca_table_kernel<DT, D>), dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, inv_freq,
+                     mscale, chunk_size, table);
+  return hipGetLastError();
+}
+
+hipError_t launch_dca_table(int dtype, int D, const float* inv_freq, float mscale, int chunk_size, float2* table,
+                            hipStream_t st) {
+#define STA_DT(DT_, D_) \
+  if (dtype == DT_ && D == D_) return launch_dca_table_t<DT_, D_>(inv_freq, mscale, chunk_size, table, st);
+  STA_DT(DT_F32, 64) STA_DT(DT_F32, 128) STA_DT(DT_BF16, 64) STA_DT(DT_BF16, 128)
+  STA_DT(DT_F16, 64) STA_DT(DT_F16, 128)
+#undef STA_DT
+  return hipErrorInvalidValue;
+}
+
 template <int DT, int D>
 static hipError_t launch_dca_rope_t(const void* x, int64_t hs, int64_t ts, int heads, int N, int Npad, int L,
-                                    int chunk_size, float mscale, int is_key, const float* inv_freq,
-                                    uint16_t* out, hipStream_t st) {
+                                    int chunk_size, int is_key, const float2* table, uint16_t* out,
+                                    hipStream_t st) {
   const int64_t total = (int64_t)(is_key ? 1 : 3) * heads * Npad * (D / 8);
   hipLaunchKernelGGL((dca_rope_kernel<DT, D>), dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, x, hs,
-                     ts, heads, N, Npad, L, chunk_size, mscale, is_key, inv_freq, out);
+                     ts, heads, N, Npad, L, chunk_size, is_key, table, out);
   return hipGetLastError();
 }
 
 hipError_t launch_dca_rope(int dtype, int D, const void* x, int64_t hs, int64_t ts, int heads, int N, int Npad,
-                           int L, int chunk_size, float mscale, int is_key, const float* inv_freq,
-                           uint16_t* out, hipStream_t st) {
+                           int L, int chunk_size, int is_key, const float2* table, uint16_t* out,
+                           hipStream_t st) {
 #define STA_DR(DT_, D_) \
   if (dtype == DT_ && D == D_) \
-    return launch_dca_rope_t<DT_, D_>(x, hs, ts, heads, N, Npad, L, chunk_size, mscale, is_key, inv_freq, out, st);
+    return launch_dca_rope_t<DT_, D_>(x, hs, ts, heads, N, Npad, L, chunk_size, is_key, table, out, st);
   STA_DR(DT_F32, 64) STA_DR(DT_F32, 128) STA_DR(DT_BF16, 64) STA_DR(DT_BF16, 128)
   STA_DR(DT_F16, 64) STA_DR(DT_F16, 128)
 #undef STA_DR

@@ -27,30 +27,45 @@ __device__ __forceinline__ float opaque_f32(float x) {
 
 // Eight rotated outputs o[e] for dims d0 + e of a row at table position t, given the row's
 // elements a[e] = x[i0 + e] and b[e] = x[D/2 + i0 + e] (i0 = d0 mod D/2; first: d0 < D/2).
+// One table entry: cos / sin of the fp32 angle fl(t * f), correctly rounded to fp32 (through
+// double), times mscale and rounded to the model dtype.  A one-ulp difference between fp32 cosine
+// implementations can flip a bf16 entry; the correctly rounded value is the one every
+// implementation approximates, and the CPU oracle computes the same.
+template <int DT>
+__device__ __forceinline__ void dca_table_entry(int t, float f, float mscale, float& cs, float& sn) {
+#pragma clang fp contract(off)
+  const float ang = (float)t * f;
+  double sd, cd;
+  sincos((double)ang, &sd, &cd);
+  cs = round_dt<DT>(opaque_f32((float)cd * mscale));
+  sn = round_dt<DT>(opaque_f32((float)sd * mscale));
+}
+
+// The rotation of eight elements with given table values (cs[e], sn[e]) for dims i0 + e.
+template <int DT>
+__device__ __forceinline__ void dca_rot8_cs(const float* a, const float* b, const float* cs, const float* sn,
+                                            bool first, float* o) {
+#pragma clang fp contract(off)
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    if (first) {                                                // x1*cos + (-x2)*sin
+      const float p = round_dt<DT>(a[e] * cs[e]), q = round_dt<DT>(-b[e] * sn[e]);
+      o[e] = round_dt<DT>(p + q);
+    } else {                                                    // x2*cos + x1*sin
+      const float p = round_dt<DT>(b[e] * cs[e]), q = round_dt<DT>(a[e] * sn[e]);
+      o[e] = round_dt<DT>(p + q);
+    }
+  }
+}
+
 template <int DT>
 __device__ __forceinline__ void dca_rot8(const float* a, const float* b, int t, int i0, bool first,
                                          const float* __restrict__ inv_freq, float mscale, float* o) {
 #pragma clang fp contract(off)
-  const float tf = (float)t;
+  float cs[8], sn[8];
 #pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    const float ang = tf * inv_freq[i0 + e];
-    // cos / sin of the fp32 angle, correctly rounded to fp32 (through double): the table is then
-    // rounded to the model dtype, where a one-ulp difference between fp32 cosine implementations
-    // can flip a bf16 entry; the correctly rounded value is the one every implementation
-    // approximates, and the CPU oracle computes the same
-    double sd, cd;
-    sincos((double)ang, &sd, &cd);
-    const float cs = round_dt<DT>(opaque_f32((float)cd * mscale));   // table value in the model dtype
-    const float sn = round_dt<DT>(opaque_f32((float)sd * mscale));
-    if (first) {                                                // x1*cos + (-x2)*sin
-      const float p = round_dt<DT>(a[e] * cs), q = round_dt<DT>(-b[e] * sn);
-      o[e] = round_dt<DT>(p + q);
-    } else {                                                    // x2*cos + x1*sin
-      const float p = round_dt<DT>(b[e] * cs), q = round_dt<DT>(a[e] * sn);
-      o[e] = round_dt<DT>(p + q);
-    }
-  }
+  for (int e = 0; e < 8; ++e) dca_table_entry<DT>(t, inv_freq[i0 + e], mscale, cs[e], sn[e]);
+  dca_rot8_cs<DT>(a, b, cs, sn, first, o);
 }
 
 }  // namespace sta

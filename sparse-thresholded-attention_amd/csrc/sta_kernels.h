@@ -317,9 +317,13 @@ hipError_t launch_abs_rope(int dtype, int D, const void* x, int64_t hs, int64_t 
 size_t stream_lds_bytes(int dtype, int D, int BN, bool fused);
 bool stream_can_fuse(int dtype, int D, int BN);   // a sweep that computes the keep bits itself exists
 // launch_stream runs the fused sweep when a.qfrag is set, else the sweep that reads a.bits
+// the remap's (cos, sin) table for positions 0 .. chunk_size, (chunk_size + 1) x D/2 float2
+size_t dca_table_bytes(int D, int chunk_size);
+hipError_t launch_dca_table(int dtype, int D, const float* inv_freq, float mscale, int chunk_size, float2* table,
+                            hipStream_t st);
 hipError_t launch_dca_rope(int dtype, int D, const void* x, int64_t hs, int64_t ts, int heads, int N, int Npad,
-                           int L, int chunk_size, float mscale, int is_key, const float* inv_freq,
-                           uint16_t* out, hipStream_t st);
+                           int L, int chunk_size, int is_key, const float2* table, uint16_t* out,
+                           hipStream_t st);
 size_t dca_lds_bytes(int dtype, int D);
 hipError_t launch_dca_attn(int dtype, int D, const DcaArgs& a, hipStream_t st);
 hipError_t launch_stream(int dtype, int D, int BN, const StreamArgs& a, hipStream_t st);

@@ -212,6 +212,7 @@ def test_dca_workspace_size_matches_layout():
     lib = native.lib()
     n = lib.sta_dca_workspace_size(ctypes.byref(_dca_args()))
     need = 32 * 65536 * 128 * 2 * 4          # rotated keys + three query variants, bf16
+    need += (4096 + 1) * 64 * 8              # (cos, sin) float pairs for positions 0 .. chunk_size
     assert need <= n < need + 4096
 
 
