@@ -50,58 +50,62 @@ __global__ __launch_bounds__(256) void dca_rope_kernel(const void* __restrict__ 
 #pragma clang fp contract(off)
   constexpr int C = D / 8;
   constexpr int P = DT == DT_F32 ? 2 : 1;
-  const int variants = is_key ? 1 : 3;
+  // one thread per (head, row, 8-dim group): the row's input is read once and rotated at the key
+  // position, or at the three query positions
   const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (gid >= (int64_t)variants * heads * Npad * C) return;
+  if (gid >= (int64_t)heads * Npad * C) return;
   const int c = (int)(gid % C);
-  int64_t r = gid / C;
+  const int64_t r = gid / C;
   const int row = (int)(r % Npad);
-  r /= Npad;
-  const int head = (int)(r % heads);
-  const int var = (int)(r / heads);
+  const int head = (int)(r / Npad);
   const int d0 = c * 8;
-  float o[8];
+  const bool first = d0 < D / 2;
+  const int i0 = first ? d0 : d0 - D / 2;
+  float a[8], b[8];
   if (row < N) {
-    int t;
-    if (is_key) {
-      t = row % L;                                               // dca_kernel.py:187-190
-    } else {
-      const int pid = row % L;
-      if (var == 0) t = pid;                                     // :181-182
-      else if (var == 1) t = min(pid + L, chunk_size);           // :185-186
-      else t = min(2 * L - 1, chunk_size);                       // the clamped index L-1, :464-467
-    }
-    const bool first = d0 < D / 2;
-    const int i0 = first ? d0 : d0 - D / 2;
-    float a[8], b[8];
     const int64_t base = (int64_t)head * head_stride + (int64_t)row * tok_stride;
     load8<DT>(x, base + i0, a);
     load8<DT>(x, base + D / 2 + i0, b);
-    float cs[8], sn[8];
-    const float4* tr = (const float4*)(table + (int64_t)t * (D / 2) + i0);
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const float4 v = tr[e];
-      cs[2 * e] = v.x;
-      sn[2 * e] = v.y;
-      cs[2 * e + 1] = v.z;
-      sn[2 * e + 1] = v.w;
-    }
-    dca_rot8_cs<DT>(a, b, cs, sn, first, o);
-  } else {
-#pragma unroll
-    for (int e = 0; e < 8; ++e) o[e] = 0.0f;
   }
-  uint16_t* dst = out + ((((int64_t)var * heads + head) * Npad + row) * P) * D + d0;
-  if constexpr (DT == DT_F32) {
-    u32x4 hi, lo;
-    split_bf16x8(o, hi, lo);
-    *(u32x4*)dst = hi;
-    *(u32x4*)(dst + D) = lo;
-  } else if constexpr (DT == DT_F16) {
-    *(u32x4*)dst = pack_f16x8(o);
-  } else {
-    *(u32x4*)dst = pack_bf16x8(o);
+  const int variants = is_key ? 1 : 3;
+  for (int var = 0; var < variants; ++var) {
+    float o[8];
+    if (row < N) {
+      int t;
+      if (is_key) {
+        t = row % L;                                               // dca_kernel.py:187-190
+      } else {
+        const int pid = row % L;
+        if (var == 0) t = pid;                                     // :181-182
+        else if (var == 1) t = min(pid + L, chunk_size);           // :185-186
+        else t = min(2 * L - 1, chunk_size);                       // the clamped index L-1, :464-467
+      }
+      float cs[8], sn[8];
+      const float4* tr = (const float4*)(table + (int64_t)t * (D / 2) + i0);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float4 v = tr[e];
+        cs[2 * e] = v.x;
+        sn[2 * e] = v.y;
+        cs[2 * e + 1] = v.z;
+        sn[2 * e + 1] = v.w;
+      }
+      dca_rot8_cs<DT>(a, b, cs, sn, first, o);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] = 0.0f;
+    }
+    uint16_t* dst = out + ((((int64_t)var * heads + head) * Npad + row) * P) * D + d0;
+    if constexpr (DT == DT_F32) {
+      u32x4 hi, lo;
+      split_bf16x8(o, hi, lo);
+      *(u32x4*)dst = hi;
+      *(u32x4*)(dst + D) = lo;
+    } else if constexpr (DT == DT_F16) {
+      *(u32x4*)dst = pack_f16x8(o);
+    } else {
+      *(u32x4*)dst = pack_bf16x8(o);
+    }
   }
 }
 
@@ -500,7 +504,7 @@ template <int DT, int D>
 static hipError_t launch_dca_rope_t(const void* x, int64_t hs, int64_t ts, int heads, int N, int Npad, int L,
                                     int chunk_size, int is_key, const float2* table, uint16_t* out,
                                     hipStream_t st) {
-  const int64_t total = (int64_t)(is_key ? 1 : 3) * heads * Npad * (D / 8);
+  const int64_t total = (int64_t)heads * Npad * (D / 8);
   hipLaunchKernelGGL((dca_rope_kernel<DT, D>), dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, x, hs,
                      ts, heads, N, Npad, L, chunk_size, is_key, table, out);
   return hipGetLastError();
