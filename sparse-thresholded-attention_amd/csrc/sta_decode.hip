@@ -305,8 +305,12 @@ __device__ __forceinline__ float dexcl_max(float v, float* tmp) {
 // Keys of the LDS store: per thread a contiguous range of `per` keys at the odd row stride
 // per | 1 (conflict-free scans); the global store (caches too long for LDS) uses stride per.
 constexpr int DEC_CAND = 128;                // keys of a bin ranked directly
-constexpr size_t DEC_AUX = 4096 * 4 + DEC_SEL_NT * 4 + 256;   // histogram, candidates, scratch
-bool decode_select_in_lds(int M) {   // the CU's 160 KB: M <= 33792
+// The histogram's 4096 bins: two 16-bit counters per word for rows staged in LDS (a bin never
+// holds more keys than the row, and those rows are far below 65536 keys), which keeps a 16k-key
+// row's workgroup under 80 KB (two per CU); 32-bit counters for the global store's long rows.
+constexpr int dec_hist_words(bool gkeys) { return gkeys ? 4096 : 2048; }
+constexpr size_t DEC_AUX = 2048 * 4 + DEC_SEL_NT * 4 + 256;   // histogram, candidates, scratch
+bool decode_select_in_lds(int M) {   // the CU's 160 KB: M <= 35840
   const int per = (M + DEC_SEL_NT - 1) / DEC_SEL_NT;
   return (size_t)DEC_SEL_NT * (per | 1) * 4 + DEC_AUX <= 160 * 1024;
 }
@@ -331,8 +335,9 @@ __global__ __launch_bounds__(NT) void decode_select_kernel(DecodeArgs a) {
   const int per = (m + NT - 1) / NT;
   const int PS = GKEYS ? per : (per | 1);
   uint32_t* ks = GKEYS ? a.keys + (int64_t)hi * NT * per_max : dsm;
-  int* hist = (int*)(dsm + (GKEYS ? 0 : NT * (per_max | 1)));   // 4096
-  uint32_t* cand = (uint32_t*)(hist + 4096);   // NT (16-byte aligned)
+  constexpr bool HPACK = !GKEYS;                // 16-bit bins, two per word
+  uint32_t* hist = dsm + (GKEYS ? 0 : NT * (per_max | 1));
+  uint32_t* cand = hist + dec_hist_words(GKEYS);   // NT (16-byte aligned)
   int* tmp = (int*)(cand + NT);        // NW
   int* misc = tmp + NW;                // 8
   const int j0 = tid * per, j1 = min(j0 + per, m);
@@ -381,13 +386,17 @@ __global__ __launch_bounds__(NT) void decode_select_kernel(DecodeArgs a) {
     for (int lv = 0; lv < 3; ++lv) {
       const int shift = lv == 0 ? 20 : (lv == 1 ? 8 : 0);
       const int nb = lv == 2 ? 256 : 4096;
-      for (int b = tid; b < nb; b += NT) hist[b] = 0;
+      for (int b = tid; b < (HPACK ? nb / 2 : nb); b += NT) hist[b] = 0u;
       cand[tid] = 0u;                          // 0 ranks below every key
       if (tid == 0) misc[4] = 0;
       __syncthreads();
       for (int e = 0; e < per; ++e) {
         const uint32_t k = myrow[e];
-        if (k != 0 && j0 + e < m && (k & pmask) == prefix) atomicAdd(&hist[(k >> shift) & (uint32_t)(nb - 1)], 1);
+        if (k != 0 && j0 + e < m && (k & pmask) == prefix) {
+          const uint32_t bin = (k >> shift) & (uint32_t)(nb - 1);
+          if constexpr (HPACK) atomicAdd(&hist[bin >> 1], 1u << ((bin & 1u) * 16));
+          else atomicAdd(&hist[bin], 1u);
+        }
       }
       __syncthreads();
       // bins in descending order, BPT per thread
@@ -395,7 +404,11 @@ __global__ __launch_bounds__(NT) void decode_select_kernel(DecodeArgs a) {
       const bool own = BPT * tid < nb;
       int c[BPT], sl = 0;
 #pragma unroll
-      for (int e = 0; e < BPT; ++e) { c[e] = own ? hist[nb - 1 - BPT * tid - e] : 0; sl += c[e]; }
+      for (int e = 0; e < BPT; ++e) {
+        const int bb = nb - 1 - BPT * tid - e;
+        c[e] = !own ? 0 : HPACK ? (int)((hist[bb >> 1] >> ((bb & 1) * 16)) & 0xffffu) : (int)hist[bb];
+        sl += c[e];
+      }
       const int excl = dexcl_sum<NW>(sl, tmp);
       if (own && excl < need && excl + sl >= need) {
         int acc = excl, d = nb - 1 - BPT * tid, e = 0;
@@ -562,7 +575,7 @@ __global__ __launch_bounds__(NT) void decode_select_kernel(DecodeArgs a) {
   // from the query backwards; key j of block b sits at dist = d[b] + (min(q_pos, end of b) - j)
   // with d[b] = kept keys after block b = total - (kept keys up to the end of b).  The inclusive
   // count at every block end goes to LDS (over the histogram, free by now).
-  int* bend = hist;
+  int* bend = (int*)hist;
   if (stream) {
     int rank = base - 1, tie = tie_base;
     for (int e = 0; e < j1 - j0; ++e) {
@@ -852,7 +865,7 @@ template <int NT>
 static hipError_t launch_select_t(const DecodeArgs& a, hipStream_t st) {
   const int per = (a.M + NT - 1) / NT;
   const bool in_lds = decode_select_in_lds(a.M);   // (the 1024-thread bound covers 512 threads)
-  const size_t lds = (in_lds ? (size_t)NT * (per | 1) * 4 : 0) + 4096 * 4 + NT * 4 + 256;
+  const size_t lds = (in_lds ? (size_t)NT * (per | 1) * 4 : 0) + (size_t)dec_hist_words(!in_lds) * 4 + NT * 4 + 256;
   if (in_lds) {
     hipError_t e = hipFuncSetAttribute((const void*)decode_select_kernel<false, NT>,
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);

@@ -256,7 +256,7 @@ def test_decode_workspace_size_matches_layout():
     n = lib.sta_decode_workspace_size(ctypes.byref(_decode_args()))
     need = 32 * 128 * 4 + 32 * 12288 * 4 + 32 * 4 + 32 * 32 * 130 * 4    # qrot, scores, sizes, splits
     assert need <= n < need + 5 * 256
-    # past the LDS key store (M > 33792) the selection keeps its keys in the workspace
+    # past the LDS key store (M > 35840) the selection keeps its keys in the workspace
     n2 = lib.sta_decode_workspace_size(ctypes.byref(_decode_args(M=40000, q_pos0=39999)))
     need2 = 32 * 128 * 4 + 32 * 40000 * 4 + 32 * 1024 * 40 * 4 + 32 * 4 + 32 * 32 * 130 * 4
     assert need2 <= n2 < need2 + 5 * 256
