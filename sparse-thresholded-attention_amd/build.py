@@ -17,7 +17,7 @@ OUT = os.path.join(HERE, "libsta_hip.so")
 BUILD = os.path.join(HERE, "_build")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = os.environ.get("STA_OFFLOAD_ARCH", "gfx950")
-SOURCES = ["sta_score.hip", "sta_select.hip", "sta_select_w.hip", "sta_gather.hip", "sta_pq.hip", "sta_stream.hip", "sta_api.hip",
+SOURCES = ["sta_score.hip", "sta_score6.hip", "sta_select.hip", "sta_select_w.hip", "sta_gather.hip", "sta_pq.hip", "sta_stream.hip", "sta_api.hip",
            "sta_dca.hip", "sta_api_pq.hip", "sta_api_stream.hip", "sta_api_dca.hip", "sta_decode.hip",
            "sta_api_decode.hip", "sta_rows.hip", "sta_dca_sel.hip", "sta_dca_dec.hip", "sta_chunk.hip"]
 FLAGS = ["--offload-arch=" + ARCH, "-O3", "-fPIC", "-std=c++17", "-Wall",
@@ -28,6 +28,7 @@ FLAGS = ["--offload-arch=" + ARCH, "-O3", "-fPIC", "-std=c++17", "-Wall",
 # per-source code-generation options: the score kernel keeps its MFMA accumulators in VGPRs (its
 # epilogue reads them every block) and its Q operands in AGPRs
 EXTRA = {"sta_score.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
+         "sta_score6.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
          "sta_rows.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]}
 
 

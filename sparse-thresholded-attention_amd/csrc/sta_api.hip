@@ -63,10 +63,12 @@ Layout layout_of(const sta_shared_args* a) {
   L.k_rows_pad = (int)(((kneed > a->N ? kneed : a->N) + 127) / 128 * 128);
   L.votes_stride = ((int64_t)a->N + 15) / 16 * 16;
   size_t off = 0;
+  // 16-bit inputs: the fragment regions carry the fp6 operands of pass 2
+  const bool with6 = a->dtype != STA_DTYPE_F32;
   L.qfrag_off = off;
-  off = align256(off + frag_region_bytes(a->H, L.q_rows_pad, a->D));
+  off = align256(off + frag_region_bytes(a->H, L.q_rows_pad, a->D, with6));
   L.kfrag_off = off;
-  off = align256(off + frag_region_bytes(a->Hkv, L.k_rows_pad, a->D));
+  off = align256(off + frag_region_bytes(a->Hkv, L.k_rows_pad, a->D, with6));
   L.votes_off = off;
   off = align256(off + (size_t)a->H * L.nt * L.votes_stride);
   L.wv_off = off;   // weighted votes (H, nt, votes_stride) fp32, for a weighted select_score only
@@ -169,12 +171,15 @@ int run_kernel_a(const sta_shared_args* a, const Layout& L, hipStream_t st) {
   u32x4* kfrag = (u32x4*)(ws + L.kfrag_off);
   int rc = mark(a, 0, st);
   if (rc != STA_OK) return rc;
+  // 16-bit inputs with plain votes score pass 2 with the fp6 correction (sta_fp6.h); fp32 inputs
+  // keep the three-product scores throughout
+  const bool want6 = a->dtype != STA_DTYPE_F32 && a->select_score == STA_SCORE_FREQ && !a->row_counts;
   hipError_t e = launch_rope_frag(a->dtype, a->D, a->q, a->q_head_stride, a->q_tok_stride, a->H, a->N,
                                   L.q_rows_pad, a->q_pos_base, a->pos_scale_a, a->rope_scale_a,
-                                  a->inv_freq_a, qfrag, st);
+                                  a->inv_freq_a, qfrag, st, want6);
   if (e != hipSuccess) return hip_fail(e, "rope pre-kernel (q)");
   e = launch_rope_frag(a->dtype, a->D, a->k, a->k_head_stride, a->k_tok_stride, a->Hkv, a->N,
-                       L.k_rows_pad, 0, a->pos_scale_a, a->rope_scale_a, a->inv_freq_a, kfrag, st);
+                       L.k_rows_pad, 0, a->pos_scale_a, a->rope_scale_a, a->inv_freq_a, kfrag, st, want6);
   if (e != hipSuccess) return hip_fail(e, "rope pre-kernel (k)");
   if ((rc = mark(a, 1, st)) != STA_OK) return rc;
   ScoreArgs sa{};
@@ -195,6 +200,7 @@ int run_kernel_a(const sta_shared_args* a, const Layout& L, hipStream_t st) {
   sa.votes_stride = L.votes_stride;
   sa.row_max = a->row_max;
   sa.row_counts = a->row_counts;
+  sa.want_fast6 = want6 ? 1 : 0;
   if (a->select_score != STA_SCORE_FREQ) {
     sa.wvotes = (float*)(ws + L.wv_off);
     e = launch_score_weighted(a->D, a->tile, a->select_score, sa, st);

@@ -259,6 +259,11 @@ __device__ __forceinline__ float min_arg_for(float thr, float c) {
 __device__ __forceinline__ void copy16_to_lds(const void* gsrc, uint32_t lds_base) {
   asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(gsrc), "{m0}"(lds_base) : "memory");
 }
+// the same copy with a wave-uniform 64-bit base in SGPRs and a per-lane 32-bit byte offset (lane
+// l's 16 bytes from sbase + voff): one offset register serves every copy of a wave
+__device__ __forceinline__ void copy16_to_lds_s(const void* sbase, uint32_t voff, uint32_t lds_base) {
+  asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "{m0}"(lds_base) : "memory");
+}
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   return (uint32_t)(size_t)(const __attribute__((address_space(3))) void*)p;
 }

@@ -3,6 +3,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 #include "sta_device.h"
+#include "sta_fp6.h"
 
 namespace sta {
 
@@ -10,10 +11,35 @@ namespace sta {
 // fragments (hi/lo bf16, 4 bytes per element), then per row (||hi||, ||lo||), then per head the
 // maxima of those two norms over its rows -- all three written by the RoPE pre-kernel -- then,
 // for the query side, the screened pass 1's results: each row's exact raw maximum and one
-// fallback flag per 256-row workgroup.
-inline size_t frag_region_bytes(int heads, int rows_pad, int D) {
+// fallback flag per 256-row workgroup.  After them (256-byte aligned) the fp6 correction
+// operands of the pass-2 kernel that scores with one bf16 product plus an fp6 correction
+// (sta_fp6.h): the e2m3 planes of each row's [hi | x - hi] vector, one E8M0 scale per 32
+// elements, per row the norms of the two halves' quantisation errors, and their per-head maxima.
+inline size_t frag_a256(size_t x) { return (x + 255) & ~(size_t)255; }
+inline size_t frag_base_bytes(int heads, int rows_pad, int D) {
   return (size_t)heads * rows_pad * D * 4 + (size_t)heads * rows_pad * 8 + (size_t)heads * 8 +
          (size_t)heads * rows_pad * 4 + (size_t)heads * (rows_pad / 256 + 1) * 4;
+}
+// fp6 planes: per (head, 32-row block) D/32 units of 3 planes x 64 lanes x 8 bytes (1.5 D bytes
+// per row); scales: per (head, 32-row block) 64 lane dwords
+inline size_t frag6_plane_bytes(int heads, int rows_pad, int D) { return (size_t)heads * rows_pad * D * 3 / 2; }
+// with6: the region carries the fp6 operands (only the shared path's pass 2 reads them)
+inline size_t frag_region_bytes(int heads, int rows_pad, int D, bool with6 = false) {
+  if (!with6) return frag_base_bytes(heads, rows_pad, D);
+  return frag_a256(frag_base_bytes(heads, rows_pad, D)) + frag_a256(frag6_plane_bytes(heads, rows_pad, D)) +
+         (size_t)heads * rows_pad * 8 + (size_t)heads * rows_pad * 8 + (size_t)heads * 8;
+}
+inline uint64_t* frag6_planes(const u32x4* frag, int heads, int rows_pad, int D) {
+  return (uint64_t*)((char*)frag + frag_a256(frag_base_bytes(heads, rows_pad, D)));
+}
+inline uint32_t* frag6_scales(const u32x4* frag, int heads, int rows_pad, int D) {
+  return (uint32_t*)((char*)frag6_planes(frag, heads, rows_pad, D) + frag_a256(frag6_plane_bytes(heads, rows_pad, D)));
+}
+inline float2* frag6_dnorms(const u32x4* frag, int heads, int rows_pad, int D) {
+  return (float2*)(frag6_scales(frag, heads, rows_pad, D) + (size_t)heads * rows_pad * 2);
+}
+inline float2* frag6_dnorm_max(const u32x4* frag, int heads, int rows_pad, int D) {
+  return frag6_dnorms(frag, heads, rows_pad, D) + (size_t)heads * rows_pad;
 }
 inline float2* frag_norms(const u32x4* frag, int heads, int rows_pad, int D) {
   return (float2*)((char*)frag + (size_t)heads * rows_pad * D * 4);
@@ -50,6 +76,18 @@ struct ScoreArgs {
   float* srmax;           // (H, q_rows_pad) the screen's exact raw row maxima
   int* sflags;            // (H, ngroups) the screen's fallback flags
   float* xthr;            // thresholds-only instance: (H, q_rows_pad) each row's x0 (+inf: no row)
+  // pass 2 with one bf16 product plus an fp6 correction (plain votes only, sta_score6.hip)
+  int want_fast6;         // caller: the fragments carry the fp6 operands (16-bit inputs)
+  int fast6;              // set by the launcher: the fp6 pass-2 kernel runs before the
+                          // three-product one, which then skips the workgroups it served
+  const float2* qnorm_max;// (H,) maxima of (||q_hi||, ||q_lo||)
+  const uint64_t* q6;     // fp6 planes / scales / error norms of the Q and K fragments
+  const uint32_t* q6sc;
+  const float2* q6dn;     // (H, q_rows_pad) per row
+  const float2* q6dmax;   // (H,)
+  const uint64_t* k6;
+  const uint32_t* k6sc;
+  const float2* k6dmax;   // (Hkv,)
 };
 
 struct SelectArgs {
@@ -290,9 +328,31 @@ hipError_t launch_decode_select(const DecodeArgs& a, hipStream_t st);
 int decode_nsplit(int k_max);
 hipError_t launch_decode_attend(int dtype, int D, const DecodeArgs& a, hipStream_t st);
 
+// Whether the fp6 pass-2 kernel (sta_score6.hip) serves workgroup g (wg_rows query rows) of
+// head h in the plain pass 2; the three-product kernel then skips it.  It does when the launcher
+// enabled it, the screened pass 1 resolved every row of the workgroup (its 256-row workgroups
+// raised no fallback flag) and the head's fp6 error estimate stays within the limit.  Both
+// kernels evaluate this one function on the same inputs.
+__device__ inline bool fast6_serves(const ScoreArgs& a, int h, int g, int D, int wg_rows) {
+  if (!a.fast6) return false;
+  const int rows_total = a.q_rows_pad;
+  constexpr int SG = 256;
+  const int ng_s = (rows_total + SG - 1) / SG;
+  for (int gs = g * wg_rows / SG; gs < min((g + 1) * wg_rows / SG, ng_s); ++gs)
+    if (a.sflags[h * ng_s + gs] != 0) return false;
+  const int kvh = h / (a.H / a.Hkv);
+  const float2 qn = a.qnorm_max[h], kn = a.knorm_max[kvh], qd = a.q6dmax[h], kd = a.k6dmax[kvh];
+  const float sg = fast6_sigma(qn.x, qn.y, qd.x, qd.y, kn.x, kn.y, kd.x, kd.y, a.sm_scale, D);
+  return sg <= FAST6_SIGMA_LIMIT;
+}
+
+// want6: also write the fp6 correction operands of the fragment region
 hipError_t launch_rope_frag(int dtype, int D, const void* x, int64_t head_stride, int64_t tok_stride,
                             int heads, int N, int rows_pad, int pos_base, float pos_scale,
-                            float rope_scale, const float* inv_freq, u32x4* frag, hipStream_t st);
+                            float rope_scale, const float* inv_freq, u32x4* frag, hipStream_t st,
+                            bool want6 = false);
+// the fp6 pass-2 kernel (plain votes); the launcher of the score passes calls it
+hipError_t launch_score6(int D, int tile, const ScoreArgs& a, hipStream_t st);
 hipError_t launch_score(int D, int tile, const ScoreArgs& a, hipStream_t st);
 hipError_t launch_score_pq(int D, int wmode, const ScoreArgs& a, hipStream_t st);
 // the screen + pass 1 only, writing each row's keep threshold to a.xthr (tile 32)

@@ -14,6 +14,7 @@
 // A 32-row block's operand for one k step is one contiguous 1 KB load per wave.
 #include "sta_device.h"
 #include "sta_kernels.h"
+#include "sta_fp6.h"
 
 #include <float.h>
 #include <stdlib.h>
@@ -36,12 +37,87 @@ namespace sta {
 // they are computed once and reused for every head of the group.
 constexpr int ROPE_HG = 4;
 
+// The fp6 correction operands of one row part (sta_fp6.h): the row's vector [hi | x - hi] is cut
+// into 32-element blocks, each rounded to e2m3 under its own E8M0 scale.  Block b of a 32-row
+// block's row r sits in unit b / 2, lane r + 32 (b % 2): 32 elements of 6 bits, element p at bits
+// 6p .. 6p + 5 of the lane's 24 bytes, stored as three planes of 64 lanes x 8 bytes (unit = 1536
+// bytes), so that an MFMA operand is three conflict-free 8-byte LDS reads.  The lane's scale
+// dword holds the scale of block 2m + (b % 2) in byte m.  The four threads of a block (c % 4 =
+// t) each hold 8 elements (48 bits, bits 48t ..): thread t < 3 writes plane t, which takes its
+// bits from threads t and t + 1.  Per row: (||Q6(hi) - hi||, ||Q6(x - hi) - (x - hi)||).
+template <int D>
+__device__ __forceinline__ void write_fp6(const float* o1, const float* o2, const u32x4& hi1, const u32x4& hi2, int c,
+                                          int row, int head, int rows_pad, uint64_t* planes6, uint32_t* scales6,
+                                          float2* dnorms6) {
+#pragma clang fp contract(off)
+  constexpr int C2 = D / 16, NU = D / 32;
+  float g[4][8];   // hi of dims i0.., hi of dims D/2 + i0.., and the two residuals
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    g[0][2 * e] = __uint_as_float(hi1[e] << 16);
+    g[0][2 * e + 1] = __uint_as_float(hi1[e] & 0xffff0000u);
+    g[1][2 * e] = __uint_as_float(hi2[e] << 16);
+    g[1][2 * e + 1] = __uint_as_float(hi2[e] & 0xffff0000u);
+  }
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    g[2][e] = o1[e] - g[0][e];   // exact
+    g[3][e] = o2[e] - g[1][e];
+  }
+  const int t = c & 3, b0 = (c * 8) / 32, rb = row >> 5, lr = row & 31;
+  const int blk[4] = {b0, b0 + D / 64, D / 32 + b0, D / 32 + D / 64 + b0};
+  const int64_t rbase = ((int64_t)head * (rows_pad >> 5) + rb) * NU;
+  const int lane = threadIdx.x & 63;
+  float dh = 0.0f, dr = 0.0f;
+  uint32_t sc[2] = {0u, 0u};
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    float bm = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) bm = fmaxf(bm, fabsf(g[q][e]));
+    bm = fmaxf(bm, __shfl_xor(bm, 1, 64));
+    bm = fmaxf(bm, __shfl_xor(bm, 2, 64));
+    const int ex = e2m3_block_exp(bm);
+    uint64_t v = 0;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      float qv;
+      const uint32_t code = e2m3_encode(g[q][e], ex, &qv);
+      v |= (uint64_t)code << (6 * e);
+      const float d = qv - g[q][e];
+      if (q < 2) dh = fmaf(d, d, dh); else dr = fmaf(d, d, dr);
+    }
+    const uint32_t nlo = (uint32_t)__shfl((int)(uint32_t)v, lane + 1, 64);
+    const uint32_t nhi = (uint32_t)__shfl((int)(uint32_t)(v >> 32), lane + 1, 64);
+    const uint64_t vn = ((uint64_t)nhi << 32) | nlo;
+    const int b = blk[q];
+    if (t < 3) {
+      const uint64_t w = (v >> (16 * t)) | (vn << (48 - 16 * t));
+      planes6[(rbase + (b >> 1)) * 192 + t * 64 + lr + 32 * (b & 1)] = w;
+    }
+    sc[b & 1] |= (uint32_t)(ex + 127) << (8 * (b >> 1));
+  }
+  if (t == 0) {
+    const int64_t sb = ((int64_t)head * (rows_pad >> 5) + rb) * 64 + lr;
+    if (D == 64 || b0 == 0) scales6[sb] = sc[0];
+    if (D == 64 || b0 == 1) scales6[sb + 32] = sc[1];
+  }
+#pragma unroll
+  for (int o = 1; o < C2; o <<= 1) {
+    dh += __shfl_xor(dh, o, 64);
+    dr += __shfl_xor(dr, o, 64);
+  }
+  if (c == 0) dnorms6[(int64_t)head * rows_pad + row] = make_float2(sqrtf(dh), sqrtf(dr));
+}
+
 template <int DT, int D>
 __global__ __launch_bounds__(256) void rope_frag_kernel(const void* __restrict__ x, int64_t head_stride,
                                                         int64_t tok_stride, int heads, int N, int rows_pad,
                                                         int pos_base, float pos_scale, float rope_scale,
                                                         const float* __restrict__ inv_freq,
-                                                        u32x4* __restrict__ frag, float2* __restrict__ norms) {
+                                                        u32x4* __restrict__ frag, float2* __restrict__ norms,
+                                                        uint64_t* __restrict__ planes6, uint32_t* __restrict__ scales6,
+                                                        float2* __restrict__ dnorms6) {
 #pragma clang fp contract(off)
   constexpr int C2 = D / 16;                 // threads per row
   const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
@@ -117,6 +193,7 @@ __global__ __launch_bounds__(256) void rope_frag_kernel(const void* __restrict__
       sl += __shfl_xor(sl, o, 64);
     }
     if (c == 0) norms[(int64_t)head * rows_pad + row] = make_float2(sqrtf(sh), sqrtf(sl));
+    if (planes6) write_fp6<D>(o1, o2, hi1, hi2, c, row, head, rows_pad, planes6, scales6, dnorms6);
   }
 }
 
@@ -244,6 +321,10 @@ void score_kernel(ScoreArgs a) {
       h = bid % a.H;
       g = ngroups - 1 - bid / a.H;
     }
+  }
+  // plain votes: the workgroups the fp6 pass-2 kernel served are done
+  if constexpr (MODE == 0 && PLAIN) {
+    if (fast6_serves(a, h, g, D, WG_ROWS)) return;
   }
   const int kvh = h / (a.H / a.Hkv);
   const int wrow0 = g * WG_ROWS + wave * 32 * RB;  // first row of this wave
@@ -1183,25 +1264,33 @@ void score_kernel(ScoreArgs a) {
 template <int DT, int D>
 static hipError_t launch_rope_frag_t(const void* x, int64_t hs, int64_t ts, int heads, int N, int rows_pad,
                                      int pos_base, float pos_scale, float rope_scale, const float* inv_freq,
-                                     u32x4* frag, hipStream_t st) {
+                                     u32x4* frag, hipStream_t st, bool want6) {
   const int64_t total = (int64_t)rows_pad * (D / 16);
   const int64_t blocks = (total + 255) / 256;
   float2* norms = frag_norms(frag, heads, rows_pad, D);
+  uint64_t* planes6 = want6 ? frag6_planes(frag, heads, rows_pad, D) : nullptr;
+  uint32_t* scales6 = frag6_scales(frag, heads, rows_pad, D);
+  float2* dn6 = frag6_dnorms(frag, heads, rows_pad, D);
   const dim3 grid((unsigned)blocks, (unsigned)((heads + ROPE_HG - 1) / ROPE_HG));
   hipLaunchKernelGGL((rope_frag_kernel<DT, D>), grid, dim3(256), 0, st, x, hs, ts, heads, N,
-                     rows_pad, pos_base, pos_scale, rope_scale, inv_freq, frag, norms);
+                     rows_pad, pos_base, pos_scale, rope_scale, inv_freq, frag, norms, planes6, scales6, dn6);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(norm_max_kernel, dim3(heads), dim3(1024), 0, st, (const float2*)norms, rows_pad,
                      frag_norm_max(frag, heads, rows_pad, D));
+  if (want6) {
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    hipLaunchKernelGGL(norm_max_kernel, dim3(heads), dim3(1024), 0, st, (const float2*)dn6, rows_pad,
+                       frag6_dnorm_max(frag, heads, rows_pad, D));
+  }
   return hipGetLastError();
 }
 
 hipError_t launch_rope_frag(int dtype, int D, const void* x, int64_t hs, int64_t ts, int heads, int N,
                             int rows_pad, int pos_base, float pos_scale, float rope_scale,
-                            const float* inv_freq, u32x4* frag, hipStream_t st) {
+                            const float* inv_freq, u32x4* frag, hipStream_t st, bool want6) {
 #define STA_RF(DT_, D_) \
-  if (dtype == DT_ && D == D_) return launch_rope_frag_t<DT_, D_>(x, hs, ts, heads, N, rows_pad, pos_base, pos_scale, rope_scale, inv_freq, frag, st);
+  if (dtype == DT_ && D == D_) return launch_rope_frag_t<DT_, D_>(x, hs, ts, heads, N, rows_pad, pos_base, pos_scale, rope_scale, inv_freq, frag, st, want6);
   STA_RF(DT_F32, 64) STA_RF(DT_F32, 128) STA_RF(DT_BF16, 64) STA_RF(DT_BF16, 128)
   STA_RF(DT_F16, 64) STA_RF(DT_F16, 128)
 #undef STA_RF
@@ -1209,9 +1298,14 @@ hipError_t launch_rope_frag(int dtype, int D, const void* x, int64_t hs, int64_t
 }
 
 // STA_EXACT_PASS1=1 in the environment (read at every launch) makes every workgroup run the
-// three-product pass 1 sweep, for comparisons against the screened sweep
+// three-product pass 1 sweep, for comparisons against the screened sweep; STA_EXACT_PASS2=1 keeps
+// every workgroup on the three-product pass 2 (no fp6 correction kernel)
 static int exact_pass1_forced() {
   const char* e = getenv("STA_EXACT_PASS1");
+  return e && e[0] == '1' ? 1 : 0;
+}
+static int exact_pass2_forced() {
+  const char* e = getenv("STA_EXACT_PASS2");
   return e && e[0] == '1' ? 1 : 0;
 }
 
@@ -1233,9 +1327,27 @@ static hipError_t launch_score_t(const ScoreArgs& a0, hipStream_t st) {
   a.srmax = frag_rowmax(a.qfrag, a.H, a.q_rows_pad, D);
   a.sflags = frag_flags(a.qfrag, a.H, a.q_rows_pad, D);
   a.screened = a.ib != 0 && !a.exact_pass1;
+  // plain votes from 16-bit inputs: the fp6 pass-2 kernel first (the workgroups whose screen
+  // resolved and whose head passes the error guard), the three-product kernel for the rest
+  constexpr bool PLAIN = PQ == 0 && !RC;
+  a.fast6 = (PLAIN && a.screened && a.want_fast6 && !exact_pass2_forced()) ? 1 : 0;
+  if (a.fast6) {
+    a.qnorm_max = frag_norm_max(a.qfrag, a.H, a.q_rows_pad, D);
+    a.q6 = frag6_planes(a.qfrag, a.H, a.q_rows_pad, D);
+    a.q6sc = frag6_scales(a.qfrag, a.H, a.q_rows_pad, D);
+    a.q6dn = frag6_dnorms(a.qfrag, a.H, a.q_rows_pad, D);
+    a.q6dmax = frag6_dnorm_max(a.qfrag, a.H, a.q_rows_pad, D);
+    a.k6 = frag6_planes(a.kfrag, a.Hkv, a.k_rows_pad, D);
+    a.k6sc = frag6_scales(a.kfrag, a.Hkv, a.k_rows_pad, D);
+    a.k6dmax = frag6_dnorm_max(a.kfrag, a.Hkv, a.k_rows_pad, D);
+  }
   if (a.screened) {
     // the screen is the same for every pass-2 epilogue: one instance per (D, T)
     hipLaunchKernelGGL((score_kernel<D, T, false, 0, RB, 1>), dim3(a.H * ng_s), dim3(64 * WS), 0, st, a);
+  }
+  if (a.fast6) {
+    const hipError_t e = launch_score6(D, T, a, st);
+    if (e != hipSuccess) return e;
   }
   hipLaunchKernelGGL((score_kernel<D, T, RC, PQ, RB, 0>), dim3(a.H * ng_2), dim3(64 * W2), 0, st, a);
   return hipGetLastError();

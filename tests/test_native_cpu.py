@@ -49,8 +49,12 @@ def test_workspace_size_matches_layout():
     # q / k fragments (hi + lo bf16), per-row (||hi||, ||lo||) and per-head maxima of those, then
     # the screened pass 1's row maxima and per-workgroup flags
     screen = 32 * 12288 * 4 + 32 * (12288 // 256 + 1) * 4
-    q = 32 * 12288 * 128 * 4 + 32 * 12288 * 8 + 32 * 8 + screen
-    k = 32 * 12288 * 128 * 4 + 32 * 12288 * 8 + 32 * 8 + screen
+    # the fp6 correction operands: e2m3 planes of [hi | x - hi] (1.5 D bytes per row), a scale
+    # dword per lane (8 bytes per row), per row the two quantisation-error norms, per head their
+    # maxima
+    fp6 = 32 * 12288 * 128 * 3 // 2 + 32 * 12288 * 8 + 32 * 12288 * 8 + 32 * 8
+    q = 32 * 12288 * 128 * 4 + 32 * 12288 * 8 + 32 * 8 + screen + fp6
+    k = 32 * 12288 * 128 * 4 + 32 * 12288 * 8 + 32 * 8 + screen + fp6
     votes = 32 * nt * 12288             # byte votes, one row per tile
     assert n >= q + k + votes and n < q + k + votes + 4096
 
