@@ -11,8 +11,8 @@
 // error of ~2^-5 on a term of ~2^-8 leaves an error of ~1e-4 on unit-scale scores.  That error is
 // statistical (a sum of independent roundings), so every head is guarded: the correction's
 // standard deviation for the head's largest-norm rows must stay below a quarter of the band, or
-// the head takes the three-product pass 2 (fast6_sigma below).  Plain C++: the host-side tests
-// compile this header too.
+// the head takes the three-product pass 2 (fast6_sigma below).  The rounding itself is the
+// hardware's (v_cvt_scalef32_2xpk16_fp6_f32, round to nearest even).  Plain C++.
 #pragma once
 #include <math.h>
 #include <stdint.h>
@@ -38,46 +38,18 @@ STA_HD inline uint32_t fp6_f2u(float x) {
 }
 
 // E8M0 exponent of a block whose largest magnitude is bm: the smallest e with bm <= 7.5 * 2^e
-// (7.5 is e2m3's largest value), clamped to [-127, 127]; 0 for a zero (or NaN) block.
+// (7.5 is e2m3's largest value), clamped to [-126, 127] so that 2^e is a normal fp32 scale (the
+// hardware conversion reads the scale's exponent); 0 for a zero (or NaN) block.
 // bm = 1.f * 2^(E - 127) fits under 7.5 * 2^(E - 129) exactly when 1.f <= 1.875.
 STA_HD inline int e2m3_block_exp(float bm) {
   if (!(bm > 0.0f)) return 0;
   const uint32_t u = fp6_f2u(bm);
   const int E = (int)((u >> 23) & 0xff);
-  if (E == 0) return -127;                       // subnormal: any scale down to 2^-127 fits
+  if (E == 0) return -126;                       // subnormal: the smallest scale fits
   int e = (u & 0x7fffffu) <= 0x700000u ? E - 129 : E - 128;
   if (e > 127) e = 127;
-  if (e < -127) e = -127;
+  if (e < -126) e = -126;
   return e;
-}
-
-// x / 2^e rounded to nearest even on the e2m3 grid: steps of 1/8 below 2 (the subnormals and the
-// first binade share that step), 1/4 in [2, 4) and 1/2 in [4, 7.5].  Returns the 6-bit code
-// (sign << 5 | exponent << 3 | mantissa) and the represented value times 2^e in *q.
-STA_HD inline uint32_t e2m3_encode(float x, int e, float* q) {
-  const float y = ldexpf(x, -e);
-  const float a = fabsf(y);
-  uint32_t code;
-  float v;
-  if (a < 2.0f) {
-    const float n = rintf(a * 8.0f);
-    code = (uint32_t)n;
-    v = n * 0.125f;
-  } else if (a < 4.0f) {
-    const float n = rintf(a * 4.0f);
-    code = (uint32_t)n + 8u;
-    v = n * 0.25f;
-  } else {
-    const float n = rintf(a * 2.0f);
-    code = (uint32_t)n + 16u;
-    v = n * 0.5f;
-  }
-  if (fp6_f2u(y) >> 31) {
-    code |= 32u;
-    v = -v;
-  }
-  *q = ldexpf(v, e);
-  return code;
 }
 
 // Standard deviation of the fp6 correction's error on the scaled score for rows with norms

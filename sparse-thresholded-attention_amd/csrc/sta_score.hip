@@ -37,71 +37,114 @@ namespace sta {
 // they are computed once and reused for every head of the group.
 constexpr int ROPE_HG = 4;
 
-// The fp6 correction operands of one row part (sta_fp6.h): the row's vector [hi | x - hi] is cut
-// into 32-element blocks, each rounded to e2m3 under its own E8M0 scale.  Block b of a 32-row
-// block's row r sits in unit b / 2, lane r + 32 (b % 2): 32 elements of 6 bits, element p at bits
-// 6p .. 6p + 5 of the lane's 24 bytes, stored as three planes of 64 lanes x 8 bytes (unit = 1536
-// bytes), so that an MFMA operand is three conflict-free 8-byte LDS reads.  The lane's scale
-// dword holds the scale of block 2m + (b % 2) in byte m.  The four threads of a block (c % 4 =
-// t) each hold 8 elements (48 bits, bits 48t ..): thread t < 3 writes plane t, which takes its
-// bits from threads t and t + 1.  Per row: (||Q6(hi) - hi||, ||Q6(x - hi) - (x - hi)||).
+// The fp6 correction operands (sta_fp6.h): the row's vector [hi | x - hi] is cut into 32-element
+// blocks, each rounded to e2m3 under its own E8M0 scale.  Block b of a 32-row block's row r sits
+// in unit b / 2, lane r + 32 (b % 2): 32 elements of 6 bits, element p at bits 6p .. 6p + 5 of
+// the lane's 24 bytes, stored as three planes of 64 lanes x 8 bytes (unit = 1536 bytes), so that
+// an MFMA operand is three conflict-free 8-byte LDS reads.  The lane's scale dword holds the scale
+// of block 2m + (b % 2) in byte m.  Per row: (||Q6(hi) - hi||, ||Q6(x - hi) - (x - hi)||).
+//
+// A row's C2 threads (one wave holds whole rows) each computed 8 dims of both rotation halves;
+// they trade them through the wave's LDS rows so that thread c holds all of block c, which
+// v_cvt_scalef32_2xpk16_fp6_f32 rounds to nearest even in one instruction (element 2i from its
+// first source, 2i + 1 from its second; checked on an MI355X against sta_fp6.h's software
+// encoder), and v_cvt_scalef32_pk32_f32_fp6 decodes for the error norm.  Both go through inline
+// assembly with an early-clobber result: the compiler's builtin may place the result over the
+// second source, and the instruction then reads back part of its own result.
+typedef float f32x16v __attribute__((ext_vector_type(16)));
+typedef float f32x32v __attribute__((ext_vector_type(32)));
+typedef int i32x6v __attribute__((ext_vector_type(6)));
+__device__ __forceinline__ i32x6v cvt_fp6x32(const f32x16v& even, const f32x16v& odd, float scale) {
+  i32x6v r;
+  asm volatile("v_cvt_scalef32_2xpk16_fp6_f32 %0, %1, %2, %3" : "=&v"(r) : "v"(even), "v"(odd), "v"(scale));
+  return r;
+}
+__device__ __forceinline__ f32x32v dec_fp6x32(const i32x6v& codes, float scale) {
+  f32x32v r;
+  asm volatile("v_cvt_scalef32_pk32_f32_fp6 %0, %1, %2" : "=&v"(r) : "v"(codes), "v"(scale));
+  return r;
+}
+// LDS per wave: its rows' [hi | x - hi] vectors, element p of block b at (p / 4 * NB + b) * 4 +
+// p % 4 (the reads of a block's 16-byte groups by consecutive threads are then contiguous), rows
+// 2D + 32 floats apart (two rows in one 16-lane read phase fall on different banks)
+template <int D>
+struct Fp6Rows {
+  static constexpr int NB = D / 16;                 // 32-element blocks per row
+  static constexpr int RS = 2 * D + 32;             // row stride in floats
+  static constexpr int ROWS = 64 / (D / 16);        // rows per wave
+  __device__ static __forceinline__ int at(int b, int p) { return ((p >> 2) * NB + b) * 4 + (p & 3); }
+};
 template <int D>
 __device__ __forceinline__ void write_fp6(const float* o1, const float* o2, const u32x4& hi1, const u32x4& hi2, int c,
-                                          int row, int head, int rows_pad, uint64_t* planes6, uint32_t* scales6,
-                                          float2* dnorms6) {
+                                          int row, int head, int rows_pad, float* wlds, uint64_t* planes6,
+                                          uint32_t* scales6, float2* dnorms6) {
 #pragma clang fp contract(off)
-  constexpr int C2 = D / 16, NU = D / 32;
-  float g[4][8];   // hi of dims i0.., hi of dims D/2 + i0.., and the two residuals
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    g[0][2 * e] = __uint_as_float(hi1[e] << 16);
-    g[0][2 * e + 1] = __uint_as_float(hi1[e] & 0xffff0000u);
-    g[1][2 * e] = __uint_as_float(hi2[e] << 16);
-    g[1][2 * e + 1] = __uint_as_float(hi2[e] & 0xffff0000u);
-  }
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    g[2][e] = o1[e] - g[0][e];   // exact
-    g[3][e] = o2[e] - g[1][e];
-  }
-  const int t = c & 3, b0 = (c * 8) / 32, rb = row >> 5, lr = row & 31;
-  const int blk[4] = {b0, b0 + D / 64, D / 32 + b0, D / 32 + D / 64 + b0};
-  const int64_t rbase = ((int64_t)head * (rows_pad >> 5) + rb) * NU;
+  using R = Fp6Rows<D>;
+  constexpr int C2 = D / 16, NB = R::NB;
   const int lane = threadIdx.x & 63;
-  float dh = 0.0f, dr = 0.0f;
-  uint32_t sc[2] = {0u, 0u};
+  float* rl = wlds + (lane / C2) * R::RS;
+  {
+    // this thread's 8 dims of each half: block b0 (+ D/64 for the second half, + D/32 for the
+    // residuals), positions 8 (c % 4) ..
+    float hv[2][8], rv[2][8];
 #pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    float bm = 0.0f;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) bm = fmaxf(bm, fabsf(g[q][e]));
-    bm = fmaxf(bm, __shfl_xor(bm, 1, 64));
-    bm = fmaxf(bm, __shfl_xor(bm, 2, 64));
-    const int ex = e2m3_block_exp(bm);
-    uint64_t v = 0;
+    for (int e = 0; e < 4; ++e) {
+      hv[0][2 * e] = __uint_as_float(hi1[e] << 16);
+      hv[0][2 * e + 1] = __uint_as_float(hi1[e] & 0xffff0000u);
+      hv[1][2 * e] = __uint_as_float(hi2[e] << 16);
+      hv[1][2 * e + 1] = __uint_as_float(hi2[e] & 0xffff0000u);
+    }
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      float qv;
-      const uint32_t code = e2m3_encode(g[q][e], ex, &qv);
-      v |= (uint64_t)code << (6 * e);
-      const float d = qv - g[q][e];
-      if (q < 2) dh = fmaf(d, d, dh); else dr = fmaf(d, d, dr);
+      rv[0][e] = o1[e] - hv[0][e];   // exact
+      rv[1][e] = o2[e] - hv[1][e];
     }
-    const uint32_t nlo = (uint32_t)__shfl((int)(uint32_t)v, lane + 1, 64);
-    const uint32_t nhi = (uint32_t)__shfl((int)(uint32_t)(v >> 32), lane + 1, 64);
-    const uint64_t vn = ((uint64_t)nhi << 32) | nlo;
-    const int b = blk[q];
-    if (t < 3) {
-      const uint64_t w = (v >> (16 * t)) | (vn << (48 - 16 * t));
-      planes6[(rbase + (b >> 1)) * 192 + t * 64 + lr + 32 * (b & 1)] = w;
-    }
-    sc[b & 1] |= (uint32_t)(ex + 127) << (8 * (b >> 1));
+    const int b0 = (c * 8) / 32, p0 = 8 * (c & 3);
+#pragma unroll
+    for (int half = 0; half < 2; ++half)
+#pragma unroll
+      for (int k = 0; k < 2; ++k) {
+        const int bh = b0 + half * (D / 64), br = bh + D / 32, p = p0 + 4 * k;
+        *(float4*)(rl + R::at(bh, p)) = make_float4(hv[half][4 * k], hv[half][4 * k + 1], hv[half][4 * k + 2], hv[half][4 * k + 3]);
+        *(float4*)(rl + R::at(br, p)) = make_float4(rv[half][4 * k], rv[half][4 * k + 1], rv[half][4 * k + 2], rv[half][4 * k + 3]);
+      }
   }
-  if (t == 0) {
-    const int64_t sb = ((int64_t)head * (rows_pad >> 5) + rb) * 64 + lr;
-    if (D == 64 || b0 == 0) scales6[sb] = sc[0];
-    if (D == 64 || b0 == 1) scales6[sb + 32] = sc[1];
+  // the wave's LDS operations complete in order: its rows are whole before the reads below
+  __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0)
+  __builtin_amdgcn_wave_barrier();
+  // thread c takes block c of its row
+  const int b = c;
+  f32x16v ev, od;
+  float bm = 0.0f;
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const float4 v = *(const float4*)(rl + R::at(b, 4 * k));
+    ev[2 * k] = v.x;
+    od[2 * k] = v.y;
+    ev[2 * k + 1] = v.z;
+    od[2 * k + 1] = v.w;
+    bm = fmaxf(bm, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
   }
+  __builtin_amdgcn_wave_barrier();   // the next head's writes follow every read of this one
+  const int ex = e2m3_block_exp(bm);
+  const float scale = __uint_as_float((uint32_t)(ex + 127) << 23);
+  const i32x6v codes = cvt_fp6x32(ev, od, scale);
+  const f32x32v dq = dec_fp6x32(codes, scale);
+  float d2 = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const float d0 = dq[2 * i] - ev[i], d1 = dq[2 * i + 1] - od[i];
+    d2 = fmaf(d0, d0, d2);
+    d2 = fmaf(d1, d1, d2);
+  }
+  const int rb = row >> 5, lr = row & 31;
+  const int64_t u = (((int64_t)head * (rows_pad >> 5) + rb) * (D / 32) + (b >> 1)) * 192 + lr + 32 * (b & 1);
+#pragma unroll
+  for (int j = 0; j < 3; ++j)
+    planes6[u + 64 * j] = (uint64_t)(uint32_t)codes[2 * j] | ((uint64_t)(uint32_t)codes[2 * j + 1] << 32);
+  ((uint8_t*)scales6)[(((int64_t)head * (rows_pad >> 5) + rb) * 64 + lr + 32 * (b & 1)) * 4 + (b >> 1)] = (uint8_t)(ex + 127);
+  // per row: the hi blocks' and the residual blocks' squared errors
+  float dh = b < NB / 2 ? d2 : 0.0f, dr = b < NB / 2 ? 0.0f : d2;
 #pragma unroll
   for (int o = 1; o < C2; o <<= 1) {
     dh += __shfl_xor(dh, o, 64);
@@ -110,7 +153,7 @@ __device__ __forceinline__ void write_fp6(const float* o1, const float* o2, cons
   if (c == 0) dnorms6[(int64_t)head * rows_pad + row] = make_float2(sqrtf(dh), sqrtf(dr));
 }
 
-template <int DT, int D>
+template <int DT, int D, bool W6>
 __global__ __launch_bounds__(256) void rope_frag_kernel(const void* __restrict__ x, int64_t head_stride,
                                                         int64_t tok_stride, int heads, int N, int rows_pad,
                                                         int pos_base, float pos_scale, float rope_scale,
@@ -121,6 +164,8 @@ __global__ __launch_bounds__(256) void rope_frag_kernel(const void* __restrict__
 #pragma clang fp contract(off)
   constexpr int C2 = D / 16;                 // threads per row
   const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  // the fp6 operands' row exchange (LDS, per wave: rows never span waves)
+  __shared__ float lds6[4][W6 ? Fp6Rows<D>::ROWS * Fp6Rows<D>::RS : 1];
   if (gid >= (int64_t)rows_pad * C2) return;
   const int c = (int)(gid % C2);
   const int row = (int)(gid / C2);
@@ -193,7 +238,7 @@ __global__ __launch_bounds__(256) void rope_frag_kernel(const void* __restrict__
       sl += __shfl_xor(sl, o, 64);
     }
     if (c == 0) norms[(int64_t)head * rows_pad + row] = make_float2(sqrtf(sh), sqrtf(sl));
-    if (planes6) write_fp6<D>(o1, o2, hi1, hi2, c, row, head, rows_pad, planes6, scales6, dnorms6);
+    if constexpr (W6) write_fp6<D>(o1, o2, hi1, hi2, c, row, head, rows_pad, lds6[threadIdx.x >> 6], planes6, scales6, dnorms6);
   }
 }
 
@@ -1272,8 +1317,12 @@ static hipError_t launch_rope_frag_t(const void* x, int64_t hs, int64_t ts, int 
   uint32_t* scales6 = frag6_scales(frag, heads, rows_pad, D);
   float2* dn6 = frag6_dnorms(frag, heads, rows_pad, D);
   const dim3 grid((unsigned)blocks, (unsigned)((heads + ROPE_HG - 1) / ROPE_HG));
-  hipLaunchKernelGGL((rope_frag_kernel<DT, D>), grid, dim3(256), 0, st, x, hs, ts, heads, N,
-                     rows_pad, pos_base, pos_scale, rope_scale, inv_freq, frag, norms, planes6, scales6, dn6);
+  if (want6)
+    hipLaunchKernelGGL((rope_frag_kernel<DT, D, true>), grid, dim3(256), 0, st, x, hs, ts, heads, N,
+                       rows_pad, pos_base, pos_scale, rope_scale, inv_freq, frag, norms, planes6, scales6, dn6);
+  else
+    hipLaunchKernelGGL((rope_frag_kernel<DT, D, false>), grid, dim3(256), 0, st, x, hs, ts, heads, N,
+                       rows_pad, pos_base, pos_scale, rope_scale, inv_freq, frag, norms, planes6, scales6, dn6);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(norm_max_kernel, dim3(heads), dim3(1024), 0, st, (const float2*)norms, rows_pad,
