@@ -27,6 +27,71 @@ from _shared_prefill import shared_prefill
 PER_QUERY_BATCH = 256          # queries per per-query launch: bounds the (H, Q, M) score buffer
 
 
+# ---------------------------------------------------------------------------------------------
+# what every patched forward does around its kernels
+# ---------------------------------------------------------------------------------------------
+def _cached_length(cache, layer_idx):
+    """Tokens already in the layer's cache: a transformers Cache (get_seq_length, with or without
+    the layer argument) or a legacy tuple of (k, v) per layer."""
+    if cache is None:
+        return 0
+    if hasattr(cache, "get_seq_length"):
+        try:
+            return int(cache.get_seq_length(layer_idx))
+        except TypeError:
+            return int(cache.get_seq_length())
+    return 0 if hasattr(cache, "update") else int(cache[layer_idx][0].shape[2])
+
+
+def _cache_append(cache, k, v, layer_idx):
+    """The layer's keys / values with this call's appended (the cache keeps them)."""
+    if cache is None:
+        return k, v
+    if hasattr(cache, "update"):
+        return cache.update(k, v, layer_idx)
+    pk, pv = cache[layer_idx]
+    return torch.cat([pk, k], dim=2), torch.cat([pv, v], dim=2)
+
+
+class _AttnCall:
+    """One attention call's projections: q (1, H, N, D), the new raw keys / values k_new, v_new
+    (1, Hkv, N, D), the cache's keys / values after the append, k, v (1, Hkv, past + N, D) -- the
+    cache stores keys_for_cache(k_new) -- and past, the tokens cached before the call."""
+
+    def __init__(self, module, hidden_states, past_key_values, kwargs, layer_idx, keys_for_cache=None):
+        B, N, _ = hidden_states.shape
+        assert B == 1, "batch size must be 1 (the kernels take one sequence, as the reference's)"
+        shape = (B, N, -1, module.head_dim)
+        self.N = N
+        self.q, self.k_new, self.v_new = (proj(hidden_states).view(shape).transpose(1, 2)
+                                          for proj in (module.q_proj, module.k_proj, module.v_proj))
+        # transformers passes the cache as past_key_values, or (older paths) past_key_value
+        cache = past_key_values if past_key_values is not None else kwargs.get("past_key_value", None)
+        self.past = _cached_length(cache, layer_idx)
+        stored = keys_for_cache(self.k_new, self.past) if keys_for_cache is not None else self.k_new
+        self.k, self.v = _cache_append(cache, stored, self.v_new, layer_idx)
+
+    def batches(self):
+        """(c0, c1, M): the call's queries [c0, c1) in launches of PER_QUERY_BATCH, each over the
+        cache prefix [0, M) that its last query sees."""
+        for c0 in range(0, self.N, PER_QUERY_BATCH):
+            c1 = min(self.N, c0 + PER_QUERY_BATCH)
+            yield c0, c1, self.past + c1
+
+
+def _frozen_pos_scale(geom, context_window, max_len, N):
+    """The selection's position scale, fixed at prefill: raw positions under "yarn", else
+    min(1, W / L) with L = max_len or the prefill length."""
+    if geom == "yarn":
+        return 1.0
+    return min(1.0, context_window / float(max_len if max_len is not None else N))
+
+
+def _out_proj(module, out, N):
+    """o_proj of the attention output (1, H, N, D)."""
+    return module.o_proj(out.transpose(1, 2).reshape(1, N, -1).contiguous())
+
+
 def base_inv_freq_of(model):
     """theta^(-2i/D) from the model config (the hybrid file's Kernel C frequencies,
     hybrid_exact.py:712-726)."""
@@ -99,27 +164,10 @@ def _geometry(self, pos_frozen):
 
 def spi_forward(self, hidden_states, position_embeddings=None, attention_mask=None, past_key_values=None,
                 **kwargs):
-    B, N, _ = hidden_states.shape
-    assert B == 1, "batch size must be 1 (the kernels take one sequence, as the reference's)"
-    hs = (B, N, -1, self.head_dim)
-    q = self.q_proj(hidden_states).view(hs).transpose(1, 2)
-    k = self.k_proj(hidden_states).view(hs).transpose(1, 2)
-    v = self.v_proj(hidden_states).view(hs).transpose(1, 2)
-
-    # the cache holds raw k, v; HF may pass it as past_key_values or (older) past_key_value
-    cache = past_key_values if past_key_values is not None else kwargs.get("past_key_value", None)
-    past_len = 0
-    if cache is not None:
-        try:
-            past_len = int(cache.get_seq_length(self.spi_layer_idx))
-        except TypeError:
-            past_len = int(cache.get_seq_length())
-        k, v = cache.update(k, v, self.spi_layer_idx)
-
+    c = _AttnCall(self, hidden_states, past_key_values, kwargs, self.spi_layer_idx)
     # pos_scale frozen at prefill from max_len (or the prefill length), reused at decode
-    if past_len == 0:
-        L_target = self.spi_max_len if self.spi_max_len is not None else N
-        frozen = min(1.0, self.spi_W / float(L_target))
+    if c.past == 0:
+        frozen = _frozen_pos_scale("pi", self.spi_W, self.spi_max_len, c.N)
         if self.spi_geometry == "hybrid":
             self.spi_pos_scale_c = frozen
         else:
@@ -127,10 +175,10 @@ def spi_forward(self, hidden_states, position_embeddings=None, attention_mask=No
     frozen = self.spi_pos_scale_c if self.spi_geometry == "hybrid" else self.spi_pos_scale
     ifa, psa, rsa, ifc, psc, rsc = _geometry(self, frozen)
 
-    if past_len == 0 and self.spi_prefill_mode == "shared":
+    if c.past == 0 and self.spi_prefill_mode == "shared":
         out, shared_size, kept_size, kpct, overflow, kpct_meas, overflow20 = shared_prefill(
-            q, k, v, self.tau_head_vec, ifa, psa, rsa, ifc, psc, rsc, self.spi_pct, self.scaling, self.spi_ng,
-            self.spi_nl, self.spi_tile, self.spi_kmax, past_len, self.spi_measure, self.spi_select_score)
+            c.q, c.k, c.v, self.tau_head_vec, ifa, psa, rsa, ifc, psc, rsc, self.spi_pct, self.scaling, self.spi_ng,
+            self.spi_nl, self.spi_tile, self.spi_kmax, c.past, self.spi_measure, self.spi_select_score)
         self.spi_last_shared = shared_size.detach()
         self.spi_last_kept = kept_size.detach()
         self.spi_last_kpct = kpct.detach()
@@ -138,20 +186,13 @@ def spi_forward(self, hidden_states, position_embeddings=None, attention_mask=No
         self.spi_last_kpct_meas = kpct_meas.detach()
         self.spi_last_overflow20 = overflow20.detach()
     else:
-        # each query at position past_len + i over the keys [0, past_len + i]
+        # each query at position past + i over the keys [0, past + i]
         causal = self.spi_decode_backend == "triton"
-        outs = []
-        for c0 in range(0, N, PER_QUERY_BATCH):
-            c1 = min(N, c0 + PER_QUERY_BATCH)
-            M = past_len + c1
-            outs.append(decode_attention(
-                q[0, :, c0:c1, :], k[:, :, :M, :], v[:, :, :M, :], self.tau_head_vec, ifa, past_len + c0, psa, rsa,
-                self.scaling, self.spi_ng, self.spi_nl, self.spi_kmax, self.spi_pct_decode, causal,
-                inv_freq_c=ifc, pos_scale_c=psc, rope_scale_c=rsc))
-        out = torch.cat(outs, dim=1).unsqueeze(0)              # (1, H, N, D)
-
-    attn_output = out.transpose(1, 2).reshape(B, N, -1).contiguous()
-    return self.o_proj(attn_output), None
+        out = torch.cat([decode_attention(
+            c.q[0, :, c0:c1, :], c.k[:, :, :M, :], c.v[:, :, :M, :], self.tau_head_vec, ifa, c.past + c0, psa, rsa,
+            self.scaling, self.spi_ng, self.spi_nl, self.spi_kmax, self.spi_pct_decode, causal,
+            inv_freq_c=ifc, pos_scale_c=psc, rope_scale_c=rsc) for c0, c1, M in c.batches()], dim=1).unsqueeze(0)
+    return _out_proj(self, out, c.N), None
 
 
 # ---------------------------------------------------------------------------------------------
@@ -199,53 +240,32 @@ def install_perquery(model, select_geom, apply_mscale, context_window, n_global,
 def pq_forward(self, hidden_states, position_embeddings=None, attention_mask=None, past_key_values=None,
                **kwargs):
     import shared_selection_triton_perquery as pqm
-    B, N, _ = hidden_states.shape
-    assert B == 1, "batch size must be 1 (the kernels take one sequence, as the reference's)"
-    hs = (B, N, -1, self.head_dim)
-    q = self.q_proj(hidden_states).view(hs).transpose(1, 2)
-    k = self.k_proj(hidden_states).view(hs).transpose(1, 2)
-    v = self.v_proj(hidden_states).view(hs).transpose(1, 2)
-    cache = past_key_values if past_key_values is not None else kwargs.get("past_key_value", None)
-    past_len = 0
-    if cache is not None:
-        try:
-            past_len = int(cache.get_seq_length(self.spi_layer_idx))
-        except TypeError:
-            past_len = int(cache.get_seq_length())
-        k, v = cache.update(k, v, self.spi_layer_idx)
-    # the selection's pos_scale, frozen at prefill: pi -> min(1, W / L), yarn -> raw positions
-    if past_len == 0:
-        if self.spi_geom == "yarn":
-            self.spi_pos_scale_a = 1.0
-        else:
-            L_target = self.spi_max_len if self.spi_max_len is not None else N
-            self.spi_pos_scale_a = min(1.0, self.spi_W / float(L_target))
-    if past_len == 0 and self.spi_prefill_mode == "shared":
+    c = _AttnCall(self, hidden_states, past_key_values, kwargs, self.spi_layer_idx)
+    if c.past == 0:   # the selection's pos_scale, frozen at prefill
+        self.spi_pos_scale_a = _frozen_pos_scale(self.spi_geom, self.spi_W, self.spi_max_len, c.N)
+    if c.past == 0 and self.spi_prefill_mode == "shared":
         out, usize, kept_size, overflow = pqm.shared_pq_attention(
-            q, k, v, self.tau_head_vec, self.spi_inv_freq_a, self.spi_inv_freq_c,
+            c.q, c.k, c.v, self.tau_head_vec, self.spi_inv_freq_a, self.spi_inv_freq_c,
             pos_scale_a=self.spi_pos_scale_a, rope_scale_a=self.spi_rope_scale_a, sm_scale=self.scaling,
             n_global=self.spi_ng, n_local=self.spi_nl, tile=self.spi_tile, k_max=self.spi_kmax,
-            q_pos_base=past_len, select_score=self.spi_select_score)
+            q_pos_base=c.past, select_score=self.spi_select_score)
         self.spi_last_usize = usize.detach()
         self.spi_last_kept = kept_size.detach()
         self.spi_last_overflow = overflow.detach()
     else:
-        # each query at position past_len + i over the keys [0, past_len + i], per-query rule
+        # each query at position past + i over the keys [0, past + i], per-query rule
         causal = self.spi_decode_backend == "triton"
         outs = []
-        for c0 in range(0, N, PER_QUERY_BATCH):
-            c1 = min(N, c0 + PER_QUERY_BATCH)
-            M = past_len + c1
+        for c0, c1, M in c.batches():
             st = {}
             outs.append(decode_attention(
-                q[0, :, c0:c1, :], k[:, :, :M, :], v[:, :, :M, :], self.tau_head_vec, self.spi_inv_freq_a,
-                past_len + c0, self.spi_pos_scale_a, self.spi_rope_scale_a, self.scaling, self.spi_ng, self.spi_nl,
+                c.q[0, :, c0:c1, :], c.k[:, :, :M, :], c.v[:, :, :M, :], self.tau_head_vec, self.spi_inv_freq_a,
+                c.past + c0, self.spi_pos_scale_a, self.spi_rope_scale_a, self.scaling, self.spi_ng, self.spi_nl,
                 self.spi_kmax, 100.0, causal, inv_freq_c=self.spi_inv_freq_c, pos_scale_c=1.0, rope_scale_c=1.0,
                 rule="pq", stats=st))
             pqm._record(st["overflow"], st["usize"], phase="decode")
         out = torch.cat(outs, dim=1).unsqueeze(0)
-    attn_output = out.transpose(1, 2).reshape(B, N, -1).contiguous()
-    return self.o_proj(attn_output), None
+    return _out_proj(self, out, c.N), None
 
 
 # ---------------------------------------------------------------------------------------------
@@ -294,54 +314,34 @@ def install_pqstream(model, select_geom, apply_mscale, context_window, n_global,
 def pqs_forward(self, hidden_states, position_embeddings=None, attention_mask=None, past_key_values=None,
                 **kwargs):
     import pqstream_kernel as pqs
-    B, N, _ = hidden_states.shape
-    assert B == 1, "batch size must be 1 (the kernels take one sequence, as the reference's)"
-    hs = (B, N, -1, self.head_dim)
-    q = self.q_proj(hidden_states).view(hs).transpose(1, 2)
-    k = self.k_proj(hidden_states).view(hs).transpose(1, 2)
-    v = self.v_proj(hidden_states).view(hs).transpose(1, 2)
-    cache = past_key_values if past_key_values is not None else kwargs.get("past_key_value", None)
-    past_len = 0
-    if cache is not None:
-        try:
-            past_len = int(cache.get_seq_length(self.pqs_layer_idx))
-        except TypeError:
-            past_len = int(cache.get_seq_length())
-        k, v = cache.update(k, v, self.pqs_layer_idx)
-    if past_len == 0:
-        if self.pqs_geom == "yarn":
-            self.pqs_pos_scale_a = 1.0
-        else:
-            L_target = self.pqs_max_len if self.pqs_max_len is not None else N
-            self.pqs_pos_scale_a = min(1.0, self.pqs_W / float(L_target))
-    if past_len == 0 and self.pqs_prefill_mode == "stream":
+    c = _AttnCall(self, hidden_states, past_key_values, kwargs, self.pqs_layer_idx)
+    if c.past == 0:
+        self.pqs_pos_scale_a = _frozen_pos_scale(self.pqs_geom, self.pqs_W, self.pqs_max_len, c.N)
+    if c.past == 0 and self.pqs_prefill_mode == "stream":
         out, span, kept, blocks, skipped = pqs.pqstream_attention(
-            q, k, v, self.tau_head_vec, self.pqs_inv_freq_a, self.pqs_inv_freq_c,
+            c.q, c.k, c.v, self.tau_head_vec, self.pqs_inv_freq_a, self.pqs_inv_freq_c,
             pos_scale_a=self.pqs_pos_scale_a, rope_scale_a=self.pqs_rope_scale_a, sm_scale=self.scaling,
             n_global=self.pqs_ng, n_local=self.pqs_nl, tile=self.pqs_tile, block_n=self.pqs_block_n,
-            pos_advance=self.pqs_advance, q_pos_base=past_len, use_skip=self.pqs_use_skip)
+            pos_advance=self.pqs_advance, q_pos_base=c.past, use_skip=self.pqs_use_skip)
         self.pqs_last_span = span.detach()
         self.pqs_last_kept = kept.detach()
         self.pqs_last_skipped = skipped.detach()
     else:
-        # each query at position past_len + i over the keys [0, past_len + i], the stream rule; the
-        # slot buffer is the batch's cache length rounded up to 1024
+        # each query at position past + i over the keys [0, past + i], the stream rule; the slot
+        # buffer is the batch's cache length rounded up to 1024
         causal = self.pqs_decode_backend == "triton"
         outs = []
-        for c0 in range(0, N, PER_QUERY_BATCH):
-            c1 = min(N, c0 + PER_QUERY_BATCH)
-            M = past_len + c1
+        for c0, c1, M in c.batches():
             st = {}
             outs.append(decode_attention(
-                q[0, :, c0:c1, :], k[:, :, :M, :], v[:, :, :M, :], self.tau_head_vec, self.pqs_inv_freq_a,
-                past_len + c0, self.pqs_pos_scale_a, self.pqs_rope_scale_a, self.scaling, self.pqs_ng,
+                c.q[0, :, c0:c1, :], c.k[:, :, :M, :], c.v[:, :, :M, :], self.tau_head_vec, self.pqs_inv_freq_a,
+                c.past + c0, self.pqs_pos_scale_a, self.pqs_rope_scale_a, self.scaling, self.pqs_ng,
                 self.pqs_nl, pqs._kbuf(M), 100.0, causal, inv_freq_c=self.pqs_inv_freq_c, pos_scale_c=1.0,
                 rope_scale_c=1.0, rule="stream", stats=st, block_n=self.pqs_block_n))
-            m = torch.arange(past_len + c0 + 1, M + 1, device=q.device)
+            m = torch.arange(c.past + c0 + 1, M + 1, device=c.q.device)
             pqs._record_decode(st["idx"], st["newpos_k"], st["set_size"], m, self.pqs_block_n)
         out = torch.cat(outs, dim=1).unsqueeze(0)
-    attn_output = out.transpose(1, 2).reshape(B, N, -1).contiguous()
-    return self.o_proj(attn_output), None
+    return _out_proj(self, out, c.N), None
 
 
 # ---------------------------------------------------------------------------------------------
@@ -367,55 +367,35 @@ def chunk_forward(self, hidden_states, position_embeddings=None, attention_mask=
                   **kwargs):
     import shared_selection_triton_chunked as chm
     import _sta_native as native
-    B, N, _ = hidden_states.shape
-    assert B == 1, "batch size must be 1 (the kernels take one sequence, as the reference's)"
-    hs = (B, N, -1, self.head_dim)
-    q = self.q_proj(hidden_states).view(hs).transpose(1, 2)
-    k = self.k_proj(hidden_states).view(hs).transpose(1, 2)
-    v = self.v_proj(hidden_states).view(hs).transpose(1, 2)
-    cache = past_key_values if past_key_values is not None else kwargs.get("past_key_value", None)
-    past_len = 0
-    if cache is not None:
-        try:
-            past_len = int(cache.get_seq_length(self.spi_layer_idx))
-        except TypeError:
-            past_len = int(cache.get_seq_length())
-        k, v = cache.update(k, v, self.spi_layer_idx)
-    if past_len == 0:
-        if self.spi_geom == "yarn":
-            self.spi_pos_scale_a = 1.0
-        else:
-            L_target = self.spi_max_len if self.spi_max_len is not None else N
-            self.spi_pos_scale_a = min(1.0, self.spi_W / float(L_target))
-    if past_len == 0 and self.spi_prefill_mode == "shared":
+    c = _AttnCall(self, hidden_states, past_key_values, kwargs, self.spi_layer_idx)
+    if c.past == 0:
+        self.spi_pos_scale_a = _frozen_pos_scale(self.spi_geom, self.spi_W, self.spi_max_len, c.N)
+    if c.past == 0 and self.spi_prefill_mode == "shared":
         out, usize, kept_size = chm.shared_chunk_attention(
-            q, k, v, self.tau_head_vec, self.spi_inv_freq_a, self.spi_inv_freq_c, pos_scale_a=self.spi_pos_scale_a,
-            rope_scale_a=self.spi_rope_scale_a, sm_scale=self.scaling, n_global=self.spi_ng, n_local=self.spi_nl,
-            tile=self.spi_tile, k_max=self.spi_kmax, chunk_size=self.spi_chunk_size, n_chunk=self.spi_n_chunk,
-            q_pos_base=past_len, select_score=self.spi_select_score, chunk_agg=self.spi_chunk_agg,
-            measure=self.spi_measure)
+            c.q, c.k, c.v, self.tau_head_vec, self.spi_inv_freq_a, self.spi_inv_freq_c,
+            pos_scale_a=self.spi_pos_scale_a, rope_scale_a=self.spi_rope_scale_a, sm_scale=self.scaling,
+            n_global=self.spi_ng, n_local=self.spi_nl, tile=self.spi_tile, k_max=self.spi_kmax,
+            chunk_size=self.spi_chunk_size, n_chunk=self.spi_n_chunk, q_pos_base=c.past,
+            select_score=self.spi_select_score, chunk_agg=self.spi_chunk_agg, measure=self.spi_measure)
         self.spi_last_usize = usize.detach()
         self.spi_last_kept = kept_size.detach()
     else:
-        # each query at position past_len + i over the keys [0, past_len + i], chunk rule
+        # each query at position past + i over the keys [0, past + i], chunk rule
         causal = self.spi_decode_backend == "triton"
         outs = []
-        H = q.shape[1]
-        for c0 in range(0, N, PER_QUERY_BATCH):
-            c1 = min(N, c0 + PER_QUERY_BATCH)
-            M = past_len + c1
-            plan = native.DecodePlan(q[0, :, c0:c1, :], k[:, :, :M, :], v[:, :, :M, :], self.tau_head_vec,
-                                     self.spi_inv_freq_a, past_len + c0, self.spi_pos_scale_a, self.spi_rope_scale_a,
+        H = c.q.shape[1]
+        for c0, c1, M in c.batches():
+            plan = native.DecodePlan(c.q[0, :, c0:c1, :], c.k[:, :, :M, :], c.v[:, :, :M, :], self.tau_head_vec,
+                                     self.spi_inv_freq_a, c.past + c0, self.spi_pos_scale_a, self.spi_rope_scale_a,
                                      self.scaling, self.spi_ng, self.spi_nl, self.spi_kmax, 100.0, causal,
                                      inv_freq_c=self.spi_inv_freq_c, pos_scale_c=1.0, rope_scale_c=1.0)
-            s = plan.scores(torch.empty((H, c1 - c0, M), dtype=torch.float32, device=q.device))
-            pk = torch.empty((H, c1 - c0), dtype=torch.int32, device=q.device)
-            us = torch.empty((H, c1 - c0), dtype=torch.int32, device=q.device)
+            s = plan.scores(torch.empty((H, c1 - c0, M), dtype=torch.float32, device=c.q.device))
+            pk = torch.empty((H, c1 - c0), dtype=torch.int32, device=c.q.device)
+            us = torch.empty((H, c1 - c0), dtype=torch.int32, device=c.q.device)
             r = plan.build_sets_chunk(s, self.spi_chunk_size, self.spi_n_chunk, self.spi_select_score,
                                       self.spi_chunk_agg, passers_kept=pk, usize=us)
             outs.append(plan.attend(r["idx"], r["newpos_k"], r["newpos_q"], r["set_size"]).clone())
             if self.spi_measure:
                 chm._stat_acc(pk, us, r["set_size"], "decode")
         out = torch.cat(outs, dim=1).unsqueeze(0)
-    attn_output = out.transpose(1, 2).reshape(B, N, -1).contiguous()
-    return self.o_proj(attn_output), None
+    return _out_proj(self, out, c.N), None

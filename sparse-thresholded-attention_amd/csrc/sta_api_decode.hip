@@ -21,6 +21,11 @@ struct DecLayout {
   size_t qrot_off, scores_off, keys_off, size_off, part_off, qfrag_off, kfrag_off, total;
 };
 
+// the PQ Stream rule's block-end counts in the selection's LDS (decode_bend_words)
+int dec_bend_words(const sta_decode_args* a) {
+  return a->rule == STA_RULE_STREAM && a->block_n >= 1 ? (a->M + a->block_n - 1) / a->block_n : 0;
+}
+
 DecLayout dec_layout_of(const sta_decode_args* a) {
   DecLayout L;
   L.nsplit = decode_nsplit(a->k_max);
@@ -34,7 +39,7 @@ DecLayout dec_layout_of(const sta_decode_args* a) {
   L.scores_off = off;                                 // scores (H, Q, M) when not an output
   off = align256(off + hq * a->M * 4);
   L.keys_off = off;                                   // key store of long caches
-  off = align256(off + decode_keys_bytes(a->H, a->Q, a->M));
+  off = align256(off + decode_keys_bytes(a->H, a->Q, a->M, dec_bend_words(a)));
   L.size_off = off;                                   // set sizes (H, Q) when not an output
   off = align256(off + hq * 4);
   L.part_off = off;                                   // attend split states
@@ -71,7 +76,7 @@ int dec_check(const sta_decode_args* a, bool need_pos = true) {
     return fail(STA_ERR_INVALID_ARG, "rule %d is not STA_RULE_SHARED, STA_RULE_PQ or STA_RULE_STREAM", a->rule);
   if (a->rule == STA_RULE_STREAM) {
     if (a->block_n < 1) return fail(STA_ERR_INVALID_ARG, "stream rule: block_n=%d must be >= 1", a->block_n);
-    // the block-end counts live in the selection's 4096-entry histogram
+    // one block-end count per position block in the selection's LDS (16 KB at most)
     if ((a->M + a->block_n - 1) / a->block_n > 4096)
       return fail(STA_ERR_UNSUPPORTED, "stream rule: M=%d over block_n=%d exceeds 4096 blocks", a->M, a->block_n);
   }
@@ -126,7 +131,7 @@ DecodeArgs dec_args_of(const sta_decode_args* a, const DecLayout& L) {
                                                                      // every passer)
   d.pct_frac = (float)(a->pct_decode / 100.0);                    // the float32 scalar of :561
   d.scores = a->scores ? a->scores : (float*)(ws + L.scores_off);
-  d.keys = decode_select_in_lds(a->M) ? nullptr : (uint32_t*)(ws + L.keys_off);
+  d.keys = decode_select_in_lds(a->M, dec_bend_words(a)) ? nullptr : (uint32_t*)(ws + L.keys_off);
   d.idx = a->idx;
   d.newpos_k = a->newpos_k;
   d.newpos_q = a->newpos_q;

@@ -310,15 +310,18 @@ constexpr int DEC_CAND = 128;                // keys of a bin ranked directly
 // row's workgroup under 80 KB (two per CU); 32-bit counters for the global store's long rows.
 constexpr int dec_hist_words(bool gkeys) { return gkeys ? 4096 : 2048; }
 constexpr size_t DEC_AUX = 2048 * 4 + DEC_SEL_NT * 4 + 256;   // histogram, candidates, scratch
-bool decode_select_in_lds(int M) {   // the CU's 160 KB: M <= 35840
+// The PQ Stream rule also keeps one kept-key count per position block (nbend words, after the
+// scratch); rows whose keys, histogram and block counts outgrow the LDS take the global store.
+bool decode_select_in_lds(int M, int nbend) {   // the CU's 160 KB: M <= 35840 without block counts
   const int per = (M + DEC_SEL_NT - 1) / DEC_SEL_NT;
-  return (size_t)DEC_SEL_NT * (per | 1) * 4 + DEC_AUX <= 160 * 1024;
+  return (size_t)DEC_SEL_NT * (per | 1) * 4 + DEC_AUX + (size_t)nbend * 4 <= 160 * 1024;
 }
-size_t decode_keys_bytes(int H, int Q, int M) {
-  if (decode_select_in_lds(M)) return 0;
+size_t decode_keys_bytes(int H, int Q, int M, int nbend) {
+  if (decode_select_in_lds(M, nbend)) return 0;
   const int per = (M + DEC_SEL_NT - 1) / DEC_SEL_NT;
   return (size_t)H * Q * DEC_SEL_NT * per * 4;
 }
+int decode_bend_words(const DecodeArgs& a) { return a.rule == 2 ? (a.M + a.block_n - 1) / a.block_n : 0; }
 
 // NT threads per query: 1024 for a few queries (latency), 512 for large batches (throughput)
 template <bool GKEYS, int NT>
@@ -574,8 +577,9 @@ __global__ __launch_bounds__(NT) void decode_select_kernel(DecodeArgs a) {
   // PQ Stream's positions (pqstream_kernel.py:736-749): aligned blocks of block_n keys walked
   // from the query backwards; key j of block b sits at dist = d[b] + (min(q_pos, end of b) - j)
   // with d[b] = kept keys after block b = total - (kept keys up to the end of b).  The inclusive
-  // count at every block end goes to LDS (over the histogram, free by now).
-  int* bend = (int*)hist;
+  // count at every block end goes to its own LDS region (ceil(M / block_n) words after the
+  // scratch words, sized by the launcher).
+  int* bend = misc + 8;
   if (stream) {
     int rank = base - 1, tie = tie_base;
     for (int e = 0; e < j1 - j0; ++e) {
@@ -864,8 +868,10 @@ hipError_t launch_decode_scores(int dtype, int D, const DecodeArgs& a, float* qr
 template <int NT>
 static hipError_t launch_select_t(const DecodeArgs& a, hipStream_t st) {
   const int per = (a.M + NT - 1) / NT;
-  const bool in_lds = decode_select_in_lds(a.M);   // (the 1024-thread bound covers 512 threads)
-  const size_t lds = (in_lds ? (size_t)NT * (per | 1) * 4 : 0) + (size_t)dec_hist_words(!in_lds) * 4 + NT * 4 + 256;
+  const int nbend = decode_bend_words(a);
+  const bool in_lds = decode_select_in_lds(a.M, nbend);   // (the 1024-thread bound covers 512 threads)
+  const size_t lds = (in_lds ? (size_t)NT * (per | 1) * 4 : 0) + (size_t)dec_hist_words(!in_lds) * 4 + NT * 4 + 256 +
+                     (size_t)nbend * 4;
   if (in_lds) {
     hipError_t e = hipFuncSetAttribute((const void*)decode_select_kernel<false, NT>,
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
@@ -873,6 +879,9 @@ static hipError_t launch_select_t(const DecodeArgs& a, hipStream_t st) {
     hipLaunchKernelGGL((decode_select_kernel<false, NT>), dim3(a.H * a.Q), dim3(NT), lds, st, a);
   } else {
     if (!a.keys) return hipErrorInvalidValue;   // decode_keys_bytes (1024 threads) bounds NT * per
+    hipError_t e = hipFuncSetAttribute((const void*)decode_select_kernel<true, NT>,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return e;
     hipLaunchKernelGGL((decode_select_kernel<true, NT>), dim3(a.H * a.Q), dim3(NT), lds, st, a);
   }
   return hipGetLastError();

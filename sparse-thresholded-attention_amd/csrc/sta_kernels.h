@@ -322,8 +322,10 @@ hipError_t launch_score_rows(int D, const RowsArgs& a, hipStream_t st);
 
 // qrot: workspace of (H, Q, D) floats, used when a workgroup's query rows outgrow its LDS
 hipError_t launch_decode_scores(int dtype, int D, const DecodeArgs& a, float* qrot, hipStream_t st);
-bool decode_select_in_lds(int M);
-size_t decode_keys_bytes(int H, int Q, int M);
+// nbend: the PQ Stream rule's block-end counts (decode_bend_words), 0 for the other rules
+bool decode_select_in_lds(int M, int nbend);
+size_t decode_keys_bytes(int H, int Q, int M, int nbend);
+int decode_bend_words(const DecodeArgs& a);
 hipError_t launch_decode_select(const DecodeArgs& a, hipStream_t st);
 int decode_nsplit(int k_max);
 hipError_t launch_decode_attend(int dtype, int D, const DecodeArgs& a, hipStream_t st);

@@ -19,6 +19,7 @@ import math
 import torch
 
 import _sta_native as native
+from _install import _AttnCall, _out_proj
 
 _MAX_NEW_TOKENS = 512            # table headroom for generation (dca_kernel.py:161)
 _ATTN_CLASSES = ("LlamaAttention", "LlamaFlashAttention2", "LlamaSdpaAttention")
@@ -82,19 +83,6 @@ class DcaRotaryState(torch.nn.Module):
         return self._last_mscale
 
 
-def _cache_length(cache, layer_idx):
-    if cache is None:
-        return 0
-    if hasattr(cache, "get_seq_length"):
-        try:
-            return int(cache.get_seq_length(layer_idx))
-        except TypeError:
-            return int(cache.get_seq_length())
-    if not hasattr(cache, "update"):
-        return int(cache[layer_idx][0].shape[2])
-    return 0
-
-
 def _make_dca_forward(chunk_size, pretrain_len, local_window):
     """The patched LlamaAttention.forward (dca_kernel.py:372-525).  Prefill (an empty cache, any
     number of tokens) runs sta_dca_attention over the call's tokens; decode (one token on a warm
@@ -105,58 +93,80 @@ def _make_dca_forward(chunk_size, pretrain_len, local_window):
 
     def dca_forward(self, hidden_states, position_embeddings=None, attention_mask=None, past_key_values=None,
                     **kwargs):
-        bsz, q_len, _ = hidden_states.shape
-        assert bsz == 1, "batch size must be 1 (the kernels take one sequence, as the reference's)"
-        if past_key_values is None:
-            past_key_values = kwargs.get("past_key_value", None)
-        D = self.head_dim
-        H = getattr(self, "num_heads", None) or self.config.num_attention_heads
-        H_kv = getattr(self, "num_key_value_heads", None) or self.config.num_key_value_heads
-        scale = float(getattr(self, "scaling", None) or (1.0 / math.sqrt(D)))
-        q = self.q_proj(hidden_states).view(bsz, q_len, H, D).transpose(1, 2)
-        k = self.k_proj(hidden_states).view(bsz, q_len, H_kv, D).transpose(1, 2)
-        v = self.v_proj(hidden_states).view(bsz, q_len, H_kv, D).transpose(1, 2)
+        # the table factor of this call is fixed before its keys are rotated into the cache
+        state = {}
 
-        start_pos = _cache_length(past_key_values, self.layer_idx)
-        assert start_pos == 0 or q_len == 1, (
-            f"dca_forward: chunked prefill is unsupported (start_pos={start_pos}, q_len={q_len}). "
+        def rotated(k_new, past):
+            state["mscale"] = self.rotary_emb.advance(past + k_new.shape[2])
+            return native.dca_rotate_keys(k_new, past, self.rotary_emb.inv_freq, s, w, state["mscale"]).unsqueeze(0)
+
+        call = _AttnCall(self, hidden_states, past_key_values, kwargs, self.layer_idx, keys_for_cache=rotated)
+        assert call.past == 0 or call.N == 1, (
+            f"dca_forward: chunked prefill is unsupported (start_pos={call.past}, q_len={call.N}). "
             f"Prefill must be a single pass over an empty cache; decode must be one token.")
-        rot = self.rotary_emb
-        mscale = rot.advance(start_pos + q_len)
-        inv_freq = rot.inv_freq
-
-        k_rot = native.dca_rotate_keys(k, start_pos, inv_freq, s, w, mscale).unsqueeze(0)
-        k_all, v_all = k_rot, v
-        if past_key_values is not None:
-            if hasattr(past_key_values, "update"):
-                k_all, v_all = past_key_values.update(k_rot, v, self.layer_idx)
-            else:
-                past_k, past_v = past_key_values[self.layer_idx]
-                k_all, v_all = torch.cat([past_k, k_rot], dim=2), torch.cat([past_v, v], dim=2)
-
-        if q_len > 1:
-            out = native.dca_attention(q, k, v, inv_freq, s, c, w, scale, mscale=mscale)        # (H, N, D)
-        else:
-            out = native.dca_decode(q, k_all, v_all, inv_freq, s, w, mscale, scale)[:, None]   # (H, 1, D)
-        attn_out = out.transpose(0, 1).reshape(bsz, q_len, H * D)
-        return self.o_proj(attn_out), None
+        scale = float(getattr(self, "scaling", None) or (1.0 / math.sqrt(self.head_dim)))
+        inv_freq, mscale = self.rotary_emb.inv_freq, state["mscale"]
+        if call.N > 1:   # prefill: the call's raw keys, rotated inside the kernels
+            out = native.dca_attention(call.q, call.k_new, call.v_new, inv_freq, s, c, w, scale, mscale=mscale)
+        else:            # decode: the cached rotated keys
+            out = native.dca_decode(call.q, call.k, call.v, inv_freq, s, w, mscale, scale)[:, None]
+        return _out_proj(self, out.unsqueeze(0), call.N), None
 
     return dca_forward
 
 
-def _is_patchable_llama(module):
-    """An attention module with the projections and indices the forward reads (:530-535)."""
-    required = ("q_proj", "k_proj", "v_proj", "o_proj", "head_dim", "layer_idx")
-    if not all(hasattr(module, a) for a in required):
-        return False
-    return hasattr(module, "num_heads") or (
-        hasattr(module, "config") and hasattr(module.config, "num_attention_heads"))
+class DcaPatch:
+    """What patch_model_with_dca changed, so that unpatch_model can undo exactly that: for each
+    attention class, the forward its own namespace held before the patch (or none: it inherited
+    one), and for each module that now runs the DCA forward, whether it had a rotary_emb
+    attribute and which."""
+
+    _NONE = object()
+
+    def __init__(self, model):
+        self.model = model
+        self._class_forwards = []      # (class, own forward or _NONE)
+        self._rotaries = []            # (module, previous rotary_emb or _NONE)
+
+    @property
+    def n_layers(self):
+        return len(self._rotaries)
+
+    def replace_forward(self, cls, fwd):
+        self._class_forwards.append((cls, cls.__dict__.get("forward", self._NONE)))
+        cls.forward = fwd
+
+    def give_state(self, module, state):
+        self._rotaries.append((module, getattr(module, "rotary_emb", self._NONE)))
+        module.rotary_emb = state
+
+    def restore(self):
+        for module, old in reversed(self._rotaries):
+            if old is self._NONE:
+                if hasattr(module, "rotary_emb"):
+                    delattr(module, "rotary_emb")
+            else:
+                module.rotary_emb = old
+        for cls, old in reversed(self._class_forwards):
+            if old is self._NONE:
+                del cls.forward
+            else:
+                cls.forward = old
+        n = len(self._class_forwards)
+        self._class_forwards, self._rotaries = [], []
+        return n
+
+
+def _needs_dca_state(module, fwd):
+    """A module whose class (or a base) now resolves forward to the DCA forward; that forward reads
+    its projections, head_dim, layer_idx and head counts."""
+    return getattr(type(module), "forward", None) is fwd
 
 
 def patch_model_with_dca(model, chunk_size, pretrain_len, local_window):
-    """Patch LlamaAttention.forward (class level) with the DCA forward and give every patchable
-    attention module its own table state.  Returns the `originals` dict for unpatch_model; raises
-    RuntimeError, with the classes restored, when no attention module was patchable.
+    """Patch the Llama attention classes' forward with the DCA forward and give every module that
+    runs it a table state of its own.  Returns the DcaPatch record that unpatch_model takes; raises
+    RuntimeError, with everything restored, when no module of the model runs the DCA forward.
     dca_kernel.py:538-615.
 
     The table frequencies use base = int(the module's old rotary's base, else the config's
@@ -167,64 +177,32 @@ def patch_model_with_dca(model, chunk_size, pretrain_len, local_window):
     assert 0 < local_window < chunk_size, f"need 0 < w({local_window}) < s({chunk_size})"
     assert chunk_size < pretrain_len, f"need s({chunk_size}) < c({pretrain_len})"
     fwd = _make_dca_forward(chunk_size, pretrain_len, local_window)
-    originals = {}
-    for name in _ATTN_CLASSES:
-        cls = getattr(ml, name, None)
-        if cls is not None:
-            originals[name] = cls.forward
-            cls.forward = fwd
-    rotary_originals = {}
-    n_patched = 0
-    for mod_name, m in model.named_modules():
-        if not _is_patchable_llama(m):
+    patch = DcaPatch(model)
+    for cls in {getattr(ml, name) for name in _ATTN_CLASSES if hasattr(ml, name)}:
+        patch.replace_forward(cls, fwd)
+    for m in model.modules():
+        if not _needs_dca_state(m, fwd):
             continue
-        n_patched += 1
         old = getattr(m, "rotary_emb", None)
-        rotary_originals[mod_name] = old
         base = int(getattr(old, "base", None) or getattr(m.config, "rope_theta", 10_000))
         dev = m.q_proj.weight.device
-        m.rotary_emb = DcaRotaryState(m.head_dim, max_position_embeddings=pretrain_len, base=base,
-                                      device=None if dev.type == "meta" else dev)
-    if n_patched == 0:
-        for name in _ATTN_CLASSES:
-            if name in originals:
-                getattr(ml, name).forward = originals[name]
+        patch.give_state(m, DcaRotaryState(m.head_dim, max_position_embeddings=pretrain_len, base=base,
+                                           device=None if dev.type == "meta" else dev))
+    if patch.n_layers == 0:
+        patch.restore()
         raise RuntimeError(
             "patch_model_with_dca patched 0 attention layers -- the model would have run dense. "
             "Its attention modules must expose q_proj/k_proj/v_proj/o_proj/head_dim/layer_idx.")
-    originals["_model"] = model
-    originals["_rotary_emb_originals"] = rotary_originals
-    originals["_n_patched"] = n_patched
-    print(f"  [DCA] {n_patched} attention layers on the HIP DCA kernels (s={chunk_size}, c={pretrain_len}, "
+    print(f"  [DCA] {patch.n_layers} attention layers on the HIP DCA kernels (s={chunk_size}, c={pretrain_len}, "
           f"w={local_window}, chunk_len={chunk_size - local_window})", flush=True)
-    return originals
+    return patch
 
 
 def unpatch_model(originals):
-    """Restore the forwards and the modules' rotary attributes saved by patch_model_with_dca
-    (:618-653)."""
-    try:
-        import transformers.models.llama.modeling_llama as ml
-    except ImportError:
-        return
-    n_fwd = 0
-    for name in _ATTN_CLASSES:
-        if name in originals:
-            cls = getattr(ml, name, None)
-            if cls is not None:
-                cls.forward = originals[name]
-                n_fwd += 1
-    model = originals.get("_model")
-    saved = originals.get("_rotary_emb_originals", {})
-    if model is not None and saved:
-        for mod_name, m in model.named_modules():
-            if mod_name in saved:
-                if saved[mod_name] is None:
-                    if hasattr(m, "rotary_emb"):
-                        delattr(m, "rotary_emb")
-                else:
-                    m.rotary_emb = saved[mod_name]
-    print(f"  [DCA] restored {n_fwd} attention class(es) and rotary attributes", flush=True)
+    """Undo patch_model_with_dca: its DcaPatch record restores the attention classes' forwards and
+    every patched module's rotary attribute (:618-653)."""
+    n = originals.restore()
+    print(f"  [DCA] restored {n} attention class(es) and the modules' rotary attributes", flush=True)
 
 
 def install_dca_forward(model, chunk_size=3072, context_window=4096, local_window=512):

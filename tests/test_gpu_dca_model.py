@@ -230,8 +230,8 @@ def test_patched_llama_reproduces_reference_model():
     s, c, w, N, T, seed = (int(x) for x in gm["params"])
     say(f"patched llama vs reference: s={s} c={c} w={w} N={N} T={T}")
     model = _llama(seed)
-    originals = dca.patch_model_with_dca(model, s, c, w)
-    assert originals["_n_patched"] == 2
+    patch = dca.patch_model_with_dca(model, s, c, w)
+    assert patch.n_layers == 2
     prefill, steps, toks = _greedy(model, torch.from_numpy(gm["ids"]).to(DEV), T)
     perr = float((prefill.cpu() - torch.from_numpy(gm["prefill_logits"])).abs().max())
     serr = float((steps.cpu() - torch.from_numpy(gm["step_logits"])).abs().max())
@@ -239,7 +239,7 @@ def test_patched_llama_reproduces_reference_model():
           flush=True)
     assert perr < 1e-3 and serr < 1e-3
     assert toks == gm["tokens"].tolist()
-    dca.unpatch_model(originals)
+    dca.unpatch_model(patch)
 
 
 def test_patched_llama_inside_one_chunk_is_the_dense_model():
@@ -252,7 +252,7 @@ def test_patched_llama_inside_one_chunk_is_the_dense_model():
     ids = torch.randint(0, 256, (1, 200), generator=g).to(DEV)
     ref_prefill, ref_steps, ref_toks = _greedy(model, ids, 6)
     orig = ml.LlamaAttention.forward
-    originals = dca.install_dca_forward(model, chunk_size=320, context_window=4096, local_window=64)
+    patch = dca.install_dca_forward(model, chunk_size=320, context_window=4096, local_window=64)
     assert ml.LlamaAttention.forward is not orig
     assert all(isinstance(l.self_attn.rotary_emb, dca.DcaRotaryState) for l in model.model.layers)
     prefill, steps, toks = _greedy(model, ids, 6)
@@ -260,7 +260,7 @@ def test_patched_llama_inside_one_chunk_is_the_dense_model():
     serr = float((steps - ref_steps).abs().max())
     print(f"[result] one chunk: prefill logits err {perr:.2e}, step logits err {serr:.2e}", flush=True)
     assert perr < 2e-3 and serr < 2e-3 and toks == ref_toks
-    dca.unpatch_model(originals)
+    dca.unpatch_model(patch)
     assert ml.LlamaAttention.forward is orig
     assert not any(hasattr(l.self_attn, "rotary_emb") for l in model.model.layers)
     prefill2, _, _ = _greedy(model, ids, 0)

@@ -332,6 +332,20 @@ def test_pqs_decode_every_key_kept_is_natural():
                                                                          (H, m)))
 
 
+@pytest.mark.parametrize("M,bn,Q", [(20000, 8, 2), (16000, 4, 1), (33000, 9, 2)])
+def test_pqs_decode_many_position_blocks(M, bn, Q):
+    """More position blocks than the selection's histogram has words (2500 and 4000): the block-end
+    counts have an LDS region of their own; at M = 33000 the keys, histogram and 3667 block counts
+    outgrow the LDS and the selection takes the global key store."""
+    from synthetic import planted_inputs, base_inv_freq
+    H, D = 2, 64
+    q, k, v = planted_inputs(61 + bn, H, H, M, D, 0.02, torch.bfloat16, DEV)
+    qq = q[0, :, M - Q:, :].contiguous()
+    invf = base_inv_freq(D, 10000.0).to(DEV)
+    _check_stream_decode(qq, k[0], v[0], torch.full((H,), 3.0, device=DEV), invf, 0.5, 1.0, invf, M - Q, 16, 16,
+                         bn, f"stream decode M={M} block_n={bn} ({(M + bn - 1) // bn} blocks)")
+
+
 def test_pqs_decode_rejects_bad_block_n():
     import _sta_native as native
     q = torch.zeros(2, 1, 64, device=DEV)
