@@ -510,9 +510,10 @@ def dca_decode(q, krot, v, dtype, inv_freq, chunk_size, local_window, mscale, sc
 # composition of dca_kernel.py's positions and exact_2.py's Kernel A + _build_sets)
 # ---------------------------------------------------------------------------------------------
 def dca_inter_votes(q, k, dtype, inv_freq, chunk_size, pretrain_len, local_window, tau, scale=None, T=64,
-                    band_eps=1e-3, want_band=False):
+                    band_eps=1e-3, want_band=False, tiles=None):
     """Votes (H, nt, N) int32 over each 64-query tile's inter keys [0, (c - 1) L), row_max (H, N)
-    (-inf without inter keys) and optionally band (H, nt, N)."""
+    (-inf without inter keys) and optionally band (H, nt, N).  tiles: evaluate only these tile
+    indices (the others keep zero votes and a NaN row max)."""
     q = np.ascontiguousarray(q)
     k = np.ascontiguousarray(k)
     H, N, D = q.shape
@@ -524,11 +525,15 @@ def dca_inter_votes(q, k, dtype, inv_freq, chunk_size, pretrain_len, local_windo
     rm = np.empty((H, N), np.float32)
     band = np.empty((H, nt, N), np.int32) if want_band else None
     ms = np.float32(dca_mscale(N, pretrain_len))
+    tmask = None
+    if tiles is not None:
+        tmask = np.zeros(nt, np.uint8)
+        tmask[np.asarray(tiles, np.int64)] = 1
     lib().oracle_dca_inter_votes(_p(q), _p(k), ctypes.c_int(dtype), ctypes.c_int(H), ctypes.c_int(Hkv),
                                  ctypes.c_int(N), ctypes.c_int(D), _p(_c(inv_freq, np.float32)),
                                  ctypes.c_int(chunk_size), ctypes.c_int(local_window), ctypes.c_float(ms),
                                  ctypes.c_float(scale), _p(_c(tau, np.float32)), ctypes.c_int(T),
-                                 ctypes.c_float(band_eps), _p(votes), _p(rm), _p(band))
+                                 ctypes.c_float(band_eps), _p(votes), _p(rm), _p(band), _p(tmask))
     out = {"votes": votes, "row_max": rm}
     if want_band:
         out["band"] = band

@@ -579,12 +579,14 @@ static inline float dot_f32(const float* a, const float* b, int D) {
 /*
  * Inter votes: votes (H, nt, N) int32 (0 past each tile's inter keys), row_max (H, N) fp32 (-inf
  * for rows without inter keys), band (H, nt, N) int32 or NULL (# of the tile's rows whose score for
- * the key lies within band_eps of that row's threshold).  T = 64.
+ * the key lies within band_eps of that row's threshold).  T = 64.  tile_mask (nt bytes) or NULL:
+ * only the tiles with a nonzero entry are evaluated (for sampled checks at long lengths); the
+ * others keep zero votes and a NaN row max.
  */
 void oracle_dca_inter_votes(const void* q, const void* k, int dtype, int H, int Hkv, int N, int D,
                             const float* inv_freq, int chunk_size, int local_window, float mscale, float scale,
                             const float* tau, int T, float band_eps, int32_t* votes, float* row_max,
-                            int32_t* band) {
+                            int32_t* band, const uint8_t* tile_mask) {
   const int L = chunk_size - local_window;
   const int group = H / Hkv;
   const int nt = (N + T - 1) / T;
@@ -603,6 +605,10 @@ void oracle_dca_inter_votes(const void* q, const void* k, int dtype, int H, int 
       const int ext = c >= 2 ? (c - 1) * L : 0;
       int32_t* vrow = votes + (size_t)ht * N;
       int32_t* brow = band ? band + (size_t)ht * N : NULL;
+      if (tile_mask && !tile_mask[t]) {
+        for (int i = t * T; i < t * T + T && i < N; ++i) row_max[(size_t)h * N + i] = NAN;
+        continue;
+      }
       for (int i = t * T; i < t * T + T && i < N; ++i) {
         const float* qq = qr + (((size_t)2 * H + h) * N + i) * D;
         float mx = -INFINITY;

@@ -145,7 +145,10 @@ def test_config4_geometry_16k_one_head():
 
 def test_config4_full_size_structure_and_sampled_rows():
     """Config 4 at full size (32 heads x 65536 x d128 bf16): structural invariants of every tile's
-    selection, and 48 sampled rows of two heads against the oracle given the GPU's sets."""
+    selection; head 0's sets rebuilt by the oracle from the GPU's votes (all 1024 tiles, bit for
+    bit); votes and sets of eight deep tiles of head 0 (past position 50k, up to 60928 inter keys)
+    against the oracle's own votes and sets, every differing key classified; and 48 sampled rows
+    of two heads against the oracle given the GPU's sets."""
     import _sta_native as native
     from synthetic import CONFIGS
     cfg = CONFIGS["c4"]
@@ -155,7 +158,7 @@ def test_config4_full_size_structure_and_sampled_rows():
     invf = _invf(cfg.D).to(DEV)
     say("config 4 full size")
     r = native.dca_select_attention(q, k, v, invf, s, c, w, torch.full((cfg.H,), cfg.tau), cfg.pct, cfg.k_max,
-                                    cfg.n_global)
+                                    cfg.n_global, want_votes=True, want_row_max=True)
     torch.cuda.synchronize()
     nt = (cfg.N + 63) // 64
     t = torch.arange(nt, device=DEV)
@@ -171,6 +174,48 @@ def test_config4_full_size_structure_and_sampled_rows():
     assert torch.isfinite(r["out"].float()).all()
     print(f"[result] config 4: kept mean {ks[:, 112:].float().mean().item():.1f} over tiles with inter keys, "
           f"overflow20 {int(r['overflow20'].sum())} of {ks.numel()}", flush=True)
+
+    # head 0: sets given the GPU's votes on every tile, then eight deep tiles against the oracle
+    h = 0
+    deep = [790, 830, 870, 910, 950, 990, 1010, nt - 1]
+    say(f"config 4 head {h}: oracle votes of tiles {deep}")
+    votes_g = r["votes"][h:h + 1].cpu().numpy().astype(np.int32)
+    got = {n: r[n][h:h + 1].cpu().numpy() for n in NAMES}
+    ref_g = orc.dca_build_sets(votes_g, s, w, cfg.n_global, cfg.pct, cfg.k_max, want_cut=True)
+    for name, rv in zip(NAMES, ref_g):
+        assert np.array_equal(got[name].astype(np.int64), rv.astype(np.int64)), f"head {h}: {name} given the votes"
+    qn, dt = np_of(q[0, h:h + 1])
+    kn, _ = np_of(k[0, h:h + 1])
+    vn, _ = np_of(v[0, h:h + 1])
+    a = orc.dca_inter_votes(qn, kn, dt, invf.cpu().numpy(), s, c, w, np.full(1, cfg.tau, np.float32),
+                            want_band=True, tiles=deep)
+    rows_deep = np.concatenate([np.arange(tt * 64, tt * 64 + 64) for tt in deep])
+    rm_g = r["row_max"][h, rows_deep].cpu().numpy()
+    assert np.max(np.abs(rm_g - a["row_max"][0, rows_deep])) < 1e-4, "row max of the deep tiles"
+    ref_o = orc.dca_build_sets(a["votes"], s, w, cfg.n_global, cfg.pct, cfg.k_max, want_cut=True)
+    tot = {"tiles": 0, "tiles_differ": 0, "keys": 0, "band": 0, "cut": 0, "trunc": 0}
+    ndiff = nband = 0
+    for tt in deep:
+        e_t = int(ext[tt])
+        sl = (slice(0, 1), slice(tt, tt + 1))
+        dv, db = check_votes(votes_g[sl][..., :e_t], a["votes"][sl][..., :e_t], a["band"][sl][..., :e_t])
+        ndiff += dv
+        nband += db
+        cnt = classify_set_diffs(votes_g[sl][..., :e_t], a["votes"][sl][..., :e_t], a["band"][sl][..., :e_t],
+                                 {"idx": ref_g[0][sl]}, {"idx": ref_o[0][sl]}, ref_g[7][sl], ref_o[7][sl],
+                                 64, cfg.k_max, cfg.n_global, 0, q_pos_base=tt * 64)
+        tot["tiles"] += 1
+        for n in ("tiles_differ", "keys", "band", "cut", "trunc"):
+            tot[n] += cnt[n]
+    print(f"[result] config 4 head {h}, deep tiles: vote entries differing {ndiff} (band pairs {nband}), "
+          f"inter keys {int(ext[deep[0]])}..{int(ext[deep[-1]])}", flush=True)
+    report_set_diffs(f"config 4 full size, head {h}, {len(deep)} deep tiles", tot)
+    out_ref = orc.dca_select_attn(qn, kn, vn, dt, invf.cpu().numpy(), s, c, w, got["idx"], got["kept_size"],
+                                  rows=rows_deep[::8])
+    e = check_output(r["out"][h:h + 1, rows_deep[::8]].float().cpu().numpy(), out_ref[:, rows_deep[::8]], dt,
+                     f"config 4 head {h} deep rows")
+    print(f"[result] config 4 head {h}: {len(rows_deep[::8])} deep rows, max out err {e:.2e}", flush=True)
+
     rows = list(range(5, cfg.N, cfg.N // 24))[:24] + [cfg.N - 1]
     for h in (0, 17):
         qn, dt = np_of(q[0, h:h + 1])

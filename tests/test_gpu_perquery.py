@@ -224,6 +224,60 @@ def test_perquery_config3_shape_deep_rows():
                     c.k_max, "config 3 shape, first 128 positions, 2 heads")
 
 
+def test_perquery_config3_sampled_positions_whole_sequence():
+    """Config 3 as written (N=16384, d128, bf16, tau 4, PI 1/4, k_max 2048) at every 257th position
+    of two heads, from the first query to the last: scores against the oracle's, sets given the
+    GPU's scores bit for bit, sets against the oracle's own (every differing key classified) and
+    the attend given the GPU's sets."""
+    import _sta_native as native
+    from synthetic import CONFIGS
+    c = CONFIGS["c3q"]
+    q, k, v = c.inputs(DEV)
+    invf, ps, rs = c.geometry()
+    invf_d = invf.to(DEV)
+    invf_n = invf.numpy()
+    sm = 1.0 / math.sqrt(c.D)
+    positions = list(range(0, c.N, 257)) + [c.N - 1]
+    names = ("idx", "newpos_k", "newpos_q", "set_size", "usize", "overflow")
+    for h in (0, 1):
+        say(f"config 3 sampled positions: head {h}, {len(positions)} queries")
+        tau = torch.full((1,), c.tau, device=DEV)
+        tau_n = tau.cpu().numpy()
+        tot = {"rows": 0, "keys": 0, "thr": 0, "cut": 0, "capped": 0}
+        worst_s = worst_o = 0.0
+        for p in positions:
+            qq, kk, vv = q[0, h:h + 1, p:p + 1], k[0, h:h + 1, :p + 1], v[0, h:h + 1, :p + 1]
+            r = native.decode_attention(qq, kk, vv, tau, invf_d, p, ps, rs, sm, c.n_global, c.n_local, c.k_max, 100.0,
+                                        False, want_scores=True, inv_freq_c=invf_d, pos_scale_c=1.0,
+                                        rope_scale_c=1.0, rule="pq")
+            torch.cuda.synchronize()
+            qn, dt = np_of(qq)
+            kn, _ = np_of(kk)
+            vn, _ = np_of(vv)
+            s_g = r["scores"].cpu().numpy()
+            s_o = orc.decode_scores(qn, kn, dt, invf_n, ps, rs, sm, p)
+            worst_s = max(worst_s, float(np.max(np.abs(s_g - s_o))))
+            assert worst_s < 1e-4, f"position {p}: scores differ from the oracle's by {worst_s:.3e}"
+            got = {n: r[n].cpu().numpy() for n in names}
+            ref = orc.decode_build_sets_pq(s_g, tau_n, p, c.n_global, c.n_local, c.k_max)
+            for name, rv in zip(names, ref):
+                assert np.array_equal(got[name], rv), f"position {p}: {name} differs given the GPU's scores"
+            own = orc.decode_build_sets_pq(s_o, tau_n, p, c.n_global, c.n_local, c.k_max)
+            rows, keys, nthr, ncut = classify_pq_rows(got["idx"], own[0], s_o, tau_n, p, p + 1, c.n_global,
+                                                      c.n_local, c.k_max)
+            for n_, x in zip(("rows", "keys", "thr", "cut"), (rows, keys, nthr, ncut)):
+                tot[n_] += x
+            tot["capped"] += int(got["overflow"].sum())
+            out_ref = orc.decode_attend(qn, kn, vn, dt, invf_n, 1.0, sm, p, got["idx"], got["newpos_k"],
+                                        got["newpos_q"])
+            worst_o = max(worst_o, check_output(r["out"].float().cpu().numpy(), out_ref, dt, f"position {p}"))
+        print(f"[sets] config 3 as written, head {h}, every 257th position ({len(positions)} queries, "
+              f"{tot['capped']} capped): {tot['rows']} queries' sets differ from the oracle's; {tot['keys']} keys: "
+              f"{tot['thr']} within 1e-3 of the threshold, {tot['cut']} within 1e-3 of the cap cut, 0 other",
+              flush=True)
+        print(f"[result] config 3 head {h}: max score err {worst_s:.2e}, max out err {worst_o:.2e}", flush=True)
+
+
 def test_perquery_full_prefill_plan_config3_structure():
     """The whole config-3 prefill (32 heads x 16384 positions) through the head-grouped plan:
     structural invariants on every query and the output of sampled rows of one head against the

@@ -105,6 +105,28 @@ def test_votes_against_float64_brute_force():
     assert (a["votes"] > 0).sum() > 1000
 
 
+def test_tile_subset_equals_the_full_evaluation():
+    """dca_inter_votes(tiles=...) evaluates only the listed tiles: their votes, band counts and row
+    maxima equal the full evaluation's, every other tile keeps zero votes and a NaN row max."""
+    H, Hkv, N, D = 2, 1, 1500, 64
+    q, k, _ = _inputs(5, H, Hkv, N, D)
+    invf = _invf(D)
+    tau = np.full(H, 2.5, np.float32)
+    full = orc.dca_inter_votes(q, k, orc.F32, invf, S, C, W, tau, want_band=True)
+    tiles = [9, 15, 23]
+    part = orc.dca_inter_votes(q, k, orc.F32, invf, S, C, W, tau, want_band=True, tiles=tiles)
+    nt = (N + 63) // 64
+    keep = np.zeros(nt, bool)
+    keep[tiles] = True
+    rows = np.repeat(keep, 64)[:N]
+    assert np.array_equal(part["votes"][:, keep], full["votes"][:, keep])
+    assert np.array_equal(part["band"][:, keep], full["band"][:, keep])
+    assert not part["votes"][:, ~keep].any() and not part["band"][:, ~keep].any()
+    assert np.array_equal(part["row_max"][:, rows], full["row_max"][:, rows])
+    assert np.isnan(part["row_max"][:, ~rows]).all()
+    assert (full["votes"][:, keep] > 0).sum() > 100
+
+
 def test_sets_are_build_sets_on_each_tiles_inter_axis():
     H, N, D = 2, 1500, 64
     q, k, v = _inputs(4, H, H, N, D)
