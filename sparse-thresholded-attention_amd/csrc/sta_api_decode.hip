@@ -289,6 +289,8 @@ int sta_decode_attention(const sta_decode_args* a, void* stream) {
   if ((rc = mark_event(a->stage_events, 1, st)) != STA_OK) return rc;
   if ((rc = dec_select(a, d, d.scores, st)) != STA_OK) return rc;
   if ((rc = mark_event(a->stage_events, 2, st)) != STA_OK) return rc;
+  // the per-query rule's selection just wrote newpos_k = the slot index of every slot
+  d.dense_ranks = a->rule == STA_RULE_PQ ? 1 : 0;
   if ((rc = dec_attend(a, d, st)) != STA_OK) return rc;
   return mark_event(a->stage_events, 3, st);
 }

@@ -17,6 +17,9 @@
 //                         workgroups of 64 slots, 16 lanes per slot and four slots per lane
 //                         group (every row request in flight at once), each split a softmax
 //                         state; decode_combine_kernel merges the splits
+//   decode_attend_grouped_kernel  the per-query rule's attend for a batch (perquery.py:724-778):
+//                         16 queries per workgroup, one 16-lane group per query, the dense-rank
+//                         (cos, sin) table of each 64-slot block shared in LDS
 #include <float.h>
 
 #include "sta_device.h"
@@ -802,6 +805,219 @@ __global__ __launch_bounds__(256) void decode_attend_kernel(DecodeArgs a, int st
   }
 }
 
+// ------------------------------------------------------------------------------------------
+// attend for a large batch under the per-query rule: 16 queries of one head per workgroup, one
+// 16-lane group per query sweeping all of its slots and writing the output.  Each half of a group
+// (8 lanes) takes its own slots, a lane holding D/16 rotation pairs of the slot's K and V rows, so
+// every row arrives in 16-byte loads (bf16, D = 128): the vector memory pipeline, not the
+// arithmetic, bounds this gather, and its cost goes by load instructions.  Under
+// _decode_build_sets_pq every slot s sits at its dense rank s (perquery.py:707-717: idx is
+// ascending and newpos_k gathers the ranks at idx), so the (cos, sin) of slot s are the same for
+// every query: the workgroup computes them once per block of DEC_TB slots into LDS.  The launcher
+// takes this kernel only when the selection of the same call wrote the sets (dense_ranks); sets
+// from the caller go to the split attend, which reads every slot's position.
+// ------------------------------------------------------------------------------------------
+constexpr int DEC_QPW = 16;                    // queries per workgroup
+constexpr int DEC_TB = 64;                     // slots per table block
+
+namespace {
+
+// NF consecutive elements of a row as raw 32-bit words (bf16 / f16 pairs or fp32)
+template <int DT, int NF>
+struct RowPart {
+  static constexpr int NW = NF * (DT == DT_F32 ? 4 : 2) / 4;
+  uint32_t w[NW];
+};
+
+template <int DT, int NF>
+__device__ __forceinline__ void load_part(const void* p, int64_t i, RowPart<DT, NF>& r) {
+  constexpr int NW = RowPart<DT, NF>::NW;
+  const uint32_t* src = (const uint32_t*)((const char*)p + i * (DT == DT_F32 ? 4 : 2));
+  if constexpr (NW % 4 == 0) {
+#pragma unroll
+    for (int u = 0; u < NW / 4; ++u) {
+      const u32x4 x = ((const u32x4*)src)[u];
+      r.w[4 * u] = x[0]; r.w[4 * u + 1] = x[1]; r.w[4 * u + 2] = x[2]; r.w[4 * u + 3] = x[3];
+    }
+  } else {
+    static_assert(NW == 2, "row part width");
+    const u32x2 x = *(const u32x2*)src;
+    r.w[0] = x[0]; r.w[1] = x[1];
+  }
+}
+
+template <int DT, int NF>
+__device__ __forceinline__ float part_elem(const RowPart<DT, NF>& r, int e) {
+  if constexpr (DT == DT_F32) return __uint_as_float(r.w[e]);
+  else if constexpr (DT == DT_BF16) return __uint_as_float((e & 1) ? (r.w[e >> 1] & 0xffff0000u) : (r.w[e >> 1] << 16));
+  else return f16_bits_to_f32((e & 1) ? (r.w[e >> 1] >> 16) : (r.w[e >> 1] & 0xffffu));
+}
+
+}  // namespace
+
+constexpr int DEC_GU = 4;                      // slots per half group and step
+
+template <int DT, int D, bool IDX4>
+__global__ __launch_bounds__(256) void decode_attend_grouped_kernel(DecodeArgs a) {
+#pragma clang fp contract(off)
+  constexpr int HD = D / 2;
+  constexpr int NF = D / 16;                   // rotation pairs per lane (8 lanes per slot)
+  constexpr int U = DEC_GU;
+  __shared__ __align__(16) float tcs[DEC_TB][HD];
+  __shared__ __align__(16) float tsn[DEC_TB][HD];
+  __shared__ int wmax;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int l16 = lane & 15, grp = wave * 4 + (lane >> 4);
+  const int half = l16 >> 3, l8 = l16 & 7;
+  const int f0 = l8 * NF;                      // this lane's frequencies f0 .. f0 + NF - 1
+  // workgroup -> (head, query group), the latest query groups (the largest sets) first
+  const int nqg = (a.Q + DEC_QPW - 1) / DEC_QPW;
+  const int h = blockIdx.x % a.H;
+  const int qg = nqg - 1 - (int)(blockIdx.x / a.H);
+  const int i = qg * DEC_QPW + grp;
+  const bool live = i < a.Q;
+  const int ic = live ? i : a.Q - 1;
+  const int hi = h * a.Q + ic;
+  const int hk = h / (a.H / a.Hkv);
+  const int m = a.M - (a.Q - 1 - ic);
+  const int p = a.q_pos0 + ic;
+  const int nslots = !live ? 0 : (a.set_size ? min(a.set_size[hi], a.k_max) : a.k_max);
+  if (threadIdx.x == 0) wmax = 0;
+  __syncthreads();
+  if (l16 == 0 && nslots > 0) atomicMax(&wmax, nslots);
+  // the query rotated at newpos_q, this lane's pairs
+  float q1[NF], q2[NF];
+  {
+    float x1[NF], x2[NF];
+    const int64_t qb = (int64_t)h * a.q_hs + (int64_t)ic * a.q_ts + f0;
+    load_n<DT, NF>(a.q, qb, x1);
+    load_n<DT, NF>(a.q, qb + HD, x2);
+    const float npq = a.newpos_q[hi];
+#pragma unroll
+    for (int e = 0; e < NF; ++e) {
+      float sn, cs;
+      fast_sincos(npq * a.inv_freq_c[f0 + e], sn, cs);
+      cs = cs * a.rope_scale_c;
+      sn = sn * a.rope_scale_c;
+      q1[e] = x1[e] * cs - x2[e] * sn;
+      q2[e] = x2[e] * cs + x1[e] * sn;
+    }
+  }
+  const int32_t* irow = a.idx + (int64_t)hi * a.k_max;
+  // the query's running max (the same in both halves) and each half's sum and accumulators
+  float mrun = -INFINITY, lrun = 0.0f, acc1[NF], acc2[NF];
+#pragma unroll
+  for (int e = 0; e < NF; ++e) { acc1[e] = 0.0f; acc2[e] = 0.0f; }
+  __syncthreads();
+  const int nall = wmax;
+  for (int s0 = 0; s0 < nall; s0 += DEC_TB) {
+    if (s0 > 0) __syncthreads();               // every group is done with the previous block
+    for (int x = threadIdx.x; x < DEC_TB * HD; x += 256) {
+      const int r = x / HD, f = x % HD;
+      float sn, cs;
+      fast_sincos((float)(s0 + r) * a.inv_freq_c[f], sn, cs);
+      tcs[r][f] = cs * a.rope_scale_c;
+      tsn[r][f] = sn * a.rope_scale_c;
+    }
+    __syncthreads();
+    const int send = min(nslots, s0 + DEC_TB);
+    for (int t0 = s0; t0 < send; t0 += 2 * U) {
+      const int sb = t0 + half * U;            // this half's U slots sb .. sb + U - 1
+      int jv[U];
+      bool okv[U];
+      if constexpr (IDX4 && U == 4) {          // 16-byte aligned rows: the 4 indices in one load
+        int4 iv = make_int4(-1, -1, -1, -1);
+        if (sb < send) iv = *(const int4*)(irow + sb);   // sb + 3 < k_max (k_max % 4 == 0)
+        jv[0] = iv.x; jv[1] = iv.y; jv[2] = iv.z; jv[3] = iv.w;
+      } else if constexpr (IDX4 && U == 2) {   // 8-byte aligned pairs
+        int2 iv = make_int2(-1, -1);
+        if (sb < send) iv = *(const int2*)(irow + sb);   // sb + 1 < k_max (k_max even)
+        jv[0] = iv.x; jv[1] = iv.y;
+      } else {
+#pragma unroll
+        for (int u = 0; u < U; ++u) jv[u] = sb + u < send ? irow[sb + u] : -1;
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int j = sb + u < send ? jv[u] : -1;
+        okv[u] = j >= 0 && j < m && (!a.causal || j <= p);   // sentinel m (perquery.py:739)
+        jv[u] = okv[u] ? j : 0;
+      }
+      RowPart<DT, NF> k1r[U], k2r[U], v1r[U], v2r[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int64_t kb = (int64_t)hk * a.k_hs + (int64_t)jv[u] * a.k_ts + f0;
+        const int64_t vb = (int64_t)hk * a.v_hs + (int64_t)jv[u] * a.v_ts + f0;
+        load_part<DT, NF>(a.k, kb, k1r[u]);
+        load_part<DT, NF>(a.k, kb + HD, k2r[u]);
+        load_part<DT, NF>(a.v, vb, v1r[u]);
+        load_part<DT, NF>(a.v, vb + HD, v2r[u]);
+      }
+      float sc[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int r = min(sb + u - s0, DEC_TB - 1);   // the slot's dense rank: the block's table
+        float part = 0.0f;
+#pragma unroll
+        for (int e = 0; e < NF; ++e) {
+          const float cs = tcs[r][f0 + e], sn = tsn[r][f0 + e];
+          const float x1 = part_elem(k1r[u], e), x2 = part_elem(k2r[u], e);
+          const float k1 = x1 * cs - x2 * sn;
+          const float k2 = x2 * cs + x1 * sn;
+          part = fmaf(q2[e], k2, fmaf(q1[e], k1, part));
+        }
+        part += __shfl_xor(part, 1, 64);
+        part += __shfl_xor(part, 2, 64);
+        part += __shfl_xor(part, 4, 64);
+        sc[u] = okv[u] ? part * a.sm_scale : -INFINITY;
+      }
+      // the step's max over both halves' slots, then each half folds its own slots in
+      float mst = -INFINITY;
+#pragma unroll
+      for (int u = 0; u < U; ++u) mst = fmaxf(mst, sc[u]);
+      mst = fmaxf(mst, __shfl_xor(mst, 8, 64));
+      if (mst > -INFINITY) {
+        const float mn = fmaxf(mrun, mst);
+        const float wo = mrun == -INFINITY ? 0.0f : __expf(mrun - mn);
+        lrun = lrun * wo;
+#pragma unroll
+        for (int e = 0; e < NF; ++e) {
+          acc1[e] = acc1[e] * wo;
+          acc2[e] = acc2[e] * wo;
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const float pw = okv[u] ? __expf(sc[u] - mn) : 0.0f;
+          lrun += pw;
+#pragma unroll
+          for (int e = 0; e < NF; ++e) {
+            acc1[e] = fmaf(pw, part_elem(v1r[u], e), acc1[e]);
+            acc2[e] = fmaf(pw, part_elem(v2r[u], e), acc2[e]);
+          }
+        }
+        mrun = mn;
+      }
+    }
+  }
+  // both halves' sums and accumulators; half 0 writes the first D/2 dims, half 1 the rest
+  lrun += __shfl_xor(lrun, 8, 64);
+  float o[NF];
+#pragma unroll
+  for (int e = 0; e < NF; ++e) {
+    const float x1 = acc1[e] + __shfl_xor(acc1[e], 8, 64);
+    const float x2 = acc2[e] + __shfl_xor(acc2[e], 8, 64);
+    const float x = half ? x2 : x1;
+    o[e] = lrun > 0.0f ? x / lrun : 0.0f;      // no valid slot: zeros
+  }
+  if (!live) return;
+  const int64_t ob = (int64_t)hi * D + half * HD + f0;
+#pragma unroll
+  for (int e = 0; e < NF; ++e) {
+    if constexpr (DT == DT_F32) ((float*)a.out)[ob + e] = o[e];
+    else ((uint16_t*)a.out)[ob + e] = (uint16_t)(DT == DT_BF16 ? f32_to_bf16_bits(o[e]) : f32_to_f16_bits(o[e]));
+  }
+}
+
 // merge the splits of one query: 256 threads, 256 / D per dim
 template <int DT, int D>
 __global__ __launch_bounds__(256) void decode_combine_kernel(DecodeArgs a, int ns) {
@@ -897,6 +1113,14 @@ hipError_t launch_decode_select(const DecodeArgs& a, hipStream_t st) {
 
 template <int DT, int D>
 static hipError_t launch_attend_t(const DecodeArgs& a, hipStream_t st) {
+  if (a.dense_ranks && a.Q >= DEC_QPW) {         // per-query rule, a batch: grouped queries
+    const int nqg = (a.Q + DEC_QPW - 1) / DEC_QPW;
+    if (a.k_max % 4 == 0 && (uintptr_t)a.idx % 16 == 0)
+      hipLaunchKernelGGL((decode_attend_grouped_kernel<DT, D, true>), dim3(a.H * nqg), dim3(256), 0, st, a);
+    else
+      hipLaunchKernelGGL((decode_attend_grouped_kernel<DT, D, false>), dim3(a.H * nqg), dim3(256), 0, st, a);
+    return hipGetLastError();
+  }
   const int nmax = decode_nsplit(a.k_max);
   if (nmax > 1024) return hipErrorInvalidValue;   // the merge kernel's split capacity: k_max <= 65536
   const int ns = decode_attend_splits(a.Q, a.k_max);

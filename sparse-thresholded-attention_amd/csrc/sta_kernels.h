@@ -307,6 +307,7 @@ struct DecodeArgs {
   int block_n;            // rule 2: the position blocks
   int32_t* usize;         // (H, Q) or null: rule 1, |threshold passers|
   uint8_t* overflow;      // (H, Q) or null: rule 1, passers U forced above k_max
+  int dense_ranks;        // rule 1 in one call with its selection: newpos_k[s] == s on every slot
 };
 
 // scores of a batch of queries from the RoPE pre-kernel's fragments (matrix cores)

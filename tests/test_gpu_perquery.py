@@ -224,6 +224,61 @@ def test_perquery_config3_shape_deep_rows():
                     c.k_max, "config 3 shape, first 128 positions, 2 heads")
 
 
+@pytest.mark.parametrize("D,dt", [(128, torch.bfloat16), (64, torch.float32), (128, torch.float16)])
+def test_grouped_attend_any_positions(D, dt):
+    """The batched per-query attend (16 queries per workgroup, the dense-rank (cos, sin) table in
+    LDS): a batch of 40 queries (a partial last group) against the oracle given the GPU's sets;
+    the same queries in batches of 10 (the split attend) within the output tolerance; and the
+    attend alone over sets with positions that are not the slot indices (newpos_k + 2.5,
+    newpos_q + 2.5) against the oracle: sets from the caller take the split attend, which reads
+    every slot's position."""
+    import _sta_native as native
+    from synthetic import base_inv_freq, planted_inputs
+    H, N, Q = 2, 900, 40
+    q, k, v = planted_inputs(91, H, H, N, D, 0.02, dt, DEV)
+    invf = base_inv_freq(D, 10000.0).to(DEV)
+    tau = torch.full((H,), 3.0, device=DEV)
+    q0 = N - Q
+    qq, kk, vv = q[0, :, q0:], k[0], v[0]
+    sm = 1.0 / math.sqrt(D)
+    say(f"grouped per-query attend: H={H} Q={Q} M={N} D={D} {dt}")
+    plan = native.DecodePlan(qq, kk, vv, tau, invf, q0, 0.5, 1.0, sm, 16, 16, 256, 100.0, False,
+                             inv_freq_c=invf, pos_scale_c=1.0, rope_scale_c=1.0, rule="pq")
+    r = plan.run()
+    torch.cuda.synchronize()
+    got = {n: r[n].clone() for n in ("out", "idx", "newpos_k", "newpos_q", "set_size")}
+    assert int(r["overflow"].sum()) > 0, "the cap binds for some queries"
+    qn, dtc = np_of(qq)
+    kn, _ = np_of(kk)
+    vn, _ = np_of(vv)
+    invf_n = invf.cpu().numpy()
+    out_ref = orc.decode_attend(qn, kn, vn, dtc, invf_n, 1.0, sm, q0, got["idx"].cpu().numpy(),
+                                got["newpos_k"].cpu().numpy(), got["newpos_q"].cpu().numpy())
+    e1 = check_output(got["out"].float().cpu().numpy(), out_ref, dtc, "grouped attend")
+    # the same queries through the split attend (batches below 16 queries)
+    worst = 0.0
+    for i0 in range(0, Q, 10):
+        r1 = native.decode_attention(qq[:, i0:i0 + 10], kk[:, :q0 + i0 + 10], vv[:, :q0 + i0 + 10], tau, invf,
+                                     q0 + i0, 0.5, 1.0, sm, 16, 16, 256, 100.0, False, inv_freq_c=invf,
+                                     pos_scale_c=1.0, rope_scale_c=1.0, rule="pq")
+        torch.cuda.synchronize()
+        assert torch.equal(r1["idx"], got["idx"][:, i0:i0 + 10]), "sets do not depend on the batch"
+        worst = max(worst, (r1["out"].float() - got["out"][:, i0:i0 + 10].float()).abs().max().item())
+    tol = 1e-5 if dt == torch.float32 else 2e-2
+    assert worst <= tol, f"grouped vs split attend differ by {worst:.3e}"
+    # positions that are not the slot indices
+    npk = torch.where(got["idx"] < N, got["newpos_k"] + 2.5, got["newpos_k"])
+    npq = got["newpos_q"] + 2.5
+    out2 = plan.attend(got["idx"], npk, npq, got["set_size"]).clone()
+    torch.cuda.synchronize()
+    out_ref2 = orc.decode_attend(qn, kn, vn, dtc, invf_n, 1.0, sm, q0, got["idx"].cpu().numpy(), npk.cpu().numpy(),
+                                 npq.cpu().numpy())
+    e2 = check_output(out2.float().cpu().numpy(), out_ref2, dtc, "grouped attend, shifted positions")
+    assert (out2.float() - got["out"].float()).abs().max().item() > 0, "the shifted positions changed the output"
+    print(f"[result] grouped attend {D} {dt}: max out err {e1:.2e}, vs split {worst:.2e}, shifted positions "
+          f"{e2:.2e}", flush=True)
+
+
 def test_perquery_config3_sampled_positions_whole_sequence():
     """Config 3 as written (N=16384, d128, bf16, tau 4, PI 1/4, k_max 2048) at every 257th position
     of two heads, from the first query to the last: scores against the oracle's, sets given the
