@@ -630,6 +630,320 @@ __global__ __launch_bounds__(NT) void decode_select_kernel(DecodeArgs a) {
 }
 
 // ------------------------------------------------------------------------------------------
+// _decode_build_sets_pq (perquery.py:651-720) for one query per workgroup, the row staged in LDS:
+//   1. stage the scores as order-preserving keys and take the exact max (perquery.py:683);
+//   2. one pass counts the passers s >= max - tau (:684, :688) and histograms the non-forced
+//      passers into DEC_PQ_BINS bins linear in the value between the threshold and the max;
+//   3. under the cap (:690-701) the bin holding the budget-th largest non-forced passer is found
+//      from the histogram and its keys are ranked directly: the cut V and how many keys equal to
+//      V are taken (torch.topk's exact budget; ties in ascending key order).  A bin with more
+//      than DEC_PQ_CAND keys is split again by key-space bins of its own range, as often as
+//      needed (each level divides the range by 4096);
+//   4. one pass counts each thread's kept keys and its keys equal to V (one packed scan), one
+//      pass writes idx ascending with the dense ranks (:703-719).
+// Bit-identical to decode_select_kernel's rule 1, in fewer passes over the row.
+// ------------------------------------------------------------------------------------------
+constexpr int DEC_PQ_BINS = 4096;            // 16-bit counters, two per LDS word
+constexpr int DEC_PQ_CAND = 512;             // keys of the cut bin ranked directly
+
+size_t decode_select_pq_lds_bytes(int M, int NT) {
+  const int per = (M + NT - 1) / NT;
+  return (size_t)NT * (per | 1) * 4 + DEC_PQ_BINS / 2 * 4 + DEC_PQ_CAND * 4 + 256;
+}
+
+template <int NT>
+__global__ __launch_bounds__(NT) void decode_select_pq_kernel(DecodeArgs a) {
+#pragma clang fp contract(off)
+  constexpr int NW = NT / 64;
+  constexpr int NB = DEC_PQ_BINS;
+  extern __shared__ __align__(16) uint32_t dsm[];
+  const int tid = threadIdx.x;
+  const int hi = blockIdx.x;
+  const int h = hi / a.Q, i = hi % a.Q;
+  const int m = a.M - (a.Q - 1 - i);           // keys this query sees
+  const int p = a.q_pos0 + i;                  // its position (p < m)
+  const int per_max = (a.M + NT - 1) / NT;
+  const int per = (m + NT - 1) / NT;
+  const int PS = per | 1;                      // odd row stride: conflict-free scans
+  uint32_t* ks = dsm;
+  uint32_t* hist = dsm + NT * (per_max | 1);   // NB / 2 words
+  uint32_t* cand = hist + NB / 2;              // DEC_PQ_CAND
+  int* tmp = (int*)(cand + DEC_PQ_CAND);       // NW
+  int* misc = tmp + NW;                        // 8
+  const int j0 = tid * per, j1 = min(j0 + per, m);
+  const int nk = max(j1 - j0, 0);
+  uint32_t* myrow = ks + tid * PS;
+  const float* srow = a.scores + (int64_t)hi * a.M;
+
+  // ---- 1. stage the scores as keys, exact max.  16-byte reads (four keys per lane and load,
+  // eight loads in flight) when the row is 16-byte aligned; the vector memory unit's cost goes
+  // by load instructions ----
+  uint32_t kmax = 0;
+  auto put = [&](int j, float v) {             // key j < NT * per into its owner's row
+    const uint32_t key = j < m ? okey(v) : 0u;
+    kmax = max(kmax, key);
+    const int row = j / per;
+    ks[row * PS + (j - row * per)] = key;
+  };
+  if (((uintptr_t)srow & 15) == 0) {
+    const int nq = (NT * per + 3) / 4;         // float4 units covering the keys of every row
+    for (int e0 = 0; e0 * NT < nq; e0 += 8) {
+      float4 sv[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int qd = tid + (e0 + u) * NT;    // keys 4 qd .. 4 qd + 3
+        sv[u] = (qd < nq && 4 * qd + 3 < m) ? ((const float4*)srow)[qd] : make_float4(0.f, 0.f, 0.f, 0.f);
+        if (qd < nq && 4 * qd < m && 4 * qd + 3 >= m) {   // the row's ragged end
+          sv[u].x = srow[4 * qd];
+          if (4 * qd + 1 < m) sv[u].y = srow[4 * qd + 1];
+          if (4 * qd + 2 < m) sv[u].z = srow[4 * qd + 2];
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int qd = tid + (e0 + u) * NT;
+        if (qd < nq) {
+          const int j = 4 * qd;
+          if (j < NT * per) put(j, sv[u].x);
+          if (j + 1 < NT * per) put(j + 1, sv[u].y);
+          if (j + 2 < NT * per) put(j + 2, sv[u].z);
+          if (j + 3 < NT * per) put(j + 3, sv[u].w);
+        }
+      }
+    }
+  } else {
+    for (int e0 = 0; e0 < per; e0 += 8) {
+      float sv[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int j = tid + (e0 + u) * NT;
+        sv[u] = (e0 + u < per && j < m) ? srow[j] : 0.0f;
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        if (e0 + u < per) put(tid + (e0 + u) * NT, sv[u]);
+    }
+  }
+  for (int b = tid; b < NB / 2; b += NT) hist[b] = 0u;
+  if (tid < 8) misc[tid] = 0;
+  kmax = dmax_u<NW>(kmax, (uint32_t*)tmp);       // the barrier inside also publishes the stores
+  const float vmax = okey_value(kmax);
+  const float thr = vmax - a.tau[h];                                   // perquery.py:684
+  const uint32_t kthr = okey(thr);
+  // forced keys: [0, g) U [lo, p] (global, local window, self; perquery.py:676-679)
+  const int g = min(a.n_global, m);
+  const int lo = min(max(0, p - a.n_local + 1), p);
+  const int nforced = g + max(p - max(lo, g) + 1, 0);
+  auto forced = [&](int j) { return j < g || (j >= lo && j <= p); };
+
+  // ---- 2. passers, non-forced passers with their value histogram and key range ----
+  const float span0 = vmax - thr;
+  const bool lin = span0 > 0.0f && span0 < INFINITY;   // value-linear bins over [thr, max]
+  const float inv0 = lin ? (float)NB / span0 : 0.0f;
+  int c_pass = 0, c_nf = 0;
+  uint32_t kmin_nf = 0xffffffffu, kmax_nf = 0u;
+  for (int e = 0; e < nk; ++e) {
+    const uint32_t k = myrow[e];
+    if (k >= kthr) {
+      ++c_pass;
+      if (!forced(j0 + e)) {
+        ++c_nf;
+        kmin_nf = min(kmin_nf, k);
+        kmax_nf = max(kmax_nf, k);
+        if (lin) {
+          const int b = min((int)((okey_value(k) - thr) * inv0), NB - 1);
+          atomicAdd(&hist[b >> 1], 1u << ((b & 1) * 16));
+        }
+      }
+    }
+  }
+  if (c_nf > 0) {
+    atomicMax((unsigned*)&misc[6], ~kmin_nf);   // misc[6] = ~(min key): starts at 0 = ~0xffffffff
+    atomicMax((unsigned*)&misc[7], kmax_nf);
+  }
+  const int packed = dsum<NW>(c_pass | (c_nf << 16), tmp);   // each count < 65536
+  const int ge = packed & 0xffff, n_nf = packed >> 16;
+  const int count = n_nf + nforced;            // |passers U forced| (perquery.py:687-688)
+  if (tid == 0) {
+    if (a.usize) a.usize[hi] = ge;
+    if (a.overflow) a.overflow[hi] = count > a.k_max ? 1 : 0;
+  }
+
+  // ---- 3. the cap cut over the non-forced passers (perquery.py:690-701) ----
+  bool only_forced = false, exact_cut = false;
+  uint32_t V = 0u;
+  int quota = 0;
+  if (count > a.k_max) {
+    const int budget = a.k_max - nforced;
+    if (budget <= 0) {
+      only_forced = true;
+    } else {
+      exact_cut = true;
+      int need = budget;                       // rank from the top among the keys in range
+      uint32_t rlo = ~(uint32_t)misc[6], rhi = (uint32_t)misc[7];   // key range of the level
+      bool linear = lin;                       // level 0: the value bins filled in pass 2
+      int shift = 0;
+      for (;;) {                               // levels: each divides the range by NB
+        if (!linear) {
+          if (rlo == rhi) {                    // every key in range equals the cut
+            V = rlo;
+            quota = need;
+            break;
+          }
+          shift = max(0, 32 - __clz(rhi - rlo) - 12);   // (rhi - rlo) >> shift < NB
+          __syncthreads();
+          for (int b = tid; b < NB / 2; b += NT) hist[b] = 0u;
+          __syncthreads();
+          for (int e = 0; e < nk; ++e) {
+            const uint32_t k = myrow[e];
+            if (k >= rlo && k <= rhi && !forced(j0 + e)) {
+              const int b = (int)((k - rlo) >> shift);
+              atomicAdd(&hist[b >> 1], 1u << ((b & 1) * 16));
+            }
+          }
+          __syncthreads();
+        }
+        auto bin_of = [&](uint32_t k) {
+          return linear ? min((int)((okey_value(k) - thr) * inv0), NB - 1) : (int)((k - rlo) >> shift);
+        };
+        // bins in descending order, BPT per thread: the bin holding the need-th largest
+        constexpr int BPT = NB / NT;
+        int c[BPT], sl = 0;
+#pragma unroll
+        for (int e = 0; e < BPT; ++e) {
+          const int bb = NB - 1 - BPT * tid - e;
+          c[e] = (int)((hist[bb >> 1] >> ((bb & 1) * 16)) & 0xffffu);
+          sl += c[e];
+        }
+        const int excl = dexcl_sum<NW>(sl, tmp);
+        if (excl < need && excl + sl >= need) {
+          int acc = excl, d = NB - 1 - BPT * tid, e = 0;
+          for (; e < BPT - 1; ++e) {
+            if (acc + c[e] >= need) break;
+            acc += c[e];
+            d -= 1;
+          }
+          misc[0] = d;
+          misc[1] = need - acc;                // rank within the bin
+          misc[2] = c[e];                      // keys in the bin
+          misc[3] = 0;                         // collected keys
+          misc[4] = 0;                         // ~(min key of the bin)
+          misc[5] = 0;                         // max key of the bin
+        }
+        __syncthreads();
+        const int dbin = misc[0], cd = misc[2];
+        need = misc[1];
+        auto in_bin = [&](int e, uint32_t k) {
+          return k >= kthr && (linear || (k >= rlo && k <= rhi)) && !forced(j0 + e) && bin_of(k) == dbin;
+        };
+        if (cd <= DEC_PQ_CAND) {
+          for (int e = 0; e < nk; ++e) {
+            const uint32_t k = myrow[e];
+            if (in_bin(e, k)) cand[atomicAdd(&misc[3], 1)] = k;
+          }
+          __syncthreads();
+          if (tid < cd) {
+            const uint32_t v = cand[tid];
+            int gt = 0, eq = 0;
+            for (int u = 0; u < cd; ++u) {
+              const uint32_t w = cand[u];
+              gt += w > v;
+              eq += w == v;
+            }
+            if (gt < need && gt + eq >= need) {   // the keys equal to the cut agree
+              misc[6] = (int)v;
+              misc[7] = need - gt;
+            }
+          }
+          __syncthreads();
+          V = (uint32_t)misc[6];
+          quota = misc[7];
+          break;
+        }
+        // more than DEC_PQ_CAND keys in the bin: its key range is the next level's
+        uint32_t bmin = 0xffffffffu, bmax = 0u;
+        for (int e = 0; e < nk; ++e) {
+          const uint32_t k = myrow[e];
+          if (in_bin(e, k)) {
+            bmin = min(bmin, k);
+            bmax = max(bmax, k);
+          }
+        }
+        if (bmax >= bmin) {
+          atomicMax((unsigned*)&misc[4], ~bmin);   // ~(min key)
+          atomicMax((unsigned*)&misc[5], bmax);
+        }
+        __syncthreads();
+        rlo = ~(uint32_t)misc[4];
+        rhi = (uint32_t)misc[5];
+        linear = false;
+      }
+    }
+  }
+  // 0: not kept, 1: kept, 2: equal to the cut (the first `quota` of them in key order are kept)
+  auto klass = [&](int j, uint32_t k) -> int {
+    if (forced(j)) return 1;
+    if (only_forced) return 0;
+    if (!exact_cut) return k >= kthr ? 1 : 0;
+    if (k == V) return 2;
+    return k > V ? 1 : 0;
+  };
+
+  // ---- 4. compaction with dense ranks (perquery.py:703-719) ----
+  int n1 = 0, n2 = 0;
+  for (int e = 0; e < nk; ++e) {
+    const int cl = klass(j0 + e, myrow[e]);
+    n1 += cl == 1;
+    n2 += cl == 2;
+  }
+  int tot;
+  const int pre = dexcl_sum<NW>(n1 | (n2 << 16), tmp, &tot);    // each total < 65536
+  const int pre2 = pre >> 16;
+  const int total = (tot & 0xffff) + min(tot >> 16, quota);
+  int32_t* irow = a.idx + (int64_t)hi * a.k_max;
+  float* nrow = a.newpos_k + (int64_t)hi * a.k_max;
+  // the kept keys are gathered in LDS (the histogram and candidate words, free now) and written
+  // coalesced when k_max fits there; the slot positions are the slot indices (dense ranks)
+  const bool staged = a.k_max <= NB / 2 + DEC_PQ_CAND;
+  int* obuf = (int*)hist;
+  __syncthreads();                             // every read of the histogram / candidates is done
+  {
+    int rank = (pre & 0xffff) + min(pre2, quota) - 1, tie = pre2;
+    for (int e = 0; e < nk; ++e) {
+      const int j = j0 + e;
+      const int cl = klass(j, myrow[e]);
+      const bool f = cl == 1 || (cl == 2 && tie++ < quota);
+      if (f) {
+        rank += 1;
+        if (rank < a.k_max) {
+          if (staged) {
+            obuf[rank] = j;
+          } else {
+            irow[rank] = j;
+            nrow[rank] = (float)rank;
+          }
+        }
+      }
+      if (j == p) a.newpos_q[hi] = (float)rank;   // the query itself is forced (:719)
+    }
+  }
+  const int nvalid = min(total, a.k_max);
+  if (staged) {
+    __syncthreads();
+    for (int s = tid; s < a.k_max; s += NT) {
+      irow[s] = s < nvalid ? obuf[s] : m;     // sentinel m
+      nrow[s] = s < nvalid ? (float)s : 0.0f;
+    }
+  } else {
+    for (int s = nvalid + tid; s < a.k_max; s += NT) {   // sentinel m
+      irow[s] = m;
+      nrow[s] = 0.0f;
+    }
+  }
+  if (tid == 0 && a.set_size) a.set_size[hi] = total;
+}
+
+// ------------------------------------------------------------------------------------------
 // attend: split s of query (h, i) sweeps slots [64 s, 64 s + 64); 16 lanes per slot, each lane
 // NPL rotation pairs; every 16-lane group keeps its own online-softmax state, merged in LDS.
 // A batch of many queries (the per-query prefill) gives each query fewer splits, down to one
@@ -1103,11 +1417,25 @@ static hipError_t launch_select_t(const DecodeArgs& a, hipStream_t st) {
   return hipGetLastError();
 }
 
+template <int NT>
+static hipError_t launch_select_pq_t(const DecodeArgs& a, hipStream_t st) {
+  const size_t lds = decode_select_pq_lds_bytes(a.M, NT);
+  hipError_t e = hipFuncSetAttribute((const void*)decode_select_pq_kernel<NT>,
+                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL((decode_select_pq_kernel<NT>), dim3(a.H * a.Q), dim3(NT), lds, st, a);
+  return hipGetLastError();
+}
+
 hipError_t launch_decode_select(const DecodeArgs& a, hipStream_t st) {
   // a batch that fills the chip twice over takes the 512-thread instance: more queries per CU
   // and half the waves in each block reduction (per-query prefill: 39.6 -> 31.4 ms at config 3);
   // a few queries keep 1024 threads, whose shorter per-thread ranges finish each query sooner
-  if ((int64_t)a.H * a.Q >= 512) return launch_select_t<512>(a, st);
+  const bool batch = (int64_t)a.H * a.Q >= 512;
+  // the per-query rule on rows that fit the LDS takes its own kernel (fewer passes)
+  if (a.rule == 1 && !a.use_pct && decode_select_pq_lds_bytes(a.M, batch ? 512 : 1024) <= 160 * 1024)
+    return batch ? launch_select_pq_t<512>(a, st) : launch_select_pq_t<1024>(a, st);
+  if (batch) return launch_select_t<512>(a, st);
   return launch_select_t<1024>(a, st);
 }
 

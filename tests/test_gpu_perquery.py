@@ -145,6 +145,45 @@ def test_pq_decode_sets_match_reference_goldens():
         assert np.array_equal(r["newpos_q"].cpu().numpy()[:, 0], g[p + "newpos_q"]), i
 
 
+def _crafted_rows(kind, H, Q, M, rng):
+    """Score rows (H, Q, M) fp32 that reach each path of the per-query selection's cut search."""
+    s = rng.standard_normal((H, Q, M)).astype(np.float32)
+    if kind == "tied_cut":          # most passers share one value: the cut bin holds them all
+        s[..., ::3] = np.float32(1.0)
+    elif kind == "clustered":       # > 512 distinct values within a few hundred ulps at the cut
+        c = np.float32(1.5) + np.arange(M, dtype=np.float32) * np.float32(2.0 ** -22)
+        s[..., ::2] = c[::2]
+    elif kind == "quantised":       # few distinct values: many exact ties everywhere
+        s = np.round(s * 4.0).astype(np.float32) / np.float32(4.0)
+    return s
+
+
+@pytest.mark.parametrize("kind,tau,Q", [("plain", 4.0, 1), ("plain", 4.0, 300), ("tied_cut", 4.0, 1),
+                                        ("tied_cut", 4.0, 300), ("clustered", 4.0, 1), ("clustered", 4.0, 300),
+                                        ("quantised", 4.0, 300), ("plain", float("inf"), 300),
+                                        ("quantised", 0.0, 300), ("plain", -1.0, 1)])
+def test_pq_select_crafted_rows(kind, tau, Q):
+    """The per-query rule's selection from crafted score rows (batches of 300 queries take the
+    512-thread kernel, single queries the 1024-thread one) bit for bit against the oracle: exact
+    ties at the cut, clusters of distinct values finer than the value bins (the key-space
+    refinement), quantised scores, tau = inf (every key passes), tau = 0 and tau < 0."""
+    import _sta_native as native
+    H, M, km = 2, 3000, 700
+    rng = np.random.default_rng(abs(hash((kind, Q))) % 2**32)
+    s = _crafted_rows(kind, H, Q, M, rng)
+    qp = M - Q
+    say(f"pq crafted select: {kind} tau={tau} H={H} Q={Q} M={M} k_max={km}")
+    plan = native.DecodePlan(torch.zeros(H, Q, 64, device=DEV), torch.zeros(H, M, 64, device=DEV), None,
+                             torch.full((H,), tau), torch.ones(32), qp, k_max=km, n_global=16, n_local=16,
+                             rule="pq")
+    r = plan.build_sets(torch.from_numpy(s).to(DEV))
+    ref = orc.decode_build_sets_pq(s, np.full(H, tau, np.float32), qp, 16, 16, km)
+    for name, rv in zip(("idx", "newpos_k", "newpos_q", "set_size", "usize", "overflow"), ref):
+        assert np.array_equal(r[name].cpu().numpy(), rv), name
+    print(f"[result] pq crafted select {kind} tau={tau} Q={Q}: capped {int(ref[5].sum())} of {H * Q}, "
+          f"set size mean {ref[3].mean():.1f}", flush=True)
+
+
 def test_pq_decode_composed_reference_goldens():
     import shared_selection_triton_perquery as pqm
     g = _gold("decode_pq_composed_golden.npz")
