@@ -20,8 +20,13 @@ import torch
 
 import _sta_native as native
 from _install import _AttnCall, _out_proj
+from _torch_golden import (ChunkLlamaRotaryEmbedding, _fa_block, _merge_lse, _rotate_half,  # noqa: F401
+                           apply_rotary_pos_emb, flash_attn_status)
 
 _MAX_NEW_TOKENS = 512            # table headroom for generation (dca_kernel.py:161)
+# the chunking of the last patch_model_with_dca call, the defaults of ChunkLlamaRotaryEmbedding
+_DCA_CHUNK_SIZE = None
+_DCA_LOCAL_WINDOW = None
 _ATTN_CLASSES = ("LlamaAttention", "LlamaFlashAttention2", "LlamaSdpaAttention")
 
 
@@ -176,6 +181,8 @@ def patch_model_with_dca(model, chunk_size, pretrain_len, local_window):
     import transformers.models.llama.modeling_llama as ml
     assert 0 < local_window < chunk_size, f"need 0 < w({local_window}) < s({chunk_size})"
     assert chunk_size < pretrain_len, f"need s({chunk_size}) < c({pretrain_len})"
+    global _DCA_CHUNK_SIZE, _DCA_LOCAL_WINDOW
+    _DCA_CHUNK_SIZE, _DCA_LOCAL_WINDOW = chunk_size, local_window
     fwd = _make_dca_forward(chunk_size, pretrain_len, local_window)
     patch = DcaPatch(model)
     for cls in {getattr(ml, name) for name in _ATTN_CLASSES if hasattr(ml, name)}:

@@ -12,6 +12,7 @@ import torch
 
 import _sta_native as native
 from _counters import PhaseCounters, ratio
+from _torch_golden import _rope_rotate, pqstream_attention_torch  # noqa: F401  (torch helper and golden)
 
 ADV_MAX = 0
 ADV_FULL = 1

@@ -5,6 +5,7 @@ The caller passes the YaRN inv_freq, pos_scale = 1 and rope_scale = mscale
 """
 from _shared_prefill import build_sets as _device_build_sets
 from _shared_prefill import shared_prefill
+from _torch_golden import _rope_rotate  # noqa: F401  (the reference's torch RoPE helper)
 
 
 def _build_sets(votes, pos_scale, n_global, n_local, pct, T, k_max, q_pos_base=0, measure=False,

@@ -23,6 +23,7 @@ import torch
 
 import _sta_native as native
 from _counters import PhaseCounters, ratio
+from _torch_golden import _rope_rotate, chunk_attention_torch  # noqa: F401  (torch helper and golden)
 from _sta_native import derive_n_chunk, n_forced_chunks  # noqa: F401  (the reference's budget helpers)
 
 # measurement-only chunk-quality counters per phase (get_chunk_stats keys, chunked.py:64-110):

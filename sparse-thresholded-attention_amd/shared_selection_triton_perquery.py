@@ -17,6 +17,7 @@ import torch
 
 import _sta_native as native
 from _counters import PhaseCounters, ratio
+from _torch_golden import _rope_rotate, pq_attention_torch  # noqa: F401  (torch helper and golden)
 
 
 # measurement-only statistics per phase (the reference's get_overflow_stats keys,
