@@ -416,6 +416,47 @@ def test_config2_full_length_gqa_group():
                n_global=c.n_global, n_local=c.n_local, what="config 2 full length, 2 q heads / 1 kv head")
 
 
+def test_config2_full_size_three_gqa_groups():
+    """config 2 as written (32 query heads over 8 KV heads, 32768 tokens, YaRN, bf16) in one call,
+    then two query heads of each of three GQA groups (KV heads 0, 3, 7) against the oracle: votes
+    within the band, sets given the votes bit for bit, the set-level comparison with the
+    oracle's own sets, and the outputs given the GPU's sets."""
+    import _sta_native as native
+    from synthetic import CONFIGS
+    c = CONFIGS["c2"]
+    q, k, v = c.inputs(DEV)
+    invf, ps, rs = c.geometry()
+    invf = invf.to(DEV)
+    say("config 2 full size, 32 q heads / 8 kv heads")
+    r = native.shared_attention(q, k, v, torch.full((c.H,), c.tau), invf, ps, rs, invf, ps, rs, pct=c.pct,
+                                tile=c.tile, k_max=c.k_max, want_votes=True, want_row_max=True)
+    torch.cuda.synchronize()
+    G = c.H // c.Hkv
+    total = {"tiles": 0, "tiles_differ": 0, "keys": 0, "band": 0, "cut": 0, "trunc": 0}
+    for kvh, heads in ((0, [0, 1]), (3, [12, 14]), (7, [29, 31])):
+        assert all(h // G == kvh for h in heads)
+        qn, dt = np_of(q[0, heads])
+        kn, _ = np_of(k[0, kvh:kvh + 1])
+        vn, _ = np_of(v[0, kvh:kvh + 1])
+        a = orc.select_vote(qn, kn, dt, np.full(len(heads), c.tau, np.float32), invf.cpu().numpy(), ps, rs,
+                            1.0 / math.sqrt(c.D), c.tile, band_eps=BAND, want_band=True)
+        votes_g = r["votes"][heads].cpu().numpy()
+        ndiff, nband = check_votes(votes_g, a["votes"], a["band"])
+        assert np.max(np.abs(r["row_max"][heads].cpu().numpy() - a["row_max"])) < 1e-4, "row max"
+        sets_g = {n: r[n][heads].cpu().numpy() for n in SET_NAMES}
+        check_sets_given_votes(votes_g, sets_g, ps, c.n_global, c.n_local, c.pct, c.tile, c.k_max)
+        sd = set_level_diffs(votes_g, a, ps, c.n_global, c.n_local, c.pct, c.tile, c.k_max,
+                             what=f"config 2 kv head {kvh}")
+        for n in total:
+            total[n] += sd[n]
+        out_ref = orc.gather_attn(qn, kn, vn, dt, sets_g["idx"], sets_g["newpos_k"], sets_g["newpos_q"],
+                                  invf.cpu().numpy(), rs, 1.0 / math.sqrt(c.D), c.tile, c.k_max, 64)
+        err = check_output(r["out"][heads].float().cpu().numpy(), out_ref, dt, f"c2 kv head {kvh}")
+        print(f"[result] config 2 q heads {heads} (kv head {kvh}): vote entries differing {ndiff} "
+              f"(band pairs {nband}), max out err {err:.2e}", flush=True)
+    report_set_diffs("config 2 full size, q heads 0 1 12 14 29 31", total)
+
+
 @pytest.mark.parametrize("k_max", [2048, 10000])
 def test_build_sets_slot_paths(k_max):
     """_build_sets on random votes with the kept slots staged in LDS (k_max 2048) and written
