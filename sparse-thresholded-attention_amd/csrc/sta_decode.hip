@@ -442,7 +442,8 @@ __global__ __launch_bounds__(NT) void decode_select_kernel(DecodeArgs a) {
       if (cd <= DEC_CAND) {
         for (int e = 0; e < per; ++e) {
           const uint32_t k = myrow[e];
-          if (k != 0 && j0 + e < m && (k & pmask) == prefix) cand[atomicAdd(&misc[4], 1)] = k;
+          const int slot = wave_alloc(k != 0 && j0 + e < m && (k & pmask) == prefix, &misc[4]);
+          if (slot >= 0) cand[slot] = k;
         }
         __syncthreads();
         if (tid < cd) {
@@ -757,9 +758,12 @@ __global__ __launch_bounds__(NT) void decode_select_pq_kernel(DecodeArgs a) {
       }
     }
   }
-  if (c_nf > 0) {
-    atomicMax((unsigned*)&misc[6], ~kmin_nf);   // misc[6] = ~(min key): starts at 0 = ~0xffffffff
-    atomicMax((unsigned*)&misc[7], kmax_nf);
+  {                                            // the range over the wave, then one atomic per wave
+    const uint32_t wmin = ~wave_max_u32(~kmin_nf), wmax = wave_max_u32(kmax_nf);
+    if ((tid & 63) == 0 && wmax >= wmin) {
+      atomicMax((unsigned*)&misc[6], ~wmin);    // misc[6] = ~(min key): starts at 0 = ~0xffffffff
+      atomicMax((unsigned*)&misc[7], wmax);
+    }
   }
   const int packed = dsum<NW>(c_pass | (c_nf << 16), tmp);   // each count < 65536
   const int ge = packed & 0xffff, n_nf = packed >> 16;
@@ -837,9 +841,10 @@ __global__ __launch_bounds__(NT) void decode_select_pq_kernel(DecodeArgs a) {
           return k >= kthr && (linear || (k >= rlo && k <= rhi)) && !forced(j0 + e) && bin_of(k) == dbin;
         };
         if (cd <= DEC_PQ_CAND) {
-          for (int e = 0; e < nk; ++e) {
-            const uint32_t k = myrow[e];
-            if (in_bin(e, k)) cand[atomicAdd(&misc[3], 1)] = k;
+          for (int e = 0; e < per; ++e) {        // (uniform trip count: the wave allocates slots)
+            const uint32_t k = e < nk ? myrow[e] : 0u;
+            const int slot = wave_alloc(e < nk && in_bin(e, k), &misc[3]);
+            if (slot >= 0) cand[slot] = k;
           }
           __syncthreads();
           if (tid < cd) {
@@ -869,9 +874,10 @@ __global__ __launch_bounds__(NT) void decode_select_pq_kernel(DecodeArgs a) {
             bmax = max(bmax, k);
           }
         }
-        if (bmax >= bmin) {
-          atomicMax((unsigned*)&misc[4], ~bmin);   // ~(min key)
-          atomicMax((unsigned*)&misc[5], bmax);
+        const uint32_t wmin = ~wave_max_u32(~bmin), wmax = wave_max_u32(bmax);
+        if ((tid & 63) == 0 && wmax >= wmin) {
+          atomicMax((unsigned*)&misc[4], ~wmin);   // ~(min key)
+          atomicMax((unsigned*)&misc[5], wmax);
         }
         __syncthreads();
         rlo = ~(uint32_t)misc[4];

@@ -269,6 +269,27 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
 }
 
 // xor-butterfly helpers over a 64-lane wavefront
+// Slots from an LDS counter for the lanes of a wave that take one: one atomic per wave instead of
+// one per lane (same-address LDS atomics serialise).  Every active lane of the wave must call it;
+// a taking lane gets its index, the others -1.
+__device__ __forceinline__ int wave_alloc(bool take, int* counter) {
+  const unsigned long long mask = __ballot(take);
+  if (mask == 0ull) return -1;
+  const int lane = threadIdx.x & 63;
+  const int leader = __ffsll(mask) - 1;
+  int base = 0;
+  if (lane == leader) base = atomicAdd(counter, __popcll(mask));
+  base = __shfl(base, leader, 64);
+  return take ? base + __popcll(mask & ((1ull << lane) - 1ull)) : -1;
+}
+
+// max over the 64 lanes of a wave
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v = max(v, (uint32_t)__shfl_xor((int)v, o, 64));
+  return v;
+}
+
 __device__ __forceinline__ float wave_shfl_xor(float v, int m) { return __shfl_xor(v, m, 64); }
 __device__ __forceinline__ int wave_shfl_xor(int v, int m) { return __shfl_xor(v, m, 64); }
 

@@ -301,8 +301,10 @@ __global__ __launch_bounds__(PQ_NT) void pq_select_kernel(PqSelectArgs a) {
         uint32_t kk[PQ_KB];
         order_free_keys(i0, kk);
 #pragma unroll
-        for (int e = 0; e < PQ_KB; ++e)
-          if (kk[e] != 0 && (kk[e] & pmask) == prefix) list[atomicAdd(&misc[2], 1)] = kk[e];
+        for (int e = 0; e < PQ_KB; ++e) {
+          const int slot = wave_alloc(kk[e] != 0 && (kk[e] & pmask) == prefix, &misc[2]);
+          if (slot >= 0) list[slot] = kk[e];
+        }
       }
       __syncthreads();
       cnt = misc[2];
