@@ -950,6 +950,339 @@ __global__ __launch_bounds__(NT) void decode_select_pq_kernel(DecodeArgs a) {
 }
 
 // ------------------------------------------------------------------------------------------
+// The same rule with the row in registers (rows of up to NT * 4G keys, k_max <= DEC_PQR_STAGE).
+//   - Thread t owns the 4-key groups t, t + NT, ..., t + (G - 1) NT: every pass over the row is a
+//     coalesced sweep with compile-time indexing, and no key needs a division to find its owner.
+//   - The forced keys become the key 1 once their passers are counted, below every threshold key
+//     (no value has key 0 or 1 but two negative NaN payloads), and the keys past the row's end
+//     are 0, so no later pass tests a key's index.
+//   - The histogram bins are key-space bins, (k - lo) >> shift over the level's key range (the
+//     threshold key to the row's max at level 0): two instructions per key, and a bin's key range
+//     in closed form, so the cut bin's keys are found by two comparisons.  Keys order as values,
+//     so the bins are monotone in the value and the cut is exact at every level.
+//   - Per-key LDS updates are branch-free: every wave has passers, so a branch would be taken
+//     anyway; non-passers add 0 to, and dropped keys store into, per-lane spare words.
+//   - Dense ranks come from segments of 256 consecutive keys (one wave, one group index): a wave
+//     scan inside each segment and one scan over the G * NW segment totals.
+// The sets are bit-identical to the LDS-staged kernel's: the cut value, the tie quota in key
+// order and the dense ranks do not depend on how the bins are laid out.
+// ------------------------------------------------------------------------------------------
+constexpr int DEC_PQR_BINS = 2048;                         // key-space bins, 32-bit counters
+constexpr int DEC_PQR_STAGE = DEC_PQR_BINS + DEC_PQ_CAND;  // histogram + cut-bin keys (words)
+
+template <int NT, int G>
+__global__ __launch_bounds__(NT, NT == 512 ? 6 : 4) void decode_select_pq_reg_kernel(DecodeArgs a) {
+#pragma clang fp contract(off)
+  constexpr int NW = NT / 64;
+  constexpr int NB = DEC_PQR_BINS;
+  constexpr int BPT = NB / NT;                 // bins per thread in the cut search
+  constexpr int NSEG = G * NW;                 // <= 64: one wave scans the segment totals
+  static_assert(NSEG <= 64 && BPT >= 1, "launch shape");
+  constexpr int SPARE = DEC_PQR_STAGE;         // 64 per-lane spare words after the staging area
+  __shared__ __align__(16) uint32_t lbuf[DEC_PQR_STAGE + 64];   // histogram + cut-bin keys, then idx
+  __shared__ int seg[NSEG];
+  __shared__ uint32_t red_max[NW];
+  __shared__ int red_sum[NW];
+  __shared__ int red_scan[NW];
+  __shared__ int misc[4];
+  __shared__ uint32_t cut_v;
+  __shared__ int cut_q, seg_total;
+  uint32_t* hist = lbuf;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int hi = blockIdx.x;
+  const int h = hi / a.Q, i = hi % a.Q;
+  const int m = a.M - (a.Q - 1 - i);           // keys this query sees
+  const int p = a.q_pos0 + i;                  // its position (p < m)
+  const float* srow = a.scores + (int64_t)hi * a.M;
+  // key (e, c) of this thread is j0 + 4 NT e + c.  Each pass takes j0 afresh (an empty asm the
+  // compiler cannot see through), so that no pass keeps another pass's key indices live.
+  auto fresh_j0 = [&]() {
+    int j0 = 4 * tid;
+    asm volatile("" : "+v"(j0));
+    return j0;
+  };
+
+  // ---- 1. the row as order-preserving keys (0 past the row's end), exact max ----
+  uint32_t key[G][4];
+  const int js = fresh_j0();
+  if (((uintptr_t)srow & 15) == 0) {
+    float4 sv[G];
+#pragma unroll
+    for (int e = 0; e < G; ++e) {
+      const int j = js + 4 * NT * e;
+      if (j + 3 < m) {
+        sv[e] = ((const float4*)srow)[e * NT + tid];
+      } else {
+        sv[e] = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (j < m) sv[e].x = srow[j];
+        if (j + 1 < m) sv[e].y = srow[j + 1];
+        if (j + 2 < m) sv[e].z = srow[j + 2];
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < G; ++e) {
+      const int j = js + 4 * NT * e;
+      key[e][0] = j < m ? okey(sv[e].x) : 0u;
+      key[e][1] = j + 1 < m ? okey(sv[e].y) : 0u;
+      key[e][2] = j + 2 < m ? okey(sv[e].z) : 0u;
+      key[e][3] = j + 3 < m ? okey(sv[e].w) : 0u;
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < G; ++e)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const int j = js + 4 * NT * e + c;
+        key[e][c] = j < m ? okey(srow[j]) : 0u;
+      }
+  }
+  uint32_t kmax = 0;
+#pragma unroll
+  for (int e = 0; e < G; ++e)
+#pragma unroll
+    for (int c = 0; c < 4; ++c) kmax = max(kmax, key[e][c]);
+  kmax = wave_max_u32(kmax);
+  if (lane == 0) red_max[wave] = kmax;
+  for (int b = tid; b < NB; b += NT) hist[b] = 0u;
+  __syncthreads();
+#pragma unroll
+  for (int w = 0; w < NW; ++w) kmax = max(kmax, red_max[w]);
+  const float vmax = okey_value(kmax);
+  const float thr = vmax - a.tau[h];                                   // perquery.py:684
+  const uint32_t kthr = okey(thr);
+  // level-0 bins: (k - kthr) >> shift0 over the passers' keys [kthr, kmax]
+  const uint32_t span0 = kmax >= kthr ? kmax - kthr : 0u;
+  const int shift0 = span0 == 0u ? 0 : max(0, 32 - __clz(span0) - 11);   // span0 >> shift0 < NB
+
+  // ---- 2. forced keys (perquery.py:676-679): [0, g) U [lo, p], global, local window and self;
+  // only the groups that hold one take the branch ----
+  const int g = min(a.n_global, m);
+  const int lo = min(max(0, p - a.n_local + 1), p);
+  const int nforced = g + max(p - max(lo, g) + 1, 0);
+  int c_fp = 0;                                // forced passers
+  {
+    const int jf = fresh_j0();
+#pragma unroll
+    for (int e = 0; e < G; ++e) {
+      const int j0 = jf + 4 * NT * e;
+      if (j0 < g || (j0 + 3 >= lo && j0 <= p)) {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const int j = j0 + c;
+          const bool f = j < g || (j >= lo && j <= p);
+          c_fp += (f && key[e][c] >= kthr) ? 1 : 0;
+          key[e][c] = f ? 1u : key[e][c];
+        }
+      }
+    }
+  }
+  // ---- 3. the non-forced passers: count and level-0 histogram ----
+  int c_nf = 0;
+#pragma unroll
+  for (int e = 0; e < G; ++e)
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const uint32_t k = key[e][c];
+      const bool ps = k >= kthr;
+      c_nf += ps ? 1 : 0;
+      atomicAdd(&lbuf[ps ? (k - kthr) >> shift0 : SPARE + lane], ps ? 1u : 0u);
+    }
+  int packed = (c_fp + c_nf) | (c_nf << 16);   // each count < 65536
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) packed += __shfl_xor(packed, o, 64);
+  if (lane == 0) red_sum[wave] = packed;
+  if (tid < 4) misc[tid] = 0;
+  __syncthreads();                             // (also publishes the histogram)
+  packed = 0;
+#pragma unroll
+  for (int w = 0; w < NW; ++w) packed += red_sum[w];
+  const int ge = packed & 0xffff, n_nf = packed >> 16;
+  const int count = n_nf + nforced;            // |passers U forced| (perquery.py:687-688)
+  if (tid == 0) {
+    if (a.usize) a.usize[hi] = ge;
+    if (a.overflow) a.overflow[hi] = count > a.k_max ? 1 : 0;
+  }
+
+  // ---- 4. the cap cut over the non-forced passers (perquery.py:690-701) ----
+  bool only_forced = false, exact_cut = false;
+  uint32_t V = 0u;
+  int quota = 0;
+  if (count > a.k_max) {
+    const int budget = a.k_max - nforced;
+    if (budget <= 0) {
+      only_forced = true;
+    } else {
+      exact_cut = true;
+      int need = budget;                       // rank from the top among the level's keys
+      uint32_t rlo = kthr, rhi = kmax;         // the level's key range
+      int shift = shift0;
+      for (int level = 0;; ++level) {          // each level divides the range by 2^11
+        if (level > 0) {
+          if (rlo == rhi) {                    // every key in range equals the cut
+            V = rlo;
+            quota = need;
+            break;
+          }
+          shift = max(0, 32 - __clz(rhi - rlo) - 11);
+          __syncthreads();                     // the previous level's histogram is read
+          for (int b = tid; b < NB; b += NT) hist[b] = 0u;
+          if (tid == 0) misc[3] = 0;
+          __syncthreads();
+#pragma unroll
+          for (int e = 0; e < G; ++e)
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+              const uint32_t k = key[e][c];
+              const bool in = k - rlo <= rhi - rlo;   // (rlo > 1: no forced key is in range)
+              atomicAdd(&lbuf[in ? (k - rlo) >> shift : SPARE + lane], in ? 1u : 0u);
+            }
+          __syncthreads();
+        }
+        // bins in descending order, BPT per thread: the bin holding the need-th largest
+        int cb[BPT], sl = 0;
+#pragma unroll
+        for (int e = 0; e < BPT; ++e) {
+          cb[e] = (int)hist[NB - 1 - BPT * tid - e];
+          sl += cb[e];
+        }
+        int x = sl;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+          const int y = __shfl_up(x, o, 64);
+          if (lane >= o) x += y;
+        }
+        if (lane == 63) red_scan[wave] = x;
+        __syncthreads();
+        int excl = x - sl;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) excl += w < wave ? red_scan[w] : 0;
+        if (excl < need && excl + sl >= need) {
+          int acc = excl, d = NB - 1 - BPT * tid, e = 0;
+          for (; e < BPT - 1; ++e) {
+            if (acc + cb[e] >= need) break;
+            acc += cb[e];
+            d -= 1;
+          }
+          misc[0] = d;
+          misc[1] = need - acc;                // rank within the bin
+          misc[2] = cb[e];                     // keys in the bin
+        }
+        __syncthreads();
+        const int d = misc[0], cd = misc[2];
+        need = misc[1];
+        // the cut bin's keys: [blo, bhi]
+        const uint32_t blo = rlo + ((uint32_t)d << shift);
+        const uint32_t bw = (1u << shift) - 1u;
+        const uint32_t bhi = rhi - blo <= bw ? rhi : blo + bw;
+        if (cd <= DEC_PQ_CAND) {
+#pragma unroll
+          for (int e = 0; e < G; ++e)
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {      // slots by wave; other lanes store aside
+              const uint32_t k = key[e][c];
+              const int slot = wave_alloc(k - blo <= bhi - blo, &misc[3]);
+              lbuf[slot >= 0 ? NB + slot : SPARE + lane] = k;
+            }
+          __syncthreads();
+          if (tid < cd) {
+            const uint32_t v = lbuf[NB + tid];
+            int gt = 0, eq = 0;
+            for (int u = 0; u < cd; ++u) {
+              const uint32_t w = lbuf[NB + u];
+              gt += w > v;
+              eq += w == v;
+            }
+            if (gt < need && gt + eq >= need) {   // the keys equal to the cut agree
+              cut_v = v;
+              cut_q = need - gt;
+            }
+          }
+          __syncthreads();
+          V = cut_v;
+          quota = cut_q;
+          break;
+        }
+        rlo = blo;                             // more than DEC_PQ_CAND keys: split the bin
+        rhi = bhi;
+      }
+    }
+  }
+
+  // ---- 5. compaction with dense ranks (perquery.py:703-719) ----
+  // classes: 0 dropped, 1 kept, 2 equal to the cut (the first `quota` of them in key order kept);
+  // per segment (e, wave) the lanes' packed (kept | ties << 16) counts, scanned over the wave
+  int lpre[G];
+  uint32_t cls[G];                             // the four keys' classes, 2 bits each
+#pragma unroll
+  for (int e = 0; e < G; ++e) {
+    int v = 0;
+    cls[e] = 0u;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const uint32_t k = key[e][c];
+      const bool k1 = k == 1u || (exact_cut ? k > V : (!only_forced && k >= kthr));
+      const bool k2 = exact_cut && k == V;
+      v += k1 ? 1 : (k2 ? 0x10000 : 0);
+      cls[e] |= (k1 ? 1u : (k2 ? 2u : 0u)) << (2 * c);
+    }
+    int x = v;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int y = __shfl_up(x, o, 64);
+      if (lane >= o) x += y;
+    }
+    lpre[e] = x - v;
+    if (lane == 63) seg[e * NW + wave] = x;
+  }
+  __syncthreads();                             // every read of the histogram / cut-bin keys is done
+  if (wave == 0) {                             // segments in key order: e-major, then wave
+    const int v = lane < NSEG ? seg[lane] : 0;
+    int x = v;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int y = __shfl_up(x, o, 64);
+      if (lane >= o) x += y;
+    }
+    if (lane < NSEG) seg[lane] = x - v;
+    if (lane == 63) seg_total = x;
+  }
+  __syncthreads();
+  const int tot = seg_total;
+  const int total = (tot & 0xffff) + min(tot >> 16, quota);
+  // the kept keys at their dense ranks in LDS (the histogram words, free now), dropped keys into
+  // a spare word; the query's own rank kept aside
+  int* obuf = (int*)lbuf;
+  int rq = -1;
+  const int jw = fresh_j0();
+#pragma unroll
+  for (int e = 0; e < G; ++e) {
+    const int base = seg[e * NW + wave] + lpre[e];
+    int n1 = base & 0xffff, n2 = base >> 16;   // kept keys and cut ties before this lane's keys
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int j = jw + 4 * NT * e + c;
+      const uint32_t cl = (cls[e] >> (2 * c)) & 3u;
+      const int rank = n1 + min(n2, quota);
+      const bool kept = cl == 1u || (cl == 2u && n2 < quota);
+      obuf[kept ? rank : SPARE + lane] = j;
+      rq = j == p ? rank : rq;                 // the query itself is forced (:719)
+      n1 += (int)(cl & 1u);
+      n2 += (int)(cl >> 1);
+    }
+  }
+  if (rq >= 0) a.newpos_q[hi] = (float)rq;
+  const int nvalid = min(total, a.k_max);
+  int32_t* irow = a.idx + (int64_t)hi * a.k_max;
+  float* nrow = a.newpos_k + (int64_t)hi * a.k_max;
+  __syncthreads();
+  for (int s = tid; s < a.k_max; s += NT) {     // slot positions are the slot indices
+    irow[s] = s < nvalid ? obuf[s] : m;         // sentinel m
+    nrow[s] = s < nvalid ? (float)s : 0.0f;
+  }
+  if (tid == 0 && a.set_size) a.set_size[hi] = total;
+}
+
+// ------------------------------------------------------------------------------------------
 // attend: split s of query (h, i) sweeps slots [64 s, 64 s + 64); 16 lanes per slot, each lane
 // NPL rotation pairs; every 16-lane group keeps its own online-softmax state, merged in LDS.
 // A batch of many queries (the per-query prefill) gives each query fewer splits, down to one
@@ -1433,14 +1766,45 @@ static hipError_t launch_select_pq_t(const DecodeArgs& a, hipStream_t st) {
   return hipGetLastError();
 }
 
+template <int NT, int G>
+static hipError_t launch_select_pq_reg_t(const DecodeArgs& a, hipStream_t st) {
+  hipLaunchKernelGGL((decode_select_pq_reg_kernel<NT, G>), dim3(a.H * a.Q), dim3(NT), 0, st, a);
+  return hipGetLastError();
+}
+
+// the register-resident per-query selection: the smallest instance whose NT x 4G keys hold the
+// row, or nullptr past 16384 keys (those rows take the LDS store)
+static hipError_t (*select_pq_reg_for(int M, bool batch))(const DecodeArgs&, hipStream_t) {
+  const int g = (M + (batch ? 2047 : 4095)) / (batch ? 2048 : 4096);   // 4-key groups per thread
+  if (batch) {
+    if (g <= 1) return launch_select_pq_reg_t<512, 1>;
+    if (g <= 2) return launch_select_pq_reg_t<512, 2>;
+    if (g <= 3) return launch_select_pq_reg_t<512, 3>;
+    if (g <= 4) return launch_select_pq_reg_t<512, 4>;
+    if (g <= 6) return launch_select_pq_reg_t<512, 6>;
+    if (g <= 8) return launch_select_pq_reg_t<512, 8>;
+    return nullptr;
+  }
+  if (g <= 1) return launch_select_pq_reg_t<1024, 1>;
+  if (g <= 2) return launch_select_pq_reg_t<1024, 2>;
+  if (g <= 3) return launch_select_pq_reg_t<1024, 3>;
+  if (g <= 4) return launch_select_pq_reg_t<1024, 4>;
+  return nullptr;
+}
+
 hipError_t launch_decode_select(const DecodeArgs& a, hipStream_t st) {
   // a batch that fills the chip twice over takes the 512-thread instance: more queries per CU
   // and half the waves in each block reduction (per-query prefill: 39.6 -> 31.4 ms at config 3);
   // a few queries keep 1024 threads, whose shorter per-thread ranges finish each query sooner
   const bool batch = (int64_t)a.H * a.Q >= 512;
-  // the per-query rule on rows that fit the LDS takes its own kernel (fewer passes)
-  if (a.rule == 1 && !a.use_pct && decode_select_pq_lds_bytes(a.M, batch ? 512 : 1024) <= 160 * 1024)
-    return batch ? launch_select_pq_t<512>(a, st) : launch_select_pq_t<1024>(a, st);
+  // the per-query rule takes its own kernels (fewer passes): the row in registers up to 16384
+  // keys (k_max within the LDS staging), in LDS beyond while it fits
+  if (a.rule == 1 && !a.use_pct) {
+    if (a.k_max <= DEC_PQR_STAGE)
+      if (auto f = select_pq_reg_for(a.M, batch)) return f(a, st);
+    if (decode_select_pq_lds_bytes(a.M, batch ? 512 : 1024) <= 160 * 1024)
+      return batch ? launch_select_pq_t<512>(a, st) : launch_select_pq_t<1024>(a, st);
+  }
   if (batch) return launch_select_t<512>(a, st);
   return launch_select_t<1024>(a, st);
 }

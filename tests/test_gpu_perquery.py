@@ -158,17 +158,22 @@ def _crafted_rows(kind, H, Q, M, rng):
     return s
 
 
-@pytest.mark.parametrize("kind,tau,Q", [("plain", 4.0, 1), ("plain", 4.0, 300), ("tied_cut", 4.0, 1),
-                                        ("tied_cut", 4.0, 300), ("clustered", 4.0, 1), ("clustered", 4.0, 300),
-                                        ("quantised", 4.0, 300), ("plain", float("inf"), 300),
-                                        ("quantised", 0.0, 300), ("plain", -1.0, 1)])
-def test_pq_select_crafted_rows(kind, tau, Q):
-    """The per-query rule's selection from crafted score rows (batches of 300 queries take the
-    512-thread kernel, single queries the 1024-thread one) bit for bit against the oracle: exact
-    ties at the cut, clusters of distinct values finer than the value bins (the key-space
-    refinement), quantised scores, tau = inf (every key passes), tau = 0 and tau < 0."""
+@pytest.mark.parametrize("kind,tau,Q,M", [("plain", 4.0, 1, 3000), ("plain", 4.0, 300, 3000),
+                                          ("tied_cut", 4.0, 1, 3000), ("tied_cut", 4.0, 300, 3000),
+                                          ("clustered", 4.0, 1, 3000), ("clustered", 4.0, 300, 3000),
+                                          ("quantised", 4.0, 300, 3000), ("plain", float("inf"), 300, 3000),
+                                          ("quantised", 0.0, 300, 3000), ("plain", -1.0, 1, 3000),
+                                          ("plain", 4.0, 300, 16383), ("tied_cut", 4.0, 1, 16384),
+                                          ("plain", 4.0, 300, 20000), ("tied_cut", 4.0, 300, 20000),
+                                          ("clustered", 4.0, 1, 20000), ("plain", float("inf"), 300, 20000)])
+def test_pq_select_crafted_rows(kind, tau, Q, M):
+    """The per-query rule's selection from crafted score rows bit for bit against the oracle:
+    exact ties at the cut, clusters of distinct values finer than the value bins (the key-space
+    refinement), quantised scores, tau = inf (every key passes), tau = 0 and tau < 0.  Batches of
+    300 queries take the 512-thread kernels, single queries the 1024-thread ones; rows of up to
+    16384 keys the register-resident kernel, longer ones the LDS-staged kernel."""
     import _sta_native as native
-    H, M, km = 2, 3000, 700
+    H, km = 2, 700
     rng = np.random.default_rng(abs(hash((kind, Q))) % 2**32)
     s = _crafted_rows(kind, H, Q, M, rng)
     qp = M - Q
@@ -180,7 +185,7 @@ def test_pq_select_crafted_rows(kind, tau, Q):
     ref = orc.decode_build_sets_pq(s, np.full(H, tau, np.float32), qp, 16, 16, km)
     for name, rv in zip(("idx", "newpos_k", "newpos_q", "set_size", "usize", "overflow"), ref):
         assert np.array_equal(r[name].cpu().numpy(), rv), name
-    print(f"[result] pq crafted select {kind} tau={tau} Q={Q}: capped {int(ref[5].sum())} of {H * Q}, "
+    print(f"[result] pq crafted select {kind} tau={tau} Q={Q} M={M}: capped {int(ref[5].sum())} of {H * Q}, "
           f"set size mean {ref[3].mean():.1f}", flush=True)
 
 
