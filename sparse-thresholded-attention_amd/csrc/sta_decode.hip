@@ -984,7 +984,7 @@ __global__ __launch_bounds__(NT, NT == 512 ? 6 : 4) void decode_select_pq_reg_ke
   __shared__ uint32_t red_max[NW];
   __shared__ int red_sum[NW];
   __shared__ int red_scan[NW];
-  __shared__ int misc[4];
+  __shared__ int misc[6];
   __shared__ uint32_t cut_v;
   __shared__ int cut_q, seg_total;
   uint32_t* hist = lbuf;
@@ -1050,7 +1050,13 @@ __global__ __launch_bounds__(NT, NT == 512 ? 6 : 4) void decode_select_pq_reg_ke
   const float vmax = okey_value(kmax);
   const float thr = vmax - a.tau[h];                                   // perquery.py:684
   const uint32_t kthr = okey(thr);
-  // level-0 bins: (k - kthr) >> shift0 over the passers' keys [kthr, kmax]
+  // level-0 bins: linear in the value over [thr, max] (the passers' values are spread there; key
+  // space is not, across the sign); key-space bins (k - kthr) >> shift0 when that span is not
+  // finite and positive (tau = inf, tau <= 0)
+  const float vspan = vmax - thr;
+  const bool lin = vspan > 0.0f && vspan < INFINITY;
+  const float inv0 = lin ? (float)NB / vspan : 0.0f;
+  auto vbin = [&](uint32_t k) { return min((int)((okey_value(k) - thr) * inv0), NB - 1); };
   const uint32_t span0 = kmax >= kthr ? kmax - kthr : 0u;
   const int shift0 = span0 == 0u ? 0 : max(0, 32 - __clz(span0) - 11);   // span0 >> shift0 < NB
 
@@ -1085,13 +1091,12 @@ __global__ __launch_bounds__(NT, NT == 512 ? 6 : 4) void decode_select_pq_reg_ke
       const uint32_t k = key[e][c];
       const bool ps = k >= kthr;
       c_nf += ps ? 1 : 0;
-      atomicAdd(&lbuf[ps ? (k - kthr) >> shift0 : SPARE + lane], ps ? 1u : 0u);
+      const int b = lin ? vbin(ps ? k : kthr) : (int)((ps ? k - kthr : 0u) >> shift0);
+      atomicAdd(&lbuf[ps ? b : SPARE + lane], ps ? 1u : 0u);
     }
-  int packed = (c_fp + c_nf) | (c_nf << 16);   // each count < 65536
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) packed += __shfl_xor(packed, o, 64);
+  int packed = wave_sum((c_fp + c_nf) | (c_nf << 16));   // each count < 65536
   if (lane == 0) red_sum[wave] = packed;
-  if (tid < 4) misc[tid] = 0;
+  if (tid < 6) misc[tid] = 0;
   __syncthreads();                             // (also publishes the histogram)
   packed = 0;
 #pragma unroll
@@ -1116,6 +1121,7 @@ __global__ __launch_bounds__(NT, NT == 512 ? 6 : 4) void decode_select_pq_reg_ke
       int need = budget;                       // rank from the top among the level's keys
       uint32_t rlo = kthr, rhi = kmax;         // the level's key range
       int shift = shift0;
+      bool linear = lin;                       // level 0 in value bins
       for (int level = 0;; ++level) {          // each level divides the range by 2^11
         if (level > 0) {
           if (rlo == rhi) {                    // every key in range equals the cut
@@ -1145,12 +1151,7 @@ __global__ __launch_bounds__(NT, NT == 512 ? 6 : 4) void decode_select_pq_reg_ke
           cb[e] = (int)hist[NB - 1 - BPT * tid - e];
           sl += cb[e];
         }
-        int x = sl;
-#pragma unroll
-        for (int o = 1; o < 64; o <<= 1) {
-          const int y = __shfl_up(x, o, 64);
-          if (lane >= o) x += y;
-        }
+        const int x = wave_incl_sum(sl);
         if (lane == 63) red_scan[wave] = x;
         __syncthreads();
         int excl = x - sl;
@@ -1170,18 +1171,29 @@ __global__ __launch_bounds__(NT, NT == 512 ? 6 : 4) void decode_select_pq_reg_ke
         __syncthreads();
         const int d = misc[0], cd = misc[2];
         need = misc[1];
-        // the cut bin's keys: [blo, bhi]
+        // the cut bin's keys: the value bin d, or the key range [blo, bhi]
         const uint32_t blo = rlo + ((uint32_t)d << shift);
         const uint32_t bw = (1u << shift) - 1u;
         const uint32_t bhi = rhi - blo <= bw ? rhi : blo + bw;
+        // (the threshold and scale taken afresh: the per-key bins are not hoisted out of the
+        // level loop, where 32 of them would stay live)
+        uint32_t kthr_l = kthr;
+        float thr_l = thr, inv_l = inv0;
+        asm volatile("" : "+v"(kthr_l), "+v"(thr_l), "+v"(inv_l));
+        auto in_bin = [&](uint32_t k) {
+          const uint32_t kv = k >= kthr_l ? k : kthr_l;
+          return linear ? (k >= kthr_l && min((int)((okey_value(kv) - thr_l) * inv_l), NB - 1) == d)
+                        : (k - blo <= bhi - blo);
+        };
         if (cd <= DEC_PQ_CAND) {
 #pragma unroll
           for (int e = 0; e < G; ++e)
 #pragma unroll
-            for (int c = 0; c < 4; ++c) {      // slots by wave; other lanes store aside
+            for (int c = 0; c < 4; ++c) {      // slots by wave; most waves have none
               const uint32_t k = key[e][c];
-              const int slot = wave_alloc(k - blo <= bhi - blo, &misc[3]);
-              lbuf[slot >= 0 ? NB + slot : SPARE + lane] = k;
+              const bool in = in_bin(k);
+              const int slot = wave_alloc(in, &misc[3]);
+              if (in && slot < DEC_PQ_CAND) lbuf[NB + slot] = k;   // (slot < cd)
             }
           __syncthreads();
           if (tid < cd) {
@@ -1202,8 +1214,31 @@ __global__ __launch_bounds__(NT, NT == 512 ? 6 : 4) void decode_select_pq_reg_ke
           quota = cut_q;
           break;
         }
-        rlo = blo;                             // more than DEC_PQ_CAND keys: split the bin
-        rhi = bhi;
+        // more than DEC_PQ_CAND keys: the next level splits the bin's key range
+        if (linear) {                          // (the value bin's keys: their min and max)
+          uint32_t bmin = 0xffffffffu, bmax = 0u;
+#pragma unroll
+          for (int e = 0; e < G; ++e)
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+              const uint32_t k = key[e][c];
+              const bool in = in_bin(k);
+              bmin = min(bmin, in ? k : 0xffffffffu);
+              bmax = max(bmax, in ? k : 0u);
+            }
+          const uint32_t wmin = ~wave_max_u32(~bmin), wmax = wave_max_u32(bmax);
+          if (lane == 0 && wmax >= wmin) {
+            atomicMax((unsigned*)&misc[4], ~wmin);   // ~(min key): starts at 0 = ~0xffffffff
+            atomicMax((unsigned*)&misc[5], wmax);
+          }
+          __syncthreads();
+          rlo = ~(uint32_t)misc[4];
+          rhi = (uint32_t)misc[5];
+        } else {
+          rlo = blo;
+          rhi = bhi;
+        }
+        linear = false;
       }
     }
   }
@@ -1213,6 +1248,8 @@ __global__ __launch_bounds__(NT, NT == 512 ? 6 : 4) void decode_select_pq_reg_ke
   // per segment (e, wave) the lanes' packed (kept | ties << 16) counts, scanned over the wave
   int lpre[G];
   uint32_t cls[G];                             // the four keys' classes, 2 bits each
+  uint32_t kthr5 = kthr;                       // taken afresh: the passer tests of pass 3 are
+  asm volatile("" : "+v"(kthr5));              // not kept live (as lane masks) until here
 #pragma unroll
   for (int e = 0; e < G; ++e) {
     int v = 0;
@@ -1220,29 +1257,19 @@ __global__ __launch_bounds__(NT, NT == 512 ? 6 : 4) void decode_select_pq_reg_ke
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
       const uint32_t k = key[e][c];
-      const bool k1 = k == 1u || (exact_cut ? k > V : (!only_forced && k >= kthr));
+      const bool k1 = k == 1u || (exact_cut ? k > V : (!only_forced && k >= kthr5));
       const bool k2 = exact_cut && k == V;
       v += k1 ? 1 : (k2 ? 0x10000 : 0);
       cls[e] |= (k1 ? 1u : (k2 ? 2u : 0u)) << (2 * c);
     }
-    int x = v;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-      const int y = __shfl_up(x, o, 64);
-      if (lane >= o) x += y;
-    }
+    const int x = wave_incl_sum(v);
     lpre[e] = x - v;
     if (lane == 63) seg[e * NW + wave] = x;
   }
   __syncthreads();                             // every read of the histogram / cut-bin keys is done
   if (wave == 0) {                             // segments in key order: e-major, then wave
     const int v = lane < NSEG ? seg[lane] : 0;
-    int x = v;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-      const int y = __shfl_up(x, o, 64);
-      if (lane >= o) x += y;
-    }
+    const int x = wave_incl_sum(v);
     if (lane < NSEG) seg[lane] = x - v;
     if (lane == 63) seg_total = x;
   }
@@ -1264,7 +1291,7 @@ __global__ __launch_bounds__(NT, NT == 512 ? 6 : 4) void decode_select_pq_reg_ke
       const uint32_t cl = (cls[e] >> (2 * c)) & 3u;
       const int rank = n1 + min(n2, quota);
       const bool kept = cl == 1u || (cl == 2u && n2 < quota);
-      obuf[kept ? rank : SPARE + lane] = j;
+      obuf[kept && rank < DEC_PQR_STAGE ? rank : SPARE + lane] = j;   // (rank < k_max)
       rq = j == p ? rank : rq;                 // the query itself is forced (:719)
       n1 += (int)(cl & 1u);
       n2 += (int)(cl >> 1);

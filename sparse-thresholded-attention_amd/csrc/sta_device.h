@@ -268,7 +268,6 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   return (uint32_t)(size_t)(const __attribute__((address_space(3))) void*)p;
 }
 
-// xor-butterfly helpers over a 64-lane wavefront
 // Slots from an LDS counter for the lanes of a wave that take one: one atomic per wave instead of
 // one per lane (same-address LDS atomics serialise).  Every active lane of the wave must call it;
 // a taking lane gets its index, the others -1.
@@ -279,15 +278,37 @@ __device__ __forceinline__ int wave_alloc(bool take, int* counter) {
   const int leader = __ffsll(mask) - 1;
   int base = 0;
   if (lane == leader) base = atomicAdd(counter, __popcll(mask));
-  base = __shfl(base, leader, 64);
-  return take ? base + __popcll(mask & ((1ull << lane) - 1ull)) : -1;
+  base = __builtin_amdgcn_readlane(base, leader);
+  const int below = (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32),
+                                                   __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
+  return take ? base + below : -1;
 }
 
-// max over the 64 lanes of a wave
+// Wave-wide scans and reductions on DPP lane moves (within rows of 16 lanes, then row broadcasts
+// and lane reads): no LDS round trip.  Every lane of the wave must be active.
+// Inclusive prefix sum over the 64 lanes.
+__device__ __forceinline__ int wave_incl_sum(int x) {
+  x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xf, 0xf, false);   // row_shr:1
+  x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xf, 0xf, false);   // row_shr:2
+  x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xf, 0xf, false);   // row_shr:4
+  x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xf, 0xf, false);   // row_shr:8
+  x += __builtin_amdgcn_update_dpp(0, x, 0x142, 0xa, 0xf, false);   // row_bcast:15, rows 1 and 3
+  x += __builtin_amdgcn_update_dpp(0, x, 0x143, 0xc, 0xf, false);   // row_bcast:31, rows 2 and 3
+  return x;
+}
+
+// the sum over the 64 lanes, uniform
+__device__ __forceinline__ int wave_sum(int x) { return __builtin_amdgcn_readlane(wave_incl_sum(x), 63); }
+
+// the max over the 64 lanes, uniform
 __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v = max(v, (uint32_t)__shfl_xor((int)v, o, 64));
-  return v;
+  int x = (int)v;
+  x = (int)max((uint32_t)x, (uint32_t)__builtin_amdgcn_mov_dpp(x, 0xb1, 0xf, 0xf, false));    // quad_perm 1,0,3,2
+  x = (int)max((uint32_t)x, (uint32_t)__builtin_amdgcn_mov_dpp(x, 0x4e, 0xf, 0xf, false));    // quad_perm 2,3,0,1
+  x = (int)max((uint32_t)x, (uint32_t)__builtin_amdgcn_mov_dpp(x, 0x141, 0xf, 0xf, false));   // row_half_mirror
+  x = (int)max((uint32_t)x, (uint32_t)__builtin_amdgcn_mov_dpp(x, 0x140, 0xf, 0xf, false));   // row_mirror
+  return max(max((uint32_t)__builtin_amdgcn_readlane(x, 0), (uint32_t)__builtin_amdgcn_readlane(x, 16)),
+             max((uint32_t)__builtin_amdgcn_readlane(x, 32), (uint32_t)__builtin_amdgcn_readlane(x, 48)));
 }
 
 __device__ __forceinline__ float wave_shfl_xor(float v, int m) { return __shfl_xor(v, m, 64); }
