@@ -1584,6 +1584,12 @@ __global__ __launch_bounds__(256) void decode_attend_grouped_kernel(DecodeArgs a
     }
   }
   const int32_t* irow = a.idx + (int64_t)hi * a.k_max;
+  // K / V rows by 32-bit byte offsets from the head's rows (the launcher checks that a head's
+  // cache spans less than 2 GiB): one multiply-add per slot, the upper half an immediate offset
+  constexpr int ESZ = DT == DT_F32 ? 4 : 2;
+  const char* kbase = (const char*)a.k + (int64_t)hk * a.k_hs * ESZ;
+  const char* vbase = (const char*)a.v + (int64_t)hk * a.v_hs * ESZ;
+  const uint32_t kts = (uint32_t)(a.k_ts * ESZ), vts = (uint32_t)(a.v_ts * ESZ), fo = (uint32_t)(f0 * ESZ);
   // the query's running max (the same in both halves) and each half's sum and accumulators
   float mrun = -INFINITY, lrun = 0.0f, acc1[NF], acc2[NF];
 #pragma unroll
@@ -1626,12 +1632,11 @@ __global__ __launch_bounds__(256) void decode_attend_grouped_kernel(DecodeArgs a
       RowPart<DT, NF> k1r[U], k2r[U], v1r[U], v2r[U];
 #pragma unroll
       for (int u = 0; u < U; ++u) {
-        const int64_t kb = (int64_t)hk * a.k_hs + (int64_t)jv[u] * a.k_ts + f0;
-        const int64_t vb = (int64_t)hk * a.v_hs + (int64_t)jv[u] * a.v_ts + f0;
-        load_part<DT, NF>(a.k, kb, k1r[u]);
-        load_part<DT, NF>(a.k, kb + HD, k2r[u]);
-        load_part<DT, NF>(a.v, vb, v1r[u]);
-        load_part<DT, NF>(a.v, vb + HD, v2r[u]);
+        const uint32_t ko = (uint32_t)jv[u] * kts + fo, vo = (uint32_t)jv[u] * vts + fo;
+        load_part<DT, NF>(kbase + ko, 0, k1r[u]);
+        load_part<DT, NF>(kbase + ko, HD, k2r[u]);
+        load_part<DT, NF>(vbase + vo, 0, v1r[u]);
+        load_part<DT, NF>(vbase + vo, HD, v2r[u]);
       }
       float sc[U];
 #pragma unroll
@@ -1658,21 +1663,43 @@ __global__ __launch_bounds__(256) void decode_attend_grouped_kernel(DecodeArgs a
       mst = fmaxf(mst, __shfl_xor(mst, 8, 64));
       if (mst > -INFINITY) {
         const float mn = fmaxf(mrun, mst);
-        const float wo = mrun == -INFINITY ? 0.0f : __expf(mrun - mn);
-        lrun = lrun * wo;
-#pragma unroll
-        for (int e = 0; e < NF; ++e) {
-          acc1[e] = acc1[e] * wo;
-          acc2[e] = acc2[e] * wo;
-        }
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-          const float pw = okv[u] ? __expf(sc[u] - mn) : 0.0f;
-          lrun += pw;
+        if (mn > mrun) {                       // the max moved: rescale (wo = 1 otherwise)
+          const float wo = mrun == -INFINITY ? 0.0f : __expf(mrun - mn);
+          lrun = lrun * wo;
 #pragma unroll
           for (int e = 0; e < NF; ++e) {
-            acc1[e] = fmaf(pw, part_elem(v1r[u], e), acc1[e]);
-            acc2[e] = fmaf(pw, part_elem(v2r[u], e), acc2[e]);
+            acc1[e] = acc1[e] * wo;
+            acc2[e] = acc2[e] * wo;
+          }
+        }
+        if constexpr (DT == DT_F32) {
+#pragma unroll
+          for (int u = 0; u < U; ++u) {
+            const float pw = okv[u] ? __expf(sc[u] - mn) : 0.0f;
+            lrun += pw;
+#pragma unroll
+            for (int e = 0; e < NF; ++e) {
+              acc1[e] = fmaf(pw, part_elem(v1r[u], e), acc1[e]);
+              acc2[e] = fmaf(pw, part_elem(v2r[u], e), acc2[e]);
+            }
+          }
+        } else {
+          // P.V with the weights in the value dtype, as Kernel C's tl.dot(p.to(v.dtype), v)
+          // (perquery.py:315): two slots per dot2 over a (slot u, slot u + 1) pair of values
+#pragma unroll
+          for (int u = 0; u < U; u += 2) {
+            const float p0 = okv[u] ? __expf(sc[u] - mn) : 0.0f;
+            const float p1 = okv[u + 1] ? __expf(sc[u + 1] - mn) : 0.0f;
+            lrun += p0;
+            lrun += p1;
+            const uint32_t pp = pack2_dt<DT>(p0, p1);
+#pragma unroll
+            for (int w = 0; w < RowPart<DT, NF>::NW; ++w) {
+              acc1[2 * w] = dot2_dt<DT>(__builtin_amdgcn_perm(v1r[u + 1].w[w], v1r[u].w[w], 0x05040100u), pp, acc1[2 * w]);
+              acc1[2 * w + 1] = dot2_dt<DT>(__builtin_amdgcn_perm(v1r[u + 1].w[w], v1r[u].w[w], 0x07060302u), pp, acc1[2 * w + 1]);
+              acc2[2 * w] = dot2_dt<DT>(__builtin_amdgcn_perm(v2r[u + 1].w[w], v2r[u].w[w], 0x05040100u), pp, acc2[2 * w]);
+              acc2[2 * w + 1] = dot2_dt<DT>(__builtin_amdgcn_perm(v2r[u + 1].w[w], v2r[u].w[w], 0x07060302u), pp, acc2[2 * w + 1]);
+            }
           }
         }
         mrun = mn;
@@ -1838,7 +1865,10 @@ hipError_t launch_decode_select(const DecodeArgs& a, hipStream_t st) {
 
 template <int DT, int D>
 static hipError_t launch_attend_t(const DecodeArgs& a, hipStream_t st) {
-  if (a.dense_ranks && a.Q >= DEC_QPW) {         // per-query rule, a batch: grouped queries
+  // per-query rule, a batch: grouped queries (their rows by 32-bit offsets within a head)
+  const int64_t esz = DT == DT_F32 ? 4 : 2;
+  const bool span32 = (int64_t)a.M * std::max(a.k_ts, a.v_ts) * esz + (int64_t)D * esz < (1LL << 31);
+  if (a.dense_ranks && a.Q >= DEC_QPW && span32) {
     const int nqg = (a.Q + DEC_QPW - 1) / DEC_QPW;
     if (a.k_max % 4 == 0 && (uintptr_t)a.idx % 16 == 0)
       hipLaunchKernelGGL((decode_attend_grouped_kernel<DT, D, true>), dim3(a.H * nqg), dim3(256), 0, st, a);

@@ -59,6 +59,17 @@ __device__ __forceinline__ uint32_t pack2_dt(float a, float b) {
   else return pack2_bf16(a, b);
 }
 
+// c + a.lo * b.lo + a.hi * b.hi over packed 16-bit pairs of the format DT (bf16 or f16), fp32
+// accumulation (v_dot2c_f32_bf16 / v_dot2c_f32_f16)
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+template <int DT>
+__device__ __forceinline__ float dot2_dt(uint32_t a, uint32_t b, float c) {
+  if constexpr (DT == 2)
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, a), __builtin_bit_cast(f16x2_t, b), c, false);
+  else
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a), __builtin_bit_cast(bf16x2_t, b), c, false);
+}
+
 // Transpose four rows of eight 16-bit elements (u32x4 each) into eight columns of four:
 // out[e] = {r0[e] | r1[e] << 16, r2[e] | r3[e] << 16}.  Pure bit moves.
 __device__ __forceinline__ void transpose4x8_16(const u32x4& r0, const u32x4& r1, const u32x4& r2,
