@@ -1651,16 +1651,14 @@ __global__ __launch_bounds__(256) void decode_attend_grouped_kernel(DecodeArgs a
           const float k2 = x2 * cs + x1 * sn;
           part = fmaf(q2[e], k2, fmaf(q1[e], k1, part));
         }
-        part += __shfl_xor(part, 1, 64);
-        part += __shfl_xor(part, 2, 64);
-        part += __shfl_xor(part, 4, 64);
+        part = group8_sum(part);                // the slot's 8 lanes
         sc[u] = okv[u] ? part * a.sm_scale : -INFINITY;
       }
       // the step's max over both halves' slots, then each half folds its own slots in
       float mst = -INFINITY;
 #pragma unroll
       for (int u = 0; u < U; ++u) mst = fmaxf(mst, sc[u]);
-      mst = fmaxf(mst, __shfl_xor(mst, 8, 64));
+      mst = halves16_max(mst);
       if (mst > -INFINITY) {
         const float mn = fmaxf(mrun, mst);
         if (mn > mrun) {                       // the max moved: rescale (wo = 1 otherwise)

@@ -311,6 +311,21 @@ __device__ __forceinline__ int wave_incl_sum(int x) {
 // the sum over the 64 lanes, uniform
 __device__ __forceinline__ int wave_sum(int x) { return __builtin_amdgcn_readlane(wave_incl_sum(x), 63); }
 
+// the sum over each aligned group of 8 lanes, in every lane of the group (the xor-1, xor-2
+// butterfly within quads, then the other quad of the group: the same additions as the
+// xor-1/2/4 butterfly)
+__device__ __forceinline__ float group8_sum(float x) {
+  x += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0xb1, 0xf, 0xf, false));
+  x += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0x4e, 0xf, 0xf, false));
+  x += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0x141, 0xf, 0xf, false));
+  return x;
+}
+
+// the max of the two 8-lane halves of each 16-lane row (row_mirror pairs lane i with 15 - i)
+__device__ __forceinline__ float halves16_max(float x) {
+  return fmaxf(x, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0x140, 0xf, 0xf, false)));
+}
+
 // the max over the 64 lanes, uniform
 __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
   int x = (int)v;
