@@ -18,12 +18,18 @@
 // loaded into registers while the current chunk's products run, then stored into the other LDS
 // buffer.  Query i sees the keys [0, M - (Q - 1 - i)) (its cache prefix: [0, q_pos0 + i] when the
 // batch ends at the cache's last key); scores past that are not written.
+// Each wave's 64 x 32 block of scores goes out through a per-wave LDS tile: written in the matrix
+// cores' output layout, read back as four consecutive keys per lane, so that a row's 32 scores
+// leave in 16-byte stores (8 lanes per row) rather than 4-byte ones (the store data path moves
+// about as many bytes per instruction at 16 bytes per lane as at 4).
 #include "sta_device.h"
 #include "sta_kernels.h"
 
 namespace sta {
 
 constexpr int ROWS_PIECE = 32;               // 32-key chunks per workgroup
+constexpr int ROWS_TS = 40;                  // tile row stride in floats: 16-byte rows, and the
+                                             // two row groups of one write 32 banks apart
 
 template <int D>
 __global__ __launch_bounds__(256) void score_rows_kernel(RowsArgs a, int npieces) {
@@ -31,6 +37,7 @@ __global__ __launch_bounds__(256) void score_rows_kernel(RowsArgs a, int npieces
   constexpr int CH = S * 2 * 64;             // 16-byte units of one 32-key block (hi, lo)
   constexpr int PER = CH / 256;              // units per thread and chunk
   __shared__ u32x4 lds[2][CH];
+  __shared__ __align__(16) float tile[4][64 * ROWS_TS];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g = (int)blockIdx.x / npieces, piece = (int)blockIdx.x % npieces;
   const int h = blockIdx.y;
@@ -79,6 +86,8 @@ __global__ __launch_bounds__(256) void score_rows_kernel(RowsArgs a, int npieces
   store_chunk(0);
   __syncthreads();
   float* srow = a.scores + (int64_t)h * a.Q * a.M;
+  // 16-byte stores need every row start 16-byte aligned
+  const bool vec = (a.M & 3) == 0 && ((uintptr_t)a.scores & 15) == 0;
   for (int c = c0; c < c1; ++c) {
     const int buf = (c - c0) & 1;
     if (c + 1 < c1) load_chunk(c + 1);
@@ -100,15 +109,38 @@ __global__ __launch_bounds__(256) void score_rows_kernel(RowsArgs a, int npieces
           acc[rb] = mfma32(qh[rb][s], bh, acc[rb]);
         }
       }
-      const int key = key0 + (lane & 31);
+      float* t = tile[wave];
 #pragma unroll
       for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const int row = wrow0 + rb * 32 + (i >> 2) * 8 + (lane >> 5) * 4 + (i & 3);
-          if (row < a.Q && key < a.M - (a.Q - 1 - row))
-            srow[(int64_t)row * a.M + key] = acc[rb][i] * a.sm_scale;
+        for (int i = 0; i < 16; ++i)
+          t[(rb * 32 + (i >> 2) * 8 + (lane >> 5) * 4 + (i & 3)) * ROWS_TS + (lane & 31)] = acc[rb][i] * a.sm_scale;
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      // lane: row k * 8 + lane / 8 of the wave's 64, keys key0 + 4 (lane % 8) .. + 3
+      const int kq = key0 + 4 * (lane & 7);
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const int r = k * 8 + (lane >> 3);
+        const float4 v = *(const float4*)&t[r * ROWS_TS + 4 * (lane & 7)];
+        const int row = wrow0 + r;
+        const int mrow = a.M - (a.Q - 1 - row);  // the keys this row sees
+        if (row < a.Q && kq < mrow) {
+          float* dst = srow + (int64_t)row * a.M + kq;
+          if (vec && kq + 3 < mrow) {
+            *(float4*)dst = v;
+          } else {
+            dst[0] = v.x;
+            if (kq + 1 < mrow) dst[1] = v.y;
+            if (kq + 2 < mrow) dst[2] = v.z;
+            if (kq + 3 < mrow) dst[3] = v.w;
+          }
         }
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");   // the reads before the next writes
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     }
     if (c + 1 < c1) store_chunk(buf ^ 1);   // that buffer was last read before the barrier
     __syncthreads();
