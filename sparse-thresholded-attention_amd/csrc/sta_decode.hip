@@ -950,25 +950,28 @@ __global__ __launch_bounds__(NT) void decode_select_pq_kernel(DecodeArgs a) {
 }
 
 // ------------------------------------------------------------------------------------------
-// The same rule with the row in registers (rows of up to NT * 4G keys, k_max <= DEC_PQR_STAGE).
+// The same rule with the row in registers as fp32 values (rows of up to NT * 4G keys, k_max <=
+// DEC_PQR_STAGE).
 //   - Thread t owns the 4-key groups t, t + NT, ..., t + (G - 1) NT: every pass over the row is a
 //     coalesced sweep with compile-time indexing, and no key needs a division to find its owner.
-//   - The forced keys become the key 1 once their passers are counted, below every threshold key
-//     (no value has key 0 or 1 but two negative NaN payloads), and the keys past the row's end
-//     are 0, so no later pass tests a key's index.
-//   - The histogram bins are key-space bins, (k - lo) >> shift over the level's key range (the
-//     threshold key to the row's max at level 0): two instructions per key, and a bin's key range
-//     in closed form, so the cut bin's keys are found by two comparisons.  Keys order as values,
-//     so the bins are monotone in the value and the cut is exact at every level.
+//   - The values stay floats: float comparisons order them as the LDS kernel's keys do (-0 equals
+//     +0 there too), so the threshold, the bins, the cut and its ties agree bit for bit, without
+//     a key conversion per pass.  Two quiet NaN payloads mark the keys past the row's end (before
+//     the max, which skips NaN) and the forced keys (once their passers are counted): NaN passes
+//     no comparison, so no later pass tests a key's index.  A row whose own scores hold NaN is
+//     outside that agreement (its NaN keys are never taken).
+//   - Level 0 bins are linear in the value over [max - tau, max], where the passers lie; a cut bin
+//     holding more than DEC_PQ_CAND keys is split by key-space bins of its key range (closed-form
+//     bin ranges), as often as needed.
 //   - Per-key LDS updates are branch-free: every wave has passers, so a branch would be taken
 //     anyway; non-passers add 0 to, and dropped keys store into, per-lane spare words.
 //   - Dense ranks come from segments of 256 consecutive keys (one wave, one group index): a wave
 //     scan inside each segment and one scan over the G * NW segment totals.
-// The sets are bit-identical to the LDS-staged kernel's: the cut value, the tie quota in key
-// order and the dense ranks do not depend on how the bins are laid out.
 // ------------------------------------------------------------------------------------------
-constexpr int DEC_PQR_BINS = 2048;                         // key-space bins, 32-bit counters
-constexpr int DEC_PQR_STAGE = DEC_PQR_BINS + DEC_PQ_CAND;  // histogram + cut-bin keys (words)
+constexpr int DEC_PQR_BINS = 2048;                         // level bins, 32-bit counters
+constexpr int DEC_PQR_STAGE = DEC_PQR_BINS + DEC_PQ_CAND;  // histogram + cut-bin values (words)
+constexpr uint32_t DEC_NAN_END = 0x7fc0beefu;              // past the row's end
+constexpr uint32_t DEC_NAN_FORCED = 0x7fc0f00du;           // forced
 
 template <int NT, int G>
 __global__ __launch_bounds__(NT, NT == 512 ? 6 : 4) void decode_select_pq_reg_kernel(DecodeArgs a) {
@@ -979,21 +982,23 @@ __global__ __launch_bounds__(NT, NT == 512 ? 6 : 4) void decode_select_pq_reg_ke
   constexpr int NSEG = G * NW;                 // <= 64: one wave scans the segment totals
   static_assert(NSEG <= 64 && BPT >= 1, "launch shape");
   constexpr int SPARE = DEC_PQR_STAGE;         // 64 per-lane spare words after the staging area
-  __shared__ __align__(16) uint32_t lbuf[DEC_PQR_STAGE + 64];   // histogram + cut-bin keys, then idx
+  __shared__ __align__(16) uint32_t lbuf[DEC_PQR_STAGE + 64];   // histogram + cut-bin values, then idx
   __shared__ int seg[NSEG];
-  __shared__ uint32_t red_max[NW];
+  __shared__ float red_max[NW];
   __shared__ int red_sum[NW];
   __shared__ int red_scan[NW];
   __shared__ int misc[6];
-  __shared__ uint32_t cut_v;
+  __shared__ float cut_v;
   __shared__ int cut_q, seg_total;
   uint32_t* hist = lbuf;
+  float* candv = (float*)(lbuf + NB);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int hi = blockIdx.x;
   const int h = hi / a.Q, i = hi % a.Q;
   const int m = a.M - (a.Q - 1 - i);           // keys this query sees
   const int p = a.q_pos0 + i;                  // its position (p < m)
   const float* srow = a.scores + (int64_t)hi * a.M;
+  const float nan_end = __uint_as_float(DEC_NAN_END);
   // key (e, c) of this thread is j0 + 4 NT e + c.  Each pass takes j0 afresh (an empty asm the
   // compiler cannot see through), so that no pass keeps another pass's key indices live.
   auto fresh_j0 = [&]() {
@@ -1001,31 +1006,31 @@ __global__ __launch_bounds__(NT, NT == 512 ? 6 : 4) void decode_select_pq_reg_ke
     asm volatile("" : "+v"(j0));
     return j0;
   };
+  auto is_forced = [](float v) { return __float_as_uint(v) == DEC_NAN_FORCED; };
+  // a value taken afresh (an empty asm): the rare passes' key conversions are not shared with
+  // each other, which would keep 4G of them live
+  auto fresh_f = [](float v) {
+    asm volatile("" : "+v"(v));
+    return v;
+  };
 
-  // ---- 1. the row as order-preserving keys (0 past the row's end), exact max ----
-  uint32_t key[G][4];
+  // ---- 1. the row's values (DEC_NAN_END past its end) and the exact max ----
+  float val[G][4];
   const int js = fresh_j0();
   if (((uintptr_t)srow & 15) == 0) {
-    float4 sv[G];
 #pragma unroll
     for (int e = 0; e < G; ++e) {
       const int j = js + 4 * NT * e;
+      float4 v;
       if (j + 3 < m) {
-        sv[e] = ((const float4*)srow)[e * NT + tid];
+        v = ((const float4*)srow)[e * NT + tid];
       } else {
-        sv[e] = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (j < m) sv[e].x = srow[j];
-        if (j + 1 < m) sv[e].y = srow[j + 1];
-        if (j + 2 < m) sv[e].z = srow[j + 2];
+        v = make_float4(nan_end, nan_end, nan_end, nan_end);
+        if (j < m) v.x = srow[j];
+        if (j + 1 < m) v.y = srow[j + 1];
+        if (j + 2 < m) v.z = srow[j + 2];
       }
-    }
-#pragma unroll
-    for (int e = 0; e < G; ++e) {
-      const int j = js + 4 * NT * e;
-      key[e][0] = j < m ? okey(sv[e].x) : 0u;
-      key[e][1] = j + 1 < m ? okey(sv[e].y) : 0u;
-      key[e][2] = j + 2 < m ? okey(sv[e].z) : 0u;
-      key[e][3] = j + 3 < m ? okey(sv[e].w) : 0u;
+      val[e][0] = v.x; val[e][1] = v.y; val[e][2] = v.z; val[e][3] = v.w;
     }
   } else {
 #pragma unroll
@@ -1033,31 +1038,28 @@ __global__ __launch_bounds__(NT, NT == 512 ? 6 : 4) void decode_select_pq_reg_ke
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
         const int j = js + 4 * NT * e + c;
-        key[e][c] = j < m ? okey(srow[j]) : 0u;
+        val[e][c] = j < m ? srow[j] : nan_end;
       }
   }
-  uint32_t kmax = 0;
+  float vmax = -INFINITY;
 #pragma unroll
   for (int e = 0; e < G; ++e)
 #pragma unroll
-    for (int c = 0; c < 4; ++c) kmax = max(kmax, key[e][c]);
-  kmax = wave_max_u32(kmax);
-  if (lane == 0) red_max[wave] = kmax;
+    for (int c = 0; c < 4; ++c) vmax = fmaxf(vmax, val[e][c]);   // (fmaxf skips NaN)
+  vmax = wave_max_f32(vmax);
+  if (lane == 0) red_max[wave] = vmax;
   for (int b = tid; b < NB; b += NT) hist[b] = 0u;
   __syncthreads();
 #pragma unroll
-  for (int w = 0; w < NW; ++w) kmax = max(kmax, red_max[w]);
-  const float vmax = okey_value(kmax);
+  for (int w = 0; w < NW; ++w) vmax = fmaxf(vmax, red_max[w]);
   const float thr = vmax - a.tau[h];                                   // perquery.py:684
-  const uint32_t kthr = okey(thr);
-  // level-0 bins: linear in the value over [thr, max] (the passers' values are spread there; key
-  // space is not, across the sign); key-space bins (k - kthr) >> shift0 when that span is not
-  // finite and positive (tau = inf, tau <= 0)
+  // level-0 bins: linear in the value over [thr, max]; key-space bins over the passers' keys when
+  // that span is not finite and positive (tau = inf, tau <= 0)
   const float vspan = vmax - thr;
   const bool lin = vspan > 0.0f && vspan < INFINITY;
   const float inv0 = lin ? (float)NB / vspan : 0.0f;
-  auto vbin = [&](uint32_t k) { return min((int)((okey_value(k) - thr) * inv0), NB - 1); };
-  const uint32_t span0 = kmax >= kthr ? kmax - kthr : 0u;
+  const uint32_t kthr = okey(thr), kmx = okey(vmax);
+  const uint32_t span0 = kmx >= kthr ? kmx - kthr : 0u;
   const int shift0 = span0 == 0u ? 0 : max(0, 32 - __clz(span0) - 11);   // span0 >> shift0 < NB
 
   // ---- 2. forced keys (perquery.py:676-679): [0, g) U [lo, p], global, local window and self;
@@ -1065,6 +1067,7 @@ __global__ __launch_bounds__(NT, NT == 512 ? 6 : 4) void decode_select_pq_reg_ke
   const int g = min(a.n_global, m);
   const int lo = min(max(0, p - a.n_local + 1), p);
   const int nforced = g + max(p - max(lo, g) + 1, 0);
+  const float nan_forced = __uint_as_float(DEC_NAN_FORCED);
   int c_fp = 0;                                // forced passers
   {
     const int jf = fresh_j0();
@@ -1076,24 +1079,36 @@ __global__ __launch_bounds__(NT, NT == 512 ? 6 : 4) void decode_select_pq_reg_ke
         for (int c = 0; c < 4; ++c) {
           const int j = j0 + c;
           const bool f = j < g || (j >= lo && j <= p);
-          c_fp += (f && key[e][c] >= kthr) ? 1 : 0;
-          key[e][c] = f ? 1u : key[e][c];
+          c_fp += (f && val[e][c] >= thr) ? 1 : 0;
+          val[e][c] = f ? nan_forced : val[e][c];
         }
       }
     }
   }
   // ---- 3. the non-forced passers: count and level-0 histogram ----
+  auto vbin = [&](float v) { return min((int)((v - thr) * inv0), NB - 1); };
   int c_nf = 0;
+  if (lin) {
 #pragma unroll
-  for (int e = 0; e < G; ++e)
+    for (int e = 0; e < G; ++e)
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const uint32_t k = key[e][c];
-      const bool ps = k >= kthr;
-      c_nf += ps ? 1 : 0;
-      const int b = lin ? vbin(ps ? k : kthr) : (int)((ps ? k - kthr : 0u) >> shift0);
-      atomicAdd(&lbuf[ps ? b : SPARE + lane], ps ? 1u : 0u);
-    }
+      for (int c = 0; c < 4; ++c) {
+        const float v = val[e][c];
+        const bool ps = v >= thr;
+        c_nf += ps ? 1 : 0;
+        atomicAdd(&lbuf[ps ? vbin(ps ? v : thr) : SPARE + lane], ps ? 1u : 0u);
+      }
+  } else {
+#pragma unroll
+    for (int e = 0; e < G; ++e)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const float v = fresh_f(val[e][c]);
+        const bool ps = v >= thr;
+        c_nf += ps ? 1 : 0;
+        atomicAdd(&lbuf[ps ? (int)((okey(ps ? v : thr) - kthr) >> shift0) : SPARE + lane], ps ? 1u : 0u);
+      }
+  }
   int packed = wave_sum((c_fp + c_nf) | (c_nf << 16));   // each count < 65536
   if (lane == 0) red_sum[wave] = packed;
   if (tid < 6) misc[tid] = 0;
@@ -1110,7 +1125,7 @@ __global__ __launch_bounds__(NT, NT == 512 ? 6 : 4) void decode_select_pq_reg_ke
 
   // ---- 4. the cap cut over the non-forced passers (perquery.py:690-701) ----
   bool only_forced = false, exact_cut = false;
-  uint32_t V = 0u;
+  float V = 0.0f;
   int quota = 0;
   if (count > a.k_max) {
     const int budget = a.k_max - nforced;
@@ -1119,13 +1134,13 @@ __global__ __launch_bounds__(NT, NT == 512 ? 6 : 4) void decode_select_pq_reg_ke
     } else {
       exact_cut = true;
       int need = budget;                       // rank from the top among the level's keys
-      uint32_t rlo = kthr, rhi = kmax;         // the level's key range
+      uint32_t rlo = kthr, rhi = kmx;          // the key-space level's key range
       int shift = shift0;
       bool linear = lin;                       // level 0 in value bins
-      for (int level = 0;; ++level) {          // each level divides the range by 2^11
+      for (int level = 0;; ++level) {          // each key-space level divides the range by 2^11
         if (level > 0) {
           if (rlo == rhi) {                    // every key in range equals the cut
-            V = rlo;
+            V = okey_value(rlo);
             quota = need;
             break;
           }
@@ -1138,8 +1153,9 @@ __global__ __launch_bounds__(NT, NT == 512 ? 6 : 4) void decode_select_pq_reg_ke
           for (int e = 0; e < G; ++e)
 #pragma unroll
             for (int c = 0; c < 4; ++c) {
-              const uint32_t k = key[e][c];
-              const bool in = k - rlo <= rhi - rlo;   // (rlo > 1: no forced key is in range)
+              const float v = fresh_f(val[e][c]);
+              const uint32_t k = v >= thr ? okey(v) : 0u;   // (rlo >= the threshold key > 0)
+              const bool in = k - rlo <= rhi - rlo;
               atomicAdd(&lbuf[in ? (k - rlo) >> shift : SPARE + lane], in ? 1u : 0u);
             }
           __syncthreads();
@@ -1177,34 +1193,33 @@ __global__ __launch_bounds__(NT, NT == 512 ? 6 : 4) void decode_select_pq_reg_ke
         const uint32_t bhi = rhi - blo <= bw ? rhi : blo + bw;
         // (the threshold and scale taken afresh: the per-key bins are not hoisted out of the
         // level loop, where 32 of them would stay live)
-        uint32_t kthr_l = kthr;
         float thr_l = thr, inv_l = inv0;
-        asm volatile("" : "+v"(kthr_l), "+v"(thr_l), "+v"(inv_l));
-        auto in_bin = [&](uint32_t k) {
-          const uint32_t kv = k >= kthr_l ? k : kthr_l;
-          return linear ? (k >= kthr_l && min((int)((okey_value(kv) - thr_l) * inv_l), NB - 1) == d)
-                        : (k - blo <= bhi - blo);
+        asm volatile("" : "+v"(thr_l), "+v"(inv_l));
+        auto in_bin = [&](float v) {
+          const bool ps = v >= thr_l;
+          return linear ? (ps && min((int)(((ps ? v : thr_l) - thr_l) * inv_l), NB - 1) == d)
+                        : (ps && okey(v) - blo <= bhi - blo);
         };
         if (cd <= DEC_PQ_CAND) {
 #pragma unroll
           for (int e = 0; e < G; ++e)
 #pragma unroll
             for (int c = 0; c < 4; ++c) {      // slots by wave; most waves have none
-              const uint32_t k = key[e][c];
-              const bool in = in_bin(k);
+              const float v = fresh_f(val[e][c]);
+              const bool in = in_bin(v);
               const int slot = wave_alloc(in, &misc[3]);
-              if (in && slot < DEC_PQ_CAND) lbuf[NB + slot] = k;   // (slot < cd)
+              if (in && slot < DEC_PQ_CAND) candv[slot] = v;   // (slot < cd)
             }
           __syncthreads();
           if (tid < cd) {
-            const uint32_t v = lbuf[NB + tid];
+            const float v = candv[tid];
             int gt = 0, eq = 0;
             for (int u = 0; u < cd; ++u) {
-              const uint32_t w = lbuf[NB + u];
+              const float w = candv[u];
               gt += w > v;
               eq += w == v;
             }
-            if (gt < need && gt + eq >= need) {   // the keys equal to the cut agree
+            if (gt < need && gt + eq >= need) {   // the values equal to the cut agree
               cut_v = v;
               cut_q = need - gt;
             }
@@ -1221,8 +1236,9 @@ __global__ __launch_bounds__(NT, NT == 512 ? 6 : 4) void decode_select_pq_reg_ke
           for (int e = 0; e < G; ++e)
 #pragma unroll
             for (int c = 0; c < 4; ++c) {
-              const uint32_t k = key[e][c];
-              const bool in = in_bin(k);
+              const float v = fresh_f(val[e][c]);
+              const bool in = in_bin(v);
+              const uint32_t k = okey(in ? v : thr);
               bmin = min(bmin, in ? k : 0xffffffffu);
               bmax = max(bmax, in ? k : 0u);
             }
@@ -1244,29 +1260,38 @@ __global__ __launch_bounds__(NT, NT == 512 ? 6 : 4) void decode_select_pq_reg_ke
   }
 
   // ---- 5. compaction with dense ranks (perquery.py:703-719) ----
-  // classes: 0 dropped, 1 kept, 2 equal to the cut (the first `quota` of them in key order kept);
-  // per segment (e, wave) the lanes' packed (kept | ties << 16) counts, scanned over the wave
+  // kept: forced, or above the cut (at or above the threshold when nothing is cut); ties: equal
+  // to the cut, the first `quota` of them in key order kept.  Per segment (e, wave) the lanes'
+  // packed (kept | ties << 16) counts, scanned over the wave.
+  float keep_lo = thr, tie_v = __uint_as_float(DEC_NAN_END);   // (NaN: no value ties)
+  if (exact_cut) {
+    // v > V  <=>  v >= the least float above V (+inf: a NaN bound, which nothing passes)
+    const uint32_t vb = __float_as_uint(V);
+    keep_lo = (vb & 0x7fffffffu) == 0u ? __uint_as_float(1u)
+                                       : __uint_as_float((vb & 0x80000000u) ? vb - 1u : vb + 1u);
+    tie_v = V;
+  }
+  if (only_forced) keep_lo = __uint_as_float(DEC_NAN_END);   // nothing passes a NaN bound
+  asm volatile("" : "+v"(keep_lo), "+v"(tie_v));   // (fresh: no pass-3 lane masks kept live)
   int lpre[G];
   uint32_t cls[G];                             // the four keys' classes, 2 bits each
-  uint32_t kthr5 = kthr;                       // taken afresh: the passer tests of pass 3 are
-  asm volatile("" : "+v"(kthr5));              // not kept live (as lane masks) until here
 #pragma unroll
   for (int e = 0; e < G; ++e) {
     int v = 0;
     cls[e] = 0u;
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
-      const uint32_t k = key[e][c];
-      const bool k1 = k == 1u || (exact_cut ? k > V : (!only_forced && k >= kthr5));
-      const bool k2 = exact_cut && k == V;
+      const float x = val[e][c];
+      const bool k1 = is_forced(x) || x >= keep_lo;
+      const bool k2 = x == tie_v;
       v += k1 ? 1 : (k2 ? 0x10000 : 0);
       cls[e] |= (k1 ? 1u : (k2 ? 2u : 0u)) << (2 * c);
     }
-    const int x = wave_incl_sum(v);
-    lpre[e] = x - v;
-    if (lane == 63) seg[e * NW + wave] = x;
+    const int xs = wave_incl_sum(v);
+    lpre[e] = xs - v;
+    if (lane == 63) seg[e * NW + wave] = xs;
   }
-  __syncthreads();                             // every read of the histogram / cut-bin keys is done
+  __syncthreads();                             // every read of the histogram / cut-bin values is done
   if (wave == 0) {                             // segments in key order: e-major, then wave
     const int v = lane < NSEG ? seg[lane] : 0;
     const int x = wave_incl_sum(v);

@@ -326,6 +326,19 @@ __device__ __forceinline__ float halves16_max(float x) {
   return fmaxf(x, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0x140, 0xf, 0xf, false)));
 }
 
+// the fp32 max over the 64 lanes (NaN lanes skipped), uniform
+__device__ __forceinline__ float wave_max_f32(float v) {
+  v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xb1, 0xf, 0xf, false)));
+  v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x4e, 0xf, 0xf, false)));
+  v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x141, 0xf, 0xf, false)));
+  v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x140, 0xf, 0xf, false)));
+  const int x = __builtin_bit_cast(int, v);
+  return fmaxf(fmaxf(__builtin_bit_cast(float, __builtin_amdgcn_readlane(x, 0)),
+                     __builtin_bit_cast(float, __builtin_amdgcn_readlane(x, 16))),
+               fmaxf(__builtin_bit_cast(float, __builtin_amdgcn_readlane(x, 32)),
+                     __builtin_bit_cast(float, __builtin_amdgcn_readlane(x, 48))));
+}
+
 // the max over the 64 lanes, uniform
 __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
   int x = (int)v;
