@@ -165,13 +165,17 @@ def _crafted_rows(kind, H, Q, M, rng):
                                           ("quantised", 0.0, 300, 3000), ("plain", -1.0, 1, 3000),
                                           ("plain", 4.0, 300, 16383), ("tied_cut", 4.0, 1, 16384),
                                           ("plain", 4.0, 300, 20000), ("tied_cut", 4.0, 300, 20000),
-                                          ("clustered", 4.0, 1, 20000), ("plain", float("inf"), 300, 20000)])
+                                          ("clustered", 4.0, 1, 20000), ("plain", float("inf"), 300, 20000),
+                                          ("plain", 4.0, 2100, 3000), ("tied_cut", 4.0, 2100, 8192),
+                                          ("clustered", 4.0, 2100, 16384), ("quantised", 0.0, 2100, 6000),
+                                          ("plain", 4.0, 2100, 3001)])
 def test_pq_select_crafted_rows(kind, tau, Q, M):
     """The per-query rule's selection from crafted score rows bit for bit against the oracle:
     exact ties at the cut, clusters of distinct values finer than the value bins (the key-space
     refinement), quantised scores, tau = inf (every key passes), tau = 0 and tau < 0.  Batches of
     300 queries take the 512-thread kernels, single queries the 1024-thread ones; rows of up to
-    16384 keys the register-resident kernel, longer ones the LDS-staged kernel."""
+    16384 keys the register-resident kernel, longer ones the LDS-staged kernel; batches of 4200
+    rows as the per-query prefill's launches have them."""
     import _sta_native as native
     H, km = 2, 700
     rng = np.random.default_rng(abs(hash((kind, Q))) % 2**32)
