@@ -129,7 +129,8 @@ __global__ __launch_bounds__(256) void score_rows_kernel(RowsArgs a, int npieces
         if (row < a.Q && kq < mrow) {
           float* dst = srow + (int64_t)row * a.M + kq;
           if (vec && kq + 3 < mrow) {
-            *(float4*)dst = v;
+            // written once, read once by the selection: non-temporal, past the caches' allocation
+            __builtin_nontemporal_store(floatx4{v.x, v.y, v.z, v.w}, (floatx4*)dst);
           } else {
             dst[0] = v.x;
             if (kq + 1 < mrow) dst[1] = v.y;
