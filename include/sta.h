@@ -479,7 +479,9 @@ typedef struct sta_decode_args {
   /* outputs (device) */
   void* out;                /* (H, Q, D) contiguous, input dtype */
   int32_t* idx;             /* (H, Q, k_max) ascending kept positions, sentinel m_i */
-  float* newpos_k;          /* (H, Q, k_max) repositioned key positions, 0 at sentinels */
+  float* newpos_k;          /* (H, Q, k_max) repositioned key positions, 0 at sentinels; may be
+                               NULL under STA_RULE_PQ (selection and attend: the positions are
+                               then the slot indices, the rule's dense ranks) */
   float* newpos_q;          /* (H, Q) repositioned query positions */
   /* optional outputs (NULL to skip) */
   int32_t* set_size;        /* (H, Q) |selected set| before the truncation to k_max */

@@ -1224,8 +1224,9 @@ class PerQueryPrefillPlan:
     do not depend on the chunking.  query_chunk=None runs the prompt as one batch.
 
     Outputs: out (H, N, D) in the input dtype; set_size, usize (H, N) int32 and overflow (H, N)
-    bool per query.  The per-launch idx / newpos buffers are reused; a chunk's per-query outputs
-    land in staging buffers and are copied into place on the same stream."""
+    bool per query.  The per-launch idx / newpos_q buffers are reused (newpos_k is not written: the
+    per-query rule's positions are the slot indices); a chunk's per-query outputs land in staging
+    buffers and are copied into place on the same stream."""
 
     def __init__(self, q, k, v, tau, inv_freq_a, inv_freq_c, pos_scale_a=1.0, rope_scale_a=1.0,
                  sm_scale=None, n_global=32, n_local=32, k_max=4096, heads_per_group=None,
@@ -1259,7 +1260,6 @@ class PerQueryPrefillPlan:
             "overflow": torch.empty((H, N), dtype=torch.bool, device=dev),
         }
         self._idx = torch.empty((hg, qc, k_max), dtype=torch.int32, device=dev)
-        self._npk = torch.empty((hg, qc, k_max), dtype=torch.float32, device=dev)
         self._npq = torch.empty((hg, qc), dtype=torch.float32, device=dev)
         whole = len(chunks) == 1
         if not whole:   # a chunk's (heads, queries) outputs are not a contiguous slice of (H, N)
@@ -1294,7 +1294,7 @@ class PerQueryPrefillPlan:
                 a.pct_decode, a.causal, a.rule = 100.0, 0, RULES["pq"]
                 dst = self.out if whole else self._stage
                 a.out = _ptr(dst["out"][h0:h1] if whole else dst["out"])
-                a.idx, a.newpos_k, a.newpos_q = _ptr(self._idx), _ptr(self._npk), _ptr(self._npq)
+                a.idx, a.newpos_k, a.newpos_q = _ptr(self._idx), None, _ptr(self._npq)
                 for name in ("set_size", "usize", "overflow"):
                     setattr(a, name, _ptr(dst[name][h0:h1] if whole else dst[name]))
                 n = lib().sta_decode_workspace_size(ctypes.byref(a))

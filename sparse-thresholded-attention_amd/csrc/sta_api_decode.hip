@@ -182,9 +182,12 @@ int dec_scores(const sta_decode_args* a, const DecLayout& L, DecodeArgs d, float
   return e == hipSuccess ? STA_OK : hip_fail(e, "decode scores: score rows");
 }
 
+// newpos_k may be NULL under STA_RULE_PQ: its positions are the slot indices (dense ranks)
+bool newpos_k_ok(const sta_decode_args* a) { return a->newpos_k || a->rule == STA_RULE_PQ; }
+
 int dec_select(const sta_decode_args* a, DecodeArgs d, const float* scores, hipStream_t st) {
-  if (!a->tau || !a->idx || !a->newpos_k || !a->newpos_q)
-    return fail(STA_ERR_INVALID_ARG, "tau, idx, newpos_k and newpos_q must be non-NULL");
+  if (!a->tau || !a->idx || !newpos_k_ok(a) || !a->newpos_q)
+    return fail(STA_ERR_INVALID_ARG, "tau, idx, newpos_k (unless STA_RULE_PQ) and newpos_q must be non-NULL");
   if (!scores) return fail(STA_ERR_INVALID_ARG, "scores must be non-NULL");
   d.scores = (float*)scores;
   hipError_t e = launch_decode_select(d, st);
@@ -196,8 +199,9 @@ int dec_attend(const sta_decode_args* a, const DecodeArgs& d, hipStream_t st) {
                               a->k_tok_stride, a->v_head_stride, a->v_tok_stride};
   int rc = check_qkv_ptrs(a->dtype, a->q, a->k, a->v, strides, true);
   if (rc != STA_OK) return rc;
-  if (!a->inv_freq_c || !a->out || !a->idx || !a->newpos_k || !a->newpos_q)
-    return fail(STA_ERR_INVALID_ARG, "inv_freq_c, out, idx, newpos_k and newpos_q must be non-NULL");
+  if (!a->inv_freq_c || !a->out || !a->idx || !newpos_k_ok(a) || !a->newpos_q)
+    return fail(STA_ERR_INVALID_ARG,
+                "inv_freq_c, out, idx, newpos_k (unless STA_RULE_PQ) and newpos_q must be non-NULL");
   hipError_t e = launch_decode_attend(a->dtype, a->D, d, st);
   return e == hipSuccess ? STA_OK : hip_fail(e, "decode attend");
 }

@@ -618,14 +618,14 @@ __global__ __launch_bounds__(NT) void decode_select_kernel(DecodeArgs a) {
       }
       if (f && rank < a.k_max) {
         irow[rank] = j;
-        nrow[rank] = np;
+        if (a.newpos_k) nrow[rank] = np;       // (NULL under the per-query rule: dense ranks)
       }
       if (j == p) a.newpos_q[hi] = stream ? 0.0f : np;                   // :603; pqstream :770
     }
   }
   for (int s = min(total, a.k_max) + tid; s < a.k_max; s += NT) {   // sentinel m (:594-600)
     irow[s] = m;
-    nrow[s] = 0.0f;
+    if (a.newpos_k) nrow[s] = 0.0f;
   }
   if (tid == 0 && a.set_size) a.set_size[hi] = total;
 }
@@ -926,7 +926,7 @@ __global__ __launch_bounds__(NT) void decode_select_pq_kernel(DecodeArgs a) {
             obuf[rank] = j;
           } else {
             irow[rank] = j;
-            nrow[rank] = (float)rank;
+            if (a.newpos_k) nrow[rank] = (float)rank;
           }
         }
       }
@@ -938,12 +938,12 @@ __global__ __launch_bounds__(NT) void decode_select_pq_kernel(DecodeArgs a) {
     __syncthreads();
     for (int s = tid; s < a.k_max; s += NT) {
       irow[s] = s < nvalid ? obuf[s] : m;     // sentinel m
-      nrow[s] = s < nvalid ? (float)s : 0.0f;
+      if (a.newpos_k) nrow[s] = s < nvalid ? (float)s : 0.0f;
     }
   } else {
     for (int s = nvalid + tid; s < a.k_max; s += NT) {   // sentinel m
       irow[s] = m;
-      nrow[s] = 0.0f;
+      if (a.newpos_k) nrow[s] = 0.0f;
     }
   }
   if (tid == 0 && a.set_size) a.set_size[hi] = total;
@@ -1329,7 +1329,7 @@ __global__ __launch_bounds__(NT, NT == 512 ? 6 : 4) void decode_select_pq_reg_ke
   __syncthreads();
   for (int s = tid; s < a.k_max; s += NT) {     // slot positions are the slot indices
     irow[s] = s < nvalid ? obuf[s] : m;         // sentinel m
-    nrow[s] = s < nvalid ? (float)s : 0.0f;
+    if (a.newpos_k) nrow[s] = s < nvalid ? (float)s : 0.0f;   // (NULL: not kept)
   }
   if (tid == 0 && a.set_size) a.set_size[hi] = total;
 }
@@ -1407,7 +1407,7 @@ __global__ __launch_bounds__(256) void decode_attend_kernel(DecodeArgs a, int st
     const int j = s < s1 ? irow[s] : -1;
     okv[u] = j >= 0 && j < m && (!a.causal || j <= p);   // sentinel m (exact_2.py:615; :195, 210)
     jv[u] = okv[u] ? j : 0;
-    npk[u] = s < s1 ? nrow[s] : 0.0f;
+    npk[u] = s < s1 ? (a.newpos_k ? nrow[s] : (float)s) : 0.0f;   // (NULL: dense ranks)
   }
   float x1[U][NPL], x2[U][NPL], v1[U][NPL], v2[U][NPL];
 #pragma unroll

@@ -416,6 +416,30 @@ def test_perquery_full_prefill_plan_config3_structure():
 
 
 
+def test_perquery_prefill_split_attend_without_key_positions():
+    """The plan passes no newpos_k (the per-query rule's positions are the slot indices).  Chunks
+    of 10 queries take the split attend, which then reads the slot index as the position: bit for
+    bit the direct decode calls on the same chunks, which pass newpos_k."""
+    import _sta_native as native
+    from synthetic import base_inv_freq, planted_inputs
+    H, N, D = 2, 300, 64
+    q, k, v = planted_inputs(85, H, H, N, D, 0.02, torch.float32, DEV)
+    invf = base_inv_freq(D, 10000.0).to(DEV)
+    tau = torch.full((H,), 3.0, device=DEV)
+    say("per-query prefill: split attend (chunks of 10) without newpos_k against direct decode calls")
+    plan = native.PerQueryPrefillPlan(q, k, v, tau, invf, invf, 0.5, 1.0, None, 8, 8, 64, query_chunk=10).run()
+    torch.cuda.synchronize()
+    capped = 0
+    for i0 in range(0, N, 10):
+        i1 = min(N, i0 + 10)
+        d = native.decode_attention(q[0, :, i0:i1], k[0, :, :i1], v[0, :, :i1], tau, invf, i0, 0.5, 1.0, None, 8, 8,
+                                    64, inv_freq_c=invf, pos_scale_c=1.0, rope_scale_c=1.0, rule="pq")
+        assert torch.equal(d["out"], plan["out"][:, i0:i1]), i0
+        assert torch.equal(d["overflow"].bool(), plan["overflow"][:, i0:i1]), i0
+        capped += int(d["overflow"].sum())
+    assert capped > 0
+
+
 def test_perquery_prefill_chunking_is_transparent():
     """The per-query prefill over chunks of positions (each a decode batch over its cache prefix)
     gives the one-batch run's outputs bit for bit: a query's scores, set and attend depend on
