@@ -1007,6 +1007,10 @@ __global__ __launch_bounds__(NT, NT == 512 ? 6 : 4) void decode_select_pq_reg_ke
     return j0;
   };
   auto is_forced = [](float v) { return __float_as_uint(v) == DEC_NAN_FORCED; };
+  // group e of this wave holds keys [4 (e NT + 64 wave), + 256): the passes skip the groups that
+  // start past the row's end (wave-uniform branches; their keys would all be past the end)
+  const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+  auto live = [&](int e) { return 4 * (e * NT + 64 * wave_u) < m; };
   // a value taken afresh (an empty asm): the rare passes' key conversions are not shared with
   // each other, which would keep 4G of them live
   auto fresh_f = [](float v) {
@@ -1022,7 +1026,9 @@ __global__ __launch_bounds__(NT, NT == 512 ? 6 : 4) void decode_select_pq_reg_ke
     for (int e = 0; e < G; ++e) {
       const int j = js + 4 * NT * e;
       float4 v;
-      if (j + 3 < m) {
+      if (!live(e)) {
+        v = make_float4(nan_end, nan_end, nan_end, nan_end);
+      } else if (j + 3 < m) {
         v = ((const float4*)srow)[e * NT + tid];
       } else {
         v = make_float4(nan_end, nan_end, nan_end, nan_end);
@@ -1090,7 +1096,8 @@ __global__ __launch_bounds__(NT, NT == 512 ? 6 : 4) void decode_select_pq_reg_ke
   int c_nf = 0;
   if (lin) {
 #pragma unroll
-    for (int e = 0; e < G; ++e)
+    for (int e = 0; e < G; ++e) {
+      if (!live(e)) continue;
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
         const float v = val[e][c];
@@ -1098,6 +1105,7 @@ __global__ __launch_bounds__(NT, NT == 512 ? 6 : 4) void decode_select_pq_reg_ke
         c_nf += ps ? 1 : 0;
         atomicAdd(&lbuf[ps ? vbin(ps ? v : thr) : SPARE + lane], ps ? 1u : 0u);
       }
+    }
   } else {
 #pragma unroll
     for (int e = 0; e < G; ++e)
@@ -1202,7 +1210,8 @@ __global__ __launch_bounds__(NT, NT == 512 ? 6 : 4) void decode_select_pq_reg_ke
         };
         if (cd <= DEC_PQ_CAND) {
 #pragma unroll
-          for (int e = 0; e < G; ++e)
+          for (int e = 0; e < G; ++e) {
+            if (!live(e)) continue;
 #pragma unroll
             for (int c = 0; c < 4; ++c) {      // slots by wave; most waves have none
               const float v = fresh_f(val[e][c]);
@@ -1210,6 +1219,7 @@ __global__ __launch_bounds__(NT, NT == 512 ? 6 : 4) void decode_select_pq_reg_ke
               const int slot = wave_alloc(in, &misc[3]);
               if (in && slot < DEC_PQ_CAND) candv[slot] = v;   // (slot < cd)
             }
+          }
           __syncthreads();
           if (tid < cd) {
             const float v = candv[tid];
@@ -1279,6 +1289,11 @@ __global__ __launch_bounds__(NT, NT == 512 ? 6 : 4) void decode_select_pq_reg_ke
   for (int e = 0; e < G; ++e) {
     int v = 0;
     cls[e] = 0u;
+    lpre[e] = 0;
+    if (!live(e)) {
+      if (lane == 63) seg[e * NW + wave] = 0;
+      continue;
+    }
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
       const float x = val[e][c];
@@ -1308,6 +1323,7 @@ __global__ __launch_bounds__(NT, NT == 512 ? 6 : 4) void decode_select_pq_reg_ke
   const int jw = fresh_j0();
 #pragma unroll
   for (int e = 0; e < G; ++e) {
+    if (!live(e)) continue;
     const int base = seg[e * NW + wave] + lpre[e];
     int n1 = base & 0xffff, n2 = base >> 16;   // kept keys and cut ties before this lane's keys
 #pragma unroll
