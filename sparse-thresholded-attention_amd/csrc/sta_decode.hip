@@ -989,7 +989,7 @@ __global__ __launch_bounds__(NT, NT == 512 ? 6 : 4) void decode_select_pq_reg_ke
   __shared__ int red_scan[NW];
   __shared__ int misc[6];
   __shared__ float cut_v;
-  __shared__ int cut_q, seg_total;
+  __shared__ int cut_q, cut_eq, seg_total;
   uint32_t* hist = lbuf;
   float* candv = (float*)(lbuf + NB);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -1133,6 +1133,7 @@ __global__ __launch_bounds__(NT, NT == 512 ? 6 : 4) void decode_select_pq_reg_ke
 
   // ---- 4. the cap cut over the non-forced passers (perquery.py:690-701) ----
   bool only_forced = false, exact_cut = false;
+  bool ties_all = true;                        // every key equal to the cut is kept
   float V = 0.0f;
   int quota = 0;
   if (count > a.k_max) {
@@ -1145,11 +1146,13 @@ __global__ __launch_bounds__(NT, NT == 512 ? 6 : 4) void decode_select_pq_reg_ke
       uint32_t rlo = kthr, rhi = kmx;          // the key-space level's key range
       int shift = shift0;
       bool linear = lin;                       // level 0 in value bins
+      int range_n = n_nf;                      // keys in the level's range
       for (int level = 0;; ++level) {          // each key-space level divides the range by 2^11
         if (level > 0) {
           if (rlo == rhi) {                    // every key in range equals the cut
             V = okey_value(rlo);
             quota = need;
+            ties_all = need == range_n;
             break;
           }
           shift = max(0, 32 - __clz(rhi - rlo) - 11);
@@ -1232,11 +1235,13 @@ __global__ __launch_bounds__(NT, NT == 512 ? 6 : 4) void decode_select_pq_reg_ke
             if (gt < need && gt + eq >= need) {   // the values equal to the cut agree
               cut_v = v;
               cut_q = need - gt;
+              cut_eq = eq;
             }
           }
           __syncthreads();
           V = cut_v;
           quota = cut_q;
+          ties_all = cut_q == cut_eq;
           break;
         }
         // more than DEC_PQ_CAND keys: the next level splits the bin's key range
@@ -1265,6 +1270,7 @@ __global__ __launch_bounds__(NT, NT == 512 ? 6 : 4) void decode_select_pq_reg_ke
           rhi = bhi;
         }
         linear = false;
+        range_n = cd;
       }
     }
   }
@@ -1283,59 +1289,110 @@ __global__ __launch_bounds__(NT, NT == 512 ? 6 : 4) void decode_select_pq_reg_ke
   }
   if (only_forced) keep_lo = __uint_as_float(DEC_NAN_END);   // nothing passes a NaN bound
   asm volatile("" : "+v"(keep_lo), "+v"(tie_v));   // (fresh: no pass-3 lane masks kept live)
-  int lpre[G];
-  uint32_t cls[G];                             // the four keys' classes, 2 bits each
-#pragma unroll
-  for (int e = 0; e < G; ++e) {
-    int v = 0;
-    cls[e] = 0u;
-    lpre[e] = 0;
-    if (!live(e)) {
-      if (lane == 63) seg[e * NW + wave] = 0;
-      continue;
-    }
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const float x = val[e][c];
-      const bool k1 = is_forced(x) || x >= keep_lo;
-      const bool k2 = x == tie_v;
-      v += k1 ? 1 : (k2 ? 0x10000 : 0);
-      cls[e] |= (k1 ? 1u : (k2 ? 2u : 0u)) << (2 * c);
-    }
-    const int xs = wave_incl_sum(v);
-    lpre[e] = xs - v;
-    if (lane == 63) seg[e * NW + wave] = xs;
-  }
-  __syncthreads();                             // every read of the histogram / cut-bin values is done
-  if (wave == 0) {                             // segments in key order: e-major, then wave
-    const int v = lane < NSEG ? seg[lane] : 0;
-    const int x = wave_incl_sum(v);
-    if (lane < NSEG) seg[lane] = x - v;
-    if (lane == 63) seg_total = x;
-  }
-  __syncthreads();
-  const int tot = seg_total;
-  const int total = (tot & 0xffff) + min(tot >> 16, quota);
-  // the kept keys at their dense ranks in LDS (the histogram words, free now), dropped keys into
-  // a spare word; the query's own rank kept aside
   int* obuf = (int*)lbuf;
-  int rq = -1;
-  const int jw = fresh_j0();
+  int rq = -1, total = 0;
+  if (ties_all) {
+    // every tie kept (or none to cut): kept = forced or at or above one bound, one bit per key
+    const float kb = exact_cut ? V : keep_lo;
+    float keep_b = kb;
+    asm volatile("" : "+v"(keep_b));
+    int lpre1[G];
+    uint32_t kbits[G];
 #pragma unroll
-  for (int e = 0; e < G; ++e) {
-    if (!live(e)) continue;
-    const int base = seg[e * NW + wave] + lpre[e];
-    int n1 = base & 0xffff, n2 = base >> 16;   // kept keys and cut ties before this lane's keys
+    for (int e = 0; e < G; ++e) {
+      lpre1[e] = 0;
+      kbits[e] = 0u;
+      if (!live(e)) {
+        if (lane == 63) seg[e * NW + wave] = 0;
+        continue;
+      }
+      int v = 0;
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const int j = jw + 4 * NT * e + c;
-      const uint32_t cl = (cls[e] >> (2 * c)) & 3u;
-      const int rank = n1 + min(n2, quota);
-      const bool kept = cl == 1u || (cl == 2u && n2 < quota);
-      obuf[kept && rank < DEC_PQR_STAGE ? rank : SPARE + lane] = j;   // (rank < k_max)
-      rq = j == p ? rank : rq;                 // the query itself is forced (:719)
-      n1 += (int)(cl & 1u);
-      n2 += (int)(cl >> 1);
+      for (int c = 0; c < 4; ++c) {
+        const float x = val[e][c];
+        const bool kp = is_forced(x) || x >= keep_b;
+        v += kp ? 1 : 0;
+        kbits[e] |= (kp ? 1u : 0u) << c;
+      }
+      const int xs = wave_incl_sum(v);
+      lpre1[e] = xs - v;
+      if (lane == 63) seg[e * NW + wave] = xs;
+    }
+    __syncthreads();                           // every read of the histogram / cut-bin values is done
+    if (wave == 0) {                           // segments in key order: e-major, then wave
+      const int v = lane < NSEG ? seg[lane] : 0;
+      const int x = wave_incl_sum(v);
+      if (lane < NSEG) seg[lane] = x - v;
+      if (lane == 63) seg_total = x;
+    }
+    __syncthreads();
+    total = seg_total;
+    const int jw = fresh_j0();
+#pragma unroll
+    for (int e = 0; e < G; ++e) {
+      if (!live(e)) continue;
+      int rank = seg[e * NW + wave] + lpre1[e];   // kept keys before this lane's keys
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const int j = jw + 4 * NT * e + c;
+        const bool kp = (kbits[e] >> c) & 1u;
+        obuf[kp && rank < DEC_PQR_STAGE ? rank : SPARE + lane] = j;   // (rank < k_max)
+        rq = j == p ? rank : rq;               // the query itself is forced (:719)
+        rank += kp ? 1 : 0;
+      }
+    }
+  } else {
+    // ties at the cut taken in part: classes of 2 bits (kept / tie) and tie counts in the scans
+    int lpre[G];
+    uint32_t cls[G];                             // the four keys' classes, 2 bits each
+#pragma unroll
+    for (int e = 0; e < G; ++e) {
+      int v = 0;
+      cls[e] = 0u;
+      lpre[e] = 0;
+      if (!live(e)) {
+        if (lane == 63) seg[e * NW + wave] = 0;
+        continue;
+      }
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const float x = val[e][c];
+        const bool k1 = is_forced(x) || x >= keep_lo;
+        const bool k2 = x == tie_v;
+        v += k1 ? 1 : (k2 ? 0x10000 : 0);
+        cls[e] |= (k1 ? 1u : (k2 ? 2u : 0u)) << (2 * c);
+      }
+      const int xs = wave_incl_sum(v);
+      lpre[e] = xs - v;
+      if (lane == 63) seg[e * NW + wave] = xs;
+    }
+    __syncthreads();                             // every read of the histogram / cut-bin values is done
+    if (wave == 0) {                             // segments in key order: e-major, then wave
+      const int v = lane < NSEG ? seg[lane] : 0;
+      const int x = wave_incl_sum(v);
+      if (lane < NSEG) seg[lane] = x - v;
+      if (lane == 63) seg_total = x;
+    }
+    __syncthreads();
+    const int tot = seg_total;
+    total = (tot & 0xffff) + min(tot >> 16, quota);
+    const int jw = fresh_j0();
+#pragma unroll
+    for (int e = 0; e < G; ++e) {
+      if (!live(e)) continue;
+      const int base = seg[e * NW + wave] + lpre[e];
+      int n1 = base & 0xffff, n2 = base >> 16;   // kept keys and cut ties before this lane's keys
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const int j = jw + 4 * NT * e + c;
+        const uint32_t cl = (cls[e] >> (2 * c)) & 3u;
+        const int rank = n1 + min(n2, quota);
+        const bool kept = cl == 1u || (cl == 2u && n2 < quota);
+        obuf[kept && rank < DEC_PQR_STAGE ? rank : SPARE + lane] = j;   // (rank < k_max)
+        rq = j == p ? rank : rq;                 // the query itself is forced (:719)
+        n1 += (int)(cl & 1u);
+        n2 += (int)(cl >> 1);
+      }
     }
   }
   if (rq >= 0) a.newpos_q[hi] = (float)rq;
