@@ -1212,15 +1212,54 @@ __global__ __launch_bounds__(NT, NT == 512 ? 6 : 4) void decode_select_pq_reg_ke
                         : (ps && okey(v) - blo <= bhi - blo);
         };
         if (cd <= DEC_PQ_CAND) {
+          // The bin as a value interval [lo_b, hi_b): in key space from its key range; in value
+          // bins by searching the first value of bin d and of bin d + 1 within +-32 ulps of
+          // their nominal edges, one candidate per lane (the bins are monotone in the value).
+          // A search that does not bracket its edge falls back to the bin test per key.
+          float lo_b = okey_value(blo), hi_b = okey_value(bhi + 1u);   // (bhi + 1 = 0: NaN)
+          bool bounded = true;
+          if (linear) {
+            auto first_of = [&](int dd, float& out) {   // the least v >= thr in a bin >= dd
+              if (dd >= NB) {                  // past the clamped top bin: none
+                out = __uint_as_float(DEC_NAN_END);
+                return true;
+              }
+              const float x0 = thr_l + (float)dd / inv_l;
+              const float cv = okey_value(okey(x0) + (uint32_t)(lane - 32));
+              const bool ge = cv >= thr_l && min((int)((cv - thr_l) * inv_l), NB - 1) >= dd;
+              const unsigned long long msk = __ballot(ge);
+              const int first = __ffsll(msk) - 1;  // the values rise with the lane
+              if (first <= 0 || (msk >> first) != (~0ull >> first)) return false;
+              out = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, cv), first));
+              return true;
+            };
+            if (d == 0) lo_b = thr_l;
+            else bounded = first_of(d, lo_b);
+            bounded = bounded && first_of(d + 1, hi_b);
+          }
+          if (bounded) {
 #pragma unroll
-          for (int e = 0; e < G; ++e) {
-            if (!live(e)) continue;
+            for (int e = 0; e < G; ++e) {
+              if (!live(e)) continue;
 #pragma unroll
-            for (int c = 0; c < 4; ++c) {      // slots by wave; most waves have none
-              const float v = fresh_f(val[e][c]);
-              const bool in = in_bin(v);
-              const int slot = wave_alloc(in, &misc[3]);
-              if (in && slot < DEC_PQ_CAND) candv[slot] = v;   // (slot < cd)
+              for (int c = 0; c < 4; ++c) {    // slots by wave; most waves have none
+                const float v = val[e][c];
+                const bool in = v >= lo_b && !(v >= hi_b);
+                const int slot = wave_alloc(in, &misc[3]);
+                if (in && slot < DEC_PQ_CAND) candv[slot] = v;   // (slot < cd)
+              }
+            }
+          } else {
+#pragma unroll
+            for (int e = 0; e < G; ++e) {
+              if (!live(e)) continue;
+#pragma unroll
+              for (int c = 0; c < 4; ++c) {
+                const float v = fresh_f(val[e][c]);
+                const bool in = in_bin(v);
+                const int slot = wave_alloc(in, &misc[3]);
+                if (in && slot < DEC_PQ_CAND) candv[slot] = v;   // (slot < cd)
+              }
             }
           }
           __syncthreads();

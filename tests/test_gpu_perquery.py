@@ -155,6 +155,9 @@ def _crafted_rows(kind, H, Q, M, rng):
         s[..., ::2] = c[::2]
     elif kind == "quantised":       # few distinct values: many exact ties everywhere
         s = np.round(s * 4.0).astype(np.float32) / np.float32(4.0)
+    elif kind == "near_zero":       # the cut among values ~1e-3 under a threshold near -8: a value
+        s = s * np.float32(1e-3)    # bin's edges are far more ulps apart than the search window
+        s[..., ::97] = np.float32(8.0)
     return s
 
 
@@ -168,11 +171,14 @@ def _crafted_rows(kind, H, Q, M, rng):
                                           ("clustered", 4.0, 1, 20000), ("plain", float("inf"), 300, 20000),
                                           ("plain", 4.0, 2100, 3000), ("tied_cut", 4.0, 2100, 8192),
                                           ("clustered", 4.0, 2100, 16384), ("quantised", 0.0, 2100, 6000),
-                                          ("plain", 4.0, 2100, 3001)])
+                                          ("plain", 4.0, 2100, 3001), ("near_zero", 16.0, 300, 3000),
+                                          ("near_zero", 16.0, 2100, 8192)])
 def test_pq_select_crafted_rows(kind, tau, Q, M):
     """The per-query rule's selection from crafted score rows bit for bit against the oracle:
     exact ties at the cut, clusters of distinct values finer than the value bins (the key-space
-    refinement), quantised scores, tau = inf (every key passes), tau = 0 and tau < 0.  Batches of
+    refinement), quantised scores, a cut among values near 0 under a threshold near -8 (the value
+    bin's edges not found near their nominal values: the per-key bin test), tau = inf (every key
+    passes), tau = 0 and tau < 0.  Batches of
     300 queries take the 512-thread kernels, single queries the 1024-thread ones; rows of up to
     16384 keys the register-resident kernel, longer ones the LDS-staged kernel; batches of 4200
     rows as the per-query prefill's launches have them."""
