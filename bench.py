@@ -282,15 +282,15 @@ def bench_perquery(args, cfg, q, k, v, q_cpu, k_cpu, v_cpu, invf, ps, rs, tau):
                 / args.steps for j, s in enumerate(DECODE_STAGES)}
     r = plan.out
     esz = q.element_size()
-    # scores: one fp32 dot of D per causal (query, key) pair; attend: each query's kept K and V
-    # rows plus its 8 B of index / position per slot, the query read and the output written
-    # scores: the fp32 score rows written (4 B per causal (query, key) pair); attend: each query's
-    # kept K and V rows plus its index per slot, the query read and the output written.  The
-    # attend's rows come mostly from L2 (neighbouring queries of a head share the cache rows), so
-    # its roofline is the HBM traffic the counters measure (the traffic file holds each kernel's
-    # bytes per step, summed over the plan's launches), not the algorithmic bytes, which exceed
-    # what HBM could deliver.
+    # scores: the fp32 score rows written (4 B per causal (query, key) pair); select: those rows
+    # read and the k_max index slots of every query written; attend: each query's kept K and V
+    # rows plus its index per slot, the query read and the output written.  The attend's rows
+    # come mostly from L2 (neighbouring queries of a head share the cache rows), so its roofline
+    # is the HBM traffic the counters measure (the traffic file holds each kernel's bytes per
+    # step, summed over the plan's launches), not the algorithmic bytes, which exceed what HBM
+    # could deliver.
     sbytes = 4 * cfg.H * cfg.N * (cfg.N + 1) // 2
+    selbytes = sbytes + 4 * cfg.k_max * cfg.H * cfg.N
     kept = r["set_size"].clamp(max=cfg.k_max).to(torch.int64)
     abytes = int(kept.sum().item()) * (2 * cfg.D * esz + 4) + 2 * cfg.H * cfg.N * cfg.D * esz
 
@@ -311,11 +311,14 @@ def bench_perquery(args, cfg, q, k, v, q_cpu, k_cpu, v_cpu, invf, ps, rs, tau):
         "scores": hbm_roof("score_rows_kernel", sbytes, stage_ms["scores"],
                            "the fp32 score rows of every (query, key) pair are written once and read by the "
                            "selection"),
+        "select": hbm_roof("decode_select_pq_reg_kernel", selbytes, stage_ms["select"],
+                           "one pass over each score row held in registers; the vector ALU (70% busy) "
+                           "bounds it, not HBM"),
         "attend": hbm_roof("decode_attend_grouped_kernel", abytes, stage_ms["attend"],
                            "each query gathers its own K / V rows, served mostly from L2; the counters put the "
-                           "vector memory data path at about 90% busy, the pipeline that bounds it"),
+                           "vector memory data path at 88% busy and the vector ALU at 82%, which bound it"),
     }
-    dominant = max(("scores", "attend"), key=lambda n: stage_ms[n])
+    dominant = max(("scores", "select", "attend"), key=lambda n: stage_ms[n])
     print(f"[bench] {ms_per_step:.3f} ms/step; stages {stage_ms}", file=sys.stderr, flush=True)
     cpu = None
     if args.cpu_baseline_seconds > 0:
