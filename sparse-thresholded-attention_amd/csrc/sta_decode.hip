@@ -1626,8 +1626,9 @@ __global__ __launch_bounds__(256) void decode_attend_kernel(DecodeArgs a, int st
 // attend for a large batch under the per-query rule: 16 queries of one head per workgroup, one
 // 16-lane group per query sweeping all of its slots and writing the output.  Each half of a group
 // (8 lanes) takes its own slots, a lane holding D/16 rotation pairs of the slot's K and V rows, so
-// every row arrives in 16-byte loads (bf16, D = 128): the vector memory pipeline, not the
-// arithmetic, bounds this gather, and its cost goes by load instructions.  Under
+// every row arrives in 16-byte loads (bf16, D = 128): the vector memory pipeline bounds this
+// gather, with the arithmetic close behind (bf16 scores take one dot2 per pair of K elements
+// against the query's coefficients at the slot's rank, instead of rotating K).  Under
 // _decode_build_sets_pq every slot s sits at its dense rank s (perquery.py:707-717: idx is
 // ascending and newpos_k gathers the ranks at idx), so the (cos, sin) of slot s are the same for
 // every query: the workgroup computes them once per block of DEC_TB slots into LDS.  The launcher
@@ -1635,7 +1636,7 @@ __global__ __launch_bounds__(256) void decode_attend_kernel(DecodeArgs a, int st
 // from the caller go to the split attend, which reads every slot's position.
 // ------------------------------------------------------------------------------------------
 constexpr int DEC_QPW = 16;                    // queries per workgroup
-constexpr int DEC_TB = 64;                     // slots per table block
+constexpr int DEC_TB = 32;                     // slots per table block: 16 KB of LDS at D = 128
 
 namespace {
 
@@ -1675,13 +1676,18 @@ __device__ __forceinline__ float part_elem(const RowPart<DT, NF>& r, int e) {
 constexpr int DEC_GU = 4;                      // slots per half group and step
 
 template <int DT, int D, bool IDX4>
-__global__ __launch_bounds__(256) void decode_attend_grouped_kernel(DecodeArgs a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(DT == DT_F32 ? 1 : 5)))
+void decode_attend_grouped_kernel(DecodeArgs a) {
 #pragma clang fp contract(off)
   constexpr int HD = D / 2;
   constexpr int NF = D / 16;                   // rotation pairs per lane (8 lanes per slot)
   constexpr int U = DEC_GU;
+  static_assert(U == 4 && DEC_TB % (2 * U) == 0, "a step's slots stay inside one table block");
+  static_assert(256 % HD == 0 && DEC_QPW * DEC_TB / 4 <= 256, "table and index staging shapes");
   __shared__ __align__(16) float tcs[DEC_TB][HD];
   __shared__ __align__(16) float tsn[DEC_TB][HD];
+  __shared__ __align__(16) int sidx[DEC_QPW][DEC_TB];   // every query's slot indices in the block
+  __shared__ int gns[DEC_QPW];                          // every query's slot count
   __shared__ int wmax;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int l16 = lane & 15, grp = wave * 4 + (lane >> 4);
@@ -1698,10 +1704,15 @@ __global__ __launch_bounds__(256) void decode_attend_grouped_kernel(DecodeArgs a
   const int hk = h / (a.H / a.Hkv);
   const int m = a.M - (a.Q - 1 - ic);
   const int p = a.q_pos0 + ic;
+  // a slot's key is attended when 0 <= j < m and, causal, j <= p: one unsigned compare with jlim
+  const uint32_t jlim = (uint32_t)max(0, a.causal ? min(m, p + 1) : m);
   const int nslots = !live ? 0 : (a.set_size ? min(a.set_size[hi], a.k_max) : a.k_max);
   if (threadIdx.x == 0) wmax = 0;
   __syncthreads();
-  if (l16 == 0 && nslots > 0) atomicMax(&wmax, nslots);
+  if (l16 == 0) {
+    gns[grp] = nslots;
+    if (nslots > 0) atomicMax(&wmax, nslots);
+  }
   // the query rotated at newpos_q, this lane's pairs
   float q1[NF], q2[NF];
   {
@@ -1720,7 +1731,6 @@ __global__ __launch_bounds__(256) void decode_attend_grouped_kernel(DecodeArgs a
       q2[e] = x2[e] * cs + x1[e] * sn;
     }
   }
-  const int32_t* irow = a.idx + (int64_t)hi * a.k_max;
   // K / V rows by 32-bit byte offsets from the head's rows (the launcher checks that a head's
   // cache spans less than 2 GiB): one multiply-add per slot, the upper half an immediate offset
   constexpr int ESZ = DT == DT_F32 ? 4 : 2;
@@ -1731,6 +1741,7 @@ __global__ __launch_bounds__(256) void decode_attend_grouped_kernel(DecodeArgs a
   float mrun = -INFINITY, lrun = 0.0f, acc1[NF], acc2[NF];
 #pragma unroll
   for (int e = 0; e < NF; ++e) { acc1[e] = 0.0f; acc2[e] = 0.0f; }
+  const float tf = a.inv_freq_c[threadIdx.x % HD];   // this thread's frequency in the table
   __syncthreads();
   const int nall = wmax;
   for (int s0 = 0; s0 < nall; s0 += DEC_TB) {
@@ -1738,32 +1749,41 @@ __global__ __launch_bounds__(256) void decode_attend_grouped_kernel(DecodeArgs a
     for (int x = threadIdx.x; x < DEC_TB * HD; x += 256) {
       const int r = x / HD, f = x % HD;
       float sn, cs;
-      fast_sincos((float)(s0 + r) * a.inv_freq_c[f], sn, cs);
+      fast_sincos((float)(s0 + r) * tf, sn, cs);
       tcs[r][f] = cs * a.rope_scale_c;
       tsn[r][f] = sn * a.rope_scale_c;
+    }
+    // the block's slot indices of every query, four per thread (16-byte loads when the rows are
+    // 16-byte aligned and k_max % 4 == 0: s + 3 < k_max); the steps read them from LDS
+    if (threadIdx.x < DEC_QPW * DEC_TB / 4) {
+      const int g = threadIdx.x / (DEC_TB / 4), c = 4 * (threadIdx.x % (DEC_TB / 4)), s = s0 + c;
+      const int ns = gns[g];                   // 0 for a query past Q
+      int4 iv = make_int4(-1, -1, -1, -1);
+      if (s < ns) {
+        const int32_t* row = a.idx + ((int64_t)h * a.Q + qg * DEC_QPW + g) * a.k_max + s;
+        if constexpr (IDX4) {
+          iv = *(const int4*)row;
+        } else {
+          iv.x = row[0];
+          if (s + 1 < ns) iv.y = row[1];
+          if (s + 2 < ns) iv.z = row[2];
+          if (s + 3 < ns) iv.w = row[3];
+        }
+      }
+      *(int4*)&sidx[g][c] = iv;
     }
     __syncthreads();
     const int send = min(nslots, s0 + DEC_TB);
     for (int t0 = s0; t0 < send; t0 += 2 * U) {
       const int sb = t0 + half * U;            // this half's U slots sb .. sb + U - 1
+      const int4 iv = *(const int4*)&sidx[grp][sb - s0];   // sb - s0 is a multiple of 4
+      const int jr[U] = {iv.x, iv.y, iv.z, iv.w};
       int jv[U];
       bool okv[U];
-      if constexpr (IDX4 && U == 4) {          // 16-byte aligned rows: the 4 indices in one load
-        int4 iv = make_int4(-1, -1, -1, -1);
-        if (sb < send) iv = *(const int4*)(irow + sb);   // sb + 3 < k_max (k_max % 4 == 0)
-        jv[0] = iv.x; jv[1] = iv.y; jv[2] = iv.z; jv[3] = iv.w;
-      } else if constexpr (IDX4 && U == 2) {   // 8-byte aligned pairs
-        int2 iv = make_int2(-1, -1);
-        if (sb < send) iv = *(const int2*)(irow + sb);   // sb + 1 < k_max (k_max even)
-        jv[0] = iv.x; jv[1] = iv.y;
-      } else {
-#pragma unroll
-        for (int u = 0; u < U; ++u) jv[u] = sb + u < send ? irow[sb + u] : -1;
-      }
 #pragma unroll
       for (int u = 0; u < U; ++u) {
-        const int j = sb + u < send ? jv[u] : -1;
-        okv[u] = j >= 0 && j < m && (!a.causal || j <= p);   // sentinel m (perquery.py:739)
+        const int j = sb + u < send ? jr[u] : -1;
+        okv[u] = (uint32_t)j < jlim;            // sentinel m and j = -1 fail it (perquery.py:739)
         jv[u] = okv[u] ? j : 0;
       }
       RowPart<DT, NF> k1r[U], k2r[U], v1r[U], v2r[U];
@@ -1778,15 +1798,31 @@ __global__ __launch_bounds__(256) void decode_attend_grouped_kernel(DecodeArgs a
       float sc[U];
 #pragma unroll
       for (int u = 0; u < U; ++u) {
-        const int r = min(sb + u - s0, DEC_TB - 1);   // the slot's dense rank: the block's table
+        const int r = sb + u - s0;              // the slot's dense rank in the block's table (< DEC_TB)
         float part = 0.0f;
+        if constexpr (DT == DT_BF16) {
+          // q . rot(k) = k1 (q1 cs + q2 sn) + k2 (q2 cs - q1 sn): the query's coefficients at the
+          // slot's rank, rounded to bf16 as the rotated operands of Kernel C's dot are to TF32
+          // (perquery.py:294), and one dot2 per pair of raw bf16 K elements, fp32 accumulation
 #pragma unroll
-        for (int e = 0; e < NF; ++e) {
-          const float cs = tcs[r][f0 + e], sn = tsn[r][f0 + e];
-          const float x1 = part_elem(k1r[u], e), x2 = part_elem(k2r[u], e);
-          const float k1 = x1 * cs - x2 * sn;
-          const float k2 = x2 * cs + x1 * sn;
-          part = fmaf(q2[e], k2, fmaf(q1[e], k1, part));
+          for (int w = 0; w < NF / 2; ++w) {
+            const int e = 2 * w;
+            const float c0 = tcs[r][f0 + e], c1 = tcs[r][f0 + e + 1];
+            const float n0 = tsn[r][f0 + e], n1 = tsn[r][f0 + e + 1];
+            const float a0 = fmaf(q1[e], c0, q2[e] * n0), a1 = fmaf(q1[e + 1], c1, q2[e + 1] * n1);
+            const float b0 = fmaf(q2[e], c0, -(q1[e] * n0)), b1 = fmaf(q2[e + 1], c1, -(q1[e + 1] * n1));
+            part = dot2_dt<DT>(k1r[u].w[w], pack2_dt<DT>(a0, a1), part);
+            part = dot2_dt<DT>(k2r[u].w[w], pack2_dt<DT>(b0, b1), part);
+          }
+        } else {
+#pragma unroll
+          for (int e = 0; e < NF; ++e) {
+            const float cs = tcs[r][f0 + e], sn = tsn[r][f0 + e];
+            const float x1 = part_elem(k1r[u], e), x2 = part_elem(k2r[u], e);
+            const float k1 = fmaf(x1, cs, -(x2 * sn));
+            const float k2 = fmaf(x2, cs, x1 * sn);
+            part = fmaf(q2[e], k2, fmaf(q1[e], k1, part));
+          }
         }
         part = group8_sum(part);                // the slot's 8 lanes
         sc[u] = okv[u] ? part * a.sm_scale : -INFINITY;

@@ -313,11 +313,12 @@ __device__ __forceinline__ int wave_sum(int x) { return __builtin_amdgcn_readlan
 
 // the sum over each aligned group of 8 lanes, in every lane of the group (the xor-1, xor-2
 // butterfly within quads, then the other quad of the group: the same additions as the
-// xor-1/2/4 butterfly)
+// xor-1/2/4 butterfly).  Every lane's source is inside its row, so bound_ctrl changes no value;
+// with it set the compiler folds each move into its add (v_add_f32_dpp).
 __device__ __forceinline__ float group8_sum(float x) {
-  x += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0xb1, 0xf, 0xf, false));
-  x += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0x4e, 0xf, 0xf, false));
-  x += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0x141, 0xf, 0xf, false));
+  x = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0xb1, 0xf, 0xf, true)) + x;
+  x = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x4e, 0xf, 0xf, true)) + x;
+  x = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x141, 0xf, 0xf, true)) + x;
   return x;
 }
 
