@@ -36,8 +36,9 @@ DecLayout dec_layout_of(const sta_decode_args* a) {
   size_t off = 0;
   L.qrot_off = off;                                   // rotated queries (H, Q, D) fp32
   off = align256(off + hq * a->D * 4);
-  L.scores_off = off;                                 // scores (H, Q, M) when not an output
-  off = align256(off + hq * a->M * 4);
+  L.scores_off = off;                                 // scores when not an output: (H, Q, M), or
+                                                      // 64 x 32 tiles from the score rows kernel
+  off = align256(off + (L.rows ? (size_t)a->H * score_tiles_per_head(a->Q, a->M) : hq * a->M) * 4);
   L.keys_off = off;                                   // key store of long caches
   off = align256(off + decode_keys_bytes(a->H, a->Q, a->M, dec_bend_words(a)));
   L.size_off = off;                                   // set sizes (H, Q) when not an output
@@ -178,6 +179,7 @@ int dec_scores(const sta_decode_args* a, const DecLayout& L, DecodeArgs d, float
   r.k_rows_pad = L.k_rows_pad;
   r.sm_scale = a->sm_scale;
   r.scores = scores;
+  r.tiles = d.score_tiles;
   e = launch_score_rows(a->D, r, st);
   return e == hipSuccess ? STA_OK : hip_fail(e, "decode scores: score rows");
 }
@@ -288,6 +290,8 @@ int sta_decode_attention(const sta_decode_args* a, void* stream) {
   DecodeArgs d = dec_args_of(a, L);
   // the attend sweeps only the selected slots: the set sizes always exist (output or workspace)
   if (!d.set_size) d.set_size = (int32_t*)((char*)a->workspace + L.size_off);
+  // scores that only this call's selection reads leave the score rows kernel in 64 x 32 tiles
+  d.score_tiles = L.rows && !a->scores ? 1 : 0;
   if ((rc = mark_event(a->stage_events, 0, st)) != STA_OK) return rc;
   if ((rc = dec_scores(a, L, d, d.scores, st)) != STA_OK) return rc;
   if ((rc = mark_event(a->stage_events, 1, st)) != STA_OK) return rc;

@@ -327,6 +327,20 @@ size_t decode_keys_bytes(int H, int Q, int M, int nbend) {
 int decode_bend_words(const DecodeArgs& a) { return a.rule == 2 ? (a.M + a.block_n - 1) / a.block_n : 0; }
 
 // NT threads per query: 1024 for a few queries (latency), 512 for large batches (throughput)
+// query i of head h's score row: key j at at(j) = p + (j / SCORE_TW) * ps + j % SCORE_TW, with
+// ps = SCORE_TW for row-major (H, Q, M) scores and 64 SCORE_TW for the tiles of score_tile_row
+struct ScoreRow {
+  const float* p;
+  int ps;
+  __device__ __forceinline__ const float* at(int j) const {
+    return p + (j >> SCORE_TW_LG) * ps + (j & (SCORE_TW - 1));
+  }
+};
+__device__ __forceinline__ ScoreRow score_row_of(const DecodeArgs& a, int h, int i) {
+  if (a.score_tiles) return {a.scores + score_tile_row(h, i, a.Q, a.M), 64 * SCORE_TW};
+  return {a.scores + ((int64_t)h * a.Q + i) * a.M, SCORE_TW};
+}
+
 template <bool GKEYS, int NT>
 __global__ __launch_bounds__(NT) void decode_select_kernel(DecodeArgs a) {
 #pragma clang fp contract(off)
@@ -348,7 +362,7 @@ __global__ __launch_bounds__(NT) void decode_select_kernel(DecodeArgs a) {
   int* misc = tmp + NW;                // 8
   const int j0 = tid * per, j1 = min(j0 + per, m);
   uint32_t* myrow = ks + tid * PS;
-  const float* srow = a.scores + (int64_t)hi * a.M;
+  const ScoreRow sr = score_row_of(a, h, i);
 
   // ---- stage the scores as keys (coalesced reads, eight in flight per lane), exact max
   // (exact_2.py:549) ----
@@ -359,7 +373,7 @@ __global__ __launch_bounds__(NT) void decode_select_kernel(DecodeArgs a) {
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
       const int j = tid + (e0 + u) * NT;
-      sv[u] = (e0 + u < per && j < m) ? srow[j] : 0.0f;
+      sv[u] = (e0 + u < per && j < m) ? *sr.at(j) : 0.0f;
     }
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
@@ -674,7 +688,7 @@ __global__ __launch_bounds__(NT) void decode_select_pq_kernel(DecodeArgs a) {
   const int j0 = tid * per, j1 = min(j0 + per, m);
   const int nk = max(j1 - j0, 0);
   uint32_t* myrow = ks + tid * PS;
-  const float* srow = a.scores + (int64_t)hi * a.M;
+  const ScoreRow sr = score_row_of(a, h, i);
 
   // ---- 1. stage the scores as keys, exact max.  16-byte reads (four keys per lane and load,
   // eight loads in flight) when the row is 16-byte aligned; the vector memory unit's cost goes
@@ -686,18 +700,18 @@ __global__ __launch_bounds__(NT) void decode_select_pq_kernel(DecodeArgs a) {
     const int row = j / per;
     ks[row * PS + (j - row * per)] = key;
   };
-  if (((uintptr_t)srow & 15) == 0) {
+  if (((uintptr_t)sr.p & 15) == 0) {
     const int nq = (NT * per + 3) / 4;         // float4 units covering the keys of every row
     for (int e0 = 0; e0 * NT < nq; e0 += 8) {
       float4 sv[8];
 #pragma unroll
       for (int u = 0; u < 8; ++u) {
         const int qd = tid + (e0 + u) * NT;    // keys 4 qd .. 4 qd + 3
-        sv[u] = (qd < nq && 4 * qd + 3 < m) ? ((const float4*)srow)[qd] : make_float4(0.f, 0.f, 0.f, 0.f);
+        sv[u] = (qd < nq && 4 * qd + 3 < m) ? *(const float4*)sr.at(4 * qd) : make_float4(0.f, 0.f, 0.f, 0.f);
         if (qd < nq && 4 * qd < m && 4 * qd + 3 >= m) {   // the row's ragged end
-          sv[u].x = srow[4 * qd];
-          if (4 * qd + 1 < m) sv[u].y = srow[4 * qd + 1];
-          if (4 * qd + 2 < m) sv[u].z = srow[4 * qd + 2];
+          sv[u].x = *sr.at(4 * qd);
+          if (4 * qd + 1 < m) sv[u].y = *sr.at(4 * qd + 1);
+          if (4 * qd + 2 < m) sv[u].z = *sr.at(4 * qd + 2);
         }
       }
 #pragma unroll
@@ -718,7 +732,7 @@ __global__ __launch_bounds__(NT) void decode_select_pq_kernel(DecodeArgs a) {
 #pragma unroll
       for (int u = 0; u < 8; ++u) {
         const int j = tid + (e0 + u) * NT;
-        sv[u] = (e0 + u < per && j < m) ? srow[j] : 0.0f;
+        sv[u] = (e0 + u < per && j < m) ? *sr.at(j) : 0.0f;
       }
 #pragma unroll
       for (int u = 0; u < 8; ++u)
@@ -997,7 +1011,7 @@ __global__ __launch_bounds__(NT, NT == 512 ? 6 : 4) void decode_select_pq_reg_ke
   const int h = hi / a.Q, i = hi % a.Q;
   const int m = a.M - (a.Q - 1 - i);           // keys this query sees
   const int p = a.q_pos0 + i;                  // its position (p < m)
-  const float* srow = a.scores + (int64_t)hi * a.M;
+  const ScoreRow sr = score_row_of(a, h, i);
   const float nan_end = __uint_as_float(DEC_NAN_END);
   // key (e, c) of this thread is j0 + 4 NT e + c.  Each pass takes j0 afresh (an empty asm the
   // compiler cannot see through), so that no pass keeps another pass's key indices live.
@@ -1021,7 +1035,7 @@ __global__ __launch_bounds__(NT, NT == 512 ? 6 : 4) void decode_select_pq_reg_ke
   // ---- 1. the row's values (DEC_NAN_END past its end) and the exact max ----
   float val[G][4];
   const int js = fresh_j0();
-  if (((uintptr_t)srow & 15) == 0) {
+  if (((uintptr_t)sr.p & 15) == 0) {
 #pragma unroll
     for (int e = 0; e < G; ++e) {
       const int j = js + 4 * NT * e;
@@ -1029,12 +1043,12 @@ __global__ __launch_bounds__(NT, NT == 512 ? 6 : 4) void decode_select_pq_reg_ke
       if (!live(e)) {
         v = make_float4(nan_end, nan_end, nan_end, nan_end);
       } else if (j + 3 < m) {
-        v = ((const float4*)srow)[e * NT + tid];
+        v = *(const float4*)sr.at(j);
       } else {
         v = make_float4(nan_end, nan_end, nan_end, nan_end);
-        if (j < m) v.x = srow[j];
-        if (j + 1 < m) v.y = srow[j + 1];
-        if (j + 2 < m) v.z = srow[j + 2];
+        if (j < m) v.x = *sr.at(j);
+        if (j + 1 < m) v.y = *sr.at(j + 1);
+        if (j + 2 < m) v.z = *sr.at(j + 2);
       }
       val[e][0] = v.x; val[e][1] = v.y; val[e][2] = v.z; val[e][3] = v.w;
     }
@@ -1044,7 +1058,7 @@ __global__ __launch_bounds__(NT, NT == 512 ? 6 : 4) void decode_select_pq_reg_ke
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
         const int j = js + 4 * NT * e + c;
-        val[e][c] = j < m ? srow[j] : nan_end;
+        val[e][c] = j < m ? *sr.at(j) : nan_end;
       }
   }
   float vmax = -INFINITY;

@@ -273,6 +273,21 @@ int dca_dec_nblocks(int M);
 int dca_dec_max_group();
 hipError_t launch_dca_decode(int dtype, int D, const DcaDecArgs& a, hipStream_t st);
 
+// Score rows in 64-row tiles: (H, ceil(Q / 64), ceil(M / SCORE_TW), 64, SCORE_TW) floats, the
+// layout the batched score rows kernel writes when only the selection of the same call reads the
+// scores.  Key j of query i sits at score_tile_row(...) + (j / SCORE_TW) * 64 * SCORE_TW +
+// j % SCORE_TW; rows past Q and keys past M are padding.  A wave's 64 x 32 block of scores then
+// lands inside one 32 KB tile, and a row is read in 512-byte pieces.
+constexpr int SCORE_TW_LG = 7;
+constexpr int SCORE_TW = 1 << SCORE_TW_LG;
+__host__ __device__ inline int64_t score_tiles_per_head(int Q, int M) {
+  return (int64_t)((Q + 63) / 64) * 64 * (((M + SCORE_TW - 1) / SCORE_TW) * SCORE_TW);
+}
+__host__ __device__ inline int64_t score_tile_row(int h, int i, int Q, int M) {
+  return h * score_tiles_per_head(Q, M) + ((int64_t)(i >> 6) * ((M + SCORE_TW - 1) / SCORE_TW) << (6 + SCORE_TW_LG)) +
+         ((i & 63) << SCORE_TW_LG);
+}
+
 // decode: Q queries over one cache of M keys, query i at position q_pos0 + i seeing keys
 // [0, M - (Q - 1 - i)): shared_selection_triton_exact_2.py:235-271, 505-655
 struct DecodeArgs {
@@ -292,7 +307,8 @@ struct DecodeArgs {
   int n_global, n_local, k_max;
   int use_pct;            // pct_decode < 100
   float pct_frac;         // float32(pct_decode / 100)
-  float* scores;          // (H, Q, M)
+  float* scores;          // (H, Q, M), or 64 x 32 tiles when score_tiles
+  int score_tiles;        // the scores' layout (score_tile_row)
   uint32_t* keys;         // key store of the selection when the cache is too long for LDS
   int32_t* idx;           // (H, Q, k_max)
   float* newpos_k;        // (H, Q, k_max)
@@ -317,7 +333,9 @@ struct RowsArgs {
   int H, Hkv, Q, M, q_pos0;
   int q_rows_pad, k_rows_pad;   // multiples of 32; k_rows_pad >= M
   float sm_scale;
-  float* scores;          // (H, Q, M): row i written for its keys [0, M - (Q - 1 - i))
+  float* scores;          // (H, Q, M), or 64 x 32 tiles (score_tile_row) when tiles: row i
+                          // written for its keys [0, M - (Q - 1 - i))
+  int tiles;
 };
 hipError_t launch_score_rows(int D, const RowsArgs& a, hipStream_t st);
 

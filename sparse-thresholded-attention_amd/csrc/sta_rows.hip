@@ -21,7 +21,10 @@
 // Each wave's 64 x 32 block of scores goes out through a per-wave LDS tile: written in the matrix
 // cores' output layout, read back as four consecutive keys per lane, so that a row's 32 scores
 // leave in 16-byte stores (8 lanes per row) rather than 4-byte ones (the store data path moves
-// about as many bytes per instruction at 16 bytes per lane as at 4).
+// about as many bytes per instruction at 16 bytes per lane as at 4).  Row-major (H, Q, M) rows
+// put each row's 128 bytes of a block 4M bytes from the next row's; in the tiled layout
+// (score_tile_row, for scores that only the selection reads) the block's rows lie 512 bytes
+// apart inside one 32 KB tile, which the memory writes at a higher rate.
 #include "sta_device.h"
 #include "sta_kernels.h"
 
@@ -85,9 +88,8 @@ __global__ __launch_bounds__(256) void score_rows_kernel(RowsArgs a, int npieces
   load_chunk(c0);
   store_chunk(0);
   __syncthreads();
-  float* srow = a.scores + (int64_t)h * a.Q * a.M;
-  // 16-byte stores need every row start 16-byte aligned
-  const bool vec = (a.M & 3) == 0 && ((uintptr_t)a.scores & 15) == 0;
+  // 16-byte stores need every row start 16-byte aligned (tiles: 128-byte rows)
+  const bool vec = (a.tiles || (a.M & 3) == 0) && ((uintptr_t)a.scores & 15) == 0;
   for (int c = c0; c < c1; ++c) {
     const int buf = (c - c0) & 1;
     if (c + 1 < c1) load_chunk(c + 1);
@@ -127,7 +129,9 @@ __global__ __launch_bounds__(256) void score_rows_kernel(RowsArgs a, int npieces
         const int row = wrow0 + r;
         const int mrow = a.M - (a.Q - 1 - row);  // the keys this row sees
         if (row < a.Q && kq < mrow) {
-          float* dst = srow + (int64_t)row * a.M + kq;
+          float* dst = a.tiles ? a.scores + score_tile_row(h, row, a.Q, a.M) +
+                                     ((int64_t)(kq >> SCORE_TW_LG) << (6 + SCORE_TW_LG)) + (kq & (SCORE_TW - 1))
+                               : a.scores + ((int64_t)h * a.Q + row) * a.M + kq;
           if (vec && kq + 3 < mrow) {
             // written once, read once by the selection: non-temporal, past the caches' allocation
             __builtin_nontemporal_store(floatx4{v.x, v.y, v.z, v.w}, (floatx4*)dst);

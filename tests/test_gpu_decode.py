@@ -254,3 +254,34 @@ def test_decode_hybrid_two_geometries():
     assert _bits_equal(r["newpos_k"].cpu().numpy(), on) and _bits_equal(r["newpos_q"].cpu().numpy(), oq)
     ref = orc.decode_attend(qn, kn, vn, dc, invf_c.numpy(), 1.0, sm, M - 1, oi, on, oq)
     check_output(out_f32(r["out"]), ref, dc, "decode hybrid")
+
+
+@pytest.mark.parametrize("case", [
+    # (rule, H, Hkv, Q, M, D, dtype, k_max, pct_decode, causal): the selection kernel each reaches
+    ("pq", 2, 1, 200, 1500, 128, torch.bfloat16, 256, 100.0, False),     # the row in registers
+    ("pq", 2, 2, 70, 20000, 64, torch.bfloat16, 2048, 100.0, False),     # the row in LDS
+    ("shared", 2, 2, 96, 900, 64, torch.float16, 128, 30.0, True),       # the general selection
+    ("pq", 2, 1, 65, 39000, 64, torch.bfloat16, 1024, 100.0, False),     # the global key store
+])
+def test_decode_tiled_scores_match_row_major(case):
+    """A batch's scores that only the selection of the same call reads leave the score rows kernel
+    in 64 x 32 tiles; a call that also returns them writes (H, Q, M) rows.  Both calls give the
+    same sets and outputs bit for bit (Q not a multiple of 64, M not a multiple of 32), and every
+    selection kernel reads both layouts."""
+    import _sta_native as native
+    from synthetic import base_inv_freq, planted_inputs
+    rule, H, Hkv, Q, M, D, dt, km, pctd, causal = case
+    say(f"tiled vs row-major scores: {rule} H={H} Hkv={Hkv} Q={Q} M={M} D={D} {dt} k_max={km}")
+    qa, k, v = planted_inputs(29, H, Hkv, M, D, 0.01, dt, DEV)
+    q = qa[0, :, M - Q:, :].contiguous()
+    invf = base_inv_freq(D, 10000.0)
+    tau = torch.full((H,), 4.0)
+    kw = dict(inv_freq_c=invf, pos_scale_c=1.0, rope_scale_c=1.0, rule="pq") if rule == "pq" else {}
+    runs = [native.decode_attention(q, k, v, tau, invf, M - Q, 0.5, 1.0, None, 16, 16, km, pctd, causal,
+                                    want_scores=ws, **kw) for ws in (False, True)]
+    torch.cuda.synchronize()
+    tiled, rows = runs
+    names = ["out", "idx", "newpos_q", "set_size"] + (["usize", "overflow"] if rule == "pq" else ["newpos_k"])
+    for name in names:
+        assert torch.equal(tiled[name], rows[name]), name
+    assert int((tiled["set_size"] > 0).sum()) == H * Q
