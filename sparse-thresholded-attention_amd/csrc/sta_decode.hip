@@ -1078,6 +1078,7 @@ __global__ __launch_bounds__(NT, NT == 512 ? 6 : 4) void decode_select_pq_reg_ke
   const float vspan = vmax - thr;
   const bool lin = vspan > 0.0f && vspan < INFINITY;
   const float inv0 = lin ? (float)NB / vspan : 0.0f;
+  const float boff = -(thr * inv0);            // value bin of v: fma(v, inv0, boff), monotone in v
   const uint32_t kthr = okey(thr), kmx = okey(vmax);
   const uint32_t span0 = kmx >= kthr ? kmx - kthr : 0u;
   const int shift0 = span0 == 0u ? 0 : max(0, 32 - __clz(span0) - 11);   // span0 >> shift0 < NB
@@ -1106,7 +1107,7 @@ __global__ __launch_bounds__(NT, NT == 512 ? 6 : 4) void decode_select_pq_reg_ke
     }
   }
   // ---- 3. the non-forced passers: count and level-0 histogram ----
-  auto vbin = [&](float v) { return min((int)((v - thr) * inv0), NB - 1); };
+  auto vbin = [&](float v) { return min((int)fmaf(v, inv0, boff), NB - 1); };
   int c_nf = 0;
   if (lin) {
 #pragma unroll
@@ -1117,7 +1118,7 @@ __global__ __launch_bounds__(NT, NT == 512 ? 6 : 4) void decode_select_pq_reg_ke
         const float v = val[e][c];
         const bool ps = v >= thr;
         c_nf += ps ? 1 : 0;
-        atomicAdd(&lbuf[ps ? vbin(ps ? v : thr) : SPARE + lane], ps ? 1u : 0u);
+        atomicAdd(&lbuf[ps ? vbin(ps ? v : thr) : SPARE + lane], 1u);   // (spare words: never read)
       }
     }
   } else {
@@ -1218,11 +1219,11 @@ __global__ __launch_bounds__(NT, NT == 512 ? 6 : 4) void decode_select_pq_reg_ke
         const uint32_t bhi = rhi - blo <= bw ? rhi : blo + bw;
         // (the threshold and scale taken afresh: the per-key bins are not hoisted out of the
         // level loop, where 32 of them would stay live)
-        float thr_l = thr, inv_l = inv0;
-        asm volatile("" : "+v"(thr_l), "+v"(inv_l));
+        float thr_l = thr, inv_l = inv0, boff_l = boff;
+        asm volatile("" : "+v"(thr_l), "+v"(inv_l), "+v"(boff_l));
         auto in_bin = [&](float v) {
           const bool ps = v >= thr_l;
-          return linear ? (ps && min((int)(((ps ? v : thr_l) - thr_l) * inv_l), NB - 1) == d)
+          return linear ? (ps && min((int)fmaf(ps ? v : thr_l, inv_l, boff_l), NB - 1) == d)
                         : (ps && okey(v) - blo <= bhi - blo);
         };
         if (cd <= DEC_PQ_CAND) {
@@ -1240,7 +1241,7 @@ __global__ __launch_bounds__(NT, NT == 512 ? 6 : 4) void decode_select_pq_reg_ke
               }
               const float x0 = thr_l + (float)dd / inv_l;
               const float cv = okey_value(okey(x0) + (uint32_t)(lane - 32));
-              const bool ge = cv >= thr_l && min((int)((cv - thr_l) * inv_l), NB - 1) >= dd;
+              const bool ge = cv >= thr_l && min((int)fmaf(cv, inv_l, boff_l), NB - 1) >= dd;
               const unsigned long long msk = __ballot(ge);
               const int first = __ffsll(msk) - 1;  // the values rise with the lane
               if (first <= 0 || (msk >> first) != (~0ull >> first)) return false;
@@ -1350,23 +1351,17 @@ __global__ __launch_bounds__(NT, NT == 512 ? 6 : 4) void decode_select_pq_reg_ke
     float keep_b = kb;
     asm volatile("" : "+v"(keep_b));
     int lpre1[G];
-    uint32_t kbits[G];
+    auto kept1 = [&](float x) { return is_forced(x) || x >= keep_b; };
 #pragma unroll
     for (int e = 0; e < G; ++e) {
       lpre1[e] = 0;
-      kbits[e] = 0u;
       if (!live(e)) {
         if (lane == 63) seg[e * NW + wave] = 0;
         continue;
       }
       int v = 0;
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const float x = val[e][c];
-        const bool kp = is_forced(x) || x >= keep_b;
-        v += kp ? 1 : 0;
-        kbits[e] |= (kp ? 1u : 0u) << c;
-      }
+      for (int c = 0; c < 4; ++c) v += kept1(val[e][c]) ? 1 : 0;
       const int xs = wave_incl_sum(v);
       lpre1[e] = xs - v;
       if (lane == 63) seg[e * NW + wave] = xs;
@@ -1387,12 +1382,22 @@ __global__ __launch_bounds__(NT, NT == 512 ? 6 : 4) void decode_select_pq_reg_ke
       int rank = seg[e * NW + wave] + lpre1[e];   // kept keys before this lane's keys
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
-        const int j = jw + 4 * NT * e + c;
-        const bool kp = (kbits[e] >> c) & 1u;
-        obuf[kp && rank < DEC_PQR_STAGE ? rank : SPARE + lane] = j;   // (rank < k_max)
-        rq = j == p ? rank : rq;               // the query itself is forced (:719)
+        const bool kp = kept1(val[e][c]);
+        obuf[kp && rank < DEC_PQR_STAGE ? rank : SPARE + lane] = jw + 4 * NT * e + c;   // (rank < k_max)
         rank += kp ? 1 : 0;
       }
+    }
+    // the query's own rank (it is forced, :719), in the thread that holds key p
+    if (tid == ((p >> 2) & (NT - 1))) {
+      const int ep = (p >> 2) / NT, cp = p & 3;
+#pragma unroll
+      for (int e = 0; e < G; ++e)
+        if (e == ep) {
+          int r = seg[e * NW + wave] + lpre1[e];
+#pragma unroll
+          for (int c = 0; c < 3; ++c) r += c < cp && kept1(val[e][c]) ? 1 : 0;
+          rq = r;
+        }
     }
   } else {
     // ties at the cut taken in part: classes of 2 bits (kept / tie) and tie counts in the scans
