@@ -978,26 +978,45 @@ __global__ __launch_bounds__(NT) void decode_select_pq_kernel(DecodeArgs a) {
 //     holding more than DEC_PQ_CAND keys is split by key-space bins of its key range (closed-form
 //     bin ranges), as often as needed.
 //   - Per-key LDS updates are branch-free: every wave has passers, so a branch would be taken
-//     anyway; non-passers add 0 to, and dropped keys store into, per-lane spare words.
+//     anyway; non-passers add to, and dropped keys store into, per-lane spare words.
 //   - Dense ranks come from segments of 256 consecutive keys (one wave, one group index): a wave
 //     scan inside each segment and one scan over the G * NW segment totals.
+//   - SH: the shared files' rule without a top-pct cut (exact_2.py:549-603), the same passers,
+//     forced keys and cap by score, except that every key equal to the cut is kept (score >=
+//     cut_c, :582) and the first k_max kept keys in key order take the slots; positions are the
+//     reposition rank + cummax(fl(j pos_scale) - rank) over the kept keys (:587-592), a max scan
+//     over the same segments.
 // ------------------------------------------------------------------------------------------
 constexpr int DEC_PQR_BINS = 2048;                         // level bins, 32-bit counters
 constexpr int DEC_PQR_STAGE = DEC_PQR_BINS + DEC_PQ_CAND;  // histogram + cut-bin values (words)
 constexpr uint32_t DEC_NAN_END = 0x7fc0beefu;              // past the row's end
 constexpr uint32_t DEC_NAN_FORCED = 0x7fc0f00du;           // forced
 
-template <int NT, int G>
+// float max-scan over the 64 lanes (no NaN), the shifted-in lanes at -inf
+__device__ __forceinline__ float wave_incl_max_f32(float x) {
+  const int ninf = __builtin_bit_cast(int, -INFINITY);
+  x = fmaxf(x, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(ninf, __builtin_bit_cast(int, x), 0x111, 0xf, 0xf, false)));
+  x = fmaxf(x, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(ninf, __builtin_bit_cast(int, x), 0x112, 0xf, 0xf, false)));
+  x = fmaxf(x, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(ninf, __builtin_bit_cast(int, x), 0x114, 0xf, 0xf, false)));
+  x = fmaxf(x, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(ninf, __builtin_bit_cast(int, x), 0x118, 0xf, 0xf, false)));
+  x = fmaxf(x, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(ninf, __builtin_bit_cast(int, x), 0x142, 0xa, 0xf, false)));
+  x = fmaxf(x, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(ninf, __builtin_bit_cast(int, x), 0x143, 0xc, 0xf, false)));
+  return x;
+}
+
+template <int NT, int G, bool SH>
 __global__ __launch_bounds__(NT, NT == 512 ? 6 : 4) void decode_select_pq_reg_kernel(DecodeArgs a) {
 #pragma clang fp contract(off)
   constexpr int NW = NT / 64;
   constexpr int NB = DEC_PQR_BINS;
   constexpr int BPT = NB / NT;                 // bins per thread in the cut search
   constexpr int NSEG = G * NW;                 // <= 64: one wave scans the segment totals
-  static_assert(NSEG <= 64 && BPT >= 1, "launch shape");
+  constexpr int SPL = (NSEG + 63) / 64;        // segments per lane in the scans over them
+  static_assert(NSEG <= 128 && BPT >= 1, "launch shape");
   constexpr int SPARE = DEC_PQR_STAGE;         // 64 per-lane spare words after the staging area
   __shared__ __align__(16) uint32_t lbuf[DEC_PQR_STAGE + 64];   // histogram + cut-bin values, then idx
   __shared__ int seg[NSEG];
+  __shared__ float segm[SH ? NSEG : 1];       // SH: each segment's max of fl(j ps - rank)
   __shared__ float red_max[NW];
   __shared__ int red_sum[NW];
   __shared__ int red_scan[NW];
@@ -1021,6 +1040,24 @@ __global__ __launch_bounds__(NT, NT == 512 ? 6 : 4) void decode_select_pq_reg_ke
     return j0;
   };
   auto is_forced = [](float v) { return __float_as_uint(v) == DEC_NAN_FORCED; };
+  // wave 0: the segment counts in key order to exclusive prefix sums in place, and their total;
+  // SPL consecutive segments per lane
+  auto seg_scan = [&]() {
+    int v[SPL], t = 0;
+#pragma unroll
+    for (int k = 0; k < SPL; ++k) {
+      v[k] = lane * SPL + k < NSEG ? seg[lane * SPL + k] : 0;
+      t += v[k];
+    }
+    const int x = wave_incl_sum(t);
+    int run = x - t;
+#pragma unroll
+    for (int k = 0; k < SPL; ++k) {
+      if (lane * SPL + k < NSEG) seg[lane * SPL + k] = run;
+      run += v[k];
+    }
+    if (lane == 63) seg_total = x;
+  };
   // group e of this wave holds keys [4 (e NT + 64 wave), + 256): the passes skip the groups that
   // start past the row's end (wave-uniform branches; their keys would all be past the end)
   const int wave_u = __builtin_amdgcn_readfirstlane(wave);
@@ -1329,6 +1366,8 @@ __global__ __launch_bounds__(NT, NT == 512 ? 6 : 4) void decode_select_pq_reg_ke
     }
   }
 
+  if constexpr (SH) ties_all = true;           // every key equal to the cut (exact_2.py:582)
+
   // ---- 5. compaction with dense ranks (perquery.py:703-719) ----
   // kept: forced, or above the cut (at or above the threshold when nothing is cut); ties: equal
   // to the cut, the first `quota` of them in key order kept.  Per segment (e, wave) the lanes'
@@ -1367,28 +1406,76 @@ __global__ __launch_bounds__(NT, NT == 512 ? 6 : 4) void decode_select_pq_reg_ke
       if (lane == 63) seg[e * NW + wave] = xs;
     }
     __syncthreads();                           // every read of the histogram / cut-bin values is done
-    if (wave == 0) {                           // segments in key order: e-major, then wave
-      const int v = lane < NSEG ? seg[lane] : 0;
-      const int x = wave_incl_sum(v);
-      if (lane < NSEG) seg[lane] = x - v;
-      if (lane == 63) seg_total = x;
-    }
+    if (wave == 0) seg_scan();                 // segments in key order: e-major, then wave
     __syncthreads();
     total = seg_total;
     const int jw = fresh_j0();
+    float lexc[SH ? G : 1];                      // SH: the max over this wave's lanes before this one
 #pragma unroll
     for (int e = 0; e < G; ++e) {
-      if (!live(e)) continue;
+      if (!live(e)) {
+        if constexpr (SH) {
+          lexc[e] = -INFINITY;
+          if (lane == 63) segm[e * NW + wave] = -INFINITY;
+        }
+        continue;
+      }
       int rank = seg[e * NW + wave] + lpre1[e];   // kept keys before this lane's keys
+      float mx = -INFINITY;
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
         const bool kp = kept1(val[e][c]);
-        obuf[kp && rank < DEC_PQR_STAGE ? rank : SPARE + lane] = jw + 4 * NT * e + c;   // (rank < k_max)
+        const int j = jw + 4 * NT * e + c;
+        obuf[kp && rank < DEC_PQR_STAGE ? rank : SPARE + lane] = j;   // (rank < k_max, or past it: SH)
+        if constexpr (SH) mx = kp ? fmaxf(mx, (float)j * a.pos_scale_c - (float)rank) : mx;   // :590-591
         rank += kp ? 1 : 0;
       }
+      if constexpr (SH) {
+        const float x = wave_incl_max_f32(mx);
+        const float up = __shfl_up(x, 1, 64);
+        lexc[e] = lane == 0 ? -INFINITY : up;
+        if (lane == 63) segm[e * NW + wave] = x;
+      }
     }
-    // the query's own rank (it is forced, :719), in the thread that holds key p
-    if (tid == ((p >> 2) & (NT - 1))) {
+    if constexpr (SH) {
+      // the segments' exclusive max in key order, then every kept key's position rank + cummax,
+      // written straight to its slot (:592, :601); the query's own at key p (:603)
+      __syncthreads();
+      if (wave == 0) {                         // SPL consecutive segments per lane
+        float v[SPL], t = -INFINITY;
+#pragma unroll
+        for (int k = 0; k < SPL; ++k) {
+          v[k] = lane * SPL + k < NSEG ? segm[lane * SPL + k] : -INFINITY;
+          t = fmaxf(t, v[k]);
+        }
+        const float up = __shfl_up(wave_incl_max_f32(t), 1, 64);
+        float run = lane == 0 ? -INFINITY : up;
+#pragma unroll
+        for (int k = 0; k < SPL; ++k) {
+          if (lane * SPL + k < NSEG) segm[lane * SPL + k] = run;
+          run = fmaxf(run, v[k]);
+        }
+      }
+      __syncthreads();
+      float* nrow = a.newpos_k + (int64_t)hi * a.k_max;
+#pragma unroll
+      for (int e = 0; e < G; ++e) {
+        if (!live(e)) continue;
+        int rank = seg[e * NW + wave] + lpre1[e];
+        float run = fmaxf(segm[e * NW + wave], lexc[e]);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const bool kp = kept1(val[e][c]);
+          const int j = jw + 4 * NT * e + c;
+          run = kp ? fmaxf(run, (float)j * a.pos_scale_c - (float)rank) : run;
+          const float np = (float)rank + run;
+          if (kp && rank < a.k_max) nrow[rank] = np;
+          if (j == p) a.newpos_q[hi] = np;
+          rank += kp ? 1 : 0;
+        }
+      }
+    } else if (tid == ((p >> 2) & (NT - 1))) {
+      // the query's own rank (it is forced, :719), in the thread that holds key p
       const int ep = (p >> 2) / NT, cp = p & 3;
 #pragma unroll
       for (int e = 0; e < G; ++e)
@@ -1425,12 +1512,7 @@ __global__ __launch_bounds__(NT, NT == 512 ? 6 : 4) void decode_select_pq_reg_ke
       if (lane == 63) seg[e * NW + wave] = xs;
     }
     __syncthreads();                             // every read of the histogram / cut-bin values is done
-    if (wave == 0) {                             // segments in key order: e-major, then wave
-      const int v = lane < NSEG ? seg[lane] : 0;
-      const int x = wave_incl_sum(v);
-      if (lane < NSEG) seg[lane] = x - v;
-      if (lane == 63) seg_total = x;
-    }
+    if (wave == 0) seg_scan();                   // segments in key order: e-major, then wave
     __syncthreads();
     const int tot = seg_total;
     total = (tot & 0xffff) + min(tot >> 16, quota);
@@ -1458,9 +1540,9 @@ __global__ __launch_bounds__(NT, NT == 512 ? 6 : 4) void decode_select_pq_reg_ke
   int32_t* irow = a.idx + (int64_t)hi * a.k_max;
   float* nrow = a.newpos_k + (int64_t)hi * a.k_max;
   __syncthreads();
-  for (int s = tid; s < a.k_max; s += NT) {     // slot positions are the slot indices
-    irow[s] = s < nvalid ? obuf[s] : m;         // sentinel m
-    if (a.newpos_k) nrow[s] = s < nvalid ? (float)s : 0.0f;   // (NULL: not kept)
+  for (int s = tid; s < a.k_max; s += NT) {     // slot positions are the slot indices (SH: written
+    irow[s] = s < nvalid ? obuf[s] : m;         // above); sentinel m
+    if (SH ? s >= nvalid : a.newpos_k != nullptr) nrow[s] = s < nvalid ? (float)s : 0.0f;   // (NULL: not kept)
   }
   if (tid == 0 && a.set_size) a.set_size[hi] = total;
 }
@@ -2010,29 +2092,32 @@ static hipError_t launch_select_pq_t(const DecodeArgs& a, hipStream_t st) {
   return hipGetLastError();
 }
 
-template <int NT, int G>
+template <int NT, int G, bool SH>
 static hipError_t launch_select_pq_reg_t(const DecodeArgs& a, hipStream_t st) {
-  hipLaunchKernelGGL((decode_select_pq_reg_kernel<NT, G>), dim3(a.H * a.Q), dim3(NT), 0, st, a);
+  hipLaunchKernelGGL((decode_select_pq_reg_kernel<NT, G, SH>), dim3(a.H * a.Q), dim3(NT), 0, st, a);
   return hipGetLastError();
 }
 
-// the register-resident per-query selection: the smallest instance whose NT x 4G keys hold the
-// row, or nullptr past 16384 keys (those rows take the LDS store)
-static hipError_t (*select_pq_reg_for(int M, bool batch))(const DecodeArgs&, hipStream_t) {
+// the register-resident selection: the smallest instance whose NT x 4G keys hold the row, or
+// nullptr past 16384 keys in a batch and 32768 keys otherwise (those rows take the LDS store)
+template <bool SH>
+static hipError_t (*select_reg_for(int M, bool batch))(const DecodeArgs&, hipStream_t) {
   const int g = (M + (batch ? 2047 : 4095)) / (batch ? 2048 : 4096);   // 4-key groups per thread
   if (batch) {
-    if (g <= 1) return launch_select_pq_reg_t<512, 1>;
-    if (g <= 2) return launch_select_pq_reg_t<512, 2>;
-    if (g <= 3) return launch_select_pq_reg_t<512, 3>;
-    if (g <= 4) return launch_select_pq_reg_t<512, 4>;
-    if (g <= 6) return launch_select_pq_reg_t<512, 6>;
-    if (g <= 8) return launch_select_pq_reg_t<512, 8>;
+    if (g <= 1) return launch_select_pq_reg_t<512, 1, SH>;
+    if (g <= 2) return launch_select_pq_reg_t<512, 2, SH>;
+    if (g <= 3) return launch_select_pq_reg_t<512, 3, SH>;
+    if (g <= 4) return launch_select_pq_reg_t<512, 4, SH>;
+    if (g <= 6) return launch_select_pq_reg_t<512, 6, SH>;
+    if (g <= 8) return launch_select_pq_reg_t<512, 8, SH>;
     return nullptr;
   }
-  if (g <= 1) return launch_select_pq_reg_t<1024, 1>;
-  if (g <= 2) return launch_select_pq_reg_t<1024, 2>;
-  if (g <= 3) return launch_select_pq_reg_t<1024, 3>;
-  if (g <= 4) return launch_select_pq_reg_t<1024, 4>;
+  if (g <= 1) return launch_select_pq_reg_t<1024, 1, SH>;
+  if (g <= 2) return launch_select_pq_reg_t<1024, 2, SH>;
+  if (g <= 3) return launch_select_pq_reg_t<1024, 3, SH>;
+  if (g <= 4) return launch_select_pq_reg_t<1024, 4, SH>;
+  if (g <= 6) return launch_select_pq_reg_t<1024, 6, SH>;
+  if (g <= 8) return launch_select_pq_reg_t<1024, 8, SH>;
   return nullptr;
 }
 
@@ -2042,13 +2127,17 @@ hipError_t launch_decode_select(const DecodeArgs& a, hipStream_t st) {
   // a few queries keep 1024 threads, whose shorter per-thread ranges finish each query sooner
   const bool batch = (int64_t)a.H * a.Q >= 512;
   // the per-query rule takes its own kernels (fewer passes): the row in registers up to 16384
-  // keys (k_max within the LDS staging), in LDS beyond while it fits
+  // keys in a batch and 32768 otherwise (k_max within the LDS staging), in LDS beyond while it
+  // fits; the shared rule without a top-pct cut takes the register kernel too (c1d's selection
+  // 29.1 -> 15.1 us)
   if (a.rule == 1 && !a.use_pct) {
     if (a.k_max <= DEC_PQR_STAGE)
-      if (auto f = select_pq_reg_for(a.M, batch)) return f(a, st);
+      if (auto f = select_reg_for<false>(a.M, batch)) return f(a, st);
     if (decode_select_pq_lds_bytes(a.M, batch ? 512 : 1024) <= 160 * 1024)
       return batch ? launch_select_pq_t<512>(a, st) : launch_select_pq_t<1024>(a, st);
   }
+  if (a.rule == 0 && !a.use_pct && a.k_max <= DEC_PQR_STAGE)
+    if (auto f = select_reg_for<true>(a.M, batch)) return f(a, st);
   if (batch) return launch_select_t<512>(a, st);
   return launch_select_t<1024>(a, st);
 }

@@ -90,6 +90,13 @@ def test_decode_sets_match_reference_goldens():
     (8, 4, 160, 2500, 256, 32, 32, 100.0, None, 1.0 / 3.0),
     (9, 2, 300, 3000, 64, 8, 8, 30.0, 0.25, 0.5),         # ties at both cuts
     (10, 1, 512, 36000, 300, 16, 16, 25.0, 0.125, 1.0),   # its global key store
+    # no top-pct cut: the register selection (every key equal to the cap cut kept)
+    (11, 2, 3, 5000, 64, 8, 8, 100.0, 0.25, 0.5),         # ties at the cap cut
+    (12, 2, 300, 3001, 64, 8, 8, 100.0, 0.25, 0.5),       # a batch, ties, rows of odd length
+    (13, 1, 2, 16384, 512, 16, 16, 100.0, None, 0.25),    # the longest batch row in registers
+    (14, 1, 2, 16385, 512, 16, 16, 100.0, None, 0.25),    # past it: a few queries, 6 groups
+    (15, 2, 2, 32768, 2048, 32, 32, 100.0, 0.25, 1.0 / 3.0),   # 8 groups of 1024 threads, ties
+    (16, 1, 2, 32769, 2048, 32, 32, 100.0, None, 1.0 / 3.0),   # one key past it (LDS store)
 ])
 def test_decode_select_matches_oracle_on_crafted_scores(case):
     seed, H, Q, M, km, ng, nl, pctd, quant, ps = case
@@ -100,14 +107,7 @@ def test_decode_select_matches_oracle_on_crafted_scores(case):
     tau = rng.uniform(2.0, 8.0, H).astype(np.float32)
     q_pos0 = M - Q
     say(f"decode select crafted: H={H} Q={Q} M={M} k_max={km} pct={pctd} quant={quant}")
-    plan = _plan_for_scores(s, tau, q_pos0, ps, ng, nl, km, pctd)
-    r = plan.build_sets(torch.from_numpy(s).to(DEV))
-    torch.cuda.synchronize()
-    idx, npk, npq, size = orc.decode_build_sets(s, tau, q_pos0, ps, ng, nl, km, pctd)
-    assert np.array_equal(r["idx"].cpu().numpy(), idx)
-    assert _bits_equal(r["newpos_k"].cpu().numpy(), npk)
-    assert _bits_equal(r["newpos_q"].cpu().numpy(), npq)
-    assert np.array_equal(r["set_size"].cpu().numpy(), size)
+    size = _check_crafted(s, tau, q_pos0, ps, ng, nl, km, pctd)
     print(f"[result] crafted select: set sizes {size.ravel()[:6].tolist()}", flush=True)
 
 
@@ -162,6 +162,33 @@ def test_decode_batched_matches_per_token_loop():
     assert _bits_equal(r["newpos_k"].cpu().numpy(), g["newpos_k"])
     assert _bits_equal(r["newpos_q"].cpu().numpy(), g["newpos_q"])
     check_output(out_f32(r["out"]), g["out"], orc.F32, "batched decode")
+
+
+def _check_crafted(s, tau, q_pos0, ps, ng, nl, km, pctd):
+    """The selection from given scores against the oracle's, bit for bit; returns the set sizes."""
+    plan = _plan_for_scores(s, tau, q_pos0, ps, ng, nl, km, pctd)
+    r = plan.build_sets(torch.from_numpy(s).to(DEV))
+    torch.cuda.synchronize()
+    idx, npk, npq, size = orc.decode_build_sets(s, tau, q_pos0, ps, ng, nl, km, pctd)
+    assert np.array_equal(r["idx"].cpu().numpy(), idx)
+    assert _bits_equal(r["newpos_k"].cpu().numpy(), npk)
+    assert _bits_equal(r["newpos_q"].cpu().numpy(), npq)
+    assert np.array_equal(r["set_size"].cpu().numpy(), size)
+    return size
+
+
+@pytest.mark.parametrize("tau", [0.0, float("inf"), -1.0, 1e-3])
+def test_decode_select_shared_rule_thresholds(tau):
+    """The shared rule without a top-pct cut at thresholds the value bins do not cover (tau = 0, inf:
+    key-space bins), at none (tau < 0: only the forced keys pass) and with a narrow band, on rows
+    with exact ties, against the oracle bit for bit."""
+    rng = np.random.default_rng(21)
+    H, Q, M, km = 2, 3, 4000, 128
+    s = (rng.standard_normal((H, Q, M)) * 2.0).astype(np.float32)
+    s[..., ::7] = np.round(s[..., ::7])
+    say(f"decode select shared rule: tau={tau}")
+    size = _check_crafted(s, np.full(H, tau, np.float32), M - Q, 0.5, 8, 8, km, 100.0)
+    print(f"[result] shared rule tau={tau}: set sizes {size.ravel().tolist()}", flush=True)
 
 
 @pytest.mark.parametrize("case", [
@@ -262,6 +289,7 @@ def test_decode_hybrid_two_geometries():
     ("pq", 2, 2, 70, 20000, 64, torch.bfloat16, 2048, 100.0, False),     # the row in LDS
     ("shared", 2, 2, 96, 900, 64, torch.float16, 128, 30.0, True),       # the general selection
     ("pq", 2, 1, 65, 39000, 64, torch.bfloat16, 1024, 100.0, False),     # the global key store
+    ("pq", 4, 2, 100, 3000, 128, torch.float32, 512, 100.0, False),      # fp32 fragments
 ])
 def test_decode_tiled_scores_match_row_major(case):
     """A batch's scores that only the selection of the same call reads leave the score rows kernel
