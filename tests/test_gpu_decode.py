@@ -290,6 +290,8 @@ def test_decode_hybrid_two_geometries():
     ("shared", 2, 2, 96, 900, 64, torch.float16, 128, 30.0, True),       # the general selection
     ("pq", 2, 1, 65, 39000, 64, torch.bfloat16, 1024, 100.0, False),     # the global key store
     ("pq", 4, 2, 100, 3000, 128, torch.float32, 512, 100.0, False),      # fp32 fragments
+    ("shared", 2, 1, 80, 2000, 64, torch.bfloat16, 256, 100.0, False),   # the shared rule in registers
+    ("stream", 2, 2, 70, 1500, 64, torch.bfloat16, 4096, 100.0, False),  # PQ Stream positions
 ])
 def test_decode_tiled_scores_match_row_major(case):
     """A batch's scores that only the selection of the same call reads leave the score rows kernel
@@ -304,7 +306,9 @@ def test_decode_tiled_scores_match_row_major(case):
     q = qa[0, :, M - Q:, :].contiguous()
     invf = base_inv_freq(D, 10000.0)
     tau = torch.full((H,), 4.0)
-    kw = dict(inv_freq_c=invf, pos_scale_c=1.0, rope_scale_c=1.0, rule="pq") if rule == "pq" else {}
+    kw = {"pq": dict(inv_freq_c=invf, pos_scale_c=1.0, rope_scale_c=1.0, rule="pq"),
+          "stream": dict(inv_freq_c=invf, pos_scale_c=1.0, rope_scale_c=1.0, rule="stream", block_n=32),
+          "shared": {}}[rule]
     runs = [native.decode_attention(q, k, v, tau, invf, M - Q, 0.5, 1.0, None, 16, 16, km, pctd, causal,
                                     want_scores=ws, **kw) for ws in (False, True)]
     torch.cuda.synchronize()
