@@ -1004,8 +1004,10 @@ __device__ __forceinline__ float wave_incl_max_f32(float x) {
   return x;
 }
 
+// 512-thread instances at 64 VGPRs (eight waves per SIMD, four rows per CU; the 8-group
+// instance spills a few registers and still measured 6.91 -> 6.67 ms at config 3 as written)
 template <int NT, int G, bool SH>
-__global__ __launch_bounds__(NT, NT == 512 ? 6 : 4) void decode_select_pq_reg_kernel(DecodeArgs a) {
+__global__ __launch_bounds__(NT, NT == 512 ? 8 : 4) void decode_select_pq_reg_kernel(DecodeArgs a) {
 #pragma clang fp contract(off)
   constexpr int NW = NT / 64;
   constexpr int NB = DEC_PQR_BINS;
