@@ -312,11 +312,11 @@ def bench_perquery(args, cfg, q, k, v, q_cpu, k_cpu, v_cpu, invf, ps, rs, tau):
                            "the fp32 score rows of every (query, key) pair are written once, in 64-row tiles, "
                            "and read by the selection"),
         "select": hbm_roof("decode_select_pq_reg_kernel", selbytes, stage_ms["select"],
-                           "one pass over each score row held in registers; the vector ALU (72% busy) "
+                           "one pass over each score row held in registers; the vector ALU (68% busy) "
                            "bounds it, not HBM"),
         "attend": hbm_roof("decode_attend_grouped_kernel", abytes, stage_ms["attend"],
                            "each query gathers its own K / V rows, served mostly from L2; the counters put the "
-                           "vector memory data path at 92% busy, which bounds it, and the vector ALU at 80%"),
+                           "vector memory data path at 92% busy, which bounds it, and the vector ALU at 79%"),
     }
     dominant = max(("scores", "select", "attend"), key=lambda n: stage_ms[n])
     print(f"[bench] {ms_per_step:.3f} ms/step; stages {stage_ms}", file=sys.stderr, flush=True)
