@@ -243,11 +243,15 @@ __global__ __launch_bounds__(256) void rope_frag_kernel(const void* __restrict__
 }
 
 // per head: the maxima of (||hi||, ||lo||) over its rows_pad rows (rows_pad even); 1024 threads
-// read two rows per 16-byte load, several loads in flight per thread
-__global__ __launch_bounds__(1024) void norm_max_kernel(const float2* __restrict__ norms, int rows_pad,
-                                                        float2* __restrict__ out) {
+// read two rows per 16-byte load, several loads in flight per thread.  blockIdx.y picks one of two
+// (norms, out) pairs, so the fp6 rounding norms take the same launch.
+__global__ __launch_bounds__(1024) void norm_max_kernel(const float2* __restrict__ norms0, float2* __restrict__ out0,
+                                                        const float2* __restrict__ norms1, float2* __restrict__ out1,
+                                                        int rows_pad) {
   __shared__ float red[2][16];
   const int head = blockIdx.x, tid = threadIdx.x;
+  const float2* norms = blockIdx.y == 0 ? norms0 : norms1;
+  float2* out = blockIdx.y == 0 ? out0 : out1;
   const float4* p = (const float4*)(norms + (int64_t)head * rows_pad);
   const int n4 = rows_pad / 2;
   float mh = 0.0f, ml = 0.0f;
@@ -1325,13 +1329,10 @@ static hipError_t launch_rope_frag_t(const void* x, int64_t hs, int64_t ts, int 
                        rows_pad, pos_base, pos_scale, rope_scale, inv_freq, frag, norms, planes6, scales6, dn6);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(norm_max_kernel, dim3(heads), dim3(1024), 0, st, (const float2*)norms, rows_pad,
-                     frag_norm_max(frag, heads, rows_pad, D));
-  if (want6) {
-    if ((e = hipGetLastError()) != hipSuccess) return e;
-    hipLaunchKernelGGL(norm_max_kernel, dim3(heads), dim3(1024), 0, st, (const float2*)dn6, rows_pad,
-                       frag6_dnorm_max(frag, heads, rows_pad, D));
-  }
+  // the row norms' maxima, and with the fp6 planes their rounding norms' in the same launch
+  hipLaunchKernelGGL(norm_max_kernel, dim3(heads, want6 ? 2 : 1), dim3(1024), 0, st, (const float2*)norms,
+                     frag_norm_max(frag, heads, rows_pad, D), (const float2*)dn6,
+                     frag6_dnorm_max(frag, heads, rows_pad, D), rows_pad);
   return hipGetLastError();
 }
 
