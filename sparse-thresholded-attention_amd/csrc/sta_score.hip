@@ -685,12 +685,16 @@ void score_kernel(ScoreArgs a) {
   constexpr int FMAX = 1536;                     // candidate (row, key) pairs per wave
   constexpr int LOADS_H = LOADS / 2;             // 1 KB copies per wave per chunk, hi halves only
   static_assert(LOADS_H * NW * 2 * 64 == CHUNK_UNITS, "hi-half copies");
+  // wave-uniform chunk bases in SGPRs and one lane offset: per-lane 64-bit addresses would hold
+  // VGPRs through the sweep
+  const uint32_t loff_h = (uint32_t)lane * 16u;
+  const int wave_s = __builtin_amdgcn_readfirstlane(wave);
   auto issue_hi = [&](int c, u32x4* dst) {
-    const u32x4* src = kbase + (int64_t)c * CHUNK_UNITS + lane;
+    const u32x4* src = kbase + (int64_t)c * CHUNK_UNITS;
 #pragma unroll
     for (int e = 0; e < LOADS_H; ++e) {
-      const int b = e * NW + wave;             // (32-key block, k step) b: its hi units, packed
-      copy16_to_lds(src + 128 * b, lds_addr(dst + 64 * b));
+      const int b = e * NW + wave_s;           // (32-key block, k step) b: its hi units, packed
+      copy16_to_lds_s(src + 128 * b, loff_h, lds_addr(dst + 64 * b));
     }
   };
   auto ldbh = [&](const u32x4* buf, int sb, int s) { return buf[(sb * S + s) * 64 + lane]; };
@@ -977,13 +981,15 @@ void score_kernel(ScoreArgs a) {
     amb |= total > FMAX;
     if (__syncthreads_or(amb)) return true;
 
-    // ---- exact dots of the candidates: pair f is evaluated by lanes f % 32 and f % 32 + 32,
-    // each over half of the dims (the fragment layout's lane halves), 32 pairs per round ----
+    // ---- exact scores of the candidates on the matrix cores, 32 list entries per round: entry
+    // f's key is B column f (lanes f and f + 32 load its two dims halves: the fragment layout),
+    // the wave's rows are the A operands (qhi held since the sweep, qlo loaded here in the same
+    // layout), and the four products hi.hi + hi.lo + lo.hi + lo.lo over a 32-row block give each
+    // (row, key) score of the round in fp32 (every product exact, the sums rounded within the
+    // 2^-14 allowance of E); entry f reads its own (row, key) score from the result block.  The
+    // next round's key fragments load while a round's scores are read out. ----
     if (active) {
       const int g = lane >> 5;
-      // Q operands come from registers: qhi is held since the sweep, qlo is loaded once here in
-      // the same layout (lane l holds row l % 32 of each row block, dims half l / 32), and a pair's
-      // row is fetched from its owner lane with a bpermute; only the keys are gathered from memory.
       u32x4 qlo1[RB][S];
 #pragma unroll
       for (int rb = 0; rb < RB; ++rb) {
@@ -994,62 +1000,54 @@ void score_kernel(ScoreArgs a) {
           qlo1[rb][s] = ok ? a.qfrag[u + 64] : u32x4{0, 0, 0, 0};
         }
       }
-      auto bperm = [](int addr, const u32x4& x) {
-        u32x4 r;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) r[e] = (uint32_t)__builtin_amdgcn_ds_bpermute(addr, (int)x[e]);
-        return r;
-      };
-      for (int it = 0; it * 32 < total; ++it) {
-        const int f = it * 32 + (lane & 31);
-        const bool valid = f < total;
-        const int row = valid ? frow[f] : 0;
-        const int key = valid ? fkey[f] : 0;
+      u32x4 kh[S], kl[S];
+      auto load_keys = [&](int key) {
         const u32x4* kp = kbase + (int64_t)(key >> 5) * S * 128 + (key & 31) + 32 * g;
-        u32x4 kh[S], kl[S];
 #pragma unroll
         for (int s = 0; s < S; ++s) {
           kh[s] = kp[s * 128];
           kl[s] = kp[s * 128 + 64];
         }
-        const int src = ((row & 31) + (lane & 32)) << 2;   // the row's owner lane, same dims half
+      };
+      auto scores = [&](int rb) {
+        floatx16 acc = {};
+#pragma unroll
+        for (int s = 0; s < S; ++s) {
+          acc = mfma32(qhi[rb][s], kh[s], acc);
+          acc = mfma32(qhi[rb][s], kl[s], acc);
+          acc = mfma32(qlo1[rb][s], kh[s], acc);
+          acc = mfma32(qlo1[rb][s], kl[s], acc);
+        }
+        return acc;
+      };
+      int f = col;
+      bool valid = f < total;
+      int row = valid ? frow[f] : 0;
+      load_keys(valid ? fkey[f] : 0);          // key 0 stands in for a padding entry
+      for (int it = 0; it * 32 < total; ++it) {
         const int rbr = row >> 5;
-        // rows are listed in order, so a round's pairs mostly share one row block
+        // rows are listed in order, so a round's entries mostly share one row block
         const bool in0 = __ballot(valid && rbr == 0) != 0, in1 = __ballot(valid && rbr == 1) != 0;
-        float acc = 0.0f;
-        auto dot = [&](auto modec) {
-          constexpr int MODE_RB = decltype(modec)::value;   // 0 / 1: that row block; 2: either
+        floatx16 acc0 = {}, acc1 = {};
+        if (in0) acc0 = scores(0);
+        if (in1) acc1 = scores(RB - 1);
+        const int fn = f + 32;
+        const bool validn = fn < total;
+        const int rown = validn ? frow[fn] : 0;
+        if ((it + 1) * 32 < total) load_keys(validn ? fkey[fn] : 0);
+        // (row r, column col) of a 32x32 block: lane col + 32 ((r >> 2) & 1), element (r >> 3) * 4 + (r & 3)
+        const int rr = row & 31;
+        const int e0 = (rr >> 3) * 4 + (rr & 3);
+        float v = 0.0f;
 #pragma unroll
-          for (int s = 0; s < S; ++s) {
-            u32x4 qh, ql;
-            if constexpr (MODE_RB < 2) {
-              qh = bperm(src, qhi[MODE_RB][s]);
-              ql = bperm(src, qlo1[MODE_RB][s]);
-            } else {
-              const u32x4 h0 = bperm(src, qhi[0][s]), h1 = bperm(src, qhi[RB - 1][s]);
-              const u32x4 l0 = bperm(src, qlo1[0][s]), l1 = bperm(src, qlo1[RB - 1][s]);
-              qh = rbr == 0 ? h0 : h1;
-              ql = rbr == 0 ? l0 : l1;
-            }
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              const float x0 = __uint_as_float(qh[e] << 16) + __uint_as_float(ql[e] << 16);
-              const float x1 = __uint_as_float(qh[e] & 0xffff0000u) + __uint_as_float(ql[e] & 0xffff0000u);
-              const float y0 = __uint_as_float(kh[s][e] << 16) + __uint_as_float(kl[s][e] << 16);
-              const float y1 = __uint_as_float(kh[s][e] & 0xffff0000u) + __uint_as_float(kl[s][e] & 0xffff0000u);
-              acc = fmaf(x0, y0, acc);
-              acc = fmaf(x1, y1, acc);
-            }
-          }
-        };
-        if (!in1) dot(std::integral_constant<int, 0>{});
-        else if (!in0) dot(std::integral_constant<int, RB - 1>{});
-        else dot(std::integral_constant<int, 2>{});
-        const float tot = acc + __shfl_xor(acc, 32, 64);
+        for (int e = 0; e < 16; ++e) v = e == e0 ? (rbr == 0 ? acc0[e] : acc1[e]) : v;
         // order-preserving key of an fp32 value (every key of a real value is nonzero)
-        const uint32_t tb = __float_as_uint(tot + 0.0f);
+        const uint32_t tb = __float_as_uint(v + 0.0f);
         const uint32_t okey = (tb & 0x80000000u) ? ~tb : (tb | 0x80000000u);
-        if (valid && g == 0) atomicMax(&rowbest[row], okey);
+        if (valid && ((rr >> 2) & 1) == g) atomicMax(&rowbest[row], okey);
+        f = fn;
+        valid = validn;
+        row = rown;
       }
     }
     __syncthreads();
