@@ -52,7 +52,7 @@ namespace {
 struct Layout {
   int nt, q_rows_pad, k_rows_pad;
   int64_t votes_stride;
-  size_t qfrag_off, kfrag_off, votes_off, wv_off, total;
+  size_t qfrag_off, kfrag_off, ktrig_off, votes_off, wv_off, total;
 };
 
 Layout layout_of(const sta_shared_args* a) {
@@ -69,6 +69,8 @@ Layout layout_of(const sta_shared_args* a) {
   off = align256(off + frag_region_bytes(a->H, L.q_rows_pad, a->D, with6));
   L.kfrag_off = off;
   off = align256(off + frag_region_bytes(a->Hkv, L.k_rows_pad, a->D, with6));
+  L.ktrig_off = off;   // the K rotation's (cos, sin) per key row, for the screened pass 1
+  off = align256(off + (size_t)L.k_rows_pad * (a->D / 2) * sizeof(float2));
   L.votes_off = off;
   off = align256(off + (size_t)a->H * L.nt * L.votes_stride);
   L.wv_off = off;   // weighted votes (H, nt, votes_stride) fp32, for a weighted select_score only
@@ -179,7 +181,8 @@ int run_kernel_a(const sta_shared_args* a, const Layout& L, hipStream_t st) {
                                   a->inv_freq_a, qfrag, st, want6);
   if (e != hipSuccess) return hip_fail(e, "rope pre-kernel (q)");
   e = launch_rope_frag(a->dtype, a->D, a->k, a->k_head_stride, a->k_tok_stride, a->Hkv, a->N,
-                       L.k_rows_pad, 0, a->pos_scale_a, a->rope_scale_a, a->inv_freq_a, kfrag, st, want6);
+                       L.k_rows_pad, 0, a->pos_scale_a, a->rope_scale_a, a->inv_freq_a, kfrag, st, want6,
+                       (float2*)(ws + L.ktrig_off));
   if (e != hipSuccess) return hip_fail(e, "rope pre-kernel (k)");
   if ((rc = mark(a, 1, st)) != STA_OK) return rc;
   ScoreArgs sa{};
@@ -187,6 +190,11 @@ int run_kernel_a(const sta_shared_args* a, const Layout& L, hipStream_t st) {
   sa.kfrag = kfrag;
   sa.qnorm = frag_norms(qfrag, a->H, L.q_rows_pad, a->D);
   sa.knorm_max = frag_norm_max(kfrag, a->Hkv, L.k_rows_pad, a->D);
+  sa.ktrig = (const float2*)(ws + L.ktrig_off);
+  sa.kraw = a->k;
+  sa.kraw_hs = a->k_head_stride;
+  sa.kraw_ts = a->k_tok_stride;
+  sa.kraw_dt = a->dtype;
   sa.H = a->H;
   sa.Hkv = a->Hkv;
   sa.N = a->N;

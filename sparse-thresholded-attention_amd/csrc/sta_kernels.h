@@ -88,6 +88,13 @@ struct ScoreArgs {
   const uint64_t* k6;
   const uint32_t* k6sc;
   const float2* k6dmax;   // (Hkv,)
+  // The screened pass 1 scores its candidate keys from the raw K rows and the K rotation's
+  // (cos, sin) table (key-major: a few cache lines per key) when ktrig is set, else from the K
+  // fragments.  kraw: the K input as the rope pre-kernel read it (dtype kraw_dt, strides in elements).
+  const float2* ktrig;    // (k_rows_pad, D/2) scaled (cos, sin) of every key row, or null
+  const void* kraw;
+  int64_t kraw_hs, kraw_ts;
+  int kraw_dt;
 };
 
 struct SelectArgs {
@@ -367,11 +374,12 @@ __device__ inline bool fast6_serves(const ScoreArgs& a, int h, int g, int D, int
   return sg <= FAST6_SIGMA_LIMIT;
 }
 
-// want6: also write the fp6 correction operands of the fragment region
+// want6: also write the fp6 correction operands of the fragment region; trig: also write each
+// row's scaled (cos, sin) pairs, (rows_pad, D/2) float2 (ScoreArgs::ktrig)
 hipError_t launch_rope_frag(int dtype, int D, const void* x, int64_t head_stride, int64_t tok_stride,
                             int heads, int N, int rows_pad, int pos_base, float pos_scale,
                             float rope_scale, const float* inv_freq, u32x4* frag, hipStream_t st,
-                            bool want6 = false);
+                            bool want6 = false, float2* trig = nullptr);
 // the fp6 pass-2 kernel (plain votes); the launcher of the score passes calls it
 hipError_t launch_score6(int D, int tile, const ScoreArgs& a, hipStream_t st);
 hipError_t launch_score(int D, int tile, const ScoreArgs& a, hipStream_t st);

@@ -160,7 +160,7 @@ __global__ __launch_bounds__(256) void rope_frag_kernel(const void* __restrict__
                                                         const float* __restrict__ inv_freq,
                                                         u32x4* __restrict__ frag, float2* __restrict__ norms,
                                                         uint64_t* __restrict__ planes6, uint32_t* __restrict__ scales6,
-                                                        float2* __restrict__ dnorms6) {
+                                                        float2* __restrict__ dnorms6, float2* __restrict__ trig) {
 #pragma clang fp contract(off)
   constexpr int C2 = D / 16;                 // threads per row
   const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
@@ -182,6 +182,13 @@ __global__ __launch_bounds__(256) void rope_frag_kernel(const void* __restrict__
       sincosf(ang, &sn[e], &cs[e]);
       cs[e] = cs[e] * rope_scale;
       sn[e] = sn[e] * rope_scale;
+    }
+    // the row's (cos, sin) table, written once (first head group): the screened pass 1 rebuilds
+    // a candidate key's fragments from its raw row and this table, 2 + 4 cache lines per key
+    if (trig && blockIdx.y == 0) {
+      float4* t = (float4*)(trig + (int64_t)row * (D / 2) + i0);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) t[e] = make_float4(cs[2 * e], sn[2 * e], cs[2 * e + 1], sn[2 * e + 1]);
     }
   }
   const int rb = row >> 5, lr = row & 31, g = c & 1;
@@ -1001,12 +1008,47 @@ void score_kernel(ScoreArgs a) {
         }
       }
       u32x4 kh[S], kl[S];
+      // a key's hi / lo operands of k steps s (dims s * 16 + 8 g ..) for this lane's half g: from
+      // its raw row and (cos, sin) table row with the rope pre-kernel's own arithmetic (the same
+      // fp32 rotation and split, so the same bits as its fragments), or from the fragments
+      auto load8_rt = [&](int64_t i, float* out) {
+        if (a.kraw_dt == DT_BF16) load8<DT_BF16>(a.kraw, i, out);
+        else if (a.kraw_dt == DT_F16) load8<DT_F16>(a.kraw, i, out);
+        else load8<DT_F32>(a.kraw, i, out);
+      };
       auto load_keys = [&](int key) {
-        const u32x4* kp = kbase + (int64_t)(key >> 5) * S * 128 + (key & 31) + 32 * g;
+        if (a.ktrig) {
+          const float4* tp = (const float4*)(a.ktrig + (int64_t)key * (D / 2));
+          const int64_t rbase = (int64_t)kvh * a.kraw_hs + (int64_t)key * a.kraw_ts;
 #pragma unroll
-        for (int s = 0; s < S; ++s) {
-          kh[s] = kp[s * 128];
-          kl[s] = kp[s * 128 + 64];
+          for (int s = 0; s < S / 2; ++s) {
+            const int d0 = s * 16 + g * 8;       // dims d0.. in step s, D/2 + d0.. in step s + S/2
+            float x1[8], x2[8], o1[8], o2[8];
+            load8_rt(rbase + d0, x1);
+            load8_rt(rbase + D / 2 + d0, x2);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const float4 t = tp[d0 / 2 + e];   // (cos, sin) of dims d0 + 2e and d0 + 2e + 1
+              const float c2[2] = {t.x, t.z}, s2[2] = {t.y, t.w};
+#pragma unroll
+              for (int j = 0; j < 2; ++j) {
+                const float xa = x1[2 * e + j], xb = x2[2 * e + j];
+                const float p1 = xa * c2[j], q1 = xb * s2[j];
+                o1[2 * e + j] = p1 - q1;
+                const float p2 = xb * c2[j], q2 = xa * s2[j];
+                o2[2 * e + j] = p2 + q2;
+              }
+            }
+            split_bf16x8(o1, kh[s], kl[s]);
+            split_bf16x8(o2, kh[s + S / 2], kl[s + S / 2]);
+          }
+        } else {
+          const u32x4* kp = kbase + (int64_t)(key >> 5) * S * 128 + (key & 31) + 32 * g;
+#pragma unroll
+          for (int s = 0; s < S; ++s) {
+            kh[s] = kp[s * 128];
+            kl[s] = kp[s * 128 + 64];
+          }
         }
       };
       auto scores = [&](int rb) {
@@ -1311,7 +1353,7 @@ void score_kernel(ScoreArgs a) {
 template <int DT, int D>
 static hipError_t launch_rope_frag_t(const void* x, int64_t hs, int64_t ts, int heads, int N, int rows_pad,
                                      int pos_base, float pos_scale, float rope_scale, const float* inv_freq,
-                                     u32x4* frag, hipStream_t st, bool want6) {
+                                     u32x4* frag, hipStream_t st, bool want6, float2* trig) {
   const int64_t total = (int64_t)rows_pad * (D / 16);
   const int64_t blocks = (total + 255) / 256;
   float2* norms = frag_norms(frag, heads, rows_pad, D);
@@ -1321,10 +1363,10 @@ static hipError_t launch_rope_frag_t(const void* x, int64_t hs, int64_t ts, int 
   const dim3 grid((unsigned)blocks, (unsigned)((heads + ROPE_HG - 1) / ROPE_HG));
   if (want6)
     hipLaunchKernelGGL((rope_frag_kernel<DT, D, true>), grid, dim3(256), 0, st, x, hs, ts, heads, N,
-                       rows_pad, pos_base, pos_scale, rope_scale, inv_freq, frag, norms, planes6, scales6, dn6);
+                       rows_pad, pos_base, pos_scale, rope_scale, inv_freq, frag, norms, planes6, scales6, dn6, trig);
   else
     hipLaunchKernelGGL((rope_frag_kernel<DT, D, false>), grid, dim3(256), 0, st, x, hs, ts, heads, N,
-                       rows_pad, pos_base, pos_scale, rope_scale, inv_freq, frag, norms, planes6, scales6, dn6);
+                       rows_pad, pos_base, pos_scale, rope_scale, inv_freq, frag, norms, planes6, scales6, dn6, trig);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   // the row norms' maxima, and with the fp6 planes their rounding norms' in the same launch
@@ -1336,9 +1378,9 @@ static hipError_t launch_rope_frag_t(const void* x, int64_t hs, int64_t ts, int 
 
 hipError_t launch_rope_frag(int dtype, int D, const void* x, int64_t hs, int64_t ts, int heads, int N,
                             int rows_pad, int pos_base, float pos_scale, float rope_scale,
-                            const float* inv_freq, u32x4* frag, hipStream_t st, bool want6) {
+                            const float* inv_freq, u32x4* frag, hipStream_t st, bool want6, float2* trig) {
 #define STA_RF(DT_, D_) \
-  if (dtype == DT_ && D == D_) return launch_rope_frag_t<DT_, D_>(x, hs, ts, heads, N, rows_pad, pos_base, pos_scale, rope_scale, inv_freq, frag, st, want6);
+  if (dtype == DT_ && D == D_) return launch_rope_frag_t<DT_, D_>(x, hs, ts, heads, N, rows_pad, pos_base, pos_scale, rope_scale, inv_freq, frag, st, want6, trig);
   STA_RF(DT_F32, 64) STA_RF(DT_F32, 128) STA_RF(DT_BF16, 64) STA_RF(DT_BF16, 128)
   STA_RF(DT_F16, 64) STA_RF(DT_F16, 128)
 #undef STA_RF
