@@ -18,7 +18,7 @@ namespace {
 struct PqLayout {
   int nt, q_rows_pad, k_rows_pad;
   int64_t stride;
-  size_t qfrag_off, kfrag_off, bits_off, wv_off, total;
+  size_t qfrag_off, kfrag_off, ktrig_off, bits_off, wv_off, total;
 };
 
 PqLayout pq_layout_of(const sta_pq_args* a) {
@@ -33,6 +33,8 @@ PqLayout pq_layout_of(const sta_pq_args* a) {
   off = align256(off + frag_region_bytes(a->H, L.q_rows_pad, a->D));
   L.kfrag_off = off;
   off = align256(off + frag_region_bytes(a->Hkv, L.k_rows_pad, a->D));
+  L.ktrig_off = off;   // the K rotation's (cos, sin) per key row, for the screened pass 1
+  off = align256(off + (size_t)L.k_rows_pad * (a->D / 2) * sizeof(float2));
   L.bits_off = off;
   off = align256(off + (size_t)a->H * L.nt * L.stride * 4);
   L.wv_off = off;
@@ -95,7 +97,8 @@ int pq_run_kernel_a(const sta_pq_args* a, const PqLayout& L, hipStream_t st) {
                                   a->inv_freq_a, qfrag, st);
   if (e != hipSuccess) return hip_fail(e, "rope pre-kernel (q)");
   e = launch_rope_frag(a->dtype, a->D, a->k, a->k_head_stride, a->k_tok_stride, a->Hkv, a->N,
-                       L.k_rows_pad, 0, a->pos_scale_a, a->rope_scale_a, a->inv_freq_a, kfrag, st);
+                       L.k_rows_pad, 0, a->pos_scale_a, a->rope_scale_a, a->inv_freq_a, kfrag, st, false,
+                       (float2*)(ws + L.ktrig_off));
   if (e != hipSuccess) return hip_fail(e, "rope pre-kernel (k)");
   if ((rc = mark_event(a->stage_events, 1, st)) != STA_OK) return rc;
   ScoreArgs sa{};
@@ -103,6 +106,11 @@ int pq_run_kernel_a(const sta_pq_args* a, const PqLayout& L, hipStream_t st) {
   sa.kfrag = kfrag;
   sa.qnorm = frag_norms(qfrag, a->H, L.q_rows_pad, a->D);
   sa.knorm_max = frag_norm_max(kfrag, a->Hkv, L.k_rows_pad, a->D);
+  sa.ktrig = (const float2*)(ws + L.ktrig_off);
+  sa.kraw = a->k;
+  sa.kraw_hs = a->k_head_stride;
+  sa.kraw_ts = a->k_tok_stride;
+  sa.kraw_dt = a->dtype;
   sa.H = a->H;
   sa.Hkv = a->Hkv;
   sa.N = a->N;

@@ -23,7 +23,7 @@ struct StreamLayout {
   int nt, q_rows_pad, k_rows_pad, Npad, planes;
   bool fused;
   int64_t stride;
-  size_t qfrag_off, kfrag_off, bits_off, xthr_off, ktil_off, total;
+  size_t qfrag_off, kfrag_off, ktrig_off, bits_off, xthr_off, ktil_off, total;
 };
 
 StreamLayout stream_layout_of(const sta_pqstream_args* a) {
@@ -40,6 +40,8 @@ StreamLayout stream_layout_of(const sta_pqstream_args* a) {
   off = align256(off + frag_region_bytes(a->H, L.q_rows_pad, a->D));
   L.kfrag_off = off;
   off = align256(off + frag_region_bytes(a->Hkv, L.k_rows_pad, a->D));
+  L.ktrig_off = off;   // the K rotation's (cos, sin) per key row, for the screened pass 1
+  off = align256(off + (size_t)L.k_rows_pad * (a->D / 2) * sizeof(float2));
   // the keep-bit buffer holds H * nt * N words: the fused sweep replaces it where asked to, or
   // automatically once it would pass kStreamBitsAuto bytes
   const size_t bits_bytes = (size_t)a->H * L.nt * L.stride * 4;
@@ -123,7 +125,8 @@ int sta_pqstream_attention(const sta_pqstream_args* a, void* stream) {
                                   L.q_rows_pad, 0, a->pos_scale_a, a->rope_scale_a, a->inv_freq_a, qfrag, st);
   if (e != hipSuccess) return hip_fail(e, "rope pre-kernel (q)");
   e = launch_rope_frag(a->dtype, a->D, a->k, a->k_head_stride, a->k_tok_stride, a->Hkv, a->N, L.k_rows_pad, 0,
-                       a->pos_scale_a, a->rope_scale_a, a->inv_freq_a, kfrag, st);
+                       a->pos_scale_a, a->rope_scale_a, a->inv_freq_a, kfrag, st, false,
+                       (float2*)(ws + L.ktrig_off));
   if (e != hipSuccess) return hip_fail(e, "rope pre-kernel (k)");
 
   // pass 1 (exact row max) + keep bits s >= m - tau per (query, key): pqstream_kernel.py:229-244, 285
@@ -133,6 +136,11 @@ int sta_pqstream_attention(const sta_pqstream_args* a, void* stream) {
   sa.kfrag = kfrag;
   sa.qnorm = frag_norms(qfrag, a->H, L.q_rows_pad, a->D);
   sa.knorm_max = frag_norm_max(kfrag, a->Hkv, L.k_rows_pad, a->D);
+  sa.ktrig = (const float2*)(ws + L.ktrig_off);
+  sa.kraw = a->k;
+  sa.kraw_hs = a->k_head_stride;
+  sa.kraw_ts = a->k_tok_stride;
+  sa.kraw_dt = a->dtype;
   sa.H = a->H;
   sa.Hkv = a->Hkv;
   sa.N = a->N;

@@ -1394,6 +1394,12 @@ static int exact_pass1_forced() {
   const char* e = getenv("STA_EXACT_PASS1");
   return e && e[0] == '1' ? 1 : 0;
 }
+// STA_SCREEN_GATHER=1: the screen gathers its candidate keys from the K fragments even where the
+// (cos, sin) table is there, for comparisons
+static int screen_gather_forced() {
+  const char* e = getenv("STA_SCREEN_GATHER");
+  return e && e[0] == '1' ? 1 : 0;
+}
 static int exact_pass2_forced() {
   const char* e = getenv("STA_EXACT_PASS2");
   return e && e[0] == '1' ? 1 : 0;
@@ -1409,6 +1415,7 @@ static hipError_t launch_score_t(const ScoreArgs& a0, hipStream_t st) {
   while ((1 << ib) < a.k_rows_pad / 32) ++ib;
   a.ib = (ib <= 13 && a.qnorm && a.knorm_max) ? ib : 0;
   a.exact_pass1 = exact_pass1_forced();
+  if (screen_gather_forced()) a.ktrig = nullptr;
   const int rows = a.nt * T;
   constexpr int WS = score_waves<false, 0, 1>(), W2 = score_waves<RC, PQ, 0>();
   const int ng_s = (rows + 32 * RB * WS - 1) / (32 * RB * WS);

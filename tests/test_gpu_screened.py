@@ -173,6 +173,20 @@ def test_negative_tau_keeps_no_key():
         assert int(votes.abs().sum()) == 0 and int(rc.abs().sum()) == 0, f"exact_pass1={exact}"
 
 
+def _gathered(fn):
+    """fn() with STA_SCREEN_GATHER=1: the screen takes its candidate keys from the K fragments."""
+    old = os.environ.pop("STA_SCREEN_GATHER", None)
+    os.environ["STA_SCREEN_GATHER"] = "1"
+    try:
+        r = fn()
+        torch.cuda.synchronize()
+    finally:
+        os.environ.pop("STA_SCREEN_GATHER", None)
+        if old is not None:
+            os.environ["STA_SCREEN_GATHER"] = old
+    return r
+
+
 @pytest.mark.parametrize("case", [
     # (H, Hkv, N, D, dtype, q_pos_base, pos_scale)
     (2, 1, 3000, 128, torch.bfloat16, 0, 1.0 / 3.0),
@@ -180,10 +194,10 @@ def test_negative_tau_keeps_no_key():
     (2, 2, 1000, 64, torch.float32, 0, 1.0),
 ])
 def test_screen_candidates_rebuilt_from_table_match_fragment_gathers(case):
-    """The shared path's screen scores its candidate keys from the raw K rows and the K rope's
-    (cos, sin) table; the per-query path's screen (same kernel instance, no table) gathers the
-    same keys from the K fragments.  The rebuild repeats the rope pre-kernel's fp32 rotation and
-    split, so both feed the matrix cores the same bits and the row maxima agree bit for bit."""
+    """The screen scores its candidate keys from the raw K rows and the K rope's (cos, sin) table;
+    STA_SCREEN_GATHER=1 makes the same kernel gather those keys from the K fragments instead.  The
+    rebuild repeats the rope pre-kernel's fp32 rotation and split, so both feed the matrix cores
+    the same bits and the row maxima agree bit for bit, on the shared path and the per-query one."""
     import _sta_native as native
     from synthetic import base_inv_freq, planted_inputs
     H, Hkv, N, D, dt, qpb, ps = case
@@ -192,9 +206,12 @@ def test_screen_candidates_rebuilt_from_table_match_fragment_gathers(case):
     invf = base_inv_freq(D, 10000.0).to(DEV)
     tau = torch.full((H,), 4.0)
     sm = 1.0 / math.sqrt(D)
-    _, _, rm_shared = native.select_vote(q, k, tau, invf, ps, 1.0, sm, 32, qpb)
-    rm_pq = native.pq_select_bits(q, k, tau, invf, ps, 1.0, sm, 32, qpb)["row_max"]
-    torch.cuda.synchronize()
-    nd = int((rm_shared != rm_pq).sum())
-    print(f"[result] row maxima differing: {nd} of {rm_shared.numel()}", flush=True)
-    assert nd == 0, f"{nd} row maxima differ between the table rebuild and the fragment gathers"
+    shared = lambda: native.select_vote(q, k, tau, invf, ps, 1.0, sm, 32, qpb)[2]
+    pq = lambda: native.pq_select_bits(q, k, tau, invf, ps, 1.0, sm, 32, qpb)["row_max"]
+    for name, fn in (("shared", shared), ("per-query", pq)):
+        rm_table = fn()
+        torch.cuda.synchronize()
+        rm_gather = _gathered(fn)
+        nd = int((rm_table != rm_gather).sum())
+        print(f"[result] {name}: row maxima differing {nd} of {rm_table.numel()}", flush=True)
+        assert nd == 0, f"{name}: {nd} row maxima differ between the table rebuild and the gathers"
