@@ -56,7 +56,8 @@ def test_workspace_size_matches_layout():
     q = 32 * 12288 * 128 * 4 + 32 * 12288 * 8 + 32 * 8 + screen + fp6
     k = 32 * 12288 * 128 * 4 + 32 * 12288 * 8 + 32 * 8 + screen + fp6
     votes = 32 * nt * 12288             # byte votes, one row per tile
-    assert n >= q + k + votes and n < q + k + votes + 4096
+    trig = 12288 * (128 // 2) * 8       # the K rotation's (cos, sin) per key row (float2 per pair)
+    assert n >= q + k + trig + votes and n < q + k + trig + votes + 4096
 
 
 @pytest.mark.parametrize("field,value,code", [
@@ -186,6 +187,7 @@ def test_pqstream_workspace_size_matches_layout():
     N, H, D = 16384, 32, 128
     frags = 2 * (H * N * D * 4 + H * N * 8 + H * 8 + H * N * 4 + H * (N // 256 + 1) * 4)   # q/k fragments
     need = frags + H * (N // 32) * N * 4 + H * N * D * 2   # + keep bits, K~
+    need += N * (D // 2) * 8                               # + the K rotation's (cos, sin) table
     assert need <= n < need + 8192
 
 
