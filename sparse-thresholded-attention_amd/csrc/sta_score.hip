@@ -997,16 +997,15 @@ void score_kernel(ScoreArgs a) {
     // next round's key fragments load while a round's scores are read out. ----
     if (active) {
       const int g = lane >> 5;
-      u32x4 qlo1[RB][S];
-#pragma unroll
-      for (int rb = 0; rb < RB; ++rb) {
-        const bool ok = wrow0 + 32 * rb < rows_total;
+      // the rows' lo fragments, loaded per round for the row block it needs (from the L2: the
+      // wave reads the same 16 KB every round) rather than held through the phase
+      auto load_qlo = [&](int rb, u32x4* ql) {
 #pragma unroll
         for (int s = 0; s < S; ++s) {
           const int64_t u = (((int64_t)h * (a.q_rows_pad >> 5) + wrow0 / 32 + rb) * S + s) * 128 + lane;
-          qlo1[rb][s] = ok ? a.qfrag[u + 64] : u32x4{0, 0, 0, 0};
+          ql[s] = a.qfrag[u + 64];
         }
-      }
+      };
       u32x4 kh[S], kl[S];
       // a key's hi / lo operands of k steps s (dims s * 16 + 8 g ..) for this lane's half g: from
       // its raw row and (cos, sin) table row with the rope pre-kernel's own arithmetic (the same
@@ -1052,13 +1051,15 @@ void score_kernel(ScoreArgs a) {
         }
       };
       auto scores = [&](int rb) {
+        u32x4 ql[S];
+        load_qlo(rb, ql);
         floatx16 acc = {};
 #pragma unroll
         for (int s = 0; s < S; ++s) {
           acc = mfma32(qhi[rb][s], kh[s], acc);
           acc = mfma32(qhi[rb][s], kl[s], acc);
-          acc = mfma32(qlo1[rb][s], kh[s], acc);
-          acc = mfma32(qlo1[rb][s], kl[s], acc);
+          acc = mfma32(ql[s], kh[s], acc);
+          acc = mfma32(ql[s], kl[s], acc);
         }
         return acc;
       };
