@@ -1111,9 +1111,9 @@ void score_kernel(ScoreArgs a) {
 
   // row max over the 32 lanes holding a row's keys (mx: the raw dot's running max per row slot),
   // then the keep threshold x0 on the raw dot, and the weighted-vote origins.
-  // screened: the maximum came from the screen's fp32 dots of the (hi + lo) operands, which
-  // differ from pass 2's three-product value of the same key by the lo.lo term and the two
-  // summation orders.  For tau >= 0 the threshold is then capped at max - delta, with delta a
+  // screened: the maximum came from the screen's four-product fp32 scores of the (hi + lo)
+  // operands, which differ from pass 2's three-product value of the same key by the lo.lo term
+  // and the two summation orders.  For tau >= 0 the threshold is then capped at max - delta, with delta a
   // bound on that difference, so the row's best key keeps its vote (the reference's two passes
   // share one dot, exact_2.py:100, 118, so qk == m passes whenever tau >= 0); for tau above
   // delta * scale (1e-5 at unit-scale rows) the cap changes nothing.  A negative tau keeps no key
